@@ -1,0 +1,182 @@
+/*
+ * leankv_amd — C ABI of the MI355X (gfx950) decode hot path of LeanKV.
+ *
+ * All entry points take plain device pointers, sizes and a hipStream_t passed
+ * as `void*` (NULL = the legacy default stream).  They enqueue work and return
+ * immediately; nothing synchronises the host.  Return value: LKV_OK (0) or a
+ * negative LKV_ERR_* code; lkv_last_error() then holds a message (per thread).
+ *
+ * fp16 data is passed as `const void*` / `void*` holding IEEE binary16 values.
+ * Every entry point validates shapes, alignment and workspace size on the host
+ * before it launches anything; a rejected call launches nothing.
+ *
+ * Workspaces: the split-K entry points need a caller-provided device workspace
+ * of at least the size returned by the matching *_workspace_bytes() query.  It
+ * must be zero-filled once when first allocated; each call leaves its ticket
+ * counters at zero again, so the same workspace can be reused by later calls
+ * on the same stream without clearing.  Calls that share a workspace must not
+ * overlap (use one workspace per concurrently running stream).
+ */
+#ifndef LEANKV_AMD_H
+#define LEANKV_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LKV_OK 0
+#define LKV_ERR_INVALID (-1)     /* bad argument: shape, alignment, size      */
+#define LKV_ERR_HIP (-2)         /* HIP runtime error at launch               */
+#define LKV_ERR_UNSUPPORTED (-3) /* valid in the reference, not built here    */
+
+#define LKV_DTYPE_F32 0
+#define LKV_DTYPE_F16 1
+
+/* Library version (major*10000 + minor*100 + patch) and last error text. */
+int lkv_version(void);
+const char* lkv_last_error(void);
+
+/* ------------------------------------------------------------------------ */
+/* TEAL sparse GEMV                                                          */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * y[n] = sum_{z : |x[z]| > threshold} W[n, z] * x[z]      (fp32 accumulate)
+ *
+ * Replaces leankv/teal/kernels/sparse_gemv.py:143-181 `sparse_gemv(x, weight,
+ * threshold, sparsity_bin)` and its Triton kernel (:61-87).  `w_colmajor` is
+ * the weight W[N, Z] in the column-major layout that
+ * prepare_weight_for_sparse_gemv (sparse_gemv.py:229-234) produces, i.e. the
+ * row-major array A[Z][N] with A[z][n] = W[n][z]; row z holds N contiguous
+ * fp16 values.  x is fp16 [Z], y is fp16 [N].  The comparison is made in
+ * fp32 (|x| widened, threshold as given), strictly greater, as the Triton
+ * kernel does (sparse_gemv.py:82).  Rows of A whose activation fails the test
+ * are never read.  Requires N % 8 == 0 and 16-byte aligned x, A, y.
+ * Deterministic: the split-K partials are reduced in a fixed order.
+ */
+size_t lkv_sparse_gemv_workspace_bytes(int64_t N, int64_t Z);
+int lkv_sparse_gemv(const void* x, const void* w_colmajor, float threshold,
+                    int64_t N, int64_t Z, void* y,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Fused TEAL gate/up projection with the SwiGLU epilogue of a Mistral MLP:
+ *   g = sparse_gemv(x, Wg, t_gate), u = sparse_gemv(x, Wu, t_up)
+ *   h = fp16( fp16(silu(fp16(g))) * fp16(u) )
+ * x is read once.  The rounding steps reproduce the eager fp16 torch
+ * sequence `act_fn(gate_proj(x)) * up_proj(x)` of
+ * transformers/models/mistral/modeling_mistral.py:46-47 when gate_proj and
+ * up_proj are TEAL-patched (leankv/teal/patching.py:152-183).
+ * Wg, Wu: column-major [N, Z] as above (A[Z][N] rows); x fp16 [Z]; h fp16 [N].
+ * No single reference function: it fuses two reference sparse_gemv calls.
+ */
+size_t lkv_sparse_gateup_workspace_bytes(int64_t N, int64_t Z);
+int lkv_sparse_gateup_swiglu(const void* x, const void* wg_colmajor,
+                             const void* wu_colmajor, float t_gate, float t_up,
+                             int64_t N, int64_t Z, void* h,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* TurboQuant (MSE variant), head_dim 128                                    */
+/* ------------------------------------------------------------------------ */
+
+/* Bytes of one packed code row for `bits` (1..4) at dim 128: 16, 32, 64, 64. */
+int lkv_tq_packed_row_bytes(int bits);
+
+/*
+ * TurboQuantMSE.quantize (leankv/turboquant/quantizer.py:119-129):
+ *   n = ||x||;  u = x / (n + 1e-10);  y = float(u) @ Pi^T;
+ *   idx = #{b in bounds : b < y}   (torch.searchsorted, right=False);
+ *   packed = _pack_indices(idx, bits)   (quantizer.py:38-62)
+ * x: [M, 128], dtype LKV_DTYPE_F32 or LKV_DTYPE_F16 (the norm, the division
+ * and its rounding follow x's dtype, as in torch).  Pi: fp32 [128, 128]
+ * row-major.  bounds: fp32 decision boundaries, 2^bits - 1 of them
+ * (boundaries[1:-1], quantizer.py:115-117).  packed: uint8 [M, row_bytes].
+ * norms: [M] of x's dtype.  The rotation runs on fp32 MFMA.
+ */
+int lkv_tq_quantize(const void* x, int x_dtype, int64_t M, const float* Pi,
+                    const float* bounds, int bits, uint8_t* packed, void* norms,
+                    void* stream);
+
+/*
+ * The searchsorted + pack half of quantize on an already rotated fp32 y
+ * [M, 128] (quantizer.py:126-127).  Exact on every element.
+ */
+int lkv_tq_quantize_rotated(const float* y, int64_t M, const float* bounds,
+                            int bits, uint8_t* packed, void* stream);
+
+/*
+ * TurboQuantMSE.dequantize (quantizer.py:131-137):
+ *   x_hat = (centroids[unpack(packed)] @ Pi) * norm
+ * packed uint8 [M, row_bytes]; norms [M] of norm_dtype; centroids fp32
+ * [2^bits]; out [M, 128] of out_dtype (LKV_DTYPE_F16 reproduces the cache's
+ * `.to(float16)` of cache.py:176-181).  fp32 MFMA.
+ */
+int lkv_tq_dequantize(const uint8_t* packed, const void* norms, int norm_dtype,
+                      int64_t M, const float* Pi, const float* centroids, int bits,
+                      void* out, int out_dtype, void* stream);
+
+/*
+ * rotate_forward / rotate_backward (leankv/turboquant/rotation.py:45-52):
+ *   transpose == 0:  y = x @ Pi^T        transpose == 1:  y = x @ Pi
+ * x [M, 128] (F32 or F16), y fp32 [M, 128].  fp32 MFMA.
+ */
+int lkv_tq_rotate(const void* x, int x_dtype, int64_t M, const float* Pi,
+                  int transpose, float* y, void* stream);
+
+/*
+ * Decode-step cache append of TurboQuantCache.update for one layer
+ * (leankv/turboquant/cache.py:84-159) on a static ring layout.
+ * Current length before the append is *pos (device int32, read by the
+ * kernel, never written).  The hot window keeps the last `hot_cap` tokens in
+ * fp16 ring slots (token p lives in slot p % hot_cap); when pos >= hot_cap
+ * the token that leaves the window (p = pos - hot_cap) is quantized from its
+ * fp16 slot, widened to fp32 as cache.py:141-142 does, into cold row p;
+ * then the new token is written into slot pos % hot_cap.
+ *   k_new, v_new: fp16 [R, 128]       (R = batch * kv_heads)
+ *   k_hot, v_hot: fp16 [R, hot_cap, 128]
+ *   k_codes, v_codes: uint8 [R, cap, row_bytes];  k_norms, v_norms: fp32 [R, cap]
+ *   PiK, PiV: fp32 [128,128]; bounds fp32 [2^bits - 1]
+ * Rows beyond `cap` are never written: a call with pos - hot_cap >= cap
+ * skips the quantize (the host must size cap for the whole sequence).
+ */
+int lkv_tq_cache_append(const void* k_new, const void* v_new, void* k_hot, void* v_hot,
+                        uint8_t* k_codes, float* k_norms, uint8_t* v_codes, float* v_norms,
+                        const float* PiK, const float* PiV, const float* bounds, int bits,
+                        const int32_t* pos, int64_t R, int64_t hot_cap, int64_t cap,
+                        void* stream);
+
+/*
+ * Decode attention (q_len 1) over a TurboQuant cache, reading packed codes
+ * directly.  Equals SDPA over cat(dequantize(cold).fp16, hot) as built by
+ * TurboQuantCache._get_full_cache (cache.py:169-189) and consumed by
+ * transformers/integrations/sdpa_attention.py:79-105 (GQA, no mask), but never
+ * materialises the dequantized K/V:
+ *   s_t = scale * n_t * ((q @ PiK^T) . c[idx_t])     for cold tokens
+ *   o   = (sum_t p_t n_t c[idx_t]) @ PiV + sum_hot p_t v_t
+ * q: fp16 [B, Hq, 128]; codes uint8 [B, Hkv, cap, row_bytes] (bits 3/4 only:
+ * 4-bit nibbles); norms fp32 [B, Hkv, cap]; hot fp16 [B, Hkv, hot_cap, 128]
+ * ring as in lkv_tq_cache_append.  The current length L = *seq_len (device
+ * int32, includes every token already appended); cold tokens are
+ * [0, max(0, L - hot_cap)), hot tokens the rest.  max_len (host) bounds L and
+ * sizes the launch; L > max_len is clamped to max_len.  out: fp16 [B, Hq, 128].
+ * Hq must be a multiple of Hkv with Hq / Hkv <= 16.
+ */
+size_t lkv_tq_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len);
+int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const float* k_norms,
+                       const uint8_t* v_codes, const float* v_norms,
+                       const void* k_hot, const void* v_hot,
+                       const float* PiK, const float* PiV, const float* centroids, int bits,
+                       const int32_t* seq_len, int64_t max_len,
+                       int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t hot_cap,
+                       float scale, void* out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LEANKV_AMD_H */

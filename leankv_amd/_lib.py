@@ -1,0 +1,139 @@
+"""ctypes binding of ``libleankv_amd.so`` (the C ABI in include/leankv_amd.h).
+
+torch is imported first on purpose: torch ships its own ``libamdhip64.so``
+(SONAME libamdhip64.so.7); loading it before this library makes the dynamic
+loader resolve our NEEDED entry to the same HIP runtime instance, so the
+stream handles and device pointers torch hands us belong to our runtime too.
+
+There is no fallback: if the library is missing, importing the kernels raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
+
+from .build import LIB_PATH
+
+LKV_OK = 0
+LKV_DTYPE_F32 = 0
+LKV_DTYPE_F16 = 1
+
+_c_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_int = ctypes.c_int
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); the exact list exported by include/leankv_amd.h
+SIGNATURES = {
+    "lkv_version": (_int, []),
+    "lkv_last_error": (ctypes.c_char_p, []),
+    "lkv_sparse_gemv_workspace_bytes": (_sz, [_i64, _i64]),
+    "lkv_sparse_gemv": (_int, [_c_p, _c_p, _f32, _i64, _i64, _c_p, _c_p, _sz, _c_p]),
+    "lkv_sparse_gateup_workspace_bytes": (_sz, [_i64, _i64]),
+    "lkv_sparse_gateup_swiglu": (_int, [_c_p, _c_p, _c_p, _f32, _f32, _i64, _i64, _c_p, _c_p, _sz, _c_p]),
+    "lkv_tq_packed_row_bytes": (_int, [_int]),
+    "lkv_tq_quantize": (_int, [_c_p, _int, _i64, _c_p, _c_p, _int, _c_p, _c_p, _c_p]),
+    "lkv_tq_quantize_rotated": (_int, [_c_p, _i64, _c_p, _int, _c_p, _c_p]),
+    "lkv_tq_dequantize": (_int, [_c_p, _c_p, _int, _i64, _c_p, _c_p, _int, _c_p, _int, _c_p]),
+    "lkv_tq_rotate": (_int, [_c_p, _int, _i64, _c_p, _int, _c_p, _c_p]),
+    "lkv_tq_cache_append": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _int,
+                                   _c_p, _i64, _i64, _i64, _c_p]),
+    "lkv_tq_decode_attn_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "lkv_tq_decode_attn": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _int, _c_p,
+                                  _i64, _i64, _i64, _i64, _i64, _i64, _f32, _c_p, _c_p, _sz, _c_p]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class LeanKVError(RuntimeError):
+    """Raised when a leankv_amd C entry point rejects a call or fails to launch."""
+
+
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raises if it was never built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        p = path or LIB_PATH
+        if not os.path.exists(p):
+            raise ImportError(
+                "leankv_amd: %s is missing; build it with `python -m leankv_amd.build` "
+                "(there is no CPU fallback)" % p
+            )
+        lib = ctypes.CDLL(p)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    return load().lkv_last_error().decode(errors="replace")
+
+
+def check(rc: int, what: str) -> None:
+    if rc != LKV_OK:
+        raise LeanKVError("%s failed (code %d): %s" % (what, rc, last_error()))
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device | None = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return LKV_DTYPE_F32
+    if dt == torch.float16:
+        return LKV_DTYPE_F16
+    raise TypeError("leankv_amd: unsupported dtype %s (float32/float16 only)" % dt)
+
+
+def require_cuda(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise LeanKVError(
+                "leankv_amd kernels run on the GPU only; got a tensor on %s" % t.device
+            )
+
+
+class _Workspaces:
+    """Zero-filled device workspaces, one per (device, key), grown on demand.
+
+    The kernels leave their ticket counters at zero when they finish, so a
+    workspace stays reusable by later calls on the same stream without any
+    clearing (which also keeps the calls capturable in a HIP graph).
+    """
+
+    def __init__(self):
+        self._bufs: dict[tuple[int, str], torch.Tensor] = {}
+
+    def get(self, device: torch.device, key: str, nbytes: int) -> torch.Tensor:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        k = (idx, key)
+        buf = self._bufs.get(k)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, 256)
+            if buf is not None:
+                size = max(size, 2 * buf.numel())
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            self._bufs[k] = buf
+        return buf
+
+
+workspaces = _Workspaces()

@@ -1,0 +1,91 @@
+// Shared helpers for the leankv_amd HIP kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/leankv_amd.h"
+
+namespace lkv {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- errors
+void set_error(const char* fmt, ...);
+
+#define LKV_REQUIRE(cond, ...)                 \
+  do {                                         \
+    if (!(cond)) {                             \
+      ::lkv::set_error(__VA_ARGS__);           \
+      return LKV_ERR_INVALID;                  \
+    }                                          \
+  } while (0)
+
+#define LKV_LAUNCH_CHECK(what)                                                 \
+  do {                                                                         \
+    hipError_t e_ = hipGetLastError();                                         \
+    if (e_ != hipSuccess) {                                                    \
+      ::lkv::set_error("%s: launch failed: %s", what, hipGetErrorString(e_)); \
+      return LKV_ERR_HIP;                                                      \
+    }                                                                          \
+  } while (0)
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+// Number of compute units of the current device (cached per device id).
+int device_cu_count();
+
+// ---------------------------------------------------------------- device helpers
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+
+// Lane prefix count of set bits below this lane in a 64-bit wave mask.
+__device__ __forceinline__ int lane_prefix(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+}
+
+__device__ __forceinline__ uint64_t wave_ballot(bool p) {
+  return __ballot(p);
+}
+
+// Agent-scope release/acquire around the split-K ticket.  On gfx950 each XCD
+// has its own L2; agent-scope fences write back / invalidate it so partials
+// written on one XCD are visible to the block that reduces them on another.
+__device__ __forceinline__ void fence_release_agent() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+}
+__device__ __forceinline__ void fence_acquire_agent() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+__device__ __forceinline__ unsigned ticket_add(unsigned* p) {
+  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ticket_reset(unsigned* p) {
+  __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Butterfly reductions within 16-lane rows / across the wave.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+}  // namespace lkv

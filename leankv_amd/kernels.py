@@ -1,0 +1,306 @@
+"""torch-facing wrappers of the leankv_amd HIP kernels (GPU only, no fallback).
+
+Each wrapper validates dtypes/shapes/devices, takes raw device pointers and
+the current HIP stream from torch, and calls one C entry point of
+``libleankv_amd.so``.  ``*_out`` variants write into caller-owned buffers so
+that a decode step can be captured in a HIP graph without allocations.
+
+The functions are also registered as torch custom ops under the ``leankv``
+namespace (``torch.ops.leankv.sparse_gemv`` ...) for callers that go through
+the dispatcher; the Python entry points below skip the dispatcher.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from ._lib import LeanKVError, check, dtype_code, ptr, require_cuda, stream_handle, workspaces
+
+HEAD_DIM = 128
+
+
+def _lib_handle():
+    return _lib.load()
+
+
+# ----------------------------------------------------------------- TEAL GEMV
+def colmajor_rows(weight: torch.Tensor) -> tuple[int, int]:
+    """(N, Z) of a weight W[N, Z] stored column-major (strides (1, N))."""
+    if weight.dim() != 2:
+        raise LeanKVError("sparse_gemv: weight must be 2-D [N, Z], got %s" % (tuple(weight.shape),))
+    N, Z = weight.shape
+    if not weight.t().is_contiguous():
+        raise LeanKVError(
+            "sparse_gemv: weight must be column-major (strides (1, N)) as produced by "
+            "prepare_weight_for_sparse_gemv; got strides %s" % (weight.stride(),)
+        )
+    return N, Z
+
+
+def _check_x(x: torch.Tensor, Z: int, what: str) -> torch.Tensor:
+    if x.dtype != torch.float16:
+        raise LeanKVError("%s: x must be float16, got %s" % (what, x.dtype))
+    if x.numel() != Z:
+        raise LeanKVError("%s: x has %d elements, weight expects Z=%d" % (what, x.numel(), Z))
+    return x.reshape(Z).contiguous()
+
+
+def sparse_gemv_out(x: torch.Tensor, weight: torch.Tensor, threshold: float, out: torch.Tensor) -> torch.Tensor:
+    """out[N] = W @ (x * (|x| > threshold)) with W[N, Z] column-major, fp32 accumulate."""
+    N, Z = colmajor_rows(weight)
+    require_cuda(x, weight, out)
+    xf = _check_x(x, Z, "sparse_gemv")
+    if weight.dtype != torch.float16 or out.dtype != torch.float16:
+        raise LeanKVError("sparse_gemv: weight and out must be float16")
+    if out.numel() != N or not out.is_contiguous():
+        raise LeanKVError("sparse_gemv: out must be a contiguous float16 tensor of %d elements" % N)
+    lib = _lib_handle()
+    nbytes = lib.lkv_sparse_gemv_workspace_bytes(N, Z)
+    ws = workspaces.get(x.device, "gemv", nbytes)
+    check(
+        lib.lkv_sparse_gemv(ptr(xf), ptr(weight), float(threshold), N, Z, ptr(out), ptr(ws), ws.numel(),
+                            stream_handle(x.device)),
+        "lkv_sparse_gemv",
+    )
+    return out
+
+
+def sparse_gemv(x: torch.Tensor, weight: torch.Tensor, threshold: float) -> torch.Tensor:
+    N, _ = colmajor_rows(weight)
+    out = torch.empty(N, dtype=torch.float16, device=x.device)
+    return sparse_gemv_out(x, weight, threshold, out)
+
+
+def sparse_gateup_swiglu_out(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, t_gate: float,
+                             t_up: float, out: torch.Tensor) -> torch.Tensor:
+    """out[N] = fp16(silu(fp16(Wg x_g)) * fp16(Wu x_u)), x_g/x_u thresholded copies of x."""
+    N, Z = colmajor_rows(w_gate)
+    if tuple(w_up.shape) != (N, Z):
+        raise LeanKVError("sparse_gateup_swiglu: gate/up weight shapes differ")
+    colmajor_rows(w_up)
+    require_cuda(x, w_gate, w_up, out)
+    xf = _check_x(x, Z, "sparse_gateup_swiglu")
+    if w_gate.dtype != torch.float16 or w_up.dtype != torch.float16 or out.dtype != torch.float16:
+        raise LeanKVError("sparse_gateup_swiglu: weights and out must be float16")
+    if out.numel() != N or not out.is_contiguous():
+        raise LeanKVError("sparse_gateup_swiglu: out must be contiguous with %d elements" % N)
+    lib = _lib_handle()
+    nbytes = lib.lkv_sparse_gateup_workspace_bytes(N, Z)
+    ws = workspaces.get(x.device, "gateup", nbytes)
+    check(
+        lib.lkv_sparse_gateup_swiglu(ptr(xf), ptr(w_gate), ptr(w_up), float(t_gate), float(t_up), N, Z,
+                                     ptr(out), ptr(ws), ws.numel(), stream_handle(x.device)),
+        "lkv_sparse_gateup_swiglu",
+    )
+    return out
+
+
+def sparse_gateup_swiglu(x, w_gate, w_up, t_gate, t_up):
+    N, _ = colmajor_rows(w_gate)
+    out = torch.empty(N, dtype=torch.float16, device=x.device)
+    return sparse_gateup_swiglu_out(x, w_gate, w_up, t_gate, t_up, out)
+
+
+# ----------------------------------------------------------------- TurboQuant
+def packed_row_bytes(bits: int) -> int:
+    n = _lib_handle().lkv_tq_packed_row_bytes(int(bits))
+    if n < 0:
+        raise LeanKVError("TurboQuant: bits=%d cannot be bit-packed (1..4 supported)" % bits)
+    return n
+
+
+def _rows(x: torch.Tensor, what: str) -> int:
+    if x.shape[-1] != HEAD_DIM:
+        raise LeanKVError("%s: last dim must be %d, got %d" % (what, HEAD_DIM, x.shape[-1]))
+    return x.numel() // HEAD_DIM
+
+
+def _pi(Pi: torch.Tensor, device) -> torch.Tensor:
+    if tuple(Pi.shape) != (HEAD_DIM, HEAD_DIM):
+        raise LeanKVError("TurboQuant: rotation must be [128, 128], got %s" % (tuple(Pi.shape),))
+    return Pi.to(device=device, dtype=torch.float32).contiguous()
+
+
+def tq_quantize(x: torch.Tensor, Pi: torch.Tensor, bounds: torch.Tensor, bits: int):
+    """Fused norm / normalise / rotate (fp32 MFMA) / searchsorted / pack."""
+    require_cuda(x)
+    M = _rows(x, "tq_quantize")
+    xc = x.contiguous()
+    lib = _lib_handle()
+    rb = packed_row_bytes(bits)
+    packed = torch.empty(*x.shape[:-1], rb, dtype=torch.uint8, device=x.device)
+    norms = torch.empty(x.shape[:-1], dtype=x.dtype, device=x.device)
+    b = bounds.to(device=x.device, dtype=torch.float32).contiguous()
+    if b.numel() != (1 << bits) - 1:
+        raise LeanKVError("tq_quantize: %d decision boundaries for bits=%d" % (b.numel(), bits))
+    check(
+        lib.lkv_tq_quantize(ptr(xc), dtype_code(x.dtype), M, ptr(_pi(Pi, x.device)), ptr(b), int(bits),
+                            ptr(packed), ptr(norms), stream_handle(x.device)),
+        "lkv_tq_quantize",
+    )
+    return packed, norms
+
+
+def tq_quantize_rotated(y: torch.Tensor, bounds: torch.Tensor, bits: int) -> torch.Tensor:
+    require_cuda(y)
+    if y.dtype != torch.float32:
+        raise LeanKVError("tq_quantize_rotated: y must be float32")
+    M = _rows(y, "tq_quantize_rotated")
+    yc = y.contiguous()
+    packed = torch.empty(*y.shape[:-1], packed_row_bytes(bits), dtype=torch.uint8, device=y.device)
+    b = bounds.to(device=y.device, dtype=torch.float32).contiguous()
+    check(
+        _lib_handle().lkv_tq_quantize_rotated(ptr(yc), M, ptr(b), int(bits), ptr(packed), stream_handle(y.device)),
+        "lkv_tq_quantize_rotated",
+    )
+    return packed
+
+
+def tq_dequantize(packed: torch.Tensor, norms: torch.Tensor, Pi: torch.Tensor, centroids: torch.Tensor,
+                  bits: int, out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None):
+    require_cuda(packed, norms)
+    rb = packed_row_bytes(bits)
+    if packed.dtype != torch.uint8 or packed.shape[-1] != rb:
+        raise LeanKVError("tq_dequantize: packed must be uint8 [..., %d]" % rb)
+    M = packed.numel() // rb
+    if norms.numel() != M:
+        raise LeanKVError("tq_dequantize: %d norms for %d rows" % (norms.numel(), M))
+    pc = packed.contiguous()
+    nc = norms.contiguous()
+    if out is None:
+        out = torch.empty(*packed.shape[:-1], HEAD_DIM, dtype=out_dtype, device=packed.device)
+    c = centroids.to(device=packed.device, dtype=torch.float32).contiguous()
+    check(
+        _lib_handle().lkv_tq_dequantize(ptr(pc), ptr(nc), dtype_code(nc.dtype), M, ptr(_pi(Pi, packed.device)),
+                                        ptr(c), int(bits), ptr(out), dtype_code(out.dtype),
+                                        stream_handle(packed.device)),
+        "lkv_tq_dequantize",
+    )
+    return out
+
+
+def tq_rotate(x: torch.Tensor, Pi: torch.Tensor, transpose: bool = False) -> torch.Tensor:
+    """x @ Pi^T (transpose=False, rotate_forward) or x @ Pi (rotate_backward), fp32 out."""
+    require_cuda(x)
+    M = _rows(x, "tq_rotate")
+    xc = x.contiguous()
+    y = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    check(
+        _lib_handle().lkv_tq_rotate(ptr(xc), dtype_code(x.dtype), M, ptr(_pi(Pi, x.device)), int(bool(transpose)),
+                                    ptr(y), stream_handle(x.device)),
+        "lkv_tq_rotate",
+    )
+    return y
+
+
+def tq_cache_append(k_new, v_new, k_hot, v_hot, k_codes, k_norms, v_codes, v_norms, PiK, PiV, bounds, bits,
+                    pos_dev) -> None:
+    """Decode-step append on the static ring layout (see include/leankv_amd.h)."""
+    require_cuda(k_new, v_new, k_hot, v_hot, k_codes, v_codes, pos_dev)
+    R = k_new.numel() // HEAD_DIM
+    hot_cap = k_hot.shape[-2]
+    cap = k_codes.shape[-2]
+    for t, nm in ((k_new, "k_new"), (v_new, "v_new"), (k_hot, "k_hot"), (v_hot, "v_hot")):
+        if t.dtype != torch.float16 or not t.is_contiguous():
+            raise LeanKVError("tq_cache_append: %s must be contiguous float16" % nm)
+    if k_hot.numel() != R * hot_cap * HEAD_DIM or k_codes.numel() != R * cap * packed_row_bytes(bits):
+        raise LeanKVError("tq_cache_append: buffer shapes disagree with %d rows" % R)
+    if pos_dev.dtype != torch.int32:
+        raise LeanKVError("tq_cache_append: pos must be an int32 device tensor")
+    check(
+        _lib_handle().lkv_tq_cache_append(ptr(k_new), ptr(v_new), ptr(k_hot), ptr(v_hot), ptr(k_codes),
+                                          ptr(k_norms), ptr(v_codes), ptr(v_norms), ptr(PiK), ptr(PiV),
+                                          ptr(bounds), int(bits), ptr(pos_dev), R, hot_cap, cap,
+                                          stream_handle(k_new.device)),
+        "lkv_tq_cache_append",
+    )
+
+
+def decode_attn_workspace_bytes(B: int, Hq: int, Hkv: int, max_len: int) -> int:
+    return int(_lib_handle().lkv_tq_decode_attn_workspace_bytes(B, Hq, Hkv, max_len))
+
+
+def tq_decode_attn_out(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK, PiV, centroids, bits, seq_len_dev,
+                       max_len: int, scale: float, out: torch.Tensor, workspace: torch.Tensor | None = None):
+    """Single-query GQA attention over the packed cold cache + fp16 hot ring.
+
+    q: fp16 [B, Hq, 128]; codes uint8 [B, Hkv, cap, 64]; norms fp32 [B, Hkv, cap];
+    hot fp16 [B, Hkv, hot_cap, 128]; seq_len_dev int32 [1] (device); out fp16 [B, Hq, 128].
+    """
+    require_cuda(q, k_codes, v_codes, k_hot, v_hot, seq_len_dev, out)
+    if q.dtype != torch.float16 or q.dim() != 3 or q.shape[-1] != HEAD_DIM or not q.is_contiguous():
+        raise LeanKVError("tq_decode_attn: q must be contiguous float16 [B, Hq, 128]")
+    B, Hq, _ = q.shape
+    Hkv, cap = k_codes.shape[1], k_codes.shape[2]
+    hot_cap = k_hot.shape[2]
+    if out.shape != q.shape or out.dtype != torch.float16 or not out.is_contiguous():
+        raise LeanKVError("tq_decode_attn: out must be contiguous float16 like q")
+    lib = _lib_handle()
+    nbytes = lib.lkv_tq_decode_attn_workspace_bytes(B, Hq, Hkv, max_len)
+    if workspace is None:
+        workspace = workspaces.get(q.device, "attn", nbytes)
+    check(
+        lib.lkv_tq_decode_attn(ptr(q), ptr(k_codes), ptr(k_norms), ptr(v_codes), ptr(v_norms), ptr(k_hot),
+                               ptr(v_hot), ptr(PiK), ptr(PiV), ptr(centroids), int(bits), ptr(seq_len_dev),
+                               int(max_len), B, Hq, Hkv, cap, hot_cap, float(scale), ptr(out), ptr(workspace),
+                               workspace.numel(), stream_handle(q.device)),
+        "lkv_tq_decode_attn",
+    )
+    return out
+
+
+def tq_decode_attn(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK, PiV, centroids, bits, seq_len_dev,
+                   max_len: int, scale: float | None = None):
+    out = torch.empty_like(q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(HEAD_DIM)
+    return tq_decode_attn_out(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK, PiV, centroids, bits,
+                              seq_len_dev, max_len, scale, out)
+
+
+# ------------------------------------------------------- torch custom ops
+_LIB_DEF = None
+
+
+def _register_ops() -> None:
+    """Expose the kernels as torch.ops.leankv.* (CUDA impl + Meta shape fns)."""
+    global _LIB_DEF
+    if _LIB_DEF is not None:
+        return
+    lib = torch.library.Library("leankv", "DEF")
+    lib.define("sparse_gemv(Tensor x, Tensor weight, float threshold) -> Tensor")
+    lib.define("sparse_gateup_swiglu(Tensor x, Tensor w_gate, Tensor w_up, float t_gate, float t_up) -> Tensor")
+    lib.define("tq_quantize(Tensor x, Tensor Pi, Tensor bounds, int bits) -> (Tensor, Tensor)")
+    lib.define("tq_quantize_rotated(Tensor y, Tensor bounds, int bits) -> Tensor")
+    lib.define("tq_dequantize(Tensor packed, Tensor norms, Tensor Pi, Tensor centroids, int bits) -> Tensor")
+    lib.define("tq_rotate(Tensor x, Tensor Pi, bool transpose) -> Tensor")
+    lib.impl("sparse_gemv", lambda x, w, t: sparse_gemv(x, w, t), "CUDA")
+    lib.impl("sparse_gateup_swiglu", lambda x, wg, wu, tg, tu: sparse_gateup_swiglu(x, wg, wu, tg, tu), "CUDA")
+    lib.impl("tq_quantize", lambda x, Pi, b, bits: tq_quantize(x, Pi, b, bits), "CUDA")
+    lib.impl("tq_quantize_rotated", lambda y, b, bits: tq_quantize_rotated(y, b, bits), "CUDA")
+    lib.impl("tq_dequantize", lambda p, n, Pi, c, bits: tq_dequantize(p, n, Pi, c, bits), "CUDA")
+    lib.impl("tq_rotate", lambda x, Pi, tr: tq_rotate(x, Pi, tr), "CUDA")
+
+    def _meta_gemv(x, w, t):
+        return x.new_empty(w.shape[0], dtype=torch.float16)
+
+    def _meta_gateup(x, wg, wu, tg, tu):
+        return x.new_empty(wg.shape[0], dtype=torch.float16)
+
+    def _meta_quant(x, Pi, b, bits):
+        rb = {1: 16, 2: 32}.get(int(bits), 64)
+        return (x.new_empty(*x.shape[:-1], rb, dtype=torch.uint8), x.new_empty(x.shape[:-1]))
+
+    lib.impl("sparse_gemv", _meta_gemv, "Meta")
+    lib.impl("sparse_gateup_swiglu", _meta_gateup, "Meta")
+    lib.impl("tq_quantize", _meta_quant, "Meta")
+    _LIB_DEF = lib
+
+
+try:
+    _register_ops()
+except RuntimeError:  # already registered in this process (module reload)
+    pass

@@ -1,0 +1,56 @@
+"""TEAL sparse GEMV entry points with the reference's signatures, on HIP.
+
+Drop-in for leankv/teal/kernels/sparse_gemv.py:
+  sparse_gemv(x, weight, threshold, sparsity_bin)        (:143-181)
+  batched_sparse_gemm(x, weight, threshold, sparsity_bin) (:184-226)
+  prepare_weight_for_sparse_gemv(weight)                 (:229-234)
+plus sparse_gateup_swiglu (no reference counterpart: it fuses the gate and up
+sparse_gemv calls of a TEAL-patched Mistral MLP so x is read once).
+
+sparsity_bin only keyed the Triton autotuner; the HIP kernel picks its launch
+shape from (N, Z) and the argument is accepted and ignored.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ... import kernels as _k
+
+
+def prepare_weight_for_sparse_gemv(weight: torch.Tensor) -> torch.Tensor:
+    """Column-major copy of W[N, Z] (row z of the storage = weight column z)."""
+    return weight.t().contiguous().t()
+
+
+def sparse_gemv(x: torch.Tensor, weight: torch.Tensor, threshold: float, sparsity_bin: int = 5) -> torch.Tensor:
+    """[1, 1, N] = sparse(x[1, 1, Z]) @ W^T for column-major fp16 W[N, Z]."""
+    N, Z = weight.shape
+    xh = x.reshape(Z)
+    if xh.dtype != torch.float16:
+        xh = xh.to(torch.float16)
+    out = _k.sparse_gemv(xh, weight, threshold).reshape(1, 1, N)
+    if x.dtype != torch.float16:
+        out = out.to(x.dtype)
+    return out
+
+
+def batched_sparse_gemm(x: torch.Tensor, weight: torch.Tensor, threshold: float,
+                        sparsity_bin: int = 5) -> torch.Tensor:
+    """[B, N]: each row of x[B, Z] gets its own mask (one sparse GEMV per row)."""
+    N, Z = weight.shape
+    xs = x.reshape(-1, Z)
+    out = torch.empty(xs.shape[0], N, dtype=torch.float16, device=x.device)
+    for b in range(xs.shape[0]):
+        _k.sparse_gemv_out(xs[b].to(torch.float16), weight, threshold, out[b])
+    return out if x.dtype == torch.float16 else out.to(x.dtype)
+
+
+def sparse_gateup_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, t_gate: float,
+                         t_up: float) -> torch.Tensor:
+    """fp16 [1, 1, N] = silu(gate(x)) * up(x) with TEAL thresholds on both inputs."""
+    N, Z = w_gate.shape
+    xh = x.reshape(Z)
+    if xh.dtype != torch.float16:
+        xh = xh.to(torch.float16)
+    return _k.sparse_gateup_swiglu(xh, w_gate, w_up, t_gate, t_up).reshape(1, 1, N)

@@ -1,0 +1,221 @@
+"""Apply TEAL activation sparsity to a HuggingFace decoder, on HIP kernels.
+
+Drop-in for leankv/teal/patching.py:
+  apply_teal(model, sparsity, thresholds, thresholds_path, calibration_data,
+             use_triton)                                   (:57-149)
+  remove_teal(model), get_sparsity_report, print_sparsity_report (:186-238)
+  _collect_input_activations                               (:241-256)
+
+Threshold selection, the "exactly one source" rule and the hook-based
+correctness mode are the reference's.  ``use_triton=True`` (name kept for
+drop-in callers; ``use_hip`` is an alias) routes every projection with t > 0
+to the HIP sparse GEMV at B=1 single-token decode and keeps the dense F.linear
+otherwise, the reference's dispatch rule (:169-180).  In addition, when both
+gate_proj and up_proj of a layer are patched, the MLP forward is patched so the
+two projections and the SwiGLU run as one fused HIP kernel reading x once
+(``fuse_mlp=False`` turns this off).
+"""
+
+from __future__ import annotations
+
+import json
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from .kernels.sparse_gemv import prepare_weight_for_sparse_gemv, sparse_gateup_swiglu, sparse_gemv
+from .sparse_fns import SparsifyFn, compute_threshold_for_sparsity
+
+PROJ_NAMES = ["q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"]
+ATTN_PROJS = {"q_proj", "k_proj", "v_proj", "o_proj"}
+MLP_PROJS = {"gate_proj", "up_proj", "down_proj"}
+
+
+def _get_layers(model):
+    if hasattr(model, "model") and hasattr(model.model, "layers"):
+        return model.model.layers
+    raise ValueError(
+        "Cannot find transformer layers in model of type %s. Expected model.model.layers attribute." % type(model)
+    )
+
+
+def _get_projection(layer, proj_name: str) -> nn.Linear:
+    return getattr(layer.self_attn if proj_name in ATTN_PROJS else layer.mlp, proj_name)
+
+
+def _is_single_token(x: torch.Tensor) -> bool:
+    return x.shape[-2] == 1 and (x.shape[0] if x.dim() == 3 else 1) == 1
+
+
+def apply_teal(
+    model,
+    sparsity: Optional[float] = None,
+    thresholds: Optional[dict] = None,
+    thresholds_path: Optional[str] = None,
+    calibration_data: Optional[list] = None,
+    use_triton: bool = False,
+    use_hip: Optional[bool] = None,
+    fuse_mlp: bool = True,
+):
+    """Install TEAL on all 7 projections of every layer; returns {(layer, proj): SparsifyFn}."""
+    if sum(v is not None for v in (sparsity, thresholds, thresholds_path)) != 1:
+        raise ValueError("Exactly one of sparsity, thresholds, or thresholds_path must be provided.")
+    use_kernel = bool(use_triton if use_hip is None else use_hip)
+
+    if thresholds_path is not None:
+        with open(thresholds_path, "r") as f:
+            thresholds = {int(k): v for k, v in json.load(f).items()}
+
+    layers = _get_layers(model)
+    sparsifiers = {}
+    hooks = []
+    for layer_idx, layer in enumerate(layers):
+        for proj_name in PROJ_NAMES:
+            proj = _get_projection(layer, proj_name)
+            if thresholds is not None:
+                t = thresholds.get(layer_idx, thresholds.get(str(layer_idx), {})).get(proj_name, 0.0)
+            elif sparsity is not None and sparsity > 0:
+                if calibration_data is not None:
+                    with torch.no_grad():
+                        acts = _collect_input_activations(model, proj, calibration_data)
+                        t = compute_threshold_for_sparsity(acts, sparsity)
+                else:
+                    t = sparsity * 0.1
+            else:
+                t = 0.0
+            sf = SparsifyFn(threshold=t, enabled=(t > 0))
+            sparsifiers[(layer_idx, proj_name)] = sf
+            if use_kernel and t > 0:
+                _patch_linear_with_kernel(proj, t)
+            else:
+                def make_hook(fn):
+                    def hook_fn(module, args):
+                        return (fn(args[0]),) + args[1:]
+                    return hook_fn
+                hooks.append(proj.register_forward_pre_hook(make_hook(sf)))
+        if use_kernel and fuse_mlp:
+            _maybe_patch_mlp(layer.mlp)
+
+    if not hasattr(model, "_teal_hooks"):
+        model._teal_hooks = []
+    model._teal_hooks.extend(hooks)
+    model._teal_sparsifiers = sparsifiers
+    print("[TEAL] Using HIP sparse GEMV kernels (gfx950)" if use_kernel
+          else "[TEAL] Using hook-based sparsification (correctness only)")
+    return sparsifiers
+
+
+def _patch_linear_with_kernel(linear: nn.Linear, threshold: float) -> None:
+    """Relayout the weight column-major (permanent) and route B=1 decode to HIP."""
+    with torch.no_grad():
+        linear.weight.data = prepare_weight_for_sparse_gemv(linear.weight.data)
+    N = linear.weight.shape[0]
+
+    def sparse_forward(x):
+        if _is_single_token(x):
+            out = sparse_gemv(x.reshape(1, 1, x.shape[-1]), linear.weight, threshold)
+            out = out.reshape(x.shape[:-1] + (N,))
+            if linear.bias is not None:
+                out = out + linear.bias
+            return out
+        return torch.nn.functional.linear(x, linear.weight, linear.bias)
+
+    linear._teal_original_forward = linear.forward
+    linear.forward = sparse_forward
+    linear._teal_patched = True
+    linear._teal_threshold = threshold
+
+
+# Reference name kept for callers that reach into the module.
+def _patch_linear_with_triton(linear: nn.Linear, threshold: float, sparsity: float = 0.4) -> None:
+    _patch_linear_with_kernel(linear, threshold)
+
+
+def _maybe_patch_mlp(mlp: nn.Module) -> None:
+    """Fuse gate/up + SwiGLU when both projections carry a kernel patch."""
+    gate, up, down = getattr(mlp, "gate_proj", None), getattr(mlp, "up_proj", None), getattr(mlp, "down_proj", None)
+    if gate is None or up is None or down is None:
+        return
+    if not (getattr(gate, "_teal_patched", False) and getattr(up, "_teal_patched", False)):
+        return
+    if gate.bias is not None or up.bias is not None:
+        return
+    act = getattr(mlp, "act_fn", None)
+    if act is None or not isinstance(act, nn.SiLU):
+        return
+    original = mlp.forward
+
+    def fused_forward(x):
+        if _is_single_token(x):
+            h = sparse_gateup_swiglu(x, gate.weight, up.weight, gate._teal_threshold, up._teal_threshold)
+            h = h.reshape(x.shape[:-1] + (gate.weight.shape[0],))
+            if x.dtype != torch.float16:
+                h = h.to(x.dtype)
+            return down(h)
+        return original(x)
+
+    mlp._teal_original_forward = original
+    mlp.forward = fused_forward
+    mlp._teal_fused = True
+
+
+def remove_teal(model):
+    """Remove TEAL hooks and restore patched forwards (weights stay column-major)."""
+    if hasattr(model, "_teal_hooks"):
+        for h in model._teal_hooks:
+            h.remove()
+        model._teal_hooks.clear()
+    if hasattr(model, "_teal_sparsifiers"):
+        del model._teal_sparsifiers
+    try:
+        layers = _get_layers(model)
+    except ValueError:
+        return
+    for layer in layers:
+        mods = [_get_projection(layer, p) for p in PROJ_NAMES] + [layer.mlp]
+        for m in mods:
+            if hasattr(m, "_teal_original_forward"):
+                m.forward = m._teal_original_forward
+                del m._teal_original_forward
+                for a in ("_teal_patched", "_teal_fused"):
+                    if hasattr(m, a):
+                        delattr(m, a)
+
+
+def get_sparsity_report(model) -> dict:
+    if not hasattr(model, "_teal_sparsifiers"):
+        return {}
+    return {k: sf.last_sparsity for k, sf in model._teal_sparsifiers.items()}
+
+
+def print_sparsity_report(model):
+    report = get_sparsity_report(model)
+    if not report:
+        print("No TEAL sparsifiers found on model.")
+        return
+    by_layer: dict = {}
+    for (li, pn), s in report.items():
+        by_layer.setdefault(li, {})[pn] = s
+    print("%-8s" % "Layer" + "".join("%-12s" % p for p in PROJ_NAMES) + "%-8s" % "Avg")
+    print("-" * (8 + 12 * 7 + 8))
+    for li in sorted(by_layer):
+        vals = [by_layer[li].get(p, 0.0) for p in PROJ_NAMES]
+        print("%-8d" % li + "".join("%10.1f%%  " % (100 * v) for v in vals) + "%6.1f%%" % (100 * sum(vals) / len(vals)))
+
+
+def _collect_input_activations(model, target_module, data_samples):
+    """Inputs seen by target_module over up to 10 calibration samples (CPU copies)."""
+    acts = []
+
+    def hook_fn(module, args):
+        acts.append(args[0].detach().cpu())
+
+    handle = target_module.register_forward_pre_hook(hook_fn)
+    try:
+        for sample in data_samples[:10]:
+            with torch.no_grad():
+                model(sample.to(model.device))
+    finally:
+        handle.remove()
+    return torch.cat(acts, dim=0)
