@@ -57,6 +57,12 @@ __device__ __forceinline__ uint64_t wave_ballot(bool p) {
   return __ballot(p);
 }
 
+// Every split-K workspace starts with a fixed ticket area: kTicketBytes of
+// uint32 counters at offset 0, whatever the call's shape, so counters of one
+// call never land on another call's partial sums.  Kernels leave counters at 0.
+constexpr size_t kTicketBytes = 64 * 1024;
+constexpr int64_t kMaxTickets = static_cast<int64_t>(kTicketBytes / 4);
+
 // Agent-scope release/acquire around the split-K ticket.  On gfx950 each XCD
 // has its own L2; agent-scope fences write back / invalidate it so partials
 // written on one XCD are visible to the block that reduces them on another.
@@ -66,8 +72,9 @@ __device__ __forceinline__ void fence_release_agent() {
 __device__ __forceinline__ void fence_acquire_agent() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
+// Relaxed: callers bracket it with the explicit fences above (one thread per block).
 __device__ __forceinline__ unsigned ticket_add(unsigned* p) {
-  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void ticket_reset(unsigned* p) {
   __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

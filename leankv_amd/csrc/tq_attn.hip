@@ -344,12 +344,15 @@ __global__ __launch_bounds__(kThreads) void tq_decode_attn_kernel(AttnParams P) 
   }
 
   // ---------------------------------------------------------------- combine
-  fence_release_agent();
   __syncthreads();
-  if (tid == 0) s_last = (ticket_add(&P.tickets[bh]) == static_cast<unsigned>(P.nsplit));
+  if (tid == 0) {
+    fence_release_agent();
+    const bool last = ticket_add(&P.tickets[bh]) == static_cast<unsigned>(P.nsplit);
+    if (last) fence_acquire_agent();
+    s_last = last;
+  }
   __syncthreads();
   if (!s_last) return;
-  fence_acquire_agent();
 
   // LDS reuse: s_o[0..1] hold the (nsplit+1) x G merge weights (the host
   // keeps nsplit + 1 <= 256), s_o[2] the rotated cold sum [G][128].
@@ -442,10 +445,10 @@ AttnPlan plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_c
   p.split_tokens = static_cast<int>(ts);
   const int64_t G = Hkv > 0 ? Hq / Hkv : 1;
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
-  p.qrot_off = 0;
-  p.part_off = al(static_cast<size_t>(B * Hq * kD) * 4);
-  p.tick_off = p.part_off + al(static_cast<size_t>(B * Hkv * (ns_cap + 1) * G * (2 + kD)) * 4);
-  p.total = p.tick_off + al(static_cast<size_t>(B * Hkv) * 4);
+  p.tick_off = 0;  // fixed ticket area shared with every other split-K entry point
+  p.qrot_off = kTicketBytes;
+  p.part_off = p.qrot_off + al(static_cast<size_t>(B * Hq * kD) * 4);
+  p.total = p.part_off + al(static_cast<size_t>(B * Hkv * (ns_cap + 1) * G * (2 + kD)) * 4);
   return p;
 }
 
@@ -455,7 +458,7 @@ AttnPlan plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_c
 using namespace lkv;
 
 extern "C" size_t lkv_tq_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len) {
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len < 0) return 256;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len < 0) return kTicketBytes;
   // hot_cap only shifts the cold range; size for the largest split count.
   return plan(B, Hq, Hkv, max_len, 0).total;
 }
@@ -476,6 +479,8 @@ extern "C" int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const f
               "tq_decode_attn: max_len=%lld exceeds cap+hot_cap=%lld", (long long)max_len,
               (long long)(cap + hot_cap));
   LKV_REQUIRE(max_len < (1ll << 31) && cap < (1ll << 31), "tq_decode_attn: length too large");
+  LKV_REQUIRE(B * Hkv <= kMaxTickets, "tq_decode_attn: batch*kv_heads=%lld exceeds %lld tickets",
+              (long long)(B * Hkv), (long long)kMaxTickets);
   if (B == 0) return LKV_OK;
   LKV_REQUIRE(q && k_codes && k_norms && v_codes && v_norms && k_hot && v_hot && PiK && PiV && centroids &&
                   seq_len && out && workspace,

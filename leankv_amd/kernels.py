@@ -119,9 +119,21 @@ def _rows(x: torch.Tensor, what: str) -> int:
 
 
 def _pi(Pi: torch.Tensor, device) -> torch.Tensor:
+    """Row-major fp32 [128, 128] on `device` (no copy when it already is).
+
+    torch.linalg.qr returns Q column-major, so a rotation built from it must be
+    made contiguous before its pointer reaches a kernel.
+    """
     if tuple(Pi.shape) != (HEAD_DIM, HEAD_DIM):
         raise LeanKVError("TurboQuant: rotation must be [128, 128], got %s" % (tuple(Pi.shape),))
     return Pi.to(device=device, dtype=torch.float32).contiguous()
+
+
+def _vec(t: torch.Tensor, device, n: int | None = None, what: str = "table") -> torch.Tensor:
+    v = t.to(device=device, dtype=torch.float32).contiguous()
+    if n is not None and v.numel() != n:
+        raise LeanKVError("TurboQuant: %s must have %d entries, got %d" % (what, n, v.numel()))
+    return v
 
 
 def tq_quantize(x: torch.Tensor, Pi: torch.Tensor, bounds: torch.Tensor, bits: int):
@@ -210,11 +222,19 @@ def tq_cache_append(k_new, v_new, k_hot, v_hot, k_codes, k_norms, v_codes, v_nor
         raise LeanKVError("tq_cache_append: buffer shapes disagree with %d rows" % R)
     if pos_dev.dtype != torch.int32:
         raise LeanKVError("tq_cache_append: pos must be an int32 device tensor")
+    for t, nm in ((k_norms, "k_norms"), (v_norms, "v_norms")):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != R * cap:
+            raise LeanKVError("tq_cache_append: %s must be contiguous float32 [R, cap]" % nm)
+    if not (k_codes.is_contiguous() and v_codes.is_contiguous()) or v_codes.shape != k_codes.shape:
+        raise LeanKVError("tq_cache_append: code stores must be contiguous and alike")
+    dev = k_new.device
+    PiK, PiV = _pi(PiK, dev), _pi(PiV, dev)
+    bounds = _vec(bounds, dev, (1 << bits) - 1, "decision boundaries")
     check(
         _lib_handle().lkv_tq_cache_append(ptr(k_new), ptr(v_new), ptr(k_hot), ptr(v_hot), ptr(k_codes),
                                           ptr(k_norms), ptr(v_codes), ptr(v_norms), ptr(PiK), ptr(PiV),
                                           ptr(bounds), int(bits), ptr(pos_dev), R, hot_cap, cap,
-                                          stream_handle(k_new.device)),
+                                          stream_handle(dev)),
         "lkv_tq_cache_append",
     )
 
@@ -238,6 +258,19 @@ def tq_decode_attn_out(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK,
     hot_cap = k_hot.shape[2]
     if out.shape != q.shape or out.dtype != torch.float16 or not out.is_contiguous():
         raise LeanKVError("tq_decode_attn: out must be contiguous float16 like q")
+    for t, nm in ((k_codes, "k_codes"), (v_codes, "v_codes"), (k_norms, "k_norms"), (v_norms, "v_norms"),
+                  (k_hot, "k_hot"), (v_hot, "v_hot")):
+        if not t.is_contiguous():
+            raise LeanKVError("tq_decode_attn: %s must be contiguous" % nm)
+    if k_norms.dtype != torch.float32 or v_norms.dtype != torch.float32:
+        raise LeanKVError("tq_decode_attn: norms must be float32")
+    if k_hot.dtype != torch.float16 or v_hot.dtype != torch.float16:
+        raise LeanKVError("tq_decode_attn: hot window must be float16")
+    if seq_len_dev.dtype != torch.int32:
+        raise LeanKVError("tq_decode_attn: seq_len must be an int32 device tensor")
+    dev = q.device
+    PiK, PiV = _pi(PiK, dev), _pi(PiV, dev)
+    centroids = _vec(centroids, dev, 1 << bits, "centroids")
     lib = _lib_handle()
     nbytes = lib.lkv_tq_decode_attn_workspace_bytes(B, Hq, Hkv, max_len)
     if workspace is None:

@@ -22,7 +22,8 @@ def generate_rotation_matrix(d: int, device=None, dtype: torch.dtype = torch.flo
     G = torch.randn(d, d, generator=gen, dtype=torch.float32)
     Q, R = torch.linalg.qr(G)
     Q = Q * torch.sign(torch.diag(R)).unsqueeze(0)
-    return Q.to(device=device, dtype=dtype)
+    # LAPACK hands Q back column-major; the kernels take row-major pointers.
+    return Q.to(device=device, dtype=dtype).contiguous()
 
 
 def generate_qjl_matrix(d: int, device=None, dtype: torch.dtype = torch.float32, seed: int = 12345) -> torch.Tensor:

@@ -1,0 +1,339 @@
+"""GPU parity tests: HIP kernels (through the C ABI) vs the CPU oracle.
+
+Tolerances (stated by the north star): GEMV / attention outputs within 1e-2
+relative (fp16 storage, fp32 accumulate) -- measured as ||a - r|| / ||r|| and
+max|a - r| / max|r|; quantized codes and packed bytes bit-exact, except that a
+coordinate whose fp64 rotated value lies within TIE of a decision boundary may
+round either way (two fp32 summation orders of the 128-term rotation differ by
+a few ulp); such flips are counted and must stay rare.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import teal as ot
+from oracle import turboquant as oq
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-2
+TIE = 2e-6
+
+
+def _seeded_gemv(N, Z, seed=0, q=0.4):
+    g = torch.Generator().manual_seed(seed)
+    W = (torch.randn(N, Z, generator=g) * 0.02).to(torch.float16)
+    lap = torch.distributions.Laplace(0.0, 0.05)
+    torch.manual_seed(seed)
+    x = lap.sample((Z,)).to(torch.float16)
+    k = int(q * Z)
+    t = torch.kthvalue(x.float().abs(), k).values.item() if k > 0 else 0.0
+    return W, x, t
+
+
+def _gemv(x, W, t, dev):
+    from leankv_amd import kernels
+
+    wc = W.to(dev).t().contiguous().t()
+    return kernels.sparse_gemv(x.to(dev), wc, t).cpu()
+
+
+# ----------------------------------------------------------------- TEAL GEMV
+def test_sparse_gemv_config1(cuda):
+    """W[4096, 14336] ~N(0,.02), x ~Laplace(0,.05), t = 40% quantile."""
+    W, x, t = _seeded_gemv(4096, 14336)
+    y = _gemv(x, W, t, cuda)
+    ref = ot.sparse_gemv(x.numpy(), W.numpy(), t)
+    assert ot.rel_err(y.numpy(), ref) < 1e-3
+    assert ot.max_rel_err(y.numpy(), ref) < RTOL
+    # exactly the intended sparsity: 40% of activations dropped
+    # at least the intended 40% dropped (fp16 ties at the threshold drop more)
+    assert int((x.float().abs() <= t).sum()) >= int(0.4 * 14336)
+
+
+@pytest.mark.parametrize("N,Z,q", [(8, 1, 0.0), (24, 1000, 0.5), (1032, 333, 0.3), (4096, 4096, 0.4),
+                                   (1024, 4096, 0.4), (14336, 4096, 0.4), (520, 70000, 0.9), (2048, 257, 0.0)])
+def test_sparse_gemv_shapes(cuda, N, Z, q):
+    W, x, t = _seeded_gemv(N, Z, seed=N + Z, q=q)
+    y = _gemv(x, W, t, cuda)
+    ref = ot.sparse_gemv(x.numpy(), W.numpy(), t)
+    assert ot.rel_err(y.numpy(), ref) < 1e-3
+    assert ot.max_rel_err(y.numpy(), ref) < RTOL
+
+
+def test_sparse_gemv_all_dropped_and_all_kept(cuda):
+    W, x, _ = _seeded_gemv(1024, 4096, seed=5)
+    y0 = _gemv(x, W, 1e4, cuda)
+    assert torch.count_nonzero(y0) == 0
+    yd = _gemv(x, W, -1.0, cuda)  # every row kept: dense matvec
+    ref = W.double() @ x.double()
+    assert ot.rel_err(yd.numpy(), ref.numpy()) < 1e-3
+
+
+def test_sparse_gemv_deterministic_and_reusable_workspace(cuda):
+    W, x, t = _seeded_gemv(4096, 14336, seed=9)
+    a = _gemv(x, W, t, cuda)
+    W2, x2, t2 = _seeded_gemv(1024, 4096, seed=10)
+    _gemv(x2, W2, t2, cuda)  # a different shape in between reuses the workspace
+    b = _gemv(x, W, t, cuda)
+    assert torch.equal(a, b)
+
+
+def test_gateup_swiglu_config2(cuda):
+    """x[4096] ~N(0,1) at 40%, Wg/Wu [14336, 4096], then down at 40% of |h|."""
+    from leankv_amd import kernels
+
+    g = torch.Generator().manual_seed(0)
+    Wg = (torch.randn(14336, 4096, generator=g) * 0.02).half()
+    Wu = (torch.randn(14336, 4096, generator=g) * 0.02).half()
+    Wd = (torch.randn(4096, 14336, generator=g) * 0.02).half()
+    x = torch.randn(4096, generator=g).half()
+    tx = ot.threshold_for_sparsity(x.float(), 0.4)
+    h = kernels.sparse_gateup_swiglu(x.to(cuda), Wg.to(cuda).t().contiguous().t(),
+                                     Wu.to(cuda).t().contiguous().t(), tx, tx).cpu()
+    href = ot.gateup_swiglu(x.numpy(), Wg.numpy(), Wu.numpy(), tx, tx)
+    assert ot.rel_err(h.numpy(), href) < 2e-3
+    assert ot.max_rel_err(h.numpy(), href) < RTOL
+    th = ot.threshold_for_sparsity(torch.from_numpy(href.astype(np.float32)), 0.4)
+    y = kernels.sparse_gemv(torch.from_numpy(href).to(cuda), Wd.to(cuda).t().contiguous().t(), th).cpu()
+    yref = ot.sparse_gemv(href, Wd.numpy(), th)
+    assert ot.rel_err(y.numpy(), yref) < 1e-3
+
+
+def test_gateup_distinct_thresholds(cuda):
+    from leankv_amd import kernels
+
+    g = torch.Generator().manual_seed(1)
+    Wg = (torch.randn(1024, 512, generator=g) * 0.05).half()
+    Wu = (torch.randn(1024, 512, generator=g) * 0.05).half()
+    x = torch.randn(512, generator=g).half()
+    h = kernels.sparse_gateup_swiglu(x.to(cuda), Wg.to(cuda).t().contiguous().t(),
+                                     Wu.to(cuda).t().contiguous().t(), 0.3, 0.9).cpu()
+    href = ot.gateup_swiglu(x.numpy(), Wg.numpy(), Wu.numpy(), 0.3, 0.9)
+    assert ot.max_rel_err(h.numpy(), href) < RTOL
+
+
+# ----------------------------------------------------------------- TurboQuant
+def _kv(shape, seed, outliers=(0, 31, 64, 127)):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*shape, generator=g)
+    x[..., list(outliers)] *= 10
+    return x.half()
+
+
+def _codes_match(p_gpu, p_ref, y64, bounds, bits):
+    """Bit-exact codes except coordinates within TIE of a boundary; returns #flips."""
+    cg = oq.unpack_indices(p_gpu, bits, 128)
+    cr = oq.unpack_indices(p_ref, bits, 128)
+    diff = cg != cr
+    if not diff.any():
+        return 0
+    inner = bounds[1:-1].double().numpy()
+    near = (np.abs(y64[..., None] - inner) < TIE).any(-1)
+    assert not (diff & ~near).any(), "code mismatch away from any boundary"
+    assert (np.abs(cg.astype(int) - cr.astype(int))[diff] == 1).all()
+    return int(diff.sum())
+
+
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.float16])
+def test_tq_quantize_config3(cuda, in_dtype):
+    """K,V [8, 4096, 128] ~N(0,1), channels {0,31,64,127} x10, Pi seeds 42/43."""
+    from leankv_amd import kernels
+
+    c, b = oq.codebook_tensors(3)
+    flips = 0
+    for seed, pseed in ((0, 42), (1, 43)):
+        x = _kv((8, 4096, 128), seed).to(in_dtype)
+        Pi = oq.rotation_matrix(128, pseed)
+        p_ref, n_ref, _ = oq.quantize(x, Pi, b, 3)
+        p, n = kernels.tq_quantize(x.to(cuda), Pi.to(cuda), b[1:-1].to(cuda), 3)
+        p, n = p.cpu().numpy(), n.cpu()
+        assert p.shape == (8, 4096, 64) and n.dtype == in_dtype
+        torch.testing.assert_close(n.float(), n_ref.float(), rtol=2e-6 if in_dtype == torch.float32 else 1e-3,
+                                   atol=0)
+        y64 = oq.rotated_fp64(x, Pi)
+        if in_dtype == torch.float16:
+            # An fp16 norm is the rounding of an fp32 sum whose order differs between
+            # torch's CPU reduction and the kernel; where the two round to different
+            # fp16 values (a norm tie, ~1e-4 of rows) the whole unit vector differs by
+            # one fp16 ulp.  Those rows are excluded and counted.
+            same = (n == n_ref).numpy()
+            assert (~same).sum() <= 1e-3 * same.size, (~same).sum()
+            p, p_ref, y64 = p[same], p_ref[same], y64[same]
+        flips += _codes_match(p, p_ref, y64, b, 3)
+    assert flips <= 64, flips  # out of 8.4M coordinates
+    print("near-tie code flips:", flips)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4])
+def test_tq_quantize_other_bits(cuda, bits):
+    from leankv_amd import kernels
+
+    c, b = oq.codebook_tensors(bits)
+    x = _kv((3, 77, 128), 7).float()
+    Pi = oq.rotation_matrix(128, 50)
+    p_ref, _, _ = oq.quantize(x, Pi, b, bits)
+    p, _ = kernels.tq_quantize(x.to(cuda), Pi.to(cuda), b[1:-1].to(cuda), bits)
+    _codes_match(p.cpu().numpy(), p_ref, oq.rotated_fp64(x, Pi), b, bits)
+
+
+def test_tq_quantize_zero_vector_and_ragged_rows(cuda):
+    from leankv_amd import kernels
+
+    c, b = oq.codebook_tensors(3)
+    x = torch.randn(37, 128)
+    x[5] = 0
+    Pi = oq.rotation_matrix(128, 42)
+    p, n = kernels.tq_quantize(x.to(cuda), Pi.to(cuda), b[1:-1].to(cuda), 3)
+    p_ref, _, _ = oq.quantize(x, Pi, b, 3)
+    _codes_match(p.cpu().numpy(), p_ref, oq.rotated_fp64(x, Pi), b, 3)
+    assert n[5].item() == 0
+    # y = 0 -> code = #(boundaries < 0) = 3 in every coordinate
+    assert (oq.unpack_indices(p.cpu().numpy()[5], 3, 128) == 3).all()
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_tq_quantize_rotated_bit_exact(cuda, bits):
+    from leankv_amd import kernels
+
+    c, b = oq.codebook_tensors(bits)
+    g = torch.Generator().manual_seed(bits)
+    y = torch.randn(4099, 128, generator=g) * 0.09
+    y[0, : (1 << bits) - 1] = b[1:-1]  # exactly on the boundaries -> lower code
+    p = kernels.tq_quantize_rotated(y.to(cuda), b[1:-1].to(cuda), bits).cpu().numpy()
+    idx = torch.searchsorted(b[1:-1].contiguous(), y)
+    assert np.array_equal(p, oq.pack_indices(idx.numpy(), bits))
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_tq_dequantize(cuda, bits):
+    from leankv_amd import kernels
+
+    c, b = oq.codebook_tensors(bits)
+    x = _kv((4, 300, 128), 3).float()
+    Pi = oq.rotation_matrix(128, 44)
+    p_ref, n_ref, _ = oq.quantize(x, Pi, b, bits)
+    ref = oq.dequantize(p_ref, n_ref, Pi, c, bits)
+    out = kernels.tq_dequantize(torch.from_numpy(p_ref).to(cuda), n_ref.to(cuda), Pi.to(cuda), c.to(cuda), bits,
+                                out_dtype=torch.float32).cpu()
+    torch.testing.assert_close(out, ref, rtol=1e-5, atol=1e-5)
+    out16 = kernels.tq_dequantize(torch.from_numpy(p_ref).to(cuda), n_ref.to(cuda), Pi.to(cuda), c.to(cuda), bits,
+                                  out_dtype=torch.float16).cpu()
+    torch.testing.assert_close(out16, ref.half(), rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_tq_rotate(cuda, transpose):
+    from leankv_amd import kernels
+
+    x = torch.randn(333, 128)
+    Pi = oq.rotation_matrix(128, 45)
+    ref = x.double() @ (Pi.double() if transpose else Pi.double().T)
+    y = kernels.tq_rotate(x.to(cuda), Pi.to(cuda), transpose).cpu()
+    torch.testing.assert_close(y.double(), ref, rtol=1e-5, atol=1e-5)
+    yh = kernels.tq_rotate(x.half().to(cuda), Pi.to(cuda), transpose).cpu()
+    torch.testing.assert_close(yh.double(), x.half().double() @ (Pi.double() if transpose else Pi.double().T),
+                               rtol=1e-5, atol=1e-5)
+
+
+def test_tq_cache_append_matches_reference_cache(cuda):
+    """Static ring append == TurboQuantCache.update hot/cold semantics (cache.py:84-159)."""
+    from leankv_amd import kernels
+
+    c, b = oq.codebook_tensors(3)
+    PiK, PiV = oq.rotation_matrix(128, 42), oq.rotation_matrix(128, 43)
+    B, H, hot, cap, steps = 2, 3, 8, 64, 30
+    ref = oq.CacheRef(PiK, PiV, c, b, 3, hot=hot)
+    kh = torch.zeros(B, H, hot, 128, dtype=torch.float16, device=cuda)
+    vh = torch.zeros_like(kh)
+    kc = torch.zeros(B, H, cap, 64, dtype=torch.uint8, device=cuda)
+    vc = torch.zeros_like(kc)
+    kn = torch.zeros(B, H, cap, device=cuda)
+    vn = torch.zeros_like(kn)
+    pos = torch.zeros(1, dtype=torch.int32, device=cuda)
+    PiKd, PiVd, bd = PiK.to(cuda), PiV.to(cuda), b[1:-1].contiguous().to(cuda)
+    g = torch.Generator().manual_seed(0)
+    ks, vs = [], []
+    for s in range(steps):
+        k = torch.randn(B, H, 1, 128, generator=g).half()
+        v = torch.randn(B, H, 1, 128, generator=g).half()
+        ks.append(k)
+        vs.append(v)
+        ref.update(k, v)
+        kernels.tq_cache_append(k.to(cuda), v.to(cuda), kh, vh, kc, kn, vc, vn, PiKd, PiVd, bd, 3, pos)
+        pos += 1
+    ncold = steps - hot
+    pk, nk, pv, nv = ref.cold_arrays()
+    assert pk.shape[2] == ncold
+    allk, allv = torch.cat(ks, dim=2), torch.cat(vs, dim=2)
+    for got, want, nrm_g, nrm_w, Pi, src in ((kc, pk, kn, nk, PiK, allk), (vc, pv, vn, nv, PiV, allv)):
+        y64 = oq.rotated_fp64(src[:, :, :ncold].float(), Pi)
+        _codes_match(got[:, :, :ncold].cpu().numpy(), want, y64, b, 3)
+        torch.testing.assert_close(nrm_g[:, :, :ncold].cpu(), nrm_w.float(), rtol=2e-6, atol=0)
+    # rows beyond the cold length were never written
+    assert int(kc[:, :, ncold:].count_nonzero()) == 0
+    # hot ring holds the last `hot` tokens at slot p % hot
+    hk = kh.cpu()
+    for j in range(hot):
+        p = steps - hot + j
+        assert torch.equal(hk[:, :, p % hot], ref.hot_k[:, :, j])
+
+
+# ----------------------------------------------------------------- attention
+def _attn_case(B, Hq, Hkv, L, hot, seed, dev, bits=3):
+    """Build a cache of L tokens (cold = L - hot) with the oracle, run the HIP kernel."""
+    from leankv_amd import kernels
+
+    c, b = oq.codebook_tensors(bits)
+    PiK, PiV = oq.rotation_matrix(128, 42), oq.rotation_matrix(128, 43)
+    cold = max(0, L - hot)
+    hot_len = L - cold
+    K = _kv((B, Hkv, L, 128), seed)
+    V = _kv((B, Hkv, L, 128), seed + 1000)
+    q = torch.randn(B, Hq, 128, generator=torch.Generator().manual_seed(seed + 7)).half()
+    cap = max(cold, 1)
+    kc = torch.zeros(B, Hkv, cap, 64, dtype=torch.uint8)
+    vc = torch.zeros_like(kc)
+    kn = torch.zeros(B, Hkv, cap)
+    vn = torch.zeros_like(kn)
+    Kref, Vref = K.clone(), V.clone()
+    if cold:
+        pk, nk, _ = oq.quantize(K[:, :, :cold].float(), PiK, b, bits)
+        pv, nv, _ = oq.quantize(V[:, :, :cold].float(), PiV, b, bits)
+        kc[:, :, :cold] = torch.from_numpy(pk)
+        vc[:, :, :cold] = torch.from_numpy(pv)
+        kn[:, :, :cold] = nk
+        vn[:, :, :cold] = nv
+        Kref[:, :, :cold] = oq.dequantize(pk, nk, PiK, c, bits).half()
+        Vref[:, :, :cold] = oq.dequantize(pv, nv, PiV, c, bits).half()
+    kh = torch.zeros(B, Hkv, hot, 128, dtype=torch.float16)
+    vh = torch.zeros_like(kh)
+    for j in range(hot_len):
+        p = cold + j
+        kh[:, :, p % hot] = K[:, :, p]
+        vh[:, :, p % hot] = V[:, :, p]
+    seq = torch.tensor([L], dtype=torch.int32, device=dev)
+    out = kernels.tq_decode_attn(q.to(dev), kc.to(dev), kn.to(dev), vc.to(dev), vn.to(dev), kh.to(dev), vh.to(dev),
+                                 PiK.to(dev), PiV.to(dev), c.to(dev), bits, seq, L).cpu()
+    ref = oq.decode_attention(q.unsqueeze(2), Kref, Vref).squeeze(2)
+    return out, ref
+
+
+@pytest.mark.parametrize("B", [1, 4, 16])
+def test_decode_attn_config4(cuda, B):
+    """32 q heads over 8 kv heads, ctx 4096 cold + 64-token fp16 hot tail."""
+    out, ref = _attn_case(B, 32, 8, 4096 + 64, 64, seed=B, dev=cuda)
+    assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
+    assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,hot", [(1, 32, 8, 1, 64), (1, 32, 8, 64, 64), (1, 32, 8, 65, 64),
+                                            (2, 8, 8, 1000, 64), (1, 16, 2, 333, 16), (3, 32, 4, 4096, 64),
+                                            (1, 64, 4, 2048, 64)])
+def test_decode_attn_edges(cuda, B, Hq, Hkv, L, hot):
+    out, ref = _attn_case(B, Hq, Hkv, L, hot, seed=L, dev=cuda)
+    assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
+    assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
