@@ -4,6 +4,12 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
 Workloads:
+  decode  config 5 (default): random-init fp16 Mistral-7B-v0.3-shaped decoder, 4096-token
+          random prompt, per-projection TEAL sparsity ~U[0.3,0.5] (thresholds from a seeded
+          calibration pass), 3-bit TurboQuant KV (64-token fp16 window), greedy B=1 decode of
+          warmup+steps = 128 tokens through the graph-captured LeanKV engine; the dense fp16
+          engine (fp16 KV, torch F.linear + SDPA, also graph-captured) runs the same prompt.
+          value = decode tok/s of the LeanKV engine (prefill excluded).
   gemv    config 1: TEAL sparse GEMV W[4096,14336], x ~Laplace(0,.05), 40 % sparse
   mlp     config 2: fused gate/up SwiGLU [14336,4096] + sparse down [4096,14336]
   quant   config 3: TurboQuant 3-bit quantize of K,V [8,4096,128] (fp32 MFMA rotation)
@@ -32,10 +38,14 @@ MFMA_F32_PEAK_TFLOPS = 157.3
 def _parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="gemv", choices=["gemv", "mlp", "quant", "attn"])
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "mlp", "quant", "attn"])
+    ap.add_argument("--prompt", type=int, default=4096)
+    ap.add_argument("--layers", type=int, default=32, help="decoder layers (config 5 uses 32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-dense", action="store_true", help="skip the dense fp16 comparison run")
+    ap.add_argument("--no-roofline", action="store_true", help="skip the config-1 GEMV roofline measurement")
     ap.add_argument("--sets", type=int, default=5, help="independent buffer sets rotated per step")
     return ap.parse_args()
 
@@ -139,6 +149,111 @@ def cpu_gemv(torch, s, N, Z):
             "ms_per_call": round(dt * 1e3, 3)}
 
 
+def _fill_gemv_defaults(args):
+    if args.steps is None:
+        args.steps = 200
+    if args.warmup is None:
+        args.warmup = 20
+
+
+# ------------------------------------------------------------------ config 5
+def bench_decode(args, torch):
+    from leankv_amd.engine import DenseEngine, LeanKVEngine, random_mistral
+    from leankv_amd.teal.calibrate import calibrate_thresholds, uniform_random_sparsity
+    from leankv_amd.teal.patching import apply_teal
+    from leankv_amd.turboquant.attention import use_on
+    from leankv_amd.turboquant.cache import TurboQuantCache
+    from transformers import DynamicCache
+
+    if args.steps is None:
+        args.steps = 120
+    if args.warmup is None:
+        args.warmup = 8
+    dev = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    model = random_mistral(device=dev, seed=0, num_hidden_layers=args.layers)
+    _log("model built in %.1fs" % (time.perf_counter() - t0))
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, model.config.vocab_size, (1, args.prompt), generator=g).to(dev)
+    calib = [torch.randint(0, model.config.vocab_size, (1, 512), generator=g)]
+    max_len = args.prompt + args.warmup + args.steps + 2
+
+    def timed_decode(eng):
+        with torch.no_grad():
+            eng.step()
+            eng.capture()
+            for _ in range(args.warmup - 1):
+                eng.step()
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            toks = []
+            for _ in range(args.steps):
+                eng.step()
+                toks.append(eng.tok)
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t
+        return dt, [int(x) for x in torch.cat(toks).tolist()]
+
+    # ---- dense fp16 baseline (weights still row-major)
+    dense_tps = None
+    if not args.skip_dense:
+      with torch.no_grad():
+        dc = DynamicCache(config=model.config)
+        out = model(prompt, past_key_values=dc, use_cache=True)
+        first_dense = torch.argmax(out.logits[0, -1])
+        dense = DenseEngine(model, max_len)
+        dense.start(first_dense, dense.load_cache(dc))
+        del dc, out
+      dt_dense, _ = timed_decode(dense)
+      dense_tps = args.steps / dt_dense
+      _log("dense fp16: %.1f tok/s" % dense_tps)
+      del dense
+      torch.cuda.empty_cache()
+
+    # ---- LeanKV: TEAL thresholds from a calibration pass, HIP kernels, TurboQuant KV
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        th = calibrate_thresholds(model, calib, uniform_random_sparsity(0.3, 0.5, seed=0))
+    apply_teal(model, thresholds=th, use_triton=True)
+    cache = TurboQuantCache(bits=3, head_dim=128, num_layers=model.config.num_hidden_layers, device=dev,
+                            max_seq_len=max_len)
+    use_on(model)
+    with torch.no_grad():
+        out = model(prompt, past_key_values=cache, use_cache=True)
+        first = torch.argmax(out.logits[0, -1])
+        del out
+    _log("calibrate + patch + TurboQuant prefill in %.1fs" % (time.perf_counter() - t0))
+    eng = LeanKVEngine(model, cache, max_len)
+    eng.start(first, args.prompt)
+    dt, toks = timed_decode(eng)
+    tps = args.steps / dt
+    _log("leankv: %.1f tok/s" % tps)
+    res = {
+        "metric": "B=1 decode tok/s (Mistral-7B shape, 40% sparse, 3-bit KV)",
+        "value": round(tps, 2),
+        "unit": "tok/s",
+        "ms_per_step": round(dt * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "dtype": "f16 (fp32 accumulate)",
+        "data": "synthetic: random-init weights N(0,0.02), random 4096-token prompt (seeded)",
+        "config": {"workload": "config5_mistral7b_decode", "layers": model.config.num_hidden_layers,
+                   "hidden": model.config.hidden_size, "ffn": model.config.intermediate_size, "heads": "32/8",
+                   "vocab": model.config.vocab_size, "prompt": args.prompt, "new_tokens": args.warmup + args.steps,
+                   "batch": 1, "teal_sparsity": "U[0.3,0.5] per projection, mean 0.4", "kv_bits": 3,
+                   "hot_window": 64},
+        "dense_fp16": {"value": round(dense_tps, 2) if dense_tps else None, "unit": "tok/s",
+                       "what": "same model, fp16 KV, torch F.linear + SDPA, graph-captured"},
+        "speedup_vs_dense": round(tps / dense_tps, 3) if dense_tps else None,
+    }
+    del eng, cache, model
+    torch.cuda.empty_cache()
+    return res
+
+
+def _log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -150,8 +265,20 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
-    fn = {"gemv": bench_gemv}[args.workload]
-    res = fn(args, torch)
+    if args.workload == "decode":
+        res = bench_decode(args, torch)
+        # roofline block: the dominant kernel (TEAL sparse GEMV, config 1 shape)
+        if not args.no_roofline:
+            gargs = argparse.Namespace(**vars(args))
+            gargs.steps, gargs.warmup = 200, 20
+            g = bench_gemv(gargs, torch)
+            res["roofline"] = g["roofline"]
+            if "cpu_baseline" in g:
+                res["cpu_baseline_gemv"] = g["cpu_baseline"]
+    else:
+        _fill_gemv_defaults(args)
+        fn = {"gemv": bench_gemv}[args.workload]
+        res = fn(args, torch)
     out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"), "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup}
     out.update(res)

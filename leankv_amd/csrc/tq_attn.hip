@@ -10,22 +10,26 @@
 // so the query is rotated once, cold scores and the cold value sum stay in the
 // rotated domain, and PiV is applied once per (batch, kv head) at the end.
 //
-// Kernel layout (grid = (splits + 1) x kv_heads x batch, 4 waves per block):
-//   * blocks 0..splits-1 each own a contiguous range of cold tokens; each wave
-//     walks 32-token blocks of it;
-//   * scores: v_mfma_f32_16x16x32_f16 with A = rotated query rows (the G heads
-//     sharing this kv head, zero padded to 16) and B = 16 tokens x 32 dims of
-//     centroid values.  A lane loads 16 contiguous code bytes of one token and
-//     unpacks them in registers through a 256-entry LDS table that maps one
-//     code byte to the fp16 pair (c[lo nibble], c[hi nibble]);
-//   * online softmax in the exp2 domain per head;
-//   * values: the same MFMA with A = p * n_t (fp16, via a 1 KB LDS tile) and
-//     B = 32 tokens x 16 dims of centroid values; a lane loads one code dword
-//     (8 dims) of 8 tokens and transposes the fp16 pairs with v_perm;
-//   * block (splits) handles the fp16 hot window on plain fp32 VALU;
-//   * every block writes (m, l, acc) per head; the last block of a
-//     (batch, kv head) -- agent-scope ticket -- merges them, applies PiV to the
-//     cold sum, adds the hot sum, normalises and writes fp16.
+// Three launches (all on the caller's stream, no inter-block waits):
+//   1. q_rot = q @ PiK^T on fp32 MFMA (tq_quant.hip's rotate kernel);
+//   2. split kernel, grid (splits + 1) x kv_heads x batch, 4 waves per block:
+//      * blocks 0..splits-1 own a contiguous range of cold tokens; each wave
+//        walks 32-token blocks of it, prefetching the next block's codes and
+//        norms while it computes the current one;
+//      * scores: v_mfma_f32_16x16x32_f16 with A = rotated query rows (the G
+//        heads sharing this kv head, zero padded to 16) and B = 16 tokens x 32
+//        dims of centroid values.  A lane loads 16 contiguous code bytes of
+//        one token and unpacks them in registers through a 256-entry LDS
+//        table that maps one code byte to the fp16 pair (c[lo], c[hi]);
+//      * online softmax in the exp2 domain per head;
+//      * values: the same MFMA with A = p * n_t (fp16, via a 1 KB LDS tile)
+//        and B = 32 tokens x 16 dims of centroid values; a lane loads one code
+//        dword (8 dims) of 8 tokens and transposes the fp16 pairs in registers;
+//      * block `splits` handles the fp16 hot window from LDS on fp32 VALU;
+//      * every block writes (m, l, acc[G][128]) per head to the workspace;
+//   3. combine kernel, one block per (batch, kv head): merges the records in
+//      split order (loads batched 16 deep), applies PiV to the cold sum, adds
+//      the hot sum, normalises, writes fp16.
 #include "common.h"
 
 namespace lkv {
@@ -34,16 +38,15 @@ namespace {
 constexpr int kD = 128;
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kBlk = 32;     // tokens per wave step
-constexpr int kRowB = 64;    // code bytes per token (4-bit nibbles, dim 128)
+constexpr int kBlk = 32;    // tokens per wave step
+constexpr int kRowB = 64;   // code bytes per token (4-bit nibbles, dim 128)
+constexpr int kHotMax = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ half8 as_half8(const u32x4& v) {
-  return __builtin_bit_cast(half8, v);
-}
+__device__ __forceinline__ half8 as_half8(const u32x4& v) { return __builtin_bit_cast(half8, v); }
 
 __device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a), as_half8(b), c, 0, 0, 0);
@@ -66,8 +69,8 @@ __device__ __forceinline__ float group16_sum(float v) {
 }
 
 struct AttnParams {
-  const float* qrot;        // [B, Hq, 128] fp32, already multiplied by scale*log2(e)
-  const uint16_t* q;        // [B, Hq, 128] fp16 (hot window uses the unrotated query)
+  const float* qrot;        // [B, Hq, 128] fp32 = q @ PiK^T
+  const uint16_t* q;        // [B, Hq, 128] fp16 (the hot window uses the unrotated query)
   const uint8_t* k_codes;   // [B, Hkv, cap, 64]
   const float* k_norms;     // [B, Hkv, cap]
   const uint8_t* v_codes;
@@ -78,21 +81,48 @@ struct AttnParams {
   const float* centroids;   // [2^bits]
   const int32_t* seq_len;
   float* partials;          // [B, Hkv, nsplit + 1, rec]
-  unsigned* tickets;        // [B, Hkv]
   uint16_t* out;            // [B, Hq, 128]
-  float scale_log2;         // scale * log2(e) for the hot window
+  float scale_log2;         // scale * log2(e)
   int max_len, Hq, Hkv, G, cap, hot_cap, nsplit, split_tokens, ncent;
 };
 
 __device__ __forceinline__ int rec_floats(int G) { return G * (2 + kD); }
 
+// Code bytes / norms of the two 16-token score tiles and the 8 value tokens
+// one lane needs for a 32-token block starting at t0.
+struct BlockRegs {
+  u32x4 kraw[2];
+  float knorm[2];
+  uint32_t vdw[8];
+  float vnorm[2];
+};
+
+__device__ __forceinline__ void load_block(BlockRegs& R, int t0, int t_end, int lane, const uint8_t* kc,
+                                           const float* kn, const uint8_t* vc, const float* vn) {
+  const int g = lane >> 4, w = lane & 15;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int tok = t0 + 16 * tt + (lane & 15);
+    const bool ok = tok < t_end;
+    R.kraw[tt] = ok ? *reinterpret_cast<const u32x4*>(kc + static_cast<size_t>(tok) * kRowB + 16 * g)
+                    : u32x4{0u, 0u, 0u, 0u};
+    R.knorm[tt] = ok ? kn[tok] : 0.f;
+    R.vnorm[tt] = ok ? vn[tok] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int tok = t0 + 8 * g + i;
+    R.vdw[i] = tok < t_end ? *reinterpret_cast<const uint32_t*>(vc + static_cast<size_t>(tok) * kRowB + 4 * w) : 0u;
+  }
+}
+
 template <int GMAX>
-__global__ __launch_bounds__(kThreads) void tq_decode_attn_kernel(AttnParams P) {
+__global__ __launch_bounds__(kThreads) void tq_attn_split_kernel(AttnParams P) {
   __shared__ uint32_t s_lut[256];
   __shared__ __align__(16) uint16_t s_p[kWaves][16][kBlk];  // p * n_t, fp16, per wave
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
   __shared__ __align__(16) float s_o[kWaves][GMAX][kD];
-  __shared__ int s_last;
+  __shared__ __align__(16) uint16_t s_hot[2][kHotMax][kD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -106,333 +136,345 @@ __global__ __launch_bounds__(kThreads) void tq_decode_attn_kernel(AttnParams P) 
     // ------------------------------------------------------------ cold split
     const int t_begin = split * P.split_tokens;
     const int t_end = min(cold_len, t_begin + P.split_tokens);
-    if (t_begin < t_end) {
-      {
-        const int lo = tid & 15, hi = tid >> 4;
-        const int cmax = P.ncent - 1;
-        s_lut[tid] = pack2h(P.centroids[min(lo, cmax)], P.centroids[min(hi, cmax)]);
+    if (t_begin >= t_end) {
+      if (tid < G) {
+        rec[tid] = -INFINITY;
+        rec[G + tid] = 0.f;
       }
-      // A operand of the score MFMA: rotated query, head h = lane%16, dims
-      // 32*(lane/16) + 8*kb + i for k-block kb.
-      const int h = lane & 15, g = lane >> 4;
-      u32x4 qa[4];
+      return;
+    }
+    {
+      const int lo = tid & 15, hi = tid >> 4;
+      const int cmax = P.ncent - 1;
+      s_lut[tid] = pack2h(P.centroids[min(lo, cmax)], P.centroids[min(hi, cmax)]);
+    }
+    // A operand of the score MFMA: rotated query x scale*log2(e), head
+    // h = lane%16, dims 32*(lane/16) + 8*kb + i for k-block kb.
+    const int h = lane & 15, g = lane >> 4;
+    u32x4 qa[4];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        if (h < G) {
-          const float* src = P.qrot + (static_cast<size_t>(b) * P.Hq + kvh * G + h) * kD + 32 * g + 8 * kb;
-          const float4 f0 = reinterpret_cast<const float4*>(src)[0];
-          const float4 f1 = reinterpret_cast<const float4*>(src)[1];
-          const float sl = P.scale_log2;
-          qa[kb] = u32x4{pack2h(f0.x * sl, f0.y * sl), pack2h(f0.z * sl, f0.w * sl),
-                         pack2h(f1.x * sl, f1.y * sl), pack2h(f1.z * sl, f1.w * sl)};
-        } else {
-          qa[kb] = u32x4{0u, 0u, 0u, 0u};
-        }
+    for (int kb = 0; kb < 4; ++kb) {
+      if (h < G) {
+        const float* src = P.qrot + (static_cast<size_t>(b) * P.Hq + kvh * G + h) * kD + 32 * g + 8 * kb;
+        const float4 f0 = reinterpret_cast<const float4*>(src)[0];
+        const float4 f1 = reinterpret_cast<const float4*>(src)[1];
+        const float sl = P.scale_log2;
+        qa[kb] = u32x4{pack2h(f0.x * sl, f0.y * sl), pack2h(f0.z * sl, f0.w * sl), pack2h(f1.x * sl, f1.y * sl),
+                       pack2h(f1.z * sl, f1.w * sl)};
+      } else {
+        qa[kb] = u32x4{0u, 0u, 0u, 0u};
       }
-      __syncthreads();  // LUT ready
+    }
+    const uint8_t* kc = P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB;
+    const uint8_t* vc = P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB;
+    const float* kn = P.k_norms + bh * static_cast<size_t>(P.cap);
+    const float* vn = P.v_norms + bh * static_cast<size_t>(P.cap);
 
-      const uint8_t* kc = P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB;
-      const uint8_t* vc = P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB;
-      const float* kn = P.k_norms + bh * static_cast<size_t>(P.cap);
-      const float* vn = P.v_norms + bh * static_cast<size_t>(P.cap);
+    float m[4], l[4];
+    f32x4 o[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      m[i] = -INFINITY;
+      l[i] = 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-      float m[4], l[4];
-      f32x4 o[8];
+    BlockRegs cur;
+    int t0 = t_begin + wave * kBlk;
+    if (t0 < t_end) load_block(cur, t0, t_end, lane, kc, kn, vc, vn);
+    __syncthreads();  // LUT ready
+    for (; t0 < t_end; t0 += kWaves * kBlk) {
+      const int tn = t0 + kWaves * kBlk;
+      BlockRegs nxt;
+      if (tn < t_end) load_block(nxt, tn, t_end, lane, kc, kn, vc, vn);
+      // ---- scores for tokens t0 .. t0+31 (two 16-token MFMA tiles)
+      f32x4 sc[2];
+      bool valid[2];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        valid[tt] = t0 + 16 * tt + (lane & 15) < t_end;
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const uint32_t w = cur.kraw[tt][kb];
+          const u32x4 bop = u32x4{s_lut[w & 0xffu], s_lut[(w >> 8) & 0xffu], s_lut[(w >> 16) & 0xffu], s_lut[w >> 24]};
+          acc = mfma16x16x32(qa[kb], bop, acc);
+        }
+        sc[tt] = acc;
+      }
+      // ---- online softmax (log2 domain); lane holds heads 4g+i, token lane%16
+      float p[2][4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        m[i] = -INFINITY;
-        l[i] = 0.f;
+        const float s0 = valid[0] ? sc[0][i] * cur.knorm[0] : -INFINITY;
+        const float s1 = valid[1] ? sc[1][i] * cur.knorm[1] : -INFINITY;
+        const float bmax = group16_max(fmaxf(s0, s1));
+        const float mnew = fmaxf(m[i], bmax);
+        float alpha, p0, p1;
+        if (mnew == -INFINITY) {
+          alpha = 1.f;
+          p0 = p1 = 0.f;
+        } else {
+          alpha = exp2f(m[i] - mnew);
+          p0 = valid[0] ? exp2f(s0 - mnew) : 0.f;
+          p1 = valid[1] ? exp2f(s1 - mnew) : 0.f;
+        }
+        l[i] = l[i] * alpha + group16_sum(p0 + p1);
+        m[i] = mnew;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) o[t][i] *= alpha;
+        p[0][i] = p0;
+        p[1][i] = p1;
+      }
+      // ---- p * n_t into the per-wave LDS tile [head][token]
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          s_p[wave][4 * g + i][16 * tt + (lane & 15)] = f2h(valid[tt] ? p[tt][i] * cur.vnorm[tt] : 0.f);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      // ---- P V: A = p*n (head h = lane%16, tokens 8g..8g+7), B = codes
+      u32x4 pa = u32x4{0u, 0u, 0u, 0u};
+      if (h < G) pa = *reinterpret_cast<const u32x4*>(&s_p[wave][h][8 * g]);
+      uint32_t r[8][4];  // r[token i][byte bb] = (c[dim 8w+2bb], c[dim 8w+2bb+1])
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t dw = cur.vdw[i];
+        r[i][0] = s_lut[dw & 0xffu];
+        r[i][1] = s_lut[(dw >> 8) & 0xffu];
+        r[i][2] = s_lut[(dw >> 16) & 0xffu];
+        r[i][3] = s_lut[dw >> 24];
       }
 #pragma unroll
-      for (int t = 0; t < 8; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-      for (int t0 = t_begin + wave * kBlk; t0 < t_end; t0 += kWaves * kBlk) {
-        // ---- scores for tokens t0 .. t0+31 (two 16-token MFMA tiles)
-        f32x4 sc[2];
-        float knorm[2];
-        bool valid[2];
+      for (int t = 0; t < 8; ++t) {
+        // dword pp = (token 2pp, token 2pp+1) of dim 8w + t: low halves of
+        // r[..][t/2] for even t, high halves for odd t.
+        const int bb = t >> 1;
+        u32x4 bop;
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const int tok = t0 + 16 * tt + (lane & 15);
-          valid[tt] = tok < t_end;
-          u32x4 raw = u32x4{0u, 0u, 0u, 0u};
-          knorm[tt] = 0.f;
-          if (valid[tt]) {
-            raw = *reinterpret_cast<const u32x4*>(kc + static_cast<size_t>(tok) * kRowB + 16 * g);
-            knorm[tt] = kn[tok];
-          }
-          f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb) {
-            const uint32_t w = raw[kb];
-            const u32x4 bop = u32x4{s_lut[w & 0xffu], s_lut[(w >> 8) & 0xffu], s_lut[(w >> 16) & 0xffu],
-                                    s_lut[w >> 24]};
-            acc = mfma16x16x32(qa[kb], bop, acc);
-          }
-          sc[tt] = acc;
+        for (int pp = 0; pp < 4; ++pp) {
+          const uint32_t x0 = r[2 * pp][bb], x1 = r[2 * pp + 1][bb];
+          bop[pp] = (t & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
         }
-        // ---- online softmax (log2 domain); lane holds heads 4g+i, token lane%16
-        float p[2][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float s0 = valid[0] ? sc[0][i] * knorm[0] : -INFINITY;
-          const float s1 = valid[1] ? sc[1][i] * knorm[1] : -INFINITY;
-          const float bmax = group16_max(fmaxf(s0, s1));
-          const float mnew = fmaxf(m[i], bmax);
-          float alpha, p0, p1;
-          if (mnew == -INFINITY) {
-            alpha = 1.f;
-            p0 = p1 = 0.f;
-          } else {
-            alpha = exp2f(m[i] - mnew);
-            p0 = valid[0] ? exp2f(s0 - mnew) : 0.f;
-            p1 = valid[1] ? exp2f(s1 - mnew) : 0.f;
-          }
-          l[i] = l[i] * alpha + group16_sum(p0 + p1);
-          m[i] = mnew;
-#pragma unroll
-          for (int t = 0; t < 8; ++t) o[t][i] *= alpha;
-          p[0][i] = p0;
-          p[1][i] = p1;
-        }
-        // ---- p * n_t into the per-wave LDS tile [head][token]
-        {
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt) {
-            const int tok = t0 + 16 * tt + (lane & 15);
-            const float vnorm = valid[tt] ? vn[tok] : 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int hh = 4 * g + i;
-              s_p[wave][hh][16 * tt + (lane & 15)] = f2h(valid[tt] ? p[tt][i] * vnorm : 0.f);
-            }
-          }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        // ---- P V: A = p*n (head h = lane%16, tokens 8g..8g+7), B = codes
-        u32x4 pa = u32x4{0u, 0u, 0u, 0u};
-        if (h < G) pa = *reinterpret_cast<const u32x4*>(&s_p[wave][h][8 * g]);
-        uint32_t r[8][4];  // r[token i][byte b] = (c[dim 8w+2b], c[dim 8w+2b+1])
-        {
-          const int w = lane & 15;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int tok = t0 + 8 * g + i;
-            uint32_t dw = 0;
-            if (tok < t_end) dw = *reinterpret_cast<const uint32_t*>(vc + static_cast<size_t>(tok) * kRowB + 4 * w);
-            r[i][0] = s_lut[dw & 0xffu];
-            r[i][1] = s_lut[(dw >> 8) & 0xffu];
-            r[i][2] = s_lut[(dw >> 16) & 0xffu];
-            r[i][3] = s_lut[dw >> 24];
-          }
-        }
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          // dword p = (token 2p, token 2p+1) of dim 8w + t: low halves of
-          // r[..][t/2] for even t, high halves for odd t.
-          const int bb = t >> 1;
-          u32x4 bop;
-#pragma unroll
-          for (int pp = 0; pp < 4; ++pp) {
-            const uint32_t x0 = r[2 * pp][bb], x1 = r[2 * pp + 1][bb];
-            bop[pp] = (t & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
-          }
-          o[t] = mfma16x16x32(pa, bop, o[t]);
-        }
-        __builtin_amdgcn_wave_barrier();
+        o[t] = mfma16x16x32(pa, bop, o[t]);
       }
-
-      // ---- merge the 4 waves of the block through LDS
-      if ((lane & 15) == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int hh = 4 * g + i;
-          if (hh < G) {
-            s_m[wave][hh] = m[i];
-            s_l[wave][hh] = l[i];
-          }
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < 8; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int hh = 4 * g + i;
-          if (hh < G) s_o[wave][hh][8 * (lane & 15) + t] = o[t][i];
-        }
-      __syncthreads();
-      for (int e = tid; e < G * kD; e += kThreads) {
-        const int hh = e / kD, d = e % kD;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hh]);
-        float acc = 0.f, lsum = 0.f;
-        if (M != -INFINITY) {
-#pragma unroll
-          for (int w = 0; w < kWaves; ++w) {
-            const float wt = exp2f(s_m[w][hh] - M);
-            acc += wt * s_o[w][hh][d];
-            lsum += wt * s_l[w][hh];
-          }
-        }
-        rec[2 * G + hh * kD + d] = acc;
-        if (d == 0) {
-          rec[hh] = M;
-          rec[G + hh] = lsum;
-        }
-      }
-    } else if (tid < G) {
-      rec[tid] = -INFINITY;
-      rec[G + tid] = 0.f;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      if (tn < t_end) cur = nxt;
     }
-  } else {
-    // ------------------------------------------------------------ hot window
-    // tokens at positions [cold_len, L) live in ring slots pos % hot_cap.
-    const int hot_len = L - cold_len;
-    float* s_q = &s_o[0][0][0];                       // [G][128] fp32 query
-    float* s_s = &s_o[1][0][0];                       // [G][64] scores / probs
-    for (int e = tid; e < G * kD; e += kThreads)
-      s_q[e] = h2f(P.q[(static_cast<size_t>(b) * P.Hq + kvh * G) * kD + e]);
-    __syncthreads();
-    const uint16_t* kh = P.k_hot + bh * static_cast<size_t>(P.hot_cap) * kD;
-    const uint16_t* vh = P.v_hot + bh * static_cast<size_t>(P.hot_cap) * kD;
-    for (int e = tid; e < G * P.hot_cap; e += kThreads) {
-      const int hh = e / P.hot_cap, j = e % P.hot_cap;
-      float s = -INFINITY;
-      if (j < hot_len) {
-        const int slot = (cold_len + j) % P.hot_cap;
-        const uint16_t* kr = kh + static_cast<size_t>(slot) * kD;
-        float acc = 0.f;
-        for (int d = 0; d < kD; d += 8) {
-          const uint4 u = *reinterpret_cast<const uint4*>(kr + d);
-          const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+
+    // ---- merge the 4 waves of the block through LDS
+    if ((lane & 15) == 0) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            acc = fmaf(s_q[hh * kD + d + 2 * i], h2f(static_cast<uint16_t>(w[i] & 0xffffu)), acc);
-            acc = fmaf(s_q[hh * kD + d + 2 * i + 1], h2f(static_cast<uint16_t>(w[i] >> 16)), acc);
-          }
+      for (int i = 0; i < 4; ++i) {
+        const int hh = 4 * g + i;
+        if (hh < G) {
+          s_m[wave][hh] = m[i];
+          s_l[wave][hh] = l[i];
         }
-        s = acc * P.scale_log2;
       }
-      s_s[hh * 64 + j] = s;
     }
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int hh = 4 * g + i;
+        if (hh < G) s_o[wave][hh][8 * (lane & 15) + t] = o[t][i];
+      }
     __syncthreads();
-    // per-head max and sum (one wave per head, looping over heads)
-    for (int hh = wave; hh < G; hh += kWaves) {
-      const float v = lane < P.hot_cap ? s_s[hh * 64 + lane] : -INFINITY;
-      const float M = wave_max(v);
-      const float pv = (M == -INFINITY || v == -INFINITY) ? 0.f : exp2f(v - M);
-      const float lsum = wave_sum(pv);
-      if (lane < P.hot_cap) s_s[hh * 64 + lane] = pv;
-      if (lane == 0) {
+    for (int e = tid; e < G * kD; e += kThreads) {
+      const int hh = e / kD, d = e % kD;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hh]);
+      float acc = 0.f, lsum = 0.f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const float wt = exp2f(s_m[w][hh] - M);
+          acc += wt * s_o[w][hh][d];
+          lsum += wt * s_l[w][hh];
+        }
+      }
+      rec[2 * G + hh * kD + d] = acc;
+      if (d == 0) {
         rec[hh] = M;
         rec[G + hh] = lsum;
       }
     }
-    __syncthreads();
-    for (int e = tid; e < G * kD; e += kThreads) {
-      const int hh = e / kD, d = e % kD;
+    return;
+  }
+
+  // -------------------------------------------------------------- hot window
+  // tokens at positions [cold_len, L) live in ring slots pos % hot_cap; the
+  // window is staged in LDS with 16-byte loads first.
+  const int hot_len = L - cold_len;
+  float* s_q = &s_o[0][0][0];  // [G][128] fp32 query
+  float* s_s = &s_o[1][0][0];  // [G][64] scores / probs
+  for (int e = tid; e < G * kD; e += kThreads) s_q[e] = h2f(P.q[(static_cast<size_t>(b) * P.Hq + kvh * G) * kD + e]);
+  {
+    const uint16_t* kh = P.k_hot + bh * static_cast<size_t>(P.hot_cap) * kD;
+    const uint16_t* vh = P.v_hot + bh * static_cast<size_t>(P.hot_cap) * kD;
+    for (int e = tid; e < hot_len * (kD / 8); e += kThreads) {
+      const int j = e / (kD / 8), c8 = (e % (kD / 8)) * 8;
+      const int slot = (cold_len + j) % P.hot_cap;
+      *reinterpret_cast<uint4*>(&s_hot[0][j][c8]) = *reinterpret_cast<const uint4*>(kh + slot * kD + c8);
+      *reinterpret_cast<uint4*>(&s_hot[1][j][c8]) = *reinterpret_cast<const uint4*>(vh + slot * kD + c8);
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < G * kHotMax; e += kThreads) {
+    const int hh = e / kHotMax, j = e % kHotMax;
+    float s = -INFINITY;
+    if (j < hot_len) {
       float acc = 0.f;
-      for (int j = 0; j < hot_len; ++j) {
-        const int slot = (cold_len + j) % P.hot_cap;
-        acc = fmaf(s_s[hh * 64 + j], h2f(vh[static_cast<size_t>(slot) * kD + d]), acc);
-      }
-      rec[2 * G + hh * kD + d] = acc;
+#pragma unroll 8
+      for (int d = 0; d < kD; ++d) acc = fmaf(s_q[hh * kD + d], h2f(s_hot[0][j][d]), acc);
+      s = acc * P.scale_log2;
     }
-  }
-
-  // ---------------------------------------------------------------- combine
-  __syncthreads();
-  if (tid == 0) {
-    fence_release_agent();
-    const bool last = ticket_add(&P.tickets[bh]) == static_cast<unsigned>(P.nsplit);
-    if (last) fence_acquire_agent();
-    s_last = last;
+    s_s[hh * kHotMax + j] = s;
   }
   __syncthreads();
-  if (!s_last) return;
-
-  // LDS reuse: s_o[0..1] hold the (nsplit+1) x G merge weights (the host
-  // keeps nsplit + 1 <= 256), s_o[2] the rotated cold sum [G][128].
-  float* s_wt = &s_o[0][0][0];
-  float* s_rot = &s_o[2][0][0];
-  __shared__ float s_Ltot[16];
-  const float* base = P.partials + bh * (P.nsplit + 1) * rec_floats(G);
-  const int ns = P.nsplit + 1;
-  // weights per (split, head)
-  if (tid < G) {
-    float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, base[s * rec_floats(G) + tid]);
-    float Lt = 0.f;
-    for (int s = 0; s < ns; ++s) {
-      const float ms = base[s * rec_floats(G) + tid];
-      const float wt = (M == -INFINITY || ms == -INFINITY) ? 0.f : exp2f(ms - M);
-      s_wt[s * G + tid] = wt;
-      Lt += wt * base[s * rec_floats(G) + G + tid];
+  // per-head max and sum (one wave per head, looping over heads)
+  for (int hh = wave; hh < G; hh += kWaves) {
+    const float v = s_s[hh * kHotMax + lane];
+    const float M = wave_max(v);
+    const float pv = (M == -INFINITY || v == -INFINITY) ? 0.f : exp2f(v - M);
+    const float lsum = wave_sum(pv);
+    s_s[hh * kHotMax + lane] = pv;
+    if (lane == 0) {
+      rec[hh] = M;
+      rec[G + hh] = lsum;
     }
-    s_Ltot[tid] = Lt;
   }
   __syncthreads();
   for (int e = tid; e < G * kD; e += kThreads) {
+    const int hh = e / kD, d = e % kD;
     float acc = 0.f;
-    for (int s = 0; s < P.nsplit; ++s) {
-      const float wt = s_wt[s * G + e / kD];
-      if (wt != 0.f) acc += wt * base[s * rec_floats(G) + 2 * G + e];
-    }
-    s_rot[e] = acc;
+    for (int j = 0; j < hot_len; ++j) acc = fmaf(s_s[hh * kHotMax + j], h2f(s_hot[1][j][d]), acc);
+    rec[2 * G + hh * kD + d] = acc;
+  }
+}
+
+// Merge the records of one (batch, kv head) and write fp16 output.
+template <int GMAX>
+__global__ __launch_bounds__(kThreads) void tq_attn_combine_kernel(AttnParams P) {
+  constexpr int kMaxW = 4096;
+  __shared__ float s_w[kMaxW];  // merge weight per (split, head)
+  __shared__ float s_L[GMAX];
+  __shared__ __align__(16) float s_rot[GMAX][kD];
+  const int tid = threadIdx.x;
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int G = P.G;
+  const int ns = P.nsplit + 1;
+  const size_t bh = static_cast<size_t>(b) * P.Hkv + kvh;
+  const int RF = rec_floats(G);
+  const float* base = P.partials + bh * ns * RF;
+  // m of every record into s_w, then per-head max / weights / L
+  for (int e = tid; e < ns * G; e += kThreads) s_w[e] = base[(e / G) * RF + (e % G)];
+  __syncthreads();
+  if (tid < G) {
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, s_w[s * G + tid]);
+    s_L[tid] = M;
   }
   __syncthreads();
-  // out[h][j] = (sum_k rot[h][k] * PiV[k][j] + w_hot * hot[h][j]) / L
-  {
-    const int j = tid & (kD - 1);
-    const int h0 = tid >> 7;  // 0 or 1
-    float acc[GMAX / 2];
+  for (int e = tid; e < ns * G; e += kThreads) {
+    const float M = s_L[e % G];
+    const float ms = s_w[e];
+    s_w[e] = (M == -INFINITY || ms == -INFINITY) ? 0.f : exp2f(ms - M);
+  }
+  __syncthreads();
+  if (tid < G) {
+    float Lt = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 16) {
+      float v[16];
 #pragma unroll
-    for (int u = 0; u < GMAX / 2; ++u) acc[u] = 0.f;
-    for (int k = 0; k < kD; ++k) {
-      const float pv = P.PiV[k * kD + j];
+      for (int i = 0; i < 16; ++i) v[i] = (s0 + i < ns) ? base[(s0 + i) * RF + G + tid] : 0.f;
 #pragma unroll
-      for (int u = 0; u < GMAX / 2; ++u) {
-        const int hh = h0 + 2 * u;
-        if (hh < G) acc[u] = fmaf(s_rot[hh * kD + k], pv, acc[u]);
+      for (int i = 0; i < 16; ++i)
+        if (s0 + i < ns) Lt += s_w[(s0 + i) * G + tid] * v[i];
+    }
+    s_L[tid] = Lt;
+  }
+  // rotated cold sum, records read 16 deep
+  for (int e = tid; e < G * kD; e += kThreads) {
+    const int hh = e / kD;
+    float acc = 0.f;
+    for (int s0 = 0; s0 < P.nsplit; s0 += 16) {
+      float v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int s = s0 + i;
+        v[i] = (s < P.nsplit) ? base[s * RF + 2 * G + e] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int s = s0 + i;
+        if (s < P.nsplit) {
+          const float wt = s_w[s * G + hh];
+          if (wt != 0.f) acc += wt * v[i];
+        }
       }
     }
+    s_rot[hh][e % kD] = acc;
+  }
+  __syncthreads();
+  // out[h][j] = (sum_k rot[h][k] PiV[k][j] + w_hot hot[h][j]) / L
+  const int j = tid & (kD - 1);
+  const int h0 = tid >> 7;  // 0 or 1
+  float acc[GMAX / 2];
+#pragma unroll
+  for (int u = 0; u < GMAX / 2; ++u) acc[u] = 0.f;
+#pragma unroll 8
+  for (int k = 0; k < kD; ++k) {
+    const float pv = P.PiV[k * kD + j];
 #pragma unroll
     for (int u = 0; u < GMAX / 2; ++u) {
       const int hh = h0 + 2 * u;
-      if (hh < G) {
-        const float wh = s_wt[P.nsplit * G + hh];
-        float v = acc[u];
-        if (wh != 0.f) v += wh * base[P.nsplit * rec_floats(G) + 2 * G + hh * kD + j];
-        const float Lt = s_Ltot[hh];
-        v = (Lt > 0.f) ? v / Lt : 0.f;
-        P.out[(static_cast<size_t>(b) * P.Hq + kvh * G + hh) * kD + j] = f2h(v);
-      }
+      if (hh < G) acc[u] = fmaf(s_rot[hh][k], pv, acc[u]);
     }
   }
-  if (tid == 0) ticket_reset(&P.tickets[bh]);
+  const float* hot = base + P.nsplit * RF;
+#pragma unroll
+  for (int u = 0; u < GMAX / 2; ++u) {
+    const int hh = h0 + 2 * u;
+    if (hh < G) {
+      const float wh = s_w[P.nsplit * G + hh];
+      float v = acc[u];
+      if (wh != 0.f) v += wh * hot[2 * G + hh * kD + j];
+      const float Lt = s_L[hh];
+      v = (Lt > 0.f) ? v / Lt : 0.f;
+      P.out[(static_cast<size_t>(b) * P.Hq + kvh * G + hh) * kD + j] = f2h(v);
+    }
+  }
 }
 
 struct AttnPlan {
   int nsplit, split_tokens;
-  size_t qrot_off, part_off, tick_off, total;
+  size_t qrot_off, part_off, total;
 };
 
-// Upper bound on the number of cold splits: enough blocks for ~2 per CU, and
-// nsplit + 1 <= 256 so the merge weights fit the LDS the combine step reuses.
-int64_t max_splits(int64_t B, int64_t Hkv) {
+// Upper bound on the number of cold splits: enough blocks for ~2 per CU,
+// nsplit + 1 <= 256 records and (nsplit + 1) * G <= 4096 merge weights in the
+// combine kernel's LDS.
+int64_t max_splits(int64_t B, int64_t Hkv, int64_t G) {
   const int64_t target = 2 * static_cast<int64_t>(device_cu_count());
   int64_t ns = (target + B * Hkv - 1) / (B * Hkv);
   if (ns > 255) ns = 255;
+  const int64_t gcap = 4096 / (G > 0 ? G : 1) - 1;
+  if (ns > gcap) ns = gcap;
   return ns < 1 ? 1 : ns;
 }
 
 AttnPlan plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_cap) {
   AttnPlan p{};
+  const int64_t G = Hkv > 0 ? Hq / Hkv : 1;
   const int64_t cold_max = max_len > hot_cap ? max_len - hot_cap : 0;
-  const int64_t ns_cap = max_splits(B, Hkv);
+  const int64_t ns_cap = max_splits(B, Hkv, G);
   int64_t ns = ns_cap;
   const int64_t maxs = (cold_max + kBlk - 1) / kBlk;
   if (ns > maxs) ns = maxs;
@@ -443,10 +485,8 @@ AttnPlan plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_c
   ns = cold_max > 0 ? (cold_max + ts - 1) / ts : 1;
   p.nsplit = static_cast<int>(ns);
   p.split_tokens = static_cast<int>(ts);
-  const int64_t G = Hkv > 0 ? Hq / Hkv : 1;
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
-  p.tick_off = 0;  // fixed ticket area shared with every other split-K entry point
-  p.qrot_off = kTicketBytes;
+  p.qrot_off = kTicketBytes;  // keeps the shared workspace layout: ticket area first
   p.part_off = p.qrot_off + al(static_cast<size_t>(B * Hq * kD) * 4);
   p.total = p.part_off + al(static_cast<size_t>(B * Hkv * (ns_cap + 1) * G * (2 + kD)) * 4);
   return p;
@@ -459,7 +499,7 @@ using namespace lkv;
 
 extern "C" size_t lkv_tq_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len < 0) return kTicketBytes;
-  // hot_cap only shifts the cold range; size for the largest split count.
+  // hot_cap only shifts the cold range; the record area is sized for the cap.
   return plan(B, Hq, Hkv, max_len, 0).total;
 }
 
@@ -474,28 +514,23 @@ extern "C" int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const f
   LKV_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16,
               "tq_decode_attn: need Hq %% Hkv == 0 and Hq/Hkv <= 16 (Hq=%lld Hkv=%lld)", (long long)Hq,
               (long long)Hkv);
-  LKV_REQUIRE(hot_cap >= 1 && hot_cap <= 64, "tq_decode_attn: hot_cap must be 1..64");
-  LKV_REQUIRE(max_len >= 0 && max_len <= cap + hot_cap,
-              "tq_decode_attn: max_len=%lld exceeds cap+hot_cap=%lld", (long long)max_len,
-              (long long)(cap + hot_cap));
+  LKV_REQUIRE(hot_cap >= 1 && hot_cap <= kHotMax, "tq_decode_attn: hot_cap must be 1..64");
+  LKV_REQUIRE(max_len >= 0 && max_len <= cap + hot_cap, "tq_decode_attn: max_len=%lld exceeds cap+hot_cap=%lld",
+              (long long)max_len, (long long)(cap + hot_cap));
   LKV_REQUIRE(max_len < (1ll << 31) && cap < (1ll << 31), "tq_decode_attn: length too large");
-  LKV_REQUIRE(B * Hkv <= kMaxTickets, "tq_decode_attn: batch*kv_heads=%lld exceeds %lld tickets",
-              (long long)(B * Hkv), (long long)kMaxTickets);
   if (B == 0) return LKV_OK;
   LKV_REQUIRE(q && k_codes && k_norms && v_codes && v_norms && k_hot && v_hot && PiK && PiV && centroids &&
                   seq_len && out && workspace,
               "tq_decode_attn: null pointer");
-  LKV_REQUIRE(aligned16(q) && aligned16(k_codes) && aligned16(v_codes) && aligned16(k_hot) &&
-                  aligned16(v_hot) && aligned16(PiK) && aligned16(out) && aligned16(workspace),
+  LKV_REQUIRE(aligned16(q) && aligned16(k_codes) && aligned16(v_codes) && aligned16(k_hot) && aligned16(v_hot) &&
+                  aligned16(PiK) && aligned16(out) && aligned16(workspace),
               "tq_decode_attn: q, codes, hot, PiK, out and workspace must be 16-byte aligned");
   const AttnPlan pl = plan(B, Hq, Hkv, max_len, hot_cap);
-  LKV_REQUIRE(workspace_bytes >= pl.total, "tq_decode_attn: workspace of %zu bytes required, got %zu",
-              pl.total, workspace_bytes);
+  LKV_REQUIRE(workspace_bytes >= pl.total, "tq_decode_attn: workspace of %zu bytes required, got %zu", pl.total,
+              workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   float* qrot = reinterpret_cast<float*>(ws + pl.qrot_off);
-  // Pre-scale by scale*log2(e) after rotation: rotate into qrot, then the
-  // kernel folds the factor in when it packs the fp16 operand.
   if (int e = lkv_tq_rotate(q, LKV_DTYPE_F16, B * Hq, PiK, 0, qrot, stream)) return e;
   AttnParams P;
   P.qrot = qrot;
@@ -510,7 +545,6 @@ extern "C" int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const f
   P.centroids = centroids;
   P.seq_len = seq_len;
   P.partials = reinterpret_cast<float*>(ws + pl.part_off);
-  P.tickets = reinterpret_cast<unsigned*>(ws + pl.tick_off);
   P.out = static_cast<uint16_t*>(out);
   P.scale_log2 = scale * kLog2e;
   P.max_len = static_cast<int>(max_len);
@@ -523,12 +557,17 @@ extern "C" int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const f
   P.split_tokens = pl.split_tokens;
   P.ncent = 1 << bits;
   dim3 grid(static_cast<unsigned>(pl.nsplit + 1), static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
-  if (P.G <= 4)
-    hipLaunchKernelGGL((tq_decode_attn_kernel<4>), grid, dim3(kThreads), 0, st, P);
-  else if (P.G <= 8)
-    hipLaunchKernelGGL((tq_decode_attn_kernel<8>), grid, dim3(kThreads), 0, st, P);
-  else
-    hipLaunchKernelGGL((tq_decode_attn_kernel<16>), grid, dim3(kThreads), 0, st, P);
+  dim3 cgrid(static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
+  if (P.G <= 4) {
+    hipLaunchKernelGGL((tq_attn_split_kernel<4>), grid, dim3(kThreads), 0, st, P);
+    hipLaunchKernelGGL((tq_attn_combine_kernel<4>), cgrid, dim3(kThreads), 0, st, P);
+  } else if (P.G <= 8) {
+    hipLaunchKernelGGL((tq_attn_split_kernel<8>), grid, dim3(kThreads), 0, st, P);
+    hipLaunchKernelGGL((tq_attn_combine_kernel<8>), cgrid, dim3(kThreads), 0, st, P);
+  } else {
+    hipLaunchKernelGGL((tq_attn_split_kernel<16>), grid, dim3(kThreads), 0, st, P);
+    hipLaunchKernelGGL((tq_attn_combine_kernel<16>), cgrid, dim3(kThreads), 0, st, P);
+  }
   LKV_LAUNCH_CHECK("tq_decode_attn");
   return LKV_OK;
 }

@@ -262,3 +262,32 @@ def test_attention_oracle_closed_form():
     V = torch.arange(10, dtype=torch.float32).view(1, 1, 10, 1).expand(1, 1, 10, 128)
     o = oq.decode_attention(q, K, V)
     assert torch.allclose(o, torch.full_like(o, 4.5, dtype=torch.float64))
+
+
+def test_reference_model_matches_hf_mistral_without_compression():
+    """The oracle decoder (no TEAL, hot window larger than the sequence) equals HF Mistral in fp32."""
+    from transformers import MistralConfig, MistralForCausalLM
+
+    from oracle.model import RefModel
+
+    cfg = MistralConfig(vocab_size=300, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                        num_attention_heads=2, num_key_value_heads=1, head_dim=128, max_position_embeddings=512,
+                        rope_theta=1e6, rms_norm_eps=1e-5)
+    torch.manual_seed(0)
+    m = MistralForCausalLM(cfg).float().eval()
+    with torch.no_grad():
+        for p in m.parameters():
+            if p.dim() == 2:
+                p.normal_(0, 0.05)
+    ref = RefModel(m.state_dict(), cfg, None, hot=10_000)
+    ids = torch.randint(0, 300, (20,))
+    with torch.no_grad():
+        hf_pref = m(ids.view(1, -1)).logits[0, -1]
+    lg = ref.forward(ids)
+    assert torch.allclose(lg, hf_pref, rtol=2e-2, atol=2e-2 * hf_pref.abs().max().item())
+    # one decode step after the prompt
+    nxt = torch.tensor([7])
+    with torch.no_grad():
+        hf_dec = m(torch.cat([ids, nxt]).view(1, -1)).logits[0, -1]
+    lg2 = ref.forward(nxt)
+    assert (lg2 - hf_dec).norm() / hf_dec.norm() < 2e-2
