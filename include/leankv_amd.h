@@ -12,10 +12,9 @@
  *
  * Workspaces: the split-K entry points need a caller-provided device workspace
  * of at least the size returned by the matching *_workspace_bytes() query.  It
- * must be zero-filled once when first allocated; each call leaves its ticket
- * counters at zero again, so the same workspace can be reused by later calls
- * on the same stream without clearing.  Calls that share a workspace must not
- * overlap (use one workspace per concurrently running stream).
+ * needs no initialisation: every call writes the partial sums it later reads.
+ * Calls that share a workspace must not overlap (use one workspace per
+ * concurrently running stream).
  */
 #ifndef LEANKV_AMD_H
 #define LEANKV_AMD_H
@@ -174,6 +173,104 @@ int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const float* k_nor
                        int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t hot_cap,
                        float scale, void* out,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Fused B=1 decode step                                                     */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * One greedy decode step of a Mistral/Llama-shaped decoder (head_dim 128) with
+ * TEAL sparse projections and a TurboQuant cache, as a fixed sequence of
+ * launches on device-resident state, so that it can be captured into a HIP
+ * graph and replayed per token.  No single reference function corresponds:
+ * the step runs, per layer, what the reference executes through HF
+ * MistralDecoderLayer (transformers/models/mistral/modeling_mistral.py) with
+ * every projection patched by _patch_linear_with_triton
+ * (leankv/teal/patching.py:152-183), keys/values going through
+ * TurboQuantCache.update (leankv/turboquant/cache.py:84-189) and attention
+ * over its output; then the final RMSNorm, the dense lm_head and argmax of
+ * scripts/benchmark.py's greedy loop.  Per layer (9 launches):
+ *   1. q/k/v GEMV, RMSNorm(x) computed in the prologue;
+ *   2. q/k/v epilogue: reduce partials, RoPE, quantize the token leaving the
+ *      hot window (lkv_tq_cache_append arithmetic), write the new token to the
+ *      hot ring, rotate q (lkv_tq_rotate arithmetic);
+ *   3-4. packed-KV attention split + combine (lkv_tq_decode_attn kernels);
+ *   5. o_proj GEMV;  6. x += o (fp16 residual);
+ *   7. gate/up GEMV, RMSNorm(x) in the prologue;
+ *   8. down GEMV, SwiGLU of the gate/up partials in the prologue;
+ *   9. x += down.
+ * Rounding follows the fp16 HF modules: projections, RMSNorm output, RoPE
+ * products and sums, SwiGLU and residual adds are rounded to fp16 where HF
+ * stores fp16 tensors.  A threshold of 0 keeps every nonzero input (dense).
+ *
+ * Weights are fp16 in the column-major layout of lkv_sparse_gemv (row z holds
+ * the N weights of input z), including lm_head ([hidden][vocab]).
+ * Device state: tok (int64, the token fed next) and pos (int64, its
+ * position); lkv_decode_head writes the argmax into tok and increments pos.
+ * Positions at or beyond max_len are clamped (results are then meaningless);
+ * the caller bounds the number of steps.
+ */
+typedef struct lkv_decode_dims {
+  int64_t hidden;        /* model width, multiple of 256 */
+  int64_t ffn;           /* MLP width, multiple of 256 */
+  int64_t vocab;         /* multiple of 8 */
+  int64_t n_heads;       /* query heads */
+  int64_t n_kv_heads;    /* n_heads / n_kv_heads <= 8 */
+  int64_t max_len;       /* RoPE table rows; tokens the cache holds */
+  int64_t cap;           /* cold rows per (layer, kv head) */
+  int64_t hot_cap;       /* fp16 window, 1..64 */
+  int32_t bits;          /* 3 or 4 */
+  float eps;             /* RMSNorm epsilon */
+  float scale;           /* attention scale */
+  const float* bounds;   /* 2^bits - 1 decision boundaries (fp32) */
+  const float* centroids;/* 2^bits centroids (fp32) */
+  const void* rope_cos;  /* fp16 [max_len][128] */
+  const void* rope_sin;  /* fp16 [max_len][128] */
+} lkv_decode_dims;
+
+typedef struct lkv_decode_layer {
+  const void* input_norm;  /* fp16 [hidden] */
+  const void* post_norm;   /* fp16 [hidden] */
+  const void* wq;          /* [hidden][n_heads * 128] */
+  const void* wk;          /* [hidden][n_kv_heads * 128] */
+  const void* wv;
+  const void* wo;          /* [n_heads * 128][hidden] */
+  const void* wg;          /* [hidden][ffn] */
+  const void* wu;
+  const void* wd;          /* [ffn][hidden] */
+  float tq, tk, tv, to, tg, tu, td;  /* TEAL thresholds */
+  void* k_codes;           /* uint8 [n_kv_heads, cap, 64] */
+  void* k_norms;           /* fp32 [n_kv_heads, cap] */
+  void* v_codes;
+  void* v_norms;
+  void* k_hot;             /* fp16 [n_kv_heads, hot_cap, 128] ring */
+  void* v_hot;
+  const float* PiK;        /* fp32 [128, 128] */
+  const float* PiV;
+} lkv_decode_layer;
+
+/*
+ * y = RMSNorm(x) * w for M rows of Z fp16 values (x 16-byte aligned, Z % 8 == 0):
+ * HF MistralRMSNorm (modeling_mistral.py:190-197) with the summation order of
+ * the RMSNorm fused into lkv_decode_layer_step's GEMV prologues, so a caller
+ * gets bit-identical normalised activations (and therefore identical TEAL
+ * masks) outside the fused step.
+ */
+int lkv_rmsnorm(const void* x, const void* w, float eps, int64_t M, int64_t Z, void* y, void* stream);
+
+/* Workspace shared by the three calls below (no initialisation needed). */
+size_t lkv_decode_workspace_bytes(const lkv_decode_dims* dims);
+/* x = embed[tok] (embed fp16 [vocab][hidden] row-major); latches pos. */
+int lkv_decode_begin(const lkv_decode_dims* dims, const void* embed, const int64_t* tok, const int64_t* pos,
+                     void* x, void* workspace, size_t workspace_bytes, void* stream);
+/* One decoder layer on the fp16 residual stream x [hidden], in place. */
+int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_decode_layer* layer, void* x,
+                          void* workspace, size_t workspace_bytes, void* stream);
+/* logits = lm_head(RMSNorm(x) * final_norm) (fp16 [vocab]); tok = argmax
+ * (lowest index among equal maxima); pos += 1. */
+int lkv_decode_head(const lkv_decode_dims* dims, const void* final_norm, const void* lm_head, const void* x,
+                    void* logits, int64_t* tok, int64_t* pos, void* workspace, size_t workspace_bytes,
+                    void* stream);
 
 #ifdef __cplusplus
 }

@@ -46,7 +46,34 @@ SIGNATURES = {
     "lkv_tq_decode_attn_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "lkv_tq_decode_attn": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _int, _c_p,
                                   _i64, _i64, _i64, _i64, _i64, _i64, _f32, _c_p, _c_p, _sz, _c_p]),
+    "lkv_rmsnorm": (_int, [_c_p, _c_p, _f32, _i64, _i64, _c_p, _c_p]),
+    "lkv_decode_workspace_bytes": (_sz, [_c_p]),
+    "lkv_decode_begin": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
+    "lkv_decode_layer_step": (_int, [_c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
+    "lkv_decode_head": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
 }
+
+
+class DecodeDims(ctypes.Structure):
+    """lkv_decode_dims (include/leankv_amd.h)."""
+
+    _fields_ = [
+        ("hidden", _i64), ("ffn", _i64), ("vocab", _i64), ("n_heads", _i64), ("n_kv_heads", _i64),
+        ("max_len", _i64), ("cap", _i64), ("hot_cap", _i64), ("bits", ctypes.c_int32), ("eps", _f32),
+        ("scale", _f32), ("bounds", _c_p), ("centroids", _c_p), ("rope_cos", _c_p), ("rope_sin", _c_p),
+    ]
+
+
+class DecodeLayer(ctypes.Structure):
+    """lkv_decode_layer (include/leankv_amd.h)."""
+
+    _fields_ = [
+        ("input_norm", _c_p), ("post_norm", _c_p), ("wq", _c_p), ("wk", _c_p), ("wv", _c_p), ("wo", _c_p),
+        ("wg", _c_p), ("wu", _c_p), ("wd", _c_p),
+        ("tq", _f32), ("tk", _f32), ("tv", _f32), ("to", _f32), ("tg", _f32), ("tu", _f32), ("td", _f32),
+        ("k_codes", _c_p), ("k_norms", _c_p), ("v_codes", _c_p), ("v_norms", _c_p), ("k_hot", _c_p),
+        ("v_hot", _c_p), ("PiK", _c_p), ("PiV", _c_p),
+    ]
 
 _lib = None
 _lock = threading.Lock()
@@ -113,11 +140,11 @@ def require_cuda(*tensors: torch.Tensor) -> None:
 
 
 class _Workspaces:
-    """Zero-filled device workspaces, one per (device, key), grown on demand.
+    """Device workspaces, one per (device, key), grown on demand.
 
-    The kernels leave their ticket counters at zero when they finish, so a
-    workspace stays reusable by later calls on the same stream without any
-    clearing (which also keeps the calls capturable in a HIP graph).
+    No entry point reads workspace contents left by an earlier call, so a
+    workspace is reused by later calls on the same stream without clearing
+    (which also keeps the calls capturable in a HIP graph).
     """
 
     def __init__(self):

@@ -1,0 +1,608 @@
+// Fused B=1 decode step: 9 launches per decoder layer, all state on the device.
+//
+// The reference decodes through HF generate(): per token, Python walks the
+// layers of MistralDecoderLayer (transformers/models/mistral/
+// modeling_mistral.py), each TEAL-patched projection launches its own GEMV
+// (leankv/teal/patching.py:152-183) and TurboQuantCache.update dequantizes
+// the cold store (leankv/turboquant/cache.py:84-189).  Here the same
+// arithmetic is regrouped around the GEMVs, which dominate the bytes:
+//
+//   x (fp16 residual)
+//   1. GEMV q|k|v (one launch, 3 segments), prologue x -> RMSNorm(x) * w
+//   2. prep: q/k/v partial sums -> fp16, RoPE, quantize the token leaving
+//      the hot window, new k/v into the hot ring, q rotation -> q_rot
+//   3. attention split (cold codes), 4. combine (+ hot window, PiV)
+//   5. GEMV o_proj                                6. x += o
+//   7. GEMV gate|up (dual), prologue RMSNorm       8. GEMV down, prologue
+//      SwiGLU of the gate/up partial sums          9. x += down
+//   head: GEMV lm_head (prologue final RMSNorm), logits + per-block argmax,
+//   final argmax -> tok, pos + 1.
+//
+// Split-K partial sums are reduced in chunk order by their consumer, so every
+// projection equals the standalone lkv_sparse_gemv result for the same chunk
+// size.  Rounding follows the fp16 HF modules (see each kernel).
+#include "kernels.h"
+#include "tq_common.h"
+
+namespace lkv {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kThreads = 256;
+constexpr int kMaxG = 8;  // query heads per kv head handled by the prep kernel
+
+struct Plan {
+  int64_t Hq, Hkv, G, nq, nkv;                 // q / k,v projection widths
+  int64_t sq, sk, sh, sf, svoc;                // column slabs
+  int bz_qkv, bz_o, bz_gu, bz_d, bz_lm;
+  int nc_qkv, nc_o, nc_gu, nc_d, nc_lm;
+  AttnPlan attn;
+  size_t off_state, off_pqkv, off_po, off_pgu, off_pd, off_plm, off_q16, off_qrot, off_attn, off_rec, off_cand,
+      total;
+};
+
+size_t al256(size_t v) { return (v + 255) / 256 * 256; }
+
+Plan make_plan(const lkv_decode_dims& d) {
+  Plan p{};
+  p.Hq = d.n_heads;
+  p.Hkv = d.n_kv_heads;
+  p.G = d.n_heads / d.n_kv_heads;
+  p.nq = d.n_heads * kD;
+  p.nkv = d.n_kv_heads * kD;
+  p.sq = gemv_slabs(p.nq);
+  p.sk = gemv_slabs(p.nkv);
+  p.sh = gemv_slabs(d.hidden);
+  p.sf = gemv_slabs(d.ffn);
+  p.svoc = gemv_slabs(d.vocab);
+  p.bz_qkv = gemv_pick_bz(p.sq + 2 * p.sk, d.hidden);
+  p.bz_o = gemv_pick_bz(p.sh, p.nq);
+  p.bz_gu = gemv_pick_bz(p.sf, d.hidden);
+  p.bz_d = gemv_pick_bz(p.sh, d.ffn);
+  p.bz_lm = gemv_pick_bz(p.svoc, d.hidden);
+  p.nc_qkv = static_cast<int>(gemv_chunks(d.hidden, p.bz_qkv));
+  p.nc_o = static_cast<int>(gemv_chunks(p.nq, p.bz_o));
+  p.nc_gu = static_cast<int>(gemv_chunks(d.hidden, p.bz_gu));
+  p.nc_d = static_cast<int>(gemv_chunks(d.ffn, p.bz_d));
+  p.nc_lm = static_cast<int>(gemv_chunks(d.hidden, p.bz_lm));
+  p.attn = attn_plan(1, p.Hq, p.Hkv, d.max_len, d.hot_cap);
+  size_t o = kTicketBytes;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += al256(bytes);
+    return at;
+  };
+  p.off_state = take(2 * sizeof(int32_t));
+  p.off_pqkv = take((gemv_part_floats(p.nq, p.nc_qkv) + 2 * gemv_part_floats(p.nkv, p.nc_qkv)) * 4);
+  p.off_po = take(gemv_part_floats(d.hidden, p.nc_o) * 4);
+  p.off_pgu = take(2 * gemv_part_floats(d.ffn, p.nc_gu) * 4);
+  p.off_pd = take(gemv_part_floats(d.hidden, p.nc_d) * 4);
+  p.off_plm = take(gemv_part_floats(d.vocab, p.nc_lm) * 4);
+  p.off_q16 = take(static_cast<size_t>(p.nq) * 2);
+  p.off_qrot = take(static_cast<size_t>(p.nq) * 4);
+  p.off_attn = take(static_cast<size_t>(p.nq) * 2);
+  p.off_rec = take(p.attn.total - p.attn.part_off);
+  p.off_cand = take(static_cast<size_t>(p.svoc) * 8);
+  p.total = o;
+  return p;
+}
+
+int check_dims(const lkv_decode_dims* d) {
+  LKV_REQUIRE(d != nullptr, "decode: null dims");
+  LKV_REQUIRE(d->hidden > 0 && d->hidden % 256 == 0, "decode: hidden=%lld must be a positive multiple of 256",
+              (long long)d->hidden);
+  LKV_REQUIRE(d->ffn > 0 && d->ffn % 256 == 0, "decode: ffn=%lld must be a positive multiple of 256",
+              (long long)d->ffn);
+  LKV_REQUIRE(d->vocab > 0 && d->vocab % 8 == 0, "decode: vocab=%lld must be a positive multiple of 8",
+              (long long)d->vocab);
+  LKV_REQUIRE(d->n_heads > 0 && d->n_kv_heads > 0 && d->n_heads % d->n_kv_heads == 0 &&
+                  d->n_heads / d->n_kv_heads <= kMaxG,
+              "decode: n_heads=%lld must be a multiple of n_kv_heads=%lld with at most %d query heads per kv head",
+              (long long)d->n_heads, (long long)d->n_kv_heads, kMaxG);
+  LKV_REQUIRE(d->hot_cap >= 1 && d->hot_cap <= 64, "decode: hot_cap must be 1..64");
+  LKV_REQUIRE(d->max_len >= 1 && d->max_len < (1ll << 30), "decode: max_len=%lld out of range", (long long)d->max_len);
+  LKV_REQUIRE(d->cap >= d->max_len - d->hot_cap && d->cap < (1ll << 30),
+              "decode: cap=%lld cannot hold max_len - hot_cap = %lld cold tokens", (long long)d->cap,
+              (long long)(d->max_len - d->hot_cap));
+  LKV_REQUIRE(d->bits == 3 || d->bits == 4, "decode: bits=%d unsupported (3 or 4)", d->bits);
+  LKV_REQUIRE(d->bounds && d->centroids && d->rope_cos && d->rope_sin, "decode: null codebook or RoPE table");
+  LKV_REQUIRE(aligned16(d->rope_cos) && aligned16(d->rope_sin), "decode: RoPE tables must be 16-byte aligned");
+  const int64_t wmax = d->hidden * (d->ffn > d->vocab ? d->ffn : d->vocab);
+  LKV_REQUIRE(wmax * 2 < (1ll << 32) && d->hidden * d->n_heads * kD * 2 < (1ll << 32),
+              "decode: a weight matrix exceeds the 4 GiB buffer-descriptor range");
+  return LKV_OK;
+}
+
+int check_ws(const Plan& p, const void* ws, size_t bytes) {
+  LKV_REQUIRE(ws && aligned16(ws) && bytes >= p.total, "decode: workspace of %zu bytes (16-byte aligned) required, got %zu",
+              p.total, bytes);
+  return LKV_OK;
+}
+
+// ------------------------------------------------------------------ kernels
+
+// x = embed[tok]; state = {pos, pos + 1} (pos clamped into the tables).
+__global__ __launch_bounds__(kThreads) void begin_kernel(const uint16_t* __restrict__ embed,
+                                                         const int64_t* __restrict__ tok,
+                                                         const int64_t* __restrict__ pos, uint16_t* __restrict__ x,
+                                                         int32_t* __restrict__ state, int64_t hidden, int64_t vocab,
+                                                         int64_t max_len) {
+  int64_t t = *tok;
+  t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 8;
+  if (i < hidden)
+    *reinterpret_cast<uint4*>(x + i) = *reinterpret_cast<const uint4*>(embed + t * hidden + i);
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    int64_t p = *pos;
+    p = p < 0 ? 0 : (p >= max_len ? max_len - 1 : p);
+    state[0] = static_cast<int32_t>(p);
+    state[1] = static_cast<int32_t>(p + 1);
+  }
+}
+
+// x[n] = fp16(x[n] + fp16(sum of chunks)): the fp16 residual add of the decoder layer.
+__global__ __launch_bounds__(kThreads) void residual_kernel(uint16_t* __restrict__ x, const float* __restrict__ part,
+                                                            int N, int nchunk) {
+  const int n = blockIdx.x * kThreads + threadIdx.x;
+  if (n >= N) return;
+  x[n] = f2h(h2f(x[n]) + h2f(f2h(column_sum(part, n, nchunk))));
+}
+
+// y = RMSNorm(x) * w for M rows of Z; block (j, m) writes columns
+// [256 j, 256 j + 256) of row m after computing the row's rstd itself.
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ w, float eps, int Z,
+                                                           uint16_t* __restrict__ y) {
+  __shared__ float s_wsum[kThreads / kWave];
+  const size_t row = static_cast<size_t>(blockIdx.y) * Z;
+  const float rstd = rms_rstd(x + row, Z, eps, s_wsum);
+  const int z = blockIdx.x * kThreads + threadIdx.x;
+  if (z < Z) y[row + z] = f2h(rms_apply(x[row + z], w[z], rstd));
+}
+
+struct PrepArgs {
+  const float* part;  // q|k|v partials
+  size_t off[3];
+  int nchunk;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  const int32_t* state;
+  uint16_t* k_hot;
+  uint16_t* v_hot;
+  uint8_t* k_codes;
+  float* k_norms;
+  uint8_t* v_codes;
+  float* v_norms;
+  const float* PiK;
+  const float* PiV;
+  const float* bounds;
+  int hot_cap, cap, Hq, Hkv;
+  uint16_t* q16;
+  float* qrot;
+};
+
+// One block per kv head: its G query heads, its key and its value.
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
+  constexpr int kCols = (kMaxG + 2) * kD / kThreads;
+  __shared__ float s_raw[kMaxG + 2][kD];   // q heads, k, v as projected (fp16 values)
+  __shared__ float s_rope[kMaxG + 1][kD];  // q heads, k after RoPE
+  __shared__ uint8_t s_codes[2][tq::kRows * kD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kvh = blockIdx.x;
+  const int G = A.Hq / A.Hkv;
+  const int ncol = (G + 2) * kD;
+  const int nc = A.nchunk;
+
+  // ---- 1. projections, summed over chunks in chunk order, rounded to fp16
+  {
+    const float* src[kCols];
+    bool ok[kCols];
+    float acc[kCols];
+#pragma unroll
+    for (int e = 0; e < kCols; ++e) {
+      const int c = e * kThreads + tid;
+      ok[e] = c < ncol;
+      const int which = c / kD, d = c % kD;
+      int seg, col;
+      if (which < G) {
+        seg = 0;
+        col = (kvh * G + which) * kD + d;
+      } else {
+        seg = which == G ? 1 : 2;
+        col = kvh * kD + d;
+      }
+      src[e] = ok[e] ? A.part + A.off[seg] + static_cast<size_t>(col / kGemvBN) * nc * kGemvBN + (col % kGemvBN)
+                     : A.part;
+      acc[e] = 0.f;
+    }
+    for (int k0 = 0; k0 < nc; k0 += 8) {
+      float v[kCols][8];
+#pragma unroll
+      for (int e = 0; e < kCols; ++e)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          v[e][i] = (ok[e] && k0 + i < nc) ? src[e][static_cast<size_t>(k0 + i) * kGemvBN] : 0.f;
+#pragma unroll
+      for (int e = 0; e < kCols; ++e)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[e] += v[e][i];
+    }
+#pragma unroll
+    for (int e = 0; e < kCols; ++e) {
+      const int c = e * kThreads + tid;
+      if (ok[e]) s_raw[c / kD][c % kD] = h2f(f2h(acc[e]));
+    }
+  }
+  __syncthreads();
+
+  // ---- 2. RoPE: x*cos + rotate_half(x)*sin with fp16 products and sum
+  //      (apply_rotary_pos_emb on fp16 tensors, modeling_mistral.py)
+  const int pos = A.state[0];
+  {
+    const uint16_t* cs = A.cos + static_cast<size_t>(pos) * kD;
+    const uint16_t* sn = A.sin + static_cast<size_t>(pos) * kD;
+    for (int e = tid; e < (G + 1) * kD; e += kThreads) {
+      const int r = e / kD, d = e % kD;
+      const float xv = s_raw[r][d];
+      const float rh = d < kD / 2 ? -s_raw[r][d + kD / 2] : s_raw[r][d - kD / 2];
+      const float o = h2f(f2h(h2f(f2h(xv * h2f(cs[d]))) + h2f(f2h(rh * h2f(sn[d])))));
+      s_rope[r][d] = o;
+      if (r < G) A.q16[static_cast<size_t>(kvh * G + r) * kD + d] = f2h(o);
+    }
+  }
+  __syncthreads();
+
+  // ---- 3. one K tile (row 0: the key leaving the hot window, normalised;
+  //      rows 1..G: the query heads) and one V tile (row 0: the value).
+  const int slot = pos % A.hot_cap;
+  const int ev = pos - A.hot_cap;
+  const bool evict = pos >= A.hot_cap && ev < A.cap;
+  float bK[2][32], bV[2][32];
+  tq::load_pi_operand(A.PiK, false, wave, lane, bK);
+  tq::load_pi_operand(A.PiV, false, wave, lane, bV);
+  const int r = lane & 15, c0 = 32 * (lane >> 4);
+  const size_t hrow = (static_cast<size_t>(kvh) * A.hot_cap + slot) * kD;
+  float aK[32], aV[32];
+  if (r == 0 && evict) {
+    tq::load_row_f16(A.k_hot + hrow + c0, aK);
+    tq::load_row_f16(A.v_hot + hrow + c0, aV);
+  } else {
+#pragma unroll
+    for (int s = 0; s < 32; ++s) {
+      aK[s] = (r >= 1 && r <= G) ? s_rope[r - 1][c0 + s] : 0.f;
+      aV[s] = 0.f;
+    }
+  }
+  // cache.py:141 quantizes flush_k.float(): fp32 semantics on the fp16 data.
+  const float nK = tq::normalize_row_f32_if(aK, r == 0);
+  const float nV = tq::normalize_row_f32_if(aV, r == 0);
+  f32x4 accK[2], accV[2];
+  tq::rotate_tile(aK, bK, accK);
+  tq::rotate_tile(aV, bV, accV);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * (lane >> 4) + i;
+      const int dim = 8 * (lane & 15) + 2 * wave + t;
+      if (row >= 1 && row <= G) A.qrot[static_cast<size_t>(kvh * G + row - 1) * kD + dim] = accK[t][i];
+    }
+  if (evict) {
+    float bd[(1 << BITS) - 1];
+#pragma unroll
+    for (int i = 0; i < (1 << BITS) - 1; ++i) bd[i] = A.bounds[i];
+    tq::codes_to_lds<BITS>(accK, bd, wave, lane, s_codes[0]);
+    tq::codes_to_lds<BITS>(accV, bd, wave, lane, s_codes[1]);
+    if (tid == 0) {
+      A.k_norms[static_cast<size_t>(kvh) * A.cap + ev] = nK;
+      A.v_norms[static_cast<size_t>(kvh) * A.cap + ev] = nV;
+    }
+  }
+  __syncthreads();  // codes staged; every read of the old hot slot is done
+  if (evict) {
+    const int64_t roff = (static_cast<int64_t>(kvh) * A.cap + ev) * tq::row_bytes_for(BITS);
+    tq::pack_store<BITS>(s_codes[0], A.k_codes, 0, 1, [=](int64_t) { return roff; });
+    tq::pack_store<BITS>(s_codes[1], A.v_codes, 0, 1, [=](int64_t) { return roff; });
+  }
+  // ---- 4. the new token into its ring slot
+  if (tid < kD) {
+    A.k_hot[hrow + tid] = f2h(s_rope[G][tid]);
+    A.v_hot[hrow + tid] = f2h(s_raw[G + 1][tid]);
+  }
+}
+
+struct Cand {
+  float v;
+  int i;
+};
+
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+__device__ __forceinline__ void block_argmax(float& v, int& i, Cand* s_c) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) argmax_merge(v, i, __shfl_xor(v, o), __shfl_xor(i, o));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) s_c[wave] = Cand{v, i};
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kThreads / kWave; ++w) argmax_merge(v, i, s_c[w].v, s_c[w].i);
+  }
+}
+
+// logits[n] = fp16(sum of chunks); per-block (max, lowest index of max).
+__global__ __launch_bounds__(kThreads) void logits_kernel(const float* __restrict__ part, int vocab, int nchunk,
+                                                          uint16_t* __restrict__ logits, Cand* __restrict__ cand) {
+  __shared__ Cand s_c[kThreads / kWave];
+  const int n = blockIdx.x * kThreads + threadIdx.x;
+  float v = -INFINITY;
+  int i = n < vocab ? n : 0x7fffffff;
+  if (n < vocab) {
+    const uint16_t h = f2h(column_sum(part, n, nchunk));
+    logits[n] = h;
+    v = h2f(h);
+  }
+  block_argmax(v, i, s_c);
+  if (threadIdx.x == 0) cand[blockIdx.x] = Cand{v, i};
+}
+
+__global__ __launch_bounds__(kThreads) void argmax_kernel(const Cand* __restrict__ cand, int ncand,
+                                                          int64_t* __restrict__ tok, int64_t* __restrict__ pos) {
+  __shared__ Cand s_c[kThreads / kWave];
+  float v = -INFINITY;
+  int i = 0x7fffffff;
+  for (int c = threadIdx.x; c < ncand; c += kThreads) argmax_merge(v, i, cand[c].v, cand[c].i);
+  block_argmax(v, i, s_c);
+  if (threadIdx.x == 0) {
+    *tok = i == 0x7fffffff ? 0 : i;
+    *pos = *pos + 1;
+  }
+}
+
+}  // namespace
+}  // namespace lkv
+
+using namespace lkv;
+
+extern "C" int lkv_rmsnorm(const void* x, const void* w, float eps, int64_t M, int64_t Z, void* y, void* stream) {
+  LKV_REQUIRE(M >= 0 && Z > 0 && Z % 8 == 0 && Z < (1 << 30), "rmsnorm: Z=%lld must be a positive multiple of 8",
+              (long long)Z);
+  LKV_REQUIRE(M < 65536, "rmsnorm: M=%lld rows exceeds 65535", (long long)M);
+  if (M == 0) return LKV_OK;
+  LKV_REQUIRE(x && w && y && aligned16(x), "rmsnorm: null pointer or x not 16-byte aligned");
+  const dim3 grid(static_cast<unsigned>((Z + kThreads - 1) / kThreads), static_cast<unsigned>(M));
+  hipLaunchKernelGGL(rmsnorm_kernel, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), eps, static_cast<int>(Z),
+                     static_cast<uint16_t*>(y));
+  LKV_LAUNCH_CHECK("rmsnorm");
+  return LKV_OK;
+}
+
+extern "C" size_t lkv_decode_workspace_bytes(const lkv_decode_dims* dims) {
+  if (check_dims(dims) != LKV_OK) return 0;
+  return make_plan(*dims).total;
+}
+
+extern "C" int lkv_decode_begin(const lkv_decode_dims* dims, const void* embed, const int64_t* tok,
+                                const int64_t* pos, void* x, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int e = check_dims(dims)) return e;
+  const Plan p = make_plan(*dims);
+  if (int e = check_ws(p, workspace, workspace_bytes)) return e;
+  LKV_REQUIRE(embed && tok && pos && x && aligned16(embed) && aligned16(x),
+              "decode_begin: embed and x must be non-null and 16-byte aligned");
+  char* ws = static_cast<char*>(workspace);
+  const unsigned grid = static_cast<unsigned>((dims->hidden / 8 + kThreads - 1) / kThreads);
+  hipLaunchKernelGGL(begin_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(embed), tok, pos, static_cast<uint16_t*>(x),
+                     reinterpret_cast<int32_t*>(ws + p.off_state), dims->hidden, dims->vocab, dims->max_len);
+  LKV_LAUNCH_CHECK("decode_begin");
+  return LKV_OK;
+}
+
+extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_decode_layer* L, void* x, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (int e = check_dims(dims)) return e;
+  const lkv_decode_dims& d = *dims;
+  const Plan p = make_plan(d);
+  if (int e = check_ws(p, workspace, workspace_bytes)) return e;
+  LKV_REQUIRE(L && x && aligned16(x), "decode_layer: null layer or unaligned x");
+  LKV_REQUIRE(L->input_norm && L->post_norm && L->wq && L->wk && L->wv && L->wo && L->wg && L->wu && L->wd,
+              "decode_layer: null weight");
+  LKV_REQUIRE(aligned16(L->wq) && aligned16(L->wk) && aligned16(L->wv) && aligned16(L->wo) && aligned16(L->wg) &&
+                  aligned16(L->wu) && aligned16(L->wd),
+              "decode_layer: weights must be 16-byte aligned");
+  LKV_REQUIRE(L->k_codes && L->k_norms && L->v_codes && L->v_norms && L->k_hot && L->v_hot && L->PiK && L->PiV,
+              "decode_layer: null cache pointer");
+  LKV_REQUIRE(aligned16(L->k_codes) && aligned16(L->v_codes) && aligned16(L->k_hot) && aligned16(L->v_hot),
+              "decode_layer: cache buffers must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* xx = static_cast<uint16_t*>(x);
+  const int32_t* state = reinterpret_cast<const int32_t*>(ws + p.off_state);
+  const int H = static_cast<int>(d.hidden);
+
+  // 1. q|k|v
+  {
+    GemvArgs G{};
+    G.x = xx;
+    G.norm_w = static_cast<const uint16_t*>(L->input_norm);
+    G.eps = d.eps;
+    G.nseg = 3;
+    const void* w[3] = {L->wq, L->wk, L->wv};
+    const int64_t n[3] = {p.nq, p.nkv, p.nkv};
+    const float t[3] = {L->tq, L->tk, L->tv};
+    size_t off = 0;
+    int slab = 0;
+    for (int s = 0; s < 3; ++s) {
+      G.A[s] = static_cast<const uint16_t*>(w[s]);
+      G.a_bytes[s] = static_cast<uint32_t>(d.hidden * n[s] * 2);
+      G.N[s] = static_cast<int>(n[s]);
+      G.t[s] = t[s];
+      G.slab0[s] = slab;
+      G.part_off[s] = off;
+      slab += static_cast<int>(gemv_slabs(n[s]));
+      off += gemv_part_floats(n[s], p.nc_qkv);
+    }
+    G.slab0[3] = slab;
+    G.Z = H;
+    G.nchunk = p.nc_qkv;
+    G.part = reinterpret_cast<float*>(ws + p.off_pqkv);
+    if (int e = gemv_launch(G, p.bz_qkv, false, kInRmsNorm, slab, st)) return e;
+  }
+  // 2. prep
+  {
+    PrepArgs A{};
+    A.part = reinterpret_cast<const float*>(ws + p.off_pqkv);
+    A.off[0] = 0;
+    A.off[1] = gemv_part_floats(p.nq, p.nc_qkv);
+    A.off[2] = A.off[1] + gemv_part_floats(p.nkv, p.nc_qkv);
+    A.nchunk = p.nc_qkv;
+    A.cos = static_cast<const uint16_t*>(d.rope_cos);
+    A.sin = static_cast<const uint16_t*>(d.rope_sin);
+    A.state = state;
+    A.k_hot = static_cast<uint16_t*>(L->k_hot);
+    A.v_hot = static_cast<uint16_t*>(L->v_hot);
+    A.k_codes = static_cast<uint8_t*>(L->k_codes);
+    A.k_norms = static_cast<float*>(L->k_norms);
+    A.v_codes = static_cast<uint8_t*>(L->v_codes);
+    A.v_norms = static_cast<float*>(L->v_norms);
+    A.PiK = L->PiK;
+    A.PiV = L->PiV;
+    A.bounds = d.bounds;
+    A.hot_cap = static_cast<int>(d.hot_cap);
+    A.cap = static_cast<int>(d.cap);
+    A.Hq = static_cast<int>(p.Hq);
+    A.Hkv = static_cast<int>(p.Hkv);
+    A.q16 = reinterpret_cast<uint16_t*>(ws + p.off_q16);
+    A.qrot = reinterpret_cast<float*>(ws + p.off_qrot);
+    if (d.bits == 3)
+      hipLaunchKernelGGL((prep_kernel<3>), dim3(static_cast<unsigned>(p.Hkv)), dim3(kThreads), 0, st, A);
+    else
+      hipLaunchKernelGGL((prep_kernel<4>), dim3(static_cast<unsigned>(p.Hkv)), dim3(kThreads), 0, st, A);
+    LKV_LAUNCH_CHECK("decode prep");
+  }
+  // 3-4. attention
+  {
+    AttnCall c{};
+    c.qrot = reinterpret_cast<const float*>(ws + p.off_qrot);
+    c.q = reinterpret_cast<const uint16_t*>(ws + p.off_q16);
+    c.k_codes = static_cast<const uint8_t*>(L->k_codes);
+    c.k_norms = static_cast<const float*>(L->k_norms);
+    c.v_codes = static_cast<const uint8_t*>(L->v_codes);
+    c.v_norms = static_cast<const float*>(L->v_norms);
+    c.k_hot = static_cast<const uint16_t*>(L->k_hot);
+    c.v_hot = static_cast<const uint16_t*>(L->v_hot);
+    c.PiV = L->PiV;
+    c.centroids = d.centroids;
+    c.seq_len = state + 1;
+    c.partials = reinterpret_cast<float*>(ws + p.off_rec);
+    c.out = reinterpret_cast<uint16_t*>(ws + p.off_attn);
+    c.scale = d.scale;
+    c.max_len = d.max_len;
+    c.B = 1;
+    c.Hq = p.Hq;
+    c.Hkv = p.Hkv;
+    c.cap = d.cap;
+    c.hot_cap = d.hot_cap;
+    c.bits = d.bits;
+    if (int e = attn_launch(c, p.attn, st)) return e;
+  }
+  // 5-6. o_proj, residual
+  {
+    GemvArgs G{};
+    G.x = reinterpret_cast<const uint16_t*>(ws + p.off_attn);
+    G.nseg = 1;
+    G.A[0] = static_cast<const uint16_t*>(L->wo);
+    G.a_bytes[0] = static_cast<uint32_t>(p.nq * d.hidden * 2);
+    G.N[0] = H;
+    G.t[0] = L->to;
+    G.slab0[1] = static_cast<int>(p.sh);
+    G.Z = static_cast<int>(p.nq);
+    G.nchunk = p.nc_o;
+    G.part = reinterpret_cast<float*>(ws + p.off_po);
+    if (int e = gemv_launch(G, p.bz_o, false, kInRaw, static_cast<int>(p.sh), st)) return e;
+    hipLaunchKernelGGL(residual_kernel, dim3(static_cast<unsigned>(p.sh)), dim3(kThreads), 0, st, xx, G.part, H,
+                       p.nc_o);
+    LKV_LAUNCH_CHECK("decode residual");
+  }
+  // 7. gate|up
+  {
+    GemvArgs G{};
+    G.x = xx;
+    G.norm_w = static_cast<const uint16_t*>(L->post_norm);
+    G.eps = d.eps;
+    G.nseg = 1;
+    G.A[0] = static_cast<const uint16_t*>(L->wg);
+    G.A_up = static_cast<const uint16_t*>(L->wu);
+    G.a_bytes[0] = static_cast<uint32_t>(d.hidden * d.ffn * 2);
+    G.N[0] = static_cast<int>(d.ffn);
+    G.t[0] = L->tg;
+    G.t_up = L->tu;
+    G.slab0[1] = static_cast<int>(p.sf);
+    G.Z = H;
+    G.nchunk = p.nc_gu;
+    G.part = reinterpret_cast<float*>(ws + p.off_pgu);
+    G.part_up_off = gemv_part_floats(d.ffn, p.nc_gu);
+    if (int e = gemv_launch(G, p.bz_gu, true, kInRmsNorm, static_cast<int>(p.sf), st)) return e;
+  }
+  // 8-9. down (SwiGLU prologue), residual
+  {
+    GemvArgs G{};
+    G.in_part = reinterpret_cast<const float*>(ws + p.off_pgu);
+    G.in_nslab = static_cast<int>(p.sf);
+    G.in_nchunk = p.nc_gu;
+    G.nseg = 1;
+    G.A[0] = static_cast<const uint16_t*>(L->wd);
+    G.a_bytes[0] = static_cast<uint32_t>(d.ffn * d.hidden * 2);
+    G.N[0] = H;
+    G.t[0] = L->td;
+    G.slab0[1] = static_cast<int>(p.sh);
+    G.Z = static_cast<int>(d.ffn);
+    G.nchunk = p.nc_d;
+    G.part = reinterpret_cast<float*>(ws + p.off_pd);
+    if (int e = gemv_launch(G, p.bz_d, false, kInSwiglu, static_cast<int>(p.sh), st)) return e;
+    hipLaunchKernelGGL(residual_kernel, dim3(static_cast<unsigned>(p.sh)), dim3(kThreads), 0, st, xx, G.part, H,
+                       p.nc_d);
+    LKV_LAUNCH_CHECK("decode residual");
+  }
+  return LKV_OK;
+}
+
+extern "C" int lkv_decode_head(const lkv_decode_dims* dims, const void* final_norm, const void* lm_head, const void* x,
+                               void* logits, int64_t* tok, int64_t* pos, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  if (int e = check_dims(dims)) return e;
+  const lkv_decode_dims& d = *dims;
+  const Plan p = make_plan(d);
+  if (int e = check_ws(p, workspace, workspace_bytes)) return e;
+  LKV_REQUIRE(final_norm && lm_head && x && logits && tok && pos, "decode_head: null pointer");
+  LKV_REQUIRE(aligned16(lm_head) && aligned16(x), "decode_head: lm_head and x must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  GemvArgs G{};
+  G.x = static_cast<const uint16_t*>(x);
+  G.norm_w = static_cast<const uint16_t*>(final_norm);
+  G.eps = d.eps;
+  G.nseg = 1;
+  G.A[0] = static_cast<const uint16_t*>(lm_head);
+  G.a_bytes[0] = static_cast<uint32_t>(d.hidden * d.vocab * 2);
+  G.N[0] = static_cast<int>(d.vocab);
+  G.t[0] = 0.f;
+  G.slab0[1] = static_cast<int>(p.svoc);
+  G.Z = static_cast<int>(d.hidden);
+  G.nchunk = p.nc_lm;
+  G.part = reinterpret_cast<float*>(ws + p.off_plm);
+  if (int e = gemv_launch(G, p.bz_lm, false, kInRmsNorm, static_cast<int>(p.svoc), st)) return e;
+  Cand* cand = reinterpret_cast<Cand*>(ws + p.off_cand);
+  hipLaunchKernelGGL(logits_kernel, dim3(static_cast<unsigned>(p.svoc)), dim3(kThreads), 0, st, G.part,
+                     static_cast<int>(d.vocab), p.nc_lm, static_cast<uint16_t*>(logits), cand);
+  LKV_LAUNCH_CHECK("decode logits");
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kThreads), 0, st, cand, static_cast<int>(p.svoc), tok, pos);
+  LKV_LAUNCH_CHECK("decode argmax");
+  return LKV_OK;
+}

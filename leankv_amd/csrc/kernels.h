@@ -1,0 +1,147 @@
+// Internal interfaces shared by the kernel translation units: the sparse GEMV
+// launcher with its input prologues, the split-K partial-sum layout, and the
+// packed-KV attention launcher.  Not part of the C ABI.
+#pragma once
+
+#include "common.h"
+
+namespace lkv {
+
+// ------------------------------------------------------------------ GEMV
+// A GEMV launch covers column slabs of kGemvBN outputs x row chunks of BZ
+// inputs.  Each (slab, chunk) block writes kGemvBN fp32 partial sums; the sum
+// over chunks, in chunk order, happens in a consumer.  Partials of one matrix
+// are laid out [slab][chunk][kGemvBN].
+constexpr int kGemvThreads = 256;
+constexpr int kGemvBN = 256;
+constexpr int kMaxSeg = 3;
+
+enum GemvIn {
+  kInRaw = 0,      // x fp16 as given
+  kInRmsNorm = 1,  // x = RMSNorm(x_resid) * norm_w, computed per block
+  kInSwiglu = 2,   // x = SwiGLU(gate, up), gate/up summed from partials
+};
+
+struct GemvArgs {
+  const uint16_t* x;       // kInRaw / kInRmsNorm: fp16 [Z], 16-byte aligned
+  const uint16_t* norm_w;  // kInRmsNorm: fp16 [Z]
+  float eps;
+  const float* in_part;    // kInSwiglu: [2][in_nslab][in_nchunk][kGemvBN] (gate, then up)
+  int in_nslab, in_nchunk;
+  // Segments: weight matrices that share x, each [Z][N[s]] column-major fp16
+  // (row z = the N[s] weights of input z).  Global column slab g belongs to
+  // segment s when slab0[s] <= g < slab0[s + 1].
+  int nseg;
+  const uint16_t* A[kMaxSeg];
+  const uint16_t* A_up;    // dual mode: the up matrix, same shape as A[0]
+  uint32_t a_bytes[kMaxSeg];
+  int N[kMaxSeg];
+  float t[kMaxSeg];
+  float t_up;
+  int slab0[kMaxSeg + 1];
+  int Z, nchunk;
+  float* part;             // partials of segment s at part + part_off[s]
+  size_t part_off[kMaxSeg];
+  size_t part_up_off;      // dual mode: the up matrix's partials
+  uint16_t* y;             // non-null only when nchunk == 1 and nseg == 1: write fp16 (SwiGLU if dual)
+};
+
+int gemv_pick_bz(int64_t slabs, int64_t Z);
+int gemv_launch(const GemvArgs& G, int bz, bool dual, int mode, int nslab_total, hipStream_t st);
+
+inline int64_t gemv_slabs(int64_t N) { return (N + kGemvBN - 1) / kGemvBN; }
+inline int64_t gemv_chunks(int64_t Z, int bz) { return Z > 0 ? (Z + bz - 1) / bz : 1; }
+inline size_t gemv_part_floats(int64_t N, int64_t nchunk) {
+  return static_cast<size_t>(gemv_slabs(N)) * nchunk * kGemvBN;
+}
+
+// Column n of a [slab][chunk][kGemvBN] partial array summed over chunks in
+// chunk order, starting from 0.  Loads are issued 16 at a time.
+__device__ __forceinline__ float column_sum(const float* __restrict__ P, int n, int nchunk) {
+  constexpr int kBatch = 16;
+  const float* p = P + static_cast<size_t>(n / kGemvBN) * nchunk * kGemvBN + (n % kGemvBN);
+  float s = 0.f;
+  for (int k0 = 0; k0 < nchunk; k0 += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) v[i] = (k0 + i < nchunk) ? p[static_cast<size_t>(k0 + i) * kGemvBN] : 0.f;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) s += v[i];
+  }
+  return s;
+}
+
+// 1 / sqrt(mean(x^2) + eps) over fp16 x[0..Z) in fp32, computed by a whole
+// block of kGemvThreads threads (every thread gets the result).  Fixed
+// summation order: thread t accumulates x[8t .. 8t+7], x[8t + 2048 ..], ...
+// with fmaf, then a wave butterfly, then the 4 wave sums in order.  Requires
+// Z % 8 == 0 and 16-byte aligned x.  Every RMSNorm of this library goes
+// through it, so all of them round identically.
+__device__ __forceinline__ float rms_rstd(const uint16_t* __restrict__ x, int Z, float eps, float* s_wsum) {
+  const int tid = threadIdx.x;
+  float ss = 0.f;
+  for (int z = tid * 8; z < Z; z += kGemvThreads * 8) {
+    const uint4 u = *reinterpret_cast<const uint4*>(x + z);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = h2f(static_cast<uint16_t>(w[i] & 0xffffu));
+      const float b = h2f(static_cast<uint16_t>(w[i] >> 16));
+      ss = fmaf(a, a, ss);
+      ss = fmaf(b, b, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & (kWave - 1)) == 0) s_wsum[tid / kWave] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kGemvThreads / kWave; ++w) tot += s_wsum[w];
+  return rsqrtf(tot / static_cast<float>(Z) + eps);
+}
+
+// HF MistralRMSNorm output element (modeling_mistral.py:190-197): x * rstd in
+// fp32 cast to fp16, times the fp16 weight, product rounded to fp16.
+__device__ __forceinline__ float rms_apply(uint16_t x, uint16_t w, float rstd) {
+  return h2f(f2h(h2f(w) * h2f(f2h(h2f(x) * rstd))));
+}
+
+// SwiGLU with the rounding of the eager fp16 torch sequence of
+// transformers/models/mistral/modeling_mistral.py:46-47 on fp16 projection
+// outputs: silu(fp16 g) -> fp16, times fp16 u -> fp16.
+__device__ __forceinline__ uint16_t swiglu_f16(float g, float u) {
+  const float g16 = h2f(f2h(g));
+  const float u16 = h2f(f2h(u));
+  const float s16 = h2f(f2h(g16 / (1.0f + expf(-g16))));
+  return f2h(s16 * u16);
+}
+
+// ------------------------------------------------------------- attention
+struct AttnPlan {
+  int nsplit, split_tokens;
+  size_t qrot_off, part_off, total;
+};
+AttnPlan attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_cap);
+
+struct AttnCall {
+  const float* qrot;        // [B, Hq, 128] fp32 = q @ PiK^T
+  const uint16_t* q;        // [B, Hq, 128] fp16 (the fp16 hot window uses the unrotated query)
+  const uint8_t* k_codes;   // [B, Hkv, cap, 64]
+  const float* k_norms;     // [B, Hkv, cap]
+  const uint8_t* v_codes;
+  const float* v_norms;
+  const uint16_t* k_hot;    // [B, Hkv, hot_cap, 128] ring, token t in slot t % hot_cap
+  const uint16_t* v_hot;
+  const float* PiV;         // [128, 128]
+  const float* centroids;   // [2^bits]
+  const int32_t* seq_len;   // device scalar: tokens in the cache (after this step's append)
+  float* partials;          // split records (workspace)
+  uint16_t* out;            // [B, Hq, 128] fp16
+  float scale;
+  int64_t max_len, B, Hq, Hkv, cap, hot_cap;
+  int bits;
+};
+// Launch the split and combine kernels (q already rotated into call.qrot).
+int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st);
+
+}  // namespace lkv

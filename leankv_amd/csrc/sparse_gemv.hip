@@ -1,4 +1,5 @@
-// TEAL magnitude-thresholded sparse GEMV and the fused gate/up SwiGLU variant.
+// TEAL magnitude-thresholded sparse GEMV, the fused gate/up SwiGLU variant,
+// and the input prologues the decode step fuses into them.
 //
 // Semantics: leankv/teal/kernels/sparse_gemv.py:61-87 (one program sums
 // A[z, n] * x[z] over the rows z of its block whose |x[z]| > threshold) and the
@@ -6,34 +7,38 @@
 // prepare_weight_for_sparse_gemv (:229-234): row z of A[Z][N] is N contiguous
 // fp16 values, so a surviving activation selects one contiguous weight row.
 //
-// Work decomposition:
-//   grid = (N / BN column slabs) x (Z / BZ row chunks), 256 threads per block.
-//   1. Compaction: the block reads its BZ activations, tests |x| > t, and
-//      builds the list of surviving rows in LDS with a wave ballot and mbcnt
-//      lane prefix (plus a 4-entry cross-wave prefix).  The list is padded to
-//      a whole number of streaming batches with copies of its last row and a
+// Work decomposition: grid = (column slabs of 256) x (row chunks of BZ),
+// 256 threads per block.
+//   0. Input prologue: x as given, or computed from what produced it --
+//      RMSNorm of the fp16 residual stream (each block reads the whole 8 KB
+//      vector for the sum of squares), or SwiGLU of the gate/up partial sums
+//      (each block sums the chunks of its own BZ inputs) -- so a projection
+//      input never round-trips through a kernel of its own.
+//   1. Compaction: the block tests |x| > t on its BZ activations and builds
+//      the list of surviving rows in LDS with a wave ballot and mbcnt lane
+//      prefix (plus a 4-entry cross-wave prefix).  The list is padded to a
+//      whole number of streaming batches with copies of its last row and a
 //      zero activation: padded loads hit the line just fetched and add 0.
-//   2. Streaming: BN/8 lanes cover one row segment with 16-byte buffer loads
-//      (SGPR descriptor + 32-bit offset); the 256/(BN/8) row slots of the
-//      block walk the list U rows at a time, so U independent 16-byte loads
-//      per lane are in flight.  fp16 x fp32 -> fp32 FMAs.
-//   3. The row slots are reduced through LDS into BN fp32 column sums.
-//   4. Split-K over the row chunks, two variants:
-//      * ticket: the block writes its partials, one thread releases them at
-//        agent scope (one L2 write-back per block) and takes a ticket; the
-//        last block of the slab sums all chunks in chunk order and writes fp16.
-//      * two kernels: the block only writes partials; gemv_reduce_kernel sums
-//        them after the kernel boundary.
-//      Both reduce in a fixed order, so y is deterministic (the reference
-//      accumulates with fp16 atomic_add, :87).
+//   2. Streaming: 32 lanes cover one 512-byte row segment with 16-byte buffer
+//      loads (SGPR descriptor + 32-bit offset; loads past the end read 0); the
+//      8 row slots of the block walk the list 8 rows at a time, so 8
+//      independent 16-byte loads per lane are in flight.  fp16 x fp32 -> fp32.
+//   3. The row slots are reduced through LDS into 256 fp32 column sums.
+//   4. The block writes its partial sums.  The reduction over chunks happens
+//      after the kernel boundary, in chunk order (so results are
+//      deterministic, unlike the reference's fp16 atomic_add, :87): in
+//      gemv_reduce_kernel for the standalone entry points, or in the
+//      prologue of whichever decode-step kernel consumes the projection.
+//   Weight matrices that share x (q/k/v of a layer) are one launch: column
+//   slabs are numbered across the segments.
 #include <stdlib.h>
 
-#include "common.h"
+#include "kernels.h"
 
 namespace lkv {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kUnroll = 8;
 
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
@@ -51,10 +56,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 
 // Stream the padded survivor list: total is a multiple of kUnroll * SLOTS.
-template <int SLOTS, int kUnroll>
+template <int SLOTS>
 __device__ __forceinline__ void stream_rows(__amdgpu_buffer_rsrc_t A, uint32_t row_bytes, uint32_t col_bytes,
-                                            const int* __restrict__ idx, const float* __restrict__ xv,
-                                            int total, int slot, int aux, float (&acc)[8]) {
+                                            const int* __restrict__ idx, const float* __restrict__ xv, int total,
+                                            int slot, float (&acc)[8]) {
   for (int s = slot; s < total; s += kUnroll * SLOTS) {
     int r[kUnroll];
     float xs[kUnroll];
@@ -66,96 +71,122 @@ __device__ __forceinline__ void stream_rows(__amdgpu_buffer_rsrc_t A, uint32_t r
     u32x4v w[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
-      w[u] = aux ? __builtin_amdgcn_raw_buffer_load_b128(A, static_cast<uint32_t>(r[u]) * row_bytes + col_bytes, 0, 2)
-                 : __builtin_amdgcn_raw_buffer_load_b128(A, static_cast<uint32_t>(r[u]) * row_bytes + col_bytes, 0, 0);
+      w[u] = __builtin_amdgcn_raw_buffer_load_b128(A, static_cast<uint32_t>(r[u]) * row_bytes + col_bytes, 0, 0);
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) fma8(acc, w[u], xs[u]);
   }
 }
 
-// Reduce the SLOTS row-slot accumulators of the block into out[0..BN/256).
-template <int BN, int SLOTS>
-__device__ __forceinline__ void block_reduce_cols(float* s_red, const float (&acc)[8], int slot, int c,
-                                                  float* out_cols) {
-  float4* dst = reinterpret_cast<float4*>(s_red + slot * BN + c * 8);
-  dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-  dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
-  __syncthreads();
+// x[z0 .. z0 + BZ) into s_x (0 past Z) for the three input modes.
+template <int BZ, int MODE>
+__device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float* s_x, float* s_wsum) {
+  constexpr int E = BZ / kGemvThreads;  // inputs per thread
+  const int tid = threadIdx.x;
+  const int Z = G.Z;
+  if (MODE == kInRmsNorm) {
+    const float rstd = rms_rstd(G.x, Z, G.eps, s_wsum);
 #pragma unroll
-  for (int j = 0; j < BN / kThreads; ++j) {
-    const int cc = threadIdx.x + j * kThreads;
-    float s = 0.f;
+    for (int e = 0; e < E; ++e) {
+      const int i = e * kGemvThreads + tid;
+      const int z = z0 + i;
+      s_x[i] = z < Z ? rms_apply(G.x[z], G.norm_w[z], rstd) : 0.f;
+    }
+  } else if (MODE == kInSwiglu) {
+    // h = SwiGLU(sum of gate chunks, sum of up chunks); chunk loads for all E
+    // inputs of the thread are issued together, 8 chunks deep.
+    const size_t mat = static_cast<size_t>(G.in_nslab) * G.in_nchunk * kGemvBN;
+    const int nc = G.in_nchunk;
+    float g[E], u[E];
+    const float* pg[E];
 #pragma unroll
-    for (int sl = 0; sl < SLOTS; ++sl) s += s_red[sl * BN + cc];
-    out_cols[j] = s;
+    for (int e = 0; e < E; ++e) {
+      const int z = min(z0 + e * kGemvThreads + tid, Z - 1);
+      pg[e] = G.in_part + static_cast<size_t>(z / kGemvBN) * nc * kGemvBN + (z % kGemvBN);
+      g[e] = 0.f;
+      u[e] = 0.f;
+    }
+    for (int k0 = 0; k0 < nc; k0 += 8) {
+      float vg[E][8], vu[E][8];
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const bool ok = k0 + i < nc;
+          vg[e][i] = ok ? pg[e][static_cast<size_t>(k0 + i) * kGemvBN] : 0.f;
+          vu[e][i] = ok ? pg[e][mat + static_cast<size_t>(k0 + i) * kGemvBN] : 0.f;
+        }
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          g[e] += vg[e][i];
+          u[e] += vu[e][i];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = e * kGemvThreads + tid;
+      s_x[i] = z0 + i < Z ? h2f(swiglu_f16(g[e], u[e])) : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = e * kGemvThreads + tid;
+      s_x[i] = z0 + i < Z ? h2f(G.x[z0 + i]) : 0.f;
+    }
   }
   __syncthreads();
 }
 
-// Sum nchunk partials spaced `stride` floats apart, in chunk order.  Loads are
-// issued 16 at a time so the sum costs ceil(nchunk / 16) memory round trips
-// instead of nchunk.
-__device__ __forceinline__ float sum_chunks(const float* __restrict__ P, size_t stride, int nchunk) {
-  constexpr int kBatch = 16;
-  float s = 0.f;
-  for (int k0 = 0; k0 < nchunk; k0 += kBatch) {
-    float v[kBatch];
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) v[i] = (k0 + i < nchunk) ? P[static_cast<size_t>(k0 + i) * stride] : 0.f;
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) s += v[i];
-  }
-  return s;
-}
-
-// SwiGLU epilogue with the rounding of the eager fp16 torch sequence
-// silu(fp16 g) -> fp16, times fp16 u -> fp16.
-__device__ __forceinline__ uint16_t swiglu_f16(float g, float u) {
-  const float g16 = h2f(f2h(g));
-  const float u16 = h2f(f2h(u));
-  const float s16 = h2f(f2h(g16 / (1.0f + expf(-g16))));
-  return f2h(s16 * u16);
-}
-
-template <int BN, int BZ, bool DUAL, bool TICKET, int kUnroll>
-__global__ __launch_bounds__(kThreads) void sparse_gemv_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ A0, const uint16_t* __restrict__ A1,
-    uint32_t a_bytes, float t0, float t1, int N, int Z, int nchunk, uint16_t* __restrict__ y,
-    float* __restrict__ partials, unsigned* __restrict__ tickets, int aux) {
-  constexpr int LPR = BN / 8;            // lanes per row segment
-  constexpr int SLOTS = kThreads / LPR;  // rows processed side by side
+template <int BZ, bool DUAL, int MODE>
+__global__ __launch_bounds__(kGemvThreads) void sparse_gemv_kernel(GemvArgs G) {
+  constexpr int BN = kGemvBN;
+  constexpr int LPR = BN / 8;                // lanes per row segment
+  constexpr int SLOTS = kGemvThreads / LPR;  // rows processed side by side
   constexpr int NL = DUAL ? 2 : 1;
-  constexpr int PAD = kUnroll * SLOTS;   // list granularity
-  static_assert(BN % kThreads == 0 && LPR <= kThreads, "BN must be 256..2048");
+  constexpr int PAD = kUnroll * SLOTS;       // list granularity
+  static_assert(BZ % kGemvThreads == 0, "BZ must be a multiple of 256");
 
   __shared__ int s_idx[NL][BZ + PAD];
   __shared__ float s_xv[NL][BZ + PAD];
-  __shared__ int s_cnt[NL][kThreads / kWave];
+  __shared__ float s_x[BZ];
+  __shared__ int s_cnt[NL][kGemvThreads / kWave];
+  __shared__ float s_wsum[kGemvThreads / kWave];
   __shared__ __align__(16) float s_red[SLOTS * BN];
-  __shared__ int s_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const int slab = blockIdx.x;
+  const int gslab = blockIdx.x;
   const int chunk = blockIdx.y;
-  const int nslab = gridDim.x;
-  const int n0 = slab * BN;
   const int z0 = chunk * BZ;
+  const int Z = G.Z;
+
+  int seg = 0;
+#pragma unroll
+  for (int s = 1; s < kMaxSeg; ++s)
+    if (s < G.nseg && gslab >= G.slab0[s]) seg = s;
+  const int slab = gslab - G.slab0[seg];
+  const int N = G.N[seg];
+  const float t0 = G.t[seg];
+  const int n0 = slab * BN;
+
+  input_prologue<BZ, MODE>(G, z0, s_x, s_wsum);
 
   // ---- 1. compaction of surviving activation rows
   int total[NL];
 #pragma unroll
   for (int l = 0; l < NL; ++l) total[l] = 0;
-  for (int base = 0; base < BZ; base += kThreads) {
+#pragma unroll
+  for (int base = 0; base < BZ; base += kGemvThreads) {
     const int z = z0 + base + tid;
-    const bool valid = (base + tid < BZ) && (z < Z);
-    const float v = valid ? h2f(x[z]) : 0.f;
+    const bool valid = z < Z;
+    const float v = s_x[base + tid];
     const float a = fabsf(v);
     bool pred[NL];
     uint64_t mask[NL];
     pred[0] = valid && (a > t0);
-    if (DUAL) pred[NL - 1] = valid && (a > t1);
+    if (DUAL) pred[NL - 1] = valid && (a > G.t_up);
 #pragma unroll
     for (int l = 0; l < NL; ++l) {
       mask[l] = wave_ballot(pred[l]);
@@ -166,7 +197,7 @@ __global__ __launch_bounds__(kThreads) void sparse_gemv_kernel(
     for (int l = 0; l < NL; ++l) {
       int off = total[l], tot = 0;
 #pragma unroll
-      for (int w = 0; w < kThreads / kWave; ++w) {
+      for (int w = 0; w < kGemvThreads / kWave; ++w) {
         const int cw = s_cnt[l][w];
         off += (w < wave) ? cw : 0;
         tot += cw;
@@ -197,6 +228,7 @@ __global__ __launch_bounds__(kThreads) void sparse_gemv_kernel(
   const int slot = tid / LPR;
   const int col = n0 + c * 8;
   const uint32_t row_bytes = static_cast<uint32_t>(N) * 2u;
+  const uint32_t a_bytes = G.a_bytes[seg];
   // Columns past N would alias the next row: push them past the descriptor end.
   const uint32_t col_bytes = col < N ? static_cast<uint32_t>(col) * 2u : a_bytes;
   float acc[NL][8];
@@ -204,189 +236,106 @@ __global__ __launch_bounds__(kThreads) void sparse_gemv_kernel(
   for (int l = 0; l < NL; ++l)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[l][j] = 0.f;
-  stream_rows<SLOTS, kUnroll>(make_rsrc(A0, a_bytes), row_bytes, col_bytes, s_idx[0], s_xv[0], total[0], slot,
-                              aux, acc[0]);
+  stream_rows<SLOTS>(make_rsrc(G.A[seg], a_bytes), row_bytes, col_bytes, s_idx[0], s_xv[0], total[0], slot, acc[0]);
   if (DUAL)
-    stream_rows<SLOTS, kUnroll>(make_rsrc(A1, a_bytes), row_bytes, col_bytes, s_idx[NL - 1], s_xv[NL - 1],
-                                total[NL - 1], slot, aux, acc[NL - 1]);
+    stream_rows<SLOTS>(make_rsrc(G.A_up, a_bytes), row_bytes, col_bytes, s_idx[NL - 1], s_xv[NL - 1], total[NL - 1],
+                       slot, acc[NL - 1]);
 
   // ---- 3. cross-slot reduction through LDS
-  float sums[NL][BN / kThreads];
-#pragma unroll
-  for (int l = 0; l < NL; ++l) block_reduce_cols<BN, SLOTS>(s_red, acc[l], slot, c, sums[l]);
-
-  if (nchunk == 1) {
-#pragma unroll
-    for (int j = 0; j < BN / kThreads; ++j) {
-      const int n = n0 + tid + j * kThreads;
-      if (n < N) y[n] = DUAL ? swiglu_f16(sums[0][j], sums[NL - 1][j]) : f2h(sums[0][j]);
-    }
-    return;
-  }
-
-  // ---- 4. split-K partials
-  const size_t mat_stride = static_cast<size_t>(nslab) * nchunk * BN;
+  float sums[NL];
 #pragma unroll
   for (int l = 0; l < NL; ++l) {
-    float* P = partials + l * mat_stride + (static_cast<size_t>(slab) * nchunk + chunk) * BN;
+    float4* dst = reinterpret_cast<float4*>(s_red + slot * BN + c * 8);
+    dst[0] = make_float4(acc[l][0], acc[l][1], acc[l][2], acc[l][3]);
+    dst[1] = make_float4(acc[l][4], acc[l][5], acc[l][6], acc[l][7]);
+    __syncthreads();
+    float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < BN / kThreads; ++j) P[tid + j * kThreads] = sums[l][j];
+    for (int sl = 0; sl < SLOTS; ++sl) s += s_red[sl * BN + tid];
+    sums[l] = s;
+    __syncthreads();
   }
-  if (!TICKET) return;
-  // The barrier completes every thread's partial stores (to this XCD's L2);
-  // one agent-scope release by thread 0 then publishes them all.  Only the
-  // block that takes the last ticket pays the acquire (L1/L2 invalidate).
-  __syncthreads();
-  if (tid == 0) {
-    fence_release_agent();
-    const bool last = ticket_add(&tickets[slab]) == static_cast<unsigned>(nchunk - 1);
-    if (last) fence_acquire_agent();
-    s_last = last;
+
+  // ---- 4. output: fp16 directly (single chunk) or partial sums
+  if (G.y != nullptr) {
+    if (n0 + tid < N) G.y[n0 + tid] = DUAL ? swiglu_f16(sums[0], sums[NL - 1]) : f2h(sums[0]);
+    return;
   }
-  __syncthreads();
-  if (!s_last) return;
 #pragma unroll
-  for (int j = 0; j < BN / kThreads; ++j) {
-    const int cc = tid + j * kThreads;
-    const int n = n0 + cc;
-    float r[NL];
-#pragma unroll
-    for (int l = 0; l < NL; ++l)
-      r[l] = sum_chunks(partials + l * mat_stride + static_cast<size_t>(slab) * nchunk * BN + cc, BN, nchunk);
-    if (n < N) y[n] = DUAL ? swiglu_f16(r[0], r[NL - 1]) : f2h(r[0]);
+  for (int l = 0; l < NL; ++l) {
+    float* P = G.part + (l == 0 ? G.part_off[seg] : G.part_up_off) +
+               (static_cast<size_t>(slab) * G.nchunk + chunk) * BN;
+    P[tid] = sums[l];
   }
-  if (tid == 0) ticket_reset(&tickets[slab]);
 }
 
-// Second kernel of the two-kernel split-K: y[n] = sum over chunks, in order.
-template <int BN, bool DUAL>
-__global__ __launch_bounds__(kThreads) void gemv_reduce_kernel(const float* __restrict__ partials, int N, int nslab,
-                                                               int nchunk, uint16_t* __restrict__ y) {
-  const int n = blockIdx.x * kThreads + threadIdx.x;
+// y[n] = sum over chunks of the partials, in chunk order (standalone entry points).
+template <bool DUAL>
+__global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(const float* __restrict__ partials, int N, int nslab,
+                                                                   int nchunk, uint16_t* __restrict__ y) {
+  const int n = blockIdx.x * kGemvThreads + threadIdx.x;
   if (n >= N) return;
-  const int slab = n / BN, cc = n % BN;
-  const size_t mat_stride = static_cast<size_t>(nslab) * nchunk * BN;
-  const float* P = partials + static_cast<size_t>(slab) * nchunk * BN + cc;
-  const float g = sum_chunks(P, BN, nchunk);
+  const float g = column_sum(partials, n, nchunk);
   if (DUAL)
-    y[n] = swiglu_f16(g, sum_chunks(P + mat_stride, BN, nchunk));
+    y[n] = swiglu_f16(g, column_sum(partials + static_cast<size_t>(nslab) * nchunk * kGemvBN, n, nchunk));
   else
     y[n] = f2h(g);
 }
 
-struct GemvCfg {
-  int bn;
-  int bz;
-  bool ticket;
-  int unroll;
-  int aux;
-};
+}  // namespace
 
-// Shapes are chosen so the grid holds ~1.5-2 blocks per CU while each block
-// streams as many rows as possible (fewer partials, fewer per-block costs).
-GemvCfg pick_cfg(int64_t N, int64_t Z, bool dual) {
-  GemvCfg cfg{256, 512, false, 8, 0};
-  const char* mode = getenv("LKV_GEMV_SPLITK");  // "two" (default) or "ticket"
-  if (mode && mode[0] == 't' && mode[1] == 'i') cfg.ticket = true;
-  if (const char* u = getenv("LKV_GEMV_UNROLL")) cfg.unroll = atoi(u) == 16 ? 16 : 8;
-  if (const char* a = getenv("LKV_GEMV_NT")) cfg.aux = atoi(a) ? 1 : 0;
-  const char* env = getenv(dual ? "LKV_GATEUP_CFG" : "LKV_GEMV_CFG");
-  if (env) {
-    int bn = 0, bz = 0;
-    if (sscanf(env, "%d,%d", &bn, &bz) == 2) {
-      cfg.bn = bn;
-      cfg.bz = bz;
-      return cfg;
-    }
+// Row-chunk size for a GEMV with Z inputs over `slabs` column slabs: the
+// largest chunk that still gives ~1.5 blocks per CU (fewer partials and
+// per-block costs), overridable with LKV_GEMV_BZ for tuning sweeps.
+int gemv_pick_bz(int64_t slabs, int64_t Z) {
+  if (const char* env = getenv("LKV_GEMV_BZ")) {
+    const int bz = atoi(env);
+    if (bz == 256 || bz == 512 || bz == 1024) return bz;
   }
   const int64_t target = 3 * static_cast<int64_t>(device_cu_count()) / 2;
-  const int64_t nslab = (N + cfg.bn - 1) / cfg.bn;
-  static const int bzs[] = {1024, 512, 256};
-  for (int bz : bzs) {
-    const int64_t nchunk = (Z + bz - 1) / bz;
-    if (nslab * nchunk >= target) {
-      cfg.bz = bz;
-      return cfg;
-    }
-  }
-  cfg.bz = 256;
-  return cfg;
+  static const int bzs[] = {1024, 512};
+  for (int bz : bzs)
+    if (slabs * gemv_chunks(Z, bz) >= target) return bz;
+  return 256;
 }
 
-size_t ws_bytes_for(const GemvCfg& c, int64_t N, int64_t Z, bool dual) {
-  const int64_t nslab = (N + c.bn - 1) / c.bn;
-  const int64_t nchunk = Z > 0 ? (Z + c.bz - 1) / c.bz : 1;
-  return kTicketBytes + static_cast<size_t>(dual ? 2 : 1) * nslab * nchunk * c.bn * sizeof(float);
+namespace {
+
+template <int BZ>
+bool launch_bz(const GemvArgs& G, bool dual, int mode, dim3 grid, hipStream_t st) {
+  const dim3 blk(kGemvThreads);
+  switch (mode * 2 + (dual ? 1 : 0)) {
+    case kInRaw * 2: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, false, kInRaw>), grid, blk, 0, st, G); return true;
+    case kInRaw * 2 + 1: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, true, kInRaw>), grid, blk, 0, st, G); return true;
+    case kInRmsNorm * 2: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, false, kInRmsNorm>), grid, blk, 0, st, G); return true;
+    case kInRmsNorm * 2 + 1: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, true, kInRmsNorm>), grid, blk, 0, st, G); return true;
+    case kInSwiglu * 2: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, false, kInSwiglu>), grid, blk, 0, st, G); return true;
+    default: return false;
+  }
 }
 
-template <bool DUAL>
-int launch(const GemvCfg& cfg, const void* x, const void* A0, const void* A1, float t0, float t1, int64_t N,
-           int64_t Z, void* y, void* ws, hipStream_t st) {
-  const int64_t nslab = (N + cfg.bn - 1) / cfg.bn;
-  const int64_t nchunk = Z > 0 ? (Z + cfg.bz - 1) / cfg.bz : 1;
-  if (nslab > kMaxTickets) {
-    set_error("sparse_gemv: N=%lld needs %lld column slabs, more than %lld tickets", (long long)N,
-              (long long)nslab, (long long)kMaxTickets);
-    return LKV_ERR_INVALID;
-  }
-  unsigned* tickets = static_cast<unsigned*>(ws);
-  float* partials = reinterpret_cast<float*>(static_cast<char*>(ws) + kTicketBytes);
-  dim3 grid(static_cast<unsigned>(nslab), static_cast<unsigned>(nchunk));
-  const uint16_t* xx = static_cast<const uint16_t*>(x);
-  const uint16_t* a0 = static_cast<const uint16_t*>(A0);
-  const uint16_t* a1 = static_cast<const uint16_t*>(A1);
-  uint16_t* yy = static_cast<uint16_t*>(y);
-  const uint32_t a_bytes = static_cast<uint32_t>(N * Z * 2);
-  const int n = static_cast<int>(N), z = static_cast<int>(Z), nc = static_cast<int>(nchunk);
-  const bool ticket = cfg.ticket || nchunk == 1;
-  bool launched = false;
-#define LKV_GEMV_LAUNCH(BN_, BZ_, T_, U_)                                                                    \
-  hipLaunchKernelGGL((sparse_gemv_kernel<BN_, BZ_, DUAL, T_, U_>), grid, dim3(kThreads), 0, st, xx, a0, a1,      \
-                     a_bytes, t0, t1, n, z, nc, yy, partials, tickets, cfg.aux)
-#define LKV_GEMV_CASE(BN_, BZ_)                                                                              \
-  if (!launched && cfg.bn == BN_ && cfg.bz == BZ_) {                                                          \
-    if (ticket) {                                                                                            \
-      if (cfg.unroll == 16) LKV_GEMV_LAUNCH(BN_, BZ_, true, 16); else LKV_GEMV_LAUNCH(BN_, BZ_, true, 8);    \
-    } else {                                                                                                 \
-      if (cfg.unroll == 16) LKV_GEMV_LAUNCH(BN_, BZ_, false, 16); else LKV_GEMV_LAUNCH(BN_, BZ_, false, 8);  \
-    }                                                                                                        \
-    launched = true;                                                                                         \
-  }
-  LKV_GEMV_CASE(256, 256)
-  LKV_GEMV_CASE(256, 512)
-  LKV_GEMV_CASE(256, 1024)
-  LKV_GEMV_CASE(512, 512)
-  LKV_GEMV_CASE(1024, 256)
-#undef LKV_GEMV_CASE
-#undef LKV_GEMV_LAUNCH
-  if (!launched) {
-    set_error("sparse_gemv: no kernel instantiated for BN=%d BZ=%d", cfg.bn, cfg.bz);
+}  // namespace
+
+int gemv_launch(const GemvArgs& G, int bz, bool dual, int mode, int nslab_total, hipStream_t st) {
+  if (nslab_total <= 0) return LKV_OK;
+  const dim3 grid(static_cast<unsigned>(nslab_total), static_cast<unsigned>(G.nchunk));
+  bool ok = false;
+  if (bz == 256) ok = launch_bz<256>(G, dual, mode, grid, st);
+  else if (bz == 512) ok = launch_bz<512>(G, dual, mode, grid, st);
+  else if (bz == 1024) ok = launch_bz<1024>(G, dual, mode, grid, st);
+  if (!ok) {
+    set_error("sparse_gemv: no kernel for chunk %d, mode %d, dual %d", bz, mode, dual ? 1 : 0);
     return LKV_ERR_INVALID;
   }
   LKV_LAUNCH_CHECK("sparse_gemv");
-  if (!ticket) {
-    const unsigned rgrid = static_cast<unsigned>((N + kThreads - 1) / kThreads);  // kReduceThreads per block
-    switch (cfg.bn) {
-      case 256:
-        hipLaunchKernelGGL((gemv_reduce_kernel<256, DUAL>), dim3(rgrid), dim3(kThreads), 0, st, partials, n,
-                           static_cast<int>(nslab), nc, yy);
-        break;
-      case 512:
-        hipLaunchKernelGGL((gemv_reduce_kernel<512, DUAL>), dim3(rgrid), dim3(kThreads), 0, st, partials, n,
-                           static_cast<int>(nslab), nc, yy);
-        break;
-      case 1024:
-        hipLaunchKernelGGL((gemv_reduce_kernel<1024, DUAL>), dim3(rgrid), dim3(kThreads), 0, st, partials, n,
-                           static_cast<int>(nslab), nc, yy);
-        break;
-      default:
-        hipLaunchKernelGGL((gemv_reduce_kernel<2048, DUAL>), dim3(rgrid), dim3(kThreads), 0, st, partials, n,
-                           static_cast<int>(nslab), nc, yy);
-        break;
-    }
-    LKV_LAUNCH_CHECK("sparse_gemv reduce");
-  }
   return LKV_OK;
+}
+
+namespace {
+
+size_t ws_bytes_for(int64_t N, int64_t Z, bool dual) {
+  const int bz = gemv_pick_bz(gemv_slabs(N), Z);
+  return kTicketBytes + (dual ? 2 : 1) * gemv_part_floats(N, gemv_chunks(Z, bz)) * sizeof(float);
 }
 
 int check_common(const void* x, const void* A, int64_t N, int64_t Z, const void* y) {
@@ -399,6 +348,47 @@ int check_common(const void* x, const void* A, int64_t N, int64_t Z, const void*
   return LKV_OK;
 }
 
+int standalone(const void* x, const void* A0, const void* A1, float t0, float t1, int64_t N, int64_t Z, void* y,
+               void* ws, size_t ws_bytes, hipStream_t st, bool dual) {
+  const int64_t nslab = gemv_slabs(N);
+  const int bz = gemv_pick_bz(nslab, Z);
+  const int64_t nchunk = gemv_chunks(Z, bz);
+  const size_t need = ws_bytes_for(N, Z, dual);
+  LKV_REQUIRE(ws && ws_bytes >= need && aligned16(ws),
+              "sparse_gemv: workspace of %zu bytes (16-byte aligned) required, got %zu", need, ws_bytes);
+  GemvArgs G{};
+  G.x = static_cast<const uint16_t*>(x);
+  G.nseg = 1;
+  G.A[0] = static_cast<const uint16_t*>(A0);
+  G.A_up = static_cast<const uint16_t*>(A1);
+  G.a_bytes[0] = static_cast<uint32_t>(N * Z * 2);
+  G.N[0] = static_cast<int>(N);
+  G.t[0] = t0;
+  G.t_up = t1;
+  G.slab0[0] = 0;
+  G.slab0[1] = static_cast<int>(nslab);
+  G.Z = static_cast<int>(Z);
+  G.nchunk = static_cast<int>(nchunk);
+  G.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kTicketBytes);
+  G.part_off[0] = 0;
+  G.part_up_off = gemv_part_floats(N, nchunk);
+  G.y = nchunk == 1 ? static_cast<uint16_t*>(y) : nullptr;
+  if (int e = gemv_launch(G, bz, dual, kInRaw, static_cast<int>(nslab), st)) return e;
+  if (nchunk > 1) {
+    const unsigned rgrid = static_cast<unsigned>((N + kGemvThreads - 1) / kGemvThreads);
+    if (dual)
+      hipLaunchKernelGGL((gemv_reduce_kernel<true>), dim3(rgrid), dim3(kGemvThreads), 0, st, G.part,
+                         static_cast<int>(N), static_cast<int>(nslab), static_cast<int>(nchunk),
+                         static_cast<uint16_t*>(y));
+    else
+      hipLaunchKernelGGL((gemv_reduce_kernel<false>), dim3(rgrid), dim3(kGemvThreads), 0, st, G.part,
+                         static_cast<int>(N), static_cast<int>(nslab), static_cast<int>(nchunk),
+                         static_cast<uint16_t*>(y));
+    LKV_LAUNCH_CHECK("sparse_gemv reduce");
+  }
+  return LKV_OK;
+}
+
 }  // namespace
 }  // namespace lkv
 
@@ -406,23 +396,20 @@ using namespace lkv;
 
 extern "C" size_t lkv_sparse_gemv_workspace_bytes(int64_t N, int64_t Z) {
   if (N <= 0) return kTicketBytes;
-  return ws_bytes_for(pick_cfg(N, Z, false), N, Z, false);
+  return ws_bytes_for(N, Z, false);
 }
 
 extern "C" size_t lkv_sparse_gateup_workspace_bytes(int64_t N, int64_t Z) {
   if (N <= 0) return kTicketBytes;
-  return ws_bytes_for(pick_cfg(N, Z, true), N, Z, true);
+  return ws_bytes_for(N, Z, true);
 }
 
 extern "C" int lkv_sparse_gemv(const void* x, const void* w, float threshold, int64_t N, int64_t Z, void* y,
                                void* workspace, size_t workspace_bytes, void* stream) {
   if (int e = check_common(x, w, N, Z, y)) return e;
   if (N == 0) return LKV_OK;
-  const GemvCfg cfg = pick_cfg(N, Z, false);
-  const size_t need = ws_bytes_for(cfg, N, Z, false);
-  LKV_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace),
-              "sparse_gemv: workspace of %zu bytes (16-byte aligned) required, got %zu", need, workspace_bytes);
-  return launch<false>(cfg, x, w, w, threshold, threshold, N, Z, y, workspace, static_cast<hipStream_t>(stream));
+  return standalone(x, w, w, threshold, threshold, N, Z, y, workspace, workspace_bytes,
+                    static_cast<hipStream_t>(stream), false);
 }
 
 extern "C" int lkv_sparse_gateup_swiglu(const void* x, const void* wg, const void* wu, float t_gate, float t_up,
@@ -431,9 +418,6 @@ extern "C" int lkv_sparse_gateup_swiglu(const void* x, const void* wg, const voi
   if (int e = check_common(x, wg, N, Z, h)) return e;
   LKV_REQUIRE(wu && (aligned16(wu) || N == 0), "sparse_gateup: up weight must be 16-byte aligned");
   if (N == 0) return LKV_OK;
-  const GemvCfg cfg = pick_cfg(N, Z, true);
-  const size_t need = ws_bytes_for(cfg, N, Z, true);
-  LKV_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace),
-              "sparse_gateup: workspace of %zu bytes (16-byte aligned) required, got %zu", need, workspace_bytes);
-  return launch<true>(cfg, x, wg, wu, t_gate, t_up, N, Z, h, workspace, static_cast<hipStream_t>(stream));
+  return standalone(x, wg, wu, t_gate, t_up, N, Z, h, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                    true);
 }

@@ -8,14 +8,15 @@
 //   q . K_hat_t = n_t * (q @ PiK^T) . c[idx_t]
 //   sum_t p_t V_hat_t = (sum_t p_t n_t c[idx_t]) @ PiV
 // so the query is rotated once, cold scores and the cold value sum stay in the
-// rotated domain, and PiV is applied once per (batch, kv head) at the end.
+// rotated domain, and PiV is applied once per query head at the end.
 //
-// Three launches (all on the caller's stream, no inter-block waits):
-//   1. q_rot = q @ PiK^T on fp32 MFMA (tq_quant.hip's rotate kernel);
-//   2. split kernel, grid (splits + 1) x kv_heads x batch, 4 waves per block:
-//      * blocks 0..splits-1 own a contiguous range of cold tokens; each wave
-//        walks 32-token blocks of it, prefetching the next block's codes and
-//        norms while it computes the current one;
+// Launches (all on the caller's stream, no inter-block waits):
+//   1. q_rot = q @ PiK^T on fp32 MFMA, one block per (batch, kv head)
+//      (the decode step computes it inside its QKV epilogue instead);
+//   2. split kernel, grid splits x kv_heads x batch, 4 waves per block, each
+//      block owning a contiguous range of cold tokens; each wave walks
+//      32-token blocks of it, prefetching the next block's codes and norms
+//      while it computes the current one:
 //      * scores: v_mfma_f32_16x16x32_f16 with A = rotated query rows (the G
 //        heads sharing this kv head, zero padded to 16) and B = 16 tokens x 32
 //        dims of centroid values.  A lane loads 16 contiguous code bytes of
@@ -25,12 +26,14 @@
 //      * values: the same MFMA with A = p * n_t (fp16, via a 1 KB LDS tile)
 //        and B = 32 tokens x 16 dims of centroid values; a lane loads one code
 //        dword (8 dims) of 8 tokens and transposes the fp16 pairs in registers;
-//      * block `splits` handles the fp16 hot window from LDS on fp32 VALU;
-//      * every block writes (m, l, acc[G][128]) per head to the workspace;
-//   3. combine kernel, one block per (batch, kv head): merges the records in
-//      split order (loads batched 16 deep), applies PiV to the cold sum, adds
-//      the hot sum, normalises, writes fp16.
-#include "common.h"
+//      * the block writes (m, l, acc[G][128]) per head to the workspace;
+//   3. combine kernel, one block of 8 waves per (batch, query head): issues
+//      every load it needs at once (split maxima and sums, the rotated
+//      partial sums, the fp16 hot window and the PiV column slice), then
+//      computes the hot scores, merges hot and cold softmax statistics,
+//      applies PiV to the cold sum, adds the hot sum, normalises, writes fp16.
+#include "kernels.h"
+#include "tq_common.h"
 
 namespace lkv {
 namespace {
@@ -80,7 +83,7 @@ struct AttnParams {
   const float* PiV;         // [128, 128]
   const float* centroids;   // [2^bits]
   const int32_t* seq_len;
-  float* partials;          // [B, Hkv, nsplit + 1, rec]
+  float* partials;          // [B, Hkv, nsplit, rec]
   uint16_t* out;            // [B, Hq, 128]
   float scale_log2;         // scale * log2(e)
   int max_len, Hq, Hkv, G, cap, hot_cap, nsplit, split_tokens, ncent;
@@ -122,7 +125,6 @@ __global__ __launch_bounds__(kThreads) void tq_attn_split_kernel(AttnParams P) {
   __shared__ __align__(16) uint16_t s_p[kWaves][16][kBlk];  // p * n_t, fp16, per wave
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
   __shared__ __align__(16) float s_o[kWaves][GMAX][kD];
-  __shared__ __align__(16) uint16_t s_hot[2][kHotMax][kD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -130,369 +132,429 @@ __global__ __launch_bounds__(kThreads) void tq_attn_split_kernel(AttnParams P) {
   const int L = min(*P.seq_len, P.max_len);
   const int cold_len = max(0, L - P.hot_cap);
   const size_t bh = static_cast<size_t>(b) * P.Hkv + kvh;
-  float* rec = P.partials + (bh * (P.nsplit + 1) + split) * rec_floats(G);
+  float* rec = P.partials + (bh * P.nsplit + split) * rec_floats(G);
 
-  if (split < P.nsplit) {
-    // ------------------------------------------------------------ cold split
-    const int t_begin = split * P.split_tokens;
-    const int t_end = min(cold_len, t_begin + P.split_tokens);
-    if (t_begin >= t_end) {
-      if (tid < G) {
-        rec[tid] = -INFINITY;
-        rec[G + tid] = 0.f;
-      }
-      return;
-    }
-    {
-      const int lo = tid & 15, hi = tid >> 4;
-      const int cmax = P.ncent - 1;
-      s_lut[tid] = pack2h(P.centroids[min(lo, cmax)], P.centroids[min(hi, cmax)]);
-    }
-    // A operand of the score MFMA: rotated query x scale*log2(e), head
-    // h = lane%16, dims 32*(lane/16) + 8*kb + i for k-block kb.
-    const int h = lane & 15, g = lane >> 4;
-    u32x4 qa[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      if (h < G) {
-        const float* src = P.qrot + (static_cast<size_t>(b) * P.Hq + kvh * G + h) * kD + 32 * g + 8 * kb;
-        const float4 f0 = reinterpret_cast<const float4*>(src)[0];
-        const float4 f1 = reinterpret_cast<const float4*>(src)[1];
-        const float sl = P.scale_log2;
-        qa[kb] = u32x4{pack2h(f0.x * sl, f0.y * sl), pack2h(f0.z * sl, f0.w * sl), pack2h(f1.x * sl, f1.y * sl),
-                       pack2h(f1.z * sl, f1.w * sl)};
-      } else {
-        qa[kb] = u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-    const uint8_t* kc = P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB;
-    const uint8_t* vc = P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB;
-    const float* kn = P.k_norms + bh * static_cast<size_t>(P.cap);
-    const float* vn = P.v_norms + bh * static_cast<size_t>(P.cap);
-
-    float m[4], l[4];
-    f32x4 o[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      m[i] = -INFINITY;
-      l[i] = 0.f;
-    }
-#pragma unroll
-    for (int t = 0; t < 8; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    BlockRegs cur;
-    int t0 = t_begin + wave * kBlk;
-    if (t0 < t_end) load_block(cur, t0, t_end, lane, kc, kn, vc, vn);
-    __syncthreads();  // LUT ready
-    for (; t0 < t_end; t0 += kWaves * kBlk) {
-      const int tn = t0 + kWaves * kBlk;
-      BlockRegs nxt;
-      if (tn < t_end) load_block(nxt, tn, t_end, lane, kc, kn, vc, vn);
-      // ---- scores for tokens t0 .. t0+31 (two 16-token MFMA tiles)
-      f32x4 sc[2];
-      bool valid[2];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        valid[tt] = t0 + 16 * tt + (lane & 15) < t_end;
-        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          const uint32_t w = cur.kraw[tt][kb];
-          const u32x4 bop = u32x4{s_lut[w & 0xffu], s_lut[(w >> 8) & 0xffu], s_lut[(w >> 16) & 0xffu], s_lut[w >> 24]};
-          acc = mfma16x16x32(qa[kb], bop, acc);
-        }
-        sc[tt] = acc;
-      }
-      // ---- online softmax (log2 domain); lane holds heads 4g+i, token lane%16
-      float p[2][4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float s0 = valid[0] ? sc[0][i] * cur.knorm[0] : -INFINITY;
-        const float s1 = valid[1] ? sc[1][i] * cur.knorm[1] : -INFINITY;
-        const float bmax = group16_max(fmaxf(s0, s1));
-        const float mnew = fmaxf(m[i], bmax);
-        float alpha, p0, p1;
-        if (mnew == -INFINITY) {
-          alpha = 1.f;
-          p0 = p1 = 0.f;
-        } else {
-          alpha = exp2f(m[i] - mnew);
-          p0 = valid[0] ? exp2f(s0 - mnew) : 0.f;
-          p1 = valid[1] ? exp2f(s1 - mnew) : 0.f;
-        }
-        l[i] = l[i] * alpha + group16_sum(p0 + p1);
-        m[i] = mnew;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) o[t][i] *= alpha;
-        p[0][i] = p0;
-        p[1][i] = p1;
-      }
-      // ---- p * n_t into the per-wave LDS tile [head][token]
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          s_p[wave][4 * g + i][16 * tt + (lane & 15)] = f2h(valid[tt] ? p[tt][i] * cur.vnorm[tt] : 0.f);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      // ---- P V: A = p*n (head h = lane%16, tokens 8g..8g+7), B = codes
-      u32x4 pa = u32x4{0u, 0u, 0u, 0u};
-      if (h < G) pa = *reinterpret_cast<const u32x4*>(&s_p[wave][h][8 * g]);
-      uint32_t r[8][4];  // r[token i][byte bb] = (c[dim 8w+2bb], c[dim 8w+2bb+1])
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t dw = cur.vdw[i];
-        r[i][0] = s_lut[dw & 0xffu];
-        r[i][1] = s_lut[(dw >> 8) & 0xffu];
-        r[i][2] = s_lut[(dw >> 16) & 0xffu];
-        r[i][3] = s_lut[dw >> 24];
-      }
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        // dword pp = (token 2pp, token 2pp+1) of dim 8w + t: low halves of
-        // r[..][t/2] for even t, high halves for odd t.
-        const int bb = t >> 1;
-        u32x4 bop;
-#pragma unroll
-        for (int pp = 0; pp < 4; ++pp) {
-          const uint32_t x0 = r[2 * pp][bb], x1 = r[2 * pp + 1][bb];
-          bop[pp] = (t & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
-        }
-        o[t] = mfma16x16x32(pa, bop, o[t]);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-      if (tn < t_end) cur = nxt;
-    }
-
-    // ---- merge the 4 waves of the block through LDS
-    if ((lane & 15) == 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int hh = 4 * g + i;
-        if (hh < G) {
-          s_m[wave][hh] = m[i];
-          s_l[wave][hh] = l[i];
-        }
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int hh = 4 * g + i;
-        if (hh < G) s_o[wave][hh][8 * (lane & 15) + t] = o[t][i];
-      }
-    __syncthreads();
-    for (int e = tid; e < G * kD; e += kThreads) {
-      const int hh = e / kD, d = e % kD;
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hh]);
-      float acc = 0.f, lsum = 0.f;
-      if (M != -INFINITY) {
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-          const float wt = exp2f(s_m[w][hh] - M);
-          acc += wt * s_o[w][hh][d];
-          lsum += wt * s_l[w][hh];
-        }
-      }
-      rec[2 * G + hh * kD + d] = acc;
-      if (d == 0) {
-        rec[hh] = M;
-        rec[G + hh] = lsum;
-      }
+  const int t_begin = split * P.split_tokens;
+  const int t_end = min(cold_len, t_begin + P.split_tokens);
+  if (t_begin >= t_end) {
+    if (tid < G) {
+      rec[tid] = -INFINITY;
+      rec[G + tid] = 0.f;
     }
     return;
   }
-
-  // -------------------------------------------------------------- hot window
-  // tokens at positions [cold_len, L) live in ring slots pos % hot_cap; the
-  // window is staged in LDS with 16-byte loads first.
-  const int hot_len = L - cold_len;
-  float* s_q = &s_o[0][0][0];  // [G][128] fp32 query
-  float* s_s = &s_o[1][0][0];  // [G][64] scores / probs
-  for (int e = tid; e < G * kD; e += kThreads) s_q[e] = h2f(P.q[(static_cast<size_t>(b) * P.Hq + kvh * G) * kD + e]);
   {
-    const uint16_t* kh = P.k_hot + bh * static_cast<size_t>(P.hot_cap) * kD;
-    const uint16_t* vh = P.v_hot + bh * static_cast<size_t>(P.hot_cap) * kD;
-    for (int e = tid; e < hot_len * (kD / 8); e += kThreads) {
-      const int j = e / (kD / 8), c8 = (e % (kD / 8)) * 8;
-      const int slot = (cold_len + j) % P.hot_cap;
-      *reinterpret_cast<uint4*>(&s_hot[0][j][c8]) = *reinterpret_cast<const uint4*>(kh + slot * kD + c8);
-      *reinterpret_cast<uint4*>(&s_hot[1][j][c8]) = *reinterpret_cast<const uint4*>(vh + slot * kD + c8);
+    const int lo = tid & 15, hi = tid >> 4;
+    const int cmax = P.ncent - 1;
+    s_lut[tid] = pack2h(P.centroids[min(lo, cmax)], P.centroids[min(hi, cmax)]);
+  }
+  // A operand of the score MFMA: rotated query x scale*log2(e), head
+  // h = lane%16, dims 32*(lane/16) + 8*kb + i for k-block kb.
+  const int h = lane & 15, g = lane >> 4;
+  u32x4 qa[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    if (h < G) {
+      const float* src = P.qrot + (static_cast<size_t>(b) * P.Hq + kvh * G + h) * kD + 32 * g + 8 * kb;
+      const float4 f0 = reinterpret_cast<const float4*>(src)[0];
+      const float4 f1 = reinterpret_cast<const float4*>(src)[1];
+      const float sl = P.scale_log2;
+      qa[kb] = u32x4{pack2h(f0.x * sl, f0.y * sl), pack2h(f0.z * sl, f0.w * sl), pack2h(f1.x * sl, f1.y * sl),
+                     pack2h(f1.z * sl, f1.w * sl)};
+    } else {
+      qa[kb] = u32x4{0u, 0u, 0u, 0u};
     }
   }
-  __syncthreads();
-  for (int e = tid; e < G * kHotMax; e += kThreads) {
-    const int hh = e / kHotMax, j = e % kHotMax;
-    float s = -INFINITY;
-    if (j < hot_len) {
-      float acc = 0.f;
-#pragma unroll 8
-      for (int d = 0; d < kD; ++d) acc = fmaf(s_q[hh * kD + d], h2f(s_hot[0][j][d]), acc);
-      s = acc * P.scale_log2;
-    }
-    s_s[hh * kHotMax + j] = s;
+  const uint8_t* kc = P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB;
+  const uint8_t* vc = P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB;
+  const float* kn = P.k_norms + bh * static_cast<size_t>(P.cap);
+  const float* vn = P.v_norms + bh * static_cast<size_t>(P.cap);
+
+  float m[4], l[4];
+  f32x4 o[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
   }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  BlockRegs cur;
+  int t0 = t_begin + wave * kBlk;
+  if (t0 < t_end) load_block(cur, t0, t_end, lane, kc, kn, vc, vn);
+  __syncthreads();  // LUT ready
+  for (; t0 < t_end; t0 += kWaves * kBlk) {
+    const int tn = t0 + kWaves * kBlk;
+    BlockRegs nxt;
+    if (tn < t_end) load_block(nxt, tn, t_end, lane, kc, kn, vc, vn);
+    // ---- scores for tokens t0 .. t0+31 (two 16-token MFMA tiles)
+    f32x4 sc[2];
+    bool valid[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      valid[tt] = t0 + 16 * tt + (lane & 15) < t_end;
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const uint32_t w = cur.kraw[tt][kb];
+        const u32x4 bop = u32x4{s_lut[w & 0xffu], s_lut[(w >> 8) & 0xffu], s_lut[(w >> 16) & 0xffu], s_lut[w >> 24]};
+        acc = mfma16x16x32(qa[kb], bop, acc);
+      }
+      sc[tt] = acc;
+    }
+    // ---- online softmax (log2 domain); lane holds heads 4g+i, token lane%16
+    float p[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float s0 = valid[0] ? sc[0][i] * cur.knorm[0] : -INFINITY;
+      const float s1 = valid[1] ? sc[1][i] * cur.knorm[1] : -INFINITY;
+      const float bmax = group16_max(fmaxf(s0, s1));
+      const float mnew = fmaxf(m[i], bmax);
+      float alpha, p0, p1;
+      if (mnew == -INFINITY) {
+        alpha = 1.f;
+        p0 = p1 = 0.f;
+      } else {
+        alpha = exp2f(m[i] - mnew);
+        p0 = valid[0] ? exp2f(s0 - mnew) : 0.f;
+        p1 = valid[1] ? exp2f(s1 - mnew) : 0.f;
+      }
+      l[i] = l[i] * alpha + group16_sum(p0 + p1);
+      m[i] = mnew;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) o[t][i] *= alpha;
+      p[0][i] = p0;
+      p[1][i] = p1;
+    }
+    // ---- p * n_t into the per-wave LDS tile [head][token]
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        s_p[wave][4 * g + i][16 * tt + (lane & 15)] = f2h(valid[tt] ? p[tt][i] * cur.vnorm[tt] : 0.f);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // ---- P V: A = p*n (head h = lane%16, tokens 8g..8g+7), B = codes
+    u32x4 pa = u32x4{0u, 0u, 0u, 0u};
+    if (h < G) pa = *reinterpret_cast<const u32x4*>(&s_p[wave][h][8 * g]);
+    uint32_t r[8][4];  // r[token i][byte bb] = (c[dim 8w+2bb], c[dim 8w+2bb+1])
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t dw = cur.vdw[i];
+      r[i][0] = s_lut[dw & 0xffu];
+      r[i][1] = s_lut[(dw >> 8) & 0xffu];
+      r[i][2] = s_lut[(dw >> 16) & 0xffu];
+      r[i][3] = s_lut[dw >> 24];
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      // dword pp = (token 2pp, token 2pp+1) of dim 8w + t: low halves of
+      // r[..][t/2] for even t, high halves for odd t.
+      const int bb = t >> 1;
+      u32x4 bop;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const uint32_t x0 = r[2 * pp][bb], x1 = r[2 * pp + 1][bb];
+        bop[pp] = (t & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
+      }
+      o[t] = mfma16x16x32(pa, bop, o[t]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    if (tn < t_end) cur = nxt;
+  }
+
+  // ---- merge the 4 waves of the block through LDS
+  if ((lane & 15) == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int hh = 4 * g + i;
+      if (hh < G) {
+        s_m[wave][hh] = m[i];
+        s_l[wave][hh] = l[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int hh = 4 * g + i;
+      if (hh < G) s_o[wave][hh][8 * (lane & 15) + t] = o[t][i];
+    }
   __syncthreads();
-  // per-head max and sum (one wave per head, looping over heads)
-  for (int hh = wave; hh < G; hh += kWaves) {
-    const float v = s_s[hh * kHotMax + lane];
-    const float M = wave_max(v);
-    const float pv = (M == -INFINITY || v == -INFINITY) ? 0.f : exp2f(v - M);
-    const float lsum = wave_sum(pv);
-    s_s[hh * kHotMax + lane] = pv;
-    if (lane == 0) {
+  for (int e = tid; e < G * kD; e += kThreads) {
+    const int hh = e / kD, d = e % kD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hh]);
+    float acc = 0.f, lsum = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float wt = exp2f(s_m[w][hh] - M);
+        acc += wt * s_o[w][hh][d];
+        lsum += wt * s_l[w][hh];
+      }
+    }
+    rec[2 * G + hh * kD + d] = acc;
+    if (d == 0) {
       rec[hh] = M;
       rec[G + hh] = lsum;
     }
   }
-  __syncthreads();
-  for (int e = tid; e < G * kD; e += kThreads) {
-    const int hh = e / kD, d = e % kD;
-    float acc = 0.f;
-    for (int j = 0; j < hot_len; ++j) acc = fmaf(s_s[hh * kHotMax + j], h2f(s_hot[1][j][d]), acc);
-    rec[2 * G + hh * kD + d] = acc;
-  }
 }
 
-// Merge the records of one (batch, kv head) and write fp16 output.
-template <int GMAX>
-__global__ __launch_bounds__(kThreads) void tq_attn_combine_kernel(AttnParams P) {
-  constexpr int kMaxW = 4096;
-  __shared__ float s_w[kMaxW];  // merge weight per (split, head)
-  __shared__ float s_L[GMAX];
-  __shared__ __align__(16) float s_rot[GMAX][kD];
-  const int tid = threadIdx.x;
-  const int kvh = blockIdx.x, b = blockIdx.y;
-  const int G = P.G;
-  const int ns = P.nsplit + 1;
+
+constexpr int kCombThreads = 512;
+constexpr int kCombWaves = kCombThreads / kWave;
+constexpr int kMaxSplits = 256;
+
+__device__ __forceinline__ float dot8_f16(const uint4& a, const uint4& b) {
+  const uint32_t x[4] = {a.x, a.y, a.z, a.w}, y[4] = {b.x, b.y, b.z, b.w};
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s = fmaf(h2f(static_cast<uint16_t>(x[i] & 0xffffu)), h2f(static_cast<uint16_t>(y[i] & 0xffffu)), s);
+    s = fmaf(h2f(static_cast<uint16_t>(x[i] >> 16)), h2f(static_cast<uint16_t>(y[i] >> 16)), s);
+  }
+  return s;
+}
+
+// One block per (query head, batch).  Thread (d = tid % 128, quarter qd =
+// tid / 128) owns output dim d for the splits / hot tokens / PiV rows of its
+// quarter; the 4 quarters are summed through LDS in a fixed order.
+__global__ __launch_bounds__(kCombThreads) void tq_attn_combine_kernel(AttnParams P) {
+  __shared__ float s_w[kMaxSplits];
+  __shared__ float s_p[kHotMax];
+  __shared__ float s_red[kCombWaves];
+  __shared__ __align__(16) float s_part[2][4][kD];
+  __shared__ float s_rot[kD], s_hv[kD];
+  __shared__ float s_o[4][kD];
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int hq = blockIdx.x, b = blockIdx.y;
+  const int G = P.G, kvh = hq / G, hh = hq % G;
+  const int ns = P.nsplit;
+  const int L = min(*P.seq_len, P.max_len);
+  const int cold_len = max(0, L - P.hot_cap);
+  const int hot_len = L - cold_len;
   const size_t bh = static_cast<size_t>(b) * P.Hkv + kvh;
   const int RF = rec_floats(G);
-  const float* base = P.partials + bh * ns * RF;
-  // m of every record into s_w, then per-head max / weights / L
-  for (int e = tid; e < ns * G; e += kThreads) s_w[e] = base[(e / G) * RF + (e % G)];
+  const float* recs = P.partials + bh * ns * RF;
+  const size_t hot_base = bh * static_cast<size_t>(P.hot_cap) * kD;
+  const int d = tid & (kD - 1), qd = tid >> 7;
+
+  // ---- A. every independent load up front
+  float ms = -INFINITY, ls = 0.f;
+  if (tid < ns) {
+    ms = recs[static_cast<size_t>(tid) * RF + hh];
+    ls = recs[static_cast<size_t>(tid) * RF + G + hh];
+  }
+  // hot score partial: token j = tid / 8, dims 16 * (tid % 8) .. +16
+  const int j = tid >> 3, part = tid & 7;
+  const bool hj = j < hot_len;
+  float sdot = 0.f;
+  {
+    const int slot = hj ? (cold_len + j) % P.hot_cap : 0;
+    const uint4* kp = reinterpret_cast<const uint4*>(P.k_hot + hot_base + static_cast<size_t>(slot) * kD + 16 * part);
+    const uint4* qp = reinterpret_cast<const uint4*>(P.q + (static_cast<size_t>(b) * P.Hq + hq) * kD + 16 * part);
+    const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+    const uint4 k0 = hj ? kp[0] : z4, k1 = hj ? kp[1] : z4;
+    const uint4 q0 = qp[0], q1 = qp[1];
+    sdot = dot8_f16(k0, q0) + dot8_f16(k1, q1);
+  }
+  float piv[32];
+#pragma unroll
+  for (int k = 0; k < 32; ++k) piv[k] = P.PiV[(32 * qd + k) * kD + d];
+  uint16_t hv[kHotMax / 4];
+#pragma unroll
+  for (int i = 0; i < kHotMax / 4; ++i) {
+    const int jj = qd + 4 * i;
+    hv[i] = jj < hot_len ? P.v_hot[hot_base + static_cast<size_t>((cold_len + jj) % P.hot_cap) * kD + d] : 0;
+  }
+  float ca[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int s = qd + 4 * i;
+    ca[i] = s < ns ? recs[static_cast<size_t>(s) * RF + 2 * G + hh * kD + d] : 0.f;
+  }
+
+  // ---- B. softmax statistics over cold splits and hot tokens
+  sdot += __shfl_xor(sdot, 1);
+  sdot += __shfl_xor(sdot, 2);
+  sdot += __shfl_xor(sdot, 4);
+  const float score = hj ? sdot * P.scale_log2 : -INFINITY;
+  float v = fmaxf(ms, part == 0 ? score : -INFINITY);
+  v = wave_max(v);
+  if (lane == 0) s_red[wave] = v;
   __syncthreads();
-  if (tid < G) {
-    float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, s_w[s * G + tid]);
-    s_L[tid] = M;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kCombWaves; ++w) M = fmaxf(M, s_red[w]);
+  __syncthreads();
+  const float wsp = (tid < ns && ms != -INFINITY) ? exp2f(ms - M) : 0.f;
+  const float pj = hj ? exp2f(score - M) : 0.f;
+  if (tid < ns) s_w[tid] = wsp;
+  if (part == 0 && j < kHotMax) s_p[j] = pj;
+  float lv = wsp * ls + (part == 0 ? pj : 0.f);
+  lv = wave_sum(lv);
+  if (lane == 0) s_red[wave] = lv;
+  __syncthreads();
+  float Lt = 0.f;
+#pragma unroll
+  for (int w = 0; w < kCombWaves; ++w) Lt += s_red[w];
+
+  // ---- C. weighted sums of this quarter: rotated cold, unrotated hot
+  float cold = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int s = qd + 4 * i;
+    const float w = s < ns ? s_w[s] : 0.f;
+    cold += (w != 0.f) ? w * ca[i] : 0.f;
+  }
+  for (int s0 = 64; s0 < ns; s0 += 64) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int s = s0 + qd + 4 * i;
+      ca[i] = s < ns ? recs[static_cast<size_t>(s) * RF + 2 * G + hh * kD + d] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int s = s0 + qd + 4 * i;
+      const float w = s < ns ? s_w[s] : 0.f;
+      cold += (w != 0.f) ? w * ca[i] : 0.f;
+    }
+  }
+  float hot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kHotMax / 4; ++i) {
+    const int jj = qd + 4 * i;
+    if (jj < hot_len) hot = fmaf(s_p[jj], h2f(hv[i]), hot);
+  }
+  s_part[0][qd][d] = cold;
+  s_part[1][qd][d] = hot;
+  __syncthreads();
+  if (tid < kD) {
+    s_rot[tid] = ((s_part[0][0][tid] + s_part[0][1][tid]) + s_part[0][2][tid]) + s_part[0][3][tid];
+    s_hv[tid] = ((s_part[1][0][tid] + s_part[1][1][tid]) + s_part[1][2][tid]) + s_part[1][3][tid];
   }
   __syncthreads();
-  for (int e = tid; e < ns * G; e += kThreads) {
-    const float M = s_L[e % G];
-    const float ms = s_w[e];
-    s_w[e] = (M == -INFINITY || ms == -INFINITY) ? 0.f : exp2f(ms - M);
-  }
+
+  // ---- D. un-rotate the cold sum: out[d] = sum_k rot[k] PiV[k][d]
+  float o = 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) o = fmaf(s_rot[32 * qd + k], piv[k], o);
+  s_o[qd][d] = o;
   __syncthreads();
-  if (tid < G) {
-    float Lt = 0.f;
-    for (int s0 = 0; s0 < ns; s0 += 16) {
-      float v[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = (s0 + i < ns) ? base[(s0 + i) * RF + G + tid] : 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (s0 + i < ns) Lt += s_w[(s0 + i) * G + tid] * v[i];
-    }
-    s_L[tid] = Lt;
-  }
-  // rotated cold sum, records read 16 deep
-  for (int e = tid; e < G * kD; e += kThreads) {
-    const int hh = e / kD;
-    float acc = 0.f;
-    for (int s0 = 0; s0 < P.nsplit; s0 += 16) {
-      float v[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int s = s0 + i;
-        v[i] = (s < P.nsplit) ? base[s * RF + 2 * G + e] : 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int s = s0 + i;
-        if (s < P.nsplit) {
-          const float wt = s_w[s * G + hh];
-          if (wt != 0.f) acc += wt * v[i];
-        }
-      }
-    }
-    s_rot[hh][e % kD] = acc;
-  }
-  __syncthreads();
-  // out[h][j] = (sum_k rot[h][k] PiV[k][j] + w_hot hot[h][j]) / L
-  const int j = tid & (kD - 1);
-  const int h0 = tid >> 7;  // 0 or 1
-  float acc[GMAX / 2];
-#pragma unroll
-  for (int u = 0; u < GMAX / 2; ++u) acc[u] = 0.f;
-#pragma unroll 8
-  for (int k = 0; k < kD; ++k) {
-    const float pv = P.PiV[k * kD + j];
-#pragma unroll
-    for (int u = 0; u < GMAX / 2; ++u) {
-      const int hh = h0 + 2 * u;
-      if (hh < G) acc[u] = fmaf(s_rot[hh][k], pv, acc[u]);
-    }
-  }
-  const float* hot = base + P.nsplit * RF;
-#pragma unroll
-  for (int u = 0; u < GMAX / 2; ++u) {
-    const int hh = h0 + 2 * u;
-    if (hh < G) {
-      const float wh = s_w[P.nsplit * G + hh];
-      float v = acc[u];
-      if (wh != 0.f) v += wh * hot[2 * G + hh * kD + j];
-      const float Lt = s_L[hh];
-      v = (Lt > 0.f) ? v / Lt : 0.f;
-      P.out[(static_cast<size_t>(b) * P.Hq + kvh * G + hh) * kD + j] = f2h(v);
-    }
+  if (tid < kD) {
+    const float r = (((s_o[0][tid] + s_o[1][tid]) + s_o[2][tid]) + s_o[3][tid]) + s_hv[tid];
+    P.out[(static_cast<size_t>(b) * P.Hq + hq) * kD + tid] = f2h(Lt > 0.f ? r / Lt : 0.f);
   }
 }
 
-struct AttnPlan {
-  int nsplit, split_tokens;
-  size_t qrot_off, part_off, total;
-};
+// q_rot = q @ PiK^T for the G query heads of one (kv head, batch): one
+// 16-row rotation tile (rows >= G are zero), the arithmetic of tq_rotate.
+__global__ __launch_bounds__(tq::kThreads) void qrot_kernel(const uint16_t* __restrict__ q,
+                                                            const float* __restrict__ PiK,
+                                                            float* __restrict__ qrot, int Hq, int Hkv) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kvh = blockIdx.x, b = blockIdx.y, G = Hq / Hkv;
+  float bop[2][32];
+  tq::load_pi_operand(PiK, false, wave, lane, bop);
+  const int r = lane & 15;
+  float a[32];
+  if (r < G) {
+    tq::load_row_f16(q + (static_cast<size_t>(b) * Hq + kvh * G + r) * kD + 32 * (lane >> 4), a);
+  } else {
+#pragma unroll
+    for (int s = 0; s < 32; ++s) a[s] = 0.f;
+  }
+  f32x4 acc[2];
+  tq::rotate_tile(a, bop, acc);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * (lane >> 4) + i;
+      const int dim = 8 * (lane & 15) + 2 * wave + t;
+      if (row < G) qrot[(static_cast<size_t>(b) * Hq + kvh * G + row) * kD + dim] = acc[t][i];
+    }
+}
 
-// Upper bound on the number of cold splits: enough blocks for ~2 per CU,
-// nsplit + 1 <= 256 records and (nsplit + 1) * G <= 4096 merge weights in the
-// combine kernel's LDS.
-int64_t max_splits(int64_t B, int64_t Hkv, int64_t G) {
+constexpr int kSplitGran = kWaves * kBlk;  // tokens one pass of a block covers
+
+// Split count that gives ~2 blocks per CU, at most kMaxSplits - 1.
+int64_t target_splits(int64_t B, int64_t Hkv) {
   const int64_t target = 2 * static_cast<int64_t>(device_cu_count());
   int64_t ns = (target + B * Hkv - 1) / (B * Hkv);
-  if (ns > 255) ns = 255;
-  const int64_t gcap = 4096 / (G > 0 ? G : 1) - 1;
-  if (ns > gcap) ns = gcap;
+  if (ns > kMaxSplits - 1) ns = kMaxSplits - 1;
   return ns < 1 ? 1 : ns;
 }
 
-AttnPlan plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_cap) {
+}  // namespace
+
+AttnPlan attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_cap) {
   AttnPlan p{};
   const int64_t G = Hkv > 0 ? Hq / Hkv : 1;
   const int64_t cold_max = max_len > hot_cap ? max_len - hot_cap : 0;
-  const int64_t ns_cap = max_splits(B, Hkv, G);
-  int64_t ns = ns_cap;
-  const int64_t maxs = (cold_max + kBlk - 1) / kBlk;
-  if (ns > maxs) ns = maxs;
+  const int64_t ns_cap = target_splits(B, Hkv);
+  int64_t ts = (cold_max + ns_cap - 1) / ns_cap;
+  ts = (ts + kSplitGran - 1) / kSplitGran * kSplitGran;
+  if (ts < kSplitGran) ts = kSplitGran;
+  int64_t ns = (cold_max + ts - 1) / ts;
   if (ns < 1) ns = 1;
-  int64_t ts = (cold_max + ns - 1) / ns;
-  ts = ((ts + kBlk - 1) / kBlk) * kBlk;
-  if (ts < kBlk) ts = kBlk;
-  ns = cold_max > 0 ? (cold_max + ts - 1) / ts : 1;
   p.nsplit = static_cast<int>(ns);
   p.split_tokens = static_cast<int>(ts);
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
   p.qrot_off = kTicketBytes;  // keeps the shared workspace layout: ticket area first
   p.part_off = p.qrot_off + al(static_cast<size_t>(B * Hq * kD) * 4);
-  p.total = p.part_off + al(static_cast<size_t>(B * Hkv * (ns_cap + 1) * G * (2 + kD)) * 4);
+  // sized for ns_cap so a workspace sized without hot_cap fits every call
+  p.total = p.part_off + al(static_cast<size_t>(B * Hkv * ns_cap * G * (2 + kD)) * 4);
   return p;
 }
 
-}  // namespace
+int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st) {
+  AttnParams P;
+  P.qrot = c.qrot;
+  P.q = c.q;
+  P.k_codes = c.k_codes;
+  P.k_norms = c.k_norms;
+  P.v_codes = c.v_codes;
+  P.v_norms = c.v_norms;
+  P.k_hot = c.k_hot;
+  P.v_hot = c.v_hot;
+  P.PiV = c.PiV;
+  P.centroids = c.centroids;
+  P.seq_len = c.seq_len;
+  P.partials = c.partials;
+  P.out = c.out;
+  P.scale_log2 = c.scale * kLog2e;
+  P.max_len = static_cast<int>(c.max_len);
+  P.Hq = static_cast<int>(c.Hq);
+  P.Hkv = static_cast<int>(c.Hkv);
+  P.G = static_cast<int>(c.Hq / c.Hkv);
+  P.cap = static_cast<int>(c.cap);
+  P.hot_cap = static_cast<int>(c.hot_cap);
+  P.nsplit = pl.nsplit;
+  P.split_tokens = pl.split_tokens;
+  P.ncent = 1 << c.bits;
+  const dim3 grid(static_cast<unsigned>(pl.nsplit), static_cast<unsigned>(c.Hkv), static_cast<unsigned>(c.B));
+  const dim3 cgrid(static_cast<unsigned>(c.Hq), static_cast<unsigned>(c.B));
+  if (P.G <= 4)
+    hipLaunchKernelGGL((tq_attn_split_kernel<4>), grid, dim3(kThreads), 0, st, P);
+  else if (P.G <= 8)
+    hipLaunchKernelGGL((tq_attn_split_kernel<8>), grid, dim3(kThreads), 0, st, P);
+  else
+    hipLaunchKernelGGL((tq_attn_split_kernel<16>), grid, dim3(kThreads), 0, st, P);
+  LKV_LAUNCH_CHECK("tq_decode_attn split");
+  hipLaunchKernelGGL(tq_attn_combine_kernel, cgrid, dim3(kCombThreads), 0, st, P);
+  LKV_LAUNCH_CHECK("tq_decode_attn combine");
+  return LKV_OK;
+}
+
 }  // namespace lkv
 
 using namespace lkv;
@@ -500,7 +562,7 @@ using namespace lkv;
 extern "C" size_t lkv_tq_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len < 0) return kTicketBytes;
   // hot_cap only shifts the cold range; the record area is sized for the cap.
-  return plan(B, Hq, Hkv, max_len, 0).total;
+  return attn_plan(B, Hq, Hkv, max_len, 0).total;
 }
 
 extern "C" int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const float* k_norms,
@@ -525,49 +587,36 @@ extern "C" int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const f
   LKV_REQUIRE(aligned16(q) && aligned16(k_codes) && aligned16(v_codes) && aligned16(k_hot) && aligned16(v_hot) &&
                   aligned16(PiK) && aligned16(out) && aligned16(workspace),
               "tq_decode_attn: q, codes, hot, PiK, out and workspace must be 16-byte aligned");
-  const AttnPlan pl = plan(B, Hq, Hkv, max_len, hot_cap);
+  const AttnPlan pl = attn_plan(B, Hq, Hkv, max_len, hot_cap);
   LKV_REQUIRE(workspace_bytes >= pl.total, "tq_decode_attn: workspace of %zu bytes required, got %zu", pl.total,
               workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   float* qrot = reinterpret_cast<float*>(ws + pl.qrot_off);
-  if (int e = lkv_tq_rotate(q, LKV_DTYPE_F16, B * Hq, PiK, 0, qrot, stream)) return e;
-  AttnParams P;
-  P.qrot = qrot;
-  P.q = static_cast<const uint16_t*>(q);
-  P.k_codes = k_codes;
-  P.k_norms = k_norms;
-  P.v_codes = v_codes;
-  P.v_norms = v_norms;
-  P.k_hot = static_cast<const uint16_t*>(k_hot);
-  P.v_hot = static_cast<const uint16_t*>(v_hot);
-  P.PiV = PiV;
-  P.centroids = centroids;
-  P.seq_len = seq_len;
-  P.partials = reinterpret_cast<float*>(ws + pl.part_off);
-  P.out = static_cast<uint16_t*>(out);
-  P.scale_log2 = scale * kLog2e;
-  P.max_len = static_cast<int>(max_len);
-  P.Hq = static_cast<int>(Hq);
-  P.Hkv = static_cast<int>(Hkv);
-  P.G = static_cast<int>(Hq / Hkv);
-  P.cap = static_cast<int>(cap);
-  P.hot_cap = static_cast<int>(hot_cap);
-  P.nsplit = pl.nsplit;
-  P.split_tokens = pl.split_tokens;
-  P.ncent = 1 << bits;
-  dim3 grid(static_cast<unsigned>(pl.nsplit + 1), static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
-  dim3 cgrid(static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
-  if (P.G <= 4) {
-    hipLaunchKernelGGL((tq_attn_split_kernel<4>), grid, dim3(kThreads), 0, st, P);
-    hipLaunchKernelGGL((tq_attn_combine_kernel<4>), cgrid, dim3(kThreads), 0, st, P);
-  } else if (P.G <= 8) {
-    hipLaunchKernelGGL((tq_attn_split_kernel<8>), grid, dim3(kThreads), 0, st, P);
-    hipLaunchKernelGGL((tq_attn_combine_kernel<8>), cgrid, dim3(kThreads), 0, st, P);
-  } else {
-    hipLaunchKernelGGL((tq_attn_split_kernel<16>), grid, dim3(kThreads), 0, st, P);
-    hipLaunchKernelGGL((tq_attn_combine_kernel<16>), cgrid, dim3(kThreads), 0, st, P);
-  }
-  LKV_LAUNCH_CHECK("tq_decode_attn");
-  return LKV_OK;
+  hipLaunchKernelGGL(qrot_kernel, dim3(static_cast<unsigned>(Hkv), static_cast<unsigned>(B)), dim3(tq::kThreads), 0,
+                     st, static_cast<const uint16_t*>(q), PiK, qrot, static_cast<int>(Hq), static_cast<int>(Hkv));
+  LKV_LAUNCH_CHECK("tq_decode_attn q rotation");
+  AttnCall c{};
+  c.qrot = qrot;
+  c.q = static_cast<const uint16_t*>(q);
+  c.k_codes = k_codes;
+  c.k_norms = k_norms;
+  c.v_codes = v_codes;
+  c.v_norms = v_norms;
+  c.k_hot = static_cast<const uint16_t*>(k_hot);
+  c.v_hot = static_cast<const uint16_t*>(v_hot);
+  c.PiV = PiV;
+  c.centroids = centroids;
+  c.seq_len = seq_len;
+  c.partials = reinterpret_cast<float*>(ws + pl.part_off);
+  c.out = static_cast<uint16_t*>(out);
+  c.scale = scale;
+  c.max_len = max_len;
+  c.B = B;
+  c.Hq = Hq;
+  c.Hkv = Hkv;
+  c.cap = cap;
+  c.hot_cap = hot_cap;
+  c.bits = bits;
+  return attn_launch(c, pl, st);
 }

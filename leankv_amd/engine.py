@@ -21,12 +21,13 @@ dense fp16 baseline (scripts/raw_baseline.py), also graph-captured.
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
 import torch.nn.functional as F
 
-from . import kernels as _k
+from . import _lib
 from .turboquant.cache import TurboQuantCache
 
 
@@ -110,82 +111,97 @@ class _Base:
 
 
 class LeanKVEngine(_Base):
-    """TEAL sparse projections + TurboQuant packed KV, HIP kernels, one graph per step."""
+    """TEAL sparse projections + TurboQuant packed KV through the fused C decode step.
+
+    Per token: lkv_decode_begin, lkv_decode_layer_step per layer (9 kernels:
+    q|k|v GEMV with the RMSNorm prologue, RoPE/append/q-rotation epilogue,
+    attention split + combine, o_proj, residual, gate|up GEMV with the
+    RMSNorm prologue, down GEMV with the SwiGLU prologue, residual) and
+    lkv_decode_head (lm_head GEMV, logits, argmax), captured into one graph.
+
+    Projections patched by apply_teal already hold their weight column-major
+    (leankv/teal/patching.py:171); unpatched ones get a column-major copy and
+    threshold 0 (dense).  lm_head gets a column-major copy.
+    """
 
     def __init__(self, model, cache: TurboQuantCache, max_len: int):
         super().__init__(model, max_len)
         self.cache = cache
         if cache.cold_capacity(0) < max_len - cache.hot_buffer_size:
             raise ValueError("TurboQuantCache cold capacity %d < max_len - hot" % cache.cold_capacity(0))
-        self.pos32 = torch.zeros(1, dtype=torch.int32, device=self.dev)
-        self.len32 = torch.zeros(1, dtype=torch.int32, device=self.dev)
-        self.proj = []
-        for layer in self.layers:
-            ent = {}
-            for name, mod in (("q", layer.self_attn.q_proj), ("k", layer.self_attn.k_proj),
-                              ("v", layer.self_attn.v_proj), ("o", layer.self_attn.o_proj),
-                              ("gate", layer.mlp.gate_proj), ("up", layer.mlp.up_proj),
-                              ("down", layer.mlp.down_proj)):
-                t = getattr(mod, "_teal_threshold", None)
-                ent[name] = (mod.weight, t)
-            self.proj.append(ent)
-        # static activations
+        if self.D != 128:
+            raise ValueError("the fused decode step needs head_dim 128, got %d" % self.D)
+        lib = _lib.load()
         d = self.dev
-        f16 = torch.float16
-        self.q = torch.empty(self.H * self.D, dtype=f16, device=d)
-        self.k = torch.empty(self.Hkv * self.D, dtype=f16, device=d)
-        self.v = torch.empty(self.Hkv * self.D, dtype=f16, device=d)
-        self.attn = torch.empty(1, self.H, self.D, dtype=f16, device=d)
-        self.o = torch.empty(self.hidden, dtype=f16, device=d)
-        self.m = torch.empty(self.cfg.intermediate_size, dtype=f16, device=d)
-        self.dn = torch.empty(self.hidden, dtype=f16, device=d)
-        self.x = torch.empty(1, self.hidden, dtype=f16, device=d)
-        self.attn_ws = torch.zeros(_k.decode_attn_workspace_bytes(1, self.H, self.Hkv, max_len), dtype=torch.uint8,
-                                   device=d)
+        self._keep = []  # tensors whose pointers the C structs hold
+        self.dims = _lib.DecodeDims(
+            hidden=self.hidden, ffn=self.cfg.intermediate_size, vocab=self.cfg.vocab_size, n_heads=self.H,
+            n_kv_heads=self.Hkv, max_len=max_len, cap=cache.cold_capacity(0), hot_cap=cache.hot_buffer_size,
+            bits=cache.bits, eps=self.eps, scale=self.scale,
+            bounds=self._hold(cache.decision_boundaries.to(d, torch.float32).contiguous()),
+            centroids=self._hold(cache.centroids.to(d, torch.float32).contiguous()),
+            rope_cos=self._hold(self.cos), rope_sin=self._hold(self.sin))
+        self.layer_structs = []
+        self.thresholds = []
+        for i, layer in enumerate(self.layers):
+            at, mlp = layer.self_attn, layer.mlp
+            w, t = {}, {}
+            for name, mod in (("q", at.q_proj), ("k", at.k_proj), ("v", at.v_proj), ("o", at.o_proj),
+                              ("g", mlp.gate_proj), ("u", mlp.up_proj), ("d", mlp.down_proj)):
+                if getattr(mod, "bias", None) is not None:
+                    raise ValueError("the fused decode step has no projection bias")
+                th = getattr(mod, "_teal_threshold", None)
+                t[name] = float(th) if th else 0.0
+                w[name] = self._hold(_colmajor(mod.weight))
+            self.thresholds.append(t)
+            self.layer_structs.append(_lib.DecodeLayer(
+                input_norm=self._hold(layer.input_layernorm.weight.detach()),
+                post_norm=self._hold(layer.post_attention_layernorm.weight.detach()),
+                wq=w["q"], wk=w["k"], wv=w["v"], wo=w["o"], wg=w["g"], wu=w["u"], wd=w["d"],
+                tq=t["q"], tk=t["k"], tv=t["v"], to=t["o"], tg=t["g"], tu=t["u"], td=t["d"],
+                k_codes=self._hold(cache._k_codes[i]), k_norms=self._hold(cache._k_norms[i]),
+                v_codes=self._hold(cache._v_codes[i]), v_norms=self._hold(cache._v_norms[i]),
+                k_hot=self._hold(cache._k_hot[i]), v_hot=self._hold(cache._v_hot[i]),
+                PiK=self._hold(cache.PiK[i].contiguous()), PiV=self._hold(cache.PiV[i].contiguous())))
+        self.final_norm = model.model.norm.weight.detach()
+        self.lm_head_cm = model.lm_head.weight.detach().t().contiguous()  # [hidden][vocab]
+        nbytes = lib.lkv_decode_workspace_bytes(ctypes.byref(self.dims))
+        if nbytes == 0:
+            raise _lib.LeanKVError("lkv_decode_workspace_bytes rejected the model shape: %s" % _lib.last_error())
+        self.ws = torch.empty(nbytes, dtype=torch.uint8, device=d)
+        self.x = torch.empty(self.hidden, dtype=torch.float16, device=d)
 
-    def _lin(self, x, w, t, out):
-        if t is not None and t > 0:
-            return _k.sparse_gemv_out(x, w, t, out)
-        out.copy_(F.linear(x.view(1, -1), w).view(-1))
-        return out
+    def _hold(self, t: torch.Tensor) -> int:
+        if not t.is_cuda:
+            raise _lib.LeanKVError("decode state must live on the GPU")
+        self._keep.append(t)
+        return t.data_ptr()
 
     def start(self, first_token: torch.Tensor, length: int) -> None:
-        """Set the token to feed next and the cache length (after prefill)."""
+        """Set the token to feed next and its position (the cache length after prefill)."""
         self.tok.copy_(first_token.view(1))
         self.pos64.fill_(length)
 
     def _step(self) -> None:
-        c = self.cache
-        x = self.model.model.embed_tokens.weight.index_select(0, self.tok)  # [1, hidden]
-        self.pos32.copy_(self.pos64)
-        self.len32.copy_(self.pos64 + 1)
-        for i, layer in enumerate(self.layers):
-            p = self.proj[i]
-            h = _rms(x, layer.input_layernorm.weight, self.eps)
-            self._lin(h, *p["q"], self.q)
-            self._lin(h, *p["k"], self.k)
-            self._lin(h, *p["v"], self.v)
-            q, k = self._rope(self.q.view(1, self.H, self.D), self.k.view(1, self.Hkv, self.D))
-            _k.tq_cache_append(k.contiguous(), self.v.view(1, self.Hkv, self.D), c._k_hot[i], c._v_hot[i],
-                               c._k_codes[i], c._k_norms[i], c._v_codes[i], c._v_norms[i], c.PiK[i], c.PiV[i],
-                               c.decision_boundaries, c.bits, self.pos32)
-            _k.tq_decode_attn_out(q.contiguous(), c._k_codes[i], c._k_norms[i], c._v_codes[i], c._v_norms[i],
-                                  c._k_hot[i], c._v_hot[i], c.PiK[i], c.PiV[i], c.centroids, c.bits, self.len32,
-                                  self.max_len, self.scale, self.attn, self.attn_ws)
-            self._lin(self.attn.view(-1), *p["o"], self.o)
-            x = x + self.o.view(1, -1)
-            h = _rms(x, layer.post_attention_layernorm.weight, self.eps)
-            wg, tg = p["gate"]
-            wu, tu = p["up"]
-            if tg and tu:
-                _k.sparse_gateup_swiglu_out(h, wg, wu, tg, tu, self.m)
-            else:
-                g = F.linear(h, wg) if not tg else _k.sparse_gemv(h, wg, tg).view(1, -1)
-                u = F.linear(h, wu) if not tu else _k.sparse_gemv(h, wu, tu).view(1, -1)
-                self.m.copy_((F.silu(g) * u).view(-1))
-            self._lin(self.m, *p["down"], self.dn)
-            x = x + self.dn.view(1, -1)
-        self._finish(x)
+        lib = _lib.load()
+        st = _lib.stream_handle(self.dev)
+        ws, nb = self.ws.data_ptr(), self.ws.numel()
+        dims = ctypes.byref(self.dims)
+        _lib.check(lib.lkv_decode_begin(dims, self.model.model.embed_tokens.weight.data_ptr(), self.tok.data_ptr(),
+                                        self.pos64.data_ptr(), self.x.data_ptr(), ws, nb, st), "lkv_decode_begin")
+        for ls in self.layer_structs:
+            _lib.check(lib.lkv_decode_layer_step(dims, ctypes.byref(ls), self.x.data_ptr(), ws, nb, st),
+                       "lkv_decode_layer_step")
+        _lib.check(lib.lkv_decode_head(dims, self.final_norm.data_ptr(), self.lm_head_cm.data_ptr(),
+                                       self.x.data_ptr(), self.logits.data_ptr(), self.tok.data_ptr(),
+                                       self.pos64.data_ptr(), ws, nb, st), "lkv_decode_head")
+
+
+def _colmajor(w: torch.Tensor) -> torch.Tensor:
+    """[Z][N] row-major view of a weight W[N, Z] (column-major storage), copying only if needed."""
+    w = w.detach()
+    wt = w.t()
+    return wt if wt.is_contiguous() else wt.contiguous()
 
 
 class DenseEngine(_Base):

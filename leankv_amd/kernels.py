@@ -294,6 +294,29 @@ def tq_decode_attn(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK, PiV
                               seq_len_dev, max_len, scale, out)
 
 
+# ------------------------------------------------------------------ RMSNorm
+def rms_norm_out(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor) -> torch.Tensor:
+    """out = RMSNorm(x) * weight over the last dim (fp16), rounded like HF MistralRMSNorm.
+
+    Same summation order as the RMSNorm fused into the decode step's GEMV
+    prologues (lkv_rmsnorm), so both give bit-identical activations."""
+    require_cuda(x, weight, out)
+    Z = x.shape[-1]
+    if x.dtype != torch.float16 or weight.dtype != torch.float16 or out.dtype != torch.float16:
+        raise LeanKVError("rms_norm: x, weight and out must be float16")
+    if weight.numel() != Z or out.shape != x.shape or not out.is_contiguous():
+        raise LeanKVError("rms_norm: weight must have %d elements and out the shape of x" % Z)
+    xc = x.contiguous()
+    M = xc.numel() // Z if Z else 0
+    check(_lib_handle().lkv_rmsnorm(ptr(xc), ptr(weight.contiguous()), float(eps), M, Z, ptr(out),
+                                    stream_handle(x.device)), "lkv_rmsnorm")
+    return out
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    return rms_norm_out(x, weight, eps, torch.empty_like(x, memory_format=torch.contiguous_format))
+
+
 # ------------------------------------------------------- torch custom ops
 _LIB_DEF = None
 
@@ -310,12 +333,14 @@ def _register_ops() -> None:
     lib.define("tq_quantize_rotated(Tensor y, Tensor bounds, int bits) -> Tensor")
     lib.define("tq_dequantize(Tensor packed, Tensor norms, Tensor Pi, Tensor centroids, int bits) -> Tensor")
     lib.define("tq_rotate(Tensor x, Tensor Pi, bool transpose) -> Tensor")
+    lib.define("rms_norm(Tensor x, Tensor weight, float eps) -> Tensor")
     lib.impl("sparse_gemv", lambda x, w, t: sparse_gemv(x, w, t), "CUDA")
     lib.impl("sparse_gateup_swiglu", lambda x, wg, wu, tg, tu: sparse_gateup_swiglu(x, wg, wu, tg, tu), "CUDA")
     lib.impl("tq_quantize", lambda x, Pi, b, bits: tq_quantize(x, Pi, b, bits), "CUDA")
     lib.impl("tq_quantize_rotated", lambda y, b, bits: tq_quantize_rotated(y, b, bits), "CUDA")
     lib.impl("tq_dequantize", lambda p, n, Pi, c, bits: tq_dequantize(p, n, Pi, c, bits), "CUDA")
     lib.impl("tq_rotate", lambda x, Pi, tr: tq_rotate(x, Pi, tr), "CUDA")
+    lib.impl("rms_norm", lambda x, w, eps: rms_norm(x, w, eps), "CUDA")
 
     def _meta_gemv(x, w, t):
         return x.new_empty(w.shape[0], dtype=torch.float16)

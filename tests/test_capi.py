@@ -88,3 +88,47 @@ def test_python_wrappers_refuse_cpu_tensors():
         kernels.sparse_gemv(torch.zeros(8, dtype=torch.float16), w, 0.1)
     with pytest.raises(LeanKVError):
         kernels.colmajor_rows(torch.zeros(16, 8, dtype=torch.float16))  # row-major weight
+
+
+def _mistral_dims(**kw):
+    from leankv_amd import _lib
+
+    d = dict(hidden=4096, ffn=14336, vocab=32768, n_heads=32, n_kv_heads=8, max_len=4224, cap=4160, hot_cap=64,
+             bits=3, eps=1e-5, scale=128 ** -0.5, bounds=16, centroids=16, rope_cos=16, rope_sin=16)
+    d.update(kw)
+    return _lib.DecodeDims(**d)
+
+
+def test_decode_struct_layout_matches_header():
+    """ctypes mirrors of lkv_decode_dims / lkv_decode_layer have the C layout (field order, padding)."""
+    from leankv_amd import _lib
+
+    src = open(HEADER).read()
+    for cls, cname in ((_lib.DecodeDims, "lkv_decode_dims"), (_lib.DecodeLayer, "lkv_decode_layer")):
+        body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (cname, cname), src, flags=re.S).group(1)
+        body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+        names = re.findall(r"(\w+)\s*(?=[,;])", body)
+        assert [f[0] for f in cls._fields_] == names, cname
+    assert ctypes.sizeof(_lib.DecodeDims) == 8 * 8 + 4 * 3 + 4 + 8 * 4  # 4 bytes of padding before bounds
+    assert ctypes.sizeof(_lib.DecodeLayer) == 9 * 8 + 7 * 4 + 4 + 8 * 8
+
+
+def test_decode_dims_validated_without_launch():
+    from leankv_amd import _lib
+
+    lib = _lib.load()
+    ok = _mistral_dims()
+    assert lib.lkv_decode_workspace_bytes(ctypes.byref(ok)) > 0
+    for bad, msg in ((dict(hidden=4000), "hidden"), (dict(n_heads=36), "n_heads"), (dict(n_kv_heads=2), "n_heads"),
+                     (dict(bits=2), "bits"), (dict(hot_cap=65), "hot_cap"), (dict(cap=100), "cap"),
+                     (dict(rope_cos=None), "RoPE"), (dict(vocab=32770), "vocab")):
+        d = _mistral_dims(**bad)
+        assert lib.lkv_decode_workspace_bytes(ctypes.byref(d)) == 0, bad
+        p = ctypes.c_void_p(16)
+        assert lib.lkv_decode_begin(ctypes.byref(d), p, p, p, p, p, 1 << 30, None) == -1
+        assert msg in _lib.last_error(), (bad, _lib.last_error())
+    # workspace too small / null layer are rejected before any launch
+    p = ctypes.c_void_p(16)
+    assert lib.lkv_decode_begin(ctypes.byref(ok), p, p, p, p, p, 1024, None) == -1
+    assert "workspace" in _lib.last_error()
+    assert lib.lkv_decode_layer_step(ctypes.byref(ok), None, p, p, 1 << 30, None) == -1

@@ -122,11 +122,55 @@ def test_hf_path_teal_projections_match_reference(cuda):
         assert err < RTOL, (name, li, err)
 
 
+def test_engine_matches_reference_teal_off(cuda):
+    """Fused decode step (TEAL off: every projection dense through the same kernels) vs the CPU reference."""
+    from leankv_amd.engine import LeanKVEngine
+
+    model, _, prompt, state = _setup(cuda, seed=4)
+    ref = RefModel(state, model.config, None)
+    cache = _apply(model, None)
+    with torch.no_grad():
+        out = model(prompt.view(1, -1).to(cuda), past_key_values=cache, use_cache=True)
+    ref.forward(prompt)
+    eng = LeanKVEngine(model, cache, MAXLEN)
+    eng.start(torch.argmax(out.logits[0, -1]), PROMPT)
+    errs = []
+    with torch.no_grad():
+        for i in range(STEPS):
+            if i == 1:
+                eng.capture()
+            fed = int(eng.tok)
+            eng.step()
+            r = ref.forward(torch.tensor([fed]))
+            errs.append(ot.rel_err(eng.logits.float().cpu().numpy(), r.numpy()))
+    print("engine (TEAL off) vs reference: max step rel err %.3e" % max(errs))
+    assert max(errs) < RTOL
+    assert int(eng.pos64) == PROMPT + STEPS
+
+
+def _hip_rmsnorm(model):
+    """Route every RMSNorm module of the HF path through lkv_rmsnorm.
+
+    TEAL thresholds are fp16 quantile values, so activations exactly at a
+    threshold are common; a one-ulp difference in the RMSNorm output (torch's
+    reduction order vs the fused GEMV prologue's) then flips a mask bit, which
+    moves that projection by a few percent.  With the same RMSNorm arithmetic
+    on both sides the comparison below is exact up to the lm_head rounding."""
+    from leankv_amd.kernels import rms_norm
+
+    for m in model.modules():
+        if type(m).__name__.endswith("RMSNorm"):
+            m.forward = (lambda x, m=m: rms_norm(x, m.weight, m.variance_epsilon))
+
+
 def test_engine_matches_hf_path(cuda):
-    """Graph-captured engine == HF-patched path (same kernels, same glue semantics), token for token."""
+    """Fused decode step vs the HF-patched path (TEAL on), both fed the engine's tokens: the same
+    projections (TEAL masks included), RoPE, cache append, attention, SwiGLU and residual adds;
+    only lm_head differs (torch dense GEMM there, the sparse GEMV kernel at threshold 0 here)."""
     from leankv_amd.engine import LeanKVEngine
 
     model, th, prompt, _ = _setup(cuda, seed=3)
+    _hip_rmsnorm(model)
     cache = _apply(model, th)
     cache2 = _apply_cache_only(model)
     with torch.no_grad():
@@ -136,21 +180,26 @@ def test_engine_matches_hf_path(cuda):
     first = torch.argmax(out.logits[0, -1])
     eng = LeanKVEngine(model, cache2, MAXLEN)
     eng.start(first, PROMPT)
-    tok = int(first)
     errs, same = [], []
     with torch.no_grad():
         for i in range(STEPS):
             if i == 1:
                 eng.capture()
+            fed = int(eng.tok)
             eng.step()
-            hf = model(torch.tensor([[tok]], device=cuda), past_key_values=cache, use_cache=True).logits[0, -1]
+            hf = model(torch.tensor([[fed]], device=cuda), past_key_values=cache, use_cache=True).logits[0, -1]
             errs.append(float((eng.logits.float() - hf.float()).norm() / hf.float().norm()))
             same.append(int(eng.tok) == int(torch.argmax(hf)))
-            tok = int(eng.tok)
-    print("engine vs hf max rel err", max(errs), "token agreement", sum(same), "/", len(same))
+    print("engine vs hf: rel err max %.3e median %.3e, token agreement %d/%d"
+          % (max(errs), float(np.median(errs)), sum(same), len(same)))
     assert max(errs) < 1e-3
     assert all(same)
     assert int(eng.pos64) == PROMPT + STEPS
+    # the caches the two paths built are identical
+    for li in range(model.config.num_hidden_layers):
+        for a, b in ((cache._k_codes, cache2._k_codes), (cache._v_codes, cache2._v_codes),
+                     (cache._k_norms, cache2._k_norms), (cache._k_hot, cache2._k_hot), (cache._v_hot, cache2._v_hot)):
+            assert torch.equal(a[li], b[li]), li
 
 
 def _apply_cache_only(model, max_len=MAXLEN):

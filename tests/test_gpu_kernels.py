@@ -116,6 +116,24 @@ def test_gateup_distinct_thresholds(cuda):
     assert ot.max_rel_err(h.numpy(), href) < RTOL
 
 
+@pytest.mark.parametrize("M,Z", [(1, 4096), (3, 512), (2, 14336)])
+def test_rms_norm_matches_hf_rounding(cuda, M, Z):
+    """lkv_rmsnorm vs HF MistralRMSNorm in fp64 (modeling_mistral.py:190-197): every element within one
+    fp16 ulp of the fp64-exact RMSNorm, the fp16 product with the weight as HF rounds it."""
+    from leankv_amd import kernels
+
+    g = torch.Generator().manual_seed(M * Z)
+    x = (torch.randn(M, Z, generator=g) * 3).half()
+    w = (1 + 0.1 * torch.randn(Z, generator=g)).half()
+    y = kernels.rms_norm(x.to(cuda), w.to(cuda), 1e-5).cpu()
+    x64 = x.double()
+    u = (x64 * torch.rsqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-5)).half()  # exact rstd, fp16 cast
+    ref = (w.double() * u.double()).half()
+    ulp = torch.finfo(torch.float16).eps * ref.double().abs().clamp_min(2 ** -14)
+    assert ((y.double() - ref.double()).abs() <= 2 * ulp).all()
+    assert (y != ref).float().mean() < 0.02  # almost all bit-equal; the rest one rounding step apart
+
+
 # ----------------------------------------------------------------- TurboQuant
 def _kv(shape, seed, outliers=(0, 31, 64, 127)):
     g = torch.Generator().manual_seed(seed)
