@@ -161,8 +161,9 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* __res
 }
 
 struct PrepArgs {
-  const float* part;  // q|k|v partials
-  size_t off[3];
+  const float* pq;  // q, k, v partials ([slab][chunk][256] each)
+  const float* pk;
+  const float* pv;
   int nchunk;
   const uint16_t* cos;
   const uint16_t* sin;
@@ -181,52 +182,94 @@ struct PrepArgs {
   float* qrot;
 };
 
-// One block per kv head: its G query heads, its key and its value.
+// Grid (kv heads, 2): block (h, 0) is the key side -- its G query heads and
+// key: RoPE, the key leaving the hot window quantized with PiK, the query
+// heads rotated by PiK (rows 1..G of the same MFMA tile), the new key into the
+// ring; block (h, 1) is the value side with PiV.  The block's 64 KB rotation
+// matrix is fetched first, with fully coalesced 16-byte loads, and staged in
+// LDS for the MFMA operand reads; the MFMA arithmetic is tq_common.h's, so the
+// codes equal lkv_tq_cache_append's and q_rot equals lkv_tq_rotate's.
 template <int BITS>
 __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
-  constexpr int kCols = (kMaxG + 2) * kD / kThreads;
-  __shared__ float s_raw[kMaxG + 2][kD];   // q heads, k, v as projected (fp16 values)
-  __shared__ float s_rope[kMaxG + 1][kD];  // q heads, k after RoPE
-  __shared__ uint8_t s_codes[2][tq::kRows * kD];
+  constexpr int kCols = (kMaxG + 1) * kD / kThreads + 1;
+  constexpr int kPiLd = kD + 1;  // padded LDS row
+  __shared__ float s_pi[kD * kPiLd];
+  __shared__ float s_raw[kMaxG + 1][kD];   // key side: q heads then k; value side: v in row 0
+  __shared__ float s_rope[kMaxG + 1][kD];  // key side: q heads then k after RoPE
+  __shared__ uint8_t s_codes[tq::kRows * kD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kvh = blockIdx.x;
+  const bool vside = blockIdx.y == 1;
   const int G = A.Hq / A.Hkv;
-  const int ncol = (G + 2) * kD;
+  const int nvec = vside ? 1 : G + 1;  // projected vectors this block needs
+  const int ncol = nvec * kD;
   const int nc = A.nchunk;
+  const float* Pi = vside ? A.PiV : A.PiK;
 
-  // ---- 1. projections, summed over chunks in chunk order, rounded to fp16
+  // ---- 0. the rotation matrix, 16 coalesced float4 per thread, in flight
+  //      while the projections are summed
+  const int pos = A.state[0];
+  float4 pr[kD * kD / 4 / kThreads];
+#pragma unroll
+  for (int i = 0; i < kD * kD / 4 / kThreads; ++i) pr[i] = reinterpret_cast<const float4*>(Pi)[i * kThreads + tid];
+  float bd[(1 << BITS) - 1];
+#pragma unroll
+  for (int i = 0; i < (1 << BITS) - 1; ++i) bd[i] = A.bounds[i];
+  // Everything that depends only on pos, also in flight during the sums:
+  // the row leaving the hot window (row 0 of the MFMA tile: lanes r == 0 use
+  // it, the others load the same 64 bytes) and this position's RoPE row.
+  const int slot = pos % A.hot_cap;
+  const int ev = pos - A.hot_cap;
+  const bool evict = pos >= A.hot_cap && ev < A.cap;
+  const int r = lane & 15, c0 = 32 * (lane >> 4);
+  const size_t hrow = (static_cast<size_t>(kvh) * A.hot_cap + slot) * kD;
+  uint16_t* hot = vside ? A.v_hot : A.k_hot;
+  uint4 hraw[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) hraw[v] = reinterpret_cast<const uint4*>(hot + hrow + c0)[v];
+  const uint16_t cs_d = A.cos[static_cast<size_t>(pos) * kD + (tid & (kD - 1))];
+  const uint16_t sn_d = A.sin[static_cast<size_t>(pos) * kD + (tid & (kD - 1))];
+
+  // ---- 1. projections, summed over chunks in chunk order, rounded to fp16.
+  //      A wave's 64 columns never straddle a 128-column head, so validity
+  //      and the source matrix are uniform per wave (scalar branches, loads
+  //      issued back to back).
   {
     const float* src[kCols];
     bool ok[kCols];
     float acc[kCols];
 #pragma unroll
     for (int e = 0; e < kCols; ++e) {
-      const int c = e * kThreads + tid;
-      ok[e] = c < ncol;
+      const int c0 = __builtin_amdgcn_readfirstlane(e * kThreads + (tid & ~(kWave - 1)));
+      ok[e] = c0 < ncol;
+      const int c = c0 + lane;
       const int which = c / kD, d = c % kD;
-      int seg, col;
-      if (which < G) {
-        seg = 0;
-        col = (kvh * G + which) * kD + d;
-      } else {
-        seg = which == G ? 1 : 2;
+      int col;
+      const float* base;
+      if (vside) {
         col = kvh * kD + d;
+        base = A.pv;
+      } else {
+        col = which < G ? (kvh * G + which) * kD + d : kvh * kD + d;
+        base = which < G ? A.pq : A.pk;
       }
-      src[e] = ok[e] ? A.part + A.off[seg] + static_cast<size_t>(col / kGemvBN) * nc * kGemvBN + (col % kGemvBN)
-                     : A.part;
+      src[e] = base + static_cast<size_t>(col / kGemvBN) * nc * kGemvBN + (col % kGemvBN);
       acc[e] = 0.f;
     }
     for (int k0 = 0; k0 < nc; k0 += 8) {
       float v[kCols][8];
 #pragma unroll
       for (int e = 0; e < kCols; ++e)
+        if (ok[e]) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          v[e][i] = (ok[e] && k0 + i < nc) ? src[e][static_cast<size_t>(k0 + i) * kGemvBN] : 0.f;
+          for (int i = 0; i < 8; ++i) v[e][i] = src[e][static_cast<size_t>(min(k0 + i, nc - 1)) * kGemvBN];
+        }
 #pragma unroll
       for (int e = 0; e < kCols; ++e)
+        if (ok[e]) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[e] += v[e][i];
+          for (int i = 0; i < 8; ++i) acc[e] += k0 + i < nc ? v[e][i] : 0.f;
+        }
     }
 #pragma unroll
     for (int e = 0; e < kCols; ++e) {
@@ -234,82 +277,82 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
       if (ok[e]) s_raw[c / kD][c % kD] = h2f(f2h(acc[e]));
     }
   }
+#pragma unroll
+  for (int i = 0; i < kD * kD / 4 / kThreads; ++i) {
+    const int f = i * kThreads + tid;  // float4 index: row f / 32, columns 4 (f % 32) ..
+    float* dst = s_pi + (f >> 5) * kPiLd + 4 * (f & 31);
+    dst[0] = pr[i].x;
+    dst[1] = pr[i].y;
+    dst[2] = pr[i].z;
+    dst[3] = pr[i].w;
+  }
   __syncthreads();
 
   // ---- 2. RoPE: x*cos + rotate_half(x)*sin with fp16 products and sum
   //      (apply_rotary_pos_emb on fp16 tensors, modeling_mistral.py)
-  const int pos = A.state[0];
-  {
-    const uint16_t* cs = A.cos + static_cast<size_t>(pos) * kD;
-    const uint16_t* sn = A.sin + static_cast<size_t>(pos) * kD;
+  if (!vside) {
+    const float cf = h2f(cs_d), sf = h2f(sn_d);  // this thread's d = tid % 128 for every e below
     for (int e = tid; e < (G + 1) * kD; e += kThreads) {
-      const int r = e / kD, d = e % kD;
-      const float xv = s_raw[r][d];
-      const float rh = d < kD / 2 ? -s_raw[r][d + kD / 2] : s_raw[r][d - kD / 2];
-      const float o = h2f(f2h(h2f(f2h(xv * h2f(cs[d]))) + h2f(f2h(rh * h2f(sn[d])))));
-      s_rope[r][d] = o;
-      if (r < G) A.q16[static_cast<size_t>(kvh * G + r) * kD + d] = f2h(o);
+      const int rr = e / kD, d = e % kD;
+      const float xv = s_raw[rr][d];
+      const float rh = d < kD / 2 ? -s_raw[rr][d + kD / 2] : s_raw[rr][d - kD / 2];
+      const float o = h2f(f2h(h2f(f2h(xv * cf)) + h2f(f2h(rh * sf))));
+      s_rope[rr][d] = o;
+      if (rr < G) A.q16[static_cast<size_t>(kvh * G + rr) * kD + d] = f2h(o);
     }
+    __syncthreads();
   }
-  __syncthreads();
 
-  // ---- 3. one K tile (row 0: the key leaving the hot window, normalised;
-  //      rows 1..G: the query heads) and one V tile (row 0: the value).
-  const int slot = pos % A.hot_cap;
-  const int ev = pos - A.hot_cap;
-  const bool evict = pos >= A.hot_cap && ev < A.cap;
-  float bK[2][32], bV[2][32];
-  tq::load_pi_operand(A.PiK, false, wave, lane, bK);
-  tq::load_pi_operand(A.PiV, false, wave, lane, bV);
-  const int r = lane & 15, c0 = 32 * (lane >> 4);
-  const size_t hrow = (static_cast<size_t>(kvh) * A.hot_cap + slot) * kD;
-  float aK[32], aV[32];
-  if (r == 0 && evict) {
-    tq::load_row_f16(A.k_hot + hrow + c0, aK);
-    tq::load_row_f16(A.v_hot + hrow + c0, aV);
+  // ---- 3. one 16-row tile: row 0 = the vector leaving the hot window
+  //      (normalised), rows 1..G = the query heads on the key side
+  float a[32];
+  if (r == 0) {
+    // tq::load_row_f16's conversion of the preloaded row (zero when nothing leaves)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint32_t w[4] = {hraw[v].x, hraw[v].y, hraw[v].z, hraw[v].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[8 * v + 2 * i] = evict ? h2f(static_cast<uint16_t>(w[i] & 0xffffu)) : 0.f;
+        a[8 * v + 2 * i + 1] = evict ? h2f(static_cast<uint16_t>(w[i] >> 16)) : 0.f;
+      }
+    }
   } else {
 #pragma unroll
-    for (int s = 0; s < 32; ++s) {
-      aK[s] = (r >= 1 && r <= G) ? s_rope[r - 1][c0 + s] : 0.f;
-      aV[s] = 0.f;
-    }
+    for (int s = 0; s < 32; ++s) a[s] = (!vside && r <= G) ? s_rope[r - 1][c0 + s] : 0.f;
+  }
+  float bop[2][32];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const float* row = s_pi + (8 * (lane & 15) + 2 * wave + t) * kPiLd + c0;
+#pragma unroll
+    for (int s = 0; s < 32; ++s) bop[t][s] = row[s];
   }
   // cache.py:141 quantizes flush_k.float(): fp32 semantics on the fp16 data.
-  const float nK = tq::normalize_row_f32_if(aK, r == 0);
-  const float nV = tq::normalize_row_f32_if(aV, r == 0);
-  f32x4 accK[2], accV[2];
-  tq::rotate_tile(aK, bK, accK);
-  tq::rotate_tile(aV, bV, accV);
+  const float nrm = tq::normalize_row_f32_if(a, r == 0);
+  f32x4 acc[2];
+  tq::rotate_tile(a, bop, acc);
+  if (!vside) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * (lane >> 4) + i;
-      const int dim = 8 * (lane & 15) + 2 * wave + t;
-      if (row >= 1 && row <= G) A.qrot[static_cast<size_t>(kvh * G + row - 1) * kD + dim] = accK[t][i];
-    }
+      for (int i = 0; i < 4; ++i) {
+        const int row = 4 * (lane >> 4) + i;
+        const int dim = 8 * (lane & 15) + 2 * wave + t;
+        if (row >= 1 && row <= G) A.qrot[static_cast<size_t>(kvh * G + row - 1) * kD + dim] = acc[t][i];
+      }
+  }
   if (evict) {
-    float bd[(1 << BITS) - 1];
-#pragma unroll
-    for (int i = 0; i < (1 << BITS) - 1; ++i) bd[i] = A.bounds[i];
-    tq::codes_to_lds<BITS>(accK, bd, wave, lane, s_codes[0]);
-    tq::codes_to_lds<BITS>(accV, bd, wave, lane, s_codes[1]);
-    if (tid == 0) {
-      A.k_norms[static_cast<size_t>(kvh) * A.cap + ev] = nK;
-      A.v_norms[static_cast<size_t>(kvh) * A.cap + ev] = nV;
-    }
+    tq::codes_to_lds<BITS>(acc, bd, wave, lane, s_codes);
+    if (tid == 0) (vside ? A.v_norms : A.k_norms)[static_cast<size_t>(kvh) * A.cap + ev] = nrm;
   }
   __syncthreads();  // codes staged; every read of the old hot slot is done
   if (evict) {
     const int64_t roff = (static_cast<int64_t>(kvh) * A.cap + ev) * tq::row_bytes_for(BITS);
-    tq::pack_store<BITS>(s_codes[0], A.k_codes, 0, 1, [=](int64_t) { return roff; });
-    tq::pack_store<BITS>(s_codes[1], A.v_codes, 0, 1, [=](int64_t) { return roff; });
+    tq::pack_store<BITS>(s_codes, vside ? A.v_codes : A.k_codes, 0, 1, [=](int64_t) { return roff; });
   }
   // ---- 4. the new token into its ring slot
-  if (tid < kD) {
-    A.k_hot[hrow + tid] = f2h(s_rope[G][tid]);
-    A.v_hot[hrow + tid] = f2h(s_raw[G + 1][tid]);
-  }
+  if (tid < kD) hot[hrow + tid] = f2h(vside ? s_raw[0][tid] : s_rope[G][tid]);
 }
 
 struct Cand {
@@ -457,10 +500,9 @@ extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_deco
   // 2. prep
   {
     PrepArgs A{};
-    A.part = reinterpret_cast<const float*>(ws + p.off_pqkv);
-    A.off[0] = 0;
-    A.off[1] = gemv_part_floats(p.nq, p.nc_qkv);
-    A.off[2] = A.off[1] + gemv_part_floats(p.nkv, p.nc_qkv);
+    A.pq = reinterpret_cast<const float*>(ws + p.off_pqkv);
+    A.pk = A.pq + gemv_part_floats(p.nq, p.nc_qkv);
+    A.pv = A.pk + gemv_part_floats(p.nkv, p.nc_qkv);
     A.nchunk = p.nc_qkv;
     A.cos = static_cast<const uint16_t*>(d.rope_cos);
     A.sin = static_cast<const uint16_t*>(d.rope_sin);
@@ -481,9 +523,9 @@ extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_deco
     A.q16 = reinterpret_cast<uint16_t*>(ws + p.off_q16);
     A.qrot = reinterpret_cast<float*>(ws + p.off_qrot);
     if (d.bits == 3)
-      hipLaunchKernelGGL((prep_kernel<3>), dim3(static_cast<unsigned>(p.Hkv)), dim3(kThreads), 0, st, A);
+      hipLaunchKernelGGL((prep_kernel<3>), dim3(static_cast<unsigned>(p.Hkv), 2), dim3(kThreads), 0, st, A);
     else
-      hipLaunchKernelGGL((prep_kernel<4>), dim3(static_cast<unsigned>(p.Hkv)), dim3(kThreads), 0, st, A);
+      hipLaunchKernelGGL((prep_kernel<4>), dim3(static_cast<unsigned>(p.Hkv), 2), dim3(kThreads), 0, st, A);
     LKV_LAUNCH_CHECK("decode prep");
   }
   // 3-4. attention

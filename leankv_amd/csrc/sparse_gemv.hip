@@ -38,8 +38,6 @@
 namespace lkv {
 namespace {
 
-constexpr int kUnroll = 8;
-
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void fma8(float (&acc)[8], const u32x4v& w, float xv) {
@@ -55,25 +53,25 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
 
-// Stream the padded survivor list: total is a multiple of kUnroll * SLOTS.
-template <int SLOTS>
+// Stream the padded survivor list: total is a multiple of U * SLOTS.
+template <int SLOTS, int U>
 __device__ __forceinline__ void stream_rows(__amdgpu_buffer_rsrc_t A, uint32_t row_bytes, uint32_t col_bytes,
                                             const int* __restrict__ idx, const float* __restrict__ xv, int total,
                                             int slot, float (&acc)[8]) {
-  for (int s = slot; s < total; s += kUnroll * SLOTS) {
-    int r[kUnroll];
-    float xs[kUnroll];
+  for (int s = slot; s < total; s += U * SLOTS) {
+    int r[U];
+    float xs[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       r[u] = idx[s + u * SLOTS];
       xs[u] = xv[s + u * SLOTS];
     }
-    u32x4v w[kUnroll];
+    u32x4v w[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
+    for (int u = 0; u < U; ++u)
       w[u] = __builtin_amdgcn_raw_buffer_load_b128(A, static_cast<uint32_t>(r[u]) * row_bytes + col_bytes, 0, 0);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) fma8(acc, w[u], xs[u]);
+    for (int u = 0; u < U; ++u) fma8(acc, w[u], xs[u]);
   }
 }
 
@@ -138,13 +136,13 @@ __device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float*
   __syncthreads();
 }
 
-template <int BZ, bool DUAL, int MODE>
+template <int BZ, bool DUAL, int MODE, int U>
 __global__ __launch_bounds__(kGemvThreads) void sparse_gemv_kernel(GemvArgs G) {
   constexpr int BN = kGemvBN;
   constexpr int LPR = BN / 8;                // lanes per row segment
   constexpr int SLOTS = kGemvThreads / LPR;  // rows processed side by side
   constexpr int NL = DUAL ? 2 : 1;
-  constexpr int PAD = kUnroll * SLOTS;       // list granularity
+  constexpr int PAD = U * SLOTS;             // list granularity
   static_assert(BZ % kGemvThreads == 0, "BZ must be a multiple of 256");
 
   __shared__ int s_idx[NL][BZ + PAD];
@@ -236,9 +234,9 @@ __global__ __launch_bounds__(kGemvThreads) void sparse_gemv_kernel(GemvArgs G) {
   for (int l = 0; l < NL; ++l)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[l][j] = 0.f;
-  stream_rows<SLOTS>(make_rsrc(G.A[seg], a_bytes), row_bytes, col_bytes, s_idx[0], s_xv[0], total[0], slot, acc[0]);
+  stream_rows<SLOTS, U>(make_rsrc(G.A[seg], a_bytes), row_bytes, col_bytes, s_idx[0], s_xv[0], total[0], slot, acc[0]);
   if (DUAL)
-    stream_rows<SLOTS>(make_rsrc(G.A_up, a_bytes), row_bytes, col_bytes, s_idx[NL - 1], s_xv[NL - 1], total[NL - 1],
+    stream_rows<SLOTS, U>(make_rsrc(G.A_up, a_bytes), row_bytes, col_bytes, s_idx[NL - 1], s_xv[NL - 1], total[NL - 1],
                        slot, acc[NL - 1]);
 
   // ---- 3. cross-slot reduction through LDS
@@ -301,17 +299,26 @@ int gemv_pick_bz(int64_t slabs, int64_t Z) {
 
 namespace {
 
-template <int BZ>
+template <int BZ, int U>
 bool launch_bz(const GemvArgs& G, bool dual, int mode, dim3 grid, hipStream_t st) {
   const dim3 blk(kGemvThreads);
   switch (mode * 2 + (dual ? 1 : 0)) {
-    case kInRaw * 2: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, false, kInRaw>), grid, blk, 0, st, G); return true;
-    case kInRaw * 2 + 1: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, true, kInRaw>), grid, blk, 0, st, G); return true;
-    case kInRmsNorm * 2: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, false, kInRmsNorm>), grid, blk, 0, st, G); return true;
-    case kInRmsNorm * 2 + 1: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, true, kInRmsNorm>), grid, blk, 0, st, G); return true;
-    case kInSwiglu * 2: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, false, kInSwiglu>), grid, blk, 0, st, G); return true;
+    case kInRaw * 2: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, false, kInRaw, U>), grid, blk, 0, st, G); return true;
+    case kInRaw * 2 + 1: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, true, kInRaw, U>), grid, blk, 0, st, G); return true;
+    case kInRmsNorm * 2: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, false, kInRmsNorm, U>), grid, blk, 0, st, G); return true;
+    case kInRmsNorm * 2 + 1: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, true, kInRmsNorm, U>), grid, blk, 0, st, G); return true;
+    case kInSwiglu * 2: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, false, kInSwiglu, U>), grid, blk, 0, st, G); return true;
     default: return false;
   }
+}
+
+// Rows each lane keeps in flight (8 default; LKV_GEMV_UNROLL=16 for tuning sweeps).
+int gemv_unroll() {
+  static const int u = [] {
+    const char* env = getenv("LKV_GEMV_UNROLL");
+    return env && atoi(env) == 16 ? 16 : 8;
+  }();
+  return u;
 }
 
 }  // namespace
@@ -320,9 +327,10 @@ int gemv_launch(const GemvArgs& G, int bz, bool dual, int mode, int nslab_total,
   if (nslab_total <= 0) return LKV_OK;
   const dim3 grid(static_cast<unsigned>(nslab_total), static_cast<unsigned>(G.nchunk));
   bool ok = false;
-  if (bz == 256) ok = launch_bz<256>(G, dual, mode, grid, st);
-  else if (bz == 512) ok = launch_bz<512>(G, dual, mode, grid, st);
-  else if (bz == 1024) ok = launch_bz<1024>(G, dual, mode, grid, st);
+  const bool u16 = gemv_unroll() == 16;
+  if (bz == 256) ok = u16 ? launch_bz<256, 16>(G, dual, mode, grid, st) : launch_bz<256, 8>(G, dual, mode, grid, st);
+  else if (bz == 512) ok = u16 ? launch_bz<512, 16>(G, dual, mode, grid, st) : launch_bz<512, 8>(G, dual, mode, grid, st);
+  else if (bz == 1024) ok = u16 ? launch_bz<1024, 16>(G, dual, mode, grid, st) : launch_bz<1024, 8>(G, dual, mode, grid, st);
   if (!ok) {
     set_error("sparse_gemv: no kernel for chunk %d, mode %d, dual %d", bz, mode, dual ? 1 : 0);
     return LKV_ERR_INVALID;

@@ -100,23 +100,36 @@ struct BlockRegs {
   float vnorm[2];
 };
 
+// Loads past t_end read the last valid token (t_end - 1 >= t0) and are zeroed
+// afterwards: every load is unconditional, so they issue back to back
+// instead of one branch + wait per element.
 __device__ __forceinline__ void load_block(BlockRegs& R, int t0, int t_end, int lane, const uint8_t* kc,
                                            const float* kn, const uint8_t* vc, const float* vn) {
   const int g = lane >> 4, w = lane & 15;
+  u32x4 kr[2];
+  float knv[2], vnv[2];
+  uint32_t vd[8];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
-    const int tok = t0 + 16 * tt + (lane & 15);
-    const bool ok = tok < t_end;
-    R.kraw[tt] = ok ? *reinterpret_cast<const u32x4*>(kc + static_cast<size_t>(tok) * kRowB + 16 * g)
-                    : u32x4{0u, 0u, 0u, 0u};
-    R.knorm[tt] = ok ? kn[tok] : 0.f;
-    R.vnorm[tt] = ok ? vn[tok] : 0.f;
+    const int tok = min(t0 + 16 * tt + (lane & 15), t_end - 1);
+    kr[tt] = *reinterpret_cast<const u32x4*>(kc + static_cast<size_t>(tok) * kRowB + 16 * g);
+    knv[tt] = kn[tok];
+    vnv[tt] = vn[tok];
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int tok = t0 + 8 * g + i;
-    R.vdw[i] = tok < t_end ? *reinterpret_cast<const uint32_t*>(vc + static_cast<size_t>(tok) * kRowB + 4 * w) : 0u;
+    const int tok = min(t0 + 8 * g + i, t_end - 1);
+    vd[i] = *reinterpret_cast<const uint32_t*>(vc + static_cast<size_t>(tok) * kRowB + 4 * w);
   }
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const bool ok = t0 + 16 * tt + (lane & 15) < t_end;
+    R.kraw[tt] = ok ? kr[tt] : u32x4{0u, 0u, 0u, 0u};
+    R.knorm[tt] = ok ? knv[tt] : 0.f;
+    R.vnorm[tt] = ok ? vnv[tt] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) R.vdw[i] = t0 + 8 * g + i < t_end ? vd[i] : 0u;
 }
 
 template <int GMAX>
@@ -143,32 +156,43 @@ __global__ __launch_bounds__(kThreads) void tq_attn_split_kernel(AttnParams P) {
     }
     return;
   }
+  // Loads first, in the order they are consumed: the wave's first token
+  // block, the centroid pairs of the LUT, the rotated query.  They are all in
+  // flight before the first wait.
+  const uint8_t* kc = P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB;
+  const uint8_t* vc = P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB;
+  const float* kn = P.k_norms + bh * static_cast<size_t>(P.cap);
+  const float* vn = P.v_norms + bh * static_cast<size_t>(P.cap);
+  BlockRegs cur;
+  int t0 = t_begin + wave * kBlk;
+  load_block(cur, min(t0, t_end - 1), t_end, lane, kc, kn, vc, vn);  // waves past t_end never use it
+  float c_lo, c_hi;
   {
-    const int lo = tid & 15, hi = tid >> 4;
     const int cmax = P.ncent - 1;
-    s_lut[tid] = pack2h(P.centroids[min(lo, cmax)], P.centroids[min(hi, cmax)]);
+    c_lo = P.centroids[min(tid & 15, cmax)];
+    c_hi = P.centroids[min(tid >> 4, cmax)];
   }
   // A operand of the score MFMA: rotated query x scale*log2(e), head
   // h = lane%16, dims 32*(lane/16) + 8*kb + i for k-block kb.
   const int h = lane & 15, g = lane >> 4;
   u32x4 qa[4];
+  {
+    // rows h >= G read head G - 1 and are zeroed: unconditional loads
+    const float4* src = reinterpret_cast<const float4*>(
+        P.qrot + (static_cast<size_t>(b) * P.Hq + kvh * G + min(h, G - 1)) * kD + 32 * g);
+    float4 f[8];
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    if (h < G) {
-      const float* src = P.qrot + (static_cast<size_t>(b) * P.Hq + kvh * G + h) * kD + 32 * g + 8 * kb;
-      const float4 f0 = reinterpret_cast<const float4*>(src)[0];
-      const float4 f1 = reinterpret_cast<const float4*>(src)[1];
-      const float sl = P.scale_log2;
-      qa[kb] = u32x4{pack2h(f0.x * sl, f0.y * sl), pack2h(f0.z * sl, f0.w * sl), pack2h(f1.x * sl, f1.y * sl),
-                     pack2h(f1.z * sl, f1.w * sl)};
-    } else {
-      qa[kb] = u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < 8; ++i) f[i] = src[i];
+    s_lut[tid] = pack2h(c_lo, c_hi);
+    const float sl = P.scale_log2;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const float4 f0 = f[2 * kb], f1 = f[2 * kb + 1];
+      qa[kb] = h < G ? u32x4{pack2h(f0.x * sl, f0.y * sl), pack2h(f0.z * sl, f0.w * sl), pack2h(f1.x * sl, f1.y * sl),
+                             pack2h(f1.z * sl, f1.w * sl)}
+                     : u32x4{0u, 0u, 0u, 0u};
     }
   }
-  const uint8_t* kc = P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB;
-  const uint8_t* vc = P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB;
-  const float* kn = P.k_norms + bh * static_cast<size_t>(P.cap);
-  const float* vn = P.v_norms + bh * static_cast<size_t>(P.cap);
 
   float m[4], l[4];
   f32x4 o[8];
@@ -179,10 +203,6 @@ __global__ __launch_bounds__(kThreads) void tq_attn_split_kernel(AttnParams P) {
   }
 #pragma unroll
   for (int t = 0; t < 8; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  BlockRegs cur;
-  int t0 = t_begin + wave * kBlk;
-  if (t0 < t_end) load_block(cur, t0, t_end, lane, kc, kn, vc, vn);
   __syncthreads();  // LUT ready
   for (; t0 < t_end; t0 += kWaves * kBlk) {
     const int tn = t0 + kWaves * kBlk;
@@ -348,23 +368,15 @@ __global__ __launch_bounds__(kCombThreads) void tq_attn_combine_kernel(AttnParam
   const int d = tid & (kD - 1), qd = tid >> 7;
 
   // ---- A. every independent load up front
-  float ms = -INFINITY, ls = 0.f;
-  if (tid < ns) {
-    ms = recs[static_cast<size_t>(tid) * RF + hh];
-    ls = recs[static_cast<size_t>(tid) * RF + G + hh];
-  }
-  // hot score partial: token j = tid / 8, dims 16 * (tid % 8) .. +16
-  const int j = tid >> 3, part = tid & 7;
-  const bool hj = j < hot_len;
-  float sdot = 0.f;
+  // Every load below is unconditional from a clamped, always valid address
+  // (split ns - 1, hot token 0 / slot cold_len % hot_cap) and zeroed after,
+  // so all of them are in flight together.
+  float ms, ls;
   {
-    const int slot = hj ? (cold_len + j) % P.hot_cap : 0;
-    const uint4* kp = reinterpret_cast<const uint4*>(P.k_hot + hot_base + static_cast<size_t>(slot) * kD + 16 * part);
-    const uint4* qp = reinterpret_cast<const uint4*>(P.q + (static_cast<size_t>(b) * P.Hq + hq) * kD + 16 * part);
-    const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
-    const uint4 k0 = hj ? kp[0] : z4, k1 = hj ? kp[1] : z4;
-    const uint4 q0 = qp[0], q1 = qp[1];
-    sdot = dot8_f16(k0, q0) + dot8_f16(k1, q1);
+    const size_t sr = static_cast<size_t>(min(tid, ns - 1)) * RF;
+    const float m_ = recs[sr + hh], l_ = recs[sr + G + hh];
+    ms = tid < ns ? m_ : -INFINITY;
+    ls = tid < ns ? l_ : 0.f;
   }
   float piv[32];
 #pragma unroll
@@ -373,15 +385,25 @@ __global__ __launch_bounds__(kCombThreads) void tq_attn_combine_kernel(AttnParam
 #pragma unroll
   for (int i = 0; i < kHotMax / 4; ++i) {
     const int jj = qd + 4 * i;
-    hv[i] = jj < hot_len ? P.v_hot[hot_base + static_cast<size_t>((cold_len + jj) % P.hot_cap) * kD + d] : 0;
+    hv[i] = P.v_hot[hot_base + static_cast<size_t>((cold_len + (jj < hot_len ? jj : 0)) % P.hot_cap) * kD + d];
   }
   float ca[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int s = qd + 4 * i;
-    ca[i] = s < ns ? recs[static_cast<size_t>(s) * RF + 2 * G + hh * kD + d] : 0.f;
-  }
+  for (int i = 0; i < 16; ++i)
+    ca[i] = recs[static_cast<size_t>(min(qd + 4 * i, ns - 1)) * RF + 2 * G + hh * kD + d];
 
+  // hot score partial: token j = tid / 8, dims 16 * (tid % 8) .. +16
+  const int j = tid >> 3, part = tid & 7;
+  const bool hj = j < hot_len;
+  float sdot = 0.f;
+  {
+    const int slot = (cold_len + (hj ? j : 0)) % P.hot_cap;
+    const uint4* kp = reinterpret_cast<const uint4*>(P.k_hot + hot_base + static_cast<size_t>(slot) * kD + 16 * part);
+    const uint4* qp = reinterpret_cast<const uint4*>(P.q + (static_cast<size_t>(b) * P.Hq + hq) * kD + 16 * part);
+    const uint4 k0 = kp[0], k1 = kp[1];
+    const uint4 q0 = qp[0], q1 = qp[1];
+    sdot = dot8_f16(k0, q0) + dot8_f16(k1, q1);  // tokens past hot_len are masked by `score`
+  }
   // ---- B. softmax statistics over cold splits and hot tokens
   sdot += __shfl_xor(sdot, 1);
   sdot += __shfl_xor(sdot, 2);
@@ -417,10 +439,8 @@ __global__ __launch_bounds__(kCombThreads) void tq_attn_combine_kernel(AttnParam
   }
   for (int s0 = 64; s0 < ns; s0 += 64) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int s = s0 + qd + 4 * i;
-      ca[i] = s < ns ? recs[static_cast<size_t>(s) * RF + 2 * G + hh * kD + d] : 0.f;
-    }
+    for (int i = 0; i < 16; ++i)
+      ca[i] = recs[static_cast<size_t>(min(s0 + qd + 4 * i, ns - 1)) * RF + 2 * G + hh * kD + d];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int s = s0 + qd + 4 * i;
@@ -432,7 +452,8 @@ __global__ __launch_bounds__(kCombThreads) void tq_attn_combine_kernel(AttnParam
 #pragma unroll
   for (int i = 0; i < kHotMax / 4; ++i) {
     const int jj = qd + 4 * i;
-    if (jj < hot_len) hot = fmaf(s_p[jj], h2f(hv[i]), hot);
+    const float t = s_p[jj < hot_len ? jj : 0] * h2f(hv[i]);
+    hot += jj < hot_len ? t : 0.f;  // select after the product: an unwritten slot may hold NaN
   }
   s_part[0][qd][d] = cold;
   s_part[1][qd][d] = hot;
