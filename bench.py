@@ -104,27 +104,119 @@ def bench_gemv(args, torch):
     def launch(i):
         x, Wc, t, _, y = sets[i]
         kernels.sparse_gemv_out(x, Wc, t, y)
-    wall, kmean, kmed = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
+    wall, omean, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
     surv = statistics.mean(s[3] for s in sets)
     alg_bytes = surv * N * 2 + Z * 2 + N * 2
-    achieved = alg_bytes / (kmean * 1e-3) / 1e9
+    roof = _roofline_partials(torch, [(s[0], s[1], s[2], None, 0.0) for s in sets], N, Z, alg_bytes,
+                              args.steps, args.warmup, "sparse_gemv_kernel (config 1 split-K pass)")
     res = {
         "metric": "sparse GEMV HBM GB/s (W[4096,14336] fp16, 40% sparse x)",
-        "value": round(achieved, 1),
+        "value": round(alg_bytes / (omean * 1e-3) / 1e9, 1),
         "unit": "GB/s",
         "ms_per_step": round(wall, 5),
         "higher_is_better": True,
         "dtype": "f16 (fp32 accumulate)",
         "config": {"workload": "config1_sparse_gemv", "N": N, "Z": Z, "sparsity": 0.4,
-                   "buffer_sets": len(sets), "working_set_MB": round(len(sets) * N * Z * 2 / 1e6)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "sparse_gemv_kernel", "kernel_us_mean": round(kmean * 1e3, 3),
-                     "kernel_us_median": round(kmed * 1e3, 3), "alg_bytes_per_launch": int(alg_bytes)},
+                   "buffer_sets": len(sets), "working_set_MB": round(len(sets) * N * Z * 2 / 1e6),
+                   "what": "value: whole op (split-K pass + chunk reduction) per call; roofline: split-K pass"},
+        "roofline": roof,
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_gemv(torch, sets[0], N, Z)
     return res
+
+
+def _traffic(kernel_key):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 PMC summary (None if absent)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel_key, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def _roofline_partials(torch, sets, N, Z, alg_bytes, steps, warmup, name, key=None):
+    """Average duration of the split-K GEMV kernel alone, from HIP events around each launch.
+
+    sets: (x, w_gate, t_gate, w_up or None, t_up); one kernel per launch."""
+    from leankv_amd import kernels
+
+    outs = [kernels.sparse_gemv_partials(x, wg, tg, wu, tu) for x, wg, tg, wu, tu in sets]
+
+    def launch(i):
+        x, wg, tg, wu, tu = sets[i]
+        kernels.sparse_gemv_partials(x, wg, tg, wu, tu, out=outs[i])
+    _, kmean, kmed = _timed_loop(launch, len(sets), steps, warmup, torch)
+    achieved = alg_bytes / (kmean * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(key or "gemv_config1"),
+            "kernel": name, "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3),
+            "alg_bytes_per_launch": int(alg_bytes)}
+
+
+def roofline_gateup(args, torch):
+    """The dominant decode kernel: fused TEAL gate/up GEMV at the Mistral-7B shape (config 2 inputs).
+
+    Wg, Wu [14336, 4096] ~N(0,.02), x[4096] ~N(0,1), both thresholds at the 40 % quantile of |x|;
+    3 buffer sets (705 MB) rotate so the Infinity Cache cannot serve them."""
+    dev = torch.device("cuda:0")
+    N, Z = 14336, 4096
+    sets, surv = [], []
+    for s in range(3):
+        g = torch.Generator(device=dev).manual_seed(100 + s)
+        wg = (torch.randn(N, Z, generator=g, device=dev) * 0.02).half().t().contiguous().t()
+        wu = (torch.randn(N, Z, generator=g, device=dev) * 0.02).half().t().contiguous().t()
+        x = torch.randn(Z, generator=g, device=dev).half()
+        t = torch.kthvalue(x.float().abs().cpu(), int(0.4 * Z)).values.item()
+        surv.append(int((x.float().abs() > t).sum()))
+        sets.append((x, wg, t, wu, t))
+    alg = 2 * statistics.mean(surv) * N * 2 + Z * 2 + 2 * N * 2
+    r = _roofline_partials(torch, sets, N, Z, alg, 200, 20, "sparse_gemv_kernel (fused gate/up, config-5 shape)",
+                           key="gemv_gateup_config5")
+    del sets
+    torch.cuda.empty_cache()
+    return r
+
+
+def cpu_decode(torch, model, thresholds, prompt_len, budget_s=20.0):
+    """The reference's decode path on the host (oracle restatement, torch fp32), bounded sample.
+
+    One decoder layer of the same random model with its TEAL thresholds and a TurboQuant cache
+    holding prompt_len tokens (random fp16 K/V: the cost does not depend on the values), decoding
+    token by token for ~budget_s seconds; tok/s = 1 / (32 x layer time + embed/norm/lm_head time)."""
+    import copy
+
+    from oracle import turboquant as oq
+    from oracle.model import RefModel
+
+    cores, cpu = _cpu_info()
+    cores = min(cores, 16)
+    torch.set_num_threads(cores)
+    cfg = copy.deepcopy(model.config)
+    cfg.num_hidden_layers = 1
+    keep = ("model.embed_tokens.", "model.layers.0.", "model.norm.", "lm_head.")
+    state = {k: v.detach().float().cpu() for k, v in model.state_dict().items() if k.startswith(keep)}
+    ref = RefModel(state, cfg, {0: thresholds[0]}, bits=3, acc_dtype=torch.float32)
+    g = torch.Generator().manual_seed(0)
+    Hkv, D = cfg.num_key_value_heads, 128
+    ref.caches[0].update(torch.randn(1, Hkv, prompt_len, D, generator=g).half(),
+                         torch.randn(1, Hkv, prompt_len, D, generator=g).half())
+    ref.pos = prompt_len
+    tok = torch.tensor([1])
+    ref.forward(tok)  # warm-up step
+    ref.t_layers = ref.t_head = 0.0
+    n, t0 = 0, time.perf_counter()
+    while n < 3 or time.perf_counter() - t0 < budget_s:
+        ref.forward(tok)
+        n += 1
+    layer_s, head_s = ref.t_layers / n, ref.t_head / n
+    L = model.config.num_hidden_layers
+    return {"value": round(1.0 / (L * layer_s + head_s), 4), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": "%d decode steps of 1 of %d layers at context %d (TEAL thresholds, 3-bit TurboQuant cache "
+                      "re-dequantized every step as the reference does), oracle torch fp32 on %s; "
+                      "per token = %d x %.1f ms/layer + %.1f ms embed/norm/lm_head"
+                      % (n, L, prompt_len, cpu, L, layer_s * 1e3, head_s * 1e3)}
 
 
 def cpu_gemv(torch, s, N, Z):
@@ -147,6 +239,52 @@ def cpu_gemv(torch, s, N, Z):
     return {"value": round(gbs, 2), "unit": "GB/s (same algorithmic bytes)", "cores": cores,
             "kind": "port", "sample": "config 1 GEMV, %d reps in ~10 s, torch fp32 on %s" % (reps, model),
             "ms_per_call": round(dt * 1e3, 3)}
+
+
+# ------------------------------------------------------------------ config 2
+def bench_mlp(args, torch):
+    """Config 2: fused sparse gate/up SwiGLU (x ~N(0,1) at 40 %) then sparse down at 40 % of |h|.
+
+    value: algorithmic bytes of both ops / their combined time per call; roofline: the gate/up
+    split-K pass alone (the decode step's dominant kernel)."""
+    from leankv_amd import kernels
+
+    dev = torch.device("cuda:0")
+    H, F = 4096, 14336
+    sets, alg = [], []
+    for s in range(args.sets if args.sets <= 3 else 3):
+        g = torch.Generator(device=dev).manual_seed(200 + s)
+        wg = (torch.randn(F, H, generator=g, device=dev) * 0.02).half().t().contiguous().t()
+        wu = (torch.randn(F, H, generator=g, device=dev) * 0.02).half().t().contiguous().t()
+        wd = (torch.randn(H, F, generator=g, device=dev) * 0.02).half().t().contiguous().t()
+        x = torch.randn(H, generator=g, device=dev).half()
+        tx = torch.kthvalue(x.float().abs().cpu(), int(0.4 * H)).values.item()
+        h = kernels.sparse_gateup_swiglu(x, wg, wu, tx, tx)
+        th = torch.kthvalue(h.float().abs().cpu(), int(0.4 * F)).values.item()
+        sx = int((x.float().abs() > tx).sum())
+        sh = int((h.float().abs() > th).sum())
+        alg.append(2 * sx * F * 2 + sh * H * 2 + H * 2 + 2 * F * 2 + H * 2)
+        sets.append((x, wg, wu, wd, tx, th, h, torch.empty(H, dtype=torch.float16, device=dev)))
+
+    def launch(i):
+        x, wg, wu, wd, tx, th, h, y = sets[i]
+        kernels.sparse_gateup_swiglu_out(x, wg, wu, tx, tx, h)
+        kernels.sparse_gemv_out(h, wd, th, y)
+    wall, omean, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
+    a = statistics.mean(alg)
+    gu_alg = statistics.mean(2 * int((x.float().abs() > tx).sum()) * F * 2 + H * 2 + 2 * F * 2
+                             for x, _, _, _, tx, _, _, _ in sets)
+    roof = _roofline_partials(torch, [(x, wg, tx, wu, tx) for x, wg, wu, _, tx, _, _, _ in sets], F, H, gu_alg,
+                              args.steps, args.warmup, "sparse_gemv_kernel (fused gate/up split-K pass)",
+                              key="gemv_gateup_config5")
+    return {
+        "metric": "fused sparse MLP HBM GB/s (gate/up [14336,4096] + down [4096,14336], 40% sparse)",
+        "value": round(a / (omean * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wall, 5),
+        "higher_is_better": True, "dtype": "f16 (fp32 accumulate)",
+        "config": {"workload": "config2_fused_mlp", "hidden": H, "ffn": F, "sparsity": 0.4,
+                   "buffer_sets": len(sets), "alg_bytes_per_call": int(a)},
+        "roofline": roof,
+    }
 
 
 def _fill_gemv_defaults(args):
@@ -245,7 +383,11 @@ def bench_decode(args, torch):
                        "what": "same model, fp16 KV, torch F.linear + SDPA, graph-captured"},
         "speedup_vs_dense": round(tps / dense_tps, 3) if dense_tps else None,
     }
-    del eng, cache, model
+    del eng, cache
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_decode(torch, model, th, args.prompt)
+    del model
     torch.cuda.empty_cache()
     return res
 
@@ -267,17 +409,15 @@ def main():
         sys.exit(1)
     if args.workload == "decode":
         res = bench_decode(args, torch)
-        # roofline block: the dominant kernel (TEAL sparse GEMV, config 1 shape)
+        # roofline block: the dominant kernel of the decode step (fused gate/up GEMV)
         if not args.no_roofline:
-            gargs = argparse.Namespace(**vars(args))
-            gargs.steps, gargs.warmup = 200, 20
-            g = bench_gemv(gargs, torch)
-            res["roofline"] = g["roofline"]
-            if "cpu_baseline" in g:
-                res["cpu_baseline_gemv"] = g["cpu_baseline"]
+            res["roofline"] = roofline_gateup(args, torch)
     else:
         _fill_gemv_defaults(args)
-        fn = {"gemv": bench_gemv}[args.workload]
+        fn = {"gemv": bench_gemv, "mlp": bench_mlp}.get(args.workload)
+        if fn is None:
+            print("bench.py: workload %s is not implemented yet" % args.workload, file=sys.stderr)
+            sys.exit(2)
         res = fn(args, torch)
     out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"), "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup}

@@ -78,6 +78,19 @@ int lkv_sparse_gateup_swiglu(const void* x, const void* wg_colmajor,
                              int64_t N, int64_t Z, void* h,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * The split-K pass of lkv_sparse_gemv / lkv_sparse_gateup_swiglu alone: the
+ * fp32 partial sums, without the reduction over row chunks, for callers that
+ * fuse that reduction into their own consumer (the decode step does this
+ * internally).  Layout: [mat][slab][chunk][256] with slab = n / 256 and
+ * lkv_sparse_gemv_chunks(N, Z) chunks; mat 1 (up) only when w_up != NULL.
+ * Summing a column's chunks in chunk order from 0 and rounding to fp16 gives
+ * lkv_sparse_gemv's output bit for bit.
+ */
+int lkv_sparse_gemv_chunks(int64_t N, int64_t Z);
+int lkv_sparse_gemv_partials(const void* x, const void* w_gate, const void* w_up, float t_gate, float t_up,
+                             int64_t N, int64_t Z, float* partials, size_t partials_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* TurboQuant (MSE variant), head_dim 128                                    */
 /* ------------------------------------------------------------------------ */

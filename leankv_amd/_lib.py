@@ -36,6 +36,8 @@ SIGNATURES = {
     "lkv_sparse_gemv": (_int, [_c_p, _c_p, _f32, _i64, _i64, _c_p, _c_p, _sz, _c_p]),
     "lkv_sparse_gateup_workspace_bytes": (_sz, [_i64, _i64]),
     "lkv_sparse_gateup_swiglu": (_int, [_c_p, _c_p, _c_p, _f32, _f32, _i64, _i64, _c_p, _c_p, _sz, _c_p]),
+    "lkv_sparse_gemv_chunks": (_int, [_i64, _i64]),
+    "lkv_sparse_gemv_partials": (_int, [_c_p, _c_p, _c_p, _f32, _f32, _i64, _i64, _c_p, _sz, _c_p]),
     "lkv_tq_packed_row_bytes": (_int, [_int]),
     "lkv_tq_quantize": (_int, [_c_p, _int, _i64, _c_p, _c_p, _int, _c_p, _c_p, _c_p]),
     "lkv_tq_quantize_rotated": (_int, [_c_p, _i64, _c_p, _int, _c_p, _c_p]),

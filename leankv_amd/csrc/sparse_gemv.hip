@@ -412,6 +412,40 @@ extern "C" size_t lkv_sparse_gateup_workspace_bytes(int64_t N, int64_t Z) {
   return ws_bytes_for(N, Z, true);
 }
 
+extern "C" int lkv_sparse_gemv_chunks(int64_t N, int64_t Z) {
+  if (N <= 0 || Z <= 0) return 1;
+  return static_cast<int>(gemv_chunks(Z, gemv_pick_bz(gemv_slabs(N), Z)));
+}
+
+extern "C" int lkv_sparse_gemv_partials(const void* x, const void* w_gate, const void* w_up, float t_gate, float t_up,
+                                        int64_t N, int64_t Z, float* partials, size_t partials_bytes, void* stream) {
+  if (int e = check_common(x, w_gate, N, Z, partials)) return e;
+  LKV_REQUIRE(w_up == nullptr || aligned16(w_up), "sparse_gemv_partials: up weight must be 16-byte aligned");
+  if (N == 0 || Z == 0) return LKV_OK;
+  const bool dual = w_up != nullptr;
+  const int64_t nslab = gemv_slabs(N);
+  const int bz = gemv_pick_bz(nslab, Z);
+  const int64_t nchunk = gemv_chunks(Z, bz);
+  const size_t need = (dual ? 2 : 1) * gemv_part_floats(N, nchunk) * sizeof(float);
+  LKV_REQUIRE(partials_bytes >= need, "sparse_gemv_partials: %zu bytes of partials required, got %zu", need,
+              partials_bytes);
+  GemvArgs G{};
+  G.x = static_cast<const uint16_t*>(x);
+  G.nseg = 1;
+  G.A[0] = static_cast<const uint16_t*>(w_gate);
+  G.A_up = static_cast<const uint16_t*>(w_up);
+  G.a_bytes[0] = static_cast<uint32_t>(N * Z * 2);
+  G.N[0] = static_cast<int>(N);
+  G.t[0] = t_gate;
+  G.t_up = t_up;
+  G.slab0[1] = static_cast<int>(nslab);
+  G.Z = static_cast<int>(Z);
+  G.nchunk = static_cast<int>(nchunk);
+  G.part = partials;
+  G.part_up_off = gemv_part_floats(N, nchunk);
+  return gemv_launch(G, bz, dual, kInRaw, static_cast<int>(nslab), static_cast<hipStream_t>(stream));
+}
+
 extern "C" int lkv_sparse_gemv(const void* x, const void* w, float threshold, int64_t N, int64_t Z, void* y,
                                void* workspace, size_t workspace_bytes, void* stream) {
   if (int e = check_common(x, w, N, Z, y)) return e;

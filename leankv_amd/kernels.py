@@ -74,6 +74,30 @@ def sparse_gemv(x: torch.Tensor, weight: torch.Tensor, threshold: float) -> torc
     return sparse_gemv_out(x, weight, threshold, out)
 
 
+def sparse_gemv_partials(x: torch.Tensor, w_gate: torch.Tensor, t_gate: float, w_up: torch.Tensor | None = None,
+                         t_up: float = 0.0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Split-K partial sums only: fp32 [mats, N/256 slabs, chunks, 256] (mats = 2 with w_up).
+
+    Summing dim 2 in chunk order and rounding to fp16 reproduces sparse_gemv
+    (or, through SwiGLU, sparse_gateup_swiglu) bit for bit."""
+    N, Z = colmajor_rows(w_gate)
+    if w_up is not None and (colmajor_rows(w_up) != (N, Z) or w_up.dtype != torch.float16):
+        raise LeanKVError("sparse_gemv_partials: up weight must match the gate weight")
+    require_cuda(x, w_gate, w_up)
+    xf = _check_x(x, Z, "sparse_gemv_partials")
+    if w_gate.dtype != torch.float16:
+        raise LeanKVError("sparse_gemv_partials: weights must be float16")
+    lib = _lib_handle()
+    shape = (2 if w_up is not None else 1, (N + 255) // 256, lib.lkv_sparse_gemv_chunks(N, Z), 256)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float32, device=x.device)
+    if tuple(out.shape) != shape or out.dtype != torch.float32 or not out.is_contiguous():
+        raise LeanKVError("sparse_gemv_partials: out must be a contiguous float32 tensor of shape %s" % (shape,))
+    check(lib.lkv_sparse_gemv_partials(ptr(xf), ptr(w_gate), ptr(w_up), float(t_gate), float(t_up), N, Z, ptr(out),
+                                       out.numel() * 4, stream_handle(x.device)), "lkv_sparse_gemv_partials")
+    return out
+
+
 def sparse_gateup_swiglu_out(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, t_gate: float,
                              t_up: float, out: torch.Tensor) -> torch.Tensor:
     """out[N] = fp16(silu(fp16(Wg x_g)) * fp16(Wu x_u)), x_g/x_u thresholded copies of x."""

@@ -15,6 +15,7 @@ Every projection output is rounded to fp16 (the kernel writes fp16).
 from __future__ import annotations
 
 import math
+import time
 
 import torch
 
@@ -43,6 +44,8 @@ class RefModel:
         self.eps = cfg.rms_norm_eps
         self.theta = getattr(cfg, "rope_theta", None) or cfg.rope_parameters["rope_theta"]
         c, b = oq.codebook_tensors(bits)
+        self.t_layers = 0.0  # seconds spent in the decoder layers / in embedding + final norm + lm_head
+        self.t_head = 0.0
         self.caches = [oq.CacheRef(oq.rotation_matrix(self.D, seed + 2 * i), oq.rotation_matrix(self.D, seed + 2 * i + 1),
                                    c, b, bits, hot) for i in range(self.L)]
         self.pos = 0
@@ -77,10 +80,12 @@ class RefModel:
     # ---------------------------------------------------------------- forward
     def forward(self, ids: torch.Tensor) -> torch.Tensor:
         """Run S new tokens (prefill if S > 1); returns fp32 logits of the last token."""
+        t0 = time.perf_counter()
         S = ids.shape[0]
         pos = torch.arange(self.pos, self.pos + S)
         cos, sin = self._rope(pos)
         x = f16(self._w("model.embed_tokens.weight")[ids])
+        t1 = time.perf_counter()
         for i in range(self.L):
             p = "model.layers.%d." % i
             h = self._rms(x, self._w(p + "input_layernorm.weight"))
@@ -105,6 +110,11 @@ class RefModel:
             u = self._lin(h, i, "up_proj", "mlp")
             m = f16(f16(g / (1 + torch.exp(-g))) * u)
             x = f16(x + self._lin(m, i, "down_proj", "mlp"))
+        t2 = time.perf_counter()
         x = self._rms(x, self._w("model.norm.weight"))
         self.pos += S
-        return x[-1:].to(self.acc).matmul(self._w("lm_head.weight").to(self.acc).T).float()[0]
+        out = x[-1:].to(self.acc).matmul(self._w("lm_head.weight").to(self.acc).T).float()[0]
+        t3 = time.perf_counter()
+        self.t_layers += t2 - t1
+        self.t_head += (t1 - t0) + (t3 - t2)
+        return out

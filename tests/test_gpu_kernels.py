@@ -116,6 +116,36 @@ def test_gateup_distinct_thresholds(cuda):
     assert ot.max_rel_err(h.numpy(), href) < RTOL
 
 
+def test_sparse_gemv_partials_reduce_to_the_full_op(cuda):
+    """Split-K partials, summed over chunks in chunk order and rounded, equal the full op bit for bit."""
+    from leankv_amd import kernels
+
+    g = torch.Generator().manual_seed(11)
+    N, Z = 1024, 4096
+    Wg = (torch.randn(N, Z, generator=g) * 0.02).half().to(cuda).t().contiguous().t()
+    Wu = (torch.randn(N, Z, generator=g) * 0.02).half().to(cuda).t().contiguous().t()
+    x = torch.randn(Z, generator=g).half().to(cuda)
+    p1 = kernels.sparse_gemv_partials(x, Wg, 0.5)
+    assert p1.shape[:2] == (1, N // 256) and p1.shape[2] > 1
+
+    def reduce(p):  # p: [slabs, chunks, 256]
+        acc = torch.zeros(p.shape[0], p.shape[2], dtype=torch.float32, device=cuda)
+        for c in range(p.shape[1]):  # chunk order, from 0, like the kernels
+            acc = acc + p[:, c]
+        return acc.reshape(-1)
+
+    assert torch.equal(reduce(p1[0]).half(), kernels.sparse_gemv(x, Wg, 0.5))
+    p2 = kernels.sparse_gemv_partials(x, Wg, 0.4, Wu, 0.7)
+    assert torch.equal(p2[0], kernels.sparse_gemv_partials(x, Wg, 0.4)[0])
+    h = kernels.sparse_gateup_swiglu(x, Wg, Wu, 0.4, 0.7)
+    gsum, usum = reduce(p2[0]).cpu().numpy(), reduce(p2[1]).cpu().numpy()
+    ref = ot.silu_f16(gsum.astype(np.float16)).astype(np.float32) * usum.astype(np.float16).astype(np.float32)
+    ref = ref.astype(np.float16)
+    # same sums; SwiGLU's exp may differ by an ulp between numpy and the device, nothing more
+    assert ot.max_rel_err(h.cpu().numpy(), ref) < 2e-3
+    assert int((h.cpu().numpy() != ref).sum()) <= N // 100
+
+
 @pytest.mark.parametrize("M,Z", [(1, 4096), (3, 512), (2, 14336)])
 def test_rms_norm_matches_hf_rounding(cuda, M, Z):
     """lkv_rmsnorm vs HF MistralRMSNorm in fp64 (modeling_mistral.py:190-197): every element within one
