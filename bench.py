@@ -14,6 +14,7 @@ Workloads:
   mlp     config 2: fused gate/up SwiGLU [14336,4096] + sparse down [4096,14336]
   quant   config 3: TurboQuant 3-bit quantize of K,V [8,4096,128] (fp32 MFMA rotation)
   attn    config 4: packed-KV decode attention, B=16, 32/8 heads, ctx 4096 + 64 hot
+  copy    a 512 MiB device copy: the known-size reference for scaling PMC byte counters
 Every workload rotates >= 3 independent buffer sets (> 512 MB) so the 256 MB
 Infinity Cache cannot serve repeated launches.  A "step" is one launch of the
 workload's kernel(s) over one buffer set.  Timing: W untimed steps, then K timed
@@ -40,7 +41,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "mlp", "quant", "attn"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "mlp", "quant", "attn", "copy"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=32, help="decoder layers (config 5 uses 32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -65,6 +66,24 @@ def _timed_loop(launch, nsets, steps, warmup, torch):
     wall = (time.perf_counter() - t0) * 1e3 / steps
     durs = [a.elapsed_time(b) for a, b in evs]
     return wall, statistics.mean(durs), statistics.median(durs)
+
+
+def _kernel_time(launch, nsets, steps, warmup, torch, batch=10):
+    """Average duration of one launch: HIP events around batches of `batch` back-to-back launches on the
+    launching stream (a lone launch between two events also times its dispatch latency)."""
+    for i in range(warmup):
+        launch(i % nsets)
+    torch.cuda.synchronize()
+    nb = max(1, steps // batch)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nb)]
+    for j, (a, b) in enumerate(evs):
+        a.record()
+        for i in range(batch):
+            launch((j * batch + i) % nsets)
+        b.record()
+    torch.cuda.synchronize()
+    per = [a.elapsed_time(b) / batch for a, b in evs]
+    return statistics.mean(per), statistics.median(per)
 
 
 def _cpu_info():
@@ -147,12 +166,13 @@ def _roofline_partials(torch, sets, N, Z, alg_bytes, steps, warmup, name, key=No
     def launch(i):
         x, wg, tg, wu, tu = sets[i]
         kernels.sparse_gemv_partials(x, wg, tg, wu, tu, out=outs[i])
-    _, kmean, kmed = _timed_loop(launch, len(sets), steps, warmup, torch)
+    kmean, kmed = _kernel_time(launch, len(sets), steps, warmup, torch)
+    _, single, _ = _timed_loop(launch, len(sets), steps // 2, 0, torch)
     achieved = alg_bytes / (kmean * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(key or "gemv_config1"),
             "kernel": name, "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3),
-            "alg_bytes_per_launch": int(alg_bytes)}
+            "kernel_us_single_launch_events": round(single * 1e3, 3), "alg_bytes_per_launch": int(alg_bytes)}
 
 
 def roofline_gateup(args, torch):
@@ -287,6 +307,19 @@ def bench_mlp(args, torch):
     }
 
 
+def bench_copy(args, torch):
+    """A plain device copy of known size (512 MiB read + 512 MiB written per step): the reference point
+    for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    dev = torch.device("cuda:0")
+    n = 512 << 20
+    a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    wall, kmean, _ = _timed_loop(lambda i: b.copy_(a), 1, args.steps, args.warmup, torch)
+    return {"metric": "device copy GB/s (read + write)", "value": round(2 * n / (kmean * 1e-3) / 1e9, 1),
+            "unit": "GB/s", "ms_per_step": round(wall, 5), "higher_is_better": True, "dtype": "u8",
+            "config": {"workload": "copy_512MiB", "bytes_read": n, "bytes_written": n}}
+
+
 def _fill_gemv_defaults(args):
     if args.steps is None:
         args.steps = 200
@@ -414,7 +447,7 @@ def main():
             res["roofline"] = roofline_gateup(args, torch)
     else:
         _fill_gemv_defaults(args)
-        fn = {"gemv": bench_gemv, "mlp": bench_mlp}.get(args.workload)
+        fn = {"gemv": bench_gemv, "mlp": bench_mlp, "copy": bench_copy}.get(args.workload)
         if fn is None:
             print("bench.py: workload %s is not implemented yet" % args.workload, file=sys.stderr)
             sys.exit(2)
