@@ -44,6 +44,7 @@ struct GemvArgs {
   size_t part_off[kMaxSeg];
   size_t part_up_off;      // dual mode: the up matrix's partials
   uint16_t* y;             // non-null only when nchunk == 1 and nseg == 1: write fp16 (SwiGLU if dual)
+  int chunk_major;         // set by gemv_launch (block order)
 };
 
 int gemv_pick_bz(int64_t slabs, int64_t Z);
@@ -72,27 +73,30 @@ __device__ __forceinline__ float column_sum(const float* __restrict__ P, int n, 
 }
 
 // 1 / sqrt(mean(x^2) + eps) over fp16 x[0..Z) in fp32, computed by a whole
-// block of kGemvThreads threads (every thread gets the result).  Fixed
-// summation order: thread t accumulates x[8t .. 8t+7], x[8t + 2048 ..], ...
-// with fmaf, then a wave butterfly, then the 4 wave sums in order.  Requires
-// Z % 8 == 0 and 16-byte aligned x.  Every RMSNorm of this library goes
-// through it, so all of them round identically.
+// block (every thread gets the result).  Fixed summation order, the same for
+// any block size: thread t < 256 accumulates x[8t .. 8t+7], x[8t + 2048 ..],
+// ... with fmaf, then a wave butterfly, then the 4 wave sums in order
+// (threads >= 256 of a larger block take no part).  Requires Z % 8 == 0 and
+// 16-byte aligned x.  Every RMSNorm of this library goes through it, so all
+// of them round identically.
 __device__ __forceinline__ float rms_rstd(const uint16_t* __restrict__ x, int Z, float eps, float* s_wsum) {
   const int tid = threadIdx.x;
   float ss = 0.f;
-  for (int z = tid * 8; z < Z; z += kGemvThreads * 8) {
-    const uint4 u = *reinterpret_cast<const uint4*>(x + z);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  if (tid < kGemvThreads) {
+    for (int z = tid * 8; z < Z; z += kGemvThreads * 8) {
+      const uint4 u = *reinterpret_cast<const uint4*>(x + z);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float a = h2f(static_cast<uint16_t>(w[i] & 0xffffu));
-      const float b = h2f(static_cast<uint16_t>(w[i] >> 16));
-      ss = fmaf(a, a, ss);
-      ss = fmaf(b, b, ss);
+      for (int i = 0; i < 4; ++i) {
+        const float a = h2f(static_cast<uint16_t>(w[i] & 0xffffu));
+        const float b = h2f(static_cast<uint16_t>(w[i] >> 16));
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+      }
     }
   }
   ss = wave_sum(ss);
-  if ((tid & (kWave - 1)) == 0) s_wsum[tid / kWave] = ss;
+  if ((tid & (kWave - 1)) == 0 && tid < kGemvThreads) s_wsum[tid / kWave] = ss;
   __syncthreads();
   float tot = 0.f;
 #pragma unroll

@@ -20,9 +20,10 @@
 //      whole number of streaming batches with copies of its last row and a
 //      zero activation: padded loads hit the line just fetched and add 0.
 //   2. Streaming: 32 lanes cover one 512-byte row segment with 16-byte buffer
-//      loads (SGPR descriptor + 32-bit offset; loads past the end read 0); the
-//      8 row slots of the block walk the list 8 rows at a time, so 8
-//      independent 16-byte loads per lane are in flight.  fp16 x fp32 -> fp32.
+//      loads (SGPR descriptor + 32-bit offset; loads past the end read 0,
+//      non-temporal cache policy); the 8 row slots of the block walk the list
+//      8 rows at a time, so 8 independent 16-byte loads per lane are in
+//      flight.  fp16 x fp32 -> fp32.
 //   3. The row slots are reduced through LDS into 256 fp32 column sums.
 //   4. The block writes its partial sums.  The reduction over chunks happens
 //      after the kernel boundary, in chunk order (so results are
@@ -53,8 +54,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
 
-// Stream the padded survivor list: total is a multiple of U * SLOTS.
-template <int SLOTS, int U>
+// Stream the padded survivor list: total is a multiple of U * SLOTS.  CP is
+// the buffer-load cache policy (2 = nt: streamed once, no L2 retention).
+template <int SLOTS, int U, int CP>
 __device__ __forceinline__ void stream_rows(__amdgpu_buffer_rsrc_t A, uint32_t row_bytes, uint32_t col_bytes,
                                             const int* __restrict__ idx, const float* __restrict__ xv, int total,
                                             int slot, float (&acc)[8]) {
@@ -69,23 +71,23 @@ __device__ __forceinline__ void stream_rows(__amdgpu_buffer_rsrc_t A, uint32_t r
     u32x4v w[U];
 #pragma unroll
     for (int u = 0; u < U; ++u)
-      w[u] = __builtin_amdgcn_raw_buffer_load_b128(A, static_cast<uint32_t>(r[u]) * row_bytes + col_bytes, 0, 0);
+      w[u] = __builtin_amdgcn_raw_buffer_load_b128(A, static_cast<uint32_t>(r[u]) * row_bytes + col_bytes, 0, CP);
 #pragma unroll
     for (int u = 0; u < U; ++u) fma8(acc, w[u], xs[u]);
   }
 }
 
 // x[z0 .. z0 + BZ) into s_x (0 past Z) for the three input modes.
-template <int BZ, int MODE>
+template <int NT, int BZ, int MODE>
 __device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float* s_x, float* s_wsum) {
-  constexpr int E = BZ / kGemvThreads;  // inputs per thread
+  constexpr int E = BZ / NT;  // inputs per thread
   const int tid = threadIdx.x;
   const int Z = G.Z;
   if (MODE == kInRmsNorm) {
     const float rstd = rms_rstd(G.x, Z, G.eps, s_wsum);
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const int i = e * kGemvThreads + tid;
+      const int i = e * NT + tid;
       const int z = z0 + i;
       s_x[i] = z < Z ? rms_apply(G.x[z], G.norm_w[z], rstd) : 0.f;
     }
@@ -98,7 +100,7 @@ __device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float*
     const float* pg[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const int z = min(z0 + e * kGemvThreads + tid, Z - 1);
+      const int z = min(z0 + e * NT + tid, Z - 1);
       pg[e] = G.in_part + static_cast<size_t>(z / kGemvBN) * nc * kGemvBN + (z % kGemvBN);
       g[e] = 0.f;
       u[e] = 0.f;
@@ -123,40 +125,44 @@ __device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float*
     }
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const int i = e * kGemvThreads + tid;
+      const int i = e * NT + tid;
       s_x[i] = z0 + i < Z ? h2f(swiglu_f16(g[e], u[e])) : 0.f;
     }
   } else {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const int i = e * kGemvThreads + tid;
+      const int i = e * NT + tid;
       s_x[i] = z0 + i < Z ? h2f(G.x[z0 + i]) : 0.f;
     }
   }
   __syncthreads();
 }
 
-template <int BZ, bool DUAL, int MODE, int U>
-__global__ __launch_bounds__(kGemvThreads) void sparse_gemv_kernel(GemvArgs G) {
+template <int NT, int BZ, bool DUAL, int MODE, int U, int CP>
+__global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
   constexpr int BN = kGemvBN;
-  constexpr int LPR = BN / 8;                // lanes per row segment
-  constexpr int SLOTS = kGemvThreads / LPR;  // rows processed side by side
+  constexpr int LPR = BN / 8;       // lanes per row segment
+  constexpr int SLOTS = NT / LPR;   // rows processed side by side
   constexpr int NL = DUAL ? 2 : 1;
-  constexpr int PAD = U * SLOTS;             // list granularity
-  static_assert(BZ % kGemvThreads == 0, "BZ must be a multiple of 256");
+  constexpr int PAD = U * SLOTS;    // list granularity
+  static_assert(BZ % NT == 0, "BZ must be a multiple of the block size");
 
   __shared__ int s_idx[NL][BZ + PAD];
   __shared__ float s_xv[NL][BZ + PAD];
   __shared__ float s_x[BZ];
-  __shared__ int s_cnt[NL][kGemvThreads / kWave];
-  __shared__ float s_wsum[kGemvThreads / kWave];
+  __shared__ int s_cnt[NL][NT / kWave];
+  __shared__ float s_wsum[NT / kWave];
   __shared__ __align__(16) float s_red[SLOTS * BN];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const int gslab = blockIdx.x;
-  const int chunk = blockIdx.y;
+  int gslab = blockIdx.x, chunk = blockIdx.y;
+  if (G.chunk_major) {  // consecutive blocks walk the chunks of one slab
+    const int lin = blockIdx.y * gridDim.x + blockIdx.x;
+    gslab = lin / G.nchunk;
+    chunk = lin % G.nchunk;
+  }
   const int z0 = chunk * BZ;
   const int Z = G.Z;
 
@@ -169,14 +175,14 @@ __global__ __launch_bounds__(kGemvThreads) void sparse_gemv_kernel(GemvArgs G) {
   const float t0 = G.t[seg];
   const int n0 = slab * BN;
 
-  input_prologue<BZ, MODE>(G, z0, s_x, s_wsum);
+  input_prologue<NT, BZ, MODE>(G, z0, s_x, s_wsum);
 
   // ---- 1. compaction of surviving activation rows
   int total[NL];
 #pragma unroll
   for (int l = 0; l < NL; ++l) total[l] = 0;
 #pragma unroll
-  for (int base = 0; base < BZ; base += kGemvThreads) {
+  for (int base = 0; base < BZ; base += NT) {
     const int z = z0 + base + tid;
     const bool valid = z < Z;
     const float v = s_x[base + tid];
@@ -195,7 +201,7 @@ __global__ __launch_bounds__(kGemvThreads) void sparse_gemv_kernel(GemvArgs G) {
     for (int l = 0; l < NL; ++l) {
       int off = total[l], tot = 0;
 #pragma unroll
-      for (int w = 0; w < kGemvThreads / kWave; ++w) {
+      for (int w = 0; w < NT / kWave; ++w) {
         const int cw = s_cnt[l][w];
         off += (w < wave) ? cw : 0;
         tot += cw;
@@ -234,9 +240,9 @@ __global__ __launch_bounds__(kGemvThreads) void sparse_gemv_kernel(GemvArgs G) {
   for (int l = 0; l < NL; ++l)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[l][j] = 0.f;
-  stream_rows<SLOTS, U>(make_rsrc(G.A[seg], a_bytes), row_bytes, col_bytes, s_idx[0], s_xv[0], total[0], slot, acc[0]);
+  stream_rows<SLOTS, U, CP>(make_rsrc(G.A[seg], a_bytes), row_bytes, col_bytes, s_idx[0], s_xv[0], total[0], slot, acc[0]);
   if (DUAL)
-    stream_rows<SLOTS, U>(make_rsrc(G.A_up, a_bytes), row_bytes, col_bytes, s_idx[NL - 1], s_xv[NL - 1], total[NL - 1],
+    stream_rows<SLOTS, U, CP>(make_rsrc(G.A_up, a_bytes), row_bytes, col_bytes, s_idx[NL - 1], s_xv[NL - 1], total[NL - 1],
                        slot, acc[NL - 1]);
 
   // ---- 3. cross-slot reduction through LDS
@@ -248,13 +254,16 @@ __global__ __launch_bounds__(kGemvThreads) void sparse_gemv_kernel(GemvArgs G) {
     dst[1] = make_float4(acc[l][4], acc[l][5], acc[l][6], acc[l][7]);
     __syncthreads();
     float s = 0.f;
+    if (tid < BN) {
 #pragma unroll
-    for (int sl = 0; sl < SLOTS; ++sl) s += s_red[sl * BN + tid];
+      for (int sl = 0; sl < SLOTS; ++sl) s += s_red[sl * BN + tid];
+    }
     sums[l] = s;
     __syncthreads();
   }
 
-  // ---- 4. output: fp16 directly (single chunk) or partial sums
+  // ---- 4. output (threads 0..255, one column each): fp16 directly (single chunk) or partial sums
+  if (tid >= BN) return;
   if (G.y != nullptr) {
     if (n0 + tid < N) G.y[n0 + tid] = DUAL ? swiglu_f16(sums[0], sums[NL - 1]) : f2h(sums[0]);
     return;
@@ -299,17 +308,52 @@ int gemv_pick_bz(int64_t slabs, int64_t Z) {
 
 namespace {
 
-template <int BZ, int U>
+template <int NT, int BZ, int U, int CP>
 bool launch_bz(const GemvArgs& G, bool dual, int mode, dim3 grid, hipStream_t st) {
-  const dim3 blk(kGemvThreads);
+  const dim3 blk(NT);
   switch (mode * 2 + (dual ? 1 : 0)) {
-    case kInRaw * 2: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, false, kInRaw, U>), grid, blk, 0, st, G); return true;
-    case kInRaw * 2 + 1: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, true, kInRaw, U>), grid, blk, 0, st, G); return true;
-    case kInRmsNorm * 2: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, false, kInRmsNorm, U>), grid, blk, 0, st, G); return true;
-    case kInRmsNorm * 2 + 1: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, true, kInRmsNorm, U>), grid, blk, 0, st, G); return true;
-    case kInSwiglu * 2: hipLaunchKernelGGL((sparse_gemv_kernel<BZ, false, kInSwiglu, U>), grid, blk, 0, st, G); return true;
+    case kInRaw * 2: hipLaunchKernelGGL((sparse_gemv_kernel<NT, BZ, false, kInRaw, U, CP>), grid, blk, 0, st, G); return true;
+    case kInRaw * 2 + 1: hipLaunchKernelGGL((sparse_gemv_kernel<NT, BZ, true, kInRaw, U, CP>), grid, blk, 0, st, G); return true;
+    case kInRmsNorm * 2: hipLaunchKernelGGL((sparse_gemv_kernel<NT, BZ, false, kInRmsNorm, U, CP>), grid, blk, 0, st, G); return true;
+    case kInRmsNorm * 2 + 1: hipLaunchKernelGGL((sparse_gemv_kernel<NT, BZ, true, kInRmsNorm, U, CP>), grid, blk, 0, st, G); return true;
+    case kInSwiglu * 2: hipLaunchKernelGGL((sparse_gemv_kernel<NT, BZ, false, kInSwiglu, U, CP>), grid, blk, 0, st, G); return true;
     default: return false;
   }
+}
+
+template <int NT, int BZ, int U>
+bool launch_cp(const GemvArgs& G, bool dual, int mode, dim3 grid, hipStream_t st, int cp) {
+  return cp == 2 ? launch_bz<NT, BZ, U, 2>(G, dual, mode, grid, st) : launch_bz<NT, BZ, U, 0>(G, dual, mode, grid, st);
+}
+
+// Tuning knobs, read once.  Weights are streamed with the nt (non-temporal)
+// cache policy: each byte is read once per call, and keeping it out of the
+// L2 leaves room for x and the partial sums (measured on MI355X: fused gate/up
+// 27.7 -> 24.3 us, config-1 GEMV 15.7 -> 14.2 us); LKV_GEMV_CPOL=0 restores
+// the default policy.  LKV_GEMV_ORDER=chunk makes consecutive blocks walk one
+// slab's chunks instead of one chunk's slabs (slower: 17.5 vs 15.7 us).
+int gemv_cpol() {
+  static const int c = [] {
+    const char* env = getenv("LKV_GEMV_CPOL");
+    return env && atoi(env) == 0 ? 0 : 2;
+  }();
+  return c;
+}
+bool gemv_chunk_major() {
+  static const bool c = [] {
+    const char* env = getenv("LKV_GEMV_ORDER");
+    return env && env[0] == 'c';
+  }();
+  return c;
+}
+
+// Threads per GEMV block (256 default; LKV_GEMV_THREADS=512 for tuning sweeps, chunks >= 512 only).
+int gemv_threads() {
+  static const int t = [] {
+    const char* env = getenv("LKV_GEMV_THREADS");
+    return env && atoi(env) == 512 ? 512 : 256;
+  }();
+  return t;
 }
 
 // Rows each lane keeps in flight (8 default; LKV_GEMV_UNROLL=16 for tuning sweeps).
@@ -327,10 +371,19 @@ int gemv_launch(const GemvArgs& G, int bz, bool dual, int mode, int nslab_total,
   if (nslab_total <= 0) return LKV_OK;
   const dim3 grid(static_cast<unsigned>(nslab_total), static_cast<unsigned>(G.nchunk));
   bool ok = false;
-  const bool u16 = gemv_unroll() == 16;
-  if (bz == 256) ok = u16 ? launch_bz<256, 16>(G, dual, mode, grid, st) : launch_bz<256, 8>(G, dual, mode, grid, st);
-  else if (bz == 512) ok = u16 ? launch_bz<512, 16>(G, dual, mode, grid, st) : launch_bz<512, 8>(G, dual, mode, grid, st);
-  else if (bz == 1024) ok = u16 ? launch_bz<1024, 16>(G, dual, mode, grid, st) : launch_bz<1024, 8>(G, dual, mode, grid, st);
+  const bool t512 = gemv_threads() == 512 && bz >= 512;
+  const int cp = gemv_cpol();
+  GemvArgs Gx = G;
+  Gx.chunk_major = gemv_chunk_major() ? 1 : 0;
+  if (gemv_unroll() == 16) {
+    if (bz == 256) ok = launch_cp<256, 256, 16>(Gx, dual, mode, grid, st, cp);
+    else if (bz == 512) ok = t512 ? launch_cp<512, 512, 16>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 512, 16>(Gx, dual, mode, grid, st, cp);
+    else if (bz == 1024) ok = t512 ? launch_cp<512, 1024, 16>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 1024, 16>(Gx, dual, mode, grid, st, cp);
+  } else {
+    if (bz == 256) ok = launch_cp<256, 256, 8>(Gx, dual, mode, grid, st, cp);
+    else if (bz == 512) ok = t512 ? launch_cp<512, 512, 8>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 512, 8>(Gx, dual, mode, grid, st, cp);
+    else if (bz == 1024) ok = t512 ? launch_cp<512, 1024, 8>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 1024, 8>(Gx, dual, mode, grid, st, cp);
+  }
   if (!ok) {
     set_error("sparse_gemv: no kernel for chunk %d, mode %d, dual %d", bz, mode, dual ? 1 : 0);
     return LKV_ERR_INVALID;
