@@ -145,7 +145,10 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(uint16_t* __restrict
                                                             int N, int nchunk) {
   const int n = blockIdx.x * kThreads + threadIdx.x;
   if (n >= N) return;
-  x[n] = f2h(h2f(x[n]) + h2f(f2h(column_sum(part, n, nchunk))));
+  // x is loaded with the partials and converted after them: one memory round trip
+  const uint16_t xv = x[n];
+  const float o = h2f(f2h(column_sum(part, n, nchunk)));
+  x[n] = f2h(h2f(xv) + o);
 }
 
 // y = RMSNorm(x) * w for M rows of Z; block (j, m) writes columns
@@ -206,8 +209,12 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
   const int nc = A.nchunk;
   const float* Pi = vside ? A.PiV : A.PiK;
 
-  // ---- 0. the rotation matrix, 16 coalesced float4 per thread, in flight
-  //      while the projections are summed
+  // ---- 0. loads, in this order, all in flight before the first wait: the
+  //      position, the rotation matrix (16 coalesced float4 per thread), the
+  //      decision boundaries, the first 16 chunks of the projection partial
+  //      sums, then what depends on the position -- the row leaving the hot
+  //      window (row 0 of the MFMA tile: lanes r == 0 use it, the others load
+  //      the same 64 bytes) and this position's RoPE row.
   const int pos = A.state[0];
   float4 pr[kD * kD / 4 / kThreads];
 #pragma unroll
@@ -215,9 +222,40 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
   float bd[(1 << BITS) - 1];
 #pragma unroll
   for (int i = 0; i < (1 << BITS) - 1; ++i) bd[i] = A.bounds[i];
-  // Everything that depends only on pos, also in flight during the sums:
-  // the row leaving the hot window (row 0 of the MFMA tile: lanes r == 0 use
-  // it, the others load the same 64 bytes) and this position's RoPE row.
+
+  // Projections, summed over chunks in chunk order, rounded to fp16.  A
+  // wave's 64 columns never straddle a 128-column head, so validity and the
+  // source matrix are uniform per wave (scalar branches).
+  const float* src[kCols];
+  bool ok[kCols];
+  float psum[kCols];
+#pragma unroll
+  for (int e = 0; e < kCols; ++e) {
+    const int cw = __builtin_amdgcn_readfirstlane(e * kThreads + (tid & ~(kWave - 1)));
+    ok[e] = cw < ncol;
+    const int c = cw + lane;
+    const int which = c / kD, d = c % kD;
+    int col;
+    const float* base;
+    if (vside) {
+      col = kvh * kD + d;
+      base = A.pv;
+    } else {
+      col = which < G ? (kvh * G + which) * kD + d : kvh * kD + d;
+      base = which < G ? A.pq : A.pk;
+    }
+    src[e] = base + static_cast<size_t>(col / kGemvBN) * nc * kGemvBN + (col % kGemvBN);
+    psum[e] = 0.f;
+  }
+  constexpr int kFirst = 16;
+  float v0[kCols][kFirst];
+#pragma unroll
+  for (int e = 0; e < kCols; ++e)
+    if (ok[e]) {
+#pragma unroll
+      for (int i = 0; i < kFirst; ++i) v0[e][i] = src[e][static_cast<size_t>(min(i, nc - 1)) * kGemvBN];
+    }
+
   const int slot = pos % A.hot_cap;
   const int ev = pos - A.hot_cap;
   const bool evict = pos >= A.hot_cap && ev < A.cap;
@@ -230,52 +268,32 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
   const uint16_t cs_d = A.cos[static_cast<size_t>(pos) * kD + (tid & (kD - 1))];
   const uint16_t sn_d = A.sin[static_cast<size_t>(pos) * kD + (tid & (kD - 1))];
 
-  // ---- 1. projections, summed over chunks in chunk order, rounded to fp16.
-  //      A wave's 64 columns never straddle a 128-column head, so validity
-  //      and the source matrix are uniform per wave (scalar branches, loads
-  //      issued back to back).
-  {
-    const float* src[kCols];
-    bool ok[kCols];
-    float acc[kCols];
+  // ---- 1. finish the projection sums
 #pragma unroll
-    for (int e = 0; e < kCols; ++e) {
-      const int c0 = __builtin_amdgcn_readfirstlane(e * kThreads + (tid & ~(kWave - 1)));
-      ok[e] = c0 < ncol;
-      const int c = c0 + lane;
-      const int which = c / kD, d = c % kD;
-      int col;
-      const float* base;
-      if (vside) {
-        col = kvh * kD + d;
-        base = A.pv;
-      } else {
-        col = which < G ? (kvh * G + which) * kD + d : kvh * kD + d;
-        base = which < G ? A.pq : A.pk;
+  for (int e = 0; e < kCols; ++e)
+    if (ok[e]) {
+#pragma unroll
+      for (int i = 0; i < kFirst; ++i) psum[e] += i < nc ? v0[e][i] : 0.f;
+    }
+  for (int k0 = kFirst; k0 < nc; k0 += 8) {
+    float v[kCols][8];
+#pragma unroll
+    for (int e = 0; e < kCols; ++e)
+      if (ok[e]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[e][i] = src[e][static_cast<size_t>(min(k0 + i, nc - 1)) * kGemvBN];
       }
-      src[e] = base + static_cast<size_t>(col / kGemvBN) * nc * kGemvBN + (col % kGemvBN);
-      acc[e] = 0.f;
-    }
-    for (int k0 = 0; k0 < nc; k0 += 8) {
-      float v[kCols][8];
 #pragma unroll
-      for (int e = 0; e < kCols; ++e)
-        if (ok[e]) {
+    for (int e = 0; e < kCols; ++e)
+      if (ok[e]) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) v[e][i] = src[e][static_cast<size_t>(min(k0 + i, nc - 1)) * kGemvBN];
-        }
+        for (int i = 0; i < 8; ++i) psum[e] += k0 + i < nc ? v[e][i] : 0.f;
+      }
+  }
 #pragma unroll
-      for (int e = 0; e < kCols; ++e)
-        if (ok[e]) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[e] += k0 + i < nc ? v[e][i] : 0.f;
-        }
-    }
-#pragma unroll
-    for (int e = 0; e < kCols; ++e) {
-      const int c = e * kThreads + tid;
-      if (ok[e]) s_raw[c / kD][c % kD] = h2f(f2h(acc[e]));
-    }
+  for (int e = 0; e < kCols; ++e) {
+    const int c = e * kThreads + tid;
+    if (ok[e]) s_raw[c / kD][c % kD] = h2f(f2h(psum[e]));
   }
 #pragma unroll
   for (int i = 0; i < kD * kD / 4 / kThreads; ++i) {

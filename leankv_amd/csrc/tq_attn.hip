@@ -60,16 +60,12 @@ __device__ __forceinline__ uint32_t pack2h(float lo, float hi) {
 }
 
 // Max / sum across the 16 lanes of a row group (lanes with equal lane/16).
-__device__ __forceinline__ float group16_max(float v) {
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-__device__ __forceinline__ float group16_sum(float v) {
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
+__device__ __forceinline__ float group16_max(float v) { return row16_max(v); }
+__device__ __forceinline__ float group16_sum(float v) { return row16_sum(v); }
+
+// 2^x on the hardware exp (v_exp_f32); arguments here are <= 0 and results
+// below 2^-126 flush to 0, which only drops contributions < 1e-38 of the max.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 struct AttnParams {
   const float* qrot;        // [B, Hq, 128] fp32 = q @ PiK^T
@@ -100,36 +96,38 @@ struct BlockRegs {
   float vnorm[2];
 };
 
-// Loads past t_end read the last valid token (t_end - 1 >= t0) and are zeroed
-// afterwards: every load is unconditional, so they issue back to back
-// instead of one branch + wait per element.
-__device__ __forceinline__ void load_block(BlockRegs& R, int t0, int t_end, int lane, const uint8_t* kc,
+// Code bytes / norms of a 32-token block starting at t0, read without any
+// condition: tokens at or past t_addr_end read token t_addr_end - 1 (valid
+// memory), so every load issues back to back; mask_block zeroes the tokens at
+// or past the valid end once it is known.
+__device__ __forceinline__ void load_block(BlockRegs& R, int t0, int t_addr_end, int lane, const uint8_t* kc,
                                            const float* kn, const uint8_t* vc, const float* vn) {
   const int g = lane >> 4, w = lane & 15;
-  u32x4 kr[2];
-  float knv[2], vnv[2];
-  uint32_t vd[8];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
-    const int tok = min(t0 + 16 * tt + (lane & 15), t_end - 1);
-    kr[tt] = *reinterpret_cast<const u32x4*>(kc + static_cast<size_t>(tok) * kRowB + 16 * g);
-    knv[tt] = kn[tok];
-    vnv[tt] = vn[tok];
+    const int tok = min(t0 + 16 * tt + (lane & 15), t_addr_end - 1);
+    R.kraw[tt] = *reinterpret_cast<const u32x4*>(kc + static_cast<size_t>(tok) * kRowB + 16 * g);
+    R.knorm[tt] = kn[tok];
+    R.vnorm[tt] = vn[tok];
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int tok = min(t0 + 8 * g + i, t_end - 1);
-    vd[i] = *reinterpret_cast<const uint32_t*>(vc + static_cast<size_t>(tok) * kRowB + 4 * w);
+    const int tok = min(t0 + 8 * g + i, t_addr_end - 1);
+    R.vdw[i] = *reinterpret_cast<const uint32_t*>(vc + static_cast<size_t>(tok) * kRowB + 4 * w);
   }
+}
+
+__device__ __forceinline__ void mask_block(BlockRegs& R, int t0, int t_end, int lane) {
+  const int g = lane >> 4;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const bool ok = t0 + 16 * tt + (lane & 15) < t_end;
-    R.kraw[tt] = ok ? kr[tt] : u32x4{0u, 0u, 0u, 0u};
-    R.knorm[tt] = ok ? knv[tt] : 0.f;
-    R.vnorm[tt] = ok ? vnv[tt] : 0.f;
+    R.kraw[tt] = ok ? R.kraw[tt] : u32x4{0u, 0u, 0u, 0u};
+    R.knorm[tt] = ok ? R.knorm[tt] : 0.f;
+    R.vnorm[tt] = ok ? R.vnorm[tt] : 0.f;
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) R.vdw[i] = t0 + 8 * g + i < t_end ? vd[i] : 0u;
+  for (int i = 0; i < 8; ++i) R.vdw[i] = t0 + 8 * g + i < t_end ? R.vdw[i] : 0u;
 }
 
 template <int GMAX>
@@ -137,35 +135,27 @@ __global__ __launch_bounds__(kThreads) void tq_attn_split_kernel(AttnParams P) {
   __shared__ uint32_t s_lut[256];
   __shared__ __align__(16) uint16_t s_p[kWaves][16][kBlk];  // p * n_t, fp16, per wave
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
-  __shared__ __align__(16) float s_o[kWaves][GMAX][kD];
+  __shared__ __align__(16) float s_o[kWaves][16][kD];  // all 16 MFMA rows: rows >= G hold zeros
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int G = P.G;
-  const int L = min(*P.seq_len, P.max_len);
-  const int cold_len = max(0, L - P.hot_cap);
   const size_t bh = static_cast<size_t>(b) * P.Hkv + kvh;
   float* rec = P.partials + (bh * P.nsplit + split) * rec_floats(G);
 
+  // The split's token range is static; the current length only masks it.
+  // So the length load, the wave's first token block, the centroid pairs of
+  // the LUT and the rotated query are all in flight before the first wait.
   const int t_begin = split * P.split_tokens;
-  const int t_end = min(cold_len, t_begin + P.split_tokens);
-  if (t_begin >= t_end) {
-    if (tid < G) {
-      rec[tid] = -INFINITY;
-      rec[G + tid] = 0.f;
-    }
-    return;
-  }
-  // Loads first, in the order they are consumed: the wave's first token
-  // block, the centroid pairs of the LUT, the rotated query.  They are all in
-  // flight before the first wait.
+  const int t_addr_end = min(t_begin + P.split_tokens, P.cap);  // valid memory
+  const int seq_len = *P.seq_len;
   const uint8_t* kc = P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB;
   const uint8_t* vc = P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB;
   const float* kn = P.k_norms + bh * static_cast<size_t>(P.cap);
   const float* vn = P.v_norms + bh * static_cast<size_t>(P.cap);
   BlockRegs cur;
   int t0 = t_begin + wave * kBlk;
-  load_block(cur, min(t0, t_end - 1), t_end, lane, kc, kn, vc, vn);  // waves past t_end never use it
+  if (t_begin < t_addr_end) load_block(cur, t0, t_addr_end, lane, kc, kn, vc, vn);
   float c_lo, c_hi;
   {
     const int cmax = P.ncent - 1;
@@ -194,6 +184,18 @@ __global__ __launch_bounds__(kThreads) void tq_attn_split_kernel(AttnParams P) {
     }
   }
 
+  const int L = min(seq_len, P.max_len);
+  const int cold_len = max(0, L - P.hot_cap);
+  const int t_end = min(cold_len, t_addr_end);
+  if (t_begin >= t_end) {  // uniform over the block: nothing of this split is cold yet
+    if (tid < G) {
+      rec[tid] = -INFINITY;
+      rec[G + tid] = 0.f;
+    }
+    return;
+  }
+  mask_block(cur, t0, t_end, lane);
+
   float m[4], l[4];
   f32x4 o[8];
 #pragma unroll
@@ -207,7 +209,10 @@ __global__ __launch_bounds__(kThreads) void tq_attn_split_kernel(AttnParams P) {
   for (; t0 < t_end; t0 += kWaves * kBlk) {
     const int tn = t0 + kWaves * kBlk;
     BlockRegs nxt;
-    if (tn < t_end) load_block(nxt, tn, t_end, lane, kc, kn, vc, vn);
+    if (tn < t_end) {
+      load_block(nxt, tn, t_end, lane, kc, kn, vc, vn);
+      mask_block(nxt, tn, t_end, lane);
+    }
     // ---- scores for tokens t0 .. t0+31 (two 16-token MFMA tiles)
     f32x4 sc[2];
     bool valid[2];
@@ -231,15 +236,12 @@ __global__ __launch_bounds__(kThreads) void tq_attn_split_kernel(AttnParams P) {
       const float s1 = valid[1] ? sc[1][i] * cur.knorm[1] : -INFINITY;
       const float bmax = group16_max(fmaxf(s0, s1));
       const float mnew = fmaxf(m[i], bmax);
-      float alpha, p0, p1;
-      if (mnew == -INFINITY) {
-        alpha = 1.f;
-        p0 = p1 = 0.f;
-      } else {
-        alpha = exp2f(m[i] - mnew);
-        p0 = valid[0] ? exp2f(s0 - mnew) : 0.f;
-        p1 = valid[1] ? exp2f(s1 - mnew) : 0.f;
-      }
+      // Branch-free: while nothing is valid (mnew = -inf) exp2(-inf - 0) = 0
+      // keeps l, o and p at 0.
+      const float mref = mnew == -INFINITY ? 0.f : mnew;
+      const float alpha = fast_exp2(m[i] - mref);
+      const float p0 = valid[0] ? fast_exp2(s0 - mref) : 0.f;
+      const float p1 = valid[1] ? fast_exp2(s1 - mref) : 0.f;
       l[i] = l[i] * alpha + group16_sum(p0 + p1);
       m[i] = mnew;
 #pragma unroll
@@ -287,23 +289,19 @@ __global__ __launch_bounds__(kThreads) void tq_attn_split_kernel(AttnParams P) {
   }
 
   // ---- merge the 4 waves of the block through LDS
+  // Unconditional stores of all 16 rows (no per-row branches); the merge
+  // below reads rows < G only.
   if ((lane & 15) == 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int hh = 4 * g + i;
-      if (hh < G) {
-        s_m[wave][hh] = m[i];
-        s_l[wave][hh] = l[i];
-      }
+      s_m[wave][4 * g + i] = m[i];
+      s_l[wave][4 * g + i] = l[i];
     }
   }
 #pragma unroll
   for (int t = 0; t < 8; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int hh = 4 * g + i;
-      if (hh < G) s_o[wave][hh][8 * (lane & 15) + t] = o[t][i];
-    }
+    for (int i = 0; i < 4; ++i) s_o[wave][4 * g + i][8 * (lane & 15) + t] = o[t][i];
   __syncthreads();
   for (int e = tid; e < G * kD; e += kThreads) {
     const int hh = e / kD, d = e % kD;
@@ -314,7 +312,7 @@ __global__ __launch_bounds__(kThreads) void tq_attn_split_kernel(AttnParams P) {
     if (M != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
-        const float wt = exp2f(s_m[w][hh] - M);
+        const float wt = fast_exp2(s_m[w][hh] - M);
         acc += wt * s_o[w][hh][d];
         lsum += wt * s_l[w][hh];
       }
@@ -358,19 +356,19 @@ __global__ __launch_bounds__(kCombThreads) void tq_attn_combine_kernel(AttnParam
   const int hq = blockIdx.x, b = blockIdx.y;
   const int G = P.G, kvh = hq / G, hh = hq % G;
   const int ns = P.nsplit;
-  const int L = min(*P.seq_len, P.max_len);
-  const int cold_len = max(0, L - P.hot_cap);
-  const int hot_len = L - cold_len;
+  const int seq_len = *P.seq_len;  // only the masks below depend on it
   const size_t bh = static_cast<size_t>(b) * P.Hkv + kvh;
   const int RF = rec_floats(G);
   const float* recs = P.partials + bh * ns * RF;
   const size_t hot_base = bh * static_cast<size_t>(P.hot_cap) * kD;
   const int d = tid & (kD - 1), qd = tid >> 7;
 
-  // ---- A. every independent load up front
-  // Every load below is unconditional from a clamped, always valid address
-  // (split ns - 1, hot token 0 / slot cold_len % hot_cap) and zeroed after,
-  // so all of them are in flight together.
+  // ---- A. every load up front.  The hot window is walked by ring slot:
+  // softmax sums do not depend on token order, and slot j holds a current
+  // token exactly when j < hot_len (the window is the last hot_len tokens and
+  // token t sits in slot t % hot_cap), so no address depends on the length.
+  // Loads are unconditional from clamped, always valid addresses (split
+  // ns - 1, slot hot_cap - 1) and masked after, so all are in flight together.
   float ms, ls;
   {
     const size_t sr = static_cast<size_t>(min(tid, ns - 1)) * RF;
@@ -385,29 +383,31 @@ __global__ __launch_bounds__(kCombThreads) void tq_attn_combine_kernel(AttnParam
 #pragma unroll
   for (int i = 0; i < kHotMax / 4; ++i) {
     const int jj = qd + 4 * i;
-    hv[i] = P.v_hot[hot_base + static_cast<size_t>((cold_len + (jj < hot_len ? jj : 0)) % P.hot_cap) * kD + d];
+    hv[i] = P.v_hot[hot_base + static_cast<size_t>(min(jj, P.hot_cap - 1)) * kD + d];
   }
   float ca[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i)
     ca[i] = recs[static_cast<size_t>(min(qd + 4 * i, ns - 1)) * RF + 2 * G + hh * kD + d];
 
-  // hot score partial: token j = tid / 8, dims 16 * (tid % 8) .. +16
+  // hot score partial: slot j = tid / 8, dims 16 * (tid % 8) .. +16
   const int j = tid >> 3, part = tid & 7;
-  const bool hj = j < hot_len;
   float sdot = 0.f;
   {
-    const int slot = (cold_len + (hj ? j : 0)) % P.hot_cap;
+    const int slot = min(j, P.hot_cap - 1);
     const uint4* kp = reinterpret_cast<const uint4*>(P.k_hot + hot_base + static_cast<size_t>(slot) * kD + 16 * part);
     const uint4* qp = reinterpret_cast<const uint4*>(P.q + (static_cast<size_t>(b) * P.Hq + hq) * kD + 16 * part);
     const uint4 k0 = kp[0], k1 = kp[1];
     const uint4 q0 = qp[0], q1 = qp[1];
-    sdot = dot8_f16(k0, q0) + dot8_f16(k1, q1);  // tokens past hot_len are masked by `score`
+    sdot = dot8_f16(k0, q0) + dot8_f16(k1, q1);  // slots past hot_len are masked by `score`
   }
+  const int L = min(seq_len, P.max_len);
+  const int hot_len = L - max(0, L - P.hot_cap);
+  const bool hj = j < hot_len;
   // ---- B. softmax statistics over cold splits and hot tokens
-  sdot += __shfl_xor(sdot, 1);
-  sdot += __shfl_xor(sdot, 2);
-  sdot += __shfl_xor(sdot, 4);
+  sdot += dpp_f<0xB1>(sdot);   // xor 1
+  sdot += dpp_f<0x4E>(sdot);   // xor 2
+  sdot += dpp_f<0x141>(sdot);  // the other quad of the 8-lane half row
   const float score = hj ? sdot * P.scale_log2 : -INFINITY;
   float v = fmaxf(ms, part == 0 ? score : -INFINITY);
   v = wave_max(v);
@@ -417,8 +417,8 @@ __global__ __launch_bounds__(kCombThreads) void tq_attn_combine_kernel(AttnParam
 #pragma unroll
   for (int w = 0; w < kCombWaves; ++w) M = fmaxf(M, s_red[w]);
   __syncthreads();
-  const float wsp = (tid < ns && ms != -INFINITY) ? exp2f(ms - M) : 0.f;
-  const float pj = hj ? exp2f(score - M) : 0.f;
+  const float wsp = (tid < ns && ms != -INFINITY) ? fast_exp2(ms - M) : 0.f;
+  const float pj = hj ? fast_exp2(score - M) : 0.f;
   if (tid < ns) s_w[tid] = wsp;
   if (part == 0 && j < kHotMax) s_p[j] = pj;
   float lv = wsp * ls + (part == 0 ? pj : 0.f);
