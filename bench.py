@@ -320,6 +320,101 @@ def bench_copy(args, torch):
             "config": {"workload": "copy_512MiB", "bytes_read": n, "bytes_written": n}}
 
 
+# ------------------------------------------------------------------ config 3
+def bench_quant(args, torch):
+    """Config 3: TurboQuant 3-bit quantize of K and V fp16 [8, 4096, 128] (4 channels x10), Pi seeds 42/43.
+
+    One step = quantize K (PiK) + quantize V (PiV): norm, normalise, fp32-MFMA rotation, bucketing and
+    nibble packing in one kernel each; 32 rotating K/V sets (537 MB)."""
+    from leankv_amd import kernels
+    from leankv_amd.turboquant.codebook import get_codebook_tensors
+    from leankv_amd.turboquant.rotation import generate_rotation_matrix
+
+    dev = torch.device("cuda:0")
+    H, T, D = 8, 4096, 128
+    _, bnd = get_codebook_tensors(D, 3, dev, torch.float32)
+    bounds = bnd[1:-1].contiguous()
+    PiK = generate_rotation_matrix(D, dev, torch.float32, 42)
+    PiV = generate_rotation_matrix(D, dev, torch.float32, 43)
+    sets = []
+    for s in range(32):
+        g = torch.Generator(device=dev).manual_seed(300 + s)
+        kv = torch.randn(2, H, T, D, generator=g, device=dev)
+        kv[..., [0, 31, 64, 127]] *= 10
+        sets.append(kv.half())
+
+    def launch(i):
+        kernels.tq_quantize(sets[i][0], PiK, bounds, 3)
+        kernels.tq_quantize(sets[i][1], PiV, bounds, 3)
+    wall, omean, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
+    kmean, kmed = _kernel_time(launch, len(sets), args.steps, args.warmup, torch)
+    nvec = 2 * H * T
+    alg_bytes = nvec * (D * 2 + 64 + 2)
+    flops = nvec * 2 * D * D
+    tflops = flops / (kmean * 1e-3) / 1e12
+    return {
+        "metric": "TurboQuant 3-bit quantize GB/s (K,V fp16 [8,4096,128])",
+        "value": round(alg_bytes / (kmean * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wall, 5),
+        "higher_is_better": True, "dtype": "fp32 rotation (fp16 in, 3-bit codes + fp16 norms out)",
+        "config": {"workload": "config3_tq_quantize", "vectors": nvec, "alg_bytes_per_step": alg_bytes,
+                   "rotation_flop_per_step": flops, "sets": len(sets)},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "quantize_kernel<3,true> (K and V launches)", "kernel_us_mean": round(kmean * 1e3, 3),
+                     "kernel_us_median": round(kmed * 1e3, 3), "hbm_GBps": round(alg_bytes / (kmean * 1e-3) / 1e9, 1)},
+    }
+
+
+# ------------------------------------------------------------------ config 4
+def bench_attn(args, torch):
+    """Config 4: decode attention on the packed 3-bit cache, B=16, 32 query / 8 kv heads, 4096 cold tokens
+    + a 64-token fp16 hot window, scale 1/sqrt(128).  The cache content is random codes / norms (the
+    kernels' cost does not depend on it); 8 rotating cache sets (570 MB)."""
+    from leankv_amd import kernels
+    from leankv_amd.turboquant.codebook import get_codebook_tensors
+    from leankv_amd.turboquant.rotation import generate_rotation_matrix
+
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, D, cold, hot = 16, 32, 8, 128, 4096, 64
+    L = cold + hot
+    cent, _ = get_codebook_tensors(D, 3, dev, torch.float32)
+    PiK = generate_rotation_matrix(D, dev, torch.float32, 42)
+    PiV = generate_rotation_matrix(D, dev, torch.float32, 43)
+    seq = torch.tensor([L], dtype=torch.int32, device=dev)
+    sets = []
+    for s in range(8):
+        g = torch.Generator(device=dev).manual_seed(400 + s)
+        kc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8)
+        vc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8)
+        kn = torch.rand(B, Hkv, cold, generator=g, device=dev) * 4 + 8
+        vn = torch.rand(B, Hkv, cold, generator=g, device=dev) * 4 + 8
+        kh = torch.randn(B, Hkv, hot, D, generator=g, device=dev).half()
+        vh = torch.randn(B, Hkv, hot, D, generator=g, device=dev).half()
+        q = torch.randn(B, Hq, D, generator=g, device=dev).half()
+        sets.append((q, kc, kn, vc, vn, kh, vh, torch.empty_like(q)))
+    ws = torch.empty(kernels.decode_attn_workspace_bytes(B, Hq, Hkv, L), dtype=torch.uint8, device=dev)
+
+    def launch(i):
+        q, kc, kn, vc, vn, kh, vh, out = sets[i]
+        kernels.tq_decode_attn_out(q, kc, kn, vc, vn, kh, vh, PiK, PiV, cent, 3, seq, L, D ** -0.5, out, ws)
+    wall, _, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
+    kmean, kmed = _kernel_time(launch, len(sets), args.steps, args.warmup, torch)
+    alg = B * Hkv * (cold * (64 + 64 + 4 + 4) + hot * D * 2 * 2) + 2 * B * Hq * D * 2
+    achieved = alg / (kmean * 1e-3) / 1e9
+    return {
+        "metric": "packed-KV decode attention HBM GB/s (B=16, 32/8 heads, 4096 cold + 64 hot)",
+        "value": round(achieved, 1), "unit": "GB/s", "ms_per_step": round(wall, 5), "higher_is_better": True,
+        "dtype": "3-bit codes, fp16 MFMA scores/values, fp32 softmax",
+        "config": {"workload": "config4_packed_attention", "batch": B, "heads": "32/8", "cold": cold, "hot": hot,
+                   "alg_bytes_per_call": alg, "sets": len(sets)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic("attn_config4"),
+                     "kernel": "q rotation + tq_attn_split_kernel + tq_attn_combine_kernel (one call)",
+                     "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3),
+                     "alg_bytes_per_launch": alg},
+    }
+
+
 def _fill_gemv_defaults(args):
     if args.steps is None:
         args.steps = 200
@@ -447,7 +542,8 @@ def main():
             res["roofline"] = roofline_gateup(args, torch)
     else:
         _fill_gemv_defaults(args)
-        fn = {"gemv": bench_gemv, "mlp": bench_mlp, "copy": bench_copy}.get(args.workload)
+        fn = {"gemv": bench_gemv, "mlp": bench_mlp, "copy": bench_copy, "quant": bench_quant,
+              "attn": bench_attn}.get(args.workload)
         if fn is None:
             print("bench.py: workload %s is not implemented yet" % args.workload, file=sys.stderr)
             sys.exit(2)

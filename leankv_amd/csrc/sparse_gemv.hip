@@ -157,11 +157,18 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  int gslab = blockIdx.x, chunk = blockIdx.y;
-  if (G.chunk_major) {  // consecutive blocks walk the chunks of one slab
-    const int lin = blockIdx.y * gridDim.x + blockIdx.x;
-    gslab = lin / G.nchunk;
-    chunk = lin % G.nchunk;
+  // Work items are (slab, chunk) pairs.  The usual grid has one block per
+  // item (the loop runs once); a persistent grid walks them with a stride.
+  const int nslab_tot = G.slab0[G.nseg];
+  const int nitems = nslab_tot * G.nchunk;
+  for (int item = blockIdx.y * gridDim.x + blockIdx.x; item < nitems; item += gridDim.x * gridDim.y) {
+  int gslab, chunk;
+  if (G.chunk_major) {  // consecutive items walk the chunks of one slab
+    gslab = item / G.nchunk;
+    chunk = item % G.nchunk;
+  } else {
+    gslab = item % nslab_tot;
+    chunk = item / nslab_tot;
   }
   const int z0 = chunk * BZ;
   const int Z = G.Z;
@@ -263,16 +270,19 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
   }
 
   // ---- 4. output (threads 0..255, one column each): fp16 directly (single chunk) or partial sums
-  if (tid >= BN) return;
-  if (G.y != nullptr) {
-    if (n0 + tid < N) G.y[n0 + tid] = DUAL ? swiglu_f16(sums[0], sums[NL - 1]) : f2h(sums[0]);
-    return;
-  }
+  if (tid < BN) {
+    if (G.y != nullptr) {
+      if (n0 + tid < N) G.y[n0 + tid] = DUAL ? swiglu_f16(sums[0], sums[NL - 1]) : f2h(sums[0]);
+    } else {
 #pragma unroll
-  for (int l = 0; l < NL; ++l) {
-    float* P = G.part + (l == 0 ? G.part_off[seg] : G.part_up_off) +
-               (static_cast<size_t>(slab) * G.nchunk + chunk) * BN;
-    P[tid] = sums[l];
+      for (int l = 0; l < NL; ++l) {
+        float* P = G.part + (l == 0 ? G.part_off[seg] : G.part_up_off) +
+                   (static_cast<size_t>(slab) * G.nchunk + chunk) * BN;
+        P[tid] = sums[l];
+      }
+    }
+  }
+  __syncthreads();  // LDS is reused by the next item
   }
 }
 
@@ -339,6 +349,15 @@ int gemv_cpol() {
   }();
   return c;
 }
+// LKV_GEMV_PERSIST=k: a grid of k blocks per CU walks the (slab, chunk) items.
+int gemv_persist() {
+  static const int k = [] {
+    const char* env = getenv("LKV_GEMV_PERSIST");
+    const int v = env ? atoi(env) : 0;
+    return v > 0 && v <= 8 ? v : 0;
+  }();
+  return k;
+}
 bool gemv_chunk_major() {
   static const bool c = [] {
     const char* env = getenv("LKV_GEMV_ORDER");
@@ -369,7 +388,12 @@ int gemv_unroll() {
 
 int gemv_launch(const GemvArgs& G, int bz, bool dual, int mode, int nslab_total, hipStream_t st) {
   if (nslab_total <= 0) return LKV_OK;
-  const dim3 grid(static_cast<unsigned>(nslab_total), static_cast<unsigned>(G.nchunk));
+  dim3 grid(static_cast<unsigned>(nslab_total), static_cast<unsigned>(G.nchunk));
+  if (const int k = gemv_persist()) {
+    const int64_t items = static_cast<int64_t>(nslab_total) * G.nchunk;
+    const int64_t blocks = static_cast<int64_t>(k) * device_cu_count();
+    if (blocks < items) grid = dim3(static_cast<unsigned>(blocks), 1);
+  }
   bool ok = false;
   const bool t512 = gemv_threads() == 512 && bz >= 512;
   const int cp = gemv_cpol();

@@ -131,7 +131,7 @@ __device__ __forceinline__ void mask_block(BlockRegs& R, int t0, int t_end, int 
 }
 
 template <int GMAX>
-__global__ __launch_bounds__(kThreads) void tq_attn_split_kernel(AttnParams P) {
+__global__ __launch_bounds__(kThreads, 4) void tq_attn_split_kernel(AttnParams P) {
   __shared__ uint32_t s_lut[256];
   __shared__ __align__(16) uint16_t s_p[kWaves][16][kBlk];  // p * n_t, fp16, per wave
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
@@ -507,9 +507,11 @@ __global__ __launch_bounds__(tq::kThreads) void qrot_kernel(const uint16_t* __re
 
 constexpr int kSplitGran = kWaves * kBlk;  // tokens one pass of a block covers
 
-// Split count that gives ~2 blocks per CU, at most kMaxSplits - 1.
+// Split count that gives ~4 blocks per CU (each wave's token loop is a
+// latency chain, so more resident waves overlap more of them), at most
+// kMaxSplits - 1.
 int64_t target_splits(int64_t B, int64_t Hkv) {
-  const int64_t target = 2 * static_cast<int64_t>(device_cu_count());
+  const int64_t target = 4 * static_cast<int64_t>(device_cu_count());
   int64_t ns = (target + B * Hkv - 1) / (B * Hkv);
   if (ns > kMaxSplits - 1) ns = kMaxSplits - 1;
   return ns < 1 ? 1 : ns;
