@@ -185,47 +185,55 @@ struct PrepArgs {
   float* qrot;
 };
 
-// Grid (kv heads, 2): block (h, 0) is the key side -- its G query heads and
-// key: RoPE, the key leaving the hot window quantized with PiK, the query
-// heads rotated by PiK (rows 1..G of the same MFMA tile), the new key into the
-// ring; block (h, 1) is the value side with PiV.  The block's 64 KB rotation
-// matrix is fetched first, with fully coalesced 16-byte loads, and staged in
-// LDS for the MFMA operand reads; the MFMA arithmetic is tq_common.h's, so the
-// codes equal lkv_tq_cache_append's and q_rot equals lkv_tq_rotate's.
+// Grid (kv heads, 3).  Block (h, 0) is the key side: RoPE of the key, the
+// key leaving the hot window quantized with PiK, the new key into the ring;
+// block (h, 1) is the value side with PiV; block (h, 2) is the query side:
+// RoPE of the G query heads (fp16 copies for the hot-window scores) and
+// q_rot = q @ PiK^T by rotate_query_hilo, the split kernel's own arithmetic,
+// so the decode step and lkv_tq_decode_attn see identical rotated queries.
+// The key/value blocks fetch their 64 KB rotation matrix first, with fully
+// coalesced 16-byte loads, and stage it in LDS for the MFMA operand reads;
+// the MFMA arithmetic is tq_common.h's, so the codes equal
+// lkv_tq_cache_append's.
 template <int BITS>
 __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
-  constexpr int kCols = (kMaxG + 1) * kD / kThreads + 1;
-  constexpr int kPiLd = kD + 1;  // padded LDS row
-  __shared__ float s_pi[kD * kPiLd];
-  __shared__ float s_raw[kMaxG + 1][kD];   // key side: q heads then k; value side: v in row 0
-  __shared__ float s_rope[kMaxG + 1][kD];  // key side: q heads then k after RoPE
+  constexpr int kCols = kMaxG * kD / kThreads;  // projected columns per thread (query side at most)
+  constexpr int kPiLd = kD + 1;                 // padded LDS row
+  constexpr int kPartLd = kD + 4;               // query side: rotate_query_hilo partials in s_pi
+  static_assert(4 * 16 * kPartLd <= kD * kPiLd, "query partials fit in s_pi");
+  __shared__ __align__(16) float s_pi[kD * kPiLd];
+  __shared__ float s_raw[kMaxG][kD];   // query side: the G heads; key / value side: row 0
+  __shared__ float s_rope[kMaxG][kD];  // after RoPE (query and key sides)
   __shared__ uint8_t s_codes[tq::kRows * kD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kvh = blockIdx.x;
-  const bool vside = blockIdx.y == 1;
+  const int side = blockIdx.y;  // 0 key, 1 value, 2 query
+  const bool vside = side == 1, qside = side == 2;
   const int G = A.Hq / A.Hkv;
-  const int nvec = vside ? 1 : G + 1;  // projected vectors this block needs
-  const int ncol = nvec * kD;
+  const int ncol = (qside ? G : 1) * kD;  // projected columns this block needs
   const int nc = A.nchunk;
   const float* Pi = vside ? A.PiV : A.PiK;
 
   // ---- 0. loads, in this order, all in flight before the first wait: the
-  //      position, the rotation matrix (16 coalesced float4 per thread), the
-  //      decision boundaries, the first 16 chunks of the projection partial
-  //      sums, then what depends on the position -- the row leaving the hot
-  //      window (row 0 of the MFMA tile: lanes r == 0 use it, the others load
-  //      the same 64 bytes) and this position's RoPE row.
+  //      position, the rotation matrix (key / value side: 16 coalesced float4
+  //      per thread), the decision boundaries, the first 16 chunks of the
+  //      projection partial sums, then what depends on the position -- the
+  //      row leaving the hot window (row 0 of the MFMA tile: lanes r == 0
+  //      use it, the others load the same 64 bytes) and this position's
+  //      RoPE row.
   const int pos = A.state[0];
   float4 pr[kD * kD / 4 / kThreads];
-#pragma unroll
-  for (int i = 0; i < kD * kD / 4 / kThreads; ++i) pr[i] = reinterpret_cast<const float4*>(Pi)[i * kThreads + tid];
   float bd[(1 << BITS) - 1];
+  if (!qside) {
 #pragma unroll
-  for (int i = 0; i < (1 << BITS) - 1; ++i) bd[i] = A.bounds[i];
+    for (int i = 0; i < kD * kD / 4 / kThreads; ++i) pr[i] = reinterpret_cast<const float4*>(Pi)[i * kThreads + tid];
+#pragma unroll
+    for (int i = 0; i < (1 << BITS) - 1; ++i) bd[i] = A.bounds[i];
+  }
 
   // Projections, summed over chunks in chunk order, rounded to fp16.  A
-  // wave's 64 columns never straddle a 128-column head, so validity and the
-  // source matrix are uniform per wave (scalar branches).
+  // wave's 64 columns never straddle a 128-column head, so validity is
+  // uniform per wave (scalar branches).
   const float* src[kCols];
   bool ok[kCols];
   float psum[kCols];
@@ -235,15 +243,8 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
     ok[e] = cw < ncol;
     const int c = cw + lane;
     const int which = c / kD, d = c % kD;
-    int col;
-    const float* base;
-    if (vside) {
-      col = kvh * kD + d;
-      base = A.pv;
-    } else {
-      col = which < G ? (kvh * G + which) * kD + d : kvh * kD + d;
-      base = which < G ? A.pq : A.pk;
-    }
+    const int col = qside ? (kvh * G + which) * kD + d : kvh * kD + d;
+    const float* base = qside ? A.pq : vside ? A.pv : A.pk;
     src[e] = base + static_cast<size_t>(col / kGemvBN) * nc * kGemvBN + (col % kGemvBN);
     psum[e] = 0.f;
   }
@@ -258,13 +259,15 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
 
   const int slot = pos % A.hot_cap;
   const int ev = pos - A.hot_cap;
-  const bool evict = pos >= A.hot_cap && ev < A.cap;
+  const bool evict = !qside && pos >= A.hot_cap && ev < A.cap;
   const int r = lane & 15, c0 = 32 * (lane >> 4);
   const size_t hrow = (static_cast<size_t>(kvh) * A.hot_cap + slot) * kD;
   uint16_t* hot = vside ? A.v_hot : A.k_hot;
   uint4 hraw[4];
+  if (!qside) {
 #pragma unroll
-  for (int v = 0; v < 4; ++v) hraw[v] = reinterpret_cast<const uint4*>(hot + hrow + c0)[v];
+    for (int v = 0; v < 4; ++v) hraw[v] = reinterpret_cast<const uint4*>(hot + hrow + c0)[v];
+  }
   const uint16_t cs_d = A.cos[static_cast<size_t>(pos) * kD + (tid & (kD - 1))];
   const uint16_t sn_d = A.sin[static_cast<size_t>(pos) * kD + (tid & (kD - 1))];
 
@@ -295,14 +298,16 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
     const int c = e * kThreads + tid;
     if (ok[e]) s_raw[c / kD][c % kD] = h2f(f2h(psum[e]));
   }
+  if (!qside) {
 #pragma unroll
-  for (int i = 0; i < kD * kD / 4 / kThreads; ++i) {
-    const int f = i * kThreads + tid;  // float4 index: row f / 32, columns 4 (f % 32) ..
-    float* dst = s_pi + (f >> 5) * kPiLd + 4 * (f & 31);
-    dst[0] = pr[i].x;
-    dst[1] = pr[i].y;
-    dst[2] = pr[i].z;
-    dst[3] = pr[i].w;
+    for (int i = 0; i < kD * kD / 4 / kThreads; ++i) {
+      const int f = i * kThreads + tid;  // float4 index: row f / 32, columns 4 (f % 32) ..
+      float* dst = s_pi + (f >> 5) * kPiLd + 4 * (f & 31);
+      dst[0] = pr[i].x;
+      dst[1] = pr[i].y;
+      dst[2] = pr[i].z;
+      dst[3] = pr[i].w;
+    }
   }
   __syncthreads();
 
@@ -310,34 +315,48 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
   //      (apply_rotary_pos_emb on fp16 tensors, modeling_mistral.py)
   if (!vside) {
     const float cf = h2f(cs_d), sf = h2f(sn_d);  // this thread's d = tid % 128 for every e below
-    for (int e = tid; e < (G + 1) * kD; e += kThreads) {
+    for (int e = tid; e < ncol; e += kThreads) {
       const int rr = e / kD, d = e % kD;
       const float xv = s_raw[rr][d];
       const float rh = d < kD / 2 ? -s_raw[rr][d + kD / 2] : s_raw[rr][d - kD / 2];
       const float o = h2f(f2h(h2f(f2h(xv * cf)) + h2f(f2h(rh * sf))));
       s_rope[rr][d] = o;
-      if (rr < G) A.q16[static_cast<size_t>(kvh * G + rr) * kD + d] = f2h(o);
+      if (qside) A.q16[static_cast<size_t>(kvh * G + rr) * kD + d] = f2h(o);
     }
     __syncthreads();
   }
 
-  // ---- 3. one 16-row tile: row 0 = the vector leaving the hot window
-  //      (normalised), rows 1..G = the query heads on the key side
-  float a[32];
-  if (r == 0) {
-    // tq::load_row_f16's conversion of the preloaded row (zero when nothing leaves)
+  if (qside) {
+    // ---- 3q. the rotated query heads (s_pi holds the partials)
+    const int h = lane & 15, g = lane >> 4;
+    u32x4 qb = u32x4{0u, 0u, 0u, 0u};
+    if (h < G) {
+      const float* q = &s_rope[h][32 * wave + 8 * g];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const uint32_t w[4] = {hraw[v].x, hraw[v].y, hraw[v].z, hraw[v].w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[8 * v + 2 * i] = evict ? h2f(static_cast<uint16_t>(w[i] & 0xffffu)) : 0.f;
-        a[8 * v + 2 * i + 1] = evict ? h2f(static_cast<uint16_t>(w[i] >> 16)) : 0.f;
-      }
+      for (int j = 0; j < 4; ++j)
+        qb[j] = static_cast<uint32_t>(f2h(q[2 * j])) | (static_cast<uint32_t>(f2h(q[2 * j + 1])) << 16);
     }
-  } else {
+    float4 out[8];
+    rotate_query_hilo(A.PiK, qb, wave, lane, s_pi, kPartLd, out);
+    if (h < G) {
+      float4* dst = reinterpret_cast<float4*>(A.qrot + static_cast<size_t>(kvh * G + h) * kD + 32 * g);
 #pragma unroll
-    for (int s = 0; s < 32; ++s) a[s] = (!vside && r <= G) ? s_rope[r - 1][c0 + s] : 0.f;
+      for (int i = 0; i < 8; ++i) dst[i] = out[i];
+    }
+    return;
+  }
+
+  // ---- 3. one 16-row tile: row 0 = the vector leaving the hot window
+  //      (normalised), the other rows zero
+  float a[32];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const uint32_t w[4] = {hraw[v].x, hraw[v].y, hraw[v].z, hraw[v].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[8 * v + 2 * i] = (evict && r == 0) ? h2f(static_cast<uint16_t>(w[i] & 0xffffu)) : 0.f;
+      a[8 * v + 2 * i + 1] = (evict && r == 0) ? h2f(static_cast<uint16_t>(w[i] >> 16)) : 0.f;
+    }
   }
   float bop[2][32];
 #pragma unroll
@@ -350,16 +369,6 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
   const float nrm = tq::normalize_row_f32_if(a, r == 0);
   f32x4 acc[2];
   tq::rotate_tile(a, bop, acc);
-  if (!vside) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 4 * (lane >> 4) + i;
-        const int dim = 8 * (lane & 15) + 2 * wave + t;
-        if (row >= 1 && row <= G) A.qrot[static_cast<size_t>(kvh * G + row - 1) * kD + dim] = acc[t][i];
-      }
-  }
   if (evict) {
     tq::codes_to_lds<BITS>(acc, bd, wave, lane, s_codes);
     if (tid == 0) (vside ? A.v_norms : A.k_norms)[static_cast<size_t>(kvh) * A.cap + ev] = nrm;
@@ -370,7 +379,7 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
     tq::pack_store<BITS>(s_codes, vside ? A.v_codes : A.k_codes, 0, 1, [=](int64_t) { return roff; });
   }
   // ---- 4. the new token into its ring slot
-  if (tid < kD) hot[hrow + tid] = f2h(vside ? s_raw[0][tid] : s_rope[G][tid]);
+  if (tid < kD) hot[hrow + tid] = f2h(vside ? s_raw[0][tid] : s_rope[0][tid]);
 }
 
 struct Cand {
@@ -541,9 +550,9 @@ extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_deco
     A.q16 = reinterpret_cast<uint16_t*>(ws + p.off_q16);
     A.qrot = reinterpret_cast<float*>(ws + p.off_qrot);
     if (d.bits == 3)
-      hipLaunchKernelGGL((prep_kernel<3>), dim3(static_cast<unsigned>(p.Hkv), 2), dim3(kThreads), 0, st, A);
+      hipLaunchKernelGGL((prep_kernel<3>), dim3(static_cast<unsigned>(p.Hkv), 3), dim3(kThreads), 0, st, A);
     else
-      hipLaunchKernelGGL((prep_kernel<4>), dim3(static_cast<unsigned>(p.Hkv), 2), dim3(kThreads), 0, st, A);
+      hipLaunchKernelGGL((prep_kernel<4>), dim3(static_cast<unsigned>(p.Hkv), 3), dim3(kThreads), 0, st, A);
     LKV_LAUNCH_CHECK("decode prep");
   }
   // 3-4. attention

@@ -121,6 +121,69 @@ __device__ __forceinline__ uint16_t swiglu_f16(float g, float u) {
 }
 
 // ------------------------------------------------------------- attention
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+}
+
+// q_rot = q @ PiK^T for the query heads (at most 16) of one kv head: the one
+// arithmetic of the attention's rotated query, shared by the split kernel
+// and the decode step so both give identical bits.  PiK is split into
+// hi = fp16(x) (toward zero) and lo = fp16((x - hi) * 2^11) (toward zero),
+// q is fp16, so both products run on v_mfma_f32_16x16x32_f16 with exact
+// fp32 products: q_rot = acc_hi + acc_lo * 2^-11, error ~2^-20 relative.
+// The tile is transposed (rows = output dims, columns = heads).  Wave w
+// covers input dims 32w .. 32w+31 (lane group g' holding 32w + 8g' .. +7)
+// for 8 output tiles; tile c row r is output dim 32(r/4) + 4c + r%4, so lane
+// (h = lane%16, g = lane/16) ends with dims 32g .. 32g+31 of head h.  The 4
+// wave partials are summed through LDS in the fixed order ((w0+w1)+w2)+w3.
+// Called by all 4 waves of a 256-thread block (one __syncthreads inside).
+//   qb   this lane's q[h][32w + 8g .. +7] as fp16 pairs (zero for unused h)
+//   part LDS scratch, 4 x 16 rows of `ld` floats (ld >= 128, ld % 4 == 0)
+//   out  out[i] = q_rot[h][32g + 4i .. 4i+3]
+__device__ __forceinline__ void rotate_query_hilo(const float* __restrict__ PiK, const u32x4& qb, int wave,
+                                                  int lane, float* part, int ld, float4 (&out)[8]) {
+  const int h = lane & 15, g = lane >> 4;
+  float4 pa[8][2];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int row = 32 * (h >> 2) + 4 * c + (h & 3);  // lane % 16 is the A row here
+    const float4* src = reinterpret_cast<const float4*>(PiK + row * 128 + 32 * wave + 8 * g);
+    pa[c][0] = src[0];
+    pa[c][1] = src[1];
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const float x[8] = {pa[c][0].x, pa[c][0].y, pa[c][0].z, pa[c][0].w,
+                        pa[c][1].x, pa[c][1].y, pa[c][1].z, pa[c][1].w};
+    u32x4 hi, lo;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const auto hp = __builtin_amdgcn_cvt_pkrtz(x[2 * j], x[2 * j + 1]);
+      const float r0 = (x[2 * j] - static_cast<float>(hp[0])) * 2048.f;
+      const float r1 = (x[2 * j + 1] - static_cast<float>(hp[1])) * 2048.f;
+      hi[j] = __builtin_bit_cast(uint32_t, hp);
+      lo[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+    }
+    const f32x4 ah = mfma16x16x32(hi, qb, f32x4{0.f, 0.f, 0.f, 0.f});
+    const f32x4 al = mfma16x16x32(lo, qb, f32x4{0.f, 0.f, 0.f, 0.f});
+    *reinterpret_cast<float4*>(part + (wave * 16 + h) * ld + 32 * g + 4 * c) =
+        make_float4(fmaf(al[0], 1.f / 2048.f, ah[0]), fmaf(al[1], 1.f / 2048.f, ah[1]),
+                    fmaf(al[2], 1.f / 2048.f, ah[2]), fmaf(al[3], 1.f / 2048.f, ah[3]));
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float4 p[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) p[w] = *reinterpret_cast<const float4*>(part + (w * 16 + h) * ld + 32 * g + 4 * i);
+    out[i] = make_float4(((p[0].x + p[1].x) + p[2].x) + p[3].x, ((p[0].y + p[1].y) + p[2].y) + p[3].y,
+                         ((p[0].z + p[1].z) + p[2].z) + p[3].z, ((p[0].w + p[1].w) + p[2].w) + p[3].w);
+  }
+}
+
 struct AttnPlan {
   int nsplit, split_tokens;
   size_t qrot_off, part_off, total;
@@ -128,7 +191,7 @@ struct AttnPlan {
 AttnPlan attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_cap);
 
 struct AttnCall {
-  const float* qrot;        // [B, Hq, 128] fp32 = q @ PiK^T
+  const float* qrot;        // [B, Hq, 128] fp32 = q @ PiK^T (when PiK is null)
   const uint16_t* q;        // [B, Hq, 128] fp16 (the fp16 hot window uses the unrotated query)
   const uint8_t* k_codes;   // [B, Hkv, cap, 64]
   const float* k_norms;     // [B, Hkv, cap]
@@ -137,6 +200,7 @@ struct AttnCall {
   const uint16_t* k_hot;    // [B, Hkv, hot_cap, 128] ring, token t in slot t % hot_cap
   const uint16_t* v_hot;
   const float* PiV;         // [128, 128]
+  const float* PiK;         // non-null: rotate q in the split kernel (qrot unused); null: qrot given
   const float* centroids;   // [2^bits]
   const int32_t* seq_len;   // device scalar: tokens in the cache (after this step's append)
   float* partials;          // split records (workspace)
@@ -145,7 +209,7 @@ struct AttnCall {
   int64_t max_len, B, Hq, Hkv, cap, hot_cap;
   int bits;
 };
-// Launch the split and combine kernels (q already rotated into call.qrot).
+// Launch the split and combine kernels.
 int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st);
 
 }  // namespace lkv

@@ -11,23 +11,28 @@
 // rotated domain, and PiV is applied once per query head at the end.
 //
 // Launches (all on the caller's stream, no inter-block waits):
-//   1. q_rot = q @ PiK^T on fp32 MFMA, one block per (batch, kv head)
-//      (the decode step computes it inside its QKV epilogue instead);
-//   2. split kernel, grid splits x kv_heads x batch, 4 waves per block, each
-//      block owning a contiguous range of cold tokens; each wave walks
-//      32-token blocks of it, prefetching the next block's codes and norms
-//      while it computes the current one:
-//      * scores: v_mfma_f32_16x16x32_f16 with A = rotated query rows (the G
-//        heads sharing this kv head, zero padded to 16) and B = 16 tokens x 32
-//        dims of centroid values.  A lane loads 16 contiguous code bytes of
-//        one token and unpacks them in registers through a 256-entry LDS
-//        table that maps one code byte to the fp16 pair (c[lo], c[hi]);
-//      * online softmax in the exp2 domain per head;
-//      * values: the same MFMA with A = p * n_t (fp16, via a 1 KB LDS tile)
-//        and B = 32 tokens x 16 dims of centroid values; a lane loads one code
-//        dword (8 dims) of 8 tokens and transposes the fp16 pairs in registers;
-//      * the block writes (m, l, acc[G][128]) per head to the workspace;
-//   3. combine kernel, one block of 8 waves per (batch, query head): issues
+//   1. split kernel, grid splits x kv_heads x batch, 4 waves per block, each
+//      block owning a contiguous range of cold tokens.  Its prologue rotates
+//      the G query heads of its kv head, q_rot = q @ PiK^T on fp32 MFMA
+//      (the decode step passes q_rot from its own QKV epilogue instead),
+//      while the first token blocks load.  Each wave then walks 32-token
+//      blocks with two register sets in turn (the next block's codes and
+//      norms load while the current one is computed):
+//      * scores, transposed: v_mfma_f32_16x16x32_f16 with A = 16 tokens x 32
+//        dims of centroid values and B = the rotated query (16 head
+//        columns, G used), so a lane holds one head's scores for 8 tokens.
+//        3-bit codes are decoded on the VALU with v_perm_b32 table lookups;
+//        4-bit codes through a 256-entry LDS table (byte -> fp16 pair);
+//      * online softmax in the exp2 domain, per lane, with the max taken
+//        across the 4 lanes of a head by two permlane swaps; the rescale of
+//        the accumulators runs only when some head's max grew;
+//      * values, transposed: the same MFMA with A = 16 dims x 32 tokens of
+//        centroid values (a lane's 8 tokens of one dim, transposed from the
+//        decoded code dwords with v_perm_b32) and B = p * n_t taken straight
+//        from the lane's own softmax registers (same 8 tokens);
+//      * the 4 waves merge through LDS and the block writes
+//        (m, l, acc[G][128]) per head to the workspace;
+//   2. combine kernel, one block of 8 waves per (batch, query head): issues
 //      every load it needs at once (split maxima and sums, the rotated
 //      partial sums, the fp16 hot window and the PiV column slice), then
 //      computes the hot scores, merges hot and cold softmax statistics,
@@ -45,15 +50,6 @@ constexpr int kBlk = 32;    // tokens per wave step
 constexpr int kRowB = 64;   // code bytes per token (4-bit nibbles, dim 128)
 constexpr int kHotMax = 64;
 constexpr float kLog2e = 1.4426950408889634f;
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ half8 as_half8(const u32x4& v) { return __builtin_bit_cast(half8, v); }
-
-__device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a), as_half8(b), c, 0, 0, 0);
-}
 
 __device__ __forceinline__ uint32_t pack2h(float lo, float hi) {
   return static_cast<uint32_t>(f2h(lo)) | (static_cast<uint32_t>(f2h(hi)) << 16);
@@ -77,6 +73,7 @@ struct AttnParams {
   const uint16_t* k_hot;    // [B, Hkv, hot_cap, 128]
   const uint16_t* v_hot;
   const float* PiV;         // [128, 128]
+  const float* PiK;         // non-null: the split kernel rotates q itself (qrot unused)
   const float* centroids;   // [2^bits]
   const int32_t* seq_len;
   float* partials;          // [B, Hkv, nsplit, rec]
@@ -87,100 +84,322 @@ struct AttnParams {
 
 __device__ __forceinline__ int rec_floats(int G) { return G * (2 + kD); }
 
-// Code bytes / norms of the two 16-token score tiles and the 8 value tokens
-// one lane needs for a 32-token block starting at t0.
-struct BlockRegs {
-  u32x4 kraw[2];
-  float knorm[2];
-  uint32_t vdw[8];
-  float vnorm[2];
+// Buffer resource over `bytes` bytes at base (raw addressing, stride 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// The (batch, kv head) slice of the cold store as four buffer resources.
+struct ColdRsrc {
+  __amdgpu_buffer_rsrc_t kc, vc, kn, vn;
 };
 
-// Code bytes / norms of a 32-token block starting at t0, read without any
-// condition: tokens at or past t_addr_end read token t_addr_end - 1 (valid
-// memory), so every load issues back to back; mask_block zeroes the tokens at
-// or past the valid end once it is known.
-__device__ __forceinline__ void load_block(BlockRegs& R, int t0, int t_addr_end, int lane, const uint8_t* kc,
-                                           const float* kn, const uint8_t* vc, const float* vn) {
+// Registers of one 32-token block t0 .. t0+31 (two 16-token tiles tt) for
+// lane l = 16g + w:
+//   kraw[tt]    code bytes 16g .. 16g+15 of token t0 + 16tt + w  (score operand)
+//   kn[tt][i]   key norm   of token t0 + 16tt + 4g + i
+//   vn[tt][i]   value norm of token t0 + 16tt + 4g + i
+//   vdw[4tt+i]  code dword w (dims 8w .. 8w+7) of token t0 + 16tt + 4g + i
+// The score MFMA leaves the score of token t0 + 16tt + 4g + i for head w in
+// lane l, element i of tile tt, so the softmax weights, the value norms and
+// the value codes a lane needs all belong to the same eight tokens: the value
+// MFMA takes its probability operand straight from the lane's registers.
+struct BlockRegs {
+  u32x4 kraw[2];
+  f32x4 kn[2], vn[2];
+  uint32_t vdw[8];
+};
+
+// A block entirely below the valid end.  Each load's voffset is one of two
+// lane bases; everything that depends on the block or the load is in the
+// scalar soffset (so no per-load vector address registers stay live).
+__device__ __forceinline__ void load_full(BlockRegs& R, const ColdRsrc& rs, int t0, int lane) {
+  const int g = lane >> 4, w = lane & 15;
+  const int vk = w * kRowB + 16 * g;   // key codes: token w, bytes 16g..
+  const int vv = 4 * g * kRowB + 4 * w;  // value codes: token 4g, dword w
+  const int vnrm = 16 * g;             // norms: token 4g
+  const int sc = t0 * kRowB, sn = t0 * 4;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    R.kraw[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kc, vk, sc + 16 * tt * kRowB, 0));
+    R.kn[tt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kn, vnrm, sn + 64 * tt, 0));
+    R.vn[tt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.vn, vnrm, sn + 64 * tt, 0));
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    R.vdw[j] = __builtin_amdgcn_raw_buffer_load_b32(rs.vc, vv, sc + (16 * (j >> 2) + (j & 3)) * kRowB, 0);
+}
+
+// A block reaching past t_lim: tokens at or past t_lim read token t_lim - 1
+// (valid memory); the caller masks them.
+__device__ __forceinline__ void load_clamped(BlockRegs& R, const ColdRsrc& rs, int t0, int t_lim, int lane) {
   const int g = lane >> 4, w = lane & 15;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
-    const int tok = min(t0 + 16 * tt + (lane & 15), t_addr_end - 1);
-    R.kraw[tt] = *reinterpret_cast<const u32x4*>(kc + static_cast<size_t>(tok) * kRowB + 16 * g);
-    R.knorm[tt] = kn[tok];
-    R.vnorm[tt] = vn[tok];
+    const int tk = min(t0 + 16 * tt + w, t_lim - 1);
+    R.kraw[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kc, tk * kRowB + 16 * g, 0, 0));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tn = min(t0 + 16 * tt + 4 * g + i, t_lim - 1);
+      R.kn[tt][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.kn, tn * 4, 0, 0));
+      R.vn[tt][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.vn, tn * 4, 0, 0));
+    }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int tok = min(t0 + 8 * g + i, t_addr_end - 1);
-    R.vdw[i] = *reinterpret_cast<const uint32_t*>(vc + static_cast<size_t>(tok) * kRowB + 4 * w);
+  for (int j = 0; j < 8; ++j) {
+    const int tv = min(t0 + 16 * (j >> 2) + 4 * g + (j & 3), t_lim - 1);
+    R.vdw[j] = __builtin_amdgcn_raw_buffer_load_b32(rs.vc, tv * kRowB + 4 * w, 0, 0);
   }
 }
 
-__device__ __forceinline__ void mask_block(BlockRegs& R, int t0, int t_end, int lane) {
+__device__ __forceinline__ void fetch_block(BlockRegs& R, const ColdRsrc& rs, int t0, int t_addr_end, int lane) {
+  t0 = __builtin_amdgcn_readfirstlane(t0);  // wave-uniform: keeps the token offset scalar
+  if (t0 + kBlk <= t_addr_end)
+    load_full(R, rs, t0, lane);
+  else
+    load_clamped(R, rs, t0, t_addr_end, lane);
+}
+
+// 3-bit codes decoded on the VALU: one code dword = 8 nibbles (dims 0..7)
+// becomes 4 dwords of fp16 pairs in the dim order [0,2 | 4,6 | 1,3 | 5,7].
+// tab[0..1] hold the low bytes of the 8 fp16 centroids, tab[2..3] the high
+// bytes; v_perm_b32 picks 4 of those 8 bytes per instruction (selector bytes
+// 0..7 address {S0: bytes 4-7, S1: bytes 0-3}), so a lookup is 4 nibbles per
+// instruction with no LDS traffic.  The query operand uses the same dim
+// order, so each MFMA sees the same fp16 products as with natural order.
+__device__ __forceinline__ void decode8(uint32_t w, const uint32_t (&tab)[4], uint32_t (&d)[4]) {
+  const uint32_t lo = w & 0x0F0F0F0Fu;         // codes of dims 0, 2, 4, 6 (one per byte)
+  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // dims 1, 3, 5, 7
+  const uint32_t llo = __builtin_amdgcn_perm(tab[1], tab[0], lo), hlo = __builtin_amdgcn_perm(tab[3], tab[2], lo);
+  const uint32_t lhi = __builtin_amdgcn_perm(tab[1], tab[0], hi), hhi = __builtin_amdgcn_perm(tab[3], tab[2], hi);
+  d[0] = __builtin_amdgcn_perm(hlo, llo, 0x05010400u);  // dims 0, 2
+  d[1] = __builtin_amdgcn_perm(hlo, llo, 0x07030602u);  // dims 4, 6
+  d[2] = __builtin_amdgcn_perm(hhi, lhi, 0x05010400u);  // dims 1, 3
+  d[3] = __builtin_amdgcn_perm(hhi, lhi, 0x07030602u);  // dims 5, 7
+}
+// Position p of a decoded group holds dim kPermDim[p].
+__device__ constexpr int kPermDim[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+
+// PERM: decode8 (3-bit codes).  Otherwise a 256-entry LDS table maps one
+// code byte to the fp16 pair (c[lo nibble], c[hi nibble]) in natural order.
+template <bool PERM>
+__device__ __forceinline__ void decode_dw(uint32_t w, const uint32_t (&tab)[4], const uint32_t* s_lut,
+                                          uint32_t (&d)[4]) {
+  if constexpr (PERM) {
+    decode8(w, tab, d);
+  } else {
+    d[0] = s_lut[w & 0xffu];
+    d[1] = s_lut[(w >> 8) & 0xffu];
+    d[2] = s_lut[(w >> 16) & 0xffu];
+    d[3] = s_lut[w >> 24];
+  }
+}
+// Pairs 2*half and 2*half + 1 of decode_dw (the value pass decodes in two
+// halves to halve the live registers).
+template <bool PERM>
+__device__ __forceinline__ void decode_half(uint32_t w, int half, const uint32_t (&tab)[4], const uint32_t* s_lut,
+                                            uint32_t (&d)[2]) {
+  if constexpr (PERM) {
+    const uint32_t c = (half ? (w >> 4) : w) & 0x0F0F0F0Fu;
+    const uint32_t lo = __builtin_amdgcn_perm(tab[1], tab[0], c), hi = __builtin_amdgcn_perm(tab[3], tab[2], c);
+    d[0] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+    d[1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+  } else {
+    d[0] = s_lut[(w >> (16 * half)) & 0xffu];
+    d[1] = s_lut[(w >> (16 * half + 8)) & 0xffu];
+  }
+}
+
+__device__ __forceinline__ float vmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// Max / sum over the four lanes l, l^16, l^32, l^48 (the lane groups that
+// hold the other tokens of the same head), result in all four.
+__device__ __forceinline__ float xgroup_max(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float xgroup_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Online-softmax state of one lane: head w = lane % 16, output dims
+// 32g + 8i + dim(t) in o[t][i] (dim(t) = kPermDim[t] with PERM, else t).
+struct SoftmaxState {
+  float m, l;  // running max (log2 domain) and this lane's share of the sum
+  f32x4 o[8];
+};
+
+// One 32-token block.  MASKED: tokens at or past t_end take no part.
+template <bool PERM, bool MASKED>
+__device__ __forceinline__ void attend_block(const BlockRegs& R, int t0, int t_end, const u32x4 (&qa)[4],
+                                             const uint32_t (&tab)[4], const uint32_t* s_lut, int lane,
+                                             SoftmaxState& S) {
   const int g = lane >> 4;
+  // ---- scores, transposed: A = 16 tokens x 32 dims of centroids, B = the
+  // rotated query (16 heads); lane gets head lane%16, tokens 4g+i of tile tt.
+  float s[8];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
-    const bool ok = t0 + 16 * tt + (lane & 15) < t_end;
-    R.kraw[tt] = ok ? R.kraw[tt] : u32x4{0u, 0u, 0u, 0u};
-    R.knorm[tt] = ok ? R.knorm[tt] : 0.f;
-    R.vnorm[tt] = ok ? R.vnorm[tt] : 0.f;
-  }
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) R.vdw[i] = t0 + 8 * g + i < t_end ? R.vdw[i] : 0u;
+    for (int kb = 0; kb < 4; ++kb) {
+      uint32_t dd[4];
+      decode_dw<PERM>(R.kraw[tt][kb], tab, s_lut, dd);
+      acc = mfma16x16x32(u32x4{dd[0], dd[1], dd[2], dd[3]}, qa[kb], acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = acc[i] * R.kn[tt][i];
+      s[4 * tt + i] = (!MASKED || t0 + 16 * tt + 4 * g + i < t_end) ? v : -INFINITY;
+    }
+  }
+  // ---- online softmax; the rescale runs only when some head's max grew
+  float bm = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+  bm = xgroup_max(bm);  // finite: token t0 of the block is always valid
+  const float mn = fmaxf(S.m, bm);
+  if (__builtin_amdgcn_ballot_w64(mn > S.m) != 0) {
+    const float alpha = fast_exp2(S.m - mn);  // 0 on the first block (m = -inf)
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) S.o[t][i] *= alpha;
+    S.l *= alpha;
+    S.m = mn;
+  }
+  float pv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float p = fast_exp2(s[j] - S.m);  // masked: exp2(-inf) = 0
+    S.l += p;
+    const float v = p * R.vn[j >> 2][j & 3];
+    pv[j] = (!MASKED || t0 + 16 * (j >> 2) + 4 * g + (j & 3) < t_end) ? v : 0.f;
+  }
+  const u32x4 pb = u32x4{pack2h(pv[0], pv[1]), pack2h(pv[2], pv[3]), pack2h(pv[4], pv[5]), pack2h(pv[6], pv[7])};
+  // ---- values, transposed: A = 16 dims x 32 tokens of centroids (the
+  // lane's 8 tokens of dim 8w + dim(t)), B = p * n_v (the lane's 8 tokens).
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    uint32_t r[8][2];  // r[token j][q] = fp16 pair of positions 4half+2q, 4half+2q+1 of dims 8w..8w+7
+#pragma unroll
+    for (int j = 0; j < 8; ++j) decode_half<PERM>(R.vdw[j], half, tab, s_lut, r[j]);
+#pragma unroll
+    for (int tq = 0; tq < 4; ++tq) {
+      const int t = 4 * half + tq, q = tq >> 1;
+      u32x4 a;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const uint32_t x0 = r[2 * pp][q], x1 = r[2 * pp + 1][q];
+        a[pp] = (t & 1) ? __builtin_amdgcn_perm(x1, x0, 0x07060302u) : __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+      }
+      S.o[t] = mfma16x16x32(a, pb, S.o[t]);
+    }
+  }
 }
 
-template <int GMAX>
-__global__ __launch_bounds__(kThreads, 4) void tq_attn_split_kernel(AttnParams P) {
-  __shared__ uint32_t s_lut[256];
-  __shared__ __align__(16) uint16_t s_p[kWaves][16][kBlk];  // p * n_t, fp16, per wave
-  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
-  __shared__ __align__(16) float s_o[kWaves][16][kD];  // all 16 MFMA rows: rows >= G hold zeros
+template <bool PERM>
+__device__ __forceinline__ void attend(const BlockRegs& R, int t0, int t_end, const u32x4 (&qa)[4],
+                                       const uint32_t (&tab)[4], const uint32_t* s_lut, int lane, SoftmaxState& S) {
+  if (t0 + kBlk <= t_end)
+    attend_block<PERM, false>(R, t0, t_end, qa, tab, s_lut, lane, S);
+  else
+    attend_block<PERM, true>(R, t0, t_end, qa, tab, s_lut, lane, S);
+}
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+constexpr int kORow = kD + 4;  // padded LDS row of the per-wave outputs
+#ifndef LKV_ATTN_BLOCKS_PER_CU
+#define LKV_ATTN_BLOCKS_PER_CU 2
+#endif
+// Resident split blocks per CU (one wave per SIMD each): sets the register
+// budget and the split count.
+constexpr int kSplitBlocksPerCU = LKV_ATTN_BLOCKS_PER_CU;
+
+template <bool PERM>
+__global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_kernel(AttnParams P) {
+  __shared__ uint32_t s_lut[256];
+  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+  __shared__ __align__(16) float s_o[kWaves][16][kORow];  // all 16 heads: rows >= G are never read
+
+  // wave index made wave-uniform (scalar) so block offsets become scalar soffsets
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int G = P.G;
   const size_t bh = static_cast<size_t>(b) * P.Hkv + kvh;
   float* rec = P.partials + (bh * P.nsplit + split) * rec_floats(G);
 
   // The split's token range is static; the current length only masks it.
-  // So the length load, the wave's first token block, the centroid pairs of
-  // the LUT and the rotated query are all in flight before the first wait.
+  // So the length load, the wave's first token block, the centroids and the
+  // rotated query are all in flight before the first wait.
   const int t_begin = split * P.split_tokens;
   const int t_addr_end = min(t_begin + P.split_tokens, P.cap);  // valid memory
-  const int seq_len = *P.seq_len;
-  const uint8_t* kc = P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB;
-  const uint8_t* vc = P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB;
-  const float* kn = P.k_norms + bh * static_cast<size_t>(P.cap);
-  const float* vn = P.v_norms + bh * static_cast<size_t>(P.cap);
-  BlockRegs cur;
+  const int seq_len = __builtin_amdgcn_readfirstlane(*P.seq_len);
+  ColdRsrc rs;
+  rs.kc = make_rsrc(P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB, static_cast<uint32_t>(P.cap) * kRowB);
+  rs.vc = make_rsrc(P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB, static_cast<uint32_t>(P.cap) * kRowB);
+  rs.kn = make_rsrc(P.k_norms + bh * static_cast<size_t>(P.cap), static_cast<uint32_t>(P.cap) * 4);
+  rs.vn = make_rsrc(P.v_norms + bh * static_cast<size_t>(P.cap), static_cast<uint32_t>(P.cap) * 4);
+  BlockRegs ra, rb;
   int t0 = t_begin + wave * kBlk;
-  if (t_begin < t_addr_end) load_block(cur, t0, t_addr_end, lane, kc, kn, vc, vn);
-  float c_lo, c_hi;
-  {
+  if (t0 < t_addr_end) fetch_block(ra, rs, t0, t_addr_end, lane);
+  float c_lo = 0.f, c_hi = 0.f;
+  uint32_t tab[4] = {0u, 0u, 0u, 0u};
+  if constexpr (PERM) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t c16 = f2h(P.centroids[j]);
+      tab[j >> 2] |= (c16 & 0xffu) << (8 * (j & 3));
+      tab[2 + (j >> 2)] |= (c16 >> 8) << (8 * (j & 3));
+    }
+  } else {
     const int cmax = P.ncent - 1;
     c_lo = P.centroids[min(tid & 15, cmax)];
     c_hi = P.centroids[min(tid >> 4, cmax)];
   }
-  // A operand of the score MFMA: rotated query x scale*log2(e), head
-  // h = lane%16, dims 32*(lane/16) + 8*kb + i for k-block kb.
+  // B operand of the score MFMA: rotated query x scale*log2(e), head
+  // h = lane%16, dims 32*(lane/16) + 8*kb + position (permuted with PERM).
   const int h = lane & 15, g = lane >> 4;
   u32x4 qa[4];
   {
     // rows h >= G read head G - 1 and are zeroed: unconditional loads
-    const float4* src = reinterpret_cast<const float4*>(
-        P.qrot + (static_cast<size_t>(b) * P.Hq + kvh * G + min(h, G - 1)) * kD + 32 * g);
     float4 f[8];
+    if (P.PiK != nullptr) {
+      // q_rot on MFMA (rotate_query_hilo), overlapping the first block's
+      // loads; s_o is free until the merge.
+      u32x4 qb;
+      {
+        const uint4 u = *reinterpret_cast<const uint4*>(
+            P.q + (static_cast<size_t>(b) * P.Hq + kvh * G + min(h, G - 1)) * kD + 32 * wave + 8 * g);
+        qb = h < G ? u32x4{u.x, u.y, u.z, u.w} : u32x4{0u, 0u, 0u, 0u};
+      }
+      rotate_query_hilo(P.PiK, qb, wave, lane, &s_o[0][0][0], kORow, f);
+      __syncthreads();  // s_o is written again by the merge
+    } else {
+      const float4* src = reinterpret_cast<const float4*>(
+          P.qrot + (static_cast<size_t>(b) * P.Hq + kvh * G + min(h, G - 1)) * kD + 32 * g);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = src[i];
-    s_lut[tid] = pack2h(c_lo, c_hi);
+      for (int i = 0; i < 8; ++i) f[i] = src[i];
+    }
+    if constexpr (!PERM) s_lut[tid] = pack2h(c_lo, c_hi);
     const float sl = P.scale_log2;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const float4 f0 = f[2 * kb], f1 = f[2 * kb + 1];
-      qa[kb] = h < G ? u32x4{pack2h(f0.x * sl, f0.y * sl), pack2h(f0.z * sl, f0.w * sl), pack2h(f1.x * sl, f1.y * sl),
-                             pack2h(f1.z * sl, f1.w * sl)}
-                     : u32x4{0u, 0u, 0u, 0u};
+      const float x[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+      u32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = PERM ? kPermDim[2 * j] : 2 * j, d1 = PERM ? kPermDim[2 * j + 1] : 2 * j + 1;
+        v[j] = pack2h(x[d0] * sl, x[d1] * sl);
+      }
+      qa[kb] = h < G ? v : u32x4{0u, 0u, 0u, 0u};
     }
   }
 
@@ -194,133 +413,64 @@ __global__ __launch_bounds__(kThreads, 4) void tq_attn_split_kernel(AttnParams P
     }
     return;
   }
-  mask_block(cur, t0, t_end, lane);
 
-  float m[4], l[4];
-  f32x4 o[8];
+  SoftmaxState S;
+  S.m = -INFINITY;
+  S.l = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) S.o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (!PERM) __syncthreads();  // LUT ready
+  // Two register sets in turn: the next block's loads are in flight while
+  // the current one is computed, with no register copies between them.
+  constexpr int kStep = kWaves * kBlk;
+  while (t0 < t_end) {
+    const int t1 = t0 + kStep;
+    if (t1 < t_end) fetch_block(rb, rs, t1, t_addr_end, lane);
+    attend<PERM>(ra, t0, t_end, qa, tab, s_lut, lane, S);
+    if (t1 >= t_end) break;
+    const int t2 = t1 + kStep;
+    if (t2 < t_end) fetch_block(ra, rs, t2, t_addr_end, lane);
+    attend<PERM>(rb, t1, t_end, qa, tab, s_lut, lane, S);
+    t0 = t2;
+  }
+
+  // ---- merge the 4 waves of the block through LDS.  A wave that had no
+  // block keeps m = -inf, l = 0, o = 0.
+  const float lsum = xgroup_sum(S.l);
+  if (g == 0) {
+    s_m[wave][h] = S.m;
+    s_l[wave][h] = lsum;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    m[i] = -INFINITY;
-    l[i] = 0.f;
-  }
-#pragma unroll
-  for (int t = 0; t < 8; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  __syncthreads();  // LUT ready
-  for (; t0 < t_end; t0 += kWaves * kBlk) {
-    const int tn = t0 + kWaves * kBlk;
-    BlockRegs nxt;
-    if (tn < t_end) {
-      load_block(nxt, tn, t_end, lane, kc, kn, vc, vn);
-      mask_block(nxt, tn, t_end, lane);
-    }
-    // ---- scores for tokens t0 .. t0+31 (two 16-token MFMA tiles)
-    f32x4 sc[2];
-    bool valid[2];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      valid[tt] = t0 + 16 * tt + (lane & 15) < t_end;
-      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const uint32_t w = cur.kraw[tt][kb];
-        const u32x4 bop = u32x4{s_lut[w & 0xffu], s_lut[(w >> 8) & 0xffu], s_lut[(w >> 16) & 0xffu], s_lut[w >> 24]};
-        acc = mfma16x16x32(qa[kb], bop, acc);
-      }
-      sc[tt] = acc;
-    }
-    // ---- online softmax (log2 domain); lane holds heads 4g+i, token lane%16
-    float p[2][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float s0 = valid[0] ? sc[0][i] * cur.knorm[0] : -INFINITY;
-      const float s1 = valid[1] ? sc[1][i] * cur.knorm[1] : -INFINITY;
-      const float bmax = group16_max(fmaxf(s0, s1));
-      const float mnew = fmaxf(m[i], bmax);
-      // Branch-free: while nothing is valid (mnew = -inf) exp2(-inf - 0) = 0
-      // keeps l, o and p at 0.
-      const float mref = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = fast_exp2(m[i] - mref);
-      const float p0 = valid[0] ? fast_exp2(s0 - mref) : 0.f;
-      const float p1 = valid[1] ? fast_exp2(s1 - mref) : 0.f;
-      l[i] = l[i] * alpha + group16_sum(p0 + p1);
-      m[i] = mnew;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) o[t][i] *= alpha;
-      p[0][i] = p0;
-      p[1][i] = p1;
-    }
-    // ---- p * n_t into the per-wave LDS tile [head][token]
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        s_p[wave][4 * g + i][16 * tt + (lane & 15)] = f2h(valid[tt] ? p[tt][i] * cur.vnorm[tt] : 0.f);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    // ---- P V: A = p*n (head h = lane%16, tokens 8g..8g+7), B = codes
-    u32x4 pa = u32x4{0u, 0u, 0u, 0u};
-    if (h < G) pa = *reinterpret_cast<const u32x4*>(&s_p[wave][h][8 * g]);
-    uint32_t r[8][4];  // r[token i][byte bb] = (c[dim 8w+2bb], c[dim 8w+2bb+1])
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t dw = cur.vdw[i];
-      r[i][0] = s_lut[dw & 0xffu];
-      r[i][1] = s_lut[(dw >> 8) & 0xffu];
-      r[i][2] = s_lut[(dw >> 16) & 0xffu];
-      r[i][3] = s_lut[dw >> 24];
-    }
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      // dword pp = (token 2pp, token 2pp+1) of dim 8w + t: low halves of
-      // r[..][t/2] for even t, high halves for odd t.
-      const int bb = t >> 1;
-      u32x4 bop;
-#pragma unroll
-      for (int pp = 0; pp < 4; ++pp) {
-        const uint32_t x0 = r[2 * pp][bb], x1 = r[2 * pp + 1][bb];
-        bop[pp] = (t & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
-      }
-      o[t] = mfma16x16x32(pa, bop, o[t]);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    if (tn < t_end) cur = nxt;
-  }
-
-  // ---- merge the 4 waves of the block through LDS
-  // Unconditional stores of all 16 rows (no per-row branches); the merge
-  // below reads rows < G only.
-  if ((lane & 15) == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      s_m[wave][4 * g + i] = m[i];
-      s_l[wave][4 * g + i] = l[i];
+    float4* dst = reinterpret_cast<float4*>(&s_o[wave][h][32 * g + 8 * i]);
+    if constexpr (PERM) {  // dims 0..7 sit in tiles 0, 4, 1, 5, 2, 6, 3, 7
+      dst[0] = make_float4(S.o[0][i], S.o[4][i], S.o[1][i], S.o[5][i]);
+      dst[1] = make_float4(S.o[2][i], S.o[6][i], S.o[3][i], S.o[7][i]);
+    } else {
+      dst[0] = make_float4(S.o[0][i], S.o[1][i], S.o[2][i], S.o[3][i]);
+      dst[1] = make_float4(S.o[4][i], S.o[5][i], S.o[6][i], S.o[7][i]);
     }
   }
-#pragma unroll
-  for (int t = 0; t < 8; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s_o[wave][4 * g + i][8 * (lane & 15) + t] = o[t][i];
   __syncthreads();
   for (int e = tid; e < G * kD; e += kThreads) {
     const int hh = e / kD, d = e % kD;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hh]);
-    float acc = 0.f, lsum = 0.f;
+    float acc = 0.f, ls = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
         const float wt = fast_exp2(s_m[w][hh] - M);
         acc += wt * s_o[w][hh][d];
-        lsum += wt * s_l[w][hh];
+        ls += wt * s_l[w][hh];
       }
     }
     rec[2 * G + hh * kD + d] = acc;
     if (d == 0) {
       rec[hh] = M;
-      rec[G + hh] = lsum;
+      rec[G + hh] = ls;
     }
   }
 }
@@ -344,7 +494,7 @@ __device__ __forceinline__ float dot8_f16(const uint4& a, const uint4& b) {
 // One block per (query head, batch).  Thread (d = tid % 128, quarter qd =
 // tid / 128) owns output dim d for the splits / hot tokens / PiV rows of its
 // quarter; the 4 quarters are summed through LDS in a fixed order.
-__global__ __launch_bounds__(kCombThreads) void tq_attn_combine_kernel(AttnParams P) {
+__global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnParams P) {  // 2 blocks per CU
   __shared__ float s_w[kMaxSplits];
   __shared__ float s_p[kHotMax];
   __shared__ float s_red[kCombWaves];
@@ -476,42 +626,13 @@ __global__ __launch_bounds__(kCombThreads) void tq_attn_combine_kernel(AttnParam
   }
 }
 
-// q_rot = q @ PiK^T for the G query heads of one (kv head, batch): one
-// 16-row rotation tile (rows >= G are zero), the arithmetic of tq_rotate.
-__global__ __launch_bounds__(tq::kThreads) void qrot_kernel(const uint16_t* __restrict__ q,
-                                                            const float* __restrict__ PiK,
-                                                            float* __restrict__ qrot, int Hq, int Hkv) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int kvh = blockIdx.x, b = blockIdx.y, G = Hq / Hkv;
-  float bop[2][32];
-  tq::load_pi_operand(PiK, false, wave, lane, bop);
-  const int r = lane & 15;
-  float a[32];
-  if (r < G) {
-    tq::load_row_f16(q + (static_cast<size_t>(b) * Hq + kvh * G + r) * kD + 32 * (lane >> 4), a);
-  } else {
-#pragma unroll
-    for (int s = 0; s < 32; ++s) a[s] = 0.f;
-  }
-  f32x4 acc[2];
-  tq::rotate_tile(a, bop, acc);
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * (lane >> 4) + i;
-      const int dim = 8 * (lane & 15) + 2 * wave + t;
-      if (row < G) qrot[(static_cast<size_t>(b) * Hq + kvh * G + row) * kD + dim] = acc[t][i];
-    }
-}
-
 constexpr int kSplitGran = kWaves * kBlk;  // tokens one pass of a block covers
 
 // Split count that gives ~4 blocks per CU (each wave's token loop is a
 // latency chain, so more resident waves overlap more of them), at most
 // kMaxSplits - 1.
 int64_t target_splits(int64_t B, int64_t Hkv) {
-  const int64_t target = 4 * static_cast<int64_t>(device_cu_count());
+  const int64_t target = kSplitBlocksPerCU * static_cast<int64_t>(device_cu_count());
   int64_t ns = (target + B * Hkv - 1) / (B * Hkv);
   if (ns > kMaxSplits - 1) ns = kMaxSplits - 1;
   return ns < 1 ? 1 : ns;
@@ -550,6 +671,7 @@ int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st) {
   P.k_hot = c.k_hot;
   P.v_hot = c.v_hot;
   P.PiV = c.PiV;
+  P.PiK = c.PiK;
   P.centroids = c.centroids;
   P.seq_len = c.seq_len;
   P.partials = c.partials;
@@ -566,12 +688,10 @@ int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st) {
   P.ncent = 1 << c.bits;
   const dim3 grid(static_cast<unsigned>(pl.nsplit), static_cast<unsigned>(c.Hkv), static_cast<unsigned>(c.B));
   const dim3 cgrid(static_cast<unsigned>(c.Hq), static_cast<unsigned>(c.B));
-  if (P.G <= 4)
-    hipLaunchKernelGGL((tq_attn_split_kernel<4>), grid, dim3(kThreads), 0, st, P);
-  else if (P.G <= 8)
-    hipLaunchKernelGGL((tq_attn_split_kernel<8>), grid, dim3(kThreads), 0, st, P);
+  if (c.bits == 3)
+    hipLaunchKernelGGL((tq_attn_split_kernel<true>), grid, dim3(kThreads), 0, st, P);
   else
-    hipLaunchKernelGGL((tq_attn_split_kernel<16>), grid, dim3(kThreads), 0, st, P);
+    hipLaunchKernelGGL((tq_attn_split_kernel<false>), grid, dim3(kThreads), 0, st, P);
   LKV_LAUNCH_CHECK("tq_decode_attn split");
   hipLaunchKernelGGL(tq_attn_combine_kernel, cgrid, dim3(kCombThreads), 0, st, P);
   LKV_LAUNCH_CHECK("tq_decode_attn combine");
@@ -615,12 +735,9 @@ extern "C" int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const f
               workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  float* qrot = reinterpret_cast<float*>(ws + pl.qrot_off);
-  hipLaunchKernelGGL(qrot_kernel, dim3(static_cast<unsigned>(Hkv), static_cast<unsigned>(B)), dim3(tq::kThreads), 0,
-                     st, static_cast<const uint16_t*>(q), PiK, qrot, static_cast<int>(Hq), static_cast<int>(Hkv));
-  LKV_LAUNCH_CHECK("tq_decode_attn q rotation");
   AttnCall c{};
-  c.qrot = qrot;
+  c.qrot = nullptr;
+  c.PiK = PiK;  // the split kernel rotates the query
   c.q = static_cast<const uint16_t*>(q);
   c.k_codes = k_codes;
   c.k_norms = k_norms;
