@@ -409,7 +409,7 @@ def bench_attn(args, torch):
                    "alg_bytes_per_call": alg, "sets": len(sets)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic("attn_config4"),
-                     "kernel": "q rotation + tq_attn_split_kernel + tq_attn_combine_kernel (one call)",
+                     "kernel": "tq_attn_split_kernel (q rotation in its prologue) + tq_attn_combine_kernel (one call)",
                      "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3),
                      "alg_bytes_per_launch": alg},
     }
