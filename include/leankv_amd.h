@@ -271,12 +271,25 @@ typedef struct lkv_decode_layer {
  */
 int lkv_rmsnorm(const void* x, const void* w, float eps, int64_t M, int64_t Z, void* y, void* stream);
 
-/* Workspace shared by the three calls below (no initialisation needed). */
+/* Workspace shared by the four calls below (no initialisation needed).
+ * A step is: lkv_decode_begin, lkv_decode_evict, lkv_decode_layer_step per
+ * layer, lkv_decode_head, all on one stream. */
 size_t lkv_decode_workspace_bytes(const lkv_decode_dims* dims);
 /* x = embed[tok] (embed fp16 [vocab][hidden] row-major); latches pos. */
 int lkv_decode_begin(const lkv_decode_dims* dims, const void* embed, const int64_t* tok, const int64_t* pos,
                      void* x, void* workspace, size_t workspace_bytes, void* stream);
-/* One decoder layer on the fp16 residual stream x [hidden], in place. */
+/* The token leaving every layer's hot window at the latched position
+ * (cache.py:84-141 `_flush_to_cold`: once the window exceeds hot_cap its
+ * oldest token is quantized to the cold store): for each of the n_layers
+ * layers (host array; only the cache fields and PiK / PiV are read), token
+ * pos - hot_cap is read from ring slot pos % hot_cap, quantized with the
+ * layer's rotation and written to cold slot pos - hot_cap, with the codes of
+ * lkv_tq_cache_append.  Must run after lkv_decode_begin and before the
+ * step's first lkv_decode_layer_step (which overwrites that ring slot). */
+int lkv_decode_evict(const lkv_decode_dims* dims, const lkv_decode_layer* layers, int64_t n_layers,
+                     void* workspace, size_t workspace_bytes, void* stream);
+/* One decoder layer on the fp16 residual stream x [hidden], in place; the
+ * step's new key / value enter the hot ring (eviction is lkv_decode_evict's). */
 int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_decode_layer* layer, void* x,
                           void* workspace, size_t workspace_bytes, void* stream);
 /* logits = lm_head(RMSNorm(x) * final_norm) (fp16 [vocab]); tok = argmax

@@ -51,6 +51,7 @@ SIGNATURES = {
     "lkv_rmsnorm": (_int, [_c_p, _c_p, _f32, _i64, _i64, _c_p, _c_p]),
     "lkv_decode_workspace_bytes": (_sz, [_c_p]),
     "lkv_decode_begin": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
+    "lkv_decode_evict": (_int, [_c_p, _c_p, ctypes.c_int64, _c_p, _sz, _c_p]),
     "lkv_decode_layer_step": (_int, [_c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
     "lkv_decode_head": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
 }

@@ -173,64 +173,133 @@ struct PrepArgs {
   const int32_t* state;
   uint16_t* k_hot;
   uint16_t* v_hot;
+  const float* PiK;
+  int hot_cap, Hq, Hkv;
+  uint16_t* q16;
+  float* qrot;
+};
+
+// The token leaving the hot window at this step, for up to kEvictLayers
+// layers per launch: the layer table travels as kernel arguments.
+constexpr int kEvictLayers = 32;
+struct EvictLayer {
+  const uint16_t* k_hot;
+  const uint16_t* v_hot;
   uint8_t* k_codes;
   float* k_norms;
   uint8_t* v_codes;
   float* v_norms;
   const float* PiK;
   const float* PiV;
+};
+struct EvictArgs {
+  const int32_t* state;
   const float* bounds;
-  int hot_cap, cap, Hq, Hkv;
-  uint16_t* q16;
-  float* qrot;
+  int hot_cap, cap;
+  EvictLayer L[kEvictLayers];
 };
 
-// Grid (kv heads, 3).  Block (h, 0) is the key side: RoPE of the key, the
-// key leaving the hot window quantized with PiK, the new key into the ring;
-// block (h, 1) is the value side with PiV; block (h, 2) is the query side:
-// RoPE of the G query heads (fp16 copies for the hot-window scores) and
-// q_rot = q @ PiK^T by rotate_query_hilo, the split kernel's own arithmetic,
-// so the decode step and lkv_tq_decode_attn see identical rotated queries.
-// The key/value blocks fetch their 64 KB rotation matrix first, with fully
-// coalesced 16-byte loads, and stage it in LDS for the MFMA operand reads;
-// the MFMA arithmetic is tq_common.h's, so the codes equal
-// lkv_tq_cache_append's.
+// Grid (kv heads, {key, value}, layers).  At position pos the token pos -
+// hot_cap leaves the hot window (cache.py:84-141 flushes the oldest hot token
+// once the window exceeds hot_cap): it is normalised, rotated with Pi and
+// bucketed on one 16-row MFMA tile (row 0; tq_common.h's arithmetic, so the
+// codes equal lkv_tq_cache_append's), and its codes and norm go to cold slot
+// pos - hot_cap.  Its ring slot, pos % hot_cap, is the one this step's new
+// token overwrites, so this kernel runs before the step's first layer; none
+// of the step's layer work depends on it until attention, so one launch
+// covers every layer.  The block's 64 KB rotation matrix is fetched first
+// with coalesced 16-byte loads and staged in LDS for the operand reads.
 template <int BITS>
+__global__ __launch_bounds__(kThreads) void evict_kernel(EvictArgs A) {
+  constexpr int kPiLd = kD + 1;  // padded LDS row
+  __shared__ float s_pi[kD * kPiLd];
+  __shared__ uint8_t s_codes[tq::kRows * kD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kvh = blockIdx.x;
+  const bool vside = blockIdx.y == 1;
+  const EvictLayer& Ly = A.L[blockIdx.z];
+  const int pos = A.state[0];
+  const int ev = pos - A.hot_cap;
+  if (!(pos >= A.hot_cap && ev < A.cap)) return;  // uniform: nothing leaves the window
+  const float* Pi = vside ? Ly.PiV : Ly.PiK;
+  float4 pr[kD * kD / 4 / kThreads];
+#pragma unroll
+  for (int i = 0; i < kD * kD / 4 / kThreads; ++i) pr[i] = reinterpret_cast<const float4*>(Pi)[i * kThreads + tid];
+  float bd[(1 << BITS) - 1];
+#pragma unroll
+  for (int i = 0; i < (1 << BITS) - 1; ++i) bd[i] = A.bounds[i];
+  const int r = lane & 15, c0 = 32 * (lane >> 4);
+  const int slot = pos % A.hot_cap;
+  const uint16_t* hot = vside ? Ly.v_hot : Ly.k_hot;
+  uint4 hraw[4];  // every lane loads the row's 64 bytes of its column group; rows r != 0 discard them
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    hraw[v] = reinterpret_cast<const uint4*>(hot + (static_cast<size_t>(kvh) * A.hot_cap + slot) * kD + c0)[v];
+#pragma unroll
+  for (int i = 0; i < kD * kD / 4 / kThreads; ++i) {
+    const int f = i * kThreads + tid;  // float4 index: row f / 32, columns 4 (f % 32) ..
+    float* dst = s_pi + (f >> 5) * kPiLd + 4 * (f & 31);
+    dst[0] = pr[i].x;
+    dst[1] = pr[i].y;
+    dst[2] = pr[i].z;
+    dst[3] = pr[i].w;
+  }
+  __syncthreads();
+  // tq::load_row_f16's conversion of the preloaded row; the other rows are zero
+  float a[32];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const uint32_t w[4] = {hraw[v].x, hraw[v].y, hraw[v].z, hraw[v].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[8 * v + 2 * i] = r == 0 ? h2f(static_cast<uint16_t>(w[i] & 0xffffu)) : 0.f;
+      a[8 * v + 2 * i + 1] = r == 0 ? h2f(static_cast<uint16_t>(w[i] >> 16)) : 0.f;
+    }
+  }
+  float bop[2][32];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const float* row = s_pi + (8 * (lane & 15) + 2 * wave + t) * kPiLd + c0;
+#pragma unroll
+    for (int s = 0; s < 32; ++s) bop[t][s] = row[s];
+  }
+  // cache.py:141 quantizes flush_k.float(): fp32 semantics on the fp16 data.
+  const float nrm = tq::normalize_row_f32_if(a, r == 0);
+  f32x4 acc[2];
+  tq::rotate_tile(a, bop, acc);
+  tq::codes_to_lds<BITS>(acc, bd, wave, lane, s_codes);
+  if (tid == 0) (vside ? Ly.v_norms : Ly.k_norms)[static_cast<size_t>(kvh) * A.cap + ev] = nrm;
+  __syncthreads();
+  const int64_t roff = (static_cast<int64_t>(kvh) * A.cap + ev) * tq::row_bytes_for(BITS);
+  tq::pack_store<BITS>(s_codes, vside ? Ly.v_codes : Ly.k_codes, 0, 1, [=](int64_t) { return roff; });
+}
+
+
+// Grid (kv heads, 3).  Block (h, 0) is the key side: RoPE of the key and
+// the new key into its ring slot; block (h, 1) the value side; block (h, 2)
+// the query side: RoPE of the G query heads (fp16 copies for the hot-window
+// scores) and q_rot = q @ PiK^T by rotate_query_hilo, the split kernel's own
+// arithmetic, so the decode step and lkv_tq_decode_attn see identical rotated
+// queries.  The token leaving the hot window was quantized by evict_kernel
+// at the start of the step.
 __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
   constexpr int kCols = kMaxG * kD / kThreads;  // projected columns per thread (query side at most)
-  constexpr int kPiLd = kD + 1;                 // padded LDS row
-  constexpr int kPartLd = kD + 4;               // query side: rotate_query_hilo partials in s_pi
-  static_assert(4 * 16 * kPartLd <= kD * kPiLd, "query partials fit in s_pi");
-  __shared__ __align__(16) float s_pi[kD * kPiLd];
+  constexpr int kPartLd = kD + 4;               // rotate_query_hilo partial rows
+  __shared__ __align__(16) float s_part[4 * 16 * kPartLd];
   __shared__ float s_raw[kMaxG][kD];   // query side: the G heads; key / value side: row 0
   __shared__ float s_rope[kMaxG][kD];  // after RoPE (query and key sides)
-  __shared__ uint8_t s_codes[tq::kRows * kD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kvh = blockIdx.x;
   const int side = blockIdx.y;  // 0 key, 1 value, 2 query
   const bool vside = side == 1, qside = side == 2;
   const int G = A.Hq / A.Hkv;
   const int ncol = (qside ? G : 1) * kD;  // projected columns this block needs
-  const int nc = A.nchunk;
-  const float* Pi = vside ? A.PiV : A.PiK;
 
-  // ---- 0. loads, in this order, all in flight before the first wait: the
-  //      position, the rotation matrix (key / value side: 16 coalesced float4
-  //      per thread), the decision boundaries, the first 16 chunks of the
-  //      projection partial sums, then what depends on the position -- the
-  //      row leaving the hot window (row 0 of the MFMA tile: lanes r == 0
-  //      use it, the others load the same 64 bytes) and this position's
+  // ---- 0. loads, all in flight before the first wait: the position, the
+  //      first 16 chunks of the projection partial sums, this position's
   //      RoPE row.
   const int pos = A.state[0];
-  float4 pr[kD * kD / 4 / kThreads];
-  float bd[(1 << BITS) - 1];
-  if (!qside) {
-#pragma unroll
-    for (int i = 0; i < kD * kD / 4 / kThreads; ++i) pr[i] = reinterpret_cast<const float4*>(Pi)[i * kThreads + tid];
-#pragma unroll
-    for (int i = 0; i < (1 << BITS) - 1; ++i) bd[i] = A.bounds[i];
-  }
-
+  const int nc = A.nchunk;
   // Projections, summed over chunks in chunk order, rounded to fp16.  A
   // wave's 64 columns never straddle a 128-column head, so validity is
   // uniform per wave (scalar branches).
@@ -256,18 +325,6 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
 #pragma unroll
       for (int i = 0; i < kFirst; ++i) v0[e][i] = src[e][static_cast<size_t>(min(i, nc - 1)) * kGemvBN];
     }
-
-  const int slot = pos % A.hot_cap;
-  const int ev = pos - A.hot_cap;
-  const bool evict = !qside && pos >= A.hot_cap && ev < A.cap;
-  const int r = lane & 15, c0 = 32 * (lane >> 4);
-  const size_t hrow = (static_cast<size_t>(kvh) * A.hot_cap + slot) * kD;
-  uint16_t* hot = vside ? A.v_hot : A.k_hot;
-  uint4 hraw[4];
-  if (!qside) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) hraw[v] = reinterpret_cast<const uint4*>(hot + hrow + c0)[v];
-  }
   const uint16_t cs_d = A.cos[static_cast<size_t>(pos) * kD + (tid & (kD - 1))];
   const uint16_t sn_d = A.sin[static_cast<size_t>(pos) * kD + (tid & (kD - 1))];
 
@@ -298,17 +355,6 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
     const int c = e * kThreads + tid;
     if (ok[e]) s_raw[c / kD][c % kD] = h2f(f2h(psum[e]));
   }
-  if (!qside) {
-#pragma unroll
-    for (int i = 0; i < kD * kD / 4 / kThreads; ++i) {
-      const int f = i * kThreads + tid;  // float4 index: row f / 32, columns 4 (f % 32) ..
-      float* dst = s_pi + (f >> 5) * kPiLd + 4 * (f & 31);
-      dst[0] = pr[i].x;
-      dst[1] = pr[i].y;
-      dst[2] = pr[i].z;
-      dst[3] = pr[i].w;
-    }
-  }
   __syncthreads();
 
   // ---- 2. RoPE: x*cos + rotate_half(x)*sin with fp16 products and sum
@@ -327,7 +373,7 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
   }
 
   if (qside) {
-    // ---- 3q. the rotated query heads (s_pi holds the partials)
+    // ---- 3. the rotated query heads
     const int h = lane & 15, g = lane >> 4;
     u32x4 qb = u32x4{0u, 0u, 0u, 0u};
     if (h < G) {
@@ -337,7 +383,7 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
         qb[j] = static_cast<uint32_t>(f2h(q[2 * j])) | (static_cast<uint32_t>(f2h(q[2 * j + 1])) << 16);
     }
     float4 out[8];
-    rotate_query_hilo(A.PiK, qb, wave, lane, s_pi, kPartLd, out);
+    rotate_query_hilo(A.PiK, qb, wave, lane, s_part, kPartLd, out);
     if (h < G) {
       float4* dst = reinterpret_cast<float4*>(A.qrot + static_cast<size_t>(kvh * G + h) * kD + 32 * g);
 #pragma unroll
@@ -345,41 +391,10 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
     }
     return;
   }
-
-  // ---- 3. one 16-row tile: row 0 = the vector leaving the hot window
-  //      (normalised), the other rows zero
-  float a[32];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const uint32_t w[4] = {hraw[v].x, hraw[v].y, hraw[v].z, hraw[v].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      a[8 * v + 2 * i] = (evict && r == 0) ? h2f(static_cast<uint16_t>(w[i] & 0xffffu)) : 0.f;
-      a[8 * v + 2 * i + 1] = (evict && r == 0) ? h2f(static_cast<uint16_t>(w[i] >> 16)) : 0.f;
-    }
-  }
-  float bop[2][32];
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const float* row = s_pi + (8 * (lane & 15) + 2 * wave + t) * kPiLd + c0;
-#pragma unroll
-    for (int s = 0; s < 32; ++s) bop[t][s] = row[s];
-  }
-  // cache.py:141 quantizes flush_k.float(): fp32 semantics on the fp16 data.
-  const float nrm = tq::normalize_row_f32_if(a, r == 0);
-  f32x4 acc[2];
-  tq::rotate_tile(a, bop, acc);
-  if (evict) {
-    tq::codes_to_lds<BITS>(acc, bd, wave, lane, s_codes);
-    if (tid == 0) (vside ? A.v_norms : A.k_norms)[static_cast<size_t>(kvh) * A.cap + ev] = nrm;
-  }
-  __syncthreads();  // codes staged; every read of the old hot slot is done
-  if (evict) {
-    const int64_t roff = (static_cast<int64_t>(kvh) * A.cap + ev) * tq::row_bytes_for(BITS);
-    tq::pack_store<BITS>(s_codes, vside ? A.v_codes : A.k_codes, 0, 1, [=](int64_t) { return roff; });
-  }
-  // ---- 4. the new token into its ring slot
-  if (tid < kD) hot[hrow + tid] = f2h(vside ? s_raw[0][tid] : s_rope[0][tid]);
+  // ---- 3. the new token into its ring slot (evict_kernel has read the old one)
+  uint16_t* hot = vside ? A.v_hot : A.k_hot;
+  if (tid < kD)
+    hot[(static_cast<size_t>(kvh) * A.hot_cap + pos % A.hot_cap) * kD + tid] = f2h(vside ? s_raw[0][tid] : s_rope[0][tid]);
 }
 
 struct Cand {
@@ -474,6 +489,47 @@ extern "C" int lkv_decode_begin(const lkv_decode_dims* dims, const void* embed, 
   return LKV_OK;
 }
 
+extern "C" int lkv_decode_evict(const lkv_decode_dims* dims, const lkv_decode_layer* layers, int64_t n_layers,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  if (int e = check_dims(dims)) return e;
+  const lkv_decode_dims& d = *dims;
+  const Plan p = make_plan(d);
+  if (int e = check_ws(p, workspace, workspace_bytes)) return e;
+  LKV_REQUIRE(layers && n_layers >= 0, "decode_evict: null layer table or negative count");
+  for (int64_t l = 0; l < n_layers; ++l) {
+    const lkv_decode_layer& L = layers[l];
+    LKV_REQUIRE(L.k_codes && L.k_norms && L.v_codes && L.v_norms && L.k_hot && L.v_hot && L.PiK && L.PiV,
+                "decode_evict: null cache pointer in layer %lld", (long long)l);
+    LKV_REQUIRE(aligned16(L.k_codes) && aligned16(L.v_codes) && aligned16(L.k_hot) && aligned16(L.v_hot) &&
+                    aligned16(L.PiK) && aligned16(L.PiV),
+                "decode_evict: cache buffers and rotations of layer %lld must be 16-byte aligned", (long long)l);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  for (int64_t l0 = 0; l0 < n_layers; l0 += kEvictLayers) {
+    const int nl = static_cast<int>(n_layers - l0 < kEvictLayers ? n_layers - l0 : kEvictLayers);
+    EvictArgs A{};
+    A.state = reinterpret_cast<const int32_t*>(ws + p.off_state);
+    A.bounds = d.bounds;
+    A.hot_cap = static_cast<int>(d.hot_cap);
+    A.cap = static_cast<int>(d.cap);
+    for (int i = 0; i < nl; ++i) {
+      const lkv_decode_layer& L = layers[l0 + i];
+      A.L[i] = EvictLayer{static_cast<const uint16_t*>(L.k_hot), static_cast<const uint16_t*>(L.v_hot),
+                          static_cast<uint8_t*>(L.k_codes),      static_cast<float*>(L.k_norms),
+                          static_cast<uint8_t*>(L.v_codes),      static_cast<float*>(L.v_norms),
+                          L.PiK,                                 L.PiV};
+    }
+    const dim3 grid(static_cast<unsigned>(p.Hkv), 2, static_cast<unsigned>(nl));
+    if (d.bits == 3)
+      hipLaunchKernelGGL((evict_kernel<3>), grid, dim3(kThreads), 0, st, A);
+    else
+      hipLaunchKernelGGL((evict_kernel<4>), grid, dim3(kThreads), 0, st, A);
+    LKV_LAUNCH_CHECK("decode_evict");
+  }
+  return LKV_OK;
+}
+
 extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_decode_layer* L, void* x, void* workspace,
                                      size_t workspace_bytes, void* stream) {
   if (int e = check_dims(dims)) return e;
@@ -536,23 +592,13 @@ extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_deco
     A.state = state;
     A.k_hot = static_cast<uint16_t*>(L->k_hot);
     A.v_hot = static_cast<uint16_t*>(L->v_hot);
-    A.k_codes = static_cast<uint8_t*>(L->k_codes);
-    A.k_norms = static_cast<float*>(L->k_norms);
-    A.v_codes = static_cast<uint8_t*>(L->v_codes);
-    A.v_norms = static_cast<float*>(L->v_norms);
     A.PiK = L->PiK;
-    A.PiV = L->PiV;
-    A.bounds = d.bounds;
     A.hot_cap = static_cast<int>(d.hot_cap);
-    A.cap = static_cast<int>(d.cap);
     A.Hq = static_cast<int>(p.Hq);
     A.Hkv = static_cast<int>(p.Hkv);
     A.q16 = reinterpret_cast<uint16_t*>(ws + p.off_q16);
     A.qrot = reinterpret_cast<float*>(ws + p.off_qrot);
-    if (d.bits == 3)
-      hipLaunchKernelGGL((prep_kernel<3>), dim3(static_cast<unsigned>(p.Hkv), 3), dim3(kThreads), 0, st, A);
-    else
-      hipLaunchKernelGGL((prep_kernel<4>), dim3(static_cast<unsigned>(p.Hkv), 3), dim3(kThreads), 0, st, A);
+    hipLaunchKernelGGL(prep_kernel, dim3(static_cast<unsigned>(p.Hkv), 3), dim3(kThreads), 0, st, A);
     LKV_LAUNCH_CHECK("decode prep");
   }
   // 3-4. attention

@@ -113,10 +113,11 @@ class _Base:
 class LeanKVEngine(_Base):
     """TEAL sparse projections + TurboQuant packed KV through the fused C decode step.
 
-    Per token: lkv_decode_begin, lkv_decode_layer_step per layer (9 kernels:
-    q|k|v GEMV with the RMSNorm prologue, RoPE/append/q-rotation epilogue,
-    attention split + combine, o_proj, residual, gate|up GEMV with the
-    RMSNorm prologue, down GEMV with the SwiGLU prologue, residual) and
+    Per token: lkv_decode_begin, lkv_decode_evict (the token leaving every
+    layer's hot window, one launch), lkv_decode_layer_step per layer (9
+    kernels: q|k|v GEMV with the RMSNorm prologue, RoPE/append/q-rotation
+    epilogue, attention split + combine, o_proj, residual, gate|up GEMV with
+    the RMSNorm prologue, down GEMV with the SwiGLU prologue, residual) and
     lkv_decode_head (lm_head GEMV, logits, argmax), captured into one graph.
 
     Projections patched by apply_teal already hold their weight column-major
@@ -163,6 +164,7 @@ class LeanKVEngine(_Base):
                 v_codes=self._hold(cache._v_codes[i]), v_norms=self._hold(cache._v_norms[i]),
                 k_hot=self._hold(cache._k_hot[i]), v_hot=self._hold(cache._v_hot[i]),
                 PiK=self._hold(cache.PiK[i].contiguous()), PiV=self._hold(cache.PiV[i].contiguous())))
+        self.layer_table = (_lib.DecodeLayer * len(self.layer_structs))(*self.layer_structs)
         self.final_norm = model.model.norm.weight.detach()
         self.lm_head_cm = model.lm_head.weight.detach().t().contiguous()  # [hidden][vocab]
         nbytes = lib.lkv_decode_workspace_bytes(ctypes.byref(self.dims))
@@ -189,6 +191,8 @@ class LeanKVEngine(_Base):
         dims = ctypes.byref(self.dims)
         _lib.check(lib.lkv_decode_begin(dims, self.model.model.embed_tokens.weight.data_ptr(), self.tok.data_ptr(),
                                         self.pos64.data_ptr(), self.x.data_ptr(), ws, nb, st), "lkv_decode_begin")
+        _lib.check(lib.lkv_decode_evict(dims, self.layer_table, len(self.layer_structs), ws, nb, st),
+                   "lkv_decode_evict")
         for ls in self.layer_structs:
             _lib.check(lib.lkv_decode_layer_step(dims, ctypes.byref(ls), self.x.data_ptr(), ws, nb, st),
                        "lkv_decode_layer_step")

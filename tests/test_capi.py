@@ -132,3 +132,10 @@ def test_decode_dims_validated_without_launch():
     assert lib.lkv_decode_begin(ctypes.byref(ok), p, p, p, p, p, 1024, None) == -1
     assert "workspace" in _lib.last_error()
     assert lib.lkv_decode_layer_step(ctypes.byref(ok), None, p, p, 1 << 30, None) == -1
+    # eviction: null table, and a layer with a null cache pointer, are rejected before any launch
+    assert lib.lkv_decode_evict(ctypes.byref(ok), None, 1, p, 1 << 30, None) == -1
+    layers = (_lib.DecodeLayer * 2)()
+    assert lib.lkv_decode_evict(ctypes.byref(ok), layers, 2, p, 1 << 30, None) == -1
+    assert "layer 0" in _lib.last_error()
+    assert lib.lkv_decode_evict(ctypes.byref(ok), layers, 2, p, 1024, None) == -1
+    assert "workspace" in _lib.last_error()
