@@ -18,6 +18,122 @@ using namespace tq;
 enum Mode { kQuant = 0, kRotate = 1, kDequant = 2, kAppend = 3 };
 
 // ---------------------------------------------------------------- quantize
+// Nibble layouts (3- and 4-bit codes): one wave owns a whole 16-vector tile
+// and computes all 8 output column tiles, so each vector is loaded and
+// normalised once (the 4-wave kernel below repeats both in every wave).
+// Column tile c holds output dims 8n + c (n = lane % 16): exactly nibble c
+// of packed dword n, so a lane packs the dwords of its 4 rows in registers
+// and stores them directly.  Each output's MFMA chain -- the same 32 k-steps
+// with the same operands in the same order as rotate_tile -- is unchanged,
+// so the codes equal every other quantizing kernel's bit for bit.  The B
+// operands of the 8 tiles are staged once per block in LDS in MFMA operand
+// order: s_b[c][kq][lane] = Pi[8n + c][32q + 4kq .. +3] for lane = 16q + n.
+// #(b < y) over the 2^BITS - 1 sorted decision boundaries by binary search
+// (BITS compares instead of 2^BITS - 1): the same count as bucket<BITS>.
+// Every boundary index is a compile-time constant (selects, no indexing).
+template <int BITS>
+__device__ __forceinline__ int bucket_bsearch(float y, const float (&bd)[(1 << BITS) - 1]) {
+  static_assert(BITS == 3 || BITS == 4, "nibble layouts");
+  if constexpr (BITS == 3) {
+    const bool h2 = bd[3] < y;
+    const bool h1 = (h2 ? bd[5] : bd[1]) < y;
+    const float t0 = h2 ? (h1 ? bd[6] : bd[4]) : (h1 ? bd[2] : bd[0]);
+    return (h2 ? 4 : 0) + (h1 ? 2 : 0) + (t0 < y ? 1 : 0);
+  } else {
+    const bool h3 = bd[7] < y;
+    const bool h2 = (h3 ? bd[11] : bd[3]) < y;
+    const float t1 = h3 ? (h2 ? bd[13] : bd[9]) : (h2 ? bd[5] : bd[1]);
+    const bool h1 = t1 < y;
+    const float t0 = h3 ? (h2 ? (h1 ? bd[14] : bd[12]) : (h1 ? bd[10] : bd[8]))
+                        : (h2 ? (h1 ? bd[6] : bd[4]) : (h1 ? bd[2] : bd[0]));
+    return (h3 ? 8 : 0) + (h2 ? 4 : 0) + (h1 ? 2 : 0) + (t0 < y ? 1 : 0);
+  }
+}
+
+template <int BITS, bool F16>
+__global__ __launch_bounds__(kThreads, 2) void quantize_wave_kernel(const void* __restrict__ xin, int64_t M,
+                                                                    const float* __restrict__ Pi,
+                                                                    const float* __restrict__ bounds,
+                                                                    uint8_t* __restrict__ packed,
+                                                                    void* __restrict__ norms) {
+  static_assert(pack_bits(BITS) == 4 && row_bytes_for(BITS) == 64, "nibble layouts only");
+  __shared__ float4 s_b[8][8][64];  // 64 KB
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int64_t ntiles = (M + kRows - 1) / kRows;
+  int64_t tile = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  // The first tile's vectors load while the rotation matrix is staged.
+  float a[32];
+  auto load_a = [&](int64_t tl) {
+    const int64_t r = tl * kRows + n;
+    const int64_t rl = r < M ? r : M - 1;  // rows past M read row M - 1 and are zeroed after
+    if (F16)
+      load_row_f16(static_cast<const uint16_t*>(xin) + rl * kD + 32 * g, a);
+    else
+      load_row_f32(static_cast<const float*>(xin) + rl * kD + 32 * g, a);
+  };
+  if (tile < ntiles) load_a(tile);
+  // Pi, coalesced: thread tid holds float4 f = 256 i + tid (row f / 32, columns
+  // 4 (f % 32) ..), written to its operand slot.
+  float4 pr[kD * kD / 4 / kThreads];
+#pragma unroll
+  for (int i = 0; i < kD * kD / 4 / kThreads; ++i) pr[i] = reinterpret_cast<const float4*>(Pi)[i * kThreads + threadIdx.x];
+  float bd[(1 << BITS) - 1];
+#pragma unroll
+  for (int i = 0; i < (1 << BITS) - 1; ++i) bd[i] = bounds[i];
+#pragma unroll
+  for (int i = 0; i < kD * kD / 4 / kThreads; ++i) {
+    const int f = i * kThreads + threadIdx.x;
+    const int j = f >> 5, c4 = f & 31;  // Pi row j = 8n' + c, columns 32q' + 4kq ..
+    s_b[j & 7][c4 & 7][16 * (c4 >> 3) + (j >> 3)] = pr[i];
+  }
+  __syncthreads();
+  for (; tile < ntiles; tile += static_cast<int64_t>(gridDim.x) * 4) {
+    const int64_t row0 = tile * kRows;
+    const int64_t r = row0 + n;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) a[k] = r < M ? a[k] : 0.f;
+    const float nrm = normalize_row<F16>(a);
+    if (g == 0 && r < M) {
+      if (F16)
+        static_cast<uint16_t*>(norms)[r] = f2h(nrm);
+      else
+        static_cast<float*>(norms)[r] = nrm;
+    }
+    f32x4 acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kq = 0; kq < 8; ++kq) {
+      float4 bv[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) bv[c] = s_b[c][kq][lane];
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        const float av = a[4 * kq + cc];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float b = cc == 0 ? bv[c].x : cc == 1 ? bv[c].y : cc == 2 ? bv[c].z : bv[c].w;
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b, acc[c], 0, 0, 0);
+        }
+      }
+      // keeps the next k-quarter's LDS reads after these MFMAs (the compiler
+      // otherwise hoists all 256 operand values and spills)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const int64_t next = tile + static_cast<int64_t>(gridDim.x) * 4;
+    if (next < ntiles) load_a(next);  // in flight during the bucketing and stores
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = row0 + 4 * g + i;
+      uint32_t v = 0;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) v |= static_cast<uint32_t>(bucket_bsearch<BITS>(acc[c][i], bd)) << (4 * c);
+      if (row < M) *reinterpret_cast<uint32_t*>(packed + row * 64 + 4 * n) = v;
+    }
+  }
+}
+
 template <int BITS, bool F16>
 __global__ __launch_bounds__(kThreads) void quantize_kernel(const void* __restrict__ xin, int64_t M,
                                                             const float* __restrict__ Pi,
@@ -281,6 +397,24 @@ extern "C" int lkv_tq_quantize(const void* x, int x_dtype, int64_t M, const floa
   LKV_REQUIRE(aligned16(x) && aligned16(Pi) && aligned4(packed),
               "tq_quantize: x and Pi must be 16-byte aligned, packed 4-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (bits >= 3) {  // nibble layouts: one wave per 16-vector tile
+    const int64_t ntiles = (M + kRows - 1) / kRows;
+    const int64_t cap = 2 * static_cast<int64_t>(device_cu_count());  // 64 KB of LDS: 2 blocks per CU
+    const int gw = static_cast<int>(std::min<int64_t>((ntiles + 3) / 4, cap));
+    if (x_dtype == LKV_DTYPE_F16) {
+      if (bits == 3)
+        hipLaunchKernelGGL((quantize_wave_kernel<3, true>), dim3(gw), dim3(kThreads), 0, st, x, M, Pi, bounds, packed, norms);
+      else
+        hipLaunchKernelGGL((quantize_wave_kernel<4, true>), dim3(gw), dim3(kThreads), 0, st, x, M, Pi, bounds, packed, norms);
+    } else {
+      if (bits == 3)
+        hipLaunchKernelGGL((quantize_wave_kernel<3, false>), dim3(gw), dim3(kThreads), 0, st, x, M, Pi, bounds, packed, norms);
+      else
+        hipLaunchKernelGGL((quantize_wave_kernel<4, false>), dim3(gw), dim3(kThreads), 0, st, x, M, Pi, bounds, packed, norms);
+    }
+    LKV_LAUNCH_CHECK("tq_quantize");
+    return LKV_OK;
+  }
   const int g = grid_for(M);
   if (x_dtype == LKV_DTYPE_F16) {
     LKV_BITS_SWITCH(bits, hipLaunchKernelGGL((quantize_kernel<B_, true>), dim3(g), dim3(kThreads), 0, st,
