@@ -321,6 +321,12 @@ def test_tq_cache_append_matches_reference_cache(cuda):
         y64 = oq.rotated_fp64(src[:, :, :ncold].float(), Pi)
         _codes_match(got[:, :, :ncold].cpu().numpy(), want, y64, b, 3)
         torch.testing.assert_close(nrm_g[:, :, :ncold].cpu(), nrm_w.float(), rtol=2e-6, atol=0)
+    # the bulk quantizer (one wave per 16-vector tile) gives the append path's
+    # codes and norms bit for bit: both run the same per-output MFMA chain
+    for got, nrm_g, Pi, src in ((kc, kn, PiKd, allk), (vc, vn, PiVd, allv)):
+        pq, nq = kernels.tq_quantize(src[:, :, :ncold].float().contiguous().to(cuda), Pi, bd, 3)
+        assert torch.equal(pq, got[:, :, :ncold])
+        assert torch.equal(nq, nrm_g[:, :, :ncold])
     # rows beyond the cold length were never written
     assert int(kc[:, :, ncold:].count_nonzero()) == 0
     # hot ring holds the last `hot` tokens at slot p % hot
