@@ -391,3 +391,13 @@ def test_decode_attn_edges(cuda, B, Hq, Hkv, L, hot):
     out, ref = _attn_case(B, Hq, Hkv, L, hot, seed=L, dev=cuda)
     assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
     assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
+
+
+# Large batches (many (batch, kv head) pairs, few splits each): hot-only,
+# boundary and short cold ranges, a 16-token window, 16 query heads per kv head.
+@pytest.mark.parametrize("B,Hq,Hkv,L,hot", [(16, 32, 8, 1, 64), (16, 32, 8, 65, 64), (16, 32, 8, 700, 64),
+                                            (32, 16, 4, 333, 16), (16, 128, 8, 300, 64), (64, 8, 2, 200, 64)])
+def test_decode_attn_large_batch(cuda, B, Hq, Hkv, L, hot):
+    out, ref = _attn_case(B, Hq, Hkv, L, hot, seed=L + B, dev=cuda)
+    assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
+    assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
