@@ -37,6 +37,8 @@
 //      partial sums, the fp16 hot window and the PiV column slice), then
 //      computes the hot scores, merges hot and cold softmax statistics,
 //      applies PiV to the cold sum, adds the hot sum, normalises, writes fp16.
+#include <stdlib.h>
+
 #include "kernels.h"
 #include "tq_common.h"
 
@@ -631,8 +633,48 @@ constexpr int kSplitGran = kWaves * kBlk;  // tokens one pass of a block covers
 // Split count that gives ~4 blocks per CU (each wave's token loop is a
 // latency chain, so more resident waves overlap more of them), at most
 // kMaxSplits - 1.
+// Tuning knobs, read once.  LKV_ATTN_SPLIT_TARGET=k: aim for k split blocks
+// per CU (default: the resident count, kSplitBlocksPerCU).  LKV_ATTN_QROT=kernel:
+// lkv_tq_decode_attn rotates the query in its own launch instead of in every
+// split block's prologue.
+int attn_split_target() {
+  static const int k = [] {
+    const char* env = getenv("LKV_ATTN_SPLIT_TARGET");
+    const int v = env ? atoi(env) : 0;
+    return v > 0 && v <= 16 ? v : kSplitBlocksPerCU;
+  }();
+  return k;
+}
+bool attn_qrot_kernel() {
+  static const bool k = [] {
+    const char* env = getenv("LKV_ATTN_QROT");
+    return env && env[0] == 'k';
+  }();
+  return k;
+}
+
+// q_rot = q @ PiK^T in a launch of its own: one 4-wave block per (kv head, batch).
+__global__ __launch_bounds__(kThreads) void qrot_hilo_kernel(const uint16_t* __restrict__ q,
+                                                             const float* __restrict__ PiK, float* __restrict__ qrot,
+                                                             int Hq, int Hkv) {
+  __shared__ __align__(16) float s_part[4 * 16 * kORow];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kvh = blockIdx.x, b = blockIdx.y, G = Hq / Hkv;
+  const int h = lane & 15, g = lane >> 4;
+  const uint4 u = *reinterpret_cast<const uint4*>(q + (static_cast<size_t>(b) * Hq + kvh * G + min(h, G - 1)) * kD +
+                                                  32 * wave + 8 * g);
+  const u32x4 qb = h < G ? u32x4{u.x, u.y, u.z, u.w} : u32x4{0u, 0u, 0u, 0u};
+  float4 out[8];
+  rotate_query_hilo(PiK, qb, wave, lane, s_part, kORow, out);
+  if (h < G && wave == 0) {
+    float4* dst = reinterpret_cast<float4*>(qrot + (static_cast<size_t>(b) * Hq + kvh * G + h) * kD + 32 * g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = out[i];
+  }
+}
+
 int64_t target_splits(int64_t B, int64_t Hkv) {
-  const int64_t target = kSplitBlocksPerCU * static_cast<int64_t>(device_cu_count());
+  const int64_t target = attn_split_target() * static_cast<int64_t>(device_cu_count());
   int64_t ns = (target + B * Hkv - 1) / (B * Hkv);
   if (ns > kMaxSplits - 1) ns = kMaxSplits - 1;
   return ns < 1 ? 1 : ns;
@@ -736,8 +778,17 @@ extern "C" int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const f
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   AttnCall c{};
-  c.qrot = nullptr;
-  c.PiK = PiK;  // the split kernel rotates the query
+  if (attn_qrot_kernel()) {
+    float* qr = reinterpret_cast<float*>(ws + pl.qrot_off);
+    hipLaunchKernelGGL(qrot_hilo_kernel, dim3(static_cast<unsigned>(Hkv), static_cast<unsigned>(B)), dim3(kThreads), 0,
+                       st, static_cast<const uint16_t*>(q), PiK, qr, static_cast<int>(Hq), static_cast<int>(Hkv));
+    LKV_LAUNCH_CHECK("tq_decode_attn q rotation");
+    c.qrot = qr;
+    c.PiK = nullptr;
+  } else {
+    c.qrot = nullptr;
+    c.PiK = PiK;  // the split kernel rotates the query
+  }
   c.q = static_cast<const uint16_t*>(q);
   c.k_codes = k_codes;
   c.k_norms = k_norms;
