@@ -360,7 +360,7 @@ def bench_quant(args, torch):
                    "rotation_flop_per_step": flops, "sets": len(sets)},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "quantize_kernel<3,true> (K and V launches)", "kernel_us_mean": round(kmean * 1e3, 3),
+                     "kernel": "quantize_wave_kernel<3,true> (K and V launches)", "kernel_us_mean": round(kmean * 1e3, 3),
                      "kernel_us_median": round(kmed * 1e3, 3), "hbm_GBps": round(alg_bytes / (kmean * 1e-3) / 1e9, 1)},
     }
 
