@@ -202,16 +202,18 @@ int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const float* k_nor
  * (leankv/teal/patching.py:152-183), keys/values going through
  * TurboQuantCache.update (leankv/turboquant/cache.py:84-189) and attention
  * over its output; then the final RMSNorm, the dense lm_head and argmax of
- * scripts/benchmark.py's greedy loop.  Per layer (9 launches):
+ * scripts/benchmark.py's greedy loop.  Per step, before the layers,
+ * lkv_decode_evict quantizes the token leaving every layer's hot window
+ * (lkv_tq_cache_append arithmetic).  Per layer (8 launches):
  *   1. q/k/v GEMV, RMSNorm(x) computed in the prologue;
- *   2. q/k/v epilogue: reduce partials, RoPE, quantize the token leaving the
- *      hot window (lkv_tq_cache_append arithmetic), write the new token to the
- *      hot ring, rotate q (lkv_tq_rotate arithmetic);
- *   3-4. packed-KV attention split + combine (lkv_tq_decode_attn kernels);
- *   5. o_proj GEMV;  6. x += o (fp16 residual);
- *   7. gate/up GEMV, RMSNorm(x) in the prologue;
- *   8. down GEMV, SwiGLU of the gate/up partials in the prologue;
- *   9. x += down.
+ *   2-3. packed-KV attention split + combine (lkv_tq_decode_attn kernels);
+ *      the split kernel's prologue reduces the q/k/v partials, applies RoPE,
+ *      rotates q (the arithmetic of lkv_tq_decode_attn's own rotation) and
+ *      writes the new token's key and value to the hot ring;
+ *   4. o_proj GEMV;  5. x += o (fp16 residual);
+ *   6. gate/up GEMV, RMSNorm(x) in the prologue;
+ *   7. down GEMV, SwiGLU of the gate/up partials in the prologue;
+ *   8. x += down.
  * Rounding follows the fp16 HF modules: projections, RMSNorm output, RoPE
  * products and sums, SwiGLU and residual adds are rounded to fp16 where HF
  * stores fp16 tensors.  A threshold of 0 keeps every nonzero input (dense).

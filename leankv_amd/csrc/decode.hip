@@ -1,4 +1,4 @@
-// Fused B=1 decode step: 9 launches per decoder layer, all state on the device.
+// Fused B=1 decode step: 8 launches per decoder layer, all state on the device.
 //
 // The reference decodes through HF generate(): per token, Python walks the
 // layers of MistralDecoderLayer (transformers/models/mistral/
@@ -9,12 +9,14 @@
 //
 //   x (fp16 residual)
 //   1. GEMV q|k|v (one launch, 3 segments), prologue x -> RMSNorm(x) * w
-//   2. prep: q/k/v partial sums -> fp16, RoPE, quantize the token leaving
-//      the hot window, new k/v into the hot ring, q rotation -> q_rot
-//   3. attention split (cold codes), 4. combine (+ hot window, PiV)
-//   5. GEMV o_proj                                6. x += o
-//   7. GEMV gate|up (dual), prologue RMSNorm       8. GEMV down, prologue
-//      SwiGLU of the gate/up partial sums          9. x += down
+//   2. attention split (cold codes), prologue: q|k|v partial sums -> fp16,
+//      RoPE, q rotation; new k/v into the hot ring (one block per kv head)
+//   3. combine (+ hot window, PiV)
+//   4. GEMV o_proj                                5. x += o
+//   6. GEMV gate|up (dual), prologue RMSNorm       7. GEMV down, prologue
+//      SwiGLU of the gate/up partial sums          8. x += down
+//   Per step, before the layers: evict_kernel quantizes, for every layer,
+//   the token leaving the hot window.
 //   head: GEMV lm_head (prologue final RMSNorm), logits + per-block argmax,
 //   final argmax -> tok, pos + 1.
 //
@@ -29,7 +31,7 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kThreads = 256;
-constexpr int kMaxG = 8;  // query heads per kv head handled by the prep kernel
+constexpr int kMaxG = 8;  // query heads per kv head of the decode step
 
 struct Plan {
   int64_t Hq, Hkv, G, nq, nkv;                 // q / k,v projection widths
@@ -37,7 +39,7 @@ struct Plan {
   int bz_qkv, bz_o, bz_gu, bz_d, bz_lm;
   int nc_qkv, nc_o, nc_gu, nc_d, nc_lm;
   AttnPlan attn;
-  size_t off_state, off_pqkv, off_po, off_pgu, off_pd, off_plm, off_q16, off_qrot, off_attn, off_rec, off_cand,
+  size_t off_state, off_pqkv, off_po, off_pgu, off_pd, off_plm, off_q16, off_attn, off_rec, off_cand,
       total;
 };
 
@@ -79,7 +81,6 @@ Plan make_plan(const lkv_decode_dims& d) {
   p.off_pd = take(gemv_part_floats(d.hidden, p.nc_d) * 4);
   p.off_plm = take(gemv_part_floats(d.vocab, p.nc_lm) * 4);
   p.off_q16 = take(static_cast<size_t>(p.nq) * 2);
-  p.off_qrot = take(static_cast<size_t>(p.nq) * 4);
   p.off_attn = take(static_cast<size_t>(p.nq) * 2);
   p.off_rec = take(p.attn.total - p.attn.part_off);
   p.off_cand = take(static_cast<size_t>(p.svoc) * 8);
@@ -162,22 +163,6 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* __res
   const int z = blockIdx.x * kThreads + threadIdx.x;
   if (z < Z) y[row + z] = f2h(rms_apply(x[row + z], w[z], rstd));
 }
-
-struct PrepArgs {
-  const float* pq;  // q, k, v partials ([slab][chunk][256] each)
-  const float* pk;
-  const float* pv;
-  int nchunk;
-  const uint16_t* cos;
-  const uint16_t* sin;
-  const int32_t* state;
-  uint16_t* k_hot;
-  uint16_t* v_hot;
-  const float* PiK;
-  int hot_cap, Hq, Hkv;
-  uint16_t* q16;
-  float* qrot;
-};
 
 // The token leaving the hot window at this step, for up to kEvictLayers
 // layers per launch: the layer table travels as kernel arguments.
@@ -274,128 +259,6 @@ __global__ __launch_bounds__(kThreads) void evict_kernel(EvictArgs A) {
   tq::pack_store<BITS>(s_codes, vside ? Ly.v_codes : Ly.k_codes, 0, 1, [=](int64_t) { return roff; });
 }
 
-
-// Grid (kv heads, 3).  Block (h, 0) is the key side: RoPE of the key and
-// the new key into its ring slot; block (h, 1) the value side; block (h, 2)
-// the query side: RoPE of the G query heads (fp16 copies for the hot-window
-// scores) and q_rot = q @ PiK^T by rotate_query_hilo, the split kernel's own
-// arithmetic, so the decode step and lkv_tq_decode_attn see identical rotated
-// queries.  The token leaving the hot window was quantized by evict_kernel
-// at the start of the step.
-__global__ __launch_bounds__(kThreads) void prep_kernel(PrepArgs A) {
-  constexpr int kCols = kMaxG * kD / kThreads;  // projected columns per thread (query side at most)
-  constexpr int kPartLd = kD + 4;               // rotate_query_hilo partial rows
-  __shared__ __align__(16) float s_part[4 * 16 * kPartLd];
-  __shared__ float s_raw[kMaxG][kD];   // query side: the G heads; key / value side: row 0
-  __shared__ float s_rope[kMaxG][kD];  // after RoPE (query and key sides)
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int kvh = blockIdx.x;
-  const int side = blockIdx.y;  // 0 key, 1 value, 2 query
-  const bool vside = side == 1, qside = side == 2;
-  const int G = A.Hq / A.Hkv;
-  const int ncol = (qside ? G : 1) * kD;  // projected columns this block needs
-
-  // ---- 0. loads, all in flight before the first wait: the position, the
-  //      first 16 chunks of the projection partial sums, this position's
-  //      RoPE row.
-  const int pos = A.state[0];
-  const int nc = A.nchunk;
-  // Projections, summed over chunks in chunk order, rounded to fp16.  A
-  // wave's 64 columns never straddle a 128-column head, so validity is
-  // uniform per wave (scalar branches).
-  const float* src[kCols];
-  bool ok[kCols];
-  float psum[kCols];
-#pragma unroll
-  for (int e = 0; e < kCols; ++e) {
-    const int cw = __builtin_amdgcn_readfirstlane(e * kThreads + (tid & ~(kWave - 1)));
-    ok[e] = cw < ncol;
-    const int c = cw + lane;
-    const int which = c / kD, d = c % kD;
-    const int col = qside ? (kvh * G + which) * kD + d : kvh * kD + d;
-    const float* base = qside ? A.pq : vside ? A.pv : A.pk;
-    src[e] = base + static_cast<size_t>(col / kGemvBN) * nc * kGemvBN + (col % kGemvBN);
-    psum[e] = 0.f;
-  }
-  constexpr int kFirst = 16;
-  float v0[kCols][kFirst];
-#pragma unroll
-  for (int e = 0; e < kCols; ++e)
-    if (ok[e]) {
-#pragma unroll
-      for (int i = 0; i < kFirst; ++i) v0[e][i] = src[e][static_cast<size_t>(min(i, nc - 1)) * kGemvBN];
-    }
-  const uint16_t cs_d = A.cos[static_cast<size_t>(pos) * kD + (tid & (kD - 1))];
-  const uint16_t sn_d = A.sin[static_cast<size_t>(pos) * kD + (tid & (kD - 1))];
-
-  // ---- 1. finish the projection sums
-#pragma unroll
-  for (int e = 0; e < kCols; ++e)
-    if (ok[e]) {
-#pragma unroll
-      for (int i = 0; i < kFirst; ++i) psum[e] += i < nc ? v0[e][i] : 0.f;
-    }
-  for (int k0 = kFirst; k0 < nc; k0 += 8) {
-    float v[kCols][8];
-#pragma unroll
-    for (int e = 0; e < kCols; ++e)
-      if (ok[e]) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[e][i] = src[e][static_cast<size_t>(min(k0 + i, nc - 1)) * kGemvBN];
-      }
-#pragma unroll
-    for (int e = 0; e < kCols; ++e)
-      if (ok[e]) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) psum[e] += k0 + i < nc ? v[e][i] : 0.f;
-      }
-  }
-#pragma unroll
-  for (int e = 0; e < kCols; ++e) {
-    const int c = e * kThreads + tid;
-    if (ok[e]) s_raw[c / kD][c % kD] = h2f(f2h(psum[e]));
-  }
-  __syncthreads();
-
-  // ---- 2. RoPE: x*cos + rotate_half(x)*sin with fp16 products and sum
-  //      (apply_rotary_pos_emb on fp16 tensors, modeling_mistral.py)
-  if (!vside) {
-    const float cf = h2f(cs_d), sf = h2f(sn_d);  // this thread's d = tid % 128 for every e below
-    for (int e = tid; e < ncol; e += kThreads) {
-      const int rr = e / kD, d = e % kD;
-      const float xv = s_raw[rr][d];
-      const float rh = d < kD / 2 ? -s_raw[rr][d + kD / 2] : s_raw[rr][d - kD / 2];
-      const float o = h2f(f2h(h2f(f2h(xv * cf)) + h2f(f2h(rh * sf))));
-      s_rope[rr][d] = o;
-      if (qside) A.q16[static_cast<size_t>(kvh * G + rr) * kD + d] = f2h(o);
-    }
-    __syncthreads();
-  }
-
-  if (qside) {
-    // ---- 3. the rotated query heads
-    const int h = lane & 15, g = lane >> 4;
-    u32x4 qb = u32x4{0u, 0u, 0u, 0u};
-    if (h < G) {
-      const float* q = &s_rope[h][32 * wave + 8 * g];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        qb[j] = static_cast<uint32_t>(f2h(q[2 * j])) | (static_cast<uint32_t>(f2h(q[2 * j + 1])) << 16);
-    }
-    float4 out[8];
-    rotate_query_hilo(A.PiK, qb, wave, lane, s_part, kPartLd, out);
-    if (h < G) {
-      float4* dst = reinterpret_cast<float4*>(A.qrot + static_cast<size_t>(kvh * G + h) * kD + 32 * g);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) dst[i] = out[i];
-    }
-    return;
-  }
-  // ---- 3. the new token into its ring slot (evict_kernel has read the old one)
-  uint16_t* hot = vside ? A.v_hot : A.k_hot;
-  if (tid < kD)
-    hot[(static_cast<size_t>(kvh) * A.hot_cap + pos % A.hot_cap) * kD + tid] = f2h(vside ? s_raw[0][tid] : s_rope[0][tid]);
-}
 
 struct Cand {
   float v;
@@ -580,38 +443,25 @@ extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_deco
     G.part = reinterpret_cast<float*>(ws + p.off_pqkv);
     if (int e = gemv_launch(G, p.bz_qkv, false, kInRmsNorm, slab, st)) return e;
   }
-  // 2. prep
-  {
-    PrepArgs A{};
-    A.pq = reinterpret_cast<const float*>(ws + p.off_pqkv);
-    A.pk = A.pq + gemv_part_floats(p.nq, p.nc_qkv);
-    A.pv = A.pk + gemv_part_floats(p.nkv, p.nc_qkv);
-    A.nchunk = p.nc_qkv;
-    A.cos = static_cast<const uint16_t*>(d.rope_cos);
-    A.sin = static_cast<const uint16_t*>(d.rope_sin);
-    A.state = state;
-    A.k_hot = static_cast<uint16_t*>(L->k_hot);
-    A.v_hot = static_cast<uint16_t*>(L->v_hot);
-    A.PiK = L->PiK;
-    A.hot_cap = static_cast<int>(d.hot_cap);
-    A.Hq = static_cast<int>(p.Hq);
-    A.Hkv = static_cast<int>(p.Hkv);
-    A.q16 = reinterpret_cast<uint16_t*>(ws + p.off_q16);
-    A.qrot = reinterpret_cast<float*>(ws + p.off_qrot);
-    hipLaunchKernelGGL(prep_kernel, dim3(static_cast<unsigned>(p.Hkv), 3), dim3(kThreads), 0, st, A);
-    LKV_LAUNCH_CHECK("decode prep");
-  }
-  // 3-4. attention
+  // 2-3. attention: the split kernel reduces the q|k|v partials itself (RoPE,
+  // query rotation, the new key and value into the ring)
   {
     AttnCall c{};
-    c.qrot = reinterpret_cast<const float*>(ws + p.off_qrot);
-    c.q = reinterpret_cast<const uint16_t*>(ws + p.off_q16);
+    c.pq = reinterpret_cast<const float*>(ws + p.off_pqkv);
+    c.pk = c.pq + gemv_part_floats(p.nq, p.nc_qkv);
+    c.pv = c.pk + gemv_part_floats(p.nkv, p.nc_qkv);
+    c.nchunk = p.nc_qkv;
+    c.rope_cos = static_cast<const uint16_t*>(d.rope_cos);
+    c.rope_sin = static_cast<const uint16_t*>(d.rope_sin);
+    c.pos = state;
+    c.q16 = reinterpret_cast<uint16_t*>(ws + p.off_q16);
+    c.k_ring = static_cast<uint16_t*>(L->k_hot);
+    c.v_ring = static_cast<uint16_t*>(L->v_hot);
+    c.PiK = L->PiK;
     c.k_codes = static_cast<const uint8_t*>(L->k_codes);
     c.k_norms = static_cast<const float*>(L->k_norms);
     c.v_codes = static_cast<const uint8_t*>(L->v_codes);
     c.v_norms = static_cast<const float*>(L->v_norms);
-    c.k_hot = static_cast<const uint16_t*>(L->k_hot);
-    c.v_hot = static_cast<const uint16_t*>(L->v_hot);
     c.PiV = L->PiV;
     c.centroids = d.centroids;
     c.seq_len = state + 1;
@@ -627,7 +477,7 @@ extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_deco
     c.bits = d.bits;
     if (int e = attn_launch(c, p.attn, st)) return e;
   }
-  // 5-6. o_proj, residual
+  // 4-5. o_proj, residual
   {
     GemvArgs G{};
     G.x = reinterpret_cast<const uint16_t*>(ws + p.off_attn);
@@ -645,7 +495,7 @@ extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_deco
                        p.nc_o);
     LKV_LAUNCH_CHECK("decode residual");
   }
-  // 7. gate|up
+  // 6. gate|up
   {
     GemvArgs G{};
     G.x = xx;
@@ -665,7 +515,7 @@ extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_deco
     G.part_up_off = gemv_part_floats(d.ffn, p.nc_gu);
     if (int e = gemv_launch(G, p.bz_gu, true, kInRmsNorm, static_cast<int>(p.sf), st)) return e;
   }
-  // 8-9. down (SwiGLU prologue), residual
+  // 7-8. down (SwiGLU prologue), residual
   {
     GemvArgs G{};
     G.in_part = reinterpret_cast<const float*>(ws + p.off_pgu);

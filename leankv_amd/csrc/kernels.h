@@ -59,7 +59,7 @@ inline size_t gemv_part_floats(int64_t N, int64_t nchunk) {
 // Column n of a [slab][chunk][kGemvBN] partial array summed over chunks in
 // chunk order, starting from 0.  Loads are issued 16 at a time.
 __device__ __forceinline__ float column_sum(const float* __restrict__ P, int n, int nchunk) {
-  constexpr int kBatch = 16;
+  constexpr int kBatch = 32;
   const float* p = P + static_cast<size_t>(n / kGemvBN) * nchunk * kGemvBN + (n % kGemvBN);
   float s = 0.f;
   for (int k0 = 0; k0 < nchunk; k0 += kBatch) {
@@ -208,6 +208,22 @@ struct AttnCall {
   float scale;
   int64_t max_len, B, Hq, Hkv, cap, hot_cap;
   int bits;
+  // Decode step (B = 1), set when pq is non-null: the query, key and value
+  // of the new token arrive as q|k|v GEMV partials ([slab][chunk][kGemvBN]).
+  // The split kernel sums them, applies RoPE at position *pos, rotates the
+  // query with PiK (q_rot and q are then unused as inputs); its last split
+  // block writes the RoPE'd query to q16 (read by the combine as q) and the
+  // new key / value into ring slot *pos % hot_cap.
+  const float* pq;
+  const float* pk;
+  const float* pv;
+  int nchunk;
+  const uint16_t* rope_cos;  // [max_len, 128] fp16
+  const uint16_t* rope_sin;
+  const int32_t* pos;
+  uint16_t* q16;
+  uint16_t* k_ring;
+  uint16_t* v_ring;
 };
 // Launch the split and combine kernels.
 int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st);

@@ -82,6 +82,17 @@ struct AttnParams {
   uint16_t* out;            // [B, Hq, 128]
   float scale_log2;         // scale * log2(e)
   int max_len, Hq, Hkv, G, cap, hot_cap, nsplit, split_tokens, ncent;
+  // decode step only (AttnCall: q|k|v partials, RoPE, ring write)
+  const float* pq;
+  const float* pk;
+  const float* pv;
+  int nchunk;
+  const uint16_t* rope_cos;
+  const uint16_t* rope_sin;
+  const int32_t* pos;
+  uint16_t* q16;
+  uint16_t* k_ring;
+  uint16_t* v_ring;
 };
 
 __device__ __forceinline__ int rec_floats(int G) { return G * (2 + kD); }
@@ -316,6 +327,48 @@ __device__ __forceinline__ void attend(const BlockRegs& R, int t0, int t_end, co
     attend_block<PERM, true>(R, t0, t_end, qa, tab, s_lut, lane, S);
 }
 
+// Columns n0 and n1 of a [slab][chunk][kGemvBN] GEMV partial array, each
+// summed over the chunks in chunk order from 0 (column_sum's order), with the
+// loads of both columns in flight together.
+__device__ __forceinline__ void column_sum2(const float* __restrict__ P, int n0, int n1, int nchunk, float& s0,
+                                            float& s1) {
+  constexpr int kB = 16;
+  const float* p0 = P + static_cast<size_t>(n0 / kGemvBN) * nchunk * kGemvBN + (n0 % kGemvBN);
+  const float* p1 = P + static_cast<size_t>(n1 / kGemvBN) * nchunk * kGemvBN + (n1 % kGemvBN);
+  s0 = 0.f;
+  s1 = 0.f;
+  for (int k0 = 0; k0 < nchunk; k0 += kB) {
+    float a[kB], c[kB];
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      const size_t o = static_cast<size_t>(min(k0 + i, nchunk - 1)) * kGemvBN;
+      a[i] = p0[o];
+      c[i] = p1[o];
+    }
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      s0 += k0 + i < nchunk ? a[i] : 0.f;
+      s1 += k0 + i < nchunk ? c[i] : 0.f;
+    }
+  }
+}
+
+// RoPE of the dim pair (d, d + 64) of an fp16 row, x * cos + rotate_half(x) *
+// sin with fp16 products and sum (apply_rotary_pos_emb on fp16 tensors,
+// modeling_mistral.py); x0, x1 are the fp32 projection sums, rounded to fp16
+// first as the fp16 projection output is.  Each product is rounded to fp16
+// before the sum: contraction is off here, since the compiler otherwise turns
+// the fp16 product and the fp32 add into one fma and skips that rounding.
+__device__ __forceinline__ void rope_pair(float x0, float x1, const uint16_t* __restrict__ cos_row,
+                                          const uint16_t* __restrict__ sin_row, int d, float& o0, float& o1) {
+#pragma clang fp contract(off)
+  const float a = h2f(f2h(x0)), c = h2f(f2h(x1));
+  const float c0 = h2f(cos_row[d]), c1 = h2f(cos_row[d + kD / 2]);
+  const float s0 = h2f(sin_row[d]), s1 = h2f(sin_row[d + kD / 2]);
+  o0 = h2f(f2h(h2f(f2h(a * c0)) + h2f(f2h(-c * s0))));
+  o1 = h2f(f2h(h2f(f2h(c * c1)) + h2f(f2h(a * s1))));
+}
+
 constexpr int kORow = kD + 4;  // padded LDS row of the per-wave outputs
 #ifndef LKV_ATTN_BLOCKS_PER_CU
 #define LKV_ATTN_BLOCKS_PER_CU 2
@@ -324,7 +377,7 @@ constexpr int kORow = kD + 4;  // padded LDS row of the per-wave outputs
 // budget and the split count.
 constexpr int kSplitBlocksPerCU = LKV_ATTN_BLOCKS_PER_CU;
 
-template <bool PERM>
+template <bool PERM, bool DECODE>
 __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_kernel(AttnParams P) {
   __shared__ uint32_t s_lut[256];
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
@@ -372,7 +425,58 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
   {
     // rows h >= G read head G - 1 and are zeroed: unconditional loads
     float4 f[8];
-    if (P.PiK != nullptr) {
+    if constexpr (DECODE) {
+      // The G query heads from the q|k|v partials: sums, fp16, RoPE at pos,
+      // then the rotation below.  Thread pairs (head e / 64, dims e % 64 and
+      // e % 64 + 64).  The last split block also publishes the RoPE'd query
+      // (fp16, for the combine's hot-window scores) and puts the new key and
+      // value into their ring slot; evict_kernel has already quantized the
+      // token that slot held.
+      __shared__ float s_q[16][kD];
+      const int pos = __builtin_amdgcn_readfirstlane(*P.pos);
+      const uint16_t* cos_row = P.rope_cos + static_cast<size_t>(pos) * kD;
+      const uint16_t* sin_row = P.rope_sin + static_cast<size_t>(pos) * kD;
+      const bool writer = split == P.nsplit - 1;
+      for (int e = tid; e < G * (kD / 2); e += kThreads) {
+        const int hh = e / (kD / 2), dd = e % (kD / 2);
+        const int col = (kvh * G + hh) * kD + dd;
+        float x0, x1, o0, o1;
+        column_sum2(P.pq, col, col + kD / 2, P.nchunk, x0, x1);
+        rope_pair(x0, x1, cos_row, sin_row, dd, o0, o1);
+        s_q[hh][dd] = o0;
+        s_q[hh][dd + kD / 2] = o1;
+        if (writer) {
+          P.q16[col] = f2h(o0);
+          P.q16[col + kD / 2] = f2h(o1);
+        }
+      }
+      if (writer) {
+        const size_t slot = (static_cast<size_t>(kvh) * P.hot_cap + pos % P.hot_cap) * kD;
+        if (tid < kD / 2) {  // key pair (tid, tid + 64), RoPE'd
+          float x0, x1, o0, o1;
+          column_sum2(P.pk, kvh * kD + tid, kvh * kD + tid + kD / 2, P.nchunk, x0, x1);
+          rope_pair(x0, x1, cos_row, sin_row, tid, o0, o1);
+          P.k_ring[slot + tid] = f2h(o0);
+          P.k_ring[slot + tid + kD / 2] = f2h(o1);
+        } else if (tid < kD) {  // value dims (tid - 64, tid): no RoPE
+          const int dd = tid - kD / 2;
+          float x0, x1;
+          column_sum2(P.pv, kvh * kD + dd, kvh * kD + dd + kD / 2, P.nchunk, x0, x1);
+          P.v_ring[slot + dd] = f2h(x0);
+          P.v_ring[slot + dd + kD / 2] = f2h(x1);
+        }
+      }
+      __syncthreads();
+      u32x4 qb = u32x4{0u, 0u, 0u, 0u};
+      if (h < G) {
+        const float* q = &s_q[h][32 * wave + 8 * g];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          qb[jj] = static_cast<uint32_t>(f2h(q[2 * jj])) | (static_cast<uint32_t>(f2h(q[2 * jj + 1])) << 16);
+      }
+      rotate_query_hilo(P.PiK, qb, wave, lane, &s_o[0][0][0], kORow, f);
+      __syncthreads();  // s_o is written again by the merge
+    } else if (P.PiK != nullptr) {
       // q_rot on MFMA (rotate_query_hilo), overlapping the first block's
       // loads; s_o is free until the merge.
       u32x4 qb;
@@ -730,10 +834,29 @@ int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st) {
   P.ncent = 1 << c.bits;
   const dim3 grid(static_cast<unsigned>(pl.nsplit), static_cast<unsigned>(c.Hkv), static_cast<unsigned>(c.B));
   const dim3 cgrid(static_cast<unsigned>(c.Hq), static_cast<unsigned>(c.B));
-  if (c.bits == 3)
-    hipLaunchKernelGGL((tq_attn_split_kernel<true>), grid, dim3(kThreads), 0, st, P);
-  else
-    hipLaunchKernelGGL((tq_attn_split_kernel<false>), grid, dim3(kThreads), 0, st, P);
+  P.pq = c.pq;
+  P.pk = c.pk;
+  P.pv = c.pv;
+  P.nchunk = c.nchunk;
+  P.rope_cos = c.rope_cos;
+  P.rope_sin = c.rope_sin;
+  P.pos = c.pos;
+  P.q16 = c.q16;
+  P.k_ring = c.k_ring;
+  P.v_ring = c.v_ring;
+  if (c.pq != nullptr) {
+    P.q = c.q16;  // the combine's hot-window query
+    P.k_hot = c.k_ring;
+    P.v_hot = c.v_ring;
+    if (c.bits == 3)
+      hipLaunchKernelGGL((tq_attn_split_kernel<true, true>), grid, dim3(kThreads), 0, st, P);
+    else
+      hipLaunchKernelGGL((tq_attn_split_kernel<false, true>), grid, dim3(kThreads), 0, st, P);
+  } else if (c.bits == 3) {
+    hipLaunchKernelGGL((tq_attn_split_kernel<true, false>), grid, dim3(kThreads), 0, st, P);
+  } else {
+    hipLaunchKernelGGL((tq_attn_split_kernel<false, false>), grid, dim3(kThreads), 0, st, P);
+  }
   LKV_LAUNCH_CHECK("tq_decode_attn split");
   hipLaunchKernelGGL(tq_attn_combine_kernel, cgrid, dim3(kCombThreads), 0, st, P);
   LKV_LAUNCH_CHECK("tq_decode_attn combine");
