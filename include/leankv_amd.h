@@ -187,6 +187,33 @@ int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const float* k_nor
                        float scale, void* out,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Causal prefill attention (S >= 1 new queries) over a TurboQuant cache,
+ * reading packed codes directly.  Equals HF SDPA with the causal mask over
+ * cat(dequantize(cold).fp16, hot) as TurboQuantCache.update returns it for an
+ * update of several tokens (cache.py:119-125, 169-189;
+ * transformers/integrations/sdpa_attention.py:79-105), without materialising
+ * the dequantized K/V.  The cache holds kv_len tokens (every new token already
+ * appended): cold tokens [0, max(0, kv_len - hot_cap)) as codes, the rest in
+ * the hot ring (token t in slot t % hot_cap).  The S queries are the newest S
+ * tokens: query i sits at position kv_len - S + i and sees keys
+ * 0 .. kv_len - S + i.
+ *   s_t = scale * n_t * ((q @ PiK^T) . c[idx_t])       cold keys
+ *   s_t = scale * (q @ PiK^T) . fp16(k_t @ PiK^T)       hot keys
+ *   o   = (sum_t p_t n_t c[idx_t] + sum_hot p_t fp16(v_t @ PiV^T)) @ PiV
+ * q: fp16 [B, Hq, S, 128] (post-RoPE); codes uint8 [B, Hkv, cap, 64] (bits 3
+ * or 4); norms fp32 [B, Hkv, cap]; hot fp16 [B, Hkv, hot_cap, 128];
+ * out fp16 [B, Hq, S, 128].  Hq / Hkv must be 1, 2, 4, 8 or 16.
+ */
+size_t lkv_tq_prefill_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hot_cap);
+int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const float* k_norms,
+                        const uint8_t* v_codes, const float* v_norms,
+                        const void* k_hot, const void* v_hot,
+                        const float* PiK, const float* PiV, const float* centroids, int bits,
+                        int64_t kv_len, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
+                        int64_t cap, int64_t hot_cap, float scale, void* out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Fused B=1 decode step                                                     */
 /* ------------------------------------------------------------------------ */

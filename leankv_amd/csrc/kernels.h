@@ -184,6 +184,11 @@ __device__ __forceinline__ void rotate_query_hilo(const float* __restrict__ PiK,
   }
 }
 
+// y = x @ Pi^T (transpose 0) or x @ Pi (transpose 1) for M rows of 128, fp32
+// MFMA (the lkv_tq_rotate kernel); x and y fp32 or fp16.
+int rotate_rows(const void* x, bool x_f16, int64_t M, const float* Pi, int transpose, void* y, bool y_f16,
+                hipStream_t st);
+
 struct AttnPlan {
   int nsplit, split_tokens;
   size_t qrot_off, part_off, total;

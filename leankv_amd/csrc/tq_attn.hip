@@ -40,6 +40,7 @@
 #include <stdlib.h>
 
 #include "kernels.h"
+#include "tq_attn_common.h"
 #include "tq_common.h"
 
 namespace lkv {
@@ -53,17 +54,9 @@ constexpr int kRowB = 64;   // code bytes per token (4-bit nibbles, dim 128)
 constexpr int kHotMax = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
-__device__ __forceinline__ uint32_t pack2h(float lo, float hi) {
-  return static_cast<uint32_t>(f2h(lo)) | (static_cast<uint32_t>(f2h(hi)) << 16);
-}
-
 // Max / sum across the 16 lanes of a row group (lanes with equal lane/16).
 __device__ __forceinline__ float group16_max(float v) { return row16_max(v); }
 __device__ __forceinline__ float group16_sum(float v) { return row16_sum(v); }
-
-// 2^x on the hardware exp (v_exp_f32); arguments here are <= 0 and results
-// below 2^-126 flush to 0, which only drops contributions < 1e-38 of the max.
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 struct AttnParams {
   const float* qrot;        // [B, Hq, 128] fp32 = q @ PiK^T
@@ -171,77 +164,6 @@ __device__ __forceinline__ void fetch_block(BlockRegs& R, const ColdRsrc& rs, in
     load_full(R, rs, t0, lane);
   else
     load_clamped(R, rs, t0, t_addr_end, lane);
-}
-
-// 3-bit codes decoded on the VALU: one code dword = 8 nibbles (dims 0..7)
-// becomes 4 dwords of fp16 pairs in the dim order [0,2 | 4,6 | 1,3 | 5,7].
-// tab[0..1] hold the low bytes of the 8 fp16 centroids, tab[2..3] the high
-// bytes; v_perm_b32 picks 4 of those 8 bytes per instruction (selector bytes
-// 0..7 address {S0: bytes 4-7, S1: bytes 0-3}), so a lookup is 4 nibbles per
-// instruction with no LDS traffic.  The query operand uses the same dim
-// order, so each MFMA sees the same fp16 products as with natural order.
-__device__ __forceinline__ void decode8(uint32_t w, const uint32_t (&tab)[4], uint32_t (&d)[4]) {
-  const uint32_t lo = w & 0x0F0F0F0Fu;         // codes of dims 0, 2, 4, 6 (one per byte)
-  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // dims 1, 3, 5, 7
-  const uint32_t llo = __builtin_amdgcn_perm(tab[1], tab[0], lo), hlo = __builtin_amdgcn_perm(tab[3], tab[2], lo);
-  const uint32_t lhi = __builtin_amdgcn_perm(tab[1], tab[0], hi), hhi = __builtin_amdgcn_perm(tab[3], tab[2], hi);
-  d[0] = __builtin_amdgcn_perm(hlo, llo, 0x05010400u);  // dims 0, 2
-  d[1] = __builtin_amdgcn_perm(hlo, llo, 0x07030602u);  // dims 4, 6
-  d[2] = __builtin_amdgcn_perm(hhi, lhi, 0x05010400u);  // dims 1, 3
-  d[3] = __builtin_amdgcn_perm(hhi, lhi, 0x07030602u);  // dims 5, 7
-}
-// Position p of a decoded group holds dim kPermDim[p].
-__device__ constexpr int kPermDim[8] = {0, 2, 4, 6, 1, 3, 5, 7};
-
-// PERM: decode8 (3-bit codes).  Otherwise a 256-entry LDS table maps one
-// code byte to the fp16 pair (c[lo nibble], c[hi nibble]) in natural order.
-template <bool PERM>
-__device__ __forceinline__ void decode_dw(uint32_t w, const uint32_t (&tab)[4], const uint32_t* s_lut,
-                                          uint32_t (&d)[4]) {
-  if constexpr (PERM) {
-    decode8(w, tab, d);
-  } else {
-    d[0] = s_lut[w & 0xffu];
-    d[1] = s_lut[(w >> 8) & 0xffu];
-    d[2] = s_lut[(w >> 16) & 0xffu];
-    d[3] = s_lut[w >> 24];
-  }
-}
-// Pairs 2*half and 2*half + 1 of decode_dw (the value pass decodes in two
-// halves to halve the live registers).
-template <bool PERM>
-__device__ __forceinline__ void decode_half(uint32_t w, int half, const uint32_t (&tab)[4], const uint32_t* s_lut,
-                                            uint32_t (&d)[2]) {
-  if constexpr (PERM) {
-    const uint32_t c = (half ? (w >> 4) : w) & 0x0F0F0F0Fu;
-    const uint32_t lo = __builtin_amdgcn_perm(tab[1], tab[0], c), hi = __builtin_amdgcn_perm(tab[3], tab[2], c);
-    d[0] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
-    d[1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
-  } else {
-    d[0] = s_lut[(w >> (16 * half)) & 0xffu];
-    d[1] = s_lut[(w >> (16 * half + 8)) & 0xffu];
-  }
-}
-
-__device__ __forceinline__ float vmax(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-
-// Max / sum over the four lanes l, l^16, l^32, l^48 (the lane groups that
-// hold the other tokens of the same head), result in all four.
-__device__ __forceinline__ float xgroup_max(float v) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float xgroup_sum(float v) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Online-softmax state of one lane: head w = lane % 16, output dims

@@ -444,6 +444,25 @@ extern "C" int lkv_tq_quantize_rotated(const float* y, int64_t M, const float* b
   return LKV_OK;
 }
 
+namespace lkv {
+int rotate_rows(const void* x, bool x_f16, int64_t M, const float* Pi, int transpose, void* y, bool y_f16,
+                hipStream_t st) {
+  if (M == 0) return LKV_OK;
+  const int g = grid_for(M);
+#define LKV_ROT(IF, OF)                                                                                         \
+  hipLaunchKernelGGL((rotate_kernel<kRotate, 4, IF, OF>), dim3(g), dim3(kThreads), 0, st, x, nullptr, M, Pi, \
+                     transpose, nullptr, y)
+  if (x_f16) {
+    if (y_f16) { LKV_ROT(true, true); } else { LKV_ROT(true, false); }
+  } else {
+    if (y_f16) { LKV_ROT(false, true); } else { LKV_ROT(false, false); }
+  }
+#undef LKV_ROT
+  LKV_LAUNCH_CHECK("tq_rotate");
+  return LKV_OK;
+}
+}  // namespace lkv
+
 extern "C" int lkv_tq_rotate(const void* x, int x_dtype, int64_t M, const float* Pi, int transpose,
                              float* y, void* stream) {
   LKV_REQUIRE(M >= 0, "tq_rotate: negative M");
@@ -451,16 +470,7 @@ extern "C" int lkv_tq_rotate(const void* x, int x_dtype, int64_t M, const float*
   if (M == 0) return LKV_OK;
   LKV_REQUIRE(x && Pi && y, "tq_rotate: null pointer");
   LKV_REQUIRE(aligned16(x) && aligned16(Pi) && aligned16(y), "tq_rotate: pointers must be 16-byte aligned");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int g = grid_for(M);
-  if (x_dtype == LKV_DTYPE_F16)
-    hipLaunchKernelGGL((rotate_kernel<kRotate, 4, true, false>), dim3(g), dim3(kThreads), 0, st, x,
-                       nullptr, M, Pi, transpose, nullptr, y);
-  else
-    hipLaunchKernelGGL((rotate_kernel<kRotate, 4, false, false>), dim3(g), dim3(kThreads), 0, st, x,
-                       nullptr, M, Pi, transpose, nullptr, y);
-  LKV_LAUNCH_CHECK("tq_rotate");
-  return LKV_OK;
+  return rotate_rows(x, x_dtype == LKV_DTYPE_F16, M, Pi, transpose, y, false, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int lkv_tq_dequantize(const uint8_t* packed, const void* norms, int norm_dtype, int64_t M,

@@ -318,6 +318,55 @@ def tq_decode_attn(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK, PiV
                               seq_len_dev, max_len, scale, out)
 
 
+def tq_prefill_attn_out(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK, PiV, centroids, bits, kv_len: int,
+                        scale: float, out: torch.Tensor, workspace: torch.Tensor | None = None):
+    """Causal attention of the newest S tokens' queries over the packed cold cache + fp16 hot ring.
+
+    q: fp16 [B, Hq, S, 128] (post-RoPE, positions kv_len - S ..); codes uint8 [B, Hkv, cap, 64];
+    norms fp32 [B, Hkv, cap]; hot fp16 [B, Hkv, hot_cap, 128]; out fp16 [B, Hq, S, 128].
+    """
+    require_cuda(q, k_codes, v_codes, k_hot, v_hot, out)
+    if q.dtype != torch.float16 or q.dim() != 4 or q.shape[-1] != HEAD_DIM or not q.is_contiguous():
+        raise LeanKVError("tq_prefill_attn: q must be contiguous float16 [B, Hq, S, 128]")
+    B, Hq, S, _ = q.shape
+    Hkv, cap = k_codes.shape[1], k_codes.shape[2]
+    hot_cap = k_hot.shape[2]
+    if out.shape != q.shape or out.dtype != torch.float16 or not out.is_contiguous():
+        raise LeanKVError("tq_prefill_attn: out must be contiguous float16 like q")
+    for t, nm in ((k_codes, "k_codes"), (v_codes, "v_codes"), (k_norms, "k_norms"), (v_norms, "v_norms"),
+                  (k_hot, "k_hot"), (v_hot, "v_hot")):
+        if not t.is_contiguous():
+            raise LeanKVError("tq_prefill_attn: %s must be contiguous" % nm)
+    if k_norms.dtype != torch.float32 or v_norms.dtype != torch.float32:
+        raise LeanKVError("tq_prefill_attn: norms must be float32")
+    if k_hot.dtype != torch.float16 or v_hot.dtype != torch.float16:
+        raise LeanKVError("tq_prefill_attn: hot window must be float16")
+    dev = q.device
+    PiK, PiV = _pi(PiK, dev), _pi(PiV, dev)
+    centroids = _vec(centroids, dev, 1 << bits, "centroids")
+    lib = _lib_handle()
+    nbytes = lib.lkv_tq_prefill_attn_workspace_bytes(B, Hq, Hkv, S, hot_cap)
+    if workspace is None:
+        workspace = workspaces.get(q.device, "prefill", nbytes)
+    check(
+        lib.lkv_tq_prefill_attn(ptr(q), ptr(k_codes), ptr(k_norms), ptr(v_codes), ptr(v_norms), ptr(k_hot),
+                                ptr(v_hot), ptr(PiK), ptr(PiV), ptr(centroids), int(bits), int(kv_len), B, Hq, Hkv,
+                                S, cap, hot_cap, float(scale), ptr(out), ptr(workspace), workspace.numel(),
+                                stream_handle(q.device)),
+        "lkv_tq_prefill_attn",
+    )
+    return out
+
+
+def tq_prefill_attn(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK, PiV, centroids, bits, kv_len: int,
+                    scale: float | None = None):
+    out = torch.empty_like(q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(HEAD_DIM)
+    return tq_prefill_attn_out(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK, PiV, centroids, bits,
+                               kv_len, scale, out)
+
+
 # ------------------------------------------------------------------ RMSNorm
 def rms_norm_out(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor) -> torch.Tensor:
     """out = RMSNorm(x) * weight over the last dim (fp16), rounded like HF MistralRMSNorm.

@@ -13,12 +13,14 @@ Storage is MI355X-shaped instead of a list of torch.cat'ed tensors:
 so a decode step writes 64 + 4 bytes per (head, K/V) instead of re-concatenating
 the whole store, and ``cap`` grows by doubling when a sequence outgrows it.
 
-update() with one new token and ``fused_attention=True`` (the default when the
-model uses the "leankv_tq" attention implementation registered by
-leankv_amd.turboquant.attention) appends with one HIP launch and defers
-attention to the packed-KV decode kernel: no dequantized K/V is formed.  Any
-other update (prefill, several tokens, fused attention off) returns the
-reference's full K/V -- cold dequantized by the HIP kernel to fp16, then hot.
+update() with ``fused_attention=True`` (the default; the model must use the
+"leankv_tq" attention implementation registered by
+leankv_amd.turboquant.attention) defers attention to the packed-KV kernels:
+one new token appends with one HIP launch and runs the split-K decode kernel,
+several tokens (a prefill or a chunk) are appended with the bulk quantizer and
+run the causal prefill kernel; no dequantized K/V is formed either way.  With
+fused attention off, an update of several tokens returns the reference's full
+K/V -- cold dequantized by the HIP kernel to fp16, then hot.
 """
 
 from __future__ import annotations
@@ -79,7 +81,8 @@ class TurboQuantCache:
         self._v_hot = [None] * num_layers
         self._pos_dev = [None] * num_layers     # int32 [1]: length before the pending append
         self._len_dev = [None] * num_layers     # int32 [1]: length after it (attention input)
-        self._fused_pending = [False] * num_layers
+        self._fused_pending = [False] * num_layers   # a one-token update awaits decode_attention
+        self._prefill_pending = [False] * num_layers  # a several-token update awaits prefill_attention
         self._pending_len = [0] * num_layers
 
     # ----------------------------------------------------------- storage
@@ -146,6 +149,11 @@ class TurboQuantCache:
             self._pending_len[layer_idx] = T
             return key_states, value_states
         self._fused_pending[layer_idx] = False
+        if self.fused_attention and S > 1:
+            self._prefill_pending[layer_idx] = True
+            self._pending_len[layer_idx] = T
+            return key_states, value_states
+        self._prefill_pending[layer_idx] = False
         return self._get_full_cache(layer_idx)
 
     def _bulk_update(self, li: int, k16: torch.Tensor, v16: torch.Tensor, p0: int) -> None:
@@ -209,6 +217,27 @@ class TurboQuantCache:
                                 self._len_dev[layer_idx], L, scale)
         return out.reshape(B, Hq, 1, D)
 
+    def prefill_attention(self, layer_idx: int, query: torch.Tensor, scaling: float | None = None) -> torch.Tensor:
+        """Causal attention of the newest S tokens' queries [B, Hq, S, D] over this layer's cache -> [B, Hq, S, D].
+
+        Query i sits at position L - S + i and sees keys 0 .. L - S + i, the reference's
+        SDPA over cat(dequantize(cold).fp16, hot) with HF's causal mask (cache.py:119-125)."""
+        if not self._prefill_pending[layer_idx]:
+            raise RuntimeError("TurboQuantCache.prefill_attention: no update pending for layer %d" % layer_idx)
+        self._prefill_pending[layer_idx] = False
+        D = query.shape[-1]
+        q = query.to(torch.float16).contiguous()
+        L = self._pending_len[layer_idx]
+        scale = float(scaling) if scaling is not None else 1.0 / math.sqrt(D)
+        return _k.tq_prefill_attn(q, self._k_codes[layer_idx], self._k_norms[layer_idx], self._v_codes[layer_idx],
+                                  self._v_norms[layer_idx], self._k_hot[layer_idx], self._v_hot[layer_idx],
+                                  self.PiK[layer_idx], self.PiV[layer_idx], self.centroids, self.bits, L, scale)
+
+    def take_full_cache(self, layer_idx: int):
+        """The reference's K/V for a pending several-token update (the attention runs elsewhere)."""
+        self._prefill_pending[layer_idx] = False
+        return self._get_full_cache(layer_idx)
+
     # ----------------------------------------------------------- HF interface
     def get_seq_length(self, layer_idx: int = 0) -> int:
         return self._seq_lengths[layer_idx] if layer_idx < len(self._seq_lengths) else 0
@@ -250,6 +279,7 @@ class TurboQuantCache:
                 lst[i] = None
         self._seq_lengths = [0] * self.num_layers
         self._fused_pending = [False] * self.num_layers
+        self._prefill_pending = [False] * self.num_layers
         self._seen_tokens = 0
 
     @property

@@ -9,6 +9,7 @@ References (under /root/reference, read as text):
   leankv/turboquant/quantizer.py:131-137 TurboQuantMSE.dequantize
   leankv/turboquant/cache.py:84-189     TurboQuantCache.update / flush / full cache
   transformers/integrations/sdpa_attention.py:79-105  GQA SDPA on the returned K/V
+  transformers/masking_utils.py causal_mask_function   causal mask with the cache offset (prefill)
 """
 
 from __future__ import annotations
@@ -172,3 +173,25 @@ def decode_attention(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, scale: f
     s = torch.matmul(qd, Kd.transpose(-1, -2)) * scale
     p = torch.softmax(s, dim=-1)
     return torch.matmul(p, Vd)
+
+
+def prefill_attention(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, scale: float | None = None):
+    """Causal GQA attention of the newest S tokens' queries in fp64.
+
+    q [B, Hq, S, D], K/V [B, Hkv, L, D] with L >= S -> [B, Hq, S, D] fp64.  Query i
+    sits at position L - S + i and sees keys 0 .. L - S + i: HF's causal mask
+    with the cache offset (masking_utils causal_mask_function, kv_idx <= q_idx)
+    applied by SDPA (sdpa_attention.py:79-105) to the K/V the cache returns.
+    """
+    B, Hq, S, D = q.shape
+    Hkv, L = K.shape[1], K.shape[2]
+    G = Hq // Hkv
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    Kd = K.double().repeat_interleave(G, dim=1)
+    Vd = V.double().repeat_interleave(G, dim=1)
+    s = torch.matmul(q.double(), Kd.transpose(-1, -2)) * scale
+    qpos = torch.arange(S).view(S, 1) + (L - S)
+    visible = torch.arange(L).view(1, L) <= qpos
+    s = s.masked_fill(~visible, float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), Vd)

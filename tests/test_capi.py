@@ -20,7 +20,8 @@ def _declared():
 def test_header_declares_expected_entry_points():
     names = _declared()
     for n in ("lkv_sparse_gemv", "lkv_sparse_gateup_swiglu", "lkv_tq_quantize", "lkv_tq_quantize_rotated",
-              "lkv_tq_dequantize", "lkv_tq_rotate", "lkv_tq_cache_append", "lkv_tq_decode_attn"):
+              "lkv_tq_dequantize", "lkv_tq_rotate", "lkv_tq_cache_append", "lkv_tq_decode_attn",
+              "lkv_tq_prefill_attn"):
         assert n in names
 
 
@@ -72,7 +73,22 @@ def test_invalid_arguments_rejected_without_launch():
     assert lib.lkv_tq_decode_attn(p, p, p, p, p, p, p, p, p, p, 3, p, 1000, 1, 32, 8, 64, 64, 0.1, p, p,
                                   1 << 20, None) == -1
     assert "max_len" in _lib.last_error()
+    # prefill: query heads per kv head not a power of two <= 16, S beyond the cache, too few cold rows
+    assert lib.lkv_tq_prefill_attn(p, p, p, p, p, p, p, p, p, p, 3, 100, 1, 12, 4, 100, 64, 64, 0.1, p, p,
+                                   1 << 30, None) == -1
+    assert "Hq/Hkv" in _lib.last_error()
+    assert lib.lkv_tq_prefill_attn(p, p, p, p, p, p, p, p, p, p, 3, 100, 1, 8, 2, 101, 64, 64, 0.1, p, p,
+                                   1 << 30, None) == -1
+    assert "S <= kv_len" in _lib.last_error()
+    assert lib.lkv_tq_prefill_attn(p, p, p, p, p, p, p, p, p, p, 3, 200, 1, 8, 2, 100, 64, 64, 0.1, p, p,
+                                   1 << 30, None) == -1
+    assert "exceed cap" in _lib.last_error()
+    assert lib.lkv_tq_prefill_attn(p, p, p, p, p, p, p, p, p, p, 3, 100, 1, 8, 2, 100, 64, 64, 0.1, p, p,
+                                   1024, None) == -1
+    assert "workspace" in _lib.last_error()
+    assert lib.lkv_tq_prefill_attn_workspace_bytes(1, 32, 8, 4096, 64) >= 32 * 4096 * 128 * 4
     # empty problems are no-ops
+    assert lib.lkv_tq_prefill_attn(p, p, p, p, p, p, p, p, p, p, 3, 100, 1, 8, 2, 0, 64, 64, 0.1, p, p, 0, None) == 0
     assert lib.lkv_sparse_gemv(p, p, 0.1, 0, 16, p, p, 0, None) == 0
     assert lib.lkv_tq_quantize(p, 0, 0, p, p, 3, p, p, None) == 0
 

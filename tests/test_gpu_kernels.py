@@ -393,6 +393,56 @@ def test_decode_attn_edges(cuda, B, Hq, Hkv, L, hot):
     assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
 
 
+def _prefill_case(B, Hq, Hkv, L, S, hot, seed, dev, bits=3):
+    """A cache of L tokens (cold = L - hot, built with the oracle) and the newest S tokens' queries:
+    the HIP prefill kernel vs causal fp64 attention over cat(dequantize(cold).fp16, hot)."""
+    from leankv_amd import kernels
+
+    c, b = oq.codebook_tensors(bits)
+    PiK, PiV = oq.rotation_matrix(128, 42), oq.rotation_matrix(128, 43)
+    cold = max(0, L - hot)
+    K = _kv((B, Hkv, L, 128), seed)
+    V = _kv((B, Hkv, L, 128), seed + 1000)
+    q = torch.randn(B, Hq, S, 128, generator=torch.Generator().manual_seed(seed + 7)).half()
+    cap = max(cold, 1)
+    kc = torch.zeros(B, Hkv, cap, 64, dtype=torch.uint8)
+    vc = torch.zeros_like(kc)
+    kn = torch.zeros(B, Hkv, cap)
+    vn = torch.zeros_like(kn)
+    Kref, Vref = K.clone(), V.clone()
+    if cold:
+        pk, nk, _ = oq.quantize(K[:, :, :cold].float(), PiK, b, bits)
+        pv, nv, _ = oq.quantize(V[:, :, :cold].float(), PiV, b, bits)
+        kc[:, :, :cold] = torch.from_numpy(pk)
+        vc[:, :, :cold] = torch.from_numpy(pv)
+        kn[:, :, :cold] = nk
+        vn[:, :, :cold] = nv
+        Kref[:, :, :cold] = oq.dequantize(pk, nk, PiK, c, bits).half()
+        Vref[:, :, :cold] = oq.dequantize(pv, nv, PiV, c, bits).half()
+    kh = torch.full((B, Hkv, hot, 128), float("nan"), dtype=torch.float16)  # slots past the window stay NaN
+    vh = torch.full_like(kh, float("nan"))
+    for p in range(cold, L):
+        kh[:, :, p % hot] = K[:, :, p]
+        vh[:, :, p % hot] = V[:, :, p]
+    out = kernels.tq_prefill_attn(q.to(dev), kc.to(dev), kn.to(dev), vc.to(dev), vn.to(dev), kh.to(dev), vh.to(dev),
+                                  PiK.to(dev), PiV.to(dev), c.to(dev), bits, L).cpu()
+    ref = oq.prefill_attention(q, Kref, Vref)
+    return out, ref
+
+
+# (B, Hq, Hkv, L, S, hot, bits): fresh prefills (S = L), chunks (S < L), all-hot and one-cold-token
+# caches, a single query, 1 / 2 / 4 / 8 / 16 query heads per kv head, 4-bit codes, a 16-token window.
+@pytest.mark.parametrize("B,Hq,Hkv,L,S,hot,bits", [
+    (1, 8, 2, 100, 100, 64, 3), (1, 4, 4, 37, 37, 64, 3), (1, 32, 8, 200, 1, 64, 3), (2, 16, 2, 300, 77, 16, 3),
+    (1, 16, 1, 130, 130, 64, 4), (1, 32, 8, 700, 700, 64, 3), (1, 2, 2, 64, 64, 64, 3), (1, 8, 4, 65, 65, 64, 3),
+    (3, 8, 8, 257, 129, 64, 4), (1, 32, 4, 333, 333, 64, 3)])
+def test_prefill_attn(cuda, B, Hq, Hkv, L, S, hot, bits):
+    out, ref = _prefill_case(B, Hq, Hkv, L, S, hot, seed=L + S, dev=cuda, bits=bits)
+    assert torch.isfinite(out).all()
+    assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
+    assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
+
+
 # Large batches (many (batch, kv head) pairs, few splits each): hot-only,
 # boundary and short cold ranges, a 16-token window, 16 query heads per kv head.
 @pytest.mark.parametrize("B,Hq,Hkv,L,hot", [(16, 32, 8, 1, 64), (16, 32, 8, 65, 64), (16, 32, 8, 700, 64),

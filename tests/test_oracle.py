@@ -264,6 +264,30 @@ def test_attention_oracle_closed_form():
     assert torch.allclose(o, torch.full_like(o, 4.5, dtype=torch.float64))
 
 
+def test_prefill_oracle_pins():
+    """Causal prefill oracle: S = 1 is the decode oracle; S = L is torch's fp64 causal SDPA (top-left
+    alignment is exact there); a chunk (S < L) matches a brute-force loop over the visible keys."""
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(2, 4, 6, 16, generator=g)
+    K = torch.randn(2, 2, 9, 16, generator=g)
+    V = torch.randn(2, 2, 9, 16, generator=g)
+    assert torch.allclose(oq.prefill_attention(q[:, :, -1:], K, V), oq.decode_attention(q[:, :, -1:], K, V),
+                          rtol=0, atol=1e-14)
+    Ks, Vs = K[:, :, :6], V[:, :, :6]
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q.double(), Ks.double().repeat_interleave(2, dim=1), Vs.double().repeat_interleave(2, dim=1), is_causal=True)
+    assert torch.allclose(oq.prefill_attention(q, Ks, Vs), ref, rtol=0, atol=1e-12)
+    out = oq.prefill_attention(q[:, :, :4], K, V)  # 4 queries at positions 5..8
+    for b in range(2):
+        for h in range(4):
+            for i in range(4):
+                pos = 9 - 4 + i
+                k, v = K[b, h // 2, : pos + 1].double(), V[b, h // 2, : pos + 1].double()
+                w = [math.exp(float(q[b, h, i].double() @ k[t]) / 4.0) for t in range(pos + 1)]
+                o = sum(wt * v[t] for t, wt in enumerate(w)) / sum(w)
+                assert torch.allclose(out[b, h, i], o, rtol=0, atol=1e-12)
+
+
 def test_reference_model_matches_hf_mistral_without_compression():
     """The oracle decoder (no TEAL, hot window larger than the sequence) equals HF Mistral in fp32."""
     from transformers import MistralConfig, MistralForCausalLM
