@@ -14,6 +14,9 @@ Workloads:
   mlp     config 2: fused gate/up SwiGLU [14336,4096] + sparse down [4096,14336]
   quant   config 3: TurboQuant 3-bit quantize of K,V [8,4096,128] (fp32 MFMA rotation)
   attn    config 4: packed-KV decode attention, B=16, 32/8 heads, ctx 4096 + 64 hot
+  prefill causal prefill attention of one config-5 layer over its packed cache (4096-token
+          prompt, 32/8 heads; MFMA-bound, so 3 buffer sets), beside the reference path
+          (dequantize + torch SDPA) on the same GPU
   copy    a 512 MiB device copy: the known-size reference for scaling PMC byte counters
 Every workload rotates >= 3 independent buffer sets (> 512 MB) so the 256 MB
 Infinity Cache cannot serve repeated launches.  A "step" is one launch of the
@@ -34,6 +37,7 @@ import time
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, AMD spec
 MFMA_F32_PEAK_TFLOPS = 157.3
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16
 
 
 def _parse():
@@ -41,7 +45,8 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "mlp", "quant", "attn", "copy"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "mlp", "quant", "attn", "prefill",
+                                                                    "copy"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=32, help="decoder layers (config 5 uses 32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -368,8 +373,8 @@ def bench_quant(args, torch):
 # ------------------------------------------------------------------ config 4
 def bench_attn(args, torch):
     """Config 4: decode attention on the packed 3-bit cache, B=16, 32 query / 8 kv heads, 4096 cold tokens
-    + a 64-token fp16 hot window, scale 1/sqrt(128).  The cache content is random codes / norms (the
-    kernels' cost does not depend on it); 8 rotating cache sets (570 MB)."""
+    + a 64-token fp16 hot window, scale 1/sqrt(128).  The cache content is random 3-bit codes (both
+    nibbles 0..7) and norms (the kernels' cost does not depend on it); 8 rotating cache sets (570 MB)."""
     from leankv_amd import kernels
     from leankv_amd.turboquant.codebook import get_codebook_tensors
     from leankv_amd.turboquant.rotation import generate_rotation_matrix
@@ -384,8 +389,8 @@ def bench_attn(args, torch):
     sets = []
     for s in range(8):
         g = torch.Generator(device=dev).manual_seed(400 + s)
-        kc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8)
-        vc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8)
+        kc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8) & 0x77
+        vc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8) & 0x77
         kn = torch.rand(B, Hkv, cold, generator=g, device=dev) * 4 + 8
         vn = torch.rand(B, Hkv, cold, generator=g, device=dev) * 4 + 8
         kh = torch.randn(B, Hkv, hot, D, generator=g, device=dev).half()
@@ -413,6 +418,111 @@ def bench_attn(args, torch):
                      "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3),
                      "alg_bytes_per_launch": alg},
     }
+
+
+# ------------------------------------------------------------------ prefill
+def bench_prefill(args, torch):
+    """Causal prefill attention of one config-5 layer over its packed 3-bit cache: B=1, 32 query / 8 kv
+    heads, a 4096-token prompt (4032 cold tokens as codes + the 64-token fp16 hot window), scale
+    1/sqrt(128).  Timed beside it on the same GPU: the reference's algorithm for the same call,
+    dequantize the cold store to fp16, concatenate the hot window, torch's causal SDPA (cache.py:169-189,
+    sdpa_attention.py:79-105).  The CPU baseline is the fp64 oracle on the same layer."""
+    from leankv_amd import kernels
+    from leankv_amd.turboquant.codebook import get_codebook_tensors
+    from leankv_amd.turboquant.rotation import generate_rotation_matrix
+
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, D, S, hot = 1, 32, 8, 128, 4096, 64
+    cold = S - hot
+    cent, _ = get_codebook_tensors(D, 3, dev, torch.float32)
+    PiK = generate_rotation_matrix(D, dev, torch.float32, 42)
+    PiV = generate_rotation_matrix(D, dev, torch.float32, 43)
+    order = torch.tensor([p % hot for p in range(cold, S)], device=dev)
+    sets = []
+    for s_ in range(3):
+        g = torch.Generator(device=dev).manual_seed(500 + s_)
+        kc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8) & 0x77
+        vc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8) & 0x77
+        kn = torch.rand(B, Hkv, cold, generator=g, device=dev) * 4 + 8
+        vn = torch.rand(B, Hkv, cold, generator=g, device=dev) * 4 + 8
+        kh = torch.randn(B, Hkv, hot, D, generator=g, device=dev).half()
+        vh = torch.randn(B, Hkv, hot, D, generator=g, device=dev).half()
+        q = torch.randn(B, Hq, S, D, generator=g, device=dev).half()
+        sets.append((q, kc, kn, vc, vn, kh, vh, torch.empty_like(q)))
+    ws = torch.empty(kernels._lib_handle().lkv_tq_prefill_attn_workspace_bytes(B, Hq, Hkv, S, hot), dtype=torch.uint8,
+                     device=dev)
+    scale = D ** -0.5
+
+    def launch(i):
+        q, kc, kn, vc, vn, kh, vh, out = sets[i]
+        kernels.tq_prefill_attn_out(q, kc, kn, vc, vn, kh, vh, PiK, PiV, cent, 3, S, scale, out, ws)
+
+    def reference(i):
+        q, kc, kn, vc, vn, kh, vh, _ = sets[i]
+        ck = kernels.tq_dequantize(kc, kn, PiK, cent, 3, out_dtype=torch.float16)
+        cv = kernels.tq_dequantize(vc, vn, PiV, cent, 3, out_dtype=torch.float16)
+        K = torch.cat([ck, kh.index_select(2, order)], dim=2)
+        V = torch.cat([cv, vh.index_select(2, order)], dim=2)
+        return torch.nn.functional.scaled_dot_product_attention(q, K, V, is_causal=True, scale=scale, enable_gqa=True)
+
+    # agreement with the reference path on the first set (same inputs)
+    launch(0)
+    ref0 = reference(0).float()
+    agree = float((sets[0][7].float() - ref0).norm() / ref0.norm())
+    wall, _, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
+    kmean, kmed = _kernel_time(launch, len(sets), args.steps, args.warmup, torch)
+    rmean, _ = _kernel_time(reference, len(sets), args.steps, args.warmup, torch)
+    pairs = S * (S + 1) // 2  # (query, key) pairs under the causal mask, per query head
+    flops = 4 * Hq * D * pairs
+    tflops = flops / (kmean * 1e-3) / 1e12
+    res = {
+        "metric": "packed-KV causal prefill attention TFLOP/s (one layer: 4096-token prompt, 32/8 heads)",
+        "value": round(tflops, 1), "unit": "TFLOP/s", "ms_per_step": round(wall, 5), "higher_is_better": True,
+        "dtype": "3-bit codes, fp16 MFMA scores/values, fp32 softmax",
+        "config": {"workload": "prefill_packed_attention", "batch": B, "heads": "32/8", "prompt": S, "cold": cold,
+                   "hot": hot, "flop_per_call": flops, "sets": len(sets)},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "q / hot rotations + tq_prefill_attn_kernel + output un-rotation (one call)",
+                     "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3)},
+        "prompt_tokens_per_s_per_layer": round(S / (kmean * 1e-3), 1),
+        "reference_path_gpu": {"what": "tq_dequantize (fp16) + cat(hot) + torch causal SDPA, same GPU",
+                               "us_mean": round(rmean * 1e3, 3), "speedup": round(rmean / kmean, 3),
+                               "rel_diff_vs_packed": round(agree, 6)},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = _cpu_prefill(torch, S, hot, D)
+    return res
+
+
+def _cpu_prefill(torch, S, hot, D):
+    """fp64 oracle on the whole layer: per kv head, dequantize its cold store and run the causal attention
+    of its 4 query heads (one kv head at a time bounds the score matrix to 0.5 GB)."""
+    from oracle import turboquant as oq
+
+    cores, model = _cpu_info()
+    torch.set_num_threads(cores)
+    cold = S - hot
+    c, _ = oq.codebook_tensors(3)
+    PiK, PiV = oq.rotation_matrix(D, 42), oq.rotation_matrix(D, 43)
+    g = torch.Generator().manual_seed(7)
+    dt = 0.0
+    for _ in range(8):  # kv heads of one layer
+        kc = (torch.randint(0, 256, (1, 1, cold, 64), generator=g, dtype=torch.uint8) & 0x77).numpy()
+        vc = (torch.randint(0, 256, (1, 1, cold, 64), generator=g, dtype=torch.uint8) & 0x77).numpy()
+        kn = torch.rand(1, 1, cold, generator=g) * 4 + 8
+        vn = torch.rand(1, 1, cold, generator=g) * 4 + 8
+        kh = torch.randn(1, 1, hot, D, generator=g).half()
+        vh = torch.randn(1, 1, hot, D, generator=g).half()
+        q = torch.randn(1, 4, S, D, generator=g).half()
+        t = time.perf_counter()
+        K = torch.cat([oq.dequantize(kc, kn, PiK, c, 3).half(), kh], dim=2)
+        V = torch.cat([oq.dequantize(vc, vn, PiV, c, 3).half(), vh], dim=2)
+        oq.prefill_attention(q, K, V)
+        dt += time.perf_counter() - t
+    return {"value": round(S / dt, 2), "unit": "prompt tokens/s per layer", "cores": cores, "kind": "port",
+            "sample": "oracle fp64 (dequantize + causal attention), the whole layer (8 kv heads, 32 query "
+                      "heads, 4096-token prompt); %s" % model}
 
 
 def _fill_gemv_defaults(args):
@@ -543,7 +653,7 @@ def main():
     else:
         _fill_gemv_defaults(args)
         fn = {"gemv": bench_gemv, "mlp": bench_mlp, "copy": bench_copy, "quant": bench_quant,
-              "attn": bench_attn}.get(args.workload)
+              "attn": bench_attn, "prefill": bench_prefill}.get(args.workload)
         if fn is None:
             print("bench.py: workload %s is not implemented yet" % args.workload, file=sys.stderr)
             sys.exit(2)

@@ -14,8 +14,9 @@
 // and one un-rotation by PiV finishes each output row.
 //
 // Launches of lkv_tq_prefill_attn (all on the caller's stream):
-//   1. q_rot = q @ PiK^T (fp32), hot rings k @ PiK^T and v @ PiV^T (fp16)
-//      with the rotate kernel of lkv_tq_rotate;
+//   1. rotate16_kernel (fp16 MFMA, PiK / PiV split exactly into fp16 hi + lo
+//      parts): q_rot = (q @ PiK^T) * scale * log2(e) in fp16, the score
+//      operand; hot rings k @ PiK^T and v @ PiV^T (fp16);
 //   2. tq_prefill_attn_kernel: grid (query tiles, kv heads, batch), 4 waves.
 //      A block owns 128 (query, head) columns: 128 / G consecutive queries x
 //      the G heads of one kv head, 32 columns per wave.  It walks the keys in
@@ -28,9 +29,10 @@
 //        max and sum across the 4 lanes of a column by permlane swaps);
 //      * values transposed, A = 16 dims x 32 keys from LDS, B = p * n_t from
 //        the lane's own softmax registers.
-//      The next tile's codes load while the current one is computed.  Each
-//      block writes its normalised rotated rows over its own q_rot rows;
-//   3. out = rows @ PiV (fp16) with the rotate kernel.
+//      Each thread loads its share of a tile's codes two tiles ahead into
+//      registers and decodes them into one of two LDS buffers: one barrier
+//      per tile.  The block writes its normalised rotated rows (fp32);
+//   3. rotate16_kernel: out = rows @ PiV (fp16; the rows split into hi + lo too).
 #include "kernels.h"
 #include "tq_attn_common.h"
 #include "tq_common.h"
@@ -44,11 +46,12 @@ constexpr int kKT = 32;         // keys per tile
 constexpr int kCols = 128;      // (query, head) columns per block
 constexpr int kRowB = 64;       // code bytes per token (4-bit nibbles)
 constexpr int kKRow = kD + 8;   // fp16 row of the decoded key tile (padded)
-constexpr int kVRow = kKT + 8;  // fp16 row of the transposed value tile (padded)
+constexpr int kVRow = kKT + 4;  // fp16 row of the transposed value tile (padded: conflict-free 8-byte reads)
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct PrefillParams {
-  float* rows;             // [B, Hq, S, 128] fp32: q @ PiK^T in, normalised rotated output out
+  const uint16_t* q16;     // [B, Hq, S, 128] fp16: (q @ PiK^T) * scale * log2(e)
+  float* orot;             // [B, Hq, S, 128] fp32: normalised output, rotated domain
   const uint8_t* k_codes;  // [B, Hkv, cap, 64]
   const float* k_norms;    // [B, Hkv, cap]
   const uint8_t* v_codes;
@@ -56,9 +59,103 @@ struct PrefillParams {
   const uint16_t* hk;      // [B, Hkv, hot_cap, 128] fp16: hot keys @ PiK^T (ring slots)
   const uint16_t* hv;      // hot values @ PiV^T
   const float* centroids;  // [2^bits]
-  float scale_log2;        // scale * log2(e)
   int S, Hq, Hkv, G, cap, hot_cap, kv_len, cold_len, ncent;
 };
+
+// y = scale * (x @ Pi^T) (TRANS false) or scale * (x @ Pi) (TRANS true) for M
+// rows of 128, on fp16 MFMA: Pi split exactly into hi + lo / 2048 fp16 parts,
+// and x too when it is fp32, fp32 accumulate (error ~2^-22 relative, the
+// x_lo * Pi_lo term dropped).  Wave w computes output dims 32 w .. 32 w + 31 of
+// every 16-row tile the block takes; its Pi operands stay in registers.
+template <bool IN_F16, bool OUT_F16, bool TRANS>
+__global__ __launch_bounds__(kThreads) void rotate16_kernel(const void* __restrict__ x, int64_t M,
+                                                            const float* __restrict__ Pi, float scale,
+                                                            void* __restrict__ y) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, g = lane >> 4;
+  // B operands: column d = 32 wave + 16 dt + c16, k = input dim e = 32 kb + 8 g + i
+  u32x4 bh[2][4], bl[2][4];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int d = 32 * wave + 16 * dt + c16, e0 = 32 * kb + 8 * g;
+      float p[8];
+      if constexpr (!TRANS) {  // B[e][d] = Pi[d][e]
+        const float4 u0 = *reinterpret_cast<const float4*>(Pi + d * kD + e0);
+        const float4 u1 = *reinterpret_cast<const float4*>(Pi + d * kD + e0 + 4);
+        p[0] = u0.x; p[1] = u0.y; p[2] = u0.z; p[3] = u0.w;
+        p[4] = u1.x; p[5] = u1.y; p[6] = u1.z; p[7] = u1.w;
+      } else {  // B[e][d] = Pi[e][d]
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p[i] = Pi[(e0 + i) * kD + d];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint16_t h0 = f2h(p[2 * j]), h1 = f2h(p[2 * j + 1]);
+        bh[dt][kb][j] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+        bl[dt][kb][j] = pack2h((p[2 * j] - h2f(h0)) * 2048.f, (p[2 * j + 1] - h2f(h1)) * 2048.f);
+      }
+    }
+  const int64_t ntiles = (M + 15) / 16;
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t r = min(tile * 16 + c16, M - 1);  // A row (rows past M read the last row, not stored)
+    u32x4 ah[4], al[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      if constexpr (IN_F16) {
+        const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + r * kD + 32 * kb + 8 * g);
+        ah[kb] = u32x4{u.x, u.y, u.z, u.w};
+      } else {
+        const float* src = static_cast<const float*>(x) + r * kD + 32 * kb + 8 * g;
+        const float4 u0 = *reinterpret_cast<const float4*>(src), u1 = *reinterpret_cast<const float4*>(src + 4);
+        const float v[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint16_t h0 = f2h(v[2 * j]), h1 = f2h(v[2 * j + 1]);
+          ah[kb][j] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+          al[kb][j] = pack2h((v[2 * j] - h2f(h0)) * 2048.f, (v[2 * j + 1] - h2f(h1)) * 2048.f);
+        }
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}, accl = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        acc = mfma16x16x32(ah[kb], bh[dt][kb], acc);
+        accl = mfma16x16x32(ah[kb], bl[dt][kb], accl);
+        if constexpr (!IN_F16) accl = mfma16x16x32(al[kb], bh[dt][kb], accl);
+      }
+      // D: column d = 32 wave + 16 dt + c16, rows tile * 16 + 4 g + i
+      const int d = 32 * wave + 16 * dt + c16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = tile * 16 + 4 * g + i;
+        const float v = (acc[i] + accl[i] * (1.f / 2048.f)) * scale;
+        if (row < M) {
+          if constexpr (OUT_F16)
+            static_cast<uint16_t*>(y)[row * kD + d] = f2h(v);
+          else
+            static_cast<float*>(y)[row * kD + d] = v;
+        }
+      }
+    }
+  }
+}
+
+template <bool IN_F16, bool OUT_F16, bool TRANS>
+int rotate16(const void* x, int64_t M, const float* Pi, float scale, void* y, hipStream_t st) {
+  if (M <= 0) return LKV_OK;
+  int64_t g = (M + 15) / 16;
+  const int64_t cap = 4 * static_cast<int64_t>(device_cu_count());
+  if (g > cap) g = cap;
+  hipLaunchKernelGGL((rotate16_kernel<IN_F16, OUT_F16, TRANS>), dim3(static_cast<unsigned>(g)), dim3(kThreads), 0,
+                     st, x, M, Pi, scale, y);
+  LKV_LAUNCH_CHECK("tq_prefill_attn rotation");
+  return LKV_OK;
+}
 
 // fp16 positions 0..7 of a natural-order group reordered to kPermDim.
 __device__ __forceinline__ uint4 perm_group(uint4 a) {
@@ -68,10 +165,9 @@ __device__ __forceinline__ uint4 perm_group(uint4 a) {
 
 template <bool PERM>
 __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillParams P) {
-  __shared__ __align__(16) uint16_t sK[kKT * kKRow];
-  __shared__ __align__(16) uint16_t sVt[kD * kVRow];
-  __shared__ __align__(16) uint8_t sRaw[2 * kKT * kRowB];  // key codes, then value codes
-  __shared__ __align__(16) float sN[2][kKT];                 // key, value norms (1 for hot, 0 past the end)
+  __shared__ __align__(16) uint16_t sK[2 * kKT * kKRow];  // two buffers of decoded keys
+  __shared__ __align__(16) uint16_t sVt[2 * kD * kVRow];  // two buffers of transposed values
+  __shared__ __align__(16) float sN[2][2][kKT];           // [buffer][key, value] norms (1 hot, 0 past the end)
   __shared__ uint32_t s_lut[256];
   __shared__ uint16_t s_cent[16];
 
@@ -114,19 +210,13 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
     const bool ok = qq < P.S;
     lim[ct] = ok ? qpos0 + qq + 1 : 0;
     if (ok) wmin = min(wmin, lim[ct]);
-    const float* src =
-        P.rows + ((static_cast<size_t>(b) * P.Hq + kvh * G + hh) * P.S + min(qq, P.S - 1)) * kD + 8 * g;
+    const uint16_t* src =
+        P.q16 + ((static_cast<size_t>(b) * P.Hq + kvh * G + hh) * P.S + min(qq, P.S - 1)) * kD + 8 * g;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const float4 f0 = *reinterpret_cast<const float4*>(src + 32 * kb);
-      const float4 f1 = *reinterpret_cast<const float4*>(src + 32 * kb + 4);
-      const float x[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-      u32x4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d0 = PERM ? kPermDim[2 * j] : 2 * j, d1 = PERM ? kPermDim[2 * j + 1] : 2 * j + 1;
-        v[j] = pack2h(x[d0] * P.scale_log2, x[d1] * P.scale_log2);
-      }
+      uint4 u = *reinterpret_cast<const uint4*>(src + 32 * kb);
+      if constexpr (PERM) u = perm_group(u);
+      const u32x4 v = u32x4{u.x, u.y, u.z, u.w};
       qa[ct][kb] = ok ? v : u32x4{0u, 0u, 0u, 0u};
     }
   }
@@ -138,50 +228,46 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
   const int kend = qpos0 + min(q0 + QT, P.S);
   const int ntile = (kend + kKT - 1) / kKT;
 
-  // ---- staging: thread t loads 16 code bytes of key (t & 127) / 4 of the
-  // key (t < 128) or value side; threads < 64 one norm each.
-  const int side = tid >> 7, rr = (tid & 127) >> 2, cb = 16 * (tid & 3);
-  const uint8_t* codes = (side ? P.v_codes : P.k_codes) + bh * static_cast<size_t>(P.cap) * kRowB;
+  // ---- per-thread code registers of one key tile, loaded two tiles ahead:
+  //   kw   key codes of key tid / 8, bytes 8 (tid % 8) .. +8 (dims 16 (tid % 8) ..)
+  //   vw   value codes of keys 2 (tid % 16) + e, bytes 4 (tid / 16) .. +4 (dims 8 (tid / 16) ..)
+  //   nrm  threads < 64: key (tid < 32) or value norm of key tid % 32
+  const uint8_t* kcod = P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB;
+  const uint8_t* vcod = P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB;
   const float* norms = ((tid >> 5) & 1 ? P.v_norms : P.k_norms) + bh * static_cast<size_t>(P.cap);
-  auto load_raw = [&](int t0) -> uint4 {
-    if (cold_len <= 0) return uint4{0u, 0u, 0u, 0u};
-    const int tc = min(t0 + rr, cold_len - 1);  // clamped valid row; keys past cold_len are not decoded from it
-    return *reinterpret_cast<const uint4*>(codes + static_cast<size_t>(tc) * kRowB + cb);
+  const int kk = tid >> 3, part = tid & 7;  // key decode
+  const int kp = tid & 15, j4 = tid >> 4;   // value decode
+  struct TileRegs {
+    uint2 kw;
+    uint32_t vw[2];
+    float nrm;
   };
-  auto load_norm = [&](int t0) -> float {
-    const int tk = t0 + (tid & 31);
-    const float n = cold_len > 0 ? norms[min(tk, cold_len - 1)] : 0.f;
-    return tk < cold_len ? n : (tk < kv_len ? 1.f : 0.f);
-  };
-  uint4 raw = load_raw(0);
-  float nrm = tid < 64 ? load_norm(0) : 0.f;
-
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-  f32x4 o[2][8];
+  auto load_tile = [&](TileRegs& R, int t0) {
+    if (cold_len > 0) {  // rows past cold_len read the last cold row (valid memory), decoded from elsewhere
+      R.kw = *reinterpret_cast<const uint2*>(kcod + static_cast<size_t>(min(t0 + kk, cold_len - 1)) * kRowB + 8 * part);
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[ct][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (int it = 0; it < ntile; ++it) {
-    const int t0 = it * kKT;
-    // ---- stage the tile's codes and norms; then the next tile's loads
-    *reinterpret_cast<uint4*>(sRaw + side * kKT * kRowB + rr * kRowB + cb) = raw;
-    if (tid < 64) sN[tid >> 5][tid & 31] = nrm;
-    __syncthreads();  // also: every wave is done with the previous tile's sK / sVt
-    if (it + 1 < ntile) {
-      raw = load_raw(t0 + kKT);
-      if (tid < 64) nrm = load_norm(t0 + kKT);
+      for (int e = 0; e < 2; ++e)
+        R.vw[e] = *reinterpret_cast<const uint32_t*>(
+            vcod + static_cast<size_t>(min(t0 + 2 * kp + e, cold_len - 1)) * kRowB + 4 * j4);
     }
-    // ---- keys -> sK [key][dim] (kPermDim order within each 8-dim group with PERM)
+    if (tid < 64) {
+      const int tk = t0 + (tid & 31);
+      const float n = cold_len > 0 ? norms[min(tk, cold_len - 1)] : 0.f;
+      R.nrm = tk < cold_len ? n : (tk < kv_len ? 1.f : 0.f);
+    }
+  };
+  // decode a tile's registers into LDS buffer `buf`: keys [key][dim] (kPermDim
+  // order within 8-dim groups with PERM), values transposed [dim][key]
+  auto decode_tile = [&](const TileRegs& R, int t0, int buf) {
+    uint16_t* sKb = sK + buf * (kKT * kKRow);
+    uint16_t* sVb = sVt + buf * (kD * kVRow);
     {
-      const int kk = tid >> 3, part = tid & 7, tk = t0 + kk;
+      const int tk = t0 + kk;
       uint4 o0, o1;
       if (tk < cold_len) {
-        const uint2 w = *reinterpret_cast<const uint2*>(sRaw + kk * kRowB + 8 * part);
         uint32_t d0[4], d1[4];
-        decode_dw<PERM>(w.x, tab, s_lut, d0);
-        decode_dw<PERM>(w.y, tab, s_lut, d1);
+        decode_dw<PERM>(R.kw.x, tab, s_lut, d0);
+        decode_dw<PERM>(R.kw.y, tab, s_lut, d1);
         o0 = uint4{d0[0], d0[1], d0[2], d0[3]};
         o1 = uint4{d1[0], d1[1], d1[2], d1[3]};
       } else if (tk < kv_len) {
@@ -196,66 +282,74 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
       } else {
         o0 = o1 = uint4{0u, 0u, 0u, 0u};
       }
-      *reinterpret_cast<uint4*>(sK + kk * kKRow + 16 * part) = o0;
-      *reinterpret_cast<uint4*>(sK + kk * kKRow + 16 * part + 8) = o1;
+      *reinterpret_cast<uint4*>(sKb + kk * kKRow + 16 * part) = o0;
+      *reinterpret_cast<uint4*>(sKb + kk * kKRow + 16 * part + 8) = o1;
     }
-    // ---- values -> sVt [dim][key]: thread = dims 2j, 2j+1 of keys 8 kg .. 8 kg + 7
     {
-      const int j = tid & 63, kg = tid >> 6, tb = t0 + 8 * kg;
-      const uint8_t* vr = sRaw + kKT * kRowB + (8 * kg) * kRowB + j;
-      uint32_t r0[4], r1[4];  // fp16 pairs (keys 2e, 2e+1) of dim 2j and of dim 2j+1
-      if (tb + 8 <= cold_len) {
-        const uint32_t wa = vr[0] | (static_cast<uint32_t>(vr[kRowB]) << 8) |
-                            (static_cast<uint32_t>(vr[2 * kRowB]) << 16) | (static_cast<uint32_t>(vr[3 * kRowB]) << 24);
-        const uint32_t wb = vr[4 * kRowB] | (static_cast<uint32_t>(vr[5 * kRowB]) << 8) |
-                            (static_cast<uint32_t>(vr[6 * kRowB]) << 16) | (static_cast<uint32_t>(vr[7 * kRowB]) << 24);
+      const int tb = t0 + 2 * kp;
+      uint32_t pr[8];  // fp16 pair (key tb, key tb + 1) of dim 8 j4 + dd
+      if (tb + 2 <= cold_len) {
         if constexpr (PERM) {
-          // byte k of wa / wb is key k's byte j: low nibble dim 2j, high nibble dim 2j + 1
-          uint32_t da[4], db[4];
-          decode8(wa, tab, da);
-          decode8(wb, tab, db);
-          r0[0] = da[0]; r0[1] = da[1]; r0[2] = db[0]; r0[3] = db[1];
-          r1[0] = da[2]; r1[1] = da[3]; r1[2] = db[2]; r1[3] = db[3];
+          // decode8 pairs: [0] dims (0, 2), [1] (4, 6), [2] (1, 3), [3] (5, 7)
+          uint32_t a[4], c[4];
+          decode8(R.vw[0], tab, a);
+          decode8(R.vw[1], tab, c);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int dlo = (q & 1) * 4 + (q >> 1);  // first dim of pair q: 0, 4, 1, 5
+            pr[dlo] = __builtin_amdgcn_perm(c[q], a[q], 0x05040100u);
+            pr[dlo + 2] = __builtin_amdgcn_perm(c[q], a[q], 0x07060302u);
+          }
         } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t w = e < 2 ? wa : wb;
-            const uint32_t x0 = s_lut[(w >> (16 * (e & 1))) & 0xffu], x1 = s_lut[(w >> (16 * (e & 1) + 8)) & 0xffu];
-            r0[e] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
-            r1[e] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+          for (int bt = 0; bt < 4; ++bt) {
+            const uint32_t x0 = s_lut[(R.vw[0] >> (8 * bt)) & 0xffu], x1 = s_lut[(R.vw[1] >> (8 * bt)) & 0xffu];
+            pr[2 * bt] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+            pr[2 * bt + 1] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
           }
         }
       } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          uint32_t lo2 = 0u, hi2 = 0u;
+        for (int dd = 0; dd < 8; ++dd) pr[dd] = 0u;
 #pragma unroll
-          for (int k = 0; k < 2; ++k) {
-            const int tk = tb + 2 * e + k;
-            uint32_t lo = 0u, hi = 0u;
-            if (tk < cold_len) {
-              const uint32_t byte = vr[(2 * e + k) * kRowB];
-              lo = s_cent[byte & 15u];
-              hi = s_cent[byte >> 4];
-            } else if (tk < kv_len) {
-              const uint32_t pr = *reinterpret_cast<const uint32_t*>(
-                  P.hv + (bh * P.hot_cap + static_cast<size_t>(tk % P.hot_cap)) * kD + 2 * j);
-              lo = pr & 0xffffu;
-              hi = pr >> 16;
-            }
-            lo2 |= lo << (16 * k);
-            hi2 |= hi << (16 * k);
+        for (int e = 0; e < 2; ++e) {
+          const int tk = tb + e;
+          uint32_t v[8];
+          if (tk < cold_len) {
+#pragma unroll
+            for (int dd = 0; dd < 8; ++dd) v[dd] = s_cent[(R.vw[e] >> (4 * dd)) & 15u];
+          } else if (tk < kv_len) {
+            const uint4 h = *reinterpret_cast<const uint4*>(
+                P.hv + (bh * P.hot_cap + static_cast<size_t>(tk % P.hot_cap)) * kD + 8 * j4);
+            const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+            for (int dd = 0; dd < 8; ++dd) v[dd] = (w[dd >> 1] >> (16 * (dd & 1))) & 0xffffu;
+          } else {
+#pragma unroll
+            for (int dd = 0; dd < 8; ++dd) v[dd] = 0u;
           }
-          r0[e] = lo2;
-          r1[e] = hi2;
+#pragma unroll
+          for (int dd = 0; dd < 8; ++dd) pr[dd] |= v[dd] << (16 * e);
         }
       }
-      *reinterpret_cast<uint4*>(sVt + (2 * j) * kVRow + 8 * kg) = uint4{r0[0], r0[1], r0[2], r0[3]};
-      *reinterpret_cast<uint4*>(sVt + (2 * j + 1) * kVRow + 8 * kg) = uint4{r1[0], r1[1], r1[2], r1[3]};
+#pragma unroll
+      for (int dd = 0; dd < 8; ++dd) *reinterpret_cast<uint32_t*>(sVb + (8 * j4 + dd) * kVRow + 2 * kp) = pr[dd];
     }
-    __syncthreads();
+    if (tid < 64) sN[buf][tid >> 5][tid & 31] = R.nrm;
+  };
 
-    // ---- scores: S^T tiles [ct][tt] = keys 16 tt .. x columns of ct
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+  f32x4 o[2][8];
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[ct][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // one key tile from LDS buffer `buf`
+  auto compute_tile = [&](int t0, int buf) {
+    const uint16_t* sKb = sK + buf * (kKT * kKRow);
+    const uint16_t* sVb = sVt + buf * (kD * kVRow);
+    // scores: S^T tiles [ct][tt] = keys 16 tt .. x columns of ct
     f32x4 sc[2][2];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
@@ -265,15 +359,15 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(sK + (16 * tt + h16) * kKRow + 32 * kb + 8 * g);
+        const u32x4 a = *reinterpret_cast<const u32x4*>(sKb + (16 * tt + h16) * kKRow + 32 * kb + 8 * g);
         sc[0][tt] = mfma16x16x32(a, qa[0][kb], sc[0][tt]);
         sc[1][tt] = mfma16x16x32(a, qa[1][kb], sc[1][tt]);
       }
     // the lane's keys: t0 + 16 tt + 4 g + i, i.e. slot j = 4 tt + i
-    const f32x4 kn0 = *reinterpret_cast<const f32x4*>(&sN[0][4 * g]);
-    const f32x4 kn1 = *reinterpret_cast<const f32x4*>(&sN[0][16 + 4 * g]);
-    const f32x4 vn0 = *reinterpret_cast<const f32x4*>(&sN[1][4 * g]);
-    const f32x4 vn1 = *reinterpret_cast<const f32x4*>(&sN[1][16 + 4 * g]);
+    const f32x4 kn0 = *reinterpret_cast<const f32x4*>(&sN[buf][0][4 * g]);
+    const f32x4 kn1 = *reinterpret_cast<const f32x4*>(&sN[buf][0][16 + 4 * g]);
+    const f32x4 vn0 = *reinterpret_cast<const f32x4*>(&sN[buf][1][4 * g]);
+    const f32x4 vn1 = *reinterpret_cast<const f32x4*>(&sN[buf][1][16 + 4 * g]);
     const bool masked = t0 + kKT > wmin;  // wave-uniform
     u32x4 pb[2];
 #pragma unroll
@@ -311,19 +405,44 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
       pb[ct] = u32x4{pack2h(p[0] * vn0[0], p[1] * vn0[1]), pack2h(p[2] * vn0[2], p[3] * vn0[3]),
                      pack2h(p[4] * vn1[0], p[5] * vn1[1]), pack2h(p[6] * vn1[2], p[7] * vn1[3])};
     }
-    // ---- values: O^T tiles [ct][dt] += V^T (dims 16 dt .., the lane's 8 keys) x P^T
+    // values: O^T tiles [ct][dt] += V^T (dims 16 dt .., the lane's 8 keys) x P^T
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      const uint16_t* row = sVt + (16 * dt + h16) * kVRow;
+      const uint16_t* row = sVb + (16 * dt + h16) * kVRow;
       const uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * g);
       const uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * g);
       const u32x4 a = u32x4{lo.x, lo.y, hi.x, hi.y};
       o[0][dt] = mfma16x16x32(a, pb[0], o[0][dt]);
       o[1][dt] = mfma16x16x32(a, pb[1], o[1][dt]);
     }
+  };
+
+  // Two register sets and two LDS buffers in turn: tile it decodes from the
+  // registers loaded two tiles earlier into buffer it % 2, then the loads of
+  // tile it + 2 go out, one barrier, and the tile is computed.  Buffer it % 2
+  // was last read by the compute of tile it - 2, which every wave finished
+  // before the barrier of tile it - 1.
+  TileRegs ra, rb;
+  ra.kw = uint2{0u, 0u};
+  ra.vw[0] = ra.vw[1] = 0u;
+  ra.nrm = 0.f;
+  rb = ra;
+  load_tile(ra, 0);
+  if (ntile > 1) load_tile(rb, kKT);
+  for (int it = 0;;) {
+    decode_tile(ra, it * kKT, 0);
+    if (it + 2 < ntile) load_tile(ra, (it + 2) * kKT);
+    __syncthreads();
+    compute_tile(it * kKT, 0);
+    if (++it >= ntile) break;
+    decode_tile(rb, it * kKT, 1);
+    if (it + 2 < ntile) load_tile(rb, (it + 2) * kKT);
+    __syncthreads();
+    compute_tile(it * kKT, 1);
+    if (++it >= ntile) break;
   }
 
-  // ---- normalise and write the rotated rows over the block's own q_rot rows
+  // ---- normalise and write the rotated output rows
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
     const float L = xgroup_sum(l[ct]);
@@ -331,7 +450,7 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
     const int c = 32 * wave + 16 * ct + h16;
     const int qq = q0 + c / G, hh = c % G;
     if (qq < P.S) {
-      float* dst = P.rows + ((static_cast<size_t>(b) * P.Hq + kvh * G + hh) * P.S + qq) * kD + 4 * g;
+      float* dst = P.orot + ((static_cast<size_t>(b) * P.Hq + kvh * G + hh) * P.S + qq) * kD + 4 * g;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(dst + 16 * dt) = o[ct][dt] * inv;
     }
@@ -346,9 +465,10 @@ using namespace lkv;
 extern "C" size_t lkv_tq_prefill_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
                                                       int64_t hot_cap) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || hot_cap <= 0) return 0;
-  const size_t rows = static_cast<size_t>(B * Hq * S) * kD * 4;
+  auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+  const size_t rows = static_cast<size_t>(B * Hq * S) * kD;
   const size_t hot = static_cast<size_t>(B * Hkv * hot_cap) * kD * 2;
-  return (rows + 255) / 256 * 256 + 2 * ((hot + 255) / 256 * 256);
+  return al(rows * 2) + al(rows * 4) + 2 * al(hot);  // q_rot fp16, rotated output fp32, hot rings
 }
 
 extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const float* k_norms,
@@ -380,21 +500,25 @@ extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const 
   LKV_REQUIRE(workspace_bytes >= need, "tq_prefill_attn: workspace of %zu bytes required, got %zu", need,
               workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
+  auto al = [](size_t v) { return (v + 255) / 256 * 256; };
   const int64_t nrows = B * Hq * S;
-  float* rows = reinterpret_cast<float*>(ws);
-  uint16_t* hk = reinterpret_cast<uint16_t*>(ws + (static_cast<size_t>(nrows) * kD * 4 + 255) / 256 * 256);
-  const size_t hot_bytes = (static_cast<size_t>(B * Hkv * hot_cap) * kD * 2 + 255) / 256 * 256;
-  uint16_t* hv = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(hk) + hot_bytes);
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* q16 = reinterpret_cast<uint16_t*>(ws);
+  float* orot = reinterpret_cast<float*>(ws + al(static_cast<size_t>(nrows) * kD * 2));
+  uint16_t* hk = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(orot) + al(static_cast<size_t>(nrows) * kD * 4));
+  uint16_t* hv = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(hk) +
+                                             al(static_cast<size_t>(B * Hkv * hot_cap) * kD * 2));
   const int64_t cold_len = kv_len > hot_cap ? kv_len - hot_cap : 0;
 
-  if (int e = rotate_rows(q, true, nrows, PiK, 0, rows, false, st)) return e;
-  if (kv_len > cold_len) {  // the ring holds hot tokens: rotate every slot (only current ones are read)
-    if (int e = rotate_rows(k_hot, true, B * Hkv * hot_cap, PiK, 0, hk, true, st)) return e;
-    if (int e = rotate_rows(v_hot, true, B * Hkv * hot_cap, PiV, 0, hv, true, st)) return e;
+  // q_rot * scale * log2(e) in fp16 (the score operand); the hot rings in the rotated domains
+  if (int e = rotate16<true, true, false>(q, nrows, PiK, scale * kLog2e, q16, st)) return e;
+  if (kv_len > cold_len) {  // rotate every slot; only the current tokens' slots are read
+    if (int e = rotate16<true, true, false>(k_hot, B * Hkv * hot_cap, PiK, 1.f, hk, st)) return e;
+    if (int e = rotate16<true, true, false>(v_hot, B * Hkv * hot_cap, PiV, 1.f, hv, st)) return e;
   }
   PrefillParams P;
-  P.rows = rows;
+  P.q16 = q16;
+  P.orot = orot;
   P.k_codes = k_codes;
   P.k_norms = k_norms;
   P.v_codes = v_codes;
@@ -402,7 +526,6 @@ extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const 
   P.hk = hk;
   P.hv = hv;
   P.centroids = centroids;
-  P.scale_log2 = scale * kLog2e;
   P.S = static_cast<int>(S);
   P.Hq = static_cast<int>(Hq);
   P.Hkv = static_cast<int>(Hkv);
@@ -419,5 +542,5 @@ extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const 
   else
     hipLaunchKernelGGL((tq_prefill_attn_kernel<false>), grid, dim3(kThreads), 0, st, P);
   LKV_LAUNCH_CHECK("tq_prefill_attn");
-  return rotate_rows(rows, false, nrows, PiV, 1, out, true, st);
+  return rotate16<false, true, true>(orot, nrows, PiV, 1.f, out, st);
 }

@@ -443,6 +443,40 @@ def test_prefill_attn(cuda, B, Hq, Hkv, L, S, hot, bits):
     assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
 
 
+def test_prefill_attn_full_size(cuda):
+    """Config-5 layer shape: a 4096-token prompt (4032 cold 3-bit tokens + 64 hot), 32 query / 8 kv heads.
+    Reference: torch fp32 causal SDPA on the GPU over K/V dequantized by the fp64 oracle."""
+    from leankv_amd import kernels
+
+    B, Hq, Hkv, S, hot, D = 1, 32, 8, 4096, 64, 128
+    cold = S - hot
+    c, _ = oq.codebook_tensors(3)
+    PiK, PiV = oq.rotation_matrix(D, 42), oq.rotation_matrix(D, 43)
+    g = torch.Generator().manual_seed(11)
+    # codes: 3-bit values in both nibbles; norms ~ those of unit-variance 128-vectors
+    kc = (torch.randint(0, 8, (B, Hkv, cold, 64), generator=g) | (torch.randint(0, 8, (B, Hkv, cold, 64),
+                                                                               generator=g) << 4)).to(torch.uint8)
+    vc = (torch.randint(0, 8, (B, Hkv, cold, 64), generator=g) | (torch.randint(0, 8, (B, Hkv, cold, 64),
+                                                                               generator=g) << 4)).to(torch.uint8)
+    kn = torch.rand(B, Hkv, cold, generator=g) * 4 + 9
+    vn = torch.rand(B, Hkv, cold, generator=g) * 4 + 9
+    kh = torch.randn(B, Hkv, hot, D, generator=g).half()
+    vh = torch.randn(B, Hkv, hot, D, generator=g).half()
+    q = torch.randn(B, Hq, S, D, generator=g).half()
+    out = kernels.tq_prefill_attn(q.to(cuda), kc.to(cuda), kn.to(cuda), vc.to(cuda), vn.to(cuda), kh.to(cuda),
+                                  vh.to(cuda), PiK.to(cuda), PiV.to(cuda), c.to(cuda), 3, S).float()
+    order = [p % hot for p in range(cold, S)]
+    K = torch.cat([oq.dequantize(kc.numpy(), kn, PiK, c, 3).half(), kh[:, :, order]], dim=2)
+    V = torch.cat([oq.dequantize(vc.numpy(), vn, PiV, c, 3).half(), vh[:, :, order]], dim=2)
+    Kd = K.float().repeat_interleave(Hq // Hkv, dim=1).contiguous().to(cuda)
+    Vd = V.float().repeat_interleave(Hq // Hkv, dim=1).contiguous().to(cuda)
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float().to(cuda), Kd, Vd, is_causal=True)
+    assert torch.isfinite(out).all()
+    err = float((out - ref).norm() / ref.norm())
+    assert err < RTOL, err
+    assert float((out - ref).abs().max() / ref.abs().max()) < RTOL
+
+
 # Large batches (many (batch, kv head) pairs, few splits each): hot-only,
 # boundary and short cold ranges, a 16-token window, 16 query heads per kv head.
 @pytest.mark.parametrize("B,Hq,Hkv,L,hot", [(16, 32, 8, 1, 64), (16, 32, 8, 65, 64), (16, 32, 8, 700, 64),
