@@ -65,12 +65,19 @@ struct PrefillParams {
 // y = scale * (x @ Pi^T) (TRANS false) or scale * (x @ Pi) (TRANS true) for M
 // rows of 128, on fp16 MFMA: Pi split exactly into hi + lo / 2048 fp16 parts,
 // and x too when it is fp32, fp32 accumulate (error ~2^-22 relative, the
-// x_lo * Pi_lo term dropped).  Wave w computes output dims 32 w .. 32 w + 31 of
-// every 16-row tile the block takes; its Pi operands stay in registers.
+// x_lo * Pi_lo term dropped).  Wave w computes output dims 32 w .. 32 w + 31
+// with its Pi operands in registers; a block takes 64-row tiles, staged
+// through LDS both ways so every row is read once and written with 16-byte
+// stores.
+constexpr int kRotRows = 64;
 template <bool IN_F16, bool OUT_F16, bool TRANS>
 __global__ __launch_bounds__(kThreads) void rotate16_kernel(const void* __restrict__ x, int64_t M,
                                                             const float* __restrict__ Pi, float scale,
                                                             void* __restrict__ y) {
+  constexpr int kInB = IN_F16 ? 2 : 4, kOutB = OUT_F16 ? 2 : 4;
+  constexpr int kInRow = kD * kInB + 16, kOutRow = kD * kOutB + 16;  // padded LDS rows (bytes)
+  __shared__ __align__(16) uint8_t s_in[kRotRows * kInRow];
+  __shared__ __align__(16) uint8_t s_out[kRotRows * kOutRow];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c16 = lane & 15, g = lane >> 4;
@@ -98,58 +105,82 @@ __global__ __launch_bounds__(kThreads) void rotate16_kernel(const void* __restri
         bl[dt][kb][j] = pack2h((p[2 * j] - h2f(h0)) * 2048.f, (p[2 * j + 1] - h2f(h1)) * 2048.f);
       }
     }
-  const int64_t ntiles = (M + 15) / 16;
+  constexpr int kInChunks = kRotRows * kD * kInB / 16 / kThreads;    // 16-byte loads per thread
+  constexpr int kOutChunks = kRotRows * kD * kOutB / 16 / kThreads;  // 16-byte stores per thread
+  constexpr int kInPerRow = kD * kInB / 16, kOutPerRow = kD * kOutB / 16;
+  const int64_t ntiles = (M + kRotRows - 1) / kRotRows;
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int64_t r = min(tile * 16 + c16, M - 1);  // A row (rows past M read the last row, not stored)
-    u32x4 ah[4], al[4];
+    const int64_t row0 = tile * kRotRows;
+    // ---- rows in (rows past M read row M - 1, never stored)
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      if constexpr (IN_F16) {
-        const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + r * kD + 32 * kb + 8 * g);
-        ah[kb] = u32x4{u.x, u.y, u.z, u.w};
-      } else {
-        const float* src = static_cast<const float*>(x) + r * kD + 32 * kb + 8 * g;
-        const float4 u0 = *reinterpret_cast<const float4*>(src), u1 = *reinterpret_cast<const float4*>(src + 4);
-        const float v[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint16_t h0 = f2h(v[2 * j]), h1 = f2h(v[2 * j + 1]);
-          ah[kb][j] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
-          al[kb][j] = pack2h((v[2 * j] - h2f(h0)) * 2048.f, (v[2 * j + 1] - h2f(h1)) * 2048.f);
-        }
-      }
+    for (int c = 0; c < kInChunks; ++c) {
+      const int f = c * kThreads + tid, r = f / kInPerRow, q = f % kInPerRow;
+      const int64_t gr = min(row0 + r, M - 1);
+      const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(x) + gr * (kD * kInB) + 16 * q);
+      *reinterpret_cast<uint4*>(s_in + r * kInRow + 16 * q) = u;
     }
+    __syncthreads();
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
-      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}, accl = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rg = 0; rg < kRotRows / 16; ++rg) {
+      u32x4 ah[4], al[4];
+      const uint8_t* arow = s_in + (16 * rg + c16) * kInRow;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        acc = mfma16x16x32(ah[kb], bh[dt][kb], acc);
-        accl = mfma16x16x32(ah[kb], bl[dt][kb], accl);
-        if constexpr (!IN_F16) accl = mfma16x16x32(al[kb], bh[dt][kb], accl);
-      }
-      // D: column d = 32 wave + 16 dt + c16, rows tile * 16 + 4 g + i
-      const int d = 32 * wave + 16 * dt + c16;
+        if constexpr (IN_F16) {
+          const uint4 u = *reinterpret_cast<const uint4*>(arow + 2 * (32 * kb + 8 * g));
+          ah[kb] = u32x4{u.x, u.y, u.z, u.w};
+        } else {
+          const float4 u0 = *reinterpret_cast<const float4*>(arow + 4 * (32 * kb + 8 * g));
+          const float4 u1 = *reinterpret_cast<const float4*>(arow + 4 * (32 * kb + 8 * g) + 16);
+          const float v[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t row = tile * 16 + 4 * g + i;
-        const float v = (acc[i] + accl[i] * (1.f / 2048.f)) * scale;
-        if (row < M) {
+          for (int j = 0; j < 4; ++j) {
+            const uint16_t h0 = f2h(v[2 * j]), h1 = f2h(v[2 * j + 1]);
+            ah[kb][j] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+            al[kb][j] = pack2h((v[2 * j] - h2f(h0)) * 2048.f, (v[2 * j + 1] - h2f(h1)) * 2048.f);
+          }
+        }
+      }
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}, accl = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          acc = mfma16x16x32(ah[kb], bh[dt][kb], acc);
+          accl = mfma16x16x32(ah[kb], bl[dt][kb], accl);
+          if constexpr (!IN_F16) accl = mfma16x16x32(al[kb], bh[dt][kb], accl);
+        }
+        // D: column d = 32 wave + 16 dt + c16, rows 16 rg + 4 g + i
+        const int d = 32 * wave + 16 * dt + c16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = (acc[i] + accl[i] * (1.f / 2048.f)) * scale;
+          uint8_t* dst = s_out + (16 * rg + 4 * g + i) * kOutRow + kOutB * d;
           if constexpr (OUT_F16)
-            static_cast<uint16_t*>(y)[row * kD + d] = f2h(v);
+            *reinterpret_cast<uint16_t*>(dst) = f2h(v);
           else
-            static_cast<float*>(y)[row * kD + d] = v;
+            *reinterpret_cast<float*>(dst) = v;
         }
       }
     }
+    __syncthreads();
+    // ---- rows out
+#pragma unroll
+    for (int c = 0; c < kOutChunks; ++c) {
+      const int f = c * kThreads + tid, r = f / kOutPerRow, q = f % kOutPerRow;
+      if (row0 + r < M)
+        *reinterpret_cast<uint4*>(static_cast<uint8_t*>(y) + (row0 + r) * (kD * kOutB) + 16 * q) =
+            *reinterpret_cast<const uint4*>(s_out + r * kOutRow + 16 * q);
+    }
+    __syncthreads();  // s_in and s_out are rewritten by the next tile
   }
 }
 
 template <bool IN_F16, bool OUT_F16, bool TRANS>
 int rotate16(const void* x, int64_t M, const float* Pi, float scale, void* y, hipStream_t st) {
   if (M <= 0) return LKV_OK;
-  int64_t g = (M + 15) / 16;
-  const int64_t cap = 4 * static_cast<int64_t>(device_cu_count());
+  int64_t g = (M + kRotRows - 1) / kRotRows;
+  const int64_t cap = 2 * static_cast<int64_t>(device_cu_count());
   if (g > cap) g = cap;
   hipLaunchKernelGGL((rotate16_kernel<IN_F16, OUT_F16, TRANS>), dim3(static_cast<unsigned>(g)), dim3(kThreads), 0,
                      st, x, M, Pi, scale, y);
