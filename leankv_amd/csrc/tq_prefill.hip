@@ -42,11 +42,12 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kThreads = 256;
-constexpr int kKT = 32;         // keys per tile
+constexpr int kKT = 64;         // keys per tile
 constexpr int kCols = 128;      // (query, head) columns per block
 constexpr int kRowB = 64;       // code bytes per token (4-bit nibbles)
 constexpr int kKRow = kD + 8;   // fp16 row of the decoded key tile (padded)
 constexpr int kVRow = kKT + 4;  // fp16 row of the transposed value tile (padded: conflict-free 8-byte reads)
+static_assert(kKT == 64, "the decode / compute lane maps assume 64-key tiles");
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct PrefillParams {
@@ -260,29 +261,29 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
   const int ntile = (kend + kKT - 1) / kKT;
 
   // ---- per-thread code registers of one key tile, loaded two tiles ahead:
-  //   kw   key codes of key tid / 8, bytes 8 (tid % 8) .. +8 (dims 16 (tid % 8) ..)
-  //   vw   value codes of keys 2 (tid % 16) + e, bytes 4 (tid / 16) .. +4 (dims 8 (tid / 16) ..)
-  //   nrm  threads < 64: key (tid < 32) or value norm of key tid % 32
+  //   kw   key codes of key tid / 4, bytes 16 (tid % 4) .. +16 (dims 32 (tid % 4) ..)
+  //   vw   value codes of keys 4 (tid % 16) + e, bytes 4 (tid / 16) .. +4 (dims 8 (tid / 16) ..)
+  //   nrm  threads < 128: key (tid < 64) or value norm of key tid % 64
   const uint8_t* kcod = P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB;
   const uint8_t* vcod = P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB;
-  const float* norms = ((tid >> 5) & 1 ? P.v_norms : P.k_norms) + bh * static_cast<size_t>(P.cap);
-  const int kk = tid >> 3, part = tid & 7;  // key decode
+  const float* norms = ((tid >> 6) & 1 ? P.v_norms : P.k_norms) + bh * static_cast<size_t>(P.cap);
+  const int kk = tid >> 2, part = tid & 3;  // key decode
   const int kp = tid & 15, j4 = tid >> 4;   // value decode
   struct TileRegs {
-    uint2 kw;
-    uint32_t vw[2];
+    uint4 kw;
+    uint32_t vw[4];
     float nrm;
   };
   auto load_tile = [&](TileRegs& R, int t0) {
     if (cold_len > 0) {  // rows past cold_len read the last cold row (valid memory), decoded from elsewhere
-      R.kw = *reinterpret_cast<const uint2*>(kcod + static_cast<size_t>(min(t0 + kk, cold_len - 1)) * kRowB + 8 * part);
+      R.kw = *reinterpret_cast<const uint4*>(kcod + static_cast<size_t>(min(t0 + kk, cold_len - 1)) * kRowB + 16 * part);
 #pragma unroll
-      for (int e = 0; e < 2; ++e)
+      for (int e = 0; e < 4; ++e)
         R.vw[e] = *reinterpret_cast<const uint32_t*>(
-            vcod + static_cast<size_t>(min(t0 + 2 * kp + e, cold_len - 1)) * kRowB + 4 * j4);
+            vcod + static_cast<size_t>(min(t0 + 4 * kp + e, cold_len - 1)) * kRowB + 4 * j4);
     }
-    if (tid < 64) {
-      const int tk = t0 + (tid & 31);
+    if (tid < 128) {
+      const int tk = t0 + (tid & 63);
       const float n = cold_len > 0 ? norms[min(tk, cold_len - 1)] : 0.f;
       R.nrm = tk < cold_len ? n : (tk < kv_len ? 1.f : 0.f);
     }
@@ -294,56 +295,64 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
     uint16_t* sVb = sVt + buf * (kD * kVRow);
     {
       const int tk = t0 + kk;
-      uint4 o0, o1;
+      uint4 o[4];
       if (tk < cold_len) {
-        uint32_t d0[4], d1[4];
-        decode_dw<PERM>(R.kw.x, tab, s_lut, d0);
-        decode_dw<PERM>(R.kw.y, tab, s_lut, d1);
-        o0 = uint4{d0[0], d0[1], d0[2], d0[3]};
-        o1 = uint4{d1[0], d1[1], d1[2], d1[3]};
+        const uint32_t w[4] = {R.kw.x, R.kw.y, R.kw.z, R.kw.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t d[4];
+          decode_dw<PERM>(w[q], tab, s_lut, d);
+          o[q] = uint4{d[0], d[1], d[2], d[3]};
+        }
       } else if (tk < kv_len) {
         const uint4* src = reinterpret_cast<const uint4*>(
-            P.hk + (bh * P.hot_cap + static_cast<size_t>(tk % P.hot_cap)) * kD + 16 * part);
-        o0 = src[0];
-        o1 = src[1];
-        if constexpr (PERM) {
-          o0 = perm_group(o0);
-          o1 = perm_group(o1);
+            P.hk + (bh * P.hot_cap + static_cast<size_t>(tk % P.hot_cap)) * kD + 32 * part);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          o[q] = src[q];
+          if constexpr (PERM) o[q] = perm_group(o[q]);
         }
       } else {
-        o0 = o1 = uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = uint4{0u, 0u, 0u, 0u};
       }
-      *reinterpret_cast<uint4*>(sKb + kk * kKRow + 16 * part) = o0;
-      *reinterpret_cast<uint4*>(sKb + kk * kKRow + 16 * part + 8) = o1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) *reinterpret_cast<uint4*>(sKb + kk * kKRow + 32 * part + 8 * q) = o[q];
     }
     {
-      const int tb = t0 + 2 * kp;
-      uint32_t pr[8];  // fp16 pair (key tb, key tb + 1) of dim 8 j4 + dd
-      if (tb + 2 <= cold_len) {
-        if constexpr (PERM) {
-          // decode8 pairs: [0] dims (0, 2), [1] (4, 6), [2] (1, 3), [3] (5, 7)
-          uint32_t a[4], c[4];
-          decode8(R.vw[0], tab, a);
-          decode8(R.vw[1], tab, c);
+      const int tb = t0 + 4 * kp;
+      uint32_t pr[2][8];  // fp16 pairs (key tb + 2 hp, key tb + 2 hp + 1) of dim 8 j4 + dd
+      if (tb + 4 <= cold_len) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int dlo = (q & 1) * 4 + (q >> 1);  // first dim of pair q: 0, 4, 1, 5
-            pr[dlo] = __builtin_amdgcn_perm(c[q], a[q], 0x05040100u);
-            pr[dlo + 2] = __builtin_amdgcn_perm(c[q], a[q], 0x07060302u);
-          }
-        } else {
+        for (int hp = 0; hp < 2; ++hp) {
+          const uint32_t w0 = R.vw[2 * hp], w1 = R.vw[2 * hp + 1];
+          if constexpr (PERM) {
+            // decode8 pairs: [0] dims (0, 2), [1] (4, 6), [2] (1, 3), [3] (5, 7)
+            uint32_t a[4], c[4];
+            decode8(w0, tab, a);
+            decode8(w1, tab, c);
 #pragma unroll
-          for (int bt = 0; bt < 4; ++bt) {
-            const uint32_t x0 = s_lut[(R.vw[0] >> (8 * bt)) & 0xffu], x1 = s_lut[(R.vw[1] >> (8 * bt)) & 0xffu];
-            pr[2 * bt] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
-            pr[2 * bt + 1] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+            for (int q = 0; q < 4; ++q) {
+              const int dlo = (q & 1) * 4 + (q >> 1);  // first dim of pair q: 0, 4, 1, 5
+              pr[hp][dlo] = __builtin_amdgcn_perm(c[q], a[q], 0x05040100u);
+              pr[hp][dlo + 2] = __builtin_amdgcn_perm(c[q], a[q], 0x07060302u);
+            }
+          } else {
+#pragma unroll
+            for (int bt = 0; bt < 4; ++bt) {
+              const uint32_t x0 = s_lut[(w0 >> (8 * bt)) & 0xffu], x1 = s_lut[(w1 >> (8 * bt)) & 0xffu];
+              pr[hp][2 * bt] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+              pr[hp][2 * bt + 1] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+            }
           }
         }
       } else {
 #pragma unroll
-        for (int dd = 0; dd < 8; ++dd) pr[dd] = 0u;
+        for (int hp = 0; hp < 2; ++hp)
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
+          for (int dd = 0; dd < 8; ++dd) pr[hp][dd] = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
           const int tk = tb + e;
           uint32_t v[8];
           if (tk < cold_len) {
@@ -360,13 +369,14 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
             for (int dd = 0; dd < 8; ++dd) v[dd] = 0u;
           }
 #pragma unroll
-          for (int dd = 0; dd < 8; ++dd) pr[dd] |= v[dd] << (16 * e);
+          for (int dd = 0; dd < 8; ++dd) pr[e >> 1][dd] |= v[dd] << (16 * (e & 1));
         }
       }
 #pragma unroll
-      for (int dd = 0; dd < 8; ++dd) *reinterpret_cast<uint32_t*>(sVb + (8 * j4 + dd) * kVRow + 2 * kp) = pr[dd];
+      for (int dd = 0; dd < 8; ++dd)
+        *reinterpret_cast<uint2*>(sVb + (8 * j4 + dd) * kVRow + 4 * kp) = uint2{pr[0][dd], pr[1][dd]};
     }
-    if (tid < 64) sN[buf][tid >> 5][tid & 31] = R.nrm;
+    if (tid < 128) sN[buf][tid >> 6][tid & 63] = R.nrm;
   };
 
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
@@ -376,75 +386,80 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) o[ct][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // one key tile from LDS buffer `buf`
+  // one key tile from LDS buffer `buf`: the lane's keys are t0 + 16 tt + 4 g + i
+  // (tt 0..3, i 0..3); the value MFMA takes them in two halves of 32 keys
   auto compute_tile = [&](int t0, int buf) {
     const uint16_t* sKb = sK + buf * (kKT * kKRow);
     const uint16_t* sVb = sVt + buf * (kD * kVRow);
-    // scores: S^T tiles [ct][tt] = keys 16 tt .. x columns of ct
-    f32x4 sc[2][2];
+    f32x4 sc[2][4];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) sc[ct][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int tt = 0; tt < 4; ++tt) sc[ct][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         const u32x4 a = *reinterpret_cast<const u32x4*>(sKb + (16 * tt + h16) * kKRow + 32 * kb + 8 * g);
         sc[0][tt] = mfma16x16x32(a, qa[0][kb], sc[0][tt]);
         sc[1][tt] = mfma16x16x32(a, qa[1][kb], sc[1][tt]);
       }
-    // the lane's keys: t0 + 16 tt + 4 g + i, i.e. slot j = 4 tt + i
-    const f32x4 kn0 = *reinterpret_cast<const f32x4*>(&sN[buf][0][4 * g]);
-    const f32x4 kn1 = *reinterpret_cast<const f32x4*>(&sN[buf][0][16 + 4 * g]);
-    const f32x4 vn0 = *reinterpret_cast<const f32x4*>(&sN[buf][1][4 * g]);
-    const f32x4 vn1 = *reinterpret_cast<const f32x4*>(&sN[buf][1][16 + 4 * g]);
     const bool masked = t0 + kKT > wmin;  // wave-uniform
-    u32x4 pb[2];
+    u32x4 pb[2][2];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
-      float s[8];
+      float s[16];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[i] = sc[ct][0][i] * kn0[i];
-        s[4 + i] = sc[ct][1][i] * kn1[i];
+      for (int tt = 0; tt < 4; ++tt) {
+        const f32x4 kn = *reinterpret_cast<const f32x4*>(&sN[buf][0][16 * tt + 4 * g]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[4 * tt + i] = sc[ct][tt][i] * kn[i];
       }
       if (masked) {
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj)
+        for (int jj = 0; jj < 16; ++jj)
           s[jj] = t0 + 16 * (jj >> 2) + 4 * g + (jj & 3) < lim[ct] ? s[jj] : -INFINITY;
       }
       float mx = s[0];
 #pragma unroll
-      for (int jj = 1; jj < 8; ++jj) mx = vmax(mx, s[jj]);
+      for (int jj = 1; jj < 16; ++jj) mx = vmax(mx, s[jj]);
       mx = xgroup_max(mx);
       const float mn = fmaxf(m[ct], mx);
       const float mu = mn == -INFINITY ? 0.f : mn;
       const float alpha = fast_exp2(m[ct] - mu);
       m[ct] = mn;
-      float p[8], ps = 0.f;
+      float ps = 0.f;
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        p[jj] = fast_exp2(s[jj] - mu);
-        ps += p[jj];
+      for (int jj = 0; jj < 16; ++jj) {
+        s[jj] = fast_exp2(s[jj] - mu);
+        ps += s[jj];
       }
       l[ct] = l[ct] * alpha + ps;
       if (wave_ballot(alpha != 1.f) != 0) {
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) o[ct][dt] = o[ct][dt] * alpha;
       }
-      pb[ct] = u32x4{pack2h(p[0] * vn0[0], p[1] * vn0[1]), pack2h(p[2] * vn0[2], p[3] * vn0[3]),
-                     pack2h(p[4] * vn1[0], p[5] * vn1[1]), pack2h(p[6] * vn1[2], p[7] * vn1[3])};
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(&sN[buf][1][32 * hh + 4 * g]);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(&sN[buf][1][32 * hh + 16 + 4 * g]);
+        const float* p = s + 8 * hh;
+        pb[ct][hh] = u32x4{pack2h(p[0] * v0[0], p[1] * v0[1]), pack2h(p[2] * v0[2], p[3] * v0[3]),
+                           pack2h(p[4] * v1[0], p[5] * v1[1]), pack2h(p[6] * v1[2], p[7] * v1[3])};
+      }
     }
-    // values: O^T tiles [ct][dt] += V^T (dims 16 dt .., the lane's 8 keys) x P^T
+    // values: O^T tiles [ct][dt] += V^T (dims 16 dt .., the lane's 8 keys of half hh) x P^T
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const uint16_t* row = sVb + (16 * dt + h16) * kVRow;
-      const uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * g);
-      const uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * g);
-      const u32x4 a = u32x4{lo.x, lo.y, hi.x, hi.y};
-      o[0][dt] = mfma16x16x32(a, pb[0], o[0][dt]);
-      o[1][dt] = mfma16x16x32(a, pb[1], o[1][dt]);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(row + 32 * hh + 4 * g);
+        const uint2 hi = *reinterpret_cast<const uint2*>(row + 32 * hh + 16 + 4 * g);
+        const u32x4 a = u32x4{lo.x, lo.y, hi.x, hi.y};
+        o[0][dt] = mfma16x16x32(a, pb[0][hh], o[0][dt]);
+        o[1][dt] = mfma16x16x32(a, pb[1][hh], o[1][dt]);
+      }
     }
   };
 
@@ -454,8 +469,8 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
   // was last read by the compute of tile it - 2, which every wave finished
   // before the barrier of tile it - 1.
   TileRegs ra, rb;
-  ra.kw = uint2{0u, 0u};
-  ra.vw[0] = ra.vw[1] = 0u;
+  ra.kw = uint4{0u, 0u, 0u, 0u};
+  ra.vw[0] = ra.vw[1] = ra.vw[2] = ra.vw[3] = 0u;
   ra.nrm = 0.f;
   rb = ra;
   load_tile(ra, 0);
