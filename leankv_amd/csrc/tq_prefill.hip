@@ -20,7 +20,7 @@
 //   2. tq_prefill_attn_kernel: grid (query tiles, kv heads, batch), 4 waves.
 //      A block owns 128 (query, head) columns: 128 / G consecutive queries x
 //      the G heads of one kv head, 32 columns per wave.  It walks the keys in
-//      tiles of 32; per tile the block decodes the codes once into LDS --
+//      tiles of 64; per tile the block decodes the codes once into LDS --
 //      keys as [key][dim] fp16 centroid values, values transposed as
 //      [dim][key] -- and every wave runs, on v_mfma_f32_16x16x32_f16,
 //      * scores transposed, A = 16 keys x 32 dims from LDS, B = its rotated
