@@ -17,6 +17,8 @@ Workloads:
   prefill causal prefill attention of one config-5 layer over its packed cache (4096-token
           prompt, 32/8 heads; MFMA-bound, so 3 buffer sets), beside the reference path
           (dequantize + torch SDPA) on the same GPU
+  batched B=8 decode rows through one TEAL-sparse projection (config-1 shape), beside 8 single-row
+          GEMV calls and torch's dense GEMM
   copy    a 512 MiB device copy: the known-size reference for scaling PMC byte counters
 Every workload rotates >= 3 independent buffer sets (> 512 MB) so the 256 MB
 Infinity Cache cannot serve repeated launches.  A "step" is one launch of the
@@ -46,7 +48,7 @@ def _parse():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "mlp", "quant", "attn", "prefill",
-                                                                    "copy"])
+                                                                    "batched", "copy"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=32, help="decoder layers (config 5 uses 32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -420,6 +422,64 @@ def bench_attn(args, torch):
     }
 
 
+# ------------------------------------------------------------------ B > 1
+def bench_batched(args, torch):
+    """B=8 decode rows through one TEAL-sparse projection at the config-1 shape (W[4096,14336], each row
+    x ~Laplace(0,.05) with its own mask, threshold = the 40 % quantile of row 0): one
+    lkv_sparse_gemm_batched call reads the weight rows some row keeps once.  Timed beside it: 8
+    single-row sparse GEMV calls (what a per-row loop over the reference's kernel does) and torch's
+    dense fp16 GEMM of the same shape."""
+    from leankv_amd import kernels
+
+    dev = torch.device("cuda:0")
+    B, N, Z = 8, 4096, 14336
+    sets = []
+    for s_ in range(args.sets):
+        g = torch.Generator(device=dev).manual_seed(600 + s_)
+        W = (torch.randn(N, Z, generator=g, device=dev) * 0.02).half()
+        Wc = W.t().contiguous().t()
+        del W
+        torch.manual_seed(600 + s_)
+        X = torch.distributions.Laplace(0.0, 0.05).sample((B, Z)).half().to(dev)
+        t = torch.kthvalue(X[0].float().abs().cpu(), int(0.4 * Z)).values.item()
+        union = int(((X.float().abs() > t).any(dim=0)).sum())
+        sets.append((X, Wc, t, union, torch.empty(B, N, dtype=torch.float16, device=dev)))
+
+    def launch(i):
+        X, Wc, t, _, Y = sets[i]
+        kernels.sparse_gemm_batched_out(X, Wc, t, Y)
+
+    def per_row(i):
+        X, Wc, t, _, Y = sets[i]
+        for b in range(B):
+            kernels.sparse_gemv_out(X[b], Wc, t, Y[b])
+
+    def dense(i):
+        X, Wc, _, _, _ = sets[i]
+        return X @ Wc.t()
+
+    wall, _, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
+    kmean, kmed = _kernel_time(launch, len(sets), args.steps, args.warmup, torch)
+    rmean, _ = _kernel_time(per_row, len(sets), max(10, args.steps // 4), args.warmup, torch)
+    dmean, _ = _kernel_time(dense, len(sets), args.steps, args.warmup, torch)
+    union = statistics.mean(s[3] for s in sets)
+    alg = union * N * 2 + B * (Z + N) * 2
+    achieved = alg / (kmean * 1e-3) / 1e9
+    return {
+        "metric": "batched TEAL sparse GEMM HBM GB/s (B=8, W[4096,14336], 40% sparse rows)",
+        "value": round(achieved, 1), "unit": "GB/s", "ms_per_step": round(wall, 5), "higher_is_better": True,
+        "dtype": "f16 (fp32 accumulate)",
+        "config": {"workload": "batched_sparse_gemm", "B": B, "N": N, "Z": Z, "sparsity": 0.4,
+                   "union_rows_kept": round(union, 1), "alg_bytes_per_call": round(alg), "sets": len(sets)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "sparse_gemm_batched_kernel<8, BZ> + batched_reduce_kernel (one call)",
+                     "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3)},
+        "per_row_sparse_gemv_us": round(rmean * 1e3, 3), "speedup_vs_per_row": round(rmean / kmean, 3),
+        "dense_fp16_gemm_us": round(dmean * 1e3, 3),
+    }
+
+
 # ------------------------------------------------------------------ prefill
 def bench_prefill(args, torch):
     """Causal prefill attention of one config-5 layer over its packed 3-bit cache: B=1, 32 query / 8 kv
@@ -653,7 +713,7 @@ def main():
     else:
         _fill_gemv_defaults(args)
         fn = {"gemv": bench_gemv, "mlp": bench_mlp, "copy": bench_copy, "quant": bench_quant,
-              "attn": bench_attn, "prefill": bench_prefill}.get(args.workload)
+              "attn": bench_attn, "prefill": bench_prefill, "batched": bench_batched}.get(args.workload)
         if fn is None:
             print("bench.py: workload %s is not implemented yet" % args.workload, file=sys.stderr)
             sys.exit(2)

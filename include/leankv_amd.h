@@ -91,6 +91,21 @@ int lkv_sparse_gemv_chunks(int64_t N, int64_t Z);
 int lkv_sparse_gemv_partials(const void* x, const void* w_gate, const void* w_up, float t_gate, float t_up,
                              int64_t N, int64_t Z, float* partials, size_t partials_bytes, void* stream);
 
+/*
+ * batched_sparse_gemm (leankv/teal/kernels/sparse_gemv.py:184-226, kernel
+ * :92-138): B > 1 decode rows, each with its own TEAL mask, one weight.
+ *   y[b][n] = fp16( sum over z with |x[b][z]| > threshold of A[z][n] * x[b][z] )
+ * x: fp16 [B][Z] (rows contiguous); w: the column-major weight of
+ * lkv_sparse_gemv (row z of A[Z][N] holds the N weights of input z), N a
+ * multiple of 8; y: fp16 [B][N].  A weight row is read once for all batch rows
+ * that keep its activation (fp32 accumulate, chunk-ordered sums: equal to B
+ * lkv_sparse_gemv calls up to fp32 summation order, which follows the union
+ * of the batch's masks, so a row's last bits can depend on the other rows).
+ */
+size_t lkv_sparse_gemm_batched_workspace_bytes(int64_t B, int64_t N, int64_t Z);
+int lkv_sparse_gemm_batched(const void* x, const void* w, float threshold, int64_t B, int64_t N, int64_t Z,
+                            void* y, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* TurboQuant (MSE variant), head_dim 128                                    */
 /* ------------------------------------------------------------------------ */

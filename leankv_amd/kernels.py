@@ -74,6 +74,34 @@ def sparse_gemv(x: torch.Tensor, weight: torch.Tensor, threshold: float) -> torc
     return sparse_gemv_out(x, weight, threshold, out)
 
 
+def sparse_gemm_batched_out(x: torch.Tensor, weight: torch.Tensor, threshold: float, out: torch.Tensor) -> torch.Tensor:
+    """out[b] = W @ (x[b] * (|x[b]| > threshold)) for every row b of x[B, Z]; W[N, Z] column-major."""
+    N, Z = colmajor_rows(weight)
+    require_cuda(x, weight, out)
+    if x.dtype != torch.float16 or weight.dtype != torch.float16 or out.dtype != torch.float16:
+        raise LeanKVError("sparse_gemm_batched: x, weight and out must be float16")
+    if x.dim() != 2 or x.shape[1] != Z or not x.is_contiguous():
+        raise LeanKVError("sparse_gemm_batched: x must be a contiguous float16 [B, %d] tensor" % Z)
+    B = x.shape[0]
+    if tuple(out.shape) != (B, N) or not out.is_contiguous():
+        raise LeanKVError("sparse_gemm_batched: out must be a contiguous float16 [%d, %d] tensor" % (B, N))
+    lib = _lib_handle()
+    nbytes = lib.lkv_sparse_gemm_batched_workspace_bytes(B, N, Z)
+    ws = workspaces.get(x.device, "gemm_b", nbytes)
+    check(
+        lib.lkv_sparse_gemm_batched(ptr(x), ptr(weight), float(threshold), B, N, Z, ptr(out), ptr(ws), ws.numel(),
+                                    stream_handle(x.device)),
+        "lkv_sparse_gemm_batched",
+    )
+    return out
+
+
+def sparse_gemm_batched(x: torch.Tensor, weight: torch.Tensor, threshold: float) -> torch.Tensor:
+    N, _ = colmajor_rows(weight)
+    out = torch.empty(x.shape[0], N, dtype=torch.float16, device=x.device)
+    return sparse_gemm_batched_out(x, weight, threshold, out)
+
+
 def sparse_gemv_partials(x: torch.Tensor, w_gate: torch.Tensor, t_gate: float, w_up: torch.Tensor | None = None,
                          t_up: float = 0.0, out: torch.Tensor | None = None) -> torch.Tensor:
     """Split-K partial sums only: fp32 [mats, N/256 slabs, chunks, 256] (mats = 2 with w_up).

@@ -37,12 +37,11 @@ def sparse_gemv(x: torch.Tensor, weight: torch.Tensor, threshold: float, sparsit
 
 def batched_sparse_gemm(x: torch.Tensor, weight: torch.Tensor, threshold: float,
                         sparsity_bin: int = 5) -> torch.Tensor:
-    """[B, N]: each row of x[B, Z] gets its own mask (one sparse GEMV per row)."""
+    """[B, N]: each row of x[B, Z] gets its own mask (sparse_gemv.py:184-226); one pass over the weight
+    rows some row keeps (lkv_sparse_gemm_batched).  sparsity_bin is the reference's autotune key, unused."""
     N, Z = weight.shape
-    xs = x.reshape(-1, Z)
-    out = torch.empty(xs.shape[0], N, dtype=torch.float16, device=x.device)
-    for b in range(xs.shape[0]):
-        _k.sparse_gemv_out(xs[b].to(torch.float16), weight, threshold, out[b])
+    xs = x.reshape(-1, Z).to(torch.float16).contiguous()
+    out = _k.sparse_gemm_batched(xs, weight, threshold)
     return out if x.dtype == torch.float16 else out.to(x.dtype)
 
 

@@ -87,6 +87,13 @@ def test_invalid_arguments_rejected_without_launch():
                                    1024, None) == -1
     assert "workspace" in _lib.last_error()
     assert lib.lkv_tq_prefill_attn_workspace_bytes(1, 32, 8, 4096, 64) >= 32 * 4096 * 128 * 4
+    # batched sparse GEMM: N not a multiple of 8, workspace too small for a multi-chunk problem
+    assert lib.lkv_sparse_gemm_batched(p, p, 0.1, 4, 12, 16, p, p, 1 << 20, None) == -1
+    assert "multiple of 8" in _lib.last_error()
+    assert lib.lkv_sparse_gemm_batched(p, p, 0.1, 4, 4096, 14336, p, p, 1024, None) == -1
+    assert "workspace" in _lib.last_error()
+    assert lib.lkv_sparse_gemm_batched_workspace_bytes(4, 4096, 14336) > 4 * 4096 * 4
+    assert lib.lkv_sparse_gemm_batched(p, p, 0.1, 0, 4096, 14336, p, p, 0, None) == 0
     # empty problems are no-ops
     assert lib.lkv_tq_prefill_attn(p, p, p, p, p, p, p, p, p, p, 3, 100, 1, 8, 2, 0, 64, 64, 0.1, p, p, 0, None) == 0
     assert lib.lkv_sparse_gemv(p, p, 0.1, 0, 16, p, p, 0, None) == 0

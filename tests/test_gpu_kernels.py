@@ -73,6 +73,54 @@ def test_sparse_gemv_all_dropped_and_all_kept(cuda):
     assert ot.rel_err(yd.numpy(), ref.numpy()) < 1e-3
 
 
+def _batched_case(B, N, Z, q, seed, dev):
+    """B Laplace activation rows (each its own mask) against one weight; threshold = the q-quantile of row 0."""
+    from leankv_amd import kernels
+
+    g = torch.Generator().manual_seed(seed)
+    W = (torch.randn(N, Z, generator=g) * 0.02).to(torch.float16)
+    torch.manual_seed(seed)
+    X = torch.distributions.Laplace(0.0, 0.05).sample((B, Z)).to(torch.float16)
+    k = int(q * Z)
+    t = torch.kthvalue(X[0].float().abs(), k).values.item() if k > 0 else 0.0
+    wc = W.to(dev).t().contiguous().t()
+    Y = kernels.sparse_gemm_batched(X.to(dev), wc, t).cpu()
+    ref = np.stack([ot.sparse_gemv(X[b].numpy(), W.numpy(), t) for b in range(B)])
+    return Y, ref, X, W, t, wc
+
+
+# B in 1 .. 13 (groups of up to 8 rows per block, a partial last group), single-chunk and many-chunk
+# shapes, a ragged N, dense (q = 0) and 90 % sparse rows.
+@pytest.mark.parametrize("B,N,Z,q", [(2, 4096, 14336, 0.4), (4, 1024, 4096, 0.4), (8, 14336, 4096, 0.4),
+                                     (3, 1032, 333, 0.3), (13, 2048, 1000, 0.5), (1, 520, 7000, 0.9),
+                                     (5, 24, 257, 0.0), (16, 4096, 4096, 0.4)])
+def test_sparse_gemm_batched(cuda, B, N, Z, q):
+    Y, ref, X, W, t, wc = _batched_case(B, N, Z, q, seed=B * 100 + N % 97, dev=cuda)
+    assert ot.rel_err(Y.numpy(), ref) < 1e-3
+    assert ot.max_rel_err(Y.numpy(), ref) < RTOL
+
+
+def test_sparse_gemm_batched_rows_equal_single_gemv(cuda):
+    """Each output row is that row's own sparse GEMV (fp32 accumulation, up to summation order); a row
+    whose activations all fall at or below the threshold gives exactly zero; the other rows keep their
+    values (not their last bits: the union of the masks sets the summation order); the reference's
+    wrapper (batched_sparse_gemm) routes here."""
+    from leankv_amd import kernels
+    from leankv_amd.teal.kernels.sparse_gemv import batched_sparse_gemm
+
+    Y, ref, X, W, t, wc = _batched_case(6, 4096, 14336, 0.4, seed=77, dev=cuda)
+    for b in range(6):
+        yb = kernels.sparse_gemv(X[b].to(cuda), wc, t).cpu()
+        assert ot.rel_err(Y[b].numpy(), yb.numpy()) < 1e-3
+    Xz = X.clone()
+    Xz[2] = 0
+    Yz = kernels.sparse_gemm_batched(Xz.to(cuda), wc, t).cpu()
+    assert torch.count_nonzero(Yz[2]) == 0
+    for b in (0, 1, 3, 4, 5):
+        assert ot.rel_err(Yz[b].numpy(), Y[b].numpy()) < 1e-3
+    assert torch.equal(batched_sparse_gemm(X.to(cuda), wc, t, 5).cpu(), Y)
+
+
 def test_sparse_gemv_deterministic_and_reusable_workspace(cuda):
     W, x, t = _seeded_gemv(4096, 14336, seed=9)
     a = _gemv(x, W, t, cuda)
