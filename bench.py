@@ -19,6 +19,8 @@ Workloads:
           (dequantize + torch SDPA) on the same GPU
   batched B=8 decode rows through one TEAL-sparse projection (config-1 shape), beside 8 single-row
           GEMV calls and torch's dense GEMM
+  paged   batch decode attention on the paged fp16 pool (B=16, 4096 tokens, 16-token pages),
+          beside torch SDPA on the same K/V held dense
   copy    a 512 MiB device copy: the known-size reference for scaling PMC byte counters
 Every workload rotates >= 3 independent buffer sets (> 512 MB) so the 256 MB
 Infinity Cache cannot serve repeated launches.  A "step" is one launch of the
@@ -48,7 +50,7 @@ def _parse():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "mlp", "quant", "attn", "prefill",
-                                                                    "batched", "copy"])
+                                                                    "batched", "paged", "copy"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=32, help="decoder layers (config 5 uses 32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -480,6 +482,61 @@ def bench_batched(args, torch):
     }
 
 
+# ------------------------------------------------------------------ paged
+def bench_paged(args, torch):
+    """Batch decode attention on the paged fp16 pool (PagedKVCache.decode_attention, paged_cache.py:194-257):
+    B=16 sequences of 4096 tokens, 32 query / 8 kv heads, 16-token pages scattered over the pool (seeded
+    permutation).  Beside it on the same GPU: torch SDPA over the same K/V already dense (no gather), i.e.
+    what a dense fp16 cache pays for the same attention."""
+    from leankv_amd import kernels
+
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, D, L, ps = 16, 32, 8, 128, 4096, 16
+    npg = L // ps
+    sets = []
+    for s_ in range(3):
+        g = torch.Generator(device=dev).manual_seed(700 + s_)
+        pool = torch.randn(B * npg, 2, ps, Hkv, D, generator=g, device=dev).half()
+        perm = torch.randperm(B * npg, generator=g, device=dev).to(torch.int32)
+        indptr = torch.arange(0, B * npg + 1, npg, dtype=torch.int32, device=dev)
+        last = torch.full((B,), ps, dtype=torch.int32, device=dev)
+        q = torch.randn(B, Hq, D, generator=g, device=dev).half()
+        pg = perm.long().view(B, npg)
+        K = pool[pg, 0].reshape(B, L, Hkv, D).permute(0, 2, 1, 3).contiguous()
+        V = pool[pg, 1].reshape(B, L, Hkv, D).permute(0, 2, 1, 3).contiguous()
+        sets.append((q, pool, indptr, perm, last, torch.empty_like(q), K, V))
+
+    def launch(i):
+        q, pool, indptr, perm, last, out, _, _ = sets[i]
+        kernels.paged_decode_attn(q, pool, indptr, perm, last, L, D ** -0.5, out)
+
+    def dense(i):
+        q, _, _, _, _, _, K, V = sets[i]
+        return torch.nn.functional.scaled_dot_product_attention(q.unsqueeze(2), K, V, enable_gqa=True)
+
+    q0, _, _, _, _, out0, K0, V0 = sets[0]
+    launch(0)
+    ref0 = dense(0).squeeze(2).float()
+    agree = float((out0.float() - ref0).norm() / ref0.norm())
+    wall, _, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
+    kmean, kmed = _kernel_time(launch, len(sets), args.steps, args.warmup, torch)
+    dmean, _ = _kernel_time(dense, len(sets), args.steps, args.warmup, torch)
+    alg = B * Hkv * L * D * 2 * 2 + 2 * B * Hq * D * 2
+    achieved = alg / (kmean * 1e-3) / 1e9
+    return {
+        "metric": "paged fp16 KV decode attention HBM GB/s (B=16, 32/8 heads, 4096 tokens, 16-token pages)",
+        "value": round(achieved, 1), "unit": "GB/s", "ms_per_step": round(wall, 5), "higher_is_better": True,
+        "dtype": "fp16 KV, fp16 MFMA scores, fp32 softmax and value sums",
+        "config": {"workload": "paged_decode_attention", "batch": B, "heads": "32/8", "tokens": L, "page_size": ps,
+                   "alg_bytes_per_call": alg, "sets": len(sets)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "paged_split_kernel + paged_combine_kernel (one call)",
+                     "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3)},
+        "dense_sdpa_us": round(dmean * 1e3, 3), "rel_diff_vs_dense_sdpa": round(agree, 6),
+    }
+
+
 # ------------------------------------------------------------------ prefill
 def bench_prefill(args, torch):
     """Causal prefill attention of one config-5 layer over its packed 3-bit cache: B=1, 32 query / 8 kv
@@ -713,7 +770,8 @@ def main():
     else:
         _fill_gemv_defaults(args)
         fn = {"gemv": bench_gemv, "mlp": bench_mlp, "copy": bench_copy, "quant": bench_quant,
-              "attn": bench_attn, "prefill": bench_prefill, "batched": bench_batched}.get(args.workload)
+              "attn": bench_attn, "prefill": bench_prefill, "batched": bench_batched,
+              "paged": bench_paged}.get(args.workload)
         if fn is None:
             print("bench.py: workload %s is not implemented yet" % args.workload, file=sys.stderr)
             sys.exit(2)

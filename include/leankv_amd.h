@@ -229,6 +229,25 @@ int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const float* k_no
                         int64_t cap, int64_t hot_cap, float scale, void* out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Batch decode attention over a paged fp16 KV pool (one layer), the kernel
+ * PagedKVCache.decode_attention runs (leankv/turboquant/paged_cache.py:194-257,
+ * there FlashInfer BatchDecodeWithPagedKVCacheWrapper, NHD layout, no
+ * positional encoding).  kv_data: fp16 [max_pages][2 (K, V)][page_size][Hkv][128];
+ * sequence b owns pages kv_indices[kv_indptr[b] .. kv_indptr[b + 1]) (int32,
+ * device) and its last page holds kv_last_page_len[b] tokens (1 .. page_size).
+ * q fp16 [B, Hq, 128] -> out fp16 [B, Hq, 128] = softmax(q K^T * scale) V,
+ * query head h reading kv head h / (Hq / Hkv), Hq / Hkv <= 16.  max_len (host)
+ * bounds every sequence length and sizes the launch.  Page ids outside
+ * [0, max_pages) are clamped; kv_indptr must index inside kv_indices.
+ */
+size_t lkv_paged_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len);
+int lkv_paged_decode_attn(const void* q, const void* kv_data, const int32_t* kv_indptr,
+                          const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                          int64_t B, int64_t Hq, int64_t Hkv, int64_t page_size, int64_t max_pages,
+                          int64_t max_len, float scale, void* out, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Fused B=1 decode step                                                     */
 /* ------------------------------------------------------------------------ */

@@ -1,0 +1,345 @@
+// Batch decode attention over a paged fp16 KV cache (one layer).
+//
+// Reference: leankv/turboquant/paged_cache.py:194-257 (PagedKVCache.
+// decode_attention: FlashInfer BatchDecodeWithPagedKVCacheWrapper.plan + run,
+// NHD layout, no positional encoding, default scale 1/sqrt(128)) over the page
+// pool kv_data[layer] = [max_pages][2 (K, V)][page_size][Hkv][128] fp16 and
+// the CSR page table FlashInfer takes: sequence b owns pages
+// indices[indptr[b] .. indptr[b + 1]) and its last page holds last_len[b]
+// (1 .. page_size) tokens.  Output: softmax(q K^T * scale) V per query head,
+// GQA (query head h reads kv head h / (Hq / Hkv)).
+//
+// Launches: split kernel, grid (splits, kv heads, batch), 4 waves; each wave
+// walks 32-token chunks of its split:
+//   * scores on v_mfma_f32_16x16x32_f16, transposed as in the packed decode
+//     kernel: A = 16 tokens x 32 dims straight from the pages (one 16-byte
+//     load per lane, page looked up per token), B = the query (16 head
+//     columns, G used), so a lane holds one head's scores for 8 tokens;
+//   * online softmax per lane (exp2 domain, max / sum across the 4 lanes of
+//     a head by permlane swaps); the chunk's probabilities go to the wave's
+//     LDS slice;
+//   * values on the VALU: lane (8-dim group, head) streams the chunk's value
+//     rows with 16-byte loads and accumulates p * v (fp32);
+// the 4 waves merge through LDS into one (m, l, o[G][128]) record per split;
+// then a combine kernel, one block per (batch, query head), merges the split
+// records.  Page indices are clamped to the pool, lengths to the pages owned,
+// so malformed tables cannot address memory outside the pool.
+#include "kernels.h"
+#include "tq_attn_common.h"
+
+namespace lkv {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kChunk = 32;
+constexpr int kORow = kD + 4;
+constexpr int kMaxSplits = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct PagedParams {
+  const uint16_t* q;        // [B, Hq, 128] fp16
+  const uint16_t* kv;       // [max_pages, 2, ps, Hkv, 128] fp16
+  const int32_t* indptr;    // [B + 1]
+  const int32_t* indices;   // page ids
+  const int32_t* last_len;  // [B]
+  float* partials;          // [B, Hkv, nsplit, G (2 + 128)]
+  uint16_t* out;            // [B, Hq, 128] fp16
+  float scale_log2;
+  int Hq, Hkv, G, ps, nsplit, split_tokens, max_pages;
+};
+
+__device__ __forceinline__ int rec_floats(int G) { return G * (2 + kD); }
+
+// Tokens of sequence b (0 without pages); its first page-table entry.
+__device__ __forceinline__ int seq_tokens(const PagedParams& P, int b, int& first) {
+  first = P.indptr[b];
+  const int np = P.indptr[b + 1] - first;
+  if (np <= 0) return 0;
+  const int last = min(max(P.last_len[b], 0), P.ps);
+  return (np - 1) * P.ps + last;
+}
+
+// Element offset of (token t, kv head, K or V) in the pool.
+__device__ __forceinline__ size_t kv_offset(const PagedParams& P, int first, int t, int kvh, int side) {
+  const int page = min(max(P.indices[first + t / P.ps], 0), P.max_pages - 1);
+  const int slot = t % P.ps;
+  return ((static_cast<size_t>(page) * 2 + side) * P.ps + slot) * (static_cast<size_t>(P.Hkv) * kD) +
+         static_cast<size_t>(kvh) * kD;
+}
+
+__global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
+  __shared__ float s_p[kWaves][16][kChunk];
+  __shared__ size_t s_off[kWaves][kChunk];  // pool offset of each chunk token's value row
+  __shared__ float s_alpha[kWaves][16];
+  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+  __shared__ __align__(16) float s_o[kWaves][16][kORow];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int G = P.G;
+  const int h = lane & 15, g = lane >> 4;  // score layout: head column, token group
+  const int dg = lane >> 2, hq = lane & 3;  // value layout: 8-dim group, head slot
+  float* rec = P.partials + ((static_cast<size_t>(b) * P.Hkv + kvh) * P.nsplit + split) * rec_floats(G);
+
+  int first;
+  const int len = seq_tokens(P, b, first);
+  const int t_begin = split * P.split_tokens;
+  const int t_end = min(t_begin + P.split_tokens, len);
+  if (t_begin >= t_end) {  // uniform: nothing of this sequence in this split
+    if (tid < G) {
+      rec[tid] = -INFINITY;
+      rec[G + tid] = 0.f;
+    }
+    return;
+  }
+
+  // B operand: query x scale * log2(e), head h (rows h >= G zero), dims 32 kb + 8 g + i
+  u32x4 qa[4];
+  {
+    const uint16_t* qrow = P.q + (static_cast<size_t>(b) * P.Hq + kvh * G + min(h, G - 1)) * kD + 8 * g;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const uint4 u = *reinterpret_cast<const uint4*>(qrow + 32 * kb);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+      u32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        v[j] = pack2h(h2f(static_cast<uint16_t>(w[j] & 0xffffu)) * P.scale_log2,
+                      h2f(static_cast<uint16_t>(w[j] >> 16)) * P.scale_log2);
+      qa[kb] = h < G ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  float m = -INFINITY, lsum = 0.f;  // per lane: head h
+  float acc[4][8];                  // per lane: heads hq + 4 k, dims 8 dg ..
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[k][j] = 0.f;
+
+  for (int c = t_begin + kChunk * wave; c < t_end; c += kChunk * kWaves) {
+    // ---- scores: tokens c + 16 tt + (lane % 16) as A rows
+    f32x4 sc[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int tok = min(c + 16 * tt + h, t_end - 1);  // clamped valid token, masked below
+      const size_t off = kv_offset(P, first, tok, kvh, 0);
+      if (g == 0) s_off[wave][16 * tt + h] = off + static_cast<size_t>(P.ps) * P.Hkv * kD;  // its value row
+      const uint16_t* kp = P.kv + off + 8 * g;
+      u32x4 a[4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const uint4 u = *reinterpret_cast<const uint4*>(kp + 32 * kb);
+        a[kb] = u32x4{u.x, u.y, u.z, u.w};
+      }
+      sc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) sc[tt] = mfma16x16x32(a[kb], qa[kb], sc[tt]);
+    }
+    // D: lane holds head h, tokens c + 16 tt + 4 g + i
+    float s[8];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[4 * tt + i] = c + 16 * tt + 4 * g + i < t_end ? sc[tt][i] : -INFINITY;
+    float mx = s[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) mx = vmax(mx, s[j]);
+    mx = xgroup_max(mx);
+    const float mn = fmaxf(m, mx);  // finite: the chunk holds at least one token
+    const float alpha = fast_exp2(m - mn);
+    m = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = fast_exp2(s[4 * tt + i] - mn);
+        ps += p;
+        s_p[wave][h][16 * tt + 4 * g + i] = p;
+      }
+    lsum = lsum * alpha + ps;
+    if (g == 0) s_alpha[wave][h] = alpha;
+    __builtin_amdgcn_wave_barrier();
+    // ---- values: lane (dims 8 dg .., heads hq + 4 k) over the chunk's tokens
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float al = s_alpha[wave][hq + 4 * k];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[k][j] *= al;
+    }
+    // the chunk's 32 value rows, 8 loads in flight per group; tokens past the
+    // end read the last valid row (clamped offsets) with p = 0
+#pragma unroll
+    for (int t0 = 0; t0 < kChunk; t0 += 8) {
+      uint4 u[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) u[i] = *reinterpret_cast<const uint4*>(P.kv + s_off[wave][t0 + i] + 8 * dg);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[2 * e] = h2f(static_cast<uint16_t>(w[e] & 0xffffu));
+          v[2 * e + 1] = h2f(static_cast<uint16_t>(w[e] >> 16));
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (hq + 4 * k < G) {  // lanes past the G heads skip
+            const float p = s_p[wave][hq + 4 * k][t0 + i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[k][j] = fmaf(p, v[j], acc[k][j]);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // ---- merge the 4 waves (a wave without a chunk keeps m = -inf, l = 0, o = 0)
+  const float ltot = xgroup_sum(lsum);
+  if (g == 0) {
+    s_m[wave][h] = m;
+    s_l[wave][h] = ltot;
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float4* dst = reinterpret_cast<float4*>(&s_o[wave][hq + 4 * k][8 * dg]);
+    dst[0] = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+    dst[1] = make_float4(acc[k][4], acc[k][5], acc[k][6], acc[k][7]);
+  }
+  __syncthreads();
+  for (int e = tid; e < G * kD; e += kThreads) {
+    const int hh = e / kD, d = e % kD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hh]);
+    float o = 0.f, l = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float wt = s_m[w][hh] == -INFINITY ? 0.f : fast_exp2(s_m[w][hh] - M);
+        o += wt * s_o[w][hh][d];
+        l += wt * s_l[w][hh];
+      }
+    }
+    rec[2 * G + hh * kD + d] = o;
+    if (d == 0) {
+      rec[hh] = M;
+      rec[G + hh] = l;
+    }
+  }
+}
+
+// One block of 128 threads per (query head, batch): merge the split records.
+__global__ __launch_bounds__(kD) void paged_combine_kernel(PagedParams P) {
+  __shared__ float s_w[kMaxSplits];
+  __shared__ float s_red[2];
+  const int d = threadIdx.x, hq = blockIdx.x, b = blockIdx.y;
+  const int G = P.G, kvh = hq / G, hh = hq % G, ns = P.nsplit, RF = rec_floats(G);
+  const float* recs = P.partials + (static_cast<size_t>(b) * P.Hkv + kvh) * ns * RF;
+  if (d == 0) {
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, recs[s * RF + hh]);
+    float L = 0.f;
+    for (int s = 0; s < ns; ++s) {
+      const float ms = recs[s * RF + hh];
+      const float w = ms == -INFINITY ? 0.f : fast_exp2(ms - M);
+      s_w[s] = w;
+      L += w * recs[s * RF + G + hh];
+    }
+    s_red[0] = L;
+  }
+  __syncthreads();
+  float o = 0.f;
+  for (int s = 0; s < ns; ++s) {
+    const float w = s_w[s];
+    const float v = recs[s * RF + 2 * G + hh * kD + d];
+    o += w != 0.f ? w * v : 0.f;  // a split with no tokens left its o unwritten
+  }
+  const float L = s_red[0];
+  P.out[(static_cast<size_t>(b) * P.Hq + hq) * kD + d] = f2h(L > 0.f ? o / L : 0.f);
+}
+
+struct PagedPlan {
+  int nsplit, split_tokens;
+  size_t bytes;
+};
+
+PagedPlan paged_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len) {
+  PagedPlan p{};
+  const int64_t target = 2 * static_cast<int64_t>(device_cu_count());
+  int64_t ns = (target + B * Hkv - 1) / (B * Hkv);
+  ns = ns < 1 ? 1 : (ns > kMaxSplits ? kMaxSplits : ns);
+  constexpr int64_t gran = kChunk * kWaves;
+  int64_t ts = (max(max_len, int64_t{1}) + ns - 1) / ns;
+  ts = (ts + gran - 1) / gran * gran;
+  ns = (max(max_len, int64_t{1}) + ts - 1) / ts;
+  p.nsplit = static_cast<int>(ns);
+  p.split_tokens = static_cast<int>(ts);
+  p.bytes = static_cast<size_t>(B * Hkv * ns * (Hq / Hkv) * (2 + kD)) * 4 + 256;
+  return p;
+}
+
+}  // namespace
+}  // namespace lkv
+
+using namespace lkv;
+
+extern "C" size_t lkv_paged_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0) return 256;
+  return paged_plan(B, Hq, Hkv, max_len).bytes;
+}
+
+extern "C" int lkv_paged_decode_attn(const void* q, const void* kv_data, const int32_t* kv_indptr,
+                                     const int32_t* kv_indices, const int32_t* kv_last_page_len, int64_t B,
+                                     int64_t Hq, int64_t Hkv, int64_t page_size, int64_t max_pages,
+                                     int64_t max_len, float scale, void* out, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  LKV_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16,
+              "paged_decode_attn: need Hq %% Hkv == 0 and Hq/Hkv <= 16 (Hq=%lld Hkv=%lld)", (long long)Hq,
+              (long long)Hkv);
+  LKV_REQUIRE(page_size >= 1 && page_size <= 65536 && max_pages >= 1,
+              "paged_decode_attn: page_size=%lld / max_pages=%lld out of range", (long long)page_size,
+              (long long)max_pages);
+  LKV_REQUIRE(max_len >= 0 && max_len < (1ll << 30), "paged_decode_attn: max_len=%lld out of range",
+              (long long)max_len);
+  LKV_REQUIRE(max_pages * 2 * page_size * Hkv * kD < (1ll << 40), "paged_decode_attn: pool too large");
+  if (B == 0) return LKV_OK;
+  LKV_REQUIRE(q && kv_data && kv_indptr && kv_indices && kv_last_page_len && out && workspace,
+              "paged_decode_attn: null pointer");
+  LKV_REQUIRE(aligned16(q) && aligned16(kv_data) && aligned16(out) && aligned16(workspace),
+              "paged_decode_attn: q, kv_data, out and workspace must be 16-byte aligned");
+  const PagedPlan pl = paged_plan(B, Hq, Hkv, max_len);
+  LKV_REQUIRE(workspace_bytes >= pl.bytes, "paged_decode_attn: workspace of %zu bytes required, got %zu", pl.bytes,
+              workspace_bytes);
+  PagedParams P;
+  P.q = static_cast<const uint16_t*>(q);
+  P.kv = static_cast<const uint16_t*>(kv_data);
+  P.indptr = kv_indptr;
+  P.indices = kv_indices;
+  P.last_len = kv_last_page_len;
+  P.partials = static_cast<float*>(workspace);
+  P.out = static_cast<uint16_t*>(out);
+  P.scale_log2 = scale * kLog2e;
+  P.Hq = static_cast<int>(Hq);
+  P.Hkv = static_cast<int>(Hkv);
+  P.G = static_cast<int>(Hq / Hkv);
+  P.ps = static_cast<int>(page_size);
+  P.nsplit = pl.nsplit;
+  P.split_tokens = pl.split_tokens;
+  P.max_pages = static_cast<int>(max_pages);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(paged_split_kernel, dim3(static_cast<unsigned>(pl.nsplit), static_cast<unsigned>(Hkv),
+                                              static_cast<unsigned>(B)),
+                     dim3(kThreads), 0, st, P);
+  LKV_LAUNCH_CHECK("paged_decode_attn split");
+  hipLaunchKernelGGL(paged_combine_kernel, dim3(static_cast<unsigned>(Hq), static_cast<unsigned>(B)), dim3(kD), 0,
+                     st, P);
+  LKV_LAUNCH_CHECK("paged_decode_attn combine");
+  return LKV_OK;
+}

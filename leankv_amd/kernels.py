@@ -395,6 +395,40 @@ def tq_prefill_attn(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK, Pi
                                kv_len, scale, out)
 
 
+def paged_decode_attn(q: torch.Tensor, kv_data: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
+                      kv_last_page_len: torch.Tensor, max_len: int, scale: float | None = None,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention of q fp16 [B, Hq, 128] over a paged fp16 pool [max_pages, 2, page_size, Hkv, 128]
+    with FlashInfer's CSR page table (int32 device tensors)."""
+    require_cuda(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
+    if q.dtype != torch.float16 or q.dim() != 3 or q.shape[-1] != HEAD_DIM or not q.is_contiguous():
+        raise LeanKVError("paged_decode_attn: q must be contiguous float16 [B, Hq, 128]")
+    if (kv_data.dtype != torch.float16 or kv_data.dim() != 5 or kv_data.shape[1] != 2
+            or kv_data.shape[-1] != HEAD_DIM or not kv_data.is_contiguous()):
+        raise LeanKVError("paged_decode_attn: kv_data must be contiguous float16 [max_pages, 2, page_size, Hkv, 128]")
+    for t, nm in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"), (kv_last_page_len, "kv_last_page_len")):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise LeanKVError("paged_decode_attn: %s must be a contiguous int32 tensor" % nm)
+    B, Hq, _ = q.shape
+    max_pages, _, page_size, Hkv, _ = kv_data.shape
+    if kv_indptr.numel() != B + 1 or kv_last_page_len.numel() != B:
+        raise LeanKVError("paged_decode_attn: kv_indptr needs B + 1 entries and kv_last_page_len B")
+    if out is None:
+        out = torch.empty_like(q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(HEAD_DIM)
+    lib = _lib_handle()
+    nbytes = lib.lkv_paged_decode_attn_workspace_bytes(B, Hq, Hkv, max_len)
+    ws = workspaces.get(q.device, "paged", nbytes)
+    check(
+        lib.lkv_paged_decode_attn(ptr(q), ptr(kv_data), ptr(kv_indptr), ptr(kv_indices), ptr(kv_last_page_len), B,
+                                  Hq, Hkv, page_size, max_pages, int(max_len), float(scale), ptr(out), ptr(ws),
+                                  ws.numel(), stream_handle(q.device)),
+        "lkv_paged_decode_attn",
+    )
+    return out
+
+
 # ------------------------------------------------------------------ RMSNorm
 def rms_norm_out(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor) -> torch.Tensor:
     """out = RMSNorm(x) * weight over the last dim (fp16), rounded like HF MistralRMSNorm.

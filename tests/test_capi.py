@@ -94,6 +94,14 @@ def test_invalid_arguments_rejected_without_launch():
     assert "workspace" in _lib.last_error()
     assert lib.lkv_sparse_gemm_batched_workspace_bytes(4, 4096, 14336) > 4 * 4096 * 4
     assert lib.lkv_sparse_gemm_batched(p, p, 0.1, 0, 4096, 14336, p, p, 0, None) == 0
+    # paged decode attention: GQA ratio, page size, workspace
+    assert lib.lkv_paged_decode_attn(p, p, p, p, p, 1, 30, 8, 16, 64, 100, 0.1, p, p, 1 << 20, None) == -1
+    assert "Hq/Hkv" in _lib.last_error()
+    assert lib.lkv_paged_decode_attn(p, p, p, p, p, 1, 32, 8, 0, 64, 100, 0.1, p, p, 1 << 20, None) == -1
+    assert "page_size" in _lib.last_error()
+    assert lib.lkv_paged_decode_attn(p, p, p, p, p, 16, 32, 8, 16, 64, 4096, 0.1, p, p, 256, None) == -1
+    assert "workspace" in _lib.last_error()
+    assert lib.lkv_paged_decode_attn(p, p, p, p, p, 0, 32, 8, 16, 64, 100, 0.1, p, p, 0, None) == 0
     # empty problems are no-ops
     assert lib.lkv_tq_prefill_attn(p, p, p, p, p, p, p, p, p, p, 3, 100, 1, 8, 2, 0, 64, 64, 0.1, p, p, 0, None) == 0
     assert lib.lkv_sparse_gemv(p, p, 0.1, 0, 16, p, p, 0, None) == 0

@@ -525,6 +525,68 @@ def test_prefill_attn_full_size(cuda):
     assert float((out - ref).abs().max() / ref.abs().max()) < RTOL
 
 
+def _paged_case(lens, Hq, Hkv, ps, seed, dev):
+    """A shuffled page pool holding sequences of the given lengths; the HIP kernel vs fp64 attention over
+    each sequence's gathered K/V."""
+    from leankv_amd import kernels
+
+    g = torch.Generator().manual_seed(seed)
+    B = len(lens)
+    npages = [-(-n // ps) for n in lens]
+    max_pages = sum(npages) + 3
+    perm = torch.randperm(max_pages, generator=g).tolist()
+    pool = torch.randn(max_pages, 2, ps, Hkv, 128, generator=g).half()
+    indptr, indices, last = [0], [], []
+    for b in range(B):
+        mine = perm[indptr[-1]:indptr[-1] + npages[b]]
+        indices += mine
+        indptr.append(indptr[-1] + npages[b])
+        r = lens[b] % ps
+        last.append(r if r else ps)
+    q = torch.randn(B, Hq, 128, generator=g).half()
+    out = kernels.paged_decode_attn(q.to(dev), pool.to(dev), torch.tensor(indptr, dtype=torch.int32, device=dev),
+                                    torch.tensor(indices or [0], dtype=torch.int32, device=dev),
+                                    torch.tensor(last, dtype=torch.int32, device=dev), max(lens)).cpu()
+    refs = []
+    for b in range(B):
+        pg = torch.tensor(indices[indptr[b]:indptr[b + 1]], dtype=torch.long)
+        k = pool[pg, 0].reshape(-1, Hkv, 128)[: lens[b]].permute(1, 0, 2).unsqueeze(0)
+        v = pool[pg, 1].reshape(-1, Hkv, 128)[: lens[b]].permute(1, 0, 2).unsqueeze(0)
+        refs.append(oq.decode_attention(q[b:b + 1].unsqueeze(2), k, v).squeeze(2))
+    return out, torch.cat(refs)
+
+
+# (sequence lengths, Hq, Hkv, page size): one token, page boundaries, ragged batches, 4096-token contexts,
+# 1-token pages, 64-token pages, 1 / 4 / 16 query heads per kv head.
+@pytest.mark.parametrize("lens,Hq,Hkv,ps", [([1], 32, 8, 16), ([16, 17, 33], 32, 8, 16), ([4096], 32, 8, 16),
+                                            ([300, 1, 4096, 77, 129], 8, 2, 16), ([50, 51], 4, 4, 1),
+                                            ([1000, 999], 16, 1, 64), ([2049] * 16, 32, 8, 16)])
+def test_paged_decode_attn(cuda, lens, Hq, Hkv, ps):
+    out, ref = _paged_case(lens, Hq, Hkv, ps, seed=sum(lens) + ps, dev=cuda)
+    assert torch.isfinite(out).all()
+    assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
+    assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
+
+
+def test_paged_cache_decode_attention_matches_gathered(cuda):
+    """PagedKVCache end to end: a prefill and two decode appends on 2 layers, then decode_attention on the
+    pages equals fp64 attention over the gathered K/V of the same layer."""
+    from leankv_amd.turboquant.paged_cache import PagedKVCache
+
+    g = torch.Generator().manual_seed(3)
+    c = PagedKVCache(num_layers=2, num_kv_heads=2, num_q_heads=8, page_size=16, max_pages=64, device=cuda)
+    for S in (70, 1, 1):
+        for li in range(2):
+            c.update(torch.randn(3, 2, S, 128, generator=g).half().to(cuda),
+                     torch.randn(3, 2, S, 128, generator=g).half().to(cuda), li)
+    q = torch.randn(3, 8, 128, generator=g).half()
+    for li in range(2):
+        out = c.decode_attention(li, q.to(cuda)).cpu()
+        k, v = c[li]
+        ref = oq.decode_attention(q.unsqueeze(2), k.cpu(), v.cpu()).squeeze(2)
+        assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
+
+
 # Large batches (many (batch, kv head) pairs, few splits each): hot-only,
 # boundary and short cold ranges, a 16-token window, 16 query heads per kv head.
 @pytest.mark.parametrize("B,Hq,Hkv,L,hot", [(16, 32, 8, 1, 64), (16, 32, 8, 65, 64), (16, 32, 8, 700, 64),
