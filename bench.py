@@ -21,6 +21,9 @@ Workloads:
           GEMV calls and torch's dense GEMM
   paged   batch decode attention on the paged fp16 pool (B=16, 4096 tokens, 16-token pages),
           beside torch SDPA on the same K/V held dense
+  prod    TurboQuantProd 3-bit (2-bit MSE + 1-bit QJL) quantize of the config-3 K,V fp16 [8,4096,128],
+          fp32-MFMA bound (three 128x128 products per vector); dequantize and the reference's torch
+          formulation on the same GPU timed beside it
   copy    a 512 MiB device copy: the known-size reference for scaling PMC byte counters
 Every workload rotates >= 3 independent buffer sets (> 512 MB) so the 256 MB
 Infinity Cache cannot serve repeated launches.  A "step" is one launch of the
@@ -50,7 +53,7 @@ def _parse():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "mlp", "quant", "attn", "prefill",
-                                                                    "batched", "paged", "copy"])
+                                                                    "batched", "paged", "prod", "copy"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=32, help="decoder layers (config 5 uses 32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -372,6 +375,126 @@ def bench_quant(args, torch):
                      "kernel": "quantize_wave_kernel<3,true> (K and V launches)", "kernel_us_mean": round(kmean * 1e3, 3),
                      "kernel_us_median": round(kmed * 1e3, 3), "hbm_GBps": round(alg_bytes / (kmean * 1e-3) / 1e9, 1)},
     }
+
+
+# ------------------------------------------------------------------ TurboQuantProd (QJL)
+PROD_Q_BYTES = 128 * 2 + 32 + 2 + 16 + 4   # fp16 vector in; 2-bit codes, fp16 norm, signs, fp32 rnorm out
+PROD_DQ_BYTES = 32 + 2 + 16 + 4 + 128 * 4  # codes, norm, signs, rnorm in; fp32 vector out
+PROD_Q_FLOP = 3 * 2 * 128 * 128            # x Pi^T, y Pi, r S^T
+PROD_DQ_FLOP = 2 * 2 * 128 * 128           # y Pi, s S
+
+
+def bench_prod(args, torch):
+    """TurboQuantProd at 3 bits (2-bit MSE codes + 1-bit QJL signs + residual norm) of the config-3 K and V
+    fp16 [8, 4096, 128] (4 channels x10), seeds 42 (K) / 43 (V), S from seed + 1000.  One step = quantize K
+    and V, one fused kernel each (three fp32-MFMA 128x128 products per vector); dequantize (two products)
+    is timed beside it, and the reference's torch formulation of quantize on the same GPU."""
+    from leankv_amd import _lib
+    from leankv_amd.turboquant.quantizer import TurboQuantProd
+
+    dev = torch.device("cuda:0")
+    H, T, D = 8, 4096, 128
+    tqs = (TurboQuantProd(D, 3, device=dev, seed=42), TurboQuantProd(D, 3, device=dev, seed=43))
+    lib = _lib.load()
+    st = _lib.stream_handle(dev)
+    M = H * T
+    sets = []
+    for s in range(16):
+        g = torch.Generator(device=dev).manual_seed(500 + s)
+        kv = torch.randn(2, H, T, D, generator=g, device=dev)
+        kv[..., [0, 31, 64, 127]] *= 10
+        kv = kv.half()
+        outs = []
+        for h in range(2):
+            tq = tqs[h]
+            q = tq.quantize(kv[h])
+            outs.append((kv[h], q, torch.empty(H, T, D, device=dev)))
+        sets.append(outs)
+    ptr = _lib.ptr
+
+    def quant(i):  # the C ABI straight, so that host overhead cannot hide between launches
+        for h in range(2):
+            x, q, _ = sets[i][h]
+            m = tqs[h].mse_quantizer
+            lib.lkv_tq_prod_quantize(ptr(x), 1, M, ptr(m.Pi), ptr(m.decision_boundaries), ptr(m.centroids),
+                                     ptr(tqs[h].S), 2, ptr(q.mse_indices), ptr(q.norms), ptr(q.qjl_signs),
+                                     ptr(q.residual_norms), st)
+
+    def dequant(i):
+        for h in range(2):
+            _, q, out = sets[i][h]
+            m = tqs[h].mse_quantizer
+            lib.lkv_tq_prod_dequantize(ptr(q.mse_indices), ptr(q.norms), 1, ptr(q.qjl_signs), ptr(q.residual_norms),
+                                       M, ptr(m.Pi), ptr(m.centroids), ptr(tqs[h].S), 2, tqs[h].qjl_scale, ptr(out),
+                                       0, st)
+    assert _lib.dtype_code(torch.float16) == 1 and _lib.dtype_code(torch.float32) == 0
+    wall, _, _ = _timed_loop(quant, len(sets), args.steps, args.warmup, torch)
+    kq, kq_med = _kernel_time(quant, len(sets), args.steps, args.warmup, torch)
+    kd, _ = _kernel_time(dequant, len(sets), args.steps, args.warmup, torch)
+    nvec = 2 * M
+    q_bytes, q_flop = nvec * PROD_Q_BYTES, nvec * PROD_Q_FLOP
+    d_bytes, d_flop = nvec * PROD_DQ_BYTES, nvec * PROD_DQ_FLOP
+    tf = q_flop / (kq * 1e-3) / 1e12
+
+    def torch_path(i):  # quantizer.py:119-129 + 206-222 as torch ops on the GPU
+        for h in range(2):
+            x = sets[i][h][0]
+            m, S = tqs[h].mse_quantizer, tqs[h].S
+            nrm = x.norm(dim=-1)
+            y = torch.matmul((x / (nrm.unsqueeze(-1) + 1e-10)).float(), m.Pi.T)
+            idx = torch.searchsorted(m.decision_boundaries, y.contiguous())
+            packed = (idx.to(torch.uint8).reshape(H, T, 32, 4) << torch.tensor([0, 2, 4, 6], device=dev,
+                      dtype=torch.uint8)).sum(-1, dtype=torch.uint8)
+            xh = torch.matmul(m.centroids[idx], m.Pi) * nrm.unsqueeze(-1)
+            r = x - xh
+            rn = r.norm(dim=-1)
+            bits = (torch.matmul(r.float(), S.T) > 0).to(torch.uint8).reshape(H, T, 16, 8)
+            signs = (bits << torch.arange(8, device=dev, dtype=torch.uint8)).sum(-1, dtype=torch.uint8)
+            del packed, rn, signs
+    tt, _ = _kernel_time(torch_path, len(sets), min(args.steps, 50), 3, torch, batch=5)
+    res = {
+        "metric": "TurboQuantProd 3-bit quantize GB/s (K,V fp16 [8,4096,128])",
+        "value": round(q_bytes / (kq * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wall, 5),
+        "higher_is_better": True, "dtype": "fp32 MFMA (fp16 in; 2-bit codes, signs, norms out)",
+        "config": {"workload": "tq_prod_quantize_config3", "vectors": nvec, "alg_bytes_per_step": q_bytes,
+                   "flop_per_step": q_flop, "sets": len(sets),
+                   "dequantize": {"kernel": "prod_dequantize_kernel<2,true,false>", "us_per_step": round(kd * 1e3, 2),
+                                  "GBps": round(d_bytes / (kd * 1e-3) / 1e9, 1),
+                                  "TFLOPs": round(d_flop / (kd * 1e-3) / 1e12, 2),
+                                  "mfma_frac": round(d_flop / (kd * 1e-3) / 1e12 / MFMA_F32_PEAK_TFLOPS, 4)},
+                   "reference_path_gpu": {"what": "the reference's quantize as torch ops on the same GPU",
+                                          "us_per_step": round(tt * 1e3, 1), "speedup": round(tt / kq, 2)}},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "prod_quantize_kernel<2,true> (K and V launches)",
+                     "kernel_us_mean": round(kq * 1e3, 3), "kernel_us_median": round(kq_med * 1e3, 3),
+                     "hbm_GBps": round(q_bytes / (kq * 1e-3) / 1e9, 1)},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = _cpu_prod(torch)
+    return res
+
+
+def _cpu_prod(torch):
+    """The oracle's TurboQuantProd quantize (torch CPU ops, all host threads) on 8 heads' worth of K."""
+    from oracle import turboquant as oq
+
+    cores, model = _cpu_info()
+    torch.set_num_threads(cores)
+    Pi, S = oq.rotation_matrix(128, 42), oq.qjl_matrix(128, 1042)
+    c, b = oq.codebook_tensors(2)
+    g = torch.Generator().manual_seed(9)
+    n, dt = 0, 0.0
+    for _ in range(8):
+        x = torch.randn(4096, 128, generator=g)
+        x[:, [0, 31, 64, 127]] *= 10
+        x = x.half()
+        t = time.perf_counter()
+        oq.prod_quantize(x, Pi, b, c, S, 2)
+        dt += time.perf_counter() - t
+        n += x.shape[0]
+    return {"value": round(n * PROD_Q_BYTES / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": "oracle prod_quantize (torch CPU), 8 x 4096 fp16 vectors; %s" % model}
 
 
 # ------------------------------------------------------------------ config 4
@@ -771,7 +894,7 @@ def main():
         _fill_gemv_defaults(args)
         fn = {"gemv": bench_gemv, "mlp": bench_mlp, "copy": bench_copy, "quant": bench_quant,
               "attn": bench_attn, "prefill": bench_prefill, "batched": bench_batched,
-              "paged": bench_paged}.get(args.workload)
+              "paged": bench_paged, "prod": bench_prod}.get(args.workload)
         if fn is None:
             print("bench.py: workload %s is not implemented yet" % args.workload, file=sys.stderr)
             sys.exit(2)

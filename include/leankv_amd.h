@@ -155,6 +155,38 @@ int lkv_tq_rotate(const void* x, int x_dtype, int64_t M, const float* Pi,
                   int transpose, float* y, void* stream);
 
 /*
+ * TurboQuantProd.quantize (leankv/turboquant/quantizer.py:206-222), one launch:
+ *   codes, norms = TurboQuantMSE(mse_bits).quantize(x)       (as lkv_tq_quantize)
+ *   x_hat = (centroids[codes] @ Pi) * norm;  r = x - x_hat      (fp32)
+ *   rnorms = ||r||;  signs: bit i of byte j = [(r @ S^T)[8j + i] > 0]
+ *                                              (_pack_qjl_signs, :181-194)
+ * x [M, 128] (F32 or F16); Pi and S fp32 [128, 128] row-major (S is
+ * generate_qjl_matrix(128, seed + 1000), rotation.py:32-42); bounds fp32
+ * [2^mse_bits - 1]; centroids fp32 [2^mse_bits]; codes uint8 [M, row_bytes
+ * of mse_bits]; norms [M] of x's dtype; signs uint8 [M, 16]; rnorms fp32 [M].
+ * mse_bits = TurboQuantProd bits - 1, 1..4.  Codes equal lkv_tq_quantize's
+ * and the signs equal those of lkv_tq_rotate(x - lkv_tq_dequantize(...), S),
+ * bit for bit.  fp32 MFMA.
+ */
+int lkv_tq_prod_quantize(const void* x, int x_dtype, int64_t M, const float* Pi,
+                         const float* bounds, const float* centroids, const float* S,
+                         int mse_bits, uint8_t* codes, void* norms, uint8_t* signs,
+                         float* rnorms, void* stream);
+
+/*
+ * TurboQuantProd.dequantize (quantizer.py:224-237), one launch:
+ *   out = (centroids[codes] @ Pi) * norm + (s @ S) * (qjl_scale * rnorm)
+ * with s = +1 / -1 from the sign bits (_unpack_qjl_signs, :196-204) and
+ * qjl_scale = sqrt(pi / 2) / 128 for the reference's estimator.  Shapes as
+ * lkv_tq_prod_quantize; norms of norm_dtype; out [M, 128] of out_dtype.
+ */
+int lkv_tq_prod_dequantize(const uint8_t* codes, const void* norms, int norm_dtype,
+                           const uint8_t* signs, const float* rnorms, int64_t M,
+                           const float* Pi, const float* centroids, const float* S,
+                           int mse_bits, float qjl_scale, void* out, int out_dtype,
+                           void* stream);
+
+/*
  * Decode-step cache append of TurboQuantCache.update for one layer
  * (leankv/turboquant/cache.py:84-159) on a static ring layout.
  * Current length before the append is *pos (device int32, read by the

@@ -43,6 +43,9 @@ SIGNATURES = {
     "lkv_tq_quantize_rotated": (_int, [_c_p, _i64, _c_p, _int, _c_p, _c_p]),
     "lkv_tq_dequantize": (_int, [_c_p, _c_p, _int, _i64, _c_p, _c_p, _int, _c_p, _int, _c_p]),
     "lkv_tq_rotate": (_int, [_c_p, _int, _i64, _c_p, _int, _c_p, _c_p]),
+    "lkv_tq_prod_quantize": (_int, [_c_p, _int, _i64, _c_p, _c_p, _c_p, _c_p, _int, _c_p, _c_p, _c_p, _c_p, _c_p]),
+    "lkv_tq_prod_dequantize": (_int, [_c_p, _c_p, _int, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _int, _f32, _c_p, _int,
+                                      _c_p]),
     "lkv_tq_cache_append": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _int,
                                    _c_p, _i64, _i64, _i64, _c_p]),
     "lkv_tq_decode_attn_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),

@@ -260,6 +260,57 @@ def tq_rotate(x: torch.Tensor, Pi: torch.Tensor, transpose: bool = False) -> tor
     return y
 
 
+def tq_prod_quantize(x: torch.Tensor, Pi: torch.Tensor, bounds: torch.Tensor, centroids: torch.Tensor,
+                     S: torch.Tensor, mse_bits: int):
+    """TurboQuantProd quantize in one launch: MSE codes at mse_bits, norms (x's dtype), the packed signs of
+    (x - x_hat) @ S^T ([..., 16] uint8) and the residual norms (fp32)."""
+    require_cuda(x)
+    M = _rows(x, "tq_prod_quantize")
+    rb = packed_row_bytes(mse_bits)
+    xc = x.contiguous()
+    b = _vec(bounds, x.device, (1 << mse_bits) - 1, "decision boundaries")
+    c = _vec(centroids, x.device, 1 << mse_bits, "centroids")
+    codes = torch.empty(*x.shape[:-1], rb, dtype=torch.uint8, device=x.device)
+    norms = torch.empty(x.shape[:-1], dtype=x.dtype, device=x.device)
+    signs = torch.empty(*x.shape[:-1], HEAD_DIM // 8, dtype=torch.uint8, device=x.device)
+    rnorms = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    check(
+        _lib_handle().lkv_tq_prod_quantize(ptr(xc), dtype_code(x.dtype), M, ptr(_pi(Pi, x.device)), ptr(b), ptr(c),
+                                           ptr(_pi(S, x.device)), int(mse_bits), ptr(codes), ptr(norms), ptr(signs),
+                                           ptr(rnorms), stream_handle(x.device)),
+        "lkv_tq_prod_quantize",
+    )
+    return codes, norms, signs, rnorms
+
+
+def tq_prod_dequantize(codes: torch.Tensor, norms: torch.Tensor, signs: torch.Tensor, rnorms: torch.Tensor,
+                       Pi: torch.Tensor, centroids: torch.Tensor, S: torch.Tensor, mse_bits: int, qjl_scale: float,
+                       out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """(centroid[codes] @ Pi) * norm + (signs @ S) * (qjl_scale * rnorm) in one launch."""
+    require_cuda(codes, norms, signs, rnorms)
+    rb = packed_row_bytes(mse_bits)
+    if codes.dtype != torch.uint8 or codes.shape[-1] != rb:
+        raise LeanKVError("tq_prod_dequantize: codes must be uint8 [..., %d]" % rb)
+    M = codes.numel() // rb
+    if signs.dtype != torch.uint8 or signs.numel() != M * (HEAD_DIM // 8):
+        raise LeanKVError("tq_prod_dequantize: signs must be uint8 [..., %d] for %d rows" % (HEAD_DIM // 8, M))
+    if norms.numel() != M or rnorms.numel() != M:
+        raise LeanKVError("tq_prod_dequantize: %d norms / %d residual norms for %d rows"
+                          % (norms.numel(), rnorms.numel(), M))
+    nc = norms.contiguous()
+    rn = rnorms.to(torch.float32).contiguous()
+    c = _vec(centroids, codes.device, 1 << mse_bits, "centroids")
+    out = torch.empty(*codes.shape[:-1], HEAD_DIM, dtype=out_dtype, device=codes.device)
+    check(
+        _lib_handle().lkv_tq_prod_dequantize(ptr(codes.contiguous()), ptr(nc), dtype_code(nc.dtype),
+                                             ptr(signs.contiguous()), ptr(rn), M, ptr(_pi(Pi, codes.device)), ptr(c),
+                                             ptr(_pi(S, codes.device)), int(mse_bits), float(qjl_scale), ptr(out),
+                                             dtype_code(out.dtype), stream_handle(codes.device)),
+        "lkv_tq_prod_dequantize",
+    )
+    return out
+
+
 def tq_cache_append(k_new, v_new, k_hot, v_hot, k_codes, k_norms, v_codes, v_norms, PiK, PiV, bounds, bits,
                     pos_dev) -> None:
     """Decode-step append on the static ring layout (see include/leankv_amd.h)."""

@@ -7,12 +7,17 @@ Drop-in for leankv/turboquant/quantizer.py:
       quantize(x)   -> one fused HIP launch: norm, x / (norm + 1e-10),
                        fp32-MFMA rotation, searchsorted, bit-pack
       dequantize(q) -> one HIP launch: unpack, centroid gather, rotation back, x norm
-The inner-product variant TurboQuantProd (:144-237) is not part of this build
-(no cache or decode path uses it).
+  ProdQuantized(mse_indices, qjl_signs, residual_norms, norms, mse_bits)  (:29-35)
+  TurboQuantProd(dim, bits, device, dtype, seed)  (:144-237) -- MSE at bits - 1
+      plus a 1-bit QJL sketch of the residual (sign(r @ S^T), S ~ N(0, 1) with seed
+      + 1000) and ||r||, an unbiased inner-product estimator:
+      quantize(x)   -> one fused HIP launch (three fp32-MFMA products per vector)
+      dequantize(q) -> one HIP launch: x_mse + (signs @ S) * (sqrt(pi/2)/d * ||r||)
 """
 
 from __future__ import annotations
 
+import math
 from typing import NamedTuple
 
 import torch
@@ -20,13 +25,21 @@ import torch.nn.functional as F
 
 from .. import kernels as _k
 from .codebook import get_codebook_tensors
-from .rotation import generate_rotation_matrix
+from .rotation import generate_qjl_matrix, generate_rotation_matrix
 
 
 class MSEQuantized(NamedTuple):
     indices: torch.Tensor  # (..., packed_len) uint8 bit-packed
     norms: torch.Tensor    # (...,) L2 norms, dtype of the quantized input
     bits: int
+
+
+class ProdQuantized(NamedTuple):
+    mse_indices: torch.Tensor     # (..., packed_len) uint8 bit-packed, mse_bits per code
+    qjl_signs: torch.Tensor       # (..., d / 8) uint8, bit i of byte j = sign of coordinate 8j + i
+    residual_norms: torch.Tensor  # (...,) fp32 ||x - x_mse||
+    norms: torch.Tensor           # (...,) L2 norms, dtype of the quantized input
+    mse_bits: int
 
 
 def _layout(bits: int) -> tuple[int, int]:
@@ -86,6 +99,55 @@ class TurboQuantMSE(torch.nn.Module):
 
     def dequantize(self, q: MSEQuantized) -> torch.Tensor:
         return _k.tq_dequantize(q.indices, q.norms, self.Pi, self.centroids, q.bits, out_dtype=torch.float32)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.dequantize(self.quantize(x))
+
+
+class TurboQuantProd(torch.nn.Module):
+    """TurboQuant for inner products: TurboQuantMSE at bits - 1 on x, then 1-bit QJL on the residual.
+
+    Signs of S r (S i.i.d. N(0, 1), seed + 1000) and ||r|| give the unbiased
+    estimate <y, x> ~ <y, x_mse> + sqrt(pi/2)/d * ||r|| <S y, sign(S r)>.
+    """
+
+    def __init__(self, dim: int, bits: int = 3, device=None, dtype: torch.dtype = torch.float32, seed: int = 42):
+        super().__init__()
+        if bits < 2:
+            raise AssertionError("Inner product TurboQuant requires at least 2 bits (1 for MSE + 1 for QJL)")
+        self.dim, self.bits = dim, bits
+        self.mse_quantizer = TurboQuantMSE(dim=dim, bits=bits - 1, device=device, dtype=dtype, seed=seed)
+        self.device = self.mse_quantizer.device
+        self.register_buffer("S", generate_qjl_matrix(dim, self.device, dtype, seed=seed + 1000))
+        self.qjl_scale = math.sqrt(math.pi / 2.0) / dim
+
+    def _pack_qjl_signs(self, projected: torch.Tensor) -> torch.Tensor:
+        """Sign bits of `projected` (> 0 -> 1), 8 per byte, coordinate 8j + i at bit i of byte j."""
+        signs = (projected > 0).to(torch.uint8)
+        d = signs.shape[-1]
+        if d % 8:
+            signs = F.pad(signs, (0, 8 - d % 8), value=0)
+        r = signs.reshape(*signs.shape[:-1], -1, 8)
+        shifts = torch.arange(8, device=signs.device, dtype=torch.uint8)
+        return (r << shifts).sum(dim=-1, dtype=torch.uint8)
+
+    def _unpack_qjl_signs(self, packed: torch.Tensor) -> torch.Tensor:
+        """Packed sign bytes -> float +1 / -1 per coordinate."""
+        shifts = torch.arange(8, device=packed.device, dtype=torch.uint8)
+        bits = ((packed.unsqueeze(-1) >> shifts) & 1).float()
+        return 2.0 * bits.reshape(*packed.shape[:-1], -1)[..., : self.dim] - 1.0
+
+    def quantize(self, x: torch.Tensor) -> ProdQuantized:
+        m = self.mse_quantizer
+        codes, norms, signs, rnorms = _k.tq_prod_quantize(x, m.Pi, m.decision_boundaries, m.centroids, self.S,
+                                                          m.bits)
+        return ProdQuantized(mse_indices=codes, qjl_signs=signs, residual_norms=rnorms, norms=norms,
+                             mse_bits=m.bits)
+
+    def dequantize(self, q: ProdQuantized) -> torch.Tensor:
+        m = self.mse_quantizer
+        return _k.tq_prod_dequantize(q.mse_indices, q.norms, q.qjl_signs, q.residual_norms, m.Pi, m.centroids,
+                                     self.S, q.mse_bits, self.qjl_scale)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self.dequantize(self.quantize(x))

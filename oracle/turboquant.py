@@ -7,6 +7,8 @@ References (under /root/reference, read as text):
   leankv/turboquant/quantizer.py:65-85  _unpack_indices
   leankv/turboquant/quantizer.py:119-129 TurboQuantMSE.quantize
   leankv/turboquant/quantizer.py:131-137 TurboQuantMSE.dequantize
+  leankv/turboquant/rotation.py:32-42   generate_qjl_matrix (seeded i.i.d. N(0,1))
+  leankv/turboquant/quantizer.py:144-237 TurboQuantProd (sign packing, quantize, dequantize)
   leankv/turboquant/cache.py:84-189     TurboQuantCache.update / flush / full cache
   transformers/integrations/sdpa_attention.py:79-105  GQA SDPA on the returned K/V
   transformers/masking_utils.py causal_mask_function   causal mask with the cache offset (prefill)
@@ -105,6 +107,57 @@ def dequantize(packed: np.ndarray, norms: torch.Tensor, Pi: torch.Tensor, centro
     idx = torch.from_numpy(unpack_indices(packed, bits, d))
     y_hat = centroids[idx]
     return torch.matmul(y_hat, Pi) * norms.float().unsqueeze(-1)
+
+
+def qjl_matrix(d: int, seed: int) -> torch.Tensor:
+    """generate_qjl_matrix (rotation.py:32-42): i.i.d. N(0,1) from a seeded CPU generator, fp32."""
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    return torch.randn(d, d, generator=g, dtype=torch.float32)
+
+
+def pack_signs(proj: np.ndarray) -> np.ndarray:
+    """TurboQuantProd._pack_qjl_signs (quantizer.py:181-194): bit i of byte j = [proj[8j + i] > 0]."""
+    bits = (np.asarray(proj) > 0).astype(np.uint8)
+    d = bits.shape[-1]
+    if d % 8:
+        bits = np.concatenate([bits, np.zeros(bits.shape[:-1] + (8 - d % 8,), np.uint8)], axis=-1)
+    r = bits.reshape(bits.shape[:-1] + (-1, 8)).astype(np.uint32)
+    return (r << np.arange(8, dtype=np.uint32)).sum(axis=-1).astype(np.uint8)
+
+
+def unpack_signs(packed: np.ndarray, d: int = 128) -> np.ndarray:
+    """TurboQuantProd._unpack_qjl_signs (quantizer.py:196-204): +1 / -1 float32 per coordinate."""
+    p = np.asarray(packed, dtype=np.uint8)[..., None]
+    b = (p >> np.arange(8, dtype=np.uint8)) & 1
+    return (2.0 * b.reshape(p.shape[:-2] + (-1,))[..., :d] - 1.0).astype(np.float32)
+
+
+def prod_quantize(x: torch.Tensor, Pi: torch.Tensor, boundaries: torch.Tensor, centroids: torch.Tensor,
+                  S: torch.Tensor, mse_bits: int):
+    """TurboQuantProd.quantize (quantizer.py:206-222) with torch CPU ops.
+
+    MSE codes and norms at mse_bits, x_hat their dequantization, residual
+    r = x - x_hat in fp32, its norm, and the signs of r @ S^T.  Returns
+    (packed codes, norms, packed signs, residual norms fp32, r @ S^T fp32).
+    """
+    x = x.cpu()
+    packed, norms, _ = quantize(x, Pi, boundaries, mse_bits)
+    x_hat = dequantize(packed, norms, Pi, centroids, mse_bits)
+    residual = x - x_hat
+    proj = torch.matmul(residual.float(), S.T)
+    return packed, norms, pack_signs(proj.numpy()), residual.norm(dim=-1), proj
+
+
+def prod_dequantize(packed: np.ndarray, norms: torch.Tensor, signs: np.ndarray, rnorms: torch.Tensor,
+                    Pi: torch.Tensor, centroids: torch.Tensor, S: torch.Tensor, mse_bits: int,
+                    d: int = 128) -> torch.Tensor:
+    """TurboQuantProd.dequantize (quantizer.py:224-237), fp32:
+    x_mse + (signs @ S) * (sqrt(pi / 2) / d * ||r||)."""
+    x_mse = dequantize(packed, norms, Pi, centroids, mse_bits, d)
+    x_qjl = torch.matmul(torch.from_numpy(unpack_signs(signs, d)), S)
+    x_qjl = x_qjl * ((math.sqrt(math.pi / 2.0) / d) * rnorms.float().unsqueeze(-1))
+    return x_mse + x_qjl
 
 
 class CacheRef:

@@ -26,6 +26,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 
 
 def main(ref_root: str = "/root/reference") -> None:
+    sys.dont_write_bytecode = True  # leave the read-only checkout untouched (no __pycache__)
     sys.path.insert(0, ref_root)
     # Import the solver module directly: get_codebook() would try to create a
     # cache directory inside the read-only checkout (codebook.py:143).

@@ -54,6 +54,7 @@ SETTINGS = [
 
 
 def main(ref_root: str = "/root/reference") -> None:
+    sys.dont_write_bytecode = True  # leave the read-only checkout untouched (no __pycache__)
     sys.path.insert(0, ref_root)
     from leankv.teal import greedy_opt as ref  # noqa: E402
 

@@ -335,6 +335,150 @@ def test_tq_rotate(cuda, transpose):
                                rtol=1e-5, atol=1e-5)
 
 
+# ----------------------------------------------------------- TurboQuantProd (QJL)
+def _prod_tables(mb, seed=42):
+    c, b = oq.codebook_tensors(mb)
+    return oq.rotation_matrix(128, seed), oq.qjl_matrix(128, seed + 1000), c, b
+
+
+def test_tq_prod_matches_reference_golden(cuda):
+    """TurboQuantProd on the GPU reproduces the reference's recorded outputs (tests/golden/make_qjl_golden.py)."""
+    import json
+    import os
+
+    from leankv_amd.turboquant.quantizer import TurboQuantProd
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "qjl_prod_cases.json")
+    for c in json.load(open(path)):
+        print("golden case bits=%d %s" % (c["bits"], c["dtype"]), flush=True)
+        tq = TurboQuantProd(128, bits=c["bits"], device=cuda, seed=42)
+        x = torch.tensor(c["x"]).to(getattr(torch, c["dtype"])).to(cuda)
+        q = tq.quantize(x)
+        assert q.mse_bits == c["mse_bits"] and q.norms.dtype == x.dtype
+        assert np.array_equal(q.mse_indices.cpu().numpy(), np.array(c["mse_indices"], np.uint8))
+        assert np.array_equal(q.qjl_signs.cpu().numpy(), np.array(c["qjl_signs"], np.uint8))
+        torch.testing.assert_close(q.norms.float().cpu(), torch.tensor(c["norms"]), rtol=2e-6, atol=0)
+        torch.testing.assert_close(q.residual_norms.cpu(), torch.tensor(c["residual_norms"]), rtol=1e-5, atol=0)
+        out = tq.dequantize(q).cpu()
+        assert out.dtype == torch.float32
+        torch.testing.assert_close(out, torch.tensor(c["dequantized"]), rtol=1e-5, atol=1e-5)
+
+
+def _prod_case(x, mb, cuda, seed=42):
+    """GPU quantize of x vs (a) the separate MSE / rotate kernels, bit for bit, and (b) the oracle, with
+    near-tie codes and signs counted; returns (#code flips, #sign flips)."""
+    from leankv_amd import kernels
+
+    Pi, S, c, b = _prod_tables(mb, seed)
+    xd = x.to(cuda)
+    codes, norms, signs, rn = kernels.tq_prod_quantize(xd, Pi.to(cuda), b[1:-1].to(cuda), c.to(cuda), S.to(cuda), mb)
+    # (a) the fused kernel == quantize, dequantize and rotate run one after another
+    c2, n2 = kernels.tq_quantize(xd, Pi.to(cuda), b[1:-1].to(cuda), mb)
+    assert torch.equal(codes, c2) and torch.equal(norms, n2)
+    xh = kernels.tq_dequantize(codes, norms, Pi.to(cuda), c.to(cuda), mb, out_dtype=torch.float32)
+    r = xd.float() - xh
+    proj = kernels.tq_rotate(r, S.to(cuda), False)
+    assert np.array_equal(signs.cpu().numpy(), oq.pack_signs(proj.cpu().numpy()))
+    torch.testing.assert_close(rn, r.norm(dim=-1), rtol=1e-5, atol=1e-30)
+    # (b) the oracle
+    codes, norms, signs, rn = codes.cpu().numpy(), norms.cpu(), signs.cpu().numpy(), rn.cpu()
+    p_ref, n_ref, s_ref, rn_ref, proj_ref = oq.prod_quantize(x, Pi, b, c, S, mb)
+    if x.dtype == torch.float16:
+        same = (norms == n_ref).numpy()  # an fp16 norm can round the other way (see the config-3 test)
+        assert (~same).sum() <= 1e-3 * same.size
+    else:
+        torch.testing.assert_close(norms, n_ref, rtol=2e-6, atol=0)
+        same = np.ones(norms.shape, dtype=bool)
+    flips = _codes_match(codes[same], p_ref[same], oq.rotated_fp64(x, Pi)[same], b, mb)
+    ok = same & (oq.unpack_indices(codes, mb, 128) == oq.unpack_indices(p_ref, mb, 128)).all(-1)
+    torch.testing.assert_close(rn[ok], rn_ref[ok], rtol=1e-5, atol=1e-30)
+    sg = oq.unpack_signs(signs[ok])
+    sr = oq.unpack_signs(s_ref[ok])
+    band = 1e-5 * x.float().norm(dim=-1).numpy()[ok][:, None]
+    sdiff = sg != sr
+    assert not (sdiff & (np.abs(proj_ref.double().numpy()[ok]) >= band)).any(), "sign flip away from zero"
+    return flips, int(sdiff.sum())
+
+
+@pytest.mark.parametrize("mb", [1, 2, 3, 4])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_tq_prod_quantize(cuda, mb, dtype):
+    x = _kv((4, 1000, 128), 20 + mb).to(dtype)
+    flips, sflips = _prod_case(x, mb, cuda)
+    assert flips <= 8 and sflips <= 8, (flips, sflips)
+
+
+def test_tq_prod_quantize_ragged_zero_and_empty(cuda):
+    from leankv_amd import kernels
+
+    x = torch.randn(37, 128)
+    x[5] = 0
+    _prod_case(x, 2, cuda)
+    Pi, S, c, b = _prod_tables(2)
+    codes, norms, signs, rn = kernels.tq_prod_quantize(x.to(cuda), Pi.to(cuda), b[1:-1].to(cuda), c.to(cuda),
+                                                       S.to(cuda), 2)
+    # a zero vector: norm 0, every code = #(boundaries < 0), x_hat = 0, residual 0, no sign bit set
+    assert norms[5].item() == 0 and rn[5].item() == 0 and int(signs[5].sum()) == 0
+    assert (oq.unpack_indices(codes.cpu().numpy()[5], 2, 128) == int((b[1:-1] < 0).sum())).all()
+    e = kernels.tq_prod_quantize(torch.empty(0, 128, device=cuda), Pi.to(cuda), b[1:-1].to(cuda), c.to(cuda),
+                                 S.to(cuda), 2)
+    assert e[0].shape == (0, 32) and e[2].shape == (0, 16)
+
+
+@pytest.mark.parametrize("mb", [1, 2, 3, 4])
+def test_tq_prod_dequantize(cuda, mb):
+    from leankv_amd import kernels
+
+    Pi, S, c, b = _prod_tables(mb, 7)
+    x = _kv((3, 333, 128), 30 + mb).float()
+    p, n, s, rn, _ = oq.prod_quantize(x, Pi, b, c, S, mb)
+    ref = oq.prod_dequantize(p, n, s, rn, Pi, c, S, mb)
+    scale = math.sqrt(math.pi / 2) / 128
+    args = (torch.from_numpy(p).to(cuda), n.to(cuda), torch.from_numpy(s).to(cuda), rn.to(cuda), Pi.to(cuda),
+            c.to(cuda), S.to(cuda), mb, scale)
+    out = kernels.tq_prod_dequantize(*args).cpu()
+    torch.testing.assert_close(out, ref, rtol=1e-5, atol=1e-5)
+    out16 = kernels.tq_prod_dequantize(*args, out_dtype=torch.float16).cpu()
+    torch.testing.assert_close(out16, ref.half(), rtol=2e-3, atol=2e-3)
+    # fp16 norms (an fp16 input's quantization) read as their fp32 values
+    out_h = kernels.tq_prod_dequantize(args[0], n.half().to(cuda), *args[2:]).cpu()
+    ref_h = oq.prod_dequantize(p, n.half(), s, rn, Pi, c, S, mb)
+    torch.testing.assert_close(out_h, ref_h, rtol=1e-5, atol=1e-5)
+
+
+def test_tq_prod_full_size(cuda):
+    """Config-3 shape (K and V fp16 [8, 4096, 128], 4 channels x10): the fused kernel equals the separate
+    kernels bit for bit, and the sketch halves the inner-product error of the MSE part alone."""
+    from leankv_amd.turboquant.quantizer import TurboQuantProd
+
+    x = _kv((8, 4096, 128), 40).to(cuda)
+    flips, sflips = _prod_case(x[:1].cpu(), 2, cuda)  # oracle on one head (4096 vectors)
+    assert flips <= 8 and sflips <= 8
+    tq = TurboQuantProd(128, bits=3, device=cuda, seed=42)
+    q = tq.quantize(x)
+    from leankv_amd import kernels
+
+    m = tq.mse_quantizer
+    c2, n2 = kernels.tq_quantize(x, m.Pi, m.decision_boundaries, 2)
+    assert torch.equal(q.mse_indices, c2) and torch.equal(q.norms, n2)
+    xh = kernels.tq_dequantize(c2, n2, m.Pi, m.centroids, 2, out_dtype=torch.float32)
+    proj = kernels.tq_rotate(x.float() - xh, tq.S, False)
+    assert np.array_equal(q.qjl_signs.cpu().numpy(), oq.pack_signs(proj.cpu().numpy()))
+    # inner products with random queries: the QJL-corrected estimate has no systematic shrinkage
+    g = torch.Generator(device=cuda).manual_seed(1)
+    y = torch.randn(64, 128, generator=g, device=cuda)
+    xf = x.float().reshape(-1, 128)
+    est = tq.dequantize(q).reshape(-1, 128)
+    true = y @ xf.T
+    err_prod = (y @ est.T - true)
+    err_mse = (y @ xh.reshape(-1, 128).T - true)
+    assert abs(err_prod.mean().item()) < 0.02 * true.std().item()
+    # the MSE estimate is shrunk toward zero (slope < 1); the corrected one is not
+    slope_mse = float((err_mse.flatten() * true.flatten()).sum() / (true.flatten() ** 2).sum())
+    slope_prod = float((err_prod.flatten() * true.flatten()).sum() / (true.flatten() ** 2).sum())
+    assert slope_mse < -0.05 and abs(slope_prod) < 0.02, (slope_mse, slope_prod)
+
+
 def test_tq_cache_append_matches_reference_cache(cuda):
     """Static ring append == TurboQuantCache.update hot/cold semantics (cache.py:84-159)."""
     from leankv_amd import kernels

@@ -141,6 +141,92 @@ def test_product_pack_helpers_match_oracle():
         assert np.array_equal(_unpack_indices(torch.from_numpy(p), bits, 128).numpy(), idx)
 
 
+# ------------------------------------------------------------------ TurboQuantProd / QJL
+def _qjl_cases():
+    return json.load(open(os.path.join(GOLDEN, "qjl_prod_cases.json")))
+
+
+def test_qjl_oracle_matches_reference_golden():
+    """The reference's TurboQuantProd on seeded inputs (make_qjl_golden.py), bit for bit."""
+    import hashlib
+
+    S = oq.qjl_matrix(128, 42 + 1000)
+    Pi = oq.rotation_matrix(128, 42)
+    for c in _qjl_cases():
+        assert hashlib.sha256(S.numpy().tobytes()).hexdigest() == c["S_sha256"]
+        assert S[0].tolist() == c["S_row0"]
+        assert c["qjl_scale"] == math.sqrt(math.pi / 2) / 128
+        mb = c["mse_bits"]
+        assert mb == c["bits"] - 1
+        cen, b = oq.codebook_tensors(mb)
+        x = torch.tensor(c["x"]).to(getattr(torch, c["dtype"]))
+        codes, norms, signs, rn, _ = oq.prod_quantize(x, Pi, b, cen, S, mb)
+        assert np.array_equal(codes, np.array(c["mse_indices"], np.uint8))
+        assert np.array_equal(signs, np.array(c["qjl_signs"], np.uint8))
+        assert torch.equal(rn, torch.tensor(c["residual_norms"]))
+        assert torch.equal(norms.float(), torch.tensor(c["norms"]))
+        out = oq.prod_dequantize(codes, norms, signs, rn, Pi, cen, S, mb)
+        assert torch.equal(out, torch.tensor(c["dequantized"]))
+
+
+def _brute_signs(proj):
+    out = []
+    for row in np.asarray(proj).reshape(-1, proj.shape[-1]):
+        bs = []
+        for j in range(0, len(row), 8):
+            v = 0
+            for i in range(8):
+                if j + i < len(row) and row[j + i] > 0:
+                    v |= 1 << i
+            bs.append(v)
+        out.append(bs)
+    return np.array(out, dtype=np.uint8).reshape(proj.shape[:-1] + (-1,))
+
+
+@pytest.mark.parametrize("d", [128, 13, 8])
+def test_qjl_sign_packing_brute_force(d):
+    rng = np.random.default_rng(d)
+    proj = rng.standard_normal((3, 4, d)).astype(np.float32)
+    proj[0, 0, :3] = 0.0  # exactly zero packs as a 0 bit ('> 0')
+    p = oq.pack_signs(proj)
+    assert np.array_equal(p, _brute_signs(proj))
+    s = oq.unpack_signs(p, d)
+    assert np.array_equal(s, np.where(proj > 0, 1.0, -1.0).astype(np.float32))
+
+
+def test_qjl_estimator_is_unbiased():
+    """E_S[(sign(S r) @ S) * sqrt(pi/2)/d * ||r||] = r: pins the scale constant and the sign convention."""
+    g = torch.Generator().manual_seed(5)
+    d, draws = 128, 2000
+    r = torch.randn(3, d, generator=g)
+    acc = torch.zeros(3, d, dtype=torch.float64)
+    for k in range(0, draws, 250):
+        S = torch.randn(250, d, d, generator=g)
+        proj = torch.einsum("kij,bj->kbi", S, r)
+        s = torch.from_numpy(oq.unpack_signs(oq.pack_signs(proj.numpy()), d))
+        est = torch.einsum("kbi,kij->kbj", s, S) * (math.sqrt(math.pi / 2) / d * r.norm(dim=-1)).unsqueeze(-1)
+        acc += est.double().sum(0)
+    mean = acc / draws
+    rel = (mean - r.double()).norm(dim=-1) / r.double().norm(dim=-1)
+    assert (rel < 0.06).all(), rel  # expected ~0.025 at 2000 draws; sqrt(2/pi) or a flipped sign gives >= 0.36
+
+
+def test_prod_host_helpers_and_constructor():
+    from leankv_amd.turboquant.quantizer import TurboQuantProd
+
+    tq = TurboQuantProd(128, bits=3, device="cpu", seed=7)
+    assert tq.mse_quantizer.bits == 2 and torch.equal(tq.S, oq.qjl_matrix(128, 1007))
+    assert torch.equal(tq.mse_quantizer.Pi, oq.rotation_matrix(128, 7))
+    assert tq.qjl_scale == math.sqrt(math.pi / 2) / 128
+    proj = torch.randn(5, 128)
+    proj[0, :4] = 0
+    p = tq._pack_qjl_signs(proj)
+    assert np.array_equal(p.numpy(), oq.pack_signs(proj.numpy()))
+    assert np.array_equal(tq._unpack_qjl_signs(p).numpy(), oq.unpack_signs(p.numpy()))
+    with pytest.raises(AssertionError, match="at least 2 bits"):
+        TurboQuantProd(128, bits=1, device="cpu")
+
+
 # ------------------------------------------------------------------ quantize
 def test_quantize_codes_are_boundary_counts():
     """searchsorted(right=False) == number of decision boundaries strictly below y."""
