@@ -21,6 +21,8 @@ Workloads:
           GEMV calls and torch's dense GEMM
   paged   batch decode attention on the paged fp16 pool (B=16, 4096 tokens, 16-token pages),
           beside torch SDPA on the same K/V held dense
+  tqpaged config 4 through a paged 3-bit cache (4096 cold tokens per sequence in 16-token pages
+          scattered over the pool), beside the dense packed kernel on the same codes
   prod    TurboQuantProd 3-bit (2-bit MSE + 1-bit QJL) quantize of the config-3 K,V fp16 [8,4096,128],
           fp32-MFMA bound (three 128x128 products per vector); dequantize and the reference's torch
           formulation on the same GPU timed beside it
@@ -53,7 +55,7 @@ def _parse():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "mlp", "quant", "attn", "prefill",
-                                                                    "batched", "paged", "prod", "copy"])
+                                                                    "batched", "paged", "tqpaged", "prod", "copy"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=32, help="decoder layers (config 5 uses 32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -547,6 +549,78 @@ def bench_attn(args, torch):
     }
 
 
+def bench_tq_paged(args, torch):
+    """Config 4 through pages: decode attention on a paged 3-bit cache, B=16, 32/8 heads, 4096 cold tokens
+    per sequence in 16-token pages scattered over the pool by a seeded permutation, 64-token fp16 hot
+    rings; one lkv_tq_paged_decode_attn call per step over 8 rotating pools.  Beside it the dense
+    lkv_tq_decode_attn on the same codes laid out per sequence."""
+    from leankv_amd import kernels
+    from leankv_amd.turboquant.codebook import get_codebook_tensors
+    from leankv_amd.turboquant.rotation import generate_rotation_matrix
+
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, D, cold, hot, ps = 16, 32, 8, 128, 4096, 64, 16
+    L = cold + hot
+    npg = cold // ps
+    max_pages = B * npg + 8
+    cent, _ = get_codebook_tensors(D, 3, dev, torch.float32)
+    PiK = generate_rotation_matrix(D, dev, torch.float32, 42)
+    PiV = generate_rotation_matrix(D, dev, torch.float32, 43)
+    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+    seq = torch.tensor([L], dtype=torch.int32, device=dev)
+    indptr = torch.arange(0, B * npg + 1, npg, dtype=torch.int32, device=dev)
+    sets = []
+    for s in range(8):
+        g = torch.Generator(device=dev).manual_seed(700 + s)
+        perm = torch.randperm(max_pages, generator=g, device=dev)[: B * npg].to(torch.int32).contiguous()
+        kc = torch.randint(0, 256, (max_pages, Hkv, ps, 64), generator=g, device=dev, dtype=torch.uint8) & 0x77
+        vc = torch.randint(0, 256, (max_pages, Hkv, ps, 64), generator=g, device=dev, dtype=torch.uint8) & 0x77
+        kn = torch.rand(max_pages, Hkv, ps, generator=g, device=dev) * 4 + 8
+        vn = torch.rand(max_pages, Hkv, ps, generator=g, device=dev) * 4 + 8
+        kh = torch.randn(B, Hkv, hot, D, generator=g, device=dev).half()
+        vh = torch.randn(B, Hkv, hot, D, generator=g, device=dev).half()
+        q = torch.randn(B, Hq, D, generator=g, device=dev).half()
+        sets.append((q, kc, kn, vc, vn, kh, vh, perm, torch.empty_like(q)))
+
+    def launch(i):
+        q, kc, kn, vc, vn, kh, vh, perm, out = sets[i]
+        kernels.tq_paged_decode_attn(q, kc, kn, vc, vn, kh, vh, PiK, PiV, cent, 3, indptr, perm, lens, L, D ** -0.5,
+                                     out)
+    wall, _, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
+    kmean, kmed = _kernel_time(launch, len(sets), args.steps, args.warmup, torch)
+    # the same codes per sequence for the dense kernel (set 0), and the two outputs compared
+    q, kc, kn, vc, vn, kh, vh, perm, out = sets[0]
+    pg = perm.long().view(B, npg)
+    dk = kc[pg].permute(0, 2, 1, 3, 4).reshape(B, Hkv, cold, 64).contiguous()
+    dv = vc[pg].permute(0, 2, 1, 3, 4).reshape(B, Hkv, cold, 64).contiguous()
+    dkn = kn[pg].permute(0, 2, 1, 3).reshape(B, Hkv, cold).contiguous()
+    dvn = vn[pg].permute(0, 2, 1, 3).reshape(B, Hkv, cold).contiguous()
+    dout = torch.empty_like(q)
+    ws = torch.empty(kernels.decode_attn_workspace_bytes(B, Hq, Hkv, L), dtype=torch.uint8, device=dev)
+
+    def dense(_):
+        kernels.tq_decode_attn_out(q, dk, dkn, dv, dvn, kh, vh, PiK, PiV, cent, 3, seq, L, D ** -0.5, dout, ws)
+    dmean, _ = _kernel_time(dense, 1, args.steps, args.warmup, torch)
+    launch(0)
+    torch.cuda.synchronize()
+    rel = float((out.float() - dout.float()).norm() / dout.float().norm())
+    alg = B * Hkv * (cold * (64 + 64 + 4 + 4) + hot * D * 2 * 2) + 2 * B * Hq * D * 2 + B * npg * 4
+    achieved = alg / (kmean * 1e-3) / 1e9
+    return {
+        "metric": "paged packed-KV decode attention HBM GB/s (B=16, 32/8 heads, 4096 cold in 16-token pages + 64 hot)",
+        "value": round(achieved, 1), "unit": "GB/s", "ms_per_step": round(wall, 5), "higher_is_better": True,
+        "dtype": "3-bit codes, fp16 MFMA scores/values, fp32 softmax",
+        "config": {"workload": "paged_packed_attention", "batch": B, "heads": "32/8", "cold": cold, "hot": hot,
+                   "page_size": ps, "alg_bytes_per_call": alg, "sets": len(sets),
+                   "dense_layout": {"kernel": "lkv_tq_decode_attn on the same codes", "us": round(dmean * 1e3, 2),
+                                    "paged_over_dense": round(kmean / dmean, 3), "rel_diff": rel}},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "tq_attn_split_kernel<true,false,true> + tq_attn_combine_kernel (one call)",
+                     "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3)},
+    }
+
+
 # ------------------------------------------------------------------ B > 1
 def bench_batched(args, torch):
     """B=8 decode rows through one TEAL-sparse projection at the config-1 shape (W[4096,14336], each row
@@ -894,7 +968,7 @@ def main():
         _fill_gemv_defaults(args)
         fn = {"gemv": bench_gemv, "mlp": bench_mlp, "copy": bench_copy, "quant": bench_quant,
               "attn": bench_attn, "prefill": bench_prefill, "batched": bench_batched,
-              "paged": bench_paged, "prod": bench_prod}.get(args.workload)
+              "paged": bench_paged, "tqpaged": bench_tq_paged, "prod": bench_prod}.get(args.workload)
         if fn is None:
             print("bench.py: workload %s is not implemented yet" % args.workload, file=sys.stderr)
             sys.exit(2)

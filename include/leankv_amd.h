@@ -280,6 +280,33 @@ int lkv_paged_decode_attn(const void* q, const void* kv_data, const int32_t* kv_
                           int64_t max_len, float scale, void* out, void* workspace,
                           size_t workspace_bytes, void* stream);
 
+/*
+ * Decode attention over a PAGED packed (TurboQuant) cache, one layer.  No
+ * counterpart in the reference, whose paged cache (paged_cache.py:32-362) is
+ * fp16: this is lkv_tq_decode_attn with the cold store in pages, for ragged
+ * batches that grow and free pages independently.  Same math as
+ * lkv_tq_decode_attn (cache.py:169-189 semantics + sdpa_attention.py:79-105).
+ *   k_codes, v_codes: uint8 [max_pages, Hkv, page_size, 64] (4-bit nibbles)
+ *   k_norms, v_norms: fp32  [max_pages, Hkv, page_size]
+ *   sequence b's cold token t (t < seq_lens[b] - hot_cap) lies in page
+ *   kv_indices[kv_indptr[b] + t / page_size], slot t % page_size (FlashInfer's
+ *   CSR page table, int32 device arrays);
+ *   k_hot, v_hot: fp16 [B, Hkv, hot_cap, 128] rings (token t in slot t % hot_cap);
+ *   seq_lens: int32 [B] on the device, each <= max_len.
+ * page_size 16, 32, 64 or 128; the code pool below 2^32 bytes.  Page ids are
+ * clamped to the pool and tokens past a sequence's pages are not read.
+ */
+size_t lkv_tq_paged_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len,
+                                                int64_t page_size);
+int lkv_tq_paged_decode_attn(const void* q, const uint8_t* k_codes, const float* k_norms,
+                             const uint8_t* v_codes, const float* v_norms, const void* k_hot,
+                             const void* v_hot, const float* PiK, const float* PiV,
+                             const float* centroids, int bits, const int32_t* kv_indptr,
+                             const int32_t* kv_indices, const int32_t* seq_lens, int64_t B,
+                             int64_t Hq, int64_t Hkv, int64_t page_size, int64_t max_pages,
+                             int64_t max_len, int64_t hot_cap, float scale, void* out,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Fused B=1 decode step                                                     */
 /* ------------------------------------------------------------------------ */

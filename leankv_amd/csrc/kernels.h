@@ -193,7 +193,10 @@ struct AttnPlan {
   int nsplit, split_tokens;
   size_t qrot_off, part_off, total;
 };
-AttnPlan attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_cap);
+// max_split_tokens > 0 caps the tokens of one split (the paged layout stages a
+// split's page ids in LDS); the split count then grows past the target.
+AttnPlan attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_cap,
+                   int64_t max_split_tokens = 0);
 
 struct AttnCall {
   const float* qrot;        // [B, Hq, 128] fp32 = q @ PiK^T (when PiK is null)
@@ -229,6 +232,13 @@ struct AttnCall {
   uint16_t* q16;
   uint16_t* k_ring;
   uint16_t* v_ring;
+  // Paged cold store, set when indptr is non-null: k/v codes and norms are
+  // pools of [max_pages][Hkv][1 << page_shift] rows, sequence b owns pages
+  // indices[indptr[b] .. indptr[b + 1]) and seq_len holds B lengths.
+  const int32_t* indptr;
+  const int32_t* indices;
+  int page_shift;
+  int64_t max_pages;
 };
 // Launch the split and combine kernels.
 int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st);

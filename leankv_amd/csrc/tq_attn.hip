@@ -75,6 +75,12 @@ struct AttnParams {
   uint16_t* out;            // [B, Hq, 128]
   float scale_log2;         // scale * log2(e)
   int max_len, Hq, Hkv, G, cap, hot_cap, nsplit, split_tokens, ncent;
+  // paged cold store only: FlashInfer's CSR page table over pools of
+  // [max_pages][Hkv][page_size] rows, seq_len holding one length per sequence
+  const int32_t* indptr;
+  const int32_t* indices;
+  int page_shift, max_pages;
+  uint32_t pool_code_bytes, pool_norm_bytes;
   // decode step only (AttnCall: q|k|v partials, RoPE, ring write)
   const float* pq;
   const float* pk;
@@ -116,54 +122,78 @@ struct BlockRegs {
   uint32_t vdw[8];
 };
 
+// Token -> row of the buffer resources.  Dense: the (batch, kv head) slice is
+// contiguous, row = token.  Paged: token t of the split lies in page
+// s_pg[(t - t_begin) >> shift] at slot t % page_size, and the pools hold rows
+// (page * Hkv + kv head) * page_size + slot, so a 16-token tile (page size a
+// multiple of 16, tiles 16-aligned) is 16 consecutive rows.
+struct DenseRows {
+  __device__ __forceinline__ int operator()(int t) const { return t; }
+};
+struct PagedRows {
+  const int* s_pg;
+  int t_begin, shift, kvh, Hkv;
+  __device__ __forceinline__ int operator()(int t) const {
+    const int pg = s_pg[(t - t_begin) >> shift];
+    return ((pg * Hkv + kvh) << shift) + (t & ((1 << shift) - 1));
+  }
+};
+
 // A block entirely below the valid end.  Each load's voffset is one of two
 // lane bases; everything that depends on the block or the load is in the
 // scalar soffset (so no per-load vector address registers stay live).
-__device__ __forceinline__ void load_full(BlockRegs& R, const ColdRsrc& rs, int t0, int lane) {
+template <typename Rows>
+__device__ __forceinline__ void load_full(BlockRegs& R, const ColdRsrc& rs, int t0, int lane, const Rows& rows) {
   const int g = lane >> 4, w = lane & 15;
   const int vk = w * kRowB + 16 * g;   // key codes: token w, bytes 16g..
   const int vv = 4 * g * kRowB + 4 * w;  // value codes: token 4g, dword w
   const int vnrm = 16 * g;             // norms: token 4g
-  const int sc = t0 * kRowB, sn = t0 * 4;
+  const int r0 = __builtin_amdgcn_readfirstlane(rows(t0)), r1 = __builtin_amdgcn_readfirstlane(rows(t0 + 16));
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
-    R.kraw[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kc, vk, sc + 16 * tt * kRowB, 0));
-    R.kn[tt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kn, vnrm, sn + 64 * tt, 0));
-    R.vn[tt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.vn, vnrm, sn + 64 * tt, 0));
+    const int sc = (tt ? r1 : r0) * kRowB, sn = (tt ? r1 : r0) * 4;
+    R.kraw[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kc, vk, sc, 0));
+    R.kn[tt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kn, vnrm, sn, 0));
+    R.vn[tt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.vn, vnrm, sn, 0));
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j)
-    R.vdw[j] = __builtin_amdgcn_raw_buffer_load_b32(rs.vc, vv, sc + (16 * (j >> 2) + (j & 3)) * kRowB, 0);
+    R.vdw[j] = __builtin_amdgcn_raw_buffer_load_b32(rs.vc, vv, ((j >> 2) ? r1 : r0) * kRowB + (j & 3) * kRowB, 0);
 }
 
 // A block reaching past t_lim: tokens at or past t_lim read token t_lim - 1
 // (valid memory); the caller masks them.
-__device__ __forceinline__ void load_clamped(BlockRegs& R, const ColdRsrc& rs, int t0, int t_lim, int lane) {
+template <typename Rows>
+__device__ __forceinline__ void load_clamped(BlockRegs& R, const ColdRsrc& rs, int t0, int t_lim, int lane,
+                                             const Rows& rows) {
   const int g = lane >> 4, w = lane & 15;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int tk = min(t0 + 16 * tt + w, t_lim - 1);
-    R.kraw[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kc, tk * kRowB + 16 * g, 0, 0));
+    R.kraw[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kc, rows(tk) * kRowB + 16 * g, 0, 0));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tn = min(t0 + 16 * tt + 4 * g + i, t_lim - 1);
-      R.kn[tt][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.kn, tn * 4, 0, 0));
-      R.vn[tt][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.vn, tn * 4, 0, 0));
+      const int rn = rows(tn);
+      R.kn[tt][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.kn, rn * 4, 0, 0));
+      R.vn[tt][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.vn, rn * 4, 0, 0));
     }
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int tv = min(t0 + 16 * (j >> 2) + 4 * g + (j & 3), t_lim - 1);
-    R.vdw[j] = __builtin_amdgcn_raw_buffer_load_b32(rs.vc, tv * kRowB + 4 * w, 0, 0);
+    R.vdw[j] = __builtin_amdgcn_raw_buffer_load_b32(rs.vc, rows(tv) * kRowB + 4 * w, 0, 0);
   }
 }
 
-__device__ __forceinline__ void fetch_block(BlockRegs& R, const ColdRsrc& rs, int t0, int t_addr_end, int lane) {
+template <typename Rows>
+__device__ __forceinline__ void fetch_block(BlockRegs& R, const ColdRsrc& rs, int t0, int t_addr_end, int lane,
+                                            const Rows& rows) {
   t0 = __builtin_amdgcn_readfirstlane(t0);  // wave-uniform: keeps the token offset scalar
   if (t0 + kBlk <= t_addr_end)
-    load_full(R, rs, t0, lane);
+    load_full(R, rs, t0, lane, rows);
   else
-    load_clamped(R, rs, t0, t_addr_end, lane);
+    load_clamped(R, rs, t0, t_addr_end, lane, rows);
 }
 
 // Online-softmax state of one lane: head w = lane % 16, output dims
@@ -299,9 +329,13 @@ constexpr int kORow = kD + 4;  // padded LDS row of the per-wave outputs
 // budget and the split count.
 constexpr int kSplitBlocksPerCU = LKV_ATTN_BLOCKS_PER_CU;
 
-template <bool PERM, bool DECODE>
+constexpr int kMaxPg = 256;  // pages of one split in the paged layout
+
+template <bool PERM, bool DECODE, bool PAGED>
 __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_kernel(AttnParams P) {
+  static_assert(!(PAGED && DECODE), "the fused decode step uses the dense layout");
   __shared__ uint32_t s_lut[256];
+  __shared__ int s_pg[PAGED ? kMaxPg : 1];
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
   __shared__ __align__(16) float s_o[kWaves][16][kORow];  // all 16 heads: rows >= G are never read
 
@@ -316,16 +350,44 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
   // So the length load, the wave's first token block, the centroids and the
   // rotated query are all in flight before the first wait.
   const int t_begin = split * P.split_tokens;
-  const int t_addr_end = min(t_begin + P.split_tokens, P.cap);  // valid memory
-  const int seq_len = __builtin_amdgcn_readfirstlane(*P.seq_len);
+  int t_addr_end, seq_len;  // valid memory: tokens below t_addr_end
   ColdRsrc rs;
-  rs.kc = make_rsrc(P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB, static_cast<uint32_t>(P.cap) * kRowB);
-  rs.vc = make_rsrc(P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB, static_cast<uint32_t>(P.cap) * kRowB);
-  rs.kn = make_rsrc(P.k_norms + bh * static_cast<size_t>(P.cap), static_cast<uint32_t>(P.cap) * 4);
-  rs.vn = make_rsrc(P.v_norms + bh * static_cast<size_t>(P.cap), static_cast<uint32_t>(P.cap) * 4);
+  const PagedRows prow{s_pg, t_begin, P.page_shift, kvh, P.Hkv};
+  if constexpr (PAGED) {
+    // Sequence b owns pages indices[indptr[b] .. indptr[b + 1]); the split's
+    // pages go to LDS, clamped to the pool; tokens past the sequence's pages
+    // are past t_addr_end (the page of a clamped load is always one it owns).
+    seq_len = __builtin_amdgcn_readfirstlane(P.seq_len[b]);
+    const int pbeg = P.indptr[b], npg_seq = max(0, P.indptr[b + 1] - pbeg);
+    t_addr_end = min(t_begin + P.split_tokens, npg_seq << P.page_shift);
+    const int first = t_begin >> P.page_shift, npg = P.split_tokens >> P.page_shift;
+    for (int i = tid; i < npg; i += kThreads) {
+      const int pi = min(first + i, npg_seq - 1);
+      const int pg = pi >= 0 ? P.indices[pbeg + pi] : 0;
+      s_pg[i] = min(max(pg, 0), P.max_pages - 1);
+    }
+    rs.kc = make_rsrc(P.k_codes, P.pool_code_bytes);
+    rs.vc = make_rsrc(P.v_codes, P.pool_code_bytes);
+    rs.kn = make_rsrc(P.k_norms, P.pool_norm_bytes);
+    rs.vn = make_rsrc(P.v_norms, P.pool_norm_bytes);
+    __syncthreads();  // page ids
+  } else {
+    t_addr_end = min(t_begin + P.split_tokens, P.cap);
+    seq_len = __builtin_amdgcn_readfirstlane(*P.seq_len);
+    rs.kc = make_rsrc(P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB, static_cast<uint32_t>(P.cap) * kRowB);
+    rs.vc = make_rsrc(P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB, static_cast<uint32_t>(P.cap) * kRowB);
+    rs.kn = make_rsrc(P.k_norms + bh * static_cast<size_t>(P.cap), static_cast<uint32_t>(P.cap) * 4);
+    rs.vn = make_rsrc(P.v_norms + bh * static_cast<size_t>(P.cap), static_cast<uint32_t>(P.cap) * 4);
+  }
+  auto fetch = [&](BlockRegs& R, int t) {
+    if constexpr (PAGED)
+      fetch_block(R, rs, t, t_addr_end, lane, prow);
+    else
+      fetch_block(R, rs, t, t_addr_end, lane, DenseRows{});
+  };
   BlockRegs ra, rb;
   int t0 = t_begin + wave * kBlk;
-  if (t0 < t_addr_end) fetch_block(ra, rs, t0, t_addr_end, lane);
+  if (t0 < t_addr_end) fetch(ra, t0);
   float c_lo = 0.f, c_hi = 0.f;
   uint32_t tab[4] = {0u, 0u, 0u, 0u};
   if constexpr (PERM) {
@@ -453,11 +515,11 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
   constexpr int kStep = kWaves * kBlk;
   while (t0 < t_end) {
     const int t1 = t0 + kStep;
-    if (t1 < t_end) fetch_block(rb, rs, t1, t_addr_end, lane);
+    if (t1 < t_end) fetch(rb, t1);
     attend<PERM>(ra, t0, t_end, qa, tab, s_lut, lane, S);
     if (t1 >= t_end) break;
     const int t2 = t1 + kStep;
-    if (t2 < t_end) fetch_block(ra, rs, t2, t_addr_end, lane);
+    if (t2 < t_end) fetch(ra, t2);
     attend<PERM>(rb, t1, t_end, qa, tab, s_lut, lane, S);
     t0 = t2;
   }
@@ -534,7 +596,7 @@ __global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnPa
   const int hq = blockIdx.x, b = blockIdx.y;
   const int G = P.G, kvh = hq / G, hh = hq % G;
   const int ns = P.nsplit;
-  const int seq_len = *P.seq_len;  // only the masks below depend on it
+  const int seq_len = P.indptr ? P.seq_len[b] : *P.seq_len;  // only the masks below depend on it
   const size_t bh = static_cast<size_t>(b) * P.Hkv + kvh;
   const int RF = rec_floats(G);
   const float* recs = P.partials + bh * ns * RF;
@@ -708,15 +770,17 @@ int64_t target_splits(int64_t B, int64_t Hkv) {
 
 }  // namespace
 
-AttnPlan attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_cap) {
+AttnPlan attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_cap, int64_t max_split_tokens) {
   AttnPlan p{};
   const int64_t G = Hkv > 0 ? Hq / Hkv : 1;
   const int64_t cold_max = max_len > hot_cap ? max_len - hot_cap : 0;
-  const int64_t ns_cap = target_splits(B, Hkv);
+  int64_t ns_cap = target_splits(B, Hkv);
   int64_t ts = (cold_max + ns_cap - 1) / ns_cap;
   ts = (ts + kSplitGran - 1) / kSplitGran * kSplitGran;
   if (ts < kSplitGran) ts = kSplitGran;
+  if (max_split_tokens > 0 && ts > max_split_tokens) ts = max_split_tokens / kSplitGran * kSplitGran;
   int64_t ns = (cold_max + ts - 1) / ts;
+  if (ns > ns_cap) ns_cap = ns;
   if (ns < 1) ns = 1;
   p.nsplit = static_cast<int>(ns);
   p.split_tokens = static_cast<int>(ts);
@@ -766,18 +830,29 @@ int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st) {
   P.q16 = c.q16;
   P.k_ring = c.k_ring;
   P.v_ring = c.v_ring;
+  P.indptr = c.indptr;
+  P.indices = c.indices;
+  P.page_shift = c.page_shift;
+  P.max_pages = static_cast<int>(c.max_pages);
+  P.pool_code_bytes = static_cast<uint32_t>(c.max_pages * c.Hkv * (int64_t(1) << c.page_shift) * kRowB);
+  P.pool_norm_bytes = static_cast<uint32_t>(c.max_pages * c.Hkv * (int64_t(1) << c.page_shift) * 4);
   if (c.pq != nullptr) {
     P.q = c.q16;  // the combine's hot-window query
     P.k_hot = c.k_ring;
     P.v_hot = c.v_ring;
     if (c.bits == 3)
-      hipLaunchKernelGGL((tq_attn_split_kernel<true, true>), grid, dim3(kThreads), 0, st, P);
+      hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false>), grid, dim3(kThreads), 0, st, P);
     else
-      hipLaunchKernelGGL((tq_attn_split_kernel<false, true>), grid, dim3(kThreads), 0, st, P);
+      hipLaunchKernelGGL((tq_attn_split_kernel<false, true, false>), grid, dim3(kThreads), 0, st, P);
+  } else if (c.indptr != nullptr) {
+    if (c.bits == 3)
+      hipLaunchKernelGGL((tq_attn_split_kernel<true, false, true>), grid, dim3(kThreads), 0, st, P);
+    else
+      hipLaunchKernelGGL((tq_attn_split_kernel<false, false, true>), grid, dim3(kThreads), 0, st, P);
   } else if (c.bits == 3) {
-    hipLaunchKernelGGL((tq_attn_split_kernel<true, false>), grid, dim3(kThreads), 0, st, P);
+    hipLaunchKernelGGL((tq_attn_split_kernel<true, false, false>), grid, dim3(kThreads), 0, st, P);
   } else {
-    hipLaunchKernelGGL((tq_attn_split_kernel<false, false>), grid, dim3(kThreads), 0, st, P);
+    hipLaunchKernelGGL((tq_attn_split_kernel<false, false, false>), grid, dim3(kThreads), 0, st, P);
   }
   LKV_LAUNCH_CHECK("tq_decode_attn split");
   hipLaunchKernelGGL(tq_attn_combine_kernel, cgrid, dim3(kCombThreads), 0, st, P);
@@ -855,4 +930,84 @@ extern "C" int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const f
   c.hot_cap = hot_cap;
   c.bits = bits;
   return attn_launch(c, pl, st);
+}
+
+// ------------------------------------------------------------ paged cold store
+namespace {
+int page_shift_of(int64_t page_size) {
+  for (int sh = 4; sh <= 7; ++sh)
+    if (page_size == (int64_t(1) << sh)) return sh;
+  return -1;
+}
+AttnPlan paged_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t hot_cap, int64_t page_size) {
+  return attn_plan(B, Hq, Hkv, max_len, hot_cap, int64_t(kMaxPg) * page_size);
+}
+}  // namespace
+
+extern "C" size_t lkv_tq_paged_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len,
+                                                           int64_t page_size) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len < 0 || page_shift_of(page_size) < 0) return kTicketBytes;
+  return paged_plan(B, Hq, Hkv, max_len, 0, page_size).total;
+}
+
+extern "C" int lkv_tq_paged_decode_attn(const void* q, const uint8_t* k_codes, const float* k_norms,
+                                        const uint8_t* v_codes, const float* v_norms, const void* k_hot,
+                                        const void* v_hot, const float* PiK, const float* PiV, const float* centroids,
+                                        int bits, const int32_t* kv_indptr, const int32_t* kv_indices,
+                                        const int32_t* seq_lens, int64_t B, int64_t Hq, int64_t Hkv,
+                                        int64_t page_size, int64_t max_pages, int64_t max_len, int64_t hot_cap,
+                                        float scale, void* out, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+  LKV_REQUIRE(bits == 3 || bits == 4, "tq_paged_decode_attn: bits=%d unsupported (4-bit nibble layouts only)", bits);
+  LKV_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16,
+              "tq_paged_decode_attn: need Hq %% Hkv == 0 and Hq/Hkv <= 16 (Hq=%lld Hkv=%lld)", (long long)Hq,
+              (long long)Hkv);
+  const int shift = page_shift_of(page_size);
+  LKV_REQUIRE(shift >= 0, "tq_paged_decode_attn: page_size=%lld must be 16, 32, 64 or 128", (long long)page_size);
+  LKV_REQUIRE(hot_cap >= 1 && hot_cap <= kHotMax, "tq_paged_decode_attn: hot_cap must be 1..64");
+  LKV_REQUIRE(max_pages >= 1 && max_pages * Hkv * page_size * kRowB < (int64_t(1) << 32),
+              "tq_paged_decode_attn: max_pages=%lld: the code pool must hold fewer than 2^32 bytes",
+              (long long)max_pages);
+  LKV_REQUIRE(max_len >= 0 && max_len < (1ll << 31), "tq_paged_decode_attn: bad max_len");
+  if (B == 0) return LKV_OK;
+  LKV_REQUIRE(q && k_codes && k_norms && v_codes && v_norms && k_hot && v_hot && PiK && PiV && centroids &&
+                  kv_indptr && kv_indices && seq_lens && out && workspace,
+              "tq_paged_decode_attn: null pointer");
+  LKV_REQUIRE(aligned16(q) && aligned16(k_codes) && aligned16(v_codes) && aligned16(k_norms) &&
+                  aligned16(v_norms) && aligned16(k_hot) && aligned16(v_hot) && aligned16(PiK) && aligned16(out) &&
+                  aligned16(workspace),
+              "tq_paged_decode_attn: q, pools, hot rings, PiK, out and workspace must be 16-byte aligned");
+  const AttnPlan pl = paged_plan(B, Hq, Hkv, max_len, hot_cap, page_size);
+  LKV_REQUIRE(pl.nsplit <= kMaxSplits - 1, "tq_paged_decode_attn: max_len=%lld needs %d splits (at most %d)",
+              (long long)max_len, pl.nsplit, kMaxSplits - 1);
+  LKV_REQUIRE(workspace_bytes >= pl.total, "tq_paged_decode_attn: workspace of %zu bytes required, got %zu",
+              pl.total, workspace_bytes);
+  AttnCall c{};
+  c.qrot = nullptr;
+  c.PiK = PiK;
+  c.q = static_cast<const uint16_t*>(q);
+  c.k_codes = k_codes;
+  c.k_norms = k_norms;
+  c.v_codes = v_codes;
+  c.v_norms = v_norms;
+  c.k_hot = static_cast<const uint16_t*>(k_hot);
+  c.v_hot = static_cast<const uint16_t*>(v_hot);
+  c.PiV = PiV;
+  c.centroids = centroids;
+  c.seq_len = seq_lens;
+  c.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + pl.part_off);
+  c.out = static_cast<uint16_t*>(out);
+  c.scale = scale;
+  c.max_len = max_len;
+  c.B = B;
+  c.Hq = Hq;
+  c.Hkv = Hkv;
+  c.cap = 0;
+  c.hot_cap = hot_cap;
+  c.bits = bits;
+  c.indptr = kv_indptr;
+  c.indices = kv_indices;
+  c.page_shift = shift;
+  c.max_pages = max_pages;
+  return attn_launch(c, pl, static_cast<hipStream_t>(stream));
 }

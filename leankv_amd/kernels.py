@@ -200,8 +200,9 @@ def tq_quantize(x: torch.Tensor, Pi: torch.Tensor, bounds: torch.Tensor, bits: i
     b = bounds.to(device=x.device, dtype=torch.float32).contiguous()
     if b.numel() != (1 << bits) - 1:
         raise LeanKVError("tq_quantize: %d decision boundaries for bits=%d" % (b.numel(), bits))
+    Pc = _pi(Pi, x.device)  # held until the call returns: a temporary's memory could be reused
     check(
-        lib.lkv_tq_quantize(ptr(xc), dtype_code(x.dtype), M, ptr(_pi(Pi, x.device)), ptr(b), int(bits),
+        lib.lkv_tq_quantize(ptr(xc), dtype_code(x.dtype), M, ptr(Pc), ptr(b), int(bits),
                             ptr(packed), ptr(norms), stream_handle(x.device)),
         "lkv_tq_quantize",
     )
@@ -237,8 +238,9 @@ def tq_dequantize(packed: torch.Tensor, norms: torch.Tensor, Pi: torch.Tensor, c
     if out is None:
         out = torch.empty(*packed.shape[:-1], HEAD_DIM, dtype=out_dtype, device=packed.device)
     c = centroids.to(device=packed.device, dtype=torch.float32).contiguous()
+    Pc = _pi(Pi, packed.device)
     check(
-        _lib_handle().lkv_tq_dequantize(ptr(pc), ptr(nc), dtype_code(nc.dtype), M, ptr(_pi(Pi, packed.device)),
+        _lib_handle().lkv_tq_dequantize(ptr(pc), ptr(nc), dtype_code(nc.dtype), M, ptr(Pc),
                                         ptr(c), int(bits), ptr(out), dtype_code(out.dtype),
                                         stream_handle(packed.device)),
         "lkv_tq_dequantize",
@@ -252,8 +254,9 @@ def tq_rotate(x: torch.Tensor, Pi: torch.Tensor, transpose: bool = False) -> tor
     M = _rows(x, "tq_rotate")
     xc = x.contiguous()
     y = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    Pc = _pi(Pi, x.device)
     check(
-        _lib_handle().lkv_tq_rotate(ptr(xc), dtype_code(x.dtype), M, ptr(_pi(Pi, x.device)), int(bool(transpose)),
+        _lib_handle().lkv_tq_rotate(ptr(xc), dtype_code(x.dtype), M, ptr(Pc), int(bool(transpose)),
                                     ptr(y), stream_handle(x.device)),
         "lkv_tq_rotate",
     )
@@ -274,9 +277,10 @@ def tq_prod_quantize(x: torch.Tensor, Pi: torch.Tensor, bounds: torch.Tensor, ce
     norms = torch.empty(x.shape[:-1], dtype=x.dtype, device=x.device)
     signs = torch.empty(*x.shape[:-1], HEAD_DIM // 8, dtype=torch.uint8, device=x.device)
     rnorms = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    Pc, Sc = _pi(Pi, x.device), _pi(S, x.device)  # both alive until the call returns
     check(
-        _lib_handle().lkv_tq_prod_quantize(ptr(xc), dtype_code(x.dtype), M, ptr(_pi(Pi, x.device)), ptr(b), ptr(c),
-                                           ptr(_pi(S, x.device)), int(mse_bits), ptr(codes), ptr(norms), ptr(signs),
+        _lib_handle().lkv_tq_prod_quantize(ptr(xc), dtype_code(x.dtype), M, ptr(Pc), ptr(b), ptr(c),
+                                           ptr(Sc), int(mse_bits), ptr(codes), ptr(norms), ptr(signs),
                                            ptr(rnorms), stream_handle(x.device)),
         "lkv_tq_prod_quantize",
     )
@@ -301,10 +305,12 @@ def tq_prod_dequantize(codes: torch.Tensor, norms: torch.Tensor, signs: torch.Te
     rn = rnorms.to(torch.float32).contiguous()
     c = _vec(centroids, codes.device, 1 << mse_bits, "centroids")
     out = torch.empty(*codes.shape[:-1], HEAD_DIM, dtype=out_dtype, device=codes.device)
+    cc, sc = codes.contiguous(), signs.contiguous()
+    Pc, Sc = _pi(Pi, codes.device), _pi(S, codes.device)
     check(
-        _lib_handle().lkv_tq_prod_dequantize(ptr(codes.contiguous()), ptr(nc), dtype_code(nc.dtype),
-                                             ptr(signs.contiguous()), ptr(rn), M, ptr(_pi(Pi, codes.device)), ptr(c),
-                                             ptr(_pi(S, codes.device)), int(mse_bits), float(qjl_scale), ptr(out),
+        _lib_handle().lkv_tq_prod_dequantize(ptr(cc), ptr(nc), dtype_code(nc.dtype),
+                                             ptr(sc), ptr(rn), M, ptr(Pc), ptr(c),
+                                             ptr(Sc), int(mse_bits), float(qjl_scale), ptr(out),
                                              dtype_code(out.dtype), stream_handle(codes.device)),
         "lkv_tq_prod_dequantize",
     )
@@ -480,6 +486,56 @@ def paged_decode_attn(q: torch.Tensor, kv_data: torch.Tensor, kv_indptr: torch.T
     return out
 
 
+def tq_paged_decode_attn(q: torch.Tensor, k_codes: torch.Tensor, k_norms: torch.Tensor, v_codes: torch.Tensor,
+                         v_norms: torch.Tensor, k_hot: torch.Tensor, v_hot: torch.Tensor, PiK: torch.Tensor,
+                         PiV: torch.Tensor, centroids: torch.Tensor, bits: int, kv_indptr: torch.Tensor,
+                         kv_indices: torch.Tensor, seq_lens: torch.Tensor, max_len: int, scale: float | None = None,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention of q fp16 [B, Hq, 128] over a paged packed cache: code pools uint8
+    [max_pages, Hkv, page_size, 64], norm pools fp32 [max_pages, Hkv, page_size], fp16 hot rings
+    [B, Hkv, hot_cap, 128], FlashInfer's CSR page table and per-sequence lengths (int32 device tensors)."""
+    require_cuda(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, kv_indptr, kv_indices, seq_lens)
+    if q.dtype != torch.float16 or q.dim() != 3 or q.shape[-1] != HEAD_DIM or not q.is_contiguous():
+        raise LeanKVError("tq_paged_decode_attn: q must be contiguous float16 [B, Hq, 128]")
+    B, Hq, _ = q.shape
+    if k_codes.dim() != 4 or k_codes.dtype != torch.uint8 or k_codes.shape[-1] != 64:
+        raise LeanKVError("tq_paged_decode_attn: code pools must be uint8 [max_pages, Hkv, page_size, 64]")
+    max_pages, Hkv, page_size, _ = k_codes.shape
+    for t, shape, dt, nm in ((v_codes, k_codes.shape, torch.uint8, "v_codes"),
+                             (k_norms, k_codes.shape[:3], torch.float32, "k_norms"),
+                             (v_norms, k_codes.shape[:3], torch.float32, "v_norms")):
+        if tuple(t.shape) != tuple(shape) or t.dtype != dt or not t.is_contiguous():
+            raise LeanKVError("tq_paged_decode_attn: %s must be contiguous %s %s" % (nm, dt, tuple(shape)))
+    if not (k_codes.is_contiguous() and k_hot.is_contiguous() and v_hot.is_contiguous()):
+        raise LeanKVError("tq_paged_decode_attn: pools and hot rings must be contiguous")
+    if k_hot.dim() != 4 or tuple(k_hot.shape[:2]) != (B, Hkv) or k_hot.shape != v_hot.shape:
+        raise LeanKVError("tq_paged_decode_attn: hot rings must be float16 [B, Hkv, hot_cap, 128]")
+    for t, nm, n in ((kv_indptr, "kv_indptr", B + 1), (seq_lens, "seq_lens", B)):
+        if t.dtype != torch.int32 or not t.is_contiguous() or t.numel() != n:
+            raise LeanKVError("tq_paged_decode_attn: %s must be a contiguous int32 tensor of %d entries" % (nm, n))
+    if kv_indices.dtype != torch.int32 or not kv_indices.is_contiguous():
+        raise LeanKVError("tq_paged_decode_attn: kv_indices must be a contiguous int32 tensor")
+    hot_cap = k_hot.shape[2]
+    if out is None:
+        out = torch.empty_like(q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(HEAD_DIM)
+    lib = _lib_handle()
+    nbytes = lib.lkv_tq_paged_decode_attn_workspace_bytes(B, Hq, Hkv, int(max_len), page_size)
+    ws = workspaces.get(q.device, "tq_paged", nbytes)
+    PKc, PVc = _pi(PiK, q.device), _pi(PiV, q.device)  # alive until the call returns
+    cen = _vec(centroids, q.device, 1 << bits, "centroids")
+    check(
+        lib.lkv_tq_paged_decode_attn(ptr(q), ptr(k_codes), ptr(k_norms), ptr(v_codes), ptr(v_norms), ptr(k_hot),
+                                     ptr(v_hot), ptr(PKc), ptr(PVc), ptr(cen), int(bits),
+                                     ptr(kv_indptr), ptr(kv_indices), ptr(seq_lens), B, Hq, Hkv, page_size, max_pages,
+                                     int(max_len), hot_cap, float(scale), ptr(out), ptr(ws), ws.numel(),
+                                     stream_handle(q.device)),
+        "lkv_tq_paged_decode_attn",
+    )
+    return out
+
+
 # ------------------------------------------------------------------ RMSNorm
 def rms_norm_out(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor) -> torch.Tensor:
     """out = RMSNorm(x) * weight over the last dim (fp16), rounded like HF MistralRMSNorm.
@@ -494,7 +550,8 @@ def rms_norm_out(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.T
         raise LeanKVError("rms_norm: weight must have %d elements and out the shape of x" % Z)
     xc = x.contiguous()
     M = xc.numel() // Z if Z else 0
-    check(_lib_handle().lkv_rmsnorm(ptr(xc), ptr(weight.contiguous()), float(eps), M, Z, ptr(out),
+    wc = weight.contiguous()
+    check(_lib_handle().lkv_rmsnorm(ptr(xc), ptr(wc), float(eps), M, Z, ptr(out),
                                     stream_handle(x.device)), "lkv_rmsnorm")
     return out
 

@@ -21,7 +21,8 @@ def test_header_declares_expected_entry_points():
     names = _declared()
     for n in ("lkv_sparse_gemv", "lkv_sparse_gateup_swiglu", "lkv_tq_quantize", "lkv_tq_quantize_rotated",
               "lkv_tq_dequantize", "lkv_tq_rotate", "lkv_tq_cache_append", "lkv_tq_decode_attn",
-              "lkv_tq_prefill_attn", "lkv_tq_prod_quantize", "lkv_tq_prod_dequantize"):
+              "lkv_tq_prefill_attn", "lkv_tq_prod_quantize", "lkv_tq_prod_dequantize",
+              "lkv_tq_paged_decode_attn"):
         assert n in names
 
 
@@ -111,6 +112,20 @@ def test_invalid_arguments_rejected_without_launch():
     assert lib.lkv_tq_prod_dequantize(p, p, 9, p, p, 16, p, p, p, 2, 0.01, p, 0, None) == -1
     assert lib.lkv_tq_prod_quantize(p, 0, 0, p, p, p, p, 2, p, p, p, p, None) == 0
     assert lib.lkv_tq_prod_dequantize(p, p, 0, p, p, 0, p, p, p, 2, 0.01, p, 0, None) == 0
+    # paged packed attention: page size not a power of two in 16..128, pool past 2^32 bytes, bits
+    assert lib.lkv_tq_paged_decode_attn(p, p, p, p, p, p, p, p, p, p, 3, p, p, p, 2, 32, 8, 24, 64, 100, 64, 0.1,
+                                        p, p, 1 << 20, None) == -1
+    assert "page_size" in _lib.last_error()
+    assert lib.lkv_tq_paged_decode_attn(p, p, p, p, p, p, p, p, p, p, 3, p, p, p, 2, 32, 8, 16, 1 << 20, 100, 64,
+                                        0.1, p, p, 1 << 20, None) == -1
+    assert "2^32" in _lib.last_error()
+    assert lib.lkv_tq_paged_decode_attn(p, p, p, p, p, p, p, p, p, p, 2, p, p, p, 2, 32, 8, 16, 64, 100, 64, 0.1,
+                                        p, p, 1 << 20, None) == -1
+    assert lib.lkv_tq_paged_decode_attn(p, p, p, p, p, p, p, p, p, p, 3, p, p, p, 16, 32, 8, 16, 64, 4096, 64,
+                                        0.1, p, p, 256, None) == -1
+    assert "workspace" in _lib.last_error()
+    assert lib.lkv_tq_paged_decode_attn(p, p, p, p, p, p, p, p, p, p, 3, p, p, p, 0, 32, 8, 16, 64, 100, 64, 0.1,
+                                        p, p, 0, None) == 0
     # empty problems are no-ops
     assert lib.lkv_tq_prefill_attn(p, p, p, p, p, p, p, p, p, p, 3, 100, 1, 8, 2, 0, 64, 64, 0.1, p, p, 0, None) == 0
     assert lib.lkv_sparse_gemv(p, p, 0.1, 0, 16, p, p, 0, None) == 0

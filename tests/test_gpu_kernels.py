@@ -446,6 +446,27 @@ def test_tq_prod_dequantize(cuda, mb):
     torch.testing.assert_close(out_h, ref_h, rtol=1e-5, atol=1e-5)
 
 
+def test_wrappers_keep_converted_operands_alive(cuda):
+    """Non-contiguous Pi / S views (a QR factor is column-major) are copied by the wrappers; each copy
+    must stay alive until the launch, or the next copy reuses its memory.  Results equal those of
+    contiguous operands bit for bit."""
+    from leankv_amd import kernels
+
+    Pi, S, c, b = _prod_tables(2)
+    Pn = Pi.t().contiguous().t().to(cuda)  # column-major views
+    Sn = S.t().contiguous().t().to(cuda)
+    Pc, Sc = Pi.contiguous().to(cuda), S.contiguous().to(cuda)
+    assert not Pn.is_contiguous() and not Sn.is_contiguous()
+    x = _kv((2, 300, 128), 50).to(cuda)
+    a = kernels.tq_prod_quantize(x, Pn, b[1:-1], c, Sn, 2)
+    r = kernels.tq_prod_quantize(x, Pc, b[1:-1].to(cuda), c.to(cuda), Sc, 2)
+    assert all(torch.equal(u, v) for u, v in zip(a, r))
+    scale = math.sqrt(math.pi / 2) / 128
+    d1 = kernels.tq_prod_dequantize(*r, Pn, c, Sn, 2, scale)
+    d2 = kernels.tq_prod_dequantize(*r, Pc, c.to(cuda), Sc, 2, scale)
+    assert torch.equal(d1, d2)
+
+
 def test_tq_prod_full_size(cuda):
     """Config-3 shape (K and V fp16 [8, 4096, 128], 4 channels x10): the fused kernel equals the separate
     kernels bit for bit, and the sketch halves the inner-product error of the MSE part alone."""
@@ -729,6 +750,154 @@ def test_paged_cache_decode_attention_matches_gathered(cuda):
         k, v = c[li]
         ref = oq.decode_attention(q.unsqueeze(2), k.cpu(), v.cpu()).squeeze(2)
         assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
+
+
+def _paged_tq_case(lens, Hq, Hkv, hot, ps, bits, seed, dev):
+    """Sequences of the given lengths in a paged packed cache built with the oracle (cold codes in pages
+    scattered over a pool whose other rows hold random codes and norms, fp16 hot rings); the HIP kernel
+    vs fp64 attention over each sequence's cat(dequantize(cold).fp16, hot)."""
+    from leankv_amd import kernels
+
+    c, bnd = oq.codebook_tensors(bits)
+    PiK, PiV = oq.rotation_matrix(128, 42), oq.rotation_matrix(128, 43)
+    g = torch.Generator().manual_seed(seed)
+    B = len(lens)
+    colds = [max(0, n - hot) for n in lens]
+    npages = [-(-cl // ps) for cl in colds]
+    max_pages = sum(npages) + 3
+    perm = torch.randperm(max_pages, generator=g).tolist()
+    mask = 0x77 if bits == 3 else 0xFF
+    kc = torch.randint(0, 256, (max_pages, Hkv, ps, 64), generator=g, dtype=torch.uint8) & mask
+    vc = torch.randint(0, 256, (max_pages, Hkv, ps, 64), generator=g, dtype=torch.uint8) & mask
+    kn = torch.rand(max_pages, Hkv, ps, generator=g) * 50 + 50  # rows no sequence owns: large, visible if read
+    vn = torch.rand(max_pages, Hkv, ps, generator=g) * 50 + 50
+    kh = torch.randn(B, Hkv, hot, 128, generator=g).half()
+    vh = torch.randn(B, Hkv, hot, 128, generator=g).half()
+    q = torch.randn(B, Hq, 128, generator=g).half()
+    indptr, indices, refs = [0], [], []
+    for b, n in enumerate(lens):
+        mine = perm[indptr[-1]:indptr[-1] + npages[b]]
+        indices += mine
+        indptr.append(indptr[-1] + npages[b])
+        K = _kv((Hkv, n, 128), seed + 17 * b)
+        V = _kv((Hkv, n, 128), seed + 17 * b + 5)
+        cl = colds[b]
+        Kref, Vref = K.clone(), V.clone()
+        if cl:
+            pk, nk, _ = oq.quantize(K[:, :cl].float(), PiK, bnd, bits)
+            pv, nv, _ = oq.quantize(V[:, :cl].float(), PiV, bnd, bits)
+            pg = torch.tensor([mine[t // ps] for t in range(cl)])
+            sl = torch.tensor([t % ps for t in range(cl)])
+            kc[pg, :, sl] = torch.from_numpy(pk).transpose(0, 1)
+            vc[pg, :, sl] = torch.from_numpy(pv).transpose(0, 1)
+            kn[pg, :, sl] = nk.t()
+            vn[pg, :, sl] = nv.t()
+            Kref[:, :cl] = oq.dequantize(pk, nk, PiK, c, bits).half()
+            Vref[:, :cl] = oq.dequantize(pv, nv, PiV, c, bits).half()
+        for p in range(cl, n):
+            kh[b, :, p % hot] = K[:, p]
+            vh[b, :, p % hot] = V[:, p]
+        refs.append(oq.decode_attention(q[b:b + 1].unsqueeze(2), Kref.unsqueeze(0), Vref.unsqueeze(0)).squeeze(2))
+    print("paged packed case lens=%s Hq=%d Hkv=%d hot=%d ps=%d bits=%d" % (lens, Hq, Hkv, hot, ps, bits), flush=True)
+    i32 = dict(dtype=torch.int32, device=dev)
+    out = kernels.tq_paged_decode_attn(q.to(dev), kc.to(dev), kn.to(dev), vc.to(dev), vn.to(dev), kh.to(dev),
+                                       vh.to(dev), PiK.to(dev), PiV.to(dev), c.to(dev), bits,
+                                       torch.tensor(indptr, **i32), torch.tensor(indices or [0], **i32),
+                                       torch.tensor(lens, **i32), max(lens)).cpu()
+    return out, torch.cat(refs)
+
+
+# (lengths, Hq, Hkv, hot window, page size, bits): config 4 through pages; ragged batches with hot-only,
+# window-boundary and page-boundary sequences; 32 / 64 / 128-token pages; 4-bit codes; 1 / 8 query heads
+# per kv head; a 9000-token sequence in a 32-sequence batch, so that a split's pages hit the LDS table
+# cap and the split count grows past the target.
+@pytest.mark.parametrize("lens,Hq,Hkv,hot,ps,bits", [
+    ([4096 + 64] * 16, 32, 8, 64, 16, 3),
+    ([1, 64, 65, 1000, 4160, 333, 17, 129], 32, 8, 64, 16, 3),
+    ([80, 81, 2000], 32, 4, 16, 32, 3),
+    ([700, 1, 3000], 8, 8, 64, 64, 4),
+    ([5000, 129, 4097], 64, 8, 64, 128, 3),
+    ([9000] + [100] * 31, 8, 8, 64, 16, 3),
+])
+def test_tq_paged_decode_attn(cuda, lens, Hq, Hkv, hot, ps, bits):
+    out, ref = _paged_tq_case(lens, Hq, Hkv, hot, ps, bits, seed=sum(lens) % 1000 + ps, dev=cuda)
+    assert torch.isfinite(out).all()
+    assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
+    assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
+
+
+def test_paged_tq_cache_matches_dense_cache(cuda):
+    """PagedTurboQuantCache vs TurboQuantCache on the same appends (a 300-token prefill, then 70 decode
+    tokens, 2 layers, 3 sequences): every sequence's cold codes and norms equal the dense cache's bit for
+    bit, and decode attention on the pages agrees with the dense kernel and with fp64 attention."""
+    from leankv_amd.turboquant.cache import TurboQuantCache
+    from leankv_amd.turboquant.paged_tq_cache import PagedTurboQuantCache
+
+    g = torch.Generator().manual_seed(21)
+    paged = PagedTurboQuantCache(num_layers=2, num_kv_heads=2, num_q_heads=8, page_size=16, max_pages=128,
+                                 max_batch_size=4, device=cuda)
+    dense = TurboQuantCache(num_layers=2, device=cuda, fused_attention=False, max_seq_len=512)
+    for S in [300] + [1] * 70:
+        for li in range(2):
+            k = (torch.randn(3, 2, S, 128, generator=g) * 2).half().to(cuda)
+            v = torch.randn(3, 2, S, 128, generator=g).half().to(cuda)
+            kp, vp = paged.update(k, v, li)
+            kd, vd = dense.update(k, v, li)
+            if S > 1:
+                assert torch.equal(kp, kd) and torch.equal(vp, vd)
+    q = torch.randn(3, 8, 128, generator=g).half().to(cuda)
+    for li in range(2):
+        n = dense._seq_lengths[li]
+        cl = n - 64
+        for b in range(3):
+            k_c, k_n, v_c, v_n = paged.cold_arrays(li, b)
+            assert torch.equal(k_c, dense._k_codes[li][b, :, :cl]) and torch.equal(v_c, dense._v_codes[li][b, :, :cl])
+            assert torch.equal(k_n, dense._k_norms[li][b, :, :cl]) and torch.equal(v_n, dense._v_norms[li][b, :, :cl])
+        out = paged.decode_attention(li, q).cpu()
+        seq = torch.tensor([n], dtype=torch.int32, device=cuda)
+        from leankv_amd import kernels
+
+        out_d = kernels.tq_decode_attn(q, dense._k_codes[li], dense._k_norms[li], dense._v_codes[li],
+                                       dense._v_norms[li], dense._k_hot[li], dense._v_hot[li], dense.PiK[li],
+                                       dense.PiV[li], dense.centroids, 3, seq, n).cpu()
+        assert ot.rel_err(out.numpy(), out_d.numpy()) < 2e-3
+        k, v = paged.gather(li, 3)
+        ref = oq.decode_attention(q.cpu().unsqueeze(2), k.cpu(), v.cpu()).squeeze(2)
+        assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
+
+
+def test_paged_tq_cache_ragged_free_and_reuse(cuda):
+    """Sequences appended one by one to different lengths, one freed and its pages reused by a new
+    sequence: decode attention of each equals fp64 attention over its own gathered K/V."""
+    from leankv_amd.turboquant.paged_tq_cache import PagedTurboQuantCache
+
+    g = torch.Generator().manual_seed(8)
+    c = PagedTurboQuantCache(num_layers=1, num_kv_heads=4, num_q_heads=16, page_size=32, max_pages=40,
+                             max_batch_size=3, hot_buffer_size=32, device=cuda)
+
+    def add(b, S):
+        c.append(0, b, torch.randn(4, S, 128, generator=g).half().to(cuda),
+                 torch.randn(4, S, 128, generator=g).half().to(cuda))
+
+    for b, S in ((0, 500), (1, 20), (2, 33)):
+        add(b, S)
+    used = c.get_pages_used()
+    assert used == -(-(500 - 32) // 32) + 0 + 1
+    c.free_sequence(0)
+    assert c.get_pages_used() == used - 15
+    add(0, 700)  # reuses the freed pages
+    for _ in range(5):
+        for b in range(3):
+            add(b, 1)
+    q = torch.randn(3, 16, 128, generator=g).half().to(cuda)
+    out = c.decode_attention(0, q).cpu()
+    k, v = c.gather(0, 3)
+    for b, n in enumerate((705, 25, 38)):
+        ref = oq.decode_attention(q[b:b + 1].cpu().unsqueeze(2), k[b:b + 1, :, :n].cpu(),
+                                  v[b:b + 1, :, :n].cpu()).squeeze(2)
+        assert ot.rel_err(out[b:b + 1].numpy(), ref.numpy()) < RTOL
+    with pytest.raises(RuntimeError, match="out of pages"):
+        add(1, 40 * 32)
 
 
 # Large batches (many (batch, kv head) pairs, few splits each): hot-only,
