@@ -566,6 +566,7 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
 }
 
 
+constexpr int kXcds = 8;  // MI355X: 8 accelerator complex dies, one L2 each
 constexpr int kCombThreads = 512;
 constexpr int kCombWaves = kCombThreads / kWave;
 constexpr int kMaxSplits = 256;
@@ -593,7 +594,17 @@ __global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnPa
   __shared__ float s_o[4][kD];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int hq = blockIdx.x, b = blockIdx.y;
+  // Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its
+  // own L2.  The G query heads of one (batch, kv head) read the same hot window
+  // and split records, so the linear id is remapped to put them on one XCD:
+  // XCD x = p % 8 runs logical blocks x * nb / 8 .. (x + 1) * nb / 8 - 1.
+  int hq, b;
+  {
+    const int nb = static_cast<int>(gridDim.x * gridDim.y), p = static_cast<int>(blockIdx.x + blockIdx.y * gridDim.x);
+    const int l = (nb % kXcds == 0) ? (p % kXcds) * (nb / kXcds) + p / kXcds : p;
+    hq = l % static_cast<int>(gridDim.x);
+    b = l / static_cast<int>(gridDim.x);
+  }
   const int G = P.G, kvh = hq / G, hh = hq % G;
   const int ns = P.nsplit;
   const int seq_len = P.indptr ? P.seq_len[b] : *P.seq_len;  // only the masks below depend on it

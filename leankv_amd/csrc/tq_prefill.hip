@@ -49,6 +49,7 @@ constexpr int kKRow = kD + 8;   // fp16 row of the decoded key tile (padded)
 constexpr int kVRow = kKT + 4;  // fp16 row of the transposed value tile (padded: conflict-free 8-byte reads)
 static_assert(kKT == 64, "the decode / compute lane maps assume 64-key tiles");
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kXcds = 8;  // MI355X: 8 accelerator complex dies, one L2 each
 
 struct PrefillParams {
   const uint16_t* q16;     // [B, Hq, S, 128] fp16: (q @ PiK^T) * scale * log2(e)
@@ -207,9 +208,34 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h16 = lane & 15, g = lane >> 4;
   const int G = P.G, QT = kCols / G;
-  // the latest queries see the most keys: their tiles are dispatched first
-  const int qtile = static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x);
-  const int kvh = blockIdx.y, b = blockIdx.z;
+  // The latest queries see the most keys: their tiles are dispatched first.
+  // Workgroups go to the 8 XCDs round-robin by linear id and every query tile
+  // of a (batch, kv head) reads the same cold store, so the tiles are placed
+  // XCD by XCD: with I = B * Hkv items, XCD x serves items x, x + 8, .. (I a
+  // multiple of 8) or every (8 / I)-th tile of item x % I (I = 1, 2, 4), its
+  // own tiles heaviest first; other shapes keep the plain order.
+  int qtile, kvh, b;
+  {
+    const int nx = static_cast<int>(gridDim.x), I = static_cast<int>(gridDim.y * gridDim.z);
+    const int p = static_cast<int>(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+    const int x = p % kXcds, s = p / kXcds;
+    int item, t;
+    if (I % kXcds == 0) {
+      const int per = I / kXcds;  // items per XCD
+      item = x + kXcds * (s % per);
+      t = s / per;
+    } else if (kXcds % I == 0 && nx % (kXcds / I) == 0) {
+      const int k = kXcds / I;  // XCDs per item
+      item = x % I;
+      t = s * k + x / I;
+    } else {
+      item = p / nx;
+      t = p % nx;
+    }
+    qtile = nx - 1 - t;
+    kvh = item % static_cast<int>(gridDim.y);
+    b = item / static_cast<int>(gridDim.y);
+  }
   const int q0 = qtile * QT;
   const int qpos0 = P.kv_len - P.S;  // position of query 0
   const size_t bh = static_cast<size_t>(b) * P.Hkv + kvh;
