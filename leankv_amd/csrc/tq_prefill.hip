@@ -71,11 +71,29 @@ struct PrefillParams {
 // with its Pi operands in registers; a block takes 64-row tiles, staged
 // through LDS both ways so every row is read once and written with 16-byte
 // stores.
+// Up to 3 independent row sets (segments) per launch, blockIdx.y picking one:
+// the query and the two hot rings are rotated by a single launch.
 constexpr int kRotRows = 64;
+constexpr int kMaxRotSegs = 3;
+struct RotSeg {
+  const void* x;
+  const float* Pi;
+  void* y;
+  int64_t M;
+  float scale;
+};
+struct RotSegs {
+  RotSeg s[kMaxRotSegs];
+};
 template <bool IN_F16, bool OUT_F16, bool TRANS>
-__global__ __launch_bounds__(kThreads) void rotate16_kernel(const void* __restrict__ x, int64_t M,
-                                                            const float* __restrict__ Pi, float scale,
-                                                            void* __restrict__ y) {
+__global__ __launch_bounds__(kThreads) void rotate16_kernel(RotSegs segs) {
+  const RotSeg& sg = segs.s[blockIdx.y];
+  const void* __restrict__ x = sg.x;
+  const float* __restrict__ Pi = sg.Pi;
+  void* __restrict__ y = sg.y;
+  const int64_t M = sg.M;
+  const float scale = sg.scale;
+  if (static_cast<int64_t>(blockIdx.x) * kRotRows >= M) return;  // uniform: this segment has fewer tiles
   constexpr int kInB = IN_F16 ? 2 : 4, kOutB = OUT_F16 ? 2 : 4;
   constexpr int kInRow = kD * kInB + 16, kOutRow = kD * kOutB + 16;  // padded LDS rows (bytes)
   __shared__ __align__(16) uint8_t s_in[kRotRows * kInRow];
@@ -178,16 +196,30 @@ __global__ __launch_bounds__(kThreads) void rotate16_kernel(const void* __restri
   }
 }
 
+// One launch over n segments (n <= kMaxRotSegs; empty segments are skipped).
 template <bool IN_F16, bool OUT_F16, bool TRANS>
-int rotate16(const void* x, int64_t M, const float* Pi, float scale, void* y, hipStream_t st) {
-  if (M <= 0) return LKV_OK;
-  int64_t g = (M + kRotRows - 1) / kRotRows;
+int rotate16_segs(const RotSeg* segs, int n, hipStream_t st) {
+  RotSegs S{};
+  int k = 0;
+  int64_t tiles = 0;
+  for (int i = 0; i < n; ++i) {
+    if (segs[i].M <= 0) continue;
+    S.s[k++] = segs[i];
+    tiles = std::max<int64_t>(tiles, (segs[i].M + kRotRows - 1) / kRotRows);
+  }
+  if (k == 0) return LKV_OK;
   const int64_t cap = 2 * static_cast<int64_t>(device_cu_count());
-  if (g > cap) g = cap;
-  hipLaunchKernelGGL((rotate16_kernel<IN_F16, OUT_F16, TRANS>), dim3(static_cast<unsigned>(g)), dim3(kThreads), 0,
-                     st, x, M, Pi, scale, y);
+  const int64_t g = tiles < cap ? tiles : cap;
+  hipLaunchKernelGGL((rotate16_kernel<IN_F16, OUT_F16, TRANS>), dim3(static_cast<unsigned>(g), static_cast<unsigned>(k)),
+                     dim3(kThreads), 0, st, S);
   LKV_LAUNCH_CHECK("tq_prefill_attn rotation");
   return LKV_OK;
+}
+
+template <bool IN_F16, bool OUT_F16, bool TRANS>
+int rotate16(const void* x, int64_t M, const float* Pi, float scale, void* y, hipStream_t st) {
+  const RotSeg seg{x, Pi, y, M, scale};
+  return rotate16_segs<IN_F16, OUT_F16, TRANS>(&seg, 1, st);
 }
 
 // fp16 positions 0..7 of a natural-order group reordered to kPermDim.
@@ -583,10 +615,11 @@ extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const 
   const int64_t cold_len = kv_len > hot_cap ? kv_len - hot_cap : 0;
 
   // q_rot * scale * log2(e) in fp16 (the score operand); the hot rings in the rotated domains
-  if (int e = rotate16<true, true, false>(q, nrows, PiK, scale * kLog2e, q16, st)) return e;
-  if (kv_len > cold_len) {  // rotate every slot; only the current tokens' slots are read
-    if (int e = rotate16<true, true, false>(k_hot, B * Hkv * hot_cap, PiK, 1.f, hk, st)) return e;
-    if (int e = rotate16<true, true, false>(v_hot, B * Hkv * hot_cap, PiV, 1.f, hv, st)) return e;
+  // (one launch; every hot slot is rotated, only the current tokens' slots are read)
+  {
+    const int64_t nhot = kv_len > cold_len ? B * Hkv * hot_cap : 0;
+    const RotSeg segs[3] = {{q, PiK, q16, nrows, scale * kLog2e}, {k_hot, PiK, hk, nhot, 1.f}, {v_hot, PiV, hv, nhot, 1.f}};
+    if (int e = rotate16_segs<true, true, false>(segs, 3, st)) return e;
   }
   PrefillParams P;
   P.q16 = q16;
