@@ -959,6 +959,24 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    # stdout carries exactly one JSON line: whatever the workload prints (the TEAL patching notice,
+    # progress) goes to stderr
+    real_stdout = sys.stdout
+    sys.stdout = sys.stderr
+    try:
+        res = _run_workload(args, torch)
+    finally:
+        sys.stdout = real_stdout
+    out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"), "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup}
+    out.update(res)
+    out.setdefault("scaling", "weak")
+    out.setdefault("vs_baseline", None)
+    out.setdefault("data", "synthetic (seeded)")
+    print(json.dumps(out))
+
+
+def _run_workload(args, torch):
     if args.workload == "decode":
         res = bench_decode(args, torch)
         # roofline block: the dominant kernel of the decode step (fused gate/up GEMV)
@@ -973,13 +991,7 @@ def main():
             print("bench.py: workload %s is not implemented yet" % args.workload, file=sys.stderr)
             sys.exit(2)
         res = fn(args, torch)
-    out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"), "n_gpus": 1,
-           "steps": args.steps, "warmup": args.warmup}
-    out.update(res)
-    out.setdefault("scaling", "weak")
-    out.setdefault("vs_baseline", None)
-    out.setdefault("data", "synthetic (seeded)")
-    print(json.dumps(out))
+    return res
 
 
 if __name__ == "__main__":

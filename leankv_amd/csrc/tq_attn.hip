@@ -744,6 +744,19 @@ int attn_split_target() {
   }();
   return k;
 }
+// At least 256 cold tokens per split (two passes of a block): at B = 1 the
+// target split count would give 128-token splits, and each split block repeats
+// the query prologue (q partial sums, RoPE, the rotation with PiK); 256 measured
+// 392 vs 384 tok/s at config 5 (512: 383, 1024: 365).  B >= 4 already gets
+// longer splits.  LKV_ATTN_MIN_SPLIT_TOKENS=n overrides (0: none).
+int64_t attn_min_split_tokens() {
+  static const int64_t k = [] {
+    const char* env = getenv("LKV_ATTN_MIN_SPLIT_TOKENS");
+    const long v = env ? atol(env) : 256;
+    return static_cast<int64_t>(v > 0 && v <= (1 << 20) ? v : 0);
+  }();
+  return k;
+}
 bool attn_qrot_kernel() {
   static const bool k = [] {
     const char* env = getenv("LKV_ATTN_QROT");
@@ -787,6 +800,7 @@ AttnPlan attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t 
   const int64_t cold_max = max_len > hot_cap ? max_len - hot_cap : 0;
   int64_t ns_cap = target_splits(B, Hkv);
   int64_t ts = (cold_max + ns_cap - 1) / ns_cap;
+  if (ts < attn_min_split_tokens()) ts = attn_min_split_tokens();
   ts = (ts + kSplitGran - 1) / kSplitGran * kSplitGran;
   if (ts < kSplitGran) ts = kSplitGran;
   if (max_split_tokens > 0 && ts > max_split_tokens) ts = max_split_tokens / kSplitGran * kSplitGran;
