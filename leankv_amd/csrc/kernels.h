@@ -143,10 +143,11 @@ __device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, co
 //   qb   this lane's q[h][32w + 8g .. +7] as fp16 pairs (zero for unused h)
 //   part LDS scratch, 4 x 16 rows of `ld` floats (ld >= 128, ld % 4 == 0)
 //   out  out[i] = q_rot[h][32g + 4i .. 4i+3]
-__device__ __forceinline__ void rotate_query_hilo(const float* __restrict__ PiK, const u32x4& qb, int wave,
-                                                  int lane, float* part, int ld, float4 (&out)[8]) {
+// The PiK operand of rotate_query_hilo, loadable ahead of the query (the
+// decode step issues it before summing the query's partials).
+__device__ __forceinline__ void load_pik_operand(const float* __restrict__ PiK, int wave, int lane,
+                                                 float4 (&pa)[8][2]) {
   const int h = lane & 15, g = lane >> 4;
-  float4 pa[8][2];
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
     const int row = 32 * (h >> 2) + 4 * c + (h & 3);  // lane % 16 is the A row here
@@ -154,6 +155,11 @@ __device__ __forceinline__ void rotate_query_hilo(const float* __restrict__ PiK,
     pa[c][0] = src[0];
     pa[c][1] = src[1];
   }
+}
+
+__device__ __forceinline__ void rotate_query_hilo_loaded(const float4 (&pa)[8][2], const u32x4& qb, int wave,
+                                                         int lane, float* part, int ld, float4 (&out)[8]) {
+  const int h = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
     const float x[8] = {pa[c][0].x, pa[c][0].y, pa[c][0].z, pa[c][0].w,
@@ -182,6 +188,13 @@ __device__ __forceinline__ void rotate_query_hilo(const float* __restrict__ PiK,
     out[i] = make_float4(((p[0].x + p[1].x) + p[2].x) + p[3].x, ((p[0].y + p[1].y) + p[2].y) + p[3].y,
                          ((p[0].z + p[1].z) + p[2].z) + p[3].z, ((p[0].w + p[1].w) + p[2].w) + p[3].w);
   }
+}
+
+__device__ __forceinline__ void rotate_query_hilo(const float* __restrict__ PiK, const u32x4& qb, int wave,
+                                                  int lane, float* part, int ld, float4 (&out)[8]) {
+  float4 pa[8][2];
+  load_pik_operand(PiK, wave, lane, pa);
+  rotate_query_hilo_loaded(pa, qb, wave, lane, part, ld, out);
 }
 
 // y = x @ Pi^T (transpose 0) or x @ Pi (transpose 1) for M rows of 128, fp32

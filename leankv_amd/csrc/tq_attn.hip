@@ -417,6 +417,8 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
       // value into their ring slot; evict_kernel has already quantized the
       // token that slot held.
       __shared__ float s_q[16][kD];
+      float4 pik[8][2];
+      load_pik_operand(P.PiK, wave, lane, pik);  // in flight while the partials are summed
       const int pos = __builtin_amdgcn_readfirstlane(*P.pos);
       const uint16_t* cos_row = P.rope_cos + static_cast<size_t>(pos) * kD;
       const uint16_t* sin_row = P.rope_sin + static_cast<size_t>(pos) * kD;
@@ -458,7 +460,7 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
         for (int jj = 0; jj < 4; ++jj)
           qb[jj] = static_cast<uint32_t>(f2h(q[2 * jj])) | (static_cast<uint32_t>(f2h(q[2 * jj + 1])) << 16);
       }
-      rotate_query_hilo(P.PiK, qb, wave, lane, &s_o[0][0][0], kORow, f);
+      rotate_query_hilo_loaded(pik, qb, wave, lane, &s_o[0][0][0], kORow, f);
       __syncthreads();  // s_o is written again by the merge
     } else if (P.PiK != nullptr) {
       // q_rot on MFMA (rotate_query_hilo), overlapping the first block's
