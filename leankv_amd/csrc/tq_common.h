@@ -97,6 +97,7 @@ __device__ __forceinline__ void load_row_f16(const uint16_t* __restrict__ p, flo
 // as stored by the reference (fp32, or fp32 value of the fp16 norm).
 template <bool F16>
 __device__ __forceinline__ float normalize_row(float (&a)[32]) {
+#pragma clang fp contract(off)
   float ss = 0.f;
 #pragma unroll
   for (int s = 0; s < 32; ++s) ss = fmaf(a[s], a[s], ss);
@@ -111,8 +112,18 @@ __device__ __forceinline__ float normalize_row(float (&a)[32]) {
   } else {
     const float n16 = h2f(f2h(nrm));
     const float d = h2f(f2h(n16 + 1e-10f));
+    // a / d correctly rounded from one division per row: r = 1 / d (IEEE), then
+    // per element q0 = a r and one FMA correction (Markstein); e == 0 means q0
+    // is exact (and keeps the sign of a zero quotient).  Every fp16 a and
+    // positive fp16 d gives the IEEE quotient bit for bit (tests/fp16_div_check.c
+    // checks all 2.0e9 pairs); d is 0 only for an all-zero row, NaN either way.
+    const float r = 1.f / d;
 #pragma unroll
-    for (int s = 0; s < 32; ++s) a[s] = h2f(f2h(a[s] / d));
+    for (int s = 0; s < 32; ++s) {
+      const float q0 = a[s] * r;
+      const float e = fmaf(-q0, d, a[s]);
+      a[s] = h2f(f2h(e == 0.f ? q0 : fmaf(e, r, q0)));
+    }
     return n16;
   }
 }
