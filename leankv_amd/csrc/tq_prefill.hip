@@ -13,7 +13,7 @@
 // real arithmetic, rounded to fp16 here), so one accumulator serves all keys
 // and one un-rotation by PiV finishes each output row.
 //
-// Launches of lkv_tq_prefill_attn (all on the caller's stream):
+// Launches of lkv_tq_prefill_attn (two, on the caller's stream):
 //   1. rotate16_kernel (fp16 MFMA, PiK / PiV split exactly into fp16 hi + lo
 //      parts): q_rot = (q @ PiK^T) * scale * log2(e) in fp16, the score
 //      operand; hot rings k @ PiK^T and v @ PiV^T (fp16);
@@ -31,8 +31,9 @@
 //        the lane's own softmax registers.
 //      Each thread loads its share of a tile's codes two tiles ahead into
 //      registers and decodes them into one of two LDS buffers: one barrier
-//      per tile.  The block writes its normalised rotated rows (fp32);
-//   3. rotate16_kernel: out = rows @ PiV (fp16; the rows split into hi + lo too).
+//      per tile.  In its epilogue the block un-rotates its normalised rows,
+//      out = rows @ PiV on the same MFMA (PiV staged in the free tile buffers,
+//      both operands split into hi + lo), and writes them as fp16.
 #include "kernels.h"
 #include "tq_attn_common.h"
 #include "tq_common.h"
@@ -53,7 +54,8 @@ constexpr int kXcds = 8;  // MI355X: 8 accelerator complex dies, one L2 each
 
 struct PrefillParams {
   const uint16_t* q16;     // [B, Hq, S, 128] fp16: (q @ PiK^T) * scale * log2(e)
-  float* orot;             // [B, Hq, S, 128] fp32: normalised output, rotated domain
+  const float* PiV;        // [128, 128]: the output rows are un-rotated in the epilogue
+  uint16_t* out;           // [B, Hq, S, 128] fp16
   const uint8_t* k_codes;  // [B, Hkv, cap, 64]
   const float* k_norms;    // [B, Hkv, cap]
   const uint8_t* v_codes;
@@ -546,17 +548,74 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
     if (++it >= ntile) break;
   }
 
-  // ---- normalise and write the rotated output rows
+  // ---- normalise, un-rotate (out = o_rot @ PiV) and write fp16 rows.  One MFMA
+  // contraction per 16 output dims x 16 columns with the input dims in a
+  // permuted k order: in 32-dim block kb, k slot 8 g + j stands for dim
+  // 32 kb + 4 g + j (j < 4) or 32 kb + 16 + 4 g + j - 4 -- the dims this lane
+  // holds in o[ct][2 kb] and o[ct][2 kb + 1] -- so the B operand (o^T, column =
+  // the lane's column) is the lane's own registers, and A = PiV^T in the same k
+  // order comes from LDS.  Both are split exactly into fp16 hi + lo / 2048
+  // (hi.hi + hi.lo + lo.hi, the x_lo.Pi_lo term dropped: ~2^-22 relative).
+  u32x4 obh[2][4], obl[2][4];
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
     const float L = xgroup_sum(l[ct]);
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    const int c = 32 * wave + 16 * ct + h16;
-    const int qq = q0 + c / G, hh = c % G;
-    if (qq < P.S) {
-      float* dst = P.orot + ((static_cast<size_t>(b) * P.Hq + kvh * G + hh) * P.S + qq) * kD + 4 * g;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(dst + 16 * dt) = o[ct][dt] * inv;
+    for (int kb = 0; kb < 4; ++kb) {
+      const f32x4 u = o[ct][2 * kb] * inv, w = o[ct][2 * kb + 1] * inv;
+      const float v[8] = {u[0], u[1], u[2], u[3], w[0], w[1], w[2], w[3]};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint16_t h0 = f2h(v[2 * j]), h1 = f2h(v[2 * j + 1]);
+        obh[ct][kb][j] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+        obl[ct][kb][j] = pack2h((v[2 * j] - h2f(h0)) * 2048.f, (v[2 * j + 1] - h2f(h1)) * 2048.f);
+      }
+    }
+  }
+  __syncthreads();  // every wave is past its last tile: the key / value buffers are free
+  // PiV^T into LDS, [e][d] rows of kKRow: hi in sK, lo in sVt (128 x 136 fp16 each)
+  static_assert(kD * kKRow <= 2 * kKT * kKRow && kD * kKRow <= 2 * kD * kVRow, "PiV staging fits the tile buffers");
+  for (int f = tid; f < kD * kD; f += kThreads) {
+    const int d = f / kD, e = f % kD;  // coalesced over e
+    const float pv = P.PiV[f];
+    const uint16_t hi = f2h(pv);
+    sK[e * kKRow + d] = hi;
+    sVt[e * kKRow + d] = f2h((pv - h2f(hi)) * 2048.f);
+  }
+  __syncthreads();
+#pragma unroll 2
+  for (int et = 0; et < kD / 16; ++et) {
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    f32x4 accl[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const int er = (16 * et + h16) * kKRow;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int d0 = 32 * kb + 4 * g;
+      const uint2 h0 = *reinterpret_cast<const uint2*>(sK + er + d0);
+      const uint2 h1 = *reinterpret_cast<const uint2*>(sK + er + d0 + 16);
+      const uint2 l0 = *reinterpret_cast<const uint2*>(sVt + er + d0);
+      const uint2 l1 = *reinterpret_cast<const uint2*>(sVt + er + d0 + 16);
+      const u32x4 ah = u32x4{h0.x, h0.y, h1.x, h1.y}, al = u32x4{l0.x, l0.y, l1.x, l1.y};
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        acc[ct] = mfma16x16x32(ah, obh[ct][kb], acc[ct]);
+        accl[ct] = mfma16x16x32(ah, obl[ct][kb], accl[ct]);
+        accl[ct] = mfma16x16x32(al, obh[ct][kb], accl[ct]);
+      }
+    }
+    // D: output dims 16 et + 4 g + i of column 32 wave + 16 ct + h16
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int c = 32 * wave + 16 * ct + h16;
+      const int qq = q0 + c / G, hh = c % G;
+      if (qq < P.S) {
+        uint16_t* dst = P.out + ((static_cast<size_t>(b) * P.Hq + kvh * G + hh) * P.S + qq) * kD + 16 * et + 4 * g;
+        const float r0 = acc[ct][0] + accl[ct][0] * (1.f / 2048.f), r1 = acc[ct][1] + accl[ct][1] * (1.f / 2048.f);
+        const float r2 = acc[ct][2] + accl[ct][2] * (1.f / 2048.f), r3 = acc[ct][3] + accl[ct][3] * (1.f / 2048.f);
+        *reinterpret_cast<uint2*>(dst) = uint2{static_cast<uint32_t>(f2h(r0)) | (static_cast<uint32_t>(f2h(r1)) << 16),
+                                              static_cast<uint32_t>(f2h(r2)) | (static_cast<uint32_t>(f2h(r3)) << 16)};
+      }
     }
   }
 }
@@ -572,7 +631,7 @@ extern "C" size_t lkv_tq_prefill_attn_workspace_bytes(int64_t B, int64_t Hq, int
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
   const size_t rows = static_cast<size_t>(B * Hq * S) * kD;
   const size_t hot = static_cast<size_t>(B * Hkv * hot_cap) * kD * 2;
-  return al(rows * 2) + al(rows * 4) + 2 * al(hot);  // q_rot fp16, rotated output fp32, hot rings
+  return al(rows * 2) + 2 * al(hot);  // q_rot fp16, hot rings (the output is un-rotated in the kernel)
 }
 
 extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const float* k_norms,
@@ -608,8 +667,7 @@ extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const 
   const int64_t nrows = B * Hq * S;
   char* ws = static_cast<char*>(workspace);
   uint16_t* q16 = reinterpret_cast<uint16_t*>(ws);
-  float* orot = reinterpret_cast<float*>(ws + al(static_cast<size_t>(nrows) * kD * 2));
-  uint16_t* hk = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(orot) + al(static_cast<size_t>(nrows) * kD * 4));
+  uint16_t* hk = reinterpret_cast<uint16_t*>(ws + al(static_cast<size_t>(nrows) * kD * 2));
   uint16_t* hv = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(hk) +
                                              al(static_cast<size_t>(B * Hkv * hot_cap) * kD * 2));
   const int64_t cold_len = kv_len > hot_cap ? kv_len - hot_cap : 0;
@@ -623,7 +681,8 @@ extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const 
   }
   PrefillParams P;
   P.q16 = q16;
-  P.orot = orot;
+  P.PiV = PiV;
+  P.out = static_cast<uint16_t*>(out);
   P.k_codes = k_codes;
   P.k_norms = k_norms;
   P.v_codes = v_codes;
@@ -647,5 +706,5 @@ extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const 
   else
     hipLaunchKernelGGL((tq_prefill_attn_kernel<false>), grid, dim3(kThreads), 0, st, P);
   LKV_LAUNCH_CHECK("tq_prefill_attn");
-  return rotate16<false, true, true>(orot, nrows, PiV, 1.f, out, st);
+  return LKV_OK;
 }

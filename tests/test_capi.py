@@ -87,7 +87,7 @@ def test_invalid_arguments_rejected_without_launch():
     assert lib.lkv_tq_prefill_attn(p, p, p, p, p, p, p, p, p, p, 3, 100, 1, 8, 2, 100, 64, 64, 0.1, p, p,
                                    1024, None) == -1
     assert "workspace" in _lib.last_error()
-    assert lib.lkv_tq_prefill_attn_workspace_bytes(1, 32, 8, 4096, 64) >= 32 * 4096 * 128 * 4
+    assert lib.lkv_tq_prefill_attn_workspace_bytes(1, 32, 8, 4096, 64) >= 32 * 4096 * 128 * 2
     # batched sparse GEMM: N not a multiple of 8, workspace too small for a multi-chunk problem
     assert lib.lkv_sparse_gemm_batched(p, p, 0.1, 4, 12, 16, p, p, 1 << 20, None) == -1
     assert "multiple of 8" in _lib.last_error()
