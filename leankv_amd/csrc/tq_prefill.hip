@@ -576,12 +576,24 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
   __syncthreads();  // every wave is past its last tile: the key / value buffers are free
   // PiV^T into LDS, [e][d] rows of kKRow: hi in sK, lo in sVt (128 x 136 fp16 each)
   static_assert(kD * kKRow <= 2 * kKT * kKRow && kD * kKRow <= 2 * kD * kVRow, "PiV staging fits the tile buffers");
-  for (int f = tid; f < kD * kD; f += kThreads) {
-    const int d = f / kD, e = f % kD;  // coalesced over e
-    const float pv = P.PiV[f];
-    const uint16_t hi = f2h(pv);
-    sK[e * kKRow + d] = hi;
-    sVt[e * kKRow + d] = f2h((pv - h2f(hi)) * 2048.f);
+  {
+    // thread: output dim e = tid % 128, input dims 64 (tid / 128) .. +63 four at a time (global
+    // loads coalesced over e, one 8-byte LDS store per four dims)
+    const int e = tid % kD, dbase = (tid / kD) * (kD / 2);
+#pragma unroll 4
+    for (int d = dbase; d < dbase + kD / 2; d += 4) {
+      uint16_t hi[4], lo[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pv = P.PiV[(d + i) * kD + e];
+        hi[i] = f2h(pv);
+        lo[i] = f2h((pv - h2f(hi[i])) * 2048.f);
+      }
+      *reinterpret_cast<uint2*>(sK + e * kKRow + d) =
+          uint2{hi[0] | (static_cast<uint32_t>(hi[1]) << 16), hi[2] | (static_cast<uint32_t>(hi[3]) << 16)};
+      *reinterpret_cast<uint2*>(sVt + e * kKRow + d) =
+          uint2{lo[0] | (static_cast<uint32_t>(lo[1]) << 16), lo[2] | (static_cast<uint32_t>(lo[3]) << 16)};
+    }
   }
   __syncthreads();
 #pragma unroll 2
