@@ -31,7 +31,7 @@ __global__ __launch_bounds__(kThreads, 2) void prod_quantize_kernel(
     void* __restrict__ norms, uint8_t* __restrict__ signs, float* __restrict__ rnorms) {
 #pragma clang fp contract(off)
   constexpr int NC = 1 << MB;
-  __shared__ float4 s_s[4][2][8][64];                // S operand, 64 KB
+  __shared__ float4 s_s[4][2][8][65];                // S operand, 64 KB + a float4 of padding per row
   __shared__ __align__(16) float s_xh[kRows][kD + 4];  // x_hat of the tile
   __shared__ __align__(16) uint8_t s_codes[kRows * kD];
   __shared__ uint8_t s_bits[4][kRows][16];           // sign bits per wave (2 of every byte)

@@ -27,7 +27,8 @@ enum Mode { kQuant = 0, kRotate = 1, kDequant = 2, kAppend = 3 };
 // with the same operands in the same order as rotate_tile -- is unchanged,
 // so the codes equal every other quantizing kernel's bit for bit.  The B
 // operands of the 8 tiles are staged once per block in LDS in MFMA operand
-// order: s_b[c][kq][lane] = Pi[8n + c][32q + 4kq .. +3] for lane = 16q + n.
+// order: s_b[c][kq][lane] = Pi[8n + c][32q + 4kq .. +3] for lane = 16q + n
+// (rows padded by one float4 so the staging writes do not collide in banks).
 // #(b < y) over the 2^BITS - 1 sorted decision boundaries by binary search
 // (BITS compares instead of 2^BITS - 1): the same count as bucket<BITS>.
 // Every boundary index is a compile-time constant (selects, no indexing).
@@ -57,7 +58,8 @@ __global__ __launch_bounds__(kThreads, 2) void quantize_wave_kernel(const void* 
                                                                     uint8_t* __restrict__ packed,
                                                                     void* __restrict__ norms) {
   static_assert(pack_bits(BITS) == 4 && row_bytes_for(BITS) == 64, "nibble layouts only");
-  __shared__ float4 s_b[8][8][64];  // 64 KB
+  __shared__ float4 s_b[8][8][65];  // 64 KB + one float4 of padding per row: the staging writes of 8
+                                     // consecutive threads (8 k-quarters) fall in different banks
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int64_t ntiles = (M + kRows - 1) / kRows;
