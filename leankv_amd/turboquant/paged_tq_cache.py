@@ -92,6 +92,12 @@ class PagedTurboQuantCache:
         """Append S tokens [Hkv, S, 128] (or [1, Hkv, S, 128]) to sequence b of one layer."""
         if not 0 <= b < self.max_batch_size:
             raise IndexError("PagedTurboQuantCache: sequence %d outside max_batch_size %d" % (b, self.max_batch_size))
+        for t in (key_states, value_states):
+            lead = t.shape[:-3]
+            if (t.dim() not in (3, 4) or any(n != 1 for n in lead) or t.shape[-3] != self.num_kv_heads
+                    or t.shape[-1] != self.head_dim or t.shape != key_states.shape):
+                raise ValueError("PagedTurboQuantCache.append: one sequence's states [Hkv, S, %d] or [1, Hkv, S, %d] "
+                                 "expected, got %s" % (self.head_dim, self.head_dim, tuple(t.shape)))
         k16 = key_states.reshape(self.num_kv_heads, -1, self.head_dim).to(torch.float16)
         v16 = value_states.reshape(self.num_kv_heads, -1, self.head_dim).to(torch.float16)
         li, hot, ps, dev = layer_idx, self.hot_buffer_size, self.page_size, self._device

@@ -84,3 +84,17 @@ def test_optimize_model_builds_the_paged_cache():
     assert isinstance(cache, PagedKVCache)
     assert (cache.num_layers, cache.num_kv_heads, cache.num_q_heads, cache.page_size, cache.max_pages) == (2, 2, 4,
                                                                                                           16, 8)
+
+
+def test_paged_tq_cache_rejects_batched_states_in_append():
+    from leankv_amd.turboquant.paged_tq_cache import PagedTurboQuantCache
+
+    c = PagedTurboQuantCache(num_layers=1, num_kv_heads=2, num_q_heads=4, max_pages=4, max_batch_size=2,
+                             device="cpu")
+    with pytest.raises(ValueError, match="one sequence"):
+        c.append(0, 0, torch.zeros(2, 2, 3, 128), torch.zeros(2, 2, 3, 128))  # a batch of 2, not one sequence
+    with pytest.raises(ValueError, match="one sequence"):
+        c.append(0, 0, torch.zeros(3, 3, 128), torch.zeros(3, 3, 128))  # 3 heads for a 2-head cache
+    with pytest.raises(IndexError):
+        c.append(0, 2, torch.zeros(2, 3, 128), torch.zeros(2, 3, 128))
+    assert c.get_pages_used() == 0 and c.get_seq_length() == 0
