@@ -114,10 +114,11 @@ class LeanKVEngine(_Base):
     """TEAL sparse projections + TurboQuant packed KV through the fused C decode step.
 
     Per token: lkv_decode_begin, lkv_decode_evict (the token leaving every
-    layer's hot window, one launch), lkv_decode_layer_step per layer (9
-    kernels: q|k|v GEMV with the RMSNorm prologue, RoPE/append/q-rotation
-    epilogue, attention split + combine, o_proj, residual, gate|up GEMV with
-    the RMSNorm prologue, down GEMV with the SwiGLU prologue, residual) and
+    layer's hot window, one launch), lkv_decode_layer_step per layer (8
+    kernels: q|k|v GEMV with the RMSNorm prologue, attention split with the
+    q|k|v sums, RoPE, ring append and query rotation in its prologue, combine,
+    o_proj, residual, gate|up GEMV with the RMSNorm prologue, down GEMV with
+    the SwiGLU prologue, residual) and
     lkv_decode_head (lm_head GEMV, logits, argmax), captured into one graph.
 
     Projections patched by apply_teal already hold their weight column-major
