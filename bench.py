@@ -101,10 +101,15 @@ def _kernel_time(launch, nsets, steps, warmup, torch, batch=10):
 
 
 def _cpu_info():
+    """(threads for the CPU baseline, CPU model): the cores this process may run on (affinity mask),
+    capped by OMP_NUM_THREADS when the machine sets a CPU share that way."""
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        cores = min(cores, int(omp))
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -225,7 +230,6 @@ def cpu_decode(torch, model, thresholds, prompt_len, budget_s=20.0):
     from oracle.model import RefModel
 
     cores, cpu = _cpu_info()
-    cores = min(cores, 16)
     torch.set_num_threads(cores)
     cfg = copy.deepcopy(model.config)
     cfg.num_hidden_layers = 1
@@ -847,8 +851,54 @@ def _fill_gemv_defaults(args):
 
 
 # ------------------------------------------------------------------ config 5
+def _kv_bytes_per_token(L, Hkv, ctx, hot, bits_row=64):
+    """Packed KV read by one decode step over all layers at context ctx: per kv head and cold token 2 x (code
+    row + fp32 norm), per hot token 2 x 256 B of fp16."""
+    cold = max(0, ctx - hot)
+    return L * Hkv * (cold * 2 * (bits_row + 4) + min(ctx, hot) * 2 * 256)
+
+
+def _count_survivors(model, th, cache, tokens, torch):
+    """Feed `tokens` through the HF-patched model (TEAL masks and TurboQuant cache as the engine's: the two
+    paths give identical activations) and count, per projection, the inputs above its threshold.  Returns
+    {proj: (kept, total)} summed over layers and tokens."""
+    from leankv_amd.kernels import rms_norm
+
+    counts = {}
+    hooks, saved = [], []
+
+    def count(name, li, thresholds):
+        def hook(mod, args):
+            x = args[0].detach().reshape(-1).float().abs()
+            for proj in thresholds:
+                t = th[li][proj]
+                k, n = counts.get(proj, (0, 0))
+                counts[proj] = (k + int((x > t).sum()), n + x.numel())
+        return hook
+
+    for m in model.modules():  # the engine's RMSNorm arithmetic, so masks match bit for bit
+        if type(m).__name__.endswith("RMSNorm"):
+            saved.append((m, m.forward))
+            m.forward = (lambda x, m=m: rms_norm(x, m.weight, m.variance_epsilon))
+    for li, layer in enumerate(model.model.layers):
+        hooks.append(layer.self_attn.q_proj.register_forward_pre_hook(count("qkv", li, ("q_proj", "k_proj", "v_proj"))))
+        hooks.append(layer.self_attn.o_proj.register_forward_pre_hook(count("o", li, ("o_proj",))))
+        hooks.append(layer.mlp.register_forward_pre_hook(count("gu", li, ("gate_proj", "up_proj"))))
+        hooks.append(layer.mlp.down_proj.register_forward_pre_hook(count("d", li, ("down_proj",))))
+    try:
+        with torch.no_grad():
+            for t in tokens:
+                model(torch.tensor([[t]], device=model.device), past_key_values=cache, use_cache=True)
+    finally:
+        for h in hooks:
+            h.remove()
+        for m, f in saved:
+            m.forward = f
+    return counts
+
+
 def bench_decode(args, torch):
-    from leankv_amd.engine import DenseEngine, LeanKVEngine, random_mistral
+    from leankv_amd.engine import DenseEngine, LeanKVEngine, OwnDenseEngine, random_mistral
     from leankv_amd.teal.calibrate import calibrate_thresholds, uniform_random_sparsity
     from leankv_amd.teal.patching import apply_teal
     from leankv_amd.turboquant.attention import use_on
@@ -859,84 +909,174 @@ def bench_decode(args, torch):
         args.steps = 120
     if args.warmup is None:
         args.warmup = 8
+    args.warmup = max(args.warmup, 1)  # the first step runs eagerly, then the step is captured
     dev = torch.device("cuda:0")
     t0 = time.perf_counter()
     model = random_mistral(device=dev, seed=0, num_hidden_layers=args.layers)
+    cfg = model.config
     _log("model built in %.1fs" % (time.perf_counter() - t0))
     g = torch.Generator().manual_seed(1)
-    prompt = torch.randint(0, model.config.vocab_size, (1, args.prompt), generator=g).to(dev)
-    calib = [torch.randint(0, model.config.vocab_size, (1, 512), generator=g)]
-    max_len = args.prompt + args.warmup + args.steps + 2
+    prompt = torch.randint(0, cfg.vocab_size, (1, args.prompt), generator=g).to(dev)
+    calib = [torch.randint(0, cfg.vocab_size, (1, 512), generator=g)]
+    new_tokens = args.warmup + args.steps
+    max_len = args.prompt + new_tokens + 2
+    L, Hkv, hid, ffn, voc = (cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.hidden_size,
+                             cfg.intermediate_size, cfg.vocab_size)
+    nq, nkv = cfg.num_attention_heads * 128, Hkv * 128
 
     def timed_decode(eng):
+        """warmup steps (the first eager, then the captured graph), then `steps` timed replays; returns
+        (seconds, every output token in order)."""
+        outs = []
         with torch.no_grad():
             eng.step()
+            outs.append(eng.tok.clone())
             eng.capture()
             for _ in range(args.warmup - 1):
                 eng.step()
+                outs.append(eng.tok.clone())
             torch.cuda.synchronize()
             t = time.perf_counter()
-            toks = []
             for _ in range(args.steps):
                 eng.step()
-                toks.append(eng.tok)
+                outs.append(eng.tok.clone())  # an 8-byte device copy per step, inside the timed region
             torch.cuda.synchronize()
             dt = time.perf_counter() - t
-        return dt, [int(x) for x in torch.cat(toks).tolist()]
+        return dt, [int(x) for x in torch.cat(outs).tolist()]
 
-    # ---- dense fp16 baseline (weights still row-major)
-    dense_tps = None
+    def hf_generate(cache_factory, runs=2):
+        """scripts/benchmark.py:68-99: generate new_tokens from the prompt on a fresh cache, prefill included;
+        tok/s = generated tokens / wall time, mean over runs after a 10-token warm-up."""
+        model.generation_config.eos_token_id = None
+        mask = torch.ones_like(prompt)
+        with torch.no_grad():
+            model.generate(prompt, attention_mask=mask, max_new_tokens=10, past_key_values=cache_factory(),
+                           do_sample=False, pad_token_id=0)
+            rates = []
+            for _ in range(runs):
+                c = cache_factory()
+                torch.cuda.synchronize()
+                t = time.perf_counter()
+                out = model.generate(prompt, attention_mask=mask, max_new_tokens=new_tokens, past_key_values=c,
+                                     do_sample=False, pad_token_id=0)
+                torch.cuda.synchronize()
+                rates.append((out.shape[1] - prompt.shape[1]) / (time.perf_counter() - t))
+                del c, out
+        return round(statistics.mean(rates), 2)
+
+    # ---- dense fp16 baselines from one prefilled fp16 cache: torch's path and this library's kernels
+    # (every threshold 0, fp16 paged KV); weights are still row-major here, the own engine copies them
+    dense = {}
     if not args.skip_dense:
-      with torch.no_grad():
-        dc = DynamicCache(config=model.config)
-        out = model(prompt, past_key_values=dc, use_cache=True)
-        first_dense = torch.argmax(out.logits[0, -1])
-        dense = DenseEngine(model, max_len)
-        dense.start(first_dense, dense.load_cache(dc))
-        del dc, out
-      dt_dense, _ = timed_decode(dense)
-      dense_tps = args.steps / dt_dense
-      _log("dense fp16: %.1f tok/s" % dense_tps)
-      del dense
-      torch.cuda.empty_cache()
+        with torch.no_grad():
+            dc = DynamicCache(config=cfg)
+            out = model(prompt, past_key_values=dc, use_cache=True)
+            first_dense = torch.argmax(out.logits[0, -1])
+            del out
+        for name, cls in (("torch", DenseEngine), ("own", OwnDenseEngine)):
+            eng = cls(model, max_len)
+            eng.start(first_dense, eng.load_cache(dc))
+            dt_d, toks_d = timed_decode(eng)
+            dense[name] = (args.steps / dt_d, toks_d)
+            _log("dense fp16 (%s): %.1f tok/s" % (name, dense[name][0]))
+            del eng
+            torch.cuda.empty_cache()
+        del dc
+        dense["generate"] = hf_generate(lambda: DynamicCache(config=cfg))
+        _log("HF generate, dense fp16: %.1f tok/s (prefill included)" % dense["generate"])
+        torch.cuda.empty_cache()
 
     # ---- LeanKV: TEAL thresholds from a calibration pass, HIP kernels, TurboQuant KV
     t0 = time.perf_counter()
     with torch.no_grad():
         th = calibrate_thresholds(model, calib, uniform_random_sparsity(0.3, 0.5, seed=0))
     apply_teal(model, thresholds=th, use_triton=True)
-    cache = TurboQuantCache(bits=3, head_dim=128, num_layers=model.config.num_hidden_layers, device=dev,
-                            max_seq_len=max_len)
-    use_on(model)
+
+    def tq_cache():
+        return TurboQuantCache(bits=3, head_dim=128, num_layers=L, device=dev, max_seq_len=max_len,
+                               fused_attention=True)
+
+    cache, cache_count = tq_cache(), tq_cache()
+    use_on(model, cache)
     with torch.no_grad():
         out = model(prompt, past_key_values=cache, use_cache=True)
         first = torch.argmax(out.logits[0, -1])
+        model(prompt, past_key_values=cache_count, use_cache=True)
         del out
     _log("calibrate + patch + TurboQuant prefill in %.1fs" % (time.perf_counter() - t0))
     eng = LeanKVEngine(model, cache, max_len)
     eng.start(first, args.prompt)
     dt, toks = timed_decode(eng)
     tps = args.steps / dt
+    ms = dt * 1e3 / args.steps
     _log("leankv: %.1f tok/s" % tps)
+    del eng, cache
+    torch.cuda.empty_cache()
+
+    # ---- what the timed steps read: their tokens through the HF-patched path (the same activations, masks
+    # and cache as the engine's) on a cache prefilled the same way; the warm-up positions first, uncounted
+    fed = [int(first)] + toks[:-1]
+    _count_survivors(model, th, cache_count, fed[:args.warmup], torch)
+    counts = _count_survivors(model, th, cache_count, fed[args.warmup:], torch)
+    del cache_count
+    torch.cuda.empty_cache()
+    row_bytes = {"q_proj": nq * 2, "k_proj": nkv * 2, "v_proj": nkv * 2, "o_proj": hid * 2, "gate_proj": ffn * 2,
+                 "up_proj": ffn * 2, "down_proj": hid * 2}
+    in_dim = {"q_proj": hid, "k_proj": hid, "v_proj": hid, "o_proj": nq, "gate_proj": hid, "up_proj": hid,
+              "down_proj": ffn}
+    w_sparse = sum(counts[p][0] * row_bytes[p] for p in row_bytes) / args.steps
+    w_dense = L * sum(in_dim[p] * row_bytes[p] for p in row_bytes)
+    ctx = args.prompt + args.warmup + (args.steps - 1) / 2  # mean context of the timed steps
+    head = hid * voc * 2
+    lkv_bytes = w_sparse + head + _kv_bytes_per_token(L, Hkv, ctx, 64)
+    dense_bytes = w_dense + head + L * Hkv * (ctx + 1) * 2 * 256
+    sparsity = {p: round(1 - counts[p][0] / counts[p][1], 4) for p in row_bytes}
+
+    gen_lkv = hf_generate(tq_cache)
+    _log("HF generate, LeanKV (TEAL + TurboQuant, packed-KV attention): %.1f tok/s (prefill included)" % gen_lkv)
     res = {
         "metric": "B=1 decode tok/s (Mistral-7B shape, 40% sparse, 3-bit KV)",
         "value": round(tps, 2),
         "unit": "tok/s",
-        "ms_per_step": round(dt * 1e3 / args.steps, 4),
+        "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "dtype": "f16 (fp32 accumulate)",
         "data": "synthetic: random-init weights N(0,0.02), random 4096-token prompt (seeded)",
-        "config": {"workload": "config5_mistral7b_decode", "layers": model.config.num_hidden_layers,
-                   "hidden": model.config.hidden_size, "ffn": model.config.intermediate_size, "heads": "32/8",
-                   "vocab": model.config.vocab_size, "prompt": args.prompt, "new_tokens": args.warmup + args.steps,
-                   "batch": 1, "teal_sparsity": "U[0.3,0.5] per projection, mean 0.4", "kv_bits": 3,
-                   "hot_window": 64},
-        "dense_fp16": {"value": round(dense_tps, 2) if dense_tps else None, "unit": "tok/s",
-                       "what": "same model, fp16 KV, torch F.linear + SDPA, graph-captured"},
-        "speedup_vs_dense": round(tps / dense_tps, 3) if dense_tps else None,
+        "config": {"workload": "config5_mistral7b_decode", "layers": L, "hidden": hid, "ffn": ffn, "heads": "32/8",
+                   "vocab": voc, "prompt": args.prompt, "new_tokens": new_tokens, "batch": 1,
+                   "teal_sparsity": "U[0.3,0.5] per projection, mean 0.4", "kv_bits": 3, "hot_window": 64},
+        "step_roofline": {
+            "what": "algorithmic HBM bytes of one timed decode step (weight rows above threshold, counted on the "
+                    "timed tokens + packed KV + lm_head) / ms_per_step",
+            "bytes_per_token": int(lkv_bytes), "achieved_GBs": round(lkv_bytes / ms / 1e6, 1),
+            "frac": round(lkv_bytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / lkv_bytes, 1),
+            "achieved_sparsity": sparsity,
+            "mean_sparsity": round(1 - w_sparse / (w_dense / 1.0), 4),
+        },
     }
-    del eng, cache
-    torch.cuda.empty_cache()
+    if dense:
+        own_tps, torch_tps = dense["own"][0], dense["torch"][0]
+        best = max(own_tps, torch_tps)
+        res["dense_fp16"] = {
+            "own_kernels": {"value": round(own_tps, 2), "unit": "tok/s",
+                            "what": "the same fused step, every threshold 0, fp16 KV in 16-token pages, graph-captured",
+                            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / dense_bytes, 1),
+                            "frac": round(own_tps * dense_bytes / 1e9 / HBM_PEAK_GBS, 4)},
+            "torch": {"value": round(torch_tps, 2), "unit": "tok/s",
+                      "what": "torch F.linear + SDPA, fp16 KV, graph-captured"},
+            "token_agreement_own_vs_torch": round(sum(a == b for a, b in zip(dense["own"][1], dense["torch"][1]))
+                                                  / len(dense["own"][1]), 4),
+        }
+        res["speedup_vs_dense"] = round(tps / best, 3)
+        res["speedup_vs_dense_against"] = "own_kernels" if own_tps >= torch_tps else "torch"
+        res["hf_generate"] = {
+            "what": "model.generate(prompt, max_new_tokens=%d, past_key_values=fresh cache), prefill included "
+                    "(scripts/benchmark.py:68-99), mean of 2 runs" % new_tokens,
+            "leankv_tok_s": gen_lkv, "dense_fp16_tok_s": dense["generate"],
+            "speedup": round(gen_lkv / dense["generate"], 3)}
+    else:
+        res["hf_generate"] = {"leankv_tok_s": gen_lkv}
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_decode(torch, model, th, args.prompt)
     del model

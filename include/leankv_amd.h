@@ -79,6 +79,21 @@ int lkv_sparse_gateup_swiglu(const void* x, const void* wg_colmajor,
                              void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Up to 3 TEAL sparse GEMVs that share one input x, in one launch that reads
+ * x once: y[s] = sparse_gemv(x, w[s], thresholds[s]) for s < n.  This is the
+ * q/k/v step of an attention layer (leankv/teal/patching.py:169-177 patches
+ * q_proj, k_proj and v_proj, PROJ_NAMES :31, which the reference runs as
+ * three sparse_gemv calls on the same x).  w[s] is column-major [N[s], Z] as
+ * for lkv_sparse_gemv (N[s] % 8 == 0), y[s] fp16 [N[s]]; w, thresholds, N and
+ * y are host arrays of n entries.  The chunking is the fused decode step's
+ * q|k|v launch, so y[s] equals that step's projection bit for bit.
+ */
+size_t lkv_sparse_gemv_multi_workspace_bytes(int n, const int64_t* N, int64_t Z);
+int lkv_sparse_gemv_multi(const void* x, int n, const void* const* w, const float* thresholds,
+                          const int64_t* N, int64_t Z, void* const* y, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/*
  * The split-K pass of lkv_sparse_gemv / lkv_sparse_gateup_swiglu alone: the
  * fp32 partial sums, without the reduction over row chunks, for callers that
  * fuse that reduction into their own consumer (the decode step does this
@@ -397,6 +412,28 @@ int lkv_rmsnorm(const void* x, const void* w, float eps, int64_t M, int64_t Z, v
  * A step is: lkv_decode_begin, lkv_decode_evict, lkv_decode_layer_step per
  * layer, lkv_decode_head, all on one stream. */
 size_t lkv_decode_workspace_bytes(const lkv_decode_dims* dims);
+/* Where the step leaves its intermediate results in the workspace (byte
+ * offsets from its start), for callers that read a layer's projections after
+ * lkv_decode_layer_step: the split-K partial sums of every GEMV, fp32
+ * [slab][chunk][256] per matrix (slab = output column / 256; summing a
+ * column's chunks in chunk order from 0 and rounding to fp16 gives the
+ * projection, as for lkv_sparse_gemv_partials), the RoPE'd query and the
+ * attention output (fp16 [n_heads * 128]).  They hold the last call's values
+ * until the next call overwrites them.  No reference counterpart: it exposes
+ * what the reference's per-projection calls (leankv/teal/patching.py:169-180)
+ * return one by one. */
+typedef struct lkv_decode_layout {
+  size_t part_q, part_k, part_v; /* q|k|v GEMV, one region per segment */
+  size_t part_o;                 /* o_proj */
+  size_t part_gate, part_up;     /* gate|up */
+  size_t part_down;              /* down */
+  size_t part_lm;                /* lm_head (lkv_decode_head) */
+  size_t q_rope;                 /* fp16 query after RoPE */
+  size_t attn_out;               /* fp16 attention output (o_proj input) */
+  size_t total;                  /* = lkv_decode_workspace_bytes */
+  int32_t chunks_qkv, chunks_o, chunks_gateup, chunks_down, chunks_lm;
+} lkv_decode_layout;
+int lkv_decode_workspace_layout(const lkv_decode_dims* dims, lkv_decode_layout* layout);
 /* x = embed[tok] (embed fp16 [vocab][hidden] row-major); latches pos. */
 int lkv_decode_begin(const lkv_decode_dims* dims, const void* embed, const int64_t* tok, const int64_t* pos,
                      void* x, void* workspace, size_t workspace_bytes, void* stream);
@@ -414,6 +451,17 @@ int lkv_decode_evict(const lkv_decode_dims* dims, const lkv_decode_layer* layers
  * step's new key / value enter the hot ring (eviction is lkv_decode_evict's). */
 int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_decode_layer* layer, void* x,
                           void* workspace, size_t workspace_bytes, void* stream);
+/* The same decoder layer with a plain fp16 KV cache instead of the TurboQuant
+ * one: the dense-fp16 decode that the reference's baseline runs
+ * (scripts/raw_baseline.py:33-62: HF decode with an fp16 DynamicCache), on
+ * this library's kernels (with every TEAL threshold 0 the projections are
+ * dense).  The step's key and value are RoPE'd as in lkv_decode_layer_step and
+ * written to kv_pool, fp16 [ceil(max_len / 16)][2 (K, V)][16][n_kv_heads][128]
+ * (token t in page t / 16, slot t % 16, the layout of lkv_paged_decode_attn),
+ * then lkv_paged_decode_attn attends to tokens 0 .. pos.  The cache fields of
+ * `layer` are not read; lkv_decode_evict is not needed. */
+int lkv_decode_layer_step_f16kv(const lkv_decode_dims* dims, const lkv_decode_layer* layer, void* kv_pool, void* x,
+                                void* workspace, size_t workspace_bytes, void* stream);
 /* logits = lm_head(RMSNorm(x) * final_norm) (fp16 [vocab]); tok = argmax
  * (lowest index among equal maxima); pos += 1. */
 int lkv_decode_head(const lkv_decode_dims* dims, const void* final_norm, const void* lm_head, const void* x,

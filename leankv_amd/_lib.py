@@ -36,6 +36,8 @@ SIGNATURES = {
     "lkv_sparse_gemv": (_int, [_c_p, _c_p, _f32, _i64, _i64, _c_p, _c_p, _sz, _c_p]),
     "lkv_sparse_gateup_workspace_bytes": (_sz, [_i64, _i64]),
     "lkv_sparse_gateup_swiglu": (_int, [_c_p, _c_p, _c_p, _f32, _f32, _i64, _i64, _c_p, _c_p, _sz, _c_p]),
+    "lkv_sparse_gemv_multi_workspace_bytes": (_sz, [_int, _c_p, _i64]),
+    "lkv_sparse_gemv_multi": (_int, [_c_p, _int, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _sz, _c_p]),
     "lkv_sparse_gemv_chunks": (_int, [_i64, _i64]),
     "lkv_sparse_gemv_partials": (_int, [_c_p, _c_p, _c_p, _f32, _f32, _i64, _i64, _c_p, _sz, _c_p]),
     "lkv_tq_packed_row_bytes": (_int, [_int]),
@@ -64,9 +66,11 @@ SIGNATURES = {
                                    _i64, _i64, _i64, _i64, _i64, _f32, _c_p, _c_p, _sz, _c_p]),
     "lkv_rmsnorm": (_int, [_c_p, _c_p, _f32, _i64, _i64, _c_p, _c_p]),
     "lkv_decode_workspace_bytes": (_sz, [_c_p]),
+    "lkv_decode_workspace_layout": (_int, [_c_p, _c_p]),
     "lkv_decode_begin": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
     "lkv_decode_evict": (_int, [_c_p, _c_p, ctypes.c_int64, _c_p, _sz, _c_p]),
     "lkv_decode_layer_step": (_int, [_c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
+    "lkv_decode_layer_step_f16kv": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
     "lkv_decode_head": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
 }
 
@@ -91,6 +95,17 @@ class DecodeLayer(ctypes.Structure):
         ("k_codes", _c_p), ("k_norms", _c_p), ("v_codes", _c_p), ("v_norms", _c_p), ("k_hot", _c_p),
         ("v_hot", _c_p), ("PiK", _c_p), ("PiV", _c_p),
     ]
+
+class DecodeLayout(ctypes.Structure):
+    """lkv_decode_layout (include/leankv_amd.h): byte offsets of a step's results in its workspace."""
+
+    _fields_ = [
+        ("part_q", _sz), ("part_k", _sz), ("part_v", _sz), ("part_o", _sz), ("part_gate", _sz), ("part_up", _sz),
+        ("part_down", _sz), ("part_lm", _sz), ("q_rope", _sz), ("attn_out", _sz), ("total", _sz),
+        ("chunks_qkv", ctypes.c_int32), ("chunks_o", ctypes.c_int32), ("chunks_gateup", ctypes.c_int32),
+        ("chunks_down", ctypes.c_int32), ("chunks_lm", ctypes.c_int32),
+    ]
+
 
 _lib = None
 _lock = threading.Lock()

@@ -75,7 +75,7 @@ def optimize_model(model, teal_sparsity: Optional[float] = None, teal_thresholds
         if cache.fused_attention:
             from .turboquant.attention import use_on
 
-            use_on(model)
+            use_on(model, cache)
         print("[LeanKV] TurboQuant enabled (bits=%d, head_dim=%d)" % (turboquant_bits, head_dim))
     return model, cache
 

@@ -32,6 +32,7 @@ namespace {
 constexpr int kD = 128;
 constexpr int kThreads = 256;
 constexpr int kMaxG = 8;  // query heads per kv head of the decode step
+constexpr int kF16Page = 16;  // tokens per page of the fp16-KV step's pool
 
 struct Plan {
   int64_t Hq, Hkv, G, nq, nkv;                 // q / k,v projection widths
@@ -39,8 +40,9 @@ struct Plan {
   int bz_qkv, bz_o, bz_gu, bz_d, bz_lm;
   int nc_qkv, nc_o, nc_gu, nc_d, nc_lm;
   AttnPlan attn;
-  size_t off_state, off_pqkv, off_po, off_pgu, off_pd, off_plm, off_q16, off_attn, off_rec, off_cand,
-      total;
+  int64_t f16_pages;  // pages of the fp16-KV step's pool (kF16Page tokens each)
+  size_t off_state, off_pqkv, off_po, off_pgu, off_pd, off_plm, off_q16, off_attn, off_rec, off_cand, off_pt,
+      off_prec, prec_bytes, total;
 };
 
 size_t al256(size_t v) { return (v + 255) / 256 * 256; }
@@ -84,6 +86,10 @@ Plan make_plan(const lkv_decode_dims& d) {
   p.off_attn = take(static_cast<size_t>(p.nq) * 2);
   p.off_rec = take(p.attn.total - p.attn.part_off);
   p.off_cand = take(static_cast<size_t>(p.svoc) * 8);
+  p.f16_pages = (d.max_len + kF16Page - 1) / kF16Page;
+  p.off_pt = take(static_cast<size_t>(3 + p.f16_pages) * 4);
+  p.prec_bytes = lkv_paged_decode_attn_workspace_bytes(1, d.n_heads, d.n_kv_heads, d.max_len);
+  p.off_prec = take(p.prec_bytes);
   p.total = o;
   return p;
 }
@@ -150,6 +156,60 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(uint16_t* __restrict
   const uint16_t xv = x[n];
   const float o = h2f(f2h(column_sum(part, n, nchunk)));
   x[n] = f2h(h2f(xv) + o);
+}
+
+// The fp16-KV step's q|k|v epilogue (the dense baseline's cache append): the
+// q|k|v partial sums in chunk order, fp16, RoPE at pos for q and k (rope_pair,
+// the arithmetic of the TurboQuant split kernel's prologue, so both steps
+// produce the same query and key bits), the query to q16, the key and value
+// into the token's slot of the fp16 page pool kv [page][K, V][kF16Page][Hkv]
+// [128] (token t in page t / kF16Page, slot t % kF16Page), and the page table
+// of the one sequence over identity pages: pt = {indptr 0, npages,
+// last page length, pages 0 .. npages - 1}.  Items: nq / 2 query dim pairs,
+// then nkv / 2 key pairs, then nkv / 2 value pairs.
+__global__ __launch_bounds__(kThreads) void f16kv_prep_kernel(const float* __restrict__ pq,
+                                                              const float* __restrict__ pk,
+                                                              const float* __restrict__ pv, int nchunk,
+                                                              const uint16_t* __restrict__ rope_cos,
+                                                              const uint16_t* __restrict__ rope_sin,
+                                                              const int32_t* __restrict__ state,
+                                                              uint16_t* __restrict__ q16, uint16_t* __restrict__ kv,
+                                                              int32_t* __restrict__ pt, int nq, int nkv, int Hkv) {
+  const int pos = state[0];
+  const int e = blockIdx.x * kThreads + threadIdx.x;
+  const uint16_t* cos_row = rope_cos + static_cast<size_t>(pos) * kD;
+  const uint16_t* sin_row = rope_sin + static_cast<size_t>(pos) * kD;
+  const size_t page = pos / kF16Page, slot = pos % kF16Page;
+  const size_t row = static_cast<size_t>(Hkv) * kD;  // one token of one page half
+  uint16_t* kdst = kv + (page * 2 * kF16Page + slot) * row;
+  uint16_t* vdst = kv + ((page * 2 + 1) * kF16Page + slot) * row;
+  const int nqp = nq / 2, nkp = nkv / 2;
+  if (e < nqp + 2 * nkp) {
+    const bool is_q = e < nqp, is_k = !is_q && e < nqp + nkp;
+    const int i = is_q ? e : (is_k ? e - nqp : e - nqp - nkp);
+    const int col = (i / 64) * kD + i % 64;
+    const float* P = is_q ? pq : (is_k ? pk : pv);
+    float x0, x1, o0, o1;
+    column_sum2(P, col, col + 64, nchunk, x0, x1);
+    if (is_q || is_k) {
+      rope_pair(x0, x1, cos_row, sin_row, i % 64, o0, o1);
+    } else {
+      o0 = x0;
+      o1 = x1;
+    }
+    uint16_t* dst = is_q ? q16 : (is_k ? kdst : vdst);
+    dst[col] = f2h(o0);
+    dst[col + 64] = f2h(o1);
+  }
+  if (blockIdx.x == 0) {
+    const int npages = static_cast<int>(page) + 1;
+    if (threadIdx.x == 0) {
+      pt[0] = 0;
+      pt[1] = npages;
+      pt[2] = static_cast<int>(slot) + 1;
+    }
+    for (int j = threadIdx.x; j < npages; j += kThreads) pt[3 + j] = j;
+  }
 }
 
 // y = RMSNorm(x) * w for M rows of Z; block (j, m) writes columns
@@ -336,6 +396,31 @@ extern "C" size_t lkv_decode_workspace_bytes(const lkv_decode_dims* dims) {
   return make_plan(*dims).total;
 }
 
+extern "C" int lkv_decode_workspace_layout(const lkv_decode_dims* dims, lkv_decode_layout* out) {
+  if (int e = check_dims(dims)) return e;
+  LKV_REQUIRE(out != nullptr, "decode_workspace_layout: null output");
+  const Plan p = make_plan(*dims);
+  lkv_decode_layout l{};
+  l.part_q = p.off_pqkv;
+  l.part_k = l.part_q + gemv_part_floats(p.nq, p.nc_qkv) * 4;
+  l.part_v = l.part_k + gemv_part_floats(p.nkv, p.nc_qkv) * 4;
+  l.part_o = p.off_po;
+  l.part_gate = p.off_pgu;
+  l.part_up = p.off_pgu + gemv_part_floats(dims->ffn, p.nc_gu) * 4;
+  l.part_down = p.off_pd;
+  l.part_lm = p.off_plm;
+  l.q_rope = p.off_q16;
+  l.attn_out = p.off_attn;
+  l.chunks_qkv = p.nc_qkv;
+  l.chunks_o = p.nc_o;
+  l.chunks_gateup = p.nc_gu;
+  l.chunks_down = p.nc_d;
+  l.chunks_lm = p.nc_lm;
+  l.total = p.total;
+  *out = l;
+  return LKV_OK;
+}
+
 extern "C" int lkv_decode_begin(const lkv_decode_dims* dims, const void* embed, const int64_t* tok,
                                 const int64_t* pos, void* x, void* workspace, size_t workspace_bytes, void* stream) {
   if (int e = check_dims(dims)) return e;
@@ -393,18 +478,122 @@ extern "C" int lkv_decode_evict(const lkv_decode_dims* dims, const lkv_decode_la
   return LKV_OK;
 }
 
-extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_decode_layer* L, void* x, void* workspace,
-                                     size_t workspace_bytes, void* stream) {
-  if (int e = check_dims(dims)) return e;
-  const lkv_decode_dims& d = *dims;
-  const Plan p = make_plan(d);
-  if (int e = check_ws(p, workspace, workspace_bytes)) return e;
+namespace lkv {
+namespace {
+
+int check_layer_weights(const lkv_decode_layer* L, const void* x) {
   LKV_REQUIRE(L && x && aligned16(x), "decode_layer: null layer or unaligned x");
   LKV_REQUIRE(L->input_norm && L->post_norm && L->wq && L->wk && L->wv && L->wo && L->wg && L->wu && L->wd,
               "decode_layer: null weight");
   LKV_REQUIRE(aligned16(L->wq) && aligned16(L->wk) && aligned16(L->wv) && aligned16(L->wo) && aligned16(L->wg) &&
                   aligned16(L->wu) && aligned16(L->wd),
               "decode_layer: weights must be 16-byte aligned");
+  return LKV_OK;
+}
+
+// 1. q|k|v: one GEMV launch over three segments, RMSNorm of x in the prologue.
+int step_qkv(const Plan& p, const lkv_decode_dims& d, const lkv_decode_layer* L, const uint16_t* x, char* ws,
+             hipStream_t st) {
+  GemvArgs G{};
+  G.x = x;
+  G.norm_w = static_cast<const uint16_t*>(L->input_norm);
+  G.eps = d.eps;
+  G.nseg = 3;
+  const void* w[3] = {L->wq, L->wk, L->wv};
+  const int64_t n[3] = {p.nq, p.nkv, p.nkv};
+  const float t[3] = {L->tq, L->tk, L->tv};
+  size_t off = 0;
+  int slab = 0;
+  for (int s = 0; s < 3; ++s) {
+    G.A[s] = static_cast<const uint16_t*>(w[s]);
+    G.a_bytes[s] = static_cast<uint32_t>(d.hidden * n[s] * 2);
+    G.N[s] = static_cast<int>(n[s]);
+    G.t[s] = t[s];
+    G.slab0[s] = slab;
+    G.part_off[s] = off;
+    slab += static_cast<int>(gemv_slabs(n[s]));
+    off += gemv_part_floats(n[s], p.nc_qkv);
+  }
+  G.slab0[3] = slab;
+  G.Z = static_cast<int>(d.hidden);
+  G.nchunk = p.nc_qkv;
+  G.part = reinterpret_cast<float*>(ws + p.off_pqkv);
+  return gemv_launch(G, p.bz_qkv, false, kInRmsNorm, slab, st);
+}
+
+// 4-8. o_proj on the attention output, residual, gate|up (RMSNorm prologue),
+// down (SwiGLU prologue), residual.
+int step_tail(const Plan& p, const lkv_decode_dims& d, const lkv_decode_layer* L, uint16_t* xx, char* ws,
+              hipStream_t st) {
+  const int H = static_cast<int>(d.hidden);
+  {
+    GemvArgs G{};
+    G.x = reinterpret_cast<const uint16_t*>(ws + p.off_attn);
+    G.nseg = 1;
+    G.A[0] = static_cast<const uint16_t*>(L->wo);
+    G.a_bytes[0] = static_cast<uint32_t>(p.nq * d.hidden * 2);
+    G.N[0] = H;
+    G.t[0] = L->to;
+    G.slab0[1] = static_cast<int>(p.sh);
+    G.Z = static_cast<int>(p.nq);
+    G.nchunk = p.nc_o;
+    G.part = reinterpret_cast<float*>(ws + p.off_po);
+    if (int e = gemv_launch(G, p.bz_o, false, kInRaw, static_cast<int>(p.sh), st)) return e;
+    hipLaunchKernelGGL(residual_kernel, dim3(static_cast<unsigned>(p.sh)), dim3(kThreads), 0, st, xx, G.part, H,
+                       p.nc_o);
+    LKV_LAUNCH_CHECK("decode residual");
+  }
+  {
+    GemvArgs G{};
+    G.x = xx;
+    G.norm_w = static_cast<const uint16_t*>(L->post_norm);
+    G.eps = d.eps;
+    G.nseg = 1;
+    G.A[0] = static_cast<const uint16_t*>(L->wg);
+    G.A_up = static_cast<const uint16_t*>(L->wu);
+    G.a_bytes[0] = static_cast<uint32_t>(d.hidden * d.ffn * 2);
+    G.N[0] = static_cast<int>(d.ffn);
+    G.t[0] = L->tg;
+    G.t_up = L->tu;
+    G.slab0[1] = static_cast<int>(p.sf);
+    G.Z = H;
+    G.nchunk = p.nc_gu;
+    G.part = reinterpret_cast<float*>(ws + p.off_pgu);
+    G.part_up_off = gemv_part_floats(d.ffn, p.nc_gu);
+    if (int e = gemv_launch(G, p.bz_gu, true, kInRmsNorm, static_cast<int>(p.sf), st)) return e;
+  }
+  {
+    GemvArgs G{};
+    G.in_part = reinterpret_cast<const float*>(ws + p.off_pgu);
+    G.in_nslab = static_cast<int>(p.sf);
+    G.in_nchunk = p.nc_gu;
+    G.nseg = 1;
+    G.A[0] = static_cast<const uint16_t*>(L->wd);
+    G.a_bytes[0] = static_cast<uint32_t>(d.ffn * d.hidden * 2);
+    G.N[0] = H;
+    G.t[0] = L->td;
+    G.slab0[1] = static_cast<int>(p.sh);
+    G.Z = static_cast<int>(d.ffn);
+    G.nchunk = p.nc_d;
+    G.part = reinterpret_cast<float*>(ws + p.off_pd);
+    if (int e = gemv_launch(G, p.bz_d, false, kInSwiglu, static_cast<int>(p.sh), st)) return e;
+    hipLaunchKernelGGL(residual_kernel, dim3(static_cast<unsigned>(p.sh)), dim3(kThreads), 0, st, xx, G.part, H,
+                       p.nc_d);
+    LKV_LAUNCH_CHECK("decode residual");
+  }
+  return LKV_OK;
+}
+
+}  // namespace
+}  // namespace lkv
+
+extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_decode_layer* L, void* x, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (int e = check_dims(dims)) return e;
+  const lkv_decode_dims& d = *dims;
+  const Plan p = make_plan(d);
+  if (int e = check_ws(p, workspace, workspace_bytes)) return e;
+  if (int e = check_layer_weights(L, x)) return e;
   LKV_REQUIRE(L->k_codes && L->k_norms && L->v_codes && L->v_norms && L->k_hot && L->v_hot && L->PiK && L->PiV,
               "decode_layer: null cache pointer");
   LKV_REQUIRE(aligned16(L->k_codes) && aligned16(L->v_codes) && aligned16(L->k_hot) && aligned16(L->v_hot),
@@ -413,36 +602,7 @@ extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_deco
   char* ws = static_cast<char*>(workspace);
   uint16_t* xx = static_cast<uint16_t*>(x);
   const int32_t* state = reinterpret_cast<const int32_t*>(ws + p.off_state);
-  const int H = static_cast<int>(d.hidden);
-
-  // 1. q|k|v
-  {
-    GemvArgs G{};
-    G.x = xx;
-    G.norm_w = static_cast<const uint16_t*>(L->input_norm);
-    G.eps = d.eps;
-    G.nseg = 3;
-    const void* w[3] = {L->wq, L->wk, L->wv};
-    const int64_t n[3] = {p.nq, p.nkv, p.nkv};
-    const float t[3] = {L->tq, L->tk, L->tv};
-    size_t off = 0;
-    int slab = 0;
-    for (int s = 0; s < 3; ++s) {
-      G.A[s] = static_cast<const uint16_t*>(w[s]);
-      G.a_bytes[s] = static_cast<uint32_t>(d.hidden * n[s] * 2);
-      G.N[s] = static_cast<int>(n[s]);
-      G.t[s] = t[s];
-      G.slab0[s] = slab;
-      G.part_off[s] = off;
-      slab += static_cast<int>(gemv_slabs(n[s]));
-      off += gemv_part_floats(n[s], p.nc_qkv);
-    }
-    G.slab0[3] = slab;
-    G.Z = H;
-    G.nchunk = p.nc_qkv;
-    G.part = reinterpret_cast<float*>(ws + p.off_pqkv);
-    if (int e = gemv_launch(G, p.bz_qkv, false, kInRmsNorm, slab, st)) return e;
-  }
+  if (int e = step_qkv(p, d, L, xx, ws, st)) return e;
   // 2-3. attention: the split kernel reduces the q|k|v partials itself (RoPE,
   // query rotation, the new key and value into the ring)
   {
@@ -477,65 +637,37 @@ extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_deco
     c.bits = d.bits;
     if (int e = attn_launch(c, p.attn, st)) return e;
   }
-  // 4-5. o_proj, residual
-  {
-    GemvArgs G{};
-    G.x = reinterpret_cast<const uint16_t*>(ws + p.off_attn);
-    G.nseg = 1;
-    G.A[0] = static_cast<const uint16_t*>(L->wo);
-    G.a_bytes[0] = static_cast<uint32_t>(p.nq * d.hidden * 2);
-    G.N[0] = H;
-    G.t[0] = L->to;
-    G.slab0[1] = static_cast<int>(p.sh);
-    G.Z = static_cast<int>(p.nq);
-    G.nchunk = p.nc_o;
-    G.part = reinterpret_cast<float*>(ws + p.off_po);
-    if (int e = gemv_launch(G, p.bz_o, false, kInRaw, static_cast<int>(p.sh), st)) return e;
-    hipLaunchKernelGGL(residual_kernel, dim3(static_cast<unsigned>(p.sh)), dim3(kThreads), 0, st, xx, G.part, H,
-                       p.nc_o);
-    LKV_LAUNCH_CHECK("decode residual");
-  }
-  // 6. gate|up
-  {
-    GemvArgs G{};
-    G.x = xx;
-    G.norm_w = static_cast<const uint16_t*>(L->post_norm);
-    G.eps = d.eps;
-    G.nseg = 1;
-    G.A[0] = static_cast<const uint16_t*>(L->wg);
-    G.A_up = static_cast<const uint16_t*>(L->wu);
-    G.a_bytes[0] = static_cast<uint32_t>(d.hidden * d.ffn * 2);
-    G.N[0] = static_cast<int>(d.ffn);
-    G.t[0] = L->tg;
-    G.t_up = L->tu;
-    G.slab0[1] = static_cast<int>(p.sf);
-    G.Z = H;
-    G.nchunk = p.nc_gu;
-    G.part = reinterpret_cast<float*>(ws + p.off_pgu);
-    G.part_up_off = gemv_part_floats(d.ffn, p.nc_gu);
-    if (int e = gemv_launch(G, p.bz_gu, true, kInRmsNorm, static_cast<int>(p.sf), st)) return e;
-  }
-  // 7-8. down (SwiGLU prologue), residual
-  {
-    GemvArgs G{};
-    G.in_part = reinterpret_cast<const float*>(ws + p.off_pgu);
-    G.in_nslab = static_cast<int>(p.sf);
-    G.in_nchunk = p.nc_gu;
-    G.nseg = 1;
-    G.A[0] = static_cast<const uint16_t*>(L->wd);
-    G.a_bytes[0] = static_cast<uint32_t>(d.ffn * d.hidden * 2);
-    G.N[0] = H;
-    G.t[0] = L->td;
-    G.slab0[1] = static_cast<int>(p.sh);
-    G.Z = static_cast<int>(d.ffn);
-    G.nchunk = p.nc_d;
-    G.part = reinterpret_cast<float*>(ws + p.off_pd);
-    if (int e = gemv_launch(G, p.bz_d, false, kInSwiglu, static_cast<int>(p.sh), st)) return e;
-    hipLaunchKernelGGL(residual_kernel, dim3(static_cast<unsigned>(p.sh)), dim3(kThreads), 0, st, xx, G.part, H,
-                       p.nc_d);
-    LKV_LAUNCH_CHECK("decode residual");
-  }
-  return LKV_OK;
+  return step_tail(p, d, L, xx, ws, st);
+}
+
+extern "C" int lkv_decode_layer_step_f16kv(const lkv_decode_dims* dims, const lkv_decode_layer* L, void* kv_pool,
+                                           void* x, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int e = check_dims(dims)) return e;
+  const lkv_decode_dims& d = *dims;
+  const Plan p = make_plan(d);
+  if (int e = check_ws(p, workspace, workspace_bytes)) return e;
+  if (int e = check_layer_weights(L, x)) return e;
+  LKV_REQUIRE(kv_pool && aligned16(kv_pool), "decode_layer_f16kv: null or unaligned kv pool");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* xx = static_cast<uint16_t*>(x);
+  if (int e = step_qkv(p, d, L, xx, ws, st)) return e;
+  const float* pq = reinterpret_cast<const float*>(ws + p.off_pqkv);
+  const float* pk = pq + gemv_part_floats(p.nq, p.nc_qkv);
+  const float* pv = pk + gemv_part_floats(p.nkv, p.nc_qkv);
+  int32_t* pt = reinterpret_cast<int32_t*>(ws + p.off_pt);
+  uint16_t* q16 = reinterpret_cast<uint16_t*>(ws + p.off_q16);
+  const int items = static_cast<int>(p.nq / 2 + p.nkv);
+  hipLaunchKernelGGL(f16kv_prep_kernel, dim3(static_cast<unsigned>((items + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, st, pq, pk, pv, p.nc_qkv, static_cast<const uint16_t*>(d.rope_cos),
+                     static_cast<const uint16_t*>(d.rope_sin), reinterpret_cast<const int32_t*>(ws + p.off_state),
+                     q16, static_cast<uint16_t*>(kv_pool), pt, static_cast<int>(p.nq), static_cast<int>(p.nkv),
+                     static_cast<int>(p.Hkv));
+  LKV_LAUNCH_CHECK("decode f16kv prep");
+  if (int e = lkv_paged_decode_attn(q16, kv_pool, pt, pt + 3, pt + 2, 1, p.Hq, p.Hkv, kF16Page, p.f16_pages,
+                                    d.max_len, d.scale, ws + p.off_attn, ws + p.off_prec, p.prec_bytes, stream))
+    return e;
+  return step_tail(p, d, L, xx, ws, st);
 }
 
 extern "C" int lkv_decode_head(const lkv_decode_dims* dims, const void* final_norm, const void* lm_head, const void* x,

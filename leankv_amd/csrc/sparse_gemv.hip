@@ -299,6 +299,26 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_kernel(const float* 
     y[n] = f2h(g);
 }
 
+// Several matrices that share x (lkv_sparse_gemv_multi): column n of the
+// concatenated outputs belongs to segment s when n0[s] <= n < n0[s + 1].
+struct MultiReduce {
+  const float* part[kMaxSeg];
+  uint16_t* y[kMaxSeg];
+  int n0[kMaxSeg + 1];
+  int nseg, nchunk;
+};
+
+__global__ __launch_bounds__(kGemvThreads) void gemv_reduce_multi_kernel(MultiReduce R) {
+  const int n = blockIdx.x * kGemvThreads + threadIdx.x;
+  if (n >= R.n0[R.nseg]) return;
+  int s = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxSeg; ++i)
+    if (i < R.nseg && n >= R.n0[i]) s = i;
+  const int c = n - R.n0[s];
+  R.y[s][c] = f2h(column_sum(R.part[s], c, R.nchunk));
+}
+
 }  // namespace
 
 // Row-chunk size for a GEMV with Z inputs over `slabs` column slabs: the
@@ -521,6 +541,93 @@ extern "C" int lkv_sparse_gemv_partials(const void* x, const void* w_gate, const
   G.part = partials;
   G.part_up_off = gemv_part_floats(N, nchunk);
   return gemv_launch(G, bz, dual, kInRaw, static_cast<int>(nslab), static_cast<hipStream_t>(stream));
+}
+
+namespace {
+
+int multi_check(int n, const int64_t* N, int64_t Z) {
+  LKV_REQUIRE(n >= 1 && n <= kMaxSeg && N != nullptr, "sparse_gemv_multi: 1..%d matrices, got %d", kMaxSeg, n);
+  LKV_REQUIRE(Z > 0 && Z < (1 << 30), "sparse_gemv_multi: Z=%lld out of range", (long long)Z);
+  for (int s = 0; s < n; ++s) {
+    LKV_REQUIRE(N[s] > 0 && N[s] % 8 == 0 && N[s] < (1 << 30),
+                "sparse_gemv_multi: N[%d]=%lld must be a positive multiple of 8", s, (long long)N[s]);
+    LKV_REQUIRE(N[s] * Z * 2 < (1ll << 32), "sparse_gemv_multi: matrix %d exceeds the 4 GiB descriptor range", s);
+  }
+  return LKV_OK;
+}
+
+struct MultiPlan {
+  int bz, nchunk, nslab;
+  size_t part_off[kMaxSeg];
+  size_t bytes;
+};
+
+// The fused decode step's q|k|v plan (decode.hip): one chunk size for the
+// slabs of all segments together, partials of segment s after those of s - 1.
+MultiPlan multi_plan(int n, const int64_t* N, int64_t Z) {
+  MultiPlan p{};
+  for (int s = 0; s < n; ++s) p.nslab += static_cast<int>(gemv_slabs(N[s]));
+  p.bz = gemv_pick_bz(p.nslab, Z);
+  p.nchunk = static_cast<int>(gemv_chunks(Z, p.bz));
+  size_t off = 0;
+  for (int s = 0; s < n; ++s) {
+    p.part_off[s] = off;
+    off += gemv_part_floats(N[s], p.nchunk);
+  }
+  p.bytes = off * sizeof(float);
+  return p;
+}
+
+}  // namespace
+
+extern "C" size_t lkv_sparse_gemv_multi_workspace_bytes(int n, const int64_t* N, int64_t Z) {
+  if (multi_check(n, N, Z) != LKV_OK) return 0;
+  return multi_plan(n, N, Z).bytes;
+}
+
+extern "C" int lkv_sparse_gemv_multi(const void* x, int n, const void* const* w, const float* thresholds,
+                                     const int64_t* N, int64_t Z, void* const* y, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (int e = multi_check(n, N, Z)) return e;
+  LKV_REQUIRE(x && w && thresholds && y, "sparse_gemv_multi: null pointer");
+  for (int s = 0; s < n; ++s)
+    LKV_REQUIRE(w[s] && y[s] && aligned16(w[s]) && aligned16(y[s]),
+                "sparse_gemv_multi: matrix and output %d must be non-null and 16-byte aligned", s);
+  const MultiPlan p = multi_plan(n, N, Z);
+  LKV_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= p.bytes,
+              "sparse_gemv_multi: workspace of %zu bytes (16-byte aligned) required, got %zu", p.bytes,
+              workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  GemvArgs G{};
+  G.x = static_cast<const uint16_t*>(x);
+  G.nseg = n;
+  MultiReduce R{};
+  R.nseg = n;
+  R.nchunk = p.nchunk;
+  int slab = 0, col = 0;
+  for (int s = 0; s < n; ++s) {
+    G.A[s] = static_cast<const uint16_t*>(w[s]);
+    G.a_bytes[s] = static_cast<uint32_t>(N[s] * Z * 2);
+    G.N[s] = static_cast<int>(N[s]);
+    G.t[s] = thresholds[s];
+    G.slab0[s] = slab;
+    G.part_off[s] = p.part_off[s];
+    slab += static_cast<int>(gemv_slabs(N[s]));
+    R.part[s] = static_cast<float*>(workspace) + p.part_off[s];
+    R.y[s] = static_cast<uint16_t*>(y[s]);
+    R.n0[s] = col;
+    col += static_cast<int>(N[s]);
+  }
+  G.slab0[n] = slab;
+  R.n0[n] = col;
+  G.Z = static_cast<int>(Z);
+  G.nchunk = p.nchunk;
+  G.part = static_cast<float*>(workspace);
+  if (int e = gemv_launch(G, p.bz, false, kInRaw, slab, st)) return e;
+  hipLaunchKernelGGL(gemv_reduce_multi_kernel, dim3(static_cast<unsigned>((col + kGemvThreads - 1) / kGemvThreads)),
+                     dim3(kGemvThreads), 0, st, R);
+  LKV_LAUNCH_CHECK("sparse_gemv_multi reduce");
+  return LKV_OK;
 }
 
 extern "C" int lkv_sparse_gemv(const void* x, const void* w, float threshold, int64_t N, int64_t Z, void* y,

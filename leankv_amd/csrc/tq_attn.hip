@@ -279,48 +279,6 @@ __device__ __forceinline__ void attend(const BlockRegs& R, int t0, int t_end, co
     attend_block<PERM, true>(R, t0, t_end, qa, tab, s_lut, lane, S);
 }
 
-// Columns n0 and n1 of a [slab][chunk][kGemvBN] GEMV partial array, each
-// summed over the chunks in chunk order from 0 (column_sum's order), with the
-// loads of both columns in flight together.
-__device__ __forceinline__ void column_sum2(const float* __restrict__ P, int n0, int n1, int nchunk, float& s0,
-                                            float& s1) {
-  constexpr int kB = 16;
-  const float* p0 = P + static_cast<size_t>(n0 / kGemvBN) * nchunk * kGemvBN + (n0 % kGemvBN);
-  const float* p1 = P + static_cast<size_t>(n1 / kGemvBN) * nchunk * kGemvBN + (n1 % kGemvBN);
-  s0 = 0.f;
-  s1 = 0.f;
-  for (int k0 = 0; k0 < nchunk; k0 += kB) {
-    float a[kB], c[kB];
-#pragma unroll
-    for (int i = 0; i < kB; ++i) {
-      const size_t o = static_cast<size_t>(min(k0 + i, nchunk - 1)) * kGemvBN;
-      a[i] = p0[o];
-      c[i] = p1[o];
-    }
-#pragma unroll
-    for (int i = 0; i < kB; ++i) {
-      s0 += k0 + i < nchunk ? a[i] : 0.f;
-      s1 += k0 + i < nchunk ? c[i] : 0.f;
-    }
-  }
-}
-
-// RoPE of the dim pair (d, d + 64) of an fp16 row, x * cos + rotate_half(x) *
-// sin with fp16 products and sum (apply_rotary_pos_emb on fp16 tensors,
-// modeling_mistral.py); x0, x1 are the fp32 projection sums, rounded to fp16
-// first as the fp16 projection output is.  Each product is rounded to fp16
-// before the sum: contraction is off here, since the compiler otherwise turns
-// the fp16 product and the fp32 add into one fma and skips that rounding.
-__device__ __forceinline__ void rope_pair(float x0, float x1, const uint16_t* __restrict__ cos_row,
-                                          const uint16_t* __restrict__ sin_row, int d, float& o0, float& o1) {
-#pragma clang fp contract(off)
-  const float a = h2f(f2h(x0)), c = h2f(f2h(x1));
-  const float c0 = h2f(cos_row[d]), c1 = h2f(cos_row[d + kD / 2]);
-  const float s0 = h2f(sin_row[d]), s1 = h2f(sin_row[d + kD / 2]);
-  o0 = h2f(f2h(h2f(f2h(a * c0)) + h2f(f2h(-c * s0))));
-  o1 = h2f(f2h(h2f(f2h(c * c1)) + h2f(f2h(a * s1))));
-}
-
 constexpr int kORow = kD + 4;  // padded LDS row of the per-wave outputs
 #ifndef LKV_ATTN_BLOCKS_PER_CU
 #define LKV_ATTN_BLOCKS_PER_CU 2

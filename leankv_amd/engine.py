@@ -14,9 +14,11 @@ token:
               fused TEAL gate/up + SwiGLU -> TEAL sparse down -> residual
   then:       final RMSNorm -> dense lm_head -> argmax (next token on device)
 
-``DenseEngine`` is the same loop with dense fp16 projections (torch F.linear)
-and an fp16 KV cache (torch SDPA), the MI355X counterpart of the reference's
-dense fp16 baseline (scripts/raw_baseline.py), also graph-captured.
+Two dense fp16 baselines run the same model with an fp16 KV cache, both
+graph-captured: ``OwnDenseEngine`` is LeanKVEngine's step on this library's
+kernels with every TEAL threshold 0 and the fp16 cache in pages (the strong
+baseline), ``DenseEngine`` is torch F.linear + SDPA (the reference's dense
+fp16 run, scripts/raw_baseline.py, as torch executes it).
 """
 
 from __future__ import annotations
@@ -70,6 +72,7 @@ class _Base:
         self.pos64 = torch.zeros(1, dtype=torch.long, device=self.dev)
         self.logits = torch.zeros(cfg.vocab_size, dtype=torch.float16, device=self.dev)
         self.graph = None
+        self._host_pos = None  # position of the next step, tracked on the host to bound it by max_len
 
     def _rope(self, q, k):
         cos = self.cos.index_select(0, self.pos64)  # [1, D]
@@ -95,14 +98,33 @@ class _Base:
         torch.cuda.current_stream().wait_stream(s)
         self.graph = g
 
+    def _set_start(self, first_token: torch.Tensor, length: int) -> None:
+        if not 0 <= int(length) < self.max_len:
+            raise _lib.LeanKVError("decode start position %d outside the engine's max_len %d"
+                                   % (int(length), self.max_len))
+        self.tok.copy_(first_token.view(1))
+        self.pos64.fill_(int(length))
+        self._host_pos = int(length)
+
     def step(self) -> None:
+        """One greedy decode step; the position it writes must stay below max_len (the RoPE table and the
+        cache are sized for it), so a step past it raises instead of overwriting the last slot."""
+        if self._host_pos is None:
+            raise _lib.LeanKVError("call start(first_token, length) before stepping the engine")
+        if self._host_pos >= self.max_len:
+            raise _lib.LeanKVError("decode position %d reached the engine's max_len %d"
+                                   % (self._host_pos, self.max_len))
         if self.graph is not None:
             self.graph.replay()
         else:
             self._step()
+        self._host_pos += 1
 
     @torch.no_grad()
     def generate(self, n: int) -> list:
+        if self._host_pos is not None and self._host_pos + n > self.max_len:
+            raise _lib.LeanKVError("%d more tokens from position %d exceed the engine's max_len %d"
+                                   % (n, self._host_pos, self.max_len))
         out = []
         for _ in range(n):
             self.step()
@@ -182,8 +204,7 @@ class LeanKVEngine(_Base):
 
     def start(self, first_token: torch.Tensor, length: int) -> None:
         """Set the token to feed next and its position (the cache length after prefill)."""
-        self.tok.copy_(first_token.view(1))
-        self.pos64.fill_(length)
+        self._set_start(first_token, length)
 
     def _step(self) -> None:
         lib = _lib.load()
@@ -197,6 +218,102 @@ class LeanKVEngine(_Base):
         for ls in self.layer_structs:
             _lib.check(lib.lkv_decode_layer_step(dims, ctypes.byref(ls), self.x.data_ptr(), ws, nb, st),
                        "lkv_decode_layer_step")
+        _lib.check(lib.lkv_decode_head(dims, self.final_norm.data_ptr(), self.lm_head_cm.data_ptr(),
+                                       self.x.data_ptr(), self.logits.data_ptr(), self.tok.data_ptr(),
+                                       self.pos64.data_ptr(), ws, nb, st), "lkv_decode_head")
+
+
+class OwnDenseEngine(_Base):
+    """Dense fp16 decode on this library's kernels: the dense baseline of the LeanKV engine.
+
+    The reference's baseline is plain HF decode with fp16 weights and an fp16 KV
+    cache (scripts/raw_baseline.py:33-62).  Here it is the fused decode step of
+    LeanKVEngine with every TEAL threshold 0 (the GEMVs read every weight row)
+    and an fp16 KV cache in 16-token pages (lkv_decode_layer_step_f16kv: the
+    step's key and value go to the pool, lkv_paged_decode_attn attends), so the
+    two engines differ only in TEAL and TurboQuant.  Weights are read
+    column-major; ones that are not get a column-major copy.  Graph-captured
+    like LeanKVEngine.
+    """
+
+    PAGE = 16  # tokens per page of the fp16 pool (lkv_decode_layer_step_f16kv)
+
+    def __init__(self, model, max_len: int):
+        super().__init__(model, max_len)
+        if self.D != 128:
+            raise ValueError("the fused decode step needs head_dim 128, got %d" % self.D)
+        from .turboquant.codebook import get_codebook_tensors
+
+        lib = _lib.load()
+        d = self.dev
+        self._keep = []
+        cent, bnd = get_codebook_tensors(128, 3, d, torch.float32)  # validated by the step, not used by it
+        self.dims = _lib.DecodeDims(
+            hidden=self.hidden, ffn=self.cfg.intermediate_size, vocab=self.cfg.vocab_size, n_heads=self.H,
+            n_kv_heads=self.Hkv, max_len=max_len, cap=max_len, hot_cap=64, bits=3, eps=self.eps, scale=self.scale,
+            bounds=self._hold(bnd[1:-1].contiguous()), centroids=self._hold(cent.contiguous()),
+            rope_cos=self._hold(self.cos), rope_sin=self._hold(self.sin))
+        self.pages = (max_len + self.PAGE - 1) // self.PAGE
+        self.pools = [torch.zeros(self.pages, 2, self.PAGE, self.Hkv, self.D, dtype=torch.float16, device=d)
+                      for _ in range(self.L)]
+        self.layer_structs = []
+        for layer in self.layers:
+            at, mlp = layer.self_attn, layer.mlp
+            w = {}
+            for name, mod in (("q", at.q_proj), ("k", at.k_proj), ("v", at.v_proj), ("o", at.o_proj),
+                              ("g", mlp.gate_proj), ("u", mlp.up_proj), ("d", mlp.down_proj)):
+                if getattr(mod, "bias", None) is not None:
+                    raise ValueError("the fused decode step has no projection bias")
+                w[name] = self._hold(_colmajor(mod.weight))
+            self.layer_structs.append(_lib.DecodeLayer(
+                input_norm=self._hold(layer.input_layernorm.weight.detach()),
+                post_norm=self._hold(layer.post_attention_layernorm.weight.detach()),
+                wq=w["q"], wk=w["k"], wv=w["v"], wo=w["o"], wg=w["g"], wu=w["u"], wd=w["d"],
+                tq=0.0, tk=0.0, tv=0.0, to=0.0, tg=0.0, tu=0.0, td=0.0))
+        self.final_norm = model.model.norm.weight.detach()
+        self.lm_head_cm = model.lm_head.weight.detach().t().contiguous()
+        nbytes = lib.lkv_decode_workspace_bytes(ctypes.byref(self.dims))
+        if nbytes == 0:
+            raise _lib.LeanKVError("lkv_decode_workspace_bytes rejected the model shape: %s" % _lib.last_error())
+        self.ws = torch.empty(nbytes, dtype=torch.uint8, device=d)
+        self.x = torch.empty(self.hidden, dtype=torch.float16, device=d)
+
+    def _hold(self, t: torch.Tensor) -> int:
+        if not t.is_cuda:
+            raise _lib.LeanKVError("decode state must live on the GPU")
+        self._keep.append(t)
+        return t.data_ptr()
+
+    def load_cache(self, past_key_values) -> int:
+        """Copy a prefilled HF DynamicCache (K/V [1, Hkv, n, 128]) into the page pools; returns its length."""
+        n = 0
+        for i in range(self.L):
+            lay = past_key_values.layers[i]
+            for half, t in ((0, lay.keys), (1, lay.values)):
+                n = t.shape[2]
+                if n > self.max_len:
+                    raise _lib.LeanKVError("prefilled cache of %d tokens exceeds max_len %d" % (n, self.max_len))
+                rows = t[0].transpose(0, 1)  # [n, Hkv, 128]
+                full, rest = divmod(n, self.PAGE)
+                if full:
+                    self.pools[i][:full, half] = rows[: full * self.PAGE].reshape(full, self.PAGE, self.Hkv, self.D)
+                if rest:
+                    self.pools[i][full, half, :rest] = rows[full * self.PAGE:]
+        return n
+
+    def start(self, first_token: torch.Tensor, length: int) -> None:
+        self._set_start(first_token, length)
+
+    def _step(self) -> None:
+        lib = _lib.load()
+        st = _lib.stream_handle(self.dev)
+        ws, nb = self.ws.data_ptr(), self.ws.numel()
+        dims = ctypes.byref(self.dims)
+        _lib.check(lib.lkv_decode_begin(dims, self.model.model.embed_tokens.weight.data_ptr(), self.tok.data_ptr(),
+                                        self.pos64.data_ptr(), self.x.data_ptr(), ws, nb, st), "lkv_decode_begin")
+        for ls, pool in zip(self.layer_structs, self.pools):
+            _lib.check(lib.lkv_decode_layer_step_f16kv(dims, ctypes.byref(ls), pool.data_ptr(), self.x.data_ptr(),
+                                                       ws, nb, st), "lkv_decode_layer_step_f16kv")
         _lib.check(lib.lkv_decode_head(dims, self.final_norm.data_ptr(), self.lm_head_cm.data_ptr(),
                                        self.x.data_ptr(), self.logits.data_ptr(), self.tok.data_ptr(),
                                        self.pos64.data_ptr(), ws, nb, st), "lkv_decode_head")
@@ -231,8 +348,7 @@ class DenseEngine(_Base):
         return n
 
     def start(self, first_token: torch.Tensor, length: int) -> None:
-        self.tok.copy_(first_token.view(1))
-        self.pos64.fill_(length)
+        self._set_start(first_token, length)
 
     def _step(self) -> None:
         x = self.model.model.embed_tokens.weight.index_select(0, self.tok)
@@ -257,14 +373,19 @@ class DenseEngine(_Base):
 
 
 # Mistral-7B-v0.3 shape (configs/mistral7b.yaml in the reference).
+# Mistral-7B-v0.3 has no sliding window ("sliding_window": null); MistralConfig's default is 4096.
 MISTRAL_7B = dict(vocab_size=32768, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
                   num_attention_heads=32, num_key_value_heads=8, head_dim=128, max_position_embeddings=32768,
-                  rope_theta=1e6, rms_norm_eps=1e-5)
+                  rope_theta=1e6, rms_norm_eps=1e-5, sliding_window=None)
 
 
 @torch.no_grad()
 def random_mistral(device="cuda", seed: int = 0, **overrides):
-    """Random-init fp16 MistralForCausalLM (weights ~N(0, 0.02), norms 1) built directly on `device`."""
+    """Random-init fp16 MistralForCausalLM (weights ~N(0, 0.02), norms 1) built directly on `device`.
+
+    The model is constructed with fp16 as the default dtype, as from_pretrained(torch_dtype=float16) does:
+    parameters are fp16 while the rotary embedding keeps its fp32 inverse frequencies (a ``.to(float16)``
+    of the whole module would round them to fp16 and shift RoPE angles by ~position * 2^-11 rad)."""
     from transformers import MistralConfig, MistralForCausalLM
 
     kw = dict(MISTRAL_7B)
@@ -272,8 +393,13 @@ def random_mistral(device="cuda", seed: int = 0, **overrides):
     cfg = MistralConfig(**kw)
     cfg._attn_implementation = "sdpa"
     torch.manual_seed(seed)
-    with torch.device(device):
-        model = MistralForCausalLM(cfg).to(torch.float16)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device(device):
+            model = MistralForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(prev)
     gen = torch.Generator(device=device).manual_seed(seed)
     for name, p in model.named_parameters():
         if p.dim() == 2:

@@ -156,6 +156,41 @@ def sparse_gateup_swiglu(x, w_gate, w_up, t_gate, t_up):
     return sparse_gateup_swiglu_out(x, w_gate, w_up, t_gate, t_up, out)
 
 
+def sparse_qkv(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor, tq: float, tk: float,
+               tv: float, out: tuple | None = None):
+    """(q, k, v) = three TEAL sparse GEMVs of one x (column-major weights [N_s, Z]) in one launch that reads x
+    once; each equals the fused decode step's projection bit for bit."""
+    ws_ = (wq, wk, wv)
+    shapes = [colmajor_rows(w) for w in ws_]
+    Z = shapes[0][1]
+    if any(z != Z for _, z in shapes):
+        raise LeanKVError("sparse_qkv: weights must share Z")
+    require_cuda(x, *ws_)
+    xf = _check_x(x, Z, "sparse_qkv")
+    if any(w.dtype != torch.float16 for w in ws_):
+        raise LeanKVError("sparse_qkv: weights must be float16")
+    Ns = [n for n, _ in shapes]
+    if out is None:
+        out = tuple(torch.empty(n, dtype=torch.float16, device=x.device) for n in Ns)
+    for o, n in zip(out, Ns):
+        if o.dtype != torch.float16 or o.numel() != n or not o.is_contiguous():
+            raise LeanKVError("sparse_qkv: outputs must be contiguous float16 with %s elements" % (Ns,))
+    lib = _lib_handle()
+    import ctypes
+
+    n_arr = (ctypes.c_int64 * 3)(*Ns)
+    nbytes = lib.lkv_sparse_gemv_multi_workspace_bytes(3, n_arr, Z)
+    ws = workspaces.get(x.device, "qkv", nbytes)
+    check(
+        lib.lkv_sparse_gemv_multi(ptr(xf), 3, (ctypes.c_void_p * 3)(*[ptr(w) for w in ws_]),
+                                  (ctypes.c_float * 3)(float(tq), float(tk), float(tv)), n_arr, Z,
+                                  (ctypes.c_void_p * 3)(*[ptr(o) for o in out]), ptr(ws), ws.numel(),
+                                  stream_handle(x.device)),
+        "lkv_sparse_gemv_multi",
+    )
+    return tuple(out)
+
+
 # ----------------------------------------------------------------- TurboQuant
 def packed_row_bytes(bits: int) -> int:
     n = _lib_handle().lkv_tq_packed_row_bytes(int(bits))
@@ -563,42 +598,120 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
 # ------------------------------------------------------- torch custom ops
 _LIB_DEF = None
 
+# Schemas of torch.ops.leankv.*: the reference's kernel contracts (sparse_gemv.py:143-181,
+# quantizer.py:119-137, rotation.py:45-52, cache.py:84-189 + sdpa_attention.py:79-105) as
+# dispatcher ops.  Every functional op has an ``.out`` overload that writes caller-owned buffers,
+# so a captured HIP graph holds no allocation; ``tq_cache_append`` mutates the cache in place.
+_SCHEMAS = (
+    "sparse_gemv(Tensor x, Tensor weight, float threshold) -> Tensor",
+    "sparse_gemv.out(Tensor x, Tensor weight, float threshold, *, Tensor(a!) out) -> Tensor(a!)",
+    "sparse_gateup_swiglu(Tensor x, Tensor w_gate, Tensor w_up, float t_gate, float t_up) -> Tensor",
+    "sparse_gateup_swiglu.out(Tensor x, Tensor w_gate, Tensor w_up, float t_gate, float t_up, *, "
+    "Tensor(a!) out) -> Tensor(a!)",
+    "sparse_qkv(Tensor x, Tensor wq, Tensor wk, Tensor wv, float tq, float tk, float tv) -> (Tensor, Tensor, Tensor)",
+    "sparse_qkv.out(Tensor x, Tensor wq, Tensor wk, Tensor wv, float tq, float tk, float tv, *, Tensor(a!) q, "
+    "Tensor(b!) k, Tensor(c!) v) -> (Tensor(a!), Tensor(b!), Tensor(c!))",
+    "tq_quantize(Tensor x, Tensor Pi, Tensor bounds, int bits) -> (Tensor, Tensor)",
+    "tq_quantize_rotated(Tensor y, Tensor bounds, int bits) -> Tensor",
+    "tq_dequantize(Tensor packed, Tensor norms, Tensor Pi, Tensor centroids, int bits, ScalarType? out_dtype=None) "
+    "-> Tensor",
+    "tq_rotate(Tensor x, Tensor Pi, bool transpose) -> Tensor",
+    "rms_norm(Tensor x, Tensor weight, float eps) -> Tensor",
+    "tq_cache_append(Tensor k_new, Tensor v_new, Tensor(a!) k_hot, Tensor(b!) v_hot, Tensor(c!) k_codes, "
+    "Tensor(d!) k_norms, Tensor(e!) v_codes, Tensor(f!) v_norms, Tensor PiK, Tensor PiV, Tensor bounds, int bits, "
+    "Tensor pos) -> ()",
+    "tq_decode_attn(Tensor q, Tensor k_codes, Tensor k_norms, Tensor v_codes, Tensor v_norms, Tensor k_hot, "
+    "Tensor v_hot, Tensor PiK, Tensor PiV, Tensor centroids, int bits, Tensor seq_len, int max_len, float scale) "
+    "-> Tensor",
+    "tq_decode_attn.out(Tensor q, Tensor k_codes, Tensor k_norms, Tensor v_codes, Tensor v_norms, Tensor k_hot, "
+    "Tensor v_hot, Tensor PiK, Tensor PiV, Tensor centroids, int bits, Tensor seq_len, int max_len, float scale, *, "
+    "Tensor(a!) out) -> Tensor(a!)",
+    "tq_prefill_attn(Tensor q, Tensor k_codes, Tensor k_norms, Tensor v_codes, Tensor v_norms, Tensor k_hot, "
+    "Tensor v_hot, Tensor PiK, Tensor PiV, Tensor centroids, int bits, int kv_len, float scale) -> Tensor",
+    "tq_prefill_attn.out(Tensor q, Tensor k_codes, Tensor k_norms, Tensor v_codes, Tensor v_norms, Tensor k_hot, "
+    "Tensor v_hot, Tensor PiK, Tensor PiV, Tensor centroids, int bits, int kv_len, float scale, *, "
+    "Tensor(a!) out) -> Tensor(a!)",
+)
+
+
+def _impls():
+    """name -> (device impl, meta impl)."""
+
+    def m_gemv(x, w, t, out=None):
+        return out if out is not None else x.new_empty(w.shape[0], dtype=torch.float16)
+
+    def m_gateup(x, wg, wu, tg, tu, out=None):
+        return out if out is not None else x.new_empty(wg.shape[0], dtype=torch.float16)
+
+    def m_qkv(x, wq, wk, wv, tq, tk, tv, q=None, k=None, v=None):
+        if q is not None:
+            return q, k, v
+        return tuple(x.new_empty(w.shape[0], dtype=torch.float16) for w in (wq, wk, wv))
+
+    def m_quant(x, Pi, b, bits):
+        rb = {1: 16, 2: 32}.get(int(bits), 64)
+        return x.new_empty(*x.shape[:-1], rb, dtype=torch.uint8), x.new_empty(x.shape[:-1])
+
+    def m_quant_rot(y, b, bits):
+        rb = {1: 16, 2: 32}.get(int(bits), 64)
+        return y.new_empty(*y.shape[:-1], rb, dtype=torch.uint8)
+
+    def m_dequant(p, n, Pi, c, bits, out_dtype=None):
+        return n.new_empty(*p.shape[:-1], HEAD_DIM, dtype=out_dtype or torch.float32)
+
+    def m_rotate(x, Pi, tr):
+        return x.new_empty(x.shape, dtype=torch.float32)
+
+    def m_rms(x, w, eps):
+        return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+    def m_append(*args):
+        return None
+
+    def m_attn(q, *args, out=None):
+        return out if out is not None else torch.empty_like(q)
+
+    return {
+        "sparse_gemv": (lambda x, w, t: sparse_gemv(x, w, t), m_gemv),
+        "sparse_gemv.out": (lambda x, w, t, out: sparse_gemv_out(x, w, t, out), m_gemv),
+        "sparse_gateup_swiglu": (lambda x, wg, wu, tg, tu: sparse_gateup_swiglu(x, wg, wu, tg, tu), m_gateup),
+        "sparse_gateup_swiglu.out": (lambda x, wg, wu, tg, tu, out: sparse_gateup_swiglu_out(x, wg, wu, tg, tu, out),
+                                     m_gateup),
+        "sparse_qkv": (lambda x, wq, wk, wv, tq, tk, tv: sparse_qkv(x, wq, wk, wv, tq, tk, tv), m_qkv),
+        "sparse_qkv.out": (lambda x, wq, wk, wv, tq, tk, tv, q, k, v: sparse_qkv(x, wq, wk, wv, tq, tk, tv,
+                                                                                out=(q, k, v)), m_qkv),
+        "tq_quantize": (lambda x, Pi, b, bits: tq_quantize(x, Pi, b, bits), m_quant),
+        "tq_quantize_rotated": (lambda y, b, bits: tq_quantize_rotated(y, b, bits), m_quant_rot),
+        "tq_dequantize": (lambda p, n, Pi, c, bits, out_dtype=None: tq_dequantize(p, n, Pi, c, bits,
+                                                                                   out_dtype or torch.float32),
+                          m_dequant),
+        "tq_rotate": (lambda x, Pi, tr: tq_rotate(x, Pi, tr), m_rotate),
+        "rms_norm": (lambda x, w, eps: rms_norm(x, w, eps), m_rms),
+        "tq_cache_append": (lambda *a: tq_cache_append(*a), m_append),
+        "tq_decode_attn": (lambda *a: tq_decode_attn(*a), m_attn),
+        "tq_decode_attn.out": (lambda *a, out: tq_decode_attn_out(*a, out), m_attn),
+        "tq_prefill_attn": (lambda *a: tq_prefill_attn(*a), m_attn),
+        "tq_prefill_attn.out": (lambda *a, out: tq_prefill_attn_out(*a, out), m_attn),
+    }
+
 
 def _register_ops() -> None:
-    """Expose the kernels as torch.ops.leankv.* (CUDA impl + Meta shape fns)."""
+    """Expose the kernels as torch.ops.leankv.* (GPU impl + Meta shape functions)."""
     global _LIB_DEF
     if _LIB_DEF is not None:
         return
     lib = torch.library.Library("leankv", "DEF")
-    lib.define("sparse_gemv(Tensor x, Tensor weight, float threshold) -> Tensor")
-    lib.define("sparse_gateup_swiglu(Tensor x, Tensor w_gate, Tensor w_up, float t_gate, float t_up) -> Tensor")
-    lib.define("tq_quantize(Tensor x, Tensor Pi, Tensor bounds, int bits) -> (Tensor, Tensor)")
-    lib.define("tq_quantize_rotated(Tensor y, Tensor bounds, int bits) -> Tensor")
-    lib.define("tq_dequantize(Tensor packed, Tensor norms, Tensor Pi, Tensor centroids, int bits) -> Tensor")
-    lib.define("tq_rotate(Tensor x, Tensor Pi, bool transpose) -> Tensor")
-    lib.define("rms_norm(Tensor x, Tensor weight, float eps) -> Tensor")
-    lib.impl("sparse_gemv", lambda x, w, t: sparse_gemv(x, w, t), "CUDA")
-    lib.impl("sparse_gateup_swiglu", lambda x, wg, wu, tg, tu: sparse_gateup_swiglu(x, wg, wu, tg, tu), "CUDA")
-    lib.impl("tq_quantize", lambda x, Pi, b, bits: tq_quantize(x, Pi, b, bits), "CUDA")
-    lib.impl("tq_quantize_rotated", lambda y, b, bits: tq_quantize_rotated(y, b, bits), "CUDA")
-    lib.impl("tq_dequantize", lambda p, n, Pi, c, bits: tq_dequantize(p, n, Pi, c, bits), "CUDA")
-    lib.impl("tq_rotate", lambda x, Pi, tr: tq_rotate(x, Pi, tr), "CUDA")
-    lib.impl("rms_norm", lambda x, w, eps: rms_norm(x, w, eps), "CUDA")
-
-    def _meta_gemv(x, w, t):
-        return x.new_empty(w.shape[0], dtype=torch.float16)
-
-    def _meta_gateup(x, wg, wu, tg, tu):
-        return x.new_empty(wg.shape[0], dtype=torch.float16)
-
-    def _meta_quant(x, Pi, b, bits):
-        rb = {1: 16, 2: 32}.get(int(bits), 64)
-        return (x.new_empty(*x.shape[:-1], rb, dtype=torch.uint8), x.new_empty(x.shape[:-1]))
-
-    lib.impl("sparse_gemv", _meta_gemv, "Meta")
-    lib.impl("sparse_gateup_swiglu", _meta_gateup, "Meta")
-    lib.impl("tq_quantize", _meta_quant, "Meta")
+    for schema in _SCHEMAS:
+        lib.define(schema)
+    for name, (dev, meta) in _impls().items():
+        lib.impl(name, dev, "CUDA")
+        lib.impl(name, meta, "Meta")
     _LIB_DEF = lib
+
+
+def op_names() -> list:
+    """Every registered torch.ops.leankv overload name ("sparse_gemv", "sparse_gemv.out", ...)."""
+    return [s.split("(", 1)[0] for s in _SCHEMAS]
 
 
 try:

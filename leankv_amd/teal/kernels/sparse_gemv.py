@@ -4,18 +4,23 @@ Drop-in for leankv/teal/kernels/sparse_gemv.py:
   sparse_gemv(x, weight, threshold, sparsity_bin)        (:143-181)
   batched_sparse_gemm(x, weight, threshold, sparsity_bin) (:184-226)
   prepare_weight_for_sparse_gemv(weight)                 (:229-234)
-plus sparse_gateup_swiglu (no reference counterpart: it fuses the gate and up
-sparse_gemv calls of a TEAL-patched Mistral MLP so x is read once).
+plus two fusions with no single reference counterpart: sparse_gateup_swiglu
+(the gate and up sparse_gemv calls of a TEAL-patched Mistral MLP and its
+SwiGLU, x read once) and sparse_qkv (the q, k and v sparse_gemv calls of an
+attention layer, x read once).
 
-sparsity_bin only keyed the Triton autotuner; the HIP kernel picks its launch
-shape from (N, Z) and the argument is accepted and ignored.
+These are the dispatcher boundary of the TEAL path: each call goes through
+torch.ops.leankv (leankv_amd.kernels registers the ops, GPU + Meta), as the
+reference's calls go through its Triton launcher.  sparsity_bin only keyed the
+Triton autotuner; the HIP kernel picks its launch shape from (N, Z) and the
+argument is accepted and ignored.
 """
 
 from __future__ import annotations
 
 import torch
 
-from ... import kernels as _k
+from ... import kernels as _k  # registers torch.ops.leankv
 
 
 def prepare_weight_for_sparse_gemv(weight: torch.Tensor) -> torch.Tensor:
@@ -29,7 +34,7 @@ def sparse_gemv(x: torch.Tensor, weight: torch.Tensor, threshold: float, sparsit
     xh = x.reshape(Z)
     if xh.dtype != torch.float16:
         xh = xh.to(torch.float16)
-    out = _k.sparse_gemv(xh, weight, threshold).reshape(1, 1, N)
+    out = torch.ops.leankv.sparse_gemv(xh, weight, float(threshold)).reshape(1, 1, N)
     if x.dtype != torch.float16:
         out = out.to(x.dtype)
     return out
@@ -52,4 +57,14 @@ def sparse_gateup_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tens
     xh = x.reshape(Z)
     if xh.dtype != torch.float16:
         xh = xh.to(torch.float16)
-    return _k.sparse_gateup_swiglu(xh, w_gate, w_up, t_gate, t_up).reshape(1, 1, N)
+    return torch.ops.leankv.sparse_gateup_swiglu(xh, w_gate, w_up, float(t_gate), float(t_up)).reshape(1, 1, N)
+
+
+def sparse_qkv(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor, tq: float, tk: float,
+               tv: float):
+    """fp16 (q, k, v) of one single-token x through three TEAL-patched projections (column-major weights)."""
+    Z = wq.shape[1]
+    xh = x.reshape(Z)
+    if xh.dtype != torch.float16:
+        xh = xh.to(torch.float16)
+    return torch.ops.leankv.sparse_qkv(xh, wq, wk, wv, float(tq), float(tk), float(tv))

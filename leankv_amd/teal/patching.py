@@ -13,7 +13,10 @@ to the HIP sparse GEMV at B=1 single-token decode and keeps the dense F.linear
 otherwise, the reference's dispatch rule (:169-180).  In addition, when both
 gate_proj and up_proj of a layer are patched, the MLP forward is patched so the
 two projections and the SwiGLU run as one fused HIP kernel reading x once
-(``fuse_mlp=False`` turns this off).
+(``fuse_mlp=False`` turns this off), and when q_proj, k_proj and v_proj are
+all patched, the three run as one launch reading x once (``fuse_qkv=False``
+turns this off): q_proj computes all three and k_proj / v_proj hand back
+their share when called on the same input tensor.
 """
 
 from __future__ import annotations
@@ -24,7 +27,7 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from .kernels.sparse_gemv import prepare_weight_for_sparse_gemv, sparse_gateup_swiglu, sparse_gemv
+from .kernels.sparse_gemv import prepare_weight_for_sparse_gemv, sparse_gateup_swiglu, sparse_gemv, sparse_qkv
 from .sparse_fns import SparsifyFn, compute_threshold_for_sparsity
 
 PROJ_NAMES = ["q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"]
@@ -57,6 +60,7 @@ def apply_teal(
     use_triton: bool = False,
     use_hip: Optional[bool] = None,
     fuse_mlp: bool = True,
+    fuse_qkv: bool = True,
 ):
     """Install TEAL on all 7 projections of every layer; returns {(layer, proj): SparsifyFn}."""
     if sum(v is not None for v in (sparsity, thresholds, thresholds_path)) != 1:
@@ -96,6 +100,8 @@ def apply_teal(
                 hooks.append(proj.register_forward_pre_hook(make_hook(sf)))
         if use_kernel and fuse_mlp:
             _maybe_patch_mlp(layer.mlp)
+        if use_kernel and fuse_qkv:
+            _maybe_patch_qkv(layer.self_attn)
 
     if not hasattr(model, "_teal_hooks"):
         model._teal_hooks = []
@@ -132,6 +138,18 @@ def _patch_linear_with_triton(linear: nn.Linear, threshold: float, sparsity: flo
     _patch_linear_with_kernel(linear, threshold)
 
 
+def _is_silu(act) -> bool:
+    """Whether the MLP activation is SiLU (torch's nn.SiLU, or transformers' own SiLU module that ACT2FN["silu"]
+    returns), judged by what it computes on a few points."""
+    if isinstance(act, nn.SiLU):
+        return True
+    try:
+        probe = torch.tensor([-3.0, -0.5, 0.0, 0.7, 4.0])
+        return bool(torch.allclose(act(probe), torch.nn.functional.silu(probe)))
+    except Exception:
+        return False
+
+
 def _maybe_patch_mlp(mlp: nn.Module) -> None:
     """Fuse gate/up + SwiGLU when both projections carry a kernel patch."""
     gate, up, down = getattr(mlp, "gate_proj", None), getattr(mlp, "up_proj", None), getattr(mlp, "down_proj", None)
@@ -142,7 +160,7 @@ def _maybe_patch_mlp(mlp: nn.Module) -> None:
     if gate.bias is not None or up.bias is not None:
         return
     act = getattr(mlp, "act_fn", None)
-    if act is None or not isinstance(act, nn.SiLU):
+    if act is None or not _is_silu(act):
         return
     original = mlp.forward
 
@@ -160,6 +178,52 @@ def _maybe_patch_mlp(mlp: nn.Module) -> None:
     mlp._teal_fused = True
 
 
+def _maybe_patch_qkv(attn: nn.Module) -> None:
+    """One launch for q/k/v when all three carry a kernel patch (no bias).
+
+    q_proj's forward runs the fused kernel on its input and keeps k and v;
+    k_proj / v_proj return them when called on the very tensor q_proj saw
+    (unchanged since: same object and version counter), which is how HF's
+    attention calls them (modeling_mistral.py:150-152); any other input takes
+    the projection's own sparse GEMV."""
+    projs = [getattr(attn, n, None) for n in ("q_proj", "k_proj", "v_proj")]
+    if any(p is None or not getattr(p, "_teal_patched", False) or p.bias is not None for p in projs):
+        return
+    q, k, v = projs
+    held: dict = {}
+
+    def q_forward(x, single=q.forward):
+        if not _is_single_token(x):
+            held.clear()
+            return single(x)
+        yq, yk, yv = sparse_qkv(x, q.weight, k.weight, v.weight, q._teal_threshold, k._teal_threshold,
+                                v._teal_threshold)
+        held.clear()
+        held.update(x=x, version=x._version, k=yk, v=yv)
+        lead = x.shape[:-1]
+        out = yq.reshape(lead + (q.weight.shape[0],))
+        return out if x.dtype == torch.float16 else out.to(x.dtype)
+
+    def share(proj, key):
+        single = proj.forward
+
+        def fwd(x):
+            if held.get("x") is x and held.get("version") == x._version and key in held:
+                y = held.pop(key)
+                if "k" not in held and "v" not in held:
+                    held.clear()
+                y = y.reshape(x.shape[:-1] + (proj.weight.shape[0],))
+                return y if x.dtype == torch.float16 else y.to(x.dtype)
+            return single(x)
+
+        return fwd
+
+    k.forward = share(k, "k")
+    v.forward = share(v, "v")
+    q.forward = q_forward
+    attn._teal_qkv_fused = True
+
+
 def remove_teal(model):
     """Remove TEAL hooks and restore patched forwards (weights stay column-major)."""
     if hasattr(model, "_teal_hooks"):
@@ -174,6 +238,8 @@ def remove_teal(model):
         return
     for layer in layers:
         mods = [_get_projection(layer, p) for p in PROJ_NAMES] + [layer.mlp]
+        if hasattr(layer.self_attn, "_teal_qkv_fused"):
+            del layer.self_attn._teal_qkv_fused
         for m in mods:
             if hasattr(m, "_teal_original_forward"):
                 m.forward = m._teal_original_forward

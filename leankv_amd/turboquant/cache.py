@@ -13,14 +13,18 @@ Storage is MI355X-shaped instead of a list of torch.cat'ed tensors:
 so a decode step writes 64 + 4 bytes per (head, K/V) instead of re-concatenating
 the whole store, and ``cap`` grows by doubling when a sequence outgrows it.
 
-update() with ``fused_attention=True`` (the default; the model must use the
-"leankv_tq" attention implementation registered by
-leankv_amd.turboquant.attention) defers attention to the packed-KV kernels:
-one new token appends with one HIP launch and runs the split-K decode kernel,
-several tokens (a prefill or a chunk) are appended with the bulk quantizer and
-run the causal prefill kernel; no dequantized K/V is formed either way.  With
-fused attention off, an update of several tokens returns the reference's full
-K/V -- cold dequantized by the HIP kernel to fp16, then hot.
+By default update() returns the reference's full K/V -- cold dequantized to
+fp16 by the HIP kernel, then hot -- so the cache works under any attention
+implementation, exactly as the reference's (cache.py:17-19 builds it and hands
+it to generate()).  ``fused_attention=True`` (what optimize_model and
+``use_on(model, cache)`` set) defers attention to the packed-KV kernels and
+requires the model to run the "leankv_tq" attention implementation
+(leankv_amd.turboquant.attention): one new token appends with one HIP launch
+and runs the split-K decode kernel, several tokens (a prefill or a chunk) are
+appended with the bulk quantizer and run the causal prefill kernel; no
+dequantized K/V is formed either way.  A deferred update that no leankv_tq
+attention call consumed makes the next update raise instead of letting another
+attention implementation read only the newest token.
 """
 
 from __future__ import annotations
@@ -30,7 +34,7 @@ import weakref
 
 import torch
 
-from .. import kernels as _k
+from .. import kernels as _k  # also registers torch.ops.leankv (the cache's kernels go through the dispatcher)
 from .codebook import get_codebook_tensors
 from .rotation import generate_rotation_matrix
 
@@ -49,20 +53,24 @@ class TurboQuantCache:
 
     def __init__(self, bits: int = 3, head_dim: int = 128, num_layers: int = 32, hot_buffer_size: int = 64,
                  device=None, dtype: torch.dtype = torch.float16, seed: int = 42, max_seq_len: int = 4096,
-                 fused_attention: bool = True):
+                 fused_attention: bool = False):
         if head_dim != _k.HEAD_DIM:
-            raise ValueError("TurboQuantCache: head_dim must be %d for the HIP kernels" % _k.HEAD_DIM)
+            raise ValueError("TurboQuantCache: head_dim=%d is not built (the HIP kernels take head_dim %d)"
+                             % (head_dim, _k.HEAD_DIM))
         if bits not in (1, 2, 3, 4):
             raise ValueError("TurboQuantCache: bits must be 1..4")
-        if fused_attention and bits not in (3, 4):
-            fused_attention = False  # the fused kernel reads 4-bit nibble rows
-        if not 1 <= hot_buffer_size <= 64:
-            raise ValueError("TurboQuantCache: hot_buffer_size must be 1..64 (one ring per wave)")
+        if hot_buffer_size < 1:
+            raise ValueError("TurboQuantCache: hot_buffer_size must be at least 1")
         self.bits, self.head_dim, self.num_layers = bits, head_dim, num_layers
         self.hot_buffer_size = hot_buffer_size
         self._device = torch.device(device) if device is not None else torch.device("cuda")
         self._dtype = dtype
-        self.fused_attention = fused_attention
+        self.fused_attention = bool(fused_attention)
+        # the packed-KV attention kernels read 4-bit nibble rows (bits 3, 4); the
+        # decode kernel keeps the fp16 window in one wave (at most 64 tokens):
+        # other caches attend to the dequantized K/V with SDPA
+        self.fused_prefill = bits in (3, 4)
+        self.fused_decode = bits in (3, 4) and hot_buffer_size <= 64
         self._seen_tokens = 0
         self._seq_lengths = [0] * num_layers
         self._init_cap = max(int(max_seq_len), 1)
@@ -122,6 +130,12 @@ class TurboQuantCache:
     # ----------------------------------------------------------- update
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int, cache_kwargs=None):
         global _ACTIVE
+        if self._fused_pending[layer_idx] or self._prefill_pending[layer_idx]:
+            raise RuntimeError(
+                "TurboQuantCache(fused_attention=True): layer %d's previous update was never attended by the "
+                "'leankv_tq' attention implementation, so the model attended to the newest tokens only; call "
+                "leankv_amd.turboquant.attention.use_on(model, cache) or build the cache with "
+                "fused_attention=False" % layer_idx)
         _ACTIVE = weakref.ref(self)
         B, H, S, D = key_states.shape
         if layer_idx == 0:
@@ -135,25 +149,23 @@ class TurboQuantCache:
         self._ensure_cap(layer_idx, self._cold_len(T))
         if S == 1:
             self._pos_dev[layer_idx].fill_(p0)
-            _k.tq_cache_append(k16.reshape(B, H, D).contiguous(), v16.reshape(B, H, D).contiguous(),
-                               self._k_hot[layer_idx], self._v_hot[layer_idx], self._k_codes[layer_idx],
-                               self._k_norms[layer_idx], self._v_codes[layer_idx], self._v_norms[layer_idx],
-                               self.PiK[layer_idx], self.PiV[layer_idx], self.decision_boundaries, self.bits,
-                               self._pos_dev[layer_idx])
+            torch.ops.leankv.tq_cache_append(
+                k16.reshape(B, H, D).contiguous(), v16.reshape(B, H, D).contiguous(), self._k_hot[layer_idx],
+                self._v_hot[layer_idx], self._k_codes[layer_idx], self._k_norms[layer_idx], self._v_codes[layer_idx],
+                self._v_norms[layer_idx], self.PiK[layer_idx], self.PiV[layer_idx], self.decision_boundaries,
+                self.bits, self._pos_dev[layer_idx])
         else:
             self._bulk_update(layer_idx, k16, v16, p0)
         self._seq_lengths[layer_idx] = T
-        if self.fused_attention and S == 1:
+        if self.fused_attention and S == 1 and self.fused_decode:
             self._len_dev[layer_idx].fill_(T)
             self._fused_pending[layer_idx] = True
             self._pending_len[layer_idx] = T
             return key_states, value_states
-        self._fused_pending[layer_idx] = False
-        if self.fused_attention and S > 1:
+        if self.fused_attention and S > 1 and self.fused_prefill:
             self._prefill_pending[layer_idx] = True
             self._pending_len[layer_idx] = T
             return key_states, value_states
-        self._prefill_pending[layer_idx] = False
         return self._get_full_cache(layer_idx)
 
     def _bulk_update(self, li: int, k16: torch.Tensor, v16: torch.Tensor, p0: int) -> None:
@@ -174,8 +186,10 @@ class TurboQuantCache:
                 nk, nv = k16[:, :, : c1 - p0], v16[:, :, : c1 - p0]
                 fk = nk if fk is None else torch.cat([fk, nk], dim=2)
                 fv = nv if fv is None else torch.cat([fv, nv], dim=2)
-            pk, nk_ = _k.tq_quantize(fk.float().contiguous(), self.PiK[li], self.decision_boundaries, self.bits)
-            pv, nv_ = _k.tq_quantize(fv.float().contiguous(), self.PiV[li], self.decision_boundaries, self.bits)
+            pk, nk_ = torch.ops.leankv.tq_quantize(fk.float().contiguous(), self.PiK[li], self.decision_boundaries,
+                                                   self.bits)
+            pv, nv_ = torch.ops.leankv.tq_quantize(fv.float().contiguous(), self.PiV[li], self.decision_boundaries,
+                                                   self.bits)
             self._k_codes[li][:, :, c0:c1] = pk
             self._v_codes[li][:, :, c0:c1] = pv
             self._k_norms[li][:, :, c0:c1] = nk_
@@ -195,10 +209,10 @@ class TurboQuantCache:
         hv = self._v_hot[layer_idx].index_select(2, idx)
         if c == 0:
             return hk.to(self._dtype), hv.to(self._dtype)
-        ck = _k.tq_dequantize(self._k_codes[layer_idx][:, :, :c], self._k_norms[layer_idx][:, :, :c],
-                              self.PiK[layer_idx], self.centroids, self.bits, out_dtype=torch.float16)
-        cv = _k.tq_dequantize(self._v_codes[layer_idx][:, :, :c], self._v_norms[layer_idx][:, :, :c],
-                              self.PiV[layer_idx], self.centroids, self.bits, out_dtype=torch.float16)
+        ck = torch.ops.leankv.tq_dequantize(self._k_codes[layer_idx][:, :, :c], self._k_norms[layer_idx][:, :, :c],
+                                            self.PiK[layer_idx], self.centroids, self.bits, torch.float16)
+        cv = torch.ops.leankv.tq_dequantize(self._v_codes[layer_idx][:, :, :c], self._v_norms[layer_idx][:, :, :c],
+                                            self.PiV[layer_idx], self.centroids, self.bits, torch.float16)
         return (torch.cat([ck, hk], dim=2).to(self._dtype), torch.cat([cv, hv], dim=2).to(self._dtype))
 
     # ----------------------------------------------------------- fused decode attention
@@ -211,10 +225,10 @@ class TurboQuantCache:
         q = query.reshape(B, Hq, D).to(torch.float16).contiguous()
         L = self._pending_len[layer_idx]
         scale = float(scaling) if scaling is not None else 1.0 / math.sqrt(D)
-        out = _k.tq_decode_attn(q, self._k_codes[layer_idx], self._k_norms[layer_idx], self._v_codes[layer_idx],
-                                self._v_norms[layer_idx], self._k_hot[layer_idx], self._v_hot[layer_idx],
-                                self.PiK[layer_idx], self.PiV[layer_idx], self.centroids, self.bits,
-                                self._len_dev[layer_idx], L, scale)
+        out = torch.ops.leankv.tq_decode_attn(
+            q, self._k_codes[layer_idx], self._k_norms[layer_idx], self._v_codes[layer_idx], self._v_norms[layer_idx],
+            self._k_hot[layer_idx], self._v_hot[layer_idx], self.PiK[layer_idx], self.PiV[layer_idx], self.centroids,
+            self.bits, self._len_dev[layer_idx], L, scale)
         return out.reshape(B, Hq, 1, D)
 
     def prefill_attention(self, layer_idx: int, query: torch.Tensor, scaling: float | None = None) -> torch.Tensor:
@@ -229,13 +243,16 @@ class TurboQuantCache:
         q = query.to(torch.float16).contiguous()
         L = self._pending_len[layer_idx]
         scale = float(scaling) if scaling is not None else 1.0 / math.sqrt(D)
-        return _k.tq_prefill_attn(q, self._k_codes[layer_idx], self._k_norms[layer_idx], self._v_codes[layer_idx],
-                                  self._v_norms[layer_idx], self._k_hot[layer_idx], self._v_hot[layer_idx],
-                                  self.PiK[layer_idx], self.PiV[layer_idx], self.centroids, self.bits, L, scale)
+        return torch.ops.leankv.tq_prefill_attn(
+            q, self._k_codes[layer_idx], self._k_norms[layer_idx], self._v_codes[layer_idx], self._v_norms[layer_idx],
+            self._k_hot[layer_idx], self._v_hot[layer_idx], self.PiK[layer_idx], self.PiV[layer_idx], self.centroids,
+            self.bits, L, scale)
 
     def take_full_cache(self, layer_idx: int):
-        """The reference's K/V for a pending several-token update (the attention runs elsewhere)."""
+        """The reference's K/V (cold dequantized to fp16, then hot) for a pending update whose attention
+        runs elsewhere (a padding mask, a sliding window shorter than the cache)."""
         self._prefill_pending[layer_idx] = False
+        self._fused_pending[layer_idx] = False
         return self._get_full_cache(layer_idx)
 
     # ----------------------------------------------------------- HF interface
@@ -247,7 +264,8 @@ class TurboQuantCache:
         return self.get_seq_length(layer_idx) + q, 0
 
     def get_query_offset(self, layer_idx: int = 0) -> int:
-        return 0
+        """Position of the first query of the next forward (transformers' Cache contract: the cached length)."""
+        return self.get_seq_length(layer_idx)
 
     def get_max_cache_shape(self, *args, **kwargs):
         return None

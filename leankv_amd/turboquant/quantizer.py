@@ -23,7 +23,7 @@ from typing import NamedTuple
 import torch
 import torch.nn.functional as F
 
-from .. import kernels as _k
+from .. import kernels as _k  # registers torch.ops.leankv
 from .codebook import get_codebook_tensors
 from .rotation import generate_qjl_matrix, generate_rotation_matrix
 
@@ -94,11 +94,11 @@ class TurboQuantMSE(torch.nn.Module):
         self.register_buffer("decision_boundaries", b[1:-1].contiguous())
 
     def quantize(self, x: torch.Tensor) -> MSEQuantized:
-        packed, norms = _k.tq_quantize(x, self.Pi, self.decision_boundaries, self.bits)
+        packed, norms = torch.ops.leankv.tq_quantize(x, self.Pi, self.decision_boundaries, self.bits)
         return MSEQuantized(indices=packed, norms=norms, bits=self.bits)
 
     def dequantize(self, q: MSEQuantized) -> torch.Tensor:
-        return _k.tq_dequantize(q.indices, q.norms, self.Pi, self.centroids, q.bits, out_dtype=torch.float32)
+        return torch.ops.leankv.tq_dequantize(q.indices, q.norms, self.Pi, self.centroids, q.bits, torch.float32)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self.dequantize(self.quantize(x))

@@ -34,6 +34,7 @@ class RefModel:
                  acc_dtype: torch.dtype = torch.float64):
         """acc_dtype: accumulation dtype of the projections (fp64 = truth; fp32 = timing baseline)."""
         self.acc = acc_dtype
+        self._acc_w = {}
         self.cfg = cfg
         self.sd = {k: v.detach().to("cpu", torch.float32) for k, v in state.items()}
         self.th = thresholds or {}
@@ -54,13 +55,21 @@ class RefModel:
     def _w(self, name):
         return self.sd[name]
 
+    def _wacc(self, name):
+        """Weight in the accumulation dtype, converted once (a full-width fp64 step would otherwise
+        re-convert ~1 GB of weights)."""
+        w = self._acc_w.get(name)
+        if w is None:
+            w = self._acc_w[name] = self._w(name).to(self.acc).T.contiguous()
+        return w
+
     def _lin(self, x, layer, proj, mod):
         """x fp32 (fp16 values) [S, Z] -> fp16-rounded y [S, N]; TEAL mask only at single-token decode."""
-        W = self._w("model.layers.%d.%s.%s.weight" % (layer, mod, proj))
+        Wt = self._wacc("model.layers.%d.%s.%s.weight" % (layer, mod, proj))
         t = self.th.get(layer, {}).get(proj, 0.0)
         if t > 0 and x.shape[0] == 1:
             x = torch.where(x.abs() > torch.tensor(t, dtype=torch.float32), x, torch.zeros_like(x))
-        return f16(x.to(self.acc).matmul(W.to(self.acc).T).float())
+        return f16(x.to(self.acc).matmul(Wt).float())
 
     def _rms(self, x, w):
         var = x.pow(2).mean(-1, keepdim=True)
@@ -113,7 +122,7 @@ class RefModel:
         t2 = time.perf_counter()
         x = self._rms(x, self._w("model.norm.weight"))
         self.pos += S
-        out = x[-1:].to(self.acc).matmul(self._w("lm_head.weight").to(self.acc).T).float()[0]
+        out = x[-1:].to(self.acc).matmul(self._wacc("lm_head.weight")).float()[0]
         t3 = time.perf_counter()
         self.t_layers += t2 - t1
         self.t_head += (t1 - t0) + (t3 - t2)

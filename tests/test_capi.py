@@ -159,13 +159,36 @@ def test_decode_struct_layout_matches_header():
     from leankv_amd import _lib
 
     src = open(HEADER).read()
-    for cls, cname in ((_lib.DecodeDims, "lkv_decode_dims"), (_lib.DecodeLayer, "lkv_decode_layer")):
+    for cls, cname in ((_lib.DecodeDims, "lkv_decode_dims"), (_lib.DecodeLayer, "lkv_decode_layer"),
+                       (_lib.DecodeLayout, "lkv_decode_layout")):
         body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (cname, cname), src, flags=re.S).group(1)
         body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
         names = re.findall(r"(\w+)\s*(?=[,;])", body)
         assert [f[0] for f in cls._fields_] == names, cname
     assert ctypes.sizeof(_lib.DecodeDims) == 8 * 8 + 4 * 3 + 4 + 8 * 4  # 4 bytes of padding before bounds
     assert ctypes.sizeof(_lib.DecodeLayer) == 9 * 8 + 7 * 4 + 4 + 8 * 8
+    assert ctypes.sizeof(_lib.DecodeLayout) == 11 * 8 + 5 * 4 + 4  # padded to 8-byte alignment
+
+
+def test_decode_workspace_layout():
+    """The layout query: regions in step order, inside the workspace, sized by their chunk counts."""
+    from leankv_amd import _lib
+
+    lib = _lib.load()
+    d = _mistral_dims()
+    lay = _lib.DecodeLayout()
+    assert lib.lkv_decode_workspace_layout(ctypes.byref(d), ctypes.byref(lay)) == 0
+    assert lay.total == lib.lkv_decode_workspace_bytes(ctypes.byref(d))
+    slabs = lambda n: (n + 255) // 256  # noqa: E731
+    assert lay.part_k - lay.part_q == slabs(4096) * lay.chunks_qkv * 256 * 4
+    assert lay.part_v - lay.part_k == slabs(1024) * lay.chunks_qkv * 256 * 4
+    assert lay.part_up - lay.part_gate == slabs(14336) * lay.chunks_gateup * 256 * 4
+    assert lay.chunks_qkv * 256 >= 4096 and lay.chunks_down > 1
+    offs = [lay.part_q, lay.part_k, lay.part_v, lay.part_o, lay.part_gate, lay.part_up, lay.part_down, lay.part_lm,
+            lay.q_rope, lay.attn_out]
+    assert offs == sorted(offs) and offs[-1] + 4096 * 2 <= lay.total
+    assert lib.lkv_decode_workspace_layout(ctypes.byref(_mistral_dims(bits=2)), ctypes.byref(lay)) == -1
+    assert lib.lkv_decode_workspace_layout(ctypes.byref(d), None) == -1
 
 
 def test_decode_dims_validated_without_launch():

@@ -1,0 +1,46 @@
+"""Host-side checks of the engine helpers (CPU only)."""
+
+import math
+
+import torch
+
+TINY = dict(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2, num_attention_heads=4,
+            num_key_value_heads=2, head_dim=128, max_position_embeddings=8192)
+
+
+def test_random_mistral_keeps_fp32_rope_frequencies():
+    """fp16 parameters, fp32 rotary inverse frequencies (as from_pretrained(torch_dtype=float16) builds them):
+    the fp16 RoPE table at a long-context position equals the fp32 closed form rounded once to fp16."""
+    from leankv_amd.engine import MISTRAL_7B, random_mistral
+
+    m = random_mistral(device="cpu", seed=0, **TINY)
+    assert m.model.layers[0].self_attn.q_proj.weight.dtype == torch.float16
+    assert m.model.rotary_emb.inv_freq.dtype == torch.float32
+    assert m.config.sliding_window is None and MISTRAL_7B["sliding_window"] is None  # Mistral-7B-v0.3
+    pos = torch.tensor([[4000]])
+    cos, sin = m.model.rotary_emb(torch.zeros(1, 1, 128, dtype=torch.float16), pos)
+    inv = [1.0 / (1e6 ** (2 * i / 128)) for i in range(64)]
+    want = torch.tensor([math.cos(4000 * f) for f in inv] * 2).half()
+    assert (cos[0, 0].float() - want.float()).abs().max() <= 2 ** -10  # one fp16 rounding (+ fp32 angle error)
+    assert torch.get_default_dtype() == torch.float32
+
+
+def test_apply_teal_installs_the_fused_qkv_and_mlp_patches():
+    """With every projection patched, apply_teal fuses q|k|v and gate|up + SwiGLU (transformers' own SiLU module
+    counts as SiLU); a zero threshold keeps that projection dense and its group unfused; remove_teal undoes it."""
+    from leankv_amd.engine import random_mistral
+    from leankv_amd.teal.patching import PROJ_NAMES, apply_teal, remove_teal
+
+    m = random_mistral(device="cpu", seed=1, **TINY)
+    th = {li: {p: 0.1 for p in PROJ_NAMES} for li in range(2)}
+    th[1]["k_proj"] = 0.0
+    th[1]["up_proj"] = 0.0
+    apply_teal(m, thresholds=th, use_triton=True)
+    l0, l1 = m.model.layers
+    assert l0.self_attn._teal_qkv_fused and l0.mlp._teal_fused
+    assert not hasattr(l1.self_attn, "_teal_qkv_fused") and not hasattr(l1.mlp, "_teal_fused")
+    assert l0.self_attn.q_proj.weight.t().is_contiguous()  # column-major relayout of patched projections
+    remove_teal(m)
+    assert not hasattr(l0.self_attn, "_teal_qkv_fused") and not hasattr(l0.mlp, "_teal_fused")
+    assert l0.self_attn.k_proj.forward.__func__ is torch.nn.Linear.forward
+    assert l0.mlp.forward.__func__ is type(l0.mlp).forward

@@ -46,8 +46,8 @@ def _apply(model, th, max_len=MAXLEN):
     if th is not None:
         apply_teal(model, thresholds=th, use_triton=True)
     cache = TurboQuantCache(bits=3, head_dim=128, num_layers=model.config.num_hidden_layers, device=model.device,
-                            max_seq_len=max_len)
-    use_on(model)
+                            max_seq_len=max_len, fused_attention=True)
+    use_on(model, cache)
     return cache
 
 
@@ -206,7 +206,7 @@ def _apply_cache_only(model, max_len=MAXLEN):
     from leankv_amd.turboquant.cache import TurboQuantCache
 
     return TurboQuantCache(bits=3, head_dim=128, num_layers=model.config.num_hidden_layers, device=model.device,
-                           max_seq_len=max_len)
+                           max_seq_len=max_len, fused_attention=True)
 
 
 def test_engine_graph_replays_equal_eager(cuda):
@@ -268,3 +268,62 @@ def test_dense_engine_matches_hf(cuda):
             errs.append(float((eng.logits.float() - hf).norm() / hf.norm()))
             tok = eng.tok.clone()
     assert max(errs) < 1e-2, errs
+
+
+def test_engine_refuses_steps_past_max_len(cuda):
+    """The engine tracks the position on the host: a step at max_len raises instead of overwriting the last
+    RoPE row and ring slot (the device position is clamped there)."""
+    from leankv_amd._lib import LeanKVError
+    from leankv_amd.engine import LeanKVEngine
+
+    model, _, prompt, _ = _setup(cuda, seed=6)
+    cache = _apply(model, None)
+    with torch.no_grad():
+        out = model(prompt.view(1, -1).to(cuda), past_key_values=cache, use_cache=True)
+    eng = LeanKVEngine(model, cache, PROMPT + 2)
+    with pytest.raises(LeanKVError):
+        eng.step()  # not started
+    with pytest.raises(LeanKVError):
+        eng.start(torch.argmax(out.logits[0, -1]), PROMPT + 2)
+    eng.start(torch.argmax(out.logits[0, -1]), PROMPT)
+    with pytest.raises(LeanKVError):
+        eng.generate(3)
+    assert len(eng.generate(2)) == 2
+    with pytest.raises(LeanKVError):
+        eng.step()
+    assert int(eng.pos64) == PROMPT + 2
+
+
+def test_own_dense_engine_matches_hf_and_oracle(cuda):
+    """The dense baseline on this library's kernels (every threshold 0, fp16 paged KV) vs HF's own fp16
+    forward with a DynamicCache and vs the CPU oracle without compression, teacher-forced logits."""
+    from transformers import DynamicCache
+
+    from leankv_amd.engine import OwnDenseEngine, random_mistral
+
+    model = random_mistral(device=cuda, seed=9, **TINY)
+    state = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    ref = RefModel(state, model.config, None, hot=1 << 20)
+    g = torch.Generator().manual_seed(10)
+    prompt = torch.randint(0, TINY["vocab_size"], (1, PROMPT - 3), generator=g)  # not a whole number of pages
+    with torch.no_grad():
+        cache = DynamicCache(config=model.config)
+        out = model(prompt.to(cuda), past_key_values=cache, use_cache=True)
+        ref.forward(prompt[0])
+        first = torch.argmax(out.logits[0, -1])
+        eng = OwnDenseEngine(model, MAXLEN)
+        n = eng.load_cache(cache)
+        eng.start(first, n)
+        errs_hf, errs_ref = [], []
+        for i in range(STEPS):
+            if i == 1:
+                eng.capture()
+            fed = eng.tok.clone()
+            eng.step()
+            hf = model(fed.view(1, 1), past_key_values=cache, use_cache=True).logits[0, -1].float()
+            errs_hf.append(float((eng.logits.float() - hf).norm() / hf.norm()))
+            errs_ref.append(ot.rel_err(eng.logits.float().cpu().numpy(), ref.forward(fed.cpu()).numpy()))
+    print("own dense engine: vs HF max %.2e, vs oracle max %.2e" % (max(errs_hf), max(errs_ref)))
+    assert max(errs_hf) < 1e-2, errs_hf
+    assert max(errs_ref) < RTOL, errs_ref
+    assert int(eng.pos64) == n + STEPS

@@ -1,0 +1,239 @@
+"""The reference's user path on the GPU: HF ``model.generate(..., past_key_values=cache)`` on a model optimized
+by ``optimize_model`` (leankv/combined.py:57-126, scripts/benchmark.py:68-99), and the TurboQuantCache
+contract around it.
+
+A small random-init Mistral (head_dim 128, GQA) is used; every step's scores are compared with the CPU
+oracle decoder (oracle.model.RefModel, the reference's semantics) fed the tokens generate chose, or with the
+same model on a cache that returns the reference's full K/V (fused_attention=False) to plain SDPA.
+"""
+
+import pytest
+import torch
+
+from oracle import teal as ot
+from oracle.model import RefModel
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2, num_attention_heads=4,
+            num_key_value_heads=2, head_dim=128, max_position_embeddings=1024)
+RTOL = 2e-2
+
+
+def _model(cuda, seed, **kw):
+    from leankv_amd.engine import random_mistral
+
+    cfg = dict(TINY)
+    cfg.update(kw)
+    return random_mistral(device=cuda, seed=seed, **cfg)
+
+
+def _state(model):
+    return {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+
+
+def _ids(n, seed, B=1):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, TINY["vocab_size"], (B, n), generator=g)
+
+
+def _ref_scores(ref, prompt, new_tokens):
+    """Teacher-forced oracle logits for each generated position."""
+    out = [ref.forward(prompt)]
+    for t in new_tokens[:-1]:
+        out.append(ref.forward(torch.tensor([int(t)])))
+    return out
+
+
+def _generate(model, ids, cache, n, attention_mask=None):
+    """Greedy generate of exactly n tokens (no eos stop) with an explicit attention mask (all ones unless
+    given): random prompt ids may hold the pad id, which generate would otherwise read as padding."""
+    model.generation_config.eos_token_id = None
+    if attention_mask is None:
+        attention_mask = torch.ones_like(ids)
+    with torch.no_grad():
+        return model.generate(ids, attention_mask=attention_mask, max_new_tokens=n, past_key_values=cache,
+                              do_sample=False, output_scores=True, return_dict_in_generate=True, pad_token_id=0)
+
+
+def test_generate_optimize_model_matches_reference(cuda):
+    """optimize_model(turboquant_bits=3) + generate: every step's scores vs the oracle decoder (TurboQuant cache
+    semantics, cache.py:84-189), the prompt longer than the fp16 window, so prefill, flushes and decode all run
+    on the packed kernels."""
+    from leankv_amd.combined import optimize_model
+
+    model = _model(cuda, 21)
+    state = _state(model)
+    model, cache = optimize_model(model, turboquant_bits=3, max_seq_len=256)
+    assert cache.fused_attention and model.config._attn_implementation == "leankv_tq"
+    prompt = _ids(100, 23)
+    res = _generate(model, prompt.to(cuda), cache, 24)
+    new = res.sequences[0, 100:].cpu()
+    assert len(new) == 24 and cache.get_seq_length(0) == 100 + 23
+    ref = RefModel(state, model.config, None)
+    errs = [ot.rel_err(s[0].float().cpu().numpy(), r.numpy()) for s, r in zip(res.scores, _ref_scores(
+        ref, prompt[0], new))]
+    print("generate vs oracle: max step rel err %.2e" % max(errs))
+    assert max(errs) < RTOL
+
+
+def test_generate_with_teal_runs_the_validated_forward(cuda):
+    """optimize_model(teal_thresholds_path=..., turboquant_bits=3) + generate: each step's scores equal, bit for
+    bit, a teacher-forced forward of the same model on a fresh cache -- generate adds nothing to the forward path
+    whose fused q|k|v, fused gate/up and single projections are checked against the oracle one by one
+    (test_gpu_engine.py, test_gpu_config5.py).  Model-level TEAL logits are not compared with the oracle: an
+    activation within an ulp of its threshold flips a mask bit under any other rounding of the RMSNorm."""
+    import json
+    import tempfile
+
+    from leankv_amd.combined import optimize_model
+    from leankv_amd.teal.calibrate import calibrate_thresholds, uniform_random_sparsity
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    model = _model(cuda, 40)
+    th = calibrate_thresholds(model, [_ids(64, 41)], uniform_random_sparsity(0.3, 0.5, 40))
+    with tempfile.NamedTemporaryFile("w", suffix=".json", delete=False) as f:
+        json.dump({str(k): v for k, v in th.items()}, f)
+    model, cache = optimize_model(model, teal_thresholds_path=f.name, turboquant_bits=3, max_seq_len=256)
+    assert all(getattr(layer.self_attn, "_teal_qkv_fused", False) and getattr(layer.mlp, "_teal_fused", False)
+               for layer in model.model.layers)
+    prompt = _ids(100, 42)
+    res = _generate(model, prompt.to(cuda), cache, 16)
+    new = res.sequences[0, 100:]
+    c2 = TurboQuantCache(bits=3, head_dim=128, num_layers=2, device=cuda, max_seq_len=256, fused_attention=True)
+    with torch.no_grad():
+        lg = model(prompt.view(1, -1).to(cuda), past_key_values=c2, use_cache=True).logits[0, -1]
+        assert torch.equal(lg.float(), res.scores[0][0])
+        for i in range(15):
+            lg = model(new[i:i + 1].view(1, 1), past_key_values=c2, use_cache=True).logits[0, -1]
+            assert torch.equal(lg.float(), res.scores[i + 1][0]), i
+
+
+def test_cache_without_use_on_returns_reference_kv(cuda):
+    """A TurboQuantCache built directly (cache.py:17-19 usage) under plain SDPA: the cache hands back the
+    reference's full K/V, so generate matches the oracle with no leankv_tq attention involved."""
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    model = _model(cuda, 24)
+    state = _state(model)
+    cache = TurboQuantCache(bits=3, head_dim=128, num_layers=2, device=cuda, max_seq_len=256)
+    assert not cache.fused_attention
+    prompt = _ids(90, 25)
+    res = _generate(model, prompt.to(cuda), cache, 16)
+    new = res.sequences[0, 90:].cpu()
+    ref = RefModel(state, model.config, None)
+    errs = [ot.rel_err(s[0].float().cpu().numpy(), r.numpy()) for s, r in zip(res.scores, _ref_scores(
+        ref, prompt[0], new))]
+    assert max(errs) < RTOL, errs
+
+
+def test_fused_cache_without_leankv_attention_raises(cuda):
+    """fused_attention=True but the model still runs SDPA: the next update raises instead of letting SDPA see
+    only the newest tokens again."""
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    model = _model(cuda, 26)
+    cache = TurboQuantCache(bits=3, head_dim=128, num_layers=2, device=cuda, max_seq_len=256, fused_attention=True)
+    with torch.no_grad():
+        model(_ids(20, 27).to(cuda), past_key_values=cache, use_cache=True)
+        with pytest.raises(RuntimeError, match="leankv_tq"):
+            model(_ids(1, 28).to(cuda), past_key_values=cache, use_cache=True)
+
+
+def _pair(cuda, seed, **kw):
+    """The same random model twice: one on the packed-KV attention (fused cache), one on SDPA over the
+    reference's K/V (fused_attention=False)."""
+    from leankv_amd.turboquant.attention import use_on
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    a, b = _model(cuda, seed, **kw), _model(cuda, seed, **kw)
+    ca = TurboQuantCache(bits=3, head_dim=128, num_layers=2, device=cuda, max_seq_len=256)
+    use_on(a, ca)
+    cb = TurboQuantCache(bits=3, head_dim=128, num_layers=2, device=cuda, max_seq_len=256)
+    return a, ca, b, cb
+
+
+def test_left_padded_batch_matches_reference_kv(cuda):
+    """B=2 prompts of different lengths, left-padded (scripts/benchmark.py:45 tokenizes with padding=True): the
+    padding mask reaches the leankv_tq attention, which then runs SDPA with it on the reference's K/V, so
+    scores equal the plain-SDPA run exactly, and the padded row equals its own unpadded B=1 run."""
+    a, ca, b, cb = _pair(cuda, 29)
+    ids = _ids(80, 30, B=2)
+    mask = torch.ones(2, 80, dtype=torch.long)
+    ids[1, :13] = 0
+    mask[1, :13] = 0
+    ra = _generate(a, ids.to(cuda), ca, 12, attention_mask=mask.to(cuda))
+    rb = _generate(b, ids.to(cuda), cb, 12, attention_mask=mask.to(cuda))
+    assert torch.equal(ra.sequences, rb.sequences)
+    for sa, sb in zip(ra.scores, rb.scores):
+        assert torch.equal(sa, sb)
+    # the padded row attends to its 67 real tokens only: its prefill scores equal that prompt alone
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    c1 = TurboQuantCache(bits=3, head_dim=128, num_layers=2, device=cuda, max_seq_len=256)
+    r1 = _generate(b, ids[1:, 13:].to(cuda), c1, 1)
+    err = ot.rel_err(ra.scores[0][1].float().cpu().numpy(), r1.scores[0][0].float().cpu().numpy())
+    assert err < RTOL, err
+
+
+def test_unpadded_batch_two_fused_decode(cuda):
+    """B=2 without padding: the packed kernels run (no mask) and agree with SDPA on the reference's K/V."""
+    a, ca, b, cb = _pair(cuda, 31)
+    ids = _ids(96, 32, B=2)
+    ra = _generate(a, ids.to(cuda), ca, 10)
+    tokens_a = ra.sequences[:, 96:]
+    # teacher force b on a's tokens so a near-tie argmax cannot make the runs diverge
+    with torch.no_grad():
+        lg = b(ids.to(cuda), past_key_values=cb, use_cache=True).logits[:, -1]
+        errs = [ot.rel_err(ra.scores[0].float().cpu().numpy(), lg.float().cpu().numpy())]
+        for i in range(9):
+            lg = b(tokens_a[:, i:i + 1], past_key_values=cb, use_cache=True).logits[:, -1]
+            errs.append(ot.rel_err(ra.scores[i + 1].float().cpu().numpy(), lg.float().cpu().numpy()))
+    assert max(errs) < RTOL, errs
+    assert ca._fused_pending == [False, False]
+
+
+def test_chunked_prefill_after_cached_tokens(cuda):
+    """A second multi-token chunk on a non-empty cache: queries sit at positions past the cached tokens
+    (get_query_offset = cached length); the packed prefill kernel's causal offset equals SDPA's explicit mask."""
+    a, ca, b, cb = _pair(cuda, 33)
+    p1, p2 = _ids(70, 34), _ids(30, 35)
+    with torch.no_grad():
+        for m, c in ((a, ca), (b, cb)):
+            m(p1.to(cuda), past_key_values=c, use_cache=True)
+        la = a(p2.to(cuda), past_key_values=ca, use_cache=True).logits[0]
+        lb = b(p2.to(cuda), past_key_values=cb, use_cache=True).logits[0]
+    assert ca.get_query_offset(0) == 100
+    assert ot.rel_err(la.float().cpu().numpy(), lb.float().cpu().numpy()) < RTOL
+
+
+def test_sliding_window_shorter_than_cache_uses_masked_sdpa(cuda):
+    """A model with a sliding window shorter than the cache: the window mask reaches the leankv_tq attention
+    and the call runs SDPA with it on the reference's K/V (same scores as the plain-SDPA run)."""
+    a, ca, b, cb = _pair(cuda, 36, sliding_window=48)
+    ids = _ids(80, 37)
+    ra = _generate(a, ids.to(cuda), ca, 8)
+    rb = _generate(b, ids.to(cuda), cb, 8)
+    assert torch.equal(ra.sequences, rb.sequences)
+    for sa, sb in zip(ra.scores, rb.scores):
+        assert torch.equal(sa, sb)
+
+
+def test_hot_window_above_64(cuda):
+    """hot_buffer_size=128 (the reference accepts any size, cache.py:35-44): prefill on the packed kernel,
+    decode on SDPA over the reference's K/V; scores vs the oracle with a 128-token window."""
+    from leankv_amd.turboquant.attention import use_on
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    model = _model(cuda, 38)
+    state = _state(model)
+    cache = TurboQuantCache(bits=3, head_dim=128, num_layers=2, hot_buffer_size=128, device=cuda, max_seq_len=512)
+    use_on(model, cache)
+    assert cache.fused_prefill and not cache.fused_decode
+    prompt = _ids(200, 39)
+    res = _generate(model, prompt.to(cuda), cache, 12)
+    new = res.sequences[0, 200:].cpu()
+    ref = RefModel(state, model.config, None, hot=128)
+    errs = [ot.rel_err(s[0].float().cpu().numpy(), r.numpy()) for s, r in zip(res.scores, _ref_scores(
+        ref, prompt[0], new))]
+    assert max(errs) < RTOL, errs
