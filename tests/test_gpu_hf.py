@@ -102,7 +102,8 @@ def test_generate_with_teal_runs_the_validated_forward(cuda):
     new = res.sequences[0, 100:]
     c2 = TurboQuantCache(bits=3, head_dim=128, num_layers=2, device=cuda, max_seq_len=256, fused_attention=True)
     with torch.no_grad():
-        lg = model(prompt.view(1, -1).to(cuda), past_key_values=c2, use_cache=True).logits[0, -1]
+        # generate's prefill computes the last position's logits only (logits_to_keep=1): the same lm_head shape
+        lg = model(prompt.view(1, -1).to(cuda), past_key_values=c2, use_cache=True, logits_to_keep=1).logits[0, -1]
         assert torch.equal(lg.float(), res.scores[0][0])
         for i in range(15):
             lg = model(new[i:i + 1].view(1, 1), past_key_values=c2, use_cache=True).logits[0, -1]
