@@ -62,6 +62,23 @@ int lkv_sparse_gemv(const void* x, const void* w_colmajor, float threshold,
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * lkv_sparse_gemv without a workspace argument and without any allocation:
+ * the same kernels and the same result bit for bit, with the split-K partial
+ * sums in a library-owned device array of lkv_sparse_gemv_noalloc_max_bytes()
+ * bytes (8 MiB; each GPU the library runs on holds its own copy until the
+ * process ends).  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Runs on the current device.
+ * Shapes whose partials exceed the array (lkv_sparse_gemv_workspace_bytes(N, Z)
+ * above the maximum) are rejected with LKV_ERR_INVALID.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams, two
+ * host threads) race and must be serialised by the caller.
+ */
+size_t lkv_sparse_gemv_noalloc_max_bytes(void);
+int lkv_sparse_gemv_noalloc(const void* x, const void* w_colmajor, float threshold,
+                            int64_t N, int64_t Z, void* y, void* stream);
+
+/*
  * Fused TEAL gate/up projection with the SwiGLU epilogue of a Mistral MLP:
  *   g = sparse_gemv(x, Wg, t_gate), u = sparse_gemv(x, Wu, t_up)
  *   h = fp16( fp16(silu(fp16(g))) * fp16(u) )

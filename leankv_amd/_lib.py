@@ -34,6 +34,8 @@ SIGNATURES = {
     "lkv_last_error": (ctypes.c_char_p, []),
     "lkv_sparse_gemv_workspace_bytes": (_sz, [_i64, _i64]),
     "lkv_sparse_gemv": (_int, [_c_p, _c_p, _f32, _i64, _i64, _c_p, _c_p, _sz, _c_p]),
+    "lkv_sparse_gemv_noalloc_max_bytes": (_sz, []),
+    "lkv_sparse_gemv_noalloc": (_int, [_c_p, _c_p, _f32, _i64, _i64, _c_p, _c_p]),
     "lkv_sparse_gateup_workspace_bytes": (_sz, [_i64, _i64]),
     "lkv_sparse_gateup_swiglu": (_int, [_c_p, _c_p, _c_p, _f32, _f32, _i64, _i64, _c_p, _c_p, _sz, _c_p]),
     "lkv_sparse_gemv_multi_workspace_bytes": (_sz, [_int, _c_p, _i64]),

@@ -34,6 +34,8 @@
 //   slabs are numbered across the segments.
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "kernels.h"
 
 namespace lkv {
@@ -636,6 +638,64 @@ extern "C" int lkv_sparse_gemv(const void* x, const void* w, float threshold, in
   if (N == 0) return LKV_OK;
   return standalone(x, w, w, threshold, threshold, N, Z, y, workspace, workspace_bytes,
                     static_cast<hipStream_t>(stream), false);
+}
+
+// ---------------------------------------------------------------- no-alloc variant
+// lkv_sparse_gemv with its split-K partials in a library-owned device array
+// instead of a caller workspace.  Each GPU holds its own copy of `scratch`;
+// the host-side name is only a stand-in for that memory, so the device
+// address is looked up once per device (hipGetSymbolAddress, with that device
+// current) and only the looked-up pointer is handed to kernels.  Every call
+// on a device shares its array: calls that overlap on one GPU race.
+namespace lkv {
+namespace {
+
+constexpr size_t kScratchBytes = size_t(8) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch array (nullptr + error text on failure).
+void* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("sparse_gemv_noalloc: no current HIP device (hipGetDevice -> %d)", dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("sparse_gemv_noalloc: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace lkv
+
+extern "C" size_t lkv_sparse_gemv_noalloc_max_bytes(void) { return lkv::kScratchBytes; }
+
+extern "C" int lkv_sparse_gemv_noalloc(const void* x, const void* w, float threshold, int64_t N, int64_t Z, void* y,
+                                       void* stream) {
+  if (int e = check_common(x, w, N, Z, y)) return e;
+  if (N == 0) return LKV_OK;
+  const size_t need = ws_bytes_for(N, Z, false);
+  LKV_REQUIRE(need <= kScratchBytes,
+              "sparse_gemv_noalloc: N=%lld Z=%lld needs %zu bytes of split-K partials, above the %zu-byte "
+              "scratch array (use lkv_sparse_gemv with a workspace)",
+              (long long)N, (long long)Z, need, kScratchBytes);
+  void* ws = scratch_on_current_device();
+  if (ws == nullptr) return LKV_ERR_HIP;
+  return standalone(x, w, w, threshold, threshold, N, Z, y, ws, kScratchBytes, static_cast<hipStream_t>(stream),
+                    false);
 }
 
 extern "C" int lkv_sparse_gateup_swiglu(const void* x, const void* wg, const void* wu, float t_gate, float t_up,

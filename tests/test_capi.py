@@ -52,6 +52,7 @@ def test_row_bytes_and_workspace_queries():
     assert lib.lkv_sparse_gemv_workspace_bytes(4096, 14336) > 0
     assert lib.lkv_sparse_gateup_workspace_bytes(14336, 4096) > lib.lkv_sparse_gemv_workspace_bytes(14336, 4096)
     assert lib.lkv_tq_decode_attn_workspace_bytes(16, 32, 8, 4160) >= 16 * 32 * 128 * 4
+    assert lib.lkv_sparse_gemv_noalloc_max_bytes() == 8 << 20
 
 
 def test_invalid_arguments_rejected_without_launch():
@@ -62,6 +63,12 @@ def test_invalid_arguments_rejected_without_launch():
     # N not a multiple of 8
     assert lib.lkv_sparse_gemv(p, p, 0.1, 12, 16, p, p, 1 << 20, None) == -1
     assert "multiple of 8" in _lib.last_error()
+    # no-alloc GEMV: a shape whose partials exceed the scratch array is refused before any HIP call
+    N, Z = 65536, 32767  # weight just under the 4 GiB descriptor range
+    assert lib.lkv_sparse_gemv_workspace_bytes(N, Z) > lib.lkv_sparse_gemv_noalloc_max_bytes()
+    assert lib.lkv_sparse_gemv_noalloc(p, p, 0.1, N, Z, p, None) == -1
+    assert "scratch" in _lib.last_error()
+    assert lib.lkv_sparse_gemv_noalloc(p, p, 0.1, 12, 16, p, None) == -1
     # unsupported bits
     assert lib.lkv_tq_quantize(p, 0, 16, p, p, 5, p, p, None) == -1
     assert "bits" in _lib.last_error()
