@@ -691,7 +691,8 @@ def bench_batched(args, torch):
 
 # ------------------------------------------------------------------ paged
 def bench_paged(args, torch):
-    """Batch decode attention on the paged fp16 pool (PagedKVCache.decode_attention, paged_cache.py:194-257):
+    """Batch decode attention on the paged fp16 pool (the dense baseline's attention; FlashInfer's batch decode in
+    the reference, paged_cache.py:194-257):
     B=16 sequences of 4096 tokens, 32 query / 8 kv heads, 16-token pages scattered over the pool (seeded
     permutation).  Beside it on the same GPU: torch SDPA over the same K/V already dense (no gather), i.e.
     what a dense fp16 cache pays for the same attention."""

@@ -8,9 +8,11 @@ Differences, all in the direction of the fast path:
     (``use_kernels=True``; the reference used the hook path here) and, when
     TurboQuant is on, selects the "leankv_tq" attention implementation so
     decode attention reads the packed cache directly.
-  * use_paged_cache=True builds leankv_amd.turboquant.paged_cache.PagedKVCache
-    (fp16 page pool, HIP batch decode attention on the pages instead of
-    FlashInfer); it takes precedence over turboquant_bits as in the reference.
+  * use_paged_cache=True asks for the reference's FlashInfer fp16 page pool
+    (leankv/turboquant/paged_cache.py), which HF generate never calls and
+    which is not built here; it raises RuntimeError, as the reference does
+    where FlashInfer is not installed (combined.py:98-102).  The paged
+    TurboQuant layout is leankv_amd.turboquant.paged_tq_cache.
 """
 
 from __future__ import annotations
@@ -60,14 +62,8 @@ def optimize_model(model, teal_sparsity: Optional[float] = None, teal_thresholds
     head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
     cache = None
     if use_paged_cache:
-        from .turboquant.paged_cache import PagedKVCache
-
-        cache = PagedKVCache(num_layers=cfg.num_hidden_layers,
-                             num_kv_heads=getattr(cfg, "num_key_value_heads", cfg.num_attention_heads),
-                             num_q_heads=cfg.num_attention_heads, head_dim=head_dim, page_size=page_size,
-                             max_pages=max_pages, device=model.device, dtype=torch.float16)
-        print("[LeanKV] PagedKVCache enabled (pages=%d, page_size=%d, pool=%.0f MB)"
-              % (max_pages, page_size, cache.get_total_pool_mb()))
+        raise RuntimeError("use_paged_cache: the FlashInfer fp16 paged cache is not part of leankv_amd; "
+                           "use leankv_amd.turboquant.paged_tq_cache.PagedTurboQuantCache for paged 3/4-bit KV")
     elif turboquant_bits is not None:
         cache = TurboQuantCache(bits=turboquant_bits, head_dim=head_dim, num_layers=cfg.num_hidden_layers,
                                 device=model.device, dtype=torch.float16, max_seq_len=max_seq_len,

@@ -1,4 +1,5 @@
-// Batch decode attention over a paged fp16 KV cache (one layer).
+// Batch decode attention over a paged fp16 KV cache (one layer): the
+// attention of the dense fp16 baseline decode step (lkv_decode_layer_step_f16kv).
 //
 // Reference: leankv/turboquant/paged_cache.py:194-257 (PagedKVCache.
 // decode_attention: FlashInfer BatchDecodeWithPagedKVCacheWrapper.plan + run,

@@ -44,3 +44,16 @@ def test_apply_teal_installs_the_fused_qkv_and_mlp_patches():
     assert not hasattr(l0.self_attn, "_teal_qkv_fused") and not hasattr(l0.mlp, "_teal_fused")
     assert l0.self_attn.k_proj.forward.__func__ is torch.nn.Linear.forward
     assert l0.mlp.forward.__func__ is type(l0.mlp).forward
+
+
+def test_optimize_model_paged_cache_raises_as_without_flashinfer():
+    """use_paged_cache=True asks for the reference's FlashInfer fp16 pool, which is not built: RuntimeError,
+    as the reference raises where FlashInfer is absent (leankv/combined.py:98-102)."""
+    import pytest
+
+    from leankv_amd.combined import optimize_model
+    from leankv_amd.engine import random_mistral
+
+    m = random_mistral(device="cpu", seed=2, **TINY)
+    with pytest.raises(RuntimeError, match="FlashInfer"):
+        optimize_model(m, use_paged_cache=True, page_size=16, max_pages=8)

@@ -727,29 +727,11 @@ def _paged_case(lens, Hq, Hkv, ps, seed, dev):
                                             ([300, 1, 4096, 77, 129], 8, 2, 16), ([50, 51], 4, 4, 1),
                                             ([1000, 999], 16, 1, 64), ([2049] * 16, 32, 8, 16)])
 def test_paged_decode_attn(cuda, lens, Hq, Hkv, ps):
+    """The fp16 page-pool attention of the dense fp16 baseline (OwnDenseEngine) vs fp64 attention."""
     out, ref = _paged_case(lens, Hq, Hkv, ps, seed=sum(lens) + ps, dev=cuda)
     assert torch.isfinite(out).all()
     assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
     assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
-
-
-def test_paged_cache_decode_attention_matches_gathered(cuda):
-    """PagedKVCache end to end: a prefill and two decode appends on 2 layers, then decode_attention on the
-    pages equals fp64 attention over the gathered K/V of the same layer."""
-    from leankv_amd.turboquant.paged_cache import PagedKVCache
-
-    g = torch.Generator().manual_seed(3)
-    c = PagedKVCache(num_layers=2, num_kv_heads=2, num_q_heads=8, page_size=16, max_pages=64, device=cuda)
-    for S in (70, 1, 1):
-        for li in range(2):
-            c.update(torch.randn(3, 2, S, 128, generator=g).half().to(cuda),
-                     torch.randn(3, 2, S, 128, generator=g).half().to(cuda), li)
-    q = torch.randn(3, 8, 128, generator=g).half()
-    for li in range(2):
-        out = c.decode_attention(li, q.to(cuda)).cpu()
-        k, v = c[li]
-        ref = oq.decode_attention(q.unsqueeze(2), k.cpu(), v.cpu()).squeeze(2)
-        assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
 
 
 def _paged_tq_case(lens, Hq, Hkv, hot, ps, bits, seed, dev):
