@@ -68,6 +68,9 @@ def _parse():
     ap.add_argument("--skip-dense", action="store_true", help="skip the dense fp16 comparison run")
     ap.add_argument("--no-roofline", action="store_true", help="skip the config-1 GEMV roofline measurement")
     ap.add_argument("--sets", type=int, default=5, help="independent buffer sets rotated per step")
+    ap.add_argument("--per-layer", action="store_true",
+                    help="decode: one lkv_decode_layer_step launch sequence per layer instead of lkv_decode_layers")
+    ap.add_argument("--cold", type=int, default=4096, help="--workload attn: cold tokens per sequence (config 4: 4096)")
     return ap.parse_args()
 
 
@@ -519,7 +522,7 @@ def bench_attn(args, torch):
     from leankv_amd.turboquant.rotation import generate_rotation_matrix
 
     dev = torch.device("cuda:0")
-    B, Hq, Hkv, D, cold, hot = 16, 32, 8, 128, 4096, 64
+    B, Hq, Hkv, D, cold, hot = 16, 32, 8, 128, args.cold, 64
     L = cold + hot
     cent, _ = get_codebook_tensors(D, 3, dev, torch.float32)
     PiK = generate_rotation_matrix(D, dev, torch.float32, 42)
@@ -1011,7 +1014,7 @@ def bench_decode(args, torch):
         model(prompt, past_key_values=cache_count, use_cache=True)
         del out
     _log("calibrate + patch + TurboQuant prefill in %.1fs" % (time.perf_counter() - t0))
-    eng = LeanKVEngine(model, cache, max_len)
+    eng = LeanKVEngine(model, cache, max_len, fused_tail=not args.per_layer)
     eng.start(first, args.prompt)
     dt, toks = timed_decode(eng)
     tps = args.steps / dt

@@ -1,0 +1,178 @@
+// The body of one TEAL sparse GEMV work item (one column slab of kGemvBN
+// outputs x one chunk of BZ input rows), shared by the standalone GEMV
+// kernel and the persistent decode-step kernel so both compute the same
+// partial sums bit for bit.
+//
+// Semantics: leankv/teal/kernels/sparse_gemv.py:61-87 -- the item sums
+// A[z, n] * x[z] over the rows z of its chunk whose |x[z]| > threshold
+// (strict, fp32 compare), fp32 accumulate.  A is the column-major weight of
+// prepare_weight_for_sparse_gemv (:229-234): row z is N contiguous fp16.
+//
+//   1. compaction: |x| > t over the chunk's BZ inputs (already in LDS) into
+//      an LDS list of surviving rows, wave ballot + mbcnt prefix + a
+//      cross-wave prefix; padded to whole streaming batches with (last row, 0);
+//   2. streaming: 32 lanes cover one 512-byte row segment with 16-byte buffer
+//      loads (out-of-range columns read 0); SLOTS row slots each keep U rows
+//      in flight per lane;
+//   3. the row slots are reduced through LDS into kGemvBN fp32 column sums,
+//      returned to threads 0 .. kGemvBN-1.
+#pragma once
+
+#include "kernels.h"
+
+namespace lkv {
+
+typedef uint32_t gemv_u32x4 __attribute__((ext_vector_type(4)));
+
+template <int NT, int BZ, bool DUAL, int U>
+struct GemvLds {
+  static constexpr int kLpr = kGemvBN / 8;   // lanes per row segment
+  static constexpr int kSlots = NT / kLpr;   // rows processed side by side
+  static constexpr int kNl = DUAL ? 2 : 1;
+  static constexpr int kPad = U * kSlots;    // list granularity
+  int idx[kNl][BZ + kPad];
+  float xv[kNl][BZ + kPad];
+  float x[BZ];                               // the chunk's inputs (filled by the caller)
+  int cnt[kNl][NT / kWave];
+  float wsum[NT / kWave];
+  alignas(16) float red[kSlots * kGemvBN];
+};
+
+__device__ __forceinline__ void gemv_fma8(float (&acc)[8], const gemv_u32x4& w, float xv) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc[2 * i] = fmaf(h2f(static_cast<uint16_t>(w[i] & 0xffffu)), xv, acc[2 * i]);
+    acc[2 * i + 1] = fmaf(h2f(static_cast<uint16_t>(w[i] >> 16)), xv, acc[2 * i + 1]);
+  }
+}
+
+// Buffer descriptor over [base, base + bytes): loads past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemv_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// Stream the padded survivor list: total is a multiple of U * SLOTS.  CP is
+// the buffer-load cache policy (2 = nt: streamed once, no L2 retention).
+template <int SLOTS, int U, int CP>
+__device__ __forceinline__ void gemv_stream_rows(__amdgpu_buffer_rsrc_t A, uint32_t row_bytes, uint32_t col_bytes,
+                                                 const int* __restrict__ idx, const float* __restrict__ xv, int total,
+                                                 int slot, float (&acc)[8]) {
+  for (int s = slot; s < total; s += U * SLOTS) {
+    int r[U];
+    float xs[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      r[u] = idx[s + u * SLOTS];
+      xs[u] = xv[s + u * SLOTS];
+    }
+    gemv_u32x4 w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      w[u] = __builtin_amdgcn_raw_buffer_load_b128(A, static_cast<uint32_t>(r[u]) * row_bytes + col_bytes, 0, CP);
+#pragma unroll
+    for (int u = 0; u < U; ++u) gemv_fma8(acc, w[u], xs[u]);
+  }
+}
+
+// Steps 1-3 for the chunk of inputs z0 .. z0 + BZ (sm.x holds them, 0 past
+// Z) and the output columns n0 .. n0 + kGemvBN of an N-column matrix A0 (and
+// A1 in dual mode, thresholds t0 / t1).  sums[l] is the column sum of matrix
+// l for column n0 + threadIdx.x (threads < kGemvBN).  Ends with a barrier, so
+// the caller may refill sm.x afterwards.
+template <int NT, int BZ, bool DUAL, int U, int CP>
+__device__ __forceinline__ void gemv_core(GemvLds<NT, BZ, DUAL, U>& sm, const uint16_t* A0, const uint16_t* A1,
+                                          uint32_t a_bytes, int N, float t0, float t1, int z0, int Z, int n0,
+                                          float (&sums)[DUAL ? 2 : 1]) {
+  using L = GemvLds<NT, BZ, DUAL, U>;
+  constexpr int NL = L::kNl, PAD = L::kPad, LPR = L::kLpr, SLOTS = L::kSlots, BN = kGemvBN;
+  static_assert(BZ % NT == 0, "BZ must be a multiple of the block size");
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+
+  // ---- 1. compaction of surviving activation rows
+  int total[NL];
+#pragma unroll
+  for (int l = 0; l < NL; ++l) total[l] = 0;
+#pragma unroll
+  for (int base = 0; base < BZ; base += NT) {
+    const int z = z0 + base + tid;
+    const bool valid = z < Z;
+    const float v = sm.x[base + tid];
+    const float a = fabsf(v);
+    bool pred[NL];
+    uint64_t mask[NL];
+    pred[0] = valid && (a > t0);
+    if (DUAL) pred[NL - 1] = valid && (a > t1);
+#pragma unroll
+    for (int l = 0; l < NL; ++l) {
+      mask[l] = wave_ballot(pred[l]);
+      if (lane == 0) sm.cnt[l][wave] = __popcll(mask[l]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int l = 0; l < NL; ++l) {
+      int off = total[l], tot = 0;
+#pragma unroll
+      for (int w = 0; w < NT / kWave; ++w) {
+        const int cw = sm.cnt[l][w];
+        off += (w < wave) ? cw : 0;
+        tot += cw;
+      }
+      if (pred[l]) {
+        const int pos = off + lane_prefix(mask[l]);
+        sm.idx[l][pos] = z;
+        sm.xv[l][pos] = v;
+      }
+      total[l] += tot;
+    }
+    __syncthreads();
+  }
+  // pad each list to a multiple of PAD with (last row, 0)
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    const int padded = (total[l] + PAD - 1) / PAD * PAD;
+    if (total[l] > 0 && tid < padded - total[l]) {
+      sm.idx[l][total[l] + tid] = sm.idx[l][total[l] - 1];
+      sm.xv[l][total[l] + tid] = 0.f;
+    }
+    total[l] = padded;
+  }
+  __syncthreads();
+
+  // ---- 2. stream surviving weight rows
+  const int c = tid % LPR;
+  const int slot = tid / LPR;
+  const int col = n0 + c * 8;
+  const uint32_t row_bytes = static_cast<uint32_t>(N) * 2u;
+  // Columns past N would alias the next row: push them past the descriptor end.
+  const uint32_t col_bytes = col < N ? static_cast<uint32_t>(col) * 2u : a_bytes;
+  float acc[NL][8];
+#pragma unroll
+  for (int l = 0; l < NL; ++l)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[l][j] = 0.f;
+  gemv_stream_rows<SLOTS, U, CP>(gemv_rsrc(A0, a_bytes), row_bytes, col_bytes, sm.idx[0], sm.xv[0], total[0], slot,
+                                 acc[0]);
+  if (DUAL)
+    gemv_stream_rows<SLOTS, U, CP>(gemv_rsrc(A1, a_bytes), row_bytes, col_bytes, sm.idx[NL - 1], sm.xv[NL - 1],
+                                   total[NL - 1], slot, acc[NL - 1]);
+
+  // ---- 3. cross-slot reduction through LDS
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    float4* dst = reinterpret_cast<float4*>(sm.red + slot * BN + c * 8);
+    dst[0] = make_float4(acc[l][0], acc[l][1], acc[l][2], acc[l][3]);
+    dst[1] = make_float4(acc[l][4], acc[l][5], acc[l][6], acc[l][7]);
+    __syncthreads();
+    float s = 0.f;
+    if (tid < BN) {
+#pragma unroll
+      for (int sl = 0; sl < SLOTS; ++sl) s += sm.red[sl * BN + tid];
+    }
+    sums[l] = s;
+    __syncthreads();
+  }
+}
+
+}  // namespace lkv

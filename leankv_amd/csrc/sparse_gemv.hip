@@ -36,48 +36,11 @@
 
 #include <mutex>
 
+#include "gemv_core.h"
 #include "kernels.h"
 
 namespace lkv {
 namespace {
-
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ void fma8(float (&acc)[8], const u32x4v& w, float xv) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    acc[2 * i] = fmaf(h2f(static_cast<uint16_t>(w[i] & 0xffffu)), xv, acc[2 * i]);
-    acc[2 * i + 1] = fmaf(h2f(static_cast<uint16_t>(w[i] >> 16)), xv, acc[2 * i + 1]);
-  }
-}
-
-// Buffer descriptor over [base, base + bytes): loads past the end return 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
-}
-
-// Stream the padded survivor list: total is a multiple of U * SLOTS.  CP is
-// the buffer-load cache policy (2 = nt: streamed once, no L2 retention).
-template <int SLOTS, int U, int CP>
-__device__ __forceinline__ void stream_rows(__amdgpu_buffer_rsrc_t A, uint32_t row_bytes, uint32_t col_bytes,
-                                            const int* __restrict__ idx, const float* __restrict__ xv, int total,
-                                            int slot, float (&acc)[8]) {
-  for (int s = slot; s < total; s += U * SLOTS) {
-    int r[U];
-    float xs[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      r[u] = idx[s + u * SLOTS];
-      xs[u] = xv[s + u * SLOTS];
-    }
-    u32x4v w[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      w[u] = __builtin_amdgcn_raw_buffer_load_b128(A, static_cast<uint32_t>(r[u]) * row_bytes + col_bytes, 0, CP);
-#pragma unroll
-    for (int u = 0; u < U; ++u) fma8(acc, w[u], xs[u]);
-  }
-}
 
 // x[z0 .. z0 + BZ) into s_x (0 past Z) for the three input modes.
 template <int NT, int BZ, int MODE>
@@ -143,148 +106,51 @@ __device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float*
 template <int NT, int BZ, bool DUAL, int MODE, int U, int CP>
 __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
   constexpr int BN = kGemvBN;
-  constexpr int LPR = BN / 8;       // lanes per row segment
-  constexpr int SLOTS = NT / LPR;   // rows processed side by side
   constexpr int NL = DUAL ? 2 : 1;
-  constexpr int PAD = U * SLOTS;    // list granularity
-  static_assert(BZ % NT == 0, "BZ must be a multiple of the block size");
-
-  __shared__ int s_idx[NL][BZ + PAD];
-  __shared__ float s_xv[NL][BZ + PAD];
-  __shared__ float s_x[BZ];
-  __shared__ int s_cnt[NL][NT / kWave];
-  __shared__ float s_wsum[NT / kWave];
-  __shared__ __align__(16) float s_red[SLOTS * BN];
+  __shared__ GemvLds<NT, BZ, DUAL, U> sm;
 
   const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
   // Work items are (slab, chunk) pairs.  The usual grid has one block per
   // item (the loop runs once); a persistent grid walks them with a stride.
   const int nslab_tot = G.slab0[G.nseg];
   const int nitems = nslab_tot * G.nchunk;
   for (int item = blockIdx.y * gridDim.x + blockIdx.x; item < nitems; item += gridDim.x * gridDim.y) {
-  int gslab, chunk;
-  if (G.chunk_major) {  // consecutive items walk the chunks of one slab
-    gslab = item / G.nchunk;
-    chunk = item % G.nchunk;
-  } else {
-    gslab = item % nslab_tot;
-    chunk = item / nslab_tot;
-  }
-  const int z0 = chunk * BZ;
-  const int Z = G.Z;
-
-  int seg = 0;
-#pragma unroll
-  for (int s = 1; s < kMaxSeg; ++s)
-    if (s < G.nseg && gslab >= G.slab0[s]) seg = s;
-  const int slab = gslab - G.slab0[seg];
-  const int N = G.N[seg];
-  const float t0 = G.t[seg];
-  const int n0 = slab * BN;
-
-  input_prologue<NT, BZ, MODE>(G, z0, s_x, s_wsum);
-
-  // ---- 1. compaction of surviving activation rows
-  int total[NL];
-#pragma unroll
-  for (int l = 0; l < NL; ++l) total[l] = 0;
-#pragma unroll
-  for (int base = 0; base < BZ; base += NT) {
-    const int z = z0 + base + tid;
-    const bool valid = z < Z;
-    const float v = s_x[base + tid];
-    const float a = fabsf(v);
-    bool pred[NL];
-    uint64_t mask[NL];
-    pred[0] = valid && (a > t0);
-    if (DUAL) pred[NL - 1] = valid && (a > G.t_up);
-#pragma unroll
-    for (int l = 0; l < NL; ++l) {
-      mask[l] = wave_ballot(pred[l]);
-      if (lane == 0) s_cnt[l][wave] = __popcll(mask[l]);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int l = 0; l < NL; ++l) {
-      int off = total[l], tot = 0;
-#pragma unroll
-      for (int w = 0; w < NT / kWave; ++w) {
-        const int cw = s_cnt[l][w];
-        off += (w < wave) ? cw : 0;
-        tot += cw;
-      }
-      if (pred[l]) {
-        const int pos = off + lane_prefix(mask[l]);
-        s_idx[l][pos] = z;
-        s_xv[l][pos] = v;
-      }
-      total[l] += tot;
-    }
-    __syncthreads();
-  }
-  // pad each list to a multiple of PAD with (last row, 0)
-#pragma unroll
-  for (int l = 0; l < NL; ++l) {
-    const int padded = (total[l] + PAD - 1) / PAD * PAD;
-    if (total[l] > 0 && tid < padded - total[l]) {
-      s_idx[l][total[l] + tid] = s_idx[l][total[l] - 1];
-      s_xv[l][total[l] + tid] = 0.f;
-    }
-    total[l] = padded;
-  }
-  __syncthreads();
-
-  // ---- 2. stream surviving weight rows
-  const int c = tid % LPR;
-  const int slot = tid / LPR;
-  const int col = n0 + c * 8;
-  const uint32_t row_bytes = static_cast<uint32_t>(N) * 2u;
-  const uint32_t a_bytes = G.a_bytes[seg];
-  // Columns past N would alias the next row: push them past the descriptor end.
-  const uint32_t col_bytes = col < N ? static_cast<uint32_t>(col) * 2u : a_bytes;
-  float acc[NL][8];
-#pragma unroll
-  for (int l = 0; l < NL; ++l)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[l][j] = 0.f;
-  stream_rows<SLOTS, U, CP>(make_rsrc(G.A[seg], a_bytes), row_bytes, col_bytes, s_idx[0], s_xv[0], total[0], slot, acc[0]);
-  if (DUAL)
-    stream_rows<SLOTS, U, CP>(make_rsrc(G.A_up, a_bytes), row_bytes, col_bytes, s_idx[NL - 1], s_xv[NL - 1], total[NL - 1],
-                       slot, acc[NL - 1]);
-
-  // ---- 3. cross-slot reduction through LDS
-  float sums[NL];
-#pragma unroll
-  for (int l = 0; l < NL; ++l) {
-    float4* dst = reinterpret_cast<float4*>(s_red + slot * BN + c * 8);
-    dst[0] = make_float4(acc[l][0], acc[l][1], acc[l][2], acc[l][3]);
-    dst[1] = make_float4(acc[l][4], acc[l][5], acc[l][6], acc[l][7]);
-    __syncthreads();
-    float s = 0.f;
-    if (tid < BN) {
-#pragma unroll
-      for (int sl = 0; sl < SLOTS; ++sl) s += s_red[sl * BN + tid];
-    }
-    sums[l] = s;
-    __syncthreads();
-  }
-
-  // ---- 4. output (threads 0..255, one column each): fp16 directly (single chunk) or partial sums
-  if (tid < BN) {
-    if (G.y != nullptr) {
-      if (n0 + tid < N) G.y[n0 + tid] = DUAL ? swiglu_f16(sums[0], sums[NL - 1]) : f2h(sums[0]);
+    int gslab, chunk;
+    if (G.chunk_major) {  // consecutive items walk the chunks of one slab
+      gslab = item / G.nchunk;
+      chunk = item % G.nchunk;
     } else {
+      gslab = item % nslab_tot;
+      chunk = item / nslab_tot;
+    }
+    const int z0 = chunk * BZ;
+
+    int seg = 0;
 #pragma unroll
-      for (int l = 0; l < NL; ++l) {
-        float* P = G.part + (l == 0 ? G.part_off[seg] : G.part_up_off) +
-                   (static_cast<size_t>(slab) * G.nchunk + chunk) * BN;
-        P[tid] = sums[l];
+    for (int s = 1; s < kMaxSeg; ++s)
+      if (s < G.nseg && gslab >= G.slab0[s]) seg = s;
+    const int slab = gslab - G.slab0[seg];
+    const int N = G.N[seg];
+    const int n0 = slab * BN;
+
+    input_prologue<NT, BZ, MODE>(G, z0, sm.x, sm.wsum);
+    float sums[NL];
+    gemv_core<NT, BZ, DUAL, U, CP>(sm, G.A[seg], G.A_up, G.a_bytes[seg], N, G.t[seg], G.t_up, z0, G.Z, n0, sums);
+
+    // ---- 4. output (threads 0..255, one column each): fp16 directly (single chunk) or partial sums
+    if (tid < BN) {
+      if (G.y != nullptr) {
+        if (n0 + tid < N) G.y[n0 + tid] = DUAL ? swiglu_f16(sums[0], sums[NL - 1]) : f2h(sums[0]);
+      } else {
+#pragma unroll
+        for (int l = 0; l < NL; ++l) {
+          float* P = G.part + (l == 0 ? G.part_off[seg] : G.part_up_off) +
+                     (static_cast<size_t>(slab) * G.nchunk + chunk) * BN;
+          P[tid] = sums[l];
+        }
       }
     }
-  }
-  __syncthreads();  // LDS is reused by the next item
+    __syncthreads();  // LDS is reused by the next item
   }
 }
 
