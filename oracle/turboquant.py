@@ -93,14 +93,6 @@ def quantize(x: torch.Tensor, Pi: torch.Tensor, boundaries: torch.Tensor, bits: 
     return pack_indices(idx.numpy(), bits), norms, y
 
 
-def rotated_fp64(x: torch.Tensor, Pi: torch.Tensor) -> np.ndarray:
-    """The same y in fp64 from the same fp32 unit vector (tie analysis only)."""
-    x = x.cpu()
-    norms = x.norm(dim=-1)
-    x_unit = (x / (norms.unsqueeze(-1) + 1e-10)).float()
-    return x_unit.double().numpy() @ Pi.double().numpy().T
-
-
 def dequantize(packed: np.ndarray, norms: torch.Tensor, Pi: torch.Tensor, centroids: torch.Tensor,
                bits: int, d: int = 128) -> torch.Tensor:
     """TurboQuantMSE.dequantize (quantizer.py:131-137), fp32."""
