@@ -68,8 +68,6 @@ def _parse():
     ap.add_argument("--skip-dense", action="store_true", help="skip the dense fp16 comparison run")
     ap.add_argument("--no-roofline", action="store_true", help="skip the config-1 GEMV roofline measurement")
     ap.add_argument("--sets", type=int, default=5, help="independent buffer sets rotated per step")
-    ap.add_argument("--per-layer", action="store_true",
-                    help="decode: one lkv_decode_layer_step launch sequence per layer instead of lkv_decode_layers")
     ap.add_argument("--cold", type=int, default=4096, help="--workload attn: cold tokens per sequence (config 4: 4096)")
     return ap.parse_args()
 
@@ -1014,7 +1012,7 @@ def bench_decode(args, torch):
         model(prompt, past_key_values=cache_count, use_cache=True)
         del out
     _log("calibrate + patch + TurboQuant prefill in %.1fs" % (time.perf_counter() - t0))
-    eng = LeanKVEngine(model, cache, max_len, fused_tail=not args.per_layer)
+    eng = LeanKVEngine(model, cache, max_len)
     eng.start(first, args.prompt)
     dt, toks = timed_decode(eng)
     tps = args.steps / dt

@@ -425,14 +425,10 @@ typedef struct lkv_decode_layer {
  */
 int lkv_rmsnorm(const void* x, const void* w, float eps, int64_t M, int64_t Z, void* y, void* stream);
 
-/* Workspace shared by the calls below.  A step is: lkv_decode_begin,
- * lkv_decode_evict, then either lkv_decode_layer_step per layer or one
- * lkv_decode_layers call for all of them, then lkv_decode_head, all on one
- * stream.  lkv_decode_layers needs the workspace zero-filled once before its
- * first step (lkv_decode_workspace_init); the per-layer path needs no
- * initialisation. */
+/* Workspace shared by the four calls below (no initialisation needed).
+ * A step is: lkv_decode_begin, lkv_decode_evict, lkv_decode_layer_step per
+ * layer, lkv_decode_head, all on one stream. */
 size_t lkv_decode_workspace_bytes(const lkv_decode_dims* dims);
-int lkv_decode_workspace_init(const lkv_decode_dims* dims, void* workspace, size_t workspace_bytes, void* stream);
 /* Where the step leaves its intermediate results in the workspace (byte
  * offsets from its start), for callers that read a layer's projections after
  * lkv_decode_layer_step: the split-K partial sums of every GEMV, fp32
@@ -451,7 +447,6 @@ typedef struct lkv_decode_layout {
   size_t part_lm;                /* lm_head (lkv_decode_head) */
   size_t q_rope;                 /* fp16 query after RoPE */
   size_t attn_out;               /* fp16 attention output (o_proj input) */
-  size_t wait_error;             /* int32, nonzero once a wait of lkv_decode_layers gave up */
   size_t total;                  /* = lkv_decode_workspace_bytes */
   int32_t chunks_qkv, chunks_o, chunks_gateup, chunks_down, chunks_lm;
 } lkv_decode_layout;
@@ -473,20 +468,6 @@ int lkv_decode_evict(const lkv_decode_dims* dims, const lkv_decode_layer* layers
  * step's new key / value enter the hot ring (eviction is lkv_decode_evict's). */
 int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_decode_layer* layer, void* x,
                           void* workspace, size_t workspace_bytes, void* stream);
-/* All n_layers decoder layers (host array) of one step, with results equal to
- * n_layers lkv_decode_layer_step calls bit for bit: the first layer's q|k|v
- * GEMV, then per layer the attention (split + combine) and one persistent
- * launch for the rest of the layer and the next layer's q|k|v.  That launch
- * keeps every block resident and passes data between its work items through
- * step-tagged words, so it must not share the GPU's compute units with other
- * kernels running at the same time (its waits then give up after a bounded
- * spin and set the layout's wait_error word).  Needs a zero-filled workspace
- * (lkv_decode_workspace_init) before the first step.  No single reference
- * counterpart: it regroups the per-layer work of
- * transformers/models/mistral/modeling_mistral.py's decoder layer with the
- * TEAL projections of leankv/teal/patching.py:152-183. */
-int lkv_decode_layers(const lkv_decode_dims* dims, const lkv_decode_layer* layers, int64_t n_layers, void* x,
-                      void* workspace, size_t workspace_bytes, void* stream);
 /* The same decoder layer with a plain fp16 KV cache instead of the TurboQuant
  * one: the dense-fp16 decode that the reference's baseline runs
  * (scripts/raw_baseline.py:33-62: HF decode with an fp16 DynamicCache), on

@@ -69,8 +69,6 @@ SIGNATURES = {
     "lkv_rmsnorm": (_int, [_c_p, _c_p, _f32, _i64, _i64, _c_p, _c_p]),
     "lkv_decode_workspace_bytes": (_sz, [_c_p]),
     "lkv_decode_workspace_layout": (_int, [_c_p, _c_p]),
-    "lkv_decode_workspace_init": (_int, [_c_p, _c_p, _sz, _c_p]),
-    "lkv_decode_layers": (_int, [_c_p, _c_p, ctypes.c_int64, _c_p, _c_p, _sz, _c_p]),
     "lkv_decode_begin": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
     "lkv_decode_evict": (_int, [_c_p, _c_p, ctypes.c_int64, _c_p, _sz, _c_p]),
     "lkv_decode_layer_step": (_int, [_c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
@@ -105,8 +103,7 @@ class DecodeLayout(ctypes.Structure):
 
     _fields_ = [
         ("part_q", _sz), ("part_k", _sz), ("part_v", _sz), ("part_o", _sz), ("part_gate", _sz), ("part_up", _sz),
-        ("part_down", _sz), ("part_lm", _sz), ("q_rope", _sz), ("attn_out", _sz), ("wait_error", _sz),
-        ("total", _sz),
+        ("part_down", _sz), ("part_lm", _sz), ("q_rope", _sz), ("attn_out", _sz), ("total", _sz),
         ("chunks_qkv", ctypes.c_int32), ("chunks_o", ctypes.c_int32), ("chunks_gateup", ctypes.c_int32),
         ("chunks_down", ctypes.c_int32), ("chunks_lm", ctypes.c_int32),
     ]

@@ -42,7 +42,7 @@ struct Plan {
   AttnPlan attn;
   int64_t f16_pages;  // pages of the fp16-KV step's pool (kF16Page tokens each)
   size_t off_state, off_pqkv, off_po, off_pgu, off_pd, off_plm, off_q16, off_attn, off_rec, off_cand, off_pt,
-      off_prec, prec_bytes, off_xt, off_tpo, off_tgu, off_th, off_tpd, total;
+      off_prec, prec_bytes, total;
 };
 
 size_t al256(size_t v) { return (v + 255) / 256 * 256; }
@@ -76,8 +76,7 @@ Plan make_plan(const lkv_decode_dims& d) {
     o += al256(bytes);
     return at;
   };
-  // state: {pos, pos + 1, step epoch, wait error}
-  p.off_state = take(4 * sizeof(int32_t));
+  p.off_state = take(2 * sizeof(int32_t));
   p.off_pqkv = take((gemv_part_floats(p.nq, p.nc_qkv) + 2 * gemv_part_floats(p.nkv, p.nc_qkv)) * 4);
   p.off_po = take(gemv_part_floats(d.hidden, p.nc_o) * 4);
   p.off_pgu = take(2 * gemv_part_floats(d.ffn, p.nc_gu) * 4);
@@ -91,12 +90,6 @@ Plan make_plan(const lkv_decode_dims& d) {
   p.off_pt = take(static_cast<size_t>(3 + p.f16_pages) * 4);
   p.prec_bytes = lkv_paged_decode_attn_workspace_bytes(1, d.n_heads, d.n_kv_heads, d.max_len);
   p.off_prec = take(p.prec_bytes);
-  // tagged (payload, tag) words of the persistent layer tail (decode_tail.hip)
-  p.off_xt = take(static_cast<size_t>(d.hidden / 2) * 8);
-  p.off_tpo = take(gemv_part_floats(d.hidden, p.nc_o) * 8);
-  p.off_tgu = take(2 * gemv_part_floats(d.ffn, p.nc_gu) * 8);
-  p.off_th = take(static_cast<size_t>(d.ffn / 2) * 8);
-  p.off_tpd = take(gemv_part_floats(d.hidden, p.nc_d) * 8);
   p.total = o;
   return p;
 }
@@ -135,7 +128,7 @@ int check_ws(const Plan& p, const void* ws, size_t bytes) {
 
 // ------------------------------------------------------------------ kernels
 
-// x = embed[tok]; state = {pos, pos + 1, epoch + 1} (pos clamped into the tables).
+// x = embed[tok]; state = {pos, pos + 1} (pos clamped into the tables).
 __global__ __launch_bounds__(kThreads) void begin_kernel(const uint16_t* __restrict__ embed,
                                                          const int64_t* __restrict__ tok,
                                                          const int64_t* __restrict__ pos, uint16_t* __restrict__ x,
@@ -151,16 +144,7 @@ __global__ __launch_bounds__(kThreads) void begin_kernel(const uint16_t* __restr
     p = p < 0 ? 0 : (p >= max_len ? max_len - 1 : p);
     state[0] = static_cast<int32_t>(p);
     state[1] = static_cast<int32_t>(p + 1);
-    state[2] = state[2] + 1;  // tags of the persistent layer tail name the step
   }
-}
-
-// Zero-fill (the workspace before its first step: no tagged word may carry a
-// tag a step could expect).
-__global__ __launch_bounds__(kThreads) void zero_kernel(uint4* __restrict__ p, size_t n16) {
-  for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n16;
-       i += static_cast<size_t>(gridDim.x) * kThreads)
-    p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
 // x[n] = fp16(x[n] + fp16(sum of chunks)): the fp16 residual add of the decoder layer.
@@ -427,7 +411,6 @@ extern "C" int lkv_decode_workspace_layout(const lkv_decode_dims* dims, lkv_deco
   l.part_lm = p.off_plm;
   l.q_rope = p.off_q16;
   l.attn_out = p.off_attn;
-  l.wait_error = p.off_state + 12;
   l.chunks_qkv = p.nc_qkv;
   l.chunks_o = p.nc_o;
   l.chunks_gateup = p.nc_gu;
@@ -660,128 +643,6 @@ extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_deco
   // query rotation, the new key and value into the ring)
   if (int e = step_attn(p, d, L, ws, st)) return e;
   return step_tail(p, d, L, xx, ws, st);
-}
-
-namespace lkv {
-namespace {
-
-// The persistent tail of layer l (decode_tail.hip): its o_proj .. second
-// residual, then layer l + 1's q|k|v (next == nullptr after the last layer).
-int step_tail_fused(const Plan& p, const lkv_decode_dims& d, const lkv_decode_layer* L,
-                    const lkv_decode_layer* next, int layer, int n_layers, uint16_t* xx, char* ws, hipStream_t st) {
-  TailArgs A{};
-  A.state = reinterpret_cast<const int32_t*>(ws + p.off_state);
-  A.err = reinterpret_cast<int32_t*>(ws + p.off_state) + 3;
-  A.n_layers = n_layers;
-  A.layer = layer;
-  A.eps = d.eps;
-  A.hidden = static_cast<int>(d.hidden);
-  A.ffn = static_cast<int>(d.ffn);
-  A.nq = static_cast<int>(p.nq);
-  A.nkv = static_cast<int>(p.nkv);
-  A.sh = static_cast<int>(p.sh);
-  A.sf = static_cast<int>(p.sf);
-  A.sq = static_cast<int>(p.sq);
-  A.sk = static_cast<int>(p.sk);
-  A.nc_o = p.nc_o;
-  A.nc_gu = p.nc_gu;
-  A.nc_d = p.nc_d;
-  A.nc_qkv = p.nc_qkv;
-  A.bz_o = p.bz_o;
-  A.bz_gu = p.bz_gu;
-  A.bz_d = p.bz_d;
-  A.bz_qkv = p.bz_qkv;
-  A.attn = reinterpret_cast<const uint16_t*>(ws + p.off_attn);
-  A.wo = static_cast<const uint16_t*>(L->wo);
-  A.wo_bytes = static_cast<uint32_t>(p.nq * d.hidden * 2);
-  A.t_o = L->to;
-  A.x = xx;
-  A.xt = reinterpret_cast<uint64_t*>(ws + p.off_xt);
-  A.po = reinterpret_cast<uint64_t*>(ws + p.off_tpo);
-  A.pgu = reinterpret_cast<uint64_t*>(ws + p.off_tgu);
-  A.ph = reinterpret_cast<uint64_t*>(ws + p.off_th);
-  A.pd = reinterpret_cast<uint64_t*>(ws + p.off_tpd);
-  A.post_norm = static_cast<const uint16_t*>(L->post_norm);
-  A.wg = static_cast<const uint16_t*>(L->wg);
-  A.wu = static_cast<const uint16_t*>(L->wu);
-  A.wgu_bytes = static_cast<uint32_t>(d.hidden * d.ffn * 2);
-  A.t_g = L->tg;
-  A.t_u = L->tu;
-  A.wd = static_cast<const uint16_t*>(L->wd);
-  A.wd_bytes = static_cast<uint32_t>(d.ffn * d.hidden * 2);
-  A.t_d = L->td;
-  int nqkv = 0;
-  if (next) {
-    A.in_norm = static_cast<const uint16_t*>(next->input_norm);
-    A.wq = static_cast<const uint16_t*>(next->wq);
-    A.wk = static_cast<const uint16_t*>(next->wk);
-    A.wv = static_cast<const uint16_t*>(next->wv);
-    A.tq = next->tq;
-    A.tk = next->tk;
-    A.tv = next->tv;
-    A.pqkv = reinterpret_cast<float*>(ws + p.off_pqkv);
-    A.pk_off = gemv_part_floats(p.nq, p.nc_qkv);
-    A.pv_off = A.pk_off + gemv_part_floats(p.nkv, p.nc_qkv);
-    nqkv = static_cast<int>((p.sq + 2 * p.sk) * p.nc_qkv);
-  }
-  const int counts[7] = {static_cast<int>(p.sh) * p.nc_o, static_cast<int>(p.sh), static_cast<int>(p.sf) * p.nc_gu,
-                         static_cast<int>(p.sf), static_cast<int>(p.sh) * p.nc_d, static_cast<int>(p.sh), nqkv};
-  A.pre[0] = 0;
-  for (int i = 0; i < 7; ++i) A.pre[i + 1] = A.pre[i] + counts[i];
-  return tail_launch(A, st);
-}
-
-bool tail_supported(const Plan& p, const lkv_decode_dims& d) {
-  auto ok = [](int bz) { return bz == 256 || bz == 512; };
-  return ok(p.bz_o) && ok(p.bz_gu) && ok(p.bz_d) && ok(p.bz_qkv) && d.hidden <= kTailMaxHidden;
-}
-
-}  // namespace
-}  // namespace lkv
-
-extern "C" int lkv_decode_workspace_init(const lkv_decode_dims* dims, void* workspace, size_t workspace_bytes,
-                                         void* stream) {
-  if (int e = check_dims(dims)) return e;
-  const Plan p = make_plan(*dims);
-  if (int e = check_ws(p, workspace, workspace_bytes)) return e;
-  const size_t n16 = p.total / 16;
-  const unsigned grid = static_cast<unsigned>((n16 + kThreads - 1) / kThreads < 1024 ? (n16 + kThreads - 1) / kThreads
-                                                                                     : 1024);
-  hipLaunchKernelGGL(zero_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                     static_cast<uint4*>(workspace), n16);
-  LKV_LAUNCH_CHECK("decode_workspace_init");
-  return LKV_OK;
-}
-
-extern "C" int lkv_decode_layers(const lkv_decode_dims* dims, const lkv_decode_layer* layers, int64_t n_layers,
-                                 void* x, void* workspace, size_t workspace_bytes, void* stream) {
-  if (int e = check_dims(dims)) return e;
-  const lkv_decode_dims& d = *dims;
-  const Plan p = make_plan(d);
-  if (int e = check_ws(p, workspace, workspace_bytes)) return e;
-  LKV_REQUIRE(layers && n_layers >= 1 && n_layers < (1 << 16), "decode_layers: need 1..65535 layers");
-  LKV_REQUIRE(tail_supported(p, d),
-              "decode_layers: chunk sizes (%d, %d, %d, %d) outside the persistent tail's 256 / 512, or hidden %lld "
-              "above %d", p.bz_o, p.bz_gu, p.bz_d, p.bz_qkv, (long long)d.hidden, kTailMaxHidden);
-  for (int64_t l = 0; l < n_layers; ++l) {
-    const lkv_decode_layer* L = layers + l;
-    if (int e = check_layer_weights(L, x)) return e;
-    LKV_REQUIRE(L->k_codes && L->k_norms && L->v_codes && L->v_norms && L->k_hot && L->v_hot && L->PiK && L->PiV,
-                "decode_layers: null cache pointer in layer %lld", (long long)l);
-    LKV_REQUIRE(aligned16(L->k_codes) && aligned16(L->v_codes) && aligned16(L->k_hot) && aligned16(L->v_hot),
-                "decode_layers: cache buffers of layer %lld must be 16-byte aligned", (long long)l);
-  }
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  uint16_t* xx = static_cast<uint16_t*>(x);
-  if (int e = step_qkv(p, d, layers, xx, ws, st)) return e;
-  for (int64_t l = 0; l < n_layers; ++l) {
-    if (int e = step_attn(p, d, layers + l, ws, st)) return e;
-    const lkv_decode_layer* next = l + 1 < n_layers ? layers + l + 1 : nullptr;
-    if (int e = step_tail_fused(p, d, layers + l, next, static_cast<int>(l), static_cast<int>(n_layers), xx, ws, st))
-      return e;
-  }
-  return LKV_OK;
 }
 
 extern "C" int lkv_decode_layer_step_f16kv(const lkv_decode_dims* dims, const lkv_decode_layer* L, void* kv_pool,

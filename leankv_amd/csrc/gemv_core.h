@@ -1,7 +1,7 @@
 // The body of one TEAL sparse GEMV work item (one column slab of kGemvBN
-// outputs x one chunk of BZ input rows), shared by the standalone GEMV
-// kernel and the persistent decode-step kernel so both compute the same
-// partial sums bit for bit.
+// outputs x one chunk of BZ input rows): every GEMV launch of the library
+// (standalone entry points and the decode step's prologue variants) runs it,
+// so all compute the same partial sums bit for bit.
 //
 // Semantics: leankv/teal/kernels/sparse_gemv.py:61-87 -- the item sums
 // A[z, n] * x[z] over the rows z of its chunk whose |x[z]| > threshold

@@ -298,55 +298,4 @@ struct AttnCall {
 // Launch the split and combine kernels.
 int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st);
 
-// ------------------------------------------------------------- decode tail
-// One decoder layer's work after attention (o_proj, residual, gate|up,
-// SwiGLU, down, residual) and the next layer's q|k|v GEMV as one persistent
-// launch (decode_tail.hip).  Item counts are prefix sums in pre[]: O, R1, GU,
-// H, D, R2, QKV (pre[0] = 0, pre[7] = total; no QKV items after the last
-// layer).  Tagged buffers hold 64-bit (payload, tag) words.
-struct TailArgs {
-  int pre[8];
-  const int32_t* state;  // state[2] = step epoch
-  int32_t* err;          // set to nonzero when a wait gave up
-  int n_layers, layer;
-  float eps;
-  int hidden, ffn, nq, nkv;
-  int sh, sf, sq, sk;    // column slabs of hidden, ffn, q, k / v
-  int nc_o, nc_gu, nc_d, nc_qkv;
-  int bz_o, bz_gu, bz_d, bz_qkv;
-  // o_proj
-  const uint16_t* attn;  // fp16 [nq], plain (the attention's output)
-  const uint16_t* wo;
-  uint32_t wo_bytes;
-  float t_o;
-  // residual stream: x plain fp16 [hidden], xt tagged fp16 pairs [hidden / 2]
-  uint16_t* x;
-  uint64_t* xt;
-  // tagged partials: po [sh][nc_o][256], pgu [2][sf][nc_gu][256], pd [sh][nc_d][256]; ph tagged h pairs [ffn / 2]
-  uint64_t* po;
-  uint64_t* pgu;
-  uint64_t* ph;
-  uint64_t* pd;
-  // gate|up, down
-  const uint16_t* post_norm;
-  const uint16_t* wg;
-  const uint16_t* wu;
-  uint32_t wgu_bytes;
-  float t_g, t_u;
-  const uint16_t* wd;
-  uint32_t wd_bytes;
-  float t_d;
-  // the next layer's q|k|v (plain partials, [slab][chunk][256] per segment)
-  const uint16_t* in_norm;
-  const uint16_t* wq;
-  const uint16_t* wk;
-  const uint16_t* wv;
-  float tq, tk, tv;
-  float* pqkv;
-  size_t pk_off, pv_off;  // floats from pqkv to the k and v segments
-};
-int tail_launch(const TailArgs& A, hipStream_t st);
-// Widest residual stream the persistent tail stages in LDS (fp16 pairs).
-constexpr int kTailMaxHidden = 8192;
-
 }  // namespace lkv

@@ -136,25 +136,21 @@ class LeanKVEngine(_Base):
     """TEAL sparse projections + TurboQuant packed KV through the fused C decode step.
 
     Per token: lkv_decode_begin, lkv_decode_evict (the token leaving every
-    layer's hot window, one launch), the layers and lkv_decode_head (lm_head
-    GEMV, logits, argmax), captured into one graph.  The layers run either as
-    lkv_decode_layer_step per layer (fused_tail=False; 8 kernels: q|k|v GEMV
-    with the RMSNorm prologue, attention split with the q|k|v sums, RoPE, ring
-    append and query rotation in its prologue, combine, o_proj, residual,
-    gate|up GEMV with the RMSNorm prologue, down GEMV with the SwiGLU prologue,
-    residual) or as one lkv_decode_layers call (default): per layer the
-    attention split and combine, then one persistent launch for o_proj through
-    the next layer's q|k|v, with the same results bit for bit.
+    layer's hot window, one launch), lkv_decode_layer_step per layer (8
+    kernels: q|k|v GEMV with the RMSNorm prologue, attention split with the
+    q|k|v sums, RoPE, ring append and query rotation in its prologue, combine,
+    o_proj, residual, gate|up GEMV with the RMSNorm prologue, down GEMV with
+    the SwiGLU prologue, residual) and
+    lkv_decode_head (lm_head GEMV, logits, argmax), captured into one graph.
 
     Projections patched by apply_teal already hold their weight column-major
     (leankv/teal/patching.py:171); unpatched ones get a column-major copy and
     threshold 0 (dense).  lm_head gets a column-major copy.
     """
 
-    def __init__(self, model, cache: TurboQuantCache, max_len: int, fused_tail: bool = True):
+    def __init__(self, model, cache: TurboQuantCache, max_len: int):
         super().__init__(model, max_len)
         self.cache = cache
-        self.fused_tail = fused_tail
         if cache.cold_capacity(0) < max_len - cache.hot_buffer_size:
             raise ValueError("TurboQuantCache cold capacity %d < max_len - hot" % cache.cold_capacity(0))
         if self.D != 128:
@@ -198,12 +194,6 @@ class LeanKVEngine(_Base):
         if nbytes == 0:
             raise _lib.LeanKVError("lkv_decode_workspace_bytes rejected the model shape: %s" % _lib.last_error())
         self.ws = torch.empty(nbytes, dtype=torch.uint8, device=d)
-        _lib.check(lib.lkv_decode_workspace_init(ctypes.byref(self.dims), self.ws.data_ptr(), nbytes,
-                                                 _lib.stream_handle(d)), "lkv_decode_workspace_init")
-        layout = _lib.DecodeLayout()
-        _lib.check(lib.lkv_decode_workspace_layout(ctypes.byref(self.dims), ctypes.byref(layout)),
-                   "lkv_decode_workspace_layout")
-        self._wait_error = self.ws[layout.wait_error:layout.wait_error + 4].view(torch.int32)
         self.x = torch.empty(self.hidden, dtype=torch.float16, device=d)
 
     def _hold(self, t: torch.Tensor) -> int:
@@ -211,19 +201,6 @@ class LeanKVEngine(_Base):
             raise _lib.LeanKVError("decode state must live on the GPU")
         self._keep.append(t)
         return t.data_ptr()
-
-    def check_waits(self) -> None:
-        """Raise if a wait inside the persistent layer tail gave up (its kernel shared the GPU with other work)."""
-        if int(self._wait_error.item()) != 0:
-            raise _lib.LeanKVError("lkv_decode_layers: a wait between work items gave up; the step's results are "
-                                   "invalid (the persistent launch needs the GPU's compute units to itself)")
-
-    @torch.no_grad()
-    def generate(self, n: int) -> list:
-        out = super().generate(n)
-        if self.fused_tail:
-            self.check_waits()
-        return out
 
     def start(self, first_token: torch.Tensor, length: int) -> None:
         """Set the token to feed next and its position (the cache length after prefill)."""
@@ -238,13 +215,9 @@ class LeanKVEngine(_Base):
                                         self.pos64.data_ptr(), self.x.data_ptr(), ws, nb, st), "lkv_decode_begin")
         _lib.check(lib.lkv_decode_evict(dims, self.layer_table, len(self.layer_structs), ws, nb, st),
                    "lkv_decode_evict")
-        if self.fused_tail:
-            _lib.check(lib.lkv_decode_layers(dims, self.layer_table, len(self.layer_structs), self.x.data_ptr(), ws,
-                                             nb, st), "lkv_decode_layers")
-        else:
-            for ls in self.layer_structs:
-                _lib.check(lib.lkv_decode_layer_step(dims, ctypes.byref(ls), self.x.data_ptr(), ws, nb, st),
-                           "lkv_decode_layer_step")
+        for ls in self.layer_structs:
+            _lib.check(lib.lkv_decode_layer_step(dims, ctypes.byref(ls), self.x.data_ptr(), ws, nb, st),
+                       "lkv_decode_layer_step")
         _lib.check(lib.lkv_decode_head(dims, self.final_norm.data_ptr(), self.lm_head_cm.data_ptr(),
                                        self.x.data_ptr(), self.logits.data_ptr(), self.tok.data_ptr(),
                                        self.pos64.data_ptr(), ws, nb, st), "lkv_decode_head")

@@ -174,7 +174,7 @@ def test_decode_struct_layout_matches_header():
         assert [f[0] for f in cls._fields_] == names, cname
     assert ctypes.sizeof(_lib.DecodeDims) == 8 * 8 + 4 * 3 + 4 + 8 * 4  # 4 bytes of padding before bounds
     assert ctypes.sizeof(_lib.DecodeLayer) == 9 * 8 + 7 * 4 + 4 + 8 * 8
-    assert ctypes.sizeof(_lib.DecodeLayout) == 12 * 8 + 5 * 4 + 4  # padded to 8-byte alignment
+    assert ctypes.sizeof(_lib.DecodeLayout) == 11 * 8 + 5 * 4 + 4  # padded to 8-byte alignment
 
 
 def test_decode_workspace_layout():

@@ -239,18 +239,6 @@ def _hip_rmsnorm_and_lm_head(model, lm_head_cm):
     head.forward = fwd
 
 
-def test_config5_fused_tail_equals_per_layer_steps(cuda):
-    """2 full-width layers, TEAL on, 1024-token context: the persistent layer tail (lkv_decode_layers, the
-    bench's path) vs one lkv_decode_layer_step per layer, bit for bit."""
-    from test_gpu_engine import fused_vs_per_layer
-
-    model = _model(cuda, 2, seed=17)
-    th = _thresholds(model, 17)
-    cache = _patch(model, th)
-    first = _prefill(model, cache, _prompt(model, 17))
-    assert fused_vs_per_layer(model, cache, first, PROMPT, MAXLEN, STEPS, cuda) == STEPS
-
-
 def test_config5_engine_matches_hf_path_32_layers(cuda):
     """All 32 layers, TEAL on: engine vs the HF-patched path on the engine's tokens, identical results."""
     from leankv_amd.engine import LeanKVEngine

@@ -241,55 +241,6 @@ def test_engine_graph_replays_equal_eager(cuda):
             _ = torch.zeros(1000, device=cuda).sum()  # eager work between replays
 
 
-def _cache_bufs(cache):
-    return (cache._k_codes, cache._v_codes, cache._k_norms, cache._v_norms, cache._k_hot, cache._v_hot)
-
-
-def fused_vs_per_layer(model, cache, first, start, max_len, steps, cuda):
-    """Run the engine's per-layer step and its persistent-tail step (lkv_decode_layers) from the same cache state:
-    logits of every step, tokens and the caches they leave must be identical; returns the number of steps."""
-    from leankv_amd.engine import LeanKVEngine
-
-    snap = [[t.clone() for t in lst] for lst in _cache_bufs(cache)]
-    runs = []
-    for fused in (False, True):
-        for lst, saved in zip(_cache_bufs(cache), snap):
-            for t, s in zip(lst, saved):
-                t.copy_(s)
-        eng = LeanKVEngine(model, cache, max_len, fused_tail=fused)
-        eng.start(first, start)
-        logits, toks = [], []
-        with torch.no_grad():
-            for i in range(steps):
-                if i == 2:
-                    eng.capture()
-                eng.step()
-                logits.append(eng.logits.clone())
-                toks.append(int(eng.tok))
-        torch.cuda.synchronize()
-        if fused:
-            eng.check_waits()
-        runs.append((logits, toks, [[t.clone() for t in lst] for lst in _cache_bufs(cache)]))
-    (l0, t0, c0), (l1, t1, c1) = runs
-    for i in range(steps):
-        assert torch.equal(l0[i], l1[i]), "step %d: fused tail logits differ" % i
-    assert t0 == t1
-    for a, b in zip(c0, c1):
-        for x, y in zip(a, b):
-            assert torch.equal(x, y)
-    return steps
-
-
-def test_fused_tail_equals_per_layer_steps(cuda):
-    """lkv_decode_layers (one persistent launch per layer tail) vs lkv_decode_layer_step per layer, TEAL on."""
-    model, th, prompt, _ = _setup(cuda, seed=7)
-    cache = _apply(model, th)
-    with torch.no_grad():
-        out = model(prompt.view(1, -1).to(cuda), past_key_values=cache, use_cache=True)
-    first = torch.argmax(out.logits[0, -1])
-    assert fused_vs_per_layer(model, cache, first, PROMPT, MAXLEN, 12, cuda) == 12
-
-
 def test_dense_engine_matches_hf(cuda):
     """Dense graph engine vs HF's own fp16 forward with a DynamicCache, teacher-forced logits."""
     from transformers import DynamicCache
