@@ -104,14 +104,18 @@ __device__ __forceinline__ void column_sum2(const float* __restrict__ P, int n0,
 // first as the fp16 projection output is.  Each product is rounded to fp16
 // before the sum: contraction is off here, since the compiler otherwise turns
 // the fp16 product and the fp32 add into one fma and skips that rounding.
-__device__ __forceinline__ void rope_pair(float x0, float x1, const uint16_t* __restrict__ cos_row,
-                                          const uint16_t* __restrict__ sin_row, int d, float& o0, float& o1) {
+__device__ __forceinline__ void rope_pair_v(float x0, float x1, uint16_t cos0, uint16_t cos1, uint16_t sin0,
+                                            uint16_t sin1, float& o0, float& o1) {
 #pragma clang fp contract(off)
   const float a = h2f(f2h(x0)), c = h2f(f2h(x1));
-  const float c0 = h2f(cos_row[d]), c1 = h2f(cos_row[d + 64]);
-  const float s0 = h2f(sin_row[d]), s1 = h2f(sin_row[d + 64]);
+  const float c0 = h2f(cos0), c1 = h2f(cos1);
+  const float s0 = h2f(sin0), s1 = h2f(sin1);
   o0 = h2f(f2h(h2f(f2h(a * c0)) + h2f(f2h(-c * s0))));
   o1 = h2f(f2h(h2f(f2h(c * c1)) + h2f(f2h(a * s1))));
+}
+__device__ __forceinline__ void rope_pair(float x0, float x1, const uint16_t* __restrict__ cos_row,
+                                          const uint16_t* __restrict__ sin_row, int d, float& o0, float& o1) {
+  rope_pair_v(x0, x1, cos_row[d], cos_row[d + 64], sin_row[d], sin_row[d + 64], o0, o1);
 }
 
 // 1 / sqrt(mean(x^2) + eps) over fp16 x[0..Z) in fp32, computed by a whole

@@ -343,9 +343,25 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
     else
       fetch_block(R, rs, t, t_addr_end, lane, DenseRows{});
   };
+  // The wave's first token block.  Dense layout: always the straight-line
+  // full-block load, whatever t is: rows past the cold store read 0 through
+  // the buffer descriptor, and tokens at or past t_end are masked by selects
+  // in attend_block, so no branch separates these loads from the query's and
+  // the query's wait need not drain them.  Paged: page ids past the split
+  // are not staged, so the load keeps its guard.
+  auto fetch_first = [&](BlockRegs& R, int t) {
+    if constexpr (PAGED) {
+      if (t < t_addr_end) fetch(R, t);
+    } else {
+      load_full(R, rs, __builtin_amdgcn_readfirstlane(t), lane, DenseRows{});
+    }
+  };
   BlockRegs ra, rb;
   int t0 = t_begin + wave * kBlk;
-  if (t0 < t_addr_end) fetch(ra, t0);
+  // The first token block is fetched right after the query's own loads are
+  // issued: memory results retire in issue order, so the query rotation then
+  // waits only for the (cached) rotation matrix and query, not for the first
+  // codes from HBM, and the codes keep streaming in while it computes.
   float c_lo = 0.f, c_hi = 0.f;
   uint32_t tab[4] = {0u, 0u, 0u, 0u};
   if constexpr (PERM) {
@@ -381,12 +397,67 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
       const uint16_t* cos_row = P.rope_cos + static_cast<size_t>(pos) * kD;
       const uint16_t* sin_row = P.rope_sin + static_cast<size_t>(pos) * kD;
       const bool writer = split == P.nsplit - 1;
+      // this thread's first query element: its first kPre chunk partials (both
+      // dims of the RoPE pair) from clamped, always valid addresses, ahead of
+      // the codes; the rest of the chunks and elements are loaded after them
+      constexpr int kPre = 16;
+      float pre0[kPre], pre1[kPre];
+      uint16_t rc0, rc1, rs0, rs1;  // its RoPE factors
+      {
+        const int e = min(tid, G * (kD / 2) - 1);
+        const int dd = e % (kD / 2);
+        rc0 = cos_row[dd];
+        rc1 = cos_row[dd + kD / 2];
+        rs0 = sin_row[dd];
+        rs1 = sin_row[dd + kD / 2];
+        const int col = (kvh * G + e / (kD / 2)) * kD + dd;
+        const float* p0 = P.pq + static_cast<size_t>(col / kGemvBN) * P.nchunk * kGemvBN + (col % kGemvBN);
+        const float* p1 = P.pq + static_cast<size_t>((col + kD / 2) / kGemvBN) * P.nchunk * kGemvBN +
+                          ((col + kD / 2) % kGemvBN);
+#pragma unroll
+        for (int i = 0; i < kPre; ++i) {
+          const size_t o = static_cast<size_t>(min(i, P.nchunk - 1)) * kGemvBN;
+          pre0[i] = p0[o];
+          pre1[i] = p1[o];
+        }
+      }
+      // the new key (threads 0..63, pair (t, t + 64)) and value (threads
+      // 64..127) of the ring write, which only the last split block stores:
+      // loaded by every block, without a branch, so that no path drains the
+      // codes' loads before the query is ready
+      float prk0[kPre], prk1[kPre];
+      {
+        const int t = tid & (kD - 1);
+        const float* src = t < kD / 2 ? P.pk : P.pv;
+        const int c0 = kvh * kD + (t & (kD / 2 - 1)), c1 = c0 + kD / 2;
+        const float* p0 = src + static_cast<size_t>(c0 / kGemvBN) * P.nchunk * kGemvBN + (c0 % kGemvBN);
+        const float* p1 = src + static_cast<size_t>(c1 / kGemvBN) * P.nchunk * kGemvBN + (c1 % kGemvBN);
+#pragma unroll
+        for (int i = 0; i < kPre; ++i) {
+          const size_t o = static_cast<size_t>(min(i, P.nchunk - 1)) * kGemvBN;
+          prk0[i] = p0[o];
+          prk1[i] = p1[o];
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the codes' (results retire in order)
+      fetch_first(ra, t0);
       for (int e = tid; e < G * (kD / 2); e += kThreads) {
         const int hh = e / (kD / 2), dd = e % (kD / 2);
         const int col = (kvh * G + hh) * kD + dd;
         float x0, x1, o0, o1;
-        column_sum2(P.pq, col, col + kD / 2, P.nchunk, x0, x1);
-        rope_pair(x0, x1, cos_row, sin_row, dd, o0, o1);
+        if (e == tid && P.nchunk <= kPre) {  // column_sum2's order: chunk order from 0
+          x0 = 0.f;
+          x1 = 0.f;
+#pragma unroll
+          for (int i = 0; i < kPre; ++i) {
+            x0 += i < P.nchunk ? pre0[i] : 0.f;
+            x1 += i < P.nchunk ? pre1[i] : 0.f;
+          }
+          rope_pair_v(x0, x1, rc0, rc1, rs0, rs1, o0, o1);
+        } else {
+          column_sum2(P.pq, col, col + kD / 2, P.nchunk, x0, x1);
+          rope_pair(x0, x1, cos_row, sin_row, dd, o0, o1);
+        }
         s_q[hh][dd] = o0;
         s_q[hh][dd + kD / 2] = o1;
         if (writer) {
@@ -396,16 +467,29 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
       }
       if (writer) {
         const size_t slot = (static_cast<size_t>(kvh) * P.hot_cap + pos % P.hot_cap) * kD;
-        if (tid < kD / 2) {  // key pair (tid, tid + 64), RoPE'd
-          float x0, x1, o0, o1;
-          column_sum2(P.pk, kvh * kD + tid, kvh * kD + tid + kD / 2, P.nchunk, x0, x1);
-          rope_pair(x0, x1, cos_row, sin_row, tid, o0, o1);
+        float x0 = 0.f, x1 = 0.f;
+        if (tid < kD) {  // column_sum2's order: chunk order from 0
+          if (P.nchunk <= kPre) {
+#pragma unroll
+            for (int i = 0; i < kPre; ++i) {
+              x0 += i < P.nchunk ? prk0[i] : 0.f;
+              x1 += i < P.nchunk ? prk1[i] : 0.f;
+            }
+          } else {
+            const int c0 = kvh * kD + (tid & (kD / 2 - 1));
+            column_sum2(tid < kD / 2 ? P.pk : P.pv, c0, c0 + kD / 2, P.nchunk, x0, x1);
+          }
+        }
+        if (tid < kD / 2) {  // key pair (tid, tid + 64), RoPE'd (the factors of query element tid)
+          float o0, o1;
+          if (P.nchunk <= kPre)
+            rope_pair_v(x0, x1, rc0, rc1, rs0, rs1, o0, o1);
+          else
+            rope_pair(x0, x1, cos_row, sin_row, tid, o0, o1);
           P.k_ring[slot + tid] = f2h(o0);
           P.k_ring[slot + tid + kD / 2] = f2h(o1);
         } else if (tid < kD) {  // value dims (tid - 64, tid): no RoPE
           const int dd = tid - kD / 2;
-          float x0, x1;
-          column_sum2(P.pv, kvh * kD + dd, kvh * kD + dd + kD / 2, P.nchunk, x0, x1);
           P.v_ring[slot + dd] = f2h(x0);
           P.v_ring[slot + dd + kD / 2] = f2h(x1);
         }
@@ -423,19 +507,23 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
     } else if (P.PiK != nullptr) {
       // q_rot on MFMA (rotate_query_hilo), overlapping the first block's
       // loads; s_o is free until the merge.
+      float4 pik[8][2];
+      load_pik_operand(P.PiK, wave, lane, pik);
       u32x4 qb;
       {
         const uint4 u = *reinterpret_cast<const uint4*>(
             P.q + (static_cast<size_t>(b) * P.Hq + kvh * G + min(h, G - 1)) * kD + 32 * wave + 8 * g);
         qb = h < G ? u32x4{u.x, u.y, u.z, u.w} : u32x4{0u, 0u, 0u, 0u};
       }
-      rotate_query_hilo(P.PiK, qb, wave, lane, &s_o[0][0][0], kORow, f);
+      fetch_first(ra, t0);
+      rotate_query_hilo_loaded(pik, qb, wave, lane, &s_o[0][0][0], kORow, f);
       __syncthreads();  // s_o is written again by the merge
     } else {
       const float4* src = reinterpret_cast<const float4*>(
           P.qrot + (static_cast<size_t>(b) * P.Hq + kvh * G + min(h, G - 1)) * kD + 32 * g);
 #pragma unroll
       for (int i = 0; i < 8; ++i) f[i] = src[i];
+      fetch_first(ra, t0);
     }
     if constexpr (!PERM) s_lut[tid] = pack2h(c_lo, c_hi);
     const float sl = P.scale_log2;
