@@ -633,8 +633,9 @@ extern "C" int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_deco
   if (int e = check_layer_weights(L, x)) return e;
   LKV_REQUIRE(L->k_codes && L->k_norms && L->v_codes && L->v_norms && L->k_hot && L->v_hot && L->PiK && L->PiV,
               "decode_layer: null cache pointer");
-  LKV_REQUIRE(aligned16(L->k_codes) && aligned16(L->v_codes) && aligned16(L->k_hot) && aligned16(L->v_hot),
-              "decode_layer: cache buffers must be 16-byte aligned");
+  LKV_REQUIRE(aligned16(L->k_codes) && aligned16(L->v_codes) && aligned16(L->k_hot) && aligned16(L->v_hot) &&
+                  aligned16(L->PiK) && aligned16(L->PiV),
+              "decode_layer: cache buffers and rotations must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   uint16_t* xx = static_cast<uint16_t*>(x);

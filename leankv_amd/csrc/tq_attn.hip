@@ -94,7 +94,10 @@ struct AttnParams {
   uint16_t* v_ring;
 };
 
-__device__ __forceinline__ int rec_floats(int G) { return G * (2 + kD); }
+// A split record: G maxima, G sums, then (from a 16-byte boundary) G x 128
+// rotated value sums; records are whole 16-byte units.
+__host__ __device__ __forceinline__ int rec_acc_off(int G) { return (2 * G + 3) & ~3; }
+__host__ __device__ __forceinline__ int rec_floats(int G) { return rec_acc_off(G) + G * kD; }
 
 // Buffer resource over `bytes` bytes at base (raw addressing, stride 0).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -605,7 +608,7 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
         ls += wt * s_l[w][hh];
       }
     }
-    rec[2 * G + hh * kD + d] = acc;
+    rec[rec_acc_off(G) + hh * kD + d] = acc;
     if (d == 0) {
       rec[hh] = M;
       rec[G + hh] = ls;
@@ -630,16 +633,28 @@ __device__ __forceinline__ float dot8_f16(const uint4& a, const uint4& b) {
   return s;
 }
 
-// One block per (query head, batch).  Thread (d = tid % 128, quarter qd =
-// tid / 128) owns output dim d for the splits / hot tokens / PiV rows of its
-// quarter; the 4 quarters are summed through LDS in a fixed order.
+// One block per (query head, batch), 512 threads.  Every load is issued up
+// front and vectorised where the data is contiguous (the combine is bound by
+// load instructions and latency, not bytes):
+//   thread (dg = tid % 32, grp = tid / 32): PiV rows 8 grp .. 8 grp + 7 at
+//   dims 4 dg .. 4 dg + 3 (float4), and the rotated sums of splits grp, grp +
+//   16, ... at the same dims (float4);
+//   thread (dh = tid % 16, jg = tid / 16): hot values of slots jg and jg + 32
+//   at dims 8 dh .. 8 dh + 7 (16-byte loads);
+//   thread (j = tid / 8, part = tid % 8): the hot score of slot j, dims
+//   16 part .. 16 part + 15;  thread s < nsplit: split s's maximum and sum.
+// Partial sums over split groups, slot groups and PiV row groups are joined
+// through LDS in a fixed order.
+constexpr int kCombSplitGroups = kCombThreads / 32;  // 16
+constexpr int kCombSlotGroups = kCombThreads / 16;   // 32
 __global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnParams P) {  // 2 blocks per CU
   __shared__ float s_w[kMaxSplits];
   __shared__ float s_p[kHotMax];
   __shared__ float s_red[kCombWaves];
-  __shared__ __align__(16) float s_part[2][4][kD];
-  __shared__ float s_rot[kD], s_hv[kD];
-  __shared__ float s_o[4][kD];
+  __shared__ __align__(16) float s_cold[kCombSplitGroups][kD];
+  __shared__ __align__(16) float s_hot[kCombSlotGroups][kD];
+  __shared__ __align__(16) float s_rot[kD];
+  __shared__ float s_hv[kD];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   // Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its
@@ -660,14 +675,12 @@ __global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnPa
   const int RF = rec_floats(G);
   const float* recs = P.partials + bh * ns * RF;
   const size_t hot_base = bh * static_cast<size_t>(P.hot_cap) * kD;
-  const int d = tid & (kD - 1), qd = tid >> 7;
+  const int dg = tid & 31, grp = tid >> 5;  // PiV rows / split groups, 4 dims
+  const int dh = tid & 15, jg = tid >> 4;   // hot value slot groups, 8 dims
 
-  // ---- A. every load up front.  The hot window is walked by ring slot:
-  // softmax sums do not depend on token order, and slot j holds a current
-  // token exactly when j < hot_len (the window is the last hot_len tokens and
-  // token t sits in slot t % hot_cap), so no address depends on the length.
-  // Loads are unconditional from clamped, always valid addresses (split
-  // ns - 1, slot hot_cap - 1) and masked after, so all are in flight together.
+  // ---- A. every load up front, from clamped, always valid addresses (split
+  // ns - 1, slot hot_cap - 1), masked after.  The hot window is walked by ring
+  // slot: slot j holds a current token exactly when j < hot_len.
   float ms, ls;
   {
     const size_t sr = static_cast<size_t>(min(tid, ns - 1)) * RF;
@@ -675,20 +688,17 @@ __global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnPa
     ms = tid < ns ? m_ : -INFINITY;
     ls = tid < ns ? l_ : 0.f;
   }
-  float piv[32];
+  float4 pv[8];
 #pragma unroll
-  for (int k = 0; k < 32; ++k) piv[k] = P.PiV[(32 * qd + k) * kD + d];
-  uint16_t hv[kHotMax / 4];
+  for (int i = 0; i < 8; ++i) pv[i] = *reinterpret_cast<const float4*>(P.PiV + (8 * grp + i) * kD + 4 * dg);
+  uint4 hv[2];
 #pragma unroll
-  for (int i = 0; i < kHotMax / 4; ++i) {
-    const int jj = qd + 4 * i;
-    hv[i] = P.v_hot[hot_base + static_cast<size_t>(min(jj, P.hot_cap - 1)) * kD + d];
+  for (int i = 0; i < 2; ++i) {
+    const int jj = min(jg + 32 * i, P.hot_cap - 1);
+    hv[i] = *reinterpret_cast<const uint4*>(P.v_hot + hot_base + static_cast<size_t>(jj) * kD + 8 * dh);
   }
-  float ca[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    ca[i] = recs[static_cast<size_t>(min(qd + 4 * i, ns - 1)) * RF + 2 * G + hh * kD + d];
-
+  float4 ca = *reinterpret_cast<const float4*>(recs + static_cast<size_t>(min(grp, ns - 1)) * RF + rec_acc_off(G) + hh * kD +
+                                              4 * dg);
   // hot score partial: slot j = tid / 8, dims 16 * (tid % 8) .. +16
   const int j = tid >> 3, part = tid & 7;
   float sdot = 0.f;
@@ -728,49 +738,69 @@ __global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnPa
 #pragma unroll
   for (int w = 0; w < kCombWaves; ++w) Lt += s_red[w];
 
-  // ---- C. weighted sums of this quarter: rotated cold, unrotated hot
-  float cold = 0.f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int s = qd + 4 * i;
-    const float w = s < ns ? s_w[s] : 0.f;
-    cold += (w != 0.f) ? w * ca[i] : 0.f;
-  }
-  for (int s0 = 64; s0 < ns; s0 += 64) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      ca[i] = recs[static_cast<size_t>(min(s0 + qd + 4 * i, ns - 1)) * RF + 2 * G + hh * kD + d];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int s = s0 + qd + 4 * i;
-      const float w = s < ns ? s_w[s] : 0.f;
-      cold += (w != 0.f) ? w * ca[i] : 0.f;
+  // ---- C. partial sums: rotated cold sum of this split group (4 dims), hot
+  // value sum of this slot group (8 dims)
+  float4 cold = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < ns; s0 += kCombSplitGroups) {
+    const int sp = s0 + grp;
+    if (s0 > 0)
+      ca = *reinterpret_cast<const float4*>(recs + static_cast<size_t>(min(sp, ns - 1)) * RF + rec_acc_off(G) + hh * kD +
+                                            4 * dg);
+    const float w = sp < ns ? s_w[sp] : 0.f;
+    if (w != 0.f) {  // an empty split's sums were never written: select, do not multiply
+      cold.x = fmaf(w, ca.x, cold.x);
+      cold.y = fmaf(w, ca.y, cold.y);
+      cold.z = fmaf(w, ca.z, cold.z);
+      cold.w = fmaf(w, ca.w, cold.w);
     }
   }
-  float hot = 0.f;
+  *reinterpret_cast<float4*>(&s_cold[grp][4 * dg]) = cold;
+  float hs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < kHotMax / 4; ++i) {
-    const int jj = qd + 4 * i;
-    const float t = s_p[jj < hot_len ? jj : 0] * h2f(hv[i]);
-    hot += jj < hot_len ? t : 0.f;  // select after the product: an unwritten slot may hold NaN
+  for (int i = 0; i < 2; ++i) {
+    const int jj = jg + 32 * i;
+    if (jj < hot_len) {  // an unwritten slot may hold NaN: skipped, never multiplied
+      const float p = s_p[jj];
+      const uint32_t w4[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        hs[2 * e] = fmaf(p, h2f(static_cast<uint16_t>(w4[e] & 0xffffu)), hs[2 * e]);
+        hs[2 * e + 1] = fmaf(p, h2f(static_cast<uint16_t>(w4[e] >> 16)), hs[2 * e + 1]);
+      }
+    }
   }
-  s_part[0][qd][d] = cold;
-  s_part[1][qd][d] = hot;
+  *reinterpret_cast<float4*>(&s_hot[jg][8 * dh]) = make_float4(hs[0], hs[1], hs[2], hs[3]);
+  *reinterpret_cast<float4*>(&s_hot[jg][8 * dh + 4]) = make_float4(hs[4], hs[5], hs[6], hs[7]);
   __syncthreads();
   if (tid < kD) {
-    s_rot[tid] = ((s_part[0][0][tid] + s_part[0][1][tid]) + s_part[0][2][tid]) + s_part[0][3][tid];
-    s_hv[tid] = ((s_part[1][0][tid] + s_part[1][1][tid]) + s_part[1][2][tid]) + s_part[1][3][tid];
+    float c = 0.f, h = 0.f;
+#pragma unroll
+    for (int g2 = 0; g2 < kCombSplitGroups; ++g2) c += s_cold[g2][tid];
+#pragma unroll
+    for (int g2 = 0; g2 < kCombSlotGroups; ++g2) h += s_hot[g2][tid];
+    s_rot[tid] = c;
+    s_hv[tid] = h;
   }
   __syncthreads();
 
-  // ---- D. un-rotate the cold sum: out[d] = sum_k rot[k] PiV[k][d]
-  float o = 0.f;
+  // ---- D. un-rotate the cold sum: out[d] = sum_k rot[k] PiV[k][d], this
+  // thread's 8 rows for its 4 dims, then the 16 row groups in order
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int k = 0; k < 32; ++k) o = fmaf(s_rot[32 * qd + k], piv[k], o);
-  s_o[qd][d] = o;
+  for (int i = 0; i < 8; ++i) {
+    const float r = s_rot[8 * grp + i];
+    o.x = fmaf(r, pv[i].x, o.x);
+    o.y = fmaf(r, pv[i].y, o.y);
+    o.z = fmaf(r, pv[i].z, o.z);
+    o.w = fmaf(r, pv[i].w, o.w);
+  }
+  *reinterpret_cast<float4*>(&s_cold[grp][4 * dg]) = o;  // s_cold is free again
   __syncthreads();
   if (tid < kD) {
-    const float r = (((s_o[0][tid] + s_o[1][tid]) + s_o[2][tid]) + s_o[3][tid]) + s_hv[tid];
+    float r = 0.f;
+#pragma unroll
+    for (int g2 = 0; g2 < kCombSplitGroups; ++g2) r += s_cold[g2][tid];
+    r += s_hv[tid];
     P.out[(static_cast<size_t>(b) * P.Hq + hq) * kD + tid] = f2h(Lt > 0.f ? r / Lt : 0.f);
   }
 }
@@ -861,7 +891,7 @@ AttnPlan attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t 
   p.qrot_off = kTicketBytes;  // keeps the shared workspace layout: ticket area first
   p.part_off = p.qrot_off + al(static_cast<size_t>(B * Hq * kD) * 4);
   // sized for ns_cap so a workspace sized without hot_cap fits every call
-  p.total = p.part_off + al(static_cast<size_t>(B * Hkv * ns_cap * G * (2 + kD)) * 4);
+  p.total = p.part_off + al(static_cast<size_t>(B * Hkv * ns_cap) * rec_floats(static_cast<int>(G)) * 4);
   return p;
 }
 
@@ -963,8 +993,8 @@ extern "C" int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const f
                   seq_len && out && workspace,
               "tq_decode_attn: null pointer");
   LKV_REQUIRE(aligned16(q) && aligned16(k_codes) && aligned16(v_codes) && aligned16(k_hot) && aligned16(v_hot) &&
-                  aligned16(PiK) && aligned16(out) && aligned16(workspace),
-              "tq_decode_attn: q, codes, hot, PiK, out and workspace must be 16-byte aligned");
+                  aligned16(PiK) && aligned16(PiV) && aligned16(out) && aligned16(workspace),
+              "tq_decode_attn: q, codes, hot, PiK, PiV, out and workspace must be 16-byte aligned");
   const AttnPlan pl = attn_plan(B, Hq, Hkv, max_len, hot_cap);
   LKV_REQUIRE(workspace_bytes >= pl.total, "tq_decode_attn: workspace of %zu bytes required, got %zu", pl.total,
               workspace_bytes);
@@ -1047,9 +1077,9 @@ extern "C" int lkv_tq_paged_decode_attn(const void* q, const uint8_t* k_codes, c
                   kv_indptr && kv_indices && seq_lens && out && workspace,
               "tq_paged_decode_attn: null pointer");
   LKV_REQUIRE(aligned16(q) && aligned16(k_codes) && aligned16(v_codes) && aligned16(k_norms) &&
-                  aligned16(v_norms) && aligned16(k_hot) && aligned16(v_hot) && aligned16(PiK) && aligned16(out) &&
-                  aligned16(workspace),
-              "tq_paged_decode_attn: q, pools, hot rings, PiK, out and workspace must be 16-byte aligned");
+                  aligned16(v_norms) && aligned16(k_hot) && aligned16(v_hot) && aligned16(PiK) && aligned16(PiV) &&
+                  aligned16(out) && aligned16(workspace),
+              "tq_paged_decode_attn: q, pools, hot rings, PiK, PiV, out and workspace must be 16-byte aligned");
   const AttnPlan pl = paged_plan(B, Hq, Hkv, max_len, hot_cap, page_size);
   LKV_REQUIRE(pl.nsplit <= kMaxSplits - 1, "tq_paged_decode_attn: max_len=%lld needs %d splits (at most %d)",
               (long long)max_len, pl.nsplit, kMaxSplits - 1);
