@@ -25,6 +25,8 @@
 // then a combine kernel, one block per (batch, query head), merges the split
 // records.  Page indices are clamped to the pool, lengths to the pages owned,
 // so malformed tables cannot address memory outside the pool.
+#include <stdlib.h>
+
 #include "kernels.h"
 #include "tq_attn_common.h"
 
@@ -51,7 +53,10 @@ struct PagedParams {
   int Hq, Hkv, G, ps, nsplit, split_tokens, max_pages;
 };
 
-__device__ __forceinline__ int rec_floats(int G) { return G * (2 + kD); }
+// A split record: G maxima, G sums, then (from a 16-byte boundary) G x 128
+// value sums; records are whole 16-byte units.
+__host__ __device__ __forceinline__ int rec_acc_off(int G) { return (2 * G + 3) & ~3; }
+__host__ __device__ __forceinline__ int rec_floats(int G) { return rec_acc_off(G) + G * kD; }
 
 // Tokens of sequence b (0 without pages); its first page-table entry.
 __device__ __forceinline__ int seq_tokens(const PagedParams& P, int b, int& first) {
@@ -70,9 +75,20 @@ __device__ __forceinline__ size_t kv_offset(const PagedParams& P, int first, int
          static_cast<size_t>(kvh) * kD;
 }
 
+constexpr int kMaxPg = 256;  // page ids of one split staged in LDS (SMALLG path)
+
+// SMALLG (at most 4 query heads per kv head, the split's pages staged in LDS):
+// a chunk's key rows (score lanes) and value rows (value lanes: 8-dim group
+// lane % 16, tokens lane / 16 + 4 i) are loaded together, one memory round
+// trip per chunk, every value row once; each value lane accumulates all G
+// heads over its tokens and the 4 token lanes of a dim group are summed at
+// the end.  Otherwise: page offsets through LDS, value rows per (8-dim group,
+// head) lane in batches of 8.
+template <bool SMALLG>
 __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
   __shared__ float s_p[kWaves][16][kChunk];
-  __shared__ size_t s_off[kWaves][kChunk];  // pool offset of each chunk token's value row
+  __shared__ size_t s_off[SMALLG ? 1 : kWaves][kChunk];  // pool offset of each chunk token's value row
+  __shared__ int s_pg[SMALLG ? kMaxPg + 1 : 1];
   __shared__ float s_alpha[kWaves][16];
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
   __shared__ __align__(16) float s_o[kWaves][16][kORow];
@@ -96,6 +112,22 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
     }
     return;
   }
+  const int pg0 = t_begin / P.ps;  // SMALLG: first page of the split
+  if constexpr (SMALLG) {
+    const int np = P.indptr[b + 1] - first;
+    const int npg = (t_end - 1) / P.ps - pg0 + 1;  // <= kMaxPg + 1 (host plan)
+    for (int i = tid; i < npg; i += kThreads) {
+      const int pi = min(pg0 + i, np - 1);
+      s_pg[i] = min(max(P.indices[first + pi], 0), P.max_pages - 1);
+    }
+    __syncthreads();
+  }
+  // pool offset of (token t of the split's range, side) for SMALLG
+  auto off_of = [&](int t, int side) -> size_t {
+    const int page = s_pg[t / P.ps - pg0];
+    return ((static_cast<size_t>(page) * 2 + side) * P.ps + t % P.ps) * (static_cast<size_t>(P.Hkv) * kD) +
+           static_cast<size_t>(kvh) * kD;
+  };
 
   // B operand: query x scale * log2(e), head h (rows h >= G zero), dims 32 kb + 8 g + i
   u32x4 qa[4];
@@ -121,67 +153,69 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[k][j] = 0.f;
 
-  for (int c = t_begin + kChunk * wave; c < t_end; c += kChunk * kWaves) {
-    // ---- scores: tokens c + 16 tt + (lane % 16) as A rows
-    f32x4 sc[2];
+  const int dv = lane & 15, sub = lane >> 4;  // SMALLG value layout: 8-dim group, token lane
+  if constexpr (SMALLG) {
+    for (int c = t_begin + kChunk * wave; c < t_end; c += kChunk * kWaves) {
+      // ---- loads: key rows of tokens c + 16 tt + (lane % 16), value rows of
+      // tokens c + lane / 16 + 4 i (clamped valid tokens, masked below)
+      u32x4 a[2][4];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int tok = min(c + 16 * tt + h, t_end - 1);  // clamped valid token, masked below
-      const size_t off = kv_offset(P, first, tok, kvh, 0);
-      if (g == 0) s_off[wave][16 * tt + h] = off + static_cast<size_t>(P.ps) * P.Hkv * kD;  // its value row
-      const uint16_t* kp = P.kv + off + 8 * g;
-      u32x4 a[4];
+      for (int tt = 0; tt < 2; ++tt) {
+        const uint16_t* kp = P.kv + off_of(min(c + 16 * tt + h, t_end - 1), 0) + 8 * g;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const uint4 u = *reinterpret_cast<const uint4*>(kp + 32 * kb);
-        a[kb] = u32x4{u.x, u.y, u.z, u.w};
+        for (int kb = 0; kb < 4; ++kb) {
+          const uint4 u = *reinterpret_cast<const uint4*>(kp + 32 * kb);
+          a[tt][kb] = u32x4{u.x, u.y, u.z, u.w};
+        }
       }
-      sc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      uint4 vr[8];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) sc[tt] = mfma16x16x32(a[kb], qa[kb], sc[tt]);
-    }
-    // D: lane holds head h, tokens c + 16 tt + 4 g + i
-    float s[8];
+      for (int i = 0; i < 8; ++i)
+        vr[i] = *reinterpret_cast<const uint4*>(P.kv + off_of(min(c + sub + 4 * i, t_end - 1), 1) + 8 * dv);
+      // ---- scores, online softmax (lane: head h, tokens c + 16 tt + 4 g + i)
+      f32x4 sc[2];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+      for (int tt = 0; tt < 2; ++tt) {
+        sc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[4 * tt + i] = c + 16 * tt + 4 * g + i < t_end ? sc[tt][i] : -INFINITY;
-    float mx = s[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) mx = vmax(mx, s[j]);
-    mx = xgroup_max(mx);
-    const float mn = fmaxf(m, mx);  // finite: the chunk holds at least one token
-    const float alpha = fast_exp2(m - mn);
-    m = mn;
-    float ps = 0.f;
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = fast_exp2(s[4 * tt + i] - mn);
-        ps += p;
-        s_p[wave][h][16 * tt + 4 * g + i] = p;
+        for (int kb = 0; kb < 4; ++kb) sc[tt] = mfma16x16x32(a[tt][kb], qa[kb], sc[tt]);
       }
-    lsum = lsum * alpha + ps;
-    if (g == 0) s_alpha[wave][h] = alpha;
-    __builtin_amdgcn_wave_barrier();
-    // ---- values: lane (dims 8 dg .., heads hq + 4 k) over the chunk's tokens
+      float s[8];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float al = s_alpha[wave][hq + 4 * k];
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[k][j] *= al;
-    }
-    // the chunk's 32 value rows, 8 loads in flight per group; tokens past the
-    // end read the last valid row (clamped offsets) with p = 0
+        for (int i = 0; i < 4; ++i) s[4 * tt + i] = c + 16 * tt + 4 * g + i < t_end ? sc[tt][i] : -INFINITY;
+      float mx = s[0];
 #pragma unroll
-    for (int t0 = 0; t0 < kChunk; t0 += 8) {
-      uint4 u[8];
+      for (int j = 1; j < 8; ++j) mx = vmax(mx, s[j]);
+      mx = xgroup_max(mx);
+      const float mn = fmaxf(m, mx);  // finite: the chunk holds at least one token
+      const float alpha = fast_exp2(m - mn);
+      m = mn;
+      float ps = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) u[i] = *reinterpret_cast<const uint4*>(P.kv + s_off[wave][t0 + i] + 8 * dg);
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = fast_exp2(s[4 * tt + i] - mn);
+          ps += p;
+          s_p[wave][h][16 * tt + 4 * g + i] = p;
+        }
+      lsum = lsum * alpha + ps;
+      if (g == 0) s_alpha[wave][h] = alpha;
+      __builtin_amdgcn_wave_barrier();
+      // ---- values: this lane's tokens for every head
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (k < G) {
+          const float al = s_alpha[wave][k];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[k][j] *= al;
+        }
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+        const uint32_t w[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
         float v[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -190,15 +224,103 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          if (hq + 4 * k < G) {  // lanes past the G heads skip
-            const float p = s_p[wave][hq + 4 * k][t0 + i];
+          if (k < G) {
+            const float p = s_p[wave][k][sub + 4 * i];  // 0 for tokens past the end
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[k][j] = fmaf(p, v[j], acc[k][j]);
           }
         }
       }
+      __builtin_amdgcn_wave_barrier();
     }
-    __builtin_amdgcn_wave_barrier();
+    // the 4 token lanes of each dim group (lanes dv, dv + 16, dv + 32, dv + 48)
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        acc[k][j] += __shfl_xor(acc[k][j], 16);
+        acc[k][j] += __shfl_xor(acc[k][j], 32);
+      }
+  } else {
+    for (int c = t_begin + kChunk * wave; c < t_end; c += kChunk * kWaves) {
+      // ---- scores: tokens c + 16 tt + (lane % 16) as A rows
+      f32x4 sc[2];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int tok = min(c + 16 * tt + h, t_end - 1);  // clamped valid token, masked below
+        const size_t off = kv_offset(P, first, tok, kvh, 0);
+        if (g == 0) s_off[wave][16 * tt + h] = off + static_cast<size_t>(P.ps) * P.Hkv * kD;  // its value row
+        const uint16_t* kp = P.kv + off + 8 * g;
+        u32x4 a[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const uint4 u = *reinterpret_cast<const uint4*>(kp + 32 * kb);
+          a[kb] = u32x4{u.x, u.y, u.z, u.w};
+        }
+        sc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) sc[tt] = mfma16x16x32(a[kb], qa[kb], sc[tt]);
+      }
+      // D: lane holds head h, tokens c + 16 tt + 4 g + i
+      float s[8];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[4 * tt + i] = c + 16 * tt + 4 * g + i < t_end ? sc[tt][i] : -INFINITY;
+      float mx = s[0];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) mx = vmax(mx, s[j]);
+      mx = xgroup_max(mx);
+      const float mn = fmaxf(m, mx);  // finite: the chunk holds at least one token
+      const float alpha = fast_exp2(m - mn);
+      m = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = fast_exp2(s[4 * tt + i] - mn);
+          ps += p;
+          s_p[wave][h][16 * tt + 4 * g + i] = p;
+        }
+      lsum = lsum * alpha + ps;
+      if (g == 0) s_alpha[wave][h] = alpha;
+      __builtin_amdgcn_wave_barrier();
+      // ---- values: lane (dims 8 dg .., heads hq + 4 k) over the chunk's tokens
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float al = s_alpha[wave][hq + 4 * k];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[k][j] *= al;
+      }
+      // the chunk's 32 value rows, 8 loads in flight per group; tokens past the
+      // end read the last valid row (clamped offsets) with p = 0
+#pragma unroll
+      for (int t0 = 0; t0 < kChunk; t0 += 8) {
+        uint4 u[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) u[i] = *reinterpret_cast<const uint4*>(P.kv + s_off[wave][t0 + i] + 8 * dg);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[2 * e] = h2f(static_cast<uint16_t>(w[e] & 0xffffu));
+            v[2 * e + 1] = h2f(static_cast<uint16_t>(w[e] >> 16));
+          }
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            if (hq + 4 * k < G) {  // lanes past the G heads skip
+              const float p = s_p[wave][hq + 4 * k][t0 + i];
+#pragma unroll
+              for (int j = 0; j < 8; ++j) acc[k][j] = fmaf(p, v[j], acc[k][j]);
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
   }
 
   // ---- merge the 4 waves (a wave without a chunk keeps m = -inf, l = 0, o = 0)
@@ -209,7 +331,8 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
   }
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    float4* dst = reinterpret_cast<float4*>(&s_o[wave][hq + 4 * k][8 * dg]);
+    if (SMALLG && sub != 0) continue;  // SMALLG: lanes 0..15 hold the sums, head k
+    float4* dst = reinterpret_cast<float4*>(SMALLG ? &s_o[wave][k][8 * dv] : &s_o[wave][hq + 4 * k][8 * dg]);
     dst[0] = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
     dst[1] = make_float4(acc[k][4], acc[k][5], acc[k][6], acc[k][7]);
   }
@@ -228,7 +351,7 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
         l += wt * s_l[w][hh];
       }
     }
-    rec[2 * G + hh * kD + d] = o;
+    rec[rec_acc_off(G) + hh * kD + d] = o;
     if (d == 0) {
       rec[hh] = M;
       rec[G + hh] = l;
@@ -236,34 +359,84 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
   }
 }
 
-// One block of 128 threads per (query head, batch): merge the split records.
-__global__ __launch_bounds__(kD) void paged_combine_kernel(PagedParams P) {
+// One block of 256 threads per (query head, batch): merge the split records.
+// Thread s < nsplit reads split s's maximum and sum (block max / sum through
+// the waves); thread (dg = tid % 32, grp = tid / 32) reads the value sums of
+// splits grp, grp + 8, ... at dims 4 dg .. 4 dg + 3 (float4), all issued
+// before the first wait; the 8 split groups are joined in LDS in order.
+constexpr int kPcThreads = 256;
+constexpr int kPcGroups = kPcThreads / 32;
+constexpr int kPcDepth = 4;  // value sums per thread loaded up front (more splits: further passes)
+__global__ __launch_bounds__(kPcThreads) void paged_combine_kernel(PagedParams P) {
   __shared__ float s_w[kMaxSplits];
-  __shared__ float s_red[2];
-  const int d = threadIdx.x, hq = blockIdx.x, b = blockIdx.y;
+  __shared__ float s_red[kPcThreads / 64];
+  __shared__ __align__(16) float s_o[kPcGroups][kD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hq = blockIdx.x, b = blockIdx.y;
   const int G = P.G, kvh = hq / G, hh = hq % G, ns = P.nsplit, RF = rec_floats(G);
   const float* recs = P.partials + (static_cast<size_t>(b) * P.Hkv + kvh) * ns * RF;
-  if (d == 0) {
-    float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, recs[s * RF + hh]);
-    float L = 0.f;
-    for (int s = 0; s < ns; ++s) {
-      const float ms = recs[s * RF + hh];
-      const float w = ms == -INFINITY ? 0.f : fast_exp2(ms - M);
-      s_w[s] = w;
-      L += w * recs[s * RF + G + hh];
-    }
-    s_red[0] = L;
+  const int dg = tid & 31, grp = tid >> 5;
+  float ms, ls;
+  {
+    const size_t sr = static_cast<size_t>(min(tid, ns - 1)) * RF;
+    const float m_ = recs[sr + hh], l_ = recs[sr + G + hh];
+    ms = tid < ns ? m_ : -INFINITY;
+    ls = tid < ns ? l_ : 0.f;
   }
+  float4 ov[kPcDepth];
+#pragma unroll
+  for (int i = 0; i < kPcDepth; ++i)
+    ov[i] = *reinterpret_cast<const float4*>(recs + static_cast<size_t>(min(grp + kPcGroups * i, ns - 1)) * RF +
+                                             rec_acc_off(G) + hh * kD + 4 * dg);
+  float v = wave_max(ms);
+  if (lane == 0) s_red[wave] = v;
   __syncthreads();
-  float o = 0.f;
-  for (int s = 0; s < ns; ++s) {
-    const float w = s_w[s];
-    const float v = recs[s * RF + 2 * G + hh * kD + d];
-    o += w != 0.f ? w * v : 0.f;  // a split with no tokens left its o unwritten
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kPcThreads / 64; ++w) M = fmaxf(M, s_red[w]);
+  __syncthreads();
+  const float w_s = (tid < ns && ms != -INFINITY) ? fast_exp2(ms - M) : 0.f;
+  if (tid < ns) s_w[tid] = w_s;
+  float lv = wave_sum(w_s * ls);
+  if (lane == 0) s_red[wave] = lv;
+  __syncthreads();
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < kPcThreads / 64; ++w) L += s_red[w];
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < ns; s0 += kPcGroups * kPcDepth) {
+#pragma unroll
+    for (int i = 0; i < kPcDepth; ++i) {
+      const int sp = s0 + grp + kPcGroups * i;
+      if (s0 > 0)
+        ov[i] = *reinterpret_cast<const float4*>(recs + static_cast<size_t>(min(sp, ns - 1)) * RF + rec_acc_off(G) +
+                                                 hh * kD + 4 * dg);
+      const float w = sp < ns ? s_w[sp] : 0.f;
+      if (w != 0.f) {  // a split with no tokens left its sums unwritten: select, never multiply
+        o.x = fmaf(w, ov[i].x, o.x);
+        o.y = fmaf(w, ov[i].y, o.y);
+        o.z = fmaf(w, ov[i].z, o.z);
+        o.w = fmaf(w, ov[i].w, o.w);
+      }
+    }
   }
-  const float L = s_red[0];
-  P.out[(static_cast<size_t>(b) * P.Hq + hq) * kD + d] = f2h(L > 0.f ? o / L : 0.f);
+  *reinterpret_cast<float4*>(&s_o[grp][4 * dg]) = o;
+  __syncthreads();
+  if (tid < kD) {
+    float r = 0.f;
+#pragma unroll
+    for (int g2 = 0; g2 < kPcGroups; ++g2) r += s_o[g2][tid];
+    P.out[(static_cast<size_t>(b) * P.Hq + hq) * kD + tid] = f2h(L > 0.f ? r / L : 0.f);
+  }
+}
+
+// Fewest tokens per split (LKV_PAGED_MIN_SPLIT_TOKENS overrides, tuning sweeps).
+int64_t paged_min_split_tokens() {
+  static const int64_t k = [] {
+    const char* env = getenv("LKV_PAGED_MIN_SPLIT_TOKENS");
+    const long v = env ? atol(env) : 256;
+    return static_cast<int64_t>(v > 0 && v <= (1 << 20) ? v : 256);
+  }();
+  return k;
 }
 
 struct PagedPlan {
@@ -278,11 +451,12 @@ PagedPlan paged_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len) {
   ns = ns < 1 ? 1 : (ns > kMaxSplits ? kMaxSplits : ns);
   constexpr int64_t gran = kChunk * kWaves;
   int64_t ts = (max(max_len, int64_t{1}) + ns - 1) / ns;
+  if (ts < paged_min_split_tokens()) ts = paged_min_split_tokens();
   ts = (ts + gran - 1) / gran * gran;
   ns = (max(max_len, int64_t{1}) + ts - 1) / ts;
   p.nsplit = static_cast<int>(ns);
   p.split_tokens = static_cast<int>(ts);
-  p.bytes = static_cast<size_t>(B * Hkv * ns * (Hq / Hkv) * (2 + kD)) * 4 + 256;
+  p.bytes = static_cast<size_t>(B * Hkv * ns) * rec_floats(static_cast<int>(Hq / Hkv)) * 4 + 256;
   return p;
 }
 
@@ -335,12 +509,16 @@ extern "C" int lkv_paged_decode_attn(const void* q, const void* kv_data, const i
   P.split_tokens = pl.split_tokens;
   P.max_pages = static_cast<int>(max_pages);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(paged_split_kernel, dim3(static_cast<unsigned>(pl.nsplit), static_cast<unsigned>(Hkv),
-                                              static_cast<unsigned>(B)),
-                     dim3(kThreads), 0, st, P);
+  const dim3 grid(static_cast<unsigned>(pl.nsplit), static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
+  // the SMALLG path stages a split's pages in LDS: (ts - 1) / ps + 2 of them at most
+  const bool small = Hq / Hkv <= 4 && (pl.split_tokens - 1) / page_size + 2 <= kMaxPg + 1;
+  if (small)
+    hipLaunchKernelGGL((paged_split_kernel<true>), grid, dim3(kThreads), 0, st, P);
+  else
+    hipLaunchKernelGGL((paged_split_kernel<false>), grid, dim3(kThreads), 0, st, P);
   LKV_LAUNCH_CHECK("paged_decode_attn split");
-  hipLaunchKernelGGL(paged_combine_kernel, dim3(static_cast<unsigned>(Hq), static_cast<unsigned>(B)), dim3(kD), 0,
-                     st, P);
+  hipLaunchKernelGGL(paged_combine_kernel, dim3(static_cast<unsigned>(Hq), static_cast<unsigned>(B)),
+                     dim3(kPcThreads), 0, st, P);
   LKV_LAUNCH_CHECK("paged_decode_attn combine");
   return LKV_OK;
 }
