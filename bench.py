@@ -16,6 +16,9 @@ Workloads:
           threshold on the timed tokens (replayed through the HF path, whose activations equal
           the engine's) and reports bytes per token over ms_per_step.
           value = decode tok/s of the LeanKV engine (prefill excluded).
+  dense   the dense fp16 baseline of config 5 alone: this library's decode step with every
+          threshold 0 and an fp16 KV cache in 16-token pages (OwnDenseEngine), graph-captured;
+          value = tok/s, step_roofline = dense bytes per token / ms_per_step (for profiling it)
   gemv    config 1: TEAL sparse GEMV W[4096,14336], x ~Laplace(0,.05), 40 % sparse
   mlp     config 2: fused gate/up SwiGLU [14336,4096] + sparse down [4096,14336]
   quant   config 3: TurboQuant 3-bit quantize of K,V [8,4096,128] (fp32 MFMA rotation)
@@ -60,8 +63,9 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "mlp", "quant", "attn", "prefill",
-                                                                    "batched", "paged", "tqpaged", "prod", "copy"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "dense", "gemv", "mlp", "quant", "attn",
+                                                                    "prefill", "batched", "paged", "tqpaged", "prod",
+                                                                    "copy"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=32, help="decoder layers (config 5 uses 32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -1090,6 +1094,59 @@ def bench_decode(args, torch):
     return res
 
 
+def bench_dense(args, torch):
+    """The dense fp16 baseline alone (OwnDenseEngine at config 5), prefill excluded."""
+    from transformers import DynamicCache
+
+    from leankv_amd.engine import OwnDenseEngine, random_mistral
+
+    if args.steps is None:
+        args.steps = 64
+    if args.warmup is None:
+        args.warmup = 4
+    dev = torch.device("cuda:0")
+    model = random_mistral(device=dev, seed=0, num_hidden_layers=args.layers)
+    cfg = model.config
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, cfg.vocab_size, (1, args.prompt), generator=g).to(dev)
+    max_len = args.prompt + args.warmup + args.steps + 2
+    with torch.no_grad():
+        dc = DynamicCache(config=cfg)
+        out = model(prompt, past_key_values=dc, use_cache=True)
+        first = torch.argmax(out.logits[0, -1])
+        del out
+    eng = OwnDenseEngine(model, max_len)
+    eng.start(first, eng.load_cache(dc))
+    del dc
+    torch.cuda.empty_cache()
+    with torch.no_grad():
+        eng.step()
+        eng.capture()
+        for _ in range(args.warmup - 1):
+            eng.step()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(args.steps):
+            eng.step()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t
+    L, Hkv, hid, ffn, voc = (cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.hidden_size,
+                             cfg.intermediate_size, cfg.vocab_size)
+    nq, nkv = cfg.num_attention_heads * 128, Hkv * 128
+    ctx = args.prompt + args.warmup + (args.steps - 1) / 2
+    dense_bytes = L * 2 * (hid * (nq + 2 * nkv) + nq * hid + 3 * hid * ffn) + hid * voc * 2 + L * Hkv * (ctx + 1) * 512
+    ms = dt * 1e3 / args.steps
+    return {
+        "metric": "B=1 dense fp16 decode tok/s (Mistral-7B shape, this library's kernels, threshold 0)",
+        "value": round(args.steps / dt, 2), "unit": "tok/s", "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "dtype": "f16 (fp32 accumulate)",
+        "config": {"workload": "config5_dense_fp16_own_kernels", "layers": L, "prompt": args.prompt, "batch": 1},
+        "step_roofline": {"bytes_per_token": int(dense_bytes), "achieved_GBs": round(dense_bytes / ms / 1e6, 1),
+                          "frac": round(dense_bytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                          "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / dense_bytes, 1)},
+    }
+
+
 def _log(msg):
     print("[bench] " + msg, file=sys.stderr, flush=True)
 
@@ -1130,7 +1187,7 @@ def _run_workload(args, torch):
             res["roofline"] = roofline_gateup(args, torch)
     else:
         _fill_gemv_defaults(args)
-        fn = {"gemv": bench_gemv, "mlp": bench_mlp, "copy": bench_copy, "quant": bench_quant,
+        fn = {"dense": bench_dense, "gemv": bench_gemv, "mlp": bench_mlp, "copy": bench_copy, "quant": bench_quant,
               "attn": bench_attn, "prefill": bench_prefill, "batched": bench_batched,
               "paged": bench_paged, "tqpaged": bench_tq_paged, "prod": bench_prod}.get(args.workload)
         if fn is None:
