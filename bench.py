@@ -95,7 +95,9 @@ def _timed_loop(launch, nsets, steps, warmup, torch):
 
 def _kernel_time(launch, nsets, steps, warmup, torch, batch=10):
     """Average duration of one launch: HIP events around batches of `batch` back-to-back launches on the
-    launching stream (a lone launch between two events also times its dispatch latency)."""
+    launching stream (a lone launch between two events also times its dispatch latency).  For a kernel of
+    ~13 us the host must issue a launch in less than that or the events time the host instead: the GEMV
+    rooflines launch through a pre-bound C entry point (_fast_partials) for that reason."""
     for i in range(warmup):
         launch(i % nsets)
     torch.cuda.synchronize()
@@ -109,6 +111,20 @@ def _kernel_time(launch, nsets, steps, warmup, torch, batch=10):
     torch.cuda.synchronize()
     per = [a.elapsed_time(b) / batch for a, b in evs]
     return statistics.mean(per), statistics.median(per)
+
+
+def _bound(name, *args):
+    """A launch closure over one C entry point with its arguments converted once (ints, floats, pointers):
+    the per-launch host cost is one ctypes call, so back-to-back launches of a ~13 us kernel are not spaced
+    by Python-side argument checks.  The caller has made the same call through the checked wrapper first."""
+    from leankv_amd import _lib
+    fn = getattr(_lib.load(), name)
+
+    def call(_i=None):
+        rc = fn(*args)
+        if rc != 0:
+            raise _lib.LeanKVError("%s failed: %s" % (name, _lib.last_error()))
+    return call
 
 
 def _cpu_info():
@@ -136,6 +152,7 @@ def _cpu_info():
 # ------------------------------------------------------------------ config 1
 def bench_gemv(args, torch):
     from leankv_amd import kernels
+    from leankv_amd._lib import workspaces
 
     dev = torch.device("cuda:0")
     N, Z = 4096, 14336
@@ -153,7 +170,13 @@ def bench_gemv(args, torch):
     def launch(i):
         x, Wc, t, _, y = sets[i]
         kernels.sparse_gemv_out(x, Wc, t, y)
-    wall, omean, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
+    wall, eager, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
+    lib = kernels._lib_handle()
+    ws = workspaces.get(dev, "gemv", lib.lkv_sparse_gemv_workspace_bytes(N, Z))
+    st = torch.cuda.current_stream().cuda_stream
+    fast = [_bound("lkv_sparse_gemv", x.data_ptr(), Wc.data_ptr(), float(t), N, Z, y.data_ptr(), ws.data_ptr(),
+                   ws.numel(), st) for x, Wc, t, _, y in sets]
+    omean, _ = _kernel_time(lambda i: fast[i](), len(sets), args.steps, args.warmup, torch)
     surv = statistics.mean(s[3] for s in sets)
     alg_bytes = surv * N * 2 + Z * 2 + N * 2
     roof = _roofline_partials(torch, [(s[0], s[1], s[2], None, 0.0) for s in sets], N, Z, alg_bytes,
@@ -163,11 +186,15 @@ def bench_gemv(args, torch):
         "value": round(alg_bytes / (omean * 1e-3) / 1e9, 1),
         "unit": "GB/s",
         "ms_per_step": round(wall, 5),
+        "op_us_back_to_back": round(omean * 1e3, 3),
+        "op_us_eager_call": round(eager * 1e3, 3),
         "higher_is_better": True,
         "dtype": "f16 (fp32 accumulate)",
         "config": {"workload": "config1_sparse_gemv", "N": N, "Z": Z, "sparsity": 0.4,
                    "buffer_sets": len(sets), "working_set_MB": round(len(sets) * N * Z * 2 / 1e6),
-                   "what": "value: whole op (split-K pass + chunk reduction) per call; roofline: split-K pass"},
+                   "what": "value: whole op (split-K pass + chunk reduction) per call, calls issued back to "
+                           "back through the C entry point; op_us_eager_call: one call through the Python "
+                           "wrapper between two events; roofline: split-K pass"},
         "roofline": roof,
     }
     if not args.no_cpu_baseline:
@@ -192,10 +219,13 @@ def _roofline_partials(torch, sets, N, Z, alg_bytes, steps, warmup, name, key=No
     from leankv_amd import kernels
 
     outs = [kernels.sparse_gemv_partials(x, wg, tg, wu, tu) for x, wg, tg, wu, tu in sets]
+    st = torch.cuda.current_stream().cuda_stream
+    fast = [_bound("lkv_sparse_gemv_partials", x.data_ptr(), wg.data_ptr(), None if wu is None else wu.data_ptr(),
+                   float(tg), float(tu), N, Z, o.data_ptr(), o.numel() * 4, st)
+            for (x, wg, tg, wu, tu), o in zip(sets, outs)]
 
     def launch(i):
-        x, wg, tg, wu, tu = sets[i]
-        kernels.sparse_gemv_partials(x, wg, tg, wu, tu, out=outs[i])
+        fast[i]()
     kmean, kmed = _kernel_time(launch, len(sets), steps, warmup, torch)
     _, single, _ = _timed_loop(launch, len(sets), steps // 2, 0, torch)
     achieved = alg_bytes / (kmean * 1e-3) / 1e9
@@ -297,6 +327,7 @@ def bench_mlp(args, torch):
     value: algorithmic bytes of both ops / their combined time per call; roofline: the gate/up
     split-K pass alone (the decode step's dominant kernel)."""
     from leankv_amd import kernels
+    from leankv_amd._lib import workspaces
 
     dev = torch.device("cuda:0")
     H, F = 4096, 14336
@@ -319,7 +350,23 @@ def bench_mlp(args, torch):
         x, wg, wu, wd, tx, th, h, y = sets[i]
         kernels.sparse_gateup_swiglu_out(x, wg, wu, tx, tx, h)
         kernels.sparse_gemv_out(h, wd, th, y)
-    wall, omean, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
+    wall, eager, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
+    lib = kernels._lib_handle()
+    st = torch.cuda.current_stream().cuda_stream
+    wgu = workspaces.get(dev, "gateup", lib.lkv_sparse_gateup_workspace_bytes(F, H))
+    wdn = workspaces.get(dev, "gemv", lib.lkv_sparse_gemv_workspace_bytes(H, F))
+    fast = []
+    for x, wg, wu, wd, tx, th, h, y in sets:
+        f1 = _bound("lkv_sparse_gateup_swiglu", x.data_ptr(), wg.data_ptr(), wu.data_ptr(), float(tx), float(tx), F, H,
+                    h.data_ptr(), wgu.data_ptr(), wgu.numel(), st)
+        f2 = _bound("lkv_sparse_gemv", h.data_ptr(), wd.data_ptr(), float(th), H, F, y.data_ptr(), wdn.data_ptr(),
+                    wdn.numel(), st)
+        fast.append((f1, f2))
+
+    def fast_launch(i):
+        fast[i][0]()
+        fast[i][1]()
+    omean, _ = _kernel_time(fast_launch, len(sets), args.steps, args.warmup, torch)
     a = statistics.mean(alg)
     gu_alg = statistics.mean(2 * int((x.float().abs() > tx).sum()) * F * 2 + H * 2 + 2 * F * 2
                              for x, _, _, _, tx, _, _, _ in sets)
@@ -329,9 +376,12 @@ def bench_mlp(args, torch):
     return {
         "metric": "fused sparse MLP HBM GB/s (gate/up [14336,4096] + down [4096,14336], 40% sparse)",
         "value": round(a / (omean * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wall, 5),
+        "op_us_back_to_back": round(omean * 1e3, 3), "op_us_eager_call": round(eager * 1e3, 3),
         "higher_is_better": True, "dtype": "f16 (fp32 accumulate)",
         "config": {"workload": "config2_fused_mlp", "hidden": H, "ffn": F, "sparsity": 0.4,
-                   "buffer_sets": len(sets), "alg_bytes_per_call": int(a)},
+                   "buffer_sets": len(sets), "alg_bytes_per_call": int(a),
+                   "what": "value: gate/up + down per call, calls issued back to back through the C entry "
+                           "points; op_us_eager_call: one call through the Python wrappers between two events"},
         "roofline": roof,
     }
 

@@ -39,6 +39,7 @@ struct GemvArgs {
   float t[kMaxSeg];
   float t_up;
   int slab0[kMaxSeg + 1];
+  int slab0_seg[kMaxSeg];  // slab0[0 .. kMaxSeg) as set by gemv_launch (selected without dynamic indexing)
   int Z, nchunk;
   float* part;             // partials of segment s at part + part_off[s]
   size_t part_off[kMaxSeg];
@@ -127,17 +128,37 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, const uint16_t* __
 // of them round identically.
 __device__ __forceinline__ float rms_rstd(const uint16_t* __restrict__ x, int Z, float eps, float* s_wsum) {
   const int tid = threadIdx.x;
+  constexpr int kStride = kGemvThreads * 8;
+  constexpr int kBatch = 4;  // vectors up to kBatch * kStride: every load issued before the first is used
   float ss = 0.f;
   if (tid < kGemvThreads) {
-    for (int z = tid * 8; z < Z; z += kGemvThreads * 8) {
-      const uint4 u = *reinterpret_cast<const uint4*>(x + z);
-      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    if (Z <= kBatch * kStride) {
+      uint4 u[kBatch];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float a = h2f(static_cast<uint16_t>(w[i] & 0xffffu));
-        const float b = h2f(static_cast<uint16_t>(w[i] >> 16));
-        ss = fmaf(a, a, ss);
-        ss = fmaf(b, b, ss);
+      for (int k = 0; k < kBatch; ++k) u[k] = *reinterpret_cast<const uint4*>(x + min(tid * 8 + k * kStride, Z - 8));
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const bool ok = tid * 8 + k * kStride < Z;
+        const uint32_t w[4] = {u[k].x, u[k].y, u[k].z, u[k].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = h2f(static_cast<uint16_t>(w[i] & 0xffffu));
+          const float b = h2f(static_cast<uint16_t>(w[i] >> 16));
+          ss = ok ? fmaf(a, a, ss) : ss;
+          ss = ok ? fmaf(b, b, ss) : ss;
+        }
+      }
+    } else {
+      for (int z = tid * 8; z < Z; z += kStride) {
+        const uint4 u = *reinterpret_cast<const uint4*>(x + z);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = h2f(static_cast<uint16_t>(w[i] & 0xffffu));
+          const float b = h2f(static_cast<uint16_t>(w[i] >> 16));
+          ss = fmaf(a, a, ss);
+          ss = fmaf(b, b, ss);
+        }
       }
     }
   }

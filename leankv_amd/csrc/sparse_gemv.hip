@@ -42,19 +42,28 @@
 namespace lkv {
 namespace {
 
-// x[z0 .. z0 + BZ) into s_x (0 past Z) for the three input modes.
+// x[z0 .. z0 + BZ) into s_x (0 past Z) for the three input modes.  Every
+// load of a mode is issued before the first is used (addresses clamped into
+// range, values selected afterwards): a conditional load compiles to a branch
+// and a wait per element, one memory round trip each.
 template <int NT, int BZ, int MODE>
 __device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float* s_x, float* s_wsum) {
   constexpr int E = BZ / NT;  // inputs per thread
   const int tid = threadIdx.x;
   const int Z = G.Z;
   if (MODE == kInRmsNorm) {
+    uint16_t xv[E], wv[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int z = min(z0 + e * NT + tid, Z - 1);
+      xv[e] = G.x[z];
+      wv[e] = G.norm_w[z];
+    }
     const float rstd = rms_rstd(G.x, Z, G.eps, s_wsum);
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int i = e * NT + tid;
-      const int z = z0 + i;
-      s_x[i] = z < Z ? rms_apply(G.x[z], G.norm_w[z], rstd) : 0.f;
+      s_x[i] = z0 + i < Z ? rms_apply(xv[e], wv[e], rstd) : 0.f;
     }
   } else if (MODE == kInSwiglu) {
     // h = SwiGLU(sum of gate chunks, sum of up chunks); chunk loads for all E
@@ -76,16 +85,17 @@ __device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float*
       for (int e = 0; e < E; ++e)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const bool ok = k0 + i < nc;
-          vg[e][i] = ok ? pg[e][static_cast<size_t>(k0 + i) * kGemvBN] : 0.f;
-          vu[e][i] = ok ? pg[e][mat + static_cast<size_t>(k0 + i) * kGemvBN] : 0.f;
+          const size_t k = static_cast<size_t>(min(k0 + i, nc - 1)) * kGemvBN;
+          vg[e][i] = pg[e][k];
+          vu[e][i] = pg[e][mat + k];
         }
 #pragma unroll
       for (int e = 0; e < E; ++e)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          g[e] += vg[e][i];
-          u[e] += vu[e][i];
+          const bool ok = k0 + i < nc;
+          g[e] += ok ? vg[e][i] : 0.f;
+          u[e] += ok ? vu[e][i] : 0.f;
         }
     }
 #pragma unroll
@@ -94,13 +104,26 @@ __device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float*
       s_x[i] = z0 + i < Z ? h2f(swiglu_f16(g[e], u[e])) : 0.f;
     }
   } else {
+    uint16_t xv[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) xv[e] = G.x[min(z0 + e * NT + tid, Z - 1)];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int i = e * NT + tid;
-      s_x[i] = z0 + i < Z ? h2f(G.x[z0 + i]) : 0.f;
+      s_x[i] = z0 + i < Z ? h2f(xv[e]) : 0.f;
     }
   }
   __syncthreads();
+}
+
+// v[seg] from a per-segment kernel-argument array without a dynamically
+// indexed (serialised) scalar load: every entry is read, one is selected.
+template <typename T>
+__device__ __forceinline__ T seg_pick(const T (&v)[kMaxSeg], int seg) {
+  T r = v[0];
+#pragma unroll
+  for (int s = 1; s < kMaxSeg; ++s) r = seg == s ? v[s] : r;
+  return r;
 }
 
 template <int NT, int BZ, bool DUAL, int MODE, int U, int CP>
@@ -112,7 +135,8 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
   const int tid = threadIdx.x;
   // Work items are (slab, chunk) pairs.  The usual grid has one block per
   // item (the loop runs once); a persistent grid walks them with a stride.
-  const int nslab_tot = G.slab0[G.nseg];
+  // gemv_launch sets slab0[s] = the total slab count for every s >= nseg
+  const int nslab_tot = G.slab0[kMaxSeg];
   const int nitems = nslab_tot * G.nchunk;
   for (int item = blockIdx.y * gridDim.x + blockIdx.x; item < nitems; item += gridDim.x * gridDim.y) {
     int gslab, chunk;
@@ -127,15 +151,15 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
 
     int seg = 0;
 #pragma unroll
-    for (int s = 1; s < kMaxSeg; ++s)
-      if (s < G.nseg && gslab >= G.slab0[s]) seg = s;
-    const int slab = gslab - G.slab0[seg];
-    const int N = G.N[seg];
+    for (int s = 1; s < kMaxSeg; ++s) seg += gslab >= G.slab0[s] ? 1 : 0;
+    const int slab = gslab - seg_pick(G.slab0_seg, seg);
+    const int N = seg_pick(G.N, seg);
     const int n0 = slab * BN;
 
     input_prologue<NT, BZ, MODE>(G, z0, sm.x, sm.wsum);
     float sums[NL];
-    gemv_core<NT, BZ, DUAL, U, CP>(sm, G.A[seg], G.A_up, G.a_bytes[seg], N, G.t[seg], G.t_up, z0, G.Z, n0, sums);
+    gemv_core<NT, BZ, DUAL, U, CP>(sm, seg_pick(G.A, seg), G.A_up, seg_pick(G.a_bytes, seg), N, seg_pick(G.t, seg),
+                                   G.t_up, z0, G.Z, n0, sums);
 
     // ---- 4. output (threads 0..255, one column each): fp16 directly (single chunk) or partial sums
     if (tid < BN) {
@@ -144,7 +168,7 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
       } else {
 #pragma unroll
         for (int l = 0; l < NL; ++l) {
-          float* P = G.part + (l == 0 ? G.part_off[seg] : G.part_up_off) +
+          float* P = G.part + (l == 0 ? seg_pick(G.part_off, seg) : G.part_up_off) +
                      (static_cast<size_t>(slab) * G.nchunk + chunk) * BN;
           P[tid] = sums[l];
         }
@@ -287,6 +311,18 @@ int gemv_launch(const GemvArgs& G, int bz, bool dual, int mode, int nslab_total,
   const int cp = gemv_cpol();
   GemvArgs Gx = G;
   Gx.chunk_major = gemv_chunk_major() ? 1 : 0;
+  // the kernel selects per-segment values without dynamic indexing: segments
+  // past nseg start at the total slab count (never selected) and copy seg 0
+  for (int s = 0; s < kMaxSeg; ++s) Gx.slab0_seg[s] = G.slab0[s];
+  for (int s = G.nseg; s <= kMaxSeg; ++s) Gx.slab0[s] = nslab_total;
+  for (int s = G.nseg; s < kMaxSeg; ++s) {
+    Gx.A[s] = G.A[0];
+    Gx.a_bytes[s] = G.a_bytes[0];
+    Gx.N[s] = G.N[0];
+    Gx.t[s] = G.t[0];
+    Gx.part_off[s] = G.part_off[0];
+    Gx.slab0_seg[s] = nslab_total;
+  }
   if (gemv_unroll() == 16) {
     if (bz == 256) ok = launch_cp<256, 256, 16>(Gx, dual, mode, grid, st, cp);
     else if (bz == 512) ok = t512 ? launch_cp<512, 512, 16>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 512, 16>(Gx, dual, mode, grid, st, cp);
