@@ -73,6 +73,8 @@ def _parse():
     ap.add_argument("--no-roofline", action="store_true", help="skip the config-1 GEMV roofline measurement")
     ap.add_argument("--sets", type=int, default=5, help="independent buffer sets rotated per step")
     ap.add_argument("--cold", type=int, default=4096, help="--workload attn: cold tokens per sequence (config 4: 4096)")
+    ap.add_argument("--bits", type=int, default=3, choices=(1, 2, 3, 4),
+                    help="--workload attn: code width of the packed cache (config 4: 3)")
     return ap.parse_args()
 
 
@@ -575,16 +577,19 @@ def bench_attn(args, torch):
 
     dev = torch.device("cuda:0")
     B, Hq, Hkv, D, cold, hot = 16, 32, 8, 128, args.cold, 64
+    bits = args.bits
+    rb = {1: 16, 2: 32}.get(bits, 64)  # packed code bytes per token
     L = cold + hot
-    cent, _ = get_codebook_tensors(D, 3, dev, torch.float32)
+    cent, _ = get_codebook_tensors(D, bits, dev, torch.float32)
     PiK = generate_rotation_matrix(D, dev, torch.float32, 42)
     PiV = generate_rotation_matrix(D, dev, torch.float32, 43)
     seq = torch.tensor([L], dtype=torch.int32, device=dev)
     sets = []
     for s in range(8):
         g = torch.Generator(device=dev).manual_seed(400 + s)
-        kc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8) & 0x77
-        vc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8) & 0x77
+        mask = 0x77 if bits == 3 else 0xFF  # every code valid at its width
+        kc = torch.randint(0, 256, (B, Hkv, cold, rb), generator=g, device=dev, dtype=torch.uint8) & mask
+        vc = torch.randint(0, 256, (B, Hkv, cold, rb), generator=g, device=dev, dtype=torch.uint8) & mask
         kn = torch.rand(B, Hkv, cold, generator=g, device=dev) * 4 + 8
         vn = torch.rand(B, Hkv, cold, generator=g, device=dev) * 4 + 8
         kh = torch.randn(B, Hkv, hot, D, generator=g, device=dev).half()
@@ -595,16 +600,17 @@ def bench_attn(args, torch):
 
     def launch(i):
         q, kc, kn, vc, vn, kh, vh, out = sets[i]
-        kernels.tq_decode_attn_out(q, kc, kn, vc, vn, kh, vh, PiK, PiV, cent, 3, seq, L, D ** -0.5, out, ws)
+        kernels.tq_decode_attn_out(q, kc, kn, vc, vn, kh, vh, PiK, PiV, cent, bits, seq, L, D ** -0.5, out, ws)
     wall, _, _ = _timed_loop(launch, len(sets), args.steps, args.warmup, torch)
     kmean, kmed = _kernel_time(launch, len(sets), args.steps, args.warmup, torch)
-    alg = B * Hkv * (cold * (64 + 64 + 4 + 4) + hot * D * 2 * 2) + 2 * B * Hq * D * 2
+    alg = B * Hkv * (cold * (rb + rb + 4 + 4) + hot * D * 2 * 2) + 2 * B * Hq * D * 2
     achieved = alg / (kmean * 1e-3) / 1e9
     return {
         "metric": "packed-KV decode attention HBM GB/s (B=16, 32/8 heads, 4096 cold + 64 hot)",
         "value": round(achieved, 1), "unit": "GB/s", "ms_per_step": round(wall, 5), "higher_is_better": True,
-        "dtype": "3-bit codes, fp16 MFMA scores/values, fp32 softmax",
+        "dtype": "%d-bit codes, fp16 MFMA scores/values, fp32 softmax" % bits,
         "config": {"workload": "config4_packed_attention", "batch": B, "heads": "32/8", "cold": cold, "hot": hot,
+                   "bits": bits,
                    "alg_bytes_per_call": alg, "sets": len(sets)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic("attn_config4"),
@@ -821,8 +827,9 @@ def bench_prefill(args, torch):
     sets = []
     for s_ in range(3):
         g = torch.Generator(device=dev).manual_seed(500 + s_)
-        kc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8) & 0x77
-        vc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8) & 0x77
+        mask = 0x77 if bits == 3 else 0xFF  # every code valid at its width
+        kc = torch.randint(0, 256, (B, Hkv, cold, rb), generator=g, device=dev, dtype=torch.uint8) & mask
+        vc = torch.randint(0, 256, (B, Hkv, cold, rb), generator=g, device=dev, dtype=torch.uint8) & mask
         kn = torch.rand(B, Hkv, cold, generator=g, device=dev) * 4 + 8
         vn = torch.rand(B, Hkv, cold, generator=g, device=dev) * 4 + 8
         kh = torch.randn(B, Hkv, hot, D, generator=g, device=dev).half()

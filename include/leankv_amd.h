@@ -248,9 +248,10 @@ int lkv_tq_cache_append(const void* k_new, const void* v_new, void* k_hot, void*
  * materialises the dequantized K/V:
  *   s_t = scale * n_t * ((q @ PiK^T) . c[idx_t])     for cold tokens
  *   o   = (sum_t p_t n_t c[idx_t]) @ PiV + sum_hot p_t v_t
- * q: fp16 [B, Hq, 128]; codes uint8 [B, Hkv, cap, row_bytes] (bits 3/4 only:
- * 4-bit nibbles); norms fp32 [B, Hkv, cap]; hot fp16 [B, Hkv, hot_cap, 128]
- * ring as in lkv_tq_cache_append.  The current length L = *seq_len (device
+ * q: fp16 [B, Hq, 128]; codes uint8 [B, Hkv, cap, row_bytes] in the packing of
+ * lkv_tq_quantize (row_bytes = lkv_tq_packed_row_bytes(bits): 64 for 3 and 4
+ * bits, 32 for 2, 16 for 1); norms fp32 [B, Hkv, cap]; hot fp16
+ * [B, Hkv, hot_cap, 128] ring as in lkv_tq_cache_append, hot_cap 1..256.  The current length L = *seq_len (device
  * int32, includes every token already appended); cold tokens are
  * [0, max(0, L - hot_cap)), hot tokens the rest.  max_len (host) bounds L and
  * sizes the launch; L > max_len is clamped to max_len.  out: fp16 [B, Hq, 128].
@@ -280,8 +281,9 @@ int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const float* k_nor
  *   s_t = scale * n_t * ((q @ PiK^T) . c[idx_t])       cold keys
  *   s_t = scale * (q @ PiK^T) . fp16(k_t @ PiK^T)       hot keys
  *   o   = (sum_t p_t n_t c[idx_t] + sum_hot p_t fp16(v_t @ PiV^T)) @ PiV
- * q: fp16 [B, Hq, S, 128] (post-RoPE); codes uint8 [B, Hkv, cap, 64] (bits 3
- * or 4); norms fp32 [B, Hkv, cap]; hot fp16 [B, Hkv, hot_cap, 128];
+ * q: fp16 [B, Hq, S, 128] (post-RoPE); codes uint8 [B, Hkv, cap, row_bytes]
+ * (row_bytes as for lkv_tq_decode_attn, bits 1..4); norms fp32 [B, Hkv, cap];
+ * hot fp16 [B, Hkv, hot_cap, 128];
  * out fp16 [B, Hq, S, 128].  Hq / Hkv must be 1, 2, 4, 8 or 16.
  */
 size_t lkv_tq_prefill_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hot_cap);
@@ -318,12 +320,14 @@ int lkv_paged_decode_attn(const void* q, const void* kv_data, const int32_t* kv_
  * fp16: this is lkv_tq_decode_attn with the cold store in pages, for ragged
  * batches that grow and free pages independently.  Same math as
  * lkv_tq_decode_attn (cache.py:169-189 semantics + sdpa_attention.py:79-105).
- *   k_codes, v_codes: uint8 [max_pages, Hkv, page_size, 64] (4-bit nibbles)
+ *   k_codes, v_codes: uint8 [max_pages, Hkv, page_size, row_bytes] (row_bytes
+ *   = lkv_tq_packed_row_bytes(bits), bits 1..4)
  *   k_norms, v_norms: fp32  [max_pages, Hkv, page_size]
  *   sequence b's cold token t (t < seq_lens[b] - hot_cap) lies in page
  *   kv_indices[kv_indptr[b] + t / page_size], slot t % page_size (FlashInfer's
  *   CSR page table, int32 device arrays);
- *   k_hot, v_hot: fp16 [B, Hkv, hot_cap, 128] rings (token t in slot t % hot_cap);
+ *   k_hot, v_hot: fp16 [B, Hkv, hot_cap, 128] rings (token t in slot t % hot_cap,
+ *   hot_cap 1..256);
  *   seq_lens: int32 [B] on the device, each <= max_len.
  * page_size 16, 32, 64 or 128; the code pool below 2^32 bytes.  Page ids are
  * clamped to the pool and tokens past a sequence's pages are not read.

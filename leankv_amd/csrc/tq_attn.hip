@@ -50,8 +50,7 @@ constexpr int kD = 128;
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kBlk = 32;    // tokens per wave step
-constexpr int kRowB = 64;   // code bytes per token (4-bit nibbles, dim 128)
-constexpr int kHotMax = 64;
+constexpr int kHotMax = 256;  // hot-window slots the combine walks (64 per slot group)
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Max / sum across the 16 lanes of a row group (lanes with equal lane/16).
@@ -99,6 +98,55 @@ struct AttnParams {
 __host__ __device__ __forceinline__ int rec_acc_off(int G) { return (2 * G + 3) & ~3; }
 __host__ __device__ __forceinline__ int rec_floats(int G) { return rec_acc_off(G) + G * kD; }
 
+// Code rows by stored width CB: 4 = nibble rows (3- and 4-bit codes, 64 B per
+// token), 2 = four 2-bit codes per byte (32 B), 1 = eight 1-bit codes per byte
+// (16 B), the packings of leankv/turboquant/quantizer.py:38-62.  Narrow rows
+// are widened to nibbles in registers as they arrive, so the decode after
+// that (v_perm over a centroid table padded with zeros) is the 3-bit one.
+template <int CB>
+__host__ __device__ constexpr int code_row_bytes() {
+  return kD * CB / 8;
+}
+// 16 bits of 2-bit codes (dims 0..7 at bits 2d) -> dims at bits 4d.
+__device__ __forceinline__ uint32_t nib_from2(uint32_t x) {
+  uint32_t t = x & 0xffffu;
+  t = (t | (t << 8)) & 0x00ff00ffu;
+  t = (t | (t << 4)) & 0x0f0f0f0fu;
+  return (t | (t << 2)) & 0x33333333u;
+}
+// 8 bits of 1-bit codes (dim d at bit d) -> dims at bits 4d.
+__device__ __forceinline__ uint32_t nib_from1(uint32_t x) {
+  uint32_t t = x & 0xffu;
+  t = (t | (t << 12)) & 0x000f000fu;
+  t = (t | (t << 6)) & 0x03030303u;
+  return (t | (t << 3)) & 0x11111111u;
+}
+// Dims 32k .. 32k+31 of a code row as 4 nibble dwords; voff/soff address the
+// row's byte 4*CB*k.
+template <int CB>
+__device__ __forceinline__ u32x4 load_codes32(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  if constexpr (CB == 4) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  } else if constexpr (CB == 2) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    const uint32_t lo = v[0], hi = v[1];
+    return u32x4{nib_from2(lo), nib_from2(lo >> 16), nib_from2(hi), nib_from2(hi >> 16)};
+  } else {
+    const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    return u32x4{nib_from1(v), nib_from1(v >> 8), nib_from1(v >> 16), nib_from1(v >> 24)};
+  }
+}
+// Dims 8k .. 8k+7 of a code row as one nibble dword (row byte CB*k).
+template <int CB>
+__device__ __forceinline__ uint32_t load_codes8(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  if constexpr (CB == 4)
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+  else if constexpr (CB == 2)
+    return nib_from2(__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0));
+  else
+    return nib_from1(__builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, 0));
+}
+
 // Buffer resource over `bytes` bytes at base (raw addressing, stride 0).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
@@ -145,35 +193,36 @@ struct PagedRows {
 // A block entirely below the valid end.  Each load's voffset is one of two
 // lane bases; everything that depends on the block or the load is in the
 // scalar soffset (so no per-load vector address registers stay live).
-template <typename Rows>
+template <int CB, typename Rows>
 __device__ __forceinline__ void load_full(BlockRegs& R, const ColdRsrc& rs, int t0, int lane, const Rows& rows) {
+  constexpr int RB = code_row_bytes<CB>();
   const int g = lane >> 4, w = lane & 15;
-  const int vk = w * kRowB + 16 * g;   // key codes: token w, bytes 16g..
-  const int vv = 4 * g * kRowB + 4 * w;  // value codes: token 4g, dword w
+  const int vk = w * RB + 4 * CB * g;  // key codes: token w, dims 32g..
+  const int vv = 4 * g * RB + CB * w;  // value codes: token 4g, dims 8w..
   const int vnrm = 16 * g;             // norms: token 4g
   const int r0 = __builtin_amdgcn_readfirstlane(rows(t0)), r1 = __builtin_amdgcn_readfirstlane(rows(t0 + 16));
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
-    const int sc = (tt ? r1 : r0) * kRowB, sn = (tt ? r1 : r0) * 4;
-    R.kraw[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kc, vk, sc, 0));
+    const int sc = (tt ? r1 : r0) * RB, sn = (tt ? r1 : r0) * 4;
+    R.kraw[tt] = load_codes32<CB>(rs.kc, vk, sc);
     R.kn[tt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kn, vnrm, sn, 0));
     R.vn[tt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.vn, vnrm, sn, 0));
   }
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    R.vdw[j] = __builtin_amdgcn_raw_buffer_load_b32(rs.vc, vv, ((j >> 2) ? r1 : r0) * kRowB + (j & 3) * kRowB, 0);
+  for (int j = 0; j < 8; ++j) R.vdw[j] = load_codes8<CB>(rs.vc, vv, ((j >> 2) ? r1 : r0) * RB + (j & 3) * RB);
 }
 
 // A block reaching past t_lim: tokens at or past t_lim read token t_lim - 1
 // (valid memory); the caller masks them.
-template <typename Rows>
+template <int CB, typename Rows>
 __device__ __forceinline__ void load_clamped(BlockRegs& R, const ColdRsrc& rs, int t0, int t_lim, int lane,
                                              const Rows& rows) {
+  constexpr int RB = code_row_bytes<CB>();
   const int g = lane >> 4, w = lane & 15;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int tk = min(t0 + 16 * tt + w, t_lim - 1);
-    R.kraw[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.kc, rows(tk) * kRowB + 16 * g, 0, 0));
+    R.kraw[tt] = load_codes32<CB>(rs.kc, rows(tk) * RB + 4 * CB * g, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tn = min(t0 + 16 * tt + 4 * g + i, t_lim - 1);
@@ -185,18 +234,18 @@ __device__ __forceinline__ void load_clamped(BlockRegs& R, const ColdRsrc& rs, i
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int tv = min(t0 + 16 * (j >> 2) + 4 * g + (j & 3), t_lim - 1);
-    R.vdw[j] = __builtin_amdgcn_raw_buffer_load_b32(rs.vc, rows(tv) * kRowB + 4 * w, 0, 0);
+    R.vdw[j] = load_codes8<CB>(rs.vc, rows(tv) * RB + CB * w, 0);
   }
 }
 
-template <typename Rows>
+template <int CB, typename Rows>
 __device__ __forceinline__ void fetch_block(BlockRegs& R, const ColdRsrc& rs, int t0, int t_addr_end, int lane,
                                             const Rows& rows) {
   t0 = __builtin_amdgcn_readfirstlane(t0);  // wave-uniform: keeps the token offset scalar
   if (t0 + kBlk <= t_addr_end)
-    load_full(R, rs, t0, lane, rows);
+    load_full<CB>(R, rs, t0, lane, rows);
   else
-    load_clamped(R, rs, t0, t_addr_end, lane, rows);
+    load_clamped<CB>(R, rs, t0, t_addr_end, lane, rows);
 }
 
 // Online-softmax state of one lane: head w = lane % 16, output dims
@@ -292,9 +341,11 @@ constexpr int kSplitBlocksPerCU = LKV_ATTN_BLOCKS_PER_CU;
 
 constexpr int kMaxPg = 256;  // pages of one split in the paged layout
 
-template <bool PERM, bool DECODE, bool PAGED>
+template <bool PERM, bool DECODE, bool PAGED, int CB>
 __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_kernel(AttnParams P) {
   static_assert(!(PAGED && DECODE), "the fused decode step uses the dense layout");
+  static_assert(CB == 4 || (PERM && !DECODE), "narrow code rows: v_perm decode, standalone calls");
+  constexpr int RB = code_row_bytes<CB>();
   __shared__ uint32_t s_lut[256];
   __shared__ int s_pg[PAGED ? kMaxPg : 1];
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
@@ -335,16 +386,16 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
   } else {
     t_addr_end = min(t_begin + P.split_tokens, P.cap);
     seq_len = __builtin_amdgcn_readfirstlane(*P.seq_len);
-    rs.kc = make_rsrc(P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB, static_cast<uint32_t>(P.cap) * kRowB);
-    rs.vc = make_rsrc(P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB, static_cast<uint32_t>(P.cap) * kRowB);
+    rs.kc = make_rsrc(P.k_codes + bh * static_cast<size_t>(P.cap) * RB, static_cast<uint32_t>(P.cap) * RB);
+    rs.vc = make_rsrc(P.v_codes + bh * static_cast<size_t>(P.cap) * RB, static_cast<uint32_t>(P.cap) * RB);
     rs.kn = make_rsrc(P.k_norms + bh * static_cast<size_t>(P.cap), static_cast<uint32_t>(P.cap) * 4);
     rs.vn = make_rsrc(P.v_norms + bh * static_cast<size_t>(P.cap), static_cast<uint32_t>(P.cap) * 4);
   }
   auto fetch = [&](BlockRegs& R, int t) {
     if constexpr (PAGED)
-      fetch_block(R, rs, t, t_addr_end, lane, prow);
+      fetch_block<CB>(R, rs, t, t_addr_end, lane, prow);
     else
-      fetch_block(R, rs, t, t_addr_end, lane, DenseRows{});
+      fetch_block<CB>(R, rs, t, t_addr_end, lane, DenseRows{});
   };
   // The wave's first token block.  Dense layout: always the straight-line
   // full-block load, whatever t is: rows past the cold store read 0 through
@@ -356,7 +407,7 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
     if constexpr (PAGED) {
       if (t < t_addr_end) fetch(R, t);
     } else {
-      load_full(R, rs, __builtin_amdgcn_readfirstlane(t), lane, DenseRows{});
+      load_full<CB>(R, rs, __builtin_amdgcn_readfirstlane(t), lane, DenseRows{});
     }
   };
   BlockRegs ra, rb;
@@ -369,8 +420,9 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
   uint32_t tab[4] = {0u, 0u, 0u, 0u};
   if constexpr (PERM) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t c16 = f2h(P.centroids[j]);
+    for (int j = 0; j < 8; ++j) {  // fewer than 8 centroids (1, 2 bits): zero entries, never selected
+      const float cj = P.centroids[min(j, P.ncent - 1)];
+      const uint32_t c16 = f2h(j < P.ncent ? cj : 0.f);
       tab[j >> 2] |= (c16 & 0xffu) << (8 * (j & 3));
       tab[2 + (j >> 2)] |= (c16 >> 8) << (8 * (j & 3));
     }
@@ -639,17 +691,20 @@ __device__ __forceinline__ float dot8_f16(const uint4& a, const uint4& b) {
 //   thread (dg = tid % 32, grp = tid / 32): PiV rows 8 grp .. 8 grp + 7 at
 //   dims 4 dg .. 4 dg + 3 (float4), and the rotated sums of splits grp, grp +
 //   16, ... at the same dims (float4);
-//   thread (dh = tid % 16, jg = tid / 16): hot values of slots jg and jg + 32
-//   at dims 8 dh .. 8 dh + 7 (16-byte loads);
-//   thread (j = tid / 8, part = tid % 8): the hot score of slot j, dims
-//   16 part .. 16 part + 15;  thread s < nsplit: split s's maximum and sum.
-// Partial sums over split groups, slot groups and PiV row groups are joined
-// through LDS in a fixed order.
+//   thread (dh = tid % 16, jg = tid / 16): hot values of slots jg + 32 i
+//   (i < 2 NHG) at dims 8 dh .. 8 dh + 7 (16-byte loads);
+//   thread (j = tid / 8, part = tid % 8): the hot scores of slots j + 64 q
+//   (q < NHG), dims 16 part .. 16 part + 15;  thread s < nsplit: split s's
+//   maximum and sum.
+// NHG: hot-window slot groups of 64 (hot_cap <= 64 NHG).  Partial sums over
+// split groups, slot groups and PiV row groups are joined through LDS in a
+// fixed order (for NHG = 1 the same order as any larger NHG on <= 64 slots).
 constexpr int kCombSplitGroups = kCombThreads / 32;  // 16
 constexpr int kCombSlotGroups = kCombThreads / 16;   // 32
+template <int NHG>
 __global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnParams P) {  // 2 blocks per CU
   __shared__ float s_w[kMaxSplits];
-  __shared__ float s_p[kHotMax];
+  __shared__ float s_p[64 * NHG];
   __shared__ float s_red[kCombWaves];
   __shared__ __align__(16) float s_cold[kCombSplitGroups][kD];
   __shared__ __align__(16) float s_hot[kCombSlotGroups][kD];
@@ -691,34 +746,46 @@ __global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnPa
   float4 pv[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) pv[i] = *reinterpret_cast<const float4*>(P.PiV + (8 * grp + i) * kD + 4 * dg);
-  uint4 hv[2];
+  uint4 hv[2 * NHG];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < 2 * NHG; ++i) {
     const int jj = min(jg + 32 * i, P.hot_cap - 1);
     hv[i] = *reinterpret_cast<const uint4*>(P.v_hot + hot_base + static_cast<size_t>(jj) * kD + 8 * dh);
   }
   float4 ca = *reinterpret_cast<const float4*>(recs + static_cast<size_t>(min(grp, ns - 1)) * RF + rec_acc_off(G) + hh * kD +
                                               4 * dg);
-  // hot score partial: slot j = tid / 8, dims 16 * (tid % 8) .. +16
+  // hot score partials: slots j + 64 q, j = tid / 8, dims 16 * (tid % 8) .. +16
   const int j = tid >> 3, part = tid & 7;
-  float sdot = 0.f;
+  float sdot[NHG];
   {
-    const int slot = min(j, P.hot_cap - 1);
-    const uint4* kp = reinterpret_cast<const uint4*>(P.k_hot + hot_base + static_cast<size_t>(slot) * kD + 16 * part);
     const uint4* qp = reinterpret_cast<const uint4*>(P.q + (static_cast<size_t>(b) * P.Hq + hq) * kD + 16 * part);
-    const uint4 k0 = kp[0], k1 = kp[1];
     const uint4 q0 = qp[0], q1 = qp[1];
-    sdot = dot8_f16(k0, q0) + dot8_f16(k1, q1);  // slots past hot_len are masked by `score`
+    uint4 k0[NHG], k1[NHG];
+#pragma unroll
+    for (int q = 0; q < NHG; ++q) {
+      const int slot = min(j + 64 * q, P.hot_cap - 1);
+      const uint4* kp = reinterpret_cast<const uint4*>(P.k_hot + hot_base + static_cast<size_t>(slot) * kD + 16 * part);
+      k0[q] = kp[0];
+      k1[q] = kp[1];
+    }
+#pragma unroll
+    for (int q = 0; q < NHG; ++q) sdot[q] = dot8_f16(k0[q], q0) + dot8_f16(k1[q], q1);  // masked by `score`
   }
   const int L = min(seq_len, P.max_len);
   const int hot_len = L - max(0, L - P.hot_cap);
-  const bool hj = j < hot_len;
   // ---- B. softmax statistics over cold splits and hot tokens
-  sdot += dpp_f<0xB1>(sdot);   // xor 1
-  sdot += dpp_f<0x4E>(sdot);   // xor 2
-  sdot += dpp_f<0x141>(sdot);  // the other quad of the 8-lane half row
-  const float score = hj ? sdot * P.scale_log2 : -INFINITY;
-  float v = fmaxf(ms, part == 0 ? score : -INFINITY);
+  float score[NHG];
+  float smax = -INFINITY;
+#pragma unroll
+  for (int q = 0; q < NHG; ++q) {
+    float d = sdot[q];
+    d += dpp_f<0xB1>(d);   // xor 1
+    d += dpp_f<0x4E>(d);   // xor 2
+    d += dpp_f<0x141>(d);  // the other quad of the 8-lane half row
+    score[q] = j + 64 * q < hot_len ? d * P.scale_log2 : -INFINITY;
+    smax = fmaxf(smax, score[q]);
+  }
+  float v = fmaxf(ms, part == 0 ? smax : -INFINITY);
   v = wave_max(v);
   if (lane == 0) s_red[wave] = v;
   __syncthreads();
@@ -727,10 +794,15 @@ __global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnPa
   for (int w = 0; w < kCombWaves; ++w) M = fmaxf(M, s_red[w]);
   __syncthreads();
   const float wsp = (tid < ns && ms != -INFINITY) ? fast_exp2(ms - M) : 0.f;
-  const float pj = hj ? fast_exp2(score - M) : 0.f;
   if (tid < ns) s_w[tid] = wsp;
-  if (part == 0 && j < kHotMax) s_p[j] = pj;
-  float lv = wsp * ls + (part == 0 ? pj : 0.f);
+  float psum = 0.f;
+#pragma unroll
+  for (int q = 0; q < NHG; ++q) {
+    const float pj = j + 64 * q < hot_len ? fast_exp2(score[q] - M) : 0.f;
+    if (part == 0) s_p[j + 64 * q] = pj;
+    psum += pj;
+  }
+  float lv = wsp * ls + (part == 0 ? psum : 0.f);
   lv = wave_sum(lv);
   if (lane == 0) s_red[wave] = lv;
   __syncthreads();
@@ -757,7 +829,7 @@ __global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnPa
   *reinterpret_cast<float4*>(&s_cold[grp][4 * dg]) = cold;
   float hs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < 2 * NHG; ++i) {
     const int jj = jg + 32 * i;
     if (jj < hot_len) {  // an unwritten slot may hold NaN: skipped, never multiplied
       const float p = s_p[jj];
@@ -937,28 +1009,38 @@ int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st) {
   P.indices = c.indices;
   P.page_shift = c.page_shift;
   P.max_pages = static_cast<int>(c.max_pages);
-  P.pool_code_bytes = static_cast<uint32_t>(c.max_pages * c.Hkv * (int64_t(1) << c.page_shift) * kRowB);
+  P.pool_code_bytes = static_cast<uint32_t>(c.max_pages * c.Hkv * (int64_t(1) << c.page_shift) * tq::row_bytes_for(c.bits));
   P.pool_norm_bytes = static_cast<uint32_t>(c.max_pages * c.Hkv * (int64_t(1) << c.page_shift) * 4);
   if (c.pq != nullptr) {
     P.q = c.q16;  // the combine's hot-window query
     P.k_hot = c.k_ring;
     P.v_hot = c.v_ring;
     if (c.bits == 3)
-      hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false>), grid, dim3(kThreads), 0, st, P);
+      hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false, 4>), grid, dim3(kThreads), 0, st, P);
     else
-      hipLaunchKernelGGL((tq_attn_split_kernel<false, true, false>), grid, dim3(kThreads), 0, st, P);
+      hipLaunchKernelGGL((tq_attn_split_kernel<false, true, false, 4>), grid, dim3(kThreads), 0, st, P);
   } else if (c.indptr != nullptr) {
-    if (c.bits == 3)
-      hipLaunchKernelGGL((tq_attn_split_kernel<true, false, true>), grid, dim3(kThreads), 0, st, P);
-    else
-      hipLaunchKernelGGL((tq_attn_split_kernel<false, false, true>), grid, dim3(kThreads), 0, st, P);
-  } else if (c.bits == 3) {
-    hipLaunchKernelGGL((tq_attn_split_kernel<true, false, false>), grid, dim3(kThreads), 0, st, P);
+    switch (c.bits) {
+      case 1: hipLaunchKernelGGL((tq_attn_split_kernel<true, false, true, 1>), grid, dim3(kThreads), 0, st, P); break;
+      case 2: hipLaunchKernelGGL((tq_attn_split_kernel<true, false, true, 2>), grid, dim3(kThreads), 0, st, P); break;
+      case 3: hipLaunchKernelGGL((tq_attn_split_kernel<true, false, true, 4>), grid, dim3(kThreads), 0, st, P); break;
+      default: hipLaunchKernelGGL((tq_attn_split_kernel<false, false, true, 4>), grid, dim3(kThreads), 0, st, P);
+    }
   } else {
-    hipLaunchKernelGGL((tq_attn_split_kernel<false, false, false>), grid, dim3(kThreads), 0, st, P);
+    switch (c.bits) {
+      case 1: hipLaunchKernelGGL((tq_attn_split_kernel<true, false, false, 1>), grid, dim3(kThreads), 0, st, P); break;
+      case 2: hipLaunchKernelGGL((tq_attn_split_kernel<true, false, false, 2>), grid, dim3(kThreads), 0, st, P); break;
+      case 3: hipLaunchKernelGGL((tq_attn_split_kernel<true, false, false, 4>), grid, dim3(kThreads), 0, st, P); break;
+      default: hipLaunchKernelGGL((tq_attn_split_kernel<false, false, false, 4>), grid, dim3(kThreads), 0, st, P);
+    }
   }
   LKV_LAUNCH_CHECK("tq_decode_attn split");
-  hipLaunchKernelGGL(tq_attn_combine_kernel, cgrid, dim3(kCombThreads), 0, st, P);
+  if (c.hot_cap <= 64)
+    hipLaunchKernelGGL(tq_attn_combine_kernel<1>, cgrid, dim3(kCombThreads), 0, st, P);
+  else if (c.hot_cap <= 128)
+    hipLaunchKernelGGL(tq_attn_combine_kernel<2>, cgrid, dim3(kCombThreads), 0, st, P);
+  else
+    hipLaunchKernelGGL(tq_attn_combine_kernel<4>, cgrid, dim3(kCombThreads), 0, st, P);
   LKV_LAUNCH_CHECK("tq_decode_attn combine");
   return LKV_OK;
 }
@@ -980,11 +1062,11 @@ extern "C" int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const f
                                   int64_t max_len, int64_t B, int64_t Hq, int64_t Hkv, int64_t cap,
                                   int64_t hot_cap, float scale, void* out, void* workspace,
                                   size_t workspace_bytes, void* stream) {
-  LKV_REQUIRE(bits == 3 || bits == 4, "tq_decode_attn: bits=%d unsupported (4-bit nibble layouts only)", bits);
+  LKV_REQUIRE(bits >= 1 && bits <= 4, "tq_decode_attn: bits=%d unsupported (1..4 are bit-packed)", bits);
   LKV_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16,
               "tq_decode_attn: need Hq %% Hkv == 0 and Hq/Hkv <= 16 (Hq=%lld Hkv=%lld)", (long long)Hq,
               (long long)Hkv);
-  LKV_REQUIRE(hot_cap >= 1 && hot_cap <= kHotMax, "tq_decode_attn: hot_cap must be 1..64");
+  LKV_REQUIRE(hot_cap >= 1 && hot_cap <= kHotMax, "tq_decode_attn: hot_cap must be 1..%d", kHotMax);
   LKV_REQUIRE(max_len >= 0 && max_len <= cap + hot_cap, "tq_decode_attn: max_len=%lld exceeds cap+hot_cap=%lld",
               (long long)max_len, (long long)(cap + hot_cap));
   LKV_REQUIRE(max_len < (1ll << 31) && cap < (1ll << 31), "tq_decode_attn: length too large");
@@ -1061,14 +1143,14 @@ extern "C" int lkv_tq_paged_decode_attn(const void* q, const uint8_t* k_codes, c
                                         int64_t page_size, int64_t max_pages, int64_t max_len, int64_t hot_cap,
                                         float scale, void* out, void* workspace, size_t workspace_bytes,
                                         void* stream) {
-  LKV_REQUIRE(bits == 3 || bits == 4, "tq_paged_decode_attn: bits=%d unsupported (4-bit nibble layouts only)", bits);
+  LKV_REQUIRE(bits >= 1 && bits <= 4, "tq_paged_decode_attn: bits=%d unsupported (1..4 are bit-packed)", bits);
   LKV_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16,
               "tq_paged_decode_attn: need Hq %% Hkv == 0 and Hq/Hkv <= 16 (Hq=%lld Hkv=%lld)", (long long)Hq,
               (long long)Hkv);
   const int shift = page_shift_of(page_size);
   LKV_REQUIRE(shift >= 0, "tq_paged_decode_attn: page_size=%lld must be 16, 32, 64 or 128", (long long)page_size);
-  LKV_REQUIRE(hot_cap >= 1 && hot_cap <= kHotMax, "tq_paged_decode_attn: hot_cap must be 1..64");
-  LKV_REQUIRE(max_pages >= 1 && max_pages * Hkv * page_size * kRowB < (int64_t(1) << 32),
+  LKV_REQUIRE(hot_cap >= 1 && hot_cap <= kHotMax, "tq_paged_decode_attn: hot_cap must be 1..%d", kHotMax);
+  LKV_REQUIRE(max_pages >= 1 && max_pages * Hkv * page_size * tq::row_bytes_for(bits) < (int64_t(1) << 32),
               "tq_paged_decode_attn: max_pages=%lld: the code pool must hold fewer than 2^32 bytes",
               (long long)max_pages);
   LKV_REQUIRE(max_len >= 0 && max_len < (1ll << 31), "tq_paged_decode_attn: bad max_len");

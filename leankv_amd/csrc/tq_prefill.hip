@@ -45,7 +45,6 @@ constexpr int kD = 128;
 constexpr int kThreads = 256;
 constexpr int kKT = 64;         // keys per tile
 constexpr int kCols = 128;      // (query, head) columns per block
-constexpr int kRowB = 64;       // code bytes per token (4-bit nibbles)
 constexpr int kKRow = kD + 8;   // fp16 row of the decoded key tile (padded)
 constexpr int kVRow = kKT + 4;  // fp16 row of the transposed value tile (padded: conflict-free 8-byte reads)
 static_assert(kKT == 64, "the decode / compute lane maps assume 64-key tiles");
@@ -230,8 +229,50 @@ __device__ __forceinline__ uint4 perm_group(uint4 a) {
                __builtin_amdgcn_perm(a.y, a.x, 0x07060302u), __builtin_amdgcn_perm(a.w, a.z, 0x07060302u)};
 }
 
-template <bool PERM>
+// Code rows of stored width CB (4: nibbles, 64 B per token; 2: four codes per
+// byte; 1: eight per byte) widened to nibble dwords as they are loaded, so the
+// decode after the load is the nibble one (bits 1 and 2 through the v_perm
+// table, zero-padded past 2^bits centroids).
+__device__ __forceinline__ uint32_t nib2(uint32_t x) {  // 8 two-bit codes -> 8 nibbles
+  uint32_t t = x & 0xffffu;
+  t = (t | (t << 8)) & 0x00ff00ffu;
+  t = (t | (t << 4)) & 0x0f0f0f0fu;
+  return (t | (t << 2)) & 0x33333333u;
+}
+__device__ __forceinline__ uint32_t nib1(uint32_t x) {  // 8 one-bit codes -> 8 nibbles
+  uint32_t t = x & 0xffu;
+  t = (t | (t << 12)) & 0x000f000fu;
+  t = (t | (t << 6)) & 0x03030303u;
+  return (t | (t << 3)) & 0x11111111u;
+}
+// dims 32k .. 32k + 31 of a row whose code bytes start at p (row byte 4 CB k)
+template <int CB>
+__device__ __forceinline__ uint4 codes32(const uint8_t* p) {
+  if constexpr (CB == 4) {
+    return *reinterpret_cast<const uint4*>(p);
+  } else if constexpr (CB == 2) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    return uint4{nib2(v.x), nib2(v.x >> 16), nib2(v.y), nib2(v.y >> 16)};
+  } else {
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(p);
+    return uint4{nib1(v), nib1(v >> 8), nib1(v >> 16), nib1(v >> 24)};
+  }
+}
+// dims 8k .. 8k + 7 (row byte CB k)
+template <int CB>
+__device__ __forceinline__ uint32_t codes8(const uint8_t* p) {
+  if constexpr (CB == 4)
+    return *reinterpret_cast<const uint32_t*>(p);
+  else if constexpr (CB == 2)
+    return nib2(*reinterpret_cast<const uint16_t*>(p));
+  else
+    return nib1(*p);
+}
+
+template <bool PERM, int CB>
 __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillParams P) {
+  static_assert(CB == 4 || PERM, "narrow code rows use the v_perm decode");
+  constexpr int RB = kD * CB / 8;  // code bytes per token
   __shared__ __align__(16) uint16_t sK[2 * kKT * kKRow];  // two buffers of decoded keys
   __shared__ __align__(16) uint16_t sVt[2 * kD * kVRow];  // two buffers of transposed values
   __shared__ __align__(16) float sN[2][2][kKT];           // [buffer][key, value] norms (1 hot, 0 past the end)
@@ -279,8 +320,9 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
   uint32_t tab[4] = {0u, 0u, 0u, 0u};
   if constexpr (PERM) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t c16 = f2h(P.centroids[j]);
+    for (int j = 0; j < 8; ++j) {  // fewer than 8 centroids (1, 2 bits): zero entries, never selected
+      const float cj = P.centroids[min(j, P.ncent - 1)];
+      const uint32_t c16 = f2h(j < P.ncent ? cj : 0.f);
       tab[j >> 2] |= (c16 & 0xffu) << (8 * (j & 3));
       tab[2 + (j >> 2)] |= (c16 >> 8) << (8 * (j & 3));
     }
@@ -321,11 +363,11 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
   const int ntile = (kend + kKT - 1) / kKT;
 
   // ---- per-thread code registers of one key tile, loaded two tiles ahead:
-  //   kw   key codes of key tid / 4, bytes 16 (tid % 4) .. +16 (dims 32 (tid % 4) ..)
-  //   vw   value codes of keys 4 (tid % 16) + e, bytes 4 (tid / 16) .. +4 (dims 8 (tid / 16) ..)
+  //   kw   key codes of key tid / 4, dims 32 (tid % 4) .. +32 (as nibbles)
+  //   vw   value codes of keys 4 (tid % 16) + e, dims 8 (tid / 16) .. +8 (as nibbles)
   //   nrm  threads < 128: key (tid < 64) or value norm of key tid % 64
-  const uint8_t* kcod = P.k_codes + bh * static_cast<size_t>(P.cap) * kRowB;
-  const uint8_t* vcod = P.v_codes + bh * static_cast<size_t>(P.cap) * kRowB;
+  const uint8_t* kcod = P.k_codes + bh * static_cast<size_t>(P.cap) * RB;
+  const uint8_t* vcod = P.v_codes + bh * static_cast<size_t>(P.cap) * RB;
   const float* norms = ((tid >> 6) & 1 ? P.v_norms : P.k_norms) + bh * static_cast<size_t>(P.cap);
   const int kk = tid >> 2, part = tid & 3;  // key decode
   const int kp = tid & 15, j4 = tid >> 4;   // value decode
@@ -336,11 +378,10 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
   };
   auto load_tile = [&](TileRegs& R, int t0) {
     if (cold_len > 0) {  // rows past cold_len read the last cold row (valid memory), decoded from elsewhere
-      R.kw = *reinterpret_cast<const uint4*>(kcod + static_cast<size_t>(min(t0 + kk, cold_len - 1)) * kRowB + 16 * part);
+      R.kw = codes32<CB>(kcod + static_cast<size_t>(min(t0 + kk, cold_len - 1)) * RB + 4 * CB * part);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        R.vw[e] = *reinterpret_cast<const uint32_t*>(
-            vcod + static_cast<size_t>(min(t0 + 4 * kp + e, cold_len - 1)) * kRowB + 4 * j4);
+        R.vw[e] = codes8<CB>(vcod + static_cast<size_t>(min(t0 + 4 * kp + e, cold_len - 1)) * RB + CB * j4);
     }
     if (tid < 128) {
       const int tk = t0 + (tid & 63);
@@ -652,7 +693,7 @@ extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const 
                                    int bits, int64_t kv_len, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
                                    int64_t cap, int64_t hot_cap, float scale, void* out, void* workspace,
                                    size_t workspace_bytes, void* stream) {
-  LKV_REQUIRE(bits == 3 || bits == 4, "tq_prefill_attn: bits=%d unsupported (4-bit nibble layouts only)", bits);
+  LKV_REQUIRE(bits >= 1 && bits <= 4, "tq_prefill_attn: bits=%d unsupported (1..4 are bit-packed)", bits);
   LKV_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "tq_prefill_attn: need Hq %% Hkv == 0 (Hq=%lld Hkv=%lld)",
               (long long)Hq, (long long)Hkv);
   const int64_t G = Hq / Hkv;
@@ -713,10 +754,12 @@ extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const 
   P.ncent = 1 << bits;
   const int64_t QT = kCols / G;
   const dim3 grid(static_cast<unsigned>((S + QT - 1) / QT), static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
-  if (bits == 3)
-    hipLaunchKernelGGL((tq_prefill_attn_kernel<true>), grid, dim3(kThreads), 0, st, P);
-  else
-    hipLaunchKernelGGL((tq_prefill_attn_kernel<false>), grid, dim3(kThreads), 0, st, P);
+  switch (bits) {
+    case 1: hipLaunchKernelGGL((tq_prefill_attn_kernel<true, 1>), grid, dim3(kThreads), 0, st, P); break;
+    case 2: hipLaunchKernelGGL((tq_prefill_attn_kernel<true, 2>), grid, dim3(kThreads), 0, st, P); break;
+    case 3: hipLaunchKernelGGL((tq_prefill_attn_kernel<true, 4>), grid, dim3(kThreads), 0, st, P); break;
+    default: hipLaunchKernelGGL((tq_prefill_attn_kernel<false, 4>), grid, dim3(kThreads), 0, st, P);
+  }
   LKV_LAUNCH_CHECK("tq_prefill_attn");
   return LKV_OK;
 }

@@ -383,6 +383,14 @@ def tq_cache_append(k_new, v_new, k_hot, v_hot, k_codes, k_norms, v_codes, v_nor
     )
 
 
+def _check_code_rows(k_codes: torch.Tensor, v_codes: torch.Tensor, bits: int, what: str) -> None:
+    rb = packed_row_bytes(bits)
+    for t, nm in ((k_codes, "k_codes"), (v_codes, "v_codes")):
+        if t.dtype != torch.uint8 or t.shape[-1] != rb:
+            raise LeanKVError("%s: %s must be uint8 rows of %d bytes at %d bits, got %s %s"
+                              % (what, nm, rb, bits, t.dtype, tuple(t.shape)))
+
+
 def decode_attn_workspace_bytes(B: int, Hq: int, Hkv: int, max_len: int) -> int:
     return int(_lib_handle().lkv_tq_decode_attn_workspace_bytes(B, Hq, Hkv, max_len))
 
@@ -391,8 +399,8 @@ def tq_decode_attn_out(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK,
                        max_len: int, scale: float, out: torch.Tensor, workspace: torch.Tensor | None = None):
     """Single-query GQA attention over the packed cold cache + fp16 hot ring.
 
-    q: fp16 [B, Hq, 128]; codes uint8 [B, Hkv, cap, 64]; norms fp32 [B, Hkv, cap];
-    hot fp16 [B, Hkv, hot_cap, 128]; seq_len_dev int32 [1] (device); out fp16 [B, Hq, 128].
+    q: fp16 [B, Hq, 128]; codes uint8 [B, Hkv, cap, packed_row_bytes(bits)]; norms fp32 [B, Hkv, cap];
+    hot fp16 [B, Hkv, hot_cap, 128] (hot_cap <= 256); seq_len_dev int32 [1] (device); out fp16 [B, Hq, 128].
     """
     require_cuda(q, k_codes, v_codes, k_hot, v_hot, seq_len_dev, out)
     if q.dtype != torch.float16 or q.dim() != 3 or q.shape[-1] != HEAD_DIM or not q.is_contiguous():
@@ -408,6 +416,7 @@ def tq_decode_attn_out(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK,
             raise LeanKVError("tq_decode_attn: %s must be contiguous" % nm)
     if k_norms.dtype != torch.float32 or v_norms.dtype != torch.float32:
         raise LeanKVError("tq_decode_attn: norms must be float32")
+    _check_code_rows(k_codes, v_codes, bits, "tq_decode_attn")
     if k_hot.dtype != torch.float16 or v_hot.dtype != torch.float16:
         raise LeanKVError("tq_decode_attn: hot window must be float16")
     if seq_len_dev.dtype != torch.int32:
@@ -442,8 +451,8 @@ def tq_prefill_attn_out(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK
                         scale: float, out: torch.Tensor, workspace: torch.Tensor | None = None):
     """Causal attention of the newest S tokens' queries over the packed cold cache + fp16 hot ring.
 
-    q: fp16 [B, Hq, S, 128] (post-RoPE, positions kv_len - S ..); codes uint8 [B, Hkv, cap, 64];
-    norms fp32 [B, Hkv, cap]; hot fp16 [B, Hkv, hot_cap, 128]; out fp16 [B, Hq, S, 128].
+    q: fp16 [B, Hq, S, 128] (post-RoPE, positions kv_len - S ..); codes uint8 [B, Hkv, cap,
+    packed_row_bytes(bits)]; norms fp32 [B, Hkv, cap]; hot fp16 [B, Hkv, hot_cap, 128]; out fp16 [B, Hq, S, 128].
     """
     require_cuda(q, k_codes, v_codes, k_hot, v_hot, out)
     if q.dtype != torch.float16 or q.dim() != 4 or q.shape[-1] != HEAD_DIM or not q.is_contiguous():
@@ -459,6 +468,7 @@ def tq_prefill_attn_out(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK
             raise LeanKVError("tq_prefill_attn: %s must be contiguous" % nm)
     if k_norms.dtype != torch.float32 or v_norms.dtype != torch.float32:
         raise LeanKVError("tq_prefill_attn: norms must be float32")
+    _check_code_rows(k_codes, v_codes, bits, "tq_prefill_attn")
     if k_hot.dtype != torch.float16 or v_hot.dtype != torch.float16:
         raise LeanKVError("tq_prefill_attn: hot window must be float16")
     dev = q.device
@@ -527,14 +537,16 @@ def tq_paged_decode_attn(q: torch.Tensor, k_codes: torch.Tensor, k_norms: torch.
                          kv_indices: torch.Tensor, seq_lens: torch.Tensor, max_len: int, scale: float | None = None,
                          out: torch.Tensor | None = None) -> torch.Tensor:
     """Decode attention of q fp16 [B, Hq, 128] over a paged packed cache: code pools uint8
-    [max_pages, Hkv, page_size, 64], norm pools fp32 [max_pages, Hkv, page_size], fp16 hot rings
+    [max_pages, Hkv, page_size, packed_row_bytes(bits)], norm pools fp32 [max_pages, Hkv, page_size], fp16 hot rings
     [B, Hkv, hot_cap, 128], FlashInfer's CSR page table and per-sequence lengths (int32 device tensors)."""
     require_cuda(q, k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, kv_indptr, kv_indices, seq_lens)
     if q.dtype != torch.float16 or q.dim() != 3 or q.shape[-1] != HEAD_DIM or not q.is_contiguous():
         raise LeanKVError("tq_paged_decode_attn: q must be contiguous float16 [B, Hq, 128]")
     B, Hq, _ = q.shape
-    if k_codes.dim() != 4 or k_codes.dtype != torch.uint8 or k_codes.shape[-1] != 64:
-        raise LeanKVError("tq_paged_decode_attn: code pools must be uint8 [max_pages, Hkv, page_size, 64]")
+    rb = packed_row_bytes(bits)
+    if k_codes.dim() != 4 or k_codes.dtype != torch.uint8 or k_codes.shape[-1] != rb:
+        raise LeanKVError("tq_paged_decode_attn: code pools must be uint8 [max_pages, Hkv, page_size, %d] at %d bits"
+                          % (rb, bits))
     max_pages, Hkv, page_size, _ = k_codes.shape
     for t, shape, dt, nm in ((v_codes, k_codes.shape, torch.uint8, "v_codes"),
                              (k_norms, k_codes.shape[:3], torch.float32, "k_norms"),

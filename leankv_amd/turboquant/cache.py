@@ -8,9 +8,10 @@ seeded ``seed + 2 i`` (keys) and ``seed + 2 i + 1`` (values); attention sees
 cold tokens dequantized, then the hot window, in position order.
 
 Storage is MI355X-shaped instead of a list of torch.cat'ed tensors:
-  codes  uint8 [B, Hkv, cap, 64]   norms fp32 [B, Hkv, cap]    (cold, per K/V)
+  codes  uint8 [B, Hkv, cap, rb]   norms fp32 [B, Hkv, cap]    (cold, per K/V)
   hot    fp16  [B, Hkv, hot, 128]  ring: token p lives in slot p % hot
-so a decode step writes 64 + 4 bytes per (head, K/V) instead of re-concatenating
+with rb the reference's packed row (64 bytes at 3 and 4 bits, 32 at 2, 16 at
+1), so a decode step writes rb + 4 bytes per (head, K/V) instead of re-concatenating
 the whole store, and ``cap`` grows by doubling when a sequence outgrows it.
 
 By default update() returns the reference's full K/V -- cold dequantized to
@@ -66,11 +67,11 @@ class TurboQuantCache:
         self._device = torch.device(device) if device is not None else torch.device("cuda")
         self._dtype = dtype
         self.fused_attention = bool(fused_attention)
-        # the packed-KV attention kernels read 4-bit nibble rows (bits 3, 4); the
-        # decode kernel keeps the fp16 window in one wave (at most 64 tokens):
-        # other caches attend to the dequantized K/V with SDPA
-        self.fused_prefill = bits in (3, 4)
-        self.fused_decode = bits in (3, 4) and hot_buffer_size <= 64
+        # the packed-KV attention kernels read every packing (1..4 bits); the
+        # decode combine walks at most 256 hot slots: a larger window attends to
+        # the dequantized K/V with SDPA
+        self.fused_prefill = True
+        self.fused_decode = hot_buffer_size <= 256
         self._seen_tokens = 0
         self._seq_lengths = [0] * num_layers
         self._init_cap = max(int(max_seq_len), 1)

@@ -5,7 +5,7 @@ No single reference counterpart: the reference's paged cache
 its TurboQuant cache (leankv/turboquant/cache.py:35-351) one dense store per
 batch.  This joins the two for ragged batches:
 
-  cold (per layer, per K / V)  codes uint8 [max_pages, Hkv, page_size, 64]
+  cold (per layer, per K / V)  codes uint8 [max_pages, Hkv, page_size, row_bytes] (64 at 3, 4 bits; 32 at 2; 16 at 1)
                                norms fp32  [max_pages, Hkv, page_size]
   hot  (per layer, per K / V)  fp16 [max_batch_size, Hkv, hot, 128], token p in slot p % hot
 
@@ -39,12 +39,12 @@ class PagedTurboQuantCache:
                  max_batch_size: int = 16, seed: int = 42, device=None):
         if head_dim != _k.HEAD_DIM:
             raise ValueError("PagedTurboQuantCache: head_dim must be %d for the HIP kernels" % _k.HEAD_DIM)
-        if bits not in (3, 4):
-            raise ValueError("PagedTurboQuantCache: bits must be 3 or 4 (4-bit nibble pages)")
+        if bits not in (1, 2, 3, 4):
+            raise ValueError("PagedTurboQuantCache: bits must be 1..4")
         if page_size not in (16, 32, 64, 128):
             raise ValueError("PagedTurboQuantCache: page_size must be 16, 32, 64 or 128")
-        if not 1 <= hot_buffer_size <= 64:
-            raise ValueError("PagedTurboQuantCache: hot_buffer_size must be 1..64")
+        if not 1 <= hot_buffer_size <= 256:
+            raise ValueError("PagedTurboQuantCache: hot_buffer_size must be 1..256")
         if num_q_heads % num_kv_heads or num_q_heads // num_kv_heads > 16:
             raise ValueError("PagedTurboQuantCache: num_q_heads must be a multiple of num_kv_heads, at most 16x")
         self.num_layers, self.num_kv_heads, self.num_q_heads = num_layers, num_kv_heads, num_q_heads
@@ -57,7 +57,8 @@ class PagedTurboQuantCache:
         self.centroids, bnd = get_codebook_tensors(head_dim, bits, dev, torch.float32)
         self.decision_boundaries = bnd[1:-1].contiguous()
         L, H, ps = num_layers, num_kv_heads, page_size
-        self.k_codes = torch.zeros(L, max_pages, H, ps, 64, dtype=torch.uint8, device=dev)
+        self._row_bytes = _k.packed_row_bytes(bits)  # 64 at 3 and 4 bits, 32 at 2, 16 at 1
+        self.k_codes = torch.zeros(L, max_pages, H, ps, self._row_bytes, dtype=torch.uint8, device=dev)
         self.v_codes = torch.zeros_like(self.k_codes)
         self.k_norms = torch.zeros(L, max_pages, H, ps, dtype=torch.float32, device=dev)
         self.v_norms = torch.zeros_like(self.k_norms)
@@ -123,7 +124,7 @@ class PagedTurboQuantCache:
             pages = self._seq_pages[b]
             pg = torch.tensor([pages[p // ps] for p in range(c0, c1)], dtype=torch.long, device=dev)
             sl = torch.tensor([p % ps for p in range(c0, c1)], dtype=torch.long, device=dev)
-            self.k_codes[li][pg, :, sl] = pk.transpose(0, 1)  # [n, Hkv, 64]
+            self.k_codes[li][pg, :, sl] = pk.transpose(0, 1)  # [n, Hkv, row bytes]
             self.v_codes[li][pg, :, sl] = pv.transpose(0, 1)
             self.k_norms[li][pg, :, sl] = nk.t()
             self.v_norms[li][pg, :, sl] = nv.t()
@@ -161,7 +162,7 @@ class PagedTurboQuantCache:
                 pages = self._seq_pages[b]
                 pg = torch.tensor([pages[p // ps] for p in range(c)], dtype=torch.long, device=self._device)
                 sl = torch.tensor([p % ps for p in range(c)], dtype=torch.long, device=self._device)
-                kc = self.k_codes[li][pg, :, sl].transpose(0, 1).contiguous()  # [Hkv, c, 64]
+                kc = self.k_codes[li][pg, :, sl].transpose(0, 1).contiguous()  # [Hkv, c, row bytes]
                 vc = self.v_codes[li][pg, :, sl].transpose(0, 1).contiguous()
                 kn = self.k_norms[li][pg, :, sl].t().contiguous()
                 vn = self.v_norms[li][pg, :, sl].t().contiguous()
@@ -176,7 +177,7 @@ class PagedTurboQuantCache:
         return keys, values
 
     def cold_arrays(self, layer_idx: int, b: int):
-        """Sequence b's cold codes and norms in position order: (k_codes [Hkv, c, 64], k_norms [Hkv, c],
+        """Sequence b's cold codes and norms in position order: (k_codes [Hkv, c, row bytes], k_norms [Hkv, c],
         v_codes, v_norms)."""
         li, ps = layer_idx, self.page_size
         c = max(0, self._lengths[li][b] - self.hot_buffer_size)
@@ -251,7 +252,7 @@ class PagedTurboQuantCache:
 
     def get_memory_usage_mb(self) -> float:
         """Cold bytes of the pages in use (codes + norms, K and V, every layer) plus the hot rings."""
-        per_page = self.num_kv_heads * self.page_size * (64 + 4) * 2
+        per_page = self.num_kv_heads * self.page_size * (self._row_bytes + 4) * 2
         hot = self.k_hot.numel() * 2 * 2
         return (self.get_pages_used() * per_page * self.num_layers + hot) / 1e6
 

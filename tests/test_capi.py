@@ -126,8 +126,19 @@ def test_invalid_arguments_rejected_without_launch():
     assert lib.lkv_tq_paged_decode_attn(p, p, p, p, p, p, p, p, p, p, 3, p, p, p, 2, 32, 8, 16, 1 << 20, 100, 64,
                                         0.1, p, p, 1 << 20, None) == -1
     assert "2^32" in _lib.last_error()
-    assert lib.lkv_tq_paged_decode_attn(p, p, p, p, p, p, p, p, p, p, 2, p, p, p, 2, 32, 8, 16, 64, 100, 64, 0.1,
+    assert lib.lkv_tq_paged_decode_attn(p, p, p, p, p, p, p, p, p, p, 5, p, p, p, 2, 32, 8, 16, 64, 100, 64, 0.1,
                                         p, p, 1 << 20, None) == -1
+    assert "bits" in _lib.last_error()
+    # hot windows up to 256 slots (the combine's slot groups)
+    assert lib.lkv_tq_paged_decode_attn(p, p, p, p, p, p, p, p, p, p, 2, p, p, p, 2, 32, 8, 16, 64, 100, 257, 0.1,
+                                        p, p, 1 << 20, None) == -1
+    assert "hot_cap" in _lib.last_error()
+    assert lib.lkv_tq_decode_attn(p, p, p, p, p, p, p, p, p, p, 1, p, 64, 1, 32, 8, 64, 257, 0.1, p, p,
+                                  1 << 20, None) == -1
+    assert "hot_cap" in _lib.last_error()
+    assert lib.lkv_tq_decode_attn(p, p, p, p, p, p, p, p, p, p, 0, p, 64, 1, 32, 8, 64, 64, 0.1, p, p,
+                                  1 << 20, None) == -1
+    assert "bits" in _lib.last_error()
     assert lib.lkv_tq_paged_decode_attn(p, p, p, p, p, p, p, p, p, p, 3, p, p, p, 16, 32, 8, 16, 64, 4096, 64,
                                         0.1, p, p, 256, None) == -1
     assert "workspace" in _lib.last_error()

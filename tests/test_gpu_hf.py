@@ -220,21 +220,25 @@ def test_sliding_window_shorter_than_cache_uses_masked_sdpa(cuda):
         assert torch.equal(sa, sb)
 
 
-def test_hot_window_above_64(cuda):
-    """hot_buffer_size=128 (the reference accepts any size, cache.py:35-44): prefill on the packed kernel,
-    decode on SDPA over the reference's K/V; scores vs the oracle with a 128-token window."""
+@pytest.mark.parametrize("bits,hot,fused", [(3, 128, True), (2, 64, True), (1, 200, True), (3, 300, False)])
+def test_cache_widths_and_windows(cuda, bits, hot, fused):
+    """The reference accepts any hot_buffer_size and bits 1..4 (cache.py:35-44, quantizer.py:38-62): 2-bit
+    and 1-bit packings and windows up to 256 tokens run both packed kernels (prefill and decode); a larger
+    window decodes on SDPA over the reference's K/V.  Scores vs the oracle decoder with the same cache."""
     from leankv_amd.turboquant.attention import use_on
     from leankv_amd.turboquant.cache import TurboQuantCache
 
-    model = _model(cuda, 38)
+    print("cache case bits=%d hot=%d" % (bits, hot), flush=True)
+    model = _model(cuda, 38 + bits)
     state = _state(model)
-    cache = TurboQuantCache(bits=3, head_dim=128, num_layers=2, hot_buffer_size=128, device=cuda, max_seq_len=512)
+    cache = TurboQuantCache(bits=bits, head_dim=128, num_layers=2, hot_buffer_size=hot, device=cuda,
+                            max_seq_len=512)
     use_on(model, cache)
-    assert cache.fused_prefill and not cache.fused_decode
-    prompt = _ids(200, 39)
+    assert cache.fused_prefill and cache.fused_decode == fused
+    prompt = _ids(320, 39)
     res = _generate(model, prompt.to(cuda), cache, 12)
-    new = res.sequences[0, 200:].cpu()
-    ref = RefModel(state, model.config, None, hot=128)
+    new = res.sequences[0, 320:].cpu()
+    ref = RefModel(state, model.config, None, bits=bits, hot=hot)
     errs = [ot.rel_err(s[0].float().cpu().numpy(), r.numpy()) for s, r in zip(res.scores, _ref_scores(
         ref, prompt[0], new))]
     assert max(errs) < RTOL, errs

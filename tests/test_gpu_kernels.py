@@ -560,6 +560,10 @@ def test_tq_cache_append_matches_reference_cache(cuda):
 
 
 # ----------------------------------------------------------------- attention
+# packed row bytes per bit width (quantizer.py:38-62: 8 / 4 / 2 codes per byte)
+_ROW_BYTES = {1: 16, 2: 32, 3: 64, 4: 64}
+
+
 def _attn_case(B, Hq, Hkv, L, hot, seed, dev, bits=3):
     """Build a cache of L tokens (cold = L - hot) with the oracle, run the HIP kernel."""
     from leankv_amd import kernels
@@ -572,7 +576,7 @@ def _attn_case(B, Hq, Hkv, L, hot, seed, dev, bits=3):
     V = _kv((B, Hkv, L, 128), seed + 1000)
     q = torch.randn(B, Hq, 128, generator=torch.Generator().manual_seed(seed + 7)).half()
     cap = max(cold, 1)
-    kc = torch.zeros(B, Hkv, cap, 64, dtype=torch.uint8)
+    kc = torch.zeros(B, Hkv, cap, _ROW_BYTES[bits], dtype=torch.uint8)
     vc = torch.zeros_like(kc)
     kn = torch.zeros(B, Hkv, cap)
     vn = torch.zeros_like(kn)
@@ -616,6 +620,21 @@ def test_decode_attn_edges(cuda, B, Hq, Hkv, L, hot):
     assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
 
 
+# Every packing the cache stores (1 and 2 bits: 8 / 4 codes per byte, widened to nibbles in registers;
+# 4 bits: the LDS table) and hot windows past one 64-slot group (128, 200, 256 slots; the window full
+# and partly filled), including config 4 at 2 bits (the reference sweep's 2.5-bit setting, int() = 2).
+@pytest.mark.parametrize("B,Hq,Hkv,L,hot,bits", [
+    (1, 32, 8, 1000, 64, 1), (4, 32, 8, 4096 + 64, 64, 2), (2, 16, 2, 333, 16, 2), (1, 32, 8, 2100, 64, 4),
+    (1, 32, 8, 1000, 128, 3), (2, 8, 4, 150, 200, 3), (1, 32, 8, 3000, 256, 2), (1, 32, 8, 130, 256, 1),
+    (3, 32, 8, 700, 100, 3)])
+def test_decode_attn_bits_and_hot(cuda, B, Hq, Hkv, L, hot, bits):
+    print("decode attn case B=%d Hq=%d Hkv=%d L=%d hot=%d bits=%d" % (B, Hq, Hkv, L, hot, bits), flush=True)
+    out, ref = _attn_case(B, Hq, Hkv, L, hot, seed=L + bits, dev=cuda, bits=bits)
+    assert torch.isfinite(out).all()
+    assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
+    assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
+
+
 def _prefill_case(B, Hq, Hkv, L, S, hot, seed, dev, bits=3):
     """A cache of L tokens (cold = L - hot, built with the oracle) and the newest S tokens' queries:
     the HIP prefill kernel vs causal fp64 attention over cat(dequantize(cold).fp16, hot)."""
@@ -628,7 +647,7 @@ def _prefill_case(B, Hq, Hkv, L, S, hot, seed, dev, bits=3):
     V = _kv((B, Hkv, L, 128), seed + 1000)
     q = torch.randn(B, Hq, S, 128, generator=torch.Generator().manual_seed(seed + 7)).half()
     cap = max(cold, 1)
-    kc = torch.zeros(B, Hkv, cap, 64, dtype=torch.uint8)
+    kc = torch.zeros(B, Hkv, cap, _ROW_BYTES[bits], dtype=torch.uint8)
     vc = torch.zeros_like(kc)
     kn = torch.zeros(B, Hkv, cap)
     vn = torch.zeros_like(kn)
@@ -658,8 +677,10 @@ def _prefill_case(B, Hq, Hkv, L, S, hot, seed, dev, bits=3):
 @pytest.mark.parametrize("B,Hq,Hkv,L,S,hot,bits", [
     (1, 8, 2, 100, 100, 64, 3), (1, 4, 4, 37, 37, 64, 3), (1, 32, 8, 200, 1, 64, 3), (2, 16, 2, 300, 77, 16, 3),
     (1, 16, 1, 130, 130, 64, 4), (1, 32, 8, 700, 700, 64, 3), (1, 2, 2, 64, 64, 64, 3), (1, 8, 4, 65, 65, 64, 3),
-    (3, 8, 8, 257, 129, 64, 4), (1, 32, 4, 333, 333, 64, 3)])
+    (3, 8, 8, 257, 129, 64, 4), (1, 32, 4, 333, 333, 64, 3),
+    (1, 32, 8, 500, 500, 64, 2), (2, 8, 2, 300, 40, 64, 1), (1, 16, 4, 700, 700, 128, 2)])
 def test_prefill_attn(cuda, B, Hq, Hkv, L, S, hot, bits):
+    print("prefill case B=%d Hq=%d Hkv=%d L=%d S=%d hot=%d bits=%d" % (B, Hq, Hkv, L, S, hot, bits), flush=True)
     out, ref = _prefill_case(B, Hq, Hkv, L, S, hot, seed=L + S, dev=cuda, bits=bits)
     assert torch.isfinite(out).all()
     assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
@@ -759,8 +780,9 @@ def _paged_tq_case(lens, Hq, Hkv, hot, ps, bits, seed, dev):
     max_pages = sum(npages) + 3
     perm = torch.randperm(max_pages, generator=g).tolist()
     mask = 0x77 if bits == 3 else 0xFF
-    kc = torch.randint(0, 256, (max_pages, Hkv, ps, 64), generator=g, dtype=torch.uint8) & mask
-    vc = torch.randint(0, 256, (max_pages, Hkv, ps, 64), generator=g, dtype=torch.uint8) & mask
+    rb = _ROW_BYTES[bits]
+    kc = torch.randint(0, 256, (max_pages, Hkv, ps, rb), generator=g, dtype=torch.uint8) & mask
+    vc = torch.randint(0, 256, (max_pages, Hkv, ps, rb), generator=g, dtype=torch.uint8) & mask
     kn = torch.rand(max_pages, Hkv, ps, generator=g) * 50 + 50  # rows no sequence owns: large, visible if read
     vn = torch.rand(max_pages, Hkv, ps, generator=g) * 50 + 50
     kh = torch.randn(B, Hkv, hot, 128, generator=g).half()
@@ -810,6 +832,9 @@ def _paged_tq_case(lens, Hq, Hkv, hot, ps, bits, seed, dev):
     ([700, 1, 3000], 8, 8, 64, 64, 4),
     ([5000, 129, 4097], 64, 8, 64, 128, 3),
     ([9000] + [100] * 31, 8, 8, 64, 16, 3),
+    ([300, 4160, 65], 32, 8, 64, 16, 2),
+    ([129, 1000], 16, 4, 128, 32, 1),
+    ([2000, 5, 256], 32, 8, 256, 16, 3),
 ])
 def test_tq_paged_decode_attn(cuda, lens, Hq, Hkv, hot, ps, bits):
     out, ref = _paged_tq_case(lens, Hq, Hkv, hot, ps, bits, seed=sum(lens) % 1000 + ps, dev=cuda)
