@@ -1101,8 +1101,17 @@ def bench_decode(args, torch):
     dense_bytes = w_dense + head + L * Hkv * (ctx + 1) * 2 * 256
     sparsity = {p: round(1 - counts[p][0] / counts[p][1], 4) for p in row_bytes}
 
+    gen_lkv_hf = hf_generate(tq_cache)
+    _log("HF generate, LeanKV on the patched HF forward: %.1f tok/s (prefill included)" % gen_lkv_hf)
+    from leankv_amd.engine import disable_generate_fast_path, enable_generate_fast_path
+
+    fp = enable_generate_fast_path(model)  # what optimize_model installs for TEAL + TurboQuant
     gen_lkv = hf_generate(tq_cache)
-    _log("HF generate, LeanKV (TEAL + TurboQuant, packed-KV attention): %.1f tok/s (prefill included)" % gen_lkv)
+    gen_steps = dict(fp.steps)
+    disable_generate_fast_path(model)
+    torch.cuda.empty_cache()
+    _log("HF generate, LeanKV with the fused decode step: %.1f tok/s (prefill included), calls %s"
+         % (gen_lkv, gen_steps))
     res = {
         "metric": "B=1 decode tok/s (Mistral-7B shape, 40% sparse, 3-bit KV)",
         "value": round(tps, 2),
@@ -1139,11 +1148,14 @@ def bench_decode(args, torch):
         res["speedup_vs_dense_against"] = "own_kernels" if own_tps >= torch_tps else "torch"
         res["hf_generate"] = {
             "what": "model.generate(prompt, max_new_tokens=%d, past_key_values=fresh cache), prefill included "
-                    "(scripts/benchmark.py:68-99), mean of 2 runs" % new_tokens,
-            "leankv_tok_s": gen_lkv, "dense_fp16_tok_s": dense["generate"],
-            "speedup": round(gen_lkv / dense["generate"], 3)}
+                    "(scripts/benchmark.py:68-99), mean of 2 runs; leankv: optimize_model's generate fast path "
+                    "(single-token calls on the fused decode step), leankv_hf_forward: the patched HF forward "
+                    "for every call" % new_tokens,
+            "leankv_tok_s": gen_lkv, "leankv_hf_forward_tok_s": gen_lkv_hf, "dense_fp16_tok_s": dense["generate"],
+            "speedup": round(gen_lkv / dense["generate"], 3), "fast_path_calls": gen_steps}
     else:
-        res["hf_generate"] = {"leankv_tok_s": gen_lkv}
+        res["hf_generate"] = {"leankv_tok_s": gen_lkv, "leankv_hf_forward_tok_s": gen_lkv_hf,
+                              "fast_path_calls": gen_steps}
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_decode(torch, model, th, args.prompt)
     del model

@@ -8,6 +8,9 @@ Differences, all in the direction of the fast path:
     (``use_kernels=True``; the reference used the hook path here) and, when
     TurboQuant is on, selects the "leankv_tq" attention implementation so
     decode attention reads the packed cache directly.
+  * with TEAL and TurboQuant both on, generate's single-token decode calls run
+    the fused decode step replayed as a HIP graph (fast_decode=True, the
+    default; see engine.GenerateFastPath).
   * use_paged_cache=True asks for the reference's FlashInfer fp16 page pool
     (leankv/turboquant/paged_cache.py), which HF generate never calls and
     which is not built here; it raises RuntimeError, as the reference does
@@ -52,8 +55,13 @@ def load_model(model_name: str, dtype=torch.float16, device_map="cuda"):
 
 def optimize_model(model, teal_sparsity: Optional[float] = None, teal_thresholds_path: Optional[str] = None,
                    turboquant_bits: Optional[int] = None, use_paged_cache: bool = False, page_size: int = 16,
-                   max_pages: int = 2048, use_kernels: bool = True, max_seq_len: int = 4096):
-    """Apply TEAL and/or TurboQuant; returns (model, cache or None)."""
+                   max_pages: int = 2048, use_kernels: bool = True, max_seq_len: int = 4096,
+                   fast_decode: bool = True):
+    """Apply TEAL and/or TurboQuant; returns (model, cache or None).
+
+    fast_decode (not in the reference): with both TEAL and TurboQuant on the HIP kernels, single-token
+    decode calls of generate run the fused, graph-replayed decode step (engine.GenerateFastPath) when the
+    call is one it serves; every other call runs the patched HF forward."""
     if teal_sparsity is not None or teal_thresholds_path is not None:
         apply_teal(model, sparsity=teal_sparsity, thresholds_path=teal_thresholds_path, use_triton=use_kernels)
         label = teal_thresholds_path or "%.0f%%" % (100 * teal_sparsity)
@@ -73,9 +81,17 @@ def optimize_model(model, teal_sparsity: Optional[float] = None, teal_thresholds
 
             use_on(model, cache)
         print("[LeanKV] TurboQuant enabled (bits=%d, head_dim=%d)" % (turboquant_bits, head_dim))
+    teal_on = teal_sparsity is not None or teal_thresholds_path is not None
+    if fast_decode and use_kernels and teal_on and cache is not None and cache.fused_attention:
+        from .engine import enable_generate_fast_path
+
+        enable_generate_fast_path(model)
     return model, cache
 
 
 def reset_optimizations(model):
+    from .engine import disable_generate_fast_path
+
+    disable_generate_fast_path(model)
     remove_teal(model)
     print("[LeanKV] All optimizations removed.")

@@ -223,6 +223,123 @@ class LeanKVEngine(_Base):
                                        self.pos64.data_ptr(), ws, nb, st), "lkv_decode_head")
 
 
+class GenerateFastPath:
+    """model.forward for HF ``generate``: single-token decode steps on the fused decode step.
+
+    The reference's user path is ``model.generate(..., past_key_values=cache)``
+    (leankv/combined.py:13, scripts/benchmark.py:68-99), whose decode steps walk
+    the HF modules in Python, one patched projection at a time.  Installed on a
+    TEAL-patched model, this wrapper sends a call that LeanKVEngine computes the
+    same way -- one new token of one sequence (input_ids [1, 1]), a fused
+    TurboQuantCache at 3 bits with a 64-token window, no padding, no sliding
+    window shorter than the sequence, no attentions or hidden states asked for
+    -- to the engine, built on that cache's own buffers and replayed as a HIP
+    graph; it appends the token to the cache as update() would and returns the
+    last position's logits.  Every other call (the prefill, batches, other
+    caches) runs the model's own forward.  ``steps`` counts the calls served
+    each way."""
+
+    def __init__(self, model):
+        import inspect
+
+        self.model = model
+        self.forward = model.forward  # the model's own forward (bound)
+        # generate inspects forward's parameters (logits_to_keep, ...): report the model's own
+        self.__signature__ = inspect.signature(self.forward)
+        self.engine = None
+        self._cache = None  # the cache the engine was built on (held weakly through id + length checks)
+        self.steps = {"engine": 0, "forward": 0}
+
+    def _eligible(self, input_ids, cache, kw) -> bool:
+        if not isinstance(cache, TurboQuantCache) or not cache.fused_attention or not cache.fused_decode:
+            return False
+        if input_ids is None or input_ids.dim() != 2 or tuple(input_ids.shape) != (1, 1):
+            return False
+        if kw.get("inputs_embeds") is not None or kw.get("output_attentions") or kw.get("output_hidden_states"):
+            return False
+        if kw.get("return_dict") is False or kw.get("use_cache") is False or kw.get("labels") is not None:
+            return False
+        if cache.bits != 3 or cache.hot_buffer_size != 64 or cache.head_dim != 128:
+            return False
+        if cache._k_codes[0] is None or cache._k_codes[0].shape[0] != 1:
+            return False
+        n = cache._seq_lengths[0]
+        if n == 0 or any(x != n for x in cache._seq_lengths) or any(cache._fused_pending) or \
+                any(cache._prefill_pending):
+            return False
+        sw = getattr(self.model.config, "sliding_window", None)
+        if sw is not None and sw <= n:
+            return False
+        mask = kw.get("attention_mask")
+        if mask is not None and (mask.shape[-1] != n + 1 or not bool(mask.all())):
+            return False
+        return True
+
+    def _engine_for(self, cache: TurboQuantCache, length: int) -> "LeanKVEngine":
+        hot = cache.hot_buffer_size
+        if self.engine is not None and self._cache is cache and length <= self.engine.max_len:
+            return self.engine
+        # the engine holds the cache's buffers: grow them first (doubling, as update() does), then build
+        need = length - hot
+        if cache.cold_capacity(0) < need:
+            for li in range(cache.num_layers):
+                cache._ensure_cap(li, need)
+        self.engine = None
+        torch.cuda.empty_cache()
+        self.engine = LeanKVEngine(self.model, cache, cache.cold_capacity(0) + hot)
+        self._cache = cache
+        return self.engine
+
+    def __call__(self, input_ids=None, *args, **kw):
+        cache = kw.get("past_key_values")
+        if args or not self._eligible(input_ids, cache, kw):
+            self.steps["forward"] += 1
+            return self.forward(input_ids, *args, **kw)
+        from transformers.modeling_outputs import CausalLMOutputWithPast
+
+        n = cache._seq_lengths[0]
+        eng = self._engine_for(cache, n + 1)
+        with torch.no_grad():
+            if eng._host_pos != n:
+                eng._set_start(input_ids.view(1), n)
+            else:
+                eng.tok.copy_(input_ids.view(1))
+            first = eng.graph is None
+            eng.step()
+            if first:
+                eng.capture()
+            # the step appended the token to every layer (ring slot, the evicted token's codes): the
+            # cache's counters follow, as update() would have moved them
+            cache._seen_tokens += 1
+            for li in range(cache.num_layers):
+                cache._seq_lengths[li] = n + 1
+            logits = eng.logits.view(1, 1, -1).clone()
+        self.steps["engine"] += 1
+        return CausalLMOutputWithPast(logits=logits, past_key_values=cache)
+
+
+def enable_generate_fast_path(model) -> GenerateFastPath:
+    """Install GenerateFastPath as model.forward (idempotent); every projection must be TEAL-patched, so the
+    engine reads the patched column-major weights instead of copying them."""
+    if isinstance(getattr(model, "forward", None), GenerateFastPath):
+        return model.forward
+    for layer in model.model.layers:
+        for mod in (layer.self_attn.q_proj, layer.self_attn.k_proj, layer.self_attn.v_proj, layer.self_attn.o_proj,
+                    layer.mlp.gate_proj, layer.mlp.up_proj, layer.mlp.down_proj):
+            if getattr(mod, "_teal_threshold", None) is None:
+                raise ValueError("enable_generate_fast_path: every projection must be TEAL-patched first")
+    fp = GenerateFastPath(model)
+    model.forward = fp
+    return fp
+
+
+def disable_generate_fast_path(model) -> None:
+    fp = getattr(model, "forward", None)
+    if isinstance(fp, GenerateFastPath):
+        model.forward = fp.forward
+        fp.engine = None
+
+
 class OwnDenseEngine(_Base):
     """Dense fp16 decode on this library's kernels: the dense baseline of the LeanKV engine.
 

@@ -242,3 +242,81 @@ def test_cache_widths_and_windows(cuda, bits, hot, fused):
     errs = [ot.rel_err(s[0].float().cpu().numpy(), r.numpy()) for s, r in zip(res.scores, _ref_scores(
         ref, prompt[0], new))]
     assert max(errs) < RTOL, errs
+
+
+def _teal_pair(cuda, seed, **kw):
+    """One random TINY model, TEAL thresholds from a calibration pass, and two optimize_model copies of it
+    (TEAL + TurboQuant): `fast` with the generate fast path, `slow` without.  Both run their RMSNorm
+    modules through lkv_rmsnorm, the arithmetic of the fused step's prologue, so TEAL masks agree."""
+    import json
+    import tempfile
+
+    from leankv_amd.combined import optimize_model
+    from leankv_amd.teal.calibrate import calibrate_thresholds, uniform_random_sparsity
+    from leankv_amd.kernels import rms_norm
+
+    fast, slow = _model(cuda, seed, **kw), _model(cuda, seed, **kw)
+    th = calibrate_thresholds(fast, [_ids(64, seed + 1)], uniform_random_sparsity(0.3, 0.5, seed))
+    with tempfile.NamedTemporaryFile("w", suffix=".json", delete=False) as f:
+        json.dump({str(k): v for k, v in th.items()}, f)
+    out = []
+    for m, fd in ((fast, True), (slow, False)):
+        for mod in m.modules():
+            if type(mod).__name__.endswith("RMSNorm"):
+                mod.forward = (lambda x, mod=mod: rms_norm(x, mod.weight, mod.variance_epsilon))
+        out.append(optimize_model(m, teal_thresholds_path=f.name, turboquant_bits=3, max_seq_len=256,
+                                  fast_decode=fd))
+    return out[0], out[1]
+
+
+def test_generate_fast_path_matches_hf_forward(cuda):
+    """optimize_model's generate fast path (single-token decode calls on the fused, graph-replayed decode step)
+    vs the patched HF forward teacher-forced on the same tokens: per-step logits within 1e-3 (lm_head is the
+    GEMV kernel at threshold 0 on one side, torch's GEMM on the other), the same greedy tokens, and the two
+    caches equal bit for bit afterwards (the step appends and evicts as TurboQuantCache.update does)."""
+    from leankv_amd.engine import GenerateFastPath
+
+    (fast, ca), (slow, cb) = _teal_pair(cuda, 50)
+    assert isinstance(fast.forward, GenerateFastPath) and not isinstance(slow.forward, GenerateFastPath)
+    prompt = _ids(100, 51)  # longer than the 64-token window: the steps evict into the cold store
+    res = _generate(fast, prompt.to(cuda), ca, 16)
+    assert fast.forward.steps == {"engine": 15, "forward": 1}, fast.forward.steps
+    assert ca.get_seq_length(0) == 115
+    new = res.sequences[0, 100:]
+    errs = []
+    with torch.no_grad():
+        lg = slow(prompt.view(1, -1).to(cuda), past_key_values=cb, use_cache=True, logits_to_keep=1).logits[0, -1]
+        assert torch.equal(lg.float(), res.scores[0][0])  # the prefill runs the HF forward on both
+        for i in range(15):
+            lg = slow(new[i:i + 1].view(1, 1), past_key_values=cb, use_cache=True).logits[0, -1].float()
+            errs.append(float((res.scores[i + 1][0] - lg).norm() / lg.norm()))
+            assert int(torch.argmax(lg)) == int(new[i + 1]), i
+    print("generate fast path vs HF forward: max step rel err %.2e" % max(errs))
+    assert max(errs) < 1e-3
+    for li in range(2):
+        for a, b in ((ca._k_codes, cb._k_codes), (ca._v_codes, cb._v_codes), (ca._k_norms, cb._k_norms),
+                     (ca._v_norms, cb._v_norms), (ca._k_hot, cb._k_hot), (ca._v_hot, cb._v_hot)):
+            assert torch.equal(a[li], b[li]), li
+    # a second generate on a fresh cache builds a new engine on that cache's buffers
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    c2 = TurboQuantCache(bits=3, head_dim=128, num_layers=2, device=cuda, max_seq_len=256, fused_attention=True)
+    res2 = _generate(fast, prompt.to(cuda), c2, 16)
+    assert torch.equal(res2.sequences, res.sequences)
+    assert fast.forward.engine.cache is c2
+
+
+def test_generate_fast_path_falls_back(cuda):
+    """Calls the fused step does not serve run the model's own forward: a batch of two, a 2-bit cache."""
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    (fast, ca), _ = _teal_pair(cuda, 52)
+    fp = fast.forward
+    _generate(fast, _ids(70, 53, B=2).to(cuda), ca, 4)
+    assert fp.steps["engine"] == 0 and fp.engine is None
+    c2 = TurboQuantCache(bits=2, head_dim=128, num_layers=2, device=cuda, max_seq_len=256, fused_attention=True)
+    from leankv_amd.turboquant.attention import use_on
+
+    use_on(fast, c2)
+    _generate(fast, _ids(70, 54).to(cuda), c2, 4)
+    assert fp.steps["engine"] == 0 and fp.engine is None
