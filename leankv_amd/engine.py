@@ -231,7 +231,7 @@ class GenerateFastPath:
     the HF modules in Python, one patched projection at a time.  Installed on a
     TEAL-patched model, this wrapper sends a call that LeanKVEngine computes the
     same way -- one new token of one sequence (input_ids [1, 1]), a fused
-    TurboQuantCache at 3 bits with a 64-token window, no padding, no sliding
+    TurboQuantCache at 3 or 4 bits with a window of at most 64 tokens, no padding, no sliding
     window shorter than the sequence, no attentions or hidden states asked for
     -- to the engine, built on that cache's own buffers and replayed as a HIP
     graph; it appends the token to the cache as update() would and returns the
@@ -259,7 +259,7 @@ class GenerateFastPath:
             return False
         if kw.get("return_dict") is False or kw.get("use_cache") is False or kw.get("labels") is not None:
             return False
-        if cache.bits != 3 or cache.hot_buffer_size != 64 or cache.head_dim != 128:
+        if cache.bits not in (3, 4) or cache.hot_buffer_size > 64 or cache.head_dim != 128:
             return False
         if cache._k_codes[0] is None or cache._k_codes[0].shape[0] != 1:
             return False

@@ -244,7 +244,7 @@ def test_cache_widths_and_windows(cuda, bits, hot, fused):
     assert max(errs) < RTOL, errs
 
 
-def _teal_pair(cuda, seed, **kw):
+def _teal_pair(cuda, seed, bits=3, hot=64, **kw):
     """One random TINY model, TEAL thresholds from a calibration pass, and two optimize_model copies of it
     (TEAL + TurboQuant): `fast` with the generate fast path, `slow` without.  Both run their RMSNorm
     modules through lkv_rmsnorm, the arithmetic of the fused step's prologue, so TEAL masks agree."""
@@ -264,19 +264,29 @@ def _teal_pair(cuda, seed, **kw):
         for mod in m.modules():
             if type(mod).__name__.endswith("RMSNorm"):
                 mod.forward = (lambda x, mod=mod: rms_norm(x, mod.weight, mod.variance_epsilon))
-        out.append(optimize_model(m, teal_thresholds_path=f.name, turboquant_bits=3, max_seq_len=256,
-                                  fast_decode=fd))
+        m, c = optimize_model(m, teal_thresholds_path=f.name, turboquant_bits=bits, max_seq_len=256,
+                              fast_decode=fd)
+        if hot != 64:  # optimize_model builds the reference's default window; another size, same settings
+            from leankv_amd.turboquant.attention import use_on
+            from leankv_amd.turboquant.cache import TurboQuantCache
+
+            c = TurboQuantCache(bits=bits, head_dim=128, num_layers=m.config.num_hidden_layers, hot_buffer_size=hot,
+                                device=cuda, max_seq_len=256, fused_attention=True)
+            use_on(m, c)
+        out.append((m, c))
     return out[0], out[1]
 
 
-def test_generate_fast_path_matches_hf_forward(cuda):
+@pytest.mark.parametrize("bits,hot", [(3, 64), (4, 32)])
+def test_generate_fast_path_matches_hf_forward(cuda, bits, hot):
     """optimize_model's generate fast path (single-token decode calls on the fused, graph-replayed decode step)
     vs the patched HF forward teacher-forced on the same tokens: per-step logits within 1e-3 (lm_head is the
     GEMV kernel at threshold 0 on one side, torch's GEMM on the other), the same greedy tokens, and the two
     caches equal bit for bit afterwards (the step appends and evicts as TurboQuantCache.update does)."""
     from leankv_amd.engine import GenerateFastPath
 
-    (fast, ca), (slow, cb) = _teal_pair(cuda, 50)
+    print("fast path case bits=%d hot=%d" % (bits, hot), flush=True)
+    (fast, ca), (slow, cb) = _teal_pair(cuda, 50 + bits, bits=bits, hot=hot)
     assert isinstance(fast.forward, GenerateFastPath) and not isinstance(slow.forward, GenerateFastPath)
     prompt = _ids(100, 51)  # longer than the 64-token window: the steps evict into the cold store
     res = _generate(fast, prompt.to(cuda), ca, 16)
@@ -300,14 +310,16 @@ def test_generate_fast_path_matches_hf_forward(cuda):
     # a second generate on a fresh cache builds a new engine on that cache's buffers
     from leankv_amd.turboquant.cache import TurboQuantCache
 
-    c2 = TurboQuantCache(bits=3, head_dim=128, num_layers=2, device=cuda, max_seq_len=256, fused_attention=True)
+    c2 = TurboQuantCache(bits=bits, head_dim=128, num_layers=2, hot_buffer_size=hot, device=cuda, max_seq_len=256,
+                         fused_attention=True)
     res2 = _generate(fast, prompt.to(cuda), c2, 16)
     assert torch.equal(res2.sequences, res.sequences)
     assert fast.forward.engine.cache is c2
 
 
 def test_generate_fast_path_falls_back(cuda):
-    """Calls the fused step does not serve run the model's own forward: a batch of two, a 2-bit cache."""
+    """Calls the fused step does not serve run the model's own forward: a batch of two, a 2-bit cache, a
+    128-token window."""
     from leankv_amd.turboquant.cache import TurboQuantCache
 
     (fast, ca), _ = _teal_pair(cuda, 52)
@@ -319,4 +331,9 @@ def test_generate_fast_path_falls_back(cuda):
 
     use_on(fast, c2)
     _generate(fast, _ids(70, 54).to(cuda), c2, 4)
+    assert fp.steps["engine"] == 0 and fp.engine is None
+    c3 = TurboQuantCache(bits=3, head_dim=128, num_layers=2, hot_buffer_size=128, device=cuda, max_seq_len=256,
+                         fused_attention=True)
+    use_on(fast, c3)
+    _generate(fast, _ids(70, 55).to(cuda), c3, 4)
     assert fp.steps["engine"] == 0 and fp.engine is None
