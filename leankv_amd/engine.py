@@ -496,6 +496,46 @@ MISTRAL_7B = dict(vocab_size=32768, hidden_size=4096, intermediate_size=14336, n
                   rope_theta=1e6, rms_norm_eps=1e-5, sliding_window=None)
 
 
+# Llama-3-8B (named beside Mistral-7B by the reference's docs): the same decoder with a 128 K
+# vocabulary and RoPE base 500000.  Llama-3.1's "llama3" frequency scaling is an override:
+# rope_scaling=LLAMA31_ROPE, max_position_embeddings=131072.
+LLAMA3_8B = dict(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
+                 num_attention_heads=32, num_key_value_heads=8, head_dim=128, max_position_embeddings=8192,
+                 rope_theta=500000.0, rms_norm_eps=1e-5)
+LLAMA31_ROPE = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                "original_max_position_embeddings": 8192}
+
+
+@torch.no_grad()
+def random_llama(device="cuda", seed: int = 0, **overrides):
+    """Random-init fp16 LlamaForCausalLM of the Llama-3-8B shape (overridable), built as random_mistral."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    kw = dict(LLAMA3_8B)
+    kw.update(overrides)
+    return _random_init(LlamaForCausalLM, LlamaConfig(**kw), device, seed)
+
+
+def _random_init(cls, cfg, device, seed):
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(seed)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device(device):
+            model = cls(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    for name, p in model.named_parameters():
+        if p.dim() == 2:
+            p.copy_(torch.randn(p.shape, generator=gen, device=device, dtype=torch.float32).mul_(0.02).to(p.dtype))
+        else:
+            p.fill_(1.0)
+    model.eval()
+    return model
+
+
 @torch.no_grad()
 def random_mistral(device="cuda", seed: int = 0, **overrides):
     """Random-init fp16 MistralForCausalLM (weights ~N(0, 0.02), norms 1) built directly on `device`.
@@ -507,21 +547,4 @@ def random_mistral(device="cuda", seed: int = 0, **overrides):
 
     kw = dict(MISTRAL_7B)
     kw.update(overrides)
-    cfg = MistralConfig(**kw)
-    cfg._attn_implementation = "sdpa"
-    torch.manual_seed(seed)
-    prev = torch.get_default_dtype()
-    torch.set_default_dtype(torch.float16)
-    try:
-        with torch.device(device):
-            model = MistralForCausalLM(cfg)
-    finally:
-        torch.set_default_dtype(prev)
-    gen = torch.Generator(device=device).manual_seed(seed)
-    for name, p in model.named_parameters():
-        if p.dim() == 2:
-            p.copy_(torch.randn(p.shape, generator=gen, device=device, dtype=torch.float32).mul_(0.02).to(p.dtype))
-        else:
-            p.fill_(1.0)
-    model.eval()
-    return model
+    return _random_init(MistralForCausalLM, MistralConfig(**kw), device, seed)

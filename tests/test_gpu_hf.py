@@ -337,3 +337,49 @@ def test_generate_fast_path_falls_back(cuda):
     use_on(fast, c3)
     _generate(fast, _ids(70, 55).to(cuda), c3, 4)
     assert fp.steps["engine"] == 0 and fp.engine is None
+
+
+@pytest.mark.parametrize("scaled_rope", [False, True])
+def test_llama_generate_fast_path_and_engine(cuda, scaled_rope):
+    """A Llama-3-shaped decoder (LlamaForCausalLM, RoPE base 500000; with Llama-3.1's "llama3" frequency
+    scaling as well): TEAL + TurboQuant through optimize_model, generate's decode steps on the fused step vs
+    the patched HF forward teacher-forced on the same tokens, and the caches equal bit for bit."""
+    import json
+    import tempfile
+
+    from leankv_amd.combined import optimize_model
+    from leankv_amd.engine import LLAMA31_ROPE, GenerateFastPath, random_llama
+    from leankv_amd.kernels import rms_norm
+    from leankv_amd.teal.calibrate import calibrate_thresholds, uniform_random_sparsity
+
+    kw = dict(TINY)
+    if scaled_rope:
+        kw.update(rope_scaling=dict(LLAMA31_ROPE), max_position_embeddings=131072)
+    fast, slow = random_llama(cuda, seed=60, **kw), random_llama(cuda, seed=60, **kw)
+    th = calibrate_thresholds(fast, [_ids(64, 61)], uniform_random_sparsity(0.3, 0.5, 60))
+    with tempfile.NamedTemporaryFile("w", suffix=".json", delete=False) as f:
+        json.dump({str(k): v for k, v in th.items()}, f)
+    pairs = []
+    for m, fd in ((fast, True), (slow, False)):
+        for mod in m.modules():
+            if type(mod).__name__.endswith("RMSNorm"):
+                mod.forward = (lambda x, mod=mod: rms_norm(x, mod.weight, mod.variance_epsilon))
+        pairs.append(optimize_model(m, teal_thresholds_path=f.name, turboquant_bits=3, max_seq_len=256,
+                                    fast_decode=fd))
+    (fast, ca), (slow, cb) = pairs
+    assert isinstance(fast.forward, GenerateFastPath)
+    prompt = _ids(90, 62)
+    res = _generate(fast, prompt.to(cuda), ca, 12)
+    assert fast.forward.steps == {"engine": 11, "forward": 1}
+    new = res.sequences[0, 90:]
+    with torch.no_grad():
+        slow(prompt.view(1, -1).to(cuda), past_key_values=cb, use_cache=True, logits_to_keep=1)
+        for i in range(11):
+            lg = slow(new[i:i + 1].view(1, 1), past_key_values=cb, use_cache=True).logits[0, -1].float()
+            err = float((res.scores[i + 1][0] - lg).norm() / lg.norm())
+            assert err < 1e-3, (i, err)
+            assert int(torch.argmax(lg)) == int(new[i + 1]), i
+    for li in range(2):
+        for a, b in ((ca._k_codes, cb._k_codes), (ca._v_codes, cb._v_codes), (ca._k_hot, cb._k_hot),
+                     (ca._v_hot, cb._v_hot)):
+            assert torch.equal(a[li], b[li]), li
