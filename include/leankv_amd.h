@@ -485,9 +485,12 @@ int lkv_decode_layer_step_f16kv(const lkv_decode_dims* dims, const lkv_decode_la
                                 void* workspace, size_t workspace_bytes, void* stream);
 /* logits = lm_head(RMSNorm(x) * final_norm) (fp16 [vocab]); tok = argmax
  * (lowest index among equal maxima); pos += 1. */
+/* tok_history (optional, int64 [history_len] on the device): the step at
+ * position p also writes its token to tok_history[p] (p < history_len), so a
+ * replayed decode loop keeps every token without a copy per step. */
 int lkv_decode_head(const lkv_decode_dims* dims, const void* final_norm, const void* lm_head, const void* x,
-                    void* logits, int64_t* tok, int64_t* pos, void* workspace, size_t workspace_bytes,
-                    void* stream);
+                    void* logits, int64_t* tok, int64_t* pos, int64_t* tok_history, int64_t history_len,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -73,7 +73,7 @@ SIGNATURES = {
     "lkv_decode_evict": (_int, [_c_p, _c_p, ctypes.c_int64, _c_p, _sz, _c_p]),
     "lkv_decode_layer_step": (_int, [_c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
     "lkv_decode_layer_step_f16kv": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
-    "lkv_decode_head": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _sz, _c_p]),
+    "lkv_decode_head": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _sz, _c_p]),
 }
 
 

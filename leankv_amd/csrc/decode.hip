@@ -360,15 +360,18 @@ __global__ __launch_bounds__(kThreads) void logits_kernel(const float* __restric
 }
 
 __global__ __launch_bounds__(kThreads) void argmax_kernel(const Cand* __restrict__ cand, int ncand,
-                                                          int64_t* __restrict__ tok, int64_t* __restrict__ pos) {
+                                                          int64_t* __restrict__ tok, int64_t* __restrict__ pos,
+                                                          int64_t* __restrict__ hist, int64_t hist_len) {
   __shared__ Cand s_c[kThreads / kWave];
   float v = -INFINITY;
   int i = 0x7fffffff;
   for (int c = threadIdx.x; c < ncand; c += kThreads) argmax_merge(v, i, cand[c].v, cand[c].i);
   block_argmax(v, i, s_c);
   if (threadIdx.x == 0) {
-    *tok = i == 0x7fffffff ? 0 : i;
-    *pos = *pos + 1;
+    const int64_t t = i == 0x7fffffff ? 0 : i, p = *pos;
+    *tok = t;
+    *pos = p + 1;
+    if (hist != nullptr && p >= 0 && p < hist_len) hist[p] = t;
   }
 }
 
@@ -677,13 +680,14 @@ extern "C" int lkv_decode_layer_step_f16kv(const lkv_decode_dims* dims, const lk
 }
 
 extern "C" int lkv_decode_head(const lkv_decode_dims* dims, const void* final_norm, const void* lm_head, const void* x,
-                               void* logits, int64_t* tok, int64_t* pos, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+                               void* logits, int64_t* tok, int64_t* pos, int64_t* tok_history,
+                               int64_t history_len, void* workspace, size_t workspace_bytes, void* stream) {
   if (int e = check_dims(dims)) return e;
   const lkv_decode_dims& d = *dims;
   const Plan p = make_plan(d);
   if (int e = check_ws(p, workspace, workspace_bytes)) return e;
   LKV_REQUIRE(final_norm && lm_head && x && logits && tok && pos, "decode_head: null pointer");
+  LKV_REQUIRE(tok_history != nullptr || history_len == 0, "decode_head: history_len without a history buffer");
   LKV_REQUIRE(aligned16(lm_head) && aligned16(x), "decode_head: lm_head and x must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
@@ -705,7 +709,8 @@ extern "C" int lkv_decode_head(const lkv_decode_dims* dims, const void* final_no
   hipLaunchKernelGGL(logits_kernel, dim3(static_cast<unsigned>(p.svoc)), dim3(kThreads), 0, st, G.part,
                      static_cast<int>(d.vocab), p.nc_lm, static_cast<uint16_t*>(logits), cand);
   LKV_LAUNCH_CHECK("decode logits");
-  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kThreads), 0, st, cand, static_cast<int>(p.svoc), tok, pos);
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kThreads), 0, st, cand, static_cast<int>(p.svoc), tok, pos,
+                     tok_history, history_len);
   LKV_LAUNCH_CHECK("decode argmax");
   return LKV_OK;
 }

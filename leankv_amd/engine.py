@@ -71,6 +71,8 @@ class _Base:
         self.tok = torch.zeros(1, dtype=torch.long, device=self.dev)
         self.pos64 = torch.zeros(1, dtype=torch.long, device=self.dev)
         self.logits = torch.zeros(cfg.vocab_size, dtype=torch.float16, device=self.dev)
+        # hist[p]: the token the step at position p produced (written on the device inside the step)
+        self.hist = torch.zeros(max_len, dtype=torch.long, device=self.dev)
         self.graph = None
         self._host_pos = None  # position of the next step, tracked on the host to bound it by max_len
 
@@ -85,6 +87,7 @@ class _Base:
         x = _rms(x, self.model.model.norm.weight, self.eps)
         self.logits.copy_(F.linear(x, self.model.lm_head.weight).view(-1))
         self.tok.copy_(torch.argmax(self.logits).view(1))
+        self.hist.index_copy_(0, self.pos64, self.tok)
         self.pos64.add_(1)
 
     def capture(self, warmup: int = 0) -> None:
@@ -125,11 +128,10 @@ class _Base:
         if self._host_pos is not None and self._host_pos + n > self.max_len:
             raise _lib.LeanKVError("%d more tokens from position %d exceed the engine's max_len %d"
                                    % (n, self._host_pos, self.max_len))
-        out = []
+        p0 = self._host_pos
         for _ in range(n):
             self.step()
-            out.append(self.tok.clone())
-        return [int(t) for t in torch.cat(out).tolist()]
+        return [int(t) for t in self.hist[p0:p0 + n].tolist()]
 
 
 class LeanKVEngine(_Base):
@@ -220,7 +222,8 @@ class LeanKVEngine(_Base):
                        "lkv_decode_layer_step")
         _lib.check(lib.lkv_decode_head(dims, self.final_norm.data_ptr(), self.lm_head_cm.data_ptr(),
                                        self.x.data_ptr(), self.logits.data_ptr(), self.tok.data_ptr(),
-                                       self.pos64.data_ptr(), ws, nb, st), "lkv_decode_head")
+                                       self.pos64.data_ptr(), self.hist.data_ptr(), self.hist.numel(), ws, nb, st),
+                   "lkv_decode_head")
 
 
 class GenerateFastPath:
@@ -433,7 +436,8 @@ class OwnDenseEngine(_Base):
                                                        ws, nb, st), "lkv_decode_layer_step_f16kv")
         _lib.check(lib.lkv_decode_head(dims, self.final_norm.data_ptr(), self.lm_head_cm.data_ptr(),
                                        self.x.data_ptr(), self.logits.data_ptr(), self.tok.data_ptr(),
-                                       self.pos64.data_ptr(), ws, nb, st), "lkv_decode_head")
+                                       self.pos64.data_ptr(), self.hist.data_ptr(), self.hist.numel(), ws, nb, st),
+                   "lkv_decode_head")
 
 
 def _colmajor(w: torch.Tensor) -> torch.Tensor:

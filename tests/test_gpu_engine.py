@@ -180,12 +180,13 @@ def test_engine_matches_hf_path(cuda):
     first = torch.argmax(out.logits[0, -1])
     eng = LeanKVEngine(model, cache2, MAXLEN)
     eng.start(first, PROMPT)
-    errs, same = [], []
+    errs, same, fed_all = [], [], []
     with torch.no_grad():
         for i in range(STEPS):
             if i == 1:
                 eng.capture()
             fed = int(eng.tok)
+            fed_all.append(fed)
             eng.step()
             hf = model(torch.tensor([[fed]], device=cuda), past_key_values=cache, use_cache=True).logits[0, -1]
             errs.append(float((eng.logits.float() - hf.float()).norm() / hf.float().norm()))
@@ -195,6 +196,8 @@ def test_engine_matches_hf_path(cuda):
     assert max(errs) < 1e-3
     assert all(same)
     assert int(eng.pos64) == PROMPT + STEPS
+    # the device token history holds every step's token (step at position p -> hist[p])
+    assert eng.hist[PROMPT:PROMPT + STEPS].tolist() == fed_all[1:] + [int(eng.tok)]
     # the caches the two paths built are identical
     for li in range(model.config.num_hidden_layers):
         for a, b in ((cache._k_codes, cache2._k_codes), (cache._v_codes, cache2._v_codes),
