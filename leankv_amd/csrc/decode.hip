@@ -240,27 +240,30 @@ struct EvictLayer {
 struct EvictArgs {
   const int32_t* state;
   const float* bounds;
-  int hot_cap, cap;
+  int hot_cap, cap, Hkv;
   EvictLayer L[kEvictLayers];
 };
 
-// Grid (kv heads, {key, value}, layers).  At position pos the token pos -
-// hot_cap leaves the hot window (cache.py:84-141 flushes the oldest hot token
-// once the window exceeds hot_cap): it is normalised, rotated with Pi and
-// bucketed on one 16-row MFMA tile (row 0; tq_common.h's arithmetic, so the
-// codes equal lkv_tq_cache_append's), and its codes and norm go to cold slot
+// Grid (groups of 16 kv heads, {key, value}, layers).  At position pos the
+// token pos - hot_cap leaves the hot window (cache.py:84-141 flushes the
+// oldest hot token once the window exceeds hot_cap): the block takes that
+// token of up to 16 kv heads of one layer as the 16 rows of one MFMA tile
+// (row r = kv head 16 blockIdx.x + r), normalises, rotates with Pi and buckets
+// them (tq_common.h's arithmetic, row by row independent, so the codes equal
+// lkv_tq_cache_append's), and their codes and norms go to cold slot
 // pos - hot_cap.  Its ring slot, pos % hot_cap, is the one this step's new
-// token overwrites, so this kernel runs before the step's first layer; none
-// of the step's layer work depends on it until attention, so one launch
-// covers every layer.  The block's 64 KB rotation matrix is fetched first
-// with coalesced 16-byte loads and staged in LDS for the operand reads.
+// token overwrites, so this kernel runs before the step's first layer; none of
+// the step's layer work depends on it until attention, so one launch covers
+// every layer.  The block's 64 KB rotation matrix is fetched once for its 16
+// heads with coalesced 16-byte loads and staged in LDS for the operand reads.
 template <int BITS>
 __global__ __launch_bounds__(kThreads) void evict_kernel(EvictArgs A) {
   constexpr int kPiLd = kD + 1;  // padded LDS row
   __shared__ float s_pi[kD * kPiLd];
   __shared__ uint8_t s_codes[tq::kRows * kD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int kvh = blockIdx.x;
+  const int h0 = 16 * blockIdx.x;
+  const int nh = min(16, A.Hkv - h0);
   const bool vside = blockIdx.y == 1;
   const EvictLayer& Ly = A.L[blockIdx.z];
   const int pos = A.state[0];
@@ -274,12 +277,16 @@ __global__ __launch_bounds__(kThreads) void evict_kernel(EvictArgs A) {
 #pragma unroll
   for (int i = 0; i < (1 << BITS) - 1; ++i) bd[i] = A.bounds[i];
   const int r = lane & 15, c0 = 32 * (lane >> 4);
+  const bool row_ok = r < nh;
   const int slot = pos % A.hot_cap;
   const uint16_t* hot = vside ? Ly.v_hot : Ly.k_hot;
-  uint4 hraw[4];  // every lane loads the row's 64 bytes of its column group; rows r != 0 discard them
+  uint4 hraw[4];  // row r: kv head h0 + r (rows past the heads read head h0 and are zeroed)
+  {
+    const int hh = h0 + (row_ok ? r : 0);
 #pragma unroll
-  for (int v = 0; v < 4; ++v)
-    hraw[v] = reinterpret_cast<const uint4*>(hot + (static_cast<size_t>(kvh) * A.hot_cap + slot) * kD + c0)[v];
+    for (int v = 0; v < 4; ++v)
+      hraw[v] = reinterpret_cast<const uint4*>(hot + (static_cast<size_t>(hh) * A.hot_cap + slot) * kD + c0)[v];
+  }
 #pragma unroll
   for (int i = 0; i < kD * kD / 4 / kThreads; ++i) {
     const int f = i * kThreads + tid;  // float4 index: row f / 32, columns 4 (f % 32) ..
@@ -290,15 +297,15 @@ __global__ __launch_bounds__(kThreads) void evict_kernel(EvictArgs A) {
     dst[3] = pr[i].w;
   }
   __syncthreads();
-  // tq::load_row_f16's conversion of the preloaded row; the other rows are zero
+  // tq::load_row_f16's conversion of the preloaded rows; rows past the heads are zero
   float a[32];
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const uint32_t w[4] = {hraw[v].x, hraw[v].y, hraw[v].z, hraw[v].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      a[8 * v + 2 * i] = r == 0 ? h2f(static_cast<uint16_t>(w[i] & 0xffffu)) : 0.f;
-      a[8 * v + 2 * i + 1] = r == 0 ? h2f(static_cast<uint16_t>(w[i] >> 16)) : 0.f;
+      a[8 * v + 2 * i] = row_ok ? h2f(static_cast<uint16_t>(w[i] & 0xffffu)) : 0.f;
+      a[8 * v + 2 * i + 1] = row_ok ? h2f(static_cast<uint16_t>(w[i] >> 16)) : 0.f;
     }
   }
   float bop[2][32];
@@ -309,14 +316,16 @@ __global__ __launch_bounds__(kThreads) void evict_kernel(EvictArgs A) {
     for (int s = 0; s < 32; ++s) bop[t][s] = row[s];
   }
   // cache.py:141 quantizes flush_k.float(): fp32 semantics on the fp16 data.
-  const float nrm = tq::normalize_row_f32_if(a, r == 0);
+  const float nrm = tq::normalize_row_f32_if(a, row_ok);
   f32x4 acc[2];
   tq::rotate_tile(a, bop, acc);
   tq::codes_to_lds<BITS>(acc, bd, wave, lane, s_codes);
-  if (tid == 0) (vside ? Ly.v_norms : Ly.k_norms)[static_cast<size_t>(kvh) * A.cap + ev] = nrm;
+  if (wave == 0 && lane < nh) (vside ? Ly.v_norms : Ly.k_norms)[static_cast<size_t>(h0 + lane) * A.cap + ev] = nrm;
   __syncthreads();
-  const int64_t roff = (static_cast<int64_t>(kvh) * A.cap + ev) * tq::row_bytes_for(BITS);
-  tq::pack_store<BITS>(s_codes, vside ? Ly.v_codes : Ly.k_codes, 0, 1, [=](int64_t) { return roff; });
+  const int cap = A.cap;
+  tq::pack_store<BITS>(s_codes, vside ? Ly.v_codes : Ly.k_codes, 0, nh, [=](int64_t row) {
+    return (static_cast<int64_t>(h0 + row) * cap + ev) * tq::row_bytes_for(BITS);
+  });
 }
 
 
@@ -464,6 +473,7 @@ extern "C" int lkv_decode_evict(const lkv_decode_dims* dims, const lkv_decode_la
     A.bounds = d.bounds;
     A.hot_cap = static_cast<int>(d.hot_cap);
     A.cap = static_cast<int>(d.cap);
+    A.Hkv = static_cast<int>(p.Hkv);
     for (int i = 0; i < nl; ++i) {
       const lkv_decode_layer& L = layers[l0 + i];
       A.L[i] = EvictLayer{static_cast<const uint16_t*>(L.k_hot), static_cast<const uint16_t*>(L.v_hot),
@@ -471,7 +481,7 @@ extern "C" int lkv_decode_evict(const lkv_decode_dims* dims, const lkv_decode_la
                           static_cast<uint8_t*>(L.v_codes),      static_cast<float*>(L.v_norms),
                           L.PiK,                                 L.PiV};
     }
-    const dim3 grid(static_cast<unsigned>(p.Hkv), 2, static_cast<unsigned>(nl));
+    const dim3 grid(static_cast<unsigned>((p.Hkv + 15) / 16), 2, static_cast<unsigned>(nl));
     if (d.bits == 3)
       hipLaunchKernelGGL((evict_kernel<3>), grid, dim3(kThreads), 0, st, A);
     else
