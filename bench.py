@@ -65,7 +65,7 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode", choices=["decode", "dense", "gemv", "mlp", "quant", "attn",
                                                                     "prefill", "batched", "paged", "tqpaged", "prod",
-                                                                    "copy"])
+                                                                    "copy", "generate"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=32, help="decoder layers (config 5 uses 32)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -1160,6 +1160,74 @@ def bench_decode(args, torch):
     return res
 
 
+def bench_generate(args, torch):
+    """Batched generate (the reference's sweep, scripts/sweep.py: batch sizes 1..32, 128 new tokens from a short
+    prompt): config 5's model with TEAL + TurboQuant 3-bit through optimize_model's pieces, model.generate at
+    B = 4 and 16 on a fresh cache, prefill included; tok/s = B x new tokens / wall time.  Decode calls go to
+    BatchedEngine (the HF forward's calls replayed as a graph; at B > 1 the reference's projections are dense)
+    or, for comparison, to the patched HF forward."""
+    from leankv_amd.engine import disable_generate_fast_path, enable_generate_fast_path, random_mistral
+    from leankv_amd.teal.calibrate import calibrate_thresholds, uniform_random_sparsity
+    from leankv_amd.teal.patching import apply_teal
+    from leankv_amd.turboquant.attention import use_on
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    dev = torch.device("cuda:0")
+    new, prompt_len = 128, 32
+    model = random_mistral(device=dev, seed=0, num_hidden_layers=args.layers)
+    cfg = model.config
+    g = torch.Generator().manual_seed(1)
+    with torch.no_grad():
+        th = calibrate_thresholds(model, [torch.randint(0, cfg.vocab_size, (1, 512), generator=g)],
+                                  uniform_random_sparsity(0.3, 0.5, seed=0))
+    apply_teal(model, thresholds=th, use_triton=True)
+    model.generation_config.eos_token_id = None
+
+    def run(B, fast):
+        ids = torch.randint(0, cfg.vocab_size, (B, prompt_len), generator=g).to(dev)
+        mask = torch.ones_like(ids)
+        cache = TurboQuantCache(bits=3, head_dim=128, num_layers=cfg.num_hidden_layers, device=dev,
+                                max_seq_len=prompt_len + new + 64, fused_attention=True)
+        use_on(model, cache)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        with torch.no_grad():
+            out = model.generate(ids, attention_mask=mask, max_new_tokens=new, past_key_values=cache,
+                                 do_sample=False, pad_token_id=0)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t
+        assert out.shape[1] == prompt_len + new
+        return B * new / dt
+
+    res_b = {}
+    fp = enable_generate_fast_path(model)
+    for B in (4, 16):
+        run(B, True)  # warm-up: builds and captures the engine for this batch
+        fast = statistics.mean(run(B, True) for _ in range(2))
+        res_b[B] = {"fast_path_tok_s": round(fast, 1)}
+        _log("B=%d generate, batched engine: %.1f tok/s" % (B, fast))
+    calls = dict(fp.steps)
+    disable_generate_fast_path(model)
+    torch.cuda.empty_cache()
+    for B in (4, 16):
+        slow = run(B, False)
+        res_b[B]["hf_forward_tok_s"] = round(slow, 1)
+        res_b[B]["speedup"] = round(res_b[B]["fast_path_tok_s"] / slow, 3)
+        _log("B=%d generate, patched HF forward: %.1f tok/s" % (B, slow))
+    return {
+        "metric": "batched generate tok/s (Mistral-7B shape, TEAL thresholds, 3-bit KV, B=16)",
+        "value": res_b[16]["fast_path_tok_s"], "unit": "tok/s", "higher_is_better": True,
+        "ms_per_step": round(16 * 1e3 / res_b[16]["fast_path_tok_s"], 4),
+        "dtype": "f16 (fp32 accumulate)", "scaling": "weak",
+        "data": "synthetic: random-init weights N(0,0.02), random %d-token prompts (seeded)" % prompt_len,
+        "config": {"workload": "batched_generate", "prompt": prompt_len, "new_tokens": new, "kv_bits": 3,
+                   "what": "model.generate(B prompts, max_new_tokens, past_key_values=fresh TurboQuantCache), prefill "
+                           "included (scripts/sweep.py); at B > 1 the reference's patched projections are dense"},
+        "batches": {str(b): v for b, v in res_b.items()},
+        "fast_path_calls": calls,
+    }
+
+
 def bench_dense(args, torch):
     """The dense fp16 baseline alone (OwnDenseEngine at config 5), prefill excluded."""
     from transformers import DynamicCache
@@ -1253,7 +1321,7 @@ def _run_workload(args, torch):
             res["roofline"] = roofline_gateup(args, torch)
     else:
         _fill_gemv_defaults(args)
-        fn = {"dense": bench_dense, "gemv": bench_gemv, "mlp": bench_mlp, "copy": bench_copy, "quant": bench_quant,
+        fn = {"generate": bench_generate, "dense": bench_dense, "gemv": bench_gemv, "mlp": bench_mlp, "copy": bench_copy, "quant": bench_quant,
               "attn": bench_attn, "prefill": bench_prefill, "batched": bench_batched,
               "paged": bench_paged, "tqpaged": bench_tq_paged, "prod": bench_prod}.get(args.workload)
         if fn is None:

@@ -226,8 +226,117 @@ class LeanKVEngine(_Base):
                    "lkv_decode_head")
 
 
+class BatchedEngine:
+    """One decode step of B > 1 sequences of equal length on a fused TurboQuantCache, captured once and
+    replayed as a HIP graph.
+
+    At B > 1 the reference's patched projections run dense F.linear (leankv/teal/patching.py:169-180);
+    HF's decoder layer then calls TurboQuantCache.update and the attention function per layer
+    (modeling_mistral.py:135-174, cache.py:84-127).  This step makes the same calls in the same order on
+    the same modules -- embedding, RMSNorm, the (patched) projections, HF's own RoPE function, the cache's
+    append and decode-attention kernels, o_proj, residual adds, the (patched) MLP, final norm and
+    lm_head -- with the position on the device, so the whole step replays without the host: the logits
+    equal the HF forward's bit for bit.  tok [B] is fed, logits [B, vocab] come out; the cache's host
+    counters are the caller's to advance (GenerateFastPath does)."""
+
+    def __init__(self, model, cache: TurboQuantCache, B: int):
+        import sys
+
+        from . import kernels
+
+        cfg = model.config
+        self.model, self.cache, self.B = model, cache, B
+        self.dev = model.device
+        self.D = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        self.Hq, self.Hkv = cfg.num_attention_heads, cfg.num_key_value_heads
+        self.max_len = cache.attn_max_len(0)
+        layers = model.model.layers
+        self._rope = sys.modules[type(layers[0].self_attn).__module__].apply_rotary_pos_emb
+        with torch.no_grad():
+            pos = torch.arange(self.max_len, device=self.dev).unsqueeze(0)
+            dummy = torch.zeros(1, 1, self.D, device=self.dev, dtype=torch.float16)
+            cos, sin = model.model.rotary_emb(dummy, pos)
+        self.cos, self.sin = cos[0].contiguous(), sin[0].contiguous()  # [max_len, D], the HF forward's values
+        self.tok = torch.zeros(B, dtype=torch.long, device=self.dev)
+        self.pos64 = torch.zeros(1, dtype=torch.long, device=self.dev)
+        self.pos32 = torch.zeros(1, dtype=torch.int32, device=self.dev)  # position of the token fed
+        self.len32 = torch.ones(1, dtype=torch.int32, device=self.dev)   # cache length after its append
+        self.logits = None
+        self.attn = torch.empty(B, self.Hq, self.D, dtype=torch.float16, device=self.dev)
+        self.attn_ws = torch.empty(kernels.decode_attn_workspace_bytes(B, self.Hq, self.Hkv, self.max_len),
+                                   dtype=torch.uint8, device=self.dev)
+        self.graph = None
+        self._host_pos = None
+
+    def _layer(self, i: int, layer, x: torch.Tensor, cos, sin) -> torch.Tensor:
+        from . import kernels
+
+        c, B, D = self.cache, self.B, self.D
+        at = layer.self_attn
+        residual = x
+        h = layer.input_layernorm(x)
+        q = at.q_proj(h).view(B, 1, -1, D).transpose(1, 2)
+        k = at.k_proj(h).view(B, 1, -1, D).transpose(1, 2)
+        v = at.v_proj(h).view(B, 1, -1, D).transpose(1, 2)
+        q, k = self._rope(q, k, cos, sin)
+        k16, v16 = k.to(torch.float16), v.to(torch.float16)
+        kernels.tq_cache_append(k16.reshape(B, self.Hkv, D).contiguous(), v16.reshape(B, self.Hkv, D).contiguous(),
+                                c._k_hot[i], c._v_hot[i], c._k_codes[i], c._k_norms[i], c._v_codes[i], c._v_norms[i],
+                                c.PiK[i], c.PiV[i], c.decision_boundaries, c.bits, self.pos32)
+        qf = q.reshape(B, self.Hq, D).to(torch.float16).contiguous()
+        kernels.tq_decode_attn_out(qf, c._k_codes[i], c._k_norms[i], c._v_codes[i], c._v_norms[i], c._k_hot[i],
+                                   c._v_hot[i], c.PiK[i], c.PiV[i], c.centroids, c.bits, self.len32, self.max_len,
+                                   float(at.scaling), self.attn, self.attn_ws)
+        o = self.attn.view(B, self.Hq, 1, D).transpose(1, 2).contiguous().to(q.dtype).reshape(B, 1, -1)
+        x = residual + at.o_proj(o)
+        residual = x
+        x = residual + layer.mlp(layer.post_attention_layernorm(x))
+        return x
+
+    def _step(self) -> None:
+        m = self.model
+        x = m.model.embed_tokens(self.tok.view(self.B, 1))
+        cos = self.cos.index_select(0, self.pos64).unsqueeze(0)  # [1, 1, D]
+        sin = self.sin.index_select(0, self.pos64).unsqueeze(0)
+        for i, layer in enumerate(m.model.layers):
+            x = self._layer(i, layer, x, cos, sin)
+        logits = m.lm_head(m.model.norm(x))
+        if self.logits is None:
+            self.logits = torch.empty_like(logits)
+        self.logits.copy_(logits)
+        self.pos64.add_(1)
+        self.pos32.add_(1)
+        self.len32.add_(1)
+
+    def set_position(self, pos: int) -> None:
+        """The position of the next token fed (the cache length before it)."""
+        self.pos64.fill_(pos)
+        self.pos32.fill_(pos)
+        self.len32.fill_(pos + 1)
+        self._host_pos = pos
+
+    @torch.no_grad()
+    def step(self) -> None:
+        if self._host_pos is None or self._host_pos >= self.max_len:
+            raise _lib.LeanKVError("BatchedEngine: position %s outside the cache's %d tokens"
+                                   % (self._host_pos, self.max_len))
+        if self.graph is None:
+            self._step()  # eager: allocates what the step needs, then capture
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(g, stream=s):
+                    self._step()
+            torch.cuda.current_stream().wait_stream(s)
+            self.graph = g
+        else:
+            self.graph.replay()
+        self._host_pos += 1
+
+
 class GenerateFastPath:
-    """model.forward for HF ``generate``: single-token decode steps on the fused decode step.
+    """model.forward for HF ``generate``: single-token decode steps on graph-replayed decode engines.
 
     The reference's user path is ``model.generate(..., past_key_values=cache)``
     (leankv/combined.py:13, scripts/benchmark.py:68-99), whose decode steps walk
@@ -238,9 +347,11 @@ class GenerateFastPath:
     window shorter than the sequence, no attentions or hidden states asked for
     -- to the engine, built on that cache's own buffers and replayed as a HIP
     graph; it appends the token to the cache as update() would and returns the
-    last position's logits.  Every other call (the prefill, batches, other
-    caches) runs the model's own forward.  ``steps`` counts the calls served
-    each way."""
+    last position's logits.  A step of B > 1 sequences of one length (no
+    padding) on a fused cache goes to BatchedEngine, the HF forward's own
+    sequence of calls replayed as a graph (equal logits).  Every other call
+    (the prefill, padded batches, other caches) runs the model's own forward.
+    ``steps`` counts the calls served each way."""
 
     def __init__(self, model):
         import inspect
@@ -250,58 +361,80 @@ class GenerateFastPath:
         # generate inspects forward's parameters (logits_to_keep, ...): report the model's own
         self.__signature__ = inspect.signature(self.forward)
         self.engine = None
-        self._cache = None  # the cache the engine was built on (held weakly through id + length checks)
-        self.steps = {"engine": 0, "forward": 0}
+        self._cache = None  # the cache the B = 1 engine was built on
+        self.batched = None  # BatchedEngine for B > 1 calls
+        self.steps = {"engine": 0, "batch": 0, "forward": 0}
 
-    def _eligible(self, input_ids, cache, kw) -> bool:
+    def _eligible(self, input_ids, cache, kw) -> str | None:
+        """"one" (the fused B=1 step), "batch" (BatchedEngine) or None (the model's forward)."""
         if not isinstance(cache, TurboQuantCache) or not cache.fused_attention or not cache.fused_decode:
-            return False
-        if input_ids is None or input_ids.dim() != 2 or tuple(input_ids.shape) != (1, 1):
-            return False
+            return None
+        if input_ids is None or input_ids.dim() != 2 or input_ids.shape[1] != 1:
+            return None
         if kw.get("inputs_embeds") is not None or kw.get("output_attentions") or kw.get("output_hidden_states"):
-            return False
+            return None
         if kw.get("return_dict") is False or kw.get("use_cache") is False or kw.get("labels") is not None:
-            return False
-        if cache.bits not in (3, 4) or cache.hot_buffer_size > 64 or cache.head_dim != 128:
-            return False
-        if cache._k_codes[0] is None or cache._k_codes[0].shape[0] != 1:
-            return False
+            return None
+        B = input_ids.shape[0]
+        if cache.head_dim != 128 or cache._k_codes[0] is None or cache._k_codes[0].shape[0] != B:
+            return None
+        if B == 1 and (cache.bits not in (3, 4) or cache.hot_buffer_size > 64):
+            return None
         n = cache._seq_lengths[0]
         if n == 0 or any(x != n for x in cache._seq_lengths) or any(cache._fused_pending) or \
                 any(cache._prefill_pending):
-            return False
+            return None
+        if n + 1 > cache.attn_max_len(0):  # the append would grow the store: the forward does that
+            return None
         sw = getattr(self.model.config, "sliding_window", None)
         if sw is not None and sw <= n:
-            return False
+            return None
         mask = kw.get("attention_mask")
         if mask is not None and (mask.shape[-1] != n + 1 or not bool(mask.all())):
-            return False
-        return True
+            return None
+        return "one" if B == 1 else "batch"
 
-    def _engine_for(self, cache: TurboQuantCache, length: int) -> "LeanKVEngine":
-        hot = cache.hot_buffer_size
-        if self.engine is not None and self._cache is cache and length <= self.engine.max_len:
+    def _engine_for(self, cache: TurboQuantCache) -> "LeanKVEngine":
+        # the engine holds the cache's buffers: a store that grew (update() reallocates it) needs a new one
+        if self.engine is not None and self._cache is cache and self.engine.max_len == cache.attn_max_len(0):
             return self.engine
-        # the engine holds the cache's buffers: grow them first (doubling, as update() does), then build
-        need = length - hot
-        if cache.cold_capacity(0) < need:
-            for li in range(cache.num_layers):
-                cache._ensure_cap(li, need)
         self.engine = None
         torch.cuda.empty_cache()
-        self.engine = LeanKVEngine(self.model, cache, cache.cold_capacity(0) + hot)
+        self.engine = LeanKVEngine(self.model, cache, cache.attn_max_len(0))
         self._cache = cache
         return self.engine
 
+    def _batched_for(self, cache: TurboQuantCache, B: int) -> BatchedEngine:
+        be = self.batched
+        if be is None or be.cache is not cache or be.B != B or be.max_len != cache.attn_max_len(0):
+            self.batched = None
+            torch.cuda.empty_cache()
+            self.batched = BatchedEngine(self.model, cache, B)
+        return self.batched
+
     def __call__(self, input_ids=None, *args, **kw):
         cache = kw.get("past_key_values")
-        if args or not self._eligible(input_ids, cache, kw):
+        kind = None if args else self._eligible(input_ids, cache, kw)
+        if kind is None:
             self.steps["forward"] += 1
             return self.forward(input_ids, *args, **kw)
         from transformers.modeling_outputs import CausalLMOutputWithPast
 
         n = cache._seq_lengths[0]
-        eng = self._engine_for(cache, n + 1)
+        if kind == "batch":
+            be = self._batched_for(cache, input_ids.shape[0])
+            with torch.no_grad():
+                if be._host_pos != n:
+                    be.set_position(n)
+                be.tok.copy_(input_ids.view(-1))
+                be.step()
+                cache._seen_tokens += 1
+                for li in range(cache.num_layers):
+                    cache._seq_lengths[li] = n + 1
+                logits = be.logits.clone()
+            self.steps["batch"] += 1
+            return CausalLMOutputWithPast(logits=logits, past_key_values=cache)
+        eng = self._engine_for(cache)
         with torch.no_grad():
             if eng._host_pos != n:
                 eng._set_start(input_ids.view(1), n)
@@ -341,6 +474,7 @@ def disable_generate_fast_path(model) -> None:
     if isinstance(fp, GenerateFastPath):
         model.forward = fp.forward
         fp.engine = None
+        fp.batched = None
 
 
 class OwnDenseEngine(_Base):

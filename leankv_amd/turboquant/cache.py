@@ -128,6 +128,11 @@ class TurboQuantCache:
     def cold_capacity(self, layer: int) -> int:
         return 0 if self._k_codes[layer] is None else self._k_codes[layer].shape[2]
 
+    def attn_max_len(self, layer: int) -> int:
+        """Tokens the layer's store holds at its current capacity: the length bound every decode-attention
+        launch over it is sized for."""
+        return self.cold_capacity(layer) + self.hot_buffer_size
+
     # ----------------------------------------------------------- update
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int, cache_kwargs=None):
         global _ACTIVE
@@ -224,7 +229,10 @@ class TurboQuantCache:
         self._fused_pending[layer_idx] = False
         B, Hq, _, D = query.shape
         q = query.reshape(B, Hq, D).to(torch.float16).contiguous()
-        L = self._pending_len[layer_idx]
+        # The launch is sized for the store's capacity, not the current length (the length itself is read on
+        # the device): the split plan, and so the fp32 summation order, is then the same at every step and
+        # the same as the graph-replayed decode engines' over this cache, which cannot change it per step.
+        L = self.attn_max_len(layer_idx)
         scale = float(scaling) if scaling is not None else 1.0 / math.sqrt(D)
         out = torch.ops.leankv.tq_decode_attn(
             q, self._k_codes[layer_idx], self._k_norms[layer_idx], self._v_codes[layer_idx], self._v_norms[layer_idx],

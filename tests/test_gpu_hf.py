@@ -290,7 +290,7 @@ def test_generate_fast_path_matches_hf_forward(cuda, bits, hot):
     assert isinstance(fast.forward, GenerateFastPath) and not isinstance(slow.forward, GenerateFastPath)
     prompt = _ids(100, 51)  # longer than the 64-token window: the steps evict into the cold store
     res = _generate(fast, prompt.to(cuda), ca, 16)
-    assert fast.forward.steps == {"engine": 15, "forward": 1}, fast.forward.steps
+    assert fast.forward.steps == {"engine": 15, "batch": 0, "forward": 1}, fast.forward.steps
     assert ca.get_seq_length(0) == 115
     new = res.sequences[0, 100:]
     errs = []
@@ -317,15 +317,46 @@ def test_generate_fast_path_matches_hf_forward(cuda, bits, hot):
     assert fast.forward.engine.cache is c2
 
 
+@pytest.mark.parametrize("bits,hot", [(3, 64), (2, 128)])
+def test_generate_fast_path_batch(cuda, bits, hot):
+    """B = 4 sequences of one length: generate's decode calls replay BatchedEngine (the HF forward's own calls
+    with the position on the device); its logits equal the patched HF forward's, teacher-forced on the same
+    tokens from the same prefill, bit for bit, and so do the caches.  A left-padded batch falls back."""
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    print("batch case bits=%d hot=%d" % (bits, hot), flush=True)
+    (fast, ca), (slow, cb) = _teal_pair(cuda, 56 + bits, bits=bits, hot=hot)
+    ids = _ids(100, 57, B=4)
+    res = _generate(fast, ids.to(cuda), ca, 12)
+    assert fast.forward.steps == {"engine": 0, "batch": 11, "forward": 1}, fast.forward.steps
+    new = res.sequences[:, 100:]
+    with torch.no_grad():
+        lg = slow(ids.to(cuda), past_key_values=cb, use_cache=True, logits_to_keep=1).logits[:, -1]
+        assert torch.equal(lg.float(), res.scores[0])
+        for i in range(11):
+            lg = slow(new[:, i:i + 1], past_key_values=cb, use_cache=True).logits[:, -1]
+            assert torch.equal(lg.float(), res.scores[i + 1]), i
+    for li in range(2):
+        for a, b in ((ca._k_codes, cb._k_codes), (ca._v_codes, cb._v_codes), (ca._k_norms, cb._k_norms),
+                     (ca._k_hot, cb._k_hot), (ca._v_hot, cb._v_hot)):
+            assert torch.equal(a[li], b[li]), li
+    # left padding: the mask is not all ones, so every call runs the forward (masked SDPA)
+    c2 = TurboQuantCache(bits=bits, head_dim=128, num_layers=2, hot_buffer_size=hot, device=cuda, max_seq_len=256,
+                         fused_attention=True)
+    mask = torch.ones(4, 100, dtype=torch.long)
+    mask[0, :9] = 0
+    before = dict(fast.forward.steps)
+    _generate(fast, ids.to(cuda), c2, 4, attention_mask=mask.to(cuda))
+    assert fast.forward.steps["batch"] == before["batch"]
+
+
 def test_generate_fast_path_falls_back(cuda):
-    """Calls the fused step does not serve run the model's own forward: a batch of two, a 2-bit cache, a
-    128-token window."""
+    """Calls the fused B = 1 step does not serve run the model's own forward: a 2-bit cache, a 128-token
+    window (B = 1)."""
     from leankv_amd.turboquant.cache import TurboQuantCache
 
     (fast, ca), _ = _teal_pair(cuda, 52)
     fp = fast.forward
-    _generate(fast, _ids(70, 53, B=2).to(cuda), ca, 4)
-    assert fp.steps["engine"] == 0 and fp.engine is None
     c2 = TurboQuantCache(bits=2, head_dim=128, num_layers=2, device=cuda, max_seq_len=256, fused_attention=True)
     from leankv_amd.turboquant.attention import use_on
 
@@ -370,7 +401,7 @@ def test_llama_generate_fast_path_and_engine(cuda, scaled_rope):
     assert isinstance(fast.forward, GenerateFastPath)
     prompt = _ids(90, 62)
     res = _generate(fast, prompt.to(cuda), ca, 12)
-    assert fast.forward.steps == {"engine": 11, "forward": 1}
+    assert fast.forward.steps == {"engine": 11, "batch": 0, "forward": 1}
     new = res.sequences[0, 90:]
     with torch.no_grad():
         slow(prompt.view(1, -1).to(cuda), past_key_values=cb, use_cache=True, logits_to_keep=1)
