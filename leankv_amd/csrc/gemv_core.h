@@ -34,6 +34,7 @@ struct GemvLds {
   float xv[kNl][BZ + kPad];
   float x[BZ];                               // the chunk's inputs (filled by the caller)
   int cnt[kNl][NT / kWave];
+  int last[kNl][NT / kWave];
   float wsum[NT / kWave];
   alignas(16) float red[kSlots * kGemvBN];
 };
@@ -90,53 +91,69 @@ __device__ __forceinline__ void gemv_core(GemvLds<NT, BZ, DUAL, U>& sm, const ui
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
 
-  // ---- 1. compaction of surviving activation rows
+  // ---- 1. compaction of surviving activation rows, one round: thread t
+  // tests inputs E t .. E t + E - 1 (E = BZ / NT), so the list comes out in
+  // ascending row order; lane offsets from one ballot per input, wave offsets
+  // from one cross-wave prefix through LDS.  The last surviving row (the
+  // padding value) is found from the per-wave counts without reading the list.
+  constexpr int E = BZ / NT;
   int total[NL];
+  {
+    float v[E];
 #pragma unroll
-  for (int l = 0; l < NL; ++l) total[l] = 0;
-#pragma unroll
-  for (int base = 0; base < BZ; base += NT) {
-    const int z = z0 + base + tid;
-    const bool valid = z < Z;
-    const float v = sm.x[base + tid];
-    const float a = fabsf(v);
-    bool pred[NL];
-    uint64_t mask[NL];
-    pred[0] = valid && (a > t0);
-    if (DUAL) pred[NL - 1] = valid && (a > t1);
+    for (int j = 0; j < E; ++j) v[j] = sm.x[E * tid + j];
+    int pre[NL], cnt[NL], lastz[NL];
 #pragma unroll
     for (int l = 0; l < NL; ++l) {
-      mask[l] = wave_ballot(pred[l]);
-      if (lane == 0) sm.cnt[l][wave] = __popcll(mask[l]);
+      pre[l] = 0;
+      cnt[l] = 0;
+      lastz[l] = -1;
+      int wtot = 0;
+#pragma unroll
+      for (int j = 0; j < E; ++j) {
+        const int z = z0 + E * tid + j;
+        const float t = (l == 0) ? t0 : t1;
+        const bool p = z < Z && fabsf(v[j]) > t;
+        const uint64_t m = wave_ballot(p);
+        pre[l] += lane_prefix(m);
+        wtot += __popcll(m);
+        cnt[l] += p ? 1 : 0;
+        lastz[l] = p ? z : lastz[l];
+      }
+      // the wave's last surviving row sits in its highest lane with a survivor
+      const uint64_t any = wave_ballot(cnt[l] > 0);
+      if (lane == 0) sm.cnt[l][wave] = wtot;
+      if (any != 0 && lane == 63 - __builtin_clzll(any)) sm.last[l][wave] = lastz[l];
     }
     __syncthreads();
 #pragma unroll
     for (int l = 0; l < NL; ++l) {
-      int off = total[l], tot = 0;
+      int off = pre[l], tot = 0, last = 0;
 #pragma unroll
       for (int w = 0; w < NT / kWave; ++w) {
         const int cw = sm.cnt[l][w];
         off += (w < wave) ? cw : 0;
         tot += cw;
+        last = cw > 0 ? sm.last[l][w] : last;
       }
-      if (pred[l]) {
-        const int pos = off + lane_prefix(mask[l]);
-        sm.idx[l][pos] = z;
-        sm.xv[l][pos] = v;
-      }
-      total[l] += tot;
-    }
-    __syncthreads();
-  }
-  // pad each list to a multiple of PAD with (last row, 0)
 #pragma unroll
-  for (int l = 0; l < NL; ++l) {
-    const int padded = (total[l] + PAD - 1) / PAD * PAD;
-    if (total[l] > 0 && tid < padded - total[l]) {
-      sm.idx[l][total[l] + tid] = sm.idx[l][total[l] - 1];
-      sm.xv[l][total[l] + tid] = 0.f;
+      for (int j = 0; j < E; ++j) {
+        const int z = z0 + E * tid + j;
+        const float t = (l == 0) ? t0 : t1;
+        if (z < Z && fabsf(v[j]) > t) {
+          sm.idx[l][off] = z;
+          sm.xv[l][off] = v[j];
+          ++off;
+        }
+      }
+      // pad each list to a multiple of PAD with (last row, 0): padded loads hit the line just fetched
+      const int padded = (tot + PAD - 1) / PAD * PAD;
+      if (tot > 0 && tid < padded - tot) {
+        sm.idx[l][tot + tid] = last;
+        sm.xv[l][tot + tid] = 0.f;
+      }
+      total[l] = padded;
     }
-    total[l] = padded;
   }
   __syncthreads();
 
