@@ -8,7 +8,7 @@
 // (strict, fp32 compare), fp32 accumulate.  A is the column-major weight of
 // prepare_weight_for_sparse_gemv (:229-234): row z is N contiguous fp16.
 //
-//   1. compaction: |x| > t over the chunk's BZ inputs (already in LDS) into
+//   1. compaction: |x| > t over the chunk's BZ inputs (in registers) into
 //      an LDS list of surviving rows, wave ballot + mbcnt prefix + a
 //      cross-wave prefix; padded to whole streaming batches with (last row, 0);
 //   2. streaming: 32 lanes cover one 512-byte row segment with 16-byte buffer
@@ -32,7 +32,6 @@ struct GemvLds {
   static constexpr int kPad = U * kSlots;    // list granularity
   int idx[kNl][BZ + kPad];
   float xv[kNl][BZ + kPad];
-  float x[BZ];                               // the chunk's inputs (filled by the caller)
   int cnt[kNl][NT / kWave];
   int last[kNl][NT / kWave];
   float wsum[NT / kWave];
@@ -75,15 +74,15 @@ __device__ __forceinline__ void gemv_stream_rows(__amdgpu_buffer_rsrc_t A, uint3
   }
 }
 
-// Steps 1-3 for the chunk of inputs z0 .. z0 + BZ (sm.x holds them, 0 past
-// Z) and the output columns n0 .. n0 + kGemvBN of an N-column matrix A0 (and
-// A1 in dual mode, thresholds t0 / t1).  sums[l] is the column sum of matrix
-// l for column n0 + threadIdx.x (threads < kGemvBN).  Ends with a barrier, so
-// the caller may refill sm.x afterwards.
+// Steps 1-3 for the chunk of inputs z0 .. z0 + BZ (thread t holds inputs
+// z0 + E t + j in v[j], E = BZ / NT, 0 past Z) and the output columns n0 ..
+// n0 + kGemvBN of an N-column matrix A0 (and A1 in dual mode, thresholds
+// t0 / t1).  sums[l] is the column sum of matrix l for column n0 + threadIdx.x
+// (threads < kGemvBN).  Ends with a barrier, so the caller may reuse the LDS.
 template <int NT, int BZ, bool DUAL, int U, int CP>
-__device__ __forceinline__ void gemv_core(GemvLds<NT, BZ, DUAL, U>& sm, const uint16_t* A0, const uint16_t* A1,
-                                          uint32_t a_bytes, int N, float t0, float t1, int z0, int Z, int n0,
-                                          float (&sums)[DUAL ? 2 : 1]) {
+__device__ __forceinline__ void gemv_core(GemvLds<NT, BZ, DUAL, U>& sm, const float (&v)[BZ / NT], const uint16_t* A0,
+                                          const uint16_t* A1, uint32_t a_bytes, int N, float t0, float t1, int z0,
+                                          int Z, int n0, float (&sums)[DUAL ? 2 : 1]) {
   using L = GemvLds<NT, BZ, DUAL, U>;
   constexpr int NL = L::kNl, PAD = L::kPad, LPR = L::kLpr, SLOTS = L::kSlots, BN = kGemvBN;
   static_assert(BZ % NT == 0, "BZ must be a multiple of the block size");
@@ -99,9 +98,6 @@ __device__ __forceinline__ void gemv_core(GemvLds<NT, BZ, DUAL, U>& sm, const ui
   constexpr int E = BZ / NT;
   int total[NL];
   {
-    float v[E];
-#pragma unroll
-    for (int j = 0; j < E; ++j) v[j] = sm.x[E * tid + j];
     int pre[NL], cnt[NL], lastz[NL];
 #pragma unroll
     for (int l = 0; l < NL; ++l) {

@@ -42,78 +42,67 @@
 namespace lkv {
 namespace {
 
-// x[z0 .. z0 + BZ) into s_x (0 past Z) for the three input modes.  Every
-// load of a mode is issued before the first is used (addresses clamped into
-// range, values selected afterwards): a conditional load compiles to a branch
-// and a wait per element, one memory round trip each.
+// The chunk's inputs for the three input modes, in registers: thread t gets
+// x[z0 + E t + j], j < E = BZ / NT (0 past Z), the layout the compaction takes.
+// Every load of a mode is issued before the first is used (addresses clamped
+// into range, values selected afterwards): a conditional load compiles to a
+// branch and a wait per element, one memory round trip each.
 template <int NT, int BZ, int MODE>
-__device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float* s_x, float* s_wsum) {
+__device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float (&v)[BZ / NT], float* s_wsum) {
   constexpr int E = BZ / NT;  // inputs per thread
-  const int tid = threadIdx.x;
+  const int zt = z0 + E * static_cast<int>(threadIdx.x);
   const int Z = G.Z;
   if (MODE == kInRmsNorm) {
     uint16_t xv[E], wv[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int z = min(z0 + e * NT + tid, Z - 1);
-      xv[e] = G.x[z];
-      wv[e] = G.norm_w[z];
+    for (int j = 0; j < E; ++j) {
+      const int z = min(zt + j, Z - 1);
+      xv[j] = G.x[z];
+      wv[j] = G.norm_w[z];
     }
     const float rstd = rms_rstd(G.x, Z, G.eps, s_wsum);
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int i = e * NT + tid;
-      s_x[i] = z0 + i < Z ? rms_apply(xv[e], wv[e], rstd) : 0.f;
-    }
+    for (int j = 0; j < E; ++j) v[j] = zt + j < Z ? rms_apply(xv[j], wv[j], rstd) : 0.f;
   } else if (MODE == kInSwiglu) {
-    // h = SwiGLU(sum of gate chunks, sum of up chunks); chunk loads for all E
-    // inputs of the thread are issued together, 8 chunks deep.
+    // h = SwiGLU(sum of gate chunks, sum of up chunks), chunks summed in order.  The thread's E inputs
+    // are consecutive in one 256-column slab of the partials (Z a multiple of 256 here), so each chunk
+    // is one E-float load per matrix, all of them issued 8 chunks deep.
+    static_assert(E == 1 || E == 2 || E == 4, "SwiGLU inputs load as 1, 2 or 4 floats");
+    typedef float fvec __attribute__((ext_vector_type(E)));
     const size_t mat = static_cast<size_t>(G.in_nslab) * G.in_nchunk * kGemvBN;
     const int nc = G.in_nchunk;
+    const int zb = min(zt, Z - E);
+    const float* pg = G.in_part + static_cast<size_t>(zb / kGemvBN) * nc * kGemvBN + (zb % kGemvBN);
     float g[E], u[E];
-    const float* pg[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int z = min(z0 + e * NT + tid, Z - 1);
-      pg[e] = G.in_part + static_cast<size_t>(z / kGemvBN) * nc * kGemvBN + (z % kGemvBN);
-      g[e] = 0.f;
-      u[e] = 0.f;
-    }
+    for (int j = 0; j < E; ++j) g[j] = u[j] = 0.f;
     for (int k0 = 0; k0 < nc; k0 += 8) {
-      float vg[E][8], vu[E][8];
+      fvec vg[8], vu[8];
 #pragma unroll
-      for (int e = 0; e < E; ++e)
+      for (int i = 0; i < 8; ++i) {
+        const size_t k = static_cast<size_t>(min(k0 + i, nc - 1)) * kGemvBN;
+        vg[i] = *reinterpret_cast<const fvec*>(pg + k);
+        vu[i] = *reinterpret_cast<const fvec*>(pg + mat + k);
+      }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const size_t k = static_cast<size_t>(min(k0 + i, nc - 1)) * kGemvBN;
-          vg[e][i] = pg[e][k];
-          vu[e][i] = pg[e][mat + k];
+      for (int i = 0; i < 8; ++i) {
+        const bool ok = k0 + i < nc;
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+          g[j] += ok ? vg[i][j] : 0.f;
+          u[j] += ok ? vu[i][j] : 0.f;
         }
-#pragma unroll
-      for (int e = 0; e < E; ++e)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const bool ok = k0 + i < nc;
-          g[e] += ok ? vg[e][i] : 0.f;
-          u[e] += ok ? vu[e][i] : 0.f;
-        }
+      }
     }
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int i = e * NT + tid;
-      s_x[i] = z0 + i < Z ? h2f(swiglu_f16(g[e], u[e])) : 0.f;
-    }
+    for (int j = 0; j < E; ++j) v[j] = zt + j < Z ? h2f(swiglu_f16(g[j], u[j])) : 0.f;
   } else {
     uint16_t xv[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) xv[e] = G.x[min(z0 + e * NT + tid, Z - 1)];
+    for (int j = 0; j < E; ++j) xv[j] = G.x[min(zt + j, Z - 1)];
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int i = e * NT + tid;
-      s_x[i] = z0 + i < Z ? h2f(xv[e]) : 0.f;
-    }
+    for (int j = 0; j < E; ++j) v[j] = zt + j < Z ? h2f(xv[j]) : 0.f;
   }
-  __syncthreads();
 }
 
 // v[seg] from a per-segment kernel-argument array without a dynamically
@@ -156,10 +145,11 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
     const int N = seg_pick(G.N, seg);
     const int n0 = slab * BN;
 
-    input_prologue<NT, BZ, MODE>(G, z0, sm.x, sm.wsum);
+    float xin[BZ / NT];
+    input_prologue<NT, BZ, MODE>(G, z0, xin, sm.wsum);
     float sums[NL];
-    gemv_core<NT, BZ, DUAL, U, CP>(sm, seg_pick(G.A, seg), G.A_up, seg_pick(G.a_bytes, seg), N, seg_pick(G.t, seg),
-                                   G.t_up, z0, G.Z, n0, sums);
+    gemv_core<NT, BZ, DUAL, U, CP>(sm, xin, seg_pick(G.A, seg), G.A_up, seg_pick(G.a_bytes, seg), N,
+                                   seg_pick(G.t, seg), G.t_up, z0, G.Z, n0, sums);
 
     // ---- 4. output (threads 0..255, one column each): fp16 directly (single chunk) or partial sums
     if (tid < BN) {
