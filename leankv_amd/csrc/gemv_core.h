@@ -35,7 +35,7 @@ struct GemvLds {
   int cnt[kNl][NT / kWave];
   int last[kNl][NT / kWave];
   float wsum[NT / kWave];
-  alignas(16) float red[kSlots * kGemvBN];
+  alignas(16) float red[kNl * kSlots * kGemvBN];
 };
 
 __device__ __forceinline__ void gemv_fma8(float (&acc)[8], const gemv_u32x4& w, float xv) {
@@ -78,7 +78,8 @@ __device__ __forceinline__ void gemv_stream_rows(__amdgpu_buffer_rsrc_t A, uint3
 // z0 + E t + j in v[j], E = BZ / NT, 0 past Z) and the output columns n0 ..
 // n0 + kGemvBN of an N-column matrix A0 (and A1 in dual mode, thresholds
 // t0 / t1).  sums[l] is the column sum of matrix l for column n0 + threadIdx.x
-// (threads < kGemvBN).  Ends with a barrier, so the caller may reuse the LDS.
+// (threads < kGemvBN).  The LDS is still being read when it returns: a caller
+// that reuses it needs a barrier first.
 template <int NT, int BZ, bool DUAL, int U, int CP>
 __device__ __forceinline__ void gemv_core(GemvLds<NT, BZ, DUAL, U>& sm, const float (&v)[BZ / NT], const uint16_t* A0,
                                           const uint16_t* A1, uint32_t a_bytes, int N, float t0, float t1, int z0,
@@ -171,20 +172,22 @@ __device__ __forceinline__ void gemv_core(GemvLds<NT, BZ, DUAL, U>& sm, const fl
     gemv_stream_rows<SLOTS, U, CP>(gemv_rsrc(A1, a_bytes), row_bytes, col_bytes, sm.idx[NL - 1], sm.xv[NL - 1],
                                    total[NL - 1], slot, acc[NL - 1]);
 
-  // ---- 3. cross-slot reduction through LDS
+  // ---- 3. cross-slot reduction through LDS, every matrix at once
 #pragma unroll
   for (int l = 0; l < NL; ++l) {
-    float4* dst = reinterpret_cast<float4*>(sm.red + slot * BN + c * 8);
+    float4* dst = reinterpret_cast<float4*>(sm.red + (l * SLOTS + slot) * BN + c * 8);
     dst[0] = make_float4(acc[l][0], acc[l][1], acc[l][2], acc[l][3]);
     dst[1] = make_float4(acc[l][4], acc[l][5], acc[l][6], acc[l][7]);
-    __syncthreads();
+  }
+  __syncthreads();
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
     float s = 0.f;
     if (tid < BN) {
 #pragma unroll
-      for (int sl = 0; sl < SLOTS; ++sl) s += sm.red[sl * BN + tid];
+      for (int sl = 0; sl < SLOTS; ++sl) s += sm.red[(l * SLOTS + sl) * BN + tid];
     }
     sums[l] = s;
-    __syncthreads();
   }
 }
 

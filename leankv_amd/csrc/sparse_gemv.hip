@@ -164,7 +164,7 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
         }
       }
     }
-    __syncthreads();  // LDS is reused by the next item
+    if (item + static_cast<int>(gridDim.x * gridDim.y) < nitems) __syncthreads();  // uniform: LDS reused next
   }
 }
 
