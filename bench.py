@@ -204,6 +204,10 @@ def bench_gemv(args, torch):
     return res
 
 
+TRAFFIC_SOURCE = ("profiles/traffic.json: committed rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE means of this kernel at "
+                  "this shape (separate counter runs, scaled by a device copy's factors), not measured in this run")
+
+
 def _traffic(kernel_key):
     """HBM bytes per launch of a kernel from the committed rocprofv3 PMC summary (None if absent)."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
@@ -232,7 +236,7 @@ def _roofline_partials(torch, sets, N, Z, alg_bytes, steps, warmup, name, key=No
     _, single, _ = _timed_loop(launch, len(sets), steps // 2, 0, torch)
     achieved = alg_bytes / (kmean * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(key or "gemv_config1"),
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(key or "gemv_config1"), "traffic_source": TRAFFIC_SOURCE,
             "kernel": name, "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3),
             "kernel_us_single_launch_events": round(single * 1e3, 3), "alg_bytes_per_launch": int(alg_bytes)}
 
@@ -613,7 +617,7 @@ def bench_attn(args, torch):
                    "bits": bits,
                    "alg_bytes_per_call": alg, "sets": len(sets)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic("attn_config4"),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic("attn_config4"), "traffic_source": TRAFFIC_SOURCE,
                      "kernel": "tq_attn_split_kernel (q rotation in its prologue) + tq_attn_combine_kernel (one call)",
                      "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3),
                      "alg_bytes_per_launch": alg},

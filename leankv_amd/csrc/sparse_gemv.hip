@@ -22,7 +22,7 @@
 //   2. Streaming: 32 lanes cover one 512-byte row segment with 16-byte buffer
 //      loads (SGPR descriptor + 32-bit offset; loads past the end read 0,
 //      non-temporal cache policy); the 8 row slots of the block walk the list
-//      8 rows at a time, so 8 independent 16-byte loads per lane are in
+//      4 rows at a time, so 4 independent 16-byte loads per lane are in
 //      flight.  fp16 x fp32 -> fp32.
 //   3. The row slots are reduced through LDS into 256 fp32 column sums.
 //   4. The block writes its partial sums.  The reduction over chunks happens
@@ -277,11 +277,16 @@ int gemv_threads() {
   return t;
 }
 
-// Rows each lane keeps in flight (8 default; LKV_GEMV_UNROLL=16 for tuning sweeps).
+// Rows each lane keeps in flight: 4 (LKV_GEMV_UNROLL=8 or 16 for tuning
+// sweeps).  Measured on one box, fused gate/up at the Mistral-7B shape: U = 2 /
+// 3 / 4 / 6 / 8 -> 30.4 / 24.7 / 23.5 / 23.8 / 24.0 us, config-5 decode 355 /
+// 407 / 419 / 416 / 415 tok/s; fewer requests in flight per lane stream faster
+// once ~1.75 blocks per CU keep 4 waves each busy.
 int gemv_unroll() {
   static const int u = [] {
     const char* env = getenv("LKV_GEMV_UNROLL");
-    return env && atoi(env) == 16 ? 16 : 8;
+    const int v = env ? atoi(env) : 4;
+    return v == 8 || v == 16 ? v : 4;
   }();
   return u;
 }
@@ -313,7 +318,11 @@ int gemv_launch(const GemvArgs& G, int bz, bool dual, int mode, int nslab_total,
     Gx.part_off[s] = G.part_off[0];
     Gx.slab0_seg[s] = nslab_total;
   }
-  if (gemv_unroll() == 16) {
+  if (gemv_unroll() == 4) {
+    if (bz == 256) ok = launch_cp<256, 256, 4>(Gx, dual, mode, grid, st, cp);
+    else if (bz == 512) ok = t512 ? launch_cp<512, 512, 4>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 512, 4>(Gx, dual, mode, grid, st, cp);
+    else if (bz == 1024) ok = t512 ? launch_cp<512, 1024, 4>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 1024, 4>(Gx, dual, mode, grid, st, cp);
+  } else if (gemv_unroll() == 16) {
     if (bz == 256) ok = launch_cp<256, 256, 16>(Gx, dual, mode, grid, st, cp);
     else if (bz == 512) ok = t512 ? launch_cp<512, 512, 16>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 512, 16>(Gx, dual, mode, grid, st, cp);
     else if (bz == 1024) ok = t512 ? launch_cp<512, 1024, 16>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 1024, 16>(Gx, dual, mode, grid, st, cp);
