@@ -48,7 +48,7 @@ struct GemvArgs {
   int chunk_major;         // set by gemv_launch (block order)
 };
 
-int gemv_pick_bz(int64_t slabs, int64_t Z);
+int gemv_pick_bz(int64_t slabs, int64_t Z, int quarter_blocks = 3);
 int gemv_launch(const GemvArgs& G, int bz, bool dual, int mode, int nslab_total, hipStream_t st);
 
 inline int64_t gemv_slabs(int64_t N) { return (N + kGemvBN - 1) / kGemvBN; }

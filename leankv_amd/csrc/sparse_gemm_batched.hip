@@ -189,10 +189,11 @@ bool launch_nb(const BatchedArgs& P, int bz, dim3 grid, hipStream_t st) {
 // Batch rows per block: the next power of two up to 8.
 int group_rows(int64_t B) { return B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8; }
 
-// Chunk size: as for one GEMV, with the batch groups counted as extra blocks.
+// Chunk size: the largest giving ~1.5 blocks (of 256 threads) per CU, with the
+// batch groups counted as extra blocks.
 int batched_bz(int64_t B, int64_t N, int64_t Z) {
   const int64_t groups = (B + group_rows(B) - 1) / group_rows(B);
-  return gemv_pick_bz(gemv_slabs(N) * groups, Z);
+  return gemv_pick_bz(gemv_slabs(N) * groups, Z, 6);
 }
 
 }  // namespace

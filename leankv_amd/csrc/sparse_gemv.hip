@@ -8,7 +8,7 @@
 // fp16 values, so a surviving activation selects one contiguous weight row.
 //
 // Work decomposition: grid = (column slabs of 256) x (row chunks of BZ),
-// 256 threads per block.
+// 512 threads per block for chunks of 512 rows and more, else 256.
 //   0. Input prologue: x as given, or computed from what produced it --
 //      RMSNorm of the fp16 residual stream (each block reads the whole 8 KB
 //      vector for the sum of squares), or SwiGLU of the gate/up partial sums
@@ -204,14 +204,19 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_reduce_multi_kernel(MultiRe
 }  // namespace
 
 // Row-chunk size for a GEMV with Z inputs over `slabs` column slabs: the
-// largest chunk that still gives ~1.5 blocks per CU (fewer partials and
-// per-block costs), overridable with LKV_GEMV_BZ for tuning sweeps.
-int gemv_pick_bz(int64_t slabs, int64_t Z) {
+// largest chunk that still gives at least quarter_blocks / 4 blocks per CU
+// (fewer partials and per-block costs), overridable with LKV_GEMV_BZ for
+// tuning sweeps.  The split-K GEMV launches chunks of 512 rows and more as
+// 512-thread blocks, so its default of 3 (0.75 blocks per CU) keeps ~6-7 waves
+// per CU, as 1.5 blocks of 256 threads did; measured on one box: config 1
+// 13.64 -> 13.23 us (1024-row chunks, 224 blocks), config-5 decode 419 -> 420
+// tok/s (q|k|v in 512-row chunks, gate|up and down in 1024-row chunks).
+int gemv_pick_bz(int64_t slabs, int64_t Z, int quarter_blocks) {
   if (const char* env = getenv("LKV_GEMV_BZ")) {
     const int bz = atoi(env);
     if (bz == 256 || bz == 512 || bz == 1024) return bz;
   }
-  const int64_t target = 3 * static_cast<int64_t>(device_cu_count()) / 2;
+  const int64_t target = quarter_blocks * static_cast<int64_t>(device_cu_count()) / 4;
   static const int bzs[] = {1024, 512};
   for (int bz : bzs)
     if (slabs * gemv_chunks(Z, bz) >= target) return bz;
@@ -268,11 +273,12 @@ bool gemv_chunk_major() {
   return c;
 }
 
-// Threads per GEMV block (256 default; LKV_GEMV_THREADS=512 for tuning sweeps, chunks >= 512 only).
+// Threads per GEMV block for chunks of 512 rows and more: 512 (LKV_GEMV_THREADS=256
+// for tuning sweeps; 256-row chunks always run 256 threads).
 int gemv_threads() {
   static const int t = [] {
     const char* env = getenv("LKV_GEMV_THREADS");
-    return env && atoi(env) == 512 ? 512 : 256;
+    return env && atoi(env) == 256 ? 256 : 512;
   }();
   return t;
 }

@@ -201,7 +201,9 @@ def test_decode_workspace_layout():
     assert lay.part_k - lay.part_q == slabs(4096) * lay.chunks_qkv * 256 * 4
     assert lay.part_v - lay.part_k == slabs(1024) * lay.chunks_qkv * 256 * 4
     assert lay.part_up - lay.part_gate == slabs(14336) * lay.chunks_gateup * 256 * 4
-    assert lay.chunks_qkv * 256 >= 4096 and lay.chunks_down > 1
+    # every chunk count covers its input dimension in chunks of 256, 512 or 1024 rows
+    assert 4096 % lay.chunks_qkv == 0 and 4096 // lay.chunks_qkv in (256, 512, 1024)
+    assert any(-(-14336 // bz) == lay.chunks_down for bz in (256, 512, 1024)) and lay.chunks_down > 1
     offs = [lay.part_q, lay.part_k, lay.part_v, lay.part_o, lay.part_gate, lay.part_up, lay.part_down, lay.part_lm,
             lay.q_rope, lay.attn_out]
     assert offs == sorted(offs) and offs[-1] + 4096 * 2 <= lay.total
