@@ -283,18 +283,20 @@ int gemv_threads() {
   return t;
 }
 
-// Rows each lane keeps in flight: 4 (LKV_GEMV_UNROLL=8 or 16 for tuning
-// sweeps).  Measured on one box, fused gate/up at the Mistral-7B shape: U = 2 /
-// 3 / 4 / 6 / 8 -> 30.4 / 24.7 / 23.5 / 23.8 / 24.0 us, config-5 decode 355 /
-// 407 / 419 / 416 / 415 tok/s; fewer requests in flight per lane stream faster
-// once ~1.75 blocks per CU keep 4 waves each busy.
-int gemv_unroll() {
+// Rows each lane keeps in flight, chosen so a block keeps ~32 KB of weight
+// rows in flight: 4 in 512-thread blocks, 8 in 256-thread blocks (256-row
+// chunks); LKV_GEMV_UNROLL=4, 8 or 16 overrides for tuning sweeps.  Measured on
+// one box, fused gate/up at the Mistral-7B shape: U = 2 / 3 / 4 / 6 / 8 ->
+// 30.4 / 24.7 / 23.5 / 23.8 / 24.0 us, config-5 decode 355 / 407 / 419 / 416 /
+// 415 tok/s; the 256-row o_proj chunks with 8 rather than 4: decode 419.4 ->
+// 420.2 tok/s, dense fp16 step 298.3 -> 301.5 tok/s.
+int gemv_unroll(int threads) {
   static const int u = [] {
     const char* env = getenv("LKV_GEMV_UNROLL");
-    const int v = env ? atoi(env) : 4;
-    return v == 8 || v == 16 ? v : 4;
+    const int v = env ? atoi(env) : 0;
+    return v == 4 || v == 8 || v == 16 ? v : 0;
   }();
-  return u;
+  return u ? u : (threads == 512 ? 4 : 8);
 }
 
 }  // namespace
@@ -324,11 +326,12 @@ int gemv_launch(const GemvArgs& G, int bz, bool dual, int mode, int nslab_total,
     Gx.part_off[s] = G.part_off[0];
     Gx.slab0_seg[s] = nslab_total;
   }
-  if (gemv_unroll() == 4) {
+  const int unroll = gemv_unroll(t512 ? 512 : 256);
+  if (unroll == 4) {
     if (bz == 256) ok = launch_cp<256, 256, 4>(Gx, dual, mode, grid, st, cp);
     else if (bz == 512) ok = t512 ? launch_cp<512, 512, 4>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 512, 4>(Gx, dual, mode, grid, st, cp);
     else if (bz == 1024) ok = t512 ? launch_cp<512, 1024, 4>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 1024, 4>(Gx, dual, mode, grid, st, cp);
-  } else if (gemv_unroll() == 16) {
+  } else if (unroll == 16) {
     if (bz == 256) ok = launch_cp<256, 256, 16>(Gx, dual, mode, grid, st, cp);
     else if (bz == 512) ok = t512 ? launch_cp<512, 512, 16>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 512, 16>(Gx, dual, mode, grid, st, cp);
     else if (bz == 1024) ok = t512 ? launch_cp<512, 1024, 16>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 1024, 16>(Gx, dual, mode, grid, st, cp);

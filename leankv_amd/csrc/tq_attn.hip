@@ -341,7 +341,9 @@ constexpr int kSplitBlocksPerCU = LKV_ATTN_BLOCKS_PER_CU;
 
 constexpr int kMaxPg = 256;  // pages of one split in the paged layout
 
-template <bool PERM, bool DECODE, bool PAGED, int CB>
+// QPRE (decode mode): q|k|v partial chunks loaded ahead of the codes, at least
+// the q|k|v GEMV's chunk count for the fast path (8 or 16).
+template <bool PERM, bool DECODE, bool PAGED, int CB, int QPRE = 16>
 __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_kernel(AttnParams P) {
   static_assert(!(PAGED && DECODE), "the fused decode step uses the dense layout");
   static_assert(CB == 4 || (PERM && !DECODE), "narrow code rows: v_perm decode, standalone calls");
@@ -455,7 +457,7 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
       // this thread's first query element: its first kPre chunk partials (both
       // dims of the RoPE pair) from clamped, always valid addresses, ahead of
       // the codes; the rest of the chunks and elements are loaded after them
-      constexpr int kPre = 16;
+      constexpr int kPre = QPRE;
       float pre0[kPre], pre1[kPre];
       uint16_t rc0, rc1, rs0, rs1;  // its RoPE factors
       {
@@ -1015,10 +1017,15 @@ int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st) {
     P.q = c.q16;  // the combine's hot-window query
     P.k_hot = c.k_ring;
     P.v_hot = c.v_ring;
-    if (c.bits == 3)
-      hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false, 4>), grid, dim3(kThreads), 0, st, P);
+    // the fewest partial loads ahead of the codes that still cover every chunk
+    if (c.bits == 3 && c.nchunk <= 8)
+      hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false, 4, 8>), grid, dim3(kThreads), 0, st, P);
+    else if (c.bits == 3)
+      hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false, 4, 16>), grid, dim3(kThreads), 0, st, P);
+    else if (c.nchunk <= 8)
+      hipLaunchKernelGGL((tq_attn_split_kernel<false, true, false, 4, 8>), grid, dim3(kThreads), 0, st, P);
     else
-      hipLaunchKernelGGL((tq_attn_split_kernel<false, true, false, 4>), grid, dim3(kThreads), 0, st, P);
+      hipLaunchKernelGGL((tq_attn_split_kernel<false, true, false, 4, 16>), grid, dim3(kThreads), 0, st, P);
   } else if (c.indptr != nullptr) {
     switch (c.bits) {
       case 1: hipLaunchKernelGGL((tq_attn_split_kernel<true, false, true, 1>), grid, dim3(kThreads), 0, st, P); break;
