@@ -6,15 +6,17 @@
 // wrapper :184-226 (x [B, Z], weight [N, Z] column-major, output fp16
 // [B, N]).  The reference accumulates with atomic_add into an output it does
 // not zero; here every output is the deterministic chunk-ordered sum, equal to
-// B independent lkv_sparse_gemv calls up to fp32 summation order.
+// B independent lkv_sparse_gemv calls up to fp32 summation order (rows are
+// accumulated in pairs by v_dot2_f32_f16).
 //
 // A weight row is needed by a block as soon as one of its batch items keeps
 // that activation, and then serves all of them: grid = (column slabs of 256) x
 // (row chunks of BZ) x (groups of up to 8 batch rows).  The block compacts the
 // union of its rows' masks into an LDS list (per row, the NB activations with
 // the ones at or below the threshold zeroed), streams each listed 512-byte
-// row segment once with 16-byte buffer loads (8 rows per lane in flight,
-// non-temporal) and accumulates NB x 8 fp32 column sums per lane; row slots
+// row segment once with 16-byte buffer loads (4 rows per lane in flight,
+// non-temporal) and accumulates NB x 8 fp32 column sums per lane, two rows per
+// v_dot2_f32_f16; row slots
 // are reduced through LDS and the block writes fp32 partials per batch row,
 // summed over chunks in chunk order by batched_reduce_kernel (or written as
 // fp16 directly when there is one chunk).  At 40 % sparsity and B = 4 the
@@ -29,10 +31,11 @@ constexpr int kNT = 256;
 constexpr int kBN = kGemvBN;    // columns per slab
 constexpr int kLPR = kBN / 8;   // lanes per row segment
 constexpr int kSlots = kNT / kLPR;
-constexpr int kU = 8;           // rows per lane in flight
+constexpr int kU = 4;           // rows per lane in flight (8: 29.8 vs 29.5 us at B = 8, config-1 shape)
 constexpr int kPad = kU * kSlots;
 
 typedef uint32_t u32x4b __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 struct BatchedArgs {
   const uint16_t* x;  // [B][Z] fp16
@@ -125,6 +128,12 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
   for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[b][j] = 0.f;
+  // Rows are taken in pairs (u, u + 1): v_perm_b32 gathers a column's two
+  // weights into one fp16 pair, the two activations are packed the same way
+  // (exactly: they are fp16 values), and v_dot2_f32_f16 adds both products
+  // into the fp32 sum, so the VALU work per row is about half that of a
+  // conversion plus an FMA per weight and batch row.
+  static_assert(kU % 2 == 0, "rows are streamed in pairs");
   for (int s = slot; s < padded; s += kU * kSlots) {
     u32x4b w[kU];
 #pragma unroll
@@ -132,18 +141,19 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
       w[u] = __builtin_amdgcn_raw_buffer_load_b128(
           rs, static_cast<uint32_t>(s_idx[s + u * kSlots]) * row_bytes + col_bytes, 0, 2);
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      float wf[8];
+    for (int u = 0; u < kU; u += 2) {
+      half2_t wp[8];  // wp[j] = (A[row u][col + j], A[row u + 1][col + j])
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        wf[2 * i] = h2f(static_cast<uint16_t>(w[u][i] & 0xffffu));
-        wf[2 * i + 1] = h2f(static_cast<uint16_t>(w[u][i] >> 16));
+        wp[2 * i] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(w[u + 1][i], w[u][i], 0x05040100u));
+        wp[2 * i + 1] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(w[u + 1][i], w[u][i], 0x07060302u));
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        const float xv = s_xv[b][s + u * kSlots];
+        const half2_t xp = __builtin_bit_cast(
+            half2_t, __builtin_amdgcn_cvt_pkrtz(s_xv[b][s + u * kSlots], s_xv[b][s + (u + 1) * kSlots]));
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[b][j] = fmaf(wf[j], xv, acc[b][j]);
+        for (int j = 0; j < 8; ++j) acc[b][j] = __builtin_amdgcn_fdot2(wp[j], xp, acc[b][j], false);
       }
     }
   }
