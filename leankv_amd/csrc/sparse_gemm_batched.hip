@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
   static_assert(BZ % kNT == 0, "BZ must be a multiple of the block size");
   __shared__ float s_x[NB][BZ];
   __shared__ int s_idx[BZ + kPad];
-  __shared__ float s_xv[NB][BZ + kPad];
+  __shared__ __align__(4) uint16_t s_xh[NB][BZ + kPad];  // fp16 activations of the listed rows (0 if dropped)
   __shared__ int s_cnt[kNT / kWave];
   __shared__ __align__(16) float s_red[kSlots * kBN];
 
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
       const int pos = off + lane_prefix(mask);
       s_idx[pos] = z;
 #pragma unroll
-      for (int b = 0; b < NB; ++b) s_xv[b][pos] = v[b];
+      for (int b = 0; b < NB; ++b) s_xh[b][pos] = f2h(v[b]);  // exact: fp16 inputs
     }
     total += tot;
     __syncthreads();
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
   if (total > 0 && tid < padded - total) {
     s_idx[total + tid] = s_idx[total - 1];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) s_xv[b][total + tid] = 0.f;
+    for (int b = 0; b < NB; ++b) s_xh[b][total + tid] = 0;
   }
   __syncthreads();
 
@@ -128,30 +128,29 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
   for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[b][j] = 0.f;
-  // Rows are taken in pairs (u, u + 1): v_perm_b32 gathers a column's two
-  // weights into one fp16 pair, the two activations are packed the same way
-  // (exactly: they are fp16 values), and v_dot2_f32_f16 adds both products
-  // into the fp32 sum, so the VALU work per row is about half that of a
-  // conversion plus an FMA per weight and batch row.
+  // The list is walked in pairs of neighbouring entries: pair q = slot + v *
+  // kSlots (v < kU / 2) holds rows s_idx[2q], s_idx[2q + 1].  v_perm_b32 gathers
+  // a column's two weights into one fp16 pair, the two activations are one
+  // 32-bit LDS read, and v_dot2_f32_f16 adds both products into the fp32 sum:
+  // about half the VALU work of a conversion plus an FMA per weight and row.
   static_assert(kU % 2 == 0, "rows are streamed in pairs");
-  for (int s = slot; s < padded; s += kU * kSlots) {
+  for (int q = slot; 2 * q < padded; q += (kU / 2) * kSlots) {
     u32x4b w[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u)
       w[u] = __builtin_amdgcn_raw_buffer_load_b128(
-          rs, static_cast<uint32_t>(s_idx[s + u * kSlots]) * row_bytes + col_bytes, 0, 2);
+          rs, static_cast<uint32_t>(s_idx[2 * (q + (u >> 1) * kSlots) + (u & 1)]) * row_bytes + col_bytes, 0, 2);
 #pragma unroll
-    for (int u = 0; u < kU; u += 2) {
-      half2_t wp[8];  // wp[j] = (A[row u][col + j], A[row u + 1][col + j])
+    for (int v = 0; v < kU / 2; ++v) {
+      half2_t wp[8];  // wp[j] = (A[row 2p][col + j], A[row 2p + 1][col + j]), p = q + v kSlots
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        wp[2 * i] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(w[u + 1][i], w[u][i], 0x05040100u));
-        wp[2 * i + 1] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(w[u + 1][i], w[u][i], 0x07060302u));
+        wp[2 * i] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(w[2 * v + 1][i], w[2 * v][i], 0x05040100u));
+        wp[2 * i + 1] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(w[2 * v + 1][i], w[2 * v][i], 0x07060302u));
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        const half2_t xp = __builtin_bit_cast(
-            half2_t, __builtin_amdgcn_cvt_pkrtz(s_xv[b][s + u * kSlots], s_xv[b][s + (u + 1) * kSlots]));
+        const half2_t xp = *reinterpret_cast<const half2_t*>(&s_xh[b][2 * (q + v * kSlots)]);
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[b][j] = __builtin_amdgcn_fdot2(wp[j], xp, acc[b][j], false);
       }
