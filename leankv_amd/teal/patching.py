@@ -9,8 +9,9 @@ Drop-in for leankv/teal/patching.py:
 Threshold selection, the "exactly one source" rule and the hook-based
 correctness mode are the reference's.  ``use_triton=True`` (name kept for
 drop-in callers; ``use_hip`` is an alias) routes every projection with t > 0
-to the HIP sparse GEMV at B=1 single-token decode and keeps the dense F.linear
-otherwise, the reference's dispatch rule (:169-180).  In addition, when both
+to the HIP sparse GEMV at B=1 single-token decode and keeps the dense product
+otherwise, the reference's dispatch rule (:169-180): a few decode rows on the
+batched kernel with threshold 0, larger inputs on torch's F.linear.  In addition, when both
 gate_proj and up_proj of a layer are patched, the MLP forward is patched so the
 two projections and the SwiGLU run as one fused HIP kernel reading x once
 (``fuse_mlp=False`` turns this off), and when q_proj, k_proj and v_proj are
@@ -27,7 +28,8 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from .kernels.sparse_gemv import prepare_weight_for_sparse_gemv, sparse_gateup_swiglu, sparse_gemv, sparse_qkv
+from .kernels.sparse_gemv import (batched_sparse_gemm, prepare_weight_for_sparse_gemv, sparse_gateup_swiglu, sparse_gemv,
+                                  sparse_qkv)
 from .sparse_fns import SparsifyFn, compute_threshold_for_sparsity
 
 PROJ_NAMES = ["q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"]
@@ -112,11 +114,23 @@ def apply_teal(
     return sparsifiers
 
 
+def _skinny_dense(rows: int, N: int, Z: int) -> bool:
+    """Whether a dense product of `rows` decode rows runs on the batched kernel (threshold 0) rather than torch's
+    GEMM.  Measured on one MI355X, eager calls at the Mistral-7B shapes over the column-major weight, torch vs the
+    batched kernel in us: down [4096 x 14336] 70 / 23-28 for 2-8 rows, 72 / 45 for 16; gate/up [14336 x 4096]
+    28 / 22-27 for 2-8 rows, 28 / 45 for 16; q/o and k/v within launch overhead of each other."""
+    return 1 < rows <= 16 and (rows <= 8 or Z > N)
+
+
 def _patch_linear_with_kernel(linear: nn.Linear, threshold: float) -> None:
-    """Relayout the weight column-major (permanent) and route B=1 decode to HIP."""
+    """Relayout the weight column-major (permanent) and route B=1 decode to HIP.
+
+    Other inputs take the dense product, as the reference dispatches them (patching.py:169-180): a few
+    decode rows (B > 1, or a short chunk) on the batched kernel with threshold 0, so every nonzero input
+    contributes (fp32 accumulate, fp16 out, as F.linear), larger inputs (prefill) on torch's GEMM."""
     with torch.no_grad():
         linear.weight.data = prepare_weight_for_sparse_gemv(linear.weight.data)
-    N = linear.weight.shape[0]
+    N, Z = linear.weight.shape
 
     def sparse_forward(x):
         if _is_single_token(x):
@@ -125,6 +139,9 @@ def _patch_linear_with_kernel(linear: nn.Linear, threshold: float) -> None:
             if linear.bias is not None:
                 out = out + linear.bias
             return out
+        rows = x.numel() // Z if x.shape[-1] == Z else 0
+        if x.dtype == torch.float16 and linear.bias is None and _skinny_dense(rows, N, Z):
+            return batched_sparse_gemm(x.reshape(rows, Z), linear.weight, 0.0).reshape(x.shape[:-1] + (N,))
         return torch.nn.functional.linear(x, linear.weight, linear.bias)
 
     linear._teal_original_forward = linear.forward
