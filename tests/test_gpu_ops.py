@@ -244,3 +244,31 @@ def test_out_ops_in_a_captured_graph(cuda):
         for i, (a, b) in enumerate(zip(got, want)):
             assert torch.equal(a, b), "replay %d, output %d differs from eager" % (r, i)
         _ = torch.zeros(1000, device=cuda).sum()  # unrelated eager work between replays
+
+
+@pytest.mark.parametrize("N,Z,rows", [(4096, 14336, 2), (4096, 14336, 16), (14336, 4096, 8), (1024, 4096, 4),
+                                      (14336, 4096, 16), (520, 333, 3)])
+def test_patched_linear_multi_row_is_dense(cuda, N, Z, rows):
+    """A TEAL-patched projection called on several decode rows computes the dense product, as the reference's
+    dispatch does (leankv/teal/patching.py:169-180), whether it runs on the batched kernel (threshold 0: up to 8
+    rows, or 16 for a down-shaped weight) or on torch's F.linear; exact zeros in x contribute nothing either way."""
+    import torch.nn as nn
+
+    from leankv_amd.teal.patching import _patch_linear_with_kernel, _skinny_dense
+
+    g = torch.Generator().manual_seed(N + Z + rows)
+    lin = nn.Linear(Z, N, bias=False).half()
+    with torch.no_grad():
+        lin.weight.copy_((torch.randn(N, Z, generator=g) * 0.02).half())
+    W = lin.weight.detach().clone()
+    lin = lin.to(cuda)
+    _patch_linear_with_kernel(lin, 0.5)  # a threshold that would drop ~60 % of the inputs at B = 1
+    x = torch.randn(1, rows, Z, generator=g).half()
+    x[0, 0, : Z // 3] = 0  # zero inputs in one row
+    with torch.no_grad():
+        y = lin(x.to(cuda)).cpu()
+    ref = np.stack([ot.sparse_gemv(x[0, r].numpy(), W.numpy(), 0.0) for r in range(rows)])  # dense (threshold 0)
+    assert tuple(y.shape) == (1, rows, N)
+    assert ot.rel_err(y[0].numpy(), ref) < GEMV_TOL
+    assert ot.max_rel_err(y[0].numpy(), ref) < 1e-2
+    assert _skinny_dense(rows, N, Z) == (rows <= 8 or Z > N)
