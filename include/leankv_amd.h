@@ -479,7 +479,9 @@ int lkv_decode_layer_step(const lkv_decode_dims* dims, const lkv_decode_layer* l
  * dense).  The step's key and value are RoPE'd as in lkv_decode_layer_step and
  * written to kv_pool, fp16 [ceil(max_len / 16)][2 (K, V)][16][n_kv_heads][128]
  * (token t in page t / 16, slot t % 16, the layout of lkv_paged_decode_attn),
- * then lkv_paged_decode_attn attends to tokens 0 .. pos.  The cache fields of
+ * and the layer attends to tokens 0 .. pos as lkv_paged_decode_attn does over
+ * identity pages (with at most 4 query heads per kv head the split kernel sums
+ * the projection partials and writes the new token itself).  The cache fields of
  * `layer` are not read; lkv_decode_evict is not needed. */
 int lkv_decode_layer_step_f16kv(const lkv_decode_dims* dims, const lkv_decode_layer* layer, void* kv_pool, void* x,
                                 void* workspace, size_t workspace_bytes, void* stream);

@@ -674,6 +674,29 @@ extern "C" int lkv_decode_layer_step_f16kv(const lkv_decode_dims* dims, const lk
   const float* pq = reinterpret_cast<const float*>(ws + p.off_pqkv);
   const float* pk = pq + gemv_part_floats(p.nq, p.nc_qkv);
   const float* pv = pk + gemv_part_floats(p.nkv, p.nc_qkv);
+  if (p.Hq / p.Hkv <= 4) {  // one launch pair: the split kernel sums the partials itself
+    F16kvStepAttn a{};
+    a.pq = pq;
+    a.pk = pk;
+    a.pv = pv;
+    a.nchunk = p.nc_qkv;
+    a.rope_cos = static_cast<const uint16_t*>(d.rope_cos);
+    a.rope_sin = static_cast<const uint16_t*>(d.rope_sin);
+    a.pos = reinterpret_cast<const int32_t*>(ws + p.off_state);
+    a.kv = static_cast<uint16_t*>(kv_pool);
+    a.Hq = p.Hq;
+    a.Hkv = p.Hkv;
+    a.page_size = kF16Page;
+    a.max_pages = p.f16_pages;
+    a.max_len = d.max_len;
+    a.scale = d.scale;
+    a.out = reinterpret_cast<uint16_t*>(ws + p.off_attn);
+    a.records = ws + p.off_prec;
+    a.record_bytes = p.prec_bytes;
+    if (int e = f16kv_step_attn(a, st)) return e;
+    return step_tail(p, d, L, xx, ws, st);
+  }
+  // more than 4 query heads per kv head: epilogue kernel, then the paged call
   int32_t* pt = reinterpret_cast<int32_t*>(ws + p.off_pt);
   uint16_t* q16 = reinterpret_cast<uint16_t*>(ws + p.off_q16);
   const int items = static_cast<int>(p.nq / 2 + p.nkv);

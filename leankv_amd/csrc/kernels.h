@@ -323,4 +323,28 @@ struct AttnCall {
 // Launch the split and combine kernels.
 int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st);
 
+// Attention of the dense fp16-KV decode step (B = 1, at most 4 query heads
+// per kv head) over the page pool kv [page][K, V][page_size][Hkv][128] fp16,
+// token t in page t / page_size (identity pages).  The query, key and value
+// of the new token arrive as q|k|v GEMV partials ([slab][chunk][kGemvBN]);
+// the split kernel sums them, applies RoPE at position *pos (query and key
+// rounded to fp16), writes the new key and value into the pool and attends
+// over tokens 0 .. *pos; then the combine writes out [Hq, 128] fp16.
+struct F16kvStepAttn {
+  const float* pq;
+  const float* pk;
+  const float* pv;
+  int nchunk;
+  const uint16_t* rope_cos;  // [max_len, 128] fp16
+  const uint16_t* rope_sin;
+  const int32_t* pos;
+  uint16_t* kv;
+  int64_t Hq, Hkv, page_size, max_pages, max_len;
+  float scale;
+  uint16_t* out;
+  void* records;  // lkv_paged_decode_attn_workspace_bytes(1, Hq, Hkv, max_len) bytes
+  size_t record_bytes;
+};
+int f16kv_step_attn(const F16kvStepAttn& a, hipStream_t st);
+
 }  // namespace lkv

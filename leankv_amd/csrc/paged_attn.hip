@@ -51,6 +51,15 @@ struct PagedParams {
   uint16_t* out;            // [B, Hq, 128] fp16
   float scale_log2;
   int Hq, Hkv, G, ps, nsplit, split_tokens, max_pages;
+  // decode step (DECODE): q|k|v GEMV partials, RoPE tables, the position
+  const float* pq;
+  const float* pk;
+  const float* pv;
+  const uint16_t* rope_cos;
+  const uint16_t* rope_sin;
+  const int32_t* pos;
+  uint16_t* kv_new;  // the pool, written at the new token's slot
+  int nchunk, max_len;
 };
 
 // A split record: G maxima, G sums, then (from a 16-byte boundary) G x 128
@@ -84,14 +93,26 @@ constexpr int kMaxPg = 256;  // page ids of one split staged in LDS (SMALLG path
 // heads over its tokens and the 4 token lanes of a dim group are summed at
 // the end.  Otherwise: page offsets through LDS, value rows per (8-dim group,
 // head) lane in batches of 8.
-template <bool SMALLG>
+//
+// DECODE (the dense fp16-KV decode step; SMALLG layout, B = 1): identity
+// pages (token t in page t / ps), length *pos + 1.  The prologue sums the
+// q|k|v GEMV partials of the new token and applies RoPE at *pos (query and
+// key rounded to fp16, exactly as a separate epilogue kernel storing fp16
+// would); the partial loads and the wave's first chunk are in flight
+// together.  The block whose split holds *pos writes the new key and value
+// into the pool and uses them, from LDS, in place of the rows it loads for
+// that token: no block reads the slot written in this launch.
+template <bool SMALLG, bool DECODE>
 __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
-  __shared__ float s_p[kWaves][16][kChunk];
+  static_assert(SMALLG || !DECODE, "the decode step runs the SMALLG layout");
+  __shared__ __align__(16) float s_p[kWaves][16][kChunk];
   __shared__ size_t s_off[SMALLG ? 1 : kWaves][kChunk];  // pool offset of each chunk token's value row
-  __shared__ int s_pg[SMALLG ? kMaxPg + 1 : 1];
+  __shared__ int s_pg[SMALLG && !DECODE ? kMaxPg + 1 : 1];
   __shared__ float s_alpha[kWaves][16];
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
   __shared__ __align__(16) float s_o[kWaves][16][kORow];
+  __shared__ float s_q[DECODE ? 4 : 1][kD];                     // decode: the RoPE'd query heads
+  __shared__ __align__(16) uint16_t s_new[DECODE ? 2 : 1][kD];  // decode: the new key and value
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -101,8 +122,13 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
   const int dg = lane >> 2, hq = lane & 3;  // value layout: 8-dim group, head slot
   float* rec = P.partials + ((static_cast<size_t>(b) * P.Hkv + kvh) * P.nsplit + split) * rec_floats(G);
 
-  int first;
-  const int len = seq_tokens(P, b, first);
+  int first = 0, len, pos = 0;
+  if constexpr (DECODE) {
+    pos = min(max(__builtin_amdgcn_readfirstlane(*P.pos), 0), P.max_len - 1);
+    len = pos + 1;
+  } else {
+    len = seq_tokens(P, b, first);
+  }
   const int t_begin = split * P.split_tokens;
   const int t_end = min(t_begin + P.split_tokens, len);
   if (t_begin >= t_end) {  // uniform: nothing of this sequence in this split
@@ -113,7 +139,7 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
     return;
   }
   const int pg0 = t_begin / P.ps;  // SMALLG: first page of the split
-  if constexpr (SMALLG) {
+  if constexpr (SMALLG && !DECODE) {
     const int np = P.indptr[b + 1] - first;
     const int npg = (t_end - 1) / P.ps - pg0 + 1;  // <= kMaxPg + 1 (host plan)
     for (int i = tid; i < npg; i += kThreads) {
@@ -124,14 +150,134 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
   }
   // pool offset of (token t of the split's range, side) for SMALLG
   auto off_of = [&](int t, int side) -> size_t {
-    const int page = s_pg[t / P.ps - pg0];
+    int page;
+    if constexpr (DECODE)
+      page = t / P.ps;
+    else
+      page = s_pg[t / P.ps - pg0];
     return ((static_cast<size_t>(page) * 2 + side) * P.ps + t % P.ps) * (static_cast<size_t>(P.Hkv) * kD) +
            static_cast<size_t>(kvh) * kD;
   };
 
+  // SMALLG chunk registers: key rows of tokens c + 16 tt + (lane % 16), value
+  // rows of tokens c + lane / 16 + 4 i (clamped valid tokens, masked later)
+  const int dv = lane & 15, sub = lane >> 4;  // SMALLG value layout: 8-dim group, token lane
+  u32x4 a[2][4];
+  uint4 vr[8];
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const uint16_t* kp = P.kv + off_of(min(c + 16 * tt + h, t_end - 1), 0) + 8 * g;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const uint4 u = *reinterpret_cast<const uint4*>(kp + 32 * kb);
+        a[tt][kb] = u32x4{u.x, u.y, u.z, u.w};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      vr[i] = *reinterpret_cast<const uint4*>(P.kv + off_of(min(c + sub + 4 * i, t_end - 1), 1) + 8 * dv);
+  };
+  const int c_first = t_begin + kChunk * wave;
+
   // B operand: query x scale * log2(e), head h (rows h >= G zero), dims 32 kb + 8 g + i
   u32x4 qa[4];
-  {
+  bool writer = false;  // DECODE: this block's split holds the new token
+  if constexpr (DECODE) {
+    const uint16_t* cos_row = P.rope_cos + static_cast<size_t>(pos) * kD;
+    const uint16_t* sin_row = P.rope_sin + static_cast<size_t>(pos) * kD;
+    writer = pos < t_begin + P.split_tokens;  // pos >= t_begin: the split is not empty
+    // Thread e < G * 64: query head e / 64, dim pair (e % 64, e % 64 + 64);
+    // threads 0..63 / 64..127 also the key / value pair (t % 64, t % 64 + 64)
+    // of the new token (loaded by every block, without a branch).  The first
+    // kPre chunk partials from clamped, always valid addresses.
+    constexpr int kPre = 8;
+    float pre0[kPre], pre1[kPre], prk0[kPre], prk1[kPre];
+    const int e = min(tid, G * (kD / 2) - 1);
+    const int hh = e / (kD / 2), dd = e % (kD / 2);
+    const uint16_t rc0 = cos_row[dd], rc1 = cos_row[dd + kD / 2];
+    const uint16_t rs0 = sin_row[dd], rs1 = sin_row[dd + kD / 2];
+    const int col = (kvh * G + hh) * kD + dd;
+    const int t = tid & (kD - 1);
+    const float* ksrc = t < kD / 2 ? P.pk : P.pv;
+    const int kc0 = kvh * kD + (t & (kD / 2 - 1));
+    {
+      const float* p0 = P.pq + static_cast<size_t>(col / kGemvBN) * P.nchunk * kGemvBN + (col % kGemvBN);
+      const float* p1 = P.pq + static_cast<size_t>((col + kD / 2) / kGemvBN) * P.nchunk * kGemvBN +
+                        ((col + kD / 2) % kGemvBN);
+      const float* k0 = ksrc + static_cast<size_t>(kc0 / kGemvBN) * P.nchunk * kGemvBN + (kc0 % kGemvBN);
+      const float* k1 = ksrc + static_cast<size_t>((kc0 + kD / 2) / kGemvBN) * P.nchunk * kGemvBN +
+                        ((kc0 + kD / 2) % kGemvBN);
+#pragma unroll
+      for (int i = 0; i < kPre; ++i) {
+        const size_t o = static_cast<size_t>(min(i, P.nchunk - 1)) * kGemvBN;
+        pre0[i] = p0[o];
+        pre1[i] = p1[o];
+        prk0[i] = k0[o];
+        prk1[i] = k1[o];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the chunk's (results retire in order)
+    if (c_first < t_end) load_chunk(c_first);
+    // sums in column_sum2's order (chunk order from 0)
+    if (tid < G * (kD / 2)) {
+      float x0 = 0.f, x1 = 0.f, o0, o1;
+      if (P.nchunk <= kPre) {
+#pragma unroll
+        for (int i = 0; i < kPre; ++i) {
+          x0 += i < P.nchunk ? pre0[i] : 0.f;
+          x1 += i < P.nchunk ? pre1[i] : 0.f;
+        }
+        rope_pair_v(x0, x1, rc0, rc1, rs0, rs1, o0, o1);
+      } else {
+        column_sum2(P.pq, col, col + kD / 2, P.nchunk, x0, x1);
+        rope_pair(x0, x1, cos_row, sin_row, dd, o0, o1);
+      }
+      s_q[hh][dd] = o0;
+      s_q[hh][dd + kD / 2] = o1;
+    }
+    if (writer && tid < kD) {
+      float x0 = 0.f, x1 = 0.f, o0, o1;
+      if (P.nchunk <= kPre) {
+#pragma unroll
+        for (int i = 0; i < kPre; ++i) {
+          x0 += i < P.nchunk ? prk0[i] : 0.f;
+          x1 += i < P.nchunk ? prk1[i] : 0.f;
+        }
+      } else {
+        column_sum2(ksrc, kc0, kc0 + kD / 2, P.nchunk, x0, x1);
+      }
+      const int side = tid < kD / 2 ? 0 : 1;
+      if (side == 0) {  // key pair (tid, tid + 64), RoPE'd (the factors of query element tid)
+        if (P.nchunk <= kPre)
+          rope_pair_v(x0, x1, rc0, rc1, rs0, rs1, o0, o1);
+        else
+          rope_pair(x0, x1, cos_row, sin_row, tid, o0, o1);
+      } else {  // value dims (t - 64, t): no RoPE
+        o0 = x0;
+        o1 = x1;
+      }
+      const int d0 = t & (kD / 2 - 1);
+      const uint16_t h0 = f2h(o0), h1 = f2h(o1);
+      s_new[side][d0] = h0;
+      s_new[side][d0 + kD / 2] = h1;
+      uint16_t* dst = P.kv_new + off_of(pos, side);
+      dst[d0] = h0;
+      dst[d0 + kD / 2] = h1;
+    }
+    __syncthreads();
+    const float* qrow = s_q[min(h, G - 1)];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      u32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * kb + 8 * g + 2 * j;
+        v[j] = pack2h(qrow[d] * P.scale_log2, qrow[d + 1] * P.scale_log2);
+      }
+      qa[kb] = h < G ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+  } else {
     const uint16_t* qrow = P.q + (static_cast<size_t>(b) * P.Hq + kvh * G + min(h, G - 1)) * kD + 8 * g;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
@@ -144,6 +290,9 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
                       h2f(static_cast<uint16_t>(w[j] >> 16)) * P.scale_log2);
       qa[kb] = h < G ? v : u32x4{0u, 0u, 0u, 0u};
     }
+    if constexpr (SMALLG) {
+      if (c_first < t_end) load_chunk(c_first);
+    }
   }
 
   float m = -INFINITY, lsum = 0.f;  // per lane: head h
@@ -153,25 +302,21 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[k][j] = 0.f;
 
-  const int dv = lane & 15, sub = lane >> 4;  // SMALLG value layout: 8-dim group, token lane
   if constexpr (SMALLG) {
-    for (int c = t_begin + kChunk * wave; c < t_end; c += kChunk * kWaves) {
-      // ---- loads: key rows of tokens c + 16 tt + (lane % 16), value rows of
-      // tokens c + lane / 16 + 4 i (clamped valid tokens, masked below)
-      u32x4 a[2][4];
+    for (int c = c_first; c < t_end;) {
+      if constexpr (DECODE) {
+        if (writer) {  // the new token's rows come from LDS, not from the slot written above
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const uint16_t* kp = P.kv + off_of(min(c + 16 * tt + h, t_end - 1), 0) + 8 * g;
+          for (int tt = 0; tt < 2; ++tt)
+            if (min(c + 16 * tt + h, t_end - 1) == pos) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          const uint4 u = *reinterpret_cast<const uint4*>(kp + 32 * kb);
-          a[tt][kb] = u32x4{u.x, u.y, u.z, u.w};
+              for (int kb = 0; kb < 4; ++kb) a[tt][kb] = *reinterpret_cast<const u32x4*>(&s_new[0][32 * kb + 8 * g]);
+            }
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (min(c + sub + 4 * i, t_end - 1) == pos) vr[i] = *reinterpret_cast<const uint4*>(&s_new[1][8 * dv]);
         }
       }
-      uint4 vr[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        vr[i] = *reinterpret_cast<const uint4*>(P.kv + off_of(min(c + sub + 4 * i, t_end - 1), 1) + 8 * dv);
       // ---- scores, online softmax (lane: head h, tokens c + 16 tt + 4 g + i)
       f32x4 sc[2];
 #pragma unroll
@@ -199,19 +344,36 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
         for (int i = 0; i < 4; ++i) {
           const float p = fast_exp2(s[4 * tt + i] - mn);
           ps += p;
-          s_p[wave][h][16 * tt + 4 * g + i] = p;
+          // chunk token t = 16 tt + 4 g + i at (t % 4) * 8 + t / 4: the 8 tokens
+          // sub + 4 i' of a value lane are then contiguous
+          s_p[wave][h][8 * i + 4 * tt + g] = p;
         }
       lsum = lsum * alpha + ps;
       if (g == 0) s_alpha[wave][h] = alpha;
       __builtin_amdgcn_wave_barrier();
-      // ---- values: this lane's tokens for every head
+      // ---- values: this lane's tokens for every head slot.  Slots k >= G
+      // (query rows of zeros: finite probabilities) are computed and never
+      // written out, so nothing here branches on G and every LDS read is
+      // issued before the first is used.
+      float pl[4][8];  // 0 for tokens past the end
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        if (k < G) {
-          const float al = s_alpha[wave][k];
+        const float4 lo = *reinterpret_cast<const float4*>(&s_p[wave][k][8 * sub]);
+        const float4 hi = *reinterpret_cast<const float4*>(&s_p[wave][k][8 * sub + 4]);
+        pl[k][0] = lo.x;
+        pl[k][1] = lo.y;
+        pl[k][2] = lo.z;
+        pl[k][3] = lo.w;
+        pl[k][4] = hi.x;
+        pl[k][5] = hi.y;
+        pl[k][6] = hi.z;
+        pl[k][7] = hi.w;
+      }
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc[k][j] *= al;
-        }
+      for (int k = 0; k < 4; ++k) {
+        const float al = s_alpha[wave][k];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[k][j] *= al;
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -223,15 +385,13 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
           v[2 * e + 1] = h2f(static_cast<uint16_t>(w[e] >> 16));
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          if (k < G) {
-            const float p = s_p[wave][k][sub + 4 * i];  // 0 for tokens past the end
+        for (int k = 0; k < 4; ++k)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[k][j] = fmaf(p, v[j], acc[k][j]);
-          }
-        }
+          for (int j = 0; j < 8; ++j) acc[k][j] = fmaf(pl[k][i], v[j], acc[k][j]);
       }
       __builtin_amdgcn_wave_barrier();
+      c += kChunk * kWaves;
+      if (c < t_end) load_chunk(c);
     }
     // the 4 token lanes of each dim group (lanes dv, dv + 16, dv + 32, dv + 48)
 #pragma unroll
@@ -433,8 +593,8 @@ __global__ __launch_bounds__(kPcThreads) void paged_combine_kernel(PagedParams P
 int64_t paged_min_split_tokens() {
   static const int64_t k = [] {
     const char* env = getenv("LKV_PAGED_MIN_SPLIT_TOKENS");
-    const long v = env ? atol(env) : 256;
-    return static_cast<int64_t>(v > 0 && v <= (1 << 20) ? v : 256);
+    const long v = env ? atol(env) : 128;
+    return static_cast<int64_t>(v > 0 && v <= (1 << 20) ? v : 128);
   }();
   return k;
 }
@@ -461,6 +621,47 @@ PagedPlan paged_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len) {
 }
 
 }  // namespace
+
+int f16kv_step_attn(const F16kvStepAttn& a, hipStream_t st) {
+  LKV_REQUIRE(a.Hq > 0 && a.Hkv > 0 && a.Hq % a.Hkv == 0 && a.Hq / a.Hkv <= 4,
+              "f16kv_step_attn: need Hq %% Hkv == 0 and Hq/Hkv <= 4 (Hq=%lld Hkv=%lld)", (long long)a.Hq,
+              (long long)a.Hkv);
+  LKV_REQUIRE(a.max_len >= 1 && a.max_len < (1ll << 30) && a.page_size >= 1 && a.max_pages >= 1 &&
+                  a.max_len <= a.max_pages * a.page_size && a.nchunk >= 1,
+              "f16kv_step_attn: max_len=%lld page_size=%lld max_pages=%lld nchunk=%d out of range",
+              (long long)a.max_len, (long long)a.page_size, (long long)a.max_pages, a.nchunk);
+  const PagedPlan pl = paged_plan(1, a.Hq, a.Hkv, a.max_len);
+  LKV_REQUIRE(a.records && a.record_bytes >= pl.bytes, "f16kv_step_attn: %zu record bytes required, got %zu",
+              pl.bytes, a.record_bytes);
+  PagedParams P{};
+  P.kv = a.kv;
+  P.partials = static_cast<float*>(a.records);
+  P.out = a.out;
+  P.scale_log2 = a.scale * kLog2e;
+  P.Hq = static_cast<int>(a.Hq);
+  P.Hkv = static_cast<int>(a.Hkv);
+  P.G = static_cast<int>(a.Hq / a.Hkv);
+  P.ps = static_cast<int>(a.page_size);
+  P.nsplit = pl.nsplit;
+  P.split_tokens = pl.split_tokens;
+  P.max_pages = static_cast<int>(a.max_pages);
+  P.pq = a.pq;
+  P.pk = a.pk;
+  P.pv = a.pv;
+  P.rope_cos = a.rope_cos;
+  P.rope_sin = a.rope_sin;
+  P.pos = a.pos;
+  P.kv_new = a.kv;
+  P.nchunk = a.nchunk;
+  P.max_len = static_cast<int>(a.max_len);
+  hipLaunchKernelGGL((paged_split_kernel<true, true>), dim3(static_cast<unsigned>(pl.nsplit), static_cast<unsigned>(a.Hkv)),
+                     dim3(kThreads), 0, st, P);
+  LKV_LAUNCH_CHECK("f16kv_step_attn split");
+  hipLaunchKernelGGL(paged_combine_kernel, dim3(static_cast<unsigned>(a.Hq)), dim3(kPcThreads), 0, st, P);
+  LKV_LAUNCH_CHECK("f16kv_step_attn combine");
+  return LKV_OK;
+}
+
 }  // namespace lkv
 
 using namespace lkv;
@@ -513,9 +714,9 @@ extern "C" int lkv_paged_decode_attn(const void* q, const void* kv_data, const i
   // the SMALLG path stages a split's pages in LDS: (ts - 1) / ps + 2 of them at most
   const bool small = Hq / Hkv <= 4 && (pl.split_tokens - 1) / page_size + 2 <= kMaxPg + 1;
   if (small)
-    hipLaunchKernelGGL((paged_split_kernel<true>), grid, dim3(kThreads), 0, st, P);
+    hipLaunchKernelGGL((paged_split_kernel<true, false>), grid, dim3(kThreads), 0, st, P);
   else
-    hipLaunchKernelGGL((paged_split_kernel<false>), grid, dim3(kThreads), 0, st, P);
+    hipLaunchKernelGGL((paged_split_kernel<false, false>), grid, dim3(kThreads), 0, st, P);
   LKV_LAUNCH_CHECK("paged_decode_attn split");
   hipLaunchKernelGGL(paged_combine_kernel, dim3(static_cast<unsigned>(Hq), static_cast<unsigned>(B)),
                      dim3(kPcThreads), 0, st, P);
