@@ -17,10 +17,12 @@
 //     load per lane, page looked up per token), B = the query (16 head
 //     columns, G used), so a lane holds one head's scores for 8 tokens;
 //   * online softmax per lane (exp2 domain, max / sum across the 4 lanes of
-//     a head by permlane swaps); the chunk's probabilities go to the wave's
-//     LDS slice;
-//   * values on the VALU: lane (8-dim group, head) streams the chunk's value
-//     rows with 16-byte loads and accumulates p * v (fp32);
+//     a head by permlane swaps);
+//   * values: at most 4 query heads per kv head (SMALLG) on MFMA as in the
+//     packed decode kernel, A = 16 dims x 32 tokens of value rows (16-byte
+//     loads, token pairs joined by v_perm), B = the probabilities in fp16
+//     (fp32 accumulate); otherwise on the VALU from the wave's LDS slice of
+//     probabilities, lane (8-dim group, head) accumulating p * v in fp32;
 // the 4 waves merge through LDS into one (m, l, o[G][128]) record per split;
 // then a combine kernel, one block per (batch, query head), merges the split
 // records.  Page indices are clamped to the pool, lengths to the pages owned,
@@ -87,11 +89,11 @@ __device__ __forceinline__ size_t kv_offset(const PagedParams& P, int first, int
 constexpr int kMaxPg = 256;  // page ids of one split staged in LDS (SMALLG path)
 
 // SMALLG (at most 4 query heads per kv head, the split's pages staged in LDS):
-// a chunk's key rows (score lanes) and value rows (value lanes: 8-dim group
-// lane % 16, tokens lane / 16 + 4 i) are loaded together, one memory round
-// trip per chunk, every value row once; each value lane accumulates all G
-// heads over its tokens and the 4 token lanes of a dim group are summed at
-// the end.  Otherwise: page offsets through LDS, value rows per (8-dim group,
+// a chunk's key rows and value rows (lane: 8-dim group lane % 16, the 8
+// tokens of its scores) are loaded together, one memory round trip per chunk,
+// every value row once; the values go through MFMA with no LDS traffic, and
+// each lane rescales the output column of the head whose running max it
+// holds.  Otherwise: page offsets through LDS, value rows per (8-dim group,
 // head) lane in batches of 8.
 //
 // DECODE (the dense fp16-KV decode step; SMALLG layout, B = 1): identity
@@ -105,10 +107,10 @@ constexpr int kMaxPg = 256;  // page ids of one split staged in LDS (SMALLG path
 template <bool SMALLG, bool DECODE>
 __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
   static_assert(SMALLG || !DECODE, "the decode step runs the SMALLG layout");
-  __shared__ __align__(16) float s_p[kWaves][16][kChunk];
+  __shared__ float s_p[SMALLG ? 1 : kWaves][16][kChunk];
   __shared__ size_t s_off[SMALLG ? 1 : kWaves][kChunk];  // pool offset of each chunk token's value row
   __shared__ int s_pg[SMALLG && !DECODE ? kMaxPg + 1 : 1];
-  __shared__ float s_alpha[kWaves][16];
+  __shared__ float s_alpha[SMALLG ? 1 : kWaves][16];
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
   __shared__ __align__(16) float s_o[kWaves][16][kORow];
   __shared__ float s_q[DECODE ? 4 : 1][kD];                     // decode: the RoPE'd query heads
@@ -159,9 +161,9 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
            static_cast<size_t>(kvh) * kD;
   };
 
-  // SMALLG chunk registers: key rows of tokens c + 16 tt + (lane % 16), value
-  // rows of tokens c + lane / 16 + 4 i (clamped valid tokens, masked later)
-  const int dv = lane & 15, sub = lane >> 4;  // SMALLG value layout: 8-dim group, token lane
+  // SMALLG chunk registers: key rows of tokens c + 16 tt + (lane % 16) (dims
+  // 8 (lane / 16) + 32 kb ..), value rows j of tokens c + 16 (j / 4) +
+  // 4 (lane / 16) + j % 4 (dims 8 (lane % 16) ..): clamped valid tokens, masked later
   u32x4 a[2][4];
   uint4 vr[8];
   auto load_chunk = [&](int c) {
@@ -175,8 +177,9 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
       }
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      vr[i] = *reinterpret_cast<const uint4*>(P.kv + off_of(min(c + sub + 4 * i, t_end - 1), 1) + 8 * dv);
+    for (int j = 0; j < 8; ++j)
+      vr[j] = *reinterpret_cast<const uint4*>(P.kv + off_of(min(c + 16 * (j >> 2) + 4 * g + (j & 3), t_end - 1), 1) +
+                                              8 * h);
   };
   const int c_first = t_begin + kChunk * wave;
 
@@ -296,11 +299,14 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
   }
 
   float m = -INFINITY, lsum = 0.f;  // per lane: head h
-  float acc[4][8];                  // per lane: heads hq + 4 k, dims 8 dg ..
+  float acc[4][8];                  // general path, per lane: heads hq + 4 k, dims 8 dg ..
+  f32x4 ov[8];                      // SMALLG: the value MFMA tiles
 #pragma unroll
   for (int k = 0; k < 4; ++k)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[k][j] = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) ov[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if constexpr (SMALLG) {
     for (int c = c_first; c < t_end;) {
@@ -313,8 +319,9 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
               for (int kb = 0; kb < 4; ++kb) a[tt][kb] = *reinterpret_cast<const u32x4*>(&s_new[0][32 * kb + 8 * g]);
             }
 #pragma unroll
-          for (int i = 0; i < 8; ++i)
-            if (min(c + sub + 4 * i, t_end - 1) == pos) vr[i] = *reinterpret_cast<const uint4*>(&s_new[1][8 * dv]);
+          for (int j = 0; j < 8; ++j)
+            if (min(c + 16 * (j >> 2) + 4 * g + (j & 3), t_end - 1) == pos)
+              vr[j] = *reinterpret_cast<const uint4*>(&s_new[1][8 * h]);
         }
       }
       // ---- scores, online softmax (lane: head h, tokens c + 16 tt + 4 g + i)
@@ -337,70 +344,38 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
       const float mn = fmaxf(m, mx);  // finite: the chunk holds at least one token
       const float alpha = fast_exp2(m - mn);
       m = mn;
-      float ps = 0.f;
+      float ps = 0.f, pr[8];
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = fast_exp2(s[4 * tt + i] - mn);
-          ps += p;
-          // chunk token t = 16 tt + 4 g + i at (t % 4) * 8 + t / 4: the 8 tokens
-          // sub + 4 i' of a value lane are then contiguous
-          s_p[wave][h][8 * i + 4 * tt + g] = p;
-        }
+      for (int j = 0; j < 8; ++j) {
+        pr[j] = fast_exp2(s[j] - mn);  // 0 for tokens past the end
+        ps += pr[j];
+      }
       lsum = lsum * alpha + ps;
-      if (g == 0) s_alpha[wave][h] = alpha;
-      __builtin_amdgcn_wave_barrier();
-      // ---- values: this lane's tokens for every head slot.  Slots k >= G
-      // (query rows of zeros: finite probabilities) are computed and never
-      // written out, so nothing here branches on G and every LDS read is
-      // issued before the first is used.
-      float pl[4][8];  // 0 for tokens past the end
+      // ---- values on MFMA, transposed: A = 16 dim rows (8 (lane % 16) + t)
+      // x 32 tokens (the lane's value rows, paired by v_perm), B = the
+      // probabilities in fp16 (lane: head lane % 16, the same 8 tokens as its
+      // scores); ov[t] row 4 (lane / 16) + i holds dim 8 (4 (lane / 16) + i) + t
+      // of head lane % 16, whose running max this lane holds: the rescale
+      // needs no exchange.
+      const u32x4 pb = u32x4{pack2h(pr[0], pr[1]), pack2h(pr[2], pr[3]), pack2h(pr[4], pr[5]), pack2h(pr[6], pr[7])};
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float4 lo = *reinterpret_cast<const float4*>(&s_p[wave][k][8 * sub]);
-        const float4 hi = *reinterpret_cast<const float4*>(&s_p[wave][k][8 * sub + 4]);
-        pl[k][0] = lo.x;
-        pl[k][1] = lo.y;
-        pl[k][2] = lo.z;
-        pl[k][3] = lo.w;
-        pl[k][4] = hi.x;
-        pl[k][5] = hi.y;
-        pl[k][6] = hi.z;
-        pl[k][7] = hi.w;
-      }
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
+        u32x4 av;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float al = s_alpha[wave][k];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[k][j] *= al;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t w[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[2 * e] = h2f(static_cast<uint16_t>(w[e] & 0xffffu));
-          v[2 * e + 1] = h2f(static_cast<uint16_t>(w[e] >> 16));
+        for (int pp = 0; pp < 4; ++pp) {
+          const uint4& r0 = vr[2 * pp];
+          const uint4& r1 = vr[2 * pp + 1];
+          const uint32_t x0 = (t >> 1) == 0 ? r0.x : (t >> 1) == 1 ? r0.y : (t >> 1) == 2 ? r0.z : r0.w;
+          const uint32_t x1 = (t >> 1) == 0 ? r1.x : (t >> 1) == 1 ? r1.y : (t >> 1) == 2 ? r1.z : r1.w;
+          av[pp] = __builtin_amdgcn_perm(x1, x0, sel);
         }
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[k][j] = fmaf(pl[k][i], v[j], acc[k][j]);
+        ov[t] = mfma16x16x32(av, pb, ov[t] * alpha);
       }
       __builtin_amdgcn_wave_barrier();
       c += kChunk * kWaves;
       if (c < t_end) load_chunk(c);
     }
-    // the 4 token lanes of each dim group (lanes dv, dv + 16, dv + 32, dv + 48)
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        acc[k][j] += __shfl_xor(acc[k][j], 16);
-        acc[k][j] += __shfl_xor(acc[k][j], 32);
-      }
   } else {
     for (int c = t_begin + kChunk * wave; c < t_end; c += kChunk * kWaves) {
       // ---- scores: tokens c + 16 tt + (lane % 16) as A rows
@@ -489,12 +464,20 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
     s_m[wave][h] = m;
     s_l[wave][h] = ltot;
   }
+  if constexpr (SMALLG) {  // lane: head h, dims 8 (4 g + i) + t
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    if (SMALLG && sub != 0) continue;  // SMALLG: lanes 0..15 hold the sums, head k
-    float4* dst = reinterpret_cast<float4*>(SMALLG ? &s_o[wave][k][8 * dv] : &s_o[wave][hq + 4 * k][8 * dg]);
-    dst[0] = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
-    dst[1] = make_float4(acc[k][4], acc[k][5], acc[k][6], acc[k][7]);
+    for (int i = 0; i < 4; ++i) {
+      float4* dst = reinterpret_cast<float4*>(&s_o[wave][h][8 * (4 * g + i)]);
+      dst[0] = make_float4(ov[0][i], ov[1][i], ov[2][i], ov[3][i]);
+      dst[1] = make_float4(ov[4][i], ov[5][i], ov[6][i], ov[7][i]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float4* dst = reinterpret_cast<float4*>(&s_o[wave][hq + 4 * k][8 * dg]);
+      dst[0] = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+      dst[1] = make_float4(acc[k][4], acc[k][5], acc[k][6], acc[k][7]);
+    }
   }
   __syncthreads();
   for (int e = tid; e < G * kD; e += kThreads) {
