@@ -191,4 +191,95 @@ __device__ __forceinline__ void gemv_core(GemvLds<NT, BZ, DUAL, U>& sm, const fl
   }
 }
 
+// Dense variant, for launches whose thresholds are all 0: every row of the
+// chunk takes part (for finite weights the same sums as the compacted list,
+// since a row whose input is exactly 0 adds 0), so there is no compaction and
+// slot k walks rows k, k + SLOTS, ... of the chunk, the order the list has when
+// nothing is dropped.  The weight loads do not depend on x: the caller issues
+// the first batch (gemv_dense_first) before its input prologue, so the two
+// memory round trips overlap.  Rows past Z read 0 through the descriptor and
+// have input 0.
+__device__ __forceinline__ uint32_t gemv_dense_off(int z, int Z, uint32_t row_bytes, uint32_t col_bytes,
+                                                   uint32_t a_bytes) {
+  return z < Z ? static_cast<uint32_t>(z) * row_bytes + col_bytes : a_bytes;  // past Z: past the descriptor end
+}
+
+template <int NT, int U, int CP>
+__device__ __forceinline__ void gemv_dense_first(const uint16_t* A0, uint32_t a_bytes, int N, int z0, int Z, int n0,
+                                                 gemv_u32x4 (&w)[U]) {
+  constexpr int LPR = kGemvBN / 8, SLOTS = NT / LPR;
+  const int tid = threadIdx.x;
+  const int col = n0 + (tid % LPR) * 8;
+  const uint32_t col_bytes = col < N ? static_cast<uint32_t>(col) * 2u : a_bytes;
+  const uint32_t row_bytes = static_cast<uint32_t>(N) * 2u;
+  const __amdgpu_buffer_rsrc_t A = gemv_rsrc(A0, a_bytes);
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    w[u] = __builtin_amdgcn_raw_buffer_load_b128(
+        A, gemv_dense_off(z0 + tid / LPR + u * SLOTS, Z, row_bytes, col_bytes, a_bytes), 0, CP);
+}
+
+template <int NT, int BZ, bool DUAL, int U, int CP>
+__device__ __forceinline__ void gemv_core_dense(GemvLds<NT, BZ, DUAL, U>& sm, const float (&v)[BZ / NT],
+                                                const gemv_u32x4 (&w0)[U], const uint16_t* A0, const uint16_t* A1,
+                                                uint32_t a_bytes, int N, int z0, int Z, int n0,
+                                                float (&sums)[DUAL ? 2 : 1]) {
+  using L = GemvLds<NT, BZ, DUAL, U>;
+  constexpr int NL = L::kNl, LPR = L::kLpr, SLOTS = L::kSlots, BN = kGemvBN, E = BZ / NT;
+  static_assert(BZ % (U * SLOTS) == 0, "whole streaming batches per chunk");
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < E; ++j) sm.xv[0][E * tid + j] = v[j];
+  __syncthreads();
+
+  const int c = tid % LPR;
+  const int slot = tid / LPR;
+  const int col = n0 + c * 8;
+  const uint32_t row_bytes = static_cast<uint32_t>(N) * 2u;
+  const uint32_t col_bytes = col < N ? static_cast<uint32_t>(col) * 2u : a_bytes;
+  const float* xs = sm.xv[0];
+  float acc[NL][8];
+#pragma unroll
+  for (int l = 0; l < NL; ++l)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[l][j] = 0.f;
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    const __amdgpu_buffer_rsrc_t A = gemv_rsrc(l == 0 ? A0 : A1, a_bytes);
+    int s = slot;
+    if (l == 0) {  // the preloaded first batch
+#pragma unroll
+      for (int u = 0; u < U; ++u) gemv_fma8(acc[0], w0[u], xs[s + u * SLOTS]);
+      s += U * SLOTS;
+    }
+    for (; s < BZ; s += U * SLOTS) {
+      gemv_u32x4 w[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        w[u] = __builtin_amdgcn_raw_buffer_load_b128(
+            A, gemv_dense_off(z0 + s + u * SLOTS, Z, row_bytes, col_bytes, a_bytes), 0, CP);
+#pragma unroll
+      for (int u = 0; u < U; ++u) gemv_fma8(acc[l], w[u], xs[s + u * SLOTS]);
+    }
+  }
+
+  // the cross-slot reduction of gemv_core
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    float4* dst = reinterpret_cast<float4*>(sm.red + (l * SLOTS + slot) * BN + c * 8);
+    dst[0] = make_float4(acc[l][0], acc[l][1], acc[l][2], acc[l][3]);
+    dst[1] = make_float4(acc[l][4], acc[l][5], acc[l][6], acc[l][7]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    float s = 0.f;
+    if (tid < BN) {
+#pragma unroll
+      for (int sl = 0; sl < SLOTS; ++sl) s += sm.red[(l * SLOTS + sl) * BN + tid];
+    }
+    sums[l] = s;
+  }
+}
+
 }  // namespace lkv

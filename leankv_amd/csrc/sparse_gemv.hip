@@ -115,7 +115,7 @@ __device__ __forceinline__ T seg_pick(const T (&v)[kMaxSeg], int seg) {
   return r;
 }
 
-template <int NT, int BZ, bool DUAL, int MODE, int U, int CP>
+template <int NT, int BZ, bool DUAL, int MODE, int U, int CP, bool DENSE = false>
 __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
   constexpr int BN = kGemvBN;
   constexpr int NL = DUAL ? 2 : 1;
@@ -146,10 +146,18 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
     const int n0 = slab * BN;
 
     float xin[BZ / NT];
-    input_prologue<NT, BZ, MODE>(G, z0, xin, sm.wsum);
     float sums[NL];
-    gemv_core<NT, BZ, DUAL, U, CP>(sm, xin, seg_pick(G.A, seg), G.A_up, seg_pick(G.a_bytes, seg), N,
-                                   seg_pick(G.t, seg), G.t_up, z0, G.Z, n0, sums);
+    if constexpr (DENSE) {
+      gemv_u32x4 w0[U];
+      gemv_dense_first<NT, U, CP>(seg_pick(G.A, seg), seg_pick(G.a_bytes, seg), N, z0, G.Z, n0, w0);
+      input_prologue<NT, BZ, MODE>(G, z0, xin, sm.wsum);
+      gemv_core_dense<NT, BZ, DUAL, U, CP>(sm, xin, w0, seg_pick(G.A, seg), G.A_up, seg_pick(G.a_bytes, seg), N, z0,
+                                           G.Z, n0, sums);
+    } else {
+      input_prologue<NT, BZ, MODE>(G, z0, xin, sm.wsum);
+      gemv_core<NT, BZ, DUAL, U, CP>(sm, xin, seg_pick(G.A, seg), G.A_up, seg_pick(G.a_bytes, seg), N,
+                                     seg_pick(G.t, seg), G.t_up, z0, G.Z, n0, sums);
+    }
 
     // ---- 4. output (threads 0..255, one column each): fp16 directly (single chunk) or partial sums
     if (tid < BN) {
@@ -236,6 +244,28 @@ bool launch_bz(const GemvArgs& G, bool dual, int mode, dim3 grid, hipStream_t st
     case kInSwiglu * 2: hipLaunchKernelGGL((sparse_gemv_kernel<NT, BZ, false, kInSwiglu, U, CP>), grid, blk, 0, st, G); return true;
     default: return false;
   }
+}
+
+// Every threshold 0: the dense variant (default launch shapes only).
+template <int NT, int BZ, int U>
+bool launch_dense(const GemvArgs& G, bool dual, int mode, dim3 grid, hipStream_t st) {
+  const dim3 blk(NT);
+  switch (mode * 2 + (dual ? 1 : 0)) {
+    case kInRaw * 2: hipLaunchKernelGGL((sparse_gemv_kernel<NT, BZ, false, kInRaw, U, 2, true>), grid, blk, 0, st, G); return true;
+    case kInRmsNorm * 2: hipLaunchKernelGGL((sparse_gemv_kernel<NT, BZ, false, kInRmsNorm, U, 2, true>), grid, blk, 0, st, G); return true;
+    case kInRmsNorm * 2 + 1: hipLaunchKernelGGL((sparse_gemv_kernel<NT, BZ, true, kInRmsNorm, U, 2, true>), grid, blk, 0, st, G); return true;
+    case kInSwiglu * 2: hipLaunchKernelGGL((sparse_gemv_kernel<NT, BZ, false, kInSwiglu, U, 2, true>), grid, blk, 0, st, G); return true;
+    default: return false;
+  }
+}
+
+// LKV_GEMV_DENSE=0 keeps zero-threshold launches on the compacting kernel (A/B sweeps).
+bool gemv_dense_enabled() {
+  static const bool d = [] {
+    const char* env = getenv("LKV_GEMV_DENSE");
+    return !(env && atoi(env) == 0);
+  }();
+  return d;
 }
 
 template <int NT, int BZ, int U>
@@ -327,7 +357,14 @@ int gemv_launch(const GemvArgs& G, int bz, bool dual, int mode, int nslab_total,
     Gx.slab0_seg[s] = nslab_total;
   }
   const int unroll = gemv_unroll(t512 ? 512 : 256);
-  if (unroll == 4) {
+  bool zero_t = !dual || G.t_up == 0.f;
+  for (int s = 0; s < G.nseg; ++s) zero_t = zero_t && G.t[s] == 0.f;
+  if (zero_t && gemv_dense_enabled() && cp == 2 && unroll == (t512 ? 4 : 8) && !gemv_persist() &&
+      !Gx.chunk_major) {
+    if (bz == 256) ok = launch_dense<256, 256, 8>(Gx, dual, mode, grid, st);
+    else if (bz == 512) ok = t512 ? launch_dense<512, 512, 4>(Gx, dual, mode, grid, st) : launch_dense<256, 512, 8>(Gx, dual, mode, grid, st);
+    else if (bz == 1024) ok = t512 ? launch_dense<512, 1024, 4>(Gx, dual, mode, grid, st) : launch_dense<256, 1024, 8>(Gx, dual, mode, grid, st);
+  } else if (unroll == 4) {
     if (bz == 256) ok = launch_cp<256, 256, 4>(Gx, dual, mode, grid, st, cp);
     else if (bz == 512) ok = t512 ? launch_cp<512, 512, 4>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 512, 4>(Gx, dual, mode, grid, st, cp);
     else if (bz == 1024) ok = t512 ? launch_cp<512, 1024, 4>(Gx, dual, mode, grid, st, cp) : launch_cp<256, 1024, 4>(Gx, dual, mode, grid, st, cp);
