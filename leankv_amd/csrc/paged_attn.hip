@@ -509,7 +509,7 @@ __global__ __launch_bounds__(kThreads) void paged_split_kernel(PagedParams P) {
 // before the first wait; the 8 split groups are joined in LDS in order.
 constexpr int kPcThreads = 256;
 constexpr int kPcGroups = kPcThreads / 32;
-constexpr int kPcDepth = 4;  // value sums per thread loaded up front (more splits: further passes)
+constexpr int kPcDepth = 8;  // value sums per thread loaded up front: 64 splits in one pass (more: further passes)
 __global__ __launch_bounds__(kPcThreads) void paged_combine_kernel(PagedParams P) {
   __shared__ float s_w[kMaxSplits];
   __shared__ float s_red[kPcThreads / 64];
