@@ -46,13 +46,18 @@ namespace {
 // x[z0 + E t + j], j < E = BZ / NT (0 past Z), the layout the compaction takes.
 // Every load of a mode is issued before the first is used (addresses clamped
 // into range, values selected afterwards): a conditional load compiles to a
-// branch and a wait per element, one memory round trip each.
-template <int NT, int BZ, int MODE>
-__device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float (&v)[BZ / NT], float* s_wsum) {
+// branch and a wait per element, one memory round trip each.  issue() runs
+// once, with no branch around it: after the mode's first loads (raw, SwiGLU),
+// so loads it issues return behind them (memory results retire in issue
+// order), or before any (RMSNorm, whose sum of squares reads the whole vector).
+template <int NT, int BZ, int MODE, bool HOOK, typename Issue>
+__device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float (&v)[BZ / NT], float* s_wsum,
+                                               Issue&& issue) {
   constexpr int E = BZ / NT;  // inputs per thread
   const int zt = z0 + E * static_cast<int>(threadIdx.x);
   const int Z = G.Z;
   if (MODE == kInRmsNorm) {
+    if constexpr (HOOK) issue();
     uint16_t xv[E], wv[E];
 #pragma unroll
     for (int j = 0; j < E; ++j) {
@@ -76,13 +81,18 @@ __device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float 
     float g[E], u[E];
 #pragma unroll
     for (int j = 0; j < E; ++j) g[j] = u[j] = 0.f;
-    for (int k0 = 0; k0 < nc; k0 += 8) {
+    auto pass = [&](int k0, bool first) {
       fvec vg[8], vu[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const size_t k = static_cast<size_t>(min(k0 + i, nc - 1)) * kGemvBN;
         vg[i] = *reinterpret_cast<const fvec*>(pg + k);
         vu[i] = *reinterpret_cast<const fvec*>(pg + mat + k);
+      }
+      if (HOOK && first) {
+        __builtin_amdgcn_sched_barrier(0);
+        issue();
+        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -93,13 +103,20 @@ __device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float 
           u[j] += ok ? vu[i][j] : 0.f;
         }
       }
-    }
+    };
+    pass(0, true);  // the first pass straight-line: issue() follows its loads with no branch between
+    for (int k0 = 8; k0 < nc; k0 += 8) pass(k0, false);
 #pragma unroll
     for (int j = 0; j < E; ++j) v[j] = zt + j < Z ? h2f(swiglu_f16(g[j], u[j])) : 0.f;
   } else {
     uint16_t xv[E];
 #pragma unroll
     for (int j = 0; j < E; ++j) xv[j] = G.x[min(zt + j, Z - 1)];
+    if constexpr (HOOK) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue();
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int j = 0; j < E; ++j) v[j] = zt + j < Z ? h2f(xv[j]) : 0.f;
   }
@@ -149,12 +166,13 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
     float sums[NL];
     if constexpr (DENSE) {
       gemv_u32x4 w0[U];
-      gemv_dense_first<NT, U, CP>(seg_pick(G.A, seg), seg_pick(G.a_bytes, seg), N, z0, G.Z, n0, w0);
-      input_prologue<NT, BZ, MODE>(G, z0, xin, sm.wsum);
+      input_prologue<NT, BZ, MODE, true>(G, z0, xin, sm.wsum, [&] {
+        gemv_dense_first<NT, U, CP>(seg_pick(G.A, seg), seg_pick(G.a_bytes, seg), N, z0, G.Z, n0, w0);
+      });
       gemv_core_dense<NT, BZ, DUAL, U, CP>(sm, xin, w0, seg_pick(G.A, seg), G.A_up, seg_pick(G.a_bytes, seg), N, z0,
                                            G.Z, n0, sums);
     } else {
-      input_prologue<NT, BZ, MODE>(G, z0, xin, sm.wsum);
+      input_prologue<NT, BZ, MODE, false>(G, z0, xin, sm.wsum, [] {});
       gemv_core<NT, BZ, DUAL, U, CP>(sm, xin, seg_pick(G.A, seg), G.A_up, seg_pick(G.a_bytes, seg), N,
                                      seg_pick(G.t, seg), G.t_up, z0, G.Z, n0, sums);
     }
