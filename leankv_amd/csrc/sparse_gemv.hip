@@ -104,8 +104,12 @@ __device__ __forceinline__ void input_prologue(const GemvArgs& G, int z0, float 
         }
       }
     };
-    pass(0, true);  // the first pass straight-line: issue() follows its loads with no branch between
-    for (int k0 = 8; k0 < nc; k0 += 8) pass(k0, false);
+    if constexpr (HOOK) {
+      pass(0, true);  // the first pass straight-line: issue() follows its loads with no branch between
+      for (int k0 = 8; k0 < nc; k0 += 8) pass(k0, false);
+    } else {
+      for (int k0 = 0; k0 < nc; k0 += 8) pass(k0, false);
+    }
 #pragma unroll
     for (int j = 0; j < E; ++j) v[j] = zt + j < Z ? h2f(swiglu_f16(g[j], u[j])) : 0.f;
   } else {
