@@ -831,9 +831,9 @@ def bench_prefill(args, torch):
     sets = []
     for s_ in range(3):
         g = torch.Generator(device=dev).manual_seed(500 + s_)
-        mask = 0x77 if bits == 3 else 0xFF  # every code valid at its width
-        kc = torch.randint(0, 256, (B, Hkv, cold, rb), generator=g, device=dev, dtype=torch.uint8) & mask
-        vc = torch.randint(0, 256, (B, Hkv, cold, rb), generator=g, device=dev, dtype=torch.uint8) & mask
+        # 3-bit codes, two per byte (64 bytes per token), every code valid
+        kc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8) & 0x77
+        vc = torch.randint(0, 256, (B, Hkv, cold, 64), generator=g, device=dev, dtype=torch.uint8) & 0x77
         kn = torch.rand(B, Hkv, cold, generator=g, device=dev) * 4 + 8
         vn = torch.rand(B, Hkv, cold, generator=g, device=dev) * 4 + 8
         kh = torch.randn(B, Hkv, hot, D, generator=g, device=dev).half()
