@@ -297,18 +297,23 @@ def test_engine_refuses_steps_past_max_len(cuda):
     assert int(eng.pos64) == PROMPT + 2
 
 
-@pytest.mark.parametrize("heads", [(4, 2), (8, 1)], ids=["G2", "G8"])
-def test_own_dense_engine_matches_hf_and_oracle(cuda, heads):
+@pytest.mark.parametrize("over", [dict(num_attention_heads=4, num_key_value_heads=2),
+                                  dict(num_attention_heads=8, num_key_value_heads=1),
+                                  dict(num_attention_heads=20, num_key_value_heads=5, hidden_size=2560,
+                                       intermediate_size=2560)], ids=["G2", "G8", "G4-10chunks"])
+def test_own_dense_engine_matches_hf_and_oracle(cuda, over):
     """The dense baseline on this library's kernels (every threshold 0, fp16 paged KV) vs HF's own fp16
     forward with a DynamicCache and vs the CPU oracle without compression, teacher-forced logits.  G2:
     the split kernel sums the projection partials and appends the token itself (the splits of 128
     tokens put the new token in the first, then the second split); G8 (more than 4 query heads per kv
-    head): the epilogue kernel and the general paged attention."""
+    head): the epilogue kernel and the general paged attention; G4-10chunks: hidden 2560 gives the
+    q|k|v GEMV 10 row chunks of 256, more than the split prologue's 8 preloaded partials, so its
+    general partial-sum path runs."""
     from transformers import DynamicCache
 
     from leankv_amd.engine import OwnDenseEngine, random_mistral
 
-    cfg = dict(TINY, num_attention_heads=heads[0], num_key_value_heads=heads[1])
+    cfg = dict(TINY, **over)
     model = random_mistral(device=cuda, seed=9, **cfg)
     state = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
     ref = RefModel(state, model.config, None, hot=1 << 20)
