@@ -169,7 +169,7 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
     float xin[BZ / NT];
     float sums[NL];
     if constexpr (DENSE) {
-      gemv_u32x4 w0[U];
+      gemv_u32x4 w0[U * kDensePf];
       input_prologue<NT, BZ, MODE, true>(G, z0, xin, sm.wsum, [&] {
         gemv_dense_first<NT, U, CP>(seg_pick(G.A, seg), seg_pick(G.a_bytes, seg), N, z0, G.Z, n0, w0);
       });
