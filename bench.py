@@ -6,7 +6,8 @@
 Workloads:
   decode  config 5 (default): random-init fp16 Mistral-7B-v0.3-shaped decoder, 4096-token
           random prompt, per-projection TEAL sparsity ~U[0.3,0.5] (thresholds from a seeded
-          calibration pass), 3-bit TurboQuant KV (64-token fp16 window), greedy B=1 decode of
+          calibration pass at the decode context: quantiles over the last 256 positions of a
+          4096-token prompt), 3-bit TurboQuant KV (64-token fp16 window), greedy B=1 decode of
           warmup+steps = 128 tokens through the graph-captured LeanKV engine.  Beside it on the
           same prompt: two dense fp16 baselines with an fp16 KV cache, both graph-captured --
           the same fused step on this library's kernels with every threshold 0 (own_kernels;
@@ -990,7 +991,9 @@ def bench_decode(args, torch):
     _log("model built in %.1fs" % (time.perf_counter() - t0))
     g = torch.Generator().manual_seed(1)
     prompt = torch.randint(0, cfg.vocab_size, (1, args.prompt), generator=g).to(dev)
-    calib = [torch.randint(0, cfg.vocab_size, (1, 512), generator=g)]
+    # TEAL calibration at the decode's context: a prompt as long as the timed one, quantiles over its last
+    # 256 positions (where the timed steps' statistics are), so the sparsity decoded is the configured one
+    calib = [torch.randint(0, cfg.vocab_size, (1, args.prompt), generator=g)]
     new_tokens = args.warmup + args.steps
     max_len = args.prompt + new_tokens + 2
     L, Hkv, hid, ffn, voc = (cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.hidden_size,
@@ -1059,7 +1062,8 @@ def bench_decode(args, torch):
     # ---- LeanKV: TEAL thresholds from a calibration pass, HIP kernels, TurboQuant KV
     t0 = time.perf_counter()
     with torch.no_grad():
-        th = calibrate_thresholds(model, calib, uniform_random_sparsity(0.3, 0.5, seed=0))
+        th = calibrate_thresholds(model, calib, uniform_random_sparsity(0.3, 0.5, seed=0),
+                                  positions=slice(-min(256, args.prompt), None))
     apply_teal(model, thresholds=th, use_triton=True)
 
     def tq_cache():

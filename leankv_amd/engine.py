@@ -32,6 +32,8 @@ import torch.nn.functional as F
 from . import _lib
 from .turboquant.cache import TurboQuantCache
 
+STEP_BITS = (3, 4)  # code widths the fused B = 1 decode step (lkv_decode_*) is built for
+
 
 def _rms(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     """HF MistralRMSNorm: fp32 variance, normalise, cast back, scale (modeling_mistral.py:190-197)."""
@@ -363,6 +365,10 @@ class GenerateFastPath:
         self.engine = None
         self._cache = None  # the cache the B = 1 engine was built on
         self.batched = None  # BatchedEngine for B > 1 calls
+        self._engine_key = None   # (cache, its storage generation, length bound) the engines were built for
+        self._batched_key = None
+        self._model_why = False   # not asked yet; then None (the engines can run the model) or the reason
+        self._step_why = {}       # cache geometry -> None or why lkv_decode_* refuses it
         self.steps = {"engine": 0, "batch": 0, "forward": 0}
 
     def _eligible(self, input_ids, cache, kw) -> str | None:
@@ -378,7 +384,9 @@ class GenerateFastPath:
         B = input_ids.shape[0]
         if cache.head_dim != 128 or cache._k_codes[0] is None or cache._k_codes[0].shape[0] != B:
             return None
-        if B == 1 and (cache.bits not in (3, 4) or cache.hot_buffer_size > 64):
+        if self._model_reason() is not None:
+            return None
+        if B == 1 and self._step_reason(cache) is not None:
             return None
         n = cache._seq_lengths[0]
         if n == 0 or any(x != n for x in cache._seq_lengths) or any(cache._fused_pending) or \
@@ -394,22 +402,81 @@ class GenerateFastPath:
             return None
         return "one" if B == 1 else "batch"
 
+    def _model_reason(self) -> str | None:
+        """Why neither engine can run this model (None if both can): the fused kernels read fp16 weights,
+        norms and embeddings through raw pointers and have no projection bias, so a model in another dtype or
+        with a bias stays on its own forward (which raises or runs as it would without this wrapper)."""
+        if self._model_why is not False:
+            return self._model_why
+        why = None
+        m = self.model
+        cfg = m.config
+        D = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        if D != 128:
+            why = "head_dim %d (the kernels take 128)" % D
+        tensors = [("embed_tokens", m.model.embed_tokens.weight), ("norm", m.model.norm.weight),
+                   ("lm_head", m.lm_head.weight)]
+        for i, layer in enumerate(m.model.layers):
+            tensors += [("layers.%d.input_layernorm" % i, layer.input_layernorm.weight),
+                        ("layers.%d.post_attention_layernorm" % i, layer.post_attention_layernorm.weight)]
+            for name, mod in (("q_proj", layer.self_attn.q_proj), ("k_proj", layer.self_attn.k_proj),
+                              ("v_proj", layer.self_attn.v_proj), ("o_proj", layer.self_attn.o_proj),
+                              ("gate_proj", layer.mlp.gate_proj), ("up_proj", layer.mlp.up_proj),
+                              ("down_proj", layer.mlp.down_proj)):
+                tensors.append(("layers.%d.%s" % (i, name), mod.weight))
+                if why is None and getattr(mod, "bias", None) is not None:
+                    why = "layers.%d.%s has a bias" % (i, name)
+        for name, t in tensors:
+            if why is None and t.dtype != torch.float16:
+                why = "%s is %s (the fused kernels read fp16)" % (name, t.dtype)
+        self._model_why = why
+        return why
+
+    def _step_reason(self, cache: TurboQuantCache) -> str | None:
+        """Why the fused B = 1 step (lkv_decode_*) cannot run this model on this cache (None if it can): the
+        library's own shape check on the step's dimensions, asked once per cache geometry."""
+        key = (cache.bits, cache.hot_buffer_size, cache.cold_capacity(0))
+        if key in self._step_why:
+            return self._step_why[key]
+        cfg = self.model.config
+        why = None
+        if cache.bits not in STEP_BITS:
+            why = "bits=%d (the fused step takes %s)" % (cache.bits, STEP_BITS)
+        else:
+            # validation only: check_dims tests the pointers for null and alignment, never dereferences them
+            fake = 256
+            dims = _lib.DecodeDims(
+                hidden=cfg.hidden_size, ffn=cfg.intermediate_size, vocab=cfg.vocab_size,
+                n_heads=cfg.num_attention_heads, n_kv_heads=cfg.num_key_value_heads,
+                max_len=cache.attn_max_len(0), cap=cache.cold_capacity(0), hot_cap=cache.hot_buffer_size,
+                bits=cache.bits, eps=float(cfg.rms_norm_eps), scale=1.0 / math.sqrt(128.0),
+                bounds=fake, centroids=fake, rope_cos=fake, rope_sin=fake)
+            if _lib.load().lkv_decode_workspace_bytes(ctypes.byref(dims)) == 0:
+                why = _lib.last_error()
+        self._step_why[key] = why
+        return why
+
     def _engine_for(self, cache: TurboQuantCache) -> "LeanKVEngine":
-        # the engine holds the cache's buffers: a store that grew (update() reallocates it) needs a new one
-        if self.engine is not None and self._cache is cache and self.engine.max_len == cache.attn_max_len(0):
+        # the engine holds raw pointers to the cache's buffers (and its graph captured them): buffers that
+        # were replaced since -- a store that grew, a reset() followed by a new prefill -- need a new engine
+        key = (id(cache), cache.storage_generation, cache.attn_max_len(0))
+        if self.engine is not None and self._cache is cache and self._engine_key == key:
             return self.engine
         self.engine = None
         torch.cuda.empty_cache()
         self.engine = LeanKVEngine(self.model, cache, cache.attn_max_len(0))
         self._cache = cache
+        self._engine_key = key
         return self.engine
 
     def _batched_for(self, cache: TurboQuantCache, B: int) -> BatchedEngine:
+        key = (id(cache), cache.storage_generation, cache.attn_max_len(0), B)
         be = self.batched
-        if be is None or be.cache is not cache or be.B != B or be.max_len != cache.attn_max_len(0):
+        if be is None or be.cache is not cache or self._batched_key != key:
             self.batched = None
             torch.cuda.empty_cache()
             self.batched = BatchedEngine(self.model, cache, B)
+            self._batched_key = key
         return self.batched
 
     def __call__(self, input_ids=None, *args, **kw):

@@ -38,8 +38,15 @@ def uniform_random_sparsity(lo: float = 0.3, hi: float = 0.5, seed: int = 0) -> 
 
 
 @torch.no_grad()
-def calibrate_thresholds(model, samples: list, sparsity: SparsitySpec) -> dict:
-    """Run `samples` (token id tensors [1, S]) through `model`; return {layer: {proj: t}}."""
+def calibrate_thresholds(model, samples: list, sparsity: SparsitySpec, positions: slice | None = None) -> dict:
+    """Run `samples` (token id tensors [1, S]) through `model`; return {layer: {proj: t}}.
+
+    By default every position of every sample feeds the quantile, as the reference's calibration_data path
+    does (patching.py:241-256).  ``positions`` keeps only those sequence positions of each sample (e.g.
+    ``slice(-256, None)``: the last 256 tokens of a long prompt), so thresholds can be taken at the context a
+    decode runs at: a projection's input statistics move with the context (an attention output averages
+    over more values at a longer context and shrinks), and a threshold from short-context positions then
+    drops more of the decode's inputs than its target sparsity asks."""
     layers = _get_layers(model)
     acts: dict = {}
     handles = []
@@ -48,7 +55,10 @@ def calibrate_thresholds(model, samples: list, sparsity: SparsitySpec) -> dict:
             mod = _get_projection(layer, pn)
 
             def hook(module, args, key=(li, pn)):
-                acts.setdefault(key, []).append(args[0].detach().reshape(-1, args[0].shape[-1]))
+                a = args[0].detach()
+                if positions is not None:
+                    a = a[..., positions, :]  # [B, S, D] -> the kept sequence positions
+                acts.setdefault(key, []).append(a.reshape(-1, a.shape[-1]))
 
             handles.append(mod.register_forward_pre_hook(hook))
     try:

@@ -93,6 +93,9 @@ class TurboQuantCache:
         self._fused_pending = [False] * num_layers   # a one-token update awaits decode_attention
         self._prefill_pending = [False] * num_layers  # a several-token update awaits prefill_attention
         self._pending_len = [0] * num_layers
+        # bumped whenever a layer's device buffers are replaced (first allocation, growth, reset): decode
+        # engines that hold raw pointers to them compare it to know when they must be rebuilt
+        self.storage_generation = 0
 
     # ----------------------------------------------------------- storage
     def _alloc(self, layer: int, B: int, H: int, cap: int) -> None:
@@ -105,6 +108,7 @@ class TurboQuantCache:
         self._v_hot[layer] = torch.zeros_like(self._k_hot[layer])
         self._pos_dev[layer] = torch.zeros(1, dtype=torch.int32, device=dev)
         self._len_dev[layer] = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.storage_generation += 1
 
     def _ensure_cap(self, layer: int, cold_needed: int) -> None:
         cur = self._k_codes[layer].shape[2]
@@ -121,6 +125,7 @@ class TurboQuantCache:
             t = torch.zeros(shape, dtype=old.dtype, device=old.device)
             t[:, :, :cur] = old
             lst[layer] = t
+        self.storage_generation += 1
 
     def _cold_len(self, n: int) -> int:
         return max(0, n - self.hot_buffer_size)
@@ -175,19 +180,22 @@ class TurboQuantCache:
         return self._get_full_cache(layer_idx)
 
     def _bulk_update(self, li: int, k16: torch.Tensor, v16: torch.Tensor, p0: int) -> None:
-        """Append S > 1 tokens: quantize every token that leaves the hot window, refill the ring."""
+        """Append S > 1 tokens: quantize every token that leaves the hot window, refill the ring.
+
+        One gather of the ring slots that leave it and one scatter of the new window per layer (slot
+        indices made on the device, no per-slot copies)."""
         hot = self.hot_buffer_size
+        dev = self._device
         S = k16.shape[2]
         T = p0 + S
         c0, c1 = self._cold_len(p0), self._cold_len(T)
         if c1 > c0:
             # tokens [c0, c1) in position order: some still in the ring, the rest new
-            ks, vs = [], []
-            for p in range(c0, min(c1, p0)):
-                ks.append(self._k_hot[li][:, :, p % hot])
-                vs.append(self._v_hot[li][:, :, p % hot])
-            fk = torch.stack(ks, dim=2) if ks else None
-            fv = torch.stack(vs, dim=2) if vs else None
+            fk = fv = None
+            if min(c1, p0) > c0:
+                slots = torch.arange(c0, min(c1, p0), device=dev) % hot
+                fk = self._k_hot[li].index_select(2, slots)
+                fv = self._v_hot[li].index_select(2, slots)
             if c1 > p0:
                 nk, nv = k16[:, :, : c1 - p0], v16[:, :, : c1 - p0]
                 fk = nk if fk is None else torch.cat([fk, nk], dim=2)
@@ -200,17 +208,17 @@ class TurboQuantCache:
             self._v_codes[li][:, :, c0:c1] = pv
             self._k_norms[li][:, :, c0:c1] = nk_
             self._v_norms[li][:, :, c0:c1] = nv_
-        for p in range(max(p0, T - hot), T):
-            self._k_hot[li][:, :, p % hot] = k16[:, :, p - p0]
-            self._v_hot[li][:, :, p % hot] = v16[:, :, p - p0]
+        first = max(p0, T - hot)  # the newest min(S, hot) tokens enter the ring, each in slot p % hot
+        slots = torch.arange(first, T, device=dev) % hot
+        self._k_hot[li].index_copy_(2, slots, k16[:, :, first - p0:])
+        self._v_hot[li].index_copy_(2, slots, v16[:, :, first - p0:])
 
     def _get_full_cache(self, layer_idx: int):
         """cat(dequantize(cold).fp16, hot) in position order (cache.py:169-189)."""
         n = self._seq_lengths[layer_idx]
         c = self._cold_len(n)
         hot = self.hot_buffer_size
-        order = [p % hot for p in range(c, n)]
-        idx = torch.tensor(order, dtype=torch.long, device=self._device)
+        idx = torch.arange(c, n, device=self._device) % hot  # ring slots in position order
         hk = self._k_hot[layer_idx].index_select(2, idx)
         hv = self._v_hot[layer_idx].index_select(2, idx)
         if c == 0:
@@ -308,6 +316,7 @@ class TurboQuantCache:
         self._fused_pending = [False] * self.num_layers
         self._prefill_pending = [False] * self.num_layers
         self._seen_tokens = 0
+        self.storage_generation += 1
 
     @property
     def seen_tokens(self):

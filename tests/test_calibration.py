@@ -118,3 +118,22 @@ def test_histograms_save_load_and_thresholds_roundtrip(tmp_path):
     assert go.load_thresholds(path) == th
     fns = apply_teal(model, thresholds_path=path)  # the reference's thresholds file layout is accepted
     assert len(fns) == 2 * len(PROJ_NAMES)
+
+
+def test_calibrate_thresholds_positions_select_the_sequence_tail():
+    """calibrate_thresholds(positions=slice(-8, None)) takes each projection's quantile over the last 8
+    positions only.  Layer 0's q/k/v/gate... inputs of a position depend on that token alone before the first
+    attention (q/k/v: RMSNorm of the embedding), so its q_proj threshold equals the one calibrated on the last 8
+    tokens by themselves; its o_proj input (the attention output) depends on the whole context, so that one
+    differs.  Slicing the wrong axis or end fails the first equality."""
+    from leankv_amd.engine import random_mistral
+    from leankv_amd.teal.calibrate import calibrate_thresholds
+
+    tiny = dict(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                num_attention_heads=4, num_key_value_heads=2, head_dim=128)
+    m = random_mistral(device="cpu", seed=5, **tiny)
+    ids = torch.randint(0, 512, (1, 40), generator=torch.Generator().manual_seed(6))
+    tail = calibrate_thresholds(m, [ids], 0.4, positions=slice(-8, None))
+    alone = calibrate_thresholds(m, [ids[:, -8:]], 0.4)
+    assert tail[0]["q_proj"] == alone[0]["q_proj"]
+    assert tail[0]["o_proj"] != alone[0]["o_proj"]

@@ -70,3 +70,84 @@ def test_multi_row_projection_dispatch_rule():
     assert not _skinny_dense(9, 14336, 4096) and not _skinny_dense(16, 4096, 4096)
     assert _skinny_dense(16, 4096, 14336) and not _skinny_dense(17, 4096, 14336)
     assert not _skinny_dense(4096, 4096, 4096)
+
+
+def _fast_path_on(m, bits=3, hot=64, n=10, B=1):
+    """A TEAL-patched model behind GenerateFastPath and a fused cache whose host state says n tokens are held."""
+    from leankv_amd.engine import enable_generate_fast_path
+    from leankv_amd.teal.patching import PROJ_NAMES, apply_teal
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    L = m.config.num_hidden_layers
+    apply_teal(m, thresholds={li: {p: 0.1 for p in PROJ_NAMES} for li in range(L)}, use_triton=True)
+    fp = enable_generate_fast_path(m)
+    cache = TurboQuantCache(bits=bits, num_layers=L, hot_buffer_size=hot, device="cpu", max_seq_len=256,
+                            fused_attention=True)
+    for li in range(L):
+        cache._alloc(li, B, m.config.num_key_value_heads, 256)
+        cache._seq_lengths[li] = n
+    return fp, cache
+
+
+def test_generate_fast_path_eligibility_follows_the_step_checks():
+    """The fast path takes a single-token call only where the fused kernels accept the model: fp16 tensors,
+    no projection bias and the dimensions lkv_decode_* accept (asked of the library itself); anything else
+    falls back to the model's own forward instead of failing mid-decode or reading bf16 as fp16."""
+    from leankv_amd.engine import random_mistral
+
+    ids = torch.zeros(1, 1, dtype=torch.long)
+    fp, cache = _fast_path_on(random_mistral(device="cpu", seed=3, **TINY))
+    assert fp._eligible(ids, cache, {}) == "one"
+    fp2, cache2 = _fast_path_on(random_mistral(device="cpu", seed=3, **TINY), B=2)
+    assert fp2._eligible(torch.zeros(2, 1, dtype=torch.long), cache2, {}) == "batch"
+
+    # bf16 weights: neither engine (raw fp16 pointers), at B = 1 or B > 1
+    m = random_mistral(device="cpu", seed=3, **TINY).to(torch.bfloat16)
+    fp, cache = _fast_path_on(m)
+    assert fp._eligible(ids, cache, {}) is None and "bfloat16" in fp._model_reason()
+    fp, cache = _fast_path_on(random_mistral(device="cpu", seed=3, **TINY).to(torch.bfloat16), B=2)
+    assert fp._eligible(torch.zeros(2, 1, dtype=torch.long), cache, {}) is None
+
+    # a vocabulary the step's lm_head GEMV does not tile (Mistral fine-tunes with 32002 tokens)
+    fp, cache = _fast_path_on(random_mistral(device="cpu", seed=3, **dict(TINY, vocab_size=514)))
+    assert fp._model_reason() is None
+    assert fp._eligible(ids, cache, {}) is None and "vocab" in fp._step_reason(cache)
+
+    # more query heads per kv head than the step holds
+    fp, cache = _fast_path_on(random_mistral(device="cpu", seed=3, **dict(
+        TINY, hidden_size=2048, num_attention_heads=16, num_key_value_heads=1)))
+    assert fp._eligible(ids, cache, {}) is None and "n_heads" in fp._step_reason(cache)
+
+    # a window wider than the step's ring, and code widths the step is not built for
+    fp, cache = _fast_path_on(random_mistral(device="cpu", seed=3, **TINY), hot=128, n=10)
+    assert fp._eligible(ids, cache, {}) is None and "hot_cap" in fp._step_reason(cache)
+
+
+def test_generate_fast_path_refuses_projection_bias():
+    from leankv_amd.engine import random_mistral
+
+    m = random_mistral(device="cpu", seed=4, **TINY)
+    lin = m.model.layers[1].self_attn.o_proj
+    lin.bias = torch.nn.Parameter(torch.zeros(lin.out_features, dtype=torch.float16))
+    fp, cache = _fast_path_on(m)
+    assert fp._eligible(torch.zeros(1, 1, dtype=torch.long), cache, {}) is None
+    assert "bias" in fp._model_reason()
+
+
+def test_cache_storage_generation_moves_with_its_buffers():
+    """Decode engines hold raw pointers to a cache's buffers; the cache's storage generation changes exactly
+    when those buffers are replaced (allocation, growth, reset), and the fast path keys its engines on it."""
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    c = TurboQuantCache(bits=3, num_layers=2, device="cpu", max_seq_len=8)
+    g0 = c.storage_generation
+    c._alloc(0, 1, 2, 8)
+    g1 = c.storage_generation
+    assert g1 > g0
+    c._ensure_cap(0, 8)  # fits: nothing replaced
+    assert c.storage_generation == g1
+    c._ensure_cap(0, 9)  # grows: codes and norms replaced
+    assert c.storage_generation > g1 and c.cold_capacity(0) == 16
+    g2 = c.storage_generation
+    c.reset()
+    assert c.storage_generation > g2 and c._k_codes[0] is None

@@ -78,11 +78,12 @@ def test_generate_optimize_model_matches_reference(cuda):
 
 
 def test_generate_with_teal_runs_the_validated_forward(cuda):
-    """optimize_model(teal_thresholds_path=..., turboquant_bits=3) + generate: each step's scores equal, bit for
-    bit, a teacher-forced forward of the same model on a fresh cache -- generate adds nothing to the forward path
-    whose fused q|k|v, fused gate/up and single projections are checked against the oracle one by one
-    (test_gpu_engine.py, test_gpu_config5.py).  Model-level TEAL logits are not compared with the oracle: an
-    activation within an ulp of its threshold flips a mask bit under any other rounding of the RMSNorm."""
+    """optimize_model(teal_thresholds_path=..., turboquant_bits=3, fast_decode=False) + generate: each step's
+    scores equal, bit for bit, a teacher-forced forward of the same model on a fresh cache -- generate adds
+    nothing to the forward path whose fused q|k|v, fused gate/up and single projections are checked against the
+    oracle one by one (test_gpu_engine.py, test_gpu_config5.py).  Model-level TEAL logits are not compared
+    with the oracle: an activation within an ulp of its threshold flips a mask bit under any other rounding of
+    the RMSNorm.  (The generate fast path is compared with this forward in the fast-path tests below.)"""
     import json
     import tempfile
 
@@ -94,7 +95,11 @@ def test_generate_with_teal_runs_the_validated_forward(cuda):
     th = calibrate_thresholds(model, [_ids(64, 41)], uniform_random_sparsity(0.3, 0.5, 40))
     with tempfile.NamedTemporaryFile("w", suffix=".json", delete=False) as f:
         json.dump({str(k): v for k, v in th.items()}, f)
-    model, cache = optimize_model(model, teal_thresholds_path=f.name, turboquant_bits=3, max_seq_len=256)
+    model, cache = optimize_model(model, teal_thresholds_path=f.name, turboquant_bits=3, max_seq_len=256,
+                                  fast_decode=False)
+    from leankv_amd.engine import GenerateFastPath
+
+    assert not isinstance(model.forward, GenerateFastPath)  # both sides below are the HF forward itself
     assert all(getattr(layer.self_attn, "_teal_qkv_fused", False) and getattr(layer.mlp, "_teal_fused", False)
                for layer in model.model.layers)
     prompt = _ids(100, 42)
@@ -244,10 +249,11 @@ def test_cache_widths_and_windows(cuda, bits, hot, fused):
     assert max(errs) < RTOL, errs
 
 
-def _teal_pair(cuda, seed, bits=3, hot=64, **kw):
+def _teal_pair(cuda, seed, bits=3, hot=64, hip_rmsnorm=True, **kw):
     """One random TINY model, TEAL thresholds from a calibration pass, and two optimize_model copies of it
-    (TEAL + TurboQuant): `fast` with the generate fast path, `slow` without.  Both run their RMSNorm
-    modules through lkv_rmsnorm, the arithmetic of the fused step's prologue, so TEAL masks agree."""
+    (TEAL + TurboQuant): `fast` with the generate fast path, `slow` without.  With hip_rmsnorm both run their
+    RMSNorm modules through lkv_rmsnorm, the arithmetic of the fused step's prologue, so TEAL masks agree;
+    without it the models keep HF's torch RMSNorm (the default configuration)."""
     import json
     import tempfile
 
@@ -262,7 +268,7 @@ def _teal_pair(cuda, seed, bits=3, hot=64, **kw):
     out = []
     for m, fd in ((fast, True), (slow, False)):
         for mod in m.modules():
-            if type(mod).__name__.endswith("RMSNorm"):
+            if hip_rmsnorm and type(mod).__name__.endswith("RMSNorm"):
                 mod.forward = (lambda x, mod=mod: rms_norm(x, mod.weight, mod.variance_epsilon))
         m, c = optimize_model(m, teal_thresholds_path=f.name, turboquant_bits=bits, max_seq_len=256,
                               fast_decode=fd)
@@ -348,6 +354,56 @@ def test_generate_fast_path_batch(cuda, bits, hot):
     before = dict(fast.forward.steps)
     _generate(fast, ids.to(cuda), c2, 4, attention_mask=mask.to(cuda))
     assert fast.forward.steps["batch"] == before["batch"]
+
+
+def test_generate_fast_path_default_rmsnorm(cuda):
+    """The default configuration: optimize_model's fast path on a model that keeps HF's torch RMSNorm, vs the
+    patched HF forward (torch RMSNorm too) teacher-forced on the fast path's tokens.  The fused step's RMSNorm
+    prologue sums in another order, so an activation that sits on its TEAL threshold can fall on the other
+    side and move that projection by a few percent: per-step logits agree within 2e-2 and the greedy tokens
+    agree on most steps (the rate is printed)."""
+    print("fast path case: torch RMSNorm", flush=True)
+    (fast, ca), (slow, cb) = _teal_pair(cuda, 64, hip_rmsnorm=False)
+    prompt = _ids(100, 65)
+    n = 24
+    res = _generate(fast, prompt.to(cuda), ca, n)
+    assert fast.forward.steps == {"engine": n - 1, "batch": 0, "forward": 1}, fast.forward.steps
+    new = res.sequences[0, 100:]
+    errs, agree = [], 0
+    with torch.no_grad():
+        slow(prompt.view(1, -1).to(cuda), past_key_values=cb, use_cache=True, logits_to_keep=1)
+        for i in range(n - 1):
+            lg = slow(new[i:i + 1].view(1, 1), past_key_values=cb, use_cache=True).logits[0, -1].float()
+            errs.append(float((res.scores[i + 1][0] - lg).norm() / lg.norm()))
+            agree += int(torch.argmax(lg)) == int(new[i + 1])
+    print("fast path (torch RMSNorm) vs HF forward: max step rel err %.2e, greedy agreement %d/%d"
+          % (max(errs), agree, n - 1))
+    assert max(errs) < RTOL, errs
+    assert agree >= (n - 1) * 3 // 4, (agree, n - 1)
+
+
+@pytest.mark.parametrize("B", [1, 4])
+def test_generate_fast_path_after_cache_reset(cuda, B):
+    """generate, then cache.reset() and a generate of another prompt of the same length on the same cache: the
+    reset replaces the cache's buffers, so the fast path must rebuild its engine (B = 1) or its captured batch
+    step (B = 4) on the new ones.  Tokens and scores equal the same generate on a fresh cache bit for bit."""
+    from leankv_amd.turboquant.cache import TurboQuantCache
+
+    print("reset case B=%d" % B, flush=True)
+    (fast, ca), _ = _teal_pair(cuda, 66)
+    fp = fast.forward
+    kind = "engine" if B == 1 else "batch"
+    _generate(fast, _ids(100, 67, B=B).to(cuda), ca, 8)
+    assert fp.steps[kind] == 7
+    p2 = _ids(100, 68, B=B)
+    ca.reset()
+    r_reset = _generate(fast, p2.to(cuda), ca, 8)
+    assert fp.steps[kind] == 14
+    fresh = TurboQuantCache(bits=3, head_dim=128, num_layers=2, device=cuda, max_seq_len=256, fused_attention=True)
+    r_fresh = _generate(fast, p2.to(cuda), fresh, 8)
+    assert torch.equal(r_reset.sequences, r_fresh.sequences)
+    for a, b in zip(r_reset.scores, r_fresh.scores):
+        assert torch.equal(a, b)
 
 
 def test_generate_fast_path_falls_back(cuda):

@@ -67,3 +67,64 @@ def test_noalloc_refuses_shapes_beyond_the_array(cuda):
     x = torch.zeros(16, dtype=torch.float16, device=cuda)
     rc = lib.lkv_sparse_gemv_noalloc(x.data_ptr(), x.data_ptr(), 0.1, N, Z, x.data_ptr(), _lib.stream_handle(cuda))
     assert rc == -1 and "scratch" in _lib.last_error()
+
+
+_CAPTURE_CHILD = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+import torch
+from leankv_amd import _lib
+
+lib = _lib.load()
+dev = torch.device("cuda:0")
+N, Z = 4096, 14336
+g = torch.Generator().manual_seed(3)
+W = (torch.randn(N, Z, generator=g) * 0.02).to(torch.float16).to(dev).t().contiguous().t()
+x = (torch.randn(Z, generator=g) * 0.05).to(torch.float16).to(dev)
+t = float(torch.kthvalue(x.float().abs().cpu(), int(0.4 * Z)).values)
+y_ws = torch.empty(N, dtype=torch.float16, device=dev)
+nbytes = lib.lkv_sparse_gemv_workspace_bytes(N, Z)
+ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+y_na = torch.zeros(N, dtype=torch.float16, device=dev)
+torch.cuda.synchronize()
+s = torch.cuda.Stream()
+s.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.stream(s):
+    with torch.cuda.graph(graph, stream=s):
+        # this process's first lkv_sparse_gemv_noalloc call, made while the stream is being captured
+        _lib.check(lib.lkv_sparse_gemv_noalloc(x.data_ptr(), W.data_ptr(), t, N, Z, y_na.data_ptr(),
+                                               _lib.stream_handle(dev)), "lkv_sparse_gemv_noalloc")
+torch.cuda.current_stream().wait_stream(s)
+_lib.check(lib.lkv_sparse_gemv(x.data_ptr(), W.data_ptr(), t, N, Z, y_ws.data_ptr(), ws.data_ptr(), nbytes,
+                               _lib.stream_handle(dev)), "lkv_sparse_gemv")
+torch.cuda.synchronize()
+want = y_ws.clone()
+for r in range(3):
+    y_na.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y_na.view(torch.int16), want.view(torch.int16)), "replay %d differs" % r
+    x.mul_(-1)  # eager work between replays; the graph reads x again, so the result flips sign exactly
+    _lib.check(lib.lkv_sparse_gemv(x.data_ptr(), W.data_ptr(), t, N, Z, y_ws.data_ptr(), ws.data_ptr(), nbytes,
+                                   _lib.stream_handle(dev)), "lkv_sparse_gemv")
+    torch.cuda.synchronize()
+    want = y_ws.clone()
+print("capture ok")
+"""
+
+
+def test_noalloc_first_call_inside_graph_capture(cuda):
+    """The entry point is for callers that cannot allocate, graph capture among them: a fresh process whose
+    first lkv_sparse_gemv_noalloc call is made inside torch.cuda.graph capture (so the scratch array's address
+    is looked up during the capture), the graph replayed three times with eager work between, each replay equal
+    bit for bit to lkv_sparse_gemv on the current input."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("noalloc capture case: child process, N=4096 Z=14336", flush=True)
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_CHILD, root], capture_output=True, text=True, timeout=150)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and "capture ok" in r.stdout
