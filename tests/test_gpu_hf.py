@@ -360,8 +360,9 @@ def test_generate_fast_path_default_rmsnorm(cuda):
     """The default configuration: optimize_model's fast path on a model that keeps HF's torch RMSNorm, vs the
     patched HF forward (torch RMSNorm too) teacher-forced on the fast path's tokens.  The fused step's RMSNorm
     prologue sums in another order, so an activation that sits on its TEAL threshold can fall on the other
-    side and move that projection by a few percent: per-step logits agree within 2e-2 and the greedy tokens
-    agree on most steps (the rate is printed)."""
+    side and move that projection by a few percent (one flip at a gate/up threshold moved a layer's MLP output
+    by 4.3 % at config 5), so per-step logits are held to 5e-2 rather than the 2e-2 of a fixed mask, and the
+    greedy tokens must agree on most steps (the error and the rate are printed; measured: 1.9e-2, 23 of 23)."""
     print("fast path case: torch RMSNorm", flush=True)
     (fast, ca), (slow, cb) = _teal_pair(cuda, 64, hip_rmsnorm=False)
     prompt = _ids(100, 65)
@@ -378,7 +379,7 @@ def test_generate_fast_path_default_rmsnorm(cuda):
             agree += int(torch.argmax(lg)) == int(new[i + 1])
     print("fast path (torch RMSNorm) vs HF forward: max step rel err %.2e, greedy agreement %d/%d"
           % (max(errs), agree, n - 1))
-    assert max(errs) < RTOL, errs
+    assert max(errs) < 5e-2, errs
     assert agree >= (n - 1) * 3 // 4, (agree, n - 1)
 
 
