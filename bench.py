@@ -75,7 +75,8 @@ def _parse():
     ap.add_argument("--sets", type=int, default=5, help="independent buffer sets rotated per step")
     ap.add_argument("--cold", type=int, default=4096, help="--workload attn: cold tokens per sequence (config 4: 4096)")
     ap.add_argument("--bits", type=int, default=3, choices=(1, 2, 3, 4),
-                    help="--workload attn: code width of the packed cache (config 4: 3)")
+                    help="--workload attn / decode: code width of the packed cache (configs 4 and 5: 3; the "
+                         "reference sweeps 2.5-4 bits, configs/mistral7b.yaml)")
     return ap.parse_args()
 
 
@@ -266,7 +267,7 @@ def roofline_gateup(args, torch):
     return r
 
 
-def cpu_decode(torch, model, thresholds, prompt_len, budget_s=20.0):
+def cpu_decode(torch, model, thresholds, prompt_len, budget_s=20.0, bits=3):
     """The reference's decode path on the host (oracle restatement, torch fp32), bounded sample.
 
     One decoder layer of the same random model with its TEAL thresholds and a TurboQuant cache
@@ -283,7 +284,7 @@ def cpu_decode(torch, model, thresholds, prompt_len, budget_s=20.0):
     cfg.num_hidden_layers = 1
     keep = ("model.embed_tokens.", "model.layers.0.", "model.norm.", "lm_head.")
     state = {k: v.detach().float().cpu() for k, v in model.state_dict().items() if k.startswith(keep)}
-    ref = RefModel(state, cfg, {0: thresholds[0]}, bits=3, acc_dtype=torch.float32)
+    ref = RefModel(state, cfg, {0: thresholds[0]}, bits=bits, acc_dtype=torch.float32)
     g = torch.Generator().manual_seed(0)
     Hkv, D = cfg.num_key_value_heads, 128
     ref.caches[0].update(torch.randn(1, Hkv, prompt_len, D, generator=g).half(),
@@ -299,10 +300,10 @@ def cpu_decode(torch, model, thresholds, prompt_len, budget_s=20.0):
     layer_s, head_s = ref.t_layers / n, ref.t_head / n
     L = model.config.num_hidden_layers
     return {"value": round(1.0 / (L * layer_s + head_s), 4), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": "%d decode steps of 1 of %d layers at context %d (TEAL thresholds, 3-bit TurboQuant cache "
+            "sample": "%d decode steps of 1 of %d layers at context %d (TEAL thresholds, %d-bit TurboQuant cache "
                       "re-dequantized every step as the reference does), oracle torch fp32 on %s; "
                       "per token = %d x %.1f ms/layer + %.1f ms embed/norm/lm_head"
-                      % (n, L, prompt_len, cpu, L, layer_s * 1e3, head_s * 1e3)}
+                      % (n, L, prompt_len, bits, cpu, L, layer_s * 1e3, head_s * 1e3)}
 
 
 def cpu_gemv(torch, s, N, Z):
@@ -1067,7 +1068,7 @@ def bench_decode(args, torch):
     apply_teal(model, thresholds=th, use_triton=True)
 
     def tq_cache():
-        return TurboQuantCache(bits=3, head_dim=128, num_layers=L, device=dev, max_seq_len=max_len,
+        return TurboQuantCache(bits=args.bits, head_dim=128, num_layers=L, device=dev, max_seq_len=max_len,
                                fused_attention=True)
 
     cache, cache_count = tq_cache(), tq_cache()
@@ -1102,7 +1103,7 @@ def bench_decode(args, torch):
     w_dense = L * sum(in_dim[p] * row_bytes[p] for p in row_bytes)
     ctx = args.prompt + args.warmup + (args.steps - 1) / 2  # mean context of the timed steps
     head = hid * voc * 2
-    lkv_bytes = w_sparse + head + _kv_bytes_per_token(L, Hkv, ctx, 64)
+    lkv_bytes = w_sparse + head + _kv_bytes_per_token(L, Hkv, ctx, 64, bits_row=16 * {1: 1, 2: 2}.get(args.bits, 4))
     dense_bytes = w_dense + head + L * Hkv * (ctx + 1) * 2 * 256
     sparsity = {p: round(1 - counts[p][0] / counts[p][1], 4) for p in row_bytes}
 
@@ -1118,7 +1119,7 @@ def bench_decode(args, torch):
     _log("HF generate, LeanKV with the fused decode step: %.1f tok/s (prefill included), calls %s"
          % (gen_lkv, gen_steps))
     res = {
-        "metric": "B=1 decode tok/s (Mistral-7B shape, 40% sparse, 3-bit KV)",
+        "metric": "B=1 decode tok/s (Mistral-7B shape, 40% sparse, %d-bit KV)" % args.bits,
         "value": round(tps, 2),
         "unit": "tok/s",
         "ms_per_step": round(ms, 4),
@@ -1127,7 +1128,7 @@ def bench_decode(args, torch):
         "data": "synthetic: random-init weights N(0,0.02), random 4096-token prompt (seeded)",
         "config": {"workload": "config5_mistral7b_decode", "layers": L, "hidden": hid, "ffn": ffn, "heads": "32/8",
                    "vocab": voc, "prompt": args.prompt, "new_tokens": new_tokens, "batch": 1,
-                   "teal_sparsity": "U[0.3,0.5] per projection, mean 0.4", "kv_bits": 3, "hot_window": 64},
+                   "teal_sparsity": "U[0.3,0.5] per projection, mean 0.4", "kv_bits": args.bits, "hot_window": 64},
         "step_roofline": {
             "what": "algorithmic HBM bytes of one timed decode step (weight rows above threshold, counted on the "
                     "timed tokens + packed KV + lm_head) / ms_per_step",
@@ -1162,7 +1163,7 @@ def bench_decode(args, torch):
         res["hf_generate"] = {"leankv_tok_s": gen_lkv, "leankv_hf_forward_tok_s": gen_lkv_hf,
                               "fast_path_calls": gen_steps}
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_decode(torch, model, th, args.prompt)
+        res["cpu_baseline"] = cpu_decode(torch, model, th, args.prompt, bits=args.bits)
     del model
     torch.cuda.empty_cache()
     return res

@@ -390,7 +390,7 @@ typedef struct lkv_decode_dims {
   int64_t max_len;       /* RoPE table rows; tokens the cache holds */
   int64_t cap;           /* cold rows per (layer, kv head) */
   int64_t hot_cap;       /* fp16 window, 1..64 */
-  int32_t bits;          /* 3 or 4 */
+  int32_t bits;          /* 1..4 (the packings of quantizer.py:38-62) */
   float eps;             /* RMSNorm epsilon */
   float scale;           /* attention scale */
   const float* bounds;   /* 2^bits - 1 decision boundaries (fp32) */

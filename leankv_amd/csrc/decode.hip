@@ -111,7 +111,7 @@ int check_dims(const lkv_decode_dims* d) {
   LKV_REQUIRE(d->cap >= d->max_len - d->hot_cap && d->cap < (1ll << 30),
               "decode: cap=%lld cannot hold max_len - hot_cap = %lld cold tokens", (long long)d->cap,
               (long long)(d->max_len - d->hot_cap));
-  LKV_REQUIRE(d->bits == 3 || d->bits == 4, "decode: bits=%d unsupported (3 or 4)", d->bits);
+  LKV_REQUIRE(d->bits >= 1 && d->bits <= 4, "decode: bits=%d unsupported (1..4)", d->bits);
   LKV_REQUIRE(d->bounds && d->centroids && d->rope_cos && d->rope_sin, "decode: null codebook or RoPE table");
   LKV_REQUIRE(aligned16(d->rope_cos) && aligned16(d->rope_sin), "decode: RoPE tables must be 16-byte aligned");
   const int64_t wmax = d->hidden * (d->ffn > d->vocab ? d->ffn : d->vocab);
@@ -482,10 +482,12 @@ extern "C" int lkv_decode_evict(const lkv_decode_dims* dims, const lkv_decode_la
                           L.PiK,                                 L.PiV};
     }
     const dim3 grid(static_cast<unsigned>((p.Hkv + 15) / 16), 2, static_cast<unsigned>(nl));
-    if (d.bits == 3)
-      hipLaunchKernelGGL((evict_kernel<3>), grid, dim3(kThreads), 0, st, A);
-    else
-      hipLaunchKernelGGL((evict_kernel<4>), grid, dim3(kThreads), 0, st, A);
+    switch (d.bits) {
+      case 1: hipLaunchKernelGGL((evict_kernel<1>), grid, dim3(kThreads), 0, st, A); break;
+      case 2: hipLaunchKernelGGL((evict_kernel<2>), grid, dim3(kThreads), 0, st, A); break;
+      case 3: hipLaunchKernelGGL((evict_kernel<3>), grid, dim3(kThreads), 0, st, A); break;
+      default: hipLaunchKernelGGL((evict_kernel<4>), grid, dim3(kThreads), 0, st, A);
+    }
     LKV_LAUNCH_CHECK("decode_evict");
   }
   return LKV_OK;

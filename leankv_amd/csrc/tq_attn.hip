@@ -366,7 +366,7 @@ constexpr int kMaxPg = 256;  // pages of one split in the paged layout
 template <bool PERM, bool DECODE, bool PAGED, int CB, int QPRE = 16>
 __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_kernel(AttnParams P) {
   static_assert(!(PAGED && DECODE), "the fused decode step uses the dense layout");
-  static_assert(CB == 4 || (PERM && !DECODE), "narrow code rows: v_perm decode, standalone calls");
+  static_assert(CB == 4 || PERM, "narrow code rows (1, 2 bits) decode through v_perm");
   constexpr int RB = code_row_bytes<CB>();
   __shared__ uint32_t s_lut[256];
   __shared__ int s_pg[PAGED ? kMaxPg : 1];
@@ -1041,14 +1041,32 @@ int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st) {
     P.k_hot = c.k_ring;
     P.v_hot = c.v_ring;
     // the fewest partial loads ahead of the codes that still cover every chunk
-    if (c.bits == 3 && c.nchunk <= 8)
-      hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false, 4, 8>), grid, dim3(kThreads), 0, st, P);
-    else if (c.bits == 3)
-      hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false, 4, 16>), grid, dim3(kThreads), 0, st, P);
-    else if (c.nchunk <= 8)
-      hipLaunchKernelGGL((tq_attn_split_kernel<false, true, false, 4, 8>), grid, dim3(kThreads), 0, st, P);
-    else
-      hipLaunchKernelGGL((tq_attn_split_kernel<false, true, false, 4, 16>), grid, dim3(kThreads), 0, st, P);
+    const bool pre8 = c.nchunk <= 8;
+    switch (c.bits) {
+      case 1:
+        if (pre8)
+          hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false, 1, 8>), grid, dim3(kThreads), 0, st, P);
+        else
+          hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false, 1, 16>), grid, dim3(kThreads), 0, st, P);
+        break;
+      case 2:
+        if (pre8)
+          hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false, 2, 8>), grid, dim3(kThreads), 0, st, P);
+        else
+          hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false, 2, 16>), grid, dim3(kThreads), 0, st, P);
+        break;
+      case 3:
+        if (pre8)
+          hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false, 4, 8>), grid, dim3(kThreads), 0, st, P);
+        else
+          hipLaunchKernelGGL((tq_attn_split_kernel<true, true, false, 4, 16>), grid, dim3(kThreads), 0, st, P);
+        break;
+      default:
+        if (pre8)
+          hipLaunchKernelGGL((tq_attn_split_kernel<false, true, false, 4, 8>), grid, dim3(kThreads), 0, st, P);
+        else
+          hipLaunchKernelGGL((tq_attn_split_kernel<false, true, false, 4, 16>), grid, dim3(kThreads), 0, st, P);
+    }
   } else if (c.indptr != nullptr) {
     switch (c.bits) {
       case 1: hipLaunchKernelGGL((tq_attn_split_kernel<true, false, true, 1>), grid, dim3(kThreads), 0, st, P); break;

@@ -207,7 +207,11 @@ def test_decode_workspace_layout():
     offs = [lay.part_q, lay.part_k, lay.part_v, lay.part_o, lay.part_gate, lay.part_up, lay.part_down, lay.part_lm,
             lay.q_rope, lay.attn_out]
     assert offs == sorted(offs) and offs[-1] + 4096 * 2 <= lay.total
-    assert lib.lkv_decode_workspace_layout(ctypes.byref(_mistral_dims(bits=2)), ctypes.byref(lay)) == -1
+    assert lib.lkv_decode_workspace_layout(ctypes.byref(_mistral_dims(bits=5)), ctypes.byref(lay)) == -1
+    for bits in (1, 2, 4):  # every packing of quantizer.py:38-62; the plan does not depend on the width
+        lay2 = _lib.DecodeLayout()
+        assert lib.lkv_decode_workspace_layout(ctypes.byref(_mistral_dims(bits=bits)), ctypes.byref(lay2)) == 0
+        assert lay2.total == lay.total
     assert lib.lkv_decode_workspace_layout(ctypes.byref(d), None) == -1
 
 
@@ -218,7 +222,8 @@ def test_decode_dims_validated_without_launch():
     ok = _mistral_dims()
     assert lib.lkv_decode_workspace_bytes(ctypes.byref(ok)) > 0
     for bad, msg in ((dict(hidden=4000), "hidden"), (dict(n_heads=36), "n_heads"), (dict(n_kv_heads=2), "n_heads"),
-                     (dict(bits=2), "bits"), (dict(hot_cap=65), "hot_cap"), (dict(cap=100), "cap"),
+                     (dict(bits=5), "bits"), (dict(bits=0), "bits"), (dict(hot_cap=65), "hot_cap"),
+                     (dict(cap=100), "cap"),
                      (dict(rope_cos=None), "RoPE"), (dict(vocab=32770), "vocab")):
         d = _mistral_dims(**bad)
         assert lib.lkv_decode_workspace_bytes(ctypes.byref(d)) == 0, bad

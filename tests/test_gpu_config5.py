@@ -58,15 +58,15 @@ def _prompt(model, seed, n=PROMPT):
     return torch.randint(0, model.config.vocab_size, (n,), generator=g)
 
 
-def _patch(model, th, maxlen=MAXLEN):
+def _patch(model, th, maxlen=MAXLEN, bits=3):
     from leankv_amd.teal.patching import apply_teal
     from leankv_amd.turboquant.attention import use_on
     from leankv_amd.turboquant.cache import TurboQuantCache
 
     if th is not None:
         apply_teal(model, thresholds=th, use_triton=True)
-    cache = TurboQuantCache(bits=3, head_dim=128, num_layers=model.config.num_hidden_layers, device=model.device,
-                            max_seq_len=maxlen, fused_attention=True)
+    cache = TurboQuantCache(bits=bits, head_dim=128, num_layers=model.config.num_hidden_layers,
+                            device=model.device, max_seq_len=maxlen, fused_attention=True)
     use_on(model, cache)
     return cache
 
@@ -121,23 +121,24 @@ def _w16(mod):
     return mod.weight.detach().cpu().numpy().astype(np.float16)
 
 
-@pytest.mark.parametrize("context", [1024, 4096])
-def test_config5_engine_layer_step_matches_oracle_teal_on(cuda, context):
+@pytest.mark.parametrize("context,bits", [(1024, 3), (4096, 3), (4096, 2), (1024, 1)])
+def test_config5_engine_layer_step_matches_oracle_teal_on(cuda, context, bits):
     """2 full-width layers, TEAL on: every fused launch of one engine layer step vs the oracle on its input, at
-    a 1024-token context and at the bench's 4096 (where the attention split runs its 16-split plan), with
+    a 1024-token context and at the bench's 4096 (where the attention split runs its 16-split plan), 3-bit
+    codes and the reference's 2- and 1-bit packings (configs/mistral7b.yaml sweeps bit widths), with
     thresholds calibrated at that context: every projection keeps a fraction of its inputs inside the band
     its configured sparsity sets."""
     from leankv_amd import _lib
     from leankv_amd.engine import LeanKVEngine
     from leankv_amd.kernels import rms_norm
 
-    print("config-5 layer step case: context %d" % context, flush=True)
+    print("config-5 layer step case: context %d, %d-bit codes" % (context, bits), flush=True)
     PROMPT = context
     maxlen = PROMPT + STEPS + 8
     model = _model(cuda, 2, seed=12)
     th = _thresholds(model, 12, PROMPT)
     prompt = _prompt(model, 12, PROMPT)
-    cache = _patch(model, th, maxlen)
+    cache = _patch(model, th, maxlen, bits)
     first = _prefill(model, cache, prompt)
     eng = LeanKVEngine(model, cache, maxlen)
     eng.start(first, PROMPT)
@@ -198,11 +199,11 @@ def test_config5_engine_layer_step_matches_oracle_teal_on(cuda, context):
     # 3. attention over the cache as the step left it: cold codes dequantized by the oracle + the hot ring
     L = PROMPT + 1
     cold = L - 64
-    c3, _ = oq.codebook_tensors(3)
+    cb, _ = oq.codebook_tensors(bits)
     Kc = oq.dequantize(cache._k_codes[0][:, :, :cold].cpu().numpy(), cache._k_norms[0][:, :, :cold].cpu(),
-                       oq.rotation_matrix(128, 42), c3, 3).half()
+                       oq.rotation_matrix(128, 42), cb, bits).half()
     Vc = oq.dequantize(cache._v_codes[0][:, :, :cold].cpu().numpy(), cache._v_norms[0][:, :, :cold].cpu(),
-                       oq.rotation_matrix(128, 43), c3, 3).half()
+                       oq.rotation_matrix(128, 43), cb, bits).half()
     order = [p % 64 for p in range(cold, L)]
     Kf = torch.cat([Kc, cache._k_hot[0][:, :, order].cpu()], dim=2)
     Vf = torch.cat([Vc, cache._v_hot[0][:, :, order].cpu()], dim=2)

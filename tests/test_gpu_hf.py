@@ -283,7 +283,7 @@ def _teal_pair(cuda, seed, bits=3, hot=64, hip_rmsnorm=True, **kw):
     return out[0], out[1]
 
 
-@pytest.mark.parametrize("bits,hot", [(3, 64), (4, 32)])
+@pytest.mark.parametrize("bits,hot", [(3, 64), (4, 32), (2, 64), (1, 64)])
 def test_generate_fast_path_matches_hf_forward(cuda, bits, hot):
     """optimize_model's generate fast path (single-token decode calls on the fused, graph-replayed decode step)
     vs the patched HF forward teacher-forced on the same tokens: per-step logits within 1e-3 (lm_head is the
@@ -408,23 +408,26 @@ def test_generate_fast_path_after_cache_reset(cuda, B):
 
 
 def test_generate_fast_path_falls_back(cuda):
-    """Calls the fused B = 1 step does not serve run the model's own forward: a 2-bit cache, a 128-token
-    window (B = 1)."""
+    """Calls the fused B = 1 step does not serve run the model's own forward: a 128-token window (the step's
+    ring holds at most 64) and an unfused cache (fused_attention=False, the reference's full K/V); a 2-bit
+    cache with the 64-token window runs on the step."""
+    from leankv_amd.turboquant.attention import use_on
     from leankv_amd.turboquant.cache import TurboQuantCache
 
     (fast, ca), _ = _teal_pair(cuda, 52)
     fp = fast.forward
-    c2 = TurboQuantCache(bits=2, head_dim=128, num_layers=2, device=cuda, max_seq_len=256, fused_attention=True)
-    from leankv_amd.turboquant.attention import use_on
-
-    use_on(fast, c2)
-    _generate(fast, _ids(70, 54).to(cuda), c2, 4)
-    assert fp.steps["engine"] == 0 and fp.engine is None
     c3 = TurboQuantCache(bits=3, head_dim=128, num_layers=2, hot_buffer_size=128, device=cuda, max_seq_len=256,
                          fused_attention=True)
     use_on(fast, c3)
     _generate(fast, _ids(70, 55).to(cuda), c3, 4)
     assert fp.steps["engine"] == 0 and fp.engine is None
+    c4 = TurboQuantCache(bits=3, head_dim=128, num_layers=2, device=cuda, max_seq_len=256)
+    _generate(fast, _ids(70, 56).to(cuda), c4, 4)
+    assert fp.steps["engine"] == 0 and fp.engine is None
+    c2 = TurboQuantCache(bits=2, head_dim=128, num_layers=2, device=cuda, max_seq_len=256, fused_attention=True)
+    use_on(fast, c2)
+    _generate(fast, _ids(70, 54).to(cuda), c2, 4)
+    assert fp.steps["engine"] == 3 and fp.engine.cache is c2
 
 
 @pytest.mark.parametrize("scaled_rope", [False, True])
