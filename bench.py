@@ -1119,7 +1119,7 @@ def bench_decode(args, torch):
     _log("HF generate, LeanKV with the fused decode step: %.1f tok/s (prefill included), calls %s"
          % (gen_lkv, gen_steps))
     res = {
-        "metric": "B=1 decode tok/s (Mistral-7B shape, 40% sparse, %d-bit KV)" % args.bits,
+        "metric": "B=1 decode tok/s (Mistral-7B shape, 40%% sparse, %d-bit KV)" % args.bits,
         "value": round(tps, 2),
         "unit": "tok/s",
         "ms_per_step": round(ms, 4),
