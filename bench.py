@@ -74,6 +74,10 @@ def _parse():
     ap.add_argument("--no-roofline", action="store_true", help="skip the config-1 GEMV roofline measurement")
     ap.add_argument("--sets", type=int, default=5, help="independent buffer sets rotated per step")
     ap.add_argument("--cold", type=int, default=4096, help="--workload attn: cold tokens per sequence (config 4: 4096)")
+    ap.add_argument("--phases", action="store_true",
+                    help="--workload attn / decode: add per-block phase times of the attention kernels; needs the "
+                         "instrumented build (python -m leankv_amd.build --stamps) loaded through "
+                         "LKV_LIBRARY=leankv_amd/libleankv_amd_stamps.so")
     ap.add_argument("--bits", type=int, default=3, choices=(1, 2, 3, 4),
                     help="--workload attn / decode: code width of the packed cache (configs 4 and 5: 3; the "
                          "reference sweeps 2.5-4 bits, configs/mistral7b.yaml)")
@@ -611,7 +615,8 @@ def bench_attn(args, torch):
     kmean, kmed = _kernel_time(launch, len(sets), args.steps, args.warmup, torch)
     alg = B * Hkv * (cold * (rb + rb + 4 + 4) + hot * D * 2 * 2) + 2 * B * Hq * D * 2
     achieved = alg / (kmean * 1e-3) / 1e9
-    return {
+    phases = _phases(torch, lambda: launch(0)) if args.phases else None
+    res = {
         "metric": "packed-KV decode attention HBM GB/s (B=16, 32/8 heads, 4096 cold + 64 hot)",
         "value": round(achieved, 1), "unit": "GB/s", "ms_per_step": round(wall, 5), "higher_is_better": True,
         "dtype": "%d-bit codes, fp16 MFMA scores/values, fp32 softmax" % bits,
@@ -624,6 +629,62 @@ def bench_attn(args, torch):
                      "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3),
                      "alg_bytes_per_launch": alg},
     }
+    if phases:
+        res["phases"] = phases
+    return res
+
+
+def _phases(torch, run):
+    """Per-block phase times (µs) of the attention kernels over one call of run(): the instrumented build's
+    split stamps (block start, token loop start, loop end, block end) and combine stamps (start, end) on the
+    100 MHz real-time clock; min / median / max over blocks, times relative to the first split block's start."""
+    import ctypes
+
+    from leankv_amd import _lib
+    lib = _lib.load()
+    if not hasattr(lib, "lkv_debug_stamps"):
+        raise SystemExit("--phases needs LKV_LIBRARY=leankv_amd/libleankv_amd_stamps.so "
+                         "(python -m leankv_amd.build --stamps)")
+    fn = lib.lkv_debug_stamps
+    fn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int]
+    n = 8 * 16384  # [block][8 stamps]
+    torch.cuda.synchronize()
+    for w in (0, 1):
+        assert fn(w, None, 0, 1) == 0, _lib.last_error()
+    run()
+    torch.cuda.synchronize()
+    buf = (ctypes.c_uint64 * n)()
+    out = {}
+    rows = {}
+    for w in (0, 1):
+        assert fn(w, ctypes.cast(buf, ctypes.c_void_p), n, 0) == 0, _lib.last_error()
+        rows[w] = [tuple(buf[8 * i: 8 * i + 8]) for i in range(n // 8) if buf[8 * i] and buf[8 * i + 3]]
+    split = rows[0]
+    t0 = min(r[0] for r in split)
+
+    def st(vals):
+        vals = sorted(v * 0.01 for v in vals)  # 100 MHz ticks -> µs
+        return {"min": round(vals[0], 2), "median": round(statistics.median(vals), 2), "max": round(vals[-1], 2)}
+    out["split_blocks"] = len(split)
+    out["split_start"] = st(r[0] - t0 for r in split)
+    out["split_prologue"] = st(r[1] - r[0] for r in split)
+    pro = [r for r in split if r[4] and r[5]]  # blocks with cold tokens: query ready, rotation done
+    if pro:
+        out["split_prologue_query_ready"] = st(r[4] - r[0] for r in pro)
+        out["split_prologue_rotation"] = st(r[5] - r[4] for r in pro)
+        out["split_prologue_after_rotation"] = st(r[1] - r[5] for r in pro)
+    out["split_token_loop"] = st(r[2] - r[1] for r in split)
+    out["split_merge_and_record"] = st(r[3] - r[2] for r in split)
+    out["split_end"] = st(r[3] - t0 for r in split)
+    comb = rows[1]
+    if comb:
+        out["combine_blocks"] = len(comb)
+        out["combine_start"] = st(r[0] - t0 for r in comb)
+        out["combine_duration"] = st(r[3] - r[0] for r in comb)
+        out["combine_end"] = st(r[3] - t0 for r in comb)
+    out["what"] = ("µs per block on the 100 MHz clock over one call (the last launch of each kernel), relative to "
+                   "the first split block's start; instrumented build (LKV_STAMPS)")
+    return out
 
 
 def bench_tq_paged(args, torch):
@@ -1085,6 +1146,8 @@ def bench_decode(args, torch):
     tps = args.steps / dt
     ms = dt * 1e3 / args.steps
     _log("leankv: %.1f tok/s" % tps)
+    # one more (untimed) step with the phase stamps: the last layer's attention launches
+    phases = _phases(torch, eng.step) if args.phases else None
     del eng, cache
     torch.cuda.empty_cache()
 
@@ -1162,6 +1225,8 @@ def bench_decode(args, torch):
     else:
         res["hf_generate"] = {"leankv_tok_s": gen_lkv, "leankv_hf_forward_tok_s": gen_lkv_hf,
                               "fast_path_calls": gen_steps}
+    if phases:
+        res["phases_last_layer_attention"] = phases
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_decode(torch, model, th, args.prompt, bits=args.bits)
     del model

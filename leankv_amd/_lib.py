@@ -125,7 +125,9 @@ def load(path: str | None = None) -> ctypes.CDLL:
     with _lock:
         if _lib is not None:
             return _lib
-        p = path or LIB_PATH
+        # LKV_LIBRARY: another build of the same sources (the phase-stamp build, `python -m leankv_amd.build
+        # --stamps`, used by bench.py --phases)
+        p = path or os.environ.get("LKV_LIBRARY") or LIB_PATH
         if not os.path.exists(p):
             raise ImportError(
                 "leankv_amd: %s is missing; build it with `python -m leankv_amd.build` "

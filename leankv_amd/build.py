@@ -46,15 +46,24 @@ def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source and link ``libleankv_amd.so``; returns its path."""
+STAMPS_LIB_PATH = os.path.join(PKG_DIR, "libleankv_amd_stamps.so")
+
+
+def build(verbose: bool = False, stamps: bool = False) -> str:
+    """Compile every HIP source and link ``libleankv_amd.so``; returns its path.
+
+    stamps=True builds ``libleankv_amd_stamps.so`` instead: the same sources with LKV_STAMPS defined, so the
+    attention kernels record per-block phase times (the 100 MHz real-time clock) that
+    ``lkv_debug_stamps`` copies out (bench.py --phases reads them); the product library never has them."""
     hipcc = _hipcc()
     srcs = sources()
+    flags = HIPCC_FLAGS + (["-DLKV_STAMPS"] if stamps else [])
+    lib_path = STAMPS_LIB_PATH if stamps else LIB_PATH
     tmp = tempfile.mkdtemp(prefix="lkv_build_")
     try:
         def compile_one(src: str) -> str:
             obj = os.path.join(tmp, os.path.basename(src) + ".o")
-            cmd = [hipcc, *HIPCC_FLAGS, "-c", src, "-o", obj]
+            cmd = [hipcc, *flags, "-c", src, "-o", obj]
             res = subprocess.run(cmd, capture_output=True, text=True)
             if res.returncode != 0:
                 raise RuntimeError("hipcc failed on %s:\n%s%s" % (src, res.stdout, res.stderr))
@@ -64,16 +73,16 @@ def build(verbose: bool = False) -> str:
 
         with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
             objs = list(ex.map(compile_one, srcs))
-        out_tmp = LIB_PATH + ".tmp"
+        out_tmp = lib_path + ".tmp"
         cmd = [hipcc, "--offload-arch=" + ARCH, "-shared", "-fPIC", *objs, "-o", out_tmp]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError("link failed:\n%s%s" % (res.stdout, res.stderr))
-        os.replace(out_tmp, LIB_PATH)
+        os.replace(out_tmp, lib_path)
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
-    return LIB_PATH
+    return lib_path
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, stamps="--stamps" in sys.argv))

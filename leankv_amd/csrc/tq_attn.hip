@@ -46,6 +46,35 @@
 namespace lkv {
 namespace {
 
+#ifdef LKV_STAMPS
+// Instrumented build only (build.py --stamps): per-block phase times on the
+// 100 MHz real-time clock, [block][8 stamps] for the split kernel (0 block
+// start, 1 token loop start, 2 token loop end, 3 block end; inside the
+// prologue 4 = query ready for the rotation, 5 = rotation done) and the
+// combine kernel (0 start, 3 end), block = linear id in the grid.  Thread 0
+// stores them.
+constexpr int kStampBlocks = 16384;
+constexpr int kStampSlots = 8;
+__device__ uint64_t g_split_stamps[kStampBlocks * kStampSlots];
+__device__ uint64_t g_comb_stamps[kStampBlocks * kStampSlots];
+__device__ __forceinline__ void stamp(uint64_t* arr, int i) {
+  if (threadIdx.x == 0) {
+    const unsigned id = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    if (id < kStampBlocks)
+      __builtin_nontemporal_store(__builtin_amdgcn_s_memrealtime(), arr + kStampSlots * id + i);
+  }
+}
+#define LKV_SPLIT_STAMP(i) stamp(g_split_stamps, i)
+#define LKV_COMB_STAMP(i) stamp(g_comb_stamps, i)
+#else
+#define LKV_SPLIT_STAMP(i) \
+  do {                     \
+  } while (0)
+#define LKV_COMB_STAMP(i) \
+  do {                    \
+  } while (0)
+#endif
+
 constexpr int kD = 128;
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
@@ -373,6 +402,7 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
   __shared__ __align__(16) float s_o[kWaves][16][kORow];  // all 16 heads: rows >= G are never read
 
+  LKV_SPLIT_STAMP(0);
   // wave index made wave-uniform (scalar) so block offsets become scalar soffsets
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -573,6 +603,7 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
         }
       }
       __syncthreads();
+      LKV_SPLIT_STAMP(4);
       u32x4 qb = u32x4{0u, 0u, 0u, 0u};
       if (h < G) {
         const float* q = &s_q[h][32 * wave + 8 * g];
@@ -582,6 +613,7 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
       }
       rotate_query_hilo_loaded(pik, qb, wave, lane, &s_o[0][0][0], kORow, f);
       __syncthreads();  // s_o is written again by the merge
+      LKV_SPLIT_STAMP(5);
     } else if (P.PiK != nullptr) {
       // q_rot on MFMA (rotate_query_hilo), overlapping the first block's
       // loads; s_o is free until the merge.
@@ -594,8 +626,10 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
         qb = h < G ? u32x4{u.x, u.y, u.z, u.w} : u32x4{0u, 0u, 0u, 0u};
       }
       fetch_first(ra, t0);
+      LKV_SPLIT_STAMP(4);
       rotate_query_hilo_loaded(pik, qb, wave, lane, &s_o[0][0][0], kORow, f);
       __syncthreads();  // s_o is written again by the merge
+      LKV_SPLIT_STAMP(5);
     } else {
       const float4* src = reinterpret_cast<const float4*>(
           P.qrot + (static_cast<size_t>(b) * P.Hq + kvh * G + min(h, G - 1)) * kD + 32 * g);
@@ -627,8 +661,12 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
       rec[tid] = -INFINITY;
       rec[G + tid] = 0.f;
     }
+    LKV_SPLIT_STAMP(1);
+    LKV_SPLIT_STAMP(2);
+    LKV_SPLIT_STAMP(3);
     return;
   }
+  LKV_SPLIT_STAMP(1);
 
   SoftmaxState S;
   S.m = -INFINITY;
@@ -651,6 +689,7 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
     attend<PERM>(rb, t1, t_end, qa, tab, s_lut, lane, S);
     t0 = t2;
   }
+  LKV_SPLIT_STAMP(2);
 
   // ---- merge the 4 waves of the block through LDS.  A wave that had no
   // block keeps m = -inf, l = 0, o = 0.
@@ -691,6 +730,7 @@ __global__ __launch_bounds__(kThreads, kSplitBlocksPerCU) void tq_attn_split_ker
       rec[G + hh] = ls;
     }
   }
+  LKV_SPLIT_STAMP(3);
 }
 
 
@@ -736,6 +776,7 @@ __global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnPa
   __shared__ __align__(16) float s_rot[kD];
   __shared__ float s_hv[kD];
 
+  LKV_COMB_STAMP(0);
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   // Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its
   // own L2.  The G query heads of one (batch, kv head) read the same hot window
@@ -900,6 +941,7 @@ __global__ __launch_bounds__(kCombThreads, 4) void tq_attn_combine_kernel(AttnPa
     r += s_hv[tid];
     P.out[(static_cast<size_t>(b) * P.Hq + hq) * kD + tid] = f2h(Lt > 0.f ? r / Lt : 0.f);
   }
+  LKV_COMB_STAMP(3);
 }
 
 constexpr int kSplitGran = kWaves * kBlk;  // tokens one pass of a block covers
@@ -1096,6 +1138,26 @@ int attn_launch(const AttnCall& c, const AttnPlan& pl, hipStream_t st) {
 }  // namespace lkv
 
 using namespace lkv;
+
+#ifdef LKV_STAMPS
+// Instrumented build only: copy the phase stamps of the last split (which = 0)
+// or combine (which = 1) launches to host memory, n <= 8 * 16384 words;
+// clear = 1 zeroes them instead.  Not declared in the public header.
+extern "C" int lkv_debug_stamps(int which, uint64_t* host, int64_t n, int clear) {
+  LKV_REQUIRE(n >= 0 && n <= kStampSlots * kStampBlocks && (clear || host), "debug_stamps: bad buffer");
+  hipError_t e;
+  if (clear) {
+    static uint64_t zeros[kStampSlots * kStampBlocks];
+    e = which ? hipMemcpyToSymbol(HIP_SYMBOL(g_comb_stamps), zeros, sizeof(zeros))
+              : hipMemcpyToSymbol(HIP_SYMBOL(g_split_stamps), zeros, sizeof(zeros));
+  } else {
+    e = which ? hipMemcpyFromSymbol(host, HIP_SYMBOL(g_comb_stamps), static_cast<size_t>(n) * 8)
+              : hipMemcpyFromSymbol(host, HIP_SYMBOL(g_split_stamps), static_cast<size_t>(n) * 8);
+  }
+  LKV_REQUIRE(e == hipSuccess, "debug_stamps: %s", hipGetErrorString(e));
+  return LKV_OK;
+}
+#endif
 
 extern "C" size_t lkv_tq_decode_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_len < 0) return kTicketBytes;
