@@ -368,6 +368,7 @@ class GenerateFastPath:
         self._engine_key = None   # (cache, its storage generation, length bound) the engines were built for
         self._batched_key = None
         self._model_why = False   # not asked yet; then None (the engines can run the model) or the reason
+        self._model_why_key = None  # the model state the answer was given for (_model_state)
         self._step_why = {}       # cache geometry -> None or why lkv_decode_* refuses it
         self.steps = {"engine": 0, "batch": 0, "forward": 0}
 
@@ -406,7 +407,8 @@ class GenerateFastPath:
         """Why neither engine can run this model (None if both can): the fused kernels read fp16 weights,
         norms and embeddings through raw pointers and have no projection bias, so a model in another dtype or
         with a bias stays on its own forward (which raises or runs as it would without this wrapper)."""
-        if self._model_why is not False:
+        state = self._model_state()
+        if self._model_why is not False and self._model_why_key == state:
             return self._model_why
         why = None
         m = self.model
@@ -430,7 +432,15 @@ class GenerateFastPath:
             if why is None and t.dtype != torch.float16:
                 why = "%s is %s (the fused kernels read fp16)" % (name, t.dtype)
         self._model_why = why
+        self._model_why_key = state
         return why
+
+    def _model_state(self) -> tuple:
+        """Identity of the tensors the engines hold raw pointers to, cheap enough to take per call: a model
+        moved to another dtype or device (model.half(), model.to(...)) replaces its embedding and lm_head
+        storage, so the eligibility is asked again and the engines are rebuilt."""
+        e, h = self.model.model.embed_tokens.weight, self.model.lm_head.weight
+        return (e.dtype, e.data_ptr(), h.dtype, h.data_ptr())
 
     def _step_reason(self, cache: TurboQuantCache) -> str | None:
         """Why the fused B = 1 step (lkv_decode_*) cannot run this model on this cache (None if it can): the
@@ -459,7 +469,7 @@ class GenerateFastPath:
     def _engine_for(self, cache: TurboQuantCache) -> "LeanKVEngine":
         # the engine holds raw pointers to the cache's buffers (and its graph captured them): buffers that
         # were replaced since -- a store that grew, a reset() followed by a new prefill -- need a new engine
-        key = (id(cache), cache.storage_generation, cache.attn_max_len(0))
+        key = (id(cache), cache.storage_generation, cache.attn_max_len(0), self._model_state())
         if self.engine is not None and self._cache is cache and self._engine_key == key:
             return self.engine
         self.engine = None
@@ -470,7 +480,7 @@ class GenerateFastPath:
         return self.engine
 
     def _batched_for(self, cache: TurboQuantCache, B: int) -> BatchedEngine:
-        key = (id(cache), cache.storage_generation, cache.attn_max_len(0), B)
+        key = (id(cache), cache.storage_generation, cache.attn_max_len(0), B, self._model_state())
         be = self.batched
         if be is None or be.cache is not cache or self._batched_key != key:
             self.batched = None

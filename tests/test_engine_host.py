@@ -151,3 +151,15 @@ def test_cache_storage_generation_moves_with_its_buffers():
     g2 = c.storage_generation
     c.reset()
     assert c.storage_generation > g2 and c._k_codes[0] is None
+
+
+def test_generate_fast_path_asks_again_after_a_dtype_change():
+    """The eligibility answer is kept per model state: a model converted to bf16 after the fast path was
+    installed (and asked once) stops being eligible instead of reusing the fp16 answer."""
+    from leankv_amd.engine import random_mistral
+
+    fp, cache = _fast_path_on(random_mistral(device="cpu", seed=7, **TINY))
+    ids = torch.zeros(1, 1, dtype=torch.long)
+    assert fp._eligible(ids, cache, {}) == "one"
+    fp.model.to(torch.bfloat16)
+    assert fp._eligible(ids, cache, {}) is None and "bfloat16" in fp._model_reason()
