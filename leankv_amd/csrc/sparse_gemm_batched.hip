@@ -14,8 +14,9 @@
 // (row chunks of BZ) x (groups of up to 8 batch rows).  The block compacts the
 // union of its rows' masks into an LDS list (per row, the NB activations with
 // the ones at or below the threshold zeroed), streams each listed 512-byte
-// row segment once with 16-byte buffer loads (4 rows per lane in flight,
-// non-temporal) and accumulates NB x 8 fp32 column sums per lane, two rows per
+// row segment once with 16-byte buffer loads (batches of 4 rows per lane, the
+// next batch in flight while the current one is summed; non-temporal) and
+// accumulates NB x 8 fp32 column sums per lane, two rows per
 // v_dot2_f32_f16; row slots
 // are reduced through LDS and the block writes fp32 partials per batch row,
 // summed over chunks in chunk order by batched_reduce_kernel (or written as
@@ -31,7 +32,7 @@ constexpr int kNT = 256;
 constexpr int kBN = kGemvBN;    // columns per slab
 constexpr int kLPR = kBN / 8;   // lanes per row segment
 constexpr int kSlots = kNT / kLPR;
-constexpr int kU = 4;           // rows per lane in flight (8: 29.8 vs 29.5 us at B = 8, config-1 shape)
+constexpr int kU = 4;           // rows per lane per batch (8, pipelined: 27.6 vs 26.2 us at B = 8, config-1 shape)
 constexpr int kPad = kU * kSlots;
 
 typedef uint32_t u32x4b __attribute__((ext_vector_type(4)));
@@ -63,14 +64,29 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
   const int z0 = chunk * BZ, n0 = slab * kBN;
   const int Z = P.Z, N = P.N;
 
-  // ---- 0. the group's activations (0 past Z and past the last batch row)
+  // ---- 0. the group's activations (0 past Z and past the last batch row).
+  // Every load is issued before the first is used (address clamped to element
+  // 0, value selected afterwards): a conditional load compiles to a branch and
+  // a wait per element, NB x BZ / kNT memory round trips in a row.
+  {
+    constexpr int E = BZ / kNT;
+    uint16_t raw[NB][E];
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int base = 0; base < BZ; base += kNT) {
-      const int z = z0 + base + tid;
-      s_x[b][base + tid] = (b < nb && z < Z) ? h2f(P.x[static_cast<size_t>(b0 + b) * Z + z]) : 0.f;
-    }
+      for (int e = 0; e < E; ++e) {
+        const int z = z0 + e * kNT + tid;
+        const bool ok = b < nb && z < Z;
+        raw[b][e] = P.x[ok ? static_cast<size_t>(b0 + b) * Z + z : 0];
+      }
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int z = z0 + e * kNT + tid;
+        s_x[b][e * kNT + tid] = (b < nb && z < Z) ? h2f(raw[b][e]) : 0.f;
+      }
+  }
   __syncthreads();
 
   // ---- 1. compaction of the rows some batch row keeps (strict |x| > t)
@@ -133,26 +149,47 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
   // a column's two weights into one fp16 pair, the two activations are one
   // 32-bit LDS read, and v_dot2_f32_f16 adds both products into the fp32 sum:
   // about half the VALU work of a conversion plus an FMA per weight and row.
+  // The next batch of kU rows is loaded before the current one is computed on,
+  // so its memory round trip overlaps the dot products (padded is a multiple of
+  // kPad, so every slot runs the same number of batches).
   static_assert(kU % 2 == 0, "rows are streamed in pairs");
-  for (int q = slot; 2 * q < padded; q += (kU / 2) * kSlots) {
+  {
+    const int iters = padded / kPad;
+    constexpr int kStep = (kU / 2) * kSlots;
     u32x4b w[kU];
+    int q = slot;
+    if (iters > 0) {
 #pragma unroll
-    for (int u = 0; u < kU; ++u)
-      w[u] = __builtin_amdgcn_raw_buffer_load_b128(
-          rs, static_cast<uint32_t>(s_idx[2 * (q + (u >> 1) * kSlots) + (u & 1)]) * row_bytes + col_bytes, 0, 2);
+      for (int u = 0; u < kU; ++u)
+        w[u] = __builtin_amdgcn_raw_buffer_load_b128(
+            rs, static_cast<uint32_t>(s_idx[2 * (q + (u >> 1) * kSlots) + (u & 1)]) * row_bytes + col_bytes, 0, 2);
+    }
+    for (int it = 0; it < iters; ++it, q += kStep) {
+      u32x4b cur[kU];
 #pragma unroll
-    for (int v = 0; v < kU / 2; ++v) {
-      half2_t wp[8];  // wp[j] = (A[row 2p][col + j], A[row 2p + 1][col + j]), p = q + v kSlots
+      for (int u = 0; u < kU; ++u) cur[u] = w[u];
+      if (it + 1 < iters) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        wp[2 * i] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(w[2 * v + 1][i], w[2 * v][i], 0x05040100u));
-        wp[2 * i + 1] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(w[2 * v + 1][i], w[2 * v][i], 0x07060302u));
+        for (int u = 0; u < kU; ++u)
+          w[u] = __builtin_amdgcn_raw_buffer_load_b128(
+              rs, static_cast<uint32_t>(s_idx[2 * (q + kStep + (u >> 1) * kSlots) + (u & 1)]) * row_bytes + col_bytes,
+              0, 2);
       }
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const half2_t xp = *reinterpret_cast<const half2_t*>(&s_xh[b][2 * (q + v * kSlots)]);
+      for (int v = 0; v < kU / 2; ++v) {
+        half2_t wp[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[b][j] = __builtin_amdgcn_fdot2(wp[j], xp, acc[b][j], false);
+        for (int i = 0; i < 4; ++i) {
+          wp[2 * i] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(cur[2 * v + 1][i], cur[2 * v][i], 0x05040100u));
+          wp[2 * i + 1] =
+              __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(cur[2 * v + 1][i], cur[2 * v][i], 0x07060302u));
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const half2_t xp = *reinterpret_cast<const half2_t*>(&s_xh[b][2 * (q + v * kSlots)]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[b][j] = __builtin_amdgcn_fdot2(wp[j], xp, acc[b][j], false);
+        }
       }
     }
   }
