@@ -205,6 +205,8 @@ def bench_gemv(args, torch):
                            "wrapper between two events; roofline: split-K pass"},
         "roofline": roof,
     }
+    if args.phases:
+        res["phases"] = _phases(torch, lambda: launch(0))
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_gemv(torch, sets[0], N, Z)
     return res
@@ -634,37 +636,9 @@ def bench_attn(args, torch):
     return res
 
 
-def _phases(torch, run):
-    """Per-block phase times (µs) of the attention kernels over one call of run(): the instrumented build's
-    split stamps (block start, token loop start, loop end, block end) and combine stamps (start, end) on the
-    100 MHz real-time clock; min / median / max over blocks, times relative to the first split block's start."""
-    import ctypes
-
-    from leankv_amd import _lib
-    lib = _lib.load()
-    if not hasattr(lib, "lkv_debug_stamps"):
-        raise SystemExit("--phases needs LKV_LIBRARY=leankv_amd/libleankv_amd_stamps.so "
-                         "(python -m leankv_amd.build --stamps)")
-    fn = lib.lkv_debug_stamps
-    fn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int]
-    n = 8 * 16384  # [block][8 stamps]
-    torch.cuda.synchronize()
-    for w in (0, 1):
-        assert fn(w, None, 0, 1) == 0, _lib.last_error()
-    run()
-    torch.cuda.synchronize()
-    buf = (ctypes.c_uint64 * n)()
-    out = {}
-    rows = {}
-    for w in (0, 1):
-        assert fn(w, ctypes.cast(buf, ctypes.c_void_p), n, 0) == 0, _lib.last_error()
-        rows[w] = [tuple(buf[8 * i: 8 * i + 8]) for i in range(n // 8) if buf[8 * i] and buf[8 * i + 3]]
-    split = rows[0]
+def _split_phases(out, split, comb, st):
+    """The attention split / combine part of _phases (times relative to the first split block's start)."""
     t0 = min(r[0] for r in split)
-
-    def st(vals):
-        vals = sorted(v * 0.01 for v in vals)  # 100 MHz ticks -> µs
-        return {"min": round(vals[0], 2), "median": round(statistics.median(vals), 2), "max": round(vals[-1], 2)}
     out["split_blocks"] = len(split)
     out["split_start"] = st(r[0] - t0 for r in split)
     out["split_prologue"] = st(r[1] - r[0] for r in split)
@@ -676,14 +650,77 @@ def _phases(torch, run):
     out["split_token_loop"] = st(r[2] - r[1] for r in split)
     out["split_merge_and_record"] = st(r[3] - r[2] for r in split)
     out["split_end"] = st(r[3] - t0 for r in split)
-    comb = rows[1]
     if comb:
         out["combine_blocks"] = len(comb)
         out["combine_start"] = st(r[0] - t0 for r in comb)
         out["combine_duration"] = st(r[3] - r[0] for r in comb)
         out["combine_end"] = st(r[3] - t0 for r in comb)
+
+
+def _phases(torch, run):
+    """Per-block phase times (µs) of the attention kernels over one call of run(): the instrumented build's
+    split stamps (block start, token loop start, loop end, block end) and combine stamps (start, end) on the
+    100 MHz real-time clock; min / median / max over blocks, times relative to the first split block's start.
+    With GEMV stamps in the build, the same for the last launch of each GEMV kind (block start, input prologue,
+    column sums, output store, block end)."""
+    import ctypes
+
+    from leankv_amd import _lib
+    lib = _lib.load()
+    if not hasattr(lib, "lkv_debug_stamps"):
+        raise SystemExit("--phases needs LKV_LIBRARY=leankv_amd/libleankv_amd_stamps.so "
+                         "(python -m leankv_amd.build --stamps)")
+    fn = lib.lkv_debug_stamps
+    fn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int]
+    gfn = getattr(lib, "lkv_debug_gemv_stamps", None)
+    if gfn is not None:
+        gfn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int]
+    n = 8 * 16384  # [block][8 stamps]
+    torch.cuda.synchronize()
+    for w in (0, 1):
+        assert fn(w, None, 0, 1) == 0, _lib.last_error()
+    if gfn is not None:
+        assert gfn(0, None, 0, 1) == 0, _lib.last_error()
+    run()
+    torch.cuda.synchronize()
+    buf = (ctypes.c_uint64 * n)()
+    out = {}
+    rows = {}
+    for w in (0, 1):
+        assert fn(w, ctypes.cast(buf, ctypes.c_void_p), n, 0) == 0, _lib.last_error()
+        rows[w] = [tuple(buf[8 * i: 8 * i + 8]) for i in range(n // 8) if buf[8 * i] and buf[8 * i + 3]]
+    split = rows[0]
+
+    def st(vals):
+        vals = sorted(v * 0.01 for v in vals)  # 100 MHz ticks -> µs
+        return {"min": round(vals[0], 2), "median": round(statistics.median(vals), 2), "max": round(vals[-1], 2)}
+    if split:
+        _split_phases(out, split, rows[1], st)
+    if gfn is not None:
+        names = {0: "gemv_raw_input", 1: "gemv_rmsnorm", 2: "gemv_swiglu", 3: "gemv_rmsnorm_dual",
+                 5: "gemv_dense_rmsnorm"}
+        for kind, name in names.items():
+            assert gfn(kind, ctypes.cast(buf, ctypes.c_void_p), n, 0) == 0, _lib.last_error()
+            g = [tuple(buf[8 * i: 8 * i + 8]) for i in range(n // 8) if buf[8 * i] and buf[8 * i + 3]]
+            if not g:
+                continue
+            g0 = min(r[0] for r in g)
+            by_xcc, by_slab, by_chunk = {}, {}, {}
+            for r in g:
+                by_xcc.setdefault(int(r[4]) & 0xF, []).append((r[3] - g0) * 0.01)
+                by_slab.setdefault(int(r[6]), []).append((r[3] - g0) * 0.01)
+                by_chunk.setdefault(int(r[7]), []).append((r[3] - g0) * 0.01)
+            slab_med = sorted(statistics.median(v) for v in by_slab.values())
+            chunk_med = sorted(statistics.median(v) for v in by_chunk.values())
+            out[name] = {"blocks": len(g), "start": st(r[0] - g0 for r in g), "input_prologue": st(r[1] - r[0] for r in g),
+                         "column_sums": st(r[2] - r[1] for r in g), "output": st(r[3] - r[2] for r in g),
+                         "end": st(r[3] - g0 for r in g),
+                         "end_median_by_xcc": {x: round(statistics.median(v), 2) for x, v in sorted(by_xcc.items())},
+                         "end_median_over_slabs_min_max": [round(slab_med[0], 2), round(slab_med[-1], 2)],
+                         "end_median_over_chunks_min_max": [round(chunk_med[0], 2), round(chunk_med[-1], 2)]}
     out["what"] = ("µs per block on the 100 MHz clock over one call (the last launch of each kernel), relative to "
-                   "the first split block's start; instrumented build (LKV_STAMPS)")
+                   "the first split block's start (GEMV kinds: to that launch's first block start); instrumented "
+                   "build (LKV_STAMPS)")
     return out
 
 
@@ -1226,7 +1263,7 @@ def bench_decode(args, torch):
         res["hf_generate"] = {"leankv_tok_s": gen_lkv, "leankv_hf_forward_tok_s": gen_lkv_hf,
                               "fast_path_calls": gen_steps}
     if phases:
-        res["phases_last_layer_attention"] = phases
+        res["phases_last_layer"] = phases
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_decode(torch, model, th, args.prompt, bits=args.bits)
     del model

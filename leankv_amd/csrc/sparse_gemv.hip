@@ -136,8 +136,36 @@ __device__ __forceinline__ T seg_pick(const T (&v)[kMaxSeg], int seg) {
   return r;
 }
 
+#ifdef LKV_STAMPS
+// Instrumented build only (build.py --stamps): per-block phase times on the
+// 100 MHz real-time clock of the last launch of each kernel kind, [kind]
+// [block][8 stamps]: 0 block start, 1 input prologue done, 2 column sums done
+// (compaction, weight stream, slot reduction), 3 block end; 4 the XCC id and
+// 5 the HW_ID register of the wave (CU, shader engine) at block start, 6 the
+// global column slab and 7 the row chunk of the item.  Kinds: 0 raw
+// input, 1 RMSNorm, 2 SwiGLU, 3 RMSNorm dual (gate|up); + 4 for the dense
+// variant.  Thread 0 stores them (first work item of a block only).
+constexpr int kGemvStampKinds = 8;
+constexpr int kGemvStampBlocks = 16384;
+__device__ uint64_t g_gemv_stamps[kGemvStampKinds * kGemvStampBlocks * 8];
+#define LKV_GEMV_STAMP(i)                                                                                     \
+  do {                                                                                                      \
+    if (threadIdx.x == 0 && item == static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x) &&                \
+        item < kGemvStampBlocks)                                                                            \
+      __builtin_nontemporal_store(__builtin_amdgcn_s_memrealtime(),                                         \
+                                  g_gemv_stamps + (kStampKind * kGemvStampBlocks + item) * 8 + (i));        \
+  } while (0)
+#else
+#define LKV_GEMV_STAMP(i) \
+  do {                    \
+  } while (0)
+#endif
+
 template <int NT, int BZ, bool DUAL, int MODE, int U, int CP, bool DENSE = false>
 __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
+#ifdef LKV_STAMPS
+  constexpr int kStampKind = (DENSE ? 4 : 0) + (DUAL ? 3 : MODE);
+#endif
   constexpr int BN = kGemvBN;
   constexpr int NL = DUAL ? 2 : 1;
   __shared__ GemvLds<NT, BZ, DUAL, U> sm;
@@ -158,6 +186,16 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
       chunk = item / nslab_tot;
     }
     const int z0 = chunk * BZ;
+    LKV_GEMV_STAMP(0);
+#ifdef LKV_STAMPS
+    if (threadIdx.x == 0 && item == static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x) && item < kGemvStampBlocks) {
+      uint64_t* r = g_gemv_stamps + (kStampKind * kGemvStampBlocks + item) * 8;
+      __builtin_nontemporal_store(static_cast<uint64_t>(__builtin_amdgcn_s_getreg(20 | (3 << 11))), r + 4);
+      __builtin_nontemporal_store(static_cast<uint64_t>(__builtin_amdgcn_s_getreg(4 | (31 << 11))), r + 5);
+      __builtin_nontemporal_store(static_cast<uint64_t>(gslab), r + 6);
+      __builtin_nontemporal_store(static_cast<uint64_t>(chunk), r + 7);
+    }
+#endif
 
     int seg = 0;
 #pragma unroll
@@ -173,13 +211,16 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
       input_prologue<NT, BZ, MODE, true>(G, z0, xin, sm.wsum, [&] {
         gemv_dense_first<NT, U, CP>(seg_pick(G.A, seg), seg_pick(G.a_bytes, seg), N, z0, G.Z, n0, w0);
       });
+      LKV_GEMV_STAMP(1);
       gemv_core_dense<NT, BZ, DUAL, U, CP>(sm, xin, w0, seg_pick(G.A, seg), G.A_up, seg_pick(G.a_bytes, seg), N, z0,
                                            G.Z, n0, sums);
     } else {
       input_prologue<NT, BZ, MODE, false>(G, z0, xin, sm.wsum, [] {});
+      LKV_GEMV_STAMP(1);
       gemv_core<NT, BZ, DUAL, U, CP>(sm, xin, seg_pick(G.A, seg), G.A_up, seg_pick(G.a_bytes, seg), N,
                                      seg_pick(G.t, seg), G.t_up, z0, G.Z, n0, sums);
     }
+    LKV_GEMV_STAMP(2);
 
     // ---- 4. output (threads 0..255, one column each): fp16 directly (single chunk) or partial sums
     if (tid < BN) {
@@ -194,6 +235,7 @@ __global__ __launch_bounds__(NT) void sparse_gemv_kernel(GemvArgs G) {
         }
       }
     }
+    LKV_GEMV_STAMP(3);
     if (item + static_cast<int>(gridDim.x * gridDim.y) < nitems) __syncthreads();  // uniform: LDS reused next
   }
 }
@@ -406,6 +448,26 @@ int gemv_launch(const GemvArgs& G, int bz, bool dual, int mode, int nslab_total,
   LKV_LAUNCH_CHECK("sparse_gemv");
   return LKV_OK;
 }
+
+#ifdef LKV_STAMPS
+// Instrumented build only: copy the stamps of GEMV kind `kind` (n <= 8 * 16384
+// words) to host memory, or zero every kind's with clear = 1.  Not declared
+// in the public header.
+extern "C" int lkv_debug_gemv_stamps(int kind, uint64_t* host, int64_t n, int clear) {
+  LKV_REQUIRE(kind >= 0 && kind < kGemvStampKinds && n >= 0 && n <= 8 * kGemvStampBlocks && (clear || host),
+              "debug_gemv_stamps: bad arguments");
+  hipError_t e;
+  if (clear) {
+    static uint64_t zeros[kGemvStampKinds * kGemvStampBlocks * 8];
+    e = hipMemcpyToSymbol(HIP_SYMBOL(g_gemv_stamps), zeros, sizeof(zeros));
+  } else {
+    e = hipMemcpyFromSymbol(host, HIP_SYMBOL(g_gemv_stamps), static_cast<size_t>(n) * 8,
+                            static_cast<size_t>(kind) * kGemvStampBlocks * 8 * 8);
+  }
+  LKV_REQUIRE(e == hipSuccess, "debug_gemv_stamps: %s", hipGetErrorString(e));
+  return LKV_OK;
+}
+#endif
 
 namespace {
 
