@@ -57,28 +57,10 @@ __device__ __forceinline__ uint64_t wave_ballot(bool p) {
   return __ballot(p);
 }
 
-// Every split-K workspace starts with a fixed ticket area: kTicketBytes of
-// uint32 counters at offset 0, whatever the call's shape, so counters of one
-// call never land on another call's partial sums.  Kernels leave counters at 0.
+// Every split-K workspace starts with a reserved area of kTicketBytes at
+// offset 0 (no kernel reads or writes it; the partial sums and records start
+// after it), so the workspace layouts and sizes stay those the C ABI reports.
 constexpr size_t kTicketBytes = 64 * 1024;
-constexpr int64_t kMaxTickets = static_cast<int64_t>(kTicketBytes / 4);
-
-// Agent-scope release/acquire around the split-K ticket.  On gfx950 each XCD
-// has its own L2; agent-scope fences write back / invalidate it so partials
-// written on one XCD are visible to the block that reduces them on another.
-__device__ __forceinline__ void fence_release_agent() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-}
-__device__ __forceinline__ void fence_acquire_agent() {
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-}
-// Relaxed: callers bracket it with the explicit fences above (one thread per block).
-__device__ __forceinline__ unsigned ticket_add(unsigned* p) {
-  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void ticket_reset(unsigned* p) {
-  __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Cross-lane reductions on DPP (VALU lane permutes, no LDS round trip).
 // Within a 16-lane row: xor 1, xor 2 (quad_perm), then the half-row and row
