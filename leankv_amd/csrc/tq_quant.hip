@@ -51,6 +51,17 @@ __device__ __forceinline__ int bucket_bsearch(float y, const float (&bd)[(1 << B
   }
 }
 
+// The 4-bit search of bucket_bsearch on a boundary table in LDS: the same
+// comparisons, the next boundary addressed by the bucket so far (kept in
+// registers, the selects between boundaries compile to an indexed load from a
+// private, memory-backed copy of the table).
+__device__ __forceinline__ int bucket_bsearch4_lds(float y, const float* s_bd) {
+  int k = s_bd[7] < y ? 8 : 0;
+  k += s_bd[k + 3] < y ? 4 : 0;
+  k += s_bd[k + 1] < y ? 2 : 0;
+  return k + (s_bd[k] < y ? 1 : 0);
+}
+
 template <int BITS, bool F16>
 __global__ __launch_bounds__(kThreads, 2) void quantize_wave_kernel(const void* __restrict__ xin, int64_t M,
                                                                     const float* __restrict__ Pi,
@@ -60,6 +71,7 @@ __global__ __launch_bounds__(kThreads, 2) void quantize_wave_kernel(const void* 
   static_assert(pack_bits(BITS) == 4 && row_bytes_for(BITS) == 64, "nibble layouts only");
   __shared__ float4 s_b[8][8][65];  // 64 KB + one float4 of padding per row: the staging writes of 8
                                      // consecutive threads (8 k-quarters) fall in different banks
+  __shared__ float s_bd[16];        // 4-bit boundaries
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int64_t ntiles = (M + kRows - 1) / kRows;
@@ -82,7 +94,8 @@ __global__ __launch_bounds__(kThreads, 2) void quantize_wave_kernel(const void* 
   for (int i = 0; i < kD * kD / 4 / kThreads; ++i) pr[i] = reinterpret_cast<const float4*>(Pi)[i * kThreads + threadIdx.x];
   float bd[(1 << BITS) - 1];
 #pragma unroll
-  for (int i = 0; i < (1 << BITS) - 1; ++i) bd[i] = bounds[i];
+  for (int i = 0; i < (1 << BITS) - 1; ++i) bd[i] = BITS == 3 ? bounds[i] : 0.f;
+  if (BITS == 4 && threadIdx.x < (1 << BITS) - 1) s_bd[threadIdx.x] = bounds[threadIdx.x];
 #pragma unroll
   for (int i = 0; i < kD * kD / 4 / kThreads; ++i) {
     const int f = i * kThreads + threadIdx.x;
@@ -130,7 +143,10 @@ __global__ __launch_bounds__(kThreads, 2) void quantize_wave_kernel(const void* 
       const int64_t row = row0 + 4 * g + i;
       uint32_t v = 0;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) v |= static_cast<uint32_t>(bucket_bsearch<BITS>(acc[c][i], bd)) << (4 * c);
+      for (int c = 0; c < 8; ++c) {
+        const int code = BITS == 3 ? bucket_bsearch<BITS>(acc[c][i], bd) : bucket_bsearch4_lds(acc[c][i], s_bd);
+        v |= static_cast<uint32_t>(code) << (4 * c);
+      }
       if (row < M) *reinterpret_cast<uint32_t*>(packed + row * 64 + 4 * n) = v;
     }
   }
