@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
-Workloads:
+Workloads (the benchmark configurations 1-5 of the decode hot path):
   decode  config 5 (default): random-init fp16 Mistral-7B-v0.3-shaped decoder, 4096-token
           random prompt, per-projection TEAL sparsity ~U[0.3,0.5] (thresholds from a seeded
           calibration pass at the decode context: quantiles over the last 256 positions of a

@@ -704,7 +704,7 @@ class DenseEngine(_Base):
         self._finish(x)
 
 
-# Mistral-7B-v0.3 shape (configs/mistral7b.yaml in the reference).
+# Mistral-7B-v0.3 shape (the config-5 decoder; configs/mistral7b.yaml in the reference).
 # Mistral-7B-v0.3 has no sliding window ("sliding_window": null); MistralConfig's default is 4096.
 MISTRAL_7B = dict(vocab_size=32768, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
                   num_attention_heads=32, num_key_value_heads=8, head_dim=128, max_position_embeddings=32768,

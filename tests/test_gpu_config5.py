@@ -30,7 +30,7 @@ pytestmark = pytest.mark.gpu
 
 PROMPT, STEPS = 1024, 8
 MAXLEN = PROMPT + STEPS + 8
-SPARSITY = (0.3, 0.5)  # per-projection TEAL sparsity drawn from U[0.3, 0.5]
+SPARSITY = (0.3, 0.5)  # per-projection TEAL sparsity drawn from U[0.3, 0.5] (the config-5 decoder)
 RTOL = 2e-2      # model logits vs the fp64 oracle (fp16 activations, fp32 sums)
 GEMV_TOL = 1e-3  # one projection vs fp64 on the same input (fp32 accumulate, fp16 output)
 

@@ -45,7 +45,7 @@ def _gemv(x, W, t, dev):
 
 # ----------------------------------------------------------------- TEAL GEMV
 def test_sparse_gemv_config1(cuda):
-    """W[4096, 14336] ~N(0,.02), x ~Laplace(0,.05), t = 40% quantile."""
+    """Config 1 (single sparse GEMV): W[4096, 14336] ~N(0,.02), x ~Laplace(0,.05), t = 40% quantile."""
     W, x, t = _seeded_gemv(4096, 14336)
     y = _gemv(x, W, t, cuda)
     ref = ot.sparse_gemv(x.numpy(), W.numpy(), t)
@@ -134,7 +134,7 @@ def test_sparse_gemv_deterministic_and_reusable_workspace(cuda):
 
 
 def test_gateup_swiglu_config2(cuda):
-    """x[4096] ~N(0,1) at 40%, Wg/Wu [14336, 4096], then down at 40% of |h|."""
+    """Config 2 (fused MLP): x[4096] ~N(0,1) at 40%, Wg/Wu [14336, 4096], then down at 40% of |h|."""
     from leankv_amd import kernels
 
     g = torch.Generator().manual_seed(0)
@@ -257,7 +257,7 @@ def _quantize_check(x, Pi, b, bits, p, n):
 
 @pytest.mark.parametrize("in_dtype", [torch.float32, torch.float16])
 def test_tq_quantize_config3(cuda, in_dtype):
-    """K,V [8, 4096, 128] ~N(0,1), channels {0,31,64,127} x10, Pi seeds 42/43."""
+    """Config 3 (TurboQuant quantize): K,V [8, 4096, 128] ~N(0,1), channels {0,31,64,127} x10, Pi seeds 42/43."""
     from leankv_amd import kernels
 
     c, b = oq.codebook_tensors(3)
@@ -606,7 +606,7 @@ def _attn_case(B, Hq, Hkv, L, hot, seed, dev, bits=3):
 
 @pytest.mark.parametrize("B", [1, 4, 16])
 def test_decode_attn_config4(cuda, B):
-    """32 q heads over 8 kv heads, ctx 4096 cold + 64-token fp16 hot tail."""
+    """Config 4 (packed-KV decode attention): 32 q heads over 8 kv heads, ctx 4096 cold + 64-token fp16 hot tail."""
     out, ref = _attn_case(B, 32, 8, 4096 + 64, 64, seed=B, dev=cuda)
     assert ot.rel_err(out.numpy(), ref.numpy()) < RTOL
     assert ot.max_rel_err(out.numpy(), ref.numpy()) < RTOL
