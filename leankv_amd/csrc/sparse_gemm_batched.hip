@@ -11,7 +11,8 @@
 //
 // A weight row is needed by a block as soon as one of its batch items keeps
 // that activation, and then serves all of them: grid = (column slabs of 256) x
-// (row chunks of BZ) x (groups of up to 8 batch rows).  The block compacts the
+// (row chunks of BZ) x (groups of up to 8 batch rows; of 16 on the
+// matrix-core kernel below, used from 8 rows on).  The block compacts the
 // union of its rows' masks into an LDS list (per row, the NB activations with
 // the ones at or below the threshold zeroed), streams each listed 512-byte
 // row segment once with 16-byte buffer loads (batches of 4 rows per lane, the
@@ -23,6 +24,8 @@
 // fp16 directly when there is one chunk).  At 40 % sparsity and B = 4 the
 // union keeps ~97 % of the rows: one pass over ~the dense weight instead of
 // 4 x 60 % of it.
+#include <stdlib.h>
+
 #include "kernels.h"
 
 namespace lkv {
@@ -214,6 +217,188 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
   }
 }
 
+// Groups of 9 to 16 batch rows on the matrix cores: the same union compaction
+// (activations of the listed rows, fp16, batch-major in LDS), then per block
+// of 32 list entries the 256-column weight tile (16 KB) goes through LDS as
+// row-pair dwords -- thread (column group c, entry quad q) loads its four
+// 16-byte row segments, v_perm_b32 pairs entries (4q, 4q + 1) and (4q + 2,
+// 4q + 3) column by column, and the pairs are stored [pair][column] -- so that
+// v_mfma_f32_16x16x32_f16 reads its B operand (8 entries of one column) as
+// four LDS words and its A operand (8 entries of one batch row) as one 16-byte
+// word.  Wave w owns columns 64 w .. 64 w + 63 (four 16-column tiles) for all
+// 16 batch rows, so no cross-wave reduction; two blocks of entries are in
+// flight per thread while the previous one is multiplied.  fp16 products are
+// exact in fp32 and the sums fp32, as in the v_dot2 kernel (summation order
+// differs).
+constexpr int kMB = 16;               // batch rows per block (the MFMA's M)
+constexpr int kKB = 32;               // list entries per block of entries (the MFMA's K)
+constexpr int kPairs = kKB / 2;       // row pairs per block of entries
+constexpr int kBRow = kBN + 4;        // words per pair row of the weight tile in LDS (bank spread)
+
+template <int BZ>
+__global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P) {
+  static_assert(BZ % kNT == 0 && BZ % kKB == 0, "chunk shape");
+  constexpr int E = BZ / kNT;
+  constexpr int kXRow = BZ + kKB + 8;  // fp16 per batch row of the listed activations (16-byte rows)
+  __shared__ int s_idx[BZ + kKB];
+  __shared__ __align__(16) uint16_t s_xh[kMB][kXRow];
+  __shared__ __align__(16) uint32_t s_w[2][kPairs * kBRow];
+  __shared__ int s_cnt[kNT / kWave];
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int slab = blockIdx.x, chunk = blockIdx.y;
+  const int b0 = blockIdx.z * kMB;
+  const int nb = min(kMB, P.B - b0);
+  const int z0 = chunk * BZ, n0 = slab * kBN;
+  const int Z = P.Z, N = P.N;
+
+  // ---- 0. the group's activations into registers, every load issued before
+  // the first is used (address clamped to element 0, value selected after)
+  float xv[kMB][E];
+  {
+    uint16_t raw[kMB][E];
+#pragma unroll
+    for (int b = 0; b < kMB; ++b)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int z = z0 + e * kNT + tid;
+        raw[b][e] = P.x[(b < nb && z < Z) ? static_cast<size_t>(b0 + b) * Z + z : 0];
+      }
+#pragma unroll
+    for (int b = 0; b < kMB; ++b)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int z = z0 + e * kNT + tid;
+        xv[b][e] = (b < nb && z < Z) ? h2f(raw[b][e]) : 0.f;
+      }
+  }
+
+  // ---- 1. compaction of the rows some batch row keeps (strict |x| > t)
+  int total = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int z = z0 + e * kNT + tid;
+    bool keep = false;
+#pragma unroll
+    for (int b = 0; b < kMB; ++b) keep = keep || fabsf(xv[b][e]) > P.t;
+    keep = keep && z < Z;
+    const uint64_t mask = wave_ballot(keep);
+    if (lane == 0) s_cnt[wave] = __popcll(mask);
+    __syncthreads();
+    int off = total, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kNT / kWave; ++w) {
+      const int cw = s_cnt[w];
+      off += (w < wave) ? cw : 0;
+      tot += cw;
+    }
+    if (keep) {
+      const int pos = off + lane_prefix(mask);
+      s_idx[pos] = z;
+#pragma unroll
+      for (int b = 0; b < kMB; ++b) s_xh[b][pos] = f2h(fabsf(xv[b][e]) > P.t ? xv[b][e] : 0.f);  // exact
+    }
+    total += tot;
+    __syncthreads();
+  }
+  // pad to whole blocks of entries with (last row, zero activations)
+  const int padded = (total + kKB - 1) / kKB * kKB;
+  if (total > 0 && tid < padded - total) {
+    s_idx[total + tid] = s_idx[total - 1];
+#pragma unroll
+    for (int b = 0; b < kMB; ++b) s_xh[b][total + tid] = 0;
+  }
+  __syncthreads();
+
+  // ---- 2. blocks of 32 entries: weight tile through LDS, MFMA
+  const int nkb = padded / kKB;
+  const int c = tid % (kBN / 8), q = tid / (kBN / 8);  // column group (8 columns), entry quad
+  const int col = n0 + 8 * c;
+  const uint32_t row_bytes = static_cast<uint32_t>(N) * 2u;
+  const uint32_t col_bytes = col < N ? static_cast<uint32_t>(col) * 2u : P.a_bytes;  // past N: reads 0
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.A), 0, P.a_bytes,
+                                                                      0x00020000);
+  // Blocks past the list load through offsets past the descriptor's end (zeros,
+  // no memory traffic): the loads stay unconditional, so no branch makes the
+  // wait for the block in flight come early.
+  auto load_tile = [&](u32x4b (&w)[4], int kb) {
+    const bool ok = kb < nkb;
+    const int kc = ok ? kb : 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t off = static_cast<uint32_t>(s_idx[kc * kKB + 4 * q + r]) * row_bytes + col_bytes;
+      w[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? off : P.a_bytes, 0, 2);
+    }
+  };
+  // pairs (4q, 4q + 1) -> pair row 2q, (4q + 2, 4q + 3) -> 2q + 1; columns 8c .. 8c + 7
+  auto store_tile = [&](const u32x4b (&w)[4], int buf) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4b o[2];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+        o[j >> 2][j & 3] = __builtin_amdgcn_perm(w[2 * h + 1][j >> 1], w[2 * h][j >> 1], sel);
+      }
+      uint32_t* dst = &s_w[buf][(2 * q + h) * kBRow + 8 * c];
+      *reinterpret_cast<u32x4b*>(dst) = o[0];
+      *reinterpret_cast<u32x4b*>(dst + 4) = o[1];
+    }
+  };
+  f32x4 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int m = lane & 15, kg = lane >> 4;
+  auto multiply = [&](int kb, int buf) {
+    const u32x4b a = *reinterpret_cast<const u32x4b*>(&s_xh[m][kb * kKB + 8 * kg]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int cc = 64 * wave + 16 * t + m;  // this lane's B column
+      u32x4b bw;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bw[i] = s_w[buf][(4 * kg + i) * kBRow + cc];
+      acc[t] = mfma16x16x32(__builtin_bit_cast(u32x4, a), __builtin_bit_cast(u32x4, bw), acc[t]);
+    }
+  };
+  if (nkb > 0) {
+    u32x4b r0[4], r1[4];
+    load_tile(r0, 0);
+    load_tile(r1, 1);
+    store_tile(r0, 0);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; kb += 2) {
+      // s_w[0] holds block kb, r1 block kb + 1 (in flight); stores of blocks
+      // past the list write zeros nobody reads
+      load_tile(r0, kb + 2);
+      multiply(kb, 0);
+      store_tile(r1, 1);
+      __syncthreads();
+      if (kb + 1 >= nkb) break;
+      load_tile(r1, kb + 3);
+      multiply(kb + 1, 1);
+      store_tile(r0, 0);
+      __syncthreads();
+    }
+  }
+
+  // ---- 3. lane (m, kg) holds batch rows 4 kg + i of column 64 wave + 16 t + m
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int lc = 64 * wave + 16 * t + m;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = 4 * kg + i;
+      if (b < nb) {
+        if (P.nchunk == 1) {
+          if (n0 + lc < N) P.y[static_cast<size_t>(b0 + b) * N + n0 + lc] = f2h(acc[t][i]);
+        } else {
+          P.part[((static_cast<size_t>(b0 + b) * P.nslab + slab) * P.nchunk + chunk) * kBN + lc] = acc[t][i];
+        }
+      }
+    }
+  }
+}
+
 // y[b][n] = fp16 of the chunk partials summed in chunk order.
 __global__ __launch_bounds__(kNT) void batched_reduce_kernel(const float* __restrict__ part, int N, int nslab,
                                                              int nchunk, uint16_t* __restrict__ y) {
@@ -232,8 +417,26 @@ bool launch_nb(const BatchedArgs& P, int bz, dim3 grid, hipStream_t st) {
   }
 }
 
-// Batch rows per block: the next power of two up to 8.
-int group_rows(int64_t B) { return B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8; }
+// Batches of at least this many rows run on the matrix-core kernel in groups
+// of 16 (LKV_BATCHED_MFMA=k for sweeps; 0 never).  Measured on one MI355X at
+// the Mistral-7B shapes (us, VALU / matrix-core kernel): 2 rows at 40 %
+// sparsity 18.1 / 21.2 (down), 6 rows 25.0 / 25.0, 8 rows 25.9 / 25.0, dense
+// 16 rows 41.1 / 26.3 (down) and 38.9 / 24.8 (gate / up).
+int64_t mfma_min_rows() {
+  static const int64_t k = [] {
+    const char* env = getenv("LKV_BATCHED_MFMA");
+    return static_cast<int64_t>(env ? atoi(env) : 8);
+  }();
+  return k;
+}
+bool use_mfma(int64_t B) { return mfma_min_rows() > 0 && B >= mfma_min_rows(); }
+
+// Batch rows per block: the next power of two up to 8 on the VALU kernel, 16
+// on the matrix-core kernel.
+int group_rows(int64_t B) {
+  if (use_mfma(B)) return kMB;
+  return B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
+}
 
 // Chunk size: the largest giving ~1.5 blocks (of 256 threads) per CU, with the
 // batch groups counted as extra blocks.
@@ -293,10 +496,20 @@ extern "C" int lkv_sparse_gemm_batched(const void* x, const void* w, float thres
   P.y = static_cast<uint16_t*>(y);
   const dim3 grid(static_cast<unsigned>(nslab), static_cast<unsigned>(nchunk),
                   static_cast<unsigned>((B + nbr - 1) / nbr));
-  const bool ok = nbr == 1 ? launch_nb<1>(P, bz, grid, st)
-                : nbr == 2 ? launch_nb<2>(P, bz, grid, st)
-                : nbr == 4 ? launch_nb<4>(P, bz, grid, st)
-                           : launch_nb<8>(P, bz, grid, st);
+  bool ok;
+  if (use_mfma(B)) {
+    switch (bz) {
+      case 256: hipLaunchKernelGGL(sparse_gemm_mfma_kernel<256>, grid, dim3(kNT), 0, st, P); ok = true; break;
+      case 512: hipLaunchKernelGGL(sparse_gemm_mfma_kernel<512>, grid, dim3(kNT), 0, st, P); ok = true; break;
+      case 1024: hipLaunchKernelGGL(sparse_gemm_mfma_kernel<1024>, grid, dim3(kNT), 0, st, P); ok = true; break;
+      default: ok = false;
+    }
+  } else {
+    ok = nbr == 1 ? launch_nb<1>(P, bz, grid, st)
+       : nbr == 2 ? launch_nb<2>(P, bz, grid, st)
+       : nbr == 4 ? launch_nb<4>(P, bz, grid, st)
+                  : launch_nb<8>(P, bz, grid, st);
+  }
   LKV_REQUIRE(ok, "sparse_gemm_batched: no kernel for chunk %d", bz);
   LKV_LAUNCH_CHECK("sparse_gemm_batched");
   if (nchunk > 1) {

@@ -116,10 +116,11 @@ def apply_teal(
 
 def _skinny_dense(rows: int, N: int, Z: int) -> bool:
     """Whether a dense product of `rows` decode rows runs on the batched kernel (threshold 0) rather than torch's
-    GEMM.  Measured on one MI355X, eager calls at the Mistral-7B shapes over the column-major weight, torch vs the
-    batched kernel in us: down [4096 x 14336] 70 / 23-28 for 2-8 rows, 72 / 45 for 16; gate/up [14336 x 4096]
-    28 / 22-27 for 2-8 rows, 28 / 45 for 16; q/o and k/v within launch overhead of each other."""
-    return 1 < rows <= 16 and (rows <= 8 or Z > N)
+    GEMM.  Measured on one MI355X, back-to-back calls at the Mistral-7B shapes over the column-major weight, torch
+    vs the batched kernel in us: down [4096 x 14336] 50 / 25 for 8 rows, 49-52 / 26 for 12-16; q|k|v
+    [6144 x 4096] 19 / 15 and o [4096 x 4096] 19 / 12-15 for 8-16 rows; gate/up [14336 x 4096] 23-24 / 24 for 8
+    rows, 23 / 25 for 12-16 (torch's GEMM then wins by a little)."""
+    return 1 < rows <= 16 and (rows <= 8 or N <= 2 * Z)
 
 
 def _patch_linear_with_kernel(linear: nn.Linear, threshold: float) -> None:
