@@ -429,6 +429,18 @@ typedef struct lkv_decode_layer {
  */
 int lkv_rmsnorm(const void* x, const void* w, float eps, int64_t M, int64_t Z, void* y, void* stream);
 
+/*
+ * RoPE of B decode rows in place, one launch for the query and the key:
+ * q fp16 [B][Hq][128], k fp16 [B][Hkv][128] (contiguous), cos_row / sin_row
+ * the 128 fp16 factors of the tokens' position.  HF apply_rotary_pos_emb on
+ * fp16 tensors (transformers/models/mistral/modeling_mistral.py:51-81,
+ * x * cos + rotate_half(x) * sin, each product and the sum rounded to fp16)
+ * bit for bit, the arithmetic of the fused step's split prologue.
+ * B * (Hq + Hkv) < 2^24.
+ */
+int lkv_rope_f16(void* q, void* k, const void* cos_row, const void* sin_row, int64_t B, int64_t Hq, int64_t Hkv,
+                 void* stream);
+
 /* Workspace shared by the four calls below (no initialisation needed).
  * A step is: lkv_decode_begin, lkv_decode_evict, lkv_decode_layer_step per
  * layer, lkv_decode_head, all on one stream. */

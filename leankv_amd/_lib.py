@@ -67,6 +67,7 @@ SIGNATURES = {
     "lkv_tq_prefill_attn": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _int, _i64, _i64,
                                    _i64, _i64, _i64, _i64, _i64, _f32, _c_p, _c_p, _sz, _c_p]),
     "lkv_rmsnorm": (_int, [_c_p, _c_p, _f32, _i64, _i64, _c_p, _c_p]),
+    "lkv_rope_f16": (_int, [_c_p, _c_p, _c_p, _c_p, _i64, _i64, _i64, _c_p]),
     "lkv_decode_workspace_bytes": (_sz, [_c_p]),
     "lkv_decode_workspace_layout": (_int, [_c_p, _c_p]),
     "lkv_decode_begin": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _sz, _c_p]),

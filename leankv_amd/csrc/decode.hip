@@ -403,6 +403,43 @@ extern "C" int lkv_rmsnorm(const void* x, const void* w, float eps, int64_t M, i
   return LKV_OK;
 }
 
+namespace lkv {
+namespace {
+// RoPE of B decode rows in place: q [B][Hq][128], k [B][Hkv][128] fp16 at one
+// position (cos / sin: that position's 128 fp16 factors).  Thread = one dim
+// pair (d, d + 64) of one head: rope_pair_v, the fp16 arithmetic of HF's
+// apply_rotary_pos_emb.
+__global__ __launch_bounds__(kThreads) void rope_f16_kernel(uint16_t* __restrict__ q, uint16_t* __restrict__ k,
+                                                            const uint16_t* __restrict__ cos_row,
+                                                            const uint16_t* __restrict__ sin_row, int rows_q,
+                                                            int rows_k) {
+  const int e = blockIdx.x * kThreads + threadIdx.x;  // (row, pair) over the q rows, then the k rows
+  const int row = e / (kD / 2), d = e % (kD / 2);
+  if (row >= rows_q + rows_k) return;
+  uint16_t* x = row < rows_q ? q + static_cast<size_t>(row) * kD : k + static_cast<size_t>(row - rows_q) * kD;
+  float o0, o1;
+  rope_pair(h2f(x[d]), h2f(x[d + kD / 2]), cos_row, sin_row, d, o0, o1);
+  x[d] = f2h(o0);
+  x[d + kD / 2] = f2h(o1);
+}
+}  // namespace
+}  // namespace lkv
+
+extern "C" int lkv_rope_f16(void* q, void* k, const void* cos_row, const void* sin_row, int64_t B, int64_t Hq,
+                            int64_t Hkv, void* stream) {
+  LKV_REQUIRE(B >= 0 && Hq >= 0 && Hkv >= 0 && B * (Hq + Hkv) < (1ll << 24),
+              "rope_f16: B=%lld Hq=%lld Hkv=%lld out of range", (long long)B, (long long)Hq, (long long)Hkv);
+  const int64_t rows = B * (Hq + Hkv);
+  if (rows == 0) return LKV_OK;
+  LKV_REQUIRE(cos_row && sin_row && (q || B * Hq == 0) && (k || B * Hkv == 0), "rope_f16: null pointer");
+  const unsigned grid = static_cast<unsigned>((rows * (kD / 2) + kThreads - 1) / kThreads);
+  hipLaunchKernelGGL(rope_f16_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<uint16_t*>(q), static_cast<uint16_t*>(k), static_cast<const uint16_t*>(cos_row),
+                     static_cast<const uint16_t*>(sin_row), static_cast<int>(B * Hq), static_cast<int>(B * Hkv));
+  LKV_LAUNCH_CHECK("rope_f16");
+  return LKV_OK;
+}
+
 extern "C" size_t lkv_decode_workspace_bytes(const lkv_decode_dims* dims) {
   if (check_dims(dims) != LKV_OK) return 0;
   return make_plan(*dims).total;

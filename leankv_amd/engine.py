@@ -228,6 +228,9 @@ class LeanKVEngine(_Base):
                    "lkv_decode_head")
 
 
+_HF_RMSNORMS = ("MistralRMSNorm", "LlamaRMSNorm")
+
+
 class BatchedEngine:
     """One decode step of B > 1 sequences of equal length on a fused TurboQuantCache, captured once and
     replayed as a HIP graph.
@@ -235,11 +238,14 @@ class BatchedEngine:
     At B > 1 the reference's patched projections run dense F.linear (leankv/teal/patching.py:169-180);
     HF's decoder layer then calls TurboQuantCache.update and the attention function per layer
     (modeling_mistral.py:135-174, cache.py:84-127).  This step makes the same calls in the same order on
-    the same modules -- embedding, RMSNorm, the (patched) projections, HF's own RoPE function, the cache's
-    append and decode-attention kernels, o_proj, residual adds, the (patched) MLP, final norm and
-    lm_head -- with the position on the device, so the whole step replays without the host: the logits
-    equal the HF forward's bit for bit.  tok [B] is fed, logits [B, vocab] come out; the cache's host
-    counters are the caller's to advance (GenerateFastPath does)."""
+    the same modules -- embedding, the (patched) projections, the cache's append and decode-attention
+    kernels, o_proj, residual adds, the (patched) MLP and lm_head -- with the position on the device, so the
+    whole step replays without the host.  RMSNorm runs as one lkv_rmsnorm launch (the B = 1 step's
+    arithmetic) and RoPE as one lkv_rope_f16 launch (HF's fp16 arithmetic bit for bit) instead of HF's
+    chains of elementwise kernels: with the model's RMSNorm modules on lkv_rmsnorm the logits equal the
+    HF forward's bit for bit; with HF's torch RMSNorm they differ from it in the last bits of the norms,
+    as the B = 1 step's do.  tok [B] is fed, logits [B, vocab] come out; the cache's host counters are the
+    caller's to advance (GenerateFastPath does)."""
 
     def __init__(self, model, cache: TurboQuantCache, B: int):
         import sys
@@ -253,7 +259,11 @@ class BatchedEngine:
         self.Hq, self.Hkv = cfg.num_attention_heads, cfg.num_key_value_heads
         self.max_len = cache.attn_max_len(0)
         layers = model.model.layers
-        self._rope = sys.modules[type(layers[0].self_attn).__module__].apply_rotary_pos_emb
+        attn_module = type(layers[0].self_attn).__module__
+        self._rope = sys.modules[attn_module].apply_rotary_pos_emb
+        # the standard rotate-half form (modeling_mistral.py:51-81, the same in modeling_llama) runs as one
+        # lkv_rope_f16 launch; other model families keep their own function
+        self._fused_rope = attn_module.rsplit(".", 1)[-1] in ("modeling_mistral", "modeling_llama") and self.D == 128
         with torch.no_grad():
             pos = torch.arange(self.max_len, device=self.dev).unsqueeze(0)
             dummy = torch.zeros(1, 1, self.D, device=self.dev, dtype=torch.float16)
@@ -276,11 +286,17 @@ class BatchedEngine:
         c, B, D = self.cache, self.B, self.D
         at = layer.self_attn
         residual = x
-        h = layer.input_layernorm(x)
-        q = at.q_proj(h).view(B, 1, -1, D).transpose(1, 2)
-        k = at.k_proj(h).view(B, 1, -1, D).transpose(1, 2)
-        v = at.v_proj(h).view(B, 1, -1, D).transpose(1, 2)
-        q, k = self._rope(q, k, cos, sin)
+        h = self._norm(layer.input_layernorm, x)
+        qp, kp, vp = at.q_proj(h), at.k_proj(h), at.v_proj(h)
+        fused = (self._fused_rope and qp.dtype == torch.float16 and kp.dtype == torch.float16
+                 and qp.is_contiguous() and kp.is_contiguous())
+        if fused:  # in place on the fresh projection outputs, one launch for both
+            kernels.rope_f16_(qp.view(B, self.Hq, D), kp.view(B, self.Hkv, D), cos.view(-1), sin.view(-1))
+        q = qp.view(B, 1, -1, D).transpose(1, 2)
+        k = kp.view(B, 1, -1, D).transpose(1, 2)
+        v = vp.view(B, 1, -1, D).transpose(1, 2)
+        if not fused:
+            q, k = self._rope(q, k, cos, sin)
         k16, v16 = k.to(torch.float16), v.to(torch.float16)
         kernels.tq_cache_append(k16.reshape(B, self.Hkv, D).contiguous(), v16.reshape(B, self.Hkv, D).contiguous(),
                                 c._k_hot[i], c._v_hot[i], c._k_codes[i], c._k_norms[i], c._v_codes[i], c._v_norms[i],
@@ -292,8 +308,21 @@ class BatchedEngine:
         o = self.attn.view(B, self.Hq, 1, D).transpose(1, 2).contiguous().to(q.dtype).reshape(B, 1, -1)
         x = residual + at.o_proj(o)
         residual = x
-        x = residual + layer.mlp(layer.post_attention_layernorm(x))
+        x = residual + layer.mlp(self._norm(layer.post_attention_layernorm, x))
         return x
+
+    @staticmethod
+    def _norm(mod, x: torch.Tensor) -> torch.Tensor:
+        """HF's Mistral / Llama RMSNorm on fp16 as one lkv_rmsnorm launch (the summation order of the B = 1
+        step's fused RMSNorm; HF's torch RMSNorm runs seven kernels and sums in another order, so its last bits
+        can differ), any other norm module as it is."""
+        from . import kernels
+
+        w = getattr(mod, "weight", None)
+        if (type(mod).__name__ in _HF_RMSNORMS and x.dtype == torch.float16 and w is not None
+                and w.dtype == torch.float16 and w.numel() == x.shape[-1] and x.shape[-1] % 8 == 0):
+            return kernels.rms_norm(x, w, mod.variance_epsilon)
+        return mod(x)
 
     def _step(self) -> None:
         m = self.model
@@ -302,7 +331,7 @@ class BatchedEngine:
         sin = self.sin.index_select(0, self.pos64).unsqueeze(0)
         for i, layer in enumerate(m.model.layers):
             x = self._layer(i, layer, x, cos, sin)
-        logits = m.lm_head(m.model.norm(x))
+        logits = m.lm_head(self._norm(m.model.norm, x))
         if self.logits is None:
             self.logits = torch.empty_like(logits)
         self.logits.copy_(logits)

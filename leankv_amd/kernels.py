@@ -607,6 +607,23 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return rms_norm_out(x, weight, eps, torch.empty_like(x, memory_format=torch.contiguous_format))
 
 
+# ------------------------------------------------------------------ RoPE
+def rope_f16_(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> None:
+    """In place: q [B, Hq, 128] and k [B, Hkv, 128] (contiguous fp16) rotated by the 128 fp16 factors of one
+    position (cos, sin: 128 elements each), HF apply_rotary_pos_emb on fp16 tensors bit for bit (lkv_rope_f16)."""
+    require_cuda(q, k, cos, sin)
+    if any(t.dtype != torch.float16 for t in (q, k, cos, sin)):
+        raise LeanKVError("rope_f16: q, k, cos and sin must be float16")
+    if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[-1] != HEAD_DIM or k.shape[-1] != HEAD_DIM:
+        raise LeanKVError("rope_f16: q and k must be [B, H, %d] with the same B" % HEAD_DIM)
+    if not (q.is_contiguous() and k.is_contiguous() and cos.is_contiguous() and sin.is_contiguous()):
+        raise LeanKVError("rope_f16: q, k, cos and sin must be contiguous")
+    if cos.numel() != HEAD_DIM or sin.numel() != HEAD_DIM:
+        raise LeanKVError("rope_f16: cos and sin must hold %d factors" % HEAD_DIM)
+    check(_lib_handle().lkv_rope_f16(ptr(q), ptr(k), ptr(cos), ptr(sin), q.shape[0], q.shape[1], k.shape[1],
+                                     stream_handle(q.device)), "lkv_rope_f16")
+
+
 # ------------------------------------------------------- torch custom ops
 _LIB_DEF = None
 

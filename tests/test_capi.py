@@ -95,6 +95,12 @@ def test_invalid_arguments_rejected_without_launch():
                                    1024, None) == -1
     assert "workspace" in _lib.last_error()
     assert lib.lkv_tq_prefill_attn_workspace_bytes(1, 32, 8, 4096, 64) >= 32 * 4096 * 128 * 2
+    # RoPE: negative sizes, null factors
+    assert lib.lkv_rope_f16(p, p, p, p, -1, 32, 8, None) == -1
+    assert "out of range" in _lib.last_error()
+    assert lib.lkv_rope_f16(p, p, None, p, 2, 32, 8, None) == -1
+    assert "null" in _lib.last_error()
+    assert lib.lkv_rope_f16(None, None, None, None, 0, 32, 8, None) == 0  # nothing to do, nothing touched
     # batched sparse GEMM: N not a multiple of 8, workspace too small for a multi-chunk problem
     assert lib.lkv_sparse_gemm_batched(p, p, 0.1, 4, 12, 16, p, p, 1 << 20, None) == -1
     assert "multiple of 8" in _lib.last_error()

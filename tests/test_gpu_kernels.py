@@ -216,6 +216,38 @@ def test_rms_norm_matches_hf_rounding(cuda, M, Z):
     assert (y != ref).float().mean() < 0.02  # almost all bit-equal; the rest one rounding step apart
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,pos", [(1, 32, 8, 0), (4, 32, 8, 777), (16, 32, 8, 4095), (3, 8, 2, 12345)])
+def test_rope_f16_equals_hf_apply_rotary_pos_emb(cuda, B, Hq, Hkv, pos):
+    """lkv_rope_f16 (in place, q and k in one launch) vs transformers' own apply_rotary_pos_emb on the same fp16
+    tensors and the model's rotary factors at `pos` (modeling_mistral.py:51-81), bit for bit; a Llama-scaled
+    rotary embedding too."""
+    from transformers import LlamaConfig, MistralConfig
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+    from transformers.models.mistral.modeling_mistral import MistralRotaryEmbedding, apply_rotary_pos_emb
+
+    from leankv_amd import kernels
+
+    cfgs = [(MistralRotaryEmbedding, MistralConfig(hidden_size=Hq * 128, num_attention_heads=Hq,
+                                                   num_key_value_heads=Hkv, rope_theta=1e6)),
+            (LlamaRotaryEmbedding, LlamaConfig(hidden_size=Hq * 128, num_attention_heads=Hq, num_key_value_heads=Hkv,
+                                               max_position_embeddings=131072,
+                                               rope_scaling={"rope_type": "llama3", "factor": 8.0,
+                                                             "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                                                             "original_max_position_embeddings": 8192}))]
+    g = torch.Generator().manual_seed(B * 1000 + pos)
+    for cls, cfg in cfgs:
+        rot = cls(config=cfg).to(cuda)
+        dummy = torch.zeros(1, 1, 128, device=cuda, dtype=torch.float16)
+        cos, sin = rot(dummy, torch.tensor([[pos]], device=cuda))  # [1, 1, 128] fp16
+        q = (torch.randn(B, Hq, 1, 128, generator=g) * 4).half().to(cuda)
+        k = (torch.randn(B, Hkv, 1, 128, generator=g) * 4).half().to(cuda)
+        q_ref, k_ref = apply_rotary_pos_emb(q, k, cos, sin)
+        qk, kk = q.reshape(B, Hq, 128).clone(), k.reshape(B, Hkv, 128).clone()
+        kernels.rope_f16_(qk, kk, cos.reshape(-1).contiguous(), sin.reshape(-1).contiguous())
+        assert torch.equal(qk, q_ref.reshape(B, Hq, 128)), cls.__name__
+        assert torch.equal(kk, k_ref.reshape(B, Hkv, 128)), cls.__name__
+
+
 # ----------------------------------------------------------------- TurboQuant
 def _kv(shape, seed, outliers=(0, 31, 64, 127)):
     g = torch.Generator().manual_seed(seed)
