@@ -138,6 +138,33 @@ size_t lkv_sparse_gemm_batched_workspace_bytes(int64_t B, int64_t N, int64_t Z);
 int lkv_sparse_gemm_batched(const void* x, const void* w, float threshold, int64_t B, int64_t N, int64_t Z,
                             void* y, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Up to 3 batched_sparse_gemm products of one x [B][Z] in one launch (a block
+ * reads its share of x once), each product's arithmetic that of its own
+ * lkv_sparse_gemm_batched call (same chunking and summation order), with an
+ * epilogue in the chunk reduce:
+ *   LKV_EPI_NONE      y[s] = lkv_sparse_gemm_batched(x, w[s], thresholds[s]), s < n
+ *   LKV_EPI_SWIGLU    n == 2, N[0] == N[1]: y[0] = fp16(fp16(silu(fp16 g)) * fp16 u)
+ *                     for g, u the two products: HF MistralMLP's
+ *                     act_fn(gate_proj(x)) * up_proj(x) (modeling_mistral.py:46-47)
+ *   LKV_EPI_RESIDUAL  n == 1: y[0] = fp16(residual + fp16(product)), the decoder
+ *                     layer's fp16 residual add (modeling_mistral.py:233, 239);
+ *                     y[0] may be residual (in place), residual fp16 [B][N[0]]
+ * The q/k/v projections of an attention layer (leankv/teal/patching.py:169-180
+ * runs them as three dense calls at B > 1) and the gate/up pair are the
+ * products that share an input.  w, thresholds and N are host arrays of n
+ * entries, y of n (1 for LKV_EPI_SWIGLU); weights column-major as for
+ * lkv_sparse_gemm_batched, outputs fp16 [B][N[s]].  Products whose
+ * chunk sizes differ run as launches of their own.
+ */
+#define LKV_EPI_NONE 0
+#define LKV_EPI_SWIGLU 1
+#define LKV_EPI_RESIDUAL 2
+size_t lkv_sparse_gemm_batched_multi_workspace_bytes(int64_t B, int n, const int64_t* N, int64_t Z);
+int lkv_sparse_gemm_batched_multi(const void* x, int64_t B, int n, const void* const* w, const float* thresholds,
+                                  const int64_t* N, int64_t Z, int epilogue, const void* residual, void* const* y,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* TurboQuant (MSE variant), head_dim 128                                    */
 /* ------------------------------------------------------------------------ */

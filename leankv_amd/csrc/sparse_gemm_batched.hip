@@ -41,15 +41,37 @@ constexpr int kPad = kU * kSlots;
 typedef uint32_t u32x4b __attribute__((ext_vector_type(4)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
-struct BatchedArgs {
-  const uint16_t* x;  // [B][Z] fp16
+// A launch covers up to kMaxSeg products of the same x (the q, k and v
+// projections of a layer, or gate and up): each segment owns grid slabs
+// slab0 .. slab0 + nslab - 1 and computes exactly what a launch of its own
+// would (same chunking, same summation order).  kMaxSeg (3) as for the GEMV.
+enum { kEpiNone = 0, kEpiSwiglu = 1, kEpiResidual = 2 };
+
+struct BatchedSeg {
   const uint16_t* A;  // [Z][N] fp16 (column-major weight)
+  float* part;        // [B][nslab][nchunk][256] fp32 (unless direct)
+  uint16_t* y;        // [B][N] fp16
   uint32_t a_bytes;
   float t;
-  int B, N, Z, nchunk, nslab;
-  float* part;        // [B][nslab][nchunk][256] fp32 (nchunk > 1)
-  uint16_t* y;        // [B][N] fp16 (written directly when nchunk == 1)
+  int N, nslab, slab0;
 };
+
+struct BatchedArgs {
+  const uint16_t* x;    // [B][Z] fp16
+  const uint16_t* res;  // [B][N] fp16 residual (kEpiResidual; may be seg[0].y)
+  int B, Z, nchunk, nseg, epi;
+  int direct;           // one chunk and no epilogue: fp16 written by the GEMM kernel, no reduce
+  BatchedSeg seg[kMaxSeg];
+};
+
+// The segment owning grid slab gs.  Uniform selects over constant indices: a
+// dynamic index into the argument struct would copy it to scratch memory.
+__device__ __forceinline__ BatchedSeg seg_of(const BatchedArgs& P, int gs) {
+  BatchedSeg S = P.seg[0];
+  if (P.nseg > 1 && gs >= P.seg[1].slab0) S = P.seg[1];
+  if (P.nseg > 2 && gs >= P.seg[2].slab0) S = P.seg[2];
+  return S;
+}
 
 template <int NB, int BZ>
 __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P) {
@@ -61,11 +83,12 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
   __shared__ __align__(16) float s_red[kSlots * kBN];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int slab = blockIdx.x, chunk = blockIdx.y;
+  const BatchedSeg S = seg_of(P, blockIdx.x);
+  const int slab = blockIdx.x - S.slab0, chunk = blockIdx.y;
   const int b0 = blockIdx.z * NB;
   const int nb = min(NB, P.B - b0);
   const int z0 = chunk * BZ, n0 = slab * kBN;
-  const int Z = P.Z, N = P.N;
+  const int Z = P.Z, N = S.N;
 
   // ---- 0. the group's activations (0 past Z and past the last batch row).
   // Every load is issued before the first is used (address clamped to element
@@ -102,7 +125,7 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const float xv = s_x[b][base + tid];
-      const bool k = fabsf(xv) > P.t;
+      const bool k = fabsf(xv) > S.t;
       v[b] = k ? xv : 0.f;
       keep = keep || k;
     }
@@ -139,8 +162,8 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
   const int c = tid % kLPR, slot = tid / kLPR;
   const int col = n0 + 8 * c;
   const uint32_t row_bytes = static_cast<uint32_t>(N) * 2u;
-  const uint32_t col_bytes = col < N ? static_cast<uint32_t>(col) * 2u : P.a_bytes;  // past N: past the end (reads 0)
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.A), 0, P.a_bytes,
+  const uint32_t col_bytes = col < N ? static_cast<uint32_t>(col) * 2u : S.a_bytes;  // past N: past the end (reads 0)
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(S.A), 0, S.a_bytes,
                                                                       0x00020000);
   float acc[NB][8];
 #pragma unroll
@@ -207,10 +230,10 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
       float sum = 0.f;
 #pragma unroll
       for (int sl = 0; sl < kSlots; ++sl) sum += s_red[sl * kBN + tid];
-      if (P.nchunk == 1) {
-        if (n0 + tid < N) P.y[static_cast<size_t>(b0 + b) * N + n0 + tid] = f2h(sum);
+      if (P.direct) {
+        if (n0 + tid < N) S.y[static_cast<size_t>(b0 + b) * N + n0 + tid] = f2h(sum);
       } else {
-        P.part[((static_cast<size_t>(b0 + b) * P.nslab + slab) * P.nchunk + chunk) * kBN + tid] = sum;
+        S.part[((static_cast<size_t>(b0 + b) * S.nslab + slab) * P.nchunk + chunk) * kBN + tid] = sum;
       }
     }
     __syncthreads();
@@ -246,11 +269,12 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
   __shared__ int s_cnt[kNT / kWave];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int slab = blockIdx.x, chunk = blockIdx.y;
+  const BatchedSeg S = seg_of(P, blockIdx.x);
+  const int slab = blockIdx.x - S.slab0, chunk = blockIdx.y;
   const int b0 = blockIdx.z * kMB;
   const int nb = min(kMB, P.B - b0);
   const int z0 = chunk * BZ, n0 = slab * kBN;
-  const int Z = P.Z, N = P.N;
+  const int Z = P.Z, N = S.N;
 
   // ---- 0. the group's activations into registers, every load issued before
   // the first is used (address clamped to element 0, value selected after)
@@ -280,7 +304,7 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
     const int z = z0 + e * kNT + tid;
     bool keep = false;
 #pragma unroll
-    for (int b = 0; b < kMB; ++b) keep = keep || fabsf(xv[b][e]) > P.t;
+    for (int b = 0; b < kMB; ++b) keep = keep || fabsf(xv[b][e]) > S.t;
     keep = keep && z < Z;
     const uint64_t mask = wave_ballot(keep);
     if (lane == 0) s_cnt[wave] = __popcll(mask);
@@ -296,7 +320,7 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
       const int pos = off + lane_prefix(mask);
       s_idx[pos] = z;
 #pragma unroll
-      for (int b = 0; b < kMB; ++b) s_xh[b][pos] = f2h(fabsf(xv[b][e]) > P.t ? xv[b][e] : 0.f);  // exact
+      for (int b = 0; b < kMB; ++b) s_xh[b][pos] = f2h(fabsf(xv[b][e]) > S.t ? xv[b][e] : 0.f);  // exact
     }
     total += tot;
     __syncthreads();
@@ -315,8 +339,8 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
   const int c = tid % (kBN / 8), q = tid / (kBN / 8);  // column group (8 columns), entry quad
   const int col = n0 + 8 * c;
   const uint32_t row_bytes = static_cast<uint32_t>(N) * 2u;
-  const uint32_t col_bytes = col < N ? static_cast<uint32_t>(col) * 2u : P.a_bytes;  // past N: reads 0
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.A), 0, P.a_bytes,
+  const uint32_t col_bytes = col < N ? static_cast<uint32_t>(col) * 2u : S.a_bytes;  // past N: reads 0
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(S.A), 0, S.a_bytes,
                                                                       0x00020000);
   // Blocks past the list load through offsets past the descriptor's end (zeros,
   // no memory traffic): the loads stay unconditional, so no branch makes the
@@ -327,7 +351,7 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t off = static_cast<uint32_t>(s_idx[kc * kKB + 4 * q + r]) * row_bytes + col_bytes;
-      w[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? off : P.a_bytes, 0, 2);
+      w[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? off : S.a_bytes, 0, 2);
     }
   };
   // pairs (4q, 4q + 1) -> pair row 2q, (4q + 2, 4q + 3) -> 2q + 1; columns 8c .. 8c + 7
@@ -389,22 +413,36 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
     for (int i = 0; i < 4; ++i) {
       const int b = 4 * kg + i;
       if (b < nb) {
-        if (P.nchunk == 1) {
-          if (n0 + lc < N) P.y[static_cast<size_t>(b0 + b) * N + n0 + lc] = f2h(acc[t][i]);
+        if (P.direct) {
+          if (n0 + lc < N) S.y[static_cast<size_t>(b0 + b) * N + n0 + lc] = f2h(acc[t][i]);
         } else {
-          P.part[((static_cast<size_t>(b0 + b) * P.nslab + slab) * P.nchunk + chunk) * kBN + lc] = acc[t][i];
+          S.part[((static_cast<size_t>(b0 + b) * S.nslab + slab) * P.nchunk + chunk) * kBN + lc] = acc[t][i];
         }
       }
     }
   }
 }
 
-// y[b][n] = fp16 of the chunk partials summed in chunk order.
-__global__ __launch_bounds__(kNT) void batched_reduce_kernel(const float* __restrict__ part, int N, int nslab,
-                                                             int nchunk, uint16_t* __restrict__ y) {
-  const int n = blockIdx.x * kNT + threadIdx.x, b = blockIdx.y;
-  if (n >= N) return;
-  y[static_cast<size_t>(b) * N + n] = f2h(column_sum(part + static_cast<size_t>(b) * nslab * nchunk * kBN, n, nchunk));
+// y[b][n] = fp16 of the chunk partials summed in chunk order, through the
+// launch's epilogue: SwiGLU of the two segments' sums (gate, up; the grid
+// covers the first segment's columns), or the fp16 residual add
+// fp16(res + fp16(sum)) (res may be the output: each element is read, then
+// written, by one thread).
+static_assert(kBN == kNT, "a reduce block covers one slab");
+__global__ __launch_bounds__(kNT) void batched_reduce_kernel(BatchedArgs P) {
+  const BatchedSeg S = seg_of(P, blockIdx.x);
+  const int n = (blockIdx.x - S.slab0) * kBN + threadIdx.x, b = blockIdx.y;
+  if (n >= S.N) return;
+  const size_t row = static_cast<size_t>(S.nslab) * P.nchunk * kBN;  // partial floats per batch row
+  const size_t o = static_cast<size_t>(b) * S.N + n;
+  const float sum = column_sum(S.part + b * row, n, P.nchunk);
+  if (P.epi == kEpiSwiglu) {
+    S.y[o] = swiglu_f16(sum, column_sum(P.seg[1].part + b * row, n, P.nchunk));
+  } else if (P.epi == kEpiResidual) {
+    S.y[o] = f2h(h2f(P.res[o]) + h2f(f2h(sum)));
+  } else {
+    S.y[o] = f2h(sum);
+  }
 }
 
 template <int NB>
@@ -445,6 +483,128 @@ int batched_bz(int64_t B, int64_t N, int64_t Z) {
   return gemv_pick_bz(gemv_slabs(N) * groups, Z, 6);
 }
 
+// Partial floats of one product of B rows at its own chunk size.
+size_t product_floats(int64_t B, int64_t N, int64_t Z) {
+  return static_cast<size_t>(B) * gemv_part_floats(N, gemv_chunks(Z, batched_bz(B, N, Z)));
+}
+
+// One GEMM launch (none when Z == 0) and one reduce (none when direct) for n
+// products of x whose chunk sizes agree; partials one product after another
+// from ws.  Shapes are checked by the caller.
+bool launch_products(const void* x, int64_t B, int64_t Z, int n, const void* const* w, const float* t,
+                     const int64_t* N, void* const* y, int epi, const void* res, float* ws, hipStream_t st) {
+  const int bz = batched_bz(B, N[0], Z);
+  const int64_t nchunk = Z > 0 ? gemv_chunks(Z, bz) : 0;
+  BatchedArgs P = {};
+  P.x = static_cast<const uint16_t*>(x);
+  P.res = static_cast<const uint16_t*>(res);
+  P.B = static_cast<int>(B);
+  P.Z = static_cast<int>(Z);
+  P.nchunk = static_cast<int>(nchunk);
+  P.nseg = n;
+  P.epi = epi;
+  P.direct = nchunk == 1 && epi == kEpiNone;
+  int slabs = 0;
+  size_t off = 0;
+  for (int s = 0; s < n; ++s) {
+    BatchedSeg& S = P.seg[s];
+    S.A = static_cast<const uint16_t*>(w[s]);
+    S.part = ws + off;
+    S.y = s < (epi == kEpiSwiglu ? 1 : n) ? static_cast<uint16_t*>(y[s]) : nullptr;  // SwiGLU: one output
+    S.a_bytes = static_cast<uint32_t>(N[s] * Z * 2);
+    S.t = t[s];
+    S.N = static_cast<int>(N[s]);
+    S.nslab = static_cast<int>(gemv_slabs(N[s]));
+    S.slab0 = slabs;
+    slabs += S.nslab;
+    off += static_cast<size_t>(B) * gemv_part_floats(N[s], nchunk);
+  }
+  if (Z > 0) {
+    const int nbr = group_rows(B);
+    const dim3 grid(static_cast<unsigned>(slabs), static_cast<unsigned>(nchunk),
+                    static_cast<unsigned>((B + nbr - 1) / nbr));
+    bool ok;
+    if (use_mfma(B)) {
+      switch (bz) {
+        case 256: hipLaunchKernelGGL(sparse_gemm_mfma_kernel<256>, grid, dim3(kNT), 0, st, P); ok = true; break;
+        case 512: hipLaunchKernelGGL(sparse_gemm_mfma_kernel<512>, grid, dim3(kNT), 0, st, P); ok = true; break;
+        case 1024: hipLaunchKernelGGL(sparse_gemm_mfma_kernel<1024>, grid, dim3(kNT), 0, st, P); ok = true; break;
+        default: ok = false;
+      }
+    } else {
+      ok = nbr == 1 ? launch_nb<1>(P, bz, grid, st)
+         : nbr == 2 ? launch_nb<2>(P, bz, grid, st)
+         : nbr == 4 ? launch_nb<4>(P, bz, grid, st)
+                    : launch_nb<8>(P, bz, grid, st);
+    }
+    if (!ok) return false;
+  }
+  if (!P.direct) {  // Z == 0: the reduce over zero chunks writes the epilogue of empty sums (a kernel, graph-safe)
+    const int rslabs = epi == kEpiSwiglu ? P.seg[0].nslab : slabs;
+    hipLaunchKernelGGL(batched_reduce_kernel, dim3(static_cast<unsigned>(rslabs), static_cast<unsigned>(B)), dim3(kNT),
+                       0, st, P);
+  }
+  return true;
+}
+
+// The shared checks and launches of lkv_sparse_gemm_batched(_multi): products
+// whose chunk sizes differ run as launches of their own (the epilogues pair
+// products of one shape, which always agree).
+int batched_products(const char* who, const void* x, int64_t B, int n, const void* const* w, const float* t,
+                     const int64_t* N, int64_t Z, int epi, const void* res, void* const* y, void* workspace,
+                     size_t workspace_bytes, hipStream_t st) {
+  LKV_REQUIRE(n >= 1 && n <= kMaxSeg, "%s: %d products (1 to %d)", who, n, kMaxSeg);
+  LKV_REQUIRE(w && t && N && y, "%s: null product array", who);
+  LKV_REQUIRE(epi == kEpiNone || (epi == kEpiSwiglu && n == 2) || (epi == kEpiResidual && n == 1),
+              "%s: epilogue %d with %d products (SwiGLU pairs 2, the residual add takes 1)", who, epi, n);
+  LKV_REQUIRE(B >= 0 && Z >= 0, "%s: negative size B=%lld Z=%lld", who, (long long)B, (long long)Z);
+  LKV_REQUIRE(B < 65536, "%s: B=%lld too large", who, (long long)B);
+  for (int s = 0; s < n; ++s) {
+    LKV_REQUIRE(N[s] >= 0, "%s: negative size N=%lld", who, (long long)N[s]);
+    LKV_REQUIRE(N[s] % 8 == 0, "%s: N=%lld must be a multiple of 8 (16-byte weight rows)", who, (long long)N[s]);
+    LKV_REQUIRE(N[s] * Z * 2 < (1ll << 32), "%s: weight of %lld bytes exceeds the 4 GiB descriptor range", who,
+                (long long)(N[s] * Z * 2));
+  }
+  LKV_REQUIRE(epi != kEpiSwiglu || N[0] == N[1], "%s: SwiGLU of products of %lld and %lld columns", who,
+              (long long)N[0], (long long)N[1]);
+  int64_t total = 0;
+  for (int s = 0; s < n; ++s) total += N[s];
+  if (B == 0 || total == 0) return LKV_OK;
+  // x and the weights are not read when Z == 0 (empty sums)
+  LKV_REQUIRE(x || Z == 0, "%s: null pointer", who);
+  const int nout = epi == kEpiSwiglu ? 1 : n;  // SwiGLU writes one output for its two products
+  for (int s = 0; s < n; ++s)
+    LKV_REQUIRE(N[s] == 0 || ((Z == 0 || (w[s] && aligned16(w[s]))) && (s >= nout || (y[s] && aligned16(y[s])))),
+                "%s: weight and output must be non-null and 16-byte aligned", who);
+  LKV_REQUIRE(epi != kEpiResidual || res, "%s: null residual", who);
+  // partials are written unless every product is one chunk without epilogue
+  size_t floats = 0;
+  bool same = true, need_ws = false;
+  for (int s = 0; s < n && Z > 0; ++s) {
+    if (N[s] == 0) continue;
+    const int bz = batched_bz(B, N[s], Z);
+    floats += product_floats(B, N[s], Z);
+    same = same && bz == batched_bz(B, N[0], Z);
+    need_ws = need_ws || gemv_chunks(Z, bz) > 1 || epi != kEpiNone;
+  }
+  const size_t need = floats * sizeof(float) + 256;
+  LKV_REQUIRE(!need_ws || (workspace && workspace_bytes >= need && aligned16(workspace)),
+              "%s: workspace of %zu bytes (16-byte aligned) required, got %zu", who, need, workspace_bytes);
+  float* ws = static_cast<float*>(workspace);
+  if (same && N[0] > 0) {
+    LKV_REQUIRE(launch_products(x, B, Z, n, w, t, N, y, epi, res, ws, st), "%s: no kernel for this chunk size", who);
+  } else {
+    for (int s = 0; s < n; ++s) {
+      if (N[s] == 0) continue;
+      LKV_REQUIRE(launch_products(x, B, Z, 1, w + s, t + s, N + s, y + s, epi, res, ws, st),
+                  "%s: no kernel for this chunk size", who);
+      ws += Z > 0 ? product_floats(B, N[s], Z) : 0;
+    }
+  }
+  LKV_LAUNCH_CHECK(who);
+  return LKV_OK;
+}
+
 }  // namespace
 }  // namespace lkv
 
@@ -452,71 +612,27 @@ using namespace lkv;
 
 extern "C" size_t lkv_sparse_gemm_batched_workspace_bytes(int64_t B, int64_t N, int64_t Z) {
   if (B <= 0 || N <= 0 || Z <= 0) return 256;
-  const int64_t nchunk = gemv_chunks(Z, batched_bz(B, N, Z));
-  return static_cast<size_t>(B) * gemv_part_floats(N, nchunk) * sizeof(float) + 256;
+  return product_floats(B, N, Z) * sizeof(float) + 256;
 }
 
 extern "C" int lkv_sparse_gemm_batched(const void* x, const void* w, float threshold, int64_t B, int64_t N,
                                        int64_t Z, void* y, void* workspace, size_t workspace_bytes, void* stream) {
-  LKV_REQUIRE(B >= 0 && N >= 0 && Z >= 0, "sparse_gemm_batched: negative size B=%lld N=%lld Z=%lld", (long long)B,
-              (long long)N, (long long)Z);
-  LKV_REQUIRE(N % 8 == 0, "sparse_gemm_batched: N=%lld must be a multiple of 8 (16-byte weight rows)", (long long)N);
-  LKV_REQUIRE(N * Z * 2 < (1ll << 32), "sparse_gemm_batched: weight of %lld bytes exceeds the 4 GiB descriptor range",
-              (long long)(N * Z * 2));
-  LKV_REQUIRE(B < 65536, "sparse_gemm_batched: B=%lld too large", (long long)B);
-  if (B == 0 || N == 0) return LKV_OK;
-  LKV_REQUIRE(x && w && y, "sparse_gemm_batched: null pointer");
-  LKV_REQUIRE(aligned16(w) && aligned16(y), "sparse_gemm_batched: weight and output must be 16-byte aligned");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (Z == 0) {  // empty sums: the reduce kernel over zero chunks writes 0 (a kernel, so graph capture stays safe)
-    hipLaunchKernelGGL(batched_reduce_kernel, dim3(static_cast<unsigned>((N + kNT - 1) / kNT), static_cast<unsigned>(B)),
-                       dim3(kNT), 0, st, static_cast<const float*>(y), static_cast<int>(N), 1, 0,  // never read
-                       static_cast<uint16_t*>(y));
-    LKV_LAUNCH_CHECK("sparse_gemm_batched zero");
-    return LKV_OK;
-  }
-  const int bz = batched_bz(B, N, Z);
-  const int64_t nslab = gemv_slabs(N), nchunk = gemv_chunks(Z, bz);
-  const size_t need = lkv_sparse_gemm_batched_workspace_bytes(B, N, Z);
-  LKV_REQUIRE(nchunk == 1 || (workspace && workspace_bytes >= need && aligned16(workspace)),
-              "sparse_gemm_batched: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
-              workspace_bytes);
-  const int nbr = group_rows(B);
-  BatchedArgs P;
-  P.x = static_cast<const uint16_t*>(x);
-  P.A = static_cast<const uint16_t*>(w);
-  P.a_bytes = static_cast<uint32_t>(N * Z * 2);
-  P.t = threshold;
-  P.B = static_cast<int>(B);
-  P.N = static_cast<int>(N);
-  P.Z = static_cast<int>(Z);
-  P.nchunk = static_cast<int>(nchunk);
-  P.nslab = static_cast<int>(nslab);
-  P.part = static_cast<float*>(workspace);
-  P.y = static_cast<uint16_t*>(y);
-  const dim3 grid(static_cast<unsigned>(nslab), static_cast<unsigned>(nchunk),
-                  static_cast<unsigned>((B + nbr - 1) / nbr));
-  bool ok;
-  if (use_mfma(B)) {
-    switch (bz) {
-      case 256: hipLaunchKernelGGL(sparse_gemm_mfma_kernel<256>, grid, dim3(kNT), 0, st, P); ok = true; break;
-      case 512: hipLaunchKernelGGL(sparse_gemm_mfma_kernel<512>, grid, dim3(kNT), 0, st, P); ok = true; break;
-      case 1024: hipLaunchKernelGGL(sparse_gemm_mfma_kernel<1024>, grid, dim3(kNT), 0, st, P); ok = true; break;
-      default: ok = false;
-    }
-  } else {
-    ok = nbr == 1 ? launch_nb<1>(P, bz, grid, st)
-       : nbr == 2 ? launch_nb<2>(P, bz, grid, st)
-       : nbr == 4 ? launch_nb<4>(P, bz, grid, st)
-                  : launch_nb<8>(P, bz, grid, st);
-  }
-  LKV_REQUIRE(ok, "sparse_gemm_batched: no kernel for chunk %d", bz);
-  LKV_LAUNCH_CHECK("sparse_gemm_batched");
-  if (nchunk > 1) {
-    hipLaunchKernelGGL(batched_reduce_kernel, dim3(static_cast<unsigned>((N + kNT - 1) / kNT), static_cast<unsigned>(B)),
-                       dim3(kNT), 0, st, P.part, static_cast<int>(N), static_cast<int>(nslab),
-                       static_cast<int>(nchunk), P.y);
-    LKV_LAUNCH_CHECK("sparse_gemm_batched reduce");
-  }
-  return LKV_OK;
+  return batched_products("sparse_gemm_batched", x, B, 1, &w, &threshold, &N, Z, kEpiNone, nullptr, &y, workspace,
+                          workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t lkv_sparse_gemm_batched_multi_workspace_bytes(int64_t B, int n, const int64_t* N, int64_t Z) {
+  if (B <= 0 || Z <= 0 || n <= 0 || n > kMaxSeg || !N) return 256;
+  size_t floats = 0;
+  for (int s = 0; s < n; ++s)
+    if (N[s] > 0) floats += product_floats(B, N[s], Z);
+  return floats * sizeof(float) + 256;
+}
+
+extern "C" int lkv_sparse_gemm_batched_multi(const void* x, int64_t B, int n, const void* const* w,
+                                             const float* thresholds, const int64_t* N, int64_t Z, int epilogue,
+                                             const void* residual, void* const* y, void* workspace,
+                                             size_t workspace_bytes, void* stream) {
+  return batched_products("sparse_gemm_batched_multi", x, B, n, w, thresholds, N, Z, epilogue, residual, y,
+                          workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }

@@ -242,7 +242,8 @@ class BatchedEngine:
     kernels, o_proj, residual adds, the (patched) MLP and lm_head -- with the position on the device, so the
     whole step replays without the host.  RMSNorm runs as one lkv_rmsnorm launch (the B = 1 step's
     arithmetic) and RoPE as one lkv_rope_f16 launch (HF's fp16 arithmetic bit for bit) instead of HF's
-    chains of elementwise kernels: with the model's RMSNorm modules on lkv_rmsnorm the logits equal the
+    chains of elementwise kernels, and the residual adds run in the reduce of the patched o_proj / down_proj
+    launches (the same bits as the add): with the model's RMSNorm modules on lkv_rmsnorm the logits equal the
     HF forward's bit for bit; with HF's torch RMSNorm they differ from it in the last bits of the norms,
     as the B = 1 step's do.  tok [B] is fed, logits [B, vocab] come out; the cache's host counters are the
     caller's to advance (GenerateFastPath does)."""
@@ -306,10 +307,39 @@ class BatchedEngine:
                                    c._v_hot[i], c.PiK[i], c.PiV[i], c.centroids, c.bits, self.len32, self.max_len,
                                    float(at.scaling), self.attn, self.attn_ws)
         o = self.attn.view(B, self.Hq, 1, D).transpose(1, 2).contiguous().to(q.dtype).reshape(B, 1, -1)
-        x = residual + at.o_proj(o)
+        x = self._residual_proj(at.o_proj, o, residual)
         residual = x
-        x = residual + layer.mlp(self._norm(layer.post_attention_layernorm, x))
-        return x
+        return self._residual_mlp(layer.mlp, self._norm(layer.post_attention_layernorm, x), residual)
+
+    def _residual_proj(self, proj, inp: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+        """residual + proj(inp).  A TEAL-patched projection that sends these B rows to the batched kernel
+        (threshold 0) runs as one launch with HF's fp16 residual add in its reduce: the same bits as the
+        projection's forward followed by torch's add."""
+        from . import kernels
+        from .teal.patching import _skinny_dense
+
+        B, w = self.B, getattr(proj, "weight", None)
+        if (getattr(proj, "_teal_patched", False) and proj.bias is None and w is not None and w.dim() == 2
+                and w.dtype == torch.float16 and inp.dtype == torch.float16 and residual.dtype == torch.float16
+                and inp.numel() == B * w.shape[1] and residual.numel() == B * w.shape[0]
+                and residual.is_contiguous() and _skinny_dense(B, w.shape[0], w.shape[1])):
+            out = torch.empty_like(residual)
+            kernels.sparse_gemm_batched_multi_out(inp.reshape(B, -1).contiguous(), [w], [0.0], [out.view(B, -1)],
+                                                  kernels.EPI_RESIDUAL, residual.view(B, -1))
+            return out
+        return residual + proj(inp)
+
+    def _residual_mlp(self, mlp, h: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+        """residual + mlp(h).  For a fused TEAL MLP whose gate/up + SwiGLU takes these rows as one batched launch,
+        the down projection then runs through _residual_proj: the MLP forward's own calls, with the add fused."""
+        from .teal.patching import _gateup_rows
+
+        down = getattr(mlp, "down_proj", None)
+        if getattr(mlp, "_teal_fused", False) and down is not None:
+            a = _gateup_rows(mlp, h)
+            if a is not None:
+                return self._residual_proj(down, a, residual)
+        return residual + mlp(h)
 
     @staticmethod
     def _norm(mod, x: torch.Tensor) -> torch.Tensor:

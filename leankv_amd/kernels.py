@@ -102,6 +102,67 @@ def sparse_gemm_batched(x: torch.Tensor, weight: torch.Tensor, threshold: float)
     return sparse_gemm_batched_out(x, weight, threshold, out)
 
 
+EPI_NONE, EPI_SWIGLU, EPI_RESIDUAL = 0, 1, 2
+
+
+def sparse_gemm_batched_multi_out(x: torch.Tensor, weights, thresholds, outs, epilogue: int = EPI_NONE,
+                                  residual: torch.Tensor | None = None):
+    """Up to 3 sparse_gemm_batched products of one x[B, Z] in one launch (lkv_sparse_gemm_batched_multi), each
+    equal to its own sparse_gemm_batched call, with an epilogue in the reduce: EPI_NONE (outs[s] = product s),
+    EPI_SWIGLU (two products g, u of one shape: outs[0] = fp16(fp16(silu(fp16 g)) * fp16 u)) or EPI_RESIDUAL
+    (one product: outs[0] = fp16(residual + fp16 product); outs[0] may be residual)."""
+    import ctypes
+
+    n = len(weights)
+    if not 1 <= n <= 3 or len(thresholds) != n:
+        raise LeanKVError("sparse_gemm_batched_multi: 1 to 3 weights with one threshold each")
+    shapes = [colmajor_rows(w) for w in weights]
+    Z = shapes[0][1]
+    if any(z != Z for _, z in shapes):
+        raise LeanKVError("sparse_gemm_batched_multi: weights of different input sizes %s" % (shapes,))
+    n_out = 1 if epilogue == EPI_SWIGLU else n
+    if len(outs) != n_out:
+        raise LeanKVError("sparse_gemm_batched_multi: %d outputs expected, got %d" % (n_out, len(outs)))
+    require_cuda(x, *weights, *outs, residual)
+    if x.dtype != torch.float16 or any(t.dtype != torch.float16 for t in (*weights, *outs)):
+        raise LeanKVError("sparse_gemm_batched_multi: x, weights and outputs must be float16")
+    if x.dim() != 2 or x.shape[1] != Z or not x.is_contiguous():
+        raise LeanKVError("sparse_gemm_batched_multi: x must be a contiguous float16 [B, %d] tensor" % Z)
+    B = x.shape[0]
+    for o, (N, _) in zip(outs, shapes):
+        if tuple(o.shape) != (B, N) or not o.is_contiguous():
+            raise LeanKVError("sparse_gemm_batched_multi: outputs must be contiguous float16 [%d, %d]" % (B, N))
+    if epilogue == EPI_RESIDUAL:
+        if residual is None or residual.dtype != torch.float16 or tuple(residual.shape) != (B, shapes[0][0]) \
+                or not residual.is_contiguous():
+            raise LeanKVError("sparse_gemm_batched_multi: residual must be a contiguous float16 [%d, %d] tensor"
+                              % (B, shapes[0][0]))
+    elif residual is not None:
+        raise LeanKVError("sparse_gemm_batched_multi: a residual needs the residual epilogue")
+    lib = _lib_handle()
+    n_arr = (ctypes.c_int64 * n)(*[N for N, _ in shapes])
+    nbytes = lib.lkv_sparse_gemm_batched_multi_workspace_bytes(B, n, n_arr, Z)
+    ws = workspaces.get(x.device, "gemm_bm", nbytes)
+    check(
+        lib.lkv_sparse_gemm_batched_multi(ptr(x), B, n, (ctypes.c_void_p * n)(*[ptr(w) for w in weights]),
+                                          (ctypes.c_float * n)(*[float(t) for t in thresholds]), n_arr, Z,
+                                          int(epilogue), ptr(residual),
+                                          (ctypes.c_void_p * n_out)(*[ptr(o) for o in outs]), ptr(ws), ws.numel(),
+                                          stream_handle(x.device)),
+        "lkv_sparse_gemm_batched_multi",
+    )
+    return outs
+
+
+def sparse_gemm_batched_multi(x: torch.Tensor, weights, thresholds, epilogue: int = EPI_NONE,
+                              residual: torch.Tensor | None = None):
+    """sparse_gemm_batched_multi_out into fresh outputs (the list of them)."""
+    N = [colmajor_rows(w)[0] for w in weights]
+    outs = [torch.empty(x.shape[0], n, dtype=torch.float16, device=x.device)
+            for n in (N[:1] if epilogue != EPI_NONE else N)]
+    return sparse_gemm_batched_multi_out(x, weights, thresholds, outs, epilogue, residual)
+
+
 def sparse_gemv_partials(x: torch.Tensor, w_gate: torch.Tensor, t_gate: float, w_up: torch.Tensor | None = None,
                          t_up: float = 0.0, out: torch.Tensor | None = None) -> torch.Tensor:
     """Split-K partial sums only: fp32 [mats, N/256 slabs, chunks, 256] (mats = 2 with w_up).

@@ -4,10 +4,13 @@ Drop-in for leankv/teal/kernels/sparse_gemv.py:
   sparse_gemv(x, weight, threshold, sparsity_bin)        (:143-181)
   batched_sparse_gemm(x, weight, threshold, sparsity_bin) (:184-226)
   prepare_weight_for_sparse_gemv(weight)                 (:229-234)
-plus two fusions with no single reference counterpart: sparse_gateup_swiglu
+plus fusions with no single reference counterpart: sparse_gateup_swiglu
 (the gate and up sparse_gemv calls of a TEAL-patched Mistral MLP and its
-SwiGLU, x read once) and sparse_qkv (the q, k and v sparse_gemv calls of an
-attention layer, x read once).
+SwiGLU, x read once), sparse_qkv (the q, k and v sparse_gemv calls of an
+attention layer, x read once) and their dense forms for a few decode rows,
+batched_qkv and batched_gateup_swiglu (the batched_sparse_gemm calls with
+threshold 0 that the reference's dense dispatch at B > 1 stands for, one
+launch each).
 
 These are the dispatcher boundary of the TEAL path: each call goes through
 torch.ops.leankv (leankv_amd.kernels registers the ops, GPU + Meta), as the
@@ -68,3 +71,16 @@ def sparse_qkv(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.Te
     if xh.dtype != torch.float16:
         xh = xh.to(torch.float16)
     return torch.ops.leankv.sparse_qkv(xh, wq, wk, wv, float(tq), float(tk), float(tv))
+
+
+def batched_qkv(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor):
+    """fp16 (q, k, v) [rows, N_s] of x[rows, Z] through three column-major weights, threshold 0, one launch: each
+    equal to its own batched_sparse_gemm(x, w, 0.0) call bit for bit."""
+    return tuple(_k.sparse_gemm_batched_multi(x.to(torch.float16).contiguous(), [wq, wk, wv], [0.0, 0.0, 0.0]))
+
+
+def batched_gateup_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """fp16 [rows, N] = silu(gate(x)) * up(x) of x[rows, Z] with the fp16 roundings of HF's eager MLP, threshold 0,
+    one launch: equal to F.silu(batched_sparse_gemm(x, w_gate, 0.0)) * batched_sparse_gemm(x, w_up, 0.0)."""
+    return _k.sparse_gemm_batched_multi(x.to(torch.float16).contiguous(), [w_gate, w_up], [0.0, 0.0],
+                                        _k.EPI_SWIGLU)[0]

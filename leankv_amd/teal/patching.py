@@ -17,7 +17,9 @@ two projections and the SwiGLU run as one fused HIP kernel reading x once
 (``fuse_mlp=False`` turns this off), and when q_proj, k_proj and v_proj are
 all patched, the three run as one launch reading x once (``fuse_qkv=False``
 turns this off): q_proj computes all three and k_proj / v_proj hand back
-their share when called on the same input tensor.
+their share when called on the same input tensor.  Both fusions also take a
+few decode rows (B > 1): the dense products as one batched launch, with the
+SwiGLU in its reduce for gate/up, each result equal to the unfused calls'.
 """
 
 from __future__ import annotations
@@ -28,8 +30,8 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from .kernels.sparse_gemv import (batched_sparse_gemm, prepare_weight_for_sparse_gemv, sparse_gateup_swiglu, sparse_gemv,
-                                  sparse_qkv)
+from .kernels.sparse_gemv import (batched_gateup_swiglu, batched_qkv, batched_sparse_gemm, prepare_weight_for_sparse_gemv,
+                                  sparse_gateup_swiglu, sparse_gemv, sparse_qkv)
 from .sparse_fns import SparsifyFn, compute_threshold_for_sparsity
 
 PROJ_NAMES = ["q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"]
@@ -114,6 +116,19 @@ def apply_teal(
     return sparsifiers
 
 
+def _rows(x: torch.Tensor, Z: int) -> int:
+    """Rows of x as a [rows, Z] matrix (0 when its last dim is not Z)."""
+    return x.numel() // Z if x.dim() > 0 and x.shape[-1] == Z and Z > 0 else 0
+
+
+def _skinny_gateup(rows: int) -> bool:
+    """Whether a fused gate/up + SwiGLU of `rows` decode rows runs as one batched launch with the SwiGLU in its
+    reduce (else the MLP's own modules run).  Up to 16 rows the grouped launch reads x once for both products
+    and saves the two elementwise kernels of the SwiGLU, where torch's GEMM only edges out the batched kernel
+    on one projection alone."""
+    return 1 < rows <= 16
+
+
 def _skinny_dense(rows: int, N: int, Z: int) -> bool:
     """Whether a dense product of `rows` decode rows runs on the batched kernel (threshold 0) rather than torch's
     GEMM.  Measured on one MI355X, back-to-back calls at the Mistral-7B shapes over the column-major weight, torch
@@ -140,7 +155,7 @@ def _patch_linear_with_kernel(linear: nn.Linear, threshold: float) -> None:
             if linear.bias is not None:
                 out = out + linear.bias
             return out
-        rows = x.numel() // Z if x.shape[-1] == Z else 0
+        rows = _rows(x, Z)
         if x.dtype == torch.float16 and linear.bias is None and _skinny_dense(rows, N, Z):
             return batched_sparse_gemm(x.reshape(rows, Z), linear.weight, 0.0).reshape(x.shape[:-1] + (N,))
         return torch.nn.functional.linear(x, linear.weight, linear.bias)
@@ -189,11 +204,24 @@ def _maybe_patch_mlp(mlp: nn.Module) -> None:
             if x.dtype != torch.float16:
                 h = h.to(x.dtype)
             return down(h)
-        return original(x)
+        h = _gateup_rows(mlp, x)
+        return original(x) if h is None else down(h)
 
     mlp._teal_original_forward = original
     mlp.forward = fused_forward
     mlp._teal_fused = True
+
+
+def _gateup_rows(mlp: nn.Module, x: torch.Tensor) -> Optional[torch.Tensor]:
+    """silu(gate_proj(x)) * up_proj(x) of a fused MLP for a few fp16 decode rows, as one batched launch with the
+    SwiGLU in its reduce: the dense products the reference dispatches at B > 1 (patching.py:169-180; threshold 0)
+    and HF's fp16 SwiGLU (modeling_mistral.py:46-47) bit for bit.  None when the rows take the modules' own path."""
+    gate, up = mlp.gate_proj, mlp.up_proj
+    N, Z = gate.weight.shape
+    rows = _rows(x, Z)
+    if x.dtype != torch.float16 or not _skinny_gateup(rows):
+        return None
+    return batched_gateup_swiglu(x.reshape(rows, Z), gate.weight, up.weight).reshape(x.shape[:-1] + (N,))
 
 
 def _maybe_patch_qkv(attn: nn.Module) -> None:
@@ -203,19 +231,27 @@ def _maybe_patch_qkv(attn: nn.Module) -> None:
     k_proj / v_proj return them when called on the very tensor q_proj saw
     (unchanged since: same object and version counter), which is how HF's
     attention calls them (modeling_mistral.py:150-152); any other input takes
-    the projection's own sparse GEMV."""
+    the projection's own sparse GEMV.  A few decode rows (B > 1) that all three
+    projections send to the batched kernel run as one batched launch the same
+    way, each output equal to the projection's own call."""
     projs = [getattr(attn, n, None) for n in ("q_proj", "k_proj", "v_proj")]
     if any(p is None or not getattr(p, "_teal_patched", False) or p.bias is not None for p in projs):
         return
     q, k, v = projs
     held: dict = {}
+    Z = q.weight.shape[1]
 
     def q_forward(x, single=q.forward):
         if not _is_single_token(x):
             held.clear()
-            return single(x)
-        yq, yk, yv = sparse_qkv(x, q.weight, k.weight, v.weight, q._teal_threshold, k._teal_threshold,
-                                v._teal_threshold)
+            rows = _rows(x, Z)
+            if x.dtype != torch.float16 or not all(_skinny_dense(rows, p.weight.shape[0], Z) for p in projs):
+                return single(x)
+            # the three dense products of a few decode rows (threshold 0), one launch
+            yq, yk, yv = batched_qkv(x.reshape(rows, Z), q.weight, k.weight, v.weight)
+        else:
+            yq, yk, yv = sparse_qkv(x, q.weight, k.weight, v.weight, q._teal_threshold, k._teal_threshold,
+                                    v._teal_threshold)
         held.clear()
         held.update(x=x, version=x._version, k=yk, v=yv)
         lead = x.shape[:-1]

@@ -71,6 +71,10 @@ def test_multi_row_projection_dispatch_rule():
     assert _skinny_dense(16, 4096, 4096) and _skinny_dense(16, 6144, 4096)
     assert _skinny_dense(16, 4096, 14336) and not _skinny_dense(17, 4096, 14336)
     assert not _skinny_dense(4096, 4096, 4096)
+    # the fused gate/up + SwiGLU takes 2-16 rows as one grouped launch, whatever the projection rule says
+    from leankv_amd.teal.patching import _skinny_gateup
+
+    assert [r for r in range(0, 40) if _skinny_gateup(r)] == list(range(2, 17))
 
 
 def _fast_path_on(m, bits=3, hot=64, n=10, B=1):

@@ -323,16 +323,18 @@ def test_generate_fast_path_matches_hf_forward(cuda, bits, hot):
     assert fast.forward.engine.cache is c2
 
 
-@pytest.mark.parametrize("bits,hot", [(3, 64), (2, 128)])
-def test_generate_fast_path_batch(cuda, bits, hot):
-    """B = 4 sequences of one length: generate's decode calls replay BatchedEngine (the HF forward's own calls
-    with the position on the device); its logits equal the patched HF forward's, teacher-forced on the same
-    tokens from the same prefill, bit for bit, and so do the caches.  A left-padded batch falls back."""
+@pytest.mark.parametrize("bits,hot,B", [(3, 64, 4), (2, 128, 4), (3, 64, 16)])
+def test_generate_fast_path_batch(cuda, bits, hot, B):
+    """B = 4 and 16 sequences of one length (the batched kernel's v_dot2 and matrix-core paths, the grouped
+    q/k/v and gate/up launches, the residual adds fused into the projections' reduce): generate's decode calls
+    replay BatchedEngine (the HF forward's own calls with the position on the device); its logits equal the
+    patched HF forward's, teacher-forced on the same tokens from the same prefill, bit for bit, and so do the
+    caches.  A left-padded batch falls back."""
     from leankv_amd.turboquant.cache import TurboQuantCache
 
-    print("batch case bits=%d hot=%d" % (bits, hot), flush=True)
+    print("batch case bits=%d hot=%d B=%d" % (bits, hot, B), flush=True)
     (fast, ca), (slow, cb) = _teal_pair(cuda, 56 + bits, bits=bits, hot=hot)
-    ids = _ids(100, 57, B=4)
+    ids = _ids(100, 57, B=B)
     res = _generate(fast, ids.to(cuda), ca, 12)
     assert fast.forward.steps == {"engine": 0, "batch": 11, "forward": 1}, fast.forward.steps
     new = res.sequences[:, 100:]
@@ -349,7 +351,7 @@ def test_generate_fast_path_batch(cuda, bits, hot):
     # left padding: the mask is not all ones, so every call runs the forward (masked SDPA)
     c2 = TurboQuantCache(bits=bits, head_dim=128, num_layers=2, hot_buffer_size=hot, device=cuda, max_seq_len=256,
                          fused_attention=True)
-    mask = torch.ones(4, 100, dtype=torch.long)
+    mask = torch.ones(B, 100, dtype=torch.long)
     mask[0, :9] = 0
     before = dict(fast.forward.steps)
     _generate(fast, ids.to(cuda), c2, 4, attention_mask=mask.to(cuda))
