@@ -150,9 +150,14 @@ int lkv_sparse_gemm_batched(const void* x, const void* w, float threshold, int64
  *   LKV_EPI_RESIDUAL  n == 1: y[0] = fp16(residual + fp16(product)), the decoder
  *                     layer's fp16 residual add (modeling_mistral.py:233, 239);
  *                     y[0] may be residual (in place), residual fp16 [B][N[0]]
+ *   LKV_EPI_ROPE      n == 2 or 3 (q, k[, v]), N[0] and N[1] multiples of 128:
+ *                     y[0], y[1] = HF's apply_rotary_pos_emb (modeling_mistral.py:
+ *                     51-81, fp16 arithmetic as lkv_rope_f16) of the fp16 products'
+ *                     heads of 128 dims at the position whose 128 fp16 factors
+ *                     cos_row / sin_row hold; y[2] = the third product as it is
  * The q/k/v projections of an attention layer (leankv/teal/patching.py:169-180
  * runs them as three dense calls at B > 1) and the gate/up pair are the
- * products that share an input.  w, thresholds and N are host arrays of n
+ * products that share an input (and RoPE follows q and k).  w, thresholds and N are host arrays of n
  * entries, y of n (1 for LKV_EPI_SWIGLU); weights column-major as for
  * lkv_sparse_gemm_batched, outputs fp16 [B][N[s]].  Products whose
  * chunk sizes differ run as launches of their own.
@@ -160,10 +165,12 @@ int lkv_sparse_gemm_batched(const void* x, const void* w, float threshold, int64
 #define LKV_EPI_NONE 0
 #define LKV_EPI_SWIGLU 1
 #define LKV_EPI_RESIDUAL 2
+#define LKV_EPI_ROPE 3
 size_t lkv_sparse_gemm_batched_multi_workspace_bytes(int64_t B, int n, const int64_t* N, int64_t Z);
 int lkv_sparse_gemm_batched_multi(const void* x, int64_t B, int n, const void* const* w, const float* thresholds,
-                                  const int64_t* N, int64_t Z, int epilogue, const void* residual, void* const* y,
-                                  void* workspace, size_t workspace_bytes, void* stream);
+                                  const int64_t* N, int64_t Z, int epilogue, const void* residual,
+                                  const void* cos_row, const void* sin_row, void* const* y, void* workspace,
+                                  size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* TurboQuant (MSE variant), head_dim 128                                    */

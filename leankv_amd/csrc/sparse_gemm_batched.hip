@@ -45,7 +45,7 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 // projections of a layer, or gate and up): each segment owns grid slabs
 // slab0 .. slab0 + nslab - 1 and computes exactly what a launch of its own
 // would (same chunking, same summation order).  kMaxSeg (3) as for the GEMV.
-enum { kEpiNone = 0, kEpiSwiglu = 1, kEpiResidual = 2 };
+enum { kEpiNone = 0, kEpiSwiglu = 1, kEpiResidual = 2, kEpiRope = 3 };
 
 struct BatchedSeg {
   const uint16_t* A;  // [Z][N] fp16 (column-major weight)
@@ -59,6 +59,8 @@ struct BatchedSeg {
 struct BatchedArgs {
   const uint16_t* x;    // [B][Z] fp16
   const uint16_t* res;  // [B][N] fp16 residual (kEpiResidual; may be seg[0].y)
+  const uint16_t* cos;  // [128] fp16 RoPE factors of the position (kEpiRope)
+  const uint16_t* sin;
   int B, Z, nchunk, nseg, epi;
   int direct;           // one chunk and no epilogue: fp16 written by the GEMM kernel, no reduce
   BatchedSeg seg[kMaxSeg];
@@ -425,16 +427,34 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
 
 // y[b][n] = fp16 of the chunk partials summed in chunk order, through the
 // launch's epilogue: SwiGLU of the two segments' sums (gate, up; the grid
-// covers the first segment's columns), or the fp16 residual add
+// covers the first segment's columns), the fp16 residual add
 // fp16(res + fp16(sum)) (res may be the output: each element is read, then
-// written, by one thread).
-static_assert(kBN == kNT, "a reduce block covers one slab");
+// written, by one thread), or RoPE at one position on the heads of 128 dims of
+// the first two segments (q, k; a third, v, is stored as it is): rope_pair, the
+// fp16 arithmetic of HF's apply_rotary_pos_emb, with the partner dim d +- 64
+// from the same block (a block's 256 columns are two whole heads).
+static_assert(kBN == kNT && kBN % 128 == 0, "a reduce block covers one slab of whole heads");
 __global__ __launch_bounds__(kNT) void batched_reduce_kernel(BatchedArgs P) {
+  __shared__ float s_sum[kNT];
   const BatchedSeg S = seg_of(P, blockIdx.x);
-  const int n = (blockIdx.x - S.slab0) * kBN + threadIdx.x, b = blockIdx.y;
-  if (n >= S.N) return;
+  const int tid = threadIdx.x;
+  const int n = (blockIdx.x - S.slab0) * kBN + tid, b = blockIdx.y;
   const size_t row = static_cast<size_t>(S.nslab) * P.nchunk * kBN;  // partial floats per batch row
   const size_t o = static_cast<size_t>(b) * S.N + n;
+  if (P.epi == kEpiRope && (P.nseg < 3 || static_cast<int>(blockIdx.x) < P.seg[2].slab0)) {
+    // every thread reaches the barrier: columns past N (N % 128 == 0, so whole
+    // heads) read the slab's partials, which exist, and store nothing
+    const float sum = column_sum(S.part + b * row, n, P.nchunk);
+    s_sum[tid] = sum;
+    __syncthreads();
+    const int d = tid & 127;
+    const bool lo = d < 64;
+    float o0, o1;
+    rope_pair(lo ? sum : s_sum[tid - 64], lo ? s_sum[tid + 64] : sum, P.cos, P.sin, d & 63, o0, o1);
+    if (n < S.N) S.y[o] = f2h(lo ? o0 : o1);
+    return;
+  }
+  if (n >= S.N) return;
   const float sum = column_sum(S.part + b * row, n, P.nchunk);
   if (P.epi == kEpiSwiglu) {
     S.y[o] = swiglu_f16(sum, column_sum(P.seg[1].part + b * row, n, P.nchunk));
@@ -492,12 +512,15 @@ size_t product_floats(int64_t B, int64_t N, int64_t Z) {
 // products of x whose chunk sizes agree; partials one product after another
 // from ws.  Shapes are checked by the caller.
 bool launch_products(const void* x, int64_t B, int64_t Z, int n, const void* const* w, const float* t,
-                     const int64_t* N, void* const* y, int epi, const void* res, float* ws, hipStream_t st) {
+                     const int64_t* N, void* const* y, int epi, const void* res, const void* cosr, const void* sinr,
+                     float* ws, hipStream_t st) {
   const int bz = batched_bz(B, N[0], Z);
   const int64_t nchunk = Z > 0 ? gemv_chunks(Z, bz) : 0;
   BatchedArgs P = {};
   P.x = static_cast<const uint16_t*>(x);
   P.res = static_cast<const uint16_t*>(res);
+  P.cos = static_cast<const uint16_t*>(cosr);
+  P.sin = static_cast<const uint16_t*>(sinr);
   P.B = static_cast<int>(B);
   P.Z = static_cast<int>(Z);
   P.nchunk = static_cast<int>(nchunk);
@@ -551,12 +574,14 @@ bool launch_products(const void* x, int64_t B, int64_t Z, int n, const void* con
 // whose chunk sizes differ run as launches of their own (the epilogues pair
 // products of one shape, which always agree).
 int batched_products(const char* who, const void* x, int64_t B, int n, const void* const* w, const float* t,
-                     const int64_t* N, int64_t Z, int epi, const void* res, void* const* y, void* workspace,
-                     size_t workspace_bytes, hipStream_t st) {
+                     const int64_t* N, int64_t Z, int epi, const void* res, const void* cosr, const void* sinr,
+                     void* const* y, void* workspace, size_t workspace_bytes, hipStream_t st) {
   LKV_REQUIRE(n >= 1 && n <= kMaxSeg, "%s: %d products (1 to %d)", who, n, kMaxSeg);
   LKV_REQUIRE(w && t && N && y, "%s: null product array", who);
-  LKV_REQUIRE(epi == kEpiNone || (epi == kEpiSwiglu && n == 2) || (epi == kEpiResidual && n == 1),
-              "%s: epilogue %d with %d products (SwiGLU pairs 2, the residual add takes 1)", who, epi, n);
+  LKV_REQUIRE(epi == kEpiNone || (epi == kEpiSwiglu && n == 2) || (epi == kEpiResidual && n == 1) ||
+                  (epi == kEpiRope && n >= 2),
+              "%s: epilogue %d with %d products (SwiGLU pairs 2, the residual add takes 1, RoPE q, k and v)", who,
+              epi, n);
   LKV_REQUIRE(B >= 0 && Z >= 0, "%s: negative size B=%lld Z=%lld", who, (long long)B, (long long)Z);
   LKV_REQUIRE(B < 65536, "%s: B=%lld too large", who, (long long)B);
   for (int s = 0; s < n; ++s) {
@@ -567,6 +592,9 @@ int batched_products(const char* who, const void* x, int64_t B, int n, const voi
   }
   LKV_REQUIRE(epi != kEpiSwiglu || N[0] == N[1], "%s: SwiGLU of products of %lld and %lld columns", who,
               (long long)N[0], (long long)N[1]);
+  LKV_REQUIRE(epi != kEpiRope || (N[0] % 128 == 0 && N[1] % 128 == 0),
+              "%s: RoPE on products of %lld and %lld columns (heads of 128 dims)", who, (long long)N[0],
+              (long long)N[1]);
   int64_t total = 0;
   for (int s = 0; s < n; ++s) total += N[s];
   if (B == 0 || total == 0) return LKV_OK;
@@ -577,6 +605,7 @@ int batched_products(const char* who, const void* x, int64_t B, int n, const voi
     LKV_REQUIRE(N[s] == 0 || ((Z == 0 || (w[s] && aligned16(w[s]))) && (s >= nout || (y[s] && aligned16(y[s])))),
                 "%s: weight and output must be non-null and 16-byte aligned", who);
   LKV_REQUIRE(epi != kEpiResidual || res, "%s: null residual", who);
+  LKV_REQUIRE(epi != kEpiRope || (cosr && sinr), "%s: null RoPE factors", who);
   // partials are written unless every product is one chunk without epilogue
   size_t floats = 0;
   bool same = true, need_ws = false;
@@ -592,11 +621,13 @@ int batched_products(const char* who, const void* x, int64_t B, int n, const voi
               "%s: workspace of %zu bytes (16-byte aligned) required, got %zu", who, need, workspace_bytes);
   float* ws = static_cast<float*>(workspace);
   if (same && N[0] > 0) {
-    LKV_REQUIRE(launch_products(x, B, Z, n, w, t, N, y, epi, res, ws, st), "%s: no kernel for this chunk size", who);
+    LKV_REQUIRE(launch_products(x, B, Z, n, w, t, N, y, epi, res, cosr, sinr, ws, st),
+                "%s: no kernel for this chunk size", who);
   } else {
     for (int s = 0; s < n; ++s) {
       if (N[s] == 0) continue;
-      LKV_REQUIRE(launch_products(x, B, Z, 1, w + s, t + s, N + s, y + s, epi, res, ws, st),
+      const int e = (epi == kEpiRope && s >= 2) ? kEpiNone : epi;  // v takes no RoPE
+      LKV_REQUIRE(launch_products(x, B, Z, 1, w + s, t + s, N + s, y + s, e, res, cosr, sinr, ws, st),
                   "%s: no kernel for this chunk size", who);
       ws += Z > 0 ? product_floats(B, N[s], Z) : 0;
     }
@@ -617,8 +648,8 @@ extern "C" size_t lkv_sparse_gemm_batched_workspace_bytes(int64_t B, int64_t N, 
 
 extern "C" int lkv_sparse_gemm_batched(const void* x, const void* w, float threshold, int64_t B, int64_t N,
                                        int64_t Z, void* y, void* workspace, size_t workspace_bytes, void* stream) {
-  return batched_products("sparse_gemm_batched", x, B, 1, &w, &threshold, &N, Z, kEpiNone, nullptr, &y, workspace,
-                          workspace_bytes, static_cast<hipStream_t>(stream));
+  return batched_products("sparse_gemm_batched", x, B, 1, &w, &threshold, &N, Z, kEpiNone, nullptr, nullptr, nullptr,
+                          &y, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t lkv_sparse_gemm_batched_multi_workspace_bytes(int64_t B, int n, const int64_t* N, int64_t Z) {
@@ -631,8 +662,9 @@ extern "C" size_t lkv_sparse_gemm_batched_multi_workspace_bytes(int64_t B, int n
 
 extern "C" int lkv_sparse_gemm_batched_multi(const void* x, int64_t B, int n, const void* const* w,
                                              const float* thresholds, const int64_t* N, int64_t Z, int epilogue,
-                                             const void* residual, void* const* y, void* workspace,
-                                             size_t workspace_bytes, void* stream) {
-  return batched_products("sparse_gemm_batched_multi", x, B, n, w, thresholds, N, Z, epilogue, residual, y,
-                          workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                                             const void* residual, const void* cos_row, const void* sin_row,
+                                             void* const* y, void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+  return batched_products("sparse_gemm_batched_multi", x, B, n, w, thresholds, N, Z, epilogue, residual, cos_row,
+                          sin_row, y, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }

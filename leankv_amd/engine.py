@@ -242,8 +242,9 @@ class BatchedEngine:
     kernels, o_proj, residual adds, the (patched) MLP and lm_head -- with the position on the device, so the
     whole step replays without the host.  RMSNorm runs as one lkv_rmsnorm launch (the B = 1 step's
     arithmetic) and RoPE as one lkv_rope_f16 launch (HF's fp16 arithmetic bit for bit) instead of HF's
-    chains of elementwise kernels, and the residual adds run in the reduce of the patched o_proj / down_proj
-    launches (the same bits as the add): with the model's RMSNorm modules on lkv_rmsnorm the logits equal the
+    chains of elementwise kernels (in the reduce of the patched q/k/v launch when there is one), and the
+    residual adds run in the reduce of the patched o_proj / down_proj launches (the same bits as the add): with
+    the model's RMSNorm modules on lkv_rmsnorm the logits equal the
     HF forward's bit for bit; with HF's torch RMSNorm they differ from it in the last bits of the norms,
     as the B = 1 step's do.  tok [B] is fed, logits [B, vocab] come out; the cache's host counters are the
     caller's to advance (GenerateFastPath does)."""
@@ -270,6 +271,7 @@ class BatchedEngine:
             dummy = torch.zeros(1, 1, self.D, device=self.dev, dtype=torch.float16)
             cos, sin = model.model.rotary_emb(dummy, pos)
         self.cos, self.sin = cos[0].contiguous(), sin[0].contiguous()  # [max_len, D], the HF forward's values
+        self._fused_rope = self._fused_rope and self.cos.dtype == torch.float16 and self.sin.dtype == torch.float16
         self.tok = torch.zeros(B, dtype=torch.long, device=self.dev)
         self.pos64 = torch.zeros(1, dtype=torch.long, device=self.dev)
         self.pos32 = torch.zeros(1, dtype=torch.int32, device=self.dev)  # position of the token fed
@@ -283,16 +285,23 @@ class BatchedEngine:
 
     def _layer(self, i: int, layer, x: torch.Tensor, cos, sin) -> torch.Tensor:
         from . import kernels
+        from .teal.patching import _qkv_rows
 
         c, B, D = self.cache, self.B, self.D
         at = layer.self_attn
         residual = x
         h = self._norm(layer.input_layernorm, x)
-        qp, kp, vp = at.q_proj(h), at.k_proj(h), at.v_proj(h)
-        fused = (self._fused_rope and qp.dtype == torch.float16 and kp.dtype == torch.float16
-                 and qp.is_contiguous() and kp.is_contiguous())
-        if fused:  # in place on the fresh projection outputs, one launch for both
-            kernels.rope_f16_(qp.view(B, self.Hq, D), kp.view(B, self.Hkv, D), cos.view(-1), sin.view(-1))
+        # a fused TEAL q/k/v patch: the three products and RoPE on q and k as one launch
+        qkv = _qkv_rows(at, h, cos.view(-1), sin.view(-1)) if self._fused_rope else None
+        if qkv is not None:
+            qp, kp, vp = qkv
+            fused = True
+        else:
+            qp, kp, vp = at.q_proj(h), at.k_proj(h), at.v_proj(h)
+            fused = (self._fused_rope and qp.dtype == torch.float16 and kp.dtype == torch.float16
+                     and qp.is_contiguous() and kp.is_contiguous())
+            if fused:  # in place on the fresh projection outputs, one launch for both
+                kernels.rope_f16_(qp.view(B, self.Hq, D), kp.view(B, self.Hkv, D), cos.view(-1), sin.view(-1))
         q = qp.view(B, 1, -1, D).transpose(1, 2)
         k = kp.view(B, 1, -1, D).transpose(1, 2)
         v = vp.view(B, 1, -1, D).transpose(1, 2)

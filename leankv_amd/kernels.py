@@ -102,15 +102,17 @@ def sparse_gemm_batched(x: torch.Tensor, weight: torch.Tensor, threshold: float)
     return sparse_gemm_batched_out(x, weight, threshold, out)
 
 
-EPI_NONE, EPI_SWIGLU, EPI_RESIDUAL = 0, 1, 2
+EPI_NONE, EPI_SWIGLU, EPI_RESIDUAL, EPI_ROPE = 0, 1, 2, 3
 
 
 def sparse_gemm_batched_multi_out(x: torch.Tensor, weights, thresholds, outs, epilogue: int = EPI_NONE,
-                                  residual: torch.Tensor | None = None):
+                                  residual: torch.Tensor | None = None, cos: torch.Tensor | None = None,
+                                  sin: torch.Tensor | None = None):
     """Up to 3 sparse_gemm_batched products of one x[B, Z] in one launch (lkv_sparse_gemm_batched_multi), each
     equal to its own sparse_gemm_batched call, with an epilogue in the reduce: EPI_NONE (outs[s] = product s),
-    EPI_SWIGLU (two products g, u of one shape: outs[0] = fp16(fp16(silu(fp16 g)) * fp16 u)) or EPI_RESIDUAL
-    (one product: outs[0] = fp16(residual + fp16 product); outs[0] may be residual)."""
+    EPI_SWIGLU (two products g, u of one shape: outs[0] = fp16(fp16(silu(fp16 g)) * fp16 u)), EPI_RESIDUAL
+    (one product: outs[0] = fp16(residual + fp16 product); outs[0] may be residual) or EPI_ROPE (q, k[, v]:
+    rope_f16_ on the first two products' heads of 128 dims with the position's fp16 factors cos / sin [128])."""
     import ctypes
 
     n = len(weights)
@@ -139,6 +141,14 @@ def sparse_gemm_batched_multi_out(x: torch.Tensor, weights, thresholds, outs, ep
                               % (B, shapes[0][0]))
     elif residual is not None:
         raise LeanKVError("sparse_gemm_batched_multi: a residual needs the residual epilogue")
+    if epilogue == EPI_ROPE:
+        require_cuda(cos, sin)
+        for f in (cos, sin):
+            if f is None or f.dtype != torch.float16 or f.numel() != HEAD_DIM or not f.is_contiguous():
+                raise LeanKVError("sparse_gemm_batched_multi: RoPE needs contiguous float16 cos / sin of %d"
+                                  % HEAD_DIM)
+    elif cos is not None or sin is not None:
+        raise LeanKVError("sparse_gemm_batched_multi: RoPE factors need the RoPE epilogue")
     lib = _lib_handle()
     n_arr = (ctypes.c_int64 * n)(*[N for N, _ in shapes])
     nbytes = lib.lkv_sparse_gemm_batched_multi_workspace_bytes(B, n, n_arr, Z)
@@ -146,7 +156,7 @@ def sparse_gemm_batched_multi_out(x: torch.Tensor, weights, thresholds, outs, ep
     check(
         lib.lkv_sparse_gemm_batched_multi(ptr(x), B, n, (ctypes.c_void_p * n)(*[ptr(w) for w in weights]),
                                           (ctypes.c_float * n)(*[float(t) for t in thresholds]), n_arr, Z,
-                                          int(epilogue), ptr(residual),
+                                          int(epilogue), ptr(residual), ptr(cos), ptr(sin),
                                           (ctypes.c_void_p * n_out)(*[ptr(o) for o in outs]), ptr(ws), ws.numel(),
                                           stream_handle(x.device)),
         "lkv_sparse_gemm_batched_multi",
@@ -155,12 +165,13 @@ def sparse_gemm_batched_multi_out(x: torch.Tensor, weights, thresholds, outs, ep
 
 
 def sparse_gemm_batched_multi(x: torch.Tensor, weights, thresholds, epilogue: int = EPI_NONE,
-                              residual: torch.Tensor | None = None):
+                              residual: torch.Tensor | None = None, cos: torch.Tensor | None = None,
+                              sin: torch.Tensor | None = None):
     """sparse_gemm_batched_multi_out into fresh outputs (the list of them)."""
     N = [colmajor_rows(w)[0] for w in weights]
     outs = [torch.empty(x.shape[0], n, dtype=torch.float16, device=x.device)
-            for n in (N[:1] if epilogue != EPI_NONE else N)]
-    return sparse_gemm_batched_multi_out(x, weights, thresholds, outs, epilogue, residual)
+            for n in (N[:1] if epilogue in (EPI_SWIGLU, EPI_RESIDUAL) else N)]
+    return sparse_gemm_batched_multi_out(x, weights, thresholds, outs, epilogue, residual, cos, sin)
 
 
 def sparse_gemv_partials(x: torch.Tensor, w_gate: torch.Tensor, t_gate: float, w_up: torch.Tensor | None = None,

@@ -73,10 +73,14 @@ def sparse_qkv(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.Te
     return torch.ops.leankv.sparse_qkv(xh, wq, wk, wv, float(tq), float(tk), float(tv))
 
 
-def batched_qkv(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor):
+def batched_qkv(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor,
+                cos: torch.Tensor | None = None, sin: torch.Tensor | None = None):
     """fp16 (q, k, v) [rows, N_s] of x[rows, Z] through three column-major weights, threshold 0, one launch: each
-    equal to its own batched_sparse_gemm(x, w, 0.0) call bit for bit."""
-    return tuple(_k.sparse_gemm_batched_multi(x.to(torch.float16).contiguous(), [wq, wk, wv], [0.0, 0.0, 0.0]))
+    equal to its own batched_sparse_gemm(x, w, 0.0) call bit for bit; with cos / sin (one position's fp16 factors
+    [128]) q and k come out rotated as HF's apply_rotary_pos_emb rotates them."""
+    epi = _k.EPI_ROPE if cos is not None else _k.EPI_NONE
+    return tuple(_k.sparse_gemm_batched_multi(x.to(torch.float16).contiguous(), [wq, wk, wv], [0.0, 0.0, 0.0], epi,
+                                              cos=cos, sin=sin))
 
 
 def batched_gateup_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:

@@ -239,16 +239,14 @@ def _maybe_patch_qkv(attn: nn.Module) -> None:
         return
     q, k, v = projs
     held: dict = {}
-    Z = q.weight.shape[1]
 
     def q_forward(x, single=q.forward):
         if not _is_single_token(x):
             held.clear()
-            rows = _rows(x, Z)
-            if x.dtype != torch.float16 or not all(_skinny_dense(rows, p.weight.shape[0], Z) for p in projs):
+            ys = _qkv_rows(attn, x)  # the three dense products of a few decode rows (threshold 0), one launch
+            if ys is None:
                 return single(x)
-            # the three dense products of a few decode rows (threshold 0), one launch
-            yq, yk, yv = batched_qkv(x.reshape(rows, Z), q.weight, k.weight, v.weight)
+            yq, yk, yv = ys
         else:
             yq, yk, yv = sparse_qkv(x, q.weight, k.weight, v.weight, q._teal_threshold, k._teal_threshold,
                                     v._teal_threshold)
@@ -276,6 +274,24 @@ def _maybe_patch_qkv(attn: nn.Module) -> None:
     v.forward = share(v, "v")
     q.forward = q_forward
     attn._teal_qkv_fused = True
+
+
+def _qkv_rows(attn: nn.Module, x: torch.Tensor, cos: Optional[torch.Tensor] = None,
+              sin: Optional[torch.Tensor] = None):
+    """(q, k, v) [rows, N] of a fused q/k/v patch for a few fp16 decode rows that all three projections send to
+    the batched kernel, as one launch, each equal to the projection's own call; with cos / sin (one position's
+    fp16 RoPE factors [128]) q and k come out rotated as HF's apply_rotary_pos_emb rotates those outputs
+    (modeling_mistral.py:51-81, heads of 128 dims).  None when the rows take the modules' own path."""
+    if not getattr(attn, "_teal_qkv_fused", False):
+        return None
+    q, k, v = attn.q_proj, attn.k_proj, attn.v_proj
+    Z = q.weight.shape[1]
+    rows = _rows(x, Z)
+    if x.dtype != torch.float16 or not all(_skinny_dense(rows, p.weight.shape[0], Z) for p in (q, k, v)):
+        return None
+    if cos is not None and (q.weight.shape[0] % 128 or k.weight.shape[0] % 128):
+        return None
+    return batched_qkv(x.reshape(rows, Z), q.weight, k.weight, v.weight, cos, sin)
 
 
 def remove_teal(model):

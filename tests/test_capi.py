@@ -109,11 +109,12 @@ def test_invalid_arguments_rejected_without_launch():
     assert lib.lkv_sparse_gemm_batched_workspace_bytes(4, 4096, 14336) > 4 * 4096 * 4
     assert lib.lkv_sparse_gemm_batched(p, p, 0.1, 0, 4096, 14336, p, p, 0, None) == 0
     # grouped batched products: product count, epilogue / count pairing, SwiGLU shapes, residual, workspace
-    def multi(n, Ns, epi, res=p, ws_bytes=1 << 30, B=4, Z=4096):
+    def multi(n, Ns, epi, res=p, ws_bytes=1 << 30, B=4, Z=4096, rope=p):
         arr = (ctypes.c_int64 * max(n, 1))(*Ns)
         ptrs = (ctypes.c_void_p * max(n, 1))(*([p] * max(n, 1)))
         ts = (ctypes.c_float * max(n, 1))(*([0.0] * max(n, 1)))
-        return lib.lkv_sparse_gemm_batched_multi(p, B, n, ptrs, ts, arr, Z, epi, res, ptrs, p, ws_bytes, None)
+        return lib.lkv_sparse_gemm_batched_multi(p, B, n, ptrs, ts, arr, Z, epi, res, rope, rope, ptrs, p, ws_bytes,
+                                                 None)
 
     assert multi(0, [4096], 0) == -1 and "products" in _lib.last_error()
     assert multi(4, [8, 8, 8, 8], 0) == -1 and "products" in _lib.last_error()
@@ -124,6 +125,9 @@ def test_invalid_arguments_rejected_without_launch():
     assert multi(3, [4096, 1020, 1024], 0) == -1 and "multiple of 8" in _lib.last_error()
     assert multi(3, [4096, 1024, 1024], 0, ws_bytes=1024) == -1 and "workspace" in _lib.last_error()
     assert multi(3, [4096, 1024, 1024], 0, B=0) == 0  # nothing to do, nothing touched
+    assert multi(1, [4096], 3) == -1 and "epilogue" in _lib.last_error()  # RoPE takes q, k[, v]
+    assert multi(3, [4096, 1000, 1024], 3) == -1 and "RoPE" in _lib.last_error()
+    assert multi(3, [4096, 1024, 1024], 3, rope=None) == -1 and "RoPE factors" in _lib.last_error()
     qkv = (ctypes.c_int64 * 3)(4096, 1024, 1024)
     assert lib.lkv_sparse_gemm_batched_multi_workspace_bytes(16, 3, qkv, 4096) == sum(
         lib.lkv_sparse_gemm_batched_workspace_bytes(16, N, 4096) - 256 for N in (4096, 1024, 1024)) + 256

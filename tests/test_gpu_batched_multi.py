@@ -109,6 +109,29 @@ def test_residual_epilogue_equals_torch_add(cuda, B, N, Z):
     assert torch.equal(inplace, ref)
 
 
+# q|k|v at the Mistral shape on both kernels, q and k only, products whose chunk sizes differ (separate
+# launches: v must stay unrotated), one chunk with an odd number of heads (a reduce block of one head)
+@pytest.mark.parametrize("B,Ns,Z", [(4, (4096, 1024, 1024), 4096), (16, (4096, 1024, 1024), 4096),
+                                    (8, (512, 256), 1000), (5, (14336, 1024, 1024), 4096),
+                                    (3, (384, 128, 256), 100)])
+def test_rope_epilogue_equals_rope_f16_on_single_calls(cuda, B, Ns, Z):
+    from leankv_amd import kernels
+
+    print("rope case B=%d Ns=%s Z=%d" % (B, Ns, Z), flush=True)
+    g = torch.Generator().manual_seed(Z + len(Ns))
+    ws = [_weight(N, Z, g, cuda) for N in Ns]
+    x = _x(B, Z, B * 3 + Z, cuda)
+    pos = torch.arange(0, 4096, 37, dtype=torch.float32)[B % 7]
+    inv = 1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))
+    ang = torch.cat([pos * inv, pos * inv])
+    cos, sin = ang.cos().half().to(cuda), ang.sin().half().to(cuda)
+    got = kernels.sparse_gemm_batched_multi(x, ws, [0.0] * len(Ns), kernels.EPI_ROPE, cos=cos, sin=sin)
+    ref = [kernels.sparse_gemm_batched(x, w, 0.0) for w in ws]
+    kernels.rope_f16_(ref[0].view(B, -1, 128), ref[1].view(B, -1, 128), cos, sin)
+    for y, r in zip(got, ref):
+        assert torch.equal(y, r)
+
+
 def test_empty_sizes(cuda):
     """Z = 0: every product is an empty sum (0; SwiGLU of zeros is 0, the residual add returns the residual);
     B = 0 touches nothing; a zero-column product beside others is skipped."""
