@@ -78,6 +78,10 @@ def _parse():
                     help="--workload attn / decode: add per-block phase times of the attention kernels; needs the "
                          "instrumented build (python -m leankv_amd.build --stamps) loaded through "
                          "LKV_LIBRARY=leankv_amd/libleankv_amd_stamps.so")
+    ap.add_argument("--batches", default="4,16",
+                    help="--workload generate: batch sizes, comma-separated (the value is the largest one's)")
+    ap.add_argument("--no-hf-forward", action="store_true",
+                    help="--workload generate: skip the comparison runs on the patched HF forward")
     ap.add_argument("--bits", type=int, default=3, choices=(1, 2, 3, 4),
                     help="--workload attn / decode: code width of the packed cache (configs 4 and 5: 3; the "
                          "reference sweeps 2.5-4 bits, configs/mistral7b.yaml)")
@@ -1310,9 +1314,13 @@ def bench_generate(args, torch):
         assert out.shape[1] == prompt_len + new
         return B * new / dt
 
+    batches = sorted({int(b) for b in args.batches.split(",")})
+    if not batches or batches[0] < 2:
+        raise SystemExit("--batches: batch sizes of at least 2 (B = 1 is --workload decode)")
+    top = batches[-1]
     res_b = {}
     fp = enable_generate_fast_path(model)
-    for B in (4, 16):
+    for B in batches:
         run(B, True)  # warm-up: builds and captures the engine for this batch
         fast = statistics.mean(run(B, True) for _ in range(2))
         res_b[B] = {"fast_path_tok_s": round(fast, 1)}
@@ -1320,15 +1328,15 @@ def bench_generate(args, torch):
     calls = dict(fp.steps)
     disable_generate_fast_path(model)
     torch.cuda.empty_cache()
-    for B in (4, 16):
+    for B in ([] if args.no_hf_forward else batches):
         slow = run(B, False)
         res_b[B]["hf_forward_tok_s"] = round(slow, 1)
         res_b[B]["speedup"] = round(res_b[B]["fast_path_tok_s"] / slow, 3)
         _log("B=%d generate, patched HF forward: %.1f tok/s" % (B, slow))
     return {
-        "metric": "batched generate tok/s (Mistral-7B shape, TEAL thresholds, 3-bit KV, B=16)",
-        "value": res_b[16]["fast_path_tok_s"], "unit": "tok/s", "higher_is_better": True,
-        "ms_per_step": round(16 * 1e3 / res_b[16]["fast_path_tok_s"], 4),
+        "metric": "batched generate tok/s (Mistral-7B shape, TEAL thresholds, 3-bit KV, B=%d)" % top,
+        "value": res_b[top]["fast_path_tok_s"], "unit": "tok/s", "higher_is_better": True,
+        "ms_per_step": round(top * 1e3 / res_b[top]["fast_path_tok_s"], 4),
         "dtype": "f16 (fp32 accumulate)", "scaling": "weak",
         "data": "synthetic: random-init weights N(0,0.02), random %d-token prompts (seeded)" % prompt_len,
         "config": {"workload": "batched_generate", "prompt": prompt_len, "new_tokens": new, "kv_bits": 3,
