@@ -1336,6 +1336,7 @@ def bench_generate(args, torch):
     return {
         "metric": "batched generate tok/s (Mistral-7B shape, TEAL thresholds, 3-bit KV, B=%d)" % top,
         "value": res_b[top]["fast_path_tok_s"], "unit": "tok/s", "higher_is_better": True,
+        "steps": 2, "warmup": 1,  # timed / warm-up generate runs per batch size (each 128 new tokens)
         "ms_per_step": round(top * 1e3 / res_b[top]["fast_path_tok_s"], 4),
         "dtype": "f16 (fp32 accumulate)", "scaling": "weak",
         "data": "synthetic: random-init weights N(0,0.02), random %d-token prompts (seeded)" % prompt_len,
