@@ -172,6 +172,24 @@ int lkv_sparse_gemm_batched_multi(const void* x, int64_t B, int n, const void* c
                                   const void* cos_row, const void* sin_row, void* const* y, void* workspace,
                                   size_t workspace_bytes, void* stream);
 
+/*
+ * One batched_sparse_gemm product followed by the decoder layer's fp16
+ * residual add and the next RMSNorm (no single reference counterpart: the
+ * patched o_proj / down_proj call at B > 1, leankv/teal/patching.py:169-180,
+ * then modeling_mistral.py:233 / 239 and the following MistralRMSNorm,
+ * :190-197):
+ *   x_out[b] = fp16(residual[b] + fp16(product[b]))   (x_out may be residual)
+ *   y_out[b] = RMSNorm(x_out[b]) * norm_w             (lkv_rmsnorm's arithmetic)
+ * x_out equals lkv_sparse_gemm_batched_multi's LKV_EPI_RESIDUAL output and
+ * y_out lkv_rmsnorm of it, bit for bit; one launch does both after the
+ * product, one block per batch row.  N % 8 == 0, N <= 8192; residual, x_out,
+ * norm_w and y_out 16-byte aligned; workspace as for lkv_sparse_gemm_batched.
+ */
+int lkv_sparse_gemm_batched_residual_rmsnorm(const void* x, const void* w, float threshold, int64_t B, int64_t N,
+                                             int64_t Z, const void* residual, const void* norm_w, float eps,
+                                             void* x_out, void* y_out, void* workspace, size_t workspace_bytes,
+                                             void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* TurboQuant (MSE variant), head_dim 128                                    */
 /* ------------------------------------------------------------------------ */

@@ -172,9 +172,16 @@ __device__ __forceinline__ float rms_rstd(const uint16_t* __restrict__ x, int Z,
 }
 
 // HF MistralRMSNorm output element (modeling_mistral.py:190-197): x * rstd in
-// fp32 cast to fp16, times the fp16 weight, product rounded to fp16.
+// fp32 cast to fp16, times the fp16 weight, product rounded to fp16.  The
+// fp32 product goes through an empty asm so that it exists as an fp32 value:
+// the compiler otherwise selects one fp16-output fma for product and cast
+// (v_fma_mixlo_f16: one rounding of the exact product instead of two) in some
+// kernels and not in others, depending on how it vectorises the element loop,
+// and two kernels' norms of one row then differ in rare elements.
 __device__ __forceinline__ float rms_apply(uint16_t x, uint16_t w, float rstd) {
-  return h2f(f2h(h2f(w) * h2f(f2h(h2f(x) * rstd))));
+  float t = h2f(x) * rstd;
+  __asm__ volatile("" : "+v"(t));
+  return h2f(f2h(h2f(w) * h2f(f2h(t))));
 }
 
 // SwiGLU with the rounding of the eager fp16 torch sequence of

@@ -45,7 +45,7 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 // projections of a layer, or gate and up): each segment owns grid slabs
 // slab0 .. slab0 + nslab - 1 and computes exactly what a launch of its own
 // would (same chunking, same summation order).  kMaxSeg (3) as for the GEMV.
-enum { kEpiNone = 0, kEpiSwiglu = 1, kEpiResidual = 2, kEpiRope = 3 };
+enum { kEpiNone = 0, kEpiSwiglu = 1, kEpiResidual = 2, kEpiRope = 3, kEpiResidualNorm = 4 };
 
 struct BatchedSeg {
   const uint16_t* A;  // [Z][N] fp16 (column-major weight)
@@ -61,6 +61,9 @@ struct BatchedArgs {
   const uint16_t* res;  // [B][N] fp16 residual (kEpiResidual; may be seg[0].y)
   const uint16_t* cos;  // [128] fp16 RoPE factors of the position (kEpiRope)
   const uint16_t* sin;
+  const uint16_t* norm_w;  // [N] fp16 RMSNorm weight, its epsilon and output [B][N] (kEpiResidualNorm)
+  float eps;
+  uint16_t* ynorm;
   int B, Z, nchunk, nseg, epi;
   int direct;           // one chunk and no epilogue: fp16 written by the GEMM kernel, no reduce
   BatchedSeg seg[kMaxSeg];
@@ -465,6 +468,79 @@ __global__ __launch_bounds__(kNT) void batched_reduce_kernel(BatchedArgs P) {
   }
 }
 
+// kEpiResidualNorm, one block per batch row: x_out = fp16(res + fp16(sum of
+// the chunk partials in chunk order)) (batched_reduce_kernel's arithmetic for
+// the residual epilogue; x_out may be res), then y = RMSNorm(x_out) * w with
+// rms_rstd / rms_apply, the arithmetic of lkv_rmsnorm, from the row staged in
+// LDS.  Thread t takes columns 4t .. 4t + 3 (and every 4096th after), all
+// chunks of them in flight together: one memory round trip where the reduce
+// and the RMSNorm launch took two launches.
+constexpr int kNormThreads = 1024;
+constexpr int kNormMaxN = 8192;
+constexpr int kNormIt = kNormMaxN / (4 * kNormThreads);  // column quads per thread
+__global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(BatchedArgs P) {
+  __shared__ __align__(16) uint16_t s_x[kNormMaxN];
+  __shared__ float s_wsum[kGemvThreads / kWave];
+  const BatchedSeg& S = P.seg[0];
+  const int b = blockIdx.x, tid = threadIdx.x, N = S.N, nchunk = P.nchunk;
+  const float* part = S.part + static_cast<size_t>(b) * S.nslab * nchunk * kBN;
+  const size_t ro = static_cast<size_t>(b) * N;
+  // the residual and the norm weight of the thread's columns first (clamped
+  // to the row: N % 8 == 0), then the partials
+  uint2 r[kNormIt], wn[kNormIt];
+#pragma unroll
+  for (int it = 0; it < kNormIt; ++it) {
+    const int cc = min(4 * tid + it * 4 * kNormThreads, N - 4);
+    r[it] = *reinterpret_cast<const uint2*>(P.res + ro + cc);
+    wn[it] = *reinterpret_cast<const uint2*>(P.norm_w + cc);
+  }
+  uint16_t xn[kNormIt][4];
+#pragma unroll
+  for (int it = 0; it < kNormIt; ++it) {
+    const int c = 4 * tid + it * 4 * kNormThreads;
+    if (c < N) {
+      const float* p = part + static_cast<size_t>(c / kBN) * nchunk * kBN + (c % kBN);
+      f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+      constexpr int kB = 16;  // zeros past the last chunk leave the sum as it is (it is never -0)
+      for (int k0 = 0; k0 < nchunk; k0 += kB) {
+        f32x4 v[kB];
+#pragma unroll
+        for (int i = 0; i < kB; ++i)  // clamped address, value selected after: the loads stay unconditional
+          v[i] = *reinterpret_cast<const f32x4*>(p + static_cast<size_t>(min(k0 + i, nchunk - 1)) * kBN);
+#pragma unroll
+        for (int i = 0; i < kB; ++i) {
+          const bool ok = k0 + i < nchunk;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sum[j] += ok ? v[i][j] : 0.f;
+        }
+      }
+      const uint16_t rr[4] = {static_cast<uint16_t>(r[it].x & 0xffffu), static_cast<uint16_t>(r[it].x >> 16),
+                              static_cast<uint16_t>(r[it].y & 0xffffu), static_cast<uint16_t>(r[it].y >> 16)};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xn[it][j] = f2h(h2f(rr[j]) + h2f(f2h(sum[j])));
+      const uint2 o = make_uint2(xn[it][0] | (static_cast<uint32_t>(xn[it][1]) << 16),
+                                 xn[it][2] | (static_cast<uint32_t>(xn[it][3]) << 16));
+      *reinterpret_cast<uint2*>(S.y + ro + c) = o;
+      *reinterpret_cast<uint2*>(s_x + c) = o;
+    }
+  }
+  __syncthreads();
+  const float rstd = rms_rstd(s_x, N, P.eps, s_wsum);
+#pragma unroll
+  for (int it = 0; it < kNormIt; ++it) {
+    const int c = 4 * tid + it * 4 * kNormThreads;
+    if (c < N) {
+      const uint16_t ww[4] = {static_cast<uint16_t>(wn[it].x & 0xffffu), static_cast<uint16_t>(wn[it].x >> 16),
+                              static_cast<uint16_t>(wn[it].y & 0xffffu), static_cast<uint16_t>(wn[it].y >> 16)};
+      uint16_t yy[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) yy[j] = f2h(rms_apply(xn[it][j], ww[j], rstd));
+      *reinterpret_cast<uint2*>(P.ynorm + ro + c) =
+          make_uint2(yy[0] | (static_cast<uint32_t>(yy[1]) << 16), yy[2] | (static_cast<uint32_t>(yy[3]) << 16));
+    }
+  }
+}
+
 template <int NB>
 bool launch_nb(const BatchedArgs& P, int bz, dim3 grid, hipStream_t st) {
   switch (bz) {
@@ -503,6 +579,17 @@ int batched_bz(int64_t B, int64_t N, int64_t Z) {
   return gemv_pick_bz(gemv_slabs(N) * groups, Z, 6);
 }
 
+// What follows the chunk sums (the entry points' epilogue arguments).
+struct EpiArgs {
+  int kind = kEpiNone;
+  const void* res = nullptr;     // residual (kEpiResidual, kEpiResidualNorm)
+  const void* cos = nullptr;     // RoPE factors (kEpiRope)
+  const void* sin = nullptr;
+  const void* norm_w = nullptr;  // RMSNorm weight, epsilon and output (kEpiResidualNorm)
+  float eps = 0.f;
+  void* ynorm = nullptr;
+};
+
 // Partial floats of one product of B rows at its own chunk size.
 size_t product_floats(int64_t B, int64_t N, int64_t Z) {
   return static_cast<size_t>(B) * gemv_part_floats(N, gemv_chunks(Z, batched_bz(B, N, Z)));
@@ -512,15 +599,18 @@ size_t product_floats(int64_t B, int64_t N, int64_t Z) {
 // products of x whose chunk sizes agree; partials one product after another
 // from ws.  Shapes are checked by the caller.
 bool launch_products(const void* x, int64_t B, int64_t Z, int n, const void* const* w, const float* t,
-                     const int64_t* N, void* const* y, int epi, const void* res, const void* cosr, const void* sinr,
-                     float* ws, hipStream_t st) {
+                     const int64_t* N, void* const* y, const EpiArgs& E, float* ws, hipStream_t st) {
+  const int epi = E.kind;
   const int bz = batched_bz(B, N[0], Z);
   const int64_t nchunk = Z > 0 ? gemv_chunks(Z, bz) : 0;
   BatchedArgs P = {};
   P.x = static_cast<const uint16_t*>(x);
-  P.res = static_cast<const uint16_t*>(res);
-  P.cos = static_cast<const uint16_t*>(cosr);
-  P.sin = static_cast<const uint16_t*>(sinr);
+  P.res = static_cast<const uint16_t*>(E.res);
+  P.cos = static_cast<const uint16_t*>(E.cos);
+  P.sin = static_cast<const uint16_t*>(E.sin);
+  P.norm_w = static_cast<const uint16_t*>(E.norm_w);
+  P.eps = E.eps;
+  P.ynorm = static_cast<uint16_t*>(E.ynorm);
   P.B = static_cast<int>(B);
   P.Z = static_cast<int>(Z);
   P.nchunk = static_cast<int>(nchunk);
@@ -562,7 +652,9 @@ bool launch_products(const void* x, int64_t B, int64_t Z, int n, const void* con
     }
     if (!ok) return false;
   }
-  if (!P.direct) {  // Z == 0: the reduce over zero chunks writes the epilogue of empty sums (a kernel, graph-safe)
+  if (epi == kEpiResidualNorm) {  // Z == 0: empty sums, the residual itself normalised
+    hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(static_cast<unsigned>(B)), dim3(kNormThreads), 0, st, P);
+  } else if (!P.direct) {  // Z == 0: the reduce over zero chunks writes the epilogue of empty sums (graph-safe)
     const int rslabs = epi == kEpiSwiglu ? P.seg[0].nslab : slabs;
     hipLaunchKernelGGL(batched_reduce_kernel, dim3(static_cast<unsigned>(rslabs), static_cast<unsigned>(B)), dim3(kNT),
                        0, st, P);
@@ -574,12 +666,13 @@ bool launch_products(const void* x, int64_t B, int64_t Z, int n, const void* con
 // whose chunk sizes differ run as launches of their own (the epilogues pair
 // products of one shape, which always agree).
 int batched_products(const char* who, const void* x, int64_t B, int n, const void* const* w, const float* t,
-                     const int64_t* N, int64_t Z, int epi, const void* res, const void* cosr, const void* sinr,
-                     void* const* y, void* workspace, size_t workspace_bytes, hipStream_t st) {
+                     const int64_t* N, int64_t Z, const EpiArgs& E, void* const* y, void* workspace,
+                     size_t workspace_bytes, hipStream_t st) {
+  const int epi = E.kind;
   LKV_REQUIRE(n >= 1 && n <= kMaxSeg, "%s: %d products (1 to %d)", who, n, kMaxSeg);
   LKV_REQUIRE(w && t && N && y, "%s: null product array", who);
   LKV_REQUIRE(epi == kEpiNone || (epi == kEpiSwiglu && n == 2) || (epi == kEpiResidual && n == 1) ||
-                  (epi == kEpiRope && n >= 2),
+                  (epi == kEpiRope && n >= 2) || (epi == kEpiResidualNorm && n == 1),
               "%s: epilogue %d with %d products (SwiGLU pairs 2, the residual add takes 1, RoPE q, k and v)", who,
               epi, n);
   LKV_REQUIRE(B >= 0 && Z >= 0, "%s: negative size B=%lld Z=%lld", who, (long long)B, (long long)Z);
@@ -604,8 +697,15 @@ int batched_products(const char* who, const void* x, int64_t B, int n, const voi
   for (int s = 0; s < n; ++s)
     LKV_REQUIRE(N[s] == 0 || ((Z == 0 || (w[s] && aligned16(w[s]))) && (s >= nout || (y[s] && aligned16(y[s])))),
                 "%s: weight and output must be non-null and 16-byte aligned", who);
-  LKV_REQUIRE(epi != kEpiResidual || res, "%s: null residual", who);
-  LKV_REQUIRE(epi != kEpiRope || (cosr && sinr), "%s: null RoPE factors", who);
+  LKV_REQUIRE((epi != kEpiResidual && epi != kEpiResidualNorm) || E.res, "%s: null residual", who);
+  LKV_REQUIRE(epi != kEpiRope || (E.cos && E.sin), "%s: null RoPE factors", who);
+  if (epi == kEpiResidualNorm) {
+    LKV_REQUIRE(N[0] <= kNormMaxN, "%s: N=%lld above the fused RMSNorm's %d columns", who, (long long)N[0],
+                kNormMaxN);
+    LKV_REQUIRE(E.norm_w && E.ynorm, "%s: null RMSNorm weight or output", who);
+    LKV_REQUIRE(aligned16(E.res) && aligned16(y[0]) && aligned16(E.norm_w) && aligned16(E.ynorm),
+                "%s: residual, RMSNorm weight and outputs must be 16-byte aligned", who);
+  }
   // partials are written unless every product is one chunk without epilogue
   size_t floats = 0;
   bool same = true, need_ws = false;
@@ -621,13 +721,13 @@ int batched_products(const char* who, const void* x, int64_t B, int n, const voi
               "%s: workspace of %zu bytes (16-byte aligned) required, got %zu", who, need, workspace_bytes);
   float* ws = static_cast<float*>(workspace);
   if (same && N[0] > 0) {
-    LKV_REQUIRE(launch_products(x, B, Z, n, w, t, N, y, epi, res, cosr, sinr, ws, st),
-                "%s: no kernel for this chunk size", who);
+    LKV_REQUIRE(launch_products(x, B, Z, n, w, t, N, y, E, ws, st), "%s: no kernel for this chunk size", who);
   } else {
     for (int s = 0; s < n; ++s) {
       if (N[s] == 0) continue;
-      const int e = (epi == kEpiRope && s >= 2) ? kEpiNone : epi;  // v takes no RoPE
-      LKV_REQUIRE(launch_products(x, B, Z, 1, w + s, t + s, N + s, y + s, e, res, cosr, sinr, ws, st),
+      EpiArgs e = E;
+      if (epi == kEpiRope && s >= 2) e.kind = kEpiNone;  // v takes no RoPE
+      LKV_REQUIRE(launch_products(x, B, Z, 1, w + s, t + s, N + s, y + s, e, ws, st),
                   "%s: no kernel for this chunk size", who);
       ws += Z > 0 ? product_floats(B, N[s], Z) : 0;
     }
@@ -648,8 +748,8 @@ extern "C" size_t lkv_sparse_gemm_batched_workspace_bytes(int64_t B, int64_t N, 
 
 extern "C" int lkv_sparse_gemm_batched(const void* x, const void* w, float threshold, int64_t B, int64_t N,
                                        int64_t Z, void* y, void* workspace, size_t workspace_bytes, void* stream) {
-  return batched_products("sparse_gemm_batched", x, B, 1, &w, &threshold, &N, Z, kEpiNone, nullptr, nullptr, nullptr,
-                          &y, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  return batched_products("sparse_gemm_batched", x, B, 1, &w, &threshold, &N, Z, EpiArgs{}, &y, workspace,
+                          workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t lkv_sparse_gemm_batched_multi_workspace_bytes(int64_t B, int n, const int64_t* N, int64_t Z) {
@@ -665,6 +765,26 @@ extern "C" int lkv_sparse_gemm_batched_multi(const void* x, int64_t B, int n, co
                                              const void* residual, const void* cos_row, const void* sin_row,
                                              void* const* y, void* workspace, size_t workspace_bytes,
                                              void* stream) {
-  return batched_products("sparse_gemm_batched_multi", x, B, n, w, thresholds, N, Z, epilogue, residual, cos_row,
-                          sin_row, y, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  EpiArgs E;
+  E.kind = epilogue;
+  E.res = residual;
+  E.cos = cos_row;
+  E.sin = sin_row;
+  LKV_REQUIRE(epilogue >= kEpiNone && epilogue <= kEpiRope, "sparse_gemm_batched_multi: epilogue %d", epilogue);
+  return batched_products("sparse_gemm_batched_multi", x, B, n, w, thresholds, N, Z, E, y, workspace,
+                          workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int lkv_sparse_gemm_batched_residual_rmsnorm(const void* x, const void* w, float threshold, int64_t B,
+                                                        int64_t N, int64_t Z, const void* residual,
+                                                        const void* norm_w, float eps, void* x_out, void* y_out,
+                                                        void* workspace, size_t workspace_bytes, void* stream) {
+  EpiArgs E;
+  E.kind = kEpiResidualNorm;
+  E.res = residual;
+  E.norm_w = norm_w;
+  E.eps = eps;
+  E.ynorm = y_out;
+  return batched_products("sparse_gemm_batched_residual_rmsnorm", x, B, 1, &w, &threshold, &N, Z, E, &x_out,
+                          workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }

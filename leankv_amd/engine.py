@@ -242,9 +242,10 @@ class BatchedEngine:
     kernels, o_proj, residual adds, the (patched) MLP and lm_head -- with the position on the device, so the
     whole step replays without the host.  RMSNorm runs as one lkv_rmsnorm launch (the B = 1 step's
     arithmetic) and RoPE as one lkv_rope_f16 launch (HF's fp16 arithmetic bit for bit) instead of HF's
-    chains of elementwise kernels (in the reduce of the patched q/k/v launch when there is one), and the
-    residual adds run in the reduce of the patched o_proj / down_proj launches (the same bits as the add): with
-    the model's RMSNorm modules on lkv_rmsnorm the logits equal the
+    chains of elementwise kernels (in the reduce of the patched q/k/v launch when there is one), and each
+    residual add runs with the RMSNorm after it in one launch behind the patched o_proj / down_proj product
+    (the same bits as the add and lkv_rmsnorm): with the model's RMSNorm modules on lkv_rmsnorm the logits
+    equal the
     HF forward's bit for bit; with HF's torch RMSNorm they differ from it in the last bits of the norms,
     as the B = 1 step's do.  tok [B] is fed, logits [B, vocab] come out; the cache's host counters are the
     caller's to advance (GenerateFastPath does)."""
@@ -283,14 +284,15 @@ class BatchedEngine:
         self.graph = None
         self._host_pos = None
 
-    def _layer(self, i: int, layer, x: torch.Tensor, cos, sin) -> torch.Tensor:
+    def _layer(self, i: int, layer, x: torch.Tensor, h: torch.Tensor, cos, sin, next_norm):
+        """One decoder layer on x (h = its input_layernorm(x)); returns the layer's output and next_norm of it
+        (the next layer's input_layernorm, or the model's final norm)."""
         from . import kernels
         from .teal.patching import _qkv_rows
 
         c, B, D = self.cache, self.B, self.D
         at = layer.self_attn
         residual = x
-        h = self._norm(layer.input_layernorm, x)
         # a fused TEAL q/k/v patch: the three products and RoPE on q and k as one launch
         qkv = _qkv_rows(at, h, cos.view(-1), sin.view(-1)) if self._fused_rope else None
         if qkv is not None:
@@ -316,14 +318,14 @@ class BatchedEngine:
                                    c._v_hot[i], c.PiK[i], c.PiV[i], c.centroids, c.bits, self.len32, self.max_len,
                                    float(at.scaling), self.attn, self.attn_ws)
         o = self.attn.view(B, self.Hq, 1, D).transpose(1, 2).contiguous().to(q.dtype).reshape(B, 1, -1)
-        x = self._residual_proj(at.o_proj, o, residual)
-        residual = x
-        return self._residual_mlp(layer.mlp, self._norm(layer.post_attention_layernorm, x), residual)
+        x, h = self._residual_proj(at.o_proj, o, residual, layer.post_attention_layernorm)
+        return self._residual_mlp(layer.mlp, h, x, next_norm)
 
-    def _residual_proj(self, proj, inp: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
-        """residual + proj(inp).  A TEAL-patched projection that sends these B rows to the batched kernel
-        (threshold 0) runs as one launch with HF's fp16 residual add in its reduce: the same bits as the
-        projection's forward followed by torch's add."""
+    def _residual_proj(self, proj, inp: torch.Tensor, residual: torch.Tensor, norm=None):
+        """(x, norm(x)) for x = residual + proj(inp).  A TEAL-patched projection that sends these B rows to the
+        batched kernel (threshold 0) runs as one launch with HF's fp16 residual add in its reduce, or, when norm
+        is an RMSNorm _norm runs on lkv_rmsnorm, with the add and the norm in one launch after the product: the
+        same bits as the projection's forward, torch's add and _norm."""
         from . import kernels
         from .teal.patching import _skinny_dense
 
@@ -333,22 +335,40 @@ class BatchedEngine:
                 and inp.numel() == B * w.shape[1] and residual.numel() == B * w.shape[0]
                 and residual.is_contiguous() and _skinny_dense(B, w.shape[0], w.shape[1])):
             out = torch.empty_like(residual)
-            kernels.sparse_gemm_batched_multi_out(inp.reshape(B, -1).contiguous(), [w], [0.0], [out.view(B, -1)],
-                                                  kernels.EPI_RESIDUAL, residual.view(B, -1))
-            return out
-        return residual + proj(inp)
+            x2 = inp.reshape(B, -1).contiguous()
+            if self._lkv_norm(norm, residual) and w.shape[0] <= 8192:
+                y = torch.empty_like(residual)
+                kernels.sparse_gemm_batched_residual_rmsnorm_out(x2, w, 0.0, residual.view(B, -1), norm.weight,
+                                                                 norm.variance_epsilon, out.view(B, -1),
+                                                                 y.view(B, -1))
+                return out, y
+            kernels.sparse_gemm_batched_multi_out(x2, [w], [0.0], [out.view(B, -1)], kernels.EPI_RESIDUAL,
+                                                  residual.view(B, -1))
+        else:
+            out = residual + proj(inp)
+        return out, (self._norm(norm, out) if norm is not None else None)
 
-    def _residual_mlp(self, mlp, h: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
-        """residual + mlp(h).  For a fused TEAL MLP whose gate/up + SwiGLU takes these rows as one batched launch,
-        the down projection then runs through _residual_proj: the MLP forward's own calls, with the add fused."""
+    def _residual_mlp(self, mlp, h: torch.Tensor, residual: torch.Tensor, norm=None):
+        """(x, norm(x)) for x = residual + mlp(h).  For a fused TEAL MLP whose gate/up + SwiGLU takes these rows
+        as one batched launch, the down projection then runs through _residual_proj: the MLP forward's own
+        calls, with the add (and the norm) fused."""
         from .teal.patching import _gateup_rows
 
         down = getattr(mlp, "down_proj", None)
         if getattr(mlp, "_teal_fused", False) and down is not None:
             a = _gateup_rows(mlp, h)
             if a is not None:
-                return self._residual_proj(down, a, residual)
-        return residual + mlp(h)
+                return self._residual_proj(down, a, residual, norm)
+        out = residual + mlp(h)
+        return out, (self._norm(norm, out) if norm is not None else None)
+
+    @staticmethod
+    def _lkv_norm(mod, x: torch.Tensor) -> bool:
+        """Whether _norm runs mod on x as lkv_rmsnorm."""
+        w = getattr(mod, "weight", None)
+        return (type(mod).__name__ in _HF_RMSNORMS and x.dtype == torch.float16 and w is not None
+                and w.dtype == torch.float16 and w.numel() == x.shape[-1] and x.shape[-1] % 8 == 0
+                and w.is_contiguous())
 
     @staticmethod
     def _norm(mod, x: torch.Tensor) -> torch.Tensor:
@@ -357,10 +377,8 @@ class BatchedEngine:
         can differ), any other norm module as it is."""
         from . import kernels
 
-        w = getattr(mod, "weight", None)
-        if (type(mod).__name__ in _HF_RMSNORMS and x.dtype == torch.float16 and w is not None
-                and w.dtype == torch.float16 and w.numel() == x.shape[-1] and x.shape[-1] % 8 == 0):
-            return kernels.rms_norm(x, w, mod.variance_epsilon)
+        if BatchedEngine._lkv_norm(mod, x):
+            return kernels.rms_norm(x, mod.weight, mod.variance_epsilon)
         return mod(x)
 
     def _step(self) -> None:
@@ -368,9 +386,12 @@ class BatchedEngine:
         x = m.model.embed_tokens(self.tok.view(self.B, 1))
         cos = self.cos.index_select(0, self.pos64).unsqueeze(0)  # [1, 1, D]
         sin = self.sin.index_select(0, self.pos64).unsqueeze(0)
-        for i, layer in enumerate(m.model.layers):
-            x = self._layer(i, layer, x, cos, sin)
-        logits = m.lm_head(self._norm(m.model.norm, x))
+        layers = m.model.layers
+        h = self._norm(layers[0].input_layernorm, x)
+        for i, layer in enumerate(layers):
+            nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else m.model.norm
+            x, h = self._layer(i, layer, x, h, cos, sin, nxt)
+        logits = m.lm_head(h)
         if self.logits is None:
             self.logits = torch.empty_like(logits)
         self.logits.copy_(logits)

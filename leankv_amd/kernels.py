@@ -164,6 +164,36 @@ def sparse_gemm_batched_multi_out(x: torch.Tensor, weights, thresholds, outs, ep
     return outs
 
 
+def sparse_gemm_batched_residual_rmsnorm_out(x: torch.Tensor, weight: torch.Tensor, threshold: float,
+                                             residual: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                                             x_out: torch.Tensor, y_out: torch.Tensor):
+    """x_out = fp16(residual + fp16(sparse_gemm_batched(x, weight, threshold))), y_out = rms_norm(x_out, norm_w,
+    eps), in one product launch and one epilogue launch (lkv_sparse_gemm_batched_residual_rmsnorm); x_out may be
+    residual.  Both equal the separate calls bit for bit."""
+    N, Z = colmajor_rows(weight)
+    require_cuda(x, weight, residual, norm_w, x_out, y_out)
+    ts = (x, weight, residual, norm_w, x_out, y_out)
+    if any(t.dtype != torch.float16 for t in ts):
+        raise LeanKVError("sparse_gemm_batched_residual_rmsnorm: every tensor must be float16")
+    if x.dim() != 2 or x.shape[1] != Z or not x.is_contiguous():
+        raise LeanKVError("sparse_gemm_batched_residual_rmsnorm: x must be a contiguous float16 [B, %d] tensor" % Z)
+    B = x.shape[0]
+    for t in (residual, x_out, y_out):
+        if tuple(t.shape) != (B, N) or not t.is_contiguous():
+            raise LeanKVError("sparse_gemm_batched_residual_rmsnorm: residual and outputs must be contiguous "
+                              "[%d, %d]" % (B, N))
+    if norm_w.numel() != N or not norm_w.is_contiguous():
+        raise LeanKVError("sparse_gemm_batched_residual_rmsnorm: norm weight of %d elements expected" % N)
+    lib = _lib_handle()
+    nbytes = lib.lkv_sparse_gemm_batched_workspace_bytes(B, N, Z)
+    ws = workspaces.get(x.device, "gemm_bn", nbytes)
+    check(lib.lkv_sparse_gemm_batched_residual_rmsnorm(ptr(x), ptr(weight), float(threshold), B, N, Z, ptr(residual),
+                                                       ptr(norm_w), float(eps), ptr(x_out), ptr(y_out), ptr(ws),
+                                                       ws.numel(), stream_handle(x.device)),
+          "lkv_sparse_gemm_batched_residual_rmsnorm")
+    return x_out, y_out
+
+
 def sparse_gemm_batched_multi(x: torch.Tensor, weights, thresholds, epilogue: int = EPI_NONE,
                               residual: torch.Tensor | None = None, cos: torch.Tensor | None = None,
                               sin: torch.Tensor | None = None):

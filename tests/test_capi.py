@@ -128,6 +128,17 @@ def test_invalid_arguments_rejected_without_launch():
     assert multi(1, [4096], 3) == -1 and "epilogue" in _lib.last_error()  # RoPE takes q, k[, v]
     assert multi(3, [4096, 1000, 1024], 3) == -1 and "RoPE" in _lib.last_error()
     assert multi(3, [4096, 1024, 1024], 3, rope=None) == -1 and "RoPE factors" in _lib.last_error()
+    assert multi(1, [4096], 4) == -1 and "epilogue" in _lib.last_error()  # the fused norm has its own entry
+    # product + residual + RMSNorm: the fused norm's column limit, null norm weight, alignment
+    rn = lib.lkv_sparse_gemm_batched_residual_rmsnorm
+    assert rn(p, p, 0.0, 4, 16384, 4096, p, p, 1e-5, p, p, p, 1 << 30, None) == -1
+    assert "8192" in _lib.last_error()
+    assert rn(p, p, 0.0, 4, 4096, 4096, p, None, 1e-5, p, p, p, 1 << 30, None) == -1
+    assert "RMSNorm weight" in _lib.last_error()
+    q = ctypes.c_void_p(24)
+    assert rn(p, p, 0.0, 4, 4096, 4096, q, p, 1e-5, p, p, p, 1 << 30, None) == -1
+    assert "aligned" in _lib.last_error()
+    assert rn(p, p, 0.0, 0, 4096, 4096, p, p, 1e-5, p, p, p, 0, None) == 0
     qkv = (ctypes.c_int64 * 3)(4096, 1024, 1024)
     assert lib.lkv_sparse_gemm_batched_multi_workspace_bytes(16, 3, qkv, 4096) == sum(
         lib.lkv_sparse_gemm_batched_workspace_bytes(16, N, 4096) - 256 for N in (4096, 1024, 1024)) + 256

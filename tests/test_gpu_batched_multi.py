@@ -1,6 +1,7 @@
 """GPU tests of lkv_sparse_gemm_batched_multi: up to three batched TEAL products of one x [B, Z] in one launch,
-with the SwiGLU or the fp16 residual add in the chunk reduce, and the TEAL patches that use it for a few decode
-rows.  Bar: bit-exact against the single-product calls (lkv_sparse_gemm_batched, whose parity with the oracle
+with the SwiGLU, the fp16 residual add or RoPE in the chunk reduce (and of
+lkv_sparse_gemm_batched_residual_rmsnorm: the residual add and the next RMSNorm), and the TEAL patches that use
+it for a few decode rows.  Bar: bit-exact against the single-product calls (lkv_sparse_gemm_batched, whose parity with the oracle
 the kernel tests check) followed by torch's own fp16 SwiGLU / add; the dense patched MLP additionally within
 1e-2 of an fp32 torch reference."""
 
@@ -130,6 +131,31 @@ def test_rope_epilogue_equals_rope_f16_on_single_calls(cuda, B, Ns, Z):
     kernels.rope_f16_(ref[0].view(B, -1, 128), ref[1].view(B, -1, 128), cos, sin)
     for y, r in zip(got, ref):
         assert torch.equal(y, r)
+
+
+@pytest.mark.parametrize("B,N,Z", [(4, 4096, 4096), (16, 4096, 14336), (3, 8192, 512), (11, 1032, 333),
+                                   (5, 24, 100), (2, 64, 0)])
+def test_residual_rmsnorm_equals_residual_epilogue_then_rms_norm(cuda, B, N, Z):
+    """The product, the fp16 residual add and the next RMSNorm with one launch after the product: x_out equals
+    the residual epilogue's output and y_out lkv_rmsnorm of it, bit for bit (also in place, x_out = residual;
+    Z = 0: the residual itself normalised)."""
+    from leankv_amd import kernels
+
+    print("residual+norm case B=%d N=%d Z=%d" % (B, N, Z), flush=True)
+    g = torch.Generator().manual_seed(N + 7 * Z)
+    w = _weight(N, Z, g, cuda)
+    x = _x(B, Z, N + Z, cuda)
+    res = (torch.randn(B, N, generator=g) * 2).to(torch.float16).to(cuda)
+    nw = (1 + 0.1 * torch.randn(N, generator=g)).to(torch.float16).to(cuda)
+    eps = 1e-5
+    (ref_x,) = kernels.sparse_gemm_batched_multi(x, [w], [0.0], kernels.EPI_RESIDUAL, res)
+    ref_y = kernels.rms_norm(ref_x, nw, eps)
+    xo, yo = torch.empty_like(res), torch.empty_like(res)
+    kernels.sparse_gemm_batched_residual_rmsnorm_out(x, w, 0.0, res, nw, eps, xo, yo)
+    assert torch.equal(xo, ref_x) and torch.equal(yo, ref_y)
+    inplace = res.clone()
+    kernels.sparse_gemm_batched_residual_rmsnorm_out(x, w, 0.0, inplace, nw, eps, inplace, yo)
+    assert torch.equal(inplace, ref_x) and torch.equal(yo, ref_y)
 
 
 def test_empty_sizes(cuda):
