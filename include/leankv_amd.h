@@ -173,6 +173,24 @@ int lkv_sparse_gemm_batched_multi(const void* x, int64_t B, int n, const void* c
                                   size_t workspace_bytes, void* stream);
 
 /*
+ * The q, k and v products of lkv_sparse_gemm_batched_multi with LKV_EPI_ROPE
+ * (w, thresholds, N and y host arrays of 3 entries), and, with k_hot / v_hot
+ * non-null, the ring half of lkv_tq_cache_append (cache.py:84-141: the new
+ * token enters the hot window): k (rotated) and v also go to ring slot
+ * *pos % hot_cap of rows (batch b, kv head h) = b * N[1] / 128 + h of
+ * k_hot / v_hot (fp16 [B * N[1] / 128][hot_cap][128]).  With
+ * lkv_tq_cache_evict run before it, the cache afterwards equals
+ * lkv_tq_cache_append's on the same k and v.  No single reference
+ * counterpart: the q/k/v calls of a decode layer at B > 1
+ * (leankv/teal/patching.py:169-180), RoPE (modeling_mistral.py:51-81) and
+ * TurboQuantCache.update's ring write.
+ */
+int lkv_sparse_gemm_batched_qkv_rope(const void* x, int64_t B, const void* const* w, const float* thresholds,
+                                     const int64_t* N, int64_t Z, const void* cos_row, const void* sin_row,
+                                     void* const* y, void* k_hot, void* v_hot, const int32_t* pos, int64_t hot_cap,
+                                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * One batched_sparse_gemm product followed by the decoder layer's fp16
  * residual add and the next RMSNorm (no single reference counterpart: the
  * patched o_proj / down_proj call at B > 1, leankv/teal/patching.py:169-180,
@@ -471,6 +489,32 @@ typedef struct lkv_decode_layer {
   const float* PiK;        /* fp32 [128, 128] */
   const float* PiV;
 } lkv_decode_layer;
+
+/*
+ * The eviction half of lkv_tq_cache_append for every layer of a decode step
+ * in one launch (cache.py:84-141: once the window holds hot_cap tokens, the
+ * oldest is quantized into the cold store): at position *pos (device int32,
+ * the position of the token this step feeds) the token pos - hot_cap leaves
+ * ring slot pos % hot_cap of each of the R rows (batch x kv head) of each
+ * layer and its codes and norms go to cold slot pos - hot_cap (nothing when
+ * pos < hot_cap or pos - hot_cap >= cap).  The codes and norms equal
+ * lkv_tq_cache_append's.  Run it before the step writes its new token into
+ * the ring (lkv_sparse_gemm_batched_qkv_rope does, as the append's second
+ * half).  Buffers as for lkv_tq_cache_append, codes 16-byte aligned; layers
+ * is a host array of n_layers entries.
+ */
+typedef struct lkv_cache_layer {
+  void* k_codes;       /* uint8 [R, cap, row bytes] */
+  void* k_norms;       /* fp32 [R, cap] */
+  void* v_codes;
+  void* v_norms;
+  const void* k_hot;   /* fp16 [R, hot_cap, 128] ring */
+  const void* v_hot;
+  const float* PiK;    /* fp32 [128, 128] */
+  const float* PiV;
+} lkv_cache_layer;
+int lkv_tq_cache_evict(const lkv_cache_layer* layers, int64_t n_layers, int64_t R, int64_t hot_cap, int64_t cap,
+                       const float* bounds, int bits, const int32_t* pos, void* stream);
 
 /*
  * y = RMSNorm(x) * w for M rows of Z fp16 values (x 16-byte aligned, Z % 8 == 0):

@@ -62,6 +62,9 @@ SIGNATURES = {
                                              _c_p, _sz, _c_p]),
     "lkv_sparse_gemm_batched_residual_rmsnorm": (_int, [_c_p, _c_p, _f32, _i64, _i64, _i64, _c_p, _c_p, _f32, _c_p,
                                                         _c_p, _c_p, _sz, _c_p]),
+    "lkv_sparse_gemm_batched_qkv_rope": (_int, [_c_p, _i64, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                                _i64, _c_p, _sz, _c_p]),
+    "lkv_tq_cache_evict": (_int, [_c_p, _i64, _i64, _i64, _i64, _c_p, _int, _c_p, _c_p]),
     "lkv_paged_decode_attn_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "lkv_tq_paged_decode_attn_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "lkv_tq_paged_decode_attn": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _int, _c_p, _c_p,

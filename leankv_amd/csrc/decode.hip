@@ -530,6 +530,51 @@ extern "C" int lkv_decode_evict(const lkv_decode_dims* dims, const lkv_decode_la
   return LKV_OK;
 }
 
+extern "C" int lkv_tq_cache_evict(const lkv_cache_layer* layers, int64_t n_layers, int64_t R, int64_t hot_cap,
+                                  int64_t cap, const float* bounds, int bits, const int32_t* pos, void* stream) {
+  LKV_REQUIRE(bits >= 1 && bits <= 4, "tq_cache_evict: bits=%d unsupported (1..4 are bit-packed)", bits);
+  LKV_REQUIRE(n_layers >= 0 && R >= 0 && R < (1 << 24) && hot_cap >= 1 && hot_cap < (1 << 30) && cap >= 0 &&
+                  cap < (1 << 30),
+              "tq_cache_evict: bad sizes layers=%lld R=%lld hot_cap=%lld cap=%lld", (long long)n_layers,
+              (long long)R, (long long)hot_cap, (long long)cap);
+  if (n_layers == 0 || R == 0) return LKV_OK;
+  LKV_REQUIRE(layers && bounds && pos, "tq_cache_evict: null pointer");
+  for (int64_t l = 0; l < n_layers; ++l) {
+    const lkv_cache_layer& L = layers[l];
+    LKV_REQUIRE(L.k_codes && L.k_norms && L.v_codes && L.v_norms && L.k_hot && L.v_hot && L.PiK && L.PiV,
+                "tq_cache_evict: null cache pointer in layer %lld", (long long)l);
+    LKV_REQUIRE(aligned16(L.k_codes) && aligned16(L.v_codes) && aligned16(L.k_hot) && aligned16(L.v_hot) &&
+                    aligned16(L.PiK) && aligned16(L.PiV),
+                "tq_cache_evict: cache buffers and rotations of layer %lld must be 16-byte aligned", (long long)l);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  for (int64_t l0 = 0; l0 < n_layers; l0 += kEvictLayers) {
+    const int nl = static_cast<int>(n_layers - l0 < kEvictLayers ? n_layers - l0 : kEvictLayers);
+    EvictArgs A{};
+    A.state = pos;  // state[0]: the position of the token fed this step
+    A.bounds = bounds;
+    A.hot_cap = static_cast<int>(hot_cap);
+    A.cap = static_cast<int>(cap);
+    A.Hkv = static_cast<int>(R);  // the kernel's rows: (batch, kv head) pairs
+    for (int i = 0; i < nl; ++i) {
+      const lkv_cache_layer& L = layers[l0 + i];
+      A.L[i] = EvictLayer{static_cast<const uint16_t*>(L.k_hot), static_cast<const uint16_t*>(L.v_hot),
+                          static_cast<uint8_t*>(L.k_codes),      static_cast<float*>(L.k_norms),
+                          static_cast<uint8_t*>(L.v_codes),      static_cast<float*>(L.v_norms),
+                          L.PiK,                                 L.PiV};
+    }
+    const dim3 grid(static_cast<unsigned>((R + 15) / 16), 2, static_cast<unsigned>(nl));
+    switch (bits) {
+      case 1: hipLaunchKernelGGL((evict_kernel<1>), grid, dim3(kThreads), 0, st, A); break;
+      case 2: hipLaunchKernelGGL((evict_kernel<2>), grid, dim3(kThreads), 0, st, A); break;
+      case 3: hipLaunchKernelGGL((evict_kernel<3>), grid, dim3(kThreads), 0, st, A); break;
+      default: hipLaunchKernelGGL((evict_kernel<4>), grid, dim3(kThreads), 0, st, A);
+    }
+    LKV_LAUNCH_CHECK("tq_cache_evict");
+  }
+  return LKV_OK;
+}
+
 namespace lkv {
 namespace {
 

@@ -51,9 +51,11 @@ struct BatchedSeg {
   const uint16_t* A;  // [Z][N] fp16 (column-major weight)
   float* part;        // [B][nslab][nchunk][256] fp32 (unless direct)
   uint16_t* y;        // [B][N] fp16
+  uint16_t* ring;     // kEpiRope: also into this hot ring, [B * N / 128][hot_cap][128] fp16 (or null)
   uint32_t a_bytes;
   float t;
   int N, nslab, slab0;
+  int rope;           // kEpiRope: this product's heads are rotated (q, k; not v)
 };
 
 struct BatchedArgs {
@@ -64,6 +66,8 @@ struct BatchedArgs {
   const uint16_t* norm_w;  // [N] fp16 RMSNorm weight, its epsilon and output [B][N] (kEpiResidualNorm)
   float eps;
   uint16_t* ynorm;
+  const int32_t* pos;      // kEpiRope with a ring: the position whose slot pos % hot_cap takes the token
+  int hot_cap;
   int B, Z, nchunk, nseg, epi;
   int direct;           // one chunk and no epilogue: fp16 written by the GEMM kernel, no reduce
   BatchedSeg seg[kMaxSeg];
@@ -433,10 +437,18 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
 // covers the first segment's columns), the fp16 residual add
 // fp16(res + fp16(sum)) (res may be the output: each element is read, then
 // written, by one thread), or RoPE at one position on the heads of 128 dims of
-// the first two segments (q, k; a third, v, is stored as it is): rope_pair, the
-// fp16 arithmetic of HF's apply_rotary_pos_emb, with the partner dim d +- 64
-// from the same block (a block's 256 columns are two whole heads).
+// the segments marked rope (q, k; v is stored as it is): rope_pair, the fp16
+// arithmetic of HF's apply_rotary_pos_emb, with the partner dim d +- 64 from
+// the same block (a block's 256 columns are two whole heads); a segment with a
+// ring (k, v) also stores its token in that hot ring.
 static_assert(kBN == kNT && kBN % 128 == 0, "a reduce block covers one slab of whole heads");
+// Element n of batch row b of a q/k/v product in its hot ring: row (b, head
+// n / 128), slot pos % hot_cap, dim n % 128 (lkv_tq_cache_append's ring).
+__device__ __forceinline__ size_t ring_index(const BatchedArgs& P, const BatchedSeg& S, int b, int n) {
+  const int slot = *P.pos % P.hot_cap;
+  const size_t r = static_cast<size_t>(b) * (S.N / 128) + n / 128;
+  return (r * P.hot_cap + slot) * 128 + (n % 128);
+}
 __global__ __launch_bounds__(kNT) void batched_reduce_kernel(BatchedArgs P) {
   __shared__ float s_sum[kNT];
   const BatchedSeg S = seg_of(P, blockIdx.x);
@@ -444,7 +456,7 @@ __global__ __launch_bounds__(kNT) void batched_reduce_kernel(BatchedArgs P) {
   const int n = (blockIdx.x - S.slab0) * kBN + tid, b = blockIdx.y;
   const size_t row = static_cast<size_t>(S.nslab) * P.nchunk * kBN;  // partial floats per batch row
   const size_t o = static_cast<size_t>(b) * S.N + n;
-  if (P.epi == kEpiRope && (P.nseg < 3 || static_cast<int>(blockIdx.x) < P.seg[2].slab0)) {
+  if (P.epi == kEpiRope && S.rope) {
     // every thread reaches the barrier: columns past N (N % 128 == 0, so whole
     // heads) read the slab's partials, which exist, and store nothing
     const float sum = column_sum(S.part + b * row, n, P.nchunk);
@@ -454,11 +466,21 @@ __global__ __launch_bounds__(kNT) void batched_reduce_kernel(BatchedArgs P) {
     const bool lo = d < 64;
     float o0, o1;
     rope_pair(lo ? sum : s_sum[tid - 64], lo ? s_sum[tid + 64] : sum, P.cos, P.sin, d & 63, o0, o1);
-    if (n < S.N) S.y[o] = f2h(lo ? o0 : o1);
+    if (n < S.N) {
+      const uint16_t h = f2h(lo ? o0 : o1);
+      S.y[o] = h;
+      if (S.ring) S.ring[ring_index(P, S, b, n)] = h;
+    }
     return;
   }
   if (n >= S.N) return;
   const float sum = column_sum(S.part + b * row, n, P.nchunk);
+  if (S.ring) {  // v of a RoPE launch: its ring slot too
+    const uint16_t h = f2h(sum);
+    S.y[o] = h;
+    S.ring[ring_index(P, S, b, n)] = h;
+    return;
+  }
   if (P.epi == kEpiSwiglu) {
     S.y[o] = swiglu_f16(sum, column_sum(P.seg[1].part + b * row, n, P.nchunk));
   } else if (P.epi == kEpiResidual) {
@@ -588,6 +610,10 @@ struct EpiArgs {
   const void* norm_w = nullptr;  // RMSNorm weight, epsilon and output (kEpiResidualNorm)
   float eps = 0.f;
   void* ynorm = nullptr;
+  void* ring[kMaxSeg] = {nullptr, nullptr, nullptr};  // per product: its hot ring (kEpiRope), or null
+  bool rope[kMaxSeg] = {true, true, false};            // kEpiRope: which products are rotated (q, k)
+  const int32_t* pos = nullptr;
+  int64_t hot_cap = 1;
 };
 
 // Partial floats of one product of B rows at its own chunk size.
@@ -611,6 +637,8 @@ bool launch_products(const void* x, int64_t B, int64_t Z, int n, const void* con
   P.norm_w = static_cast<const uint16_t*>(E.norm_w);
   P.eps = E.eps;
   P.ynorm = static_cast<uint16_t*>(E.ynorm);
+  P.pos = E.pos;
+  P.hot_cap = static_cast<int>(E.hot_cap);
   P.B = static_cast<int>(B);
   P.Z = static_cast<int>(Z);
   P.nchunk = static_cast<int>(nchunk);
@@ -624,6 +652,8 @@ bool launch_products(const void* x, int64_t B, int64_t Z, int n, const void* con
     S.A = static_cast<const uint16_t*>(w[s]);
     S.part = ws + off;
     S.y = s < (epi == kEpiSwiglu ? 1 : n) ? static_cast<uint16_t*>(y[s]) : nullptr;  // SwiGLU: one output
+    S.ring = epi == kEpiRope ? static_cast<uint16_t*>(E.ring[s]) : nullptr;
+    S.rope = epi == kEpiRope && E.rope[s];
     S.a_bytes = static_cast<uint32_t>(N[s] * Z * 2);
     S.t = t[s];
     S.N = static_cast<int>(N[s]);
@@ -685,9 +715,9 @@ int batched_products(const char* who, const void* x, int64_t B, int n, const voi
   }
   LKV_REQUIRE(epi != kEpiSwiglu || N[0] == N[1], "%s: SwiGLU of products of %lld and %lld columns", who,
               (long long)N[0], (long long)N[1]);
-  LKV_REQUIRE(epi != kEpiRope || (N[0] % 128 == 0 && N[1] % 128 == 0),
-              "%s: RoPE on products of %lld and %lld columns (heads of 128 dims)", who, (long long)N[0],
-              (long long)N[1]);
+  for (int s = 0; s < n; ++s)
+    LKV_REQUIRE(epi != kEpiRope || !(E.rope[s] || E.ring[s]) || N[s] % 128 == 0,
+                "%s: RoPE / ring on a product of %lld columns (heads of 128 dims)", who, (long long)N[s]);
   int64_t total = 0;
   for (int s = 0; s < n; ++s) total += N[s];
   if (B == 0 || total == 0) return LKV_OK;
@@ -725,8 +755,11 @@ int batched_products(const char* who, const void* x, int64_t B, int n, const voi
   } else {
     for (int s = 0; s < n; ++s) {
       if (N[s] == 0) continue;
-      EpiArgs e = E;
-      if (epi == kEpiRope && s >= 2) e.kind = kEpiNone;  // v takes no RoPE
+      EpiArgs e = E;  // this product's own epilogue
+      e.ring[0] = E.ring[s];
+      e.ring[1] = e.ring[2] = nullptr;
+      e.rope[0] = E.rope[s];
+      e.rope[1] = e.rope[2] = false;
       LKV_REQUIRE(launch_products(x, B, Z, 1, w + s, t + s, N + s, y + s, e, ws, st),
                   "%s: no kernel for this chunk size", who);
       ws += Z > 0 ? product_floats(B, N[s], Z) : 0;
@@ -773,6 +806,32 @@ extern "C" int lkv_sparse_gemm_batched_multi(const void* x, int64_t B, int n, co
   LKV_REQUIRE(epilogue >= kEpiNone && epilogue <= kEpiRope, "sparse_gemm_batched_multi: epilogue %d", epilogue);
   return batched_products("sparse_gemm_batched_multi", x, B, n, w, thresholds, N, Z, E, y, workspace,
                           workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int lkv_sparse_gemm_batched_qkv_rope(const void* x, int64_t B, const void* const* w,
+                                                const float* thresholds, const int64_t* N, int64_t Z,
+                                                const void* cos_row, const void* sin_row, void* const* y, void* k_hot,
+                                                void* v_hot, const int32_t* pos, int64_t hot_cap, void* workspace,
+                                                size_t workspace_bytes, void* stream) {
+  const char* who = "sparse_gemm_batched_qkv_rope";
+  LKV_REQUIRE(N, "%s: null product array", who);
+  LKV_REQUIRE((k_hot == nullptr) == (v_hot == nullptr), "%s: both rings or neither", who);
+  if (k_hot) {
+    LKV_REQUIRE(pos && hot_cap >= 1 && hot_cap < (1 << 30), "%s: null position or bad hot_cap %lld", who,
+                (long long)hot_cap);
+    LKV_REQUIRE(N[1] == N[2], "%s: k and v of %lld and %lld columns", who, (long long)N[1], (long long)N[2]);
+    LKV_REQUIRE(aligned16(k_hot) && aligned16(v_hot), "%s: rings must be 16-byte aligned", who);
+  }
+  EpiArgs E;
+  E.kind = kEpiRope;
+  E.cos = cos_row;
+  E.sin = sin_row;
+  E.ring[1] = k_hot;
+  E.ring[2] = v_hot;
+  E.pos = pos;
+  E.hot_cap = hot_cap;
+  return batched_products(who, x, B, 3, w, thresholds, N, Z, E, y, workspace, workspace_bytes,
+                          static_cast<hipStream_t>(stream));
 }
 
 extern "C" int lkv_sparse_gemm_batched_residual_rmsnorm(const void* x, const void* w, float threshold, int64_t B,

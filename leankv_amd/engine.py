@@ -273,6 +273,13 @@ class BatchedEngine:
             cos, sin = model.model.rotary_emb(dummy, pos)
         self.cos, self.sin = cos[0].contiguous(), sin[0].contiguous()  # [max_len, D], the HF forward's values
         self._fused_rope = self._fused_rope and self.cos.dtype == torch.float16 and self.sin.dtype == torch.float16
+        # Every layer's q/k/v one launch with RoPE: then that launch writes the new token into the hot ring and
+        # one launch per step evicts the tokens leaving every layer's window (tq_cache_append's two halves)
+        from .teal.patching import _qkv_fusable
+
+        fus = [_qkv_fusable(l.self_attn, B, torch.float16) for l in layers] if self._fused_rope else [None]
+        self._ring = all(f is not None and f[0].shape[0] % 128 == 0 and f[1].shape[0] == self.Hkv * self.D
+                         and f[2].shape[0] == self.Hkv * self.D for f in fus)
         self.tok = torch.zeros(B, dtype=torch.long, device=self.dev)
         self.pos64 = torch.zeros(1, dtype=torch.long, device=self.dev)
         self.pos32 = torch.zeros(1, dtype=torch.int32, device=self.dev)  # position of the token fed
@@ -288,14 +295,21 @@ class BatchedEngine:
         """One decoder layer on x (h = its input_layernorm(x)); returns the layer's output and next_norm of it
         (the next layer's input_layernorm, or the model's final norm)."""
         from . import kernels
-        from .teal.patching import _qkv_rows
+        from .teal.patching import _qkv_fusable, _qkv_rows
 
         c, B, D = self.cache, self.B, self.D
         at = layer.self_attn
         residual = x
-        # a fused TEAL q/k/v patch: the three products and RoPE on q and k as one launch
-        qkv = _qkv_rows(at, h, cos.view(-1), sin.view(-1)) if self._fused_rope else None
-        if qkv is not None:
+        # a fused TEAL q/k/v patch: the three products and RoPE on q and k as one launch (with the ring write)
+        appended = False
+        if self._ring:
+            ws = _qkv_fusable(at, B, h.dtype)
+            qp, kp, vp = (torch.empty(B, w.shape[0], dtype=torch.float16, device=self.dev) for w in ws)
+            kernels.sparse_gemm_batched_qkv_rope_out(h.reshape(B, -1).contiguous(), list(ws), cos.view(-1),
+                                                     sin.view(-1), [qp, kp, vp], c._k_hot[i], c._v_hot[i],
+                                                     self.pos32)
+            fused = appended = True
+        elif (qkv := _qkv_rows(at, h, cos.view(-1), sin.view(-1)) if self._fused_rope else None) is not None:
             qp, kp, vp = qkv
             fused = True
         else:
@@ -309,10 +323,12 @@ class BatchedEngine:
         v = vp.view(B, 1, -1, D).transpose(1, 2)
         if not fused:
             q, k = self._rope(q, k, cos, sin)
-        k16, v16 = k.to(torch.float16), v.to(torch.float16)
-        kernels.tq_cache_append(k16.reshape(B, self.Hkv, D).contiguous(), v16.reshape(B, self.Hkv, D).contiguous(),
-                                c._k_hot[i], c._v_hot[i], c._k_codes[i], c._k_norms[i], c._v_codes[i], c._v_norms[i],
-                                c.PiK[i], c.PiV[i], c.decision_boundaries, c.bits, self.pos32)
+        if not appended:
+            k16, v16 = k.to(torch.float16), v.to(torch.float16)
+            kernels.tq_cache_append(k16.reshape(B, self.Hkv, D).contiguous(),
+                                    v16.reshape(B, self.Hkv, D).contiguous(), c._k_hot[i], c._v_hot[i],
+                                    c._k_codes[i], c._k_norms[i], c._v_codes[i], c._v_norms[i], c.PiK[i], c.PiV[i],
+                                    c.decision_boundaries, c.bits, self.pos32)
         qf = q.reshape(B, self.Hq, D).to(torch.float16).contiguous()
         kernels.tq_decode_attn_out(qf, c._k_codes[i], c._k_norms[i], c._v_codes[i], c._v_norms[i], c._k_hot[i],
                                    c._v_hot[i], c.PiK[i], c.PiV[i], c.centroids, c.bits, self.len32, self.max_len,
@@ -382,11 +398,18 @@ class BatchedEngine:
         return mod(x)
 
     def _step(self) -> None:
+        from . import kernels
+
         m = self.model
         x = m.model.embed_tokens(self.tok.view(self.B, 1))
         cos = self.cos.index_select(0, self.pos64).unsqueeze(0)  # [1, 1, D]
         sin = self.sin.index_select(0, self.pos64).unsqueeze(0)
         layers = m.model.layers
+        if self._ring:  # the token leaving every layer's hot window, before any layer writes its new one
+            c = self.cache
+            kernels.tq_cache_evict([(c._k_codes[i], c._k_norms[i], c._v_codes[i], c._v_norms[i], c._k_hot[i],
+                                     c._v_hot[i], c.PiK[i], c.PiV[i]) for i in range(len(layers))],
+                                   c.decision_boundaries, c.bits, self.pos32)
         h = self._norm(layers[0].input_layernorm, x)
         for i, layer in enumerate(layers):
             nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else m.model.norm

@@ -194,6 +194,54 @@ def sparse_gemm_batched_residual_rmsnorm_out(x: torch.Tensor, weight: torch.Tens
     return x_out, y_out
 
 
+def sparse_gemm_batched_qkv_rope_out(x: torch.Tensor, weights, cos: torch.Tensor, sin: torch.Tensor, outs,
+                                     k_hot: torch.Tensor | None = None, v_hot: torch.Tensor | None = None,
+                                     pos_dev: torch.Tensor | None = None):
+    """q, k, v = the three threshold-0 products of x[B, Z] with RoPE on q and k (sparse_gemm_batched_multi_out with
+    EPI_ROPE), and with k_hot / v_hot [B * Hkv, hot_cap, 128] the new token of every row also written into ring
+    slot pos % hot_cap (pos_dev: int32 device position), as lkv_tq_cache_append writes it
+    (lkv_sparse_gemm_batched_qkv_rope)."""
+    import ctypes
+
+    if len(weights) != 3 or len(outs) != 3:
+        raise LeanKVError("sparse_gemm_batched_qkv_rope: q, k and v weights and outputs")
+    shapes = [colmajor_rows(w) for w in weights]
+    Z = shapes[0][1]
+    B = x.shape[0] if x.dim() == 2 else -1
+    require_cuda(x, *weights, *outs, cos, sin, k_hot, v_hot, pos_dev)
+    if x.dtype != torch.float16 or any(t.dtype != torch.float16 for t in (*weights, *outs, cos, sin)):
+        raise LeanKVError("sparse_gemm_batched_qkv_rope: x, weights, outputs and RoPE factors must be float16")
+    if x.dim() != 2 or x.shape[1] != Z or not x.is_contiguous() or any(z != Z for _, z in shapes):
+        raise LeanKVError("sparse_gemm_batched_qkv_rope: x must be a contiguous float16 [B, %d] tensor" % Z)
+    for o, (N, _) in zip(outs, shapes):
+        if tuple(o.shape) != (B, N) or not o.is_contiguous():
+            raise LeanKVError("sparse_gemm_batched_qkv_rope: outputs must be contiguous float16 [%d, %d]" % (B, N))
+    for f in (cos, sin):
+        if f.numel() != HEAD_DIM or not f.is_contiguous():
+            raise LeanKVError("sparse_gemm_batched_qkv_rope: cos / sin must be contiguous, %d each" % HEAD_DIM)
+    hot_cap = 1
+    if k_hot is not None or v_hot is not None:
+        if k_hot is None or v_hot is None or pos_dev is None or pos_dev.dtype != torch.int32:
+            raise LeanKVError("sparse_gemm_batched_qkv_rope: k_hot, v_hot and an int32 position go together")
+        hot_cap = k_hot.shape[-2]
+        rows = B * shapes[1][0] // HEAD_DIM
+        for t in (k_hot, v_hot):
+            if t.dtype != torch.float16 or not t.is_contiguous() or t.numel() != rows * hot_cap * HEAD_DIM:
+                raise LeanKVError("sparse_gemm_batched_qkv_rope: rings must be contiguous float16 [%d, %d, %d]"
+                                  % (rows, hot_cap, HEAD_DIM))
+    lib = _lib_handle()
+    n_arr = (ctypes.c_int64 * 3)(*[N for N, _ in shapes])
+    nbytes = lib.lkv_sparse_gemm_batched_multi_workspace_bytes(B, 3, n_arr, Z)
+    ws = workspaces.get(x.device, "gemm_bm", nbytes)
+    check(lib.lkv_sparse_gemm_batched_qkv_rope(ptr(x), B, (ctypes.c_void_p * 3)(*[ptr(w) for w in weights]),
+                                               (ctypes.c_float * 3)(0.0, 0.0, 0.0), n_arr, Z, ptr(cos), ptr(sin),
+                                               (ctypes.c_void_p * 3)(*[ptr(o) for o in outs]), ptr(k_hot),
+                                               ptr(v_hot), ptr(pos_dev), hot_cap, ptr(ws), ws.numel(),
+                                               stream_handle(x.device)),
+          "lkv_sparse_gemm_batched_qkv_rope")
+    return outs
+
+
 def sparse_gemm_batched_multi(x: torch.Tensor, weights, thresholds, epilogue: int = EPI_NONE,
                               residual: torch.Tensor | None = None, cos: torch.Tensor | None = None,
                               sin: torch.Tensor | None = None):
@@ -483,6 +531,50 @@ def tq_cache_append(k_new, v_new, k_hot, v_hot, k_codes, k_norms, v_codes, v_nor
                                           stream_handle(dev)),
         "lkv_tq_cache_append",
     )
+
+
+def tq_cache_evict(layers, bounds, bits: int, pos_dev: torch.Tensor) -> None:
+    """The eviction half of tq_cache_append for every layer in one launch (lkv_tq_cache_evict): layers is a list
+    of (k_codes, k_norms, v_codes, v_norms, k_hot, v_hot, PiK, PiV) on the static ring layout, R = B x kv heads
+    rows each; the token at position pos_dev - hot_cap leaves ring slot pos_dev % hot_cap for cold slot
+    pos_dev - hot_cap.  Run before the step's ring write."""
+    import ctypes
+
+    class _Layer(ctypes.Structure):
+        _fields_ = [(n, ctypes.c_void_p) for n in ("k_codes", "k_norms", "v_codes", "v_norms", "k_hot", "v_hot",
+                                                   "PiK", "PiV")]
+
+    if not layers:
+        return
+    if pos_dev.dtype != torch.int32:
+        raise LeanKVError("tq_cache_evict: pos must be an int32 device tensor")
+    k_hot0, k_codes0 = layers[0][4], layers[0][0]
+    hot_cap, cap = k_hot0.shape[-2], k_codes0.shape[-2]
+    R = k_hot0.numel() // (hot_cap * HEAD_DIM)
+    rb = packed_row_bytes(bits)
+    dev = k_hot0.device
+    arr = (_Layer * len(layers))()
+    keep = []
+    for i, (kc, kn, vc, vn, kh, vh, PiK, PiV) in enumerate(layers):
+        require_cuda(kc, kn, vc, vn, kh, vh, pos_dev)
+        for t, nm in ((kh, "k_hot"), (vh, "v_hot")):
+            if t.dtype != torch.float16 or not t.is_contiguous() or t.numel() != R * hot_cap * HEAD_DIM:
+                raise LeanKVError("tq_cache_evict: %s of layer %d must be contiguous float16 [%d, %d, %d]"
+                                  % (nm, i, R, hot_cap, HEAD_DIM))
+        for t, nm in ((kc, "k_codes"), (vc, "v_codes")):
+            if t.dtype != torch.uint8 or not t.is_contiguous() or t.numel() != R * cap * rb:
+                raise LeanKVError("tq_cache_evict: %s of layer %d must be contiguous uint8 [%d, %d, %d]"
+                                  % (nm, i, R, cap, rb))
+        for t, nm in ((kn, "k_norms"), (vn, "v_norms")):
+            if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != R * cap:
+                raise LeanKVError("tq_cache_evict: %s of layer %d must be contiguous float32 [%d, %d]"
+                                  % (nm, i, R, cap))
+        pk, pv = _pi(PiK, dev), _pi(PiV, dev)
+        keep += [pk, pv]
+        arr[i] = _Layer(ptr(kc), ptr(kn), ptr(vc), ptr(vn), ptr(kh), ptr(vh), ptr(pk), ptr(pv))
+    bd = _vec(bounds, dev, (1 << bits) - 1, "decision boundaries")
+    check(_lib_handle().lkv_tq_cache_evict(arr, len(layers), R, hot_cap, cap, ptr(bd), int(bits), ptr(pos_dev),
+                                           stream_handle(dev)), "lkv_tq_cache_evict")
 
 
 def _check_code_rows(k_codes: torch.Tensor, v_codes: torch.Tensor, bits: int, what: str) -> None:

@@ -282,16 +282,23 @@ def _qkv_rows(attn: nn.Module, x: torch.Tensor, cos: Optional[torch.Tensor] = No
     the batched kernel, as one launch, each equal to the projection's own call; with cos / sin (one position's
     fp16 RoPE factors [128]) q and k come out rotated as HF's apply_rotary_pos_emb rotates those outputs
     (modeling_mistral.py:51-81, heads of 128 dims).  None when the rows take the modules' own path."""
-    if not getattr(attn, "_teal_qkv_fused", False):
+    ws = _qkv_fusable(attn, _rows(x, attn.q_proj.weight.shape[1]) if hasattr(attn, "q_proj") else 0, x.dtype)
+    if ws is None or (cos is not None and (ws[0].shape[0] % 128 or ws[1].shape[0] % 128)):
+        return None
+    Z = ws[0].shape[1]
+    return batched_qkv(x.reshape(-1, Z), *ws, cos, sin)
+
+
+def _qkv_fusable(attn: nn.Module, rows: int, dtype):
+    """The (q, k, v) weights of a fused q/k/v patch when `rows` decode rows of `dtype` run as one batched launch
+    (every projection sends them to the batched kernel), else None."""
+    if not getattr(attn, "_teal_qkv_fused", False) or dtype != torch.float16:
         return None
     q, k, v = attn.q_proj, attn.k_proj, attn.v_proj
     Z = q.weight.shape[1]
-    rows = _rows(x, Z)
-    if x.dtype != torch.float16 or not all(_skinny_dense(rows, p.weight.shape[0], Z) for p in (q, k, v)):
+    if not all(_skinny_dense(rows, p.weight.shape[0], Z) for p in (q, k, v)):
         return None
-    if cos is not None and (q.weight.shape[0] % 128 or k.weight.shape[0] % 128):
-        return None
-    return batched_qkv(x.reshape(rows, Z), q.weight, k.weight, v.weight, cos, sin)
+    return q.weight, k.weight, v.weight
 
 
 def remove_teal(model):

@@ -139,6 +139,23 @@ def test_invalid_arguments_rejected_without_launch():
     assert rn(p, p, 0.0, 4, 4096, 4096, q, p, 1e-5, p, p, p, 1 << 30, None) == -1
     assert "aligned" in _lib.last_error()
     assert rn(p, p, 0.0, 0, 4096, 4096, p, p, 1e-5, p, p, p, 0, None) == 0
+    # q/k/v + RoPE + ring: rings go in pairs, k and v alike, a position with them
+    qr = lib.lkv_sparse_gemm_batched_qkv_rope
+    n3 = (ctypes.c_int64 * 3)(4096, 1024, 1024)
+    p3 = (ctypes.c_void_p * 3)(p, p, p)
+    t3 = (ctypes.c_float * 3)(0.0, 0.0, 0.0)
+    assert qr(p, 4, p3, t3, n3, 4096, p, p, p3, p, None, p, 64, p, 1 << 30, None) == -1
+    assert "rings" in _lib.last_error()
+    assert qr(p, 4, p3, t3, n3, 4096, p, p, p3, p, p, None, 64, p, 1 << 30, None) == -1
+    assert "position" in _lib.last_error()
+    n3b = (ctypes.c_int64 * 3)(4096, 1024, 512)
+    assert qr(p, 4, p3, t3, n3b, 4096, p, p, p3, p, p, p, 64, p, 1 << 30, None) == -1
+    assert "k and v" in _lib.last_error()
+    # batched eviction: sizes, bits, null layer table
+    assert lib.lkv_tq_cache_evict(p, 2, -1, 64, 100, p, 3, p, None) == -1 and "bad sizes" in _lib.last_error()
+    assert lib.lkv_tq_cache_evict(p, 2, 16, 64, 100, p, 5, p, None) == -1 and "bits" in _lib.last_error()
+    assert lib.lkv_tq_cache_evict(None, 2, 16, 64, 100, p, 3, p, None) == -1 and "null" in _lib.last_error()
+    assert lib.lkv_tq_cache_evict(None, 0, 16, 64, 100, None, 3, None, None) == 0
     qkv = (ctypes.c_int64 * 3)(4096, 1024, 1024)
     assert lib.lkv_sparse_gemm_batched_multi_workspace_bytes(16, 3, qkv, 4096) == sum(
         lib.lkv_sparse_gemm_batched_workspace_bytes(16, N, 4096) - 256 for N in (4096, 1024, 1024)) + 256

@@ -158,6 +158,57 @@ def test_residual_rmsnorm_equals_residual_epilogue_then_rms_norm(cuda, B, N, Z):
     assert torch.equal(inplace, ref_x) and torch.equal(yo, ref_y)
 
 
+@pytest.mark.parametrize("bits,pos,hot_cap,cap", [(3, 70, 64, 200), (3, 10, 64, 200), (4, 100, 64, 200),
+                                                  (2, 64, 64, 200), (1, 130, 32, 98), (3, 300, 64, 200)])
+def test_evict_and_ring_write_equal_cache_append(cuda, bits, pos, hot_cap, cap):
+    """tq_cache_append's two halves, split for the batched decode step: lkv_tq_cache_evict for every layer in one
+    launch, then the q/k/v launch writing the new token into the ring (lkv_sparse_gemm_batched_qkv_rope) --
+    codes, norms and rings equal tq_cache_append on the same k and v, bit for bit, and q, k, v equal the RoPE
+    epilogue's; positions before the window fills, at and after it, and past the cold store (no eviction)."""
+    from leankv_amd import kernels
+    from leankv_amd.turboquant.codebook import get_codebook_tensors
+
+    print("evict+ring case bits=%d pos=%d hot=%d cap=%d" % (bits, pos, hot_cap, cap), flush=True)
+    B, Hq, Hkv, Z, L = 4, 8, 2, 512, 3
+    g = torch.Generator().manual_seed(pos + bits)
+    rb = kernels.packed_row_bytes(bits)
+    bounds = get_codebook_tensors(128, bits, device=cuda)[1][1:-1].contiguous()
+    x = _x(B, Z, pos, cuda)
+    pos_dev = torch.tensor([pos], dtype=torch.int32, device=cuda)
+    ang = torch.arange(128, dtype=torch.float32) * 0.01 * pos
+    cos, sin = ang.cos().half().to(cuda), ang.sin().half().to(cuda)
+    caches = []
+    for li in range(L):
+        ws = [_weight(N, Z, g, cuda) for N in (Hq * 128, Hkv * 128, Hkv * 128)]
+        hot = [(torch.randn(B * Hkv, hot_cap, 128, generator=g) * 0.3).half().to(cuda) for _ in range(2)]
+        codes = [torch.randint(0, 256, (B * Hkv, cap, rb), generator=g, dtype=torch.uint8).to(cuda) for _ in range(2)]
+        norms = [torch.rand(B * Hkv, cap, generator=g).to(cuda) for _ in range(2)]
+        Pi = [torch.linalg.qr(torch.randn(128, 128, generator=g))[0].contiguous().to(cuda) for _ in range(2)]
+        caches.append((ws, hot, codes, norms, Pi))
+    # reference: the RoPE epilogue's q/k/v, then tq_cache_append per layer
+    ref = []
+    for ws, hot, codes, norms, Pi in caches:
+        q, k, v = kernels.sparse_gemm_batched_multi(x, ws, [0.0] * 3, kernels.EPI_ROPE, cos=cos, sin=sin)
+        kh, vh, kc, vc = hot[0].clone(), hot[1].clone(), codes[0].clone(), codes[1].clone()
+        kn, vn = norms[0].clone(), norms[1].clone()
+        kernels.tq_cache_append(k.view(B * Hkv, 128), v.view(B * Hkv, 128), kh, vh, kc, kn, vc, vn, Pi[0], Pi[1],
+                                bounds, bits, pos_dev)
+        ref.append((q, k, v, kh, vh, kc, kn, vc, vn))
+    # split: one evict launch for every layer, then the ring-writing q/k/v launch per layer
+    got = [(hot[0].clone(), hot[1].clone(), codes[0].clone(), norms[0].clone(), codes[1].clone(), norms[1].clone())
+           for ws, hot, codes, norms, Pi in caches]
+    kernels.tq_cache_evict([(gc[2], gc[3], gc[4], gc[5], gc[0], gc[1], c[4][0], c[4][1]) for gc, c in zip(got, caches)],
+                           bounds, bits, pos_dev)
+    for li, ((ws, hot, codes, norms, Pi), gc) in enumerate(zip(caches, got)):
+        outs = [torch.empty(B, w.shape[0], dtype=torch.float16, device=cuda) for w in ws]
+        kernels.sparse_gemm_batched_qkv_rope_out(x, ws, cos, sin, outs, gc[0], gc[1], pos_dev)
+        q, k, v, kh, vh, kc, kn, vc, vn = ref[li]
+        assert torch.equal(outs[0], q) and torch.equal(outs[1], k) and torch.equal(outs[2], v), li
+        assert torch.equal(gc[0], kh) and torch.equal(gc[1], vh), li
+        assert torch.equal(gc[2], kc) and torch.equal(gc[4], vc), li
+        assert torch.equal(gc[3], kn) and torch.equal(gc[5], vn), li
+
+
 def test_empty_sizes(cuda):
     """Z = 0: every product is an empty sum (0; SwiGLU of zeros is 0, the residual add returns the residual);
     B = 0 touches nothing; a zero-column product beside others is skipped."""
