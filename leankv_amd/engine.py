@@ -242,10 +242,11 @@ class BatchedEngine:
     kernels, o_proj, residual adds, the (patched) MLP and lm_head -- with the position on the device, so the
     whole step replays without the host.  RMSNorm runs as one lkv_rmsnorm launch (the B = 1 step's
     arithmetic) and RoPE as one lkv_rope_f16 launch (HF's fp16 arithmetic bit for bit) instead of HF's
-    chains of elementwise kernels (in the reduce of the patched q/k/v launch when there is one), and each
-    residual add runs with the RMSNorm after it in one launch behind the patched o_proj / down_proj product
-    (the same bits as the add and lkv_rmsnorm): with the model's RMSNorm modules on lkv_rmsnorm the logits
-    equal the
+    chains of elementwise kernels (in the reduce of the patched q/k/v launch when there is one, which then
+    also writes the new token into the hot ring, the token leaving every layer's window being evicted by one
+    launch at the step's start: TurboQuantCache.update's two halves), and each residual add runs with the
+    RMSNorm after it in one launch behind the patched o_proj / down_proj product (the same bits as the add and
+    lkv_rmsnorm): with the model's RMSNorm modules on lkv_rmsnorm the logits equal the
     HF forward's bit for bit; with HF's torch RMSNorm they differ from it in the last bits of the norms,
     as the B = 1 step's do.  tok [B] is fed, logits [B, vocab] come out; the cache's host counters are the
     caller's to advance (GenerateFastPath does)."""
