@@ -303,7 +303,7 @@ class BatchedEngine:
         residual = x
         # a fused TEAL q/k/v patch: the three products and RoPE on q and k as one launch (with the ring write)
         appended = False
-        if self._ring:
+        if self._ring and h.dtype == torch.float16:  # (the step's start evicted every layer's leaving token)
             ws = _qkv_fusable(at, B, h.dtype)
             qp, kp, vp = (torch.empty(B, w.shape[0], dtype=torch.float16, device=self.dev) for w in ws)
             kernels.sparse_gemm_batched_qkv_rope_out(h.reshape(B, -1).contiguous(), list(ws), cos.view(-1),
