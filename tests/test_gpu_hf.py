@@ -358,6 +358,32 @@ def test_generate_fast_path_batch(cuda, bits, hot, B):
     assert fast.forward.steps["batch"] == before["batch"]
 
 
+@pytest.mark.parametrize("B", [8, 16])
+def test_generate_fast_path_batch_mistral_shape(cuda, B):
+    """The batched decode step at the Mistral-7B layer shape (hidden 4096, ffn 14336, 32 / 8 heads; two layers,
+    a small vocabulary): the grouped q|k|v (+ RoPE, ring write), gate|up (+ SwiGLU) and residual + RMSNorm
+    launches at the chunk sizes of the real model, the per-step eviction; logits equal the patched HF forward's,
+    teacher-forced on the same tokens, bit for bit, and so do the caches."""
+    print("batch mistral-shape case B=%d" % B, flush=True)
+    shape = dict(hidden_size=4096, intermediate_size=14336, num_attention_heads=32, num_key_value_heads=8,
+                 num_hidden_layers=2)
+    (fast, ca), (slow, cb) = _teal_pair(cuda, 80 + B, bits=3, hot=64, **shape)
+    ids = _ids(80, 81, B=B)
+    res = _generate(fast, ids.to(cuda), ca, 8)
+    assert fast.forward.steps == {"engine": 0, "batch": 7, "forward": 1}, fast.forward.steps
+    new = res.sequences[:, 80:]
+    with torch.no_grad():
+        lg = slow(ids.to(cuda), past_key_values=cb, use_cache=True, logits_to_keep=1).logits[:, -1]
+        assert torch.equal(lg.float(), res.scores[0])
+        for i in range(7):
+            lg = slow(new[:, i:i + 1], past_key_values=cb, use_cache=True).logits[:, -1]
+            assert torch.equal(lg.float(), res.scores[i + 1]), i
+    for li in range(2):
+        for a, b in ((ca._k_codes, cb._k_codes), (ca._v_codes, cb._v_codes), (ca._k_norms, cb._k_norms),
+                     (ca._v_norms, cb._v_norms), (ca._k_hot, cb._k_hot), (ca._v_hot, cb._v_hot)):
+            assert torch.equal(a[li], b[li]), li
+
+
 def test_generate_fast_path_default_rmsnorm(cuda):
     """The default configuration: optimize_model's fast path on a model that keeps HF's torch RMSNorm, vs the
     patched HF forward (torch RMSNorm too) teacher-forced on the fast path's tokens.  The fused step's RMSNorm
