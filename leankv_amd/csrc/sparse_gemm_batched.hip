@@ -24,6 +24,12 @@
 // fp16 directly when there is one chunk).  At 40 % sparsity and B = 4 the
 // union keeps ~97 % of the rows: one pass over ~the dense weight instead of
 // 4 x 60 % of it.
+//
+// The decode step of B > 1 sequences also groups products of one x in one
+// launch (q, k, v; gate, up), each product keeping its own chunking, and gives
+// the chunk reduce an epilogue: HF's SwiGLU, the fp16 residual add, RoPE with
+// the new token's hot-ring write, or (in a one-block-per-row kernel of its
+// own) the residual add and the next RMSNorm.
 #include <stdlib.h>
 
 #include "kernels.h"
