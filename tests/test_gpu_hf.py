@@ -323,10 +323,12 @@ def test_generate_fast_path_matches_hf_forward(cuda, bits, hot):
     assert fast.forward.engine.cache is c2
 
 
-@pytest.mark.parametrize("bits,hot,B", [(3, 64, 4), (2, 128, 4), (3, 64, 16)])
+@pytest.mark.parametrize("bits,hot,B", [(3, 64, 4), (2, 128, 4), (3, 64, 16), (4, 32, 3), (1, 64, 11),
+                                        (3, 64, 32)])
 def test_generate_fast_path_batch(cuda, bits, hot, B):
-    """B = 4 and 16 sequences of one length (the batched kernel's v_dot2 and matrix-core paths, the grouped
-    q/k/v and gate/up launches, the residual adds fused into the projections' reduce): generate's decode calls
+    """B = 3 to 32 sequences of one length (the batched kernel's v_dot2 and matrix-core paths, the grouped
+    q/k/v and gate/up launches, the fused residual + RMSNorm, the split cache update; at B = 32 the
+    projections are torch's GEMM, the reference's dispatch for larger inputs): generate's decode calls
     replay BatchedEngine (the HF forward's own calls with the position on the device); its logits equal the
     patched HF forward's, teacher-forced on the same tokens from the same prefill, bit for bit, and so do the
     caches.  A left-padded batch falls back."""
