@@ -268,43 +268,46 @@ __global__ __launch_bounds__(kNT) void sparse_gemm_batched_kernel(BatchedArgs P)
 // flight per thread while the previous one is multiplied.  fp16 products are
 // exact in fp32 and the sums fp32, as in the v_dot2 kernel (summation order
 // differs).
-constexpr int kMB = 16;               // batch rows per block (the MFMA's M)
+constexpr int kMB = 16;               // batch rows per MFMA tile (the MFMA's M)
 constexpr int kKB = 32;               // list entries per block of entries (the MFMA's K)
 constexpr int kPairs = kKB / 2;       // row pairs per block of entries
 constexpr int kBRow = kBN + 4;        // words per pair row of the weight tile in LDS (bank spread)
 
-template <int BZ>
+// MT tiles of 16 batch rows per block (MT = 2 from 17 rows on: one weight pass
+// serves 32 rows, each weight tile read from LDS feeding both tiles' MFMAs).
+template <int BZ, int MT>
 __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P) {
   static_assert(BZ % kNT == 0 && BZ % kKB == 0, "chunk shape");
   constexpr int E = BZ / kNT;
+  constexpr int kRows = kMB * MT;
   constexpr int kXRow = BZ + kKB + 8;  // fp16 per batch row of the listed activations (16-byte rows)
   __shared__ int s_idx[BZ + kKB];
-  __shared__ __align__(16) uint16_t s_xh[kMB][kXRow];
+  __shared__ __align__(16) uint16_t s_xh[kRows][kXRow];
   __shared__ __align__(16) uint32_t s_w[2][kPairs * kBRow];
   __shared__ int s_cnt[kNT / kWave];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const BatchedSeg S = seg_of(P, blockIdx.x);
   const int slab = blockIdx.x - S.slab0, chunk = blockIdx.y;
-  const int b0 = blockIdx.z * kMB;
-  const int nb = min(kMB, P.B - b0);
+  const int b0 = blockIdx.z * kRows;
+  const int nb = min(kRows, P.B - b0);
   const int z0 = chunk * BZ, n0 = slab * kBN;
   const int Z = P.Z, N = S.N;
 
   // ---- 0. the group's activations into registers, every load issued before
   // the first is used (address clamped to element 0, value selected after)
-  float xv[kMB][E];
+  float xv[kRows][E];
   {
-    uint16_t raw[kMB][E];
+    uint16_t raw[kRows][E];
 #pragma unroll
-    for (int b = 0; b < kMB; ++b)
+    for (int b = 0; b < kRows; ++b)
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const int z = z0 + e * kNT + tid;
         raw[b][e] = P.x[(b < nb && z < Z) ? static_cast<size_t>(b0 + b) * Z + z : 0];
       }
 #pragma unroll
-    for (int b = 0; b < kMB; ++b)
+    for (int b = 0; b < kRows; ++b)
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const int z = z0 + e * kNT + tid;
@@ -319,7 +322,7 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
     const int z = z0 + e * kNT + tid;
     bool keep = false;
 #pragma unroll
-    for (int b = 0; b < kMB; ++b) keep = keep || fabsf(xv[b][e]) > S.t;
+    for (int b = 0; b < kRows; ++b) keep = keep || fabsf(xv[b][e]) > S.t;
     keep = keep && z < Z;
     const uint64_t mask = wave_ballot(keep);
     if (lane == 0) s_cnt[wave] = __popcll(mask);
@@ -335,7 +338,7 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
       const int pos = off + lane_prefix(mask);
       s_idx[pos] = z;
 #pragma unroll
-      for (int b = 0; b < kMB; ++b) s_xh[b][pos] = f2h(fabsf(xv[b][e]) > S.t ? xv[b][e] : 0.f);  // exact
+      for (int b = 0; b < kRows; ++b) s_xh[b][pos] = f2h(fabsf(xv[b][e]) > S.t ? xv[b][e] : 0.f);  // exact
     }
     total += tot;
     __syncthreads();
@@ -345,7 +348,7 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
   if (total > 0 && tid < padded - total) {
     s_idx[total + tid] = s_idx[total - 1];
 #pragma unroll
-    for (int b = 0; b < kMB; ++b) s_xh[b][total + tid] = 0;
+    for (int b = 0; b < kRows; ++b) s_xh[b][total + tid] = 0;
   }
   __syncthreads();
 
@@ -384,19 +387,25 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
       *reinterpret_cast<u32x4b*>(dst + 4) = o[1];
     }
   };
-  f32x4 acc[4];
+  f32x4 acc[MT][4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int m = lane & 15, kg = lane >> 4;
   auto multiply = [&](int kb, int buf) {
-    const u32x4b a = *reinterpret_cast<const u32x4b*>(&s_xh[m][kb * kKB + 8 * kg]);
+    u32x4b a[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) a[mt] = *reinterpret_cast<const u32x4b*>(&s_xh[kMB * mt + m][kb * kKB + 8 * kg]);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int cc = 64 * wave + 16 * t + m;  // this lane's B column
       u32x4b bw;
 #pragma unroll
       for (int i = 0; i < 4; ++i) bw[i] = s_w[buf][(4 * kg + i) * kBRow + cc];
-      acc[t] = mfma16x16x32(__builtin_bit_cast(u32x4, a), __builtin_bit_cast(u32x4, bw), acc[t]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt][t] = mfma16x16x32(__builtin_bit_cast(u32x4, a[mt]), __builtin_bit_cast(u32x4, bw), acc[mt][t]);
     }
   };
   if (nkb > 0) {
@@ -420,18 +429,20 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
     }
   }
 
-  // ---- 3. lane (m, kg) holds batch rows 4 kg + i of column 64 wave + 16 t + m
+  // ---- 3. lane (m, kg) holds batch rows 16 mt + 4 kg + i of column 64 wave + 16 t + m
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int lc = 64 * wave + 16 * t + m;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int b = 4 * kg + i;
+      const int b = kMB * mt + 4 * kg + i;
       if (b < nb) {
         if (P.direct) {
-          if (n0 + lc < N) S.y[static_cast<size_t>(b0 + b) * N + n0 + lc] = f2h(acc[t][i]);
+          if (n0 + lc < N) S.y[static_cast<size_t>(b0 + b) * N + n0 + lc] = f2h(acc[mt][t][i]);
         } else {
-          S.part[((static_cast<size_t>(b0 + b) * S.nslab + slab) * P.nchunk + chunk) * kBN + lc] = acc[t][i];
+          S.part[((static_cast<size_t>(b0 + b) * S.nslab + slab) * P.nchunk + chunk) * kBN + lc] = acc[mt][t][i];
         }
       }
     }
@@ -579,6 +590,21 @@ bool launch_nb(const BatchedArgs& P, int bz, dim3 grid, hipStream_t st) {
   }
 }
 
+template <int MT>
+bool launch_mfma(const BatchedArgs& P, int bz, dim3 grid, hipStream_t st) {
+  switch (bz) {
+    case 256: hipLaunchKernelGGL((sparse_gemm_mfma_kernel<256, MT>), grid, dim3(kNT), 0, st, P); return true;
+    case 512: hipLaunchKernelGGL((sparse_gemm_mfma_kernel<512, MT>), grid, dim3(kNT), 0, st, P); return true;
+    case 1024:
+      if constexpr (MT == 1) {  // 32-row groups stop at 512-row chunks (batched_bz)
+        hipLaunchKernelGGL((sparse_gemm_mfma_kernel<1024, MT>), grid, dim3(kNT), 0, st, P);
+        return true;
+      }
+      return false;
+    default: return false;
+  }
+}
+
 // Batches of at least this many rows run on the matrix-core kernel in groups
 // of 16 (LKV_BATCHED_MFMA=k for sweeps; 0 never).  Measured on one MI355X at
 // the Mistral-7B shapes (us, VALU / matrix-core kernel): 2 rows at 40 %
@@ -594,9 +620,9 @@ int64_t mfma_min_rows() {
 bool use_mfma(int64_t B) { return mfma_min_rows() > 0 && B >= mfma_min_rows(); }
 
 // Batch rows per block: the next power of two up to 8 on the VALU kernel, 16
-// on the matrix-core kernel.
+// on the matrix-core kernel, 32 (two MFMA tiles) above 16 rows.
 int group_rows(int64_t B) {
-  if (use_mfma(B)) return kMB;
+  if (use_mfma(B)) return B > kMB ? 2 * kMB : kMB;
   return B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
 }
 
@@ -604,7 +630,9 @@ int group_rows(int64_t B) {
 // batch groups counted as extra blocks.
 int batched_bz(int64_t B, int64_t N, int64_t Z) {
   const int64_t groups = (B + group_rows(B) - 1) / group_rows(B);
-  return gemv_pick_bz(gemv_slabs(N) * groups, Z, 6);
+  const int bz = gemv_pick_bz(gemv_slabs(N) * groups, Z, 6);
+  // 32-row groups: the 1024-row chunk's LDS would leave one block per CU
+  return group_rows(B) > kMB && bz > 512 ? 512 : bz;
 }
 
 // What follows the chunk sums (the entry points' epilogue arguments).
@@ -674,12 +702,7 @@ bool launch_products(const void* x, int64_t B, int64_t Z, int n, const void* con
                     static_cast<unsigned>((B + nbr - 1) / nbr));
     bool ok;
     if (use_mfma(B)) {
-      switch (bz) {
-        case 256: hipLaunchKernelGGL(sparse_gemm_mfma_kernel<256>, grid, dim3(kNT), 0, st, P); ok = true; break;
-        case 512: hipLaunchKernelGGL(sparse_gemm_mfma_kernel<512>, grid, dim3(kNT), 0, st, P); ok = true; break;
-        case 1024: hipLaunchKernelGGL(sparse_gemm_mfma_kernel<1024>, grid, dim3(kNT), 0, st, P); ok = true; break;
-        default: ok = false;
-      }
+      ok = nbr == kMB ? launch_mfma<1>(P, bz, grid, st) : launch_mfma<2>(P, bz, grid, st);
     } else {
       ok = nbr == 1 ? launch_nb<1>(P, bz, grid, st)
          : nbr == 2 ? launch_nb<2>(P, bz, grid, st)

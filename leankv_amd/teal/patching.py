@@ -123,10 +123,10 @@ def _rows(x: torch.Tensor, Z: int) -> int:
 
 def _skinny_gateup(rows: int) -> bool:
     """Whether a fused gate/up + SwiGLU of `rows` decode rows runs as one batched launch with the SwiGLU in its
-    reduce (else the MLP's own modules run).  Up to 16 rows the grouped launch reads x once for both products
+    reduce (else the MLP's own modules run).  Up to 32 rows the grouped launch reads x once for both products
     and saves the two elementwise kernels of the SwiGLU, where torch's GEMM only edges out the batched kernel
-    on one projection alone."""
-    return 1 < rows <= 16
+    on one projection alone (32 rows: 54.3 + 5.6 us against 2 x 24.0 + 4.9 + 4.6)."""
+    return 1 < rows <= 32
 
 
 def _skinny_dense(rows: int, N: int, Z: int) -> bool:
@@ -134,8 +134,11 @@ def _skinny_dense(rows: int, N: int, Z: int) -> bool:
     GEMM.  Measured on one MI355X, back-to-back calls at the Mistral-7B shapes over the column-major weight, torch
     vs the batched kernel in us: down [4096 x 14336] 50 / 25 for 8 rows, 49-52 / 26 for 12-16; q|k|v
     [6144 x 4096] 19 / 15 and o [4096 x 4096] 19 / 12-15 for 8-16 rows; gate/up [14336 x 4096] 23-24 / 24 for 8
-    rows, 23 / 25 for 12-16 (torch's GEMM then wins by a little)."""
-    return 1 < rows <= 16 and (rows <= 8 or N <= 2 * Z)
+    rows, 23 / 25 for 12-16 (torch's GEMM then wins by a little).  17-32 rows run as one group of 32 (two MFMA
+    tiles per weight pass): q|k|v grouped 16.2 + 3.9 (reduce) against 14.4 + 2 x 9.3, o 13.8 + 4.2 against 14.4,
+    down 28.3 + 4.2 against ~28; the decode step's fusions (RoPE, ring write, residual + RMSNorm) ride on these
+    launches, so the rule keeps every projection but gate / up on the batched kernel up to 32 rows."""
+    return 1 < rows <= 32 and (rows <= 8 or N <= 2 * Z)
 
 
 def _patch_linear_with_kernel(linear: nn.Linear, threshold: float) -> None:

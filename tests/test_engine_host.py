@@ -61,20 +61,20 @@ def test_optimize_model_paged_cache_raises_as_without_flashinfer():
 
 def test_multi_row_projection_dispatch_rule():
     """Which multi-row decode products the patched projections send to the batched kernel (dense, threshold
-    0) rather than torch's GEMM: 2-8 rows, or up to 16 unless the weight has more than twice as many outputs as
+    0) rather than torch's GEMM: 2-8 rows, or up to 32 unless the weight has more than twice as many outputs as
     inputs (gate / up); one row is the sparse GEMV's and prefill-sized inputs stay on torch."""
     from leankv_amd.teal.patching import _skinny_dense
 
     assert not _skinny_dense(1, 4096, 14336)
     assert all(_skinny_dense(r, 14336, 4096) for r in range(2, 9))
-    assert not _skinny_dense(9, 14336, 4096) and not _skinny_dense(16, 14336, 4096)
-    assert _skinny_dense(16, 4096, 4096) and _skinny_dense(16, 6144, 4096)
-    assert _skinny_dense(16, 4096, 14336) and not _skinny_dense(17, 4096, 14336)
+    assert not _skinny_dense(9, 14336, 4096) and not _skinny_dense(32, 14336, 4096)
+    assert _skinny_dense(16, 4096, 4096) and _skinny_dense(32, 6144, 4096)
+    assert _skinny_dense(32, 4096, 14336) and not _skinny_dense(33, 4096, 14336)
     assert not _skinny_dense(4096, 4096, 4096)
-    # the fused gate/up + SwiGLU takes 2-16 rows as one grouped launch, whatever the projection rule says
+    # the fused gate/up + SwiGLU takes 2-32 rows as one grouped launch, whatever the projection rule says
     from leankv_amd.teal.patching import _skinny_gateup
 
-    assert [r for r in range(0, 40) if _skinny_gateup(r)] == list(range(2, 17))
+    assert [r for r in range(0, 40) if _skinny_gateup(r)] == list(range(2, 33))
 
 
 def _fast_path_on(m, bits=3, hot=64, n=10, B=1):

@@ -36,7 +36,8 @@ def _quantile_t(x, q):
 # (gate-sized next to k-sized: separate launches inside the one call)
 CASES = [(2, (4096, 1024, 1024), 4096), (4, (4096, 1024, 1024), 4096), (8, (4096, 1024, 1024), 4096),
          (16, (4096, 1024, 1024), 4096), (11, (1032, 256, 520), 333), (3, (24, 8, 16), 100),
-         (5, (14336, 1024), 4096)]
+         (5, (14336, 1024), 4096), (24, (4096, 1024, 1024), 4096), (32, (14336, 14336), 4096),
+         (37, (1032, 256, 520), 333)]
 
 
 @pytest.mark.parametrize("B,Ns,Z", CASES)
@@ -58,7 +59,8 @@ def test_multi_equals_single_calls(cuda, B, Ns, Z):
 
 
 @pytest.mark.parametrize("B,N,Z,q", [(4, 14336, 4096, 0.0), (16, 14336, 4096, 0.0), (11, 1032, 333, 0.4),
-                                     (3, 24, 100, 0.3), (8, 2048, 1000, 0.5)])
+                                     (3, 24, 100, 0.3), (8, 2048, 1000, 0.5), (32, 14336, 4096, 0.0),
+                                     (21, 1032, 333, 0.4)])
 def test_swiglu_epilogue_equals_torch_on_single_calls(cuda, B, N, Z, q):
     from leankv_amd import kernels
 
@@ -92,7 +94,8 @@ def test_swiglu_epilogue_every_fp16_gate_value(cuda):
     assert torch.equal(h, F.silu(gate.to(cuda)) * up.to(cuda))
 
 
-@pytest.mark.parametrize("B,N,Z", [(4, 4096, 4096), (16, 4096, 14336), (11, 1032, 333), (3, 24, 100)])
+@pytest.mark.parametrize("B,N,Z", [(4, 4096, 4096), (16, 4096, 14336), (11, 1032, 333), (3, 24, 100),
+                                   (32, 4096, 14336)])
 def test_residual_epilogue_equals_torch_add(cuda, B, N, Z):
     from leankv_amd import kernels
 
@@ -114,7 +117,7 @@ def test_residual_epilogue_equals_torch_add(cuda, B, N, Z):
 # launches: v must stay unrotated), one chunk with an odd number of heads (a reduce block of one head)
 @pytest.mark.parametrize("B,Ns,Z", [(4, (4096, 1024, 1024), 4096), (16, (4096, 1024, 1024), 4096),
                                     (8, (512, 256), 1000), (5, (14336, 1024, 1024), 4096),
-                                    (3, (384, 128, 256), 100)])
+                                    (3, (384, 128, 256), 100), (32, (4096, 1024, 1024), 4096)])
 def test_rope_epilogue_equals_rope_f16_on_single_calls(cuda, B, Ns, Z):
     from leankv_amd import kernels
 
@@ -134,7 +137,7 @@ def test_rope_epilogue_equals_rope_f16_on_single_calls(cuda, B, Ns, Z):
 
 
 @pytest.mark.parametrize("B,N,Z", [(4, 4096, 4096), (16, 4096, 14336), (3, 8192, 512), (11, 1032, 333),
-                                   (5, 24, 100), (2, 64, 0)])
+                                   (5, 24, 100), (2, 64, 0), (32, 4096, 14336)])
 def test_residual_rmsnorm_equals_residual_epilogue_then_rms_norm(cuda, B, N, Z):
     """The product, the fp16 residual add and the next RMSNorm with one launch after the product: x_out equals
     the residual epilogue's output and y_out lkv_rmsnorm of it, bit for bit (also in place, x_out = residual;
@@ -254,7 +257,7 @@ class _MLP(nn.Module):
         return self.down_proj(self.act_fn(self.gate_proj(x)) * self.up_proj(x))
 
 
-@pytest.mark.parametrize("B", [4, 16])
+@pytest.mark.parametrize("B", [4, 16, 32])
 def test_patched_qkv_and_mlp_rows(cuda, B):
     """The TEAL patches at B > 1 decode rows (Mistral-7B shapes): q_proj runs the three dense products in one
     launch and k_proj / v_proj hand back theirs, each equal to its own batched call (threshold 0); the fused

@@ -360,7 +360,7 @@ def test_generate_fast_path_batch(cuda, bits, hot, B):
     assert fast.forward.steps["batch"] == before["batch"]
 
 
-@pytest.mark.parametrize("B", [8, 16])
+@pytest.mark.parametrize("B", [8, 16, 32])
 def test_generate_fast_path_batch_mistral_shape(cuda, B):
     """The batched decode step at the Mistral-7B layer shape (hidden 4096, ffn 14336, 32 / 8 heads; two layers,
     a small vocabulary): the grouped q|k|v (+ RoPE, ring write), gate|up (+ SwiGLU) and residual + RMSNorm

@@ -91,13 +91,15 @@ def _batched_case(B, N, Z, q, seed, dev):
     return Y, ref, X, W, t, wc
 
 
-# B in 1 .. 24 (the v_dot2 kernel's groups of up to 8 rows below 8 rows, the matrix-core kernel's groups
-# of 16 from 8 on, a partial last group), single-chunk and many-chunk shapes, a ragged N on both kernels,
-# dense (q = 0) and 90 % sparse rows.
+# B in 1 .. 40 (the v_dot2 kernel's groups of up to 8 rows below 8 rows, the matrix-core kernel's groups
+# of 16 from 8 on and of 32 (two MFMA tiles) from 17 on, a partial last group), single-chunk and
+# many-chunk shapes, a ragged N on both kernels, dense (q = 0) and 90 % sparse rows.
 @pytest.mark.parametrize("B,N,Z,q", [(2, 4096, 14336, 0.4), (4, 1024, 4096, 0.4), (8, 14336, 4096, 0.4),
                                      (3, 1032, 333, 0.3), (13, 2048, 1000, 0.5), (1, 520, 7000, 0.9),
                                      (5, 24, 257, 0.0), (16, 4096, 4096, 0.4), (24, 1024, 3000, 0.0),
-                                     (11, 4096, 14336, 0.4), (9, 1032, 333, 0.3), (8, 24, 100, 0.5)])
+                                     (11, 4096, 14336, 0.4), (9, 1032, 333, 0.3), (8, 24, 100, 0.5),
+                                     (24, 4096, 4096, 0.4), (32, 1032, 333, 0.3), (17, 14336, 4096, 0.0),
+                                     (40, 1024, 3000, 0.0)])
 def test_sparse_gemm_batched(cuda, B, N, Z, q):
     Y, ref, X, W, t, wc = _batched_case(B, N, Z, q, seed=B * 100 + N % 97, dev=cuda)
     assert ot.rel_err(Y.numpy(), ref) < 1e-3

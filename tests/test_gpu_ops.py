@@ -247,11 +247,12 @@ def test_out_ops_in_a_captured_graph(cuda):
 
 
 @pytest.mark.parametrize("N,Z,rows", [(4096, 14336, 2), (4096, 14336, 16), (14336, 4096, 8), (1024, 4096, 4),
-                                      (14336, 4096, 16), (520, 333, 3), (4096, 4096, 12)])
+                                      (14336, 4096, 16), (520, 333, 3), (4096, 4096, 12), (4096, 14336, 24),
+                                      (1032, 333, 32), (14336, 4096, 32)])
 def test_patched_linear_multi_row_is_dense(cuda, N, Z, rows):
     """A TEAL-patched projection called on several decode rows computes the dense product, as the reference's
     dispatch does (leankv/teal/patching.py:169-180), whether it runs on the batched kernel (threshold 0: up to 8
-    rows, or 16 unless N > 2 Z) or on torch's F.linear; exact zeros in x contribute nothing either way."""
+    rows, or 32 unless N > 2 Z) or on torch's F.linear; exact zeros in x contribute nothing either way."""
     import torch.nn as nn
 
     from leankv_amd.teal.patching import _patch_linear_with_kernel, _skinny_dense
