@@ -37,7 +37,7 @@ import torch
 
 from .. import kernels as _k  # also registers torch.ops.leankv (the cache's kernels go through the dispatcher)
 from .codebook import get_codebook_tensors
-from .rotation import generate_rotation_matrix
+from .rotation import generate_rotation_matrices
 
 _ACTIVE = None  # weakref to the cache whose update() ran last (read by the attention function)
 
@@ -75,10 +75,9 @@ class TurboQuantCache:
         self._seen_tokens = 0
         self._seq_lengths = [0] * num_layers
         self._init_cap = max(int(max_seq_len), 1)
-        self.PiK = [generate_rotation_matrix(head_dim, self._device, torch.float32, seed + 2 * i)
-                    for i in range(num_layers)]
-        self.PiV = [generate_rotation_matrix(head_dim, self._device, torch.float32, seed + 2 * i + 1)
-                    for i in range(num_layers)]
+        rot = generate_rotation_matrices(head_dim, [seed + j for j in range(2 * num_layers)], self._device,
+                                         torch.float32)
+        self.PiK, self.PiV = rot[0::2], rot[1::2]  # layer i: seeds seed + 2i, seed + 2i + 1
         self.centroids, bnd = get_codebook_tensors(head_dim, bits, self._device, torch.float32)
         self.decision_boundaries = bnd[1:-1].contiguous()
         self._row_bytes = _k.packed_row_bytes(bits)

@@ -27,7 +27,7 @@ import torch
 
 from .. import kernels as _k
 from .codebook import get_codebook_tensors
-from .rotation import generate_rotation_matrix
+from .rotation import generate_rotation_matrices
 
 
 class PagedTurboQuantCache:
@@ -52,8 +52,8 @@ class PagedTurboQuantCache:
         self.page_size, self.max_pages, self.max_batch_size = page_size, max_pages, max_batch_size
         self._device = torch.device(device) if device is not None else torch.device("cuda")
         dev = self._device
-        self.PiK = [generate_rotation_matrix(head_dim, dev, torch.float32, seed + 2 * i) for i in range(num_layers)]
-        self.PiV = [generate_rotation_matrix(head_dim, dev, torch.float32, seed + 2 * i + 1) for i in range(num_layers)]
+        rot = generate_rotation_matrices(head_dim, [seed + j for j in range(2 * num_layers)], dev, torch.float32)
+        self.PiK, self.PiV = rot[0::2], rot[1::2]  # layer i: seeds seed + 2i, seed + 2i + 1
         self.centroids, bnd = get_codebook_tensors(head_dim, bits, dev, torch.float32)
         self.decision_boundaries = bnd[1:-1].contiguous()
         L, H, ps = num_layers, num_kv_heads, page_size

@@ -98,6 +98,24 @@ def test_product_rotation_matches_oracle():
         assert torch.equal(generate_rotation_matrix(128, "cpu", torch.float32, seed), oq.rotation_matrix(128, seed))
 
 
+def test_rotation_memo_hands_out_copies():
+    """Each (d, seed) is factorised once per process: later calls, and the caches' one-copy list, must
+    still equal the oracle after a caller has written into an earlier result."""
+    from leankv_amd.turboquant.cache import TurboQuantCache
+    from leankv_amd.turboquant.rotation import generate_rotation_matrices, generate_rotation_matrix
+
+    first = generate_rotation_matrix(128, "cpu", torch.float32, 42)
+    first.zero_()
+    assert torch.equal(generate_rotation_matrix(128, "cpu", torch.float32, 42), oq.rotation_matrix(128, 42))
+    many = generate_rotation_matrices(128, [44, 42, 43], "cpu")
+    for m, seed in zip(many, (44, 42, 43)):
+        assert m.is_contiguous() and torch.equal(m, oq.rotation_matrix(128, seed))
+    c = TurboQuantCache(bits=3, num_layers=3, device="cpu", seed=7)
+    for i in range(3):
+        assert torch.equal(c.PiK[i], oq.rotation_matrix(128, 7 + 2 * i))
+        assert torch.equal(c.PiV[i], oq.rotation_matrix(128, 8 + 2 * i))
+
+
 # --------------------------------------------------------------- pack/unpack
 def _brute_pack(idx, bits):
     width = 1 if bits == 1 else (2 if bits == 2 else 4)
