@@ -24,8 +24,9 @@
 //        3-bit codes are decoded on the VALU with v_perm_b32 table lookups;
 //        4-bit codes through a 256-entry LDS table (byte -> fp16 pair);
 //      * online softmax in the exp2 domain, per lane, with the max taken
-//        across the 4 lanes of a head by two permlane swaps; the rescale of
-//        the accumulators runs only when some head's max grew;
+//        across the 4 lanes of a head by two permlane swaps; the offset keeps
+//        a headroom above the max, so the rescale of the accumulators runs
+//        only when some head's score passes it;
 //      * values, transposed: the same MFMA with A = 16 dims x 32 tokens of
 //        centroid values (a lane's 8 tokens of one dim, transposed from the
 //        decoded code dwords with v_perm_b32) and B = p * n_t taken straight
@@ -328,11 +329,12 @@ __device__ __forceinline__ void attend_block(const BlockRegs& R, int t0, int t_e
       s[4 * tt + i] = (!MASKED || t0 + 16 * tt + 4 * g + i < t_end) ? v : -INFINITY;
     }
   }
-  // ---- online softmax; the rescale runs only when some head's max grew
+  // ---- online softmax; the rescale runs only when some head's score passes
+  // its offset (the max plus kHeadroom when it last moved)
   float bm = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
   bm = xgroup_max(bm);  // finite: token t0 of the block is always valid
-  const float mn = fmaxf(S.m, bm);
-  if (__builtin_amdgcn_ballot_w64(mn > S.m) != 0) {
+  if (__builtin_amdgcn_ballot_w64(bm > S.m) != 0) {
+    const float mn = bm > S.m ? bm + kHeadroom : S.m;
     const float alpha = fast_exp2(S.m - mn);  // 0 on the first block (m = -inf)
 #pragma unroll
     for (int t = 0; t < 8; ++t)

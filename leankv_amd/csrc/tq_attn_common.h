@@ -72,6 +72,24 @@ __device__ __forceinline__ float vmax(float a, float b) {
   asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// Online-softmax offset headroom, log2 units.  When a block's score exceeds
+// the running offset m, m moves to that score plus the headroom, so the
+// following blocks, whose scores mostly stay below it, skip the rescale of
+// the accumulators.  Any offset at or above every score seen gives the same
+// softmax (sums and accumulators are relative to it); every weight stays
+// exp2(s - m) <= 1, so p * n_v cannot overflow its fp16 operand, and weights
+// shrink by at most 2^-headroom, far above the fp16 denormal floor for any
+// weight that matters.  0 gives the plain running maximum.
+#ifndef LKV_SOFTMAX_HEADROOM
+#define LKV_SOFTMAX_HEADROOM 4.0f
+#endif
+constexpr float kHeadroom = LKV_SOFTMAX_HEADROOM;
 
 // Max / sum over the four lanes l, l^16, l^32, l^48 (the lane groups that
 // hold the other tokens of the same head), result in all four.

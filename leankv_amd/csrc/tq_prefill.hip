@@ -26,7 +26,9 @@
 //      * scores transposed, A = 16 keys x 32 dims from LDS, B = its rotated
 //        queries (registers), so a lane holds 8 keys of one column;
 //      * the online softmax per lane (key norms, causal mask, exp2 domain,
-//        max and sum across the 4 lanes of a column by permlane swaps);
+//        max and sum across the 4 lanes of a column by permlane swaps; the
+//        offset keeps a headroom above the max, so most tiles skip the
+//        rescale of the accumulators);
 //      * values transposed, A = 16 dims x 32 keys from LDS, B = p * n_t from
 //        the lane's own softmax registers.
 //      Each thread loads its share of a tile's codes two tiles ahead into
@@ -521,11 +523,11 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
         for (int jj = 0; jj < 16; ++jj)
           s[jj] = t0 + 16 * (jj >> 2) + 4 * g + (jj & 3) < lim[ct] ? s[jj] : -INFINITY;
       }
-      float mx = s[0];
+      float mx = vmax3(s[0], s[1], s[2]);
 #pragma unroll
-      for (int jj = 1; jj < 16; ++jj) mx = vmax(mx, s[jj]);
+      for (int jj = 3; jj < 16; jj += 2) mx = jj + 1 < 16 ? vmax3(mx, s[jj], s[jj + 1]) : vmax(mx, s[jj]);
       mx = xgroup_max(mx);
-      const float mn = fmaxf(m[ct], mx);
+      const float mn = mx > m[ct] ? mx + kHeadroom : m[ct];  // -inf stays -inf
       const float mu = mn == -INFINITY ? 0.f : mn;
       const float alpha = fast_exp2(m[ct] - mu);
       m[ct] = mn;
