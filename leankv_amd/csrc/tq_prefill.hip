@@ -44,9 +44,19 @@ namespace lkv {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;   // rotate16_kernel
 constexpr int kKT = 64;         // keys per tile
-constexpr int kCols = 128;      // (query, head) columns per block
+#ifndef LKV_PREFILL_WAVES
+#define LKV_PREFILL_WAVES 8
+#endif
+// Waves of an attention block, 32 (query, head) columns each.  With 8, the
+// key codes of a tile are decoded by waves 0-3 and the value codes by waves
+// 4-7, so each decoded tile serves twice the columns of a 4-wave block.
+constexpr int kPWaves = LKV_PREFILL_WAVES;
+static_assert(kPWaves == 4 || kPWaves == 8, "4 or 8 waves per attention block");
+constexpr int kPThreads = 64 * kPWaves;
+constexpr bool kSplitDecode = kPWaves == 8;
+constexpr int kCols = 32 * kPWaves;  // (query, head) columns per block
 constexpr int kKRow = kD + 8;   // fp16 row of the decoded key tile (padded)
 constexpr int kVRow = kKT + 4;  // fp16 row of the transposed value tile (padded: conflict-free 8-byte reads)
 static_assert(kKT == 64, "the decode / compute lane maps assume 64-key tiles");
@@ -272,7 +282,7 @@ __device__ __forceinline__ uint32_t codes8(const uint8_t* p) {
 }
 
 template <bool PERM, int CB>
-__global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillParams P) {
+__global__ __launch_bounds__(kPThreads, 8 / kPWaves) void tq_prefill_attn_kernel(PrefillParams P) {
   static_assert(CB == 4 || PERM, "narrow code rows use the v_perm decode");
   constexpr int RB = kD * CB / 8;  // code bytes per token
   __shared__ __align__(16) uint16_t sK[2 * kKT * kKRow];  // two buffers of decoded keys
@@ -330,7 +340,7 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
     }
   } else {
     const int cmax = P.ncent - 1;
-    s_lut[tid] = pack2h(P.centroids[min(tid & 15, cmax)], P.centroids[min(tid >> 4, cmax)]);
+    if (tid < 256) s_lut[tid] = pack2h(P.centroids[min(tid & 15, cmax)], P.centroids[min(tid >> 4, cmax)]);
   }
   if (tid < 16) s_cent[tid] = f2h(P.centroids[min(tid, P.ncent - 1)]);
 
@@ -366,13 +376,16 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
 
   // ---- per-thread code registers of one key tile, loaded two tiles ahead:
   //   kw   key codes of key tid / 4, dims 32 (tid % 4) .. +32 (as nibbles)
-  //   vw   value codes of keys 4 (tid % 16) + e, dims 8 (tid / 16) .. +8 (as nibbles)
+  //   vw   value codes of keys 4 (vt % 16) + e, dims 8 (vt / 16) .. +8 (as nibbles)
   //   nrm  threads < 128: key (tid < 64) or value norm of key tid % 64
+  // with vt = tid; with the split decode, threads below 256 hold kw only and
+  // threads vt + 256 hold vw only.
   const uint8_t* kcod = P.k_codes + bh * static_cast<size_t>(P.cap) * RB;
   const uint8_t* vcod = P.v_codes + bh * static_cast<size_t>(P.cap) * RB;
   const float* norms = ((tid >> 6) & 1 ? P.v_norms : P.k_norms) + bh * static_cast<size_t>(P.cap);
-  const int kk = tid >> 2, part = tid & 3;  // key decode
-  const int kp = tid & 15, j4 = tid >> 4;   // value decode
+  const int kk = (tid & 255) >> 2, part = tid & 3;  // key decode
+  const int vt = tid & 255, kp = vt & 15, j4 = vt >> 4;  // value decode
+  const bool key_thr = !kSplitDecode || tid < 256, val_thr = !kSplitDecode || tid >= 256;  // wave-uniform
   struct TileRegs {
     uint4 kw;
     uint32_t vw[4];
@@ -380,10 +393,12 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
   };
   auto load_tile = [&](TileRegs& R, int t0) {
     if (cold_len > 0) {  // rows past cold_len read the last cold row (valid memory), decoded from elsewhere
-      R.kw = codes32<CB>(kcod + static_cast<size_t>(min(t0 + kk, cold_len - 1)) * RB + 4 * CB * part);
+      if (key_thr) R.kw = codes32<CB>(kcod + static_cast<size_t>(min(t0 + kk, cold_len - 1)) * RB + 4 * CB * part);
+      if (val_thr) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        R.vw[e] = codes8<CB>(vcod + static_cast<size_t>(min(t0 + 4 * kp + e, cold_len - 1)) * RB + CB * j4);
+        for (int e = 0; e < 4; ++e)
+          R.vw[e] = codes8<CB>(vcod + static_cast<size_t>(min(t0 + 4 * kp + e, cold_len - 1)) * RB + CB * j4);
+      }
     }
     if (tid < 128) {
       const int tk = t0 + (tid & 63);
@@ -396,7 +411,7 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
   auto decode_tile = [&](const TileRegs& R, int t0, int buf) {
     uint16_t* sKb = sK + buf * (kKT * kKRow);
     uint16_t* sVb = sVt + buf * (kD * kVRow);
-    {
+    if (key_thr) {
       const int tk = t0 + kk;
       uint4 o[4];
       if (tk < cold_len) {
@@ -422,7 +437,7 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
 #pragma unroll
       for (int q = 0; q < 4; ++q) *reinterpret_cast<uint4*>(sKb + kk * kKRow + 32 * part + 8 * q) = o[q];
     }
-    {
+    if (val_thr) {
       const int tb = t0 + 4 * kp;
       uint32_t pr[2][8];  // fp16 pairs (key tb + 2 hp, key tb + 2 hp + 1) of dim 8 j4 + dd
       if (tb + 4 <= cold_len) {
@@ -620,11 +635,12 @@ __global__ __launch_bounds__(kThreads, 2) void tq_prefill_attn_kernel(PrefillPar
   // PiV^T into LDS, [e][d] rows of kKRow: hi in sK, lo in sVt (128 x 136 fp16 each)
   static_assert(kD * kKRow <= 2 * kKT * kKRow && kD * kKRow <= 2 * kD * kVRow, "PiV staging fits the tile buffers");
   {
-    // thread: output dim e = tid % 128, input dims 64 (tid / 128) .. +63 four at a time (global
-    // loads coalesced over e, one 8-byte LDS store per four dims)
-    const int e = tid % kD, dbase = (tid / kD) * (kD / 2);
+    // thread: output dim e = tid % 128, input dims kSpan (tid / 128) .. +kSpan - 1 four at a time
+    // (global loads coalesced over e, one 8-byte LDS store per four dims)
+    constexpr int kSpan = kD / (kPThreads / kD);
+    const int e = tid % kD, dbase = (tid / kD) * kSpan;
 #pragma unroll 4
-    for (int d = dbase; d < dbase + kD / 2; d += 4) {
+    for (int d = dbase; d < dbase + kSpan; d += 4) {
       uint16_t hi[4], lo[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -757,10 +773,10 @@ extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const 
   const int64_t QT = kCols / G;
   const dim3 grid(static_cast<unsigned>((S + QT - 1) / QT), static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
   switch (bits) {
-    case 1: hipLaunchKernelGGL((tq_prefill_attn_kernel<true, 1>), grid, dim3(kThreads), 0, st, P); break;
-    case 2: hipLaunchKernelGGL((tq_prefill_attn_kernel<true, 2>), grid, dim3(kThreads), 0, st, P); break;
-    case 3: hipLaunchKernelGGL((tq_prefill_attn_kernel<true, 4>), grid, dim3(kThreads), 0, st, P); break;
-    default: hipLaunchKernelGGL((tq_prefill_attn_kernel<false, 4>), grid, dim3(kThreads), 0, st, P);
+    case 1: hipLaunchKernelGGL((tq_prefill_attn_kernel<true, 1>), grid, dim3(kPThreads), 0, st, P); break;
+    case 2: hipLaunchKernelGGL((tq_prefill_attn_kernel<true, 2>), grid, dim3(kPThreads), 0, st, P); break;
+    case 3: hipLaunchKernelGGL((tq_prefill_attn_kernel<true, 4>), grid, dim3(kPThreads), 0, st, P); break;
+    default: hipLaunchKernelGGL((tq_prefill_attn_kernel<false, 4>), grid, dim3(kPThreads), 0, st, P);
   }
   LKV_LAUNCH_CHECK("tq_prefill_attn");
   return LKV_OK;
