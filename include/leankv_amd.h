@@ -178,7 +178,8 @@ int lkv_sparse_gemm_batched_multi(const void* x, int64_t B, int n, const void* c
  * non-null, the ring half of lkv_tq_cache_append (cache.py:84-141: the new
  * token enters the hot window): k (rotated) and v also go to ring slot
  * *pos % hot_cap of rows (batch b, kv head h) = b * N[1] / 128 + h of
- * k_hot / v_hot (fp16 [B * N[1] / 128][hot_cap][128]).  With
+ * k_hot / v_hot (fp16 [B * N[1] / 128][hot_cap][128]); a negative *pos
+ * writes no ring slot.  With
  * lkv_tq_cache_evict run before it, the cache afterwards equals
  * lkv_tq_cache_append's on the same k and v.  No single reference
  * counterpart: the q/k/v calls of a decode layer at B > 1
@@ -302,7 +303,8 @@ int lkv_tq_prod_dequantize(const uint8_t* codes, const void* norms, int norm_dty
  *   k_codes, v_codes: uint8 [R, cap, row_bytes];  k_norms, v_norms: fp32 [R, cap]
  *   PiK, PiV: fp32 [128,128]; bounds fp32 [2^bits - 1]
  * Rows beyond `cap` are never written: a call with pos - hot_cap >= cap
- * skips the quantize (the host must size cap for the whole sequence).
+ * skips the quantize (the host must size cap for the whole sequence); a
+ * negative *pos writes nothing.
  */
 int lkv_tq_cache_append(const void* k_new, const void* v_new, void* k_hot, void* v_hot,
                         uint8_t* k_codes, float* k_norms, uint8_t* v_codes, float* v_norms,

@@ -461,6 +461,7 @@ __global__ __launch_bounds__(kNT, 2) void sparse_gemm_mfma_kernel(BatchedArgs P)
 static_assert(kBN == kNT && kBN % 128 == 0, "a reduce block covers one slab of whole heads");
 // Element n of batch row b of a q/k/v product in its hot ring: row (b, head
 // n / 128), slot pos % hot_cap, dim n % 128 (lkv_tq_cache_append's ring).
+// A negative position stores nothing into the ring.
 __device__ __forceinline__ size_t ring_index(const BatchedArgs& P, const BatchedSeg& S, int b, int n) {
   const int slot = *P.pos % P.hot_cap;
   const size_t r = static_cast<size_t>(b) * (S.N / 128) + n / 128;
@@ -486,7 +487,7 @@ __global__ __launch_bounds__(kNT) void batched_reduce_kernel(BatchedArgs P) {
     if (n < S.N) {
       const uint16_t h = f2h(lo ? o0 : o1);
       S.y[o] = h;
-      if (S.ring) S.ring[ring_index(P, S, b, n)] = h;
+      if (S.ring && *P.pos >= 0) S.ring[ring_index(P, S, b, n)] = h;
     }
     return;
   }
@@ -495,7 +496,7 @@ __global__ __launch_bounds__(kNT) void batched_reduce_kernel(BatchedArgs P) {
   if (S.ring) {  // v of a RoPE launch: its ring slot too
     const uint16_t h = f2h(sum);
     S.y[o] = h;
-    S.ring[ring_index(P, S, b, n)] = h;
+    if (*P.pos >= 0) S.ring[ring_index(P, S, b, n)] = h;
     return;
   }
   if (P.epi == kEpiSwiglu) {

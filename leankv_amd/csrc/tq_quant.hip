@@ -336,6 +336,7 @@ __global__ __launch_bounds__(kThreads) void append_kernel(
   const float* Pi = is_v ? PiV : PiK;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t pos = static_cast<int64_t>(*pos_p);
+  if (pos < 0) return;  // uniform: a negative position has no ring slot
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kRows;
   const int64_t slot = pos % hot_cap;
   const int64_t cold = pos - hot_cap;  // token leaving the hot window

@@ -162,12 +162,14 @@ def test_residual_rmsnorm_equals_residual_epilogue_then_rms_norm(cuda, B, N, Z):
 
 
 @pytest.mark.parametrize("bits,pos,hot_cap,cap", [(3, 70, 64, 200), (3, 10, 64, 200), (4, 100, 64, 200),
-                                                  (2, 64, 64, 200), (1, 130, 32, 98), (3, 300, 64, 200)])
+                                                  (2, 64, 64, 200), (1, 130, 32, 98), (3, 300, 64, 200),
+                                                  (3, -1, 64, 200)])
 def test_evict_and_ring_write_equal_cache_append(cuda, bits, pos, hot_cap, cap):
     """tq_cache_append's two halves, split for the batched decode step: lkv_tq_cache_evict for every layer in one
     launch, then the q/k/v launch writing the new token into the ring (lkv_sparse_gemm_batched_qkv_rope) --
     codes, norms and rings equal tq_cache_append on the same k and v, bit for bit, and q, k, v equal the RoPE
-    epilogue's; positions before the window fills, at and after it, and past the cold store (no eviction)."""
+    epilogue's; positions before the window fills, at and after it, past the cold store (no eviction), and a
+    negative one (no ring slot: the caches stay as they were)."""
     from leankv_amd import kernels
     from leankv_amd.turboquant.codebook import get_codebook_tensors
 
@@ -210,6 +212,10 @@ def test_evict_and_ring_write_equal_cache_append(cuda, bits, pos, hot_cap, cap):
         assert torch.equal(gc[0], kh) and torch.equal(gc[1], vh), li
         assert torch.equal(gc[2], kc) and torch.equal(gc[4], vc), li
         assert torch.equal(gc[3], kn) and torch.equal(gc[5], vn), li
+        if pos < 0:
+            _, hot, codes, norms, _ = caches[li]
+            assert torch.equal(kh, hot[0]) and torch.equal(vh, hot[1]) and torch.equal(kc, codes[0]), li
+            assert torch.equal(vc, codes[1]) and torch.equal(kn, norms[0]) and torch.equal(vn, norms[1]), li
 
 
 def test_empty_sizes(cuda):
