@@ -461,7 +461,7 @@ typedef struct lkv_decode_dims {
   int64_t n_kv_heads;    /* n_heads / n_kv_heads <= 8 */
   int64_t max_len;       /* RoPE table rows; tokens the cache holds */
   int64_t cap;           /* cold rows per (layer, kv head) */
-  int64_t hot_cap;       /* fp16 window, 1..64 */
+  int64_t hot_cap;       /* fp16 window, 1..256 */
   int32_t bits;          /* 1..4 (the packings of quantizer.py:38-62) */
   float eps;             /* RMSNorm epsilon */
   float scale;           /* attention scale */

@@ -106,7 +106,7 @@ int check_dims(const lkv_decode_dims* d) {
                   d->n_heads / d->n_kv_heads <= kMaxG,
               "decode: n_heads=%lld must be a multiple of n_kv_heads=%lld with at most %d query heads per kv head",
               (long long)d->n_heads, (long long)d->n_kv_heads, kMaxG);
-  LKV_REQUIRE(d->hot_cap >= 1 && d->hot_cap <= 64, "decode: hot_cap must be 1..64");
+  LKV_REQUIRE(d->hot_cap >= 1 && d->hot_cap <= 256, "decode: hot_cap must be 1..256 (the combine walks 256 slots)");
   LKV_REQUIRE(d->max_len >= 1 && d->max_len < (1ll << 30), "decode: max_len=%lld out of range", (long long)d->max_len);
   LKV_REQUIRE(d->cap >= d->max_len - d->hot_cap && d->cap < (1ll << 30),
               "decode: cap=%lld cannot hold max_len - hot_cap = %lld cold tokens", (long long)d->cap,

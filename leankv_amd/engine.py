@@ -458,7 +458,7 @@ class GenerateFastPath:
     the HF modules in Python, one patched projection at a time.  Installed on a
     TEAL-patched model, this wrapper sends a call that LeanKVEngine computes the
     same way -- one new token of one sequence (input_ids [1, 1]), a fused
-    TurboQuantCache at 1 to 4 bits with a window of at most 64 tokens, no padding, no sliding
+    TurboQuantCache at 1 to 4 bits with a window of at most 256 tokens, no padding, no sliding
     window shorter than the sequence, no attentions or hidden states asked for
     -- to the engine, built on that cache's own buffers and replayed as a HIP
     graph; it appends the token to the cache as update() would and returns the

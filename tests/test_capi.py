@@ -278,8 +278,10 @@ def test_decode_dims_validated_without_launch():
     lib = _lib.load()
     ok = _mistral_dims()
     assert lib.lkv_decode_workspace_bytes(ctypes.byref(ok)) > 0
+    for hot in (1, 128, 256):  # windows the step's combine walks (up to four groups of 64 slots)
+        assert lib.lkv_decode_workspace_bytes(ctypes.byref(_mistral_dims(hot_cap=hot, cap=4224 - hot))) > 0, hot
     for bad, msg in ((dict(hidden=4000), "hidden"), (dict(n_heads=36), "n_heads"), (dict(n_kv_heads=2), "n_heads"),
-                     (dict(bits=5), "bits"), (dict(bits=0), "bits"), (dict(hot_cap=65), "hot_cap"),
+                     (dict(bits=5), "bits"), (dict(bits=0), "bits"), (dict(hot_cap=257), "hot_cap"),
                      (dict(cap=100), "cap"),
                      (dict(rope_cos=None), "RoPE"), (dict(vocab=32770), "vocab")):
         d = _mistral_dims(**bad)

@@ -124,7 +124,7 @@ def test_generate_fast_path_eligibility_follows_the_step_checks():
     assert fp._eligible(ids, cache, {}) is None and "n_heads" in fp._step_reason(cache)
 
     # a window wider than the step's ring, and code widths the step is not built for
-    fp, cache = _fast_path_on(random_mistral(device="cpu", seed=3, **TINY), hot=128, n=10)
+    fp, cache = _fast_path_on(random_mistral(device="cpu", seed=3, **TINY), hot=320, n=10)
     assert fp._eligible(ids, cache, {}) is None and "hot_cap" in fp._step_reason(cache)
 
 

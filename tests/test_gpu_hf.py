@@ -283,22 +283,24 @@ def _teal_pair(cuda, seed, bits=3, hot=64, hip_rmsnorm=True, **kw):
     return out[0], out[1]
 
 
-@pytest.mark.parametrize("bits,hot", [(3, 64), (4, 32), (2, 64), (1, 64)])
-def test_generate_fast_path_matches_hf_forward(cuda, bits, hot):
+@pytest.mark.parametrize("bits,hot,plen", [(3, 64, 100), (4, 32, 100), (2, 64, 100), (1, 64, 100), (3, 128, 150),
+                                           (3, 256, 236)])
+def test_generate_fast_path_matches_hf_forward(cuda, bits, hot, plen):
     """optimize_model's generate fast path (single-token decode calls on the fused, graph-replayed decode step)
     vs the patched HF forward teacher-forced on the same tokens: per-step logits within 1e-3 (lm_head is the
     GEMV kernel at threshold 0 on one side, torch's GEMM on the other), the same greedy tokens, and the two
-    caches equal bit for bit afterwards (the step appends and evicts as TurboQuantCache.update does)."""
+    caches equal bit for bit afterwards (the step appends and evicts as TurboQuantCache.update does).  Windows
+    of 32 to 256 tokens; prompts longer than the window (the steps evict into the cold store) up to 128."""
     from leankv_amd.engine import GenerateFastPath
 
-    print("fast path case bits=%d hot=%d" % (bits, hot), flush=True)
+    print("fast path case bits=%d hot=%d plen=%d" % (bits, hot, plen), flush=True)
     (fast, ca), (slow, cb) = _teal_pair(cuda, 50 + bits, bits=bits, hot=hot)
     assert isinstance(fast.forward, GenerateFastPath) and not isinstance(slow.forward, GenerateFastPath)
-    prompt = _ids(100, 51)  # longer than the 64-token window: the steps evict into the cold store
+    prompt = _ids(plen, 51)
     res = _generate(fast, prompt.to(cuda), ca, 16)
     assert fast.forward.steps == {"engine": 15, "batch": 0, "forward": 1}, fast.forward.steps
-    assert ca.get_seq_length(0) == 115
-    new = res.sequences[0, 100:]
+    assert ca.get_seq_length(0) == plen + 15
+    new = res.sequences[0, plen:]
     errs = []
     with torch.no_grad():
         lg = slow(prompt.view(1, -1).to(cuda), past_key_values=cb, use_cache=True, logits_to_keep=1).logits[0, -1]
@@ -438,15 +440,15 @@ def test_generate_fast_path_after_cache_reset(cuda, B):
 
 
 def test_generate_fast_path_falls_back(cuda):
-    """Calls the fused B = 1 step does not serve run the model's own forward: a 128-token window (the step's
-    ring holds at most 64) and an unfused cache (fused_attention=False, the reference's full K/V); a 2-bit
+    """Calls the fused B = 1 step does not serve run the model's own forward: a 320-token window (the step's
+    ring holds at most 256) and an unfused cache (fused_attention=False, the reference's full K/V); a 2-bit
     cache with the 64-token window runs on the step."""
     from leankv_amd.turboquant.attention import use_on
     from leankv_amd.turboquant.cache import TurboQuantCache
 
     (fast, ca), _ = _teal_pair(cuda, 52)
     fp = fast.forward
-    c3 = TurboQuantCache(bits=3, head_dim=128, num_layers=2, hot_buffer_size=128, device=cuda, max_seq_len=256,
+    c3 = TurboQuantCache(bits=3, head_dim=128, num_layers=2, hot_buffer_size=320, device=cuda, max_seq_len=256,
                          fused_attention=True)
     use_on(fast, c3)
     _generate(fast, _ids(70, 55).to(cuda), c3, 4)
