@@ -17,12 +17,13 @@
 //   1. rotate16_kernel (fp16 MFMA, PiK / PiV split exactly into fp16 hi + lo
 //      parts): q_rot = (q @ PiK^T) * scale * log2(e) in fp16, the score
 //      operand; hot rings k @ PiK^T and v @ PiV^T (fp16);
-//   2. tq_prefill_attn_kernel: grid (query tiles, kv heads, batch), 4 waves.
-//      A block owns 128 (query, head) columns: 128 / G consecutive queries x
+//   2. tq_prefill_attn_kernel: grid (query tiles, kv heads, batch), 8 waves.
+//      A block owns 256 (query, head) columns: 256 / G consecutive queries x
 //      the G heads of one kv head, 32 columns per wave.  It walks the keys in
 //      tiles of 64; per tile the block decodes the codes once into LDS --
-//      keys as [key][dim] fp16 centroid values, values transposed as
-//      [dim][key] -- and every wave runs, on v_mfma_f32_16x16x32_f16,
+//      keys as [key][dim] fp16 centroid values (waves 0-3), values transposed
+//      as [dim][key] (waves 4-7) -- and every wave runs, on
+//      v_mfma_f32_16x16x32_f16,
 //      * scores transposed, A = 16 keys x 32 dims from LDS, B = its rotated
 //        queries (registers), so a lane holds 8 keys of one column;
 //      * the online softmax per lane (key norms, causal mask, exp2 domain,
