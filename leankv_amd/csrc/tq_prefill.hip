@@ -59,7 +59,18 @@ constexpr int kPThreads = 64 * kPWaves;
 constexpr bool kSplitDecode = kPWaves == 8;
 constexpr int kCols = 32 * kPWaves;  // (query, head) columns per block
 constexpr int kKRow = kD + 8;   // fp16 row of the decoded key tile (padded)
-constexpr int kVRow = kKT + 4;  // fp16 row of the transposed value tile (padded: conflict-free 8-byte reads)
+#ifndef LKV_PREFILL_VTR
+#define LKV_PREFILL_VTR 1
+#endif
+// Value tile layout.  1: [key][column] rows as decoded (columns in the keys'
+// dim order), the MFMA's V^T operand gathered by ds_read_b64_tr_b16; 0:
+// transposed [dim][key] by v_perm in the decode.
+constexpr bool kVTr = LKV_PREFILL_VTR;
+constexpr int kVRow = kKT + 4;    // [dim][key] row (padded: conflict-free 8-byte reads)
+// [key][column] row: 76 dwords, so the 16-byte chunks a decode store writes (rows 4 kp + e) and the 8-byte
+// chunks of a transposed read (rows 4 g + i, 4 chunks each) fall in distinct banks
+constexpr int kVRowT = kD + 24;
+constexpr int kVBuf = kVTr ? kKT * kVRowT : kD * kVRow;  // fp16 per value buffer
 static_assert(kKT == 64, "the decode / compute lane maps assume 64-key tiles");
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kXcds = 8;  // MI355X: 8 accelerator complex dies, one L2 each
@@ -287,7 +298,7 @@ __global__ __launch_bounds__(kPThreads, 8 / kPWaves) void tq_prefill_attn_kernel
   static_assert(CB == 4 || PERM, "narrow code rows use the v_perm decode");
   constexpr int RB = kD * CB / 8;  // code bytes per token
   __shared__ __align__(16) uint16_t sK[2 * kKT * kKRow];  // two buffers of decoded keys
-  __shared__ __align__(16) uint16_t sVt[2 * kD * kVRow];  // two buffers of transposed values
+  __shared__ __align__(16) uint16_t sVt[2 * kVBuf];  // two buffers of decoded values
   __shared__ __align__(16) float sN[2][2][kKT];           // [buffer][key, value] norms (1 hot, 0 past the end)
   __shared__ uint32_t s_lut[256];
   __shared__ uint16_t s_cent[16];
@@ -411,7 +422,7 @@ __global__ __launch_bounds__(kPThreads, 8 / kPWaves) void tq_prefill_attn_kernel
   // order within 8-dim groups with PERM), values transposed [dim][key]
   auto decode_tile = [&](const TileRegs& R, int t0, int buf) {
     uint16_t* sKb = sK + buf * (kKT * kKRow);
-    uint16_t* sVb = sVt + buf * (kD * kVRow);
+    uint16_t* sVb = sVt + buf * kVBuf;
     if (key_thr) {
       const int tk = t0 + kk;
       uint4 o[4];
@@ -438,7 +449,37 @@ __global__ __launch_bounds__(kPThreads, 8 / kPWaves) void tq_prefill_attn_kernel
 #pragma unroll
       for (int q = 0; q < 4; ++q) *reinterpret_cast<uint4*>(sKb + kk * kKRow + 32 * part + 8 * q) = o[q];
     }
-    if (val_thr) {
+    if (val_thr && kVTr) {
+      // keys tb .. tb + 3, columns 8 j4 .. 8 j4 + 7 (dims in the keys' order): one 16-byte chunk each
+      const int tb = t0 + 4 * kp;
+      uint4 o[4];
+      if (tb + 4 <= cold_len) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          uint32_t d[4];
+          decode_dw<PERM>(R.vw[e], tab, s_lut, d);
+          o[e] = uint4{d[0], d[1], d[2], d[3]};
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int tk = tb + e;
+          if (tk < cold_len) {
+            uint32_t d[4];
+            decode_dw<PERM>(R.vw[e], tab, s_lut, d);
+            o[e] = uint4{d[0], d[1], d[2], d[3]};
+          } else if (tk < kv_len) {
+            o[e] = *reinterpret_cast<const uint4*>(P.hv + (bh * P.hot_cap + static_cast<size_t>(tk % P.hot_cap)) * kD +
+                                                  8 * j4);
+            if constexpr (PERM) o[e] = perm_group(o[e]);
+          } else {
+            o[e] = uint4{0u, 0u, 0u, 0u};
+          }
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) *reinterpret_cast<uint4*>(sVb + (4 * kp + e) * kVRowT + 8 * j4) = o[e];
+    } else if (val_thr) {
       const int tb = t0 + 4 * kp;
       uint32_t pr[2][8];  // fp16 pairs (key tb + 2 hp, key tb + 2 hp + 1) of dim 8 j4 + dd
       if (tb + 4 <= cold_len) {
@@ -509,7 +550,7 @@ __global__ __launch_bounds__(kPThreads, 8 / kPWaves) void tq_prefill_attn_kernel
   // (tt 0..3, i 0..3); the value MFMA takes them in two halves of 32 keys
   auto compute_tile = [&](int t0, int buf) {
     const uint16_t* sKb = sK + buf * (kKT * kKRow);
-    const uint16_t* sVb = sVt + buf * (kD * kVRow);
+    const uint16_t* sVb = sVt + buf * kVBuf;
     f32x4 sc[2][4];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
@@ -567,15 +608,29 @@ __global__ __launch_bounds__(kPThreads, 8 / kPWaves) void tq_prefill_attn_kernel
                            pack2h(p[4] * v1[0], p[5] * v1[1]), pack2h(p[6] * v1[2], p[7] * v1[3])};
       }
     }
-    // values: O^T tiles [ct][dt] += V^T (dims 16 dt .., the lane's 8 keys of half hh) x P^T
+    // values: O^T tiles [ct][dt] += V^T (columns 16 dt .., the lane's 8 keys of half hh) x P^T
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      const uint16_t* row = sVb + (16 * dt + h16) * kVRow;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(row + 32 * hh + 4 * g);
-        const uint2 hi = *reinterpret_cast<const uint2*>(row + 32 * hh + 16 + 4 * g);
-        const u32x4 a = u32x4{lo.x, lo.y, hi.x, hi.y};
+        u32x4 a;
+        if constexpr (kVTr) {
+          // ds_read_b64_tr_b16: in each 16-lane group, lane l receives element l % 4 of the 8 bytes that
+          // lanes 4 i + l / 4 (i = 0..3) address.  Lane (h16, g) addresses key 32 hh + 4 g + h16 / 4 (+16),
+          // columns 16 dt + 4 (h16 % 4) .. +3, so it receives column 16 dt + h16 of keys 32 hh + 4 g + i.
+          const uint16_t* src = sVb + (32 * hh + 4 * g + (h16 >> 2)) * kVRowT + 16 * dt + 4 * (h16 & 3);
+          typedef short v4s __attribute__((ext_vector_type(4)));
+          typedef __attribute__((address_space(3))) v4s lds_v4s;
+          const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(src));
+          const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(src + 16 * kVRowT));
+          const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+          a = u32x4{l2.x, l2.y, h2.x, h2.y};
+        } else {
+          const uint16_t* row = sVb + (16 * dt + h16) * kVRow;
+          const uint2 lo = *reinterpret_cast<const uint2*>(row + 32 * hh + 4 * g);
+          const uint2 hi = *reinterpret_cast<const uint2*>(row + 32 * hh + 16 + 4 * g);
+          a = u32x4{lo.x, lo.y, hi.x, hi.y};
+        }
         o[0][dt] = mfma16x16x32(a, pb[0][hh], o[0][dt]);
         o[1][dt] = mfma16x16x32(a, pb[1][hh], o[1][dt]);
       }
@@ -633,8 +688,10 @@ __global__ __launch_bounds__(kPThreads, 8 / kPWaves) void tq_prefill_attn_kernel
     }
   }
   __syncthreads();  // every wave is past its last tile: the key / value buffers are free
-  // PiV^T into LDS, [e][d] rows of kKRow: hi in sK, lo in sVt (128 x 136 fp16 each)
-  static_assert(kD * kKRow <= 2 * kKT * kKRow && kD * kKRow <= 2 * kD * kVRow, "PiV staging fits the tile buffers");
+  // PiV^T into LDS, [e][c] rows of kKRow: hi in sK, lo in sVt (128 x 136 fp16 each).  Column c holds
+  // input dim c, or with the [key][column] value tile under PERM the dim its column c of o carries
+  // (8 (c / 8) + kPermDim[c % 8], the keys' dim order).
+  static_assert(kD * kKRow <= 2 * kKT * kKRow && kD * kKRow <= 2 * kVBuf, "PiV staging fits the tile buffers");
   {
     // thread: output dim e = tid % 128, input dims kSpan (tid / 128) .. +kSpan - 1 four at a time
     // (global loads coalesced over e, one 8-byte LDS store per four dims)
@@ -645,7 +702,9 @@ __global__ __launch_bounds__(kPThreads, 8 / kPWaves) void tq_prefill_attn_kernel
       uint16_t hi[4], lo[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float pv = P.PiV[(d + i) * kD + e];
+        const int c = d + i;
+        const int dim = (kVTr && PERM) ? (c & ~7) + ((c & 3) << 1) + ((c >> 2) & 1) : c;
+        const float pv = P.PiV[dim * kD + e];
         hi[i] = f2h(pv);
         lo[i] = f2h((pv - h2f(hi[i])) * 2048.f);
       }
