@@ -67,9 +67,9 @@ constexpr int kKRow = kD + 8;   // fp16 row of the decoded key tile (padded)
 // transposed [dim][key] by v_perm in the decode.
 constexpr bool kVTr = LKV_PREFILL_VTR;
 constexpr int kVRow = kKT + 4;    // [dim][key] row (padded: conflict-free 8-byte reads)
-// [key][column] row: 76 dwords, so the 16-byte chunks a decode store writes (rows 4 kp + e) and the 8-byte
-// chunks of a transposed read (rows 4 g + i, 4 chunks each) fall in distinct banks
-constexpr int kVRowT = kD + 24;
+// [key][column] row: 72 dwords, so the 8-byte chunks of a transposed read (rows 4 g + i, 4 chunks each)
+// fall in distinct banks
+constexpr int kVRowT = kD + 16;
 constexpr int kVBuf = kVTr ? kKT * kVRowT : kD * kVRow;  // fp16 per value buffer
 static_assert(kKT == 64, "the decode / compute lane maps assume 64-key tiles");
 constexpr float kLog2e = 1.4426950408889634f;
@@ -388,7 +388,7 @@ __global__ __launch_bounds__(kPThreads, 8 / kPWaves) void tq_prefill_attn_kernel
 
   // ---- per-thread code registers of one key tile, loaded two tiles ahead:
   //   kw   key codes of key tid / 4, dims 32 (tid % 4) .. +32 (as nibbles)
-  //   vw   value codes of keys 4 (vt % 16) + e, dims 8 (vt / 16) .. +8 (as nibbles)
+  //   vw   value codes of keys 4 kp + e, dims 8 j4 .. +8 (as nibbles)
   //   nrm  threads < 128: key (tid < 64) or value norm of key tid % 64
   // with vt = tid; with the split decode, threads below 256 hold kw only and
   // threads vt + 256 hold vw only.
@@ -396,7 +396,9 @@ __global__ __launch_bounds__(kPThreads, 8 / kPWaves) void tq_prefill_attn_kernel
   const uint8_t* vcod = P.v_codes + bh * static_cast<size_t>(P.cap) * RB;
   const float* norms = ((tid >> 6) & 1 ? P.v_norms : P.k_norms) + bh * static_cast<size_t>(P.cap);
   const int kk = (tid & 255) >> 2, part = tid & 3;  // key decode
-  const int vt = tid & 255, kp = vt & 15, j4 = vt >> 4;  // value decode
+  // value decode: with the [key][column] tile, the 16 lanes of a row group take the 16 column chunks of
+  // one row (conflict-free 16-byte stores, coalesced code loads); transposed, the 16 key quads of a column
+  const int vt = tid & 255, kp = kVTr ? vt >> 4 : vt & 15, j4 = kVTr ? vt & 15 : vt >> 4;
   const bool key_thr = !kSplitDecode || tid < 256, val_thr = !kSplitDecode || tid >= 256;  // wave-uniform
   struct TileRegs {
     uint4 kw;
