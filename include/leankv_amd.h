@@ -356,7 +356,8 @@ int lkv_tq_decode_attn(const void* q, const uint8_t* k_codes, const float* k_nor
  * q: fp16 [B, Hq, S, 128] (post-RoPE); codes uint8 [B, Hkv, cap, row_bytes]
  * (row_bytes as for lkv_tq_decode_attn, bits 1..4); norms fp32 [B, Hkv, cap];
  * hot fp16 [B, Hkv, hot_cap, 128];
- * out fp16 [B, Hq, S, 128].  Hq / Hkv must be 1, 2, 4, 8 or 16.
+ * out fp16 [B, Hq, S, 128].  Hq / Hkv must be 1, 2, 4, 8 or 16.  The workspace
+ * holds the two hot rings rotated into the key / value domains.
  */
 size_t lkv_tq_prefill_attn_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t hot_cap);
 int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const float* k_norms,

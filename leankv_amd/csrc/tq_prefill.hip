@@ -15,11 +15,13 @@
 //
 // Launches of lkv_tq_prefill_attn (two, on the caller's stream):
 //   1. rotate16_kernel (fp16 MFMA, PiK / PiV split exactly into fp16 hi + lo
-//      parts): q_rot = (q @ PiK^T) * scale * log2(e) in fp16, the score
-//      operand; hot rings k @ PiK^T and v @ PiV^T (fp16);
+//      parts): the hot rings k @ PiK^T and v @ PiV^T (fp16);
 //   2. tq_prefill_attn_kernel: grid (query tiles, kv heads, batch), 8 waves.
 //      A block owns 256 (query, head) columns: 256 / G consecutive queries x
-//      the G heads of one kv head, 32 columns per wave.  It walks the keys in
+//      the G heads of one kv head, 32 columns per wave.  Its prologue rotates
+//      the block's queries, q_rot = (q @ PiK^T) * scale * log2(e) in fp16 (the
+//      score operand), on the same MFMA with PiK split as in 1 (PiK staged in
+//      the tile buffers, each wave its own 32 columns).  It walks the keys in
 //      tiles of 64; per tile the block decodes the codes once into LDS --
 //      keys as [key][dim] fp16 centroid values (waves 0-3), values transposed
 //      as [dim][key] (waves 4-7) -- and every wave runs, on
@@ -75,8 +77,17 @@ static_assert(kKT == 64, "the decode / compute lane maps assume 64-key tiles");
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kXcds = 8;  // MI355X: 8 accelerator complex dies, one L2 each
 
+#ifndef LKV_PREFILL_QROT
+#define LKV_PREFILL_QROT 1
+#endif
+// 1: the attention kernel rotates its own queries in its prologue; 0: one
+// rotate16_kernel launch writes them first.  Same bits either way.
+constexpr bool kQRotIn = LKV_PREFILL_QROT;
+
 struct PrefillParams {
-  const uint16_t* q16;     // [B, Hq, S, 128] fp16: (q @ PiK^T) * scale * log2(e)
+  const uint16_t* q16;     // [B, Hq, S, 128] fp16: q (kQRotIn) or (q @ PiK^T) * scale * log2(e)
+  const float* PiK;        // [128, 128] (kQRotIn)
+  float scale_log2;        // scale * log2(e) (kQRotIn)
   const float* PiV;        // [128, 128]: the output rows are un-rotated in the epilogue
   uint16_t* out;           // [B, Hq, S, 128] fp16
   const uint8_t* k_codes;  // [B, Hkv, cap, 64]
@@ -361,6 +372,74 @@ __global__ __launch_bounds__(kPThreads, 8 / kPWaves) void tq_prefill_attn_kernel
   int lim[2];  // keys [0, lim) visible to the lane's column (0: no such query)
   u32x4 qa[2][4];
   int wmin = 0x7fffffff;
+  if constexpr (kQRotIn) {
+    // q_rot = (q @ PiK^T) * scale * log2(e) on fp16 MFMA, rotate16_kernel's arithmetic (PiK split into
+    // fp16 hi + lo / 2048, the same products in the same k order, so the same bits), transposed: A = 16
+    // rows of PiK, B = the wave's 16 query rows of a column tile.  Staged row R = 32 kb + 16 hf + 4 g' + i
+    // holds the PiK row of the key tile's column 32 kb + 8 g' + 4 hf + i (its dim in the decode's order),
+    // so the output lane (h16, g) of row tile 2 kb + hf holds that column tile's score operand positions
+    // 4 hf + i of dims block kb: qa[ct][kb] directly.  PiK hi in sK, lo in sVt (the tile buffers are free
+    // until the first decode).
+    {
+      const int e4 = tid & 31;  // input dims 4 e4 .. +3
+#pragma unroll
+      for (int j = 0; j < kD / (kPThreads / 32); ++j) {
+        const int R = tid / 32 + (kPThreads / 32) * j;
+        const int C = (R & ~31) + 8 * ((R >> 2) & 3) + 4 * ((R >> 4) & 1) + (R & 3);
+        const int dim = PERM ? (C & ~7) + ((C & 3) << 1) + ((C >> 2) & 1) : C;
+        const float4 pv = *reinterpret_cast<const float4*>(P.PiK + dim * kD + 4 * e4);
+        const float x[4] = {pv.x, pv.y, pv.z, pv.w};
+        uint16_t hi[4], lo[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          hi[i] = f2h(x[i]);
+          lo[i] = f2h((x[i] - h2f(hi[i])) * 2048.f);
+        }
+        *reinterpret_cast<uint2*>(sK + R * kKRow + 4 * e4) =
+            uint2{hi[0] | (static_cast<uint32_t>(hi[1]) << 16), hi[2] | (static_cast<uint32_t>(hi[3]) << 16)};
+        *reinterpret_cast<uint2*>(sVt + R * kKRow + 4 * e4) =
+            uint2{lo[0] | (static_cast<uint32_t>(lo[1]) << 16), lo[2] | (static_cast<uint32_t>(lo[3]) << 16)};
+      }
+    }
+    u32x4 bq[2][4];  // B: the column's q row, dims 32 kb + 8 g .. +7
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int c = 32 * wave + 16 * ct + h16;
+      const int qq = q0 + c / G, hh = c % G;
+      const uint16_t* src =
+          P.q16 + ((static_cast<size_t>(b) * P.Hq + kvh * G + hh) * P.S + min(qq, P.S - 1)) * kD + 8 * g;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const uint4 u = *reinterpret_cast<const uint4*>(src + 32 * kb);
+        bq[ct][kb] = u32x4{u.x, u.y, u.z, u.w};
+      }
+    }
+    __syncthreads();  // PiK staged
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      f32x4 accl[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const u32x4 ah = *reinterpret_cast<const u32x4*>(sK + (16 * t + h16) * kKRow + 32 * kb + 8 * g);
+        const u32x4 al = *reinterpret_cast<const u32x4*>(sVt + (16 * t + h16) * kKRow + 32 * kb + 8 * g);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          acc[ct] = mfma16x16x32(ah, bq[ct][kb], acc[ct]);
+          accl[ct] = mfma16x16x32(al, bq[ct][kb], accl[ct]);
+        }
+      }
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (acc[ct][i] + accl[ct][i] * (1.f / 2048.f)) * P.scale_log2;
+        qa[ct][t >> 1][2 * (t & 1)] = static_cast<uint32_t>(f2h(v[0])) | (static_cast<uint32_t>(f2h(v[1])) << 16);
+        qa[ct][t >> 1][2 * (t & 1) + 1] = static_cast<uint32_t>(f2h(v[2])) | (static_cast<uint32_t>(f2h(v[3])) << 16);
+      }
+    }
+    __syncthreads();  // every wave is past its PiK reads: the tile buffers are free
+  }
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
     const int c = 32 * wave + 16 * ct + h16;
@@ -368,14 +447,19 @@ __global__ __launch_bounds__(kPThreads, 8 / kPWaves) void tq_prefill_attn_kernel
     const bool ok = qq < P.S;
     lim[ct] = ok ? qpos0 + qq + 1 : 0;
     if (ok) wmin = min(wmin, lim[ct]);
-    const uint16_t* src =
-        P.q16 + ((static_cast<size_t>(b) * P.Hq + kvh * G + hh) * P.S + min(qq, P.S - 1)) * kD + 8 * g;
+    if constexpr (kQRotIn) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      uint4 u = *reinterpret_cast<const uint4*>(src + 32 * kb);
-      if constexpr (PERM) u = perm_group(u);
-      const u32x4 v = u32x4{u.x, u.y, u.z, u.w};
-      qa[ct][kb] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+      for (int kb = 0; kb < 4; ++kb) qa[ct][kb] = ok ? qa[ct][kb] : u32x4{0u, 0u, 0u, 0u};
+    } else {
+      const uint16_t* src =
+          P.q16 + ((static_cast<size_t>(b) * P.Hq + kvh * G + hh) * P.S + min(qq, P.S - 1)) * kD + 8 * g;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        uint4 u = *reinterpret_cast<const uint4*>(src + 32 * kb);
+        if constexpr (PERM) u = perm_group(u);
+        const u32x4 v = u32x4{u.x, u.y, u.z, u.w};
+        qa[ct][kb] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+      }
     }
   }
 #pragma unroll
@@ -762,9 +846,9 @@ extern "C" size_t lkv_tq_prefill_attn_workspace_bytes(int64_t B, int64_t Hq, int
                                                       int64_t hot_cap) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || hot_cap <= 0) return 0;
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
-  const size_t rows = static_cast<size_t>(B * Hq * S) * kD;
+  const size_t rows = kQRotIn ? 0 : static_cast<size_t>(B * Hq * S) * kD;
   const size_t hot = static_cast<size_t>(B * Hkv * hot_cap) * kD * 2;
-  return al(rows * 2) + 2 * al(hot);  // q_rot fp16, hot rings (the output is un-rotated in the kernel)
+  return al(rows * 2) + 2 * al(hot);  // q_rot fp16 (without kQRotIn), hot rings (the output is un-rotated in the kernel)
 }
 
 extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const float* k_norms,
@@ -799,8 +883,8 @@ extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const 
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
   const int64_t nrows = B * Hq * S;
   char* ws = static_cast<char*>(workspace);
-  uint16_t* q16 = reinterpret_cast<uint16_t*>(ws);
-  uint16_t* hk = reinterpret_cast<uint16_t*>(ws + al(static_cast<size_t>(nrows) * kD * 2));
+  uint16_t* q16 = kQRotIn ? const_cast<uint16_t*>(static_cast<const uint16_t*>(q)) : reinterpret_cast<uint16_t*>(ws);
+  uint16_t* hk = reinterpret_cast<uint16_t*>(ws + (kQRotIn ? 0 : al(static_cast<size_t>(nrows) * kD * 2)));
   uint16_t* hv = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(hk) +
                                              al(static_cast<size_t>(B * Hkv * hot_cap) * kD * 2));
   const int64_t cold_len = kv_len > hot_cap ? kv_len - hot_cap : 0;
@@ -809,11 +893,14 @@ extern "C" int lkv_tq_prefill_attn(const void* q, const uint8_t* k_codes, const 
   // (one launch; every hot slot is rotated, only the current tokens' slots are read)
   {
     const int64_t nhot = kv_len > cold_len ? B * Hkv * hot_cap : 0;
-    const RotSeg segs[3] = {{q, PiK, q16, nrows, scale * kLog2e}, {k_hot, PiK, hk, nhot, 1.f}, {v_hot, PiV, hv, nhot, 1.f}};
+    const RotSeg segs[3] = {{q, PiK, q16, kQRotIn ? 0 : nrows, scale * kLog2e}, {k_hot, PiK, hk, nhot, 1.f},
+                            {v_hot, PiV, hv, nhot, 1.f}};
     if (int e = rotate16_segs<true, true, false>(segs, 3, st)) return e;
   }
   PrefillParams P;
   P.q16 = q16;
+  P.PiK = PiK;
+  P.scale_log2 = scale * kLog2e;
   P.PiV = PiV;
   P.out = static_cast<uint16_t*>(out);
   P.k_codes = k_codes;

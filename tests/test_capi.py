@@ -94,7 +94,8 @@ def test_invalid_arguments_rejected_without_launch():
     assert lib.lkv_tq_prefill_attn(p, p, p, p, p, p, p, p, p, p, 3, 100, 1, 8, 2, 100, 64, 64, 0.1, p, p,
                                    1024, None) == -1
     assert "workspace" in _lib.last_error()
-    assert lib.lkv_tq_prefill_attn_workspace_bytes(1, 32, 8, 4096, 64) >= 32 * 4096 * 128 * 2
+    # the two hot rings rotated into the key / value domains (the kernel rotates its own queries)
+    assert lib.lkv_tq_prefill_attn_workspace_bytes(1, 32, 8, 4096, 64) == 2 * 8 * 64 * 128 * 2
     # RoPE: negative sizes, null factors
     assert lib.lkv_rope_f16(p, p, p, p, -1, 32, 8, None) == -1
     assert "out of range" in _lib.last_error()
